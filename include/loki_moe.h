@@ -1,0 +1,137 @@
+/* loki_moe.h -- C ABI of libloki_moe.so, the MI355X (gfx950) DeepSeek-R1 MoE feed-forward block.
+ *
+ * Drop-in for the MoE part of the reference's src/fused_layer.h: the same FLCtx / FLW / FLOut types and fl_* names and
+ * parameter lists, with hipEvent_t where the reference has cudaEvent_t. Entry points marked "additive" have no
+ * counterpart in the reference; they are the device-resident path (router, dispatch and experts on the GPU, no host
+ * round-trip) that the MI355X build is measured on.
+ *
+ * Errors: the reference prints "[fused] CUDA error" and exits (src/fused_layer.cu:17). The reference-named entry points
+ * keep that behaviour for runtime failures; the additive ones return 0 or a negative FL_E* code and leave a message in
+ * fl_last_error(ctx) instead, so a host harness can test its error paths.
+ * Threading: one HIP stream per context, not thread-safe (as the reference, src/fused_layer.cu:392-393).
+ */
+#pragma once
+#include <stdint.h>
+#include <stddef.h>
+#include <hip/hip_runtime.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct FLCtx FLCtx;
+
+/* formats (src/fused_layer.h:11); this library computes FL_IQ2 everywhere */
+enum { FL_Q4K = 0, FL_Q6K = 1, FL_Q80 = 2, FL_Q5K = 3, FL_IQ2 = 4, FL_Q2K = 5, FL_Q3K = 6 };
+/* IQ2_XXS byte layouts of expert matrices: ggml's row-major blocks, or the tiled resident layout of fl_pack_iq2xxs */
+enum { FL_LAYOUT_GGML = 0, FL_LAYOUT_TILED = 1 };
+/* status codes of the additive entry points */
+enum { FL_OK = 0, FL_EINVAL = -1, FL_ENOMEM = -2, FL_EHIP = -3, FL_ERANGE = -4, FL_ESCOPE = -5 };
+
+typedef struct FLW {   /* src/fused_layer.h:12-18, unchanged: device pointers of one layer's always-used weights */
+    const void * attn_norm, * q_a, * q_a_norm, * q_b, * kv_a, * kv_a_norm, * kv_b, * k_bT, * attn_out, * ffn_norm, * gate_inp, * probs_b;
+    const void * sh_gate, * sh_up, * sh_down;
+    const void * d_gate, * d_up, * d_down;
+    int kv_b_v;
+    int gate_f16;
+} FLW;
+
+typedef struct FLOut {   /* src/fused_layer.h:19-21, unchanged: context-owned pinned host mirrors */
+    const int * sel; const float * wts; const float * ncur; const float * fi; const float * skt; const int * sel_s; const float * wts_s;
+    const float * sc; const float * ccat; const float * h; const float * moe;
+} FLOut;
+
+/* ---------------------------------------------------------------- reference entry points (src/fused_layer.h:22-53) */
+/* fl.h:23 -- context: stream, events, buffers. kvp / sc_cap size the attention cache in the reference; kept for the ABI. */
+FLCtx * fl_init(int kvp, int sc_cap);
+/* fl.h:27 -- attention is outside this library: prints the reason and exits 7 like any fused-layer failure */
+void fl_attn(FLCtx *, const FLW *, int N, int pos0, const int * pos, void * KC, void * VC, const float * hin, int dense, int last_row, int wrow);
+/* fl.h:29 -- wide-pass buffers for wmax rows with KE experts per row */
+int fl_wide_init(FLCtx *, int wmax, int KE);
+/* fl.h:30 -- routed experts of one arena batch for up to 8 (row, k) pairs per slot; down_fmt must be FL_IQ2 */
+void fl_wide_moe(FLCtx *, const void * gate, const void * up, const void * down, int down_fmt, int nexp, const int * midx, const int * rows,
+                 const int * kidx, const float * wk, int nslots, int KE, int par);
+void fl_wide_mark(FLCtx *, int par);                 /* fl.h:31 */
+void fl_wide_wait(FLCtx *, int par);                 /* fl.h:32 */
+void fl_wide_finish(FLCtx *, int n, int KE, FLOut * out);   /* fl.h:33 -- h = base + sum_k out, moe = sum_k out, waited */
+void fl_moe_outs(FLCtx *, int b, const int * ids, const float * w, int KE, float * out);   /* fl.h:35 */
+void fl_wide_outs(FLCtx *, int row, int KE, float * out);                                  /* fl.h:36 */
+void fl_wide_skip(FLCtx *, const float * mo, int n, FLOut * out);                         /* fl.h:37 */
+/* fl.h:39 / fl.h:41 -- speculative attention and geometry sketch: outside this library (exit 7, as fl_attn) */
+void fl_spec(FLCtx *, const FLW * W1, void * KC1, void * VC1);
+void fl_sketch(FLCtx *, const float * TPROJ, const void * GSKT, int K);
+/* fl.h:43 -- what & 1: sel/wts/ncur/fi of the last routing (fl_ffn_begin) to the host mirrors, waited; other bits are attention's */
+void fl_fetch(FLCtx *, int n, int what, FLOut * out);
+/* fl.h:45 -- narrow MoE (n <= 8): gate/up/down = arena bases of nexp IQ2_XXS experts in ggml layout at ggml stride,
+ * ids/w [n][KE] with ids = slot indices into the arena; -> out->h = routed + shared + ffn_inp, out->moe = routed. Waited. */
+void fl_moe(FLCtx *, const void * gate, const void * up, const void * down, int nexp, int down_fmt, const int * ids, const float * w, int KE, int n, FLOut * out);
+void fl_skip(FLCtx *, const float * mo, int n, FLOut * out);                /* fl.h:47 -- h = mo + shared + ffn_inp, waited */
+void fl_h2d(FLCtx *, void * dst, const void * src, size_t bytes);           /* fl.h:49 */
+void fl_wait_event(FLCtx *, hipEvent_t ev);                                 /* fl.h:51 */
+double fl_gpu_ms(FLCtx *, int which);                                       /* fl.h:52 -- 1 = experts (ms, accumulated) */
+
+/* ---------------------------------------------------------------- additive: the MoE tail of fl_attn without attention
+ * Router + shared expert on N rows (N <= 64 per call; wrow >= 0 places them at rows wrow.. of a wide pass), given the
+ * ffn-normed rows ncur and the residual ffn_inp as host floats [N][7168] (the reference computes both inside fl_attn,
+ * src/fused_layer.cu:498-525). Uses W->gate_inp (F32 [256][7168]), W->probs_b, W->sh_gate/up/down (IQ2_XXS, ggml layout). */
+int fl_ffn_begin(FLCtx *, const FLW * W, int N, const float * ncur, const float * ffn_inp, int wrow);
+/* routing rule: DeepSeek-V3 groups (default 8 groups, top-4 groups, top-8, x2.5); n_group = topk_group = 1 is the reference's rule */
+int fl_set_routing(FLCtx *, int n_group, int topk_group, int topk, float scale);
+
+/* ---------------------------------------------------------------- additive: device-resident block (the measured path) */
+typedef struct FLMoeLayer {
+    const float * gate_inp;    /* [n_exp][E] F32 router weight (ffn_gate_inp), device */
+    const float * probs_b;     /* [n_exp] F32 e_score_correction_bias (exp_probs_b), device */
+    const void * gate_exps;    /* [n_exp] x IQ2_XXS [H rows][E cols] at expert stride H*E/256*66 B, device */
+    const void * up_exps;      /* as gate_exps */
+    const void * down_exps;    /* [n_exp] x IQ2_XXS [E rows][H cols] */
+    const void * sh_gate, * sh_up, * sh_down;   /* shared expert, IQ2_XXS, same layout */
+    int layout;                /* FL_LAYOUT_TILED (fl_pack_iq2xxs) */
+    int n_exp;                 /* routed experts (<= 256) */
+    int E, H;                  /* hidden (7168) and expert intermediate (2048) sizes; E, H multiples of 1024 */
+} FLMoeLayer;
+/* y[n][E] = MoE(x[n][E]) on the context's stream (x, y device pointers; asynchronous). n <= 65536. */
+int fl_moe_layer(FLCtx *, const FLMoeLayer * L, const float * x, int n, float * y);
+/* router only: sel/w [n][topk] (device), logits/probs [n][n_exp] may be NULL */
+int fl_route_dev(FLCtx *, const float * gate_inp, const float * probs_b, const float * x, int n, int n_exp, int E,
+                 float * logits, float * probs, int * sel, float * w);
+/* dispatch only: counts [n_exp], offsets [n_exp+1], perm/inv [n*topk], act [n_exp], nact [1] (device) */
+int fl_dispatch_dev(FLCtx *, const int * sel, int n, int topk, int n_exp, int * counts, int * offsets, int * perm, int * inv, int * act, int * nact);
+/* Q8_K of nrows x K floats (device): q [nrows][K] int8, d [nrows][K/256] */
+int fl_quant_q8k_dev(FLCtx *, const float * x, int nrows, int K, int8_t * q, float * d);
+/* IQ2_XXS ggml layout <-> tiled layout for nmat matrices of R x K at byte strides (device, may not alias) */
+int fl_pack_iq2xxs(FLCtx *, const void * src_ggml, size_t src_stride, void * dst_tiled, size_t dst_stride, int R, int K, int nmat);
+int fl_unpack_iq2xxs(FLCtx *, const void * src_tiled, size_t src_stride, void * dst_ggml, size_t dst_stride, int R, int K, int nmat);
+/* RMSNorm (ggml semantics, eps) of n rows of D floats, w may be NULL (ones) -- the 58-layer chain's norm */
+int fl_rmsnorm_dev(FLCtx *, const float * x, const float * w, float * y, int n, int D, float eps);
+/* synthetic data on the device: IQ2_XXS matrices (qs uniform bytes, d = fp16(|N(0, sigma^2)|)) and normal floats */
+int fl_synth_iq2xxs(FLCtx *, void * dst, size_t dst_stride, int R, int K, int nmat, int layout, uint64_t seed, uint64_t mat0, float sigma);
+int fl_synth_normal(FLCtx *, float * dst, int64_t count, uint64_t seed, uint64_t stream, float mean, float sigma);
+/* which = 0: exp, 1: sigmoid, 2: silu under the library's exp contract (device arrays) */
+int fl_probe_exp(FLCtx *, const float * x, float * y, int64_t n, int which);
+
+/* internal buffers of the last fl_moe_layer (device pointers, valid until the next call that resizes them) */
+typedef struct FLDebug {
+    const int8_t * xq; const float * xd;             /* Q8_K of x */
+    const float * logits, * probs; const int * sel; const float * wts;
+    const int * counts, * offsets, * perm, * inv, * act, * nact;
+    const float * h; const int8_t * hq; const float * hd; /* [P+n][H]: per slot, shared rows at P.. */
+    const float * o;                                   /* [P+n][E] */
+    const float * g, * u;                              /* gate / up outputs when debug capture is on */
+    int n, P, topk;
+} FLDebug;
+int fl_debug(FLCtx *, FLDebug * out);
+int fl_set_debug(FLCtx *, int capture_gate_up);
+
+hipStream_t fl_stream(FLCtx *);
+/* run on the caller's stream from now on (NULL = HIP's default stream); work queued on the previous stream finishes first */
+int fl_set_stream(FLCtx *, hipStream_t s);
+/* device -> host copy on the context's stream, waited (tests read internal buffers with it) */
+int fl_d2h(FLCtx *, void * host, const void * dev, size_t bytes);
+int fl_sync(FLCtx *);
+const char * fl_last_error(FLCtx *);
+void fl_free(FLCtx *);
+
+#ifdef __cplusplus
+}
+#endif

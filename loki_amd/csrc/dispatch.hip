@@ -1,0 +1,79 @@
+// dispatch.hip -- on-device token -> expert dispatch: histogram, exclusive scan, stable permutation.
+//
+// The order is ggml mul_mat_id's row mapping, which the reference's wide pass builds on the host
+// (byexp at src/server_core_fused.cpp:937; slot tables at :945): for token t ascending and k ascending, pair
+// (t, k) = index t*topk + k is appended to its expert's list. perm lists the pairs expert by expert (ascending id),
+// each expert's pairs in that order; inv is perm's inverse (the slot of each pair); act lists the used experts
+// ascending. One workgroup of 1024 threads: an LDS histogram, a scan, then the pairs in rounds of 1024 where a
+// thread's rank among equal experts comes from wave ballots (8 bit-planes of the expert id) plus the counts of the
+// waves before it, so the result is the stable counting sort whatever the thread timing.
+#include "moe_common.h"
+#include "moe_kernels.h"
+
+namespace lk {
+
+constexpr int DWAVES = 16;
+
+__global__ void __launch_bounds__(1024) k_dispatch(const int * __restrict__ sel, int P, int n_exp, int * __restrict__ counts,
+                                                   int * __restrict__ offsets, int * __restrict__ perm, int * __restrict__ inv,
+                                                   int * __restrict__ act, int * __restrict__ nact) {
+    __shared__ int cnt[NEXP_MAX], base[NEXP_MAX];
+    __shared__ int wc[DWAVES][NEXP_MAX];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    for (int e = tid; e < NEXP_MAX; e += 1024) { cnt[e] = 0; }
+    __syncthreads();
+    for (int i = tid; i < P; i += 1024) {
+        const int e = sel[i];
+        if (e >= 0 && e < n_exp) { atomicAdd(&cnt[e], 1); }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int acc = 0, m = 0;
+        for (int e = 0; e < n_exp; ++e) {
+            base[e] = acc; offsets[e] = acc; counts[e] = cnt[e]; acc += cnt[e];
+            if (cnt[e] > 0) { act[m++] = e; }
+        }
+        offsets[n_exp] = acc; *nact = m;
+    }
+    __syncthreads();
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int r0 = 0; r0 < P; r0 += 1024) {
+        for (int j = tid; j < DWAVES * NEXP_MAX; j += 1024) { (&wc[0][0])[j] = 0; }
+        __syncthreads();
+        const int i = r0 + tid;
+        const int e = i < P ? sel[i] : -1;
+        const bool valid = e >= 0 && e < n_exp;
+        uint64_t match = __ballot(valid);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const bool bit = valid && ((e >> b) & 1);
+            const uint64_t ones = __ballot(bit);
+            match &= bit ? ones : ~ones;
+        }
+        const int rank = __popcll(match & below);
+        if (valid && rank == 0) { wc[wave][e] = __popcll(match); }
+        __syncthreads();
+        if (valid) {
+            int pre = 0;
+            for (int w = 0; w < wave; ++w) { pre += wc[w][e]; }
+            const int pos = base[e] + pre + rank;
+            perm[pos] = i; inv[i] = pos;
+        }
+        __syncthreads();
+        if (tid < n_exp) {
+            int s = 0;
+            for (int w = 0; w < DWAVES; ++w) { s += wc[w][tid]; }
+            base[tid] += s;
+        }
+        __syncthreads();
+    }
+}
+
+hipError_t launch_dispatch(const int * sel, int P, int n_exp, int * counts, int * offsets, int * perm, int * inv,
+                           int * act, int * nact, hipStream_t st) {
+    if (n_exp > NEXP_MAX || n_exp <= 0) { return hipErrorInvalidValue; }
+    k_dispatch<<<1, 1024, 0, st>>>(sel, P, n_exp, counts, offsets, perm, inv, act, nact);
+    return hipGetLastError();
+}
+
+}  // namespace lk

@@ -1,0 +1,267 @@
+// fused_layer.hip -- FLCtx and the C ABI of include/loki_moe.h (host side of the MoE block on MI355X).
+//
+// Reference host side: src/fused_layer.cu:391-620 (FLCtx, fl_init, fl_moe, fl_wide_*, fl_fetch, fl_gpu_ms). The
+// device-resident path fl_moe_layer runs the whole block on the context's stream with no host round-trip:
+//   Q8_K(x) -> router logits (fp64 contract) -> sigmoid / grouped top-k / weights -> dispatch (histogram, scan,
+//   stable permutation) -> gate+up mat-vecs with the SwiGLU epilogue -> Q8_K(h) -> down mat-vecs -> k-ordered combine.
+#include "moe_common.h"
+#include "moe_kernels.h"
+#include "../../include/loki_moe.h"
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+using namespace lk;
+
+namespace {
+
+template <class T> struct DBuf {
+    T * p = nullptr; size_t cap = 0;
+    hipError_t ensure(size_t want) {
+        if (want <= cap && p) { return hipSuccess; }
+        if (p) { (void) hipFree(p); p = nullptr; cap = 0; }
+        const size_t n = want > 0 ? want : 1;
+        hipError_t e = hipMalloc(reinterpret_cast<void **>(&p), n * sizeof(T));
+        if (e == hipSuccess) { cap = n; } else { p = nullptr; }
+        return e;
+    }
+    void release() { if (p) { (void) hipFree(p); } p = nullptr; cap = 0; }
+};
+
+[[noreturn]] void fatal(const char * what, hipError_t e, const char * file, int line) {
+    std::fprintf(stderr, "[fused] HIP error %s (%s) at %s:%d\n", hipGetErrorString(e), what, file, line);
+    std::exit(7);
+}
+#define CK(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) { fatal(#x, e_, __FILE__, __LINE__); } } while (0)
+
+}  // namespace
+
+struct FLCtx {
+    hipStream_t st = nullptr, own = nullptr; int dev = 0, ncu = 0;
+    hipEvent_t em0 = nullptr, em1 = nullptr;
+    int n_group = 8, topk_group = 4, topk = 8; float scale = 2.5f;
+    double ms_moe = 0.0;
+    std::string err;
+    int dbg_gu = 0;
+    DBuf<int8_t> xq, hq; DBuf<float> xd, logits, probs, wts, h, hd, o, g, u;
+    DBuf<int> sel, counts, offsets, perm, inv, act, nact;
+    int last_n = 0, last_P = 0;
+};
+
+static int fail(FLCtx * c, int code, const char * fmt, ...) {
+    char buf[512]; va_list ap; va_start(ap, fmt); std::vsnprintf(buf, sizeof buf, fmt, ap); va_end(ap);
+    if (c) { c->err = buf; }
+    return code;
+}
+#define TRY(c, x) do { hipError_t e_ = (x); if (e_ != hipSuccess) { return fail((c), FL_EHIP, "%s: %s", #x, hipGetErrorString(e_)); } } while (0)
+#define ALLOC(c, buf, n) do { if ((buf).ensure(n) != hipSuccess) { (void) hipGetLastError(); return fail((c), FL_ENOMEM, "device allocation of %zu elements failed", (size_t) (n)); } } while (0)
+
+[[noreturn]] static void out_of_scope(const char * fn) {
+    std::fprintf(stderr, "[fused] %s: attention, speculation and sketches are not part of the MoE-block library\n", fn);
+    std::exit(7);
+}
+
+// ================================================================ lifecycle
+extern "C" FLCtx * fl_init(int kvp, int sc_cap) {
+    (void) kvp; (void) sc_cap;
+    FLCtx * c = new FLCtx();
+    CK(hipGetDevice(&c->dev));
+    CK(hipDeviceGetAttribute(&c->ncu, hipDeviceAttributeMultiprocessorCount, c->dev));
+    CK(hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking)); c->st = c->own;
+    CK(hipEventCreate(&c->em0)); CK(hipEventCreate(&c->em1));
+    return c;
+}
+
+extern "C" void fl_free(FLCtx * c) {
+    if (!c) { return; }
+    (void) hipStreamSynchronize(c->st);
+    c->xq.release(); c->hq.release(); c->xd.release(); c->logits.release(); c->probs.release(); c->wts.release();
+    c->h.release(); c->hd.release(); c->o.release(); c->g.release(); c->u.release();
+    c->sel.release(); c->counts.release(); c->offsets.release(); c->perm.release(); c->inv.release(); c->act.release(); c->nact.release();
+    (void) hipEventDestroy(c->em0); (void) hipEventDestroy(c->em1); (void) hipStreamDestroy(c->own);
+    delete c;
+}
+
+extern "C" hipStream_t fl_stream(FLCtx * c) { return c ? c->st : nullptr; }
+extern "C" int fl_set_stream(FLCtx * c, hipStream_t s) {
+    if (!c) { return FL_EINVAL; }
+    TRY(c, hipStreamSynchronize(c->st));   // work already queued on the old stream finishes first
+    c->st = s; return FL_OK;
+}
+extern "C" int fl_d2h(FLCtx * c, void * host, const void * dev, size_t bytes) {
+    if (!c) { return FL_EINVAL; }
+    if (bytes == 0) { return FL_OK; }
+    if (!host || !dev) { return fail(c, FL_EINVAL, "null pointer"); }
+    TRY(c, hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, c->st));
+    TRY(c, hipStreamSynchronize(c->st));
+    return FL_OK;
+}
+extern "C" int fl_sync(FLCtx * c) { if (!c) { return FL_EINVAL; } TRY(c, hipStreamSynchronize(c->st)); return FL_OK; }
+extern "C" const char * fl_last_error(FLCtx * c) { return c ? c->err.c_str() : "null context"; }
+
+extern "C" int fl_set_routing(FLCtx * c, int n_group, int topk_group, int topk, float scale) {
+    if (!c) { return FL_EINVAL; }
+    if (n_group <= 0 || topk_group <= 0 || topk_group > n_group || topk <= 0 || topk > MAXK || !(scale > 0.f)) {
+        return fail(c, FL_EINVAL, "bad routing rule (n_group %d, topk_group %d, topk %d, scale %g)", n_group, topk_group, topk, (double) scale);
+    }
+    c->n_group = n_group; c->topk_group = topk_group; c->topk = topk; c->scale = scale; return FL_OK;
+}
+extern "C" int fl_set_debug(FLCtx * c, int capture) { if (!c) { return FL_EINVAL; } c->dbg_gu = capture ? 1 : 0; return FL_OK; }
+
+// ================================================================ building blocks
+static int check_rule(FLCtx * c, int n_exp) {
+    if (n_exp <= 0 || n_exp > NEXP_MAX) { return fail(c, FL_EINVAL, "n_exp %d outside 1..%d", n_exp, NEXP_MAX); }
+    if (n_exp % c->n_group) { return fail(c, FL_EINVAL, "n_exp %d not divisible by n_group %d", n_exp, c->n_group); }
+    const int per = n_exp / c->n_group;
+    if (per < 2 || c->topk > c->topk_group * per) { return fail(c, FL_EINVAL, "top-%d cannot be drawn from %d groups of %d", c->topk, c->topk_group, per); }
+    return FL_OK;
+}
+
+extern "C" int fl_route_dev(FLCtx * c, const float * W, const float * bias, const float * x, int n, int n_exp, int E,
+                            float * logits, float * probs, int * sel, float * w) {
+    if (!c) { return FL_EINVAL; }
+    if (n < 0 || n > 65536) { return fail(c, FL_ERANGE, "n = %d outside 0..65536", n); }
+    if (n == 0) { return FL_OK; }
+    if (!W || !bias || !x || !sel || !w) { return fail(c, FL_EINVAL, "null pointer"); }
+    if (E <= 0 || E % 256) { return fail(c, FL_EINVAL, "E = %d must be a positive multiple of 256", E); }
+    if (int rc = check_rule(c, n_exp)) { return rc; }
+    if (!logits) { ALLOC(c, c->logits, (size_t) n * n_exp); logits = c->logits.p; }
+    TRY(c, launch_router_logits(W, x, n, n_exp, E, logits, c->st));
+    TRY(c, launch_router_select(logits, bias, n, n_exp, c->n_group, c->topk_group, c->topk, c->scale, probs, sel, w, c->st));
+    return FL_OK;
+}
+
+extern "C" int fl_dispatch_dev(FLCtx * c, const int * sel, int n, int topk, int n_exp, int * counts, int * offsets, int * perm, int * inv, int * act, int * nact) {
+    if (!c) { return FL_EINVAL; }
+    if (n < 0 || topk <= 0 || topk > MAXK || (int64_t) n * topk > (1 << 24)) { return fail(c, FL_ERANGE, "n*topk out of range"); }
+    if (n_exp <= 0 || n_exp > NEXP_MAX) { return fail(c, FL_EINVAL, "n_exp %d outside 1..%d", n_exp, NEXP_MAX); }
+    if (!sel || !counts || !offsets || !perm || !inv || !act || !nact) { return fail(c, FL_EINVAL, "null pointer"); }
+    TRY(c, launch_dispatch(sel, n * topk, n_exp, counts, offsets, perm, inv, act, nact, c->st));
+    return FL_OK;
+}
+
+extern "C" int fl_quant_q8k_dev(FLCtx * c, const float * x, int nrows, int K, int8_t * q, float * d) {
+    if (!c) { return FL_EINVAL; }
+    if (nrows < 0 || K <= 0 || K % 256) { return fail(c, FL_EINVAL, "K = %d must be a positive multiple of 256", K); }
+    if (nrows == 0) { return FL_OK; }
+    if (!x || !q || !d) { return fail(c, FL_EINVAL, "null pointer"); }
+    TRY(c, launch_quant_q8k(x, nrows, K, q, d, c->st));
+    return FL_OK;
+}
+
+static int pack_args(FLCtx * c, const void * s, const void * d, int R, int K, int nmat) {
+    if (!s || !d) { return fail(c, FL_EINVAL, "null pointer"); }
+    if (R <= 0 || R % 4 || K <= 0 || K % 1024 || nmat <= 0) { return fail(c, FL_EINVAL, "tiled layout needs R %% 4 == 0 and K %% 1024 == 0 (R %d, K %d)", R, K); }
+    return FL_OK;
+}
+extern "C" int fl_pack_iq2xxs(FLCtx * c, const void * src, size_t ss, void * dst, size_t ds, int R, int K, int nmat) {
+    if (!c) { return FL_EINVAL; }
+    if (int rc = pack_args(c, src, dst, R, K, nmat)) { return rc; }
+    TRY(c, launch_pack_tiled((const uint8_t *) src, ss, (uint8_t *) dst, ds, R, K, nmat, c->st));
+    return FL_OK;
+}
+extern "C" int fl_unpack_iq2xxs(FLCtx * c, const void * src, size_t ss, void * dst, size_t ds, int R, int K, int nmat) {
+    if (!c) { return FL_EINVAL; }
+    if (int rc = pack_args(c, src, dst, R, K, nmat)) { return rc; }
+    TRY(c, launch_unpack_tiled((const uint8_t *) src, ss, (uint8_t *) dst, ds, R, K, nmat, c->st));
+    return FL_OK;
+}
+extern "C" int fl_rmsnorm_dev(FLCtx * c, const float * x, const float * w, float * y, int n, int D, float eps) {
+    if (!c) { return FL_EINVAL; }
+    if (n < 0 || D <= 0) { return fail(c, FL_EINVAL, "bad shape"); }
+    if (n > 0 && (!x || !y)) { return fail(c, FL_EINVAL, "null pointer"); }
+    TRY(c, launch_rmsnorm(x, w, y, n, D, eps, c->st));
+    return FL_OK;
+}
+extern "C" int fl_synth_iq2xxs(FLCtx * c, void * dst, size_t ds, int R, int K, int nmat, int layout, uint64_t seed, uint64_t mat0, float sigma) {
+    if (!c) { return FL_EINVAL; }
+    if (int rc = pack_args(c, dst, dst, R, K, nmat)) { return rc; }
+    if (layout != FL_LAYOUT_GGML && layout != FL_LAYOUT_TILED) { return fail(c, FL_EINVAL, "unknown layout %d", layout); }
+    TRY(c, launch_synth_iq2((uint8_t *) dst, ds, R, K, nmat, layout, seed, mat0, sigma, c->st));
+    return FL_OK;
+}
+extern "C" int fl_synth_normal(FLCtx * c, float * dst, int64_t count, uint64_t seed, uint64_t stream, float mean, float sigma) {
+    if (!c) { return FL_EINVAL; }
+    if (count < 0 || (count > 0 && !dst)) { return fail(c, FL_EINVAL, "bad destination"); }
+    TRY(c, launch_synth_normal(dst, count, seed, stream, mean, sigma, c->st));
+    return FL_OK;
+}
+extern "C" int fl_probe_exp(FLCtx * c, const float * x, float * y, int64_t n, int which) {
+    if (!c) { return FL_EINVAL; }
+    if (n < 0 || which < 0 || which > 2 || (n > 0 && (!x || !y))) { return fail(c, FL_EINVAL, "bad probe arguments"); }
+    TRY(c, launch_expf_probe(x, y, n, which, c->st));
+    return FL_OK;
+}
+
+// ================================================================ the device-resident block
+extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, float * y) {
+    if (!c) { return FL_EINVAL; }
+    if (!L) { return fail(c, FL_EINVAL, "null layer"); }
+    if (n < 0 || n > 65536) { return fail(c, FL_ERANGE, "n = %d outside 0..65536", n); }
+    if (L->layout != FL_LAYOUT_TILED) { return fail(c, FL_EINVAL, "fl_moe_layer reads the tiled layout; convert with fl_pack_iq2xxs"); }
+    if (L->E <= 0 || L->E % 1024 || L->H <= 0 || L->H % 1024) { return fail(c, FL_EINVAL, "E %d and H %d must be positive multiples of 1024", L->E, L->H); }
+    if (int rc = check_rule(c, L->n_exp)) { return rc; }
+    if (n == 0) { return FL_OK; }
+    if (!x || !y || !L->gate_inp || !L->probs_b || !L->gate_exps || !L->up_exps || !L->down_exps || !L->sh_gate || !L->sh_up || !L->sh_down) {
+        return fail(c, FL_EINVAL, "null pointer in the layer or x / y");
+    }
+    const int E = L->E, H = L->H, ne = L->n_exp, tk = c->topk, P = n * tk;
+    const size_t rows = (size_t) P + n;
+    ALLOC(c, c->xq, (size_t) n * E); ALLOC(c, c->xd, (size_t) n * (E / 256));
+    ALLOC(c, c->logits, (size_t) n * ne); ALLOC(c, c->probs, (size_t) n * ne);
+    ALLOC(c, c->sel, P); ALLOC(c, c->wts, P); ALLOC(c, c->perm, P); ALLOC(c, c->inv, P);
+    ALLOC(c, c->counts, ne); ALLOC(c, c->offsets, ne + 1); ALLOC(c, c->act, ne); ALLOC(c, c->nact, 1);
+    ALLOC(c, c->h, rows * H); ALLOC(c, c->hq, rows * H); ALLOC(c, c->hd, rows * (H / 256)); ALLOC(c, c->o, rows * E);
+    if (c->dbg_gu) { ALLOC(c, c->g, rows * H); ALLOC(c, c->u, rows * H); }
+    c->last_n = n; c->last_P = P;
+    hipStream_t st = c->st;
+    TRY(c, hipEventRecord(c->em0, st));
+    TRY(c, launch_quant_q8k(x, n, E, c->xq.p, c->xd.p, st));
+    TRY(c, launch_router_logits(L->gate_inp, x, n, ne, E, c->logits.p, st));
+    TRY(c, launch_router_select(c->logits.p, L->probs_b, n, ne, c->n_group, c->topk_group, tk, c->scale, c->probs.p, c->sel.p, c->wts.p, st));
+    TRY(c, launch_dispatch(c->sel.p, P, ne, c->counts.p, c->offsets.p, c->perm.p, c->inv.p, c->act.p, c->nact.p, st));
+    GemvArgs a{};
+    a.w0 = (const uint8_t *) L->gate_exps; a.w1 = (const uint8_t *) L->up_exps; a.estride = (size_t) H * (E / 256) * IQ2B;
+    a.sh0 = (const uint8_t *) L->sh_gate; a.sh1 = (const uint8_t *) L->sh_up;
+    a.aq = c->xq.p; a.ad = c->xd.p; a.K = E; a.R = H;
+    a.act = c->act.p; a.nact = c->nact.p; a.offsets = c->offsets.p; a.perm = c->perm.p;
+    a.topk = tk; a.n = n; a.P = P; a.max_act = std::min(ne, P);
+    a.out = c->h.p; a.dbg0 = c->dbg_gu ? c->g.p : nullptr; a.dbg1 = c->dbg_gu ? c->u.p : nullptr;
+    TRY(c, launch_gemv_gateup(a, st));
+    TRY(c, launch_quant_q8k(c->h.p, (int64_t) rows, H, c->hq.p, c->hd.p, st));
+    GemvArgs d = a;
+    d.w0 = (const uint8_t *) L->down_exps; d.w1 = nullptr; d.estride = (size_t) E * (H / 256) * IQ2B;
+    d.sh0 = (const uint8_t *) L->sh_down; d.sh1 = nullptr; d.aq = c->hq.p; d.ad = c->hd.p; d.K = H; d.R = E;
+    d.out = c->o.p; d.dbg0 = nullptr; d.dbg1 = nullptr;
+    TRY(c, launch_gemv_down(d, st));
+    TRY(c, launch_combine(c->o.p, c->inv.p, c->wts.p, n, tk, E, P, nullptr, y, nullptr, st));
+    TRY(c, hipEventRecord(c->em1, st));
+    return FL_OK;
+}
+
+extern "C" int fl_debug(FLCtx * c, FLDebug * out) {
+    if (!c || !out) { return FL_EINVAL; }
+    std::memset(out, 0, sizeof(FLDebug));
+    out->xq = c->xq.p; out->xd = c->xd.p; out->logits = c->logits.p; out->probs = c->probs.p; out->sel = c->sel.p; out->wts = c->wts.p;
+    out->counts = c->counts.p; out->offsets = c->offsets.p; out->perm = c->perm.p; out->inv = c->inv.p; out->act = c->act.p; out->nact = c->nact.p;
+    out->h = c->h.p; out->hq = c->hq.p; out->hd = c->hd.p; out->o = c->o.p; out->g = c->dbg_gu ? c->g.p : nullptr; out->u = c->dbg_gu ? c->u.p : nullptr;
+    out->n = c->last_n; out->P = c->last_P; out->topk = c->topk;
+    return FL_OK;
+}
+
+// ================================================================ reference entry points
+extern "C" void fl_attn(FLCtx *, const FLW *, int, int, const int *, void *, void *, const float *, int, int, int) { out_of_scope("fl_attn"); }
+extern "C" void fl_spec(FLCtx *, const FLW *, void *, void *) { out_of_scope("fl_spec"); }
+extern "C" void fl_sketch(FLCtx *, const float *, const void *, int) { out_of_scope("fl_sketch"); }
+
+extern "C" void fl_h2d(FLCtx * c, void * dst, const void * src, size_t bytes) {
+    if (bytes == 0) { return; }
+    CK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->st));
+}
+extern "C" void fl_wait_event(FLCtx * c, hipEvent_t ev) { CK(hipStreamWaitEvent(c->st, ev, 0)); }
+extern "C" double fl_gpu_ms(FLCtx * c, int which) { return which == 1 ? c->ms_moe : 0.0; }

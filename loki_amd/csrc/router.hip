@@ -1,0 +1,137 @@
+// router.hip -- the DeepSeek-V3/R1 grouped sigmoid router on the device (no host round-trip).
+//
+// Reference: router_probs / router_topk (src/fused_layer.cu:313-332, launched at :506) and the ggml graph
+// (src/server_core_fused.cpp:646-650) compute p = sigmoid(W x), take the top-8 of p + bias with ties to the lower index,
+// and weight w_k = p[sel_k] / max(sum p[sel], 2^-14) * 2.5. This build adds the grouped rule the task names (8 groups of
+// 32 experts; a group's score is the sum of its two best biased scores; the top-4 groups stay eligible), which reduces
+// to the reference's rule with n_group = topk_group = 1.
+//
+// Logit contract (shared bit for bit with the CPU checker): K is cut into 64 chunks of K/64; each chunk is summed in
+// order in fp64 from exact fp32 x fp32 products, the 64 chunk sums are added in order in fp64, and the total is rounded
+// once to fp32. The sigmoid uses the fp64 exp contract of moe_common.h. Selection and weights are plain fp32 compares,
+// adds and one correctly rounded division, so sel and wts are bit-identical to the checker's.
+#include "moe_common.h"
+#include "moe_kernels.h"
+
+namespace lk {
+
+constexpr int RT = 8;   // tokens per router wave
+
+// one wave per (expert, 8-token tile): lane c owns chunk c for all 8 tokens, so W is read once per tile
+__global__ void __launch_bounds__(64) k_router_logits(const float * __restrict__ W, const float * __restrict__ x, int n, int n_exp, int K,
+                                                      float * __restrict__ logits) {
+    __shared__ double S[RT][64];
+    const int e = blockIdx.x, t0 = blockIdx.y * RT, lane = threadIdx.x, L = K / 64;
+    const int nt = min(RT, n - t0);
+    const float4 * w4 = reinterpret_cast<const float4 *>(W + (size_t) e * K + (size_t) lane * L);
+    double s[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) { s[t] = 0.0; }
+    for (int i = 0; i < L / 4; ++i) {
+        const float4 wv = w4[i];
+        const double w0 = wv.x, w1 = wv.y, w2 = wv.z, w3 = wv.w;
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            if (t < nt) {
+                const float4 xv = reinterpret_cast<const float4 *>(x + (size_t) (t0 + t) * K + (size_t) lane * L)[i];
+                s[t] += (double) xv.x * w0; s[t] += (double) xv.y * w1; s[t] += (double) xv.z * w2; s[t] += (double) xv.w * w3;
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < RT; ++t) { S[t][lane] = s[t]; }
+    __syncthreads();
+    if (lane < nt) {
+        double tot = S[lane][0];
+        for (int c = 1; c < 64; ++c) { tot += S[lane][c]; }
+        logits[(size_t) (t0 + lane) * n_exp + e] = (float) tot;
+    }
+}
+
+hipError_t launch_router_logits(const float * W, const float * x, int n, int n_exp, int K, float * logits, hipStream_t st) {
+    if (n <= 0) { return hipSuccess; }
+    if (K % 256 != 0) { return hipErrorInvalidValue; }
+    k_router_logits<<<dim3(n_exp, (n + RT - 1) / RT), 64, 0, st>>>(W, x, n, n_exp, K, logits);
+    return hipGetLastError();
+}
+
+struct Cand { float v; int i; };
+__device__ __forceinline__ bool better(float av, int ai, float bv, int bi) {   // valid entries have i >= 0
+    if (ai < 0) { return false; }
+    if (bi < 0) { return true; }
+    return av > bv || (av == bv && ai < bi);
+}
+
+// one wave per token; lane l holds experts 4l..4l+3 (n_exp <= 256)
+__global__ void __launch_bounds__(64) k_router_select(const float * __restrict__ logits, const float * __restrict__ bias, int n, int n_exp,
+                                                      int n_group, int topk_group, int topk, float scale,
+                                                      float * __restrict__ probs, int * __restrict__ sel, float * __restrict__ wts) {
+#pragma clang fp contract(off)
+    __shared__ float cs[NEXP_MAX], ps[NEXP_MAX], gsc[NEXP_MAX];
+    __shared__ int allow_g[NEXP_MAX], picked[MAXK];
+    const int t = blockIdx.x, lane = threadIdx.x, per = n_exp / n_group;
+    for (int e = lane; e < n_exp; e += 64) {
+        const float p = det_sigmoid(logits[(size_t) t * n_exp + e]);
+        ps[e] = p; cs[e] = p + bias[e];
+        if (probs) { probs[(size_t) t * n_exp + e] = p; }
+    }
+    __syncthreads();
+    // group scores: top1 + top2 of the group's biased scores
+    for (int g = lane; g < n_group; g += 64) {
+        float v1 = 0.f, v2 = 0.f; int i1 = -1, i2 = -1;
+        for (int e = g * per; e < (g + 1) * per; ++e) {
+            const float c = cs[e];
+            if (i1 < 0 || c > v1) { v2 = v1; i2 = i1; v1 = c; i1 = e; }
+            else if (i2 < 0 || c > v2) { v2 = c; i2 = e; }
+        }
+        gsc[g] = v1 + v2;
+    }
+    __syncthreads();
+    for (int g = lane; g < n_group; g += 64) {   // a group stays eligible if fewer than topk_group groups beat it
+        int rank = 0; const float mine = gsc[g];
+        for (int h = 0; h < n_group; ++h) { const float o = gsc[h]; rank += (o > mine || (o == mine && h < g)) ? 1 : 0; }
+        allow_g[g] = rank < topk_group;
+    }
+    __syncthreads();
+    unsigned taken = 0;   // bit j: expert 4*lane+j already selected
+    for (int r = 0; r < topk; ++r) {
+        float bv = 0.f; int bi = -1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = 4 * lane + j;
+            if (e < n_exp && !((taken >> j) & 1u) && allow_g[e / per]) {
+                const float c = cs[e];
+                if (better(c, e, bv, bi)) { bv = c; bi = e; }
+            }
+        }
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float ov = __shfl_xor(bv, off); const int oi = __shfl_xor(bi, off);
+            if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+        }
+        if (bi >= 0 && (bi >> 2) == lane) { taken |= 1u << (bi & 3); }
+        if (lane == 0) { picked[r] = bi; }
+    }
+    __syncthreads();
+    if (lane == 0) {
+        float sum = 0.f;
+        for (int r = 0; r < topk; ++r) { sum += ps[picked[r]]; }
+        sum = sum > 6.103515625e-5f ? sum : 6.103515625e-5f;
+        for (int r = 0; r < topk; ++r) {
+            sel[(size_t) t * topk + r] = picked[r];
+            wts[(size_t) t * topk + r] = ps[picked[r]] / sum * scale;
+        }
+    }
+}
+
+hipError_t launch_router_select(const float * logits, const float * bias, int n, int n_exp, int n_group, int topk_group,
+                                int topk, float scale, float * probs, int * sel, float * wts, hipStream_t st) {
+    if (n <= 0) { return hipSuccess; }
+    if (n_exp > NEXP_MAX || n_exp % n_group || topk > MAXK || topk_group > n_group || topk > topk_group * (n_exp / n_group) || n_exp / n_group < 2) {
+        return hipErrorInvalidValue;
+    }
+    k_router_select<<<n, 64, 0, st>>>(logits, bias, n, n_exp, n_group, topk_group, topk, scale, probs, sel, wts);
+    return hipGetLastError();
+}
+
+}  // namespace lk

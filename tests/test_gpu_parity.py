@@ -1,0 +1,158 @@
+"""GPU parity: every stage of the HIP MoE block against the CPU checker (oracle/), through the C ABI.
+
+The kernels reproduce the checker's arithmetic contract, so most comparisons are bit-exact: Q8_K, router logits,
+probabilities, selections, weights, dispatch, gate/up/h, down outputs and the block output. The task's tolerance
+(max relative 1e-2, L2 relative 2e-3) is asserted as well for the block output.
+"""
+import numpy as np
+import pytest
+
+from tests._helpers import E, H, NEXP, host_layer, make_layer, make_x, numpy_pack_tiled, rel_errors, iq2_bytes
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+MAX_REL, L2_REL = 1e-2, 2e-3   # the task's output tolerance
+
+
+@pytest.fixture(scope="module")
+def layer(ctx):
+    return make_layer(ctx, seed=1234)
+
+
+def test_exp_contract_bitwise(ctx):
+    import torch
+    rng = np.random.default_rng(0)
+    xs = np.concatenate([rng.normal(0, 3, 20000), rng.uniform(-120, 100, 5000), [0.0, -0.0, 1e-30, -1e-30, 88.7, 89.0, -103.9, -104.0, -150.0, 200.0]]).astype(np.float32)
+    x = torch.from_numpy(xs).cuda()
+    for which, ref in ((0, orc.expf), (1, orc.sigmoid), (2, orc.silu)):
+        y = ctx.probe_exp(x, which); ctx.sync()
+        got = y.cpu().numpy()
+        want = ref(xs)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), "exp contract mismatch (probe %d)" % which
+
+
+def test_q8k_bitwise(ctx):
+    import torch
+    rng = np.random.default_rng(1)
+    x = rng.normal(0, 1, (6, 2 * E)).astype(np.float32)
+    x[0, :256] = 0.0                                    # zero block -> d = 0, q = 0
+    x[1, :256] = 0.25; x[1, 7] = -3.0; x[1, 9] = 3.0    # first occurrence of max |x| is negative
+    mid = np.zeros(256, np.float32); mid[0] = -127.0    # iscale = 1: exact half-way products round to even
+    mid[1:9] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -126.5]
+    x[2, 256:512] = mid
+    x[3, :] *= 1e-30                                    # tiny magnitudes
+    x[4, 512:768] = 7.0                                 # all equal
+    q, d = ctx.quant_q8k(torch.from_numpy(x).cuda()); ctx.sync()
+    qo, do, _ = orc.quantize_q8k(x)
+    assert np.array_equal(q.cpu().numpy(), qo)
+    assert np.array_equal(d.cpu().numpy().view(np.uint32), do.view(np.uint32))
+
+
+def test_pack_layout(ctx):
+    import torch
+    rows, cols = 64, 2048
+    g = torch.empty(iq2_bytes(rows, cols), dtype=torch.uint8, device="cuda")
+    ctx.synth_iq2(g, rows, cols, 1, 0, seed=7, mat0=3)
+    t = ctx.pack(g, rows, cols, 1)
+    back = ctx.unpack(t, rows, cols, 1); ctx.sync()
+    gh = g.cpu().numpy()
+    assert np.array_equal(t.cpu().numpy(), numpy_pack_tiled(gh, rows, cols))
+    assert np.array_equal(back.cpu().numpy(), gh)
+    # the generator writes the same block contents in either layout
+    t2 = torch.empty_like(g)
+    ctx.synth_iq2(t2, rows, cols, 1, 1, seed=7, mat0=3); ctx.sync()
+    assert np.array_equal(t2.cpu().numpy(), t.cpu().numpy())
+
+
+@pytest.mark.parametrize("n,rule", [(1, (8, 4)), (8, (8, 4)), (64, (8, 4)), (8, (1, 1))])
+def test_router_bitwise(ctx, layer, n, rule):
+    x = make_x(ctx, n, seed=10 + n)
+    ctx.set_routing(rule[0], rule[1], 8, 2.5)
+    try:
+        logits, probs, sel, w = ctx.route(layer.gate_inp, layer.probs_b, x)
+        ctx.sync()
+    finally:
+        ctx.set_routing()
+    W, b = layer.gate_inp.cpu().numpy(), layer.probs_b.cpu().numpy()
+    lo, po, so, wo = orc.router(W, b, x.cpu().numpy(), rule[0], rule[1], 8, 2.5)
+    assert np.array_equal(logits.cpu().numpy().view(np.uint32), lo.view(np.uint32))
+    assert np.array_equal(probs.cpu().numpy().view(np.uint32), po.view(np.uint32))
+    assert np.array_equal(sel.cpu().numpy(), so)
+    assert np.array_equal(w.cpu().numpy().view(np.uint32), wo.view(np.uint32))
+
+
+@pytest.mark.parametrize("n,skew", [(1, 0), (8, 0), (512, 0), (2048, 1), (2048, 2)])
+def test_dispatch_bitwise(ctx, n, skew):
+    import torch
+    rng = np.random.default_rng(n + 17 * skew)
+    if skew == 0:
+        sel = np.stack([rng.choice(NEXP, 8, replace=False) for _ in range(n)]).astype(np.int32)
+    elif skew == 1:   # a few hot experts in almost every row
+        hot = rng.choice(NEXP, 16, replace=False)
+        sel = np.stack([np.concatenate([rng.choice(hot, 4, replace=False), rng.choice(np.setdiff1d(np.arange(NEXP), hot), 4, replace=False)]) for _ in range(n)]).astype(np.int32)
+    else:             # every row the same 8 experts
+        sel = np.tile(np.arange(8, dtype=np.int32) * 31, (n, 1))
+    counts, offsets, perm, inv, act, nact = ctx.dispatch(torch.from_numpy(sel).cuda())
+    ctx.sync()
+    co, oo, po = orc.dispatch(sel)
+    assert np.array_equal(counts.cpu().numpy(), co)
+    assert np.array_equal(offsets.cpu().numpy(), oo)
+    assert np.array_equal(perm.cpu().numpy(), po)
+    invo = np.empty_like(po); invo[po] = np.arange(po.size, dtype=np.int32)
+    assert np.array_equal(inv.cpu().numpy(), invo)
+    used = np.nonzero(co)[0]
+    assert int(nact.cpu().numpy()[0]) == used.size
+    assert np.array_equal(act.cpu().numpy()[:used.size], used)
+
+
+def _block_vs_oracle(ctx, layer, x, tokens, capture=True):
+    """Run the device block on all rows of x, compare the rows `tokens` (independent per token) with the checker."""
+    ctx.set_debug(capture)
+    y = ctx.moe_layer(layer, x)
+    ctx.sync()
+    dbg = ctx.debug()
+    ctx.set_debug(False)
+    xs = x.cpu().numpy()[tokens]
+    W, b = layer.gate_inp.cpu().numpy(), layer.probs_b.cpu().numpy()
+    _, _, so, _ = orc.router(W, b, xs)
+    _, _, gate, up, down, sh = host_layer(ctx, layer, so.ravel())
+    ref = orc.moe_forward(xs, W, b, gate, up, down, *sh, want=("g", "u", "o", "sh"))
+    return y.cpu().numpy()[tokens], ref, dbg
+
+
+@pytest.mark.parametrize("n", [1, 8])
+def test_block_decode_bitwise(ctx, layer, n):
+    x = make_x(ctx, n, seed=200 + n)
+    tokens = np.arange(n)
+    y, ref, dbg = _block_vs_oracle(ctx, layer, x, tokens)
+    mx, l2 = rel_errors(y, ref["y"])
+    assert mx <= MAX_REL and l2 <= L2_REL, (mx, l2)
+    # intermediates per (token, k) pair: the device keeps them per dispatch slot, inv maps pair -> slot
+    P = n * 8
+    inv = ctx.d2h(dbg.inv, (P,), np.int32)
+    g = ctx.d2h(dbg.g, (P + n, H), np.float32); u = ctx.d2h(dbg.u, (P + n, H), np.float32)
+    o = ctx.d2h(dbg.o, (P + n, E), np.float32)
+    assert np.array_equal(g[inv].view(np.uint32), ref["g"].view(np.uint32))
+    assert np.array_equal(u[inv].view(np.uint32), ref["u"].view(np.uint32))
+    assert np.array_equal(o[inv].view(np.uint32), ref["o"].view(np.uint32))
+    assert np.array_equal(o[P:].view(np.uint32), ref["sh"].view(np.uint32))
+    assert np.array_equal(y.view(np.uint32), ref["y"].view(np.uint32)), "block output not bit-identical (max rel %.3g)" % mx
+
+
+def test_block_prefill512_rows(ctx):
+    layer = make_layer(ctx, seed=4321, bias_sigma=0.05)
+    x = make_x(ctx, 512, seed=512)
+    tokens = np.array([0, 1, 77, 255, 256, 400, 510, 511])
+    y, ref, _ = _block_vs_oracle(ctx, layer, x, tokens, capture=False)
+    mx, l2 = rel_errors(y, ref["y"])
+    assert mx <= MAX_REL and l2 <= L2_REL, (mx, l2)
+    assert np.array_equal(y.view(np.uint32), ref["y"].view(np.uint32)), "prefill rows not bit-identical (max rel %.3g)" % mx
+
+
+def test_block_deterministic(ctx, layer):
+    x = make_x(ctx, 8, seed=99)
+    y1 = ctx.moe_layer(layer, x).clone()
+    y2 = ctx.moe_layer(layer, x)
+    ctx.sync()
+    assert np.array_equal(y1.cpu().numpy().view(np.uint32), y2.cpu().numpy().view(np.uint32))
