@@ -1,0 +1,214 @@
+#!/usr/bin/env python3
+"""bench.py -- one DeepSeek-R1 MoE layer (loki's fused_layer MoE block) on one MI355X.
+
+Default workload (the BASELINE metric's decode config): one MoE layer decoding a batch of 8 tokens:
+x [8, 7168] ~ N(0,1), fp32 router [256, 7168] ~ N(0, 0.02^2), bias ~ N(0, 0.01^2), grouped sigmoid routing
+(8 groups, top-4 groups, top-8, x2.5), 256 routed + 1 shared IQ2_XXS experts (gate/up [2048, 7168], down [7168, 2048],
+qs uniform bytes, d = fp16(|N(0, 0.002^2)|)). All inputs are generated on the device and resident in HBM before the
+timed region. Each step takes a fresh x (so different experts) and the steps rotate over --copies independently seeded
+layers (3 x 2.9 GB), so the 256 MB MALL cannot serve repeated weights.
+
+Prints ONE JSON line: value = microseconds per token of the whole block (router, dispatch, experts, combine), plus the
+achieved HBM bandwidth, the roofline of the dominant kernel (gate/up mat-vec, timed live with HIP events on the stream
+it runs on) and the CPU checker timed on this host's cores on a bounded sample of the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, published
+INT8_PEAK_TOPS = 5000.0         # MI355X dense int8 MFMA, published
+MAT_BYTES = 2048 * (7168 // 256) * 66   # one IQ2_XXS expert matrix: 3,784,704 B
+EXPERT_BYTES = 3 * MAT_BYTES            # 11,354,112 B
+ROUTER_BYTES = 256 * 7168 * 4 + 256 * 4  # router W + bias
+E, H = 7168, 2048
+
+WORKLOADS = {
+    # name: (tokens, bias sigma, hot experts, description)
+    "decode1": (1, 0.01, 0, "decode-1: one MoE layer, 1 token"),
+    "decode8": (8, 0.01, 0, "decode-8: one MoE layer, batch of 8 tokens"),
+    "prefill512": (512, 0.05, 0, "prefill-512: one MoE layer, 512 tokens"),
+    "prefill2048": (2048, 0.05, 16, "prefill-2048: one MoE layer, 2048 tokens, 16 hot experts (+0.5 bias)"),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def step_bytes(n, U):
+    """Algorithmic HBM bytes of one block call: every used expert (and the shared one) read once, the router once,
+    x read and y written once (SURVEY 8(d) formula)."""
+    return (U + 1) * EXPERT_BYTES + ROUTER_BYTES + 2 * n * E * 4
+
+
+def gateup_bytes(n, U, topk=8):
+    """Algorithmic bytes of one gate/up launch: gate+up of every used expert and the shared one, Q8_K x, h written."""
+    P = n * topk
+    return 2 * (U + 1) * MAT_BYTES + n * (E + E // 256 * 4) + (P + n) * H * 4
+
+
+def distinct_experts(ctx, layer, xs):
+    """Number of distinct routed experts per x (routing recomputed outside the timed region)."""
+    out = []
+    for x in xs:
+        _, _, sel, _ = ctx.route(layer.gate_inp, layer.probs_b, x)
+        out.append(int(sel.unique().numel()))
+    return out
+
+
+def run_workload(ctx, torch, name, steps, warmup, copies, seed=20260101):
+    from loki_amd import MoeLayerWeights
+    n, bias_sigma, nhot, desc = WORKLOADS[name]
+    layers = []
+    for c in range(copies):
+        hot = None
+        if nhot:
+            g = torch.Generator().manual_seed(seed + 7 * c)
+            hot = torch.randperm(256, generator=g)[:nhot].tolist()
+        layers.append(MoeLayerWeights.synthetic(ctx, seed + 1000 * c, bias_sigma=bias_sigma, hot=hot))
+    nx = steps + warmup
+    xs = []
+    for i in range(nx):
+        x = torch.empty((n, E), dtype=torch.float32, device="cuda")
+        ctx.synth_normal(x, seed + 17, 1000 + i, 0.0, 1.0)
+        xs.append(x)
+    y = torch.empty((n, E), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    for i in range(warmup):
+        ctx.moe_layer(layers[i % copies], xs[i], y)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        ctx.moe_layer(layers[(warmup + i) % copies], xs[warmup + i], y)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    # same steps again with per-stage HIP events (stage durations for the roofline; not used for `value`)
+    ctx.stage_ms(reset=True)
+    ctx.set_profile(True)
+    for i in range(steps):
+        ctx.moe_layer(layers[(warmup + i) % copies], xs[warmup + i], y)
+    ctx.set_profile(False)
+    calls, stage = ctx.stage_ms(reset=True)
+    stage = {k: v / max(calls, 1) for k, v in stage.items()}
+    U = [distinct_experts(ctx, layers[(warmup + i) % copies], [xs[warmup + i]])[0] for i in range(steps)]
+    mean_U = sum(U) / len(U)
+    res = dict(name=name, desc=desc, n=n, ms=ms, U=mean_U, stage_ms=stage,
+               bytes=sum(step_bytes(n, u) for u in U) / len(U),
+               gu_bytes=sum(gateup_bytes(n, u) for u in U) / len(U))
+    res["gbs"] = res["bytes"] / (ms * 1e-3) / 1e9
+    res["layers"], res["xs"] = layers, xs
+    return res
+
+
+def cpu_baseline(ctx, torch, res, budget_s=12.0, max_steps=8):
+    """The CPU checker (oracle/, restated ggml CPU semantics) on this host's cores, on a bounded sample of the same
+    workload: the first steps' x with the experts they select, timed around the oracle call only."""
+    import numpy as np
+    from oracle import oracle as orc
+    from tests._helpers import host_layer
+    threads = min(16, os.cpu_count() or 1)
+    layers, xs, n = res["layers"], res["xs"], res["n"]
+    tot_s, toks, nsteps = 0.0, 0, 0
+    for i in range(min(max_steps, len(xs))):
+        layer = layers[i % len(layers)]
+        x = xs[i].cpu().numpy()
+        W, b = layer.gate_inp.cpu().numpy(), layer.probs_b.cpu().numpy()
+        _, _, sel, _ = orc.router(W, b, x)
+        _, _, gate, up, down, sh = host_layer(ctx, layer, sel.ravel())
+        t0 = time.perf_counter()
+        orc.moe_forward(x, W, b, gate, up, down, *sh, nthreads=threads)
+        tot_s += time.perf_counter() - t0
+        toks += n; nsteps += 1
+        if tot_s >= budget_s:
+            break
+    return {"value": round(tot_s / toks * 1e6, 1), "unit": "us/token", "cores": threads, "kind": "port",
+            "sample": "%d %s step(s) (%d tokens) through oracle/moe_oracle.c (restated ggml CPU semantics: Q8_K, "
+                      "vec_dot_iq2_xxs_q8_K, grouped router, swiglu, k-ordered combine), OpenMP %d threads, "
+                      "same x and weights as the GPU steps" % (nsteps, res["name"], toks, threads)}
+
+
+def load_traffic(kernel, workload):
+    """HBM bytes per launch from committed rocprofv3 --pmc summaries (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)."""
+    p = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_%s_%s.json" % (kernel, workload))
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f).get("bytes_per_launch")
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="decode8", choices=sorted(WORKLOADS))
+    ap.add_argument("--copies", type=int, default=3, help="independently seeded layers rotated over the steps")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="skip the decode-1 / prefill-512 side measurements")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        log("bench.py: this build runs on one GPU only (the MoE block is not sharded here; see DESIGN.md for how it "
+            "would shard); got --gpus %d, WORLD_SIZE %d" % (args.gpus, world))
+        sys.exit(2)
+    import torch
+    from loki_amd import Context
+    ctx = Context()
+    res = run_workload(ctx, torch, args.workload, args.steps, args.warmup, args.copies)
+    n = res["n"]
+    gu_ms = res["stage_ms"]["gate_up"]
+    gu_gbs = res["gu_bytes"] / (gu_ms * 1e-3) / 1e9
+    log("[bench] %s: %.1f us/step, %.2f us/token, %.0f GB/s (U=%.1f); stages (us): %s" % (
+        args.workload, res["ms"] * 1e3, res["ms"] * 1e3 / n, res["gbs"], res["U"],
+        ", ".join("%s %.1f" % (k, v * 1e3) for k, v in res["stage_ms"].items())))
+    extra = {}
+    if not args.no_extra:
+        for wl, st in (("decode1", 30), ("prefill512", 5)):
+            if wl == args.workload:
+                continue
+            r = run_workload(ctx, torch, wl, st, 2, args.copies)
+            extra[wl] = {"us_per_token": round(r["ms"] * 1e3 / r["n"], 3), "ms_per_step": round(r["ms"], 4),
+                         "tokens_per_s": round(r["n"] / (r["ms"] * 1e-3), 1), "hbm_gbs": round(r["gbs"], 1),
+                         "hbm_frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "distinct_experts": round(r["U"], 1),
+                         "stage_us": {k: round(v * 1e3, 2) for k, v in r["stage_ms"].items()}}
+            log("[bench] %s: %s" % (wl, json.dumps(extra[wl])))
+            del r
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(ctx, torch, res)
+        log("[bench] cpu baseline: %s" % json.dumps(cpu))
+    out = {
+        "metric": "MoE-layer decode µs/token (HBM GB/s, % peak); prefill-512 tokens/s",
+        "value": round(res["ms"] * 1e3 / n, 3),
+        "unit": "us/token",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(res["ms"], 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (device-generated, seeded; BASELINE.json configs distribution)",
+        "config": {"workload": res["desc"], "tokens": n, "hidden": E, "expert_ffn": H, "routed_experts": 256,
+                   "shared_experts": 1, "routing": "sigmoid, 8 groups, top-4 groups, top-8, x2.5",
+                   "weights": "IQ2_XXS (activations Q8_K)", "layer_copies": args.copies},
+        "hbm_gbs": round(res["gbs"], 1),
+        "hbm_frac": round(res["gbs"] / HBM_PEAK_GBS, 4),
+        "distinct_experts": round(res["U"], 1),
+        "roofline": {"kernel": "k_iq2_gemv<gate_up>", "bound": "hbm", "achieved": round(gu_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic("gate_up", args.workload),
+                     "algorithmic_bytes_per_launch": int(res["gu_bytes"]), "avg_launch_us": round(gu_ms * 1e3, 2)},
+        "stage_us": {k: round(v * 1e3, 2) for k, v in res["stage_ms"].items()},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -123,6 +123,11 @@ typedef struct FLDebug {
 int fl_debug(FLCtx *, FLDebug * out);
 int fl_set_debug(FLCtx *, int capture_gate_up);
 
+/* stage timing with HIP events on the context's stream: stages 0..7 = quant_x, router_logits, router_select, dispatch,
+ * gate_up, quant_h, down, combine. fl_stage_ms waits for the profiled calls and returns their count (summed ms in ms[]). */
+int fl_set_profile(FLCtx *, int on);
+int fl_stage_ms(FLCtx *, double * ms, int nstage, int reset);
+
 hipStream_t fl_stream(FLCtx *);
 /* run on the caller's stream from now on (NULL = HIP's default stream); work queued on the previous stream finishes first */
 int fl_set_stream(FLCtx *, hipStream_t s);

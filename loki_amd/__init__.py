@@ -55,7 +55,7 @@ ABI_SYMBOLS = [
     "fl_wide_outs", "fl_wide_skip", "fl_spec", "fl_sketch", "fl_fetch", "fl_moe", "fl_skip", "fl_h2d", "fl_wait_event",
     "fl_gpu_ms", "fl_ffn_begin", "fl_set_routing", "fl_moe_layer", "fl_route_dev", "fl_dispatch_dev", "fl_quant_q8k_dev",
     "fl_pack_iq2xxs", "fl_unpack_iq2xxs", "fl_rmsnorm_dev", "fl_synth_iq2xxs", "fl_synth_normal", "fl_probe_exp",
-    "fl_debug", "fl_set_debug", "fl_stream", "fl_set_stream", "fl_d2h", "fl_sync", "fl_last_error", "fl_free",
+    "fl_debug", "fl_set_debug", "fl_stream", "fl_set_stream", "fl_d2h", "fl_set_profile", "fl_stage_ms", "fl_sync", "fl_last_error", "fl_free",
 ]
 
 _lib = None
@@ -95,6 +95,21 @@ def lib():
             "fl_probe_exp": (I, [P_, P_, P_, I64, I]),
             "fl_debug": (I, [P_, ctypes.POINTER(FLDebug)]),
             "fl_gpu_ms": (D, [P_, I]),
+            "fl_ffn_begin": (I, [P_, ctypes.POINTER(FLW), I, P_, P_, I]),
+            "fl_fetch": (None, [P_, I, I, ctypes.POINTER(FLOut)]),
+            "fl_moe": (None, [P_, P_, P_, P_, I, I, P_, P_, I, I, ctypes.POINTER(FLOut)]),
+            "fl_skip": (None, [P_, P_, I, ctypes.POINTER(FLOut)]),
+            "fl_moe_outs": (None, [P_, I, P_, P_, I, P_]),
+            "fl_wide_init": (I, [P_, I, I]),
+            "fl_wide_moe": (None, [P_, P_, P_, P_, I, I, P_, P_, P_, P_, I, I, I]),
+            "fl_wide_mark": (None, [P_, I]),
+            "fl_wide_wait": (None, [P_, I]),
+            "fl_wide_finish": (None, [P_, I, I, ctypes.POINTER(FLOut)]),
+            "fl_wide_outs": (None, [P_, I, I, P_]),
+            "fl_wide_skip": (None, [P_, P_, I, ctypes.POINTER(FLOut)]),
+            "fl_h2d": (None, [P_, P_, P_, S]),
+            "fl_set_profile": (I, [P_, I]),
+            "fl_stage_ms": (I, [P_, ctypes.POINTER(ctypes.c_double), I, I]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -258,6 +273,19 @@ class Context:
 
     def gpu_ms(self, which=1):
         return lib().fl_gpu_ms(self.ctx, which)
+
+    STAGES = ("quant_x", "router_logits", "router_select", "dispatch", "gate_up", "quant_h", "down", "combine")
+
+    def set_profile(self, on):
+        self.check(lib().fl_set_profile(self.ctx, 1 if on else 0))
+
+    def stage_ms(self, reset=True):
+        """(calls, {stage: summed ms}) of the profiled fl_moe_layer calls since the last reset (waits for them)."""
+        arr = (ctypes.c_double * len(self.STAGES))()
+        n = lib().fl_stage_ms(self.ctx, arr, len(self.STAGES), 1 if reset else 0)
+        if n < 0:
+            self.check(n)
+        return n, dict(zip(self.STAGES, list(arr)))
 
 
 class MoeLayerWeights:

@@ -1,0 +1,410 @@
+// compat.hip -- the reference's host-driven MoE entry points (src/fused_layer.h:29-52) on top of the device kernels.
+//
+// The reference's engine drives one layer as: fl_attn (attention + router + shared expert) -> fl_fetch (routing to the
+// host) -> host dispatch -> fl_moe (narrow, n <= 8) or fl_wide_moe per arena batch + fl_wide_finish (prefill).
+// Attention stays outside this library, so fl_ffn_begin takes the MoE tail of fl_attn (router input ncur and the
+// residual ffn_inp; src/fused_layer.cu:498-525) from the host. Everything else keeps the reference's names, parameters,
+// ownership (context-owned pinned mirrors, overwritten by the next call) and synchronisation (fl_fetch, fl_moe, fl_skip,
+// fl_wide_finish and fl_wide_skip wait; fl_ffn_begin and fl_wide_moe only enqueue). Expert arenas arrive in ggml's
+// layout and are repacked into the tiled layout on the device before the mat-vecs.
+// Summation orders follow each reference kernel: moe_combine (src/fused_layer.cu:366-372) adds slots in ascending slot
+// order with the weights of equal slots merged; base_rows/wide_finish (:351-360) add fi + shared, then the k outputs.
+#include "fl_ctx.h"
+
+using namespace lk;
+
+namespace {
+
+constexpr int RMAX = 64;           // rows per fl_ffn_begin call (the reference's RMAX, src/fused_layer.cu:402)
+constexpr int NB = 8;              // rows of a narrow pass (src/fused_layer.cu:18)
+constexpr int E_ = 7168, H_ = 2048, NEXP_ = 256;
+
+template <class T> T * pinned(size_t n) {
+    void * p = nullptr;
+    if (hipHostMalloc(&p, n * sizeof(T) > 0 ? n * sizeof(T) : 1, hipHostMallocDefault) != hipSuccess) { (void) hipGetLastError(); return nullptr; }
+    std::memset(p, 0, n * sizeof(T));
+    return static_cast<T *>(p);
+}
+
+// ---------------------------------------------------------------- small kernels with the reference's orders
+__global__ void k_combine_slots(const float * __restrict__ o, const int * __restrict__ inv, const int * __restrict__ ids,
+                                const float * __restrict__ w, int n, int KE, const float * __restrict__ sh, const float * __restrict__ fi,
+                                float * __restrict__ h, float * __restrict__ moe) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t) n * E_) { return; }
+    const int b = (int) (i / E_), e = (int) (i % E_);
+    const int * idr = ids + b * KE; const float * wr = w + b * KE;
+    float v = 0.f; int prev = -1;
+    for (;;) {   // distinct slot ids of the row, ascending
+        int m = 0x7fffffff;
+        for (int k = 0; k < KE; ++k) { if (idr[k] > prev && idr[k] < m) { m = idr[k]; } }
+        if (m == 0x7fffffff) { break; }
+        float wt = 0.f; int kf = -1;
+        for (int k = 0; k < KE; ++k) { if (idr[k] == m) { wt += wr[k]; if (kf < 0) { kf = k; } } }
+        prev = m;
+        if (wt == 0.f) { continue; }
+        v += wt * o[(size_t) inv[b * KE + kf] * E_ + e];
+    }
+    if (moe) { moe[i] = v; }
+    h[i] = (v + sh[i]) + fi[i];
+}
+
+__global__ void k_skip_rows(const float * __restrict__ mo, const float * __restrict__ sh, const float * __restrict__ fi, int64_t tot, float * __restrict__ h) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
+    if (i >= tot) { return; }
+    const float v = 0.f + mo[i];
+    h[i] = (v + sh[i]) + fi[i];
+}
+
+__global__ void k_base_rows(const float * __restrict__ fi, const float * __restrict__ sh, int64_t tot, float * __restrict__ base) {
+    const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
+    if (i < tot) { base[i] = fi[i] + sh[i]; }
+}
+
+__global__ void k_wide_scatter(const float * __restrict__ o, const int * __restrict__ prow, const int * __restrict__ pk, const float * __restrict__ pw,
+                               int npairs, int KE, float * __restrict__ out_all) {
+    const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t) npairs * E_) { return; }
+    const int p = (int) (i / E_), e = (int) (i % E_);
+    out_all[((size_t) prow[p] * KE + pk[p]) * E_ + e] = pw[p] * o[(size_t) p * E_ + e];
+}
+
+__global__ void k_wide_finish(const float * __restrict__ base, const float * __restrict__ out_all, int KE, int64_t tot,
+                              float * __restrict__ h, float * __restrict__ moe) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
+    if (i >= tot) { return; }
+    const int64_t r = i / E_, e = i % E_;
+    float m = 0.f;
+    for (int k = 0; k < KE; ++k) { m += out_all[((size_t) r * KE + k) * E_ + e]; }
+    moe[i] = m; h[i] = base[i] + m;
+}
+
+__global__ void k_wide_skip(const float * __restrict__ base, const float * __restrict__ mo, int64_t tot, float * __restrict__ h) {
+    const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
+    if (i < tot) { h[i] = base[i] + mo[i]; }
+}
+
+inline unsigned nblk(int64_t tot) { return (unsigned) ((tot + 255) / 256); }
+
+}  // namespace
+
+struct Compat {
+    // rows of the last fl_ffn_begin (narrow pass)
+    int N = 0;
+    DBuf<float> ncur, fi, logits, probs, wts, h, o, sh_o; DBuf<int8_t> xq, hq; DBuf<float> xd, hd; DBuf<int> sel;
+    DBuf<uint8_t> sh_t; const void * sh_key[3] = { nullptr, nullptr, nullptr };
+    // fl_moe
+    DBuf<uint8_t> ag, au, ad; DBuf<int> ids, counts, offsets, perm, inv, act, nact; DBuf<float> w, hout, moe;
+    std::vector<int> last_ids; int last_KE = 0, last_n = 0;
+    // wide pass
+    int wmax = 0, wke = 0;
+    DBuf<float> ncur_all, base_all, out_all, xd_all; DBuf<int8_t> xq_all;
+    DBuf<int> w_act, w_off, w_perm, w_nact, w_row, w_k; DBuf<float> w_wk;
+    hipEvent_t wev[2] = { nullptr, nullptr };
+    // pinned host mirrors
+    int * h_sel = nullptr; float * h_wts = nullptr, * h_ncur = nullptr, * h_fi = nullptr, * h_h = nullptr, * h_moe = nullptr;
+    float * h_wh = nullptr, * h_wmoe = nullptr;
+};
+
+static Compat * cs(FLCtx * c) {
+    if (!c->compat) {
+        Compat * s = new Compat();
+        s->h_sel = pinned<int>(RMAX * MAXK); s->h_wts = pinned<float>(RMAX * MAXK);
+        s->h_ncur = pinned<float>((size_t) RMAX * E_); s->h_fi = pinned<float>((size_t) RMAX * E_);
+        s->h_h = pinned<float>((size_t) RMAX * E_); s->h_moe = pinned<float>((size_t) RMAX * E_);
+        if (!s->h_sel || !s->h_wts || !s->h_ncur || !s->h_fi || !s->h_h || !s->h_moe) { fatal("hipHostMalloc (fused-layer mirrors)", hipErrorOutOfMemory, __FILE__, __LINE__); }
+        c->compat = s;
+    }
+    return c->compat;
+}
+
+void compat_free(FLCtx * c) {
+    Compat * s = c->compat;
+    if (!s) { return; }
+    for (void * p : { (void *) s->h_sel, (void *) s->h_wts, (void *) s->h_ncur, (void *) s->h_fi, (void *) s->h_h, (void *) s->h_moe, (void *) s->h_wh, (void *) s->h_wmoe }) {
+        if (p) { (void) hipHostFree(p); }
+    }
+    for (hipEvent_t e : s->wev) { if (e) { (void) hipEventDestroy(e); } }
+    s->ncur.release(); s->fi.release(); s->logits.release(); s->probs.release(); s->wts.release(); s->h.release(); s->o.release(); s->sh_o.release();
+    s->xq.release(); s->hq.release(); s->xd.release(); s->hd.release(); s->sel.release(); s->sh_t.release();
+    s->ag.release(); s->au.release(); s->ad.release(); s->ids.release(); s->counts.release(); s->offsets.release(); s->perm.release(); s->inv.release();
+    s->act.release(); s->nact.release(); s->w.release(); s->hout.release(); s->moe.release();
+    s->ncur_all.release(); s->base_all.release(); s->out_all.release(); s->xd_all.release(); s->xq_all.release();
+    s->w_act.release(); s->w_off.release(); s->w_perm.release(); s->w_nact.release(); s->w_row.release(); s->w_k.release(); s->w_wk.release();
+    delete s; c->compat = nullptr;
+}
+
+static const int * zero_int(FLCtx * c) {
+    if (!c->zero_dev_init) {
+        CK(c->zero_i.ensure(1) == hipSuccess ? hipSuccess : hipErrorOutOfMemory);
+        const int z = 0; CK(hipMemcpy(c->zero_i.p, &z, sizeof z, hipMemcpyHostToDevice));
+        c->zero_dev_init = 1;
+    }
+    return c->zero_i.p;
+}
+
+#define FCK(x) CK(x)
+#define FALLOC(buf, n) CK((buf).ensure(n))
+
+static size_t mat_bytes(int R, int K) { return (size_t) R * (K / QK) * IQ2B; }
+
+// shared expert (IQ2_XXS) of N rows whose Q8_K activations are xq/xd -> out [N][E]
+static void shared_expert(FLCtx * c, Compat * s, const int8_t * xq, const float * xd, int N, float * out) {
+    const size_t mg = mat_bytes(H_, E_);
+    FALLOC(s->h, (size_t) N * H_); FALLOC(s->hq, (size_t) N * H_); FALLOC(s->hd, (size_t) N * (H_ / QK));
+    GemvArgs a{};
+    a.sh0 = s->sh_t.p; a.sh1 = s->sh_t.p + mg; a.aq = xq; a.ad = xd; a.K = E_; a.R = H_;
+    a.act = zero_int(c); a.nact = zero_int(c); a.offsets = zero_int(c); a.perm = zero_int(c);
+    a.topk = 1; a.n = N; a.P = 0; a.max_act = 0; a.shared = 1; a.out = s->h.p;
+    FCK(launch_gemv_gateup(a, c->st));
+    FCK(launch_quant_q8k(s->h.p, N, H_, s->hq.p, s->hd.p, c->st));
+    GemvArgs d = a; d.sh0 = s->sh_t.p + 2 * mg; d.sh1 = nullptr; d.aq = s->hq.p; d.ad = s->hd.p; d.K = H_; d.R = E_; d.out = out;
+    FCK(launch_gemv_down(d, c->st));
+}
+
+// routed experts of an arena (tiled copy ag/au/ad) for the pairs described by offsets/perm/act/nact -> o [P][E]
+static void routed_experts(FLCtx * c, Compat * s, const int8_t * xq, const float * xd, int n, int P, int KE, int nexp,
+                           const int * act, const int * nact, const int * offsets, const int * perm, float * o) {
+    FALLOC(s->h, (size_t) P * H_); FALLOC(s->hq, (size_t) P * H_); FALLOC(s->hd, (size_t) P * (H_ / QK));
+    GemvArgs a{};
+    a.w0 = s->ag.p; a.w1 = s->au.p; a.estride = mat_bytes(H_, E_); a.aq = xq; a.ad = xd; a.K = E_; a.R = H_;
+    a.act = act; a.nact = nact; a.offsets = offsets; a.perm = perm; a.topk = KE; a.n = n; a.P = P;
+    a.max_act = std::min(nexp, P); a.shared = 0; a.out = s->h.p;
+    FCK(launch_gemv_gateup(a, c->st));
+    FCK(launch_quant_q8k(s->h.p, P, H_, s->hq.p, s->hd.p, c->st));
+    GemvArgs d = a; d.w0 = s->ad.p; d.w1 = nullptr; d.estride = mat_bytes(E_, H_); d.aq = s->hq.p; d.ad = s->hd.p; d.K = H_; d.R = E_; d.out = o;
+    FCK(launch_gemv_down(d, c->st));
+}
+
+static void pack_arena(FLCtx * c, Compat * s, const void * gate, const void * up, const void * down, int nexp) {
+    const size_t mg = mat_bytes(H_, E_), md = mat_bytes(E_, H_);
+    FALLOC(s->ag, (size_t) nexp * mg); FALLOC(s->au, (size_t) nexp * mg); FALLOC(s->ad, (size_t) nexp * md);
+    FCK(launch_pack_tiled((const uint8_t *) gate, mg, s->ag.p, mg, H_, E_, nexp, c->st));
+    FCK(launch_pack_tiled((const uint8_t *) up, mg, s->au.p, mg, H_, E_, nexp, c->st));
+    FCK(launch_pack_tiled((const uint8_t *) down, md, s->ad.p, md, E_, H_, nexp, c->st));
+}
+
+static void need_iq2(const char * fn, int fmt) {
+    if (fmt != FL_IQ2) {
+        std::fprintf(stderr, "[fused] %s: down format %d is not supported by this library (IQ2_XXS experts only)\n", fn, fmt);
+        std::exit(7);
+    }
+}
+
+// ================================================================ entry points
+extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur, const float * ffn_inp, int wrow) {
+    if (!c) { return FL_EINVAL; }
+    if (!W || !ncur || !ffn_inp) { return fail(c, FL_EINVAL, "null pointer"); }
+    if (N <= 0 || N > RMAX) { return fail(c, FL_ERANGE, "N = %d outside 1..%d", N, RMAX); }
+    if (W->gate_f16) { return fail(c, FL_ESCOPE, "the F16 router (ffn_gate_inp_f16) is not supported; pass the F32 router"); }
+    if (!W->gate_inp || !W->probs_b || !W->sh_gate || !W->sh_up || !W->sh_down) { return fail(c, FL_EINVAL, "router or shared-expert weight missing"); }
+    Compat * s = cs(c);
+    if (wrow >= 0 && (s->wmax == 0 || wrow + N > s->wmax)) { return fail(c, FL_ERANGE, "wide rows %d..%d exceed fl_wide_init's %d", wrow, wrow + N, s->wmax); }
+    const size_t R = (size_t) RMAX * E_;
+    ALLOC(c, s->ncur, R); ALLOC(c, s->fi, R); ALLOC(c, s->logits, RMAX * NEXP_); ALLOC(c, s->probs, RMAX * NEXP_);
+    ALLOC(c, s->sel, RMAX * MAXK); ALLOC(c, s->wts, RMAX * MAXK); ALLOC(c, s->xq, R); ALLOC(c, s->xd, RMAX * (E_ / QK)); ALLOC(c, s->sh_o, R);
+    hipStream_t st = c->st;
+    TRY(c, hipMemcpyAsync(s->ncur.p, ncur, (size_t) N * E_ * 4, hipMemcpyHostToDevice, st));
+    TRY(c, hipMemcpyAsync(s->fi.p, ffn_inp, (size_t) N * E_ * 4, hipMemcpyHostToDevice, st));
+    const size_t mg = mat_bytes(H_, E_);
+    if (s->sh_key[0] != W->sh_gate || s->sh_key[1] != W->sh_up || s->sh_key[2] != W->sh_down) {
+        ALLOC(c, s->sh_t, 3 * mg);
+        TRY(c, launch_pack_tiled((const uint8_t *) W->sh_gate, mg, s->sh_t.p, mg, H_, E_, 1, st));
+        TRY(c, launch_pack_tiled((const uint8_t *) W->sh_up, mg, s->sh_t.p + mg, mg, H_, E_, 1, st));
+        TRY(c, launch_pack_tiled((const uint8_t *) W->sh_down, mg, s->sh_t.p + 2 * mg, mg, E_, H_, 1, st));
+        s->sh_key[0] = W->sh_gate; s->sh_key[1] = W->sh_up; s->sh_key[2] = W->sh_down;
+    }
+    if (int rc = fl_route_dev(c, (const float *) W->gate_inp, (const float *) W->probs_b, s->ncur.p, N, NEXP_, E_, s->logits.p, s->probs.p, s->sel.p, s->wts.p)) { return rc; }
+    TRY(c, launch_quant_q8k(s->ncur.p, N, E_, s->xq.p, s->xd.p, st));
+    shared_expert(c, s, s->xq.p, s->xd.p, N, s->sh_o.p);
+    if (wrow >= 0) {
+        TRY(c, hipMemcpyAsync(s->ncur_all.p + (size_t) wrow * E_, s->ncur.p, (size_t) N * E_ * 4, hipMemcpyDeviceToDevice, st));
+        TRY(c, hipMemcpyAsync(s->xq_all.p + (size_t) wrow * E_, s->xq.p, (size_t) N * E_, hipMemcpyDeviceToDevice, st));
+        TRY(c, hipMemcpyAsync(s->xd_all.p + (size_t) wrow * (E_ / QK), s->xd.p, (size_t) N * (E_ / QK) * 4, hipMemcpyDeviceToDevice, st));
+        k_base_rows<<<nblk((int64_t) N * E_), 256, 0, st>>>(s->fi.p, s->sh_o.p, (int64_t) N * E_, s->base_all.p + (size_t) wrow * E_);
+        TRY(c, hipGetLastError());
+    }
+    s->N = N;
+    return FL_OK;
+}
+
+extern "C" void fl_fetch(FLCtx * c, int n, int what, FLOut * out) {
+    std::memset(out, 0, sizeof(FLOut));
+    Compat * s = cs(c);
+    if (n < 0 || n > s->N) { std::fprintf(stderr, "[fused] fl_fetch: %d rows requested, %d routed\n", n, s->N); std::exit(7); }
+    if (what & 1) {
+        CK(hipMemcpyAsync(s->h_sel, s->sel.p, (size_t) n * c->topk * 4, hipMemcpyDeviceToHost, c->st));
+        CK(hipMemcpyAsync(s->h_wts, s->wts.p, (size_t) n * c->topk * 4, hipMemcpyDeviceToHost, c->st));
+        CK(hipMemcpyAsync(s->h_ncur, s->ncur.p, (size_t) n * E_ * 4, hipMemcpyDeviceToHost, c->st));
+        CK(hipMemcpyAsync(s->h_fi, s->fi.p, (size_t) n * E_ * 4, hipMemcpyDeviceToHost, c->st));
+        out->sel = s->h_sel; out->wts = s->h_wts; out->ncur = s->h_ncur; out->fi = s->h_fi;
+    }
+    CK(hipStreamSynchronize(c->st));
+}
+
+extern "C" void fl_moe(FLCtx * c, const void * gate, const void * up, const void * down, int nexp, int down_fmt, const int * ids,
+                       const float * w, int KE, int n, FLOut * out) {
+    std::memset(out, 0, sizeof(FLOut));
+    need_iq2("fl_moe", down_fmt);
+    Compat * s = cs(c);
+    if (n <= 0 || n > NB || n > s->N || KE <= 0 || KE > MAXK || nexp <= 0 || nexp > NEXP_) {
+        std::fprintf(stderr, "[fused] fl_moe: n %d (routed rows %d), KE %d, nexp %d out of range\n", n, s->N, KE, nexp); std::exit(7);
+    }
+    for (int i = 0; i < n * KE; ++i) {
+        if (ids[i] < 0 || ids[i] >= nexp) { std::fprintf(stderr, "[fused] fl_moe: slot id %d outside the arena of %d\n", ids[i], nexp); std::exit(7); }
+    }
+    hipStream_t st = c->st; const int P = n * KE;
+    CK(hipEventRecord(c->em0, st));
+    FALLOC(s->ids, P); FALLOC(s->w, P); FALLOC(s->counts, nexp); FALLOC(s->offsets, nexp + 1); FALLOC(s->perm, P); FALLOC(s->inv, P);
+    FALLOC(s->act, nexp); FALLOC(s->nact, 1); FALLOC(s->o, (size_t) P * E_); FALLOC(s->hout, (size_t) NB * E_); FALLOC(s->moe, (size_t) NB * E_);
+    CK(hipMemcpyAsync(s->ids.p, ids, (size_t) P * 4, hipMemcpyHostToDevice, st));
+    CK(hipMemcpyAsync(s->w.p, w, (size_t) P * 4, hipMemcpyHostToDevice, st));
+    pack_arena(c, s, gate, up, down, nexp);
+    CK(launch_dispatch(s->ids.p, P, nexp, s->counts.p, s->offsets.p, s->perm.p, s->inv.p, s->act.p, s->nact.p, st));
+    routed_experts(c, s, s->xq.p, s->xd.p, n, P, KE, nexp, s->act.p, s->nact.p, s->offsets.p, s->perm.p, s->o.p);
+    k_combine_slots<<<nblk((int64_t) n * E_), 256, 0, st>>>(s->o.p, s->inv.p, s->ids.p, s->w.p, n, KE, s->sh_o.p, s->fi.p, s->hout.p, s->moe.p);
+    CK(hipGetLastError());
+    CK(hipMemcpyAsync(s->h_h, s->hout.p, (size_t) n * E_ * 4, hipMemcpyDeviceToHost, st));
+    CK(hipMemcpyAsync(s->h_moe, s->moe.p, (size_t) n * E_ * 4, hipMemcpyDeviceToHost, st));
+    CK(hipEventRecord(c->em1, st));
+    CK(hipStreamSynchronize(st));
+    float ms = 0.f; CK(hipEventElapsedTime(&ms, c->em0, c->em1)); c->ms_moe += ms;
+    s->last_ids.assign(ids, ids + P); s->last_KE = KE; s->last_n = n;
+    out->h = s->h_h; out->moe = s->h_moe;
+}
+
+extern "C" void fl_skip(FLCtx * c, const float * mo, int n, FLOut * out) {
+    std::memset(out, 0, sizeof(FLOut));
+    Compat * s = cs(c);
+    if (n <= 0 || n > s->N) { std::fprintf(stderr, "[fused] fl_skip: n %d outside the %d routed rows\n", n, s->N); std::exit(7); }
+    hipStream_t st = c->st;
+    CK(hipEventRecord(c->em0, st));
+    FALLOC(s->moe, (size_t) RMAX * E_); FALLOC(s->hout, (size_t) RMAX * E_);
+    CK(hipMemcpyAsync(s->moe.p, mo, (size_t) n * E_ * 4, hipMemcpyHostToDevice, st));
+    k_skip_rows<<<nblk((int64_t) n * E_), 256, 0, st>>>(s->moe.p, s->sh_o.p, s->fi.p, (int64_t) n * E_, s->hout.p);
+    CK(hipGetLastError());
+    CK(hipMemcpyAsync(s->h_h, s->hout.p, (size_t) n * E_ * 4, hipMemcpyDeviceToHost, st));
+    CK(hipEventRecord(c->em1, st));
+    CK(hipStreamSynchronize(st));
+    float ms = 0.f; CK(hipEventElapsedTime(&ms, c->em0, c->em1)); c->ms_moe += ms;
+    out->h = s->h_h;
+}
+
+extern "C" void fl_moe_outs(FLCtx * c, int b, const int * ids, const float * w, int KE, float * out) {
+    Compat * s = cs(c);
+    CK(hipStreamSynchronize(c->st));
+    if (b < 0 || b >= s->last_n || KE != s->last_KE) { std::fprintf(stderr, "[fused] fl_moe_outs: row %d / KE %d do not match the last fl_moe\n", b, KE); std::exit(7); }
+    std::vector<int> inv((size_t) s->last_n * KE);
+    CK(hipMemcpy(inv.data(), s->inv.p, inv.size() * 4, hipMemcpyDeviceToHost));
+    std::vector<float> row(E_);
+    for (int k = 0; k < KE; ++k) {
+        int kf = -1;
+        for (int j = 0; j < KE; ++j) { if (s->last_ids[(size_t) b * KE + j] == ids[k]) { kf = j; break; } }
+        if (kf < 0) { std::memset(out + (size_t) k * E_, 0, E_ * 4); continue; }   // this row never ran that slot
+        CK(hipMemcpy(row.data(), s->o.p + (size_t) inv[(size_t) b * KE + kf] * E_, E_ * 4, hipMemcpyDeviceToHost));
+        for (int e = 0; e < E_; ++e) { out[(size_t) k * E_ + e] = w[k] * row[e]; }
+    }
+}
+
+extern "C" int fl_wide_init(FLCtx * c, int wmax, int KE) {
+    Compat * s = cs(c);
+    if (wmax <= 0 || KE <= 0 || KE > MAXK) { std::fprintf(stderr, "[fused] fl_wide_init: wmax %d, KE %d\n", wmax, KE); std::exit(7); }
+    s->wmax = wmax; s->wke = KE;
+    const size_t R = (size_t) wmax * E_;
+    FALLOC(s->ncur_all, R); FALLOC(s->base_all, R); FALLOC(s->out_all, R * KE); FALLOC(s->xq_all, R); FALLOC(s->xd_all, (size_t) wmax * (E_ / QK));
+    CK(hipMemset(s->out_all.p, 0, R * KE * 4));
+    if (s->h_wh) { (void) hipHostFree(s->h_wh); } if (s->h_wmoe) { (void) hipHostFree(s->h_wmoe); }
+    s->h_wh = pinned<float>(R); s->h_wmoe = pinned<float>(R);
+    if (!s->h_wh || !s->h_wmoe) { fatal("hipHostMalloc (wide-pass mirrors)", hipErrorOutOfMemory, __FILE__, __LINE__); }
+    for (hipEvent_t & e : s->wev) { if (!e) { CK(hipEventCreateWithFlags(&e, hipEventDisableTiming)); } }
+    return 1;
+}
+
+extern "C" void fl_wide_moe(FLCtx * c, const void * gate, const void * up, const void * down, int down_fmt, int nexp, const int * midx,
+                            const int * rows, const int * kidx, const float * wk, int nslots, int KE, int par) {
+    need_iq2("fl_wide_moe", down_fmt);
+    Compat * s = cs(c);
+    (void) par;
+    if (KE != s->wke || nexp <= 0 || nexp > NEXP_ || nslots < 0) { std::fprintf(stderr, "[fused] fl_wide_moe: KE %d (init %d), nexp %d, nslots %d\n", KE, s->wke, nexp, nslots); std::exit(7); }
+    // the slot tables as (expert, row, k, w) pairs, grouped by expert in slot order (a stable counting sort)
+    std::vector<int> cnt(nexp + 1, 0);
+    for (int sl = 0; sl < nslots; ++sl) {
+        if (midx[sl] < 0 || midx[sl] >= nexp) { std::fprintf(stderr, "[fused] fl_wide_moe: slot expert %d outside the batch of %d\n", midx[sl], nexp); std::exit(7); }
+        for (int j = 0; j < NB; ++j) {
+            const int r = rows[sl * NB + j];
+            if (r < 0) { continue; }
+            if (r >= s->wmax || kidx[sl * NB + j] < 0 || kidx[sl * NB + j] >= KE) { std::fprintf(stderr, "[fused] fl_wide_moe: pair (row %d, k %d) out of range\n", r, kidx[sl * NB + j]); std::exit(7); }
+            cnt[midx[sl] + 1]++;
+        }
+    }
+    for (int e = 0; e < nexp; ++e) { cnt[e + 1] += cnt[e]; }
+    const int P = cnt[nexp];
+    if (P == 0) { return; }
+    std::vector<int> off(cnt), fillp(cnt.begin(), cnt.end() - 1), perm(P), prow(P), pk(P), act; std::vector<float> pw(P);
+    for (int sl = 0; sl < nslots; ++sl) {
+        for (int j = 0; j < NB; ++j) {
+            const int r = rows[sl * NB + j];
+            if (r < 0) { continue; }
+            const int pos = fillp[midx[sl]]++;
+            perm[pos] = r * KE + kidx[sl * NB + j]; prow[pos] = r; pk[pos] = kidx[sl * NB + j]; pw[pos] = wk[sl * NB + j];
+        }
+    }
+    for (int e = 0; e < nexp; ++e) { if (off[e + 1] > off[e]) { act.push_back(e); } }
+    const int na = (int) act.size();
+    hipStream_t st = c->st;
+    FALLOC(s->w_act, nexp); FALLOC(s->w_off, nexp + 1); FALLOC(s->w_perm, P); FALLOC(s->w_nact, 1); FALLOC(s->w_row, P); FALLOC(s->w_k, P); FALLOC(s->w_wk, P);
+    FALLOC(s->o, (size_t) P * E_);
+    CK(hipMemcpyAsync(s->w_act.p, act.data(), (size_t) na * 4, hipMemcpyHostToDevice, st));
+    CK(hipMemcpyAsync(s->w_off.p, off.data(), (size_t) (nexp + 1) * 4, hipMemcpyHostToDevice, st));
+    CK(hipMemcpyAsync(s->w_perm.p, perm.data(), (size_t) P * 4, hipMemcpyHostToDevice, st));
+    CK(hipMemcpyAsync(s->w_nact.p, &na, 4, hipMemcpyHostToDevice, st));
+    CK(hipMemcpyAsync(s->w_row.p, prow.data(), (size_t) P * 4, hipMemcpyHostToDevice, st));
+    CK(hipMemcpyAsync(s->w_k.p, pk.data(), (size_t) P * 4, hipMemcpyHostToDevice, st));
+    CK(hipMemcpyAsync(s->w_wk.p, pw.data(), (size_t) P * 4, hipMemcpyHostToDevice, st));
+    pack_arena(c, s, gate, up, down, nexp);
+    routed_experts(c, s, s->xq_all.p, s->xd_all.p, s->wmax, P, KE, nexp, s->w_act.p, s->w_nact.p, s->w_off.p, s->w_perm.p, s->o.p);
+    k_wide_scatter<<<nblk((int64_t) P * E_), 256, 0, st>>>(s->o.p, s->w_row.p, s->w_k.p, s->w_wk.p, P, KE, s->out_all.p);
+    CK(hipGetLastError());
+    CK(hipStreamSynchronize(st));   // host tables above are stack vectors: they must outlive the queued copies
+}
+
+extern "C" void fl_wide_mark(FLCtx * c, int par) { Compat * s = cs(c); if (s->wev[par & 1]) { CK(hipEventRecord(s->wev[par & 1], c->st)); } }
+extern "C" void fl_wide_wait(FLCtx * c, int par) { Compat * s = cs(c); if (s->wev[par & 1]) { CK(hipEventSynchronize(s->wev[par & 1])); } }
+
+extern "C" void fl_wide_finish(FLCtx * c, int n, int KE, FLOut * out) {
+    std::memset(out, 0, sizeof(FLOut));
+    Compat * s = cs(c);
+    if (n <= 0 || n > s->wmax || KE != s->wke) { std::fprintf(stderr, "[fused] fl_wide_finish: n %d (wmax %d), KE %d (init %d)\n", n, s->wmax, KE, s->wke); std::exit(7); }
+    hipStream_t st = c->st; const int64_t tot = (int64_t) n * E_;
+    FALLOC(s->hout, (size_t) tot); FALLOC(s->moe, (size_t) tot);
+    k_wide_finish<<<nblk(tot), 256, 0, st>>>(s->base_all.p, s->out_all.p, KE, tot, s->hout.p, s->moe.p);
+    CK(hipGetLastError());
+    CK(hipMemcpyAsync(s->h_wh, s->hout.p, (size_t) tot * 4, hipMemcpyDeviceToHost, st));
+    CK(hipMemcpyAsync(s->h_wmoe, s->moe.p, (size_t) tot * 4, hipMemcpyDeviceToHost, st));
+    CK(hipStreamSynchronize(st));
+    out->h = s->h_wh; out->moe = s->h_wmoe;
+}
+
+extern "C" void fl_wide_skip(FLCtx * c, const float * mo, int n, FLOut * out) {
+    std::memset(out, 0, sizeof(FLOut));
+    Compat * s = cs(c);
+    if (n <= 0 || n > s->wmax) { std::fprintf(stderr, "[fused] fl_wide_skip: n %d (wmax %d)\n", n, s->wmax); std::exit(7); }
+    hipStream_t st = c->st; const int64_t tot = (int64_t) n * E_;
+    FALLOC(s->hout, (size_t) tot); FALLOC(s->moe, (size_t) tot);
+    CK(hipMemcpyAsync(s->moe.p, mo, (size_t) tot * 4, hipMemcpyHostToDevice, st));
+    k_wide_skip<<<nblk(tot), 256, 0, st>>>(s->base_all.p, s->moe.p, tot, s->hout.p);
+    CK(hipGetLastError());
+    CK(hipMemcpyAsync(s->h_wh, s->hout.p, (size_t) tot * 4, hipMemcpyDeviceToHost, st));
+    CK(hipStreamSynchronize(st));
+    out->h = s->h_wh;
+}
+
+extern "C" void fl_wide_outs(FLCtx * c, int row, int KE, float * out) {
+    Compat * s = cs(c);
+    if (row < 0 || row >= s->wmax || KE != s->wke) { std::fprintf(stderr, "[fused] fl_wide_outs: row %d, KE %d\n", row, KE); std::exit(7); }
+    CK(hipStreamSynchronize(c->st));
+    CK(hipMemcpy(out, s->out_all.p + (size_t) row * KE * E_, (size_t) KE * E_ * 4, hipMemcpyDeviceToHost));
+}

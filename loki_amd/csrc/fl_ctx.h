@@ -1,0 +1,74 @@
+// fl_ctx.h -- FLCtx (the context behind the C ABI) and host helpers shared by fused_layer.hip and compat.hip.
+#pragma once
+#include "moe_common.h"
+#include "moe_kernels.h"
+#include "../../include/loki_moe.h"
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstring>
+#include <cstdio>
+#include <cstdlib>
+#include <string>
+#include <vector>
+
+template <class T> struct DBuf {
+    T * p = nullptr; size_t cap = 0;
+    hipError_t ensure(size_t want) {
+        if (want <= cap && p) { return hipSuccess; }
+        if (p) { (void) hipFree(p); p = nullptr; cap = 0; }
+        const size_t n = want > 0 ? want : 1;
+        hipError_t e = hipMalloc(reinterpret_cast<void **>(&p), n * sizeof(T));
+        if (e == hipSuccess) { cap = n; } else { p = nullptr; }
+        return e;
+    }
+    void release() { if (p) { (void) hipFree(p); } p = nullptr; cap = 0; }
+};
+
+[[noreturn]] inline void fatal(const char * what, hipError_t e, const char * file, int line) {
+    std::fprintf(stderr, "[fused] HIP error %s (%s) at %s:%d\n", hipGetErrorString(e), what, file, line);
+    std::exit(7);
+}
+#define CK(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) { fatal(#x, e_, __FILE__, __LINE__); } } while (0)
+
+struct FLCtx {
+    hipStream_t st = nullptr, own = nullptr; int dev = 0, ncu = 0;
+    hipEvent_t em0 = nullptr, em1 = nullptr;
+    int n_group = 8, topk_group = 4, topk = 8; float scale = 2.5f;
+    double ms_moe = 0.0;
+    std::string err;
+    int dbg_gu = 0;
+    DBuf<int8_t> xq, hq; DBuf<float> xd, logits, probs, wts, h, hd, o, g, u;
+    DBuf<int> sel, counts, offsets, perm, inv, act, nact;
+    int last_n = 0, last_P = 0;
+    // stage timing (fl_set_profile): one set of NSTAGE+1 events per profiled call, summed by fl_stage_ms
+    int prof = 0;
+    std::vector<std::vector<hipEvent_t>> ev_free, ev_pending;
+    double stage_ms[16] = {0}; long stage_n = 0;
+    int zero_dev_init = 0; DBuf<int> zero_i;   // a device int 0 (shared-expert-only launches read nact = 0)
+    struct Compat * compat = nullptr;          // reference-API state (compat.hip), created on first use
+};
+static const int NSTAGE = 8;   // quant_x, router_logits, router_select, dispatch, gate_up, quant_h, down, combine
+
+inline int fail(FLCtx * c, int code, const char * fmt, ...) {
+    char buf[512]; va_list ap; va_start(ap, fmt); std::vsnprintf(buf, sizeof buf, fmt, ap); va_end(ap);
+    if (c) { c->err = buf; }
+    return code;
+}
+#define TRY(c, x) do { hipError_t e_ = (x); if (e_ != hipSuccess) { return fail((c), FL_EHIP, "%s: %s", #x, hipGetErrorString(e_)); } } while (0)
+#define ALLOC(c, buf, n) do { if ((buf).ensure(n) != hipSuccess) { (void) hipGetLastError(); return fail((c), FL_ENOMEM, "device allocation of %zu elements failed", (size_t) (n)); } } while (0)
+
+static std::vector<hipEvent_t> * prof_begin(FLCtx * c) {
+    if (!c->prof) { return nullptr; }
+    if (c->ev_free.empty()) {
+        std::vector<hipEvent_t> ev(NSTAGE + 1);
+        for (auto & e : ev) { if (hipEventCreate(&e) != hipSuccess) { return nullptr; } }
+        c->ev_free.push_back(ev);
+    }
+    c->ev_pending.push_back(c->ev_free.back()); c->ev_free.pop_back();
+    return &c->ev_pending.back();
+}
+static void prof_mark(FLCtx * c, std::vector<hipEvent_t> * ev, int i) { if (ev) { (void) hipEventRecord((*ev)[i], c->st); } }
+
+void compat_free(FLCtx * c);   // compat.hip
+

@@ -7,6 +7,7 @@
 #include "moe_common.h"
 #include "moe_kernels.h"
 #include "../../include/loki_moe.h"
+#include "fl_ctx.h"
 
 #include <algorithm>
 #include <cstdarg>
@@ -17,49 +18,6 @@
 #include <vector>
 
 using namespace lk;
-
-namespace {
-
-template <class T> struct DBuf {
-    T * p = nullptr; size_t cap = 0;
-    hipError_t ensure(size_t want) {
-        if (want <= cap && p) { return hipSuccess; }
-        if (p) { (void) hipFree(p); p = nullptr; cap = 0; }
-        const size_t n = want > 0 ? want : 1;
-        hipError_t e = hipMalloc(reinterpret_cast<void **>(&p), n * sizeof(T));
-        if (e == hipSuccess) { cap = n; } else { p = nullptr; }
-        return e;
-    }
-    void release() { if (p) { (void) hipFree(p); } p = nullptr; cap = 0; }
-};
-
-[[noreturn]] void fatal(const char * what, hipError_t e, const char * file, int line) {
-    std::fprintf(stderr, "[fused] HIP error %s (%s) at %s:%d\n", hipGetErrorString(e), what, file, line);
-    std::exit(7);
-}
-#define CK(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) { fatal(#x, e_, __FILE__, __LINE__); } } while (0)
-
-}  // namespace
-
-struct FLCtx {
-    hipStream_t st = nullptr, own = nullptr; int dev = 0, ncu = 0;
-    hipEvent_t em0 = nullptr, em1 = nullptr;
-    int n_group = 8, topk_group = 4, topk = 8; float scale = 2.5f;
-    double ms_moe = 0.0;
-    std::string err;
-    int dbg_gu = 0;
-    DBuf<int8_t> xq, hq; DBuf<float> xd, logits, probs, wts, h, hd, o, g, u;
-    DBuf<int> sel, counts, offsets, perm, inv, act, nact;
-    int last_n = 0, last_P = 0;
-};
-
-static int fail(FLCtx * c, int code, const char * fmt, ...) {
-    char buf[512]; va_list ap; va_start(ap, fmt); std::vsnprintf(buf, sizeof buf, fmt, ap); va_end(ap);
-    if (c) { c->err = buf; }
-    return code;
-}
-#define TRY(c, x) do { hipError_t e_ = (x); if (e_ != hipSuccess) { return fail((c), FL_EHIP, "%s: %s", #x, hipGetErrorString(e_)); } } while (0)
-#define ALLOC(c, buf, n) do { if ((buf).ensure(n) != hipSuccess) { (void) hipGetLastError(); return fail((c), FL_ENOMEM, "device allocation of %zu elements failed", (size_t) (n)); } } while (0)
 
 [[noreturn]] static void out_of_scope(const char * fn) {
     std::fprintf(stderr, "[fused] %s: attention, speculation and sketches are not part of the MoE-block library\n", fn);
@@ -83,6 +41,9 @@ extern "C" void fl_free(FLCtx * c) {
     c->xq.release(); c->hq.release(); c->xd.release(); c->logits.release(); c->probs.release(); c->wts.release();
     c->h.release(); c->hd.release(); c->o.release(); c->g.release(); c->u.release();
     c->sel.release(); c->counts.release(); c->offsets.release(); c->perm.release(); c->inv.release(); c->act.release(); c->nact.release();
+    compat_free(c); c->zero_i.release();
+    for (auto & v : c->ev_free) { for (auto e : v) { (void) hipEventDestroy(e); } }
+    for (auto & v : c->ev_pending) { for (auto e : v) { (void) hipEventDestroy(e); } }
     (void) hipEventDestroy(c->em0); (void) hipEventDestroy(c->em1); (void) hipStreamDestroy(c->own);
     delete c;
 }
@@ -220,28 +181,53 @@ extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, in
     if (c->dbg_gu) { ALLOC(c, c->g, rows * H); ALLOC(c, c->u, rows * H); }
     c->last_n = n; c->last_P = P;
     hipStream_t st = c->st;
-    TRY(c, hipEventRecord(c->em0, st));
+    std::vector<hipEvent_t> * ev = prof_begin(c);
+    prof_mark(c, ev, 0);
     TRY(c, launch_quant_q8k(x, n, E, c->xq.p, c->xd.p, st));
+    prof_mark(c, ev, 1);
     TRY(c, launch_router_logits(L->gate_inp, x, n, ne, E, c->logits.p, st));
+    prof_mark(c, ev, 2);
     TRY(c, launch_router_select(c->logits.p, L->probs_b, n, ne, c->n_group, c->topk_group, tk, c->scale, c->probs.p, c->sel.p, c->wts.p, st));
+    prof_mark(c, ev, 3);
     TRY(c, launch_dispatch(c->sel.p, P, ne, c->counts.p, c->offsets.p, c->perm.p, c->inv.p, c->act.p, c->nact.p, st));
+    prof_mark(c, ev, 4);
     GemvArgs a{};
     a.w0 = (const uint8_t *) L->gate_exps; a.w1 = (const uint8_t *) L->up_exps; a.estride = (size_t) H * (E / 256) * IQ2B;
     a.sh0 = (const uint8_t *) L->sh_gate; a.sh1 = (const uint8_t *) L->sh_up;
     a.aq = c->xq.p; a.ad = c->xd.p; a.K = E; a.R = H;
     a.act = c->act.p; a.nact = c->nact.p; a.offsets = c->offsets.p; a.perm = c->perm.p;
-    a.topk = tk; a.n = n; a.P = P; a.max_act = std::min(ne, P);
+    a.topk = tk; a.n = n; a.P = P; a.max_act = std::min(ne, P); a.shared = 1;
     a.out = c->h.p; a.dbg0 = c->dbg_gu ? c->g.p : nullptr; a.dbg1 = c->dbg_gu ? c->u.p : nullptr;
     TRY(c, launch_gemv_gateup(a, st));
+    prof_mark(c, ev, 5);
     TRY(c, launch_quant_q8k(c->h.p, (int64_t) rows, H, c->hq.p, c->hd.p, st));
+    prof_mark(c, ev, 6);
     GemvArgs d = a;
     d.w0 = (const uint8_t *) L->down_exps; d.w1 = nullptr; d.estride = (size_t) E * (H / 256) * IQ2B;
     d.sh0 = (const uint8_t *) L->sh_down; d.sh1 = nullptr; d.aq = c->hq.p; d.ad = c->hd.p; d.K = H; d.R = E;
     d.out = c->o.p; d.dbg0 = nullptr; d.dbg1 = nullptr;
     TRY(c, launch_gemv_down(d, st));
+    prof_mark(c, ev, 7);
     TRY(c, launch_combine(c->o.p, c->inv.p, c->wts.p, n, tk, E, P, nullptr, y, nullptr, st));
-    TRY(c, hipEventRecord(c->em1, st));
+    prof_mark(c, ev, 8);
     return FL_OK;
+}
+
+extern "C" int fl_set_profile(FLCtx * c, int on) { if (!c) { return FL_EINVAL; } c->prof = on ? 1 : 0; return FL_OK; }
+
+// summed stage durations (ms) of every profiled call since the last reset; ms[NSTAGE], returns the call count
+extern "C" int fl_stage_ms(FLCtx * c, double * ms, int nstage, int reset) {
+    if (!c) { return FL_EINVAL; }
+    for (auto & ev : c->ev_pending) {
+        TRY(c, hipEventSynchronize(ev[NSTAGE]));
+        for (int i = 0; i < NSTAGE; ++i) { float t = 0.f; TRY(c, hipEventElapsedTime(&t, ev[i], ev[i + 1])); c->stage_ms[i] += t; }
+        c->stage_n++; c->ev_free.push_back(ev);
+    }
+    c->ev_pending.clear();
+    for (int i = 0; i < nstage && i < NSTAGE; ++i) { ms[i] = c->stage_ms[i]; }
+    const int n = (int) c->stage_n;
+    if (reset) { for (double & v : c->stage_ms) { v = 0.0; } c->stage_n = 0; }
+    return n;
 }
 
 extern "C" int fl_debug(FLCtx * c, FLDebug * out) {

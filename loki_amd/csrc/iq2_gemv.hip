@@ -48,7 +48,7 @@ __global__ void __launch_bounds__(256) k_iq2_gemv(const GemvArgs a) {
     const int bpe = a.R / 16;
     const int m = blockIdx.x / bpe;
     const int nact = *a.nact;
-    if (m > nact) { return; }
+    if (m > nact || (m == nact && !a.shared)) { return; }
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rq = (blockIdx.x % bpe) * 4 + wave;
     const bool routed = m < nact;
@@ -133,7 +133,8 @@ __global__ void __launch_bounds__(256) k_iq2_gemv(const GemvArgs a) {
 static hipError_t launch_gemv(const GemvArgs & a, bool gateup, hipStream_t st) {
     if (a.R % 16 != 0 || a.K % (QK * UBLK) != 0 || a.n < 0) { return hipErrorInvalidValue; }
     if (a.n == 0) { return hipSuccess; }
-    const unsigned grid = (unsigned) ((a.max_act + 1) * (a.R / 16));
+    const unsigned grid = (unsigned) ((a.max_act + (a.shared ? 1 : 0)) * (a.R / 16));
+    if (grid == 0) { return hipSuccess; }
     if (gateup) { k_iq2_gemv<true><<<grid, 256, 0, st>>>(a); }
     else { k_iq2_gemv<false><<<grid, 256, 0, st>>>(a); }
     return hipGetLastError();

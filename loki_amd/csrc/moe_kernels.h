@@ -29,6 +29,7 @@ struct GemvArgs {
     int K, R;                        // columns (activation length) and rows of each matrix
     const int * act, * nact, * offsets, * perm;
     int topk, n, P, max_act;         // max_act: launch bound on used experts (host side)
+    int shared;                      // 1: the shared expert runs as the extra slot m == nact (tokens 0..n-1)
     float * out;                     // gate/up: h [P+n][R]; down: o [P+n][R]
     float * dbg0, * dbg1;            // optional gate / up outputs (gate/up launch only)
 };

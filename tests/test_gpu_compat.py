@@ -1,0 +1,185 @@
+"""GPU: the reference-named entry points (fl_ffn_begin / fl_fetch / fl_moe / fl_skip / fl_wide_*) driven the way the
+reference's engine drives them (src/server_core_fused.cpp:793-818 narrow dispatch, :930-949 wide pass), and the
+device-resident block against the committed full-shape golden vector."""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests.golden import gen
+
+pytestmark = pytest.mark.gpu
+
+E, H, KE = 7168, 2048, 8
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def cptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+@pytest.fixture(scope="module")
+def small_layer():
+    """16 routed experts (ggml layout, host) from the deterministic generator, and their device copies."""
+    import torch
+    W, b, gate, up, down, sh = gen.layer(202, 16, E, H)
+    dev = dict(W=torch.from_numpy(W).cuda(), b=torch.from_numpy(b).cuda(),
+               gate=torch.from_numpy(np.concatenate(gate)).cuda(), up=torch.from_numpy(np.concatenate(up)).cuda(),
+               down=torch.from_numpy(np.concatenate(down)).cuda(),
+               sh=[torch.from_numpy(m).cuda() for m in sh])
+    return (W, b, gate, up, down, sh), dev
+
+
+def test_golden_decode_full_on_device(ctx, small_layer):
+    """fl_moe_layer (tiled copies of the generator's experts) reproduces the committed checker output bit for bit."""
+    import torch
+    from loki_amd import MoeLayerWeights
+    z = np.load(os.path.join(GOLDEN, "decode_full.npz"), allow_pickle=False)
+    (W, b, gate, up, down, sh), dev = small_layer
+    mg = H * (E // 256) * 66
+    L = MoeLayerWeights(dev["W"], dev["b"], ctx.pack(dev["gate"], H, E, 16), ctx.pack(dev["up"], H, E, 16),
+                        ctx.pack(dev["down"], E, H, 16), ctx.pack(dev["sh"][0], H, E, 1), ctx.pack(dev["sh"][1], H, E, 1),
+                        ctx.pack(dev["sh"][2], E, H, 1), n_exp=16)
+    assert mg * 16 == dev["gate"].numel()
+    y = ctx.moe_layer(L, torch.from_numpy(z["x"]).cuda())
+    ctx.sync()
+    dbg = ctx.debug()
+    assert np.array_equal(ctx.d2h(dbg.sel, z["sel"].shape, np.int32), z["sel"])
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), z["y"].view(np.uint32))
+
+
+def _flw(dev):
+    from loki_amd import FLW
+    w = FLW()
+    w.gate_inp = dev["W"].data_ptr(); w.probs_b = dev["b"].data_ptr()
+    w.sh_gate, w.sh_up, w.sh_down = (t.data_ptr() for t in dev["sh"])
+    w.gate_f16 = 0
+    return w
+
+
+def _arena(dev, used):
+    """The engine's expert arena for the experts `used`: gate/up/down of each, packed at ggml stride."""
+    import torch
+    mg = H * (E // 256) * 66
+    idx = torch.as_tensor(used, dtype=torch.long)
+    take = lambda t: t.view(16, mg)[idx.cuda()].contiguous().view(-1)
+    return take(dev["gate"]), take(dev["up"]), take(dev["down"])
+
+
+def test_narrow_pass(ctx, small_layer):
+    """fl_ffn_begin -> fl_fetch -> host dispatch (sorted unique experts, slot ids) -> fl_moe, as the engine does;
+    h = routed + shared + ffn_inp with moe_combine's ascending-slot order (src/fused_layer.cu:366-372)."""
+    from loki_amd import FLOut, lib
+    (W, b, gate, up, down, sh), dev = small_layer
+    ctx.set_routing(8, 4, 8, 2.5)
+    n = 3
+    x = gen.uniform(7, 3, (n, E), 2.0); fi = gen.uniform(7, 4, (n, E), 1.0)
+    flw = _flw(dev)
+    ctx.check(lib().fl_ffn_begin(ctx.ctx, ctypes.byref(flw), n, cptr(x), cptr(fi), -1))
+    out = FLOut()
+    lib().fl_fetch(ctx.ctx, n, 1, ctypes.byref(out))
+    sel = np.ctypeslib.as_array(out.sel, shape=(n * KE,)).reshape(n, KE).copy()
+    wts = np.ctypeslib.as_array(out.wts, shape=(n * KE,)).reshape(n, KE).copy()
+    ncur = np.ctypeslib.as_array(out.ncur, shape=(n * E,)).reshape(n, E).copy()
+    _, _, so, wo = orc.router(W, b, x, 8, 4, 8, 2.5)
+    assert np.array_equal(sel, so) and np.array_equal(wts.view(np.uint32), wo.view(np.uint32))
+    assert np.array_equal(ncur, x)
+    used = sorted(set(sel.ravel().tolist()))
+    remap = {e: i for i, e in enumerate(used)}
+    ids = np.array([[remap[e] for e in row] for row in sel], np.int32)
+    ga, ua, da = _arena(dev, used)
+    lib().fl_moe(ctx.ctx, ga.data_ptr(), ua.data_ptr(), da.data_ptr(), len(used), 4, cptr(ids), cptr(f32(wts)), KE, n, ctypes.byref(out))
+    h = np.ctypeslib.as_array(out.h, shape=(n * E,)).reshape(n, E).copy()
+    moe = np.ctypeslib.as_array(out.moe, shape=(n * E,)).reshape(n, E).copy()
+    ref = orc.moe_experts(x, so, wo, gate, up, down, *sh, want=("o", "sh"), n_exp=16)
+    o = ref["o"].reshape(n, KE, E)
+    for t in range(n):
+        v = np.zeros(E, np.float32)
+        for m in range(len(used)):
+            ks = [k for k in range(KE) if ids[t, k] == m]
+            if not ks:
+                continue
+            wt = np.float32(0)
+            for k in ks:
+                wt = np.float32(wt + wts[t, k])
+            v = (v + wt * o[t, ks[0]]).astype(np.float32)
+        assert np.array_equal(moe[t].view(np.uint32), v.view(np.uint32))
+        want = ((v + ref["sh"][t]).astype(np.float32) + fi[t]).astype(np.float32)
+        assert np.array_equal(h[t].view(np.uint32), want.view(np.uint32))
+    # attribution of row 1: w_k * expert output, as the combine added them
+    att = np.empty((KE, E), np.float32)
+    lib().fl_moe_outs(ctx.ctx, 1, cptr(ids[1].copy()), cptr(f32(wts[1])), KE, cptr(att))
+    assert np.array_equal(att.view(np.uint32), (wts[1][:, None] * o[1]).astype(np.float32).view(np.uint32))
+    # fl_skip: h = mo + shared + ffn_inp
+    mo = gen.uniform(7, 9, (n, E), 3.0)
+    lib().fl_skip(ctx.ctx, cptr(mo), n, ctypes.byref(out))
+    hs = np.ctypeslib.as_array(out.h, shape=(n * E,)).reshape(n, E).copy()
+    want = (((np.float32(0) + mo) + ref["sh"]).astype(np.float32) + fi).astype(np.float32)
+    assert np.array_equal(hs.view(np.uint32), want.view(np.uint32))
+
+
+def test_wide_pass(ctx, small_layer):
+    """fl_wide_init -> fl_ffn_begin(wrow) per group -> per arena batch fl_wide_moe (slots of <= 8 (row, k) pairs in the
+    engine's byexp order) -> fl_wide_finish; h = (ffn_inp + shared) + sum_k w_k o_k (src/fused_layer.cu:351-360)."""
+    from loki_amd import FLOut, lib
+    (W, b, gate, up, down, sh), dev = small_layer
+    n, EB = 40, 5
+    assert lib().fl_wide_init(ctx.ctx, 64, KE) == 1
+    x = gen.uniform(8, 3, (n, E), 2.0); fi = gen.uniform(8, 4, (n, E), 1.0)
+    flw = _flw(dev)
+    sels, wtss = [], []
+    out = FLOut()
+    for r0 in range(0, n, 16):   # groups of rows, as the engine's fl_attn(wrow) loop
+        g = min(16, n - r0)
+        ctx.check(lib().fl_ffn_begin(ctx.ctx, ctypes.byref(flw), g, cptr(x[r0:r0 + g].copy()), cptr(fi[r0:r0 + g].copy()), r0))
+        lib().fl_fetch(ctx.ctx, g, 1, ctypes.byref(out))
+        sels.append(np.ctypeslib.as_array(out.sel, shape=(g * KE,)).reshape(g, KE).copy())
+        wtss.append(np.ctypeslib.as_array(out.wts, shape=(g * KE,)).reshape(g, KE).copy())
+    sel, wts = np.concatenate(sels), np.concatenate(wtss)
+    used = sorted(set(sel.ravel().tolist()))
+    byexp = {e: [] for e in used}
+    for i in range(n):
+        for k in range(KE):
+            byexp[sel[i, k]].append((i, k))
+    for bi, b0 in enumerate(range(0, len(used), EB)):
+        batch = used[b0:b0 + EB]
+        par = bi & 1
+        lib().fl_wide_wait(ctx.ctx, par)
+        midx, rows, kidx, wk = [], [], [], []
+        for u, e in enumerate(batch):
+            lst = byexp[e]
+            for i0 in range(0, len(lst), 8):
+                midx.append(u)
+                for j in range(8):
+                    if i0 + j < len(lst):
+                        r, k = lst[i0 + j]; rows.append(r); kidx.append(k); wk.append(wts[r, k])
+                    else:
+                        rows.append(-1); kidx.append(0); wk.append(0.0)
+        ga, ua, da = _arena(dev, batch)
+        lib().fl_wide_moe(ctx.ctx, ga.data_ptr(), ua.data_ptr(), da.data_ptr(), 4, len(batch), cptr(np.int32(midx)),
+                          cptr(np.int32(rows)), cptr(np.int32(kidx)), cptr(f32(wk)), len(midx), KE, par)
+        lib().fl_wide_mark(ctx.ctx, par)
+    lib().fl_wide_finish(ctx.ctx, n, KE, ctypes.byref(out))
+    h = np.ctypeslib.as_array(out.h, shape=(n * E,)).reshape(n, E).copy()
+    moe = np.ctypeslib.as_array(out.moe, shape=(n * E,)).reshape(n, E).copy()
+    ref = orc.moe_experts(x, sel, wts, gate, up, down, *sh, want=("o", "sh"), n_exp=16)
+    o = ref["o"].reshape(n, KE, E)
+    m = np.zeros((n, E), np.float32)
+    for k in range(KE):
+        m = (m + wts[:, k:k + 1] * o[:, k]).astype(np.float32)
+    base = (fi + ref["sh"]).astype(np.float32)
+    assert np.array_equal(moe.view(np.uint32), m.view(np.uint32))
+    assert np.array_equal(h.view(np.uint32), (base + m).astype(np.float32).view(np.uint32))
+    outs = np.empty((KE, E), np.float32)
+    lib().fl_wide_outs(ctx.ctx, 5, KE, cptr(outs))
+    assert np.array_equal(outs.view(np.uint32), (wts[5][:, None] * o[5]).astype(np.float32).view(np.uint32))
+    mo = gen.uniform(8, 9, (n, E), 3.0)
+    lib().fl_wide_skip(ctx.ctx, cptr(mo), n, ctypes.byref(out))
+    hs = np.ctypeslib.as_array(out.h, shape=(n * E,)).reshape(n, E).copy()
+    assert np.array_equal(hs.view(np.uint32), (base + mo).astype(np.float32).view(np.uint32))
