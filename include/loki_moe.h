@@ -75,6 +75,8 @@ double fl_gpu_ms(FLCtx *, int which);                                       /* f
  * ffn-normed rows ncur and the residual ffn_inp as host floats [N][7168] (the reference computes both inside fl_attn,
  * src/fused_layer.cu:498-525). Uses W->gate_inp (F32 [256][7168]), W->probs_b, W->sh_gate/up/down (IQ2_XXS, ggml layout). */
 int fl_ffn_begin(FLCtx *, const FLW * W, int N, const float * ncur, const float * ffn_inp, int wrow);
+/* routed experts behind fl_ffn_begin / fl_moe (default 256, the model's count; FLW carries no count) */
+int fl_set_experts(FLCtx *, int n_exp);
 /* routing rule: DeepSeek-V3 groups (default 8 groups, top-4 groups, top-8, x2.5); n_group = topk_group = 1 is the reference's rule */
 int fl_set_routing(FLCtx *, int n_group, int topk_group, int topk, float scale);
 
@@ -90,7 +92,8 @@ typedef struct FLMoeLayer {
     int n_exp;                 /* routed experts (<= 256) */
     int E, H;                  /* hidden (7168) and expert intermediate (2048) sizes; E, H multiples of 1024 */
 } FLMoeLayer;
-/* y[n][E] = MoE(x[n][E]) on the context's stream (x, y device pointers; asynchronous). n <= 65536. */
+/* y[n][E] = MoE(x[n][E]) on the context's stream (x, y device pointers; asynchronous). n <= 65536.
+ * Allocation extents are checked against the shapes (hipMemGetAddressRange) before any launch. */
 int fl_moe_layer(FLCtx *, const FLMoeLayer * L, const float * x, int n, float * y);
 /* router only: sel/w [n][topk] (device), logits/probs [n][n_exp] may be NULL */
 int fl_route_dev(FLCtx *, const float * gate_inp, const float * probs_b, const float * x, int n, int n_exp, int E,

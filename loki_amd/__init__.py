@@ -53,7 +53,7 @@ class FLOut(ctypes.Structure):
 ABI_SYMBOLS = [
     "fl_init", "fl_attn", "fl_wide_init", "fl_wide_moe", "fl_wide_mark", "fl_wide_wait", "fl_wide_finish", "fl_moe_outs",
     "fl_wide_outs", "fl_wide_skip", "fl_spec", "fl_sketch", "fl_fetch", "fl_moe", "fl_skip", "fl_h2d", "fl_wait_event",
-    "fl_gpu_ms", "fl_ffn_begin", "fl_set_routing", "fl_moe_layer", "fl_route_dev", "fl_dispatch_dev", "fl_quant_q8k_dev",
+    "fl_gpu_ms", "fl_ffn_begin", "fl_set_experts", "fl_set_routing", "fl_moe_layer", "fl_route_dev", "fl_dispatch_dev", "fl_quant_q8k_dev",
     "fl_pack_iq2xxs", "fl_unpack_iq2xxs", "fl_rmsnorm_dev", "fl_synth_iq2xxs", "fl_synth_normal", "fl_probe_exp",
     "fl_debug", "fl_set_debug", "fl_stream", "fl_set_stream", "fl_d2h", "fl_set_profile", "fl_stage_ms", "fl_sync", "fl_last_error", "fl_free",
 ]
@@ -82,6 +82,7 @@ def lib():
             "fl_sync": (I, [P_]),
             "fl_last_error": (ctypes.c_char_p, [P_]),
             "fl_set_routing": (I, [P_, I, I, I, F]),
+            "fl_set_experts": (I, [P_, I]),
             "fl_set_debug": (I, [P_, I]),
             "fl_moe_layer": (I, [P_, ctypes.POINTER(FLMoeLayer), P_, I, P_]),
             "fl_route_dev": (I, [P_, P_, P_, P_, I, I, I, P_, P_, P_, P_]),
@@ -186,6 +187,9 @@ class Context:
 
     def set_routing(self, n_group=8, topk_group=4, topk=8, scale=2.5):
         self.check(lib().fl_set_routing(self.ctx, n_group, topk_group, topk, scale))
+
+    def set_experts(self, n_exp=N_EXPERT):
+        self.check(lib().fl_set_experts(self.ctx, n_exp))
 
     def set_debug(self, capture_gate_up):
         self.check(lib().fl_set_debug(self.ctx, 1 if capture_gate_up else 0))

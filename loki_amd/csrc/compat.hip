@@ -204,7 +204,14 @@ extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur,
     Compat * s = cs(c);
     if (wrow >= 0 && (s->wmax == 0 || wrow + N > s->wmax)) { return fail(c, FL_ERANGE, "wide rows %d..%d exceed fl_wide_init's %d", wrow, wrow + N, s->wmax); }
     const size_t R = (size_t) RMAX * E_;
-    ALLOC(c, s->ncur, R); ALLOC(c, s->fi, R); ALLOC(c, s->logits, RMAX * NEXP_); ALLOC(c, s->probs, RMAX * NEXP_);
+    const int ne = c->n_exp;
+    if (!covers(W->gate_inp, (size_t) ne * E_ * 4) || !covers(W->probs_b, (size_t) ne * 4)) {
+        return fail(c, FL_EINVAL, "router weight or bias allocation is smaller than %d experts x %d", ne, E_);
+    }
+    if (!covers(W->sh_gate, mat_bytes(H_, E_)) || !covers(W->sh_up, mat_bytes(H_, E_)) || !covers(W->sh_down, mat_bytes(E_, H_))) {
+        return fail(c, FL_EINVAL, "shared-expert allocation smaller than one IQ2_XXS matrix");
+    }
+    ALLOC(c, s->ncur, R); ALLOC(c, s->fi, R); ALLOC(c, s->logits, RMAX * ne); ALLOC(c, s->probs, RMAX * ne);
     ALLOC(c, s->sel, RMAX * MAXK); ALLOC(c, s->wts, RMAX * MAXK); ALLOC(c, s->xq, R); ALLOC(c, s->xd, RMAX * (E_ / QK)); ALLOC(c, s->sh_o, R);
     hipStream_t st = c->st;
     TRY(c, hipMemcpyAsync(s->ncur.p, ncur, (size_t) N * E_ * 4, hipMemcpyHostToDevice, st));
@@ -217,7 +224,7 @@ extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur,
         TRY(c, launch_pack_tiled((const uint8_t *) W->sh_down, mg, s->sh_t.p + 2 * mg, mg, E_, H_, 1, st));
         s->sh_key[0] = W->sh_gate; s->sh_key[1] = W->sh_up; s->sh_key[2] = W->sh_down;
     }
-    if (int rc = fl_route_dev(c, (const float *) W->gate_inp, (const float *) W->probs_b, s->ncur.p, N, NEXP_, E_, s->logits.p, s->probs.p, s->sel.p, s->wts.p)) { return rc; }
+    if (int rc = fl_route_dev(c, (const float *) W->gate_inp, (const float *) W->probs_b, s->ncur.p, N, ne, E_, s->logits.p, s->probs.p, s->sel.p, s->wts.p)) { return rc; }
     TRY(c, launch_quant_q8k(s->ncur.p, N, E_, s->xq.p, s->xd.p, st));
     shared_expert(c, s, s->xq.p, s->xd.p, N, s->sh_o.p);
     if (wrow >= 0) {
@@ -255,6 +262,9 @@ extern "C" void fl_moe(FLCtx * c, const void * gate, const void * up, const void
     }
     for (int i = 0; i < n * KE; ++i) {
         if (ids[i] < 0 || ids[i] >= nexp) { std::fprintf(stderr, "[fused] fl_moe: slot id %d outside the arena of %d\n", ids[i], nexp); std::exit(7); }
+    }
+    if (!covers(gate, nexp * mat_bytes(H_, E_)) || !covers(up, nexp * mat_bytes(H_, E_)) || !covers(down, nexp * mat_bytes(E_, H_))) {
+        std::fprintf(stderr, "[fused] fl_moe: an arena allocation is smaller than %d experts\n", nexp); std::exit(7);
     }
     hipStream_t st = c->st; const int P = n * KE;
     CK(hipEventRecord(c->em0, st));
@@ -343,6 +353,9 @@ extern "C" void fl_wide_moe(FLCtx * c, const void * gate, const void * up, const
     for (int e = 0; e < nexp; ++e) { cnt[e + 1] += cnt[e]; }
     const int P = cnt[nexp];
     if (P == 0) { return; }
+    if (!covers(gate, nexp * mat_bytes(H_, E_)) || !covers(up, nexp * mat_bytes(H_, E_)) || !covers(down, nexp * mat_bytes(E_, H_))) {
+        std::fprintf(stderr, "[fused] fl_wide_moe: an arena allocation is smaller than %d experts\n", nexp); std::exit(7);
+    }
     std::vector<int> off(cnt), fillp(cnt.begin(), cnt.end() - 1), perm(P), prow(P), pk(P), act; std::vector<float> pw(P);
     for (int sl = 0; sl < nslots; ++sl) {
         for (int j = 0; j < NB; ++j) {

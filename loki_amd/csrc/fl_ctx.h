@@ -35,6 +35,7 @@ struct FLCtx {
     hipStream_t st = nullptr, own = nullptr; int dev = 0, ncu = 0;
     hipEvent_t em0 = nullptr, em1 = nullptr;
     int n_group = 8, topk_group = 4, topk = 8; float scale = 2.5f;
+    int n_exp = 256;   // routed experts behind the reference-named entry points (FLW carries no count)
     double ms_moe = 0.0;
     std::string err;
     int dbg_gu = 0;
@@ -57,6 +58,13 @@ inline int fail(FLCtx * c, int code, const char * fmt, ...) {
 }
 #define TRY(c, x) do { hipError_t e_ = (x); if (e_ != hipSuccess) { return fail((c), FL_EHIP, "%s: %s", #x, hipGetErrorString(e_)); } } while (0)
 #define ALLOC(c, buf, n) do { if ((buf).ensure(n) != hipSuccess) { (void) hipGetLastError(); return fail((c), FL_ENOMEM, "device allocation of %zu elements failed", (size_t) (n)); } } while (0)
+
+// true unless the HIP allocation holding p is known to end before p + bytes (pointers HIP cannot resolve pass)
+inline bool covers(const void * p, size_t bytes) {
+    hipDeviceptr_t base = nullptr; size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t) p) != hipSuccess) { (void) hipGetLastError(); return true; }
+    return (const char *) p + bytes <= (const char *) base + size;
+}
 
 static std::vector<hipEvent_t> * prof_begin(FLCtx * c) {
     if (!c->prof) { return nullptr; }

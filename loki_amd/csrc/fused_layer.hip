@@ -72,6 +72,11 @@ extern "C" int fl_set_routing(FLCtx * c, int n_group, int topk_group, int topk, 
     }
     c->n_group = n_group; c->topk_group = topk_group; c->topk = topk; c->scale = scale; return FL_OK;
 }
+extern "C" int fl_set_experts(FLCtx * c, int n_exp) {
+    if (!c) { return FL_EINVAL; }
+    if (n_exp <= 0 || n_exp > NEXP_MAX) { return fail(c, FL_EINVAL, "n_exp %d outside 1..%d", n_exp, NEXP_MAX); }
+    c->n_exp = n_exp; return FL_OK;
+}
 extern "C" int fl_set_debug(FLCtx * c, int capture) { if (!c) { return FL_EINVAL; } c->dbg_gu = capture ? 1 : 0; return FL_OK; }
 
 // ================================================================ building blocks
@@ -91,6 +96,9 @@ extern "C" int fl_route_dev(FLCtx * c, const float * W, const float * bias, cons
     if (!W || !bias || !x || !sel || !w) { return fail(c, FL_EINVAL, "null pointer"); }
     if (E <= 0 || E % 256) { return fail(c, FL_EINVAL, "E = %d must be a positive multiple of 256", E); }
     if (int rc = check_rule(c, n_exp)) { return rc; }
+    if (!covers(W, (size_t) n_exp * E * 4) || !covers(bias, (size_t) n_exp * 4) || !covers(x, (size_t) n * E * 4)) {
+        return fail(c, FL_EINVAL, "router weight, bias or x allocation smaller than its shape (%d experts, %d rows of %d)", n_exp, n, E);
+    }
     if (!logits) { ALLOC(c, c->logits, (size_t) n * n_exp); logits = c->logits.p; }
     TRY(c, launch_router_logits(W, x, n, n_exp, E, logits, c->st));
     TRY(c, launch_router_select(logits, bias, n, n_exp, c->n_group, c->topk_group, c->topk, c->scale, probs, sel, w, c->st));
@@ -172,6 +180,14 @@ extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, in
         return fail(c, FL_EINVAL, "null pointer in the layer or x / y");
     }
     const int E = L->E, H = L->H, ne = L->n_exp, tk = c->topk, P = n * tk;
+    {
+        const size_t mg = (size_t) H * (E / 256) * IQ2B;   // one gate/up (and one down) matrix
+        if (!covers(L->gate_inp, (size_t) ne * E * 4) || !covers(L->probs_b, (size_t) ne * 4) || !covers(x, (size_t) n * E * 4) ||
+            !covers(y, (size_t) n * E * 4) || !covers(L->gate_exps, ne * mg) || !covers(L->up_exps, ne * mg) || !covers(L->down_exps, ne * mg) ||
+            !covers(L->sh_gate, mg) || !covers(L->sh_up, mg) || !covers(L->sh_down, mg)) {
+            return fail(c, FL_EINVAL, "an allocation of the layer, x or y is smaller than its shape (%d experts, E %d, H %d, n %d)", ne, E, H, n);
+        }
+    }
     const size_t rows = (size_t) P + n;
     ALLOC(c, c->xq, (size_t) n * E); ALLOC(c, c->xd, (size_t) n * (E / 256));
     ALLOC(c, c->logits, (size_t) n * ne); ALLOC(c, c->probs, (size_t) n * ne);

@@ -25,7 +25,7 @@ def cptr(a):
 
 
 @pytest.fixture(scope="module")
-def small_layer():
+def small_layer(ctx):
     """16 routed experts (ggml layout, host) from the deterministic generator, and their device copies."""
     import torch
     W, b, gate, up, down, sh = gen.layer(202, 16, E, H)
@@ -33,7 +33,9 @@ def small_layer():
                gate=torch.from_numpy(np.concatenate(gate)).cuda(), up=torch.from_numpy(np.concatenate(up)).cuda(),
                down=torch.from_numpy(np.concatenate(down)).cuda(),
                sh=[torch.from_numpy(m).cuda() for m in sh])
-    return (W, b, gate, up, down, sh), dev
+    ctx.set_experts(16)   # the reference-named entry points route over 16 experts in these tests
+    yield (W, b, gate, up, down, sh), dev
+    ctx.set_experts()
 
 
 def test_golden_decode_full_on_device(ctx, small_layer):
