@@ -125,9 +125,11 @@ typedef struct FLDebug {
 } FLDebug;
 int fl_debug(FLCtx *, FLDebug * out);
 int fl_set_debug(FLCtx *, int capture_gate_up);
+/* 1 (default): fl_moe_layer runs a decode batch (n <= 8, E 7168, H 2048) as one cooperative launch; 0: one launch per pass */
+int fl_set_fused(FLCtx *, int on);
 
-/* stage timing with HIP events on the context's stream: stages 0..7 = quant_x, router_logits, router_select, dispatch,
- * gate_up, quant_h, down, combine. fl_stage_ms waits for the profiled calls and returns their count (summed ms in ms[]). */
+/* stage timing with HIP events on the context's stream: stages 0..5 = quant_x, router_logits, router_select, dispatch,
+ * gate_up (with SwiGLU and Q8_K(h)), down (with the combine). fl_stage_ms waits for the profiled calls and returns their count (summed ms in ms[]). */
 int fl_set_profile(FLCtx *, int on);
 int fl_stage_ms(FLCtx *, double * ms, int nstage, int reset);
 

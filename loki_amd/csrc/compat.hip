@@ -155,28 +155,36 @@ static size_t mat_bytes(int R, int K) { return (size_t) R * (K / QK) * IQ2B; }
 static void shared_expert(FLCtx * c, Compat * s, const int8_t * xq, const float * xd, int N, float * out) {
     const size_t mg = mat_bytes(H_, E_);
     FALLOC(s->h, (size_t) N * H_); FALLOC(s->hq, (size_t) N * H_); FALLOC(s->hd, (size_t) N * (H_ / QK));
-    GemvArgs a{};
-    a.sh0 = s->sh_t.p; a.sh1 = s->sh_t.p + mg; a.aq = xq; a.ad = xd; a.K = E_; a.R = H_;
-    a.act = zero_int(c); a.nact = zero_int(c); a.offsets = zero_int(c); a.perm = zero_int(c);
-    a.topk = 1; a.n = N; a.P = 0; a.max_act = 0; a.shared = 1; a.out = s->h.p;
-    FCK(launch_gemv_gateup(a, c->st));
-    FCK(launch_quant_q8k(s->h.p, N, H_, s->hq.p, s->hd.p, c->st));
-    GemvArgs d = a; d.sh0 = s->sh_t.p + 2 * mg; d.sh1 = nullptr; d.aq = s->hq.p; d.ad = s->hd.p; d.K = H_; d.R = E_; d.out = out;
-    FCK(launch_gemv_down(d, c->st));
+    CK(ensure_expert_scratch(c, (size_t) N, E_, H_) == FL_OK ? hipSuccess : hipErrorOutOfMemory);
+    ExpertArgs a = expert_args(c, N, 0, 1);
+    a.sh[0] = s->sh_t.p; a.sh[1] = s->sh_t.p + mg; a.aq = xq; a.ad = xd; a.K = E_; a.R = H_; a.nmat = 2;
+    a.act = zero_int(c); a.nact = zero_int(c); a.offsets = zero_int(c); a.perm = zero_int(c); a.topk = 1;
+    a.h = s->h.p; a.hq = s->hq.p; a.hd = s->hd.p;
+    expert_counters(c, a, 0);
+    FCK(launch_experts_gateup(a, c->ncu, c->st));
+    ExpertArgs d = a;
+    d.sh[0] = s->sh_t.p + 2 * mg; d.sh[1] = nullptr; d.aq = s->hq.p; d.ad = s->hd.p; d.K = H_; d.R = E_; d.nmat = 1;
+    d.h = nullptr; d.hq = nullptr; d.hd = nullptr; d.o = out; d.y = nullptr;
+    expert_counters(c, d, 1);
+    FCK(launch_experts_down(d, c->ncu, c->st));
 }
 
 // routed experts of an arena (tiled copy ag/au/ad) for the pairs described by offsets/perm/act/nact -> o [P][E]
 static void routed_experts(FLCtx * c, Compat * s, const int8_t * xq, const float * xd, int n, int P, int KE, int nexp,
                            const int * act, const int * nact, const int * offsets, const int * perm, float * o) {
     FALLOC(s->h, (size_t) P * H_); FALLOC(s->hq, (size_t) P * H_); FALLOC(s->hd, (size_t) P * (H_ / QK));
-    GemvArgs a{};
-    a.w0 = s->ag.p; a.w1 = s->au.p; a.estride = mat_bytes(H_, E_); a.aq = xq; a.ad = xd; a.K = E_; a.R = H_;
-    a.act = act; a.nact = nact; a.offsets = offsets; a.perm = perm; a.topk = KE; a.n = n; a.P = P;
-    a.max_act = std::min(nexp, P); a.shared = 0; a.out = s->h.p;
-    FCK(launch_gemv_gateup(a, c->st));
-    FCK(launch_quant_q8k(s->h.p, P, H_, s->hq.p, s->hd.p, c->st));
-    GemvArgs d = a; d.w0 = s->ad.p; d.w1 = nullptr; d.estride = mat_bytes(E_, H_); d.aq = s->hq.p; d.ad = s->hd.p; d.K = H_; d.R = E_; d.out = o;
-    FCK(launch_gemv_down(d, c->st));
+    CK(ensure_expert_scratch(c, (size_t) P + n, E_, H_) == FL_OK ? hipSuccess : hipErrorOutOfMemory);
+    ExpertArgs a = expert_args(c, n, P, 0);
+    a.w[0] = s->ag.p; a.w[1] = s->au.p; a.estride = mat_bytes(H_, E_); a.aq = xq; a.ad = xd; a.K = E_; a.R = H_; a.nmat = 2;
+    a.act = act; a.nact = nact; a.offsets = offsets; a.perm = perm; a.topk = KE;
+    a.h = s->h.p; a.hq = s->hq.p; a.hd = s->hd.p;
+    expert_counters(c, a, 0);
+    FCK(launch_experts_gateup(a, c->ncu, c->st));
+    ExpertArgs d = a;
+    d.w[0] = s->ad.p; d.w[1] = nullptr; d.estride = mat_bytes(E_, H_); d.aq = s->hq.p; d.ad = s->hd.p; d.K = H_; d.R = E_; d.nmat = 1;
+    d.h = nullptr; d.hq = nullptr; d.hd = nullptr; d.o = o; d.y = nullptr;
+    expert_counters(c, d, 1);
+    FCK(launch_experts_down(d, c->ncu, c->st));
 }
 
 static void pack_arena(FLCtx * c, Compat * s, const void * gate, const void * up, const void * down, int nexp) {

@@ -46,10 +46,17 @@ struct FLCtx {
     int prof = 0;
     std::vector<std::vector<hipEvent_t>> ev_free, ev_pending;
     double stage_ms[16] = {0}; long stage_n = 0;
-    int zero_dev_init = 0; DBuf<int> zero_i;   // a device int 0 (shared-expert-only launches read nact = 0)
+    int zero_dev_init = 0; DBuf<int> zero_i;
+    DBuf<float> terms; DBuf<unsigned> cnt;   // per-pass expert kernels: (unused) term scratch, self-resetting counters
+    DBuf<uint4> tab;                         // LDS table image (build_table_image)
+    // single-launch decode block: counters, epoch flags, wait-timeout word; fused = 0 forces the per-pass kernels
+    DBuf<unsigned> dcnt, dflags; DBuf<int> derr; unsigned epoch = 0; int fused = 1; int dec_grid = -1;
     struct Compat * compat = nullptr;          // reference-API state (compat.hip), created on first use
 };
-static const int NSTAGE = 8;   // quant_x, router_logits, router_select, dispatch, gate_up, quant_h, down, combine
+static const int NSTAGE = 6;   // quant_x, router_logits, router_select, dispatch, gate_up (+SwiGLU, Q8_K(h)), down (+combine)
+// counters of the persistent expert kernels: per (expert slot, row group) and per h block / combine row group
+static const size_t CNT_RG = (size_t) (lk::NEXP_MAX + 1) * 112;           // 112 = 7168 / 64 row groups (the largest R)
+static const size_t CNT_ALL = 2 * (2 * CNT_RG + 2);                        // gate/up and down sets: cnt_rg, cnt_2, queue[2]
 
 inline int fail(FLCtx * c, int code, const char * fmt, ...) {
     char buf[512]; va_list ap; va_start(ap, fmt); std::vsnprintf(buf, sizeof buf, fmt, ap); va_end(ap);
@@ -79,4 +86,11 @@ static std::vector<hipEvent_t> * prof_begin(FLCtx * c) {
 static void prof_mark(FLCtx * c, std::vector<hipEvent_t> * ev, int i) { if (ev) { (void) hipEventRecord((*ev)[i], c->st); } }
 
 void compat_free(FLCtx * c);   // compat.hip
+int ensure_expert_scratch(FLCtx * c, size_t rows, int E, int H);   // fused_layer.hip
+lk::ExpertArgs expert_args(FLCtx * c, int n, int P, int shared);
+// counter sets of the two persistent kernels inside FLCtx::cnt
+inline void expert_counters(FLCtx * c, lk::ExpertArgs & a, int down) {
+    unsigned * base = c->cnt.p + (down ? 2 * CNT_RG + 2 : 0);
+    a.cnt_rg = base; a.cnt_2 = base + CNT_RG; a.queue = base + 2 * CNT_RG;
+}
 

@@ -41,7 +41,8 @@ extern "C" void fl_free(FLCtx * c) {
     c->xq.release(); c->hq.release(); c->xd.release(); c->logits.release(); c->probs.release(); c->wts.release();
     c->h.release(); c->hd.release(); c->o.release(); c->g.release(); c->u.release();
     c->sel.release(); c->counts.release(); c->offsets.release(); c->perm.release(); c->inv.release(); c->act.release(); c->nact.release();
-    compat_free(c); c->zero_i.release();
+    compat_free(c); c->zero_i.release(); c->terms.release(); c->cnt.release();
+    c->tab.release(); c->dcnt.release(); c->dflags.release(); c->derr.release();
     for (auto & v : c->ev_free) { for (auto e : v) { (void) hipEventDestroy(e); } }
     for (auto & v : c->ev_pending) { for (auto e : v) { (void) hipEventDestroy(e); } }
     (void) hipEventDestroy(c->em0); (void) hipEventDestroy(c->em1); (void) hipStreamDestroy(c->own);
@@ -62,7 +63,20 @@ extern "C" int fl_d2h(FLCtx * c, void * host, const void * dev, size_t bytes) {
     TRY(c, hipStreamSynchronize(c->st));
     return FL_OK;
 }
-extern "C" int fl_sync(FLCtx * c) { if (!c) { return FL_EINVAL; } TRY(c, hipStreamSynchronize(c->st)); return FL_OK; }
+// waits for the context's stream, then reports a wait timeout of the single-launch decode block (and clears it)
+extern "C" int fl_sync(FLCtx * c) {
+    if (!c) { return FL_EINVAL; }
+    TRY(c, hipStreamSynchronize(c->st));
+    if (c->derr.p) {
+        int e = 0;
+        TRY(c, hipMemcpy(&e, c->derr.p, sizeof e, hipMemcpyDeviceToHost));
+        if (e) {
+            TRY(c, hipMemset(c->derr.p, 0, sizeof e));
+            return fail(c, FL_EHIP, "decode block: a device-wide wait timed out (code %d); its outputs are invalid", e);
+        }
+    }
+    return FL_OK;
+}
 extern "C" const char * fl_last_error(FLCtx * c) { return c ? c->err.c_str() : "null context"; }
 
 extern "C" int fl_set_routing(FLCtx * c, int n_group, int topk_group, int topk, float scale) {
@@ -78,11 +92,13 @@ extern "C" int fl_set_experts(FLCtx * c, int n_exp) {
     c->n_exp = n_exp; return FL_OK;
 }
 extern "C" int fl_set_debug(FLCtx * c, int capture) { if (!c) { return FL_EINVAL; } c->dbg_gu = capture ? 1 : 0; return FL_OK; }
+extern "C" int fl_set_fused(FLCtx * c, int on) { if (!c) { return FL_EINVAL; } c->fused = on ? 1 : 0; return FL_OK; }
 
 // ================================================================ building blocks
 static int check_rule(FLCtx * c, int n_exp) {
     if (n_exp <= 0 || n_exp > NEXP_MAX) { return fail(c, FL_EINVAL, "n_exp %d outside 1..%d", n_exp, NEXP_MAX); }
     if (n_exp % c->n_group) { return fail(c, FL_EINVAL, "n_exp %d not divisible by n_group %d", n_exp, c->n_group); }
+    if (c->n_group > 64) { return fail(c, FL_EINVAL, "n_group %d above 64", c->n_group); }
     const int per = n_exp / c->n_group;
     if (per < 2 || c->topk > c->topk_group * per) { return fail(c, FL_EINVAL, "top-%d cannot be drawn from %d groups of %d", c->topk, c->topk_group, per); }
     return FL_OK;
@@ -167,6 +183,40 @@ extern "C" int fl_probe_exp(FLCtx * c, const float * x, float * y, int64_t n, in
     return FL_OK;
 }
 
+// ================================================================ persistent expert kernels: scratch and counters
+// block-term scratch sized for `rows` slots of both passes; the self-resetting counters are zeroed once, here
+int ensure_expert_scratch(FLCtx * c, size_t rows, int E, int H) {
+    const size_t need = std::max(experts_terms_floats(2, (int) rows, H, E), experts_terms_floats(1, (int) rows, E, H));
+    ALLOC(c, c->terms, need);
+    if (!c->cnt.p) {
+        ALLOC(c, c->cnt, CNT_ALL);
+        TRY(c, hipMemset(c->cnt.p, 0, CNT_ALL * sizeof(unsigned)));
+        TRY(c, experts_init());
+    }
+    if (!c->tab.p) {
+        ALLOC(c, c->tab, TAB_BYTES / 16);
+        TRY(c, build_table_image(c->tab.p, c->st));
+    }
+    return FL_OK;
+}
+ExpertArgs expert_args(FLCtx * c, int n, int P, int shared) {
+    ExpertArgs a{};
+    a.n = n; a.P = P; a.shared = shared; a.terms = c->terms.p; a.tab = c->tab.p;
+    return a;
+}
+
+// the single-launch decode block is available (cooperative launch, one resident workgroup per CU)
+static bool decode_ready(FLCtx * c) {
+    if (c->dec_grid < 0) {
+        int coop = 0;
+        if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, c->dev) != hipSuccess || !coop) { (void) hipGetLastError(); c->dec_grid = 0; return false; }
+        int g = 0;
+        if (decode_init(c->ncu, &g) != hipSuccess) { (void) hipGetLastError(); g = 0; }
+        c->dec_grid = g;
+    }
+    return c->dec_grid > 0;
+}
+
 // ================================================================ the device-resident block
 extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, float * y) {
     if (!c) { return FL_EINVAL; }
@@ -189,15 +239,41 @@ extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, in
         }
     }
     const size_t rows = (size_t) P + n;
+    const bool fused = c->fused && n <= 8 && E == 7168 && H == 2048 && c->n_group <= 64 && decode_ready(c);
     ALLOC(c, c->xq, (size_t) n * E); ALLOC(c, c->xd, (size_t) n * (E / 256));
     ALLOC(c, c->logits, (size_t) n * ne); ALLOC(c, c->probs, (size_t) n * ne);
     ALLOC(c, c->sel, P); ALLOC(c, c->wts, P); ALLOC(c, c->perm, P); ALLOC(c, c->inv, P);
     ALLOC(c, c->counts, ne); ALLOC(c, c->offsets, ne + 1); ALLOC(c, c->act, ne); ALLOC(c, c->nact, 1);
     ALLOC(c, c->h, rows * H); ALLOC(c, c->hq, rows * H); ALLOC(c, c->hd, rows * (H / 256)); ALLOC(c, c->o, rows * E);
-    if (c->dbg_gu) { ALLOC(c, c->g, rows * H); ALLOC(c, c->u, rows * H); }
+    if (c->dbg_gu || fused) { ALLOC(c, c->g, rows * H); ALLOC(c, c->u, rows * H); }
+    if (int rc = ensure_expert_scratch(c, rows, E, H)) { return rc; }
     c->last_n = n; c->last_P = P;
     hipStream_t st = c->st;
     std::vector<hipEvent_t> * ev = prof_begin(c);
+    if (fused) {
+        if (!c->dcnt.p) {
+            ALLOC(c, c->dcnt, DEC_CNT); ALLOC(c, c->dflags, DEC_FLAGS); ALLOC(c, c->derr, 1);
+            TRY(c, hipMemsetAsync(c->dcnt.p, 0, DEC_CNT * sizeof(unsigned), st));
+            TRY(c, hipMemsetAsync(c->derr.p, 0, sizeof(int), st));
+        }
+        if (++c->epoch == 1) { TRY(c, hipMemsetAsync(c->dflags.p, 0, DEC_FLAGS * sizeof(unsigned), st)); }   // first use, or the epoch wrapped
+        DecodeArgs d{};
+        d.tab = c->tab.p; d.x = x; d.n = n;
+        d.Wr = L->gate_inp; d.bias = L->probs_b; d.n_exp = ne; d.n_group = c->n_group; d.topk_group = c->topk_group; d.topk = tk; d.scale = c->scale;
+        d.gate = (const uint8_t *) L->gate_exps; d.up = (const uint8_t *) L->up_exps; d.down = (const uint8_t *) L->down_exps;
+        d.estride = (size_t) H * (E / 256) * IQ2B;
+        d.sh_gate = (const uint8_t *) L->sh_gate; d.sh_up = (const uint8_t *) L->sh_up; d.sh_down = (const uint8_t *) L->sh_down;
+        d.E = E; d.H = H;
+        d.xq = c->xq.p; d.xd = c->xd.p; d.logits = c->logits.p; d.probs = c->probs.p; d.sel = c->sel.p; d.wts = c->wts.p;
+        d.counts = c->counts.p; d.offsets = c->offsets.p; d.perm = c->perm.p; d.inv = c->inv.p; d.act = c->act.p; d.nact = c->nact.p;
+        d.g = c->g.p; d.u = c->u.p; d.h = c->h.p; d.hq = c->hq.p; d.hd = c->hd.p; d.o = c->o.p; d.y = y;
+        d.cnt = c->dcnt.p; d.flags = c->dflags.p; d.epoch = c->epoch; d.err = c->derr.p;
+        // stages: the whole block is one launch, reported as stage 4; the others are empty
+        for (int i = 0; i <= 4; ++i) { prof_mark(c, ev, i); }
+        TRY(c, launch_moe_decode(d, c->dec_grid, st));
+        prof_mark(c, ev, 5); prof_mark(c, ev, 6);
+        return FL_OK;
+    }
     prof_mark(c, ev, 0);
     TRY(c, launch_quant_q8k(x, n, E, c->xq.p, c->xd.p, st));
     prof_mark(c, ev, 1);
@@ -207,25 +283,24 @@ extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, in
     prof_mark(c, ev, 3);
     TRY(c, launch_dispatch(c->sel.p, P, ne, c->counts.p, c->offsets.p, c->perm.p, c->inv.p, c->act.p, c->nact.p, st));
     prof_mark(c, ev, 4);
-    GemvArgs a{};
-    a.w0 = (const uint8_t *) L->gate_exps; a.w1 = (const uint8_t *) L->up_exps; a.estride = (size_t) H * (E / 256) * IQ2B;
-    a.sh0 = (const uint8_t *) L->sh_gate; a.sh1 = (const uint8_t *) L->sh_up;
-    a.aq = c->xq.p; a.ad = c->xd.p; a.K = E; a.R = H;
-    a.act = c->act.p; a.nact = c->nact.p; a.offsets = c->offsets.p; a.perm = c->perm.p;
-    a.topk = tk; a.n = n; a.P = P; a.max_act = std::min(ne, P); a.shared = 1;
-    a.out = c->h.p; a.dbg0 = c->dbg_gu ? c->g.p : nullptr; a.dbg1 = c->dbg_gu ? c->u.p : nullptr;
-    TRY(c, launch_gemv_gateup(a, st));
+    ExpertArgs a = expert_args(c, n, P, 1);
+    a.w[0] = (const uint8_t *) L->gate_exps; a.w[1] = (const uint8_t *) L->up_exps; a.estride = (size_t) H * (E / 256) * IQ2B;
+    a.sh[0] = (const uint8_t *) L->sh_gate; a.sh[1] = (const uint8_t *) L->sh_up;
+    a.aq = c->xq.p; a.ad = c->xd.p; a.K = E; a.R = H; a.nmat = 2;
+    a.act = c->act.p; a.nact = c->nact.p; a.offsets = c->offsets.p; a.perm = c->perm.p; a.topk = tk;
+    a.h = c->h.p; a.hq = c->hq.p; a.hd = c->hd.p;
+    a.gdbg = c->dbg_gu ? c->g.p : nullptr; a.udbg = c->dbg_gu ? c->u.p : nullptr;
+    expert_counters(c, a, 0);
+    TRY(c, launch_experts_gateup(a, c->ncu, st));
     prof_mark(c, ev, 5);
-    TRY(c, launch_quant_q8k(c->h.p, (int64_t) rows, H, c->hq.p, c->hd.p, st));
+    ExpertArgs d = a;
+    d.w[0] = (const uint8_t *) L->down_exps; d.w[1] = nullptr; d.sh[0] = (const uint8_t *) L->sh_down; d.sh[1] = nullptr;
+    d.aq = c->hq.p; d.ad = c->hd.p; d.K = H; d.R = E; d.nmat = 1;
+    d.h = nullptr; d.hq = nullptr; d.hd = nullptr; d.gdbg = nullptr; d.udbg = nullptr;
+    d.o = c->o.p; d.inv = c->inv.p; d.wts = c->wts.p; d.y = y;
+    expert_counters(c, d, 1);
+    TRY(c, launch_experts_down(d, c->ncu, st));
     prof_mark(c, ev, 6);
-    GemvArgs d = a;
-    d.w0 = (const uint8_t *) L->down_exps; d.w1 = nullptr; d.estride = (size_t) E * (H / 256) * IQ2B;
-    d.sh0 = (const uint8_t *) L->sh_down; d.sh1 = nullptr; d.aq = c->hq.p; d.ad = c->hd.p; d.K = H; d.R = E;
-    d.out = c->o.p; d.dbg0 = nullptr; d.dbg1 = nullptr;
-    TRY(c, launch_gemv_down(d, st));
-    prof_mark(c, ev, 7);
-    TRY(c, launch_combine(c->o.p, c->inv.p, c->wts.p, n, tk, E, P, nullptr, y, nullptr, st));
-    prof_mark(c, ev, 8);
     return FL_OK;
 }
 

@@ -1,147 +1,252 @@
-// iq2_gemv.hip -- IQ2_XXS x Q8_K expert mat-vecs for the routed + shared experts, and the weighted combine.
+// iq2_gemv.hip -- IQ2_XXS x Q8_K expert mat-vecs (routed + shared experts) as persistent kernels, with the SwiGLU +
+// Q8_K(h) epilogue (gate/up) and the weighted combine (down) fused in.
 //
-// Reference: tc_matvec<F_IQ2> (src/fused_layer.cu:178-202; launches :604-608) dequantises 16 rows x 8 activation rows
-// through shared memory into mma.m16n8k32 int8 tiles, split-K, then swiglu_q8 (:334-341) and moe_combine (:366-372).
-// Here, for the few tokens per expert of decode:
-//   * one wave owns 4 rows of one expert's matrix and streams its tiled units (1056 B: 4 rows x 4 blocks) with one
-//     16-byte load per lane; lane l holds qs bytes [16c, 16c+16) of block b of row r (r = l/16, b = l/4 % 4, c = l % 4),
-//     i.e. sub-blocks 2c and 2c+1, and dequantises them once into 64 signed int8 weights in registers;
-//   * every token routed to the expert then costs 16 v_dot4_i32_i8 per lane; the 4 lanes of a block add their
-//     (2*(a1>>28)+1)-scaled integer sums (exact), the block term (d_w*d_x)*bsum is formed, and each row accumulates its
-//     block terms in ascending block order in fp32 -- the order of ggml_vec_dot_iq2_xxs_q8_K -- then * 0.125. The
-//     outputs are therefore bit-identical to the CPU checker's;
-//   * gate and up run in the same wave and the epilogue writes h = silu(g) * u (the exp contract), so the gate/up
-//     outputs never travel to HBM; the down pass writes o per (token, k) slot and the combine adds w_k * o_k in k order
-//     plus the shared expert (src/server_core_fused.cpp:970-975).
-// Token lists come from the device dispatch (offsets/perm); the shared expert is the extra expert slot m == nact.
-#include "moe_common.h"
+// Reference: tc_matvec<F_IQ2> (src/fused_layer.cu:178-202; launches :604-608) stages 16 rows x 4 blocks through shared
+// memory into mma.m16n8k32 int8 tiles with split-K partials, then swiglu_q8 (:334-341) and moe_combine (:366-372) run as
+// separate kernels. Here, for the few tokens per expert of decode:
+//   * One workgroup per CU fills the bank-replicated codebook/sign tables (64 KB of LDS) once; its waves then take tasks
+//     round-robin across all workgroups (task tk on workgroup tk % grid). A task is (expert slot, 16 rows): lane
+//     4 r + q owns row r and the blocks j = 4 jj + q, streamed with non-temporal 16-byte loads PD blocks ahead (tiled
+//     layout, moe_common.h). Gate and up of the same rows are streamed interleaved in the same task.
+//   * Per block a lane dequantises its row's 8 sub-blocks into signed int8 (two replicated-table lookups and two
+//     v_xad_u32 per 8 weights), runs v_dot4_i32_i8 against each token's Q8_K values (staged in LDS) into 8 independent
+//     accumulators, and forms the exact integer block sum sum_ib (2 nibble + 1) * sumi and the block term
+//     (d_w * d_x) * bsum -- the arithmetic of ggml_vec_dot_iq2_xxs_q8_K.
+//   * At every step the 4 lanes of a quad hold 4 consecutive blocks of one row, so the row total advances in block order
+//     through 4 quad broadcasts (DPP) and finally * 0.125: every output is bit-identical to the CPU checker and no
+//     partial sum leaves the wave.
+//   * Gate/up writes h = silu(g) * u; the last task of a 256-row block (device-scope counter) quantises that block of h
+//     to Q8_K for every slot of the expert. Down writes o; the last expert of a row group computes
+//     y = sum_k w_k o_k (k order) + shared (src/server_core_fused.cpp:970-975) for every token.
+// h and o cross workgroups inside a launch, so they move with agent-scope relaxed atomic stores/loads: the XCDs' L2s are
+// not coherent with each other, and an agent-scope fence would write back / invalidate a whole L2. Counters reset
+// themselves (the last arriver writes 0), so a launch needs no clearing pass and can be replayed.
+#include "moe_device.h"
 #include "moe_kernels.h"
 
 namespace lk {
 
-constexpr int GEMV_TT = 8;   // tokens per register tile
+struct TaskPtr {
+    const uint8_t * q[2]; const uint8_t * d[2];   // the task's qs / d bases (uniform) of matrix 0 / 1 at step jj = 0
+};
 
-// 64 signed weights of sub-blocks (a0, a1) and (b0, b1) into w[16] (4 weights per int), scales 2*(a1>>28)+1
-__device__ __forceinline__ void dequant_chunk(const Iq2Lds & tab, const uint4 & q, int * w, int & ls0, int & ls1) {
+template <int NR, int PD, class G, int NMAT>
+__device__ __forceinline__ void issue(const TaskPtr & tp, uint32_t lq, uint32_t ld, int s, uint4 (&pf)[NR][4], uint16_t (&pd)[NR], int slot) {
+    const int mat = NMAT == 2 ? (s & 1) : 0, jj = NMAT == 2 ? (s >> 1) : s;
+    const uint8_t * qb = tp.q[mat] + (size_t) jj * (G::QS * 4096);
 #pragma unroll
-    for (int l = 0; l < 4; ++l) { iq2_group(tab, q.x, q.y, l, w[2 * l], w[2 * l + 1]); }
-#pragma unroll
-    for (int l = 0; l < 4; ++l) { iq2_group(tab, q.z, q.w, l, w[8 + 2 * l], w[8 + 2 * l + 1]); }
-    ls0 = 2 * (int) (q.y >> 28) + 1; ls1 = 2 * (int) (q.w >> 28) + 1;
+    for (int c = 0; c < 4; ++c) { pf[slot][c] = load_nt(qb + lq + c * 1024); }
+    pd[slot] = *gptr(reinterpret_cast<const uint16_t *>(tp.d[mat] + (size_t) jj * (G::QS * 128) + ld));
 }
 
-__device__ __forceinline__ int chunk_dot(const int * w, const int * xv, int ls0, int ls1) {
-    int s0 = 0, s1 = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) { s0 = __builtin_amdgcn_sdot4(w[j], xv[j], s0, false); }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) { s1 = __builtin_amdgcn_sdot4(w[8 + j], xv[8 + j], s1, false); }
-    return ls0 * s0 + ls1 * s1;
-}
-
-template <bool GATEUP>
-__global__ void __launch_bounds__(256) k_iq2_gemv(const GemvArgs a) {
+// one tile of T tokens (slots slot0 .. slot0 + T - 1) of a task: stream the lane's blocks (gate and up interleaved),
+// fold each step's 4 blocks into the row totals, write h or o
+template <bool GATEUP, class G, int T, int PD, bool XWG>
+__device__ __forceinline__ void run_tile(const ExpertArgs & a, const uint8_t * lds, uint8_t * xs, const TaskPtr & tp,
+                                         uint32_t lq, uint32_t ld, bool routed, int slot0, int row, int q, uint32_t rep) {
 #pragma clang fp contract(off)
-    __shared__ Iq2Lds tab;
-    iq2_lds_fill(tab);
-    __syncthreads();
-    const int bpe = a.R / 16;
-    const int m = blockIdx.x / bpe;
-    const int nact = *a.nact;
-    if (m > nact || (m == nact && !a.shared)) { return; }
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int rq = (blockIdx.x % bpe) * 4 + wave;
-    const bool routed = m < nact;
-    const uint8_t * W0; const uint8_t * W1 = nullptr; int s0, cnt;
-    if (routed) {
-        const int e = a.act[m];
-        W0 = a.w0 + (size_t) e * a.estride; if (GATEUP) { W1 = a.w1 + (size_t) e * a.estride; }
-        s0 = a.offsets[e]; cnt = a.offsets[e + 1] - s0;
-    } else {
-        W0 = a.sh0; if (GATEUP) { W1 = a.sh1; }
-        s0 = a.P; cnt = a.n;
+    constexpr int NMAT = GATEUP ? 2 : 1, STEPS = NMAT * G::BPQ, NR = PD + 1;
+    static_assert(NMAT == 1 || NR % 2 == 0, "gate/up steps alternate matrices: the ring length must be even");
+    const uint8_t * xr[T];
+#pragma unroll
+    for (int u = 0; u < T; ++u) {
+        const int slot = slot0 + u;
+        const int ar = GATEUP ? (routed ? a.perm[slot] / a.topk : slot - a.P) : slot;   // gate/up: token rows, down: slot rows
+        if (XWG) {
+            xr[u] = xs + ar * G::XROW;
+        } else {
+            if (u == 0) { __builtin_amdgcn_wave_barrier(); }   // the previous tile's reads are issued before the rows are overwritten
+            stage_row<G>(xs + u * G::XROW, a.aq + (size_t) ar * G::K, a.ad + (size_t) ar * G::NB);
+            xr[u] = xs + u * G::XROW;
+        }
     }
-    const int nbq = a.K / (QK * UBLK), nbk = a.K / QK;
-    const int r = lane >> 4, b = (lane >> 2) & 3, c = lane & 3;
-    const size_t rq_off = (size_t) rq * nbq * UNIT;
-    for (int tok0 = 0; tok0 < cnt; tok0 += GEMV_TT) {
-        const int ntt = min(GEMV_TT, cnt - tok0);
-        int arow[GEMV_TT];
-        float acc0[GEMV_TT], acc1[GEMV_TT];
+    if (!XWG) {
+        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the wave's LDS writes are done before any lane reads them
+        __builtin_amdgcn_wave_barrier();
+    }
+    uint4 pf[NR][4]; uint16_t pd[NR];
 #pragma unroll
-        for (int t = 0; t < GEMV_TT; ++t) {
-            const int slot = s0 + tok0 + (t < ntt ? t : 0);
-            arow[t] = GATEUP ? (routed ? a.perm[slot] / a.topk : slot - a.P) : slot;
-            acc0[t] = 0.f; acc1[t] = 0.f;
+    for (int k = 0; k < PD; ++k) {
+        if (k < STEPS) { issue<NR, PD, G, NMAT>(tp, lq, ld, k, pf, pd, k); }
+    }
+    float acc[NMAT][T];
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m) {
+#pragma unroll
+        for (int u = 0; u < T; ++u) { acc[m][u] = 0.f; }
+    }
+#pragma unroll 1
+    for (int s0 = 0; s0 < STEPS; s0 += NR) {
+#pragma unroll
+        for (int k = 0; k < NR; ++k) {
+            const int s = s0 + k;
+            if (s < STEPS) {
+                if (s + PD < STEPS) { issue<NR, PD, G, NMAT>(tp, lq, ld, s + PD, pf, pd, (k + PD) % NR); }
+                const int mat = NMAT == 2 ? (k & 1) : 0;
+                const int j = (NMAT == 2 ? (s >> 1) : s) * G::QS + q;
+                const uint8_t * xb[T];
+#pragma unroll
+                for (int u = 0; u < T; ++u) { xb[u] = xr[u] + j * G::XBLK; }
+                int bsum[T];
+                block_bsum<T>(pf[k], rep, xb, bsum);
+                const float dw = h2f(pd[k]);
+#pragma unroll
+                for (int u = 0; u < T; ++u) {
+                    const float dx = reinterpret_cast<const float *>(xr[u] + G::NB * G::XBLK)[j];
+                    acc[mat][u] = fold_quad(acc[mat][u], (dw * dx) * (float) bsum[u]);
+                }
+            }
         }
-        for (int bq = 0; bq < nbq; ++bq) {
-            const uint8_t * u0 = W0 + rq_off + (size_t) bq * UNIT;
-            const uint4 q0 = *reinterpret_cast<const uint4 *>(u0 + 16 * lane);
-            const float d0 = h2f(*reinterpret_cast<const uint16_t *>(u0 + 1024 + 2 * (lane >> 2)));
-            int w0[16], l00, l01; dequant_chunk(tab, q0, w0, l00, l01);
-            int w1[16], l10 = 0, l11 = 0; float d1 = 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < T; ++u) {
+        const size_t o = (size_t) (slot0 + u) * a.R + row;
+        if (q == 0) {
             if (GATEUP) {
-                const uint8_t * u1 = W1 + rq_off + (size_t) bq * UNIT;
-                const uint4 q1 = *reinterpret_cast<const uint4 *>(u1 + 16 * lane);
-                d1 = h2f(*reinterpret_cast<const uint16_t *>(u1 + 1024 + 2 * (lane >> 2)));
-                dequant_chunk(tab, q1, w1, l10, l11);
-            }
-            const int blk = UBLK * bq + b;
-#pragma unroll
-            for (int t = 0; t < GEMV_TT; ++t) {
-                if (t < ntt) {
-                    const int4 * xp = reinterpret_cast<const int4 *>(a.aq + (size_t) arow[t] * a.K + (size_t) blk * QK + 64 * c);
-                    const int4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
-                    const int xv[16] = { x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w, x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w };
-                    const float dx = a.ad[(size_t) arow[t] * nbk + blk];
-                    int p0 = chunk_dot(w0, xv, l00, l01);
-                    p0 += __shfl_xor(p0, 1); p0 += __shfl_xor(p0, 2);
-                    const float t0 = (d0 * dx) * (float) p0;
-#pragma unroll
-                    for (int bb = 0; bb < UBLK; ++bb) { acc0[t] = acc0[t] + __shfl(t0, 16 * r + 4 * bb); }
-                    if (GATEUP) {
-                        int p1 = chunk_dot(w1, xv, l10, l11);
-                        p1 += __shfl_xor(p1, 1); p1 += __shfl_xor(p1, 2);
-                        const float t1 = (d1 * dx) * (float) p1;
-#pragma unroll
-                        for (int bb = 0; bb < UBLK; ++bb) { acc1[t] = acc1[t] + __shfl(t1, 16 * r + 4 * bb); }
-                    }
-                }
-            }
-        }
-        if ((lane & 15) == 0) {
-            const int row = UROWS * rq + r;
-#pragma unroll
-            for (int t = 0; t < GEMV_TT; ++t) {
-                if (t < ntt) {
-                    const size_t o = (size_t) (s0 + tok0 + t) * a.R + row;
-                    const float v0 = 0.125f * acc0[t];
-                    if (GATEUP) {
-                        const float v1 = 0.125f * acc1[t];
-                        a.out[o] = det_silu(v0) * v1;
-                        if (a.dbg0) { a.dbg0[o] = v0; }
-                        if (a.dbg1) { a.dbg1[o] = v1; }
-                    } else {
-                        a.out[o] = v0;
-                    }
-                }
+                const float g = 0.125f * acc[0][u], up = 0.125f * acc[NMAT - 1][u];
+                st_agent(a.h + o, det_silu(g) * up);
+                if (a.gdbg) { a.gdbg[o] = g; a.udbg[o] = up; }
+            } else {
+                st_agent(a.o + o, 0.125f * acc[0][u]);
             }
         }
     }
 }
 
-static hipError_t launch_gemv(const GemvArgs & a, bool gateup, hipStream_t st) {
-    if (a.R % 16 != 0 || a.K % (QK * UBLK) != 0 || a.n < 0) { return hipErrorInvalidValue; }
-    if (a.n == 0) { return hipSuccess; }
-    const unsigned grid = (unsigned) ((a.max_act + (a.shared ? 1 : 0)) * (a.R / 16));
-    if (grid == 0) { return hipSuccess; }
-    if (gateup) { k_iq2_gemv<true><<<grid, 256, 0, st>>>(a); }
-    else { k_iq2_gemv<false><<<grid, 256, 0, st>>>(a); }
+template <bool GATEUP, int BPQ, int TT, int WAVES, int PD, bool XWG>
+__global__ void __launch_bounds__(WAVES * 64) k_experts(const ExpertArgs a) {
+#pragma clang fp contract(off)
+    using G = Geo<BPQ>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    tables_copy<WAVES * 64>(lds, a.tab);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
+    uint8_t * xs = lds + TAB_BYTES;
+    if (XWG) {   // every token's activations, once per workgroup
+        for (int u = wave; u < a.n; u += WAVES) { stage_row<G>(xs + u * G::XROW, a.aq + (size_t) u * G::K, a.ad + (size_t) u * G::NB); }
+    } else {
+        xs += wave * TT * G::XROW;
+    }
+    __syncthreads();
+    const int NG = a.R / G::RPW;
+    const int nact = *a.nact;
+    const int nm = nact + (a.shared ? 1 : 0);
+    const int ntasks = nm * NG;
+    const int r = lane >> 2, q = lane & 3;
+    const uint32_t rep = lds_addr(lds) | ((uint32_t) (lane & 15) << 3);   // table base (64 KB aligned: the tables open the LDS) | replica
+    const uint32_t lq = (uint32_t) q * 4096 + 16 * r, ld = (uint32_t) q * 128 + 2 * r;   // the lane's part of its block addresses
+    const size_t dreg = (size_t) (a.R / 64) * G::NB * 4096;                              // d region of a matrix
+    // task tk runs on workgroup tk % grid: consecutive tasks spread over all CUs (and XCDs)
+    for (int tk = wave * gridDim.x + blockIdx.x; tk < ntasks; tk += gridDim.x * WAVES) {
+        const int m = tk / NG, g = tk - m * NG;
+        const bool routed = m < nact;
+        int e = 0, s0, cnt;
+        if (routed) { e = a.act[m]; s0 = a.offsets[e]; cnt = a.offsets[e + 1] - s0; }
+        else { s0 = a.P; cnt = a.n; }
+        const int rg = g >> 2, sub = g & 3;   // 64-row group and the task's 16-row quarter of it
+        TaskPtr tp;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            const uint8_t * W = (GATEUP || mt == 0) ? (routed ? a.w[mt] + (size_t) e * a.estride : a.sh[mt]) : nullptr;
+            tp.q[mt] = W + (size_t) rg * G::NB * 4096 + sub * 256;
+            tp.d[mt] = W + dreg + (size_t) rg * G::NB * 128 + sub * 32;
+        }
+        const int row = g * G::RPW + r;
+        for (int tok = 0; tok < cnt;) {
+            if (TT > 1 && cnt - tok >= TT) { run_tile<GATEUP, G, TT, PD, XWG>(a, lds, xs, tp, lq, ld, routed, s0 + tok, row, q, rep); tok += TT; }
+            else { run_tile<GATEUP, G, 1, PD, XWG>(a, lds, xs, tp, lq, ld, routed, s0 + tok, row, q, rep); tok += 1; }
+        }
+        if (GATEUP) {
+            // the last task of a 256-row block quantises that block of h for every slot of the expert
+            const int hb = (g * G::RPW) / QK;
+            if (!arrive_last(a.cnt_2 + (size_t) m * (a.R / QK) + hb, (unsigned) (QK / G::RPW))) { continue; }
+            for (int s = s0; s < s0 + cnt; ++s) {
+                const float * hbp = a.h + (size_t) s * a.R + hb * QK;
+                const float xv[4] = { ld_agent(hbp + 4 * lane), ld_agent(hbp + 4 * lane + 1), ld_agent(hbp + 4 * lane + 2), ld_agent(hbp + 4 * lane + 3) };
+                float d; const uint32_t packed = q8k_lane(xv, d);
+                reinterpret_cast<uint32_t *>(a.hq + (size_t) s * a.R + hb * QK)[lane] = packed;
+                if (lane == 0) { a.hd[(size_t) s * (a.R / QK) + hb] = d; }
+            }
+        } else if (a.y) {
+            // the last expert of a row group combines: y = sum_k w_k o_k in k order + shared, for every token
+            if (!arrive_last(a.cnt_2 + g, (unsigned) nm)) { continue; }
+            for (int i = lane; i < a.n * G::RPW; i += 64) {
+                const int tok = i / G::RPW, rr = g * G::RPW + i % G::RPW;
+                const int * iv = a.inv + (size_t) tok * a.topk; const float * w = a.wts + (size_t) tok * a.topk;
+                float ov[MAXK + 1];
+#pragma unroll
+                for (int k = 0; k < MAXK; ++k) { ov[k] = k < a.topk ? ld_agent(a.o + (size_t) iv[k] * a.R + rr) : 0.f; }
+                ov[MAXK] = ld_agent(a.o + (size_t) (a.P + tok) * a.R + rr);
+                float mv = ov[0] * w[0];
+                for (int k = 1; k < a.topk; ++k) { mv = mv + ov[k] * w[k]; }
+                a.y[(size_t) tok * a.R + rr] = mv + ov[MAXK];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- configurations and launches
+// gate/up (K = 7168, nb = 28): 7 steps of 4 blocks per matrix; down (K = 2048, nb = 8): 2 steps. 16 rows per task.
+// Decode stages every token once per workgroup; larger batches stage each wave's tile per task.
+//            GATEUP BPQ TT WAVES PD XWG
+#define GU1   true,  7,  1, 8,   5, true    // n == 1
+#define GU8   true,  7,  2, 8,   5, true    // n <= 8
+#define GUP   true,  7,  1, 8,   3, false   // larger batches
+#define DN1   false, 2,  1, 16,  2, false
+#define DN8   false, 2,  2, 16,  2, false
+constexpr int XWG_MAX = 8;
+
+template <bool GATEUP, int BPQ, int TT, int WAVES, int PD, bool XWG>
+constexpr size_t lds_of() { return TAB_BYTES + (size_t) (XWG ? XWG_MAX : WAVES * TT) * Geo<BPQ>::XROW; }
+
+template <bool GATEUP, int BPQ, int TT, int WAVES, int PD, bool XWG>
+static hipError_t set_lds() {
+    static_assert(lds_of<GATEUP, BPQ, TT, WAVES, PD, XWG>() <= 160 * 1024, "LDS budget");
+    return hipFuncSetAttribute((const void *) k_experts<GATEUP, BPQ, TT, WAVES, PD, XWG>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int) lds_of<GATEUP, BPQ, TT, WAVES, PD, XWG>());
+}
+template <bool GATEUP, int BPQ, int TT, int WAVES, int PD, bool XWG>
+static hipError_t launch(const ExpertArgs & a, int grid, hipStream_t st) {
+    k_experts<GATEUP, BPQ, TT, WAVES, PD, XWG><<<grid, WAVES * 64, lds_of<GATEUP, BPQ, TT, WAVES, PD, XWG>(), st>>>(a);
     return hipGetLastError();
 }
-hipError_t launch_gemv_gateup(const GemvArgs & a, hipStream_t st) { return launch_gemv(a, true, st); }
-hipError_t launch_gemv_down(const GemvArgs & a, hipStream_t st) { return launch_gemv(a, false, st); }
 
+hipError_t experts_init() {
+    hipError_t e = set_lds<GU1>();
+    if (e == hipSuccess) { e = set_lds<GU8>(); }
+    if (e == hipSuccess) { e = set_lds<GUP>(); }
+    if (e == hipSuccess) { e = set_lds<DN1>(); }
+    if (e == hipSuccess) { e = set_lds<DN8>(); }
+    return e;
+}
+size_t experts_terms_floats(int, int, int, int) { return 0; }
+
+// the LDS table image (layout at TAB_BYTES in moe_common.h), once, in device memory
+__global__ void k_table_image(uint64_t * img) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;   // 8-byte entry: line e = i / 32, slot r = i % 32
+    if (i >= TAB_BYTES / 8) { return; }
+    const int e = i >> 5, r = i & 31;
+    img[i] = r < 16 ? g_iq2xxs_grid[e] : sign_mask64(ksigns8((uint32_t) e & 127u));
+}
+hipError_t build_table_image(uint4 * img, hipStream_t st) {
+    k_table_image<<<TAB_BYTES / 8 / 256, 256, 0, st>>>(reinterpret_cast<uint64_t *>(img));
+    return hipGetLastError();
+}
+
+hipError_t launch_experts_gateup(const ExpertArgs & a, int grid, hipStream_t st) {
+    if (a.K != Geo<7>::K || a.R % QK || a.nmat != 2 || a.n < 0) { return hipErrorInvalidValue; }
+    if (a.n == 0 || grid <= 0) { return hipSuccess; }
+    if (a.n == 1) { return launch<GU1>(a, grid, st); }
+    if (a.n <= XWG_MAX) { return launch<GU8>(a, grid, st); }
+    return launch<GUP>(a, grid, st);
+}
+hipError_t launch_experts_down(const ExpertArgs & a, int grid, hipStream_t st) {
+    if (a.K != Geo<2>::K || a.R % 64 || a.nmat != 1 || a.n < 0) { return hipErrorInvalidValue; }
+    if (a.n == 0 || grid <= 0) { return hipSuccess; }
+    if (a.n == 1) { return launch<DN1>(a, grid, st); }
+    return launch<DN8>(a, grid, st);
+}
+
+// k-ordered combine for callers that run the down pass without the fused epilogue
 __global__ void __launch_bounds__(256) k_combine(const float * __restrict__ o, const int * __restrict__ inv, const float * __restrict__ wts,
                                                  int n, int topk, int E, int P, const float * __restrict__ resid,
                                                  float * __restrict__ y, float * __restrict__ moe) {

@@ -2,12 +2,17 @@
 //
 // Formats (ggml's, as the reference's block uses them):
 //   block_iq2_xxs = { fp16 d; u16 qs[32] } = 66 B per 256 weights (src/fused_layer.cu:19 BLK_IQ2 = 66). Sub-block ib
-//   (32 weights) is the 8 bytes qs[4ib..4ib+3]: a0 = 4 codebook indices, a1 = 4x7 sign bits + 4-bit scale (a1 >> 28).
+//   (32 weights) is the 8 bytes qs[4ib..4ib+3]: a0 = 4 codebook indices (byte l = group l), a1 = 4 x 7 sign bits
+//   (bits 7l..7l+6 = group l) + the 4-bit scale nibble (a1 >> 28).
 //   Q8_K activations: per 256 values an fp32 d and 256 int8 (quantize_row_q8_K_ref).
-// Tiled layout (this build's resident layout, produced once by fl_pack_iq2xxs): a matrix of R rows x K columns is cut
-// into units of 4 rows x 4 blocks (R % 4 == 0, K % 1024 == 0); a unit is 1056 B = 16 blocks' qs (row-major over
-// (row, block), 64 B each) followed by their 16 fp16 d. Units are ordered row-quad major, then block-quad. The total
-// size equals ggml's (66 B per block); a 64-lane wave reads one unit with one 16-byte load per lane.
+//
+// Tiled layout (the resident layout, produced once by fl_pack_iq2xxs; same 66 B per block). A matrix of R rows x K
+// columns (R % 64 == 0, K % 1024 == 0, nb = K / 256 blocks per row) is stored as
+//   qs region: [R/64 row groups][nb blocks][4 chunks][64 rows][16 B]   -- chunk c = qs bytes 16c..16c+15 of the block
+//   d region : [R/64 row groups][nb blocks][64 rows] fp16              -- after the qs region
+// so a 64-lane wave that owns 64 rows reads each 16-byte chunk of a block with one fully coalesced 1 KB load.
+// Inside every sub-block the sign word is re-packed (lossless): byte l holds group l's 7 sign bits in bits 0..6 and bit l
+// of the scale nibble in bit 7, so a byte select addresses the sign table and one udot4 rebuilds 2 * nibble + 1.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
@@ -17,8 +22,7 @@ namespace lk {
 
 constexpr int QK = 256;             // weights per block
 constexpr int IQ2B = 66;            // bytes per IQ2_XXS block
-constexpr int UROWS = 4, UBLK = 4;  // tiled unit: 4 rows x 4 blocks
-constexpr int UNIT = 1056;          // bytes per unit
+constexpr int RG = 64;              // rows per row group (one wave, one row per lane)
 constexpr int MAXK = 8;             // top-k per token supported by the fused kernels
 constexpr int NEXP_MAX = 256;       // experts per layer supported by the device router/dispatch
 
@@ -29,49 +33,83 @@ static __device__ const uint64_t g_iq2xxs_grid[256] = {
 #include "iq2xxs_grid.inc"
 };
 
-__device__ __forceinline__ uint32_t ksigns8(uint32_t i7) {   // 7 stored sign bits + parity bit 7
+__host__ __device__ inline uint32_t ksigns8(uint32_t i7) {   // 7 stored sign bits + parity bit 7
     return i7 | ((__builtin_popcount(i7) & 1u) << 7);
 }
 
 // byte masks 0x00/0xFF for the 8 signs of one 8-weight group: lo = weights 0..3, hi = 4..7
-__device__ __forceinline__ uint64_t sign_mask64(uint32_t s8) {
+__host__ __device__ inline uint64_t sign_mask64(uint32_t s8) {
     uint64_t m = 0;
-#pragma unroll
     for (int j = 0; j < 8; ++j) { m |= (uint64_t) (((s8 >> j) & 1u) * 0xFFu) << (8 * j); }
     return m;
 }
 
-// LDS tables used by the IQ2 kernels: the codebook (2 KB) and the 128 sign masks (1 KB).
-struct Iq2Lds {
-    uint64_t grid[256];
-    uint64_t smask[128];
-};
-
-__device__ __forceinline__ void iq2_lds_fill(Iq2Lds & t) {
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) { t.grid[i] = g_iq2xxs_grid[i]; }
-    for (int i = threadIdx.x; i < 128; i += blockDim.x) { t.smask[i] = sign_mask64(ksigns8((uint32_t) i)); }
+// sign word <-> tiled sign word (lossless permutation of the 32 bits)
+__host__ __device__ inline uint32_t a1_to_tiled(uint32_t a1) {
+    uint32_t o = 0;
+    for (int l = 0; l < 4; ++l) { o |= (((a1 >> (7 * l)) & 127u) | (((a1 >> (28 + l)) & 1u) << 7)) << (8 * l); }
+    return o;
+}
+__host__ __device__ inline uint32_t a1_from_tiled(uint32_t t) {
+    uint32_t a = 0;
+    for (int l = 0; l < 4; ++l) { a |= ((t >> (8 * l)) & 127u) << (7 * l); a |= ((t >> (8 * l + 7)) & 1u) << (28 + l); }
+    return a;
 }
 
-// signed int8 weights of one 8-group: grid magnitudes with the group's signs applied. Grid bytes are never 0, so the
-// per-byte two's-complement negation (g ^ 0xFF) + 1 never carries into the next byte and plain 32-bit ops suffice.
-__device__ __forceinline__ void iq2_group(const Iq2Lds & t, uint32_t a0, uint32_t a1, int l, int & lo, int & hi) {
-    const uint64_t g = t.grid[(a0 >> (8 * l)) & 255u];
-    const uint64_t m = t.smask[(a1 >> (7 * l)) & 127u];
-    const uint32_t glo = (uint32_t) g, ghi = (uint32_t) (g >> 32), mlo = (uint32_t) m, mhi = (uint32_t) (m >> 32);
-    lo = (int) ((glo ^ mlo) + (mlo & 0x01010101u));
-    hi = (int) ((ghi ^ mhi) + (mhi & 0x01010101u));
+// byte offsets inside one tiled matrix
+__host__ __device__ inline size_t tiled_qs_off(int rg, int j, int c, int nb) { return ((size_t) (rg * nb + j) * 4 + c) * 1024; }
+__host__ __device__ inline size_t tiled_d_off(int rg, int j, int row, int R, int nb) {
+    return (size_t) (R / RG) * nb * 4096 + ((size_t) (rg * nb + j) * RG + row) * 2;
 }
 
-// exact int32 dot of one sub-block (32 weights) with 32 int8 activations (8 dwords)
-__device__ __forceinline__ int iq2_sub_dot(const Iq2Lds & t, uint32_t a0, uint32_t a1, const int * xv) {
-    int s = 0;
-#pragma unroll
-    for (int l = 0; l < 4; ++l) {
-        int lo, hi; iq2_group(t, a0, a1, l, lo, hi);
-        s = __builtin_amdgcn_sdot4(lo, xv[2 * l], s, false);
-        s = __builtin_amdgcn_sdot4(hi, xv[2 * l + 1], s, false);
-    }
-    return s;
+// ---------------------------------------------------------------- bank-replicated LDS tables
+// Entry e (0..255) owns the 256-byte line [256 e, 256 e + 256): 16 replicas of the codebook word grid[e] at +0..127 and
+// 16 replicas of the sign masks of the tiled sign byte e (bit 7 = a scale bit, ignored) at +128..255. Lane l reads
+// replica l % 16, so 16 lanes' 8-byte reads cover all banks whatever the indices, and the byte address is
+// (index << 8) | (replica << 3): one v_perm_b32 builds it from the packed index word. The image is built once per
+// context (build_table_image) and copied into LDS by every workgroup (tables_copy).
+constexpr int TAB_BYTES = 256 * 256;
+
+__device__ __forceinline__ uint32_t xad(uint32_t a, uint32_t b, uint32_t c) { return (a ^ b) + c; }   // one v_xad_u32
+
+// explicit address spaces: loads through generic pointers would compile to FLAT instructions, which also count against
+// lgkmcnt and so make every LDS wait a wait for the outstanding global loads as well
+#define LK_GLOBAL __attribute__((address_space(1)))
+#define LK_LOCAL __attribute__((address_space(3)))
+template <class T> __device__ __forceinline__ const LK_GLOBAL T * gptr(const T * p) { return (const LK_GLOBAL T *) p; }
+template <class T> __device__ __forceinline__ LK_GLOBAL T * gptr(T * p) { return (LK_GLOBAL T *) p; }
+__device__ __forceinline__ uint32_t lds_addr(const void * p) { return (uint32_t) (size_t) (const LK_LOCAL uint8_t *) p; }
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 gload16(const void * p) { const u32x4 v = *(const LK_GLOBAL u32x4 *) p; return make_uint4(v.x, v.y, v.z, v.w); }
+__device__ __forceinline__ uint2 gload8(const void * p) { const u32x2 v = *(const LK_GLOBAL u32x2 *) p; return make_uint2(v.x, v.y); }
+__device__ __forceinline__ float4 gloadf4(const void * p) { const f32x4 v = *(const LK_GLOBAL f32x4 *) p; return make_float4(v.x, v.y, v.z, v.w); }
+__device__ __forceinline__ uint2 lload8(uint32_t addr) { const u32x2 v = *(const LK_LOCAL u32x2 *) (size_t) addr; return make_uint2(v.x, v.y); }
+
+// LDS byte address of the table entry for byte L of an index word: byte 1 = that byte; bytes 0, 2, 3 from `tr` = the
+// table base (64 KB aligned) | the lane's replica offset
+template <int L> __device__ __forceinline__ uint32_t tab_addr(uint32_t word, uint32_t tr) {
+    return __builtin_amdgcn_perm(word, tr, 0x03020000u | ((4u + L) << 8));
+}
+
+// signed int8 weights of a group from its codebook word g and sign masks m: magnitudes with the signs applied. Grid bytes
+// are never 0, so the per-byte two's-complement negation (g ^ 0xFF) + 1 never carries into the next byte.
+__device__ __forceinline__ void iq2_apply(uint2 g, uint2 m, uint32_t & lo, uint32_t & hi) {
+    lo = xad(g.x, m.x, m.x & 0x01010101u);
+    hi = xad(g.y, m.y, m.y & 0x01010101u);
+}
+template <int L> __device__ __forceinline__ uint2 tab_grid(uint32_t a0, uint32_t tr) { return lload8(tab_addr<L>(a0, tr)); }
+template <int L> __device__ __forceinline__ uint2 tab_sign(uint32_t a1t, uint32_t tr) { return lload8(tab_addr<L>(a1t, tr) + 128); }
+
+// 2 * scale nibble + 1 of a tiled sign word (nibble bit l = bit 7 of byte l)
+__device__ __forceinline__ int iq2_scale(uint32_t a1t) {
+    return (int) __builtin_amdgcn_udot4((a1t >> 7) & 0x01010101u, 0x10080402u, 1u, false);
+}
+
+__device__ __forceinline__ uint4 load_nt(const uint8_t * p) {   // streaming (non-temporal) 16-byte global load
+    const u32x4 v = __builtin_nontemporal_load((const LK_GLOBAL u32x4 *) p);
+    return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
@@ -114,5 +152,33 @@ __device__ __forceinline__ float det_sigmoid(float x) {
 
 // ---------------------------------------------------------------- wave helpers (wave64)
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+// Q8_K of one 256-value block by one wave (quantize_row_q8_K_ref): lane l handles values 4l..4l+3
+__device__ __forceinline__ void q8k_block_wave(const float * __restrict__ xb, int8_t * __restrict__ qb, float * __restrict__ db) {
+    const int lane = lane_id();
+    const float4 v = reinterpret_cast<const float4 *>(xb)[lane];
+    const float xs[4] = { v.x, v.y, v.z, v.w };
+    float ba = -1.f, bv = 0.f; int bi = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { const float ax = fabsf(xs[i]); if (ax > ba) { ba = ax; bv = xs[i]; bi = 4 * lane + i; } }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {   // first occurrence of the largest |x|: larger |x| wins, ties to the lower index
+        const float oa = __shfl_xor(ba, off), ov = __shfl_xor(bv, off); const int oi = __shfl_xor(bi, off);
+        if (oa > ba || (oa == ba && oi < bi)) { ba = oa; bv = ov; bi = oi; }
+    }
+    uint32_t packed = 0; float d = 0.f;
+    if (ba > 0.f) {
+        const float iscale = -127.f / bv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float p = iscale * xs[i];
+            int iv = (int) rintf(p); iv = iv < 127 ? iv : 127;
+            packed |= ((uint32_t) (iv & 0xff)) << (8 * i);
+        }
+        d = 1.f / iscale;
+    }
+    reinterpret_cast<uint32_t *>(qb)[lane] = packed;
+    if (lane == 0) { *db = d; }
+}
 
 }  // namespace lk

@@ -1,0 +1,388 @@
+// moe_device.h -- device-side building blocks of the expert kernels (gfx950, wave64): cross-workgroup exchange, the
+// IQ2_XXS x Q8_K block dot product, the in-wave block-order fold and the router's selection. Used by iq2_gemv.hip (one
+// kernel per pass) and moe_decode.hip (the single-launch decode block), so both compute bit-identical results.
+#pragma once
+#include "moe_common.h"
+
+namespace lk {
+
+// ---------------------------------------------------------------- cross-workgroup exchange
+// Values one workgroup hands to another inside a launch are written and read with agent-scope relaxed atomics: the XCDs'
+// L2 caches are not coherent with each other, and an agent-scope fence would write back / invalidate a whole L2. A
+// producer waits for its own stores to complete (vmcnt(0)) before it signals (counter RMW or flag store); a consumer
+// issues its loads only after it has seen the signal.
+__device__ __forceinline__ void st_agent(float * p, float v) { __hip_atomic_store(gptr(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void st_agent_u32(uint32_t * p, uint32_t v) { __hip_atomic_store(gptr(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ float ld_agent(const float * p) { return __hip_atomic_load(gptr(const_cast<float *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ uint32_t ld_agent_u32(const uint32_t * p) { return __hip_atomic_load(gptr(const_cast<uint32_t *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ uint64_t ld_agent_u64(const uint64_t * p) { return __hip_atomic_load(gptr(const_cast<uint64_t *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+__device__ __forceinline__ void stores_done() {   // this wave's stores have completed
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// one arrival of the calling wave on a device-scope counter; true for the wave that completes `expected` arrivals,
+// which resets the counter for the next launch
+__device__ __forceinline__ bool arrive_last(unsigned * cnt, unsigned expected) {
+    stores_done();
+    unsigned old = 0;
+    if (lane_id() == 0) { old = __hip_atomic_fetch_add(gptr(cnt), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+    old = __builtin_amdgcn_readfirstlane(old);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (old + 1 != expected) { return false; }
+    if (lane_id() == 0) { __hip_atomic_store(gptr(cnt), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+    return true;
+}
+
+// bounded wait of one wave for *flag == want; false after ~2^20 polls (the caller reports the timeout and skips)
+__device__ __forceinline__ bool wait_flag(const unsigned * flag, unsigned want) {
+    for (int i = 0; i < (1 << 20); ++i) {
+        unsigned v = 0;
+        if (lane_id() == 0) { v = ld_agent_u32(flag); }
+        v = __builtin_amdgcn_readfirstlane(v);
+        if (v == want) { __atomic_signal_fence(__ATOMIC_SEQ_CST); return true; }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    return false;
+}
+
+// ---------------------------------------------------------------- LDS tables from the prebuilt image
+// the 64 KB table image (layout at TAB_BYTES in moe_common.h) is built once per context in device memory; a workgroup copies it with
+// 16-byte loads, all issued before the first LDS write
+template <int NT>
+__device__ __forceinline__ void tables_copy(uint8_t * lds, const uint4 * img) {
+    constexpr int PER = TAB_BYTES / 16 / NT;
+    static_assert(PER * NT * 16 == TAB_BYTES, "threads must divide the image");
+    uint4 v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) { v[k] = gload16(img + k * NT + threadIdx.x); }
+#pragma unroll
+    for (int k = 0; k < PER; ++k) { reinterpret_cast<uint4 *>(lds)[k * NT + threadIdx.x] = v[k]; }
+}
+
+// ---------------------------------------------------------------- wave reductions without LDS
+// Pure-VALU maximum over the wave: DPP inside 16-lane rows (quad_perm xor 1, xor 2, row_half_mirror, row_mirror), then
+// row_bcast:15 / row_bcast:31 carry row results upwards so lane 63 ends with the maximum, read back once. __shfl would
+// go through ds_bpermute (the LDS queue the table lookups keep busy), and comparing in scalar registers would bounce
+// every step between the vector and scalar units.
+enum { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140, DPP_BCAST15 = 0x142, DPP_BCAST31 = 0x143 };
+template <int CTRL> __device__ __forceinline__ uint32_t dpp(uint32_t v) { return (uint32_t) __builtin_amdgcn_mov_dpp((int) v, CTRL, 0xF, 0xF, true); }
+template <int CTRL> __device__ __forceinline__ float dppf(float v) { return __builtin_bit_cast(float, dpp<CTRL>(__builtin_bit_cast(uint32_t, v))); }
+__device__ __forceinline__ uint32_t rdlane(uint32_t v, int l) { return (uint32_t) __builtin_amdgcn_readlane((int) v, l); }
+
+template <int CTRL, int ROWS> __device__ __forceinline__ uint64_t max64_step(uint64_t k) {
+    const uint32_t h = (uint32_t) (k >> 32), l = (uint32_t) k;
+    // lanes outside ROWS keep their own value (old operand = own value)
+    const uint32_t oh = (uint32_t) __builtin_amdgcn_update_dpp((int) h, (int) h, CTRL, ROWS, 0xF, false);
+    const uint32_t ol = (uint32_t) __builtin_amdgcn_update_dpp((int) l, (int) l, CTRL, ROWS, 0xF, false);
+    const uint64_t o = ((uint64_t) oh << 32) | ol;
+    return o > k ? o : k;
+}
+// wave-wide maximum of 64-bit keys, returned to every lane (uniform)
+__device__ __forceinline__ uint64_t wave_max64(uint64_t k) {
+    k = max64_step<DPP_XOR1, 0xF>(k); k = max64_step<DPP_XOR2, 0xF>(k);
+    k = max64_step<DPP_HALF_MIRROR, 0xF>(k); k = max64_step<DPP_MIRROR, 0xF>(k);
+    k = max64_step<DPP_BCAST15, 0xA>(k); k = max64_step<DPP_BCAST31, 0xC>(k);
+    return ((uint64_t) rdlane((uint32_t) (k >> 32), 63) << 32) | rdlane((uint32_t) k, 63);
+}
+// fp32 bits -> unsigned key with the same order (no -0 / NaN among the values compared here)
+__device__ __forceinline__ uint32_t ord_key(float f) { const uint32_t b = __builtin_bit_cast(uint32_t, f); return (b & 0x80000000u) ? ~b : (b | 0x80000000u); }
+
+// ---------------------------------------------------------------- Q8_K of one 256-value block by one wave
+// quantize_row_q8_K_ref: lane l holds values 4l..4l+3; amax with its first occurrence's signed value, iscale = -127/max,
+// q = min(127, round-half-even(iscale * x)), d = 1/iscale; an all-zero block gives d = 0. Returns the lane's 4 packed q.
+__device__ __forceinline__ uint32_t q8k_lane(const float (&xs)[4], float & d) {
+#pragma clang fp contract(off)
+    const int lane = lane_id();
+    float ba = -1.f, bv = 0.f; int bi = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { const float ax = fabsf(xs[i]); if (ax > ba) { ba = ax; bv = xs[i]; bi = 4 * lane + i; } }
+    // the largest |x|, ties to the lower index: key (|x| bits, 255 - index)
+    const uint64_t key = wave_max64(((uint64_t) __builtin_bit_cast(uint32_t, ba) << 32) | (255u - (uint32_t) bi));
+    const int wi = 255 - (int) (uint32_t) key;
+    ba = __builtin_bit_cast(float, (uint32_t) (key >> 32));
+    bv = __builtin_bit_cast(float, rdlane(__builtin_bit_cast(uint32_t, bv), wi >> 2));   // the owner lane's best is the winner
+    uint32_t packed = 0; d = 0.f;
+    if (ba > 0.f) {
+        const float iscale = -127.f / bv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float p = iscale * xs[i];
+            int iv = (int) rintf(p); iv = iv < 127 ? iv : 127;
+            packed |= ((uint32_t) (iv & 0xff)) << (8 * i);
+        }
+        d = 1.f / iscale;
+    }
+    return packed;
+}
+
+// ---------------------------------------------------------------- staged activations
+// BPQ blocks per K quarter (4 quarters); lane 4 r + q of a task owns row r and blocks j = 4 jj + q, so the 4 lanes of a
+// quad hold 4 consecutive blocks of one row at every step. One token's staged activations: per block 256 int8 (+16 B of
+// padding, so the quarters' reads of one instruction fall in different banks) re-ordered so that group l of all 8
+// sub-blocks is contiguous (byte l * 64 + ib * 8 + k = x[ib * 32 + l * 8 + k]), then the NB fp32 block scales.
+template <int BPQ_> struct Geo {
+    static constexpr int QS = 4, BPQ = BPQ_, RPW = 16, NB = QS * BPQ, K = NB * QK;
+    static constexpr int XBLK = QK + 16, XROW = NB * XBLK + NB * 4;
+};
+// staged byte offset inside a block of the 4 values 4 lane .. 4 lane + 3 (sub-block lane / 8, group (lane % 8) / 2)
+__device__ __forceinline__ int staged_word(int lane) { return ((lane & 7) >> 1) * 64 + (lane >> 3) * 8 + (lane & 1) * 4; }
+
+// one token row of Q8_K values (K int8 + NB scales in global memory) into the staged layout, by one wave
+template <class G>
+__device__ __forceinline__ void stage_row(uint8_t * dst, const int8_t * src, const float * dsrc) {
+    const int lane = lane_id();
+    constexpr int IT = G::K / 8 / 64;
+    uint2 v[IT];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) { v[it] = gload8(src + (size_t) (it * 64 + lane) * 8); }
+    const float dv = lane < G::NB ? gptr(dsrc)[lane] : 0.f;
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {   // 8-byte piece i = (block j, sub-block ib, group l)
+        const int i = it * 64 + lane, j = i >> 5, w = i & 31;
+        *reinterpret_cast<uint2 *>(dst + j * G::XBLK + (w & 3) * 64 + (w >> 2) * 8) = v[it];
+    }
+    if (lane < G::NB) { reinterpret_cast<float *>(dst + G::NB * G::XBLK)[lane] = dv; }
+}
+// the same from values another workgroup wrote in this launch (agent-scope loads)
+template <class G>
+__device__ __forceinline__ void stage_row_agent(uint8_t * dst, const int8_t * src, const float * dsrc) {
+    const int lane = lane_id();
+    constexpr int IT = G::K / 8 / 64;
+    uint64_t v[IT];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) { v[it] = ld_agent_u64(reinterpret_cast<const uint64_t *>(src) + it * 64 + lane); }
+    const float dv = lane < G::NB ? ld_agent(dsrc + lane) : 0.f;
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int i = it * 64 + lane, j = i >> 5, w = i & 31;
+        *reinterpret_cast<uint64_t *>(dst + j * G::XBLK + (w & 3) * 64 + (w >> 2) * 8) = v[it];
+    }
+    if (lane < G::NB) { reinterpret_cast<float *>(dst + G::NB * G::XBLK)[lane] = dv; }
+}
+__device__ __forceinline__ void lds_visible() {   // this wave's LDS writes are done before any of its lanes reads them
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+}
+
+// ---------------------------------------------------------------- one block: integer sums of T tokens
+template <int L, int T>
+__device__ __forceinline__ void group_step(const uint4 (&w)[4], uint32_t tr, const uint8_t * const (&xb)[T], int (&acc)[T][8]) {
+    uint2 g[8], m[8];   // all 16 table reads of the step are issued before the first is used
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) {
+        const uint4 c = w[ib >> 1];
+        g[ib] = tab_grid<L>((ib & 1) ? c.z : c.x, tr);
+        m[ib] = tab_sign<L>((ib & 1) ? c.w : c.y, tr);
+    }
+    int4 xv[T][4];
+#pragma unroll
+    for (int u = 0; u < T; ++u) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) { xv[u][k] = *reinterpret_cast<const int4 *>(xb[u] + L * 64 + k * 16); }
+    }
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) {
+        uint32_t lo, hi; iq2_apply(g[ib], m[ib], lo, hi);
+#pragma unroll
+        for (int u = 0; u < T; ++u) {
+            const int4 x = xv[u][ib >> 1];
+            acc[u][ib] = __builtin_amdgcn_sdot4((int) lo, (ib & 1) ? x.z : x.x, acc[u][ib], false);
+            acc[u][ib] = __builtin_amdgcn_sdot4((int) hi, (ib & 1) ? x.w : x.y, acc[u][ib], false);
+        }
+    }
+}
+
+// exact integer block sums sum_ib (2 nibble_ib + 1) * sumi_ib of one IQ2_XXS block (tiled chunks w) against T tokens
+template <int T>
+__device__ __forceinline__ void block_bsum(const uint4 (&w)[4], uint32_t tr, const uint8_t * const (&xb)[T], int (&bsum)[T]) {
+    int acc[T][8];
+#pragma unroll
+    for (int u = 0; u < T; ++u) {
+#pragma unroll
+        for (int ib = 0; ib < 8; ++ib) { acc[u][ib] = 0; }
+    }
+    group_step<0, T>(w, tr, xb, acc);
+    group_step<1, T>(w, tr, xb, acc);
+    group_step<2, T>(w, tr, xb, acc);
+    group_step<3, T>(w, tr, xb, acc);
+#pragma unroll
+    for (int u = 0; u < T; ++u) {
+        int s = 0;
+#pragma unroll
+        for (int ib = 0; ib < 8; ++ib) {   // |acc| <= 32 * 43 * 127 < 2^23: the 24-bit multiply is exact
+            const uint4 c = w[ib >> 1];
+            s += __mul24(acc[u][ib], iq2_scale((ib & 1) ? c.w : c.y));
+        }
+        bsum[u] = s;
+    }
+}
+
+template <int Q> __device__ __forceinline__ float quad_bcast(float v) {   // lane Q of every quad, to the whole quad
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), Q * 0x55, 0xF, 0xF, true));
+}
+// the 4 lanes of a quad hold consecutive blocks 4 jj .. 4 jj + 3 of one row: add their terms in block order
+__device__ __forceinline__ float fold_quad(float acc, float t) {
+#pragma clang fp contract(off)
+    acc = acc + quad_bcast<0>(t);
+    acc = acc + quad_bcast<1>(t);
+    acc = acc + quad_bcast<2>(t);
+    return acc + quad_bcast<3>(t);
+}
+
+// ---------------------------------------------------------------- streaming RPL x 16 rows of one matrix
+// Steps s = 0 .. RPL * BPQ - 1: row set s / BPQ (16 rows each, 256 B apart in a tiled chunk), block step jj = s % BPQ.
+// qb / db: uniform qs / d bases of the task's first row set at jj = 0; lq / ld: the lane's part of its addresses.
+template <int BPQ, int RPL, int PD>
+struct RowStream {
+    static constexpr int STEPS = RPL * BPQ, NR = PD + 1;
+    uint4 pf[NR][4]; uint16_t pd[NR];
+    __device__ __forceinline__ void issue(const uint8_t * qb, const uint8_t * db, uint32_t lq, uint32_t ld, int s, int slot) {
+        const int rs = s / BPQ, jj = s % BPQ;
+        const uint8_t * q = qb + (size_t) rs * 256 + (size_t) jj * (4 * 4096);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) { pf[slot][c] = load_nt(q + lq + c * 1024); }
+        pd[slot] = *gptr(reinterpret_cast<const uint16_t *>(db + (size_t) rs * 32 + (size_t) jj * (4 * 128) + ld));
+    }
+    __device__ __forceinline__ void prologue(const uint8_t * qb, const uint8_t * db, uint32_t lq, uint32_t ld) {
+#pragma unroll
+        for (int k = 0; k < PD; ++k) { if (k < STEPS) { issue(qb, db, lq, ld, k, k); } }
+    }
+    // row totals (before the final * 0.125) of the lane's RPL rows for T staged tokens xr[u]
+    template <int T, class G>
+    __device__ __forceinline__ void run(const uint8_t * qb, const uint8_t * db, uint32_t lq, uint32_t ld, uint32_t tr,
+                                        const uint8_t * const (&xr)[T], int q, float (&acc)[RPL][T]) {
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int rs = 0; rs < RPL; ++rs) {
+#pragma unroll
+            for (int u = 0; u < T; ++u) { acc[rs][u] = 0.f; }
+        }
+#pragma unroll 1
+        for (int s0 = 0; s0 < STEPS; s0 += NR) {
+#pragma unroll
+            for (int k = 0; k < NR; ++k) {
+                const int s = s0 + k;
+                if (s < STEPS) {
+                    if (s + PD < STEPS) { issue(qb, db, lq, ld, s + PD, (k + PD) % NR); }
+                    const int j = (s % BPQ) * 4 + q;
+                    const uint8_t * xb[T];
+#pragma unroll
+                    for (int u = 0; u < T; ++u) { xb[u] = xr[u] + j * G::XBLK; }
+                    int bsum[T];
+                    block_bsum<T>(pf[k], tr, xb, bsum);
+                    const float dw = h2f(pd[k]);
+                    const int rs = s / BPQ;
+#pragma unroll
+                    for (int u = 0; u < T; ++u) {
+                        const float dx = reinterpret_cast<const float *>(xr[u] + G::NB * G::XBLK)[j];
+                        const float t = (dw * dx) * (float) bsum[u];
+                        // rs is uniform: select the accumulator without dynamic register indexing
+#pragma unroll
+                        for (int r2 = 0; r2 < RPL; ++r2) { if (r2 == rs) { acc[r2][u] = fold_quad(acc[r2][u], t); } }
+                    }
+                }
+            }
+        }
+    }
+};
+
+// ---------------------------------------------------------------- router selection of one token by one wave
+
+// Grouped sigmoid top-k (the rule of router.hip): p = sigmoid(logit), c = p + bias; group score = top1 + top2 of c in
+// the group; groups ranked by score (ties to the lower group) keep topk_group; topk rounds of argmax over eligible
+// experts (ties to the lower index); w_r = p_r / max(sum_r p_r, 2^-14) * scale with the sum in pick order.
+// lg[j] = logit of expert 4 lane + j. scr: per-wave LDS scratch of n_exp + 2 * n_group floats (general group sizes only).
+template <int CTRL> __device__ __forceinline__ void top2_step(float & v1, float & v2) {
+    const float o1 = dppf<CTRL>(v1), o2 = dppf<CTRL>(v2);
+    const float n2 = v1 >= o1 ? fmaxf(v2, o1) : fmaxf(v1, o2);
+    v1 = fmaxf(v1, o1); v2 = n2;
+}
+__device__ __forceinline__ void select_token(const float (&lg)[4], const float * bias, int n_exp, int n_group, int topk_group, int topk,
+                                             float scale, float * scr, int * sel_out, float * w_out, float * probs_out) {
+#pragma clang fp contract(off)
+    const int lane = lane_id(), per = n_exp / n_group;
+    float p[4], c[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = 4 * lane + j;
+        p[j] = 0.f; c[j] = 0.f;
+        if (e < n_exp) {
+            p[j] = det_sigmoid(lg[j]); c[j] = p[j] + gptr(bias)[e];
+            if (probs_out) { gptr(probs_out)[e] = p[j]; }
+        }
+    }
+    bool ok[4];
+    const int lpg = per / 4;   // lanes per group
+    if (per % 4 == 0 && (lpg & (lpg - 1)) == 0 && lpg <= 16) {
+        // top1 / top2 of the group: the lane's 4, then across the group's lanes (DPP inside a 16-lane row)
+        float v1 = -INFINITY, v2 = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (4 * lane + j < n_exp) { const float v = c[j]; if (v > v1) { v2 = v1; v1 = v; } else if (v > v2) { v2 = v; } }
+        }
+        if (lpg >= 2) { top2_step<DPP_XOR1>(v1, v2); }
+        if (lpg >= 4) { top2_step<DPP_XOR2>(v1, v2); }
+        if (lpg >= 8) { top2_step<DPP_HALF_MIRROR>(v1, v2); }
+        if (lpg >= 16) { top2_step<DPP_MIRROR>(v1, v2); }
+        const float mine = v1 + v2;   // this lane's group score
+        const int gme = lane / lpg;
+        int rank = 0;
+        for (int h = 0; h < n_group; ++h) {   // a group stays eligible if fewer than topk_group groups beat it
+            const float o = __builtin_bit_cast(float, rdlane(__builtin_bit_cast(uint32_t, mine), h * lpg));
+            rank += (o > mine || (o == mine && h < gme)) ? 1 : 0;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { ok[j] = 4 * lane + j < n_exp && rank < topk_group; }
+    } else {
+        float * cs = scr; float * gsc = scr + n_exp; int * allow = reinterpret_cast<int *>(scr + n_exp + n_group);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { if (4 * lane + j < n_exp) { cs[4 * lane + j] = c[j]; } }
+        lds_visible();
+        if (lane < n_group) {   // top1 + top2 of the group's biased scores
+            float v1 = 0.f, v2 = 0.f; int i1 = -1, i2 = -1;
+            for (int e = lane * per; e < (lane + 1) * per; ++e) {
+                const float v = cs[e];
+                if (i1 < 0 || v > v1) { v2 = v1; i2 = i1; v1 = v; i1 = e; }
+                else if (i2 < 0 || v > v2) { v2 = v; i2 = e; }
+            }
+            gsc[lane] = v1 + v2;
+        }
+        lds_visible();
+        if (lane < n_group) {
+            int rank = 0; const float mine = gsc[lane];
+            for (int h = 0; h < n_group; ++h) { const float o = gsc[h]; rank += (o > mine || (o == mine && h < lane)) ? 1 : 0; }
+            allow[lane] = rank < topk_group;
+        }
+        lds_visible();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { const int e = 4 * lane + j; ok[j] = e < n_exp && allow[e / per]; }
+    }
+    // topk rounds of argmax: key (ordered c, 255 - index), then the winner's p from its owner lane
+    float sum = 0.f; float pr[MAXK]; int ir[MAXK];
+    for (int r = 0; r < topk; ++r) {
+        uint64_t kb = 0; float bp = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint64_t kj = ok[j] ? ((uint64_t) ord_key(c[j]) << 32) | (255u - (uint32_t) (4 * lane + j)) : 0;
+            if (kj > kb) { kb = kj; bp = p[j]; }
+        }
+        const float lbp = bp;
+        kb = wave_max64(kb);
+        const int bi = kb ? 255 - (int) (uint32_t) kb : -1;
+        bp = bi >= 0 ? __builtin_bit_cast(float, rdlane(__builtin_bit_cast(uint32_t, lbp), bi >> 2)) : 0.f;
+        if (bi >= 0 && (bi >> 2) == lane) { ok[bi & 3] = false; }
+        sum = sum + bp;
+#pragma unroll
+        for (int k = 0; k < MAXK; ++k) { if (k == r) { pr[k] = bp; ir[k] = bi; } }
+    }
+    sum = sum > 6.103515625e-5f ? sum : 6.103515625e-5f;
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) {
+        if (k < topk && lane == k) { sel_out[k] = ir[k]; w_out[k] = pr[k] / sum * scale; }
+    }
+}
+
+}  // namespace lk

@@ -21,20 +21,52 @@ hipError_t launch_router_select(const float * logits, const float * bias, int n,
 hipError_t launch_dispatch(const int * sel, int P, int n_exp, int * counts, int * offsets, int * perm, int * inv,
                            int * act, int * nact, hipStream_t st);
 
-struct GemvArgs {
-    const uint8_t * w0, * w1;        // routed expert bases (tiled layout), expert e at w + e * estride; w1 only for gate/up
+struct ExpertArgs {
+    const uint4 * tab;               // LDS table image (build_table_image)
+    const uint8_t * w[2];            // routed expert bases (tiled layout) of matrix 0 / 1, expert e at w + e * estride
     size_t estride;
-    const uint8_t * sh0, * sh1;      // shared expert matrices (tiled)
-    const int8_t * aq; const float * ad;   // Q8_K activations: gate/up rows = tokens, down rows = slots
-    int K, R;                        // columns (activation length) and rows of each matrix
+    const uint8_t * sh[2];           // shared expert matrices (tiled)
+    const int8_t * aq; const float * ad;   // Q8_K activations (K columns): gate/up rows = tokens, down rows = slots
+    int K, R, nmat;                  // columns, rows per matrix, matrices per task set (2 = gate+up, 1 = down)
     const int * act, * nact, * offsets, * perm;
-    int topk, n, P, max_act;         // max_act: launch bound on used experts (host side)
-    int shared;                      // 1: the shared expert runs as the extra slot m == nact (tokens 0..n-1)
-    float * out;                     // gate/up: h [P+n][R]; down: o [P+n][R]
-    float * dbg0, * dbg1;            // optional gate / up outputs (gate/up launch only)
+    int topk, n, P, shared;          // shared: 1 = the shared expert runs as slot m == nact (tokens 0..n-1, slots P..)
+    float * terms;                   // unused (no block-term scratch)
+    unsigned * cnt_rg, * cnt_2, * queue;   // self-resetting counters (zero before the first launch); queue unused
+    float * h; int8_t * hq; float * hd;    // gate/up epilogue: h [P+n][R] and its Q8_K
+    float * gdbg, * udbg;                  // optional gate / up outputs
+    float * o;                             // down epilogue: o [P+n][R]
+    const int * inv; const float * wts; float * y;   // down: fused k-ordered combine when y != null
 };
-hipError_t launch_gemv_gateup(const GemvArgs & a, hipStream_t st);
-hipError_t launch_gemv_down(const GemvArgs & a, hipStream_t st);
+// persistent launches: grid = workgroups (one per CU); experts_init sets the LDS limit once per process
+hipError_t experts_init();
+size_t experts_terms_floats(int nmat, int slots, int R, int K);
+// the 64 KB image of the codebook / sign-mask LDS tables (TAB_BYTES), built once per context
+hipError_t build_table_image(uint4 * img, hipStream_t st);
+hipError_t launch_experts_gateup(const ExpertArgs & a, int grid, hipStream_t st);
+hipError_t launch_experts_down(const ExpertArgs & a, int grid, hipStream_t st);
+
+// ---------------------------------------------------------------- single-launch decode block (moe_decode.hip)
+// counters (self-resetting, zero before the first launch) and epoch flags inside DecodeArgs::cnt / ::flags
+constexpr int CNT_LOGIT = 0, CNT_PAIR = 1, CNT_HB = CNT_PAIR + 257 * 128, CNT_HQ = CNT_HB + 257 * 8, CNT_COMB = CNT_HQ + 257,
+              DEC_CNT = CNT_COMB + 256;
+constexpr int FLAG_LOGIT = 0, FLAG_H = 1, DEC_FLAGS = FLAG_H + 257;
+struct DecodeArgs {
+    const uint4 * tab;
+    const float * x; int n;                          // tokens [n][E], n <= 8
+    const float * Wr; const float * bias; int n_exp, n_group, topk_group, topk; float scale;
+    const uint8_t * gate, * up, * down; size_t estride;   // routed experts (tiled), expert e at + e * estride
+    const uint8_t * sh_gate, * sh_up, * sh_down;
+    int E, H;                                        // 7168, 2048 (the kernel's geometry)
+    int8_t * xq; float * xd;                         // Q8_K of x (written by workgroup 0)
+    float * logits, * probs; int * sel; float * wts; int * counts, * offsets, * perm, * inv, * act, * nact;
+    float * g, * u, * h; int8_t * hq; float * hd; float * o;   // [P+n][H] / [P+n][E] per dispatch slot
+    float * y;                                       // [n][E]
+    unsigned * cnt, * flags; unsigned epoch; int * err;
+};
+hipError_t decode_init(int ncu, int * grid);
+size_t decode_lds_bytes();
+// cooperative launch of grid workgroups (at most one per CU can be resident)
+hipError_t launch_moe_decode(const DecodeArgs & a, int grid, hipStream_t st);
 
 // y[t] = sum_k (o[inv[t*topk+k]] * w[t][k]) in k order + o[P+t] (+ resid[t] when given)
 hipError_t launch_combine(const float * o, const int * inv, const float * wts, int n, int topk, int E, int P,

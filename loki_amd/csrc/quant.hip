@@ -9,33 +9,6 @@
 
 namespace lk {
 
-__device__ __forceinline__ void q8k_block_wave(const float * __restrict__ xb, int8_t * __restrict__ qb, float * __restrict__ db) {
-    const int lane = lane_id();
-    const float4 v = reinterpret_cast<const float4 *>(xb)[lane];
-    const float xs[4] = { v.x, v.y, v.z, v.w };
-    float ba = -1.f, bv = 0.f; int bi = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { const float ax = fabsf(xs[i]); if (ax > ba) { ba = ax; bv = xs[i]; bi = 4 * lane + i; } }
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {   // first occurrence of the largest |x|: larger |x| wins, ties to the lower index
-        const float oa = __shfl_xor(ba, off), ov = __shfl_xor(bv, off); const int oi = __shfl_xor(bi, off);
-        if (oa > ba || (oa == ba && oi < bi)) { ba = oa; bv = ov; bi = oi; }
-    }
-    uint32_t packed = 0; float d = 0.f;
-    if (ba > 0.f) {
-        const float iscale = -127.f / bv;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float p = iscale * xs[i];
-            int iv = (int) rintf(p); iv = iv < 127 ? iv : 127;
-            packed |= ((uint32_t) (iv & 0xff)) << (8 * i);
-        }
-        d = 1.f / iscale;
-    }
-    reinterpret_cast<uint32_t *>(qb)[lane] = packed;
-    if (lane == 0) { *db = d; }
-}
-
 __global__ void __launch_bounds__(256) k_quant_q8k(const float * __restrict__ x, int64_t nblk, int8_t * __restrict__ q, float * __restrict__ d) {
     const int64_t b = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
     if (b >= nblk) { return; }

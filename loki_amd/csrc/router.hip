@@ -10,7 +10,7 @@
 // order in fp64 from exact fp32 x fp32 products, the 64 chunk sums are added in order in fp64, and the total is rounded
 // once to fp32. The sigmoid uses the fp64 exp contract of moe_common.h. Selection and weights are plain fp32 compares,
 // adds and one correctly rounded division, so sel and wts are bit-identical to the checker's.
-#include "moe_common.h"
+#include "moe_device.h"
 #include "moe_kernels.h"
 
 namespace lk {
@@ -55,79 +55,25 @@ hipError_t launch_router_logits(const float * W, const float * x, int n, int n_e
     return hipGetLastError();
 }
 
-struct Cand { float v; int i; };
-__device__ __forceinline__ bool better(float av, int ai, float bv, int bi) {   // valid entries have i >= 0
-    if (ai < 0) { return false; }
-    if (bi < 0) { return true; }
-    return av > bv || (av == bv && ai < bi);
-}
-
-// one wave per token; lane l holds experts 4l..4l+3 (n_exp <= 256)
+// one wave per token; lane l holds experts 4l..4l+3 (n_exp <= 256); the rule is select_token's (moe_device.h)
 __global__ void __launch_bounds__(64) k_router_select(const float * __restrict__ logits, const float * __restrict__ bias, int n, int n_exp,
                                                       int n_group, int topk_group, int topk, float scale,
                                                       float * __restrict__ probs, int * __restrict__ sel, float * __restrict__ wts) {
-#pragma clang fp contract(off)
-    __shared__ float cs[NEXP_MAX], ps[NEXP_MAX], gsc[NEXP_MAX];
-    __shared__ int allow_g[NEXP_MAX], picked[MAXK];
-    const int t = blockIdx.x, lane = threadIdx.x, per = n_exp / n_group;
-    for (int e = lane; e < n_exp; e += 64) {
-        const float p = det_sigmoid(logits[(size_t) t * n_exp + e]);
-        ps[e] = p; cs[e] = p + bias[e];
-        if (probs) { probs[(size_t) t * n_exp + e] = p; }
-    }
-    __syncthreads();
-    // group scores: top1 + top2 of the group's biased scores
-    for (int g = lane; g < n_group; g += 64) {
-        float v1 = 0.f, v2 = 0.f; int i1 = -1, i2 = -1;
-        for (int e = g * per; e < (g + 1) * per; ++e) {
-            const float c = cs[e];
-            if (i1 < 0 || c > v1) { v2 = v1; i2 = i1; v1 = c; i1 = e; }
-            else if (i2 < 0 || c > v2) { v2 = c; i2 = e; }
-        }
-        gsc[g] = v1 + v2;
-    }
-    __syncthreads();
-    for (int g = lane; g < n_group; g += 64) {   // a group stays eligible if fewer than topk_group groups beat it
-        int rank = 0; const float mine = gsc[g];
-        for (int h = 0; h < n_group; ++h) { const float o = gsc[h]; rank += (o > mine || (o == mine && h < g)) ? 1 : 0; }
-        allow_g[g] = rank < topk_group;
-    }
-    __syncthreads();
-    unsigned taken = 0;   // bit j: expert 4*lane+j already selected
-    for (int r = 0; r < topk; ++r) {
-        float bv = 0.f; int bi = -1;
+    __shared__ float scr[NEXP_MAX + 2 * 64];
+    __shared__ int so[MAXK]; __shared__ float wo[MAXK];
+    const int t = blockIdx.x, lane = threadIdx.x;
+    float lg[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int e = 4 * lane + j;
-            if (e < n_exp && !((taken >> j) & 1u) && allow_g[e / per]) {
-                const float c = cs[e];
-                if (better(c, e, bv, bi)) { bv = c; bi = e; }
-            }
-        }
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float ov = __shfl_xor(bv, off); const int oi = __shfl_xor(bi, off);
-            if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-        }
-        if (bi >= 0 && (bi >> 2) == lane) { taken |= 1u << (bi & 3); }
-        if (lane == 0) { picked[r] = bi; }
-    }
-    __syncthreads();
-    if (lane == 0) {
-        float sum = 0.f;
-        for (int r = 0; r < topk; ++r) { sum += ps[picked[r]]; }
-        sum = sum > 6.103515625e-5f ? sum : 6.103515625e-5f;
-        for (int r = 0; r < topk; ++r) {
-            sel[(size_t) t * topk + r] = picked[r];
-            wts[(size_t) t * topk + r] = ps[picked[r]] / sum * scale;
-        }
-    }
+    for (int j = 0; j < 4; ++j) { const int e = 4 * lane + j; lg[j] = e < n_exp ? logits[(size_t) t * n_exp + e] : 0.f; }
+    select_token(lg, bias, n_exp, n_group, topk_group, topk, scale, scr, so, wo, probs ? probs + (size_t) t * n_exp : nullptr);
+    lds_visible();
+    if (lane < topk) { sel[(size_t) t * topk + lane] = so[lane]; wts[(size_t) t * topk + lane] = wo[lane]; }
 }
 
 hipError_t launch_router_select(const float * logits, const float * bias, int n, int n_exp, int n_group, int topk_group,
                                 int topk, float scale, float * probs, int * sel, float * wts, hipStream_t st) {
     if (n <= 0) { return hipSuccess; }
-    if (n_exp > NEXP_MAX || n_exp % n_group || topk > MAXK || topk_group > n_group || topk > topk_group * (n_exp / n_group) || n_exp / n_group < 2) {
+    if (n_exp > NEXP_MAX || n_exp % n_group || topk > MAXK || topk_group > n_group || topk > topk_group * (n_exp / n_group) || n_exp / n_group < 2 || n_group > 64) {
         return hipErrorInvalidValue;
     }
     k_router_select<<<n, 64, 0, st>>>(logits, bias, n, n_exp, n_group, topk_group, topk, scale, probs, sel, wts);

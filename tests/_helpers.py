@@ -47,9 +47,16 @@ def rel_errors(y, ref):
 
 
 def numpy_pack_tiled(ggml_bytes, rows, cols):
-    """Independent restatement of the tiled layout (units of 4 rows x 4 blocks: 16 x 64 B qs, then 16 fp16 d)."""
+    """Independent restatement of the tiled layout: 64-row groups, per block four 16-byte chunks of 64 rows each, then
+    the fp16 d of (row group, block, row); sign words re-packed so byte l = 7 sign bits of group l | scale bit l << 7."""
     nb = cols // 256
     blk = np.asarray(ggml_bytes, np.uint8).reshape(rows, nb, 66)
-    d = blk[:, :, :2].reshape(rows // 4, 4, nb // 4, 4, 2).transpose(0, 2, 1, 3, 4).reshape(rows // 4, nb // 4, 32)
-    qs = blk[:, :, 2:].reshape(rows // 4, 4, nb // 4, 4, 64).transpose(0, 2, 1, 3, 4).reshape(rows // 4, nb // 4, 1024)
-    return np.concatenate([qs, d], axis=2).reshape(-1)
+    d = blk[:, :, :2].reshape(rows // 64, 64, nb, 2).transpose(0, 2, 1, 3)
+    w = blk[:, :, 2:].copy().view("<u4").reshape(rows, nb, 16).astype(np.uint64)
+    a1 = w[:, :, 1::2]
+    t = np.zeros_like(a1)
+    for l in range(4):
+        t |= (((a1 >> np.uint64(7 * l)) & np.uint64(127)) | (((a1 >> np.uint64(28 + l)) & np.uint64(1)) << np.uint64(7))) << np.uint64(8 * l)
+    w[:, :, 1::2] = t
+    qs = w.astype("<u4").view(np.uint8).reshape(rows // 64, 64, nb, 4, 16).transpose(0, 2, 3, 1, 4)
+    return np.concatenate([qs.reshape(-1), d.reshape(-1)])

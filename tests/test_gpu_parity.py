@@ -156,3 +156,55 @@ def test_block_deterministic(ctx, layer):
     y2 = ctx.moe_layer(layer, x)
     ctx.sync()
     assert np.array_equal(y1.cpu().numpy().view(np.uint32), y2.cpu().numpy().view(np.uint32))
+
+
+def _routing_state(ctx, n):
+    """Routing outputs of the last fl_moe_layer call, copied to the host."""
+    dbg = ctx.debug()
+    P = n * 8
+    out = {
+        "sel": ctx.d2h(dbg.sel, (P,), np.int32), "wts": ctx.d2h(dbg.wts, (P,), np.float32),
+        "perm": ctx.d2h(dbg.perm, (P,), np.int32), "inv": ctx.d2h(dbg.inv, (P,), np.int32),
+        "nact": ctx.d2h(dbg.nact, (1,), np.int32), "counts": ctx.d2h(dbg.counts, (NEXP,), np.int32),
+        "offsets": ctx.d2h(dbg.offsets, (NEXP + 1,), np.int32),
+        "xq": ctx.d2h(dbg.xq, (n, E), np.int8), "xd": ctx.d2h(dbg.xd, (n, E // 256), np.float32),
+    }
+    out["act"] = ctx.d2h(dbg.act, (int(out["nact"][0]),), np.int32)
+    out["o"] = ctx.d2h(dbg.o, (P + n, E), np.float32)
+    return out
+
+
+@pytest.mark.parametrize("n", [1, 2, 5, 8])
+def test_fused_decode_matches_per_pass(ctx, layer, n):
+    """The single-launch decode block and the per-pass kernels give bit-identical outputs and routing."""
+    x = make_x(ctx, n, seed=300 + n)
+    try:
+        ctx.set_fused(False)
+        y_ref = ctx.moe_layer(layer, x).clone()
+        ctx.sync()
+        ref = _routing_state(ctx, n)
+        ctx.set_fused(True)
+        y = ctx.moe_layer(layer, x)
+        ctx.sync()
+        got = _routing_state(ctx, n)
+    finally:
+        ctx.set_fused(True)
+    for k in ref:
+        assert np.array_equal(np.asarray(got[k]).view(np.uint8), np.asarray(ref[k]).view(np.uint8)), k
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), y_ref.cpu().numpy().view(np.uint32))
+
+
+def test_fused_decode_repeated_launches(ctx, layer):
+    """Epoch flags and self-resetting counters: a sequence of launches with changing batch sizes stays exact."""
+    xs = {n: make_x(ctx, n, seed=400 + n) for n in (1, 3, 8)}
+    want = {}
+    try:
+        ctx.set_fused(False)
+        for n, x in xs.items():
+            want[n] = ctx.moe_layer(layer, x).cpu().numpy()
+    finally:
+        ctx.set_fused(True)
+    for n in (1, 8, 3, 1, 1, 8, 3, 8):
+        y = ctx.moe_layer(layer, xs[n])
+        ctx.sync()
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), want[n].view(np.uint32)), n
