@@ -9,8 +9,9 @@ timed region. Each step takes a fresh x (so different experts) and the steps rot
 layers (3 x 2.9 GB), so the 256 MB MALL cannot serve repeated weights.
 
 Prints ONE JSON line: value = microseconds per token of the whole block (router, dispatch, experts, combine), plus the
-achieved HBM bandwidth, the roofline of the dominant kernel (gate/up mat-vec, timed live with HIP events on the stream
-it runs on) and the CPU checker timed on this host's cores on a bounded sample of the same workload.
+achieved HBM bandwidth, the roofline of the dominant kernel (decode: k_moe_decode, the whole block in one cooperative
+launch; prefill: the gate/up expert kernel), timed live with HIP events recorded on the stream the kernel runs on, and
+the CPU checker timed on this host's cores on a bounded sample of the same workload.
 """
 import argparse
 import json
@@ -40,7 +41,7 @@ def log(*a):
 
 def step_bytes(n, U):
     """Algorithmic HBM bytes of one block call: every used expert (and the shared one) read once, the router once,
-    x read and y written once (SURVEY 8(d) formula)."""
+    x read and y written once."""
     return (U + 1) * EXPERT_BYTES + ROUTER_BYTES + 2 * n * E * 4
 
 
@@ -95,9 +96,10 @@ def run_workload(ctx, torch, name, steps, warmup, copies, seed=20260101):
     ctx.set_profile(False)
     calls, stage = ctx.stage_ms(reset=True)
     stage = {k: v / max(calls, 1) for k, v in stage.items()}
+    fused = bool(ctx.debug().fused)
     U = [distinct_experts(ctx, layers[(warmup + i) % copies], [xs[warmup + i]])[0] for i in range(steps)]
     mean_U = sum(U) / len(U)
-    res = dict(name=name, desc=desc, n=n, ms=ms, U=mean_U, stage_ms=stage,
+    res = dict(name=name, desc=desc, n=n, ms=ms, U=mean_U, stage_ms=stage, fused=fused,
                bytes=sum(step_bytes(n, u) for u in U) / len(U),
                gu_bytes=sum(gateup_bytes(n, u) for u in U) / len(U))
     res["gbs"] = res["bytes"] / (ms * 1e-3) / 1e9
@@ -134,7 +136,7 @@ def cpu_baseline(ctx, torch, res, budget_s=12.0, max_steps=8):
 
 def load_traffic(kernel, workload):
     """HBM bytes per launch from committed rocprofv3 --pmc summaries (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)."""
-    p = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_%s_%s.json" % (kernel, workload))
+    p = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_%s_%s.json" % (kernel.split("<")[0], workload))
     if os.path.exists(p):
         with open(p) as f:
             return json.load(f).get("bytes_per_launch")
@@ -150,22 +152,36 @@ def main():
     ap.add_argument("--copies", type=int, default=3, help="independently seeded layers rotated over the steps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the decode-1 / prefill-512 side measurements")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a plain 1 GiB device copy (the reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        log("bench.py: this build runs on one GPU only (the MoE block is not sharded here; see DESIGN.md for how it "
-            "would shard); got --gpus %d, WORLD_SIZE %d" % (args.gpus, world))
+        log("bench.py: this build runs on one GPU only (the MoE block is not sharded across GPUs); got --gpus %d, "
+            "WORLD_SIZE %d" % (args.gpus, world))
         sys.exit(2)
     import torch
     from loki_amd import Context
     ctx = Context()
     res = run_workload(ctx, torch, args.workload, args.steps, args.warmup, args.copies)
     n = res["n"]
-    gu_ms = res["stage_ms"]["gate_up"]
-    gu_gbs = res["gu_bytes"] / (gu_ms * 1e-3) / 1e9
-    log("[bench] %s: %.1f us/step, %.2f us/token, %.0f GB/s (U=%.1f); stages (us): %s" % (
-        args.workload, res["ms"] * 1e3, res["ms"] * 1e3 / n, res["gbs"], res["U"],
-        ", ".join("%s %.1f" % (k, v * 1e3) for k, v in res["stage_ms"].items())))
+    if res["fused"]:   # one launch = the whole block: its bytes are the step's
+        kname, k_ms, k_bytes = "k_moe_decode", res["stage_ms"]["gate_up"], res["bytes"]
+        stages = {"block": k_ms}
+    else:
+        kname, k_ms, k_bytes = "k_experts<gate_up>", res["stage_ms"]["gate_up"], res["gu_bytes"]
+        stages = res["stage_ms"]
+    k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
+    log("[bench] %s: %.1f us/step, %.2f us/token, %.0f GB/s (U=%.1f); kernel %s %.1f us (%.0f GB/s); stages (us): %s" % (
+        args.workload, res["ms"] * 1e3, res["ms"] * 1e3 / n, res["gbs"], res["U"], kname, k_ms * 1e3, k_gbs,
+        ", ".join("%s %.1f" % (k, v * 1e3) for k, v in stages.items())))
+    if args.copy_probe:
+        a = torch.empty(1 << 28, dtype=torch.float32, device="cuda"); b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log("[bench] copy probe: 3 x %d bytes read + written" % (a.numel() * 4))
+        del a, b
     extra = {}
     if not args.no_extra:
         for wl, st in (("decode1", 30), ("prefill512", 5)):
@@ -175,7 +191,8 @@ def main():
             extra[wl] = {"us_per_token": round(r["ms"] * 1e3 / r["n"], 3), "ms_per_step": round(r["ms"], 4),
                          "tokens_per_s": round(r["n"] / (r["ms"] * 1e-3), 1), "hbm_gbs": round(r["gbs"], 1),
                          "hbm_frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "distinct_experts": round(r["U"], 1),
-                         "stage_us": {k: round(v * 1e3, 2) for k, v in r["stage_ms"].items()}}
+                         "kernel_us": round(r["stage_ms"]["gate_up"] * 1e3, 2) if r["fused"] else None,
+                         "stage_us": None if r["fused"] else {k: round(v * 1e3, 2) for k, v in r["stage_ms"].items()}}
             log("[bench] %s: %s" % (wl, json.dumps(extra[wl])))
             del r
     cpu = None
@@ -199,11 +216,11 @@ def main():
         "hbm_gbs": round(res["gbs"], 1),
         "hbm_frac": round(res["gbs"] / HBM_PEAK_GBS, 4),
         "distinct_experts": round(res["U"], 1),
-        "roofline": {"kernel": "k_iq2_gemv<gate_up>", "bound": "hbm", "achieved": round(gu_gbs, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": load_traffic("gate_up", args.workload),
-                     "algorithmic_bytes_per_launch": int(res["gu_bytes"]), "avg_launch_us": round(gu_ms * 1e3, 2)},
-        "stage_us": {k: round(v * 1e3, 2) for k, v in res["stage_ms"].items()},
+        "roofline": {"kernel": kname, "bound": "hbm", "achieved": round(k_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(k_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic(kname, args.workload),
+                     "algorithmic_bytes_per_launch": int(k_bytes), "avg_launch_us": round(k_ms * 1e3, 2)},
+        "stage_us": {k: round(v * 1e3, 2) for k, v in stages.items()},
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -122,6 +122,7 @@ typedef struct FLDebug {
     const float * o;                                   /* [P+n][E] */
     const float * g, * u;                              /* gate / up outputs when debug capture is on */
     int n, P, topk;
+    int fused;                                         /* 1: the last fl_moe_layer call ran as one cooperative launch */
 } FLDebug;
 int fl_debug(FLCtx *, FLDebug * out);
 int fl_set_debug(FLCtx *, int capture_gate_up);

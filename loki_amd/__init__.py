@@ -33,7 +33,7 @@ class FLMoeLayer(ctypes.Structure):
 class FLDebug(ctypes.Structure):
     _fields_ = [(n, P_) for n in ("xq", "xd", "logits", "probs", "sel", "wts", "counts", "offsets", "perm", "inv",
                                   "act", "nact", "h", "hq", "hd", "o", "g", "u")] + \
-               [("n", ctypes.c_int), ("P", ctypes.c_int), ("topk", ctypes.c_int)]
+               [("n", ctypes.c_int), ("P", ctypes.c_int), ("topk", ctypes.c_int), ("fused", ctypes.c_int)]
 
 
 class FLW(ctypes.Structure):

@@ -41,7 +41,7 @@ struct FLCtx {
     int dbg_gu = 0;
     DBuf<int8_t> xq, hq; DBuf<float> xd, logits, probs, wts, h, hd, o, g, u;
     DBuf<int> sel, counts, offsets, perm, inv, act, nact;
-    int last_n = 0, last_P = 0;
+    int last_n = 0, last_P = 0, last_fused = 0;
     // stage timing (fl_set_profile): one set of NSTAGE+1 events per profiled call, summed by fl_stage_ms
     int prof = 0;
     std::vector<std::vector<hipEvent_t>> ev_free, ev_pending;

@@ -247,7 +247,7 @@ extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, in
     ALLOC(c, c->h, rows * H); ALLOC(c, c->hq, rows * H); ALLOC(c, c->hd, rows * (H / 256)); ALLOC(c, c->o, rows * E);
     if (c->dbg_gu || fused) { ALLOC(c, c->g, rows * H); ALLOC(c, c->u, rows * H); }
     if (int rc = ensure_expert_scratch(c, rows, E, H)) { return rc; }
-    c->last_n = n; c->last_P = P;
+    c->last_n = n; c->last_P = P; c->last_fused = fused ? 1 : 0;
     hipStream_t st = c->st;
     std::vector<hipEvent_t> * ev = prof_begin(c);
     if (fused) {
@@ -327,7 +327,7 @@ extern "C" int fl_debug(FLCtx * c, FLDebug * out) {
     out->xq = c->xq.p; out->xd = c->xd.p; out->logits = c->logits.p; out->probs = c->probs.p; out->sel = c->sel.p; out->wts = c->wts.p;
     out->counts = c->counts.p; out->offsets = c->offsets.p; out->perm = c->perm.p; out->inv = c->inv.p; out->act = c->act.p; out->nact = c->nact.p;
     out->h = c->h.p; out->hq = c->hq.p; out->hd = c->hd.p; out->o = c->o.p; out->g = c->dbg_gu ? c->g.p : nullptr; out->u = c->dbg_gu ? c->u.p : nullptr;
-    out->n = c->last_n; out->P = c->last_P; out->topk = c->topk;
+    out->n = c->last_n; out->P = c->last_P; out->topk = c->topk; out->fused = c->last_fused;
     return FL_OK;
 }
 
