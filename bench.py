@@ -152,6 +152,8 @@ def main():
     ap.add_argument("--copies", type=int, default=3, help="independently seeded layers rotated over the steps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the decode-1 / prefill-512 side measurements")
+    ap.add_argument("--fused", type=int, default=None, choices=(0, 1, 2),
+                    help="decode path: 1 cooperative single launch (library default), 2 regular single launch, 0 per pass")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (the reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
@@ -163,6 +165,8 @@ def main():
     import torch
     from loki_amd import Context
     ctx = Context()
+    if args.fused is not None:
+        ctx.set_fused(args.fused)
     res = run_workload(ctx, torch, args.workload, args.steps, args.warmup, args.copies)
     n = res["n"]
     if res["fused"]:   # one launch = the whole block: its bytes are the step's

@@ -126,8 +126,10 @@ typedef struct FLDebug {
 } FLDebug;
 int fl_debug(FLCtx *, FLDebug * out);
 int fl_set_debug(FLCtx *, int capture_gate_up);
-/* 1 (default): fl_moe_layer runs a decode batch (n <= 8, E 7168, H 2048) as one cooperative launch; 0: one launch per pass */
-int fl_set_fused(FLCtx *, int on);
+/* decode batches (n <= 8, E 7168, H 2048) of fl_moe_layer: 1 (default) = the whole block as one cooperative launch;
+ * 2 = the same kernel with a regular launch (assumes nothing else occupies the CUs: waits are bounded and report a
+ * timeout through fl_sync otherwise); 0 = one launch per pass */
+int fl_set_fused(FLCtx *, int mode);
 
 /* stage timing with HIP events on the context's stream: stages 0..5 = quant_x, router_logits, router_select, dispatch,
  * gate_up (with SwiGLU and Q8_K(h)), down (with the combine). fl_stage_ms waits for the profiled calls and returns their count (summed ms in ms[]). */

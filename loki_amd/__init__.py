@@ -195,9 +195,10 @@ class Context:
     def set_debug(self, capture_gate_up):
         self.check(lib().fl_set_debug(self.ctx, 1 if capture_gate_up else 0))
 
-    def set_fused(self, on):
-        """Decode batches (n <= 8) as one cooperative launch (default) or one launch per pass."""
-        self.check(lib().fl_set_fused(self.ctx, 1 if on else 0))
+    def set_fused(self, mode):
+        """Decode batches (n <= 8): 1 / True = one cooperative launch (default), 2 = the same kernel with a regular
+        launch, 0 / False = one launch per pass."""
+        self.check(lib().fl_set_fused(self.ctx, int(mode)))
 
     # ---- building blocks
     def quant_q8k(self, x):

@@ -42,7 +42,7 @@ extern "C" void fl_free(FLCtx * c) {
     c->h.release(); c->hd.release(); c->o.release(); c->g.release(); c->u.release();
     c->sel.release(); c->counts.release(); c->offsets.release(); c->perm.release(); c->inv.release(); c->act.release(); c->nact.release();
     compat_free(c); c->zero_i.release(); c->terms.release(); c->cnt.release();
-    c->tab.release(); c->dcnt.release(); c->dflags.release(); c->derr.release();
+    c->tab.release(); c->dcnt.release(); c->dflags.release(); c->derr.release(); c->dlogit.release();
     for (auto & v : c->ev_free) { for (auto e : v) { (void) hipEventDestroy(e); } }
     for (auto & v : c->ev_pending) { for (auto e : v) { (void) hipEventDestroy(e); } }
     (void) hipEventDestroy(c->em0); (void) hipEventDestroy(c->em1); (void) hipStreamDestroy(c->own);
@@ -92,7 +92,11 @@ extern "C" int fl_set_experts(FLCtx * c, int n_exp) {
     c->n_exp = n_exp; return FL_OK;
 }
 extern "C" int fl_set_debug(FLCtx * c, int capture) { if (!c) { return FL_EINVAL; } c->dbg_gu = capture ? 1 : 0; return FL_OK; }
-extern "C" int fl_set_fused(FLCtx * c, int on) { if (!c) { return FL_EINVAL; } c->fused = on ? 1 : 0; return FL_OK; }
+extern "C" int fl_set_fused(FLCtx * c, int mode) {
+    if (!c) { return FL_EINVAL; }
+    if (mode < 0 || mode > 2) { return fail(c, FL_EINVAL, "fused mode %d outside 0..2", mode); }
+    c->fused = mode; return FL_OK;
+}
 
 // ================================================================ building blocks
 static int check_rule(FLCtx * c, int n_exp) {
@@ -110,7 +114,7 @@ extern "C" int fl_route_dev(FLCtx * c, const float * W, const float * bias, cons
     if (n < 0 || n > 65536) { return fail(c, FL_ERANGE, "n = %d outside 0..65536", n); }
     if (n == 0) { return FL_OK; }
     if (!W || !bias || !x || !sel || !w) { return fail(c, FL_EINVAL, "null pointer"); }
-    if (E <= 0 || E % 256) { return fail(c, FL_EINVAL, "E = %d must be a positive multiple of 256", E); }
+    if (E <= 0 || E % 1024) { return fail(c, FL_EINVAL, "E = %d must be a positive multiple of 1024", E); }
     if (int rc = check_rule(c, n_exp)) { return rc; }
     if (!covers(W, (size_t) n_exp * E * 4) || !covers(bias, (size_t) n_exp * 4) || !covers(x, (size_t) n * E * 4)) {
         return fail(c, FL_EINVAL, "router weight, bias or x allocation smaller than its shape (%d experts, %d rows of %d)", n_exp, n, E);
@@ -252,11 +256,14 @@ extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, in
     std::vector<hipEvent_t> * ev = prof_begin(c);
     if (fused) {
         if (!c->dcnt.p) {
-            ALLOC(c, c->dcnt, DEC_CNT); ALLOC(c, c->dflags, DEC_FLAGS); ALLOC(c, c->derr, 1);
+            ALLOC(c, c->dcnt, DEC_CNT); ALLOC(c, c->dflags, DEC_FLAGS); ALLOC(c, c->derr, 1); ALLOC(c, c->dlogit, 8 * NEXP_MAX);
             TRY(c, hipMemsetAsync(c->dcnt.p, 0, DEC_CNT * sizeof(unsigned), st));
             TRY(c, hipMemsetAsync(c->derr.p, 0, sizeof(int), st));
         }
-        if (++c->epoch == 1) { TRY(c, hipMemsetAsync(c->dflags.p, 0, DEC_FLAGS * sizeof(unsigned), st)); }   // first use, or the epoch wrapped
+        if (++c->epoch == 1) {   // first use, or the epoch wrapped: no stale word may carry the new epoch
+            TRY(c, hipMemsetAsync(c->dflags.p, 0, DEC_FLAGS * sizeof(unsigned), st));
+            TRY(c, hipMemsetAsync(c->dlogit.p, 0, 8 * NEXP_MAX * sizeof(uint64_t), st));
+        }
         DecodeArgs d{};
         d.tab = c->tab.p; d.x = x; d.n = n;
         d.Wr = L->gate_inp; d.bias = L->probs_b; d.n_exp = ne; d.n_group = c->n_group; d.topk_group = c->topk_group; d.topk = tk; d.scale = c->scale;
@@ -267,10 +274,10 @@ extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, in
         d.xq = c->xq.p; d.xd = c->xd.p; d.logits = c->logits.p; d.probs = c->probs.p; d.sel = c->sel.p; d.wts = c->wts.p;
         d.counts = c->counts.p; d.offsets = c->offsets.p; d.perm = c->perm.p; d.inv = c->inv.p; d.act = c->act.p; d.nact = c->nact.p;
         d.g = c->g.p; d.u = c->u.p; d.h = c->h.p; d.hq = c->hq.p; d.hd = c->hd.p; d.o = c->o.p; d.y = y;
-        d.cnt = c->dcnt.p; d.flags = c->dflags.p; d.epoch = c->epoch; d.err = c->derr.p;
+        d.cnt = c->dcnt.p; d.flags = c->dflags.p; d.epoch = c->epoch; d.err = c->derr.p; d.tlogits = c->dlogit.p;
         // stages: the whole block is one launch, reported as stage 4; the others are empty
         for (int i = 0; i <= 4; ++i) { prof_mark(c, ev, i); }
-        TRY(c, launch_moe_decode(d, c->dec_grid, st));
+        TRY(c, launch_moe_decode(d, c->dec_grid, c->fused == 1, st));
         prof_mark(c, ev, 5); prof_mark(c, ev, 6);
         return FL_OK;
     }

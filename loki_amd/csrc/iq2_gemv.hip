@@ -222,10 +222,11 @@ size_t experts_terms_floats(int, int, int, int) { return 0; }
 
 // the LDS table image (layout at TAB_BYTES in moe_common.h), once, in device memory
 __global__ void k_table_image(uint64_t * img) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;   // 8-byte entry: line e = i / 32, slot r = i % 32
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;   // 8-byte word: line e = i / 32, slot r = i % 32
     if (i >= TAB_BYTES / 8) { return; }
     const int e = i >> 5, r = i & 31;
-    img[i] = r < 16 ? g_iq2xxs_grid[e] : sign_mask64(ksigns8((uint32_t) e & 127u));
+    const uint64_t m = sign_mask64(ksigns8((uint32_t) e & 127u));
+    img[i] = r < 16 ? g_iq2xxs_grid[e] : ((r & 1) ? (m & 0x0101010101010101ull) : m);   // sign entries: {m, m & 0x01..}
 }
 hipError_t build_table_image(uint4 * img, hipStream_t st) {
     k_table_image<<<TAB_BYTES / 8 / 256, 256, 0, st>>>(reinterpret_cast<uint64_t *>(img));

@@ -62,12 +62,14 @@ __host__ __device__ inline size_t tiled_d_off(int rg, int j, int row, int R, int
     return (size_t) (R / RG) * nb * 4096 + ((size_t) (rg * nb + j) * RG + row) * 2;
 }
 
-// ---------------------------------------------------------------- bank-replicated LDS tables
-// Entry e (0..255) owns the 256-byte line [256 e, 256 e + 256): 16 replicas of the codebook word grid[e] at +0..127 and
-// 16 replicas of the sign masks of the tiled sign byte e (bit 7 = a scale bit, ignored) at +128..255. Lane l reads
-// replica l % 16, so 16 lanes' 8-byte reads cover all banks whatever the indices, and the byte address is
-// (index << 8) | (replica << 3): one v_perm_b32 builds it from the packed index word. The image is built once per
-// context (build_table_image) and copied into LDS by every workgroup (tables_copy).
+// ---------------------------------------------------------------- LDS tables
+// Entry e (0..255) owns the 256-byte line [256 e, 256 e + 256): 16 copies of the codebook word grid[e] at +0..127 and
+// 8 copies of the 16-byte sign entry of the tiled sign byte e at +128..255 (bit 7 = a scale bit, ignored): the byte
+// masks m (0x00 / 0xFF per weight) and m & 0x01010101 per 4 weights, so applying the signs is one v_xad_u32 per 4
+// weights. Lane l reads copy l % 16 (grid) / l % 8 (signs); the byte address is (index << 8) | copy offset, which one
+// v_perm_b32 builds from the packed index word. A wave64 LDS read costs about the same for 8 and 16 bytes, so the
+// wider sign entry is free. The image is built once per context (build_table_image) and copied into LDS by every
+// workgroup (tables_copy).
 constexpr int TAB_BYTES = 256 * 256;
 
 __device__ __forceinline__ uint32_t xad(uint32_t a, uint32_t b, uint32_t c) { return (a ^ b) + c; }   // one v_xad_u32
@@ -86,6 +88,10 @@ __device__ __forceinline__ uint4 gload16(const void * p) { const u32x4 v = *(con
 __device__ __forceinline__ uint2 gload8(const void * p) { const u32x2 v = *(const LK_GLOBAL u32x2 *) p; return make_uint2(v.x, v.y); }
 __device__ __forceinline__ float4 gloadf4(const void * p) { const f32x4 v = *(const LK_GLOBAL f32x4 *) p; return make_float4(v.x, v.y, v.z, v.w); }
 __device__ __forceinline__ uint2 lload8(uint32_t addr) { const u32x2 v = *(const LK_LOCAL u32x2 *) (size_t) addr; return make_uint2(v.x, v.y); }
+__device__ __forceinline__ uint4 lload16(uint32_t addr) { const u32x4 v = *(const LK_LOCAL u32x4 *) (size_t) addr; return make_uint4(v.x, v.y, v.z, v.w); }
+// a lane's table words: grid copy (lane % 16) * 8, sign copy 128 + (lane % 8) * 16, over the table base
+__device__ __forceinline__ uint32_t tab_word_grid(uint32_t base, int lane) { return base | ((uint32_t) (lane & 15) << 3); }
+__device__ __forceinline__ uint32_t tab_word_sign(uint32_t base, int lane) { return base | 128u | ((uint32_t) (lane & 7) << 4); }
 
 // LDS byte address of the table entry for byte L of an index word: byte 1 = that byte; bytes 0, 2, 3 from `tr` = the
 // table base (64 KB aligned) | the lane's replica offset
@@ -95,12 +101,13 @@ template <int L> __device__ __forceinline__ uint32_t tab_addr(uint32_t word, uin
 
 // signed int8 weights of a group from its codebook word g and sign masks m: magnitudes with the signs applied. Grid bytes
 // are never 0, so the per-byte two's-complement negation (g ^ 0xFF) + 1 never carries into the next byte.
-__device__ __forceinline__ void iq2_apply(uint2 g, uint2 m, uint32_t & lo, uint32_t & hi) {
-    lo = xad(g.x, m.x, m.x & 0x01010101u);
-    hi = xad(g.y, m.y, m.y & 0x01010101u);
+__device__ __forceinline__ void iq2_apply(uint2 g, uint4 m, uint32_t & lo, uint32_t & hi) {
+    lo = xad(g.x, m.x, m.z);
+    hi = xad(g.y, m.y, m.w);
 }
+// tr: this lane's table word (base | copy offsets): grid copy in bits 3..6, sign copy in bits 4..6 of the +128 half
 template <int L> __device__ __forceinline__ uint2 tab_grid(uint32_t a0, uint32_t tr) { return lload8(tab_addr<L>(a0, tr)); }
-template <int L> __device__ __forceinline__ uint2 tab_sign(uint32_t a1t, uint32_t tr) { return lload8(tab_addr<L>(a1t, tr) + 128); }
+template <int L> __device__ __forceinline__ uint4 tab_sign(uint32_t a1t, uint32_t trs) { return lload16(tab_addr<L>(a1t, trs)); }
 
 // 2 * scale nibble + 1 of a tiled sign word (nibble bit l = bit 7 of byte l)
 __device__ __forceinline__ int iq2_scale(uint32_t a1t) {

@@ -4,15 +4,14 @@
 // routing (fl_fetch :587-598, eng:793-818), then per fl_moe (:599-612) quant_x, tc_matvec gate/up, swiglu_q8,
 // tc_matvec down and moe_combine as separate launches. At batch 1-8 every one of those launches is latency-bound, so
 // here one workgroup per CU (all resident: cooperative launch) runs the block end to end:
-//   1. every workgroup copies the codebook/sign table image into LDS and quantises the n token rows to Q8_K (staged
-//      layout of moe_device.h);
-//   2. workgroup b computes the router logits of expert b for every token (the fp64 64-chunk contract of router.hip),
-//      one wave per token; the last workgroup to finish raises the logits flag. Waves without a token meanwhile run the
-//      shared expert's gate/up tasks, which need no routing;
-//   3. every workgroup waits for the flag, selects each token's experts (select_token, one wave per token) and builds
-//      the dispatch (stable counting sort of the n * topk pairs) in its own LDS -- redundant, but cheaper than another
-//      device-wide hand-off;
-//   4. tasks round-robin over all waves of the grid: gate/up tasks (expert slot, 16 rows, matrix) -- the second task of
+//   1. workgroup b computes the router logits of expert b for every token (the fp64 chunk-and-tree contract) and
+//      publishes each as an epoch-tagged 64-bit word; then it copies the codebook/sign table image into LDS and
+//      quantises the n token rows to Q8_K (staged layout of moe_device.h);
+//   2. every workgroup polls the tagged logits, selects each token's experts (select_token, one wave per token) and
+//      builds the dispatch (stable counting sort of the n * topk pairs) in its own LDS -- redundant, but cheaper than
+//      another device-wide hand-off. Waves without a token meanwhile run the shared expert's gate/up tasks, which need
+//      no routing;
+//   3. tasks round-robin over all waves of the grid: gate/up tasks (expert slot, 16 rows, matrix) -- the second task of
 //      a (gate, up) pair forms h = silu(g) * u, the last of a 256-row block quantises it to Q8_K, the last block of an
 //      expert raises the expert's h flag -- then down tasks (expert slot, 32 rows) that prefetch their weights, wait for
 //      the expert's h flag, and write o; the last expert of a row group computes y = sum_k w_k o_k (k order) + shared.
@@ -123,33 +122,79 @@ __device__ __noinline__ void quant_tokens(const DecodeArgs & a, lds_t lds, int w
 }
 
 // ---------------------------------------------------------------- phase 2: router logits of expert e for token t
-// chunk c = lane (K / 64 = 112 values) summed in order in fp64 from exact fp32 x fp32 products; the 64 chunk sums added
-// in order by lane 0; one rounding to fp32
-__device__ __noinline__ void router_logit(const DecodeArgs & a, int t, int e) {
+// the contract of moe_device.h (256 in-order chunk sums, pairwise tree, one rounding); one wave per (expert, token)
+// Router logits of expert e for all n tokens by the whole workgroup. Thread (quarter w = wave & 3, lane) owns chunk
+// 64 w + lane (K/256 = 28 values) of every token t with t % 2 == wave / 4, so each thread issues its 7 + 7 * (tokens)
+// 16-byte loads at once. Tree levels 1-6 run inside the wave (one chunk per lane), 7-8 combine the four quarters'
+// totals through LDS. Each logit is published as one 64-bit word {epoch, fp32 bits}: consumers poll the words
+// themselves, so no counter, flag or store-completion wait sits between the router and the selection.
+__device__ __noinline__ void router_phase(const DecodeArgs & a, lds_t lds, int wave, int e) {
 #pragma clang fp contract(off)
-    const int lane = lane_id();
-    constexpr int L4 = DE / 64 / 4;   // 28 float4 per chunk
-    const float * w4 = a.Wr + (size_t) e * DE + (size_t) lane * (DE / 64);
-    const float * x4 = a.x + (size_t) t * DE + (size_t) lane * (DE / 64);
-    double s = 0.0;
+    constexpr int L4 = DE / 1024;   // float4 per chunk (7)
+    const int lane = lane_id(), qt = wave & 3, half = wave >> 2, c = qt * 64 + lane;
+    LK_LOCAL double * part = reinterpret_cast<LK_LOCAL double *>(lds + L_DST);   // [token][quarter]
+    constexpr int TB = 2;   // tokens per load batch (register budget)
+    float4 wv[L4];
+    const float * wc = a.Wr + (size_t) e * DE + (size_t) c * 4 * L4;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        float4 wv[L4 / 2], xv[L4 / 2];
+    for (int i = 0; i < L4; ++i) { wv[i] = gloadf4(wc + 4 * i); }
+    for (int k0 = 0; k0 < DMAX_N / 2; k0 += TB) {
+        if (2 * k0 + half >= a.n) { break; }
+        float4 xv[TB][L4];
 #pragma unroll
-        for (int i = 0; i < L4 / 2; ++i) { wv[i] = gloadf4(w4 + 4 * (h * (L4 / 2) + i)); xv[i] = gloadf4(x4 + 4 * (h * (L4 / 2) + i)); }
+        for (int k = 0; k < TB; ++k) {
+            const int t = 2 * (k0 + k) + half;
+            if (t < a.n) {
 #pragma unroll
-        for (int i = 0; i < L4 / 2; ++i) {
-            s += (double) xv[i].x * (double) wv[i].x; s += (double) xv[i].y * (double) wv[i].y;
-            s += (double) xv[i].z * (double) wv[i].z; s += (double) xv[i].w * (double) wv[i].w;
+                for (int i = 0; i < L4; ++i) { xv[k][i] = gloadf4(a.x + (size_t) t * DE + (size_t) c * 4 * L4 + 4 * i); }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < TB; ++k) {
+            const int t = 2 * (k0 + k) + half;
+            if (t < a.n) {
+                double s = 0.0;
+#pragma unroll
+                for (int i = 0; i < L4; ++i) {
+                    s += (double) xv[k][i].x * (double) wv[i].x; s += (double) xv[k][i].y * (double) wv[i].y;
+                    s += (double) xv[k][i].z * (double) wv[i].z; s += (double) xv[k][i].w * (double) wv[i].w;
+                }
+                const double q = tree64(s);
+                if (lane == 0) { part[t * 4 + qt] = q; }
+            }
         }
     }
-    // the 64 chunk sums in chunk order, read back lane by lane (uniform)
-    const uint64_t sb = __builtin_bit_cast(uint64_t, s);
-    double tot = __builtin_bit_cast(double, ((uint64_t) rdlane((uint32_t) (sb >> 32), 0) << 32) | rdlane((uint32_t) sb, 0));
-    for (int c = 1; c < 64; ++c) {
-        tot += __builtin_bit_cast(double, ((uint64_t) rdlane((uint32_t) (sb >> 32), c) << 32) | rdlane((uint32_t) sb, c));
+    __syncthreads();
+    if (threadIdx.x < (unsigned) a.n) {
+        const int t = threadIdx.x;
+        const float l = (float) ((part[t * 4 + 0] + part[t * 4 + 1]) + (part[t * 4 + 2] + part[t * 4 + 3]));
+        const size_t o = (size_t) t * a.n_exp + e;
+        __hip_atomic_store(gptr(a.tlogits + o), ((uint64_t) a.epoch << 32) | __builtin_bit_cast(uint32_t, l), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        gptr(a.logits)[o] = l;   // the layer's logits (read after the launch)
     }
-    if (lane == 0) { st_agent(a.logits + (size_t) t * a.n_exp + e, (float) tot); }
+    __syncthreads();   // part[] is reused by the next expert
+}
+
+// token t's logits of the lane's experts 4 lane + j, once every word carries this launch's epoch; false on timeout
+__device__ __forceinline__ bool wait_logits(const DecodeArgs & a, int t, float (&lg)[4]) {
+    const int lane = lane_id();
+    for (int it = 0; it < (1 << 20); ++it) {
+        bool ok = true;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = 4 * lane + j;
+            if (e < a.n_exp) {
+                const uint64_t w = __hip_atomic_load(gptr(a.tlogits + (size_t) t * a.n_exp + e), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ok = ok && (uint32_t) (w >> 32) == a.epoch;
+                lg[j] = __builtin_bit_cast(float, (uint32_t) w);
+            } else {
+                lg[j] = 0.f;
+            }
+        }
+        if (__ballot(!ok) == 0) { return true; }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    return false;
 }
 
 // ---------------------------------------------------------------- phase 3: dispatch of the n * topk pairs (one wave)
@@ -306,42 +351,36 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs a) {
     const lds_t lds = (lds_t) dyn_lds;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
     const int G = gridDim.x, n = a.n, P = n * a.topk;
-    LK_LOCAL unsigned * ctl = reinterpret_cast<LK_LOCAL unsigned *>(lds + L_CTL);   // [0] router waves done, [1] selections done, [2] routing ready (1 ok, 2 failed)
+    LK_LOCAL unsigned * ctl = reinterpret_cast<LK_LOCAL unsigned *>(lds + L_CTL);   // [1] selections done, [2] routing ready (1 ok, 2 failed), [3] a wait failed
     Lane ln;
     ln.r = lane >> 2; ln.q = lane & 3;
     ln.tr = lds_addr(dyn_lds) | ((uint32_t) (lane & 15) << 3);   // table base (64 KB aligned: the tables open the LDS) | replica
     ln.lq = (uint32_t) ln.q * 4096 + 16 * ln.r; ln.ld = (uint32_t) ln.q * 128 + 2 * ln.r;
 
-    // 1. tables and tokens
+    // 1. router logits (the whole workgroup), then tables and tokens
     TRACE(wave, 0);
     if (threadIdx.x < 4) { ctl[threadIdx.x] = 0; }
+    for (int e = blockIdx.x; e < a.n_exp; e += G) { router_phase(a, lds, wave, e); }
+    TRACE(wave, 2);
     tables_copy<DNT>(dyn_lds, a.tab);
     quant_tokens(a, lds, wave);
     __syncthreads();
     TRACE(wave, 1);
     if (lds_addr(dyn_lds) & 0xFFFFu) { report(a.err, 4); return; }   // table addressing needs a 64 KB aligned base
 
-    // 2. router logits (wave t = token t); the workgroup's last router wave arrives on the device counter, and the last
-    //    workgroup raises the logits flag. Waves without a token run the shared expert's gate/up meanwhile.
+    // 2. selection (wave t = token t, every workgroup redundantly); the last selecting wave builds the dispatch and opens
+    //    the task phase. Waves without a token run the shared expert's gate/up meanwhile.
     const bool pre = n < DW;
     if (wave < n) {
-        for (int e = blockIdx.x; e < a.n_exp; e += G) { router_logit(a, wave, e); }
-        stores_done();
-        if (lds_arrive(ctl + 0, (unsigned) n) && arrive_last(a.cnt + CNT_LOGIT, (unsigned) G)) {
-            if (lane == 0) { st_agent_u32(a.flags + FLAG_LOGIT, a.epoch); }
-        }
-        TRACE(wave, 2);
-        // 3. selection (wave t = token t); the last selecting wave builds the dispatch and opens the task phase
-        const bool ok = wait_flag(a.flags + FLAG_LOGIT, a.epoch);
+        float bv[4], lg[4];
+        load_bias(a.bias, a.n_exp, bv);
+        const bool ok = wait_logits(a, wave, lg);
         TRACE(wave, 3);
         if (!ok) { report(a.err, 2); }
-        float lg[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) { const int e = 4 * lane + j; lg[j] = ok && e < a.n_exp ? ld_agent(a.logits + (size_t) wave * a.n_exp + e) : 0.f; }
         const RT rt(lds);
         float * scr = (float *) (lds + L_DST) + wave * (NEXP_MAX + 2 * 64);
         if (ok) {
-            select_token(lg, a.bias, a.n_exp, a.n_group, a.topk_group, a.topk, a.scale, scr, (int *) (rt.sel + wave * a.topk),
+            select_token(lg, bv, a.n_exp, a.n_group, a.topk_group, a.topk, a.scale, scr, (int *) (rt.sel + wave * a.topk),
                          (float *) (rt.wts + wave * a.topk), blockIdx.x == 0 && a.probs ? a.probs + (size_t) wave * a.n_exp : nullptr);
         } else if (lane == 0) {
             __hip_atomic_fetch_or(ctl + 3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -396,10 +435,14 @@ hipError_t decode_init(int ncu, int * grid) {
     return hipSuccess;
 }
 
-hipError_t launch_moe_decode(const DecodeArgs & a, int grid, hipStream_t st) {
+hipError_t launch_moe_decode(const DecodeArgs & a, int grid, bool cooperative, hipStream_t st) {
     if (a.n < 1 || a.n > DMAX_N || a.topk < 1 || a.topk > MAXK || a.n_exp < 1 || a.n_exp > NEXP_MAX || a.n_group < 1 || a.n_group > 64 ||
         a.n_exp % a.n_group || a.E != DE || a.H != DH || grid < 1) {
         return hipErrorInvalidValue;
+    }
+    if (!cooperative) {   // one workgroup per CU fits the occupancy; co-residency is assumed, waits stay bounded
+        k_moe_decode<<<grid, DNT, DEC_LDS, st>>>(a);
+        return hipGetLastError();
     }
     DecodeArgs arg = a;
     void * params[] = { &arg };

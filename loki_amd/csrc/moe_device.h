@@ -63,30 +63,100 @@ __device__ __forceinline__ void tables_copy(uint8_t * lds, const uint4 * img) {
 }
 
 // ---------------------------------------------------------------- wave reductions without LDS
-// Pure-VALU maximum over the wave: DPP inside 16-lane rows (quad_perm xor 1, xor 2, row_half_mirror, row_mirror), then
-// row_bcast:15 / row_bcast:31 carry row results upwards so lane 63 ends with the maximum, read back once. __shfl would
+// Pure-VALU reductions: DPP inside 16-lane rows (quad_perm xor 1, xor 2, row_half_mirror, row_mirror), then
+// row_bcast:15 / row_bcast:31 carry row results upwards so lane 63 ends with the result, read back once. __shfl would
 // go through ds_bpermute (the LDS queue the table lookups keep busy), and comparing in scalar registers would bounce
-// every step between the vector and scalar units.
+// every step between the vector and scalar units. Keys are 32-bit (a dependent 64-bit compare-select costs ~2x).
 enum { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140, DPP_BCAST15 = 0x142, DPP_BCAST31 = 0x143 };
 template <int CTRL> __device__ __forceinline__ uint32_t dpp(uint32_t v) { return (uint32_t) __builtin_amdgcn_mov_dpp((int) v, CTRL, 0xF, 0xF, true); }
 template <int CTRL> __device__ __forceinline__ float dppf(float v) { return __builtin_bit_cast(float, dpp<CTRL>(__builtin_bit_cast(uint32_t, v))); }
 __device__ __forceinline__ uint32_t rdlane(uint32_t v, int l) { return (uint32_t) __builtin_amdgcn_readlane((int) v, l); }
 
-template <int CTRL, int ROWS> __device__ __forceinline__ uint64_t max64_step(uint64_t k) {
-    const uint32_t h = (uint32_t) (k >> 32), l = (uint32_t) k;
-    // lanes outside ROWS keep their own value (old operand = own value)
-    const uint32_t oh = (uint32_t) __builtin_amdgcn_update_dpp((int) h, (int) h, CTRL, ROWS, 0xF, false);
-    const uint32_t ol = (uint32_t) __builtin_amdgcn_update_dpp((int) l, (int) l, CTRL, ROWS, 0xF, false);
-    const uint64_t o = ((uint64_t) oh << 32) | ol;
-    return o > k ? o : k;
+// ---------------------------------------------------------------- router logit contract (shared with the CPU checker)
+// K % 1024 == 0: 256 chunks of K/256 consecutive products, each summed in order in fp64 from exact fp32 x fp32 products,
+// then a fixed pairwise tree over the chunk sums (entry i of the next level = entries 2i + 2i+1), rounded once to fp32.
+// Lane c owns chunks 4c..4c+3 (four independent chains); tree levels 1-2 are lane-local, levels 3-6 pair exactly the
+// sibling blocks with DPP inside 16-lane rows (xor 1, xor 2, half mirror, mirror), levels 7-8 combine the four rows.
+// fp64 addition is commutative, so which lane of a pair adds which does not change the value.
+template <int CTRL> __device__ __forceinline__ double dppd(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = dpp<CTRL>((uint32_t) b), hi = dpp<CTRL>((uint32_t) (b >> 32));
+    return __builtin_bit_cast(double, ((uint64_t) hi << 32) | lo);
 }
-// wave-wide maximum of 64-bit keys, returned to every lane (uniform)
-__device__ __forceinline__ uint64_t wave_max64(uint64_t k) {
-    k = max64_step<DPP_XOR1, 0xF>(k); k = max64_step<DPP_XOR2, 0xF>(k);
-    k = max64_step<DPP_HALF_MIRROR, 0xF>(k); k = max64_step<DPP_MIRROR, 0xF>(k);
-    k = max64_step<DPP_BCAST15, 0xA>(k); k = max64_step<DPP_BCAST31, 0xC>(k);
-    return ((uint64_t) rdlane((uint32_t) (k >> 32), 63) << 32) | rdlane((uint32_t) k, 63);
+__device__ __forceinline__ double rdlaned(double v, int l) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    return __builtin_bit_cast(double, ((uint64_t) rdlane((uint32_t) (b >> 32), l) << 32) | rdlane((uint32_t) b, l));
 }
+// tree levels over 64 consecutive chunk sums held one per lane (lane = chunk order): the block's total (uniform)
+__device__ __forceinline__ double tree64(double t) {
+#pragma clang fp contract(off)
+    t = t + dppd<DPP_XOR1>(t);
+    t = t + dppd<DPP_XOR2>(t);
+    t = t + dppd<DPP_HALF_MIRROR>(t);
+    t = t + dppd<DPP_MIRROR>(t);
+    return (rdlaned(t, 0) + rdlaned(t, 16)) + (rdlaned(t, 32) + rdlaned(t, 48));
+}
+// the lane's four chunk sums -> the wave's total (uniform)
+__device__ __forceinline__ double logit_tree(const double (&s)[4]) {
+#pragma clang fp contract(off)
+    double t = (s[0] + s[1]) + (s[2] + s[3]);
+    t = t + dppd<DPP_XOR1>(t);
+    t = t + dppd<DPP_XOR2>(t);
+    t = t + dppd<DPP_HALF_MIRROR>(t);
+    t = t + dppd<DPP_MIRROR>(t);
+    return (rdlaned(t, 0) + rdlaned(t, 16)) + (rdlaned(t, 32) + rdlaned(t, 48));
+}
+// chunk sums of the lane's 4 chunks of w . x (w, x: the row starts); L4 = K / 1024 float4 per chunk
+template <int L4>
+__device__ __forceinline__ void logit_chunks(const float * w, const float * x, double (&s)[4]) {
+#pragma clang fp contract(off)
+    const int lane = lane_id();
+    const float * wl = w + (size_t) lane * 16 * L4, * xl = x + (size_t) lane * 16 * L4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { s[j] = 0.0; }
+#pragma unroll
+    for (int i = 0; i < L4; ++i) {
+        float4 wv[4], xv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { wv[j] = gloadf4(wl + j * 4 * L4 + 4 * i); xv[j] = gloadf4(xl + j * 4 * L4 + 4 * i); }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            s[j] += (double) xv[j].x * (double) wv[j].x; s[j] += (double) xv[j].y * (double) wv[j].y;
+            s[j] += (double) xv[j].z * (double) wv[j].z; s[j] += (double) xv[j].w * (double) wv[j].w;
+        }
+    }
+}
+// the same for any K % 1024 == 0 (runtime chunk length)
+__device__ __forceinline__ void logit_chunks_any(const float * w, const float * x, int K, double (&s)[4]) {
+#pragma clang fp contract(off)
+    const int lane = lane_id(), L = K / 256;
+    const float * wl = w + (size_t) lane * 4 * L, * xl = x + (size_t) lane * 4 * L;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { s[j] = 0.0; }
+    for (int i = 0; i < L; i += 4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 wv = gloadf4(wl + j * L + i), xv = gloadf4(xl + j * L + i);
+            s[j] += (double) xv.x * (double) wv.x; s[j] += (double) xv.y * (double) wv.y;
+            s[j] += (double) xv.z * (double) wv.z; s[j] += (double) xv.w * (double) wv.w;
+        }
+    }
+}
+
+// wave-wide maximum of unsigned 32-bit values, returned to every lane (uniform)
+__device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b) { return a > b ? a : b; }
+template <int CTRL, int ROWS> __device__ __forceinline__ uint32_t max32_step(uint32_t v) {
+    return umax32(v, (uint32_t) __builtin_amdgcn_update_dpp((int) v, (int) v, CTRL, ROWS, 0xF, false));
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max32_step<DPP_XOR1, 0xF>(v); v = max32_step<DPP_XOR2, 0xF>(v);
+    v = max32_step<DPP_HALF_MIRROR, 0xF>(v); v = max32_step<DPP_MIRROR, 0xF>(v);
+    v = max32_step<DPP_BCAST15, 0xA>(v); v = max32_step<DPP_BCAST31, 0xC>(v);
+    return rdlane(v, 63);
+}
+// lowest lane whose flag is set (uniform; 64 if none)
+__device__ __forceinline__ int first_lane(bool f) { const uint64_t b = __ballot(f); return b ? __builtin_ctzll(b) : 64; }
+
 // fp32 bits -> unsigned key with the same order (no -0 / NaN among the values compared here)
 __device__ __forceinline__ uint32_t ord_key(float f) { const uint32_t b = __builtin_bit_cast(uint32_t, f); return (b & 0x80000000u) ? ~b : (b | 0x80000000u); }
 
@@ -96,14 +166,15 @@ __device__ __forceinline__ uint32_t ord_key(float f) { const uint32_t b = __buil
 __device__ __forceinline__ uint32_t q8k_lane(const float (&xs)[4], float & d) {
 #pragma clang fp contract(off)
     const int lane = lane_id();
-    float ba = -1.f, bv = 0.f; int bi = 0;
+    float ba = -1.f, bv = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) { const float ax = fabsf(xs[i]); if (ax > ba) { ba = ax; bv = xs[i]; bi = 4 * lane + i; } }
-    // the largest |x|, ties to the lower index: key (|x| bits, 255 - index)
-    const uint64_t key = wave_max64(((uint64_t) __builtin_bit_cast(uint32_t, ba) << 32) | (255u - (uint32_t) bi));
-    const int wi = 255 - (int) (uint32_t) key;
-    ba = __builtin_bit_cast(float, (uint32_t) (key >> 32));
-    bv = __builtin_bit_cast(float, rdlane(__builtin_bit_cast(uint32_t, bv), wi >> 2));   // the owner lane's best is the winner
+    for (int i = 0; i < 4; ++i) { const float ax = fabsf(xs[i]); if (ax > ba) { ba = ax; bv = xs[i]; } }
+    // the largest |x| (non-negative floats order as their bits); ties to the lower index = the lowest lane holding the
+    // maximum, whose own best is its lowest such index
+    const uint32_t mk = wave_max_u32(__builtin_bit_cast(uint32_t, ba));
+    const int wl = first_lane(__builtin_bit_cast(uint32_t, ba) == mk);
+    ba = __builtin_bit_cast(float, mk);
+    bv = __builtin_bit_cast(float, rdlane(__builtin_bit_cast(uint32_t, bv), wl));
     uint32_t packed = 0; d = 0.f;
     if (ba > 0.f) {
         const float iscale = -127.f / bv;
@@ -170,12 +241,13 @@ __device__ __forceinline__ void lds_visible() {   // this wave's LDS writes are 
 // ---------------------------------------------------------------- one block: integer sums of T tokens
 template <int L, int T>
 __device__ __forceinline__ void group_step(const uint4 (&w)[4], uint32_t tr, const uint8_t * const (&xb)[T], int (&acc)[T][8]) {
-    uint2 g[8], m[8];   // all 16 table reads of the step are issued before the first is used
+    const uint32_t trs = (tr & ~255u) | 128u | ((tr & 0x38u) << 1);   // the sign copy of this lane: (lane % 8) * 16
+    uint2 g[8]; uint4 m[8];   // all 16 table reads of the step are issued before the first is used
 #pragma unroll
     for (int ib = 0; ib < 8; ++ib) {
         const uint4 c = w[ib >> 1];
         g[ib] = tab_grid<L>((ib & 1) ? c.z : c.x, tr);
-        m[ib] = tab_sign<L>((ib & 1) ? c.w : c.y, tr);
+        m[ib] = tab_sign<L>((ib & 1) ? c.w : c.y, trs);
     }
     int4 xv[T][4];
 #pragma unroll
@@ -300,7 +372,13 @@ template <int CTRL> __device__ __forceinline__ void top2_step(float & v1, float 
     const float n2 = v1 >= o1 ? fmaxf(v2, o1) : fmaxf(v1, o2);
     v1 = fmaxf(v1, o1); v2 = n2;
 }
-__device__ __forceinline__ void select_token(const float (&lg)[4], const float * bias, int n_exp, int n_group, int topk_group, int topk,
+// the lane's 4 bias values (experts 4 lane + j), loaded ahead of the logits
+__device__ __forceinline__ void load_bias(const float * bias, int n_exp, float (&b)[4]) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { b[j] = 4 * lane + j < n_exp ? gptr(bias)[4 * lane + j] : 0.f; }
+}
+__device__ __forceinline__ void select_token(const float (&lg)[4], const float (&bias)[4], int n_exp, int n_group, int topk_group, int topk,
                                              float scale, float * scr, int * sel_out, float * w_out, float * probs_out) {
 #pragma clang fp contract(off)
     const int lane = lane_id(), per = n_exp / n_group;
@@ -310,7 +388,7 @@ __device__ __forceinline__ void select_token(const float (&lg)[4], const float *
         const int e = 4 * lane + j;
         p[j] = 0.f; c[j] = 0.f;
         if (e < n_exp) {
-            p[j] = det_sigmoid(lg[j]); c[j] = p[j] + gptr(bias)[e];
+            p[j] = det_sigmoid(lg[j]); c[j] = p[j] + bias[j];
             if (probs_out) { gptr(probs_out)[e] = p[j]; }
         }
     }
@@ -360,20 +438,30 @@ __device__ __forceinline__ void select_token(const float (&lg)[4], const float *
 #pragma unroll
         for (int j = 0; j < 4; ++j) { const int e = 4 * lane + j; ok[j] = e < n_exp && allow[e / per]; }
     }
-    // topk rounds of argmax: key (ordered c, 255 - index), then the winner's p from its owner lane
+    // topk rounds of argmax over the eligible, untaken experts: the largest ordered key of c; ties to the lower index =
+    // the lowest lane holding the maximum, whose own best is its lowest such expert
+    uint32_t kk[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { kk[j] = ok[j] ? ord_key(c[j]) : 0u; }
     float sum = 0.f; float pr[MAXK]; int ir[MAXK];
     for (int r = 0; r < topk; ++r) {
-        uint64_t kb = 0; float bp = 0.f;
+        uint32_t lb = 0; int lj = 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint64_t kj = ok[j] ? ((uint64_t) ord_key(c[j]) << 32) | (255u - (uint32_t) (4 * lane + j)) : 0;
-            if (kj > kb) { kb = kj; bp = p[j]; }
+        for (int j = 0; j < 4; ++j) { if (kk[j] > lb) { lb = kk[j]; lj = j; } }
+        const uint32_t m = wave_max_u32(lb);
+        int bi = -1; float bp = 0.f;
+        if (m) {
+            const int wl = first_lane(lb == m);
+            float lp = p[0];
+#pragma unroll
+            for (int j = 1; j < 4; ++j) { if (lj == j) { lp = p[j]; } }
+            bi = 4 * wl + (int) rdlane((uint32_t) lj, wl);
+            bp = __builtin_bit_cast(float, rdlane(__builtin_bit_cast(uint32_t, lp), wl));
+            if (lane == wl) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) { if (lj == j) { kk[j] = 0u; } }
+            }
         }
-        const float lbp = bp;
-        kb = wave_max64(kb);
-        const int bi = kb ? 255 - (int) (uint32_t) kb : -1;
-        bp = bi >= 0 ? __builtin_bit_cast(float, rdlane(__builtin_bit_cast(uint32_t, lbp), bi >> 2)) : 0.f;
-        if (bi >= 0 && (bi >> 2) == lane) { ok[bi & 3] = false; }
         sum = sum + bp;
 #pragma unroll
         for (int k = 0; k < MAXK; ++k) { if (k == r) { pr[k] = bp; ir[k] = bi; } }

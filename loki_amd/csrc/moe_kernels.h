@@ -47,9 +47,9 @@ hipError_t launch_experts_down(const ExpertArgs & a, int grid, hipStream_t st);
 
 // ---------------------------------------------------------------- single-launch decode block (moe_decode.hip)
 // counters (self-resetting, zero before the first launch) and epoch flags inside DecodeArgs::cnt / ::flags
-constexpr int CNT_LOGIT = 0, CNT_PAIR = 1, CNT_HB = CNT_PAIR + 257 * 128, CNT_HQ = CNT_HB + 257 * 8, CNT_COMB = CNT_HQ + 257,
+constexpr int CNT_PAIR = 1, CNT_HB = CNT_PAIR + 257 * 128, CNT_HQ = CNT_HB + 257 * 8, CNT_COMB = CNT_HQ + 257,
               DEC_CNT = CNT_COMB + 256;
-constexpr int FLAG_LOGIT = 0, FLAG_H = 1, DEC_FLAGS = FLAG_H + 257;
+constexpr int FLAG_H = 1, DEC_FLAGS = FLAG_H + 257;
 struct DecodeArgs {
     const uint4 * tab;
     const float * x; int n;                          // tokens [n][E], n <= 8
@@ -59,14 +59,16 @@ struct DecodeArgs {
     int E, H;                                        // 7168, 2048 (the kernel's geometry)
     int8_t * xq; float * xd;                         // Q8_K of x (written by workgroup 0)
     float * logits, * probs; int * sel; float * wts; int * counts, * offsets, * perm, * inv, * act, * nact;
+    uint64_t * tlogits;                              // [n][n_exp] logits tagged with the launch's epoch (bits 32..63)
     float * g, * u, * h; int8_t * hq; float * hd; float * o;   // [P+n][H] / [P+n][E] per dispatch slot
     float * y;                                       // [n][E]
     unsigned * cnt, * flags; unsigned epoch; int * err;
 };
 hipError_t decode_init(int ncu, int * grid);
 size_t decode_lds_bytes();
-// cooperative launch of grid workgroups (at most one per CU can be resident)
-hipError_t launch_moe_decode(const DecodeArgs & a, int grid, hipStream_t st);
+// grid workgroups (at most one per CU can be resident): a cooperative launch guarantees they are all resident; a
+// regular launch assumes it (nothing else running on the CUs) -- a violation ends in a reported wait timeout
+hipError_t launch_moe_decode(const DecodeArgs & a, int grid, bool cooperative, hipStream_t st);
 
 // y[t] = sum_k (o[inv[t*topk+k]] * w[t][k]) in k order + o[P+t] (+ resid[t] when given)
 hipError_t launch_combine(const float * o, const int * inv, const float * wts, int n, int topk, int E, int P,

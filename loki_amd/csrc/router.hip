@@ -6,10 +6,10 @@
 // 32 experts; a group's score is the sum of its two best biased scores; the top-4 groups stay eligible), which reduces
 // to the reference's rule with n_group = topk_group = 1.
 //
-// Logit contract (shared bit for bit with the CPU checker): K is cut into 64 chunks of K/64; each chunk is summed in
-// order in fp64 from exact fp32 x fp32 products, the 64 chunk sums are added in order in fp64, and the total is rounded
-// once to fp32. The sigmoid uses the fp64 exp contract of moe_common.h. Selection and weights are plain fp32 compares,
-// adds and one correctly rounded division, so sel and wts are bit-identical to the checker's.
+// Logit contract (shared bit for bit with the CPU checker, moe_device.h): 256 chunks of K/256 products, each summed in
+// order in fp64 from exact fp32 x fp32 products, a fixed pairwise tree over the chunk sums, one rounding to fp32. The
+// sigmoid uses the fp64 exp contract of moe_common.h. Selection and weights are plain fp32 compares, adds and one
+// correctly rounded division, so sel and wts are bit-identical to the checker's.
 #include "moe_device.h"
 #include "moe_kernels.h"
 
@@ -17,40 +17,23 @@ namespace lk {
 
 constexpr int RT = 8;   // tokens per router wave
 
-// one wave per (expert, 8-token tile): lane c owns chunk c for all 8 tokens, so W is read once per tile
+// one wave per (expert, 8-token tile); every token's logit is a full wave reduction (logit_tree)
 __global__ void __launch_bounds__(64) k_router_logits(const float * __restrict__ W, const float * __restrict__ x, int n, int n_exp, int K,
                                                       float * __restrict__ logits) {
-    __shared__ double S[RT][64];
-    const int e = blockIdx.x, t0 = blockIdx.y * RT, lane = threadIdx.x, L = K / 64;
+    const int e = blockIdx.x, t0 = blockIdx.y * RT;
     const int nt = min(RT, n - t0);
-    const float4 * w4 = reinterpret_cast<const float4 *>(W + (size_t) e * K + (size_t) lane * L);
-    double s[RT];
-#pragma unroll
-    for (int t = 0; t < RT; ++t) { s[t] = 0.0; }
-    for (int i = 0; i < L / 4; ++i) {
-        const float4 wv = w4[i];
-        const double w0 = wv.x, w1 = wv.y, w2 = wv.z, w3 = wv.w;
-#pragma unroll
-        for (int t = 0; t < RT; ++t) {
-            if (t < nt) {
-                const float4 xv = reinterpret_cast<const float4 *>(x + (size_t) (t0 + t) * K + (size_t) lane * L)[i];
-                s[t] += (double) xv.x * w0; s[t] += (double) xv.y * w1; s[t] += (double) xv.z * w2; s[t] += (double) xv.w * w3;
-            }
-        }
-    }
-#pragma unroll
-    for (int t = 0; t < RT; ++t) { S[t][lane] = s[t]; }
-    __syncthreads();
-    if (lane < nt) {
-        double tot = S[lane][0];
-        for (int c = 1; c < 64; ++c) { tot += S[lane][c]; }
-        logits[(size_t) (t0 + lane) * n_exp + e] = (float) tot;
+    for (int t = 0; t < nt; ++t) {
+        double s[4];
+        if (K == 7168) { logit_chunks<7>(W + (size_t) e * K, x + (size_t) (t0 + t) * K, s); }
+        else { logit_chunks_any(W + (size_t) e * K, x + (size_t) (t0 + t) * K, K, s); }
+        const double tot = logit_tree(s);
+        if (threadIdx.x == 0) { logits[(size_t) (t0 + t) * n_exp + e] = (float) tot; }
     }
 }
 
 hipError_t launch_router_logits(const float * W, const float * x, int n, int n_exp, int K, float * logits, hipStream_t st) {
     if (n <= 0) { return hipSuccess; }
-    if (K % 256 != 0) { return hipErrorInvalidValue; }
+    if (K % 1024 != 0) { return hipErrorInvalidValue; }
     k_router_logits<<<dim3(n_exp, (n + RT - 1) / RT), 64, 0, st>>>(W, x, n, n_exp, K, logits);
     return hipGetLastError();
 }
@@ -62,10 +45,11 @@ __global__ void __launch_bounds__(64) k_router_select(const float * __restrict__
     __shared__ float scr[NEXP_MAX + 2 * 64];
     __shared__ int so[MAXK]; __shared__ float wo[MAXK];
     const int t = blockIdx.x, lane = threadIdx.x;
-    float lg[4];
+    float lg[4], bv[4];
+    load_bias(bias, n_exp, bv);
 #pragma unroll
     for (int j = 0; j < 4; ++j) { const int e = 4 * lane + j; lg[j] = e < n_exp ? logits[(size_t) t * n_exp + e] : 0.f; }
-    select_token(lg, bias, n_exp, n_group, topk_group, topk, scale, scr, so, wo, probs ? probs + (size_t) t * n_exp : nullptr);
+    select_token(lg, bv, n_exp, n_group, topk_group, topk, scale, scr, so, wo, probs ? probs + (size_t) t * n_exp : nullptr);
     lds_visible();
     if (lane < topk) { sel[(size_t) t * topk + lane] = so[lane]; wts[(size_t) t * topk + lane] = wo[lane]; }
 }

@@ -178,13 +178,16 @@ void or_matvec_iq2_xxs(const uint8_t * w, int64_t rows, int64_t k, const int8_t 
 
 /* ---------------------------------------------------------------- router */
 float or_router_logit(const float * w, const float * x, int64_t k) {
-    const int64_t L = k / 64; double tot = 0.0;
-    for (int c = 0; c < 64; ++c) {
+    const int64_t L = k / 256; double t[256];
+    for (int c = 0; c < 256; ++c) {   /* chunk c: K/256 consecutive products summed in order */
         double s = 0.0;
         for (int64_t i = c * L; i < (c + 1) * L; ++i) { s += (double) x[i] * (double) w[i]; }   /* product exact in fp64 */
-        tot = c == 0 ? s : tot + s;
+        t[c] = s;
     }
-    return (float) tot;
+    for (int m = 256; m > 1; m /= 2) {   /* pairwise tree: entry i of the next level = entries 2i + 2i+1 */
+        for (int i = 0; i < m / 2; ++i) { t[i] = t[2 * i] + t[2 * i + 1]; }
+    }
+    return (float) t[0];
 }
 
 /* top-m of v[0..n) over allowed entries: descending value, ties to the lower index (the reference's argmax

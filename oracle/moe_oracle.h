@@ -28,8 +28,9 @@ float or_vec_dot_iq2_xxs_q8_K(int64_t k, const uint8_t * wblocks, const int8_t *
 /* y[r] = vec_dot(row r of an IQ2_XXS matrix [rows][k/256], q8K(x)) for every row (OpenMP over rows) */
 void or_matvec_iq2_xxs(const uint8_t * w, int64_t rows, int64_t k, const int8_t * q, const float * d, float * y);
 
-/* router logits contract: 64 chunks of K/64, each summed sequentially in fp64 from exact fp32 products,
- * chunks summed sequentially in fp64, rounded once to fp32 */
+/* router logits contract (K % 1024 == 0): 256 chunks of K/256 consecutive products, each summed in order in fp64 from
+ * exact fp32 x fp32 products; the 256 chunk sums combined by a fixed pairwise tree (level by level, entry i of the next
+ * level = entries 2i + 2i+1); rounded once to fp32 */
 float or_router_logit(const float * w, const float * x, int64_t k);
 /* grouped sigmoid router for n rows: probs [n][n_exp] (optional), sel [n][topk] (descending biased score),
  * wts [n][topk] = p[sel] / max(sum p[sel], 2^-14) * scale. Ties go to the lower index (groups and experts). */
