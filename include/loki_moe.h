@@ -118,11 +118,12 @@ typedef struct FLDebug {
     const int8_t * xq; const float * xd;             /* Q8_K of x */
     const float * logits, * probs; const int * sel; const float * wts;
     const int * counts, * offsets, * perm, * inv, * act, * nact;
-    const float * h; const int8_t * hq; const float * hd; /* [P+n][H]: per slot, shared rows at P.. */
-    const float * o;                                   /* [P+n][E] */
-    const float * g, * u;                              /* gate / up outputs when debug capture is on */
+    const float * h; const int8_t * hq; const float * hd; /* [P+n][H]: per slot, shared rows at P.. (per-pass path) */
+    const float * o;                                   /* [P+n][E] (per-pass path) */
+    const float * g, * u;                              /* gate / up outputs when debug capture is on (per-pass path) */
     int n, P, topk;
-    int fused;                                         /* 1: the last fl_moe_layer call ran as one cooperative launch */
+    int fused;                                         /* 1: the last call ran as the single-launch decode block, which
+                                                        * keeps h and o internal (h .. u are NULL then) */
 } FLDebug;
 int fl_debug(FLCtx *, FLDebug * out);
 int fl_set_debug(FLCtx *, int capture_gate_up);

@@ -42,7 +42,7 @@ extern "C" void fl_free(FLCtx * c) {
     c->h.release(); c->hd.release(); c->o.release(); c->g.release(); c->u.release();
     c->sel.release(); c->counts.release(); c->offsets.release(); c->perm.release(); c->inv.release(); c->act.release(); c->nact.release();
     compat_free(c); c->zero_i.release(); c->terms.release(); c->cnt.release();
-    c->tab.release(); c->dcnt.release(); c->dflags.release(); c->derr.release(); c->dlogit.release();
+    c->tab.release(); c->derr.release(); c->dlogit.release(); c->dth.release(); c->dto.release();
     for (auto & v : c->ev_free) { for (auto e : v) { (void) hipEventDestroy(e); } }
     for (auto & v : c->ev_pending) { for (auto e : v) { (void) hipEventDestroy(e); } }
     (void) hipEventDestroy(c->em0); (void) hipEventDestroy(c->em1); (void) hipStreamDestroy(c->own);
@@ -248,21 +248,22 @@ extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, in
     ALLOC(c, c->logits, (size_t) n * ne); ALLOC(c, c->probs, (size_t) n * ne);
     ALLOC(c, c->sel, P); ALLOC(c, c->wts, P); ALLOC(c, c->perm, P); ALLOC(c, c->inv, P);
     ALLOC(c, c->counts, ne); ALLOC(c, c->offsets, ne + 1); ALLOC(c, c->act, ne); ALLOC(c, c->nact, 1);
-    ALLOC(c, c->h, rows * H); ALLOC(c, c->hq, rows * H); ALLOC(c, c->hd, rows * (H / 256)); ALLOC(c, c->o, rows * E);
-    if (c->dbg_gu || fused) { ALLOC(c, c->g, rows * H); ALLOC(c, c->u, rows * H); }
+    if (!fused) { ALLOC(c, c->h, rows * H); ALLOC(c, c->hq, rows * H); ALLOC(c, c->hd, rows * (H / 256)); ALLOC(c, c->o, rows * E); }
+    if (c->dbg_gu) { ALLOC(c, c->g, rows * H); ALLOC(c, c->u, rows * H); }
     if (int rc = ensure_expert_scratch(c, rows, E, H)) { return rc; }
     c->last_n = n; c->last_P = P; c->last_fused = fused ? 1 : 0;
     hipStream_t st = c->st;
     std::vector<hipEvent_t> * ev = prof_begin(c);
     if (fused) {
-        if (!c->dcnt.p) {
-            ALLOC(c, c->dcnt, DEC_CNT); ALLOC(c, c->dflags, DEC_FLAGS); ALLOC(c, c->derr, 1); ALLOC(c, c->dlogit, 8 * NEXP_MAX);
-            TRY(c, hipMemsetAsync(c->dcnt.p, 0, DEC_CNT * sizeof(unsigned), st));
+        if (!c->derr.p) {
+            ALLOC(c, c->derr, 1); ALLOC(c, c->dlogit, DEC_TLOGITS); ALLOC(c, c->dth, DEC_TH); ALLOC(c, c->dto, DEC_TO);
             TRY(c, hipMemsetAsync(c->derr.p, 0, sizeof(int), st));
         }
-        if (++c->epoch == 1) {   // first use, or the epoch wrapped: no stale word may carry the new epoch
-            TRY(c, hipMemsetAsync(c->dflags.p, 0, DEC_FLAGS * sizeof(unsigned), st));
-            TRY(c, hipMemsetAsync(c->dlogit.p, 0, 8 * NEXP_MAX * sizeof(uint64_t), st));
+        if (++c->epoch == 0) { c->epoch = 1; }   // epoch 0 is the cleared state of the tagged words
+        if (c->epoch == 1) {   // first use, or the epoch wrapped: no stale word may carry the new epoch
+            TRY(c, hipMemsetAsync(c->dlogit.p, 0, DEC_TLOGITS * sizeof(uint64_t), st));
+            TRY(c, hipMemsetAsync(c->dth.p, 0, DEC_TH * sizeof(uint64_t), st));
+            TRY(c, hipMemsetAsync(c->dto.p, 0, DEC_TO * sizeof(uint64_t), st));
         }
         DecodeArgs d{};
         d.tab = c->tab.p; d.x = x; d.n = n;
@@ -273,8 +274,8 @@ extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, in
         d.E = E; d.H = H;
         d.xq = c->xq.p; d.xd = c->xd.p; d.logits = c->logits.p; d.probs = c->probs.p; d.sel = c->sel.p; d.wts = c->wts.p;
         d.counts = c->counts.p; d.offsets = c->offsets.p; d.perm = c->perm.p; d.inv = c->inv.p; d.act = c->act.p; d.nact = c->nact.p;
-        d.g = c->g.p; d.u = c->u.p; d.h = c->h.p; d.hq = c->hq.p; d.hd = c->hd.p; d.o = c->o.p; d.y = y;
-        d.cnt = c->dcnt.p; d.flags = c->dflags.p; d.epoch = c->epoch; d.err = c->derr.p; d.tlogits = c->dlogit.p;
+        d.tlogits = c->dlogit.p; d.th = c->dth.p; d.to = c->dto.p; d.y = y;
+        d.epoch = c->epoch; d.err = c->derr.p;
         // stages: the whole block is one launch, reported as stage 4; the others are empty
         for (int i = 0; i <= 4; ++i) { prof_mark(c, ev, i); }
         TRY(c, launch_moe_decode(d, c->dec_grid, c->fused == 1, st));
@@ -333,7 +334,9 @@ extern "C" int fl_debug(FLCtx * c, FLDebug * out) {
     std::memset(out, 0, sizeof(FLDebug));
     out->xq = c->xq.p; out->xd = c->xd.p; out->logits = c->logits.p; out->probs = c->probs.p; out->sel = c->sel.p; out->wts = c->wts.p;
     out->counts = c->counts.p; out->offsets = c->offsets.p; out->perm = c->perm.p; out->inv = c->inv.p; out->act = c->act.p; out->nact = c->nact.p;
-    out->h = c->h.p; out->hq = c->hq.p; out->hd = c->hd.p; out->o = c->o.p; out->g = c->dbg_gu ? c->g.p : nullptr; out->u = c->dbg_gu ? c->u.p : nullptr;
+    if (!c->last_fused) {   // the single-launch block keeps h and o in its epoch-tagged buffers only
+        out->h = c->h.p; out->hq = c->hq.p; out->hd = c->hd.p; out->o = c->o.p; out->g = c->dbg_gu ? c->g.p : nullptr; out->u = c->dbg_gu ? c->u.p : nullptr;
+    }
     out->n = c->last_n; out->P = c->last_P; out->topk = c->topk; out->fused = c->last_fused;
     return FL_OK;
 }

@@ -78,6 +78,7 @@ __device__ __forceinline__ uint32_t xad(uint32_t a, uint32_t b, uint32_t c) { re
 // lgkmcnt and so make every LDS wait a wait for the outstanding global loads as well
 #define LK_GLOBAL __attribute__((address_space(1)))
 #define LK_LOCAL __attribute__((address_space(3)))
+#define LK_CONST __attribute__((address_space(4)))   // kernel arguments: scalar loads, counted apart from vector memory
 template <class T> __device__ __forceinline__ const LK_GLOBAL T * gptr(const T * p) { return (const LK_GLOBAL T *) p; }
 template <class T> __device__ __forceinline__ LK_GLOBAL T * gptr(T * p) { return (LK_GLOBAL T *) p; }
 __device__ __forceinline__ uint32_t lds_addr(const void * p) { return (uint32_t) (size_t) (const LK_LOCAL uint8_t *) p; }

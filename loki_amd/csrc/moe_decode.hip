@@ -1,23 +1,27 @@
-// moe_decode.hip -- the whole MoE block for a decode batch (n <= 8 tokens) in one cooperative launch.
+// moe_decode.hip -- the whole MoE block for a decode batch (n <= 8 tokens) in one launch.
 //
 // Reference path (src/fused_layer.cu): router_probs + router_topk (:313-332, launched :506), a host round-trip for the
 // routing (fl_fetch :587-598, eng:793-818), then per fl_moe (:599-612) quant_x, tc_matvec gate/up, swiglu_q8,
 // tc_matvec down and moe_combine as separate launches. At batch 1-8 every one of those launches is latency-bound, so
-// here one workgroup per CU (all resident: cooperative launch) runs the block end to end:
-//   1. workgroup b computes the router logits of expert b for every token (the fp64 chunk-and-tree contract) and
-//      publishes each as an epoch-tagged 64-bit word; then it copies the codebook/sign table image into LDS and
-//      quantises the n token rows to Q8_K (staged layout of moe_device.h);
-//   2. every workgroup polls the tagged logits, selects each token's experts (select_token, one wave per token) and
-//      builds the dispatch (stable counting sort of the n * topk pairs) in its own LDS -- redundant, but cheaper than
-//      another device-wide hand-off. Waves without a token meanwhile run the shared expert's gate/up tasks, which need
-//      no routing;
-//   3. tasks round-robin over all waves of the grid: gate/up tasks (expert slot, 16 rows, matrix) -- the second task of
-//      a (gate, up) pair forms h = silu(g) * u, the last of a 256-row block quantises it to Q8_K, the last block of an
-//      expert raises the expert's h flag -- then down tasks (expert slot, 32 rows) that prefetch their weights, wait for
-//      the expert's h flag, and write o; the last expert of a row group computes y = sum_k w_k o_k (k order) + shared.
-// Arithmetic is that of the per-pass kernels (same device functions), so y is bit-identical to theirs and to the CPU
-// checker. Flags hold the launch's epoch (no clearing between launches); counters reset themselves. Every wait is
-// bounded: a timeout sets *err and the wave skips the task, so the grid always drains.
+// here one workgroup per CU (all resident) runs the block end to end:
+//   1. on entry every workgroup starts the direct global->LDS copy of the codebook/sign table image; workgroup b then
+//      computes the router logits of expert b for every token (the fp64 chunk-and-tree contract) and publishes each
+//      probability sigmoid(logit) as an epoch-tagged 64-bit word;
+//   2. wave t of every workgroup issues its poll of token t's tagged probabilities, all waves quantise the n token rows
+//      to Q8_K into LDS, then wave t selects token t's experts and the last selecting wave builds the dispatch (stable
+//      counting sort of the n * topk pairs) in its own LDS -- redundant, but cheaper than another device-wide hand-off.
+//      Waves without a token meanwhile run the shared expert's gate/up tasks (no routing needed);
+//   3. gate/up tasks round-robin over all waves of the grid: a task computes 8 gate rows and the same 8 up rows of one
+//      expert for its tokens and publishes h = silu(g) * u as epoch-tagged words;
+//   4. down units round-robin over the workgroups: a unit is 256 output rows of one expert (32 per wave). The waves
+//      issue their weight loads first, then wave w polls the tagged h of Q8_K block w for every token of the expert and
+//      quantises it into LDS; after a barrier each wave computes its rows and publishes o as epoch-tagged words;
+//   5. combine units (256 rows each): y = sum_k w_k o_k (k order) + shared, from the tagged o words.
+// No counter, flag or store-completion wait sits between producer and consumer: a consumer polls the data words
+// themselves, and a word is valid once it carries this launch's epoch (stale words hold older epochs; the host clears
+// the tagged buffers whenever the epoch restarts at 1). Arithmetic is that of the per-pass kernels (same device
+// functions), so y is bit-identical to theirs and to the CPU checker. Every wait is bounded: a timeout sets *err and the
+// wave skips the work, so the grid always drains.
 #include "moe_device.h"
 #include "moe_kernels.h"
 
@@ -25,38 +29,58 @@ namespace lk {
 
 constexpr int DW = 8, DNT = DW * 64;   // waves / threads per workgroup
 constexpr int DMAX_N = 8, DMAX_P = DMAX_N * MAXK;
-constexpr int SH = NEXP_MAX;           // counter / flag index of the shared expert
+constexpr int DMAX_PS = DMAX_P + DMAX_N;   // pair-slots: the shared expert's ceil(n/2) + one per 1-2 tokens of each active expert
+constexpr int SH = NEXP_MAX;           // expert-slot marker of the shared expert
 using GG = Geo<7>;                     // gate/up rows: K = 7168
 using GD = Geo<2>;                     // down rows: K = 2048
 constexpr int DE = GG::K, DH = GD::K;
-constexpr int NGU = DH / 16;           // gate/up tasks per matrix (16 rows)
-constexpr int DRPL = 2;                // down: row sets of 16 per task
-constexpr int NDN = DE / (16 * DRPL);  // down tasks per expert
-constexpr int GU_PD = 3, GU1_PD = 6, DN_PD = 3;   // blocks in flight per lane (single-token gate/up: deeper)
+constexpr int GU_ROWS = 8;             // h rows per gate/up task (8 gate + the same 8 up rows)
+constexpr int NGU = DH / GU_ROWS;      // gate/up tasks per expert
+constexpr int DN_ROWS = DW * 32;       // output rows per down unit (32 per wave: two row sets of 16)
+constexpr int NDN = DE / DN_ROWS;      // down units per expert (= combine units)
+constexpr int GU1_PD = 4, GU2_PD = 3, DN_PD = 3;   // blocks in flight per lane
+static_assert(DH == DW * QK, "a down unit's wave w quantises h block w");
+static_assert(DMAX_N * (MAXK + 1) * DH <= (int) DEC_TH && DMAX_N * (MAXK + 1) * DE <= (int) DEC_TO, "tagged buffer sizes");
 
 // LDS layout
-constexpr int L_XS = TAB_BYTES;                                   // staged Q8_K tokens
-constexpr int L_DST = L_XS + DMAX_N * GG::XROW;                   // per-wave down staging / router sums / selection scratch
-constexpr int DST_BYTES = DW * GD::XROW;
-constexpr int L_RT = L_DST + DST_BYTES;                           // routing tables
-constexpr int RT_INTS = 4 * DMAX_P + 3 * (DMAX_P + 1) + 1;
-constexpr int L_CTL = L_RT + RT_INTS * 4;                         // workgroup hand-off words
-constexpr int DEC_LDS = L_CTL + 16;
+constexpr int L_XS = TAB_BYTES;                                   // staged Q8_K tokens (gate/up activations)
+constexpr int L_HS = L_XS + DMAX_N * GG::XROW;                    // staged Q8_K h of the current down unit
+constexpr int HS_BYTES = DMAX_N * GD::XROW;
+constexpr int L_SCR = L_HS;                                       // router sums / selection scratch (phases 1-2) overlay HS
+constexpr int L_RT = L_HS + HS_BYTES;                             // routing tables
+constexpr int RT_INTS = 4 * DMAX_P + 3 * (DMAX_P + 1) + 1 + 2 * DMAX_PS + 1;
+constexpr int L_CTL = L_RT + RT_INTS * 4;                         // workgroup hand-off words [4], per-wave flags [DW]
+constexpr int DEC_LDS = L_CTL + (4 + DW) * 4;
 static_assert(DEC_LDS <= 160 * 1024, "LDS budget");
-static_assert(DMAX_N * 64 * 8 <= DST_BYTES && DW * (NEXP_MAX + 2 * 64) * 4 <= DST_BYTES, "scratch overlays");
+static_assert(DMAX_N * 4 * 8 <= HS_BYTES && DW * (NEXP_MAX + 2 * 64) * 4 <= HS_BYTES, "scratch overlays");
 
 typedef LK_LOCAL uint8_t * lds_t;
+typedef LK_CONST DecodeArgs DArgs;   // the launch arguments, read in place with scalar loads
 
-struct RT {   // routing of the launch, in LDS
+// Routing of the launch, in LDS. A pair-slot is one or two tokens of one expert (consecutive dispatch slots): every task
+// and unit works on one pair-slot, so their costs are alike whatever the tokens per expert. ps_mi = act index or SH,
+// ps_s = first slot | token count << 16; the shared expert's pair-slots come first.
+struct RT {
     LK_LOCAL int * sel; LK_LOCAL float * wts; LK_LOCAL int * perm, * inv, * act_e, * act_s0, * act_cnt, * nact;
+    LK_LOCAL int * ps_mi, * ps_s, * nps;
     __device__ RT(lds_t lds) {
         LK_LOCAL int * b = reinterpret_cast<LK_LOCAL int *>(lds + L_RT);
         sel = b; wts = reinterpret_cast<LK_LOCAL float *>(b + DMAX_P); perm = b + 2 * DMAX_P; inv = b + 3 * DMAX_P;
         act_e = b + 4 * DMAX_P; act_s0 = act_e + DMAX_P + 1; act_cnt = act_s0 + DMAX_P + 1; nact = act_cnt + DMAX_P + 1;
+        ps_mi = nact + 1; ps_s = ps_mi + DMAX_PS; nps = ps_s + DMAX_PS;
     }
 };
 
 __device__ __forceinline__ void report(int * err, int code) { if (lane_id() == 0) { __hip_atomic_fetch_or(gptr(err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); } }
+
+// epoch-tagged words: {epoch (bits 32..63), fp32 bits}, one 64-bit store / load each (single-copy atomic)
+__device__ __forceinline__ void st_tag(uint64_t * p, uint32_t epoch, float v) {
+    __hip_atomic_store(gptr(p), ((uint64_t) epoch << 32) | __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_tag(const uint64_t * p) { return __hip_atomic_load(gptr(const_cast<uint64_t *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ bool tag_ok(uint64_t w, uint32_t epoch) { return (uint32_t) (w >> 32) == epoch; }
+__device__ __forceinline__ float tag_val(uint64_t w) { return __builtin_bit_cast(float, (uint32_t) w); }
+constexpr int POLL_MAX = 1 << 20;   // polls before a wait gives up (each poll is a memory round trip)
 
 // workgroup hand-off in LDS: counted arrivals and a ready word (waves of one workgroup are always co-resident)
 __device__ __forceinline__ bool lds_arrive(LK_LOCAL unsigned * c, unsigned expected) {
@@ -74,13 +98,31 @@ __device__ __forceinline__ unsigned lds_wait(LK_LOCAL unsigned * w) {
     }
     return 0;
 }
+__device__ __forceinline__ bool lds_wait_count(LK_LOCAL unsigned * c, unsigned want) {
+    for (int i = 0; i < (1 << 24); ++i) {
+        if (__builtin_amdgcn_readfirstlane(__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) == want) { return true; }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return false;
+}
+// a wave-uniform pointer kept in scalar registers (a per-lane select between two of them must not become a vector load
+// of the argument block)
+__device__ __forceinline__ const uint8_t * uniform_ptr(const uint8_t * p) {
+    const uint64_t v = (uint64_t) p;
+    // the builtin returns int: both halves go through uint32_t, so the low half is not sign-extended into the high one
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) (v >> 32));
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) v);
+    return (const uint8_t *) (((uint64_t) hi << 32) | (uint64_t) lo);
+}
 
 // Timeline probe for tuning builds (-DLOKI_TRACE): per wave, 64-bit s_memrealtime stamps (100 MHz) at the phase
-// boundaries (slots 0-5, 30) and at the start and end of each of the first 12 tasks (slots 6-29); slot 31 = task count.
+// boundaries (slots 0-7), the start and end of the first 8 gate/up tasks (8 + 2k, 9 + 2k), four stamps in each of the
+// first 8 down units (24 + 4k: start, h staged, rows computed, end) and the combine (56, 58); slot 63 = counts.
 #ifdef LOKI_TRACE
-constexpr int TRACE_SLOTS = 32;
+constexpr int TRACE_SLOTS = 64;
 __device__ uint64_t g_trace[1024 * DW * TRACE_SLOTS];
 #define TRACE(wave, slot) do { if (lane_id() == 0) { g_trace[(blockIdx.x * DW + (wave)) * TRACE_SLOTS + (slot)] = __builtin_amdgcn_s_memrealtime(); } } while (0)
+#define TRACE_T(tb, k) do { if ((tb) >= 0) { TRACE(threadIdx.x >> 6, (tb) + (k)); } } while (0)
 extern "C" hipError_t fl_trace_copy(void * host, size_t bytes) { return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace), bytes); }
 extern "C" hipError_t fl_trace_clear() {
     void * p = nullptr;
@@ -89,12 +131,26 @@ extern "C" hipError_t fl_trace_clear() {
 }
 #else
 #define TRACE(wave, slot) do { } while (0)
+#define TRACE_T(tb, k) do { } while (0)
 #endif
 
-// ---------------------------------------------------------------- phase 1: Q8_K of the token rows into LDS
-__device__ __noinline__ void quant_tokens(const DecodeArgs & a, lds_t lds, int wave) {
+// ---------------------------------------------------------------- phase 1
+// The table image into LDS with direct global->LDS loads (16 B per lane, 1 KB per wave instruction), issued first so
+// they complete under the router's loads; visible to the workgroup after s_waitcnt vmcnt(0) and a barrier.
+__device__ __forceinline__ void tables_dma(lds_t lds, const uint4 * img, int wave) {
+    constexpr int PER = TAB_BYTES / 1024 / DW;
+    const int lane = lane_id();
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int c = wave * PER + k;
+        __builtin_amdgcn_global_load_lds((const LK_GLOBAL void *) (img + c * 64 + lane), (LK_LOCAL void *) (lds + c * 1024), 16, 0, 0);
+    }
+}
+
+// Q8_K of the token rows into LDS (staged layout)
+__device__ __forceinline__ void quant_tokens(const DArgs & a, lds_t lds, int wave) {
     const int lane = lane_id(), nblk = a.n * GG::NB;
-    constexpr int B = 8;   // blocks per batch: their loads are all issued before the first is used
+    constexpr int B = 14;   // blocks per batch: their loads are all issued before the first is used
     for (int b0 = wave; b0 < nblk; b0 += DW * B) {
         float4 v[B];
 #pragma unroll
@@ -121,18 +177,16 @@ __device__ __noinline__ void quant_tokens(const DecodeArgs & a, lds_t lds, int w
     }
 }
 
-// ---------------------------------------------------------------- phase 2: router logits of expert e for token t
-// the contract of moe_device.h (256 in-order chunk sums, pairwise tree, one rounding); one wave per (expert, token)
-// Router logits of expert e for all n tokens by the whole workgroup. Thread (quarter w = wave & 3, lane) owns chunk
-// 64 w + lane (K/256 = 28 values) of every token t with t % 2 == wave / 4, so each thread issues its 7 + 7 * (tokens)
-// 16-byte loads at once. Tree levels 1-6 run inside the wave (one chunk per lane), 7-8 combine the four quarters'
-// totals through LDS. Each logit is published as one 64-bit word {epoch, fp32 bits}: consumers poll the words
-// themselves, so no counter, flag or store-completion wait sits between the router and the selection.
-__device__ __noinline__ void router_phase(const DecodeArgs & a, lds_t lds, int wave, int e) {
+// Router logits of expert e for all n tokens by the whole workgroup (the contract of moe_device.h: 256 in-order chunk
+// sums, pairwise tree, one rounding). Thread (quarter w = wave & 3, lane) owns chunk 64 w + lane (K/256 = 28 values)
+// of every token t with t % 2 == wave / 4, so each thread issues its 7 + 7 * (tokens) 16-byte loads at once. Tree levels
+// 1-6 run inside the wave (one chunk per lane), 7-8 combine the four quarters' totals through LDS. Thread t then
+// publishes p = sigmoid(logit) as one 64-bit word {epoch, fp32 bits}, so the selection starts from probabilities.
+__device__ __noinline__ void router_phase(const DArgs & a, lds_t lds, int wave, int e) {
 #pragma clang fp contract(off)
     constexpr int L4 = DE / 1024;   // float4 per chunk (7)
     const int lane = lane_id(), qt = wave & 3, half = wave >> 2, c = qt * 64 + lane;
-    LK_LOCAL double * part = reinterpret_cast<LK_LOCAL double *>(lds + L_DST);   // [token][quarter]
+    LK_LOCAL double * part = reinterpret_cast<LK_LOCAL double *>(lds + L_SCR);   // [token][quarter]
     constexpr int TB = 2;   // tokens per load batch (register budget)
     float4 wv[L4];
     const float * wc = a.Wr + (size_t) e * DE + (size_t) c * 4 * L4;
@@ -169,37 +223,42 @@ __device__ __noinline__ void router_phase(const DecodeArgs & a, lds_t lds, int w
         const int t = threadIdx.x;
         const float l = (float) ((part[t * 4 + 0] + part[t * 4 + 1]) + (part[t * 4 + 2] + part[t * 4 + 3]));
         const size_t o = (size_t) t * a.n_exp + e;
-        __hip_atomic_store(gptr(a.tlogits + o), ((uint64_t) a.epoch << 32) | __builtin_bit_cast(uint32_t, l), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        gptr(a.logits)[o] = l;   // the layer's logits (read after the launch)
+        const float p = det_sigmoid(l);
+        st_tag(a.tlogits + o, a.epoch, p);
+        gptr(a.logits)[o] = l;   // the layer's logits and probabilities (read after the launch)
+        if (a.probs) { gptr(a.probs)[o] = p; }
     }
     __syncthreads();   // part[] is reused by the next expert
 }
 
-// token t's logits of the lane's experts 4 lane + j, once every word carries this launch's epoch; false on timeout
-__device__ __forceinline__ bool wait_logits(const DecodeArgs & a, int t, float (&lg)[4]) {
+// ---------------------------------------------------------------- phase 2
+// token t's tagged probabilities of the lane's experts 4 lane + j (issue, then complete: the caller works in between)
+__device__ __forceinline__ void probs_issue(const DArgs & a, int t, uint64_t (&w)[4]) {
     const int lane = lane_id();
-    for (int it = 0; it < (1 << 20); ++it) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { const int e = 4 * lane + j; w[j] = e < a.n_exp ? ld_tag(a.tlogits + (size_t) t * a.n_exp + e) : 0; }
+}
+// completes the poll: every word carries this launch's epoch (re-polled until then); false on timeout
+__device__ __forceinline__ bool probs_wait(const DArgs & a, int t, uint64_t (&w)[4], float (&p)[4]) {
+    const int lane = lane_id();
+    for (int it = 0; it < POLL_MAX; ++it) {
         bool ok = true;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int e = 4 * lane + j;
-            if (e < a.n_exp) {
-                const uint64_t w = __hip_atomic_load(gptr(a.tlogits + (size_t) t * a.n_exp + e), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                ok = ok && (uint32_t) (w >> 32) == a.epoch;
-                lg[j] = __builtin_bit_cast(float, (uint32_t) w);
-            } else {
-                lg[j] = 0.f;
-            }
+        for (int j = 0; j < 4; ++j) { ok = ok && (4 * lane + j >= a.n_exp || tag_ok(w[j], a.epoch)); }
+        if (__ballot(!ok) == 0) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { p[j] = 4 * lane + j < a.n_exp ? tag_val(w[j]) : 0.f; }
+            return true;
         }
-        if (__ballot(!ok) == 0) { return true; }
         __builtin_amdgcn_s_sleep(2);
+        probs_issue(a, t, w);
     }
     return false;
 }
 
-// ---------------------------------------------------------------- phase 3: dispatch of the n * topk pairs (one wave)
-// stable counting sort by expert: pos(i) = #{pairs with a lower expert} + #{earlier pairs with the same expert}
-__device__ __noinline__ void dispatch_wave(const DecodeArgs & a, lds_t lds, int P) {
+// dispatch of the n * topk pairs (one wave): stable counting sort by expert,
+// pos(i) = #{pairs with a lower expert} + #{earlier pairs with the same expert}
+__device__ __noinline__ void dispatch_wave(const DArgs & a, lds_t lds, int P) {
     const RT rt(lds);
     const int lane = lane_id();
     const bool valid = lane < P;
@@ -226,6 +285,17 @@ __device__ __noinline__ void dispatch_wave(const DecodeArgs & a, lds_t lds, int 
         if (rank == 0) { rt.act_e[dless] = e; rt.act_s0[dless] = less; rt.act_cnt[dless] = __popcll(match); }
     }
     if (lane == 0) { *rt.nact = __popcll(first); }
+    // pair-slots: the shared expert's (tokens 2k, 2k + 1 at slots P + 2k ..), then every active expert's in act order
+    lds_visible();
+    const int nact = __popcll(first), nsh = (a.n + 1) >> 1;
+    const int cnt_l = lane < nact ? rt.act_cnt[lane] : 0, s_l = lane < nact ? rt.act_s0[lane] : 0;
+    const int np = (cnt_l + 1) >> 1;
+    const int incl = (int) wave_scan_u32((uint32_t) np), pos0 = nsh + incl - np;
+    for (int k = 0; k < np; ++k) {
+        if (pos0 + k < DMAX_PS) { rt.ps_mi[pos0 + k] = lane; rt.ps_s[pos0 + k] = (s_l + 2 * k) | ((cnt_l - 2 * k >= 2 ? 2 : 1) << 16); }
+    }
+    if (lane < nsh) { rt.ps_mi[lane] = SH; rt.ps_s[lane] = (P + 2 * lane) | ((a.n - 2 * lane >= 2 ? 2 : 1) << 16); }
+    if (lane == 63) { *rt.nps = nsh + incl < DMAX_PS ? nsh + incl : DMAX_PS; }
     if (blockIdx.x == 0) {   // the layer's routing outputs
         if (valid) { gptr(a.perm)[pos] = lane; gptr(a.inv)[lane] = pos; gptr(a.sel)[lane] = e; gptr(a.wts)[lane] = rt.wts[lane]; }
         if (valid && rank == 0) { gptr(a.act)[dless] = e; }
@@ -239,114 +309,210 @@ __device__ __noinline__ void dispatch_wave(const DecodeArgs & a, lds_t lds, int 
     }
 }
 
-// ---------------------------------------------------------------- phase 4 tasks
-struct Lane { int q, r; uint32_t tr, lq, ld; };
+// ---------------------------------------------------------------- phase 3: gate/up tasks
+// Lane 4 r + q of a task reads row r of a 16-row set and blocks 4 jj + q; here rows r < 8 are gate rows and r >= 8 the
+// same h rows of the up matrix, so every lane streams from its own base address.
+template <int PD>
+struct LaneStream {
+    static constexpr int STEPS = GG::BPQ, NR = PD + 1;
+    static constexpr size_t QSTEP = 4 * 4096, DSTEP = 4 * 128;   // 4 blocks per step (one per quad lane)
+    uint4 pf[NR][4]; uint16_t pd[NR];
+    __device__ __forceinline__ void issue(const uint8_t * ql, const uint8_t * dl, int s, int slot) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) { pf[slot][c] = load_nt(ql + s * QSTEP + c * 1024); }
+        pd[slot] = *gptr(reinterpret_cast<const uint16_t *>(dl + s * DSTEP));
+    }
+    __device__ __forceinline__ void prologue(const uint8_t * ql, const uint8_t * dl) {
+#pragma unroll
+        for (int k = 0; k < PD; ++k) { if (k < STEPS) { issue(ql, dl, k, k); } }
+    }
+    // row totals (before * 0.125) for T staged tokens xr[u], folded over the quad in block order
+    template <int T>
+    __device__ __forceinline__ void run(const uint8_t * ql, const uint8_t * dl, uint32_t tr, const uint8_t * const (&xr)[T], int q, float (&acc)[T]) {
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int u = 0; u < T; ++u) { acc[u] = 0.f; }
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) {
+            const int k = s % NR;
+            if (s + PD < STEPS) { issue(ql, dl, s + PD, (s + PD) % NR); }
+            const int j = s * 4 + q;
+            const uint8_t * xb[T];
+#pragma unroll
+            for (int u = 0; u < T; ++u) { xb[u] = xr[u] + j * GG::XBLK; }
+            int bsum[T];
+            block_bsum<T>(pf[k], tr, xb, bsum);
+            const float dw = h2f(pd[k]);
+#pragma unroll
+            for (int u = 0; u < T; ++u) {
+                const float dx = reinterpret_cast<const float *>(xr[u] + GG::NB * GG::XBLK)[j];
+                acc[u] = fold_quad(acc[u], (dw * dx) * (float) bsum[u]);
+            }
+        }
+    }
+};
 
-__device__ __noinline__ void gate_up_task(const DecodeArgs & a, lds_t lds, const Lane & ln, int mi, int g, int mat, int P) {
+struct Lane { int q, r; uint32_t tr; };
+
+// h rows hb * 8 .. hb * 8 + 7 of expert slot mi (act index, or SH) for the c (1 or 2) tokens at dispatch slots s, s + 1
+__device__ __forceinline__ void gate_up_task(const DArgs & a, lds_t lds, const Lane ln, int mi, int s, int c, int hb, int P) {
 #pragma clang fp contract(off)
     const RT rt(lds);
     const bool routed = mi != SH;
     const int e = routed ? rt.act_e[mi] : 0;
-    const int s0 = routed ? rt.act_s0[mi] : P, cnt = routed ? rt.act_cnt[mi] : a.n;
-    const uint8_t * base = routed ? (mat ? a.up : a.gate) + (size_t) e * a.estride : (mat ? a.sh_up : a.sh_gate);
-    const uint8_t * qb = base + (size_t) (g >> 2) * GG::NB * 4096 + (g & 3) * 256;
-    const uint8_t * db = base + (size_t) (DH / 64) * GG::NB * 4096 + (size_t) (g >> 2) * GG::NB * 128 + (g & 3) * 32;
-    float * outv = mat ? a.u : a.g;
-    const int row = g * 16 + ln.r;
-    for (int tok = 0; tok < cnt;) {
-        if (cnt - tok >= 2) {
-            RowStream<GG::BPQ, 1, GU_PD> rs;
-            rs.prologue(qb, db, ln.lq, ln.ld);
-            const uint8_t * xr[2];
+    const bool up = ln.r >= 8;
+    const int row = hb * GU_ROWS + (ln.r & 7);
+    const uint8_t * gm = uniform_ptr(routed ? a.gate + (size_t) e * a.estride : a.sh_gate);
+    const uint8_t * um = uniform_ptr(routed ? a.up + (size_t) e * a.estride : a.sh_up);
+    const uint8_t * mat = up ? um : gm;
+    const uint8_t * ql = mat + (size_t) (row >> 6) * GG::NB * 4096 + ln.q * 4096 + (row & 63) * 16;
+    const uint8_t * dl = mat + (size_t) (DH / 64) * GG::NB * 4096 + (size_t) (row >> 6) * GG::NB * 128 + ln.q * 128 + (row & 63) * 2;
+    const bool writer = ln.q == 0 && !up;   // lane 4 r (r < 8) publishes h of its row
+    if (c == 2) {
+        LaneStream<GU2_PD> ls;
+        ls.prologue(ql, dl);
+        const uint8_t * xr[2];
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int s = s0 + tok + u;
-                xr[u] = (const uint8_t *) (lds + L_XS + (routed ? rt.perm[s] / a.topk : s - P) * GG::XROW);
-            }
-            float acc[1][2];
-            rs.run<2, GG>(qb, db, ln.lq, ln.ld, ln.tr, xr, ln.q, acc);
-            if (ln.q == 0) {
+        for (int u = 0; u < 2; ++u) { xr[u] = (const uint8_t *) (lds + L_XS + (routed ? rt.perm[s + u] / a.topk : s + u - P) * GG::XROW); }
+        float acc[2];
+        ls.run<2>(ql, dl, ln.tr, xr, ln.q, acc);
 #pragma unroll
-                for (int u = 0; u < 2; ++u) { st_agent(outv + (size_t) (s0 + tok + u) * DH + row, 0.125f * acc[0][u]); }
-            }
-            tok += 2;
-        } else {
-            RowStream<GG::BPQ, 1, GU1_PD> rs;
-            rs.prologue(qb, db, ln.lq, ln.ld);
-            const int s = s0 + tok;
-            const uint8_t * xr[1] = { (const uint8_t *) (lds + L_XS + (routed ? rt.perm[s] / a.topk : s - P) * GG::XROW) };
-            float acc[1][1];
-            rs.run<1, GG>(qb, db, ln.lq, ln.ld, ln.tr, xr, ln.q, acc);
-            if (ln.q == 0) { st_agent(outv + (size_t) s * DH + row, 0.125f * acc[0][0]); }
-            tok += 1;
+        for (int u = 0; u < 2; ++u) {
+            const float other = __shfl_xor(acc[u], 32);   // the up row total, to the gate row's lanes
+            if (writer) { st_tag(a.th + (size_t) (s + u) * DH + row, a.epoch, det_silu(0.125f * acc[u]) * (0.125f * other)); }
         }
+    } else {
+        LaneStream<GU1_PD> ls;
+        ls.prologue(ql, dl);
+        const uint8_t * xr[1] = { (const uint8_t *) (lds + L_XS + (routed ? rt.perm[s] / a.topk : s - P) * GG::XROW) };
+        float acc[1];
+        ls.run<1>(ql, dl, ln.tr, xr, ln.q, acc);
+        const float other = __shfl_xor(acc[0], 32);
+        if (writer) { st_tag(a.th + (size_t) s * DH + row, a.epoch, det_silu(0.125f * acc[0]) * (0.125f * other)); }
     }
-    // the second task of the (gate, up) pair forms h for the pair's 16 rows
-    if (!arrive_last(a.cnt + CNT_PAIR + mi * NGU + g, 2u)) { return; }
-    const int lane = lane_id();
-    for (int i = lane; i < cnt * 16; i += 64) {
-        const size_t o = (size_t) (s0 + i / 16) * DH + g * 16 + i % 16;
-        st_agent(a.h + o, det_silu(ld_agent(a.g + o)) * ld_agent(a.u + o));
-    }
-    // the last of the 16 pairs of a 256-row block quantises that block of h for every slot of the expert
-    const int hb = g / 16;
-    if (!arrive_last(a.cnt + CNT_HB + mi * (DH / QK) + hb, 16u)) { return; }
-    for (int s = s0; s < s0 + cnt; ++s) {
-        const float * hbp = a.h + (size_t) s * DH + hb * QK;
-        const float xs[4] = { ld_agent(hbp + 4 * lane), ld_agent(hbp + 4 * lane + 1), ld_agent(hbp + 4 * lane + 2), ld_agent(hbp + 4 * lane + 3) };
-        float d; const uint32_t packed = q8k_lane(xs, d);
-        st_agent_u32(reinterpret_cast<uint32_t *>(a.hq + (size_t) s * DH + hb * QK) + lane, packed);
-        if (lane == 0) { st_agent(a.hd + (size_t) s * (DH / QK) + hb, d); }
-    }
-    // the last block of the expert raises its flag
-    if (!arrive_last(a.cnt + CNT_HQ + mi, (unsigned) (DH / QK))) { return; }
-    if (lane == 0) { st_agent_u32(a.flags + FLAG_H + mi, a.epoch); }
 }
 
-__device__ __noinline__ void down_task(const DecodeArgs & a, lds_t lds, const Lane & ln, int wave, int mi, int g, int P, int nm) {
+// ---------------------------------------------------------------- phase 4: down units
+// Wave w of the unit's workgroup owns output rows rg * 256 + 32 w .. + 31 (two 16-row sets of one 64-row group) and
+// stages Q8_K block w of h for the unit's c (1 or 2) tokens at slots s, s + 1. The first poll of h is issued before the
+// weight loads, so its wait does not include them. Returns false if a wait timed out (the unit is skipped).
+__device__ __forceinline__ bool down_unit(const DArgs & a, lds_t lds, const Lane ln, int wave, int mi, int s, int c, int rg, int P, int tb) {
 #pragma clang fp contract(off)
     const RT rt(lds);
     const bool routed = mi != SH;
     const int e = routed ? rt.act_e[mi] : 0;
-    const int s0 = routed ? rt.act_s0[mi] : P, cnt = routed ? rt.act_cnt[mi] : a.n;
-    const uint8_t * base = routed ? a.down + (size_t) e * a.estride : a.sh_down;
-    const int rg = (g * 32) >> 6, sub = ((g * 32) & 63) >> 4;
-    const uint8_t * qb = base + (size_t) rg * GD::NB * 4096 + sub * 256;
-    const uint8_t * db = base + (size_t) (DE / 64) * GD::NB * 4096 + (size_t) rg * GD::NB * 128 + sub * 32;
-    uint8_t * xw = (uint8_t *) (lds + L_DST + wave * GD::XROW);
-    RowStream<GD::BPQ, DRPL, DN_PD> rs;
-    rs.prologue(qb, db, ln.lq, ln.ld);   // the weights do not depend on h: in flight while the wave waits
-    if (!wait_flag(a.flags + FLAG_H + mi, a.epoch)) { report(a.err, 1); return; }
-    for (int s = s0; s < s0 + cnt; ++s) {
-        if (s > s0) { rs.prologue(qb, db, ln.lq, ln.ld); }
-        __builtin_amdgcn_wave_barrier();
-        stage_row_agent<GD>(xw, a.hq + (size_t) s * DH, a.hd + (size_t) s * (DH / QK));
-        lds_visible();
-        const uint8_t * xr[1] = { xw };
-        float acc[DRPL][1];
-        rs.run<1, GD>(qb, db, ln.lq, ln.ld, ln.tr, xr, ln.q, acc);
-        if (ln.q == 0) {
+    const uint8_t * base = uniform_ptr(routed ? a.down + (size_t) e * a.estride : a.sh_down);
+    const int g64 = rg * (DN_ROWS / 64) + (wave >> 1), sub = (wave & 1) * 2;
+    const uint8_t * qb = base + (size_t) g64 * GD::NB * 4096 + sub * 256;
+    const uint8_t * db = base + (size_t) (DE / 64) * GD::NB * 4096 + (size_t) g64 * GD::NB * 128 + sub * 32;
+    const uint32_t lq = (uint32_t) ln.q * 4096 + 16 * ln.r, ld = (uint32_t) ln.q * 128 + 2 * ln.r;
+    const int lane = lane_id();
+    uint64_t w[2][4];
+    auto issue_h = [&]() {
 #pragma unroll
-            for (int r2 = 0; r2 < DRPL; ++r2) { st_agent(a.o + (size_t) s * DE + g * 32 + r2 * 16 + ln.r, 0.125f * acc[r2][0]); }
+        for (int u = 0; u < 2; ++u) {
+            if (u < c) {
+                const uint64_t * src = a.th + (size_t) (s + u) * DH + wave * QK + 4 * lane;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) { w[u][k] = ld_tag(src + k); }
+            }
+        }
+    };
+    issue_h();
+    RowStream<GD::BPQ, 2, DN_PD> rs;
+    rs.prologue(qb, db, lq, ld);   // the weights do not depend on h: in flight during the wait
+    int it = 0;
+    for (; it < POLL_MAX; ++it) {
+        bool v = true;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) { v = v && (u >= c || tag_ok(w[u][k], a.epoch)); }
+        }
+        if (__ballot(!v) == 0) { break; }
+        __builtin_amdgcn_s_sleep(1);
+        issue_h();
+    }
+    const bool ok = it < POLL_MAX;
+    if (ok) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            if (u < c) {
+                const float xs[4] = { tag_val(w[u][0]), tag_val(w[u][1]), tag_val(w[u][2]), tag_val(w[u][3]) };
+                float d; const uint32_t packed = q8k_lane(xs, d);
+                lds_t hrow = lds + L_HS + u * GD::XROW;
+                *reinterpret_cast<LK_LOCAL uint32_t *>(hrow + wave * GD::XBLK + staged_word(lane)) = packed;
+                if (lane == 0) { reinterpret_cast<LK_LOCAL float *>(hrow + GD::NB * GD::XBLK)[wave] = d; }
+            }
         }
     }
-    // the last expert of the row group combines: y = sum_k w_k o_k in k order + shared, for every token
-    if (!arrive_last(a.cnt + CNT_COMB + g, (unsigned) nm)) { return; }
-    const int lane = lane_id();
-    for (int i = lane; i < a.n * 32; i += 64) {
-        const int tok = i / 32, rr = g * 32 + i % 32;
-        float ov[MAXK + 1];
+    // every wave's staging succeeded (no __syncthreads_and: its static LDS word would move the 64 KB aligned tables)
+    LK_LOCAL unsigned * wok = reinterpret_cast<LK_LOCAL unsigned *>(lds + L_CTL) + 4;
+    if (lane == 0) { wok[wave] = ok ? 1u : 0u; }
+    __syncthreads();
+    bool all_ok = true;
 #pragma unroll
-        for (int k = 0; k < MAXK; ++k) { ov[k] = k < a.topk ? ld_agent(a.o + (size_t) rt.inv[tok * a.topk + k] * DE + rr) : 0.f; }
-        ov[MAXK] = ld_agent(a.o + (size_t) (P + tok) * DE + rr);
+    for (int w2 = 0; w2 < DW; ++w2) { all_ok = all_ok && wok[w2] != 0u; }
+    TRACE_T(tb, 1);
+    if (all_ok) {
+        // one token per pass: the second pass re-reads the unit's weights from L2
+        for (int i = 0; i < c; ++i) {
+            if (i > 0) { rs.prologue(qb, db, lq, ld); }
+            const uint8_t * xr[1] = { (const uint8_t *) (lds + L_HS + i * GD::XROW) };
+            float acc[2][1];
+            rs.run<1, GD>(qb, db, lq, ld, ln.tr, xr, ln.q, acc);
+            if (ln.q == 0) {
+#pragma unroll
+                for (int r2 = 0; r2 < 2; ++r2) { st_tag(a.to + (size_t) (s + i) * DE + rg * DN_ROWS + wave * 32 + r2 * 16 + ln.r, a.epoch, 0.125f * acc[r2][0]); }
+            }
+        }
+    }
+    TRACE_T(tb, 2);
+    __syncthreads();   // the staged h is overwritten by the next unit
+    return all_ok;
+}
+
+// ---------------------------------------------------------------- phase 5: combine
+// rows cu * 256 .. + 255 of every token: y = sum_k w_k o_k in k order + the shared expert's o; false on timeout
+__device__ __forceinline__ bool combine_unit(const DArgs & a, lds_t lds, int cu, int P) {
+#pragma clang fp contract(off)
+    const RT rt(lds);
+    const int rr = cu * DN_ROWS + (threadIdx.x & (DN_ROWS - 1));
+    bool ok = true;
+    // a wave's 64 threads share tok, so the loop and the polls are wave-uniform
+    for (int tok = threadIdx.x / DN_ROWS; tok < a.n; tok += DNT / DN_ROWS) {
+        float ov[MAXK + 1];
+        int it = 0;
+        for (; it < POLL_MAX; ++it) {
+            bool v = true;
+#pragma unroll
+            for (int k = 0; k <= MAXK; ++k) {
+                if (k < a.topk || k == MAXK) {
+                    const int s = k < MAXK ? rt.inv[tok * a.topk + k] : P + tok;
+                    const uint64_t w = ld_tag(a.to + (size_t) s * DE + rr);
+                    v = v && tag_ok(w, a.epoch); ov[k] = tag_val(w);
+                } else {
+                    ov[k] = 0.f;
+                }
+            }
+            if (__ballot(!v) == 0) { break; }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (it == POLL_MAX) { ok = false; continue; }
         float mv = ov[0] * rt.wts[tok * a.topk];
-        for (int k = 1; k < a.topk; ++k) { mv = mv + ov[k] * rt.wts[tok * a.topk + k]; }
+#pragma unroll
+        for (int k = 1; k < MAXK; ++k) { if (k < a.topk) { mv = mv + ov[k] * rt.wts[tok * a.topk + k]; } }
         gptr(a.y)[(size_t) tok * DE + rr] = mv + ov[MAXK];
     }
+    return ok;
 }
 
 // ---------------------------------------------------------------- the kernel
-__global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs a) {
+__global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
+    // The arguments are read in place in the kernarg segment (the only explicit argument, at offset 0) through a
+    // constant-space pointer, so every field is a scalar load. Naming `args` itself would make a private copy.
+    (void) sizeof(args);
+    const DArgs & a = *(const DArgs *) __builtin_amdgcn_kernarg_segment_ptr();
     extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds[];
     const lds_t lds = (lds_t) dyn_lds;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
@@ -355,33 +521,35 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs a) {
     Lane ln;
     ln.r = lane >> 2; ln.q = lane & 3;
     ln.tr = lds_addr(dyn_lds) | ((uint32_t) (lane & 15) << 3);   // table base (64 KB aligned: the tables open the LDS) | replica
-    ln.lq = (uint32_t) ln.q * 4096 + 16 * ln.r; ln.ld = (uint32_t) ln.q * 128 + 2 * ln.r;
 
-    // 1. router logits (the whole workgroup), then tables and tokens
+    // 1. table copy in flight; router (the whole workgroup)
     TRACE(wave, 0);
+    if (lds_addr(dyn_lds) & 0xFFFFu) { report(a.err, 4); return; }   // table addressing needs a 64 KB aligned base
     if (threadIdx.x < 4) { ctl[threadIdx.x] = 0; }
+    tables_dma(lds, a.tab, wave);
+    __syncthreads();   // the hand-off words are clear
     for (int e = blockIdx.x; e < a.n_exp; e += G) { router_phase(a, lds, wave, e); }
     TRACE(wave, 2);
-    tables_copy<DNT>(dyn_lds, a.tab);
-    quant_tokens(a, lds, wave);
-    __syncthreads();
-    TRACE(wave, 1);
-    if (lds_addr(dyn_lds) & 0xFFFFu) { report(a.err, 4); return; }   // table addressing needs a 64 KB aligned base
 
-    // 2. selection (wave t = token t, every workgroup redundantly); the last selecting wave builds the dispatch and opens
-    //    the task phase. Waves without a token run the shared expert's gate/up meanwhile.
+    // 2. wave t polls token t's probabilities while all waves quantise the tokens; wave t then selects token t's experts
+    //    (every workgroup redundantly) and the last selecting wave builds the dispatch and opens the task phase. Waves
+    //    without a token run the shared expert's gate/up meanwhile.
     const bool pre = n < DW;
+    float bv[4]; uint64_t pw[4];
+    if (wave < n) { load_bias(a.bias, a.n_exp, bv); probs_issue(a, wave, pw); }
+    quant_tokens(a, lds, wave);
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's table loads have landed in LDS
+    lds_arrive(ctl + 0, DW);              // [0] counts the waves whose tokens and table share are in LDS
+    TRACE(wave, 1);
     if (wave < n) {
-        float bv[4], lg[4];
-        load_bias(a.bias, a.n_exp, bv);
-        const bool ok = wait_logits(a, wave, lg);
+        float pv[4];
+        const bool ok = probs_wait(a, wave, pw, pv);
         TRACE(wave, 3);
         if (!ok) { report(a.err, 2); }
         const RT rt(lds);
-        float * scr = (float *) (lds + L_DST) + wave * (NEXP_MAX + 2 * 64);
+        float * scr = (float *) (lds + L_SCR) + wave * (NEXP_MAX + 2 * 64);
         if (ok) {
-            select_token(lg, bv, a.n_exp, a.n_group, a.topk_group, a.topk, a.scale, scr, (int *) (rt.sel + wave * a.topk),
-                         (float *) (rt.wts + wave * a.topk), blockIdx.x == 0 && a.probs ? a.probs + (size_t) wave * a.n_exp : nullptr);
+            select_token_p(pv, bv, a.n_exp, a.n_group, a.topk_group, a.topk, a.scale, scr, (int *) (rt.sel + wave * a.topk), (float *) (rt.wts + wave * a.topk));
         } else if (lane == 0) {
             __hip_atomic_fetch_or(ctl + 3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
@@ -389,41 +557,72 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs a) {
         if (lds_arrive(ctl + 1, (unsigned) n)) {
             const bool all_ok = __builtin_amdgcn_readfirstlane(__hip_atomic_load(ctl + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) == 0;
             dispatch_wave(a, lds, all_ok ? P : 0);
+            const bool staged = lds_wait_count(ctl + 0, DW);   // the tasks read the tables and the tokens
             lds_visible();
-            if (lane == 0) { __hip_atomic_store(ctl + 2, all_ok ? 1u : 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
-            TRACE(wave, 30);
+            if (lane == 0) { __hip_atomic_store(ctl + 2, all_ok && staged ? 1u : 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+            TRACE(wave, 6);
         }
-    } else if (pre) {
-        for (int tk = (wave - n) * G + blockIdx.x; tk < 2 * NGU; tk += (DW - n) * G) { gate_up_task(a, lds, ln, SH, tk >> 1, tk & 1, P); }
+    } else if (pre && lds_wait_count(ctl + 0, DW)) {   // the shared expert's pair-slots k: tokens 2k, 2k + 1
+        const int nsh = (n + 1) >> 1;
+        for (int tk = (wave - n) * G + blockIdx.x; tk < nsh * NGU; tk += (DW - n) * G) {
+            const int k = tk / NGU;
+            gate_up_task(a, lds, ln, SH, P + 2 * k, n - 2 * k >= 2 ? 2 : 1, tk % NGU, P);
+        }
     }
     const unsigned ready = lds_wait(ctl + 2);
     TRACE(wave, 5);
+    // a failed routing wait leaves every later phase without its inputs: all waves leave (the error is reported)
     if (ready != 1) { if (ready == 0) { report(a.err, 8); } return; }
 
-    // 4. expert tasks, round-robin over every wave of the grid (task tk on workgroup tk % G, wave tk / G % DW)
-    const int nact = *RT(lds).nact, nm = nact + 1;
-    const int t_gu = (nact + (pre ? 0 : 1)) * 2 * NGU, t_all = t_gu + nm * NDN;
+    // 3. gate/up tasks (pair-slot, 8 h rows), round-robin over every wave of the grid (task tk on workgroup tk % G,
+    //    wave tk / G % DW); the shared expert's pair-slots come first unless the early tasks covered them
+    const RT rt(lds);
+    const int nact = *rt.nact, nps = *rt.nps, ps0 = pre ? (n + 1) >> 1 : 0;
+    const int t_gu = (nps - ps0) * NGU;
     int ntask = 0;
-    for (int tk = wave * G + blockIdx.x; tk < t_all; tk += G * DW) {
-        if (ntask < 12) { TRACE(wave, 6 + 2 * ntask); }
-        if (tk < t_gu) {
-            const int m = tk / (2 * NGU), r = tk % (2 * NGU);
-            gate_up_task(a, lds, ln, m < nact ? m : SH, r >> 1, r & 1, P);
+    for (int tk = wave * G + blockIdx.x; tk < t_gu; tk += G * DW) {
+        if (ntask < 8) { TRACE(wave, 8 + 2 * ntask); }
+        const int ps = ps0 + tk / NGU, mi = rt.ps_mi[ps], sc = rt.ps_s[ps];
+        if ((mi == SH || (unsigned) mi < (unsigned) nact) && (sc & 0xFFFF) + (sc >> 16) <= P + n) {
+            gate_up_task(a, lds, ln, mi, sc & 0xFFFF, sc >> 16, tk % NGU, P);
         } else {
-            const int d = tk - t_gu, m = d / NDN;
-            down_task(a, lds, ln, wave, m < nact ? m : SH, d % NDN, P, nm);
+            report(a.err, 32);
         }
-        if (ntask < 12) { TRACE(wave, 7 + 2 * ntask); }
+        if (ntask < 8) { TRACE(wave, 9 + 2 * ntask); }
         ++ntask;
     }
+    TRACE(wave, 7);
+
+    // 4. down units (pair-slot, 256 rows), round-robin over the workgroups: unit u = row group u / nps of pair-slot u % nps
+    int nunit = 0;
+    for (int u = blockIdx.x; u < nps * NDN; u += G) {
+        const int ps = u % nps, mi = rt.ps_mi[ps], sc = rt.ps_s[ps];
 #ifdef LOKI_TRACE
-    if (lane == 0) { g_trace[(blockIdx.x * DW + wave) * TRACE_SLOTS + 31] = (uint64_t) ntask | ((uint64_t) t_gu << 32); }
+        const int tb = nunit < 8 ? 24 + 4 * nunit : -1;
+#else
+        const int tb = -1;
+#endif
+        TRACE_T(tb, 0);
+        const bool valid = (mi == SH || (unsigned) mi < (unsigned) nact) && (sc & 0xFFFF) + (sc >> 16) <= P + n;   // uniform in the workgroup
+        if (!valid || !down_unit(a, lds, ln, wave, mi, sc & 0xFFFF, sc >> 16, u / nps, P, tb)) { report(a.err, 1); }
+        TRACE_T(tb, 3);
+        ++nunit;
+    }
+
+    // 5. combine units on the last workgroups
+    for (int cu = G - 1 - blockIdx.x; cu < NDN; cu += G) {
+        TRACE(wave, 56);
+        if (!combine_unit(a, lds, cu, P)) { report(a.err, 16); }
+        TRACE(wave, 58);
+    }
+#ifdef LOKI_TRACE
+    if (lane == 0) { g_trace[(blockIdx.x * DW + wave) * TRACE_SLOTS + 63] = (uint64_t) ntask | ((uint64_t) nunit << 16) | ((uint64_t) t_gu << 32); }
 #endif
 }
 
 size_t decode_lds_bytes() { return DEC_LDS; }
 
-// workgroups of k_moe_decode that can be resident at once on `ncu` CUs (0: the cooperative launch is unavailable)
+// workgroups of k_moe_decode that can be resident at once on `ncu` CUs (0: the single launch is unavailable)
 hipError_t decode_init(int ncu, int * grid) {
     *grid = 0;
     hipError_t e = hipFuncSetAttribute((const void *) k_moe_decode, hipFuncAttributeMaxDynamicSharedMemorySize, DEC_LDS);
@@ -437,7 +636,7 @@ hipError_t decode_init(int ncu, int * grid) {
 
 hipError_t launch_moe_decode(const DecodeArgs & a, int grid, bool cooperative, hipStream_t st) {
     if (a.n < 1 || a.n > DMAX_N || a.topk < 1 || a.topk > MAXK || a.n_exp < 1 || a.n_exp > NEXP_MAX || a.n_group < 1 || a.n_group > 64 ||
-        a.n_exp % a.n_group || a.E != DE || a.H != DH || grid < 1) {
+        a.n_exp % a.n_group || a.E != DE || a.H != DH || grid < 1 || !a.th || !a.to || !a.tlogits) {
         return hipErrorInvalidValue;
     }
     if (!cooperative) {   // one workgroup per CU fits the occupancy; co-residency is assumed, waits stay bounded

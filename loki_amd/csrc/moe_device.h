@@ -143,16 +143,26 @@ __device__ __forceinline__ void logit_chunks_any(const float * w, const float * 
     }
 }
 
-// wave-wide maximum of unsigned 32-bit values, returned to every lane (uniform)
+// wave-wide maximum of unsigned 32-bit values, returned to every lane (uniform). Every step reads its partner through
+// DPP with bound_ctrl (lanes without a partner read 0, the identity of max), so each step is one v_max_u32_dpp; after
+// row_bcast:15 / row_bcast:31 lane 63 holds the maximum of all 64 lanes.
 __device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b) { return a > b ? a : b; }
-template <int CTRL, int ROWS> __device__ __forceinline__ uint32_t max32_step(uint32_t v) {
-    return umax32(v, (uint32_t) __builtin_amdgcn_update_dpp((int) v, (int) v, CTRL, ROWS, 0xF, false));
-}
+template <int CTRL> __device__ __forceinline__ uint32_t max32_step(uint32_t v) { return umax32(v, dpp<CTRL>(v)); }
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    v = max32_step<DPP_XOR1, 0xF>(v); v = max32_step<DPP_XOR2, 0xF>(v);
-    v = max32_step<DPP_HALF_MIRROR, 0xF>(v); v = max32_step<DPP_MIRROR, 0xF>(v);
-    v = max32_step<DPP_BCAST15, 0xA>(v); v = max32_step<DPP_BCAST31, 0xC>(v);
+    v = max32_step<DPP_XOR1>(v); v = max32_step<DPP_XOR2>(v);
+    v = max32_step<DPP_HALF_MIRROR>(v); v = max32_step<DPP_MIRROR>(v);
+    v = max32_step<DPP_BCAST15>(v); v = max32_step<DPP_BCAST31>(v);
     return rdlane(v, 63);
+}
+// inclusive prefix sum over the wave's lanes (lane l gets v_0 + .. + v_l): shifts inside 16-lane rows, then each row adds
+// the totals of the rows below it (row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3)
+template <int CTRL, int ROWS> __device__ __forceinline__ uint32_t scan_step(uint32_t v) {
+    return v + (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, CTRL, ROWS, 0xF, false);
+}
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t v) {
+    v = scan_step<0x111, 0xF>(v); v = scan_step<0x112, 0xF>(v); v = scan_step<0x114, 0xF>(v); v = scan_step<0x118, 0xF>(v);
+    v = scan_step<DPP_BCAST15, 0xA>(v); v = scan_step<DPP_BCAST31, 0xC>(v);
+    return v;
 }
 // lowest lane whose flag is set (uniform; 64 if none)
 __device__ __forceinline__ int first_lane(bool f) { const uint64_t b = __ballot(f); return b ? __builtin_ctzll(b) : 64; }
@@ -378,20 +388,14 @@ __device__ __forceinline__ void load_bias(const float * bias, int n_exp, float (
 #pragma unroll
     for (int j = 0; j < 4; ++j) { b[j] = 4 * lane + j < n_exp ? gptr(bias)[4 * lane + j] : 0.f; }
 }
-__device__ __forceinline__ void select_token(const float (&lg)[4], const float (&bias)[4], int n_exp, int n_group, int topk_group, int topk,
-                                             float scale, float * scr, int * sel_out, float * w_out, float * probs_out) {
+// the rule from the lane's 4 probabilities p[j] = sigmoid(logit) of experts 4 lane + j
+__device__ __forceinline__ void select_token_p(const float (&p)[4], const float (&bias)[4], int n_exp, int n_group, int topk_group, int topk,
+                                               float scale, float * scr, int * sel_out, float * w_out) {
 #pragma clang fp contract(off)
     const int lane = lane_id(), per = n_exp / n_group;
-    float p[4], c[4];
+    float c[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int e = 4 * lane + j;
-        p[j] = 0.f; c[j] = 0.f;
-        if (e < n_exp) {
-            p[j] = det_sigmoid(lg[j]); c[j] = p[j] + bias[j];
-            if (probs_out) { gptr(probs_out)[e] = p[j]; }
-        }
-    }
+    for (int j = 0; j < 4; ++j) { c[j] = 4 * lane + j < n_exp ? p[j] + bias[j] : 0.f; }
     bool ok[4];
     const int lpg = per / 4;   // lanes per group
     if (per % 4 == 0 && (lpg & (lpg - 1)) == 0 && lpg <= 16) {
@@ -471,6 +475,22 @@ __device__ __forceinline__ void select_token(const float (&lg)[4], const float (
     for (int k = 0; k < MAXK; ++k) {
         if (k < topk && lane == k) { sel_out[k] = ir[k]; w_out[k] = pr[k] / sum * scale; }
     }
+}
+// the same from the lane's 4 logits; probs_out (optional) receives the n_exp probabilities
+__device__ __forceinline__ void select_token(const float (&lg)[4], const float (&bias)[4], int n_exp, int n_group, int topk_group, int topk,
+                                             float scale, float * scr, int * sel_out, float * w_out, float * probs_out) {
+    const int lane = lane_id();
+    float p[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = 4 * lane + j;
+        p[j] = 0.f;
+        if (e < n_exp) {
+            p[j] = det_sigmoid(lg[j]);
+            if (probs_out) { gptr(probs_out)[e] = p[j]; }
+        }
+    }
+    select_token_p(p, bias, n_exp, n_group, topk_group, topk, scale, scr, sel_out, w_out);
 }
 
 }  // namespace lk

@@ -46,10 +46,6 @@ hipError_t launch_experts_gateup(const ExpertArgs & a, int grid, hipStream_t st)
 hipError_t launch_experts_down(const ExpertArgs & a, int grid, hipStream_t st);
 
 // ---------------------------------------------------------------- single-launch decode block (moe_decode.hip)
-// counters (self-resetting, zero before the first launch) and epoch flags inside DecodeArgs::cnt / ::flags
-constexpr int CNT_PAIR = 1, CNT_HB = CNT_PAIR + 257 * 128, CNT_HQ = CNT_HB + 257 * 8, CNT_COMB = CNT_HQ + 257,
-              DEC_CNT = CNT_COMB + 256;
-constexpr int FLAG_H = 1, DEC_FLAGS = FLAG_H + 257;
 struct DecodeArgs {
     const uint4 * tab;
     const float * x; int n;                          // tokens [n][E], n <= 8
@@ -59,11 +55,13 @@ struct DecodeArgs {
     int E, H;                                        // 7168, 2048 (the kernel's geometry)
     int8_t * xq; float * xd;                         // Q8_K of x (written by workgroup 0)
     float * logits, * probs; int * sel; float * wts; int * counts, * offsets, * perm, * inv, * act, * nact;
-    uint64_t * tlogits;                              // [n][n_exp] logits tagged with the launch's epoch (bits 32..63)
-    float * g, * u, * h; int8_t * hq; float * hd; float * o;   // [P+n][H] / [P+n][E] per dispatch slot
+    // epoch-tagged words {epoch << 32 | fp32 bits}: logits [n][n_exp], h [P+n][H], o [P+n][E] per dispatch slot
+    uint64_t * tlogits, * th, * to;
     float * y;                                       // [n][E]
-    unsigned * cnt, * flags; unsigned epoch; int * err;
+    unsigned epoch; int * err;
 };
+// sizes (64-bit words) of the tagged buffers for any n <= 8 (topk <= MAXK)
+constexpr size_t DEC_TLOGITS = 8 * 256, DEC_TH = (size_t) 8 * (MAXK + 1) * 2048, DEC_TO = (size_t) 8 * (MAXK + 1) * 7168;
 hipError_t decode_init(int ncu, int * grid);
 size_t decode_lds_bytes();
 // grid workgroups (at most one per CU can be resident): a cooperative launch guarantees they are all resident; a

@@ -125,19 +125,28 @@ def _block_vs_oracle(ctx, layer, x, tokens, capture=True):
 def test_block_decode_bitwise(ctx, layer, n):
     x = make_x(ctx, n, seed=200 + n)
     tokens = np.arange(n)
-    y, ref, dbg = _block_vs_oracle(ctx, layer, x, tokens)
-    mx, l2 = rel_errors(y, ref["y"])
-    assert mx <= MAX_REL and l2 <= L2_REL, (mx, l2)
-    # intermediates per (token, k) pair: the device keeps them per dispatch slot, inv maps pair -> slot
-    P = n * 8
-    inv = ctx.d2h(dbg.inv, (P,), np.int32)
-    g = ctx.d2h(dbg.g, (P + n, H), np.float32); u = ctx.d2h(dbg.u, (P + n, H), np.float32)
-    o = ctx.d2h(dbg.o, (P + n, E), np.float32)
-    assert np.array_equal(g[inv].view(np.uint32), ref["g"].view(np.uint32))
-    assert np.array_equal(u[inv].view(np.uint32), ref["u"].view(np.uint32))
-    assert np.array_equal(o[inv].view(np.uint32), ref["o"].view(np.uint32))
-    assert np.array_equal(o[P:].view(np.uint32), ref["sh"].view(np.uint32))
-    assert np.array_equal(y.view(np.uint32), ref["y"].view(np.uint32)), "block output not bit-identical (max rel %.3g)" % mx
+    ctx.set_fused(False)   # the per-pass kernels keep their intermediates in plain buffers
+    try:
+        y, ref, dbg = _block_vs_oracle(ctx, layer, x, tokens)
+        mx, l2 = rel_errors(y, ref["y"])
+        assert mx <= MAX_REL and l2 <= L2_REL, (mx, l2)
+        # intermediates per (token, k) pair: the device keeps them per dispatch slot, inv maps pair -> slot
+        P = n * 8
+        inv = ctx.d2h(dbg.inv, (P,), np.int32)
+        g = ctx.d2h(dbg.g, (P + n, H), np.float32); u = ctx.d2h(dbg.u, (P + n, H), np.float32)
+        o = ctx.d2h(dbg.o, (P + n, E), np.float32)
+        assert np.array_equal(g[inv].view(np.uint32), ref["g"].view(np.uint32))
+        assert np.array_equal(u[inv].view(np.uint32), ref["u"].view(np.uint32))
+        assert np.array_equal(o[inv].view(np.uint32), ref["o"].view(np.uint32))
+        assert np.array_equal(o[P:].view(np.uint32), ref["sh"].view(np.uint32))
+        assert np.array_equal(y.view(np.uint32), ref["y"].view(np.uint32)), "block output not bit-identical (max rel %.3g)" % mx
+    finally:
+        ctx.set_fused(True)
+    # the single-launch decode block on the same rows
+    yf = ctx.moe_layer(layer, x)
+    ctx.sync()
+    assert ctx.debug().fused == 1
+    assert np.array_equal(yf.cpu().numpy()[tokens].view(np.uint32), ref["y"].view(np.uint32))
 
 
 def test_block_prefill512_rows(ctx):
@@ -170,7 +179,6 @@ def _routing_state(ctx, n):
         "xq": ctx.d2h(dbg.xq, (n, E), np.int8), "xd": ctx.d2h(dbg.xd, (n, E // 256), np.float32),
     }
     out["act"] = ctx.d2h(dbg.act, (int(out["nact"][0]),), np.int32)
-    out["o"] = ctx.d2h(dbg.o, (P + n, E), np.float32)
     return out
 
 
