@@ -38,7 +38,7 @@ constexpr int GU_ROWS = 8;             // h rows per gate/up task (8 gate + the 
 constexpr int NGU = DH / GU_ROWS;      // gate/up tasks per expert
 constexpr int DN_ROWS = DW * 32;       // output rows per down unit (32 per wave: two row sets of 16)
 constexpr int NDN = DE / DN_ROWS;      // down units per expert (= combine units)
-constexpr int GU1_PD = 4, GU2_PD = 3, DN_PD = 3;   // blocks in flight per lane
+constexpr int GU_PD = 3, DN_PD = 2;   // blocks in flight per lane
 static_assert(DH == DW * QK, "a down unit's wave w quantises h block w");
 static_assert(DMAX_N * (MAXK + 1) * DH <= (int) DEC_TH && DMAX_N * (MAXK + 1) * DE <= (int) DEC_TO, "tagged buffer sizes");
 
@@ -49,10 +49,12 @@ constexpr int HS_BYTES = DMAX_N * GD::XROW;
 constexpr int L_SCR = L_HS;                                       // router sums / selection scratch (phases 1-2) overlay HS
 constexpr int L_RT = L_HS + HS_BYTES;                             // routing tables
 constexpr int RT_INTS = 4 * DMAX_P + 3 * (DMAX_P + 1) + 1 + 2 * DMAX_PS + 1;
-constexpr int L_CTL = L_RT + RT_INTS * 4;                         // workgroup hand-off words [4], per-wave flags [DW]
-constexpr int DEC_LDS = L_CTL + (4 + DW) * 4;
+constexpr int L_CTL = L_RT + RT_INTS * 4;                         // workgroup hand-off words [8], per-wave flags [2][DW]
+constexpr int DEC_LDS = L_CTL + (8 + 2 * DW) * 4;
+constexpr int L_PRE = L_SCR + DW * (NEXP_MAX + 2 * 64) * 4;      // early shared task's block terms [2][7][64] floats
 static_assert(DEC_LDS <= 160 * 1024, "LDS budget");
-static_assert(DMAX_N * 4 * 8 <= HS_BYTES && DW * (NEXP_MAX + 2 * 64) * 4 <= HS_BYTES, "scratch overlays");
+static_assert(DMAX_N * 4 * 8 <= HS_BYTES && DW * (NEXP_MAX + 2 * 64) * 4 <= HS_BYTES && 4 * GD::XROW <= HS_BYTES, "scratch overlays");
+static_assert(L_PRE + 2 * 7 * 64 * 4 <= L_HS + HS_BYTES, "early shared task terms overlay the h staging");
 
 typedef LK_LOCAL uint8_t * lds_t;
 typedef LK_CONST DecodeArgs DArgs;   // the launch arguments, read in place with scalar loads
@@ -116,8 +118,8 @@ __device__ __forceinline__ const uint8_t * uniform_ptr(const uint8_t * p) {
 }
 
 // Timeline probe for tuning builds (-DLOKI_TRACE): per wave, 64-bit s_memrealtime stamps (100 MHz) at the phase
-// boundaries (slots 0-7), the start and end of the first 8 gate/up tasks (8 + 2k, 9 + 2k), four stamps in each of the
-// first 8 down units (24 + 4k: start, h staged, rows computed, end) and the combine (56, 58); slot 63 = counts.
+// boundaries (slots 0-8), four stamps in each of the first 8 down units (24 + 4k: start, h staged, rows computed, end)
+// and the combine (56, 58); slot 63 = counts.
 #ifdef LOKI_TRACE
 constexpr int TRACE_SLOTS = 64;
 __device__ uint64_t g_trace[1024 * DW * TRACE_SLOTS];
@@ -310,166 +312,254 @@ __device__ __noinline__ void dispatch_wave(const DArgs & a, lds_t lds, int P) {
 }
 
 // ---------------------------------------------------------------- phase 3: gate/up tasks
-// Lane 4 r + q of a task reads row r of a 16-row set and blocks 4 jj + q; here rows r < 8 are gate rows and r >= 8 the
-// same h rows of the up matrix, so every lane streams from its own base address.
+// A task is 8 h rows of one pair-slot: lane 4 r + q reads row r of a 16-row set and blocks 4 jj + q (jj = the step,
+// 0..6); rows r < 8 are gate rows and r >= 8 the same h rows of the up matrix, so every lane streams from its own base
+// address. A task makes one pass over its weights per token (the second pass of a pair reads them from L2 again: two
+// tokens in one pass need more registers than the stream leaves). A wave runs its passes as one continuous stream: step
+// s of every pass uses register slot s, and the loads of the next pass's first steps are issued while the current pass
+// computes its last ones.
+struct Lane { int q, r; uint32_t tr; };
+
+struct GuTask {
+    const uint8_t * ql; const uint8_t * dl;   // this lane's qs / d address at step 0
+    int mi, s, c, row, u;                     // expert slot (act index or SH), first dispatch slot, tokens (1, 2), h row, pass
+};
+constexpr int GU_STEPS = GG::BPQ;             // 7
+constexpr size_t GU_QSTEP = 4 * 4096, GU_DSTEP = 4 * 128;   // 4 blocks per step (one per quad lane)
+
+// task tk of a wave's list: pre = the shared expert's pair-slots k = tk / NGU (tokens 2k, 2k + 1), else pair-slot
+// ps0 + tk / NGU of the routing table; false past the end (or for an invalid table entry, reported)
+__device__ __forceinline__ bool gu_task(const DArgs & a, lds_t lds, const Lane ln, int tk, int t_end, bool pre, int ps0, int P, int nact, GuTask & t) {
+    if (tk >= t_end) { return false; }
+    const RT rt(lds);
+    const int k = tk / NGU, hb = tk % NGU;
+    if (pre) {
+        t.mi = SH; t.s = P + 2 * k; t.c = a.n - 2 * k >= 2 ? 2 : 1;
+    } else {
+        const int sc = rt.ps_s[ps0 + k];
+        t.mi = rt.ps_mi[ps0 + k]; t.s = sc & 0xFFFF; t.c = sc >> 16;
+        if (!((t.mi == SH || (unsigned) t.mi < (unsigned) nact) && (t.c == 1 || t.c == 2) && t.s + t.c <= P + a.n)) { report(a.err, 32); return false; }
+    }
+    const bool routed = t.mi != SH;
+    const int e = routed ? rt.act_e[t.mi] : 0;
+    const uint8_t * gm = uniform_ptr(routed ? a.gate + (size_t) e * a.estride : a.sh_gate);
+    const uint8_t * um = uniform_ptr(routed ? a.up + (size_t) e * a.estride : a.sh_up);
+    const uint8_t * mat = ln.r >= 8 ? um : gm;
+    t.row = hb * GU_ROWS + (ln.r & 7); t.u = 0;
+    t.ql = mat + (size_t) (t.row >> 6) * GG::NB * 4096 + ln.q * 4096 + (t.row & 63) * 16;
+    t.dl = mat + (size_t) (DH / 64) * GG::NB * 4096 + (size_t) (t.row >> 6) * GG::NB * 128 + ln.q * 128 + (t.row & 63) * 2;
+    return true;
+}
+
 template <int PD>
-struct LaneStream {
-    static constexpr int STEPS = GG::BPQ, NR = PD + 1;
-    static constexpr size_t QSTEP = 4 * 4096, DSTEP = 4 * 128;   // 4 blocks per step (one per quad lane)
-    uint4 pf[NR][4]; uint16_t pd[NR];
-    __device__ __forceinline__ void issue(const uint8_t * ql, const uint8_t * dl, int s, int slot) {
+struct GuStream {
+    uint4 pf[GU_STEPS][4]; uint16_t pd[GU_STEPS];
+    __device__ __forceinline__ void issue(const GuTask & t, int s) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) { pf[slot][c] = load_nt(ql + s * QSTEP + c * 1024); }
-        pd[slot] = *gptr(reinterpret_cast<const uint16_t *>(dl + s * DSTEP));
+        for (int c = 0; c < 4; ++c) { pf[s][c] = load_nt(t.ql + s * GU_QSTEP + c * 1024); }
+        pd[s] = *gptr(reinterpret_cast<const uint16_t *>(t.dl + s * GU_DSTEP));
     }
-    __device__ __forceinline__ void prologue(const uint8_t * ql, const uint8_t * dl) {
-#pragma unroll
-        for (int k = 0; k < PD; ++k) { if (k < STEPS) { issue(ql, dl, k, k); } }
-    }
-    // row totals (before * 0.125) for T staged tokens xr[u], folded over the quad in block order
-    template <int T>
-    __device__ __forceinline__ void run(const uint8_t * ql, const uint8_t * dl, uint32_t tr, const uint8_t * const (&xr)[T], int q, float (&acc)[T]) {
+    // one pass (7 steps, one token xr): the row total before * 0.125, folded over the quad in block order; while step s
+    // computes, step s + PD of this pass or step s + PD - 7 of the next one (if any) is issued
+    __device__ __forceinline__ float pass(const GuTask & cur, const GuTask & nxt, bool has_next, uint32_t tr, const uint8_t * xr, int q, int r) {
 #pragma clang fp contract(off)
+        float acc = 0.f;
 #pragma unroll
-        for (int u = 0; u < T; ++u) { acc[u] = 0.f; }
-#pragma unroll
-        for (int s = 0; s < STEPS; ++s) {
-            const int k = s % NR;
-            if (s + PD < STEPS) { issue(ql, dl, s + PD, (s + PD) % NR); }
+        for (int s = 0; s < GU_STEPS; ++s) {
+            if (s + PD < GU_STEPS) { issue(cur, s + PD); } else if (has_next) { issue(nxt, s + PD - GU_STEPS); }
             const int j = s * 4 + q;
-            const uint8_t * xb[T];
-#pragma unroll
-            for (int u = 0; u < T; ++u) { xb[u] = xr[u] + j * GG::XBLK; }
-            int bsum[T];
-            block_bsum<T>(pf[k], tr, xb, bsum);
-            const float dw = h2f(pd[k]);
-#pragma unroll
-            for (int u = 0; u < T; ++u) {
-                const float dx = reinterpret_cast<const float *>(xr[u] + GG::NB * GG::XBLK)[j];
-                acc[u] = fold_quad(acc[u], (dw * dx) * (float) bsum[u]);
-            }
+            const int bsum = block_bsum_dpp(pf[s], tr, xr + j * GG::XBLK, r);
+            const float dx = reinterpret_cast<const float *>(xr + GG::NB * GG::XBLK)[j];
+            acc = fold_rows(acc, (h2f(pd[s]) * dx) * (float) bsum);
         }
+        return acc;
     }
 };
 
-struct Lane { int q, r; uint32_t tr; };
-
-// h rows hb * 8 .. hb * 8 + 7 of expert slot mi (act index, or SH) for the c (1 or 2) tokens at dispatch slots s, s + 1
-__device__ __forceinline__ void gate_up_task(const DArgs & a, lds_t lds, const Lane ln, int mi, int s, int c, int hb, int P) {
+// h = silu(g) * u of the task's rows for the pass's token: lanes 0..7 hold the gate totals of the 8 rows, lanes 8..15
+// the up totals (row_ror:8 brings them over)
+__device__ __forceinline__ void gu_publish(const DArgs & a, const Lane ln, const GuTask & t, float acc) {
 #pragma clang fp contract(off)
+    const float other = __builtin_bit_cast(float, dppi<0x128>(__builtin_bit_cast(int, acc)));
+    if (ln.q == 0 && ln.r < 8) { st_tag(a.th + (size_t) (t.s + t.u) * DH + t.row, a.epoch, det_silu(0.125f * acc) * (0.125f * other)); }
+}
+__device__ __forceinline__ const uint8_t * gu_xrow(const DArgs & a, lds_t lds, const GuTask & t, int P) {
     const RT rt(lds);
-    const bool routed = mi != SH;
-    const int e = routed ? rt.act_e[mi] : 0;
-    const bool up = ln.r >= 8;
-    const int row = hb * GU_ROWS + (ln.r & 7);
-    const uint8_t * gm = uniform_ptr(routed ? a.gate + (size_t) e * a.estride : a.sh_gate);
-    const uint8_t * um = uniform_ptr(routed ? a.up + (size_t) e * a.estride : a.sh_up);
-    const uint8_t * mat = up ? um : gm;
-    const uint8_t * ql = mat + (size_t) (row >> 6) * GG::NB * 4096 + ln.q * 4096 + (row & 63) * 16;
-    const uint8_t * dl = mat + (size_t) (DH / 64) * GG::NB * 4096 + (size_t) (row >> 6) * GG::NB * 128 + ln.q * 128 + (row & 63) * 2;
-    const bool writer = ln.q == 0 && !up;   // lane 4 r (r < 8) publishes h of its row
-    if (c == 2) {
-        LaneStream<GU2_PD> ls;
-        ls.prologue(ql, dl);
-        const uint8_t * xr[2];
+    const int slot = t.s + t.u;
+    return (const uint8_t *) (lds + L_XS + (t.mi != SH ? rt.perm[slot] / a.topk : slot - P) * GG::XROW);
+}
+
+// the wave's tasks tk, tk + tstep, .. < t_end (every token pass of each) as one stream; returns the number of passes
+template <int PD>
+__device__ __forceinline__ int gate_up_stream(const DArgs & a, lds_t lds, const Lane ln, int tk, int tstep, int t_end, bool pre, int ps0, int P, int nact) {
+    GuTask cur, nxt;
+    if (!gu_task(a, lds, ln, tk, t_end, pre, ps0, P, nact, cur)) { return 0; }
+    auto next_pass = [&](const GuTask & c0, GuTask & t) -> bool {   // the pair's second token, else the next task
+        if (c0.u + 1 < c0.c) { t = c0; t.u = c0.u + 1; return true; }
+        return gu_task(a, lds, ln, tk + tstep, t_end, pre, ps0, P, nact, t);
+    };
+    bool has_next = next_pass(cur, nxt);
+    GuStream<PD> st;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) { xr[u] = (const uint8_t *) (lds + L_XS + (routed ? rt.perm[s + u] / a.topk : s + u - P) * GG::XROW); }
-        float acc[2];
-        ls.run<2>(ql, dl, ln.tr, xr, ln.q, acc);
+    for (int s = 0; s < PD; ++s) { st.issue(cur, s); }
+    int npass = 0;
+    for (;;) {
+        const float acc = st.pass(cur, nxt, has_next, ln.tr, gu_xrow(a, lds, cur, P), ln.q, ln.r);
+        gu_publish(a, ln, cur, acc);
+        ++npass;
+        if (!has_next) { break; }
+        if (nxt.u == 0) { tk += tstep; }
+        cur = nxt;
+        has_next = next_pass(cur, nxt);
+    }
+    return npass;
+}
+
+// The shared expert's single pair-slot as early work (n <= 2, one task per workgroup): the waves without a token split
+// the task's 7 steps (step s on wave n + s % (DW - n)), each lane's block terms go to LDS, and the last of those waves
+// folds them in block order and publishes h -- the arithmetic of a pass, finished while the routing is still running.
+__device__ __forceinline__ void pre_shared_split(const DArgs & a, lds_t lds, const Lane ln, int wave, int P, LK_LOCAL unsigned * cnt) {
+#pragma clang fp contract(off)
+    const int nw = DW - a.n, lane = lane_id();
+    GuTask t;
+    if (!gu_task(a, lds, ln, blockIdx.x, NGU, true, 0, P, 0, t)) { return; }
+    LK_LOCAL float * terms = reinterpret_cast<LK_LOCAL float *>(lds + L_PRE);   // [u][step][lane]
+    const uint8_t * xr0 = gu_xrow(a, lds, t, P);
+    GuTask t1 = t; t1.u = 1;
+    const uint8_t * xr1 = t.c == 2 ? gu_xrow(a, lds, t1, P) : xr0;
+    for (int s = wave - a.n; s < GU_STEPS; s += nw) {
+        uint4 pf[4];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const float other = __shfl_xor(acc[u], 32);   // the up row total, to the gate row's lanes
-            if (writer) { st_tag(a.th + (size_t) (s + u) * DH + row, a.epoch, det_silu(0.125f * acc[u]) * (0.125f * other)); }
+        for (int c = 0; c < 4; ++c) { pf[c] = load_nt(t.ql + s * GU_QSTEP + c * 1024); }
+        const float dw = h2f(*gptr(reinterpret_cast<const uint16_t *>(t.dl + s * GU_DSTEP)));
+        const int j = s * 4 + ln.q;
+        for (int u = 0; u < t.c; ++u) {   // both tokens from one load
+            const uint8_t * xr = u ? xr1 : xr0;
+            const int bsum = block_bsum_dpp(pf, ln.tr, xr + j * GG::XBLK, ln.r);
+            const float dx = reinterpret_cast<const float *>(xr + GG::NB * GG::XBLK)[j];
+            terms[(u * GU_STEPS + s) * 64 + lane] = (dw * dx) * (float) bsum;
         }
-    } else {
-        LaneStream<GU1_PD> ls;
-        ls.prologue(ql, dl);
-        const uint8_t * xr[1] = { (const uint8_t *) (lds + L_XS + (routed ? rt.perm[s] / a.topk : s - P) * GG::XROW) };
-        float acc[1];
-        ls.run<1>(ql, dl, ln.tr, xr, ln.q, acc);
-        const float other = __shfl_xor(acc[0], 32);
-        if (writer) { st_tag(a.th + (size_t) s * DH + row, a.epoch, det_silu(0.125f * acc[0]) * (0.125f * other)); }
+    }
+    if (!lds_arrive(cnt, (unsigned) nw)) { return; }
+    for (int u = 0; u < t.c; ++u) {
+        float acc = 0.f;
+#pragma unroll
+        for (int s = 0; s < GU_STEPS; ++s) { acc = fold_rows(acc, terms[(u * GU_STEPS + s) * 64 + lane]); }
+        gu_publish(a, ln, u ? t1 : t, acc);
     }
 }
 
 // ---------------------------------------------------------------- phase 4: down units
-// Wave w of the unit's workgroup owns output rows rg * 256 + 32 w .. + 31 (two 16-row sets of one 64-row group) and
-// stages Q8_K block w of h for the unit's c (1 or 2) tokens at slots s, s + 1. The first poll of h is issued before the
-// weight loads, so its wait does not include them. Returns false if a wait timed out (the unit is skipped).
-__device__ __forceinline__ bool down_unit(const DArgs & a, lds_t lds, const Lane ln, int wave, int mi, int s, int c, int rg, int P, int tb) {
-#pragma clang fp contract(off)
-    const RT rt(lds);
-    const bool routed = mi != SH;
-    const int e = routed ? rt.act_e[mi] : 0;
-    const uint8_t * base = uniform_ptr(routed ? a.down + (size_t) e * a.estride : a.sh_down);
-    const int g64 = rg * (DN_ROWS / 64) + (wave >> 1), sub = (wave & 1) * 2;
-    const uint8_t * qb = base + (size_t) g64 * GD::NB * 4096 + sub * 256;
-    const uint8_t * db = base + (size_t) (DE / 64) * GD::NB * 4096 + (size_t) g64 * GD::NB * 128 + sub * 32;
-    const uint32_t lq = (uint32_t) ln.q * 4096 + 16 * ln.r, ld = (uint32_t) ln.q * 128 + 2 * ln.r;
+// A unit is row group rg (256 output rows) of one pair-slot: wave w owns rows rg * 256 + 32 w .. + 31 (two 16-row sets of
+// one 64-row group) and stages Q8_K block w of h for the unit's c (1 or 2) tokens at slots s, s + 1. The units of a
+// workgroup form a pipeline: the h words of the next unit are requested before the current one computes, and the staged
+// h alternates between two LDS buffers, so one barrier per unit suffices.
+struct DnUnit { int mi, s, c, rg; };
+__device__ __forceinline__ bool dn_unit(const RT & rt, int u, int nps, int nact, int P, int n, DnUnit & d) {
+    const int ps = u % nps, mi = rt.ps_mi[ps], sc = rt.ps_s[ps];
+    d.mi = mi; d.s = sc & 0xFFFF; d.c = sc >> 16; d.rg = u / nps;
+    return (mi == SH || (unsigned) mi < (unsigned) nact) && (d.c == 1 || d.c == 2) && d.s + d.c <= P + n;
+}
+__device__ __forceinline__ void dn_h_issue(const DArgs & a, int wave, const DnUnit & d, uint64_t (&w)[2][4]) {
     const int lane = lane_id();
-    uint64_t w[2][4];
-    auto issue_h = [&]() {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            if (u < c) {
-                const uint64_t * src = a.th + (size_t) (s + u) * DH + wave * QK + 4 * lane;
+    for (int u = 0; u < 2; ++u) {
+        if (u < d.c) {
+            const uint64_t * src = a.th + (size_t) (d.s + u) * DH + wave * QK + 4 * lane;
 #pragma unroll
-                for (int k = 0; k < 4; ++k) { w[u][k] = ld_tag(src + k); }
-            }
+            for (int k = 0; k < 4; ++k) { w[u][k] = ld_tag(src + k); }
         }
-    };
-    issue_h();
-    RowStream<GD::BPQ, 2, DN_PD> rs;
-    rs.prologue(qb, db, lq, ld);   // the weights do not depend on h: in flight during the wait
+    }
+}
+// completes the poll (re-requesting until every word carries the epoch), then Q8_K of block `wave` into buffer hs
+__device__ __forceinline__ bool dn_h_stage(const DArgs & a, int wave, const DnUnit & d, uint64_t (&w)[2][4], lds_t hs) {
+    const int lane = lane_id();
     int it = 0;
     for (; it < POLL_MAX; ++it) {
         bool v = true;
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) { v = v && (u >= c || tag_ok(w[u][k], a.epoch)); }
+            for (int k = 0; k < 4; ++k) { v = v && (u >= d.c || tag_ok(w[u][k], a.epoch)); }
         }
         if (__ballot(!v) == 0) { break; }
         __builtin_amdgcn_s_sleep(1);
-        issue_h();
+        dn_h_issue(a, wave, d, w);
     }
-    const bool ok = it < POLL_MAX;
-    if (ok) {
+    if (it == POLL_MAX) { return false; }
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            if (u < c) {
-                const float xs[4] = { tag_val(w[u][0]), tag_val(w[u][1]), tag_val(w[u][2]), tag_val(w[u][3]) };
-                float d; const uint32_t packed = q8k_lane(xs, d);
-                lds_t hrow = lds + L_HS + u * GD::XROW;
-                *reinterpret_cast<LK_LOCAL uint32_t *>(hrow + wave * GD::XBLK + staged_word(lane)) = packed;
-                if (lane == 0) { reinterpret_cast<LK_LOCAL float *>(hrow + GD::NB * GD::XBLK)[wave] = d; }
-            }
+    for (int u = 0; u < 2; ++u) {
+        if (u < d.c) {
+            const float xs[4] = { tag_val(w[u][0]), tag_val(w[u][1]), tag_val(w[u][2]), tag_val(w[u][3]) };
+            float dq; const uint32_t packed = q8k_lane(xs, dq);
+            lds_t hrow = hs + u * GD::XROW;
+            *reinterpret_cast<LK_LOCAL uint32_t *>(hrow + wave * GD::XBLK + staged_word(lane)) = packed;
+            if (lane == 0) { reinterpret_cast<LK_LOCAL float *>(hrow + GD::NB * GD::XBLK)[wave] = dq; }
         }
     }
-    // every wave's staging succeeded (no __syncthreads_and: its static LDS word would move the 64 KB aligned tables)
-    LK_LOCAL unsigned * wok = reinterpret_cast<LK_LOCAL unsigned *>(lds + L_CTL) + 4;
-    if (lane == 0) { wok[wave] = ok ? 1u : 0u; }
-    __syncthreads();
-    bool all_ok = true;
+    return true;
+}
+
+// the workgroup's units blockIdx.x, + G, .. < nps * NDN; returns the number of units run
+__device__ __forceinline__ int down_phase(const DArgs & a, lds_t lds, const Lane ln, int wave, int nps, int nact, int P) {
+#pragma clang fp contract(off)
+    const RT rt(lds);
+    const int G = gridDim.x, total = nps * NDN;
+    int u = blockIdx.x;
+    if (u >= total) { return 0; }
+    DnUnit cur, nxt;
+    bool cur_ok = dn_unit(rt, u, nps, nact, P, a.n, cur);
+    uint64_t w[2][4];
+    if (cur_ok) { dn_h_issue(a, wave, cur, w); }
+    LK_LOCAL unsigned * wok = reinterpret_cast<LK_LOCAL unsigned *>(lds + L_CTL) + 8;   // [2][DW] per-wave staging results
+    const uint32_t lq = (uint32_t) ln.q * 4096 + 16 * ln.r, ld = (uint32_t) ln.q * 128 + 2 * ln.r;
+    int k = 0;
+    for (;;) {
+#ifdef LOKI_TRACE
+        const int tb = k < 8 ? 24 + 4 * k : -1;
+#else
+        const int tb = -1;
+#endif
+        TRACE_T(tb, 0);
+        const int e = cur_ok && cur.mi != SH ? rt.act_e[cur.mi] : 0;
+        const uint8_t * base = uniform_ptr(cur.mi != SH ? a.down + (size_t) e * a.estride : a.sh_down);
+        const int g64 = cur.rg * (DN_ROWS / 64) + (wave >> 1), sub = (wave & 1) * 2;
+        const uint8_t * qb = base + (size_t) g64 * GD::NB * 4096 + sub * 256;
+        const uint8_t * db = base + (size_t) (DE / 64) * GD::NB * 4096 + (size_t) g64 * GD::NB * 128 + sub * 32;
+        RowStream<GD::BPQ, 2, DN_PD> rs;
+        if (cur_ok) { rs.prologue(qb, db, lq, ld); }   // the weights do not depend on h: in flight during the wait
+        const lds_t hs = lds + L_HS + (k & 1) * 2 * GD::XROW;
+        const bool ok = cur_ok && dn_h_stage(a, wave, cur, w, hs);
+        if (lane_id() == 0) { wok[(k & 1) * DW + wave] = ok ? 1u : 0u; }
+        __syncthreads();   // the unit's h is staged; every wave has left the unit before last (its buffer is free)
+        bool all_ok = true;
 #pragma unroll
-    for (int w2 = 0; w2 < DW; ++w2) { all_ok = all_ok && wok[w2] != 0u; }
-    TRACE_T(tb, 1);
-    if (all_ok) {
-        // one token per pass: the second pass re-reads the unit's weights from L2
-        for (int i = 0; i < c; ++i) {
-            if (i > 0) { rs.prologue(qb, db, lq, ld); }
-            const uint8_t * xr[1] = { (const uint8_t *) (lds + L_HS + i * GD::XROW) };
-            float acc[2][1];
-            rs.run<1, GD>(qb, db, lq, ld, ln.tr, xr, ln.q, acc);
-            if (ln.q == 0) {
+        for (int w2 = 0; w2 < DW; ++w2) { all_ok = all_ok && wok[(k & 1) * DW + w2] != 0u; }
+        TRACE_T(tb, 1);
+        const bool more = u + G < total;
+        const bool nxt_ok = more && dn_unit(rt, u + G, nps, nact, P, a.n, nxt);
+        if (nxt_ok) { dn_h_issue(a, wave, nxt, w); }
+        if (all_ok) {
+            // one token per pass: the second pass re-reads the unit's weights from L2
+            for (int i = 0; i < cur.c; ++i) {
+                if (i > 0) { rs.prologue(qb, db, lq, ld); }
+                float acc[2];
+                rs.run_dpp<GD>(qb, db, lq, ld, ln.tr, (const uint8_t *) (hs + i * GD::XROW), ln.q, ln.r, acc);
+                if (ln.q == 0) {
 #pragma unroll
-                for (int r2 = 0; r2 < 2; ++r2) { st_tag(a.to + (size_t) (s + i) * DE + rg * DN_ROWS + wave * 32 + r2 * 16 + ln.r, a.epoch, 0.125f * acc[r2][0]); }
+                    for (int r2 = 0; r2 < 2; ++r2) { st_tag(a.to + (size_t) (cur.s + i) * DE + cur.rg * DN_ROWS + wave * 32 + r2 * 16 + ln.r, a.epoch, 0.125f * acc[r2]); }
+                }
             }
+        } else {
+            report(a.err, 1);
         }
+        TRACE_T(tb, 2);
+        TRACE_T(tb, 3);
+        ++k;
+        if (!more) { break; }
+        u += G; cur = nxt; cur_ok = nxt_ok;
     }
-    TRACE_T(tb, 2);
-    __syncthreads();   // the staged h is overwritten by the next unit
-    return all_ok;
+    return k;
 }
 
 // ---------------------------------------------------------------- phase 5: combine
@@ -517,15 +607,17 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
     const lds_t lds = (lds_t) dyn_lds;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
     const int G = gridDim.x, n = a.n, P = n * a.topk;
-    LK_LOCAL unsigned * ctl = reinterpret_cast<LK_LOCAL unsigned *>(lds + L_CTL);   // [1] selections done, [2] routing ready (1 ok, 2 failed), [3] a wait failed
+    // [0] waves with tokens and tables staged, [1] selections done, [2] routing ready (1 ok, 2 failed), [3] a wait failed,
+    // [4] early shared task: waves done
+    LK_LOCAL unsigned * ctl = reinterpret_cast<LK_LOCAL unsigned *>(lds + L_CTL);
     Lane ln;
-    ln.r = lane >> 2; ln.q = lane & 3;
+    ln.r = lane & 15; ln.q = lane >> 4;   // lane 16 q + r: row r, block quarter q
     ln.tr = lds_addr(dyn_lds) | ((uint32_t) (lane & 15) << 3);   // table base (64 KB aligned: the tables open the LDS) | replica
 
     // 1. table copy in flight; router (the whole workgroup)
     TRACE(wave, 0);
     if (lds_addr(dyn_lds) & 0xFFFFu) { report(a.err, 4); return; }   // table addressing needs a 64 KB aligned base
-    if (threadIdx.x < 4) { ctl[threadIdx.x] = 0; }
+    if (threadIdx.x < 8) { ctl[threadIdx.x] = 0; }
     tables_dma(lds, a.tab, wave);
     __syncthreads();   // the hand-off words are clear
     for (int e = blockIdx.x; e < a.n_exp; e += G) { router_phase(a, lds, wave, e); }
@@ -563,10 +655,10 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
             TRACE(wave, 6);
         }
     } else if (pre && lds_wait_count(ctl + 0, DW)) {   // the shared expert's pair-slots k: tokens 2k, 2k + 1
-        const int nsh = (n + 1) >> 1;
-        for (int tk = (wave - n) * G + blockIdx.x; tk < nsh * NGU; tk += (DW - n) * G) {
-            const int k = tk / NGU;
-            gate_up_task(a, lds, ln, SH, P + 2 * k, n - 2 * k >= 2 ? 2 : 1, tk % NGU, P);
+        if (n <= 2 && G >= NGU) {
+            if (blockIdx.x < NGU) { pre_shared_split(a, lds, ln, wave, P, ctl + 4); }
+        } else {
+            gate_up_stream<GU_PD>(a, lds, ln, (wave - n) * G + blockIdx.x, (DW - n) * G, ((n + 1) >> 1) * NGU, true, 0, P, 0);
         }
     }
     const unsigned ready = lds_wait(ctl + 2);
@@ -579,35 +671,12 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
     const RT rt(lds);
     const int nact = *rt.nact, nps = *rt.nps, ps0 = pre ? (n + 1) >> 1 : 0;
     const int t_gu = (nps - ps0) * NGU;
-    int ntask = 0;
-    for (int tk = wave * G + blockIdx.x; tk < t_gu; tk += G * DW) {
-        if (ntask < 8) { TRACE(wave, 8 + 2 * ntask); }
-        const int ps = ps0 + tk / NGU, mi = rt.ps_mi[ps], sc = rt.ps_s[ps];
-        if ((mi == SH || (unsigned) mi < (unsigned) nact) && (sc & 0xFFFF) + (sc >> 16) <= P + n) {
-            gate_up_task(a, lds, ln, mi, sc & 0xFFFF, sc >> 16, tk % NGU, P);
-        } else {
-            report(a.err, 32);
-        }
-        if (ntask < 8) { TRACE(wave, 9 + 2 * ntask); }
-        ++ntask;
-    }
+    TRACE(wave, 8);
+    const int ntask = gate_up_stream<GU_PD>(a, lds, ln, wave * G + blockIdx.x, G * DW, t_gu, false, ps0, P, nact);
     TRACE(wave, 7);
 
     // 4. down units (pair-slot, 256 rows), round-robin over the workgroups: unit u = row group u / nps of pair-slot u % nps
-    int nunit = 0;
-    for (int u = blockIdx.x; u < nps * NDN; u += G) {
-        const int ps = u % nps, mi = rt.ps_mi[ps], sc = rt.ps_s[ps];
-#ifdef LOKI_TRACE
-        const int tb = nunit < 8 ? 24 + 4 * nunit : -1;
-#else
-        const int tb = -1;
-#endif
-        TRACE_T(tb, 0);
-        const bool valid = (mi == SH || (unsigned) mi < (unsigned) nact) && (sc & 0xFFFF) + (sc >> 16) <= P + n;   // uniform in the workgroup
-        if (!valid || !down_unit(a, lds, ln, wave, mi, sc & 0xFFFF, sc >> 16, u / nps, P, tb)) { report(a.err, 1); }
-        TRACE_T(tb, 3);
-        ++nunit;
-    }
+    const int nunit = down_phase(a, lds, ln, wave, nps, nact, P);
 
     // 5. combine units on the last workgroups
     for (int cu = G - 1 - blockIdx.x; cu < NDN; cu += G) {

@@ -314,6 +314,78 @@ __device__ __forceinline__ float fold_quad(float acc, float t) {
     return acc + quad_bcast<3>(t);
 }
 
+// ---------------------------------------------------------------- the same product with the activations in registers
+// Lane layout 16 q + r (q = block quarter, r = row): the 16 lanes of a DPP row share one activation block, so each lane
+// holds 4 of its 64 dwords (dwords 4r .. 4r + 3 of the staged block) and every dot product reads its dword by
+// row_newbcast from the lane that holds it -- one LDS read per block instead of 16. Staged dword 16 L + 2 ib + hi
+// (group L, sub-block ib, weights 0..3 / 4..7) lives in lane 4 L + ib / 2, register 2 (ib & 1) + hi.
+template <int CTRL> __device__ __forceinline__ int dppi(int v) { return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false); }
+template <int L, int IB>
+__device__ __forceinline__ void dot_ib_dpp(const uint2 (&g)[8], const uint4 (&m)[8], const uint32_t (&xq)[4], int (&acc)[8]) {
+    if constexpr (IB < 8) {
+        uint32_t lo, hi; iq2_apply(g[IB], m[IB], lo, hi);
+        constexpr int SRC = 4 * L + IB / 2;
+        acc[IB] = __builtin_amdgcn_sdot4(dppi<0x150 + SRC>((int) xq[2 * (IB & 1)]), (int) lo, acc[IB], false);
+        acc[IB] = __builtin_amdgcn_sdot4(dppi<0x150 + SRC>((int) xq[2 * (IB & 1) + 1]), (int) hi, acc[IB], false);
+        dot_ib_dpp<L, IB + 1>(g, m, xq, acc);
+    }
+}
+template <int L>
+__device__ __forceinline__ void group_step_dpp(const uint4 (&w)[4], uint32_t tr, const uint32_t (&xq)[4], int (&acc)[8]) {
+    const uint32_t trs = (tr & ~255u) | 128u | ((tr & 0x38u) << 1);
+    uint2 g[8]; uint4 m[8];
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) {
+        const uint4 c = w[ib >> 1];
+        g[ib] = tab_grid<L>((ib & 1) ? c.z : c.x, tr);
+        m[ib] = tab_sign<L>((ib & 1) ? c.w : c.y, trs);
+    }
+    dot_ib_dpp<L, 0>(g, m, xq, acc);
+}
+// block_bsum for one token whose staged block is xb (this lane reads its 16 bytes at xb + 16 r)
+__device__ __forceinline__ int block_bsum_dpp(const uint4 (&w)[4], uint32_t tr, const uint8_t * xb, int r) {
+    const u32x4 xv = *(const LK_LOCAL u32x4 *) (size_t) lds_addr(xb + 16 * r);
+    const uint32_t xq[4] = { xv.x, xv.y, xv.z, xv.w };
+    int acc[8];
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) { acc[ib] = 0; }
+    group_step_dpp<0>(w, tr, xq, acc);
+    group_step_dpp<1>(w, tr, xq, acc);
+    group_step_dpp<2>(w, tr, xq, acc);
+    group_step_dpp<3>(w, tr, xq, acc);
+    int s = 0;
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) {   // |acc| <= 32 * 43 * 127 < 2^23: the 24-bit multiply is exact
+        const uint4 c = w[ib >> 1];
+        s += __mul24(acc[ib], iq2_scale((ib & 1) ? c.w : c.y));
+    }
+    return s;
+}
+// lanes 16 q + r hold the terms of blocks 4 jj + q of row r: lanes 0..15 add the four in block order (lanes 16..63 are
+// left with partial values). v_permlane16_swap v, z exchanges v's rows 1 and 3 with z's rows 0 and 2, so z then holds
+// v's lanes 16..31 in lanes 0..15; v_permlane32_swap v, z exchanges v's lanes 32..63 with z's lanes 0..31. Written as
+// inline assembly so that which register receives which half is fixed (s_nop 1: the wait states a VALU result needs
+// before a permlane reads it).
+__device__ __forceinline__ uint32_t lanes_16_31(uint32_t v) {
+    uint32_t z = 0;
+    __asm__ volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(v), "+v"(z));
+    return z;
+}
+__device__ __forceinline__ uint32_t lanes_32_63(uint32_t v) {
+    uint32_t z = 0;
+    __asm__ volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(v), "+v"(z));
+    return z;
+}
+__device__ __forceinline__ float fold_rows(float acc, float t) {
+#pragma clang fp contract(off)
+    const uint32_t b = __builtin_bit_cast(uint32_t, t);
+    const uint32_t hi = lanes_32_63(b);   // lanes 0..15: q = 2, lanes 16..31: q = 3
+    acc = acc + t;
+    acc = acc + __builtin_bit_cast(float, lanes_16_31(b));
+    acc = acc + __builtin_bit_cast(float, hi);
+    return acc + __builtin_bit_cast(float, lanes_16_31(hi));
+}
+
 // ---------------------------------------------------------------- streaming RPL x 16 rows of one matrix
 // Steps s = 0 .. RPL * BPQ - 1: row set s / BPQ (16 rows each, 256 B apart in a tiled chunk), block step jj = s % BPQ.
 // qb / db: uniform qs / d bases of the task's first row set at jj = 0; lq / ld: the lane's part of its addresses.
@@ -365,6 +437,31 @@ struct RowStream {
 #pragma unroll
                         for (int r2 = 0; r2 < RPL; ++r2) { if (r2 == rs) { acc[r2][u] = fold_quad(acc[r2][u], t); } }
                     }
+                }
+            }
+        }
+    }
+    // the same for one token with the activations in registers (lane layout 16 q + r; totals valid in lanes 0..15)
+    template <class G>
+    __device__ __forceinline__ void run_dpp(const uint8_t * qb, const uint8_t * db, uint32_t lq, uint32_t ld, uint32_t tr,
+                                            const uint8_t * xr, int q, int r, float (&acc)[RPL]) {
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int rs = 0; rs < RPL; ++rs) { acc[rs] = 0.f; }
+#pragma unroll 1
+        for (int s0 = 0; s0 < STEPS; s0 += NR) {
+#pragma unroll
+            for (int k = 0; k < NR; ++k) {
+                const int s = s0 + k;
+                if (s < STEPS) {
+                    if (s + PD < STEPS) { issue(qb, db, lq, ld, s + PD, (k + PD) % NR); }
+                    const int j = (s % BPQ) * 4 + q;
+                    const int bsum = block_bsum_dpp(pf[k], tr, xr + j * G::XBLK, r);
+                    const float dx = reinterpret_cast<const float *>(xr + G::NB * G::XBLK)[j];
+                    const float t = (h2f(pd[k]) * dx) * (float) bsum;
+                    const int rs = s / BPQ;
+#pragma unroll
+                    for (int r2 = 0; r2 < RPL; ++r2) { if (r2 == rs) { acc[r2] = fold_rows(acc[r2], t); } }
                 }
             }
         }
