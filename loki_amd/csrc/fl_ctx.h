@@ -50,7 +50,7 @@ struct FLCtx {
     DBuf<float> terms; DBuf<unsigned> cnt;   // per-pass expert kernels: (unused) term scratch, self-resetting counters
     DBuf<uint4> tab;                         // LDS table image (build_table_image)
     // single-launch decode block: epoch-tagged logits / h / o, wait-timeout word; fused = 0 forces the per-pass kernels
-    DBuf<int> derr; DBuf<uint64_t> dlogit, dth, dto; unsigned epoch = 0; int fused = 1; int dec_grid = -1;
+    DBuf<int> derr; DBuf<uint64_t> dlogit, dtxq, dth, dto; unsigned epoch = 0; int fused = 1; int dec_grid = -1;
     struct Compat * compat = nullptr;          // reference-API state (compat.hip), created on first use
 };
 static const int NSTAGE = 6;   // quant_x, router_logits, router_select, dispatch, gate_up (+SwiGLU, Q8_K(h)), down (+combine)

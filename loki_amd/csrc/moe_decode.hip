@@ -7,8 +7,9 @@
 //   1. on entry every workgroup starts the direct global->LDS copy of the codebook/sign table image; workgroup b then
 //      computes the router logits of expert b for every token (the fp64 chunk-and-tree contract) and publishes each
 //      probability sigmoid(logit) as an epoch-tagged 64-bit word;
-//   2. wave t of every workgroup issues its poll of token t's tagged probabilities, all waves quantise the n token rows
-//      to Q8_K into LDS, then wave t selects token t's experts and the last selecting wave builds the dispatch (stable
+//      Each token block is quantised to Q8_K once (by one workgroup) and published as epoch-tagged words;
+//   2. wave t of every workgroup issues its poll of token t's tagged probabilities, all waves gather the Q8_K token
+//      blocks into LDS, then wave t selects token t's experts and the last selecting wave builds the dispatch (stable
 //      counting sort of the n * topk pairs) in its own LDS -- redundant, but cheaper than another device-wide hand-off.
 //      Waves without a token meanwhile run the shared expert's gate/up tasks (no routing needed);
 //   3. gate/up tasks round-robin over all waves of the grid: a task computes 8 gate rows and the same 8 up rows of one
@@ -38,7 +39,7 @@ constexpr int GU_ROWS = 8;             // h rows per gate/up task (8 gate + the 
 constexpr int NGU = DH / GU_ROWS;      // gate/up tasks per expert
 constexpr int DN_ROWS = DW * 32;       // output rows per down unit (32 per wave: two row sets of 16)
 constexpr int NDN = DE / DN_ROWS;      // down units per expert (= combine units)
-constexpr int GU_PD = 3, DN_PD = 2;   // blocks in flight per lane
+constexpr int GU_PD = 3, DN_PD = 3;   // blocks in flight per lane
 static_assert(DH == DW * QK, "a down unit's wave w quantises h block w");
 static_assert(DMAX_N * (MAXK + 1) * DH <= (int) DEC_TH && DMAX_N * (MAXK + 1) * DE <= (int) DEC_TO, "tagged buffer sizes");
 
@@ -118,8 +119,8 @@ __device__ __forceinline__ const uint8_t * uniform_ptr(const uint8_t * p) {
 }
 
 // Timeline probe for tuning builds (-DLOKI_TRACE): per wave, 64-bit s_memrealtime stamps (100 MHz) at the phase
-// boundaries (slots 0-8), four stamps in each of the first 8 down units (24 + 4k: start, h staged, rows computed, end)
-// and the combine (56, 58); slot 63 = counts.
+// boundaries (slots 0-8), the down phase (24: start, 25: h staged, 26: rows computed) and the combine (56, 58);
+// slot 63 = counts.
 #ifdef LOKI_TRACE
 constexpr int TRACE_SLOTS = 64;
 __device__ uint64_t g_trace[1024 * DW * TRACE_SLOTS];
@@ -149,34 +150,59 @@ __device__ __forceinline__ void tables_dma(lds_t lds, const uint4 * img, int wav
     }
 }
 
-// Q8_K of the token rows into LDS (staged layout)
-__device__ __forceinline__ void quant_tokens(const DArgs & a, lds_t lds, int wave) {
-    const int lane = lane_id(), nblk = a.n * GG::NB;
-    constexpr int B = 14;   // blocks per batch: their loads are all issued before the first is used
-    for (int b0 = wave; b0 < nblk; b0 += DW * B) {
-        float4 v[B];
+// Q8_K of the token blocks k = t * NB + j: block k by workgroup k % G (wave k / G % DW), published as 65 epoch-tagged
+// words (word l = the 4 packed int8 of values 4l .. 4l + 3, word 64 = the scale); the quantising workgroup also writes
+// the layer's xq / xd
+__device__ __forceinline__ void quant_publish(const DArgs & a, int wave) {
+    const int G = gridDim.x, nblk = a.n * GG::NB, lane = lane_id();
+    for (int k = blockIdx.x + G * wave; k < nblk; k += G * DW) {
+        const int t = k / GG::NB, j = k % GG::NB;
+        const float4 v = gloadf4(a.x + (size_t) t * DE + (size_t) j * QK + 4 * lane);
+        const float xs[4] = { v.x, v.y, v.z, v.w };
+        float d; const uint32_t packed = q8k_lane(xs, d);
+        st_tag(a.txq + (size_t) k * 65 + lane, a.epoch, __builtin_bit_cast(float, packed));
+        if (lane == 0) { st_tag(a.txq + (size_t) k * 65 + 64, a.epoch, d); }
+        gptr(reinterpret_cast<uint32_t *>(a.xq + (size_t) t * DE + (size_t) j * QK))[lane] = packed;
+        if (lane == 0) { gptr(a.xd)[k] = d; }
+    }
+}
+// every token block into this workgroup's LDS (staged layout): wave w gathers blocks w, w + DW, .., up to GB at a time;
+// false if a wait timed out
+__device__ __forceinline__ bool gather_tokens(const DArgs & a, lds_t lds, int wave) {
+    constexpr int GB = 14;
+    const int nblk = a.n * GG::NB, lane = lane_id();
+    for (int k0 = wave; k0 < nblk; k0 += DW * GB) {
+        uint64_t wq[GB], wd[GB];
+        auto issue = [&]() {
 #pragma unroll
-        for (int k = 0; k < B; ++k) {
-            const int b = b0 + k * DW;
-            if (b < nblk) { v[k] = gloadf4(a.x + (size_t) (b / GG::NB) * DE + (size_t) (b % GG::NB) * QK + 4 * lane); }
+            for (int b = 0; b < GB; ++b) {
+                const int k = k0 + b * DW;
+                if (k < nblk) { wq[b] = ld_tag(a.txq + (size_t) k * 65 + lane); wd[b] = ld_tag(a.txq + (size_t) k * 65 + 64); }
+            }
+        };
+        issue();
+        int it = 0;
+        for (; it < POLL_MAX; ++it) {
+            bool v = true;
+#pragma unroll
+            for (int b = 0; b < GB; ++b) { v = v && (k0 + b * DW >= nblk || (tag_ok(wq[b], a.epoch) && tag_ok(wd[b], a.epoch))); }
+            if (__ballot(!v) == 0) { break; }
+            __builtin_amdgcn_s_sleep(1);
+            issue();
         }
+        if (it == POLL_MAX) { return false; }
 #pragma unroll
-        for (int k = 0; k < B; ++k) {
-            const int b = b0 + k * DW;
-            if (b < nblk) {
-                const int t = b / GG::NB, j = b % GG::NB;
-                const float xs[4] = { v[k].x, v[k].y, v[k].z, v[k].w };
-                float d; const uint32_t packed = q8k_lane(xs, d);
-                lds_t row = lds + L_XS + t * GG::XROW;
-                *reinterpret_cast<LK_LOCAL uint32_t *>(row + j * GG::XBLK + staged_word(lane)) = packed;
-                if (lane == 0) { reinterpret_cast<LK_LOCAL float *>(row + GG::NB * GG::XBLK)[j] = d; }
-                if (blockIdx.x == 0) {   // the layer's xq / xd
-                    gptr(reinterpret_cast<uint32_t *>(a.xq + (size_t) t * DE + (size_t) j * QK))[lane] = packed;
-                    if (lane == 0) { gptr(a.xd)[(size_t) t * GG::NB + j] = d; }
-                }
+        for (int b = 0; b < GB; ++b) {
+            const int k = k0 + b * DW;
+            if (k < nblk) {
+                lds_t row = lds + L_XS + (k / GG::NB) * GG::XROW;
+                const int j = k % GG::NB;
+                *reinterpret_cast<LK_LOCAL uint32_t *>(row + j * GG::XBLK + staged_word(lane)) = (uint32_t) wq[b];
+                if (lane == 0) { reinterpret_cast<LK_LOCAL float *>(row + GG::NB * GG::XBLK)[j] = tag_val(wd[b]); }
             }
         }
     }
+    return true;
 }
 
 // Router logits of expert e for all n tokens by the whole workgroup (the contract of moe_device.h: 256 in-order chunk
@@ -259,32 +285,30 @@ __device__ __forceinline__ bool probs_wait(const DArgs & a, int t, uint64_t (&w)
 }
 
 // dispatch of the n * topk pairs (one wave): stable counting sort by expert,
-// pos(i) = #{pairs with a lower expert} + #{earlier pairs with the same expert}
+// pos(i) = #{pairs with a lower expert} + #{earlier pairs with the same expert}. Lane i holds pair i; comparing the
+// expert ids bit by bit from the top with ballots gives every lane the mask of lanes with a smaller id and the mask of
+// lanes with the same id (8 bits: ids < NEXP_MAX = 256).
 __device__ __noinline__ void dispatch_wave(const DArgs & a, lds_t lds, int P) {
     const RT rt(lds);
     const int lane = lane_id();
     const bool valid = lane < P;
-    const int e = valid ? rt.sel[lane] : -1;
-    uint64_t match = __ballot(valid);
+    const int e = valid ? rt.sel[lane] : 0;
+    uint64_t eq = __ballot(valid), lt = 0;
 #pragma unroll
-    for (int b = 0; b < 9; ++b) {
-        const bool bit = valid && ((e >> b) & 1);
-        const uint64_t ones = __ballot(bit);
-        match &= bit ? ones : ~ones;
+    for (int b = 7; b >= 0; --b) {
+        const bool bit = (e >> b) & 1;
+        const uint64_t ones = __ballot(valid && bit);
+        if (bit) { lt |= eq & ~ones; }
+        eq &= bit ? ones : ~ones;
     }
     const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-    const int rank = __popcll(match & below);
+    const int rank = __popcll(eq & below);
     const uint64_t first = __ballot(valid && rank == 0);
-    int less = 0, dless = 0;
-    for (int j = 0; j < P; ++j) {
-        const int ej = rt.sel[j];
-        less += ej < e ? 1 : 0;
-        dless += (ej < e && ((first >> j) & 1ull)) ? 1 : 0;
-    }
+    const int less = __popcll(lt), dless = __popcll(lt & first);
     const int pos = less + rank;
     if (valid) {
         rt.perm[pos] = lane; rt.inv[lane] = pos;
-        if (rank == 0) { rt.act_e[dless] = e; rt.act_s0[dless] = less; rt.act_cnt[dless] = __popcll(match); }
+        if (rank == 0) { rt.act_e[dless] = e; rt.act_s0[dless] = less; rt.act_cnt[dless] = __popcll(eq); }
     }
     if (lane == 0) { *rt.nact = __popcll(first); }
     // pair-slots: the shared expert's (tokens 2k, 2k + 1 at slots P + 2k ..), then every active expert's in act order
@@ -298,16 +322,19 @@ __device__ __noinline__ void dispatch_wave(const DArgs & a, lds_t lds, int P) {
     }
     if (lane < nsh) { rt.ps_mi[lane] = SH; rt.ps_s[lane] = (P + 2 * lane) | ((a.n - 2 * lane >= 2 ? 2 : 1) << 16); }
     if (lane == 63) { *rt.nps = nsh + incl < DMAX_PS ? nsh + incl : DMAX_PS; }
-    if (blockIdx.x == 0) {   // the layer's routing outputs
-        if (valid) { gptr(a.perm)[pos] = lane; gptr(a.inv)[lane] = pos; gptr(a.sel)[lane] = e; gptr(a.wts)[lane] = rt.wts[lane]; }
-        if (valid && rank == 0) { gptr(a.act)[dless] = e; }
-        if (lane == 0) { *gptr(a.nact) = __popcll(first); }
-        for (int x = lane; x <= a.n_exp; x += 64) {
-            int lt = 0, eq = 0;
-            for (int j = 0; j < P; ++j) { const int ej = rt.sel[j]; lt += ej < x ? 1 : 0; eq += ej == x ? 1 : 0; }
-            gptr(a.offsets)[x] = lt;
-            if (x < a.n_exp) { gptr(a.counts)[x] = eq; }
-        }
+}
+// the layer's routing outputs from workgroup 0's tables (one wave, after its work: they are read after the launch)
+__device__ __noinline__ void routing_outputs(const DArgs & a, lds_t lds, int P) {
+    const RT rt(lds);
+    const int lane = lane_id(), nact = *rt.nact;
+    if (lane < P) { gptr(a.perm)[rt.inv[lane]] = lane; gptr(a.inv)[lane] = rt.inv[lane]; gptr(a.sel)[lane] = rt.sel[lane]; gptr(a.wts)[lane] = rt.wts[lane]; }
+    if (lane < nact) { gptr(a.act)[lane] = rt.act_e[lane]; }
+    if (lane == 0) { *gptr(a.nact) = nact; }
+    for (int x = lane; x <= a.n_exp; x += 64) {
+        int lt = 0, eq = 0;
+        for (int j = 0; j < P; ++j) { const int ej = rt.sel[j]; lt += ej < x ? 1 : 0; eq += ej == x ? 1 : 0; }
+        gptr(a.offsets)[x] = lt;
+        if (x < a.n_exp) { gptr(a.counts)[x] = eq; }
     }
 }
 
@@ -451,115 +478,106 @@ __device__ __forceinline__ void pre_shared_split(const DArgs & a, lds_t lds, con
 
 // ---------------------------------------------------------------- phase 4: down units
 // A unit is row group rg (256 output rows) of one pair-slot: wave w owns rows rg * 256 + 32 w .. + 31 (two 16-row sets of
-// one 64-row group) and stages Q8_K block w of h for the unit's c (1 or 2) tokens at slots s, s + 1. The units of a
-// workgroup form a pipeline: the h words of the next unit are requested before the current one computes, and the staged
-// h alternates between two LDS buffers, so one barrier per unit suffices.
+// one 64-row group). Once its waves have finished their gate/up passes, a workgroup stages the h of all its units at
+// once into the LDS of the token rows (no longer needed): row 2 k + i = token i of its unit k, wave w quantising Q8_K
+// block w of every row. After one barrier each wave computes its rows of every unit without further synchronisation.
 struct DnUnit { int mi, s, c, rg; };
 __device__ __forceinline__ bool dn_unit(const RT & rt, int u, int nps, int nact, int P, int n, DnUnit & d) {
     const int ps = u % nps, mi = rt.ps_mi[ps], sc = rt.ps_s[ps];
     d.mi = mi; d.s = sc & 0xFFFF; d.c = sc >> 16; d.rg = u / nps;
     return (mi == SH || (unsigned) mi < (unsigned) nact) && (d.c == 1 || d.c == 2) && d.s + d.c <= P + n;
 }
-__device__ __forceinline__ void dn_h_issue(const DArgs & a, int wave, const DnUnit & d, uint64_t (&w)[2][4]) {
-    const int lane = lane_id();
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        if (u < d.c) {
-            const uint64_t * src = a.th + (size_t) (d.s + u) * DH + wave * QK + 4 * lane;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) { w[u][k] = ld_tag(src + k); }
-        }
-    }
-}
-// completes the poll (re-requesting until every word carries the epoch), then Q8_K of block `wave` into buffer hs
-__device__ __forceinline__ bool dn_h_stage(const DArgs & a, int wave, const DnUnit & d, uint64_t (&w)[2][4], lds_t hs) {
-    const int lane = lane_id();
-    int it = 0;
-    for (; it < POLL_MAX; ++it) {
-        bool v = true;
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) { v = v && (u >= d.c || tag_ok(w[u][k], a.epoch)); }
-        }
-        if (__ballot(!v) == 0) { break; }
-        __builtin_amdgcn_s_sleep(1);
-        dn_h_issue(a, wave, d, w);
-    }
-    if (it == POLL_MAX) { return false; }
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        if (u < d.c) {
-            const float xs[4] = { tag_val(w[u][0]), tag_val(w[u][1]), tag_val(w[u][2]), tag_val(w[u][3]) };
-            float dq; const uint32_t packed = q8k_lane(xs, dq);
-            lds_t hrow = hs + u * GD::XROW;
-            *reinterpret_cast<LK_LOCAL uint32_t *>(hrow + wave * GD::XBLK + staged_word(lane)) = packed;
-            if (lane == 0) { reinterpret_cast<LK_LOCAL float *>(hrow + GD::NB * GD::XBLK)[wave] = dq; }
-        }
-    }
-    return true;
-}
+constexpr int HROWS = DMAX_N * GG::XROW / GD::XROW;   // staged h rows that fit the token rows' LDS (28)
+constexpr int DN_KC = HROWS / 2;                      // units staged per chunk
 
-// the workgroup's units blockIdx.x, + G, .. < nps * NDN; returns the number of units run
+// the workgroup's units blockIdx.x, + G, .. < nps * NDN; returns their number
 __device__ __forceinline__ int down_phase(const DArgs & a, lds_t lds, const Lane ln, int wave, int nps, int nact, int P) {
 #pragma clang fp contract(off)
     const RT rt(lds);
-    const int G = gridDim.x, total = nps * NDN;
-    int u = blockIdx.x;
-    if (u >= total) { return 0; }
-    DnUnit cur, nxt;
-    bool cur_ok = dn_unit(rt, u, nps, nact, P, a.n, cur);
-    uint64_t w[2][4];
-    if (cur_ok) { dn_h_issue(a, wave, cur, w); }
-    LK_LOCAL unsigned * wok = reinterpret_cast<LK_LOCAL unsigned *>(lds + L_CTL) + 8;   // [2][DW] per-wave staging results
+    const int G = gridDim.x, total = nps * NDN, lane = lane_id();
+    const int K = (int) blockIdx.x < total ? (total - 1 - (int) blockIdx.x) / G + 1 : 0;
+    LK_LOCAL unsigned * wok = reinterpret_cast<LK_LOCAL unsigned *>(lds + L_CTL) + 8;   // [DW] per-wave staging results
     const uint32_t lq = (uint32_t) ln.q * 4096 + 16 * ln.r, ld = (uint32_t) ln.q * 128 + 2 * ln.r;
-    int k = 0;
-    for (;;) {
-#ifdef LOKI_TRACE
-        const int tb = k < 8 ? 24 + 4 * k : -1;
-#else
-        const int tb = -1;
-#endif
-        TRACE_T(tb, 0);
-        const int e = cur_ok && cur.mi != SH ? rt.act_e[cur.mi] : 0;
-        const uint8_t * base = uniform_ptr(cur.mi != SH ? a.down + (size_t) e * a.estride : a.sh_down);
-        const int g64 = cur.rg * (DN_ROWS / 64) + (wave >> 1), sub = (wave & 1) * 2;
-        const uint8_t * qb = base + (size_t) g64 * GD::NB * 4096 + sub * 256;
-        const uint8_t * db = base + (size_t) (DE / 64) * GD::NB * 4096 + (size_t) g64 * GD::NB * 128 + sub * 32;
-        RowStream<GD::BPQ, 2, DN_PD> rs;
-        if (cur_ok) { rs.prologue(qb, db, lq, ld); }   // the weights do not depend on h: in flight during the wait
-        const lds_t hs = lds + L_HS + (k & 1) * 2 * GD::XROW;
-        const bool ok = cur_ok && dn_h_stage(a, wave, cur, w, hs);
-        if (lane_id() == 0) { wok[(k & 1) * DW + wave] = ok ? 1u : 0u; }
-        __syncthreads();   // the unit's h is staged; every wave has left the unit before last (its buffer is free)
-        bool all_ok = true;
+    for (int k0 = 0; k0 < K; k0 += DN_KC) {
+        const int kn = K - k0 < DN_KC ? K - k0 : DN_KC;
+        __syncthreads();   // the token rows (or the previous chunk's h) are no longer read
+        TRACE(wave, 24);
+        // stage: rows r0 .. r0 + 3 at a time, all their words in flight together
+        bool ok = true;
+        for (int r0 = 0; r0 < 2 * kn && ok; r0 += 4) {
+            uint64_t w[4][4];
+            int src[4];
 #pragma unroll
-        for (int w2 = 0; w2 < DW; ++w2) { all_ok = all_ok && wok[(k & 1) * DW + w2] != 0u; }
-        TRACE_T(tb, 1);
-        const bool more = u + G < total;
-        const bool nxt_ok = more && dn_unit(rt, u + G, nps, nact, P, a.n, nxt);
-        if (nxt_ok) { dn_h_issue(a, wave, nxt, w); }
-        if (all_ok) {
-            // one token per pass: the second pass re-reads the unit's weights from L2
-            for (int i = 0; i < cur.c; ++i) {
-                if (i > 0) { rs.prologue(qb, db, lq, ld); }
-                float acc[2];
-                rs.run_dpp<GD>(qb, db, lq, ld, ln.tr, (const uint8_t *) (hs + i * GD::XROW), ln.q, ln.r, acc);
-                if (ln.q == 0) {
+            for (int rr = 0; rr < 4; ++rr) {
+                const int row = r0 + rr, k = k0 + row / 2, i = row & 1;
+                DnUnit d;
+                src[rr] = row < 2 * kn && dn_unit(rt, (int) blockIdx.x + k * G, nps, nact, P, a.n, d) && i < d.c ? d.s + i : -1;
+            }
+            auto issue = [&]() {
 #pragma unroll
-                    for (int r2 = 0; r2 < 2; ++r2) { st_tag(a.to + (size_t) (cur.s + i) * DE + cur.rg * DN_ROWS + wave * 32 + r2 * 16 + ln.r, a.epoch, 0.125f * acc[r2]); }
+                for (int rr = 0; rr < 4; ++rr) {
+                    if (src[rr] >= 0) {
+                        const uint64_t * p = a.th + (size_t) src[rr] * DH + wave * QK + 4 * lane;
+#pragma unroll
+                        for (int q4 = 0; q4 < 4; ++q4) { w[rr][q4] = ld_tag(p + q4); }
+                    }
+                }
+            };
+            issue();
+            int it = 0;
+            for (; it < POLL_MAX; ++it) {
+                bool v = true;
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; ++q4) { v = v && (src[rr] < 0 || tag_ok(w[rr][q4], a.epoch)); }
+                }
+                if (__ballot(!v) == 0) { break; }
+                __builtin_amdgcn_s_sleep(1);
+                issue();
+            }
+            if (it == POLL_MAX) { ok = false; break; }
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                if (src[rr] >= 0) {
+                    const float xs[4] = { tag_val(w[rr][0]), tag_val(w[rr][1]), tag_val(w[rr][2]), tag_val(w[rr][3]) };
+                    float dq; const uint32_t packed = q8k_lane(xs, dq);
+                    lds_t hrow = lds + L_XS + (r0 + rr) * GD::XROW;
+                    *reinterpret_cast<LK_LOCAL uint32_t *>(hrow + wave * GD::XBLK + staged_word(lane)) = packed;
+                    if (lane == 0) { reinterpret_cast<LK_LOCAL float *>(hrow + GD::NB * GD::XBLK)[wave] = dq; }
                 }
             }
-        } else {
-            report(a.err, 1);
         }
-        TRACE_T(tb, 2);
-        TRACE_T(tb, 3);
-        ++k;
-        if (!more) { break; }
-        u += G; cur = nxt; cur_ok = nxt_ok;
+        if (lane == 0) { wok[wave] = ok ? 1u : 0u; }
+        __syncthreads();   // every wave's blocks of every row are staged
+        bool all_ok = true;
+#pragma unroll
+        for (int w2 = 0; w2 < DW; ++w2) { all_ok = all_ok && wok[w2] != 0u; }
+        TRACE(wave, 25);
+        if (!all_ok) { report(a.err, 1); continue; }
+        for (int k = 0; k < kn; ++k) {
+            DnUnit d;
+            if (!dn_unit(rt, (int) blockIdx.x + (k0 + k) * G, nps, nact, P, a.n, d)) { report(a.err, 1); continue; }
+            const int e = d.mi != SH ? rt.act_e[d.mi] : 0;
+            const uint8_t * base = uniform_ptr(d.mi != SH ? a.down + (size_t) e * a.estride : a.sh_down);
+            const int g64 = d.rg * (DN_ROWS / 64) + (wave >> 1), sub = (wave & 1) * 2;
+            const uint8_t * qb = base + (size_t) g64 * GD::NB * 4096 + sub * 256;
+            const uint8_t * db = base + (size_t) (DE / 64) * GD::NB * 4096 + (size_t) g64 * GD::NB * 128 + sub * 32;
+            RowStream<GD::BPQ, 2, DN_PD> rs;
+            // one token per pass: the second pass re-reads the unit's weights from L2
+            for (int i = 0; i < d.c; ++i) {
+                rs.prologue(qb, db, lq, ld);
+                float acc[2];
+                rs.run_dpp<GD>(qb, db, lq, ld, ln.tr, (const uint8_t *) (lds + L_XS + (2 * k + i) * GD::XROW), ln.q, ln.r, acc);
+                if (ln.q == 0) {
+#pragma unroll
+                    for (int r2 = 0; r2 < 2; ++r2) { st_tag(a.to + (size_t) (d.s + i) * DE + d.rg * DN_ROWS + wave * 32 + r2 * 16 + ln.r, a.epoch, 0.125f * acc[r2]); }
+                }
+            }
+        }
+        TRACE(wave, 26);
     }
-    return k;
+    return K;
 }
 
 // ---------------------------------------------------------------- phase 5: combine
@@ -621,6 +639,7 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
     tables_dma(lds, a.tab, wave);
     __syncthreads();   // the hand-off words are clear
     for (int e = blockIdx.x; e < a.n_exp; e += G) { router_phase(a, lds, wave, e); }
+    quant_publish(a, wave);
     TRACE(wave, 2);
 
     // 2. wave t polls token t's probabilities while all waves quantise the tokens; wave t then selects token t's experts
@@ -629,7 +648,7 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
     const bool pre = n < DW;
     float bv[4]; uint64_t pw[4];
     if (wave < n) { load_bias(a.bias, a.n_exp, bv); probs_issue(a, wave, pw); }
-    quant_tokens(a, lds, wave);
+    if (!gather_tokens(a, lds, wave)) { report(a.err, 64); }
     __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's table loads have landed in LDS
     lds_arrive(ctl + 0, DW);              // [0] counts the waves whose tokens and table share are in LDS
     TRACE(wave, 1);
@@ -684,6 +703,7 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
         if (!combine_unit(a, lds, cu, P)) { report(a.err, 16); }
         TRACE(wave, 58);
     }
+    if (blockIdx.x == 0 && wave == DW - 1) { routing_outputs(a, lds, P); }
 #ifdef LOKI_TRACE
     if (lane == 0) { g_trace[(blockIdx.x * DW + wave) * TRACE_SLOTS + 63] = (uint64_t) ntask | ((uint64_t) nunit << 16) | ((uint64_t) t_gu << 32); }
 #endif
@@ -705,7 +725,7 @@ hipError_t decode_init(int ncu, int * grid) {
 
 hipError_t launch_moe_decode(const DecodeArgs & a, int grid, bool cooperative, hipStream_t st) {
     if (a.n < 1 || a.n > DMAX_N || a.topk < 1 || a.topk > MAXK || a.n_exp < 1 || a.n_exp > NEXP_MAX || a.n_group < 1 || a.n_group > 64 ||
-        a.n_exp % a.n_group || a.E != DE || a.H != DH || grid < 1 || !a.th || !a.to || !a.tlogits) {
+        a.n_exp % a.n_group || a.E != DE || a.H != DH || grid < 1 || !a.th || !a.to || !a.tlogits || !a.txq) {
         return hipErrorInvalidValue;
     }
     if (!cooperative) {   // one workgroup per CU fits the occupancy; co-residency is assumed, waits stay bounded

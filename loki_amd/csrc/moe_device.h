@@ -539,39 +539,39 @@ __device__ __forceinline__ void select_token_p(const float (&p)[4], const float 
 #pragma unroll
         for (int j = 0; j < 4; ++j) { const int e = 4 * lane + j; ok[j] = e < n_exp && allow[e / per]; }
     }
-    // topk rounds of argmax over the eligible, untaken experts: the largest ordered key of c; ties to the lower index =
-    // the lowest lane holding the maximum, whose own best is its lowest such expert
-    uint32_t kk[4];
+    // topk rounds of argmax over the eligible, untaken experts: the largest ordered key of c; ties to the lower index.
+    // Each lane first sorts its 4 (key, p, j) by key, descending and stably (adjacent exchanges on a strictly larger
+    // key: among equal keys the lower j stays first), so a round only reads the lanes' heads: the winner is the lowest
+    // lane whose head holds the maximum, and that lane drops its head.
+    uint32_t kk[4]; float pp[4]; int jj[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) { kk[j] = ok[j] ? ord_key(c[j]) : 0u; }
-    float sum = 0.f; float pr[MAXK]; int ir[MAXK];
+    for (int j = 0; j < 4; ++j) { kk[j] = ok[j] ? ord_key(c[j]) : 0u; pp[j] = p[j]; jj[j] = j; }
+    auto cex = [&](int x, int y) {
+        const bool sw = kk[y] > kk[x];
+        const uint32_t k0 = kk[x]; const float p0 = pp[x]; const int j0 = jj[x];
+        kk[x] = sw ? kk[y] : kk[x]; pp[x] = sw ? pp[y] : pp[x]; jj[x] = sw ? jj[y] : jj[x];
+        kk[y] = sw ? k0 : kk[y]; pp[y] = sw ? p0 : pp[y]; jj[y] = sw ? j0 : jj[y];
+    };
+    cex(0, 1); cex(1, 2); cex(2, 3); cex(0, 1); cex(1, 2); cex(0, 1);
+    float sum = 0.f, p_mine = 0.f; int sel_mine = -1;   // lane r keeps round r's pick
     for (int r = 0; r < topk; ++r) {
-        uint32_t lb = 0; int lj = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) { if (kk[j] > lb) { lb = kk[j]; lj = j; } }
-        const uint32_t m = wave_max_u32(lb);
+        const uint32_t m = wave_max_u32(kk[0]);
         int bi = -1; float bp = 0.f;
         if (m) {
-            const int wl = first_lane(lb == m);
-            float lp = p[0];
-#pragma unroll
-            for (int j = 1; j < 4; ++j) { if (lj == j) { lp = p[j]; } }
-            bi = 4 * wl + (int) rdlane((uint32_t) lj, wl);
-            bp = __builtin_bit_cast(float, rdlane(__builtin_bit_cast(uint32_t, lp), wl));
+            const int wl = first_lane(kk[0] == m);
+            bi = 4 * wl + (int) rdlane((uint32_t) jj[0], wl);
+            bp = __builtin_bit_cast(float, rdlane(__builtin_bit_cast(uint32_t, pp[0]), wl));
             if (lane == wl) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) { if (lj == j) { kk[j] = 0u; } }
+                kk[0] = kk[1]; kk[1] = kk[2]; kk[2] = kk[3]; kk[3] = 0u;
+                pp[0] = pp[1]; pp[1] = pp[2]; pp[2] = pp[3];
+                jj[0] = jj[1]; jj[1] = jj[2]; jj[2] = jj[3];
             }
         }
         sum = sum + bp;
-#pragma unroll
-        for (int k = 0; k < MAXK; ++k) { if (k == r) { pr[k] = bp; ir[k] = bi; } }
+        if (lane == r) { sel_mine = bi; p_mine = bp; }
     }
     sum = sum > 6.103515625e-5f ? sum : 6.103515625e-5f;
-#pragma unroll
-    for (int k = 0; k < MAXK; ++k) {
-        if (k < topk && lane == k) { sel_out[k] = ir[k]; w_out[k] = pr[k] / sum * scale; }
-    }
+    if (lane < topk) { sel_out[lane] = sel_mine; w_out[lane] = p_mine / sum * scale; }
 }
 // the same from the lane's 4 logits; probs_out (optional) receives the n_exp probabilities
 __device__ __forceinline__ void select_token(const float (&lg)[4], const float (&bias)[4], int n_exp, int n_group, int topk_group, int topk,
