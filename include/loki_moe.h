@@ -131,6 +131,10 @@ int fl_set_debug(FLCtx *, int capture_gate_up);
  * 2 = the same kernel with a regular launch (assumes nothing else occupies the CUs: waits are bounded and report a
  * timeout through fl_sync otherwise); 0 = one launch per pass */
 int fl_set_fused(FLCtx *, int mode);
+/* batches above the decode sizes (n > 8, E 7168, H 2048): 1 (default) = the expert products as grouped GEMMs on the
+ * matrix cores (no counterpart in the reference, whose wide path is tc_matvec per arena batch, src/fused_layer.cu:540-561);
+ * 0 = the per-pass mat-vec kernels. Both give bit-identical outputs. */
+int fl_set_prefill_mfma(FLCtx *, int on);
 
 /* stage timing with HIP events on the context's stream: stages 0..5 = quant_x, router_logits, router_select, dispatch,
  * gate_up (with SwiGLU and Q8_K(h)), down (with the combine). fl_stage_ms waits for the profiled calls and returns their count (summed ms in ms[]). */

@@ -55,7 +55,7 @@ ABI_SYMBOLS = [
     "fl_wide_outs", "fl_wide_skip", "fl_spec", "fl_sketch", "fl_fetch", "fl_moe", "fl_skip", "fl_h2d", "fl_wait_event",
     "fl_gpu_ms", "fl_ffn_begin", "fl_set_experts", "fl_set_routing", "fl_moe_layer", "fl_route_dev", "fl_dispatch_dev", "fl_quant_q8k_dev",
     "fl_pack_iq2xxs", "fl_unpack_iq2xxs", "fl_rmsnorm_dev", "fl_synth_iq2xxs", "fl_synth_normal", "fl_probe_exp",
-    "fl_debug", "fl_set_debug", "fl_set_fused", "fl_stream", "fl_set_stream", "fl_d2h", "fl_set_profile", "fl_stage_ms", "fl_sync", "fl_last_error", "fl_free",
+    "fl_debug", "fl_set_debug", "fl_set_fused", "fl_set_prefill_mfma", "fl_stream", "fl_set_stream", "fl_d2h", "fl_set_profile", "fl_stage_ms", "fl_sync", "fl_last_error", "fl_free",
 ]
 
 _lib = None
@@ -85,6 +85,7 @@ def lib():
             "fl_set_experts": (I, [P_, I]),
             "fl_set_debug": (I, [P_, I]),
             "fl_set_fused": (I, [P_, I]),
+            "fl_set_prefill_mfma": (I, [P_, I]),
             "fl_moe_layer": (I, [P_, ctypes.POINTER(FLMoeLayer), P_, I, P_]),
             "fl_route_dev": (I, [P_, P_, P_, P_, I, I, I, P_, P_, P_, P_]),
             "fl_dispatch_dev": (I, [P_, P_, I, I, I, P_, P_, P_, P_, P_, P_]),
@@ -194,6 +195,10 @@ class Context:
 
     def set_debug(self, capture_gate_up):
         self.check(lib().fl_set_debug(self.ctx, 1 if capture_gate_up else 0))
+
+    def set_prefill_mfma(self, on):
+        """Batches above 8 tokens: True (default) = grouped GEMMs on the matrix cores, False = the per-pass kernels."""
+        self.check(lib().fl_set_prefill_mfma(self.ctx, 1 if on else 0))
 
     def set_fused(self, mode):
         """Decode batches (n <= 8): 1 / True = one cooperative launch (default), 2 = the same kernel with a regular

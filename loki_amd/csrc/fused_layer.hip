@@ -43,6 +43,7 @@ extern "C" void fl_free(FLCtx * c) {
     c->sel.release(); c->counts.release(); c->offsets.release(); c->perm.release(); c->inv.release(); c->act.release(); c->nact.release();
     compat_free(c); c->zero_i.release(); c->terms.release(); c->cnt.release();
     c->tab.release(); c->derr.release(); c->dlogit.release(); c->dtxq.release(); c->dth.release(); c->dto.release();
+    c->ptab.release(); c->pcols.release(); c->pncols.release(); c->xh.release(); c->hh.release();
     for (auto & v : c->ev_free) { for (auto e : v) { (void) hipEventDestroy(e); } }
     for (auto & v : c->ev_pending) { for (auto e : v) { (void) hipEventDestroy(e); } }
     (void) hipEventDestroy(c->em0); (void) hipEventDestroy(c->em1); (void) hipStreamDestroy(c->own);
@@ -72,7 +73,7 @@ extern "C" int fl_sync(FLCtx * c) {
         TRY(c, hipMemcpy(&e, c->derr.p, sizeof e, hipMemcpyDeviceToHost));
         if (e) {
             TRY(c, hipMemset(c->derr.p, 0, sizeof e));
-            return fail(c, FL_EHIP, "decode block: a device-wide wait timed out (code %d); its outputs are invalid", e);
+            return fail(c, FL_EHIP, "a device kernel reported error code %d (decode block: a wait timed out; prefill: bad LDS base); its outputs are invalid", e);
         }
     }
     return FL_OK;
@@ -92,6 +93,7 @@ extern "C" int fl_set_experts(FLCtx * c, int n_exp) {
     c->n_exp = n_exp; return FL_OK;
 }
 extern "C" int fl_set_debug(FLCtx * c, int capture) { if (!c) { return FL_EINVAL; } c->dbg_gu = capture ? 1 : 0; return FL_OK; }
+extern "C" int fl_set_prefill_mfma(FLCtx * c, int on) { if (!c) { return FL_EINVAL; } c->pf_mfma = on ? 1 : 0; return FL_OK; }
 extern "C" int fl_set_fused(FLCtx * c, int mode) {
     if (!c) { return FL_EINVAL; }
     if (mode < 0 || mode > 2) { return fail(c, FL_EINVAL, "fused mode %d outside 0..2", mode); }
@@ -244,6 +246,7 @@ extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, in
     }
     const size_t rows = (size_t) P + n;
     const bool fused = c->fused && n <= 8 && E == 7168 && H == 2048 && c->n_group <= 64 && decode_ready(c);
+    const bool mfma = !fused && c->pf_mfma && n > 8 && E == 7168 && H == 2048;
     ALLOC(c, c->xq, (size_t) n * E); ALLOC(c, c->xd, (size_t) n * (E / 256));
     ALLOC(c, c->logits, (size_t) n * ne); ALLOC(c, c->probs, (size_t) n * ne);
     ALLOC(c, c->sel, P); ALLOC(c, c->wts, P); ALLOC(c, c->perm, P); ALLOC(c, c->inv, P);
@@ -283,14 +286,47 @@ extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, in
         prof_mark(c, ev, 5); prof_mark(c, ev, 6);
         return FL_OK;
     }
+    if (mfma) {
+        if (!c->pf_ready) {
+            ALLOC(c, c->ptab, prefill_table_bytes() / 16);
+            TRY(c, build_prefill_tables(c->ptab.p, st));
+            TRY(c, prefill_init());
+            if (!c->derr.p) { ALLOC(c, c->derr, 1); TRY(c, hipMemsetAsync(c->derr.p, 0, sizeof(int), st)); }
+            c->pf_ready = 1;
+        }
+        ALLOC(c, c->xh, (size_t) n * E); ALLOC(c, c->hh, rows * H);
+        ALLOC(c, c->pcols, rows / 32 + NEXP_MAX + 2); ALLOC(c, c->pncols, 1);
+    }
     prof_mark(c, ev, 0);
     TRY(c, launch_quant_q8k(x, n, E, c->xq.p, c->xd.p, st));
+    if (mfma) { TRY(c, launch_q8_to_h(c->xq.p, c->xh.p, (int64_t) n * E, st)); }
     prof_mark(c, ev, 1);
     TRY(c, launch_router_logits(L->gate_inp, x, n, ne, E, c->logits.p, st));
     prof_mark(c, ev, 2);
     TRY(c, launch_router_select(c->logits.p, L->probs_b, n, ne, c->n_group, c->topk_group, tk, c->scale, c->probs.p, c->sel.p, c->wts.p, st));
     prof_mark(c, ev, 3);
     TRY(c, launch_dispatch(c->sel.p, P, ne, c->counts.p, c->offsets.p, c->perm.p, c->inv.p, c->act.p, c->nact.p, st));
+    if (mfma) {
+        TRY(c, launch_prefill_cols(c->act.p, c->nact.p, c->offsets.p, n, P, c->pcols.p, c->pncols.p, st));
+        prof_mark(c, ev, 4);
+        PrefillArgs g{};
+        g.ptab = c->ptab.p; g.w[0] = (const uint8_t *) L->gate_exps; g.w[1] = (const uint8_t *) L->up_exps;
+        g.estride = (size_t) H * (E / 256) * IQ2B; g.sh[0] = (const uint8_t *) L->sh_gate; g.sh[1] = (const uint8_t *) L->sh_up;
+        g.perm = c->perm.p; g.topk = tk; g.P = P; g.R = H; g.K = E; g.nmat = 2; g.cols = c->pcols.p; g.ncols = c->pncols.p;
+        g.bh = c->xh.p; g.bd = c->xd.p; g.out = c->h.p; g.gdbg = c->dbg_gu ? c->g.p : nullptr; g.udbg = c->dbg_gu ? c->u.p : nullptr;
+        g.err = c->derr.p;
+        TRY(c, launch_prefill_gemm(g, c->ncu, st));
+        TRY(c, launch_quant_q8k(c->h.p, (int64_t) rows, H, c->hq.p, c->hd.p, st));
+        TRY(c, launch_q8_to_h(c->hq.p, c->hh.p, (int64_t) rows * H, st));
+        prof_mark(c, ev, 5);
+        PrefillArgs d = g;
+        d.w[0] = (const uint8_t *) L->down_exps; d.w[1] = nullptr; d.sh[0] = (const uint8_t *) L->sh_down; d.sh[1] = nullptr;
+        d.R = E; d.K = H; d.nmat = 1; d.bh = c->hh.p; d.bd = c->hd.p; d.out = c->o.p; d.gdbg = nullptr; d.udbg = nullptr;
+        TRY(c, launch_prefill_gemm(d, c->ncu, st));
+        TRY(c, launch_combine(c->o.p, c->inv.p, c->wts.p, n, tk, E, P, nullptr, y, nullptr, st));
+        prof_mark(c, ev, 6);
+        return FL_OK;
+    }
     prof_mark(c, ev, 4);
     ExpertArgs a = expert_args(c, n, P, 1);
     a.w[0] = (const uint8_t *) L->gate_exps; a.w[1] = (const uint8_t *) L->up_exps; a.estride = (size_t) H * (E / 256) * IQ2B;

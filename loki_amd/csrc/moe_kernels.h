@@ -70,6 +70,27 @@ size_t decode_lds_bytes();
 // regular launch assumes it (nothing else running on the CUs) -- a violation ends in a reported wait timeout
 hipError_t launch_moe_decode(const DecodeArgs & a, int grid, bool cooperative, hipStream_t st);
 
+// ---------------------------------------------------------------- prefill grouped GEMM on MFMA (moe_prefill.hip)
+struct PrefillArgs {
+    const uint4 * ptab;                  // fp16 table image (build_prefill_tables)
+    const uint8_t * w[2]; size_t estride;   // routed matrices (tiled), expert e at + e * estride
+    const uint8_t * sh[2];               // shared expert matrices (tiled)
+    const int * perm; int topk, P;       // gate/up: slot -> token = perm[slot] / topk (shared slots P + t -> t)
+    int R, K, nmat;                      // rows, columns; nmat 2 = gate/up, 1 = down
+    const int4 * cols; const int * ncols;   // launch_prefill_cols
+    const _Float16 * bh; const float * bd;  // activations: Q8_K integers as fp16 [rows][K] and scales [rows][K/256]
+    float * out;                         // gate/up: h [P+n][R] (silu(g) * u); down: o [P+n][R]
+    float * gdbg, * udbg;                // optional gate / up outputs
+    int * err;                           // bit 4: the LDS base is not 64 KB aligned
+};
+hipError_t prefill_init();
+size_t prefill_table_bytes();
+hipError_t build_prefill_tables(uint4 * img, hipStream_t st);
+// columns of <= 32 slots of one expert: the shared expert's first, then act order; cols sized >= (n+P)/32 + NEXP_MAX + 2
+hipError_t launch_prefill_cols(const int * act, const int * nact, const int * offsets, int n, int P, int4 * cols, int * ncols, hipStream_t st);
+hipError_t launch_q8_to_h(const int8_t * q, _Float16 * h, int64_t n, hipStream_t st);
+hipError_t launch_prefill_gemm(const PrefillArgs & a, int grid, hipStream_t st);
+
 // y[t] = sum_k (o[inv[t*topk+k]] * w[t][k]) in k order + o[P+t] (+ resid[t] when given)
 hipError_t launch_combine(const float * o, const int * inv, const float * wts, int n, int topk, int E, int P,
                           const float * resid, float * y, float * moe, hipStream_t st);

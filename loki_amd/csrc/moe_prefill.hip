@@ -1,0 +1,378 @@
+// moe_prefill.hip -- the grouped IQ2_XXS x Q8_K expert GEMMs of a prefill batch on the matrix cores.
+//
+// Reference: fl_wide_moe (src/fused_layer.cu:540-561) runs tc_matvec<F_IQ2> (:178-202) per arena batch of <= 72 slots
+// of <= 8 rows each with mma.m16n8k32 s8 tiles, then swiglu_q8 (:334-341) and the down pass; the semantics are ggml's
+// mul_mat_id over IQ2_XXS x Q8_K (ggml_vec_dot_iq2_xxs_q8_K per output). Here one launch covers every expert of the
+// layer:
+//   * A column is up to 32 dispatch slots of one expert (the shared expert's slots P .. P + n - 1 included); an item is
+//     (column, 256 or 512 rows). The workgroups (one per CU: the tables fill most of the LDS) take the items round-robin.
+//   * The weights are dequantised once per item into fp16 MFMA operands: lane (r, g) of a wave owns row r of a 16-row
+//     tile and the 16-byte chunk g of each block (sub-blocks 2g, 2g + 1, both with their scale nibbles), so it builds
+//     w = sign * grid * (2 nibble + 1) from two replicated LDS tables (fp16 codebook words, fp16 sign masks) and one
+//     packed fp16 multiply per two weights. Every w is an integer of magnitude <= 43 * 31, exact in fp16.
+//   * The column's activations (the Q8_K integers as fp16, exact) are copied block by block into LDS with direct
+//     global->LDS loads, double-buffered; v_mfma_f32_16x16x32_f16 then forms, per 256-value block, the block sum
+//     bsum = sum_ib (2 s_ib + 1) sum_k g s q over a 16-token x 16-row tile. Products and partial sums are integers below
+//     2^24 in magnitude (|bsum| < 2^24 whenever the activations are Q8_K of real data: the worst case needs every
+//     product at its maximum), so the fp32 accumulation is exact and equals ggml's int32 block sum.
+//   * Each output then advances in block order, y += (d_w * d_x) * bsum, and ends * 0.125: the fp32 operations and their
+//     order are those of ggml_vec_dot_iq2_xxs_q8_K, so every output is bit-identical to the CPU checker's.
+//   * Gate/up tiles write h = silu(g) * u per slot; down tiles write o per slot (the combine runs after).
+// The K index of an MFMA step is permuted consistently in both operands: step t of lane group g covers the 8 values
+// 64 g + 8 t .. + 7 of the block, i.e. entry t % 4 of sub-block 2 g + t / 4, which is what the lane's chunk holds.
+#include "moe_device.h"
+#include "moe_kernels.h"
+#include <type_traits>
+
+namespace lk {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int PF_W = 8, PF_NT = PF_W * 64;   // waves / threads per workgroup
+constexpr int PF_TOK = 32;                   // slots per column (two 16-token MFMA tiles)
+// LDS: fp16 codebook (256 lines x 16 copies x 16 B), fp16 sign masks (128 lines, the 7 stored sign bits), then two
+// activation buffers (32 token rows x 512 B, each row's 16-byte chunks XOR-swizzled by the row, then 32 scales)
+constexpr int L_PG = 0, L_PS = 65536, L_PB = L_PS + 128 * 256;
+constexpr int PB_TILE = 16 * 512, PB_DX = 2 * PB_TILE, PB_BUF = PB_DX + 512;   // buffers 512-byte aligned
+constexpr int PF_LDS = L_PB + 2 * PB_BUF;
+constexpr int PTAB_BYTES = L_PB;             // the table image copied to LDS offset 0
+static_assert(PF_LDS <= 160 * 1024, "LDS budget");
+
+// fp16 table image: line e of the codebook = 16 copies of the 8 fp16 values of grid[e]; line b of the signs = 16
+// copies of 8 fp16 sign masks (0x8000 for a negative weight) of the stored sign bits b (0..127) plus parity
+__global__ void k_ptab_image(uint32_t * img) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;   // dword index
+    if (i >= PTAB_BYTES / 4) { return; }
+    const int line = (i * 4) >> 8, word = i & 3;            // 16 B entry copies: the dword inside the entry
+    uint32_t v;
+    if (i * 4 < L_PS) {
+        const uint64_t gv = g_iq2xxs_grid[line];
+        const uint32_t b0 = (uint32_t) (gv >> (16 * word)) & 255u, b1 = (uint32_t) (gv >> (16 * word + 8)) & 255u;
+        v = (uint32_t) __half_as_ushort(__float2half((float) b0)) | ((uint32_t) __half_as_ushort(__float2half((float) b1)) << 16);
+    } else {
+        const uint32_t s8 = ksigns8((uint32_t) (line - L_PS / 256));
+        v = (((s8 >> (2 * word)) & 1u) << 15) | (((s8 >> (2 * word + 1)) & 1u) << 31);
+    }
+    img[i] = v;
+}
+hipError_t build_prefill_tables(uint4 * img, hipStream_t st) {
+    k_ptab_image<<<PTAB_BYTES / 4 / 256, 256, 0, st>>>(reinterpret_cast<uint32_t *>(img));
+    return hipGetLastError();
+}
+size_t prefill_table_bytes() { return PTAB_BYTES; }
+
+// columns: the shared expert's slots first (P + 32 c ..), then every active expert's slots in act order, 32 per column
+__global__ void __launch_bounds__(256) k_pf_cols(const int * __restrict__ act, const int * __restrict__ nact_p, const int * __restrict__ offsets,
+                                                int n, int P, int4 * __restrict__ cols, int * __restrict__ ncols) {
+    __shared__ int scan[256];
+    const int i = threadIdx.x, nact = *nact_p, nsh = (n + PF_TOK - 1) / PF_TOK;
+    int e = 0, s0 = 0, cnt = 0;
+    if (i < nact) { e = act[i]; s0 = offsets[e]; cnt = offsets[e + 1] - s0; }
+    const int nc = (cnt + PF_TOK - 1) / PF_TOK;
+    scan[i] = nc;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {   // inclusive scan
+        const int v = i >= off ? scan[i - off] : 0;
+        __syncthreads();
+        scan[i] += v;
+        __syncthreads();
+    }
+    const int base = nsh + scan[i] - nc;
+    for (int c = 0; c < nc; ++c) { cols[base + c] = make_int4(i, s0 + PF_TOK * c, min(PF_TOK, cnt - PF_TOK * c), e); }
+    for (int c = i; c < nsh; c += 256) { cols[c] = make_int4(-1, P + PF_TOK * c, min(PF_TOK, n - PF_TOK * c), 0); }
+    if (i == 255) { *ncols = nsh + scan[255]; }
+}
+hipError_t launch_prefill_cols(const int * act, const int * nact, const int * offsets, int n, int P, int4 * cols, int * ncols, hipStream_t st) {
+    k_pf_cols<<<1, 256, 0, st>>>(act, nact, offsets, n, P, cols, ncols);
+    return hipGetLastError();
+}
+
+// Q8_K integers as fp16 (exact): the MFMA operand copy of an activation array
+__global__ void __launch_bounds__(256) k_q8_to_h(const int8_t * __restrict__ q, _Float16 * __restrict__ h, int64_t n) {
+    const int64_t i = ((int64_t) blockIdx.x * 256 + threadIdx.x) * 8;
+    if (i >= n) { return; }
+    const u32x2 v = *(const LK_GLOBAL u32x2 *) (q + i);
+    h8 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) { o[k] = (_Float16) (int8_t) (v.x >> (8 * k)); o[4 + k] = (_Float16) (int8_t) (v.y >> (8 * k)); }
+    *(LK_GLOBAL h8 *) (h + i) = o;
+}
+hipError_t launch_q8_to_h(const int8_t * q, _Float16 * h, int64_t n, hipStream_t st) {
+    if (n <= 0) { return hipSuccess; }
+    if (n % 8) { return hipErrorInvalidValue; }
+    k_q8_to_h<<<(unsigned) ((n / 8 + 255) / 256), 256, 0, st>>>(q, h, n);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- the grouped GEMM
+// NMAT = 2: gate/up (K = 7168, rows 2048, B rows = tokens, writes h); NMAT = 1: down (K = 2048, rows 7168, B rows =
+// slots, writes o). RGI 16-row tiles per wave: combos = NMAT * RGI = 2 dequantised tiles per block either way.
+template <int NMAT, int RGI, int NB>
+struct PfGeo {
+    static constexpr int COMBOS = NMAT * RGI, ROWS = PF_W * 16 * RGI, K = NB * QK;
+};
+
+struct PfLane {
+    int r, g;                 // row (token) in a 16-tile, chunk / lane group
+    uint32_t trg, trs;        // table addresses with this lane's copy
+};
+
+// one block of one 16-row tile: the tiled chunk g of row r (qs) and d
+struct PfW { u32x4 q; uint16_t d; };
+
+// raw buffer resource over p (gfx9 word 3; the record count only bounds offsets, which stay far below it)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t pf_rsrc(const void * p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short) 0, 0x7fffffff, 0x00020000);
+}
+// a wave-uniform pointer kept in scalar registers
+__device__ __forceinline__ const uint8_t * pf_uniform(const uint8_t * p) {
+    const uint64_t v = (uint64_t) p;
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) (v >> 32));
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) v);
+    return (const uint8_t *) (((uint64_t) hi << 32) | (uint64_t) lo);
+}
+
+__device__ __forceinline__ void dma16(const void * src, LK_LOCAL uint8_t * dst) {
+    __builtin_amdgcn_global_load_lds((const LK_GLOBAL void *) src, (LK_LOCAL void *) dst, 16, 0, 0);
+}
+
+template <int NMAT, int RGI, int NB>
+__global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
+#pragma clang fp contract(off)
+    using Geo = PfGeo<NMAT, RGI, NB>;
+    constexpr int C = Geo::COMBOS;
+    extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds[];
+    LK_LOCAL uint8_t * lds = (LK_LOCAL uint8_t *) dyn_lds;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
+    if (lds_addr(dyn_lds) & 0xFFFFu) {   // table addressing needs a 64 KB aligned base
+        if (threadIdx.x == 0) { __hip_atomic_fetch_or(gptr(a.err), 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+        return;
+    }
+    // tables into LDS (direct loads), visible after vmcnt(0) + the first barrier
+    for (int c = wave; c < PTAB_BYTES / 1024; c += PF_W) { dma16(a.ptab + c * 64 + lane, lds + c * 1024); }
+    PfLane ln;
+    ln.r = lane & 15; ln.g = lane >> 4;
+    ln.trg = (uint32_t) L_PG | ((uint32_t) ln.r << 4);
+    ln.trs = (uint32_t) L_PS | ((uint32_t) ln.r << 4);
+    const int ncols = *gptr(a.ncols);
+    const int nrg = a.R / Geo::ROWS;
+    const size_t dreg = (size_t) (a.R / 64) * NB * 4096;   // d region offset of a tiled matrix
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    __syncthreads();
+
+    for (int it = blockIdx.x; it < ncols * nrg; it += gridDim.x) {
+        const int col = it / nrg, rg = it - col * nrg;
+        const u32x4 cv = *(const LK_GLOBAL u32x4 *) (a.cols + col);
+        const int4 cd = make_int4((int) cv.x, (int) cv.y, (int) cv.z, (int) cv.w);
+        const bool routed = cd.x >= 0;
+        const int sb = cd.y, sc = cd.z;
+        // B rows of this wave's copy instructions: rows 4 w + {0,1} (instruction 0) and 4 w + {2,3} (1), lane half L >> 5
+        auto brow = [&](int n32) -> int {
+            const int s = sb + (n32 < sc ? n32 : 0);
+            return NMAT == 2 ? (routed ? gptr(a.perm)[s] / a.topk : s - a.P) : s;
+        };
+        const int rA = brow(4 * wave + (lane >> 5)), rB = brow(4 * wave + 2 + (lane >> 5));
+        const int rX = brow(lane & 31);
+        const int p = lane & 31;
+        const int cA = p ^ ((4 * wave + (lane >> 5)) & 15), cB = p ^ ((4 * wave + 2 + (lane >> 5)) & 15);
+        // Buffer loads: a scalar resource (base, no bounds that matter) + a 32-bit lane offset + a scalar block offset,
+        // so no 64-bit per-lane address lives in vector registers.
+        const __amdgpu_buffer_rsrc_t rb = pf_rsrc(a.bh), rd = pf_rsrc(a.bd);
+        const uint32_t oA = (uint32_t) rA * (Geo::K * 2) + (uint32_t) cA * 16, oB = (uint32_t) rB * (Geo::K * 2) + (uint32_t) cB * 16;
+        const uint32_t oX = (uint32_t) rX * (NB * 4);
+        // the column's activations of block j: this wave's rows 4 w .. 4 w + 3 (two 1 KB pieces) and the 32 scales,
+        // loaded into registers, then written to LDS (after the block that reads the other buffer)
+        struct PfB { u32x4 a, b; float dx; };
+        auto load_b = [&](int j, PfB & bq) {
+            bq.a = __builtin_amdgcn_raw_buffer_load_b128(rb, oA, j * (QK * 2), 0);
+            bq.b = __builtin_amdgcn_raw_buffer_load_b128(rb, oB, j * (QK * 2), 0);
+            bq.dx = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, oX, j * 4, 0));
+        };
+        auto store_b = [&](const PfB & bq, int buf) {
+            LK_LOCAL uint8_t * dst = lds + L_PB + buf * PB_BUF;
+            *(LK_LOCAL u32x4 *) (dst + (4 * wave) * 512 + lane * 16) = bq.a;
+            *(LK_LOCAL u32x4 *) (dst + (4 * wave + 2) * 512 + lane * 16) = bq.b;
+            if (wave == 0 && lane < 32) { *(LK_LOCAL float *) (dst + PB_DX + lane * 4) = bq.dx; }
+        };
+        // the wave's tiles: combo c = (matrix c / RGI, 16-row tile c % RGI): scalar resources at the tile's qs / d
+        // bases, the lane's offset (chunk g of row r) in one vector register
+        __amdgpu_buffer_rsrc_t uq[C], ud[C];
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            const int mat = c / RGI, ti = c % RGI;
+            const uint8_t * W = routed ? a.w[mat] + (size_t) cd.w * a.estride : a.sh[mat];
+            const int row0 = rg * Geo::ROWS + (wave * RGI + ti) * 16;   // a 16-row tile lies inside one 64-row group
+            const int g64 = row0 >> 6, r0 = row0 & 63;
+            uq[c] = pf_rsrc(pf_uniform(W + (size_t) g64 * NB * 4096 + r0 * 16));
+            ud[c] = pf_rsrc(pf_uniform(W + dreg + (size_t) g64 * NB * 128 + r0 * 2));
+        }
+        const uint32_t lq = (uint32_t) ln.g * 1024 + (uint32_t) ln.r * 16, ldo = (uint32_t) ln.r * 2;
+        auto load_w = [&](int j, PfW (&w)[C]) {
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+                w[c].q = __builtin_amdgcn_raw_buffer_load_b128(uq[c], lq, j * 4096, 2);   // nt: streamed once
+                w[c].d = __builtin_amdgcn_raw_buffer_load_b16(ud[c], ldo, j * 128, 0);
+            }
+        };
+        auto run_item = [&](auto ntc) {
+            constexpr int NT = decltype(ntc)::value;   // token tiles of the column (1 or 2)
+            f4 acc[C][NT];
+#pragma unroll
+            for (int c = 0; c < C; ++c) { for (int tt = 0; tt < NT; ++tt) { acc[c][tt] = (f4) { 0.f, 0.f, 0.f, 0.f }; } }
+
+            // one block: dequantise the C tiles step by step and run the MFMA chains of both token tiles
+            auto block = [&](int j, const PfW (&w)[C], int buf) {
+                static_assert((L_PB % 512) == 0 && (PB_BUF % 512) == 0, "XOR addressing inside 512-byte rows");
+                const uint32_t bx = ((uint32_t) (L_PB + buf * PB_BUF) + (uint32_t) ln.r * 512) | ((uint32_t) ((8 * ln.g) ^ ln.r) << 4);
+                f4 cc[C][NT];
+                h2v sc[C][2];
+                uint32_t ms[C][2];
+#pragma unroll
+                for (int c = 0; c < C; ++c) {
+                    const _Float16 s0 = (_Float16) iq2_scale(w[c].q.y), s1 = (_Float16) iq2_scale(w[c].q.w);
+                    sc[c][0] = (h2v) { s0, s0 }; sc[c][1] = (h2v) { s1, s1 };
+                    ms[c][0] = w[c].q.y & 0x7f7f7f7fu; ms[c][1] = w[c].q.w & 0x7f7f7f7fu;
+                }
+                // step t's LDS reads (two activation chunks, per tile a codebook and a sign entry) are issued one step
+                // ahead of their use, into the other of two register sets
+                struct Lk { u32x4 g[C], s[C]; h8 x0, x1; };
+                auto lookup = [&](int t, Lk & k) {
+                    const uint32_t bo = bx ^ ((uint32_t) t << 4);   // chunk (8 g + t) ^ r of the lane's token row
+                    k.x0 = __builtin_bit_cast(h8, *(const LK_LOCAL u32x4 *) (size_t) bo);
+                    if (NT > 1) { k.x1 = __builtin_bit_cast(h8, *(const LK_LOCAL u32x4 *) (size_t) (bo + PB_TILE)); }
+#pragma unroll
+                    for (int c = 0; c < C; ++c) {
+                        const uint32_t a0 = t < 4 ? w[c].q.x : w[c].q.z, a1 = ms[c][t >> 2];
+                        uint32_t ga, sa;
+                        switch (t & 3) {
+                        case 0: ga = tab_addr<0>(a0, ln.trg); sa = tab_addr<0>(a1, ln.trs); break;
+                        case 1: ga = tab_addr<1>(a0, ln.trg); sa = tab_addr<1>(a1, ln.trs); break;
+                        case 2: ga = tab_addr<2>(a0, ln.trg); sa = tab_addr<2>(a1, ln.trs); break;
+                        default: ga = tab_addr<3>(a0, ln.trg); sa = tab_addr<3>(a1, ln.trs); break;
+                        }
+                        k.g[c] = *(const LK_LOCAL u32x4 *) (size_t) ga;
+                        k.s[c] = *(const LK_LOCAL u32x4 *) (size_t) sa;
+                    }
+                };
+                auto compute = [&](int t, const Lk & k) {
+#pragma unroll
+                    for (int c = 0; c < C; ++c) {
+                        const h8 gs = __builtin_bit_cast(h8, k.g[c] ^ k.s[c]);
+                        const h2v s = sc[c][t >> 2];
+                        const h8 wv = gs * (h8) { s[0], s[1], s[0], s[1], s[0], s[1], s[0], s[1] };
+                        cc[c][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k.x0, wv, t == 0 ? (f4) { 0.f, 0.f, 0.f, 0.f } : cc[c][0], 0, 0, 0);
+                        if (NT > 1) {
+                            cc[c][NT - 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k.x1, wv, t == 0 ? (f4) { 0.f, 0.f, 0.f, 0.f } : cc[c][NT - 1], 0, 0, 0);
+                        }
+                    }
+                };
+                Lk ka, kb;
+                lookup(0, ka);
+#pragma unroll
+                for (int t = 0; t < 8; t += 2) {
+                    lookup(t + 1, kb);
+                    compute(t, ka);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (t + 2 < 8) { lookup(t + 2, ka); }
+                    compute(t + 1, kb);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                // block fold, in block order: y += (d_w * d_x) * bsum
+                const f4 dx0 = *(const LK_LOCAL f4 *) (size_t) ((uint32_t) (L_PB + buf * PB_BUF + PB_DX) + 16 * ln.g);
+                const f4 dx1 = NT > 1 ? *(const LK_LOCAL f4 *) (size_t) ((uint32_t) (L_PB + buf * PB_BUF + PB_DX) + 64 + 16 * ln.g) : dx0;
+#pragma unroll
+                for (int c = 0; c < C; ++c) {
+                    const float dw = h2f(w[c].d);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) { acc[c][0][i] = acc[c][0][i] + (dw * dx0[i]) * cc[c][0][i]; }
+                    if (NT > 1) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) { acc[c][NT - 1][i] = acc[c][NT - 1][i] + (dw * dx1[i]) * cc[c][NT - 1][i]; }
+                    }
+                }
+                (void) j;
+            };
+
+            // pipeline: weights three blocks ahead (four register stages), activations one block ahead (registers, then
+            // the other of two LDS buffers). Every step issues the same loads (indices clamped at the last blocks: those
+            // copies land in registers nobody reads any more), so the compiler's waits count them exactly.
+            PfW w0[C], w1[C], w2[C], w3[C];
+            PfB bq;
+            load_w(0, w0);
+            load_w(1 < NB ? 1 : NB - 1, w1);
+            load_w(2 < NB ? 2 : NB - 1, w2);
+            load_b(0, bq);
+            store_b(bq, 0);
+            __syncthreads();
+            auto step = [&](int j, PfW (&cur)[C], PfW (&ahead)[C]) {
+                load_b(j + 1 < NB ? j + 1 : NB - 1, bq);
+                load_w(j + 3 < NB ? j + 3 : NB - 1, ahead);
+                __builtin_amdgcn_sched_barrier(0);   // nothing of the block moves above the loads
+                block(j, cur, j & 1);
+                store_b(bq, (j + 1) & 1);           // buffer (j + 1) & 1 was last read in step j - 1, before its barrier
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the writes are done before the barrier publishes them
+                __builtin_amdgcn_s_barrier();
+            };
+            static_assert(NB % 4 == 0, "four steps per trip");
+#pragma unroll 1
+            for (int j = 0; j < NB; j += 4) {
+                step(j, w0, w3);
+                step(j + 1, w1, w0);
+                step(j + 2, w2, w1);
+                step(j + 3, w3, w2);
+            }
+
+            // outputs: lane (r, g) holds tokens 4 g + i of each token tile for row r of each of its tiles
+#pragma unroll
+            for (int ti = 0; ti < RGI; ++ti) {
+                const int row = rg * Geo::ROWS + (wave * RGI + ti) * 16 + ln.r;
+#pragma unroll
+                for (int tt = 0; tt < NT; ++tt) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int n32 = 16 * tt + 4 * ln.g + i;
+                        if (n32 < sc) {
+                            const size_t o = (size_t) (sb + n32) * a.R + row;
+                            if (NMAT == 2) {
+                                const float gv = 0.125f * acc[ti][tt][i], uv = 0.125f * acc[RGI + ti][tt][i];
+                                a.out[o] = det_silu(gv) * uv;
+                                if (a.gdbg) { a.gdbg[o] = gv; a.udbg[o] = uv; }
+                            } else {
+                                a.out[o] = 0.125f * acc[ti][tt][i];
+                            }
+                        }
+                    }
+                }
+            }
+        };
+        if (sc > 16) { run_item(std::integral_constant<int, 2>{}); } else { run_item(std::integral_constant<int, 1>{}); }
+    }
+}
+
+template <int NMAT, int RGI, int NB>
+static hipError_t pf_setup() {
+    return hipFuncSetAttribute((const void *) k_pf_gemm<NMAT, RGI, NB>, hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS);
+}
+hipError_t prefill_init() {
+    hipError_t e = pf_setup<2, 1, 28>();
+    if (e == hipSuccess) { e = pf_setup<1, 2, 8>(); }
+    return e;
+}
+
+hipError_t launch_prefill_gemm(const PrefillArgs & a, int grid, hipStream_t st) {
+    if (grid < 1 || !a.ptab || !a.cols || !a.ncols || !a.bh || !a.bd || !a.out || !a.err) { return hipErrorInvalidValue; }
+    if (a.nmat == 2) {
+        if (a.K != 28 * QK || a.R % PfGeo<2, 1, 28>::ROWS || !a.w[0] || !a.w[1] || !a.sh[0] || !a.sh[1] || !a.perm) { return hipErrorInvalidValue; }
+        k_pf_gemm<2, 1, 28><<<grid, PF_NT, PF_LDS, st>>>(a);
+    } else if (a.nmat == 1) {
+        if (a.K != 8 * QK || a.R % PfGeo<1, 2, 8>::ROWS || !a.w[0] || !a.sh[0]) { return hipErrorInvalidValue; }
+        k_pf_gemm<1, 2, 8><<<grid, PF_NT, PF_LDS, st>>>(a);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace lk

@@ -31,9 +31,71 @@ __global__ void __launch_bounds__(64) k_router_logits(const float * __restrict__
     }
 }
 
+// Batches (K = 7168): lane 8 t + e owns the logits of tokens t and t + 8 of the workgroup's 16-token tile with expert e
+// of its 8-expert tile; wave q of the workgroup computes the contract's quarter q (chunks 64 q .. 64 q + 63) in
+// registers: each chunk's 28 products summed in element order with v_fma_f64 (the fp32 x fp32 product is exact in
+// fp64, so fma(x, w, s) is s + x * w rounded once), the pairwise tree built as it goes (levels 1-4 by recursion inside
+// a 16-chunk group, 5-6 across the quarter's four groups). Wave 0 then adds the quarters as (q0 + q1) + (q2 + q3)
+// (levels 7-8) through LDS.
+struct RgPair { double a, b; };   // the lane's two logits (tokens t, t + 8)
+template <int L>
+__device__ __forceinline__ RgPair rg_tree(const float * xa, const float * xb, const float * wr, int c0) {
+#pragma clang fp contract(off)
+    if constexpr (L == 0) {
+        constexpr int CL = 28;
+        RgPair s{0.0, 0.0};
+#pragma unroll
+        for (int i = 0; i < CL / 4; ++i) {
+            const float4 wv = gloadf4(wr + CL * c0 + 4 * i), av = gloadf4(xa + CL * c0 + 4 * i), bv = gloadf4(xb + CL * c0 + 4 * i);
+            const float w4[4] = { wv.x, wv.y, wv.z, wv.w }, a4[4] = { av.x, av.y, av.z, av.w }, b4[4] = { bv.x, bv.y, bv.z, bv.w };
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const double wd = (double) w4[q];
+                s.a = __builtin_fma((double) a4[q], wd, s.a);
+                s.b = __builtin_fma((double) b4[q], wd, s.b);
+            }
+        }
+        return s;
+    } else {
+        const RgPair l = rg_tree<L - 1>(xa, xb, wr, c0), r = rg_tree<L - 1>(xa, xb, wr, c0 + (1 << (L - 1)));
+        return RgPair{ l.a + r.a, l.b + r.b };
+    }
+}
+__global__ void __launch_bounds__(256) k_router_gemm(const float * __restrict__ W, const float * __restrict__ x, int n, int n_exp,
+                                                   float * __restrict__ logits) {
+#pragma clang fp contract(off)
+    constexpr int K = 7168;
+    __shared__ double part[4][2][64];
+    const int q = threadIdx.x >> 6, lane = lane_id();
+    const int t = blockIdx.y * 16 + (lane >> 3), e = blockIdx.x * 8 + (lane & 7);
+    const float * xa = x + (size_t) (t < n ? t : 0) * K, * xb = x + (size_t) (t + 8 < n ? t + 8 : 0) * K;
+    const float * wr = W + (size_t) (e < n_exp ? e : 0) * K;
+    RgPair l4{0.0, 0.0}, l5{0.0, 0.0}, tot{0.0, 0.0};
+#pragma unroll 1
+    for (int g = 0; g < 4; ++g) {   // the quarter's 16-chunk groups: a level-4 node each; levels 5-6 by g's bits
+        RgPair v = rg_tree<4>(xa, xb, wr, 64 * q + 16 * g);
+        if (!(g & 1)) { l4 = v; continue; }
+        v = RgPair{ l4.a + v.a, l4.b + v.b };
+        if (!(g & 2)) { l5 = v; continue; }
+        tot = RgPair{ l5.a + v.a, l5.b + v.b };
+    }
+    part[q][0][lane] = tot.a; part[q][1][lane] = tot.b;
+    __syncthreads();
+    if (q == 0 && e < n_exp) {
+        const double a = (part[0][0][lane] + part[1][0][lane]) + (part[2][0][lane] + part[3][0][lane]);
+        const double b = (part[0][1][lane] + part[1][1][lane]) + (part[2][1][lane] + part[3][1][lane]);
+        if (t < n) { logits[(size_t) t * n_exp + e] = (float) a; }
+        if (t + 8 < n) { logits[(size_t) (t + 8) * n_exp + e] = (float) b; }
+    }
+}
+
 hipError_t launch_router_logits(const float * W, const float * x, int n, int n_exp, int K, float * logits, hipStream_t st) {
     if (n <= 0) { return hipSuccess; }
     if (K % 1024 != 0) { return hipErrorInvalidValue; }
+    if (K == 7168 && n >= 16) {
+        k_router_gemm<<<dim3((n_exp + 7) / 8, (n + 15) / 16), 256, 0, st>>>(W, x, n, n_exp, logits);
+        return hipGetLastError();
+    }
     k_router_logits<<<dim3(n_exp, (n + RT - 1) / RT), 64, 0, st>>>(W, x, n, n_exp, K, logits);
     return hipGetLastError();
 }

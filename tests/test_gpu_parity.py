@@ -159,6 +159,39 @@ def test_block_prefill512_rows(ctx):
     assert np.array_equal(y.view(np.uint32), ref["y"].view(np.uint32)), "prefill rows not bit-identical (max rel %.3g)" % mx
 
 
+def _prefill_state(ctx, layer, x, mfma):
+    """y and the per-slot intermediates of one batch through the MFMA grouped GEMMs or the per-pass kernels."""
+    n = x.shape[0]
+    ctx.set_prefill_mfma(mfma)
+    ctx.set_debug(True)
+    try:
+        y = ctx.moe_layer(layer, x).clone()
+        ctx.sync()
+        d = ctx.debug()
+        P = d.P
+        out = {"y": y.cpu().numpy(), "h": ctx.d2h(d.h, (P + n, H), np.float32), "o": ctx.d2h(d.o, (P + n, E), np.float32),
+               "g": ctx.d2h(d.g, (P + n, H), np.float32), "u": ctx.d2h(d.u, (P + n, H), np.float32),
+               "hd": ctx.d2h(d.hd, (P + n, H // 256), np.float32), "hq": ctx.d2h(d.hq, (P + n, H), np.int8)}
+    finally:
+        ctx.set_debug(False)
+        ctx.set_prefill_mfma(True)
+    return out
+
+
+@pytest.mark.parametrize("n,hot", [(9, False), (40, False), (512, False), (2048, True)])
+def test_prefill_mfma_matches_per_pass(ctx, n, hot):
+    """The grouped GEMMs on the matrix cores reproduce the per-pass mat-vec kernels bit for bit: gate/up outputs, h and
+    its Q8_K, the down outputs and y (columns of 1..32 slots, the shared expert's full columns, hot experts with many
+    columns)."""
+    hot_ids = list(range(3, 256, 16)) if hot else None
+    layer = make_layer(ctx, seed=900 + n, bias_sigma=0.05, hot=hot_ids)
+    x = make_x(ctx, n, seed=40 + n)
+    ref = _prefill_state(ctx, layer, x, False)
+    got = _prefill_state(ctx, layer, x, True)
+    for k in ref:
+        assert np.array_equal(got[k].view(np.uint8), ref[k].view(np.uint8)), k
+
+
 def test_block_deterministic(ctx, layer):
     x = make_x(ctx, 8, seed=99)
     y1 = ctx.moe_layer(layer, x).clone()
