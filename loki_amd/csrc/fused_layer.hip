@@ -245,7 +245,7 @@ extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, in
         }
     }
     const size_t rows = (size_t) P + n;
-    const bool fused = c->fused && n <= 8 && E == 7168 && H == 2048 && c->n_group <= 64 && decode_ready(c);
+    const bool fused = c->fused && n <= 8 && E == 7168 && H == 2048 && decode_rule_ok(ne, c->n_group) && decode_ready(c);
     const bool mfma = !fused && c->pf_mfma && n > 8 && E == 7168 && H == 2048;
     ALLOC(c, c->xq, (size_t) n * E); ALLOC(c, c->xd, (size_t) n * (E / 256));
     ALLOC(c, c->logits, (size_t) n * ne); ALLOC(c, c->probs, (size_t) n * ne);

@@ -132,7 +132,7 @@ __global__ void __launch_bounds__(WAVES * 64) k_experts(const ExpertArgs a) {
     const int nm = nact + (a.shared ? 1 : 0);
     const int ntasks = nm * NG;
     const int r = lane >> 2, q = lane & 3;
-    const uint32_t rep = lds_addr(lds) | ((uint32_t) (lane & 15) << 3);   // table base (64 KB aligned: the tables open the LDS) | replica
+    const uint32_t rep = tab_word_grid(lds_addr(lds), lane);   // table base (64 KB aligned: the tables open the LDS) | copy
     const uint32_t lq = (uint32_t) q * 4096 + 16 * r, ld = (uint32_t) q * 128 + 2 * r;   // the lane's part of its block addresses
     const size_t dreg = (size_t) (a.R / 64) * G::NB * 4096;                              // d region of a matrix
     // task tk runs on workgroup tk % grid: consecutive tasks spread over all CUs (and XCDs)
@@ -192,7 +192,7 @@ __global__ void __launch_bounds__(WAVES * 64) k_experts(const ExpertArgs a) {
 #define GU8   true,  7,  2, 8,   5, true    // n <= 8
 #define GUP   true,  7,  1, 8,   3, false   // larger batches
 #define DN1   false, 2,  1, 16,  2, false
-#define DN8   false, 2,  2, 16,  2, false
+#define DN8   false, 2,  2, 8,   2, false
 constexpr int XWG_MAX = 8;
 
 template <bool GATEUP, int BPQ, int TT, int WAVES, int PD, bool XWG>
@@ -222,11 +222,12 @@ size_t experts_terms_floats(int, int, int, int) { return 0; }
 
 // the LDS table image (layout at TAB_BYTES in moe_common.h), once, in device memory
 __global__ void k_table_image(uint64_t * img) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;   // 8-byte word: line e = i / 32, slot r = i % 32
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;   // 8-byte word: line i / 32, 8-byte slot i % 32
     if (i >= TAB_BYTES / 8) { return; }
-    const int e = i >> 5, r = i & 31;
-    const uint64_t m = sign_mask64(ksigns8((uint32_t) e & 127u));
-    img[i] = r < 16 ? g_iq2xxs_grid[e] : ((r & 1) ? (m & 0x0101010101010101ull) : m);   // sign entries: {m, m & 0x01..}
+    const int line = i >> 5, r = i & 31;
+    if (line < 256) { img[i] = g_iq2xxs_grid[line]; return; }   // codebook: 32 copies
+    const uint64_t m = sign_mask64(ksigns8((uint32_t) (line - 256)));
+    img[i] = (r & 1) ? (m & 0x0101010101010101ull) : m;          // signs: 16 copies of {m, m & 0x01..}
 }
 hipError_t build_table_image(uint4 * img, hipStream_t st) {
     k_table_image<<<TAB_BYTES / 8 / 256, 256, 0, st>>>(reinterpret_cast<uint64_t *>(img));

@@ -63,14 +63,15 @@ __host__ __device__ inline size_t tiled_d_off(int rg, int j, int row, int R, int
 }
 
 // ---------------------------------------------------------------- LDS tables
-// Entry e (0..255) owns the 256-byte line [256 e, 256 e + 256): 16 copies of the codebook word grid[e] at +0..127 and
-// 8 copies of the 16-byte sign entry of the tiled sign byte e at +128..255 (bit 7 = a scale bit, ignored): the byte
-// masks m (0x00 / 0xFF per weight) and m & 0x01010101 per 4 weights, so applying the signs is one v_xad_u32 per 4
-// weights. Lane l reads copy l % 16 (grid) / l % 8 (signs); the byte address is (index << 8) | copy offset, which one
-// v_perm_b32 builds from the packed index word. A wave64 LDS read costs about the same for 8 and 16 bytes, so the
-// wider sign entry is free. The image is built once per context (build_table_image) and copied into LDS by every
+// Codebook: entry e (0..255) owns the 256-byte line [256 e, 256 e + 256) = 32 copies of grid[e]; lane l reads copy
+// l % 32, so the 32 lanes an LDS pass serves for an 8-byte read always hit 32 different bank pairs. Signs: the 7 stored
+// sign bits b (0..127) own the line at 65536 + 256 b = 16 copies of the 16-byte entry {m, m & 0x01010101 per 4
+// weights} (m = byte masks 0x00 / 0xFF of the 8 signs, parity included), so applying the signs is one v_xad_u32 per 4
+// weights; lane l reads copy l % 16 (16 lanes per pass for 16-byte reads). The byte address is (index << 8) | copy
+// offset, which one v_perm_b32 builds from the packed index word (sign words masked to their 7 stored bits first: bit
+// 7 of each byte is a scale bit). The image is built once per context (build_table_image) and copied into LDS by every
 // workgroup (tables_copy).
-constexpr int TAB_BYTES = 256 * 256;
+constexpr int TAB_GRID = 256 * 256, TAB_BYTES = TAB_GRID + 128 * 256;
 
 __device__ __forceinline__ uint32_t xad(uint32_t a, uint32_t b, uint32_t c) { return (a ^ b) + c; }   // one v_xad_u32
 
@@ -90,9 +91,11 @@ __device__ __forceinline__ uint2 gload8(const void * p) { const u32x2 v = *(cons
 __device__ __forceinline__ float4 gloadf4(const void * p) { const f32x4 v = *(const LK_GLOBAL f32x4 *) p; return make_float4(v.x, v.y, v.z, v.w); }
 __device__ __forceinline__ uint2 lload8(uint32_t addr) { const u32x2 v = *(const LK_LOCAL u32x2 *) (size_t) addr; return make_uint2(v.x, v.y); }
 __device__ __forceinline__ uint4 lload16(uint32_t addr) { const u32x4 v = *(const LK_LOCAL u32x4 *) (size_t) addr; return make_uint4(v.x, v.y, v.z, v.w); }
-// a lane's table words: grid copy (lane % 16) * 8, sign copy 128 + (lane % 8) * 16, over the table base
-__device__ __forceinline__ uint32_t tab_word_grid(uint32_t base, int lane) { return base | ((uint32_t) (lane & 15) << 3); }
-__device__ __forceinline__ uint32_t tab_word_sign(uint32_t base, int lane) { return base | 128u | ((uint32_t) (lane & 7) << 4); }
+// a lane's table words over the table base (64 KB aligned): grid copy (lane % 32) * 8; sign copy (lane % 16) * 16 in
+// the sign half (derived from the grid word)
+__device__ __forceinline__ uint32_t tab_word_grid(uint32_t base, int lane) { return base | ((uint32_t) (lane & 31) << 3); }
+__device__ __forceinline__ uint32_t tab_sign_word(uint32_t tr) { return ((tr & ~255u) + (uint32_t) TAB_GRID) | ((tr & 0x78u) << 1); }
+constexpr uint32_t SIGN_BITS = 0x7f7f7f7fu;   // the stored sign bits of a tiled sign word
 
 // LDS byte address of the table entry for byte L of an index word: byte 1 = that byte; bytes 0, 2, 3 from `tr` = the
 // table base (64 KB aligned) | the lane's replica offset
@@ -106,9 +109,9 @@ __device__ __forceinline__ void iq2_apply(uint2 g, uint4 m, uint32_t & lo, uint3
     lo = xad(g.x, m.x, m.z);
     hi = xad(g.y, m.y, m.w);
 }
-// tr: this lane's table word (base | copy offsets): grid copy in bits 3..6, sign copy in bits 4..6 of the +128 half
+// tr / trs: this lane's grid / sign table words; a1m = a tiled sign word masked with SIGN_BITS
 template <int L> __device__ __forceinline__ uint2 tab_grid(uint32_t a0, uint32_t tr) { return lload8(tab_addr<L>(a0, tr)); }
-template <int L> __device__ __forceinline__ uint4 tab_sign(uint32_t a1t, uint32_t trs) { return lload16(tab_addr<L>(a1t, trs)); }
+template <int L> __device__ __forceinline__ uint4 tab_sign(uint32_t a1m, uint32_t trs) { return lload16(tab_addr<L>(a1m, trs)); }
 
 // 2 * scale nibble + 1 of a tiled sign word (nibble bit l = bit 7 of byte l)
 __device__ __forceinline__ int iq2_scale(uint32_t a1t) {

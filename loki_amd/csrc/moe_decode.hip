@@ -32,8 +32,8 @@ constexpr int DW = 8, DNT = DW * 64;   // waves / threads per workgroup
 constexpr int DMAX_N = 8, DMAX_P = DMAX_N * MAXK;
 constexpr int DMAX_PS = DMAX_P + DMAX_N;   // pair-slots: the shared expert's ceil(n/2) + one per 1-2 tokens of each active expert
 constexpr int SH = NEXP_MAX;           // expert-slot marker of the shared expert
-using GG = Geo<7>;                     // gate/up rows: K = 7168
-using GD = Geo<2>;                     // down rows: K = 2048
+using GG = Geo<7, 0>;                  // gate/up rows: K = 7168 (staged without padding)
+using GD = Geo<2, 0>;                  // down rows: K = 2048
 constexpr int DE = GG::K, DH = GD::K;
 constexpr int GU_ROWS = 8;             // h rows per gate/up task (8 gate + the same 8 up rows)
 constexpr int NGU = DH / GU_ROWS;      // gate/up tasks per expert
@@ -44,18 +44,16 @@ static_assert(DH == DW * QK, "a down unit's wave w quantises h block w");
 static_assert(DMAX_N * (MAXK + 1) * DH <= (int) DEC_TH && DMAX_N * (MAXK + 1) * DE <= (int) DEC_TO, "tagged buffer sizes");
 
 // LDS layout
-constexpr int L_XS = TAB_BYTES;                                   // staged Q8_K tokens (gate/up activations)
-constexpr int L_HS = L_XS + DMAX_N * GG::XROW;                    // staged Q8_K h of the current down unit
-constexpr int HS_BYTES = DMAX_N * GD::XROW;
-constexpr int L_SCR = L_HS;                                       // router sums / selection scratch (phases 1-2) overlay HS
-constexpr int L_RT = L_HS + HS_BYTES;                             // routing tables
+constexpr int L_XS = TAB_BYTES;                                   // staged Q8_K tokens (gate/up), then the h of the down units
+constexpr int L_PRE = L_XS + DMAX_N * GG::XROW;                   // early shared task's block terms [2][7][64] floats
+constexpr int PRE_BYTES = 2 * 7 * 64 * 4;
+constexpr int L_SCR = L_PRE;                                      // router sums [token][quarter] (phase 1) overlay them
+constexpr int L_RT = L_PRE + PRE_BYTES;                           // routing tables
 constexpr int RT_INTS = 4 * DMAX_P + 3 * (DMAX_P + 1) + 1 + 2 * DMAX_PS + 1;
 constexpr int L_CTL = L_RT + RT_INTS * 4;                         // workgroup hand-off words [8], per-wave flags [2][DW]
 constexpr int DEC_LDS = L_CTL + (8 + 2 * DW) * 4;
-constexpr int L_PRE = L_SCR + DW * (NEXP_MAX + 2 * 64) * 4;      // early shared task's block terms [2][7][64] floats
 static_assert(DEC_LDS <= 160 * 1024, "LDS budget");
-static_assert(DMAX_N * 4 * 8 <= HS_BYTES && DW * (NEXP_MAX + 2 * 64) * 4 <= HS_BYTES && 4 * GD::XROW <= HS_BYTES, "scratch overlays");
-static_assert(L_PRE + 2 * 7 * 64 * 4 <= L_HS + HS_BYTES, "early shared task terms overlay the h staging");
+static_assert(DMAX_N * 4 * 8 <= PRE_BYTES, "router sums overlay the early task terms");
 
 typedef LK_LOCAL uint8_t * lds_t;
 typedef LK_CONST DecodeArgs DArgs;   // the launch arguments, read in place with scalar loads
@@ -388,11 +386,15 @@ struct GuStream {
     }
     // one pass (7 steps, one token xr): the row total before * 0.125, folded over the quad in block order; while step s
     // computes, step s + PD of this pass or step s + PD - 7 of the next one (if any) is issued
-    __device__ __forceinline__ float pass(const GuTask & cur, const GuTask & nxt, bool has_next, uint32_t tr, const uint8_t * xr, int q, int r) {
+    // hp: the wave's half of the workgroup. The two waves sharing a SIMD (w, w + 4) swap priority every step, so neither
+    // finishes its stream long before the other (with the default oldest-first arbitration, the younger wave would run
+    // its last steps alone, latency-bound)
+    __device__ __forceinline__ float pass(const GuTask & cur, const GuTask & nxt, bool has_next, uint32_t tr, const uint8_t * xr, int q, int r, int hp) {
 #pragma clang fp contract(off)
         float acc = 0.f;
 #pragma unroll
         for (int s = 0; s < GU_STEPS; ++s) {
+            if ((s & 1) ^ hp) { __builtin_amdgcn_s_setprio(1); } else { __builtin_amdgcn_s_setprio(0); }
             if (s + PD < GU_STEPS) { issue(cur, s + PD); } else if (has_next) { issue(nxt, s + PD - GU_STEPS); }
             const int j = s * 4 + q;
             const int bsum = block_bsum_dpp(pf[s], tr, xr + j * GG::XBLK, r);
@@ -431,10 +433,10 @@ __device__ __forceinline__ int gate_up_stream(const DArgs & a, lds_t lds, const 
     for (int s = 0; s < PD; ++s) { st.issue(cur, s); }
     int npass = 0;
     for (;;) {
-        const float acc = st.pass(cur, nxt, has_next, ln.tr, gu_xrow(a, lds, cur, P), ln.q, ln.r);
+        const float acc = st.pass(cur, nxt, has_next, ln.tr, gu_xrow(a, lds, cur, P), ln.q, ln.r, (int) ((threadIdx.x >> 8) & 1));
         gu_publish(a, ln, cur, acc);
         ++npass;
-        if (!has_next) { break; }
+        if (!has_next) { __builtin_amdgcn_s_setprio(0); break; }
         if (nxt.u == 0) { tk += tstep; }
         cur = nxt;
         has_next = next_pass(cur, nxt);
@@ -630,7 +632,7 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
     LK_LOCAL unsigned * ctl = reinterpret_cast<LK_LOCAL unsigned *>(lds + L_CTL);
     Lane ln;
     ln.r = lane & 15; ln.q = lane >> 4;   // lane 16 q + r: row r, block quarter q
-    ln.tr = lds_addr(dyn_lds) | ((uint32_t) (lane & 15) << 3);   // table base (64 KB aligned: the tables open the LDS) | replica
+    ln.tr = tab_word_grid(lds_addr(dyn_lds), lane);   // table base (64 KB aligned: the tables open the LDS) | copy
 
     // 1. table copy in flight; router (the whole workgroup)
     TRACE(wave, 0);
@@ -653,14 +655,15 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
     lds_arrive(ctl + 0, DW);              // [0] counts the waves whose tokens and table share are in LDS
     TRACE(wave, 1);
     if (wave < n) {
+        // the selecting waves run ahead of the streaming ones on their SIMDs until the dispatch is built
+        __builtin_amdgcn_s_setprio(3);
         float pv[4];
         const bool ok = probs_wait(a, wave, pw, pv);
         TRACE(wave, 3);
         if (!ok) { report(a.err, 2); }
         const RT rt(lds);
-        float * scr = (float *) (lds + L_SCR) + wave * (NEXP_MAX + 2 * 64);
         if (ok) {
-            select_token_p(pv, bv, a.n_exp, a.n_group, a.topk_group, a.topk, a.scale, scr, (int *) (rt.sel + wave * a.topk), (float *) (rt.wts + wave * a.topk));
+            select_token_p<false>(pv, bv, a.n_exp, a.n_group, a.topk_group, a.topk, a.scale, nullptr, (int *) (rt.sel + wave * a.topk), (float *) (rt.wts + wave * a.topk));
         } else if (lane == 0) {
             __hip_atomic_fetch_or(ctl + 3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
@@ -673,11 +676,12 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
             if (lane == 0) { __hip_atomic_store(ctl + 2, all_ok && staged ? 1u : 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
             TRACE(wave, 6);
         }
+        __builtin_amdgcn_s_setprio(0);
     } else if (pre && lds_wait_count(ctl + 0, DW)) {   // the shared expert's pair-slots k: tokens 2k, 2k + 1
         if (n <= 2 && G >= NGU) {
             if (blockIdx.x < NGU) { pre_shared_split(a, lds, ln, wave, P, ctl + 4); }
         } else {
-            gate_up_stream<GU_PD>(a, lds, ln, (wave - n) * G + blockIdx.x, (DW - n) * G, ((n + 1) >> 1) * NGU, true, 0, P, 0);
+            gate_up_stream<GU_PD>(a, lds, ln, blockIdx.x * (DW - n) + (wave - n), (DW - n) * G, ((n + 1) >> 1) * NGU, true, 0, P, 0);
         }
     }
     const unsigned ready = lds_wait(ctl + 2);
@@ -691,7 +695,7 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
     const int nact = *rt.nact, nps = *rt.nps, ps0 = pre ? (n + 1) >> 1 : 0;
     const int t_gu = (nps - ps0) * NGU;
     TRACE(wave, 8);
-    const int ntask = gate_up_stream<GU_PD>(a, lds, ln, wave * G + blockIdx.x, G * DW, t_gu, false, ps0, P, nact);
+    const int ntask = gate_up_stream<GU_PD>(a, lds, ln, blockIdx.x * DW + wave, G * DW, t_gu, false, ps0, P, nact);
     TRACE(wave, 7);
 
     // 4. down units (pair-slot, 256 rows), round-robin over the workgroups: unit u = row group u / nps of pair-slot u % nps
@@ -723,9 +727,15 @@ hipError_t decode_init(int ncu, int * grid) {
     return hipSuccess;
 }
 
+bool decode_rule_ok(int n_exp, int n_group) {   // the selection's DPP group path: 4 experts per lane, 1..16 lanes per group
+    if (n_exp < 1 || n_exp > NEXP_MAX || n_group < 1 || n_exp % n_group) { return false; }
+    const int per = n_exp / n_group, lpg = per / 4;
+    return per % 4 == 0 && lpg >= 1 && lpg <= 16 && (lpg & (lpg - 1)) == 0;
+}
+
 hipError_t launch_moe_decode(const DecodeArgs & a, int grid, bool cooperative, hipStream_t st) {
-    if (a.n < 1 || a.n > DMAX_N || a.topk < 1 || a.topk > MAXK || a.n_exp < 1 || a.n_exp > NEXP_MAX || a.n_group < 1 || a.n_group > 64 ||
-        a.n_exp % a.n_group || a.E != DE || a.H != DH || grid < 1 || !a.th || !a.to || !a.tlogits || !a.txq) {
+    if (a.n < 1 || a.n > DMAX_N || a.topk < 1 || a.topk > MAXK || !decode_rule_ok(a.n_exp, a.n_group) ||
+        a.E != DE || a.H != DH || grid < 1 || !a.th || !a.to || !a.tlogits || !a.txq) {
         return hipErrorInvalidValue;
     }
     if (!cooperative) {   // one workgroup per CU fits the occupancy; co-residency is assumed, waits stay bounded

@@ -49,7 +49,7 @@ __device__ __forceinline__ bool wait_flag(const unsigned * flag, unsigned want) 
 }
 
 // ---------------------------------------------------------------- LDS tables from the prebuilt image
-// the 64 KB table image (layout at TAB_BYTES in moe_common.h) is built once per context in device memory; a workgroup copies it with
+// the table image (layout at TAB_BYTES in moe_common.h) is built once per context in device memory; a workgroup copies it with
 // 16-byte loads, all issued before the first LDS write
 template <int NT>
 __device__ __forceinline__ void tables_copy(uint8_t * lds, const uint4 * img) {
@@ -204,9 +204,11 @@ __device__ __forceinline__ uint32_t q8k_lane(const float (&xs)[4], float & d) {
 // quad hold 4 consecutive blocks of one row at every step. One token's staged activations: per block 256 int8 (+16 B of
 // padding, so the quarters' reads of one instruction fall in different banks) re-ordered so that group l of all 8
 // sub-blocks is contiguous (byte l * 64 + ib * 8 + k = x[ib * 32 + l * 8 + k]), then the NB fp32 block scales.
-template <int BPQ_> struct Geo {
+// PAD: bytes after each staged block (the per-pass kernels' lanes read 4 different blocks at once: 16 bytes of padding
+// put them in different banks; the decode block's lanes read one block at a time and stage without padding)
+template <int BPQ_, int PAD = 16> struct Geo {
     static constexpr int QS = 4, BPQ = BPQ_, RPW = 16, NB = QS * BPQ, K = NB * QK;
-    static constexpr int XBLK = QK + 16, XROW = NB * XBLK + NB * 4;
+    static constexpr int XBLK = QK + PAD, XROW = NB * XBLK + NB * 4;
 };
 // staged byte offset inside a block of the 4 values 4 lane .. 4 lane + 3 (sub-block lane / 8, group (lane % 8) / 2)
 __device__ __forceinline__ int staged_word(int lane) { return ((lane & 7) >> 1) * 64 + (lane >> 3) * 8 + (lane & 1) * 4; }
@@ -251,13 +253,13 @@ __device__ __forceinline__ void lds_visible() {   // this wave's LDS writes are 
 // ---------------------------------------------------------------- one block: integer sums of T tokens
 template <int L, int T>
 __device__ __forceinline__ void group_step(const uint4 (&w)[4], uint32_t tr, const uint8_t * const (&xb)[T], int (&acc)[T][8]) {
-    const uint32_t trs = (tr & ~255u) | 128u | ((tr & 0x38u) << 1);   // the sign copy of this lane: (lane % 8) * 16
+    const uint32_t trs = tab_sign_word(tr);
     uint2 g[8]; uint4 m[8];   // all 16 table reads of the step are issued before the first is used
 #pragma unroll
     for (int ib = 0; ib < 8; ++ib) {
         const uint4 c = w[ib >> 1];
         g[ib] = tab_grid<L>((ib & 1) ? c.z : c.x, tr);
-        m[ib] = tab_sign<L>((ib & 1) ? c.w : c.y, trs);
+        m[ib] = tab_sign<L>(((ib & 1) ? c.w : c.y) & SIGN_BITS, trs);
     }
     int4 xv[T][4];
 #pragma unroll
@@ -332,13 +334,13 @@ __device__ __forceinline__ void dot_ib_dpp(const uint2 (&g)[8], const uint4 (&m)
 }
 template <int L>
 __device__ __forceinline__ void group_step_dpp(const uint4 (&w)[4], uint32_t tr, const uint32_t (&xq)[4], int (&acc)[8]) {
-    const uint32_t trs = (tr & ~255u) | 128u | ((tr & 0x38u) << 1);
+    const uint32_t trs = tab_sign_word(tr);
     uint2 g[8]; uint4 m[8];
 #pragma unroll
     for (int ib = 0; ib < 8; ++ib) {
         const uint4 c = w[ib >> 1];
         g[ib] = tab_grid<L>((ib & 1) ? c.z : c.x, tr);
-        m[ib] = tab_sign<L>((ib & 1) ? c.w : c.y, trs);
+        m[ib] = tab_sign<L>(((ib & 1) ? c.w : c.y) & SIGN_BITS, trs);
     }
     dot_ib_dpp<L, 0>(g, m, xq, acc);
 }
@@ -486,6 +488,8 @@ __device__ __forceinline__ void load_bias(const float * bias, int n_exp, float (
     for (int j = 0; j < 4; ++j) { b[j] = 4 * lane + j < n_exp ? gptr(bias)[4 * lane + j] : 0.f; }
 }
 // the rule from the lane's 4 probabilities p[j] = sigmoid(logit) of experts 4 lane + j
+// SCRATCH = false: the caller guarantees the DPP group path (decode_rule_ok) and passes no scratch
+template <bool SCRATCH = true>
 __device__ __forceinline__ void select_token_p(const float (&p)[4], const float (&bias)[4], int n_exp, int n_group, int topk_group, int topk,
                                                float scale, float * scr, int * sel_out, float * w_out) {
 #pragma clang fp contract(off)
@@ -515,6 +519,9 @@ __device__ __forceinline__ void select_token_p(const float (&p)[4], const float 
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) { ok[j] = 4 * lane + j < n_exp && rank < topk_group; }
+    } else if constexpr (!SCRATCH) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { ok[j] = false; }   // not reached (the caller checked the rule)
     } else {
         float * cs = scr; float * gsc = scr + n_exp; int * allow = reinterpret_cast<int *>(scr + n_exp + n_group);
 #pragma unroll

@@ -40,7 +40,7 @@ struct ExpertArgs {
 // persistent launches: grid = workgroups (one per CU); experts_init sets the LDS limit once per process
 hipError_t experts_init();
 size_t experts_terms_floats(int nmat, int slots, int R, int K);
-// the 64 KB image of the codebook / sign-mask LDS tables (TAB_BYTES), built once per context
+// the image of the codebook / sign-mask LDS tables (TAB_BYTES, 96 KB), built once per context
 hipError_t build_table_image(uint4 * img, hipStream_t st);
 hipError_t launch_experts_gateup(const ExpertArgs & a, int grid, hipStream_t st);
 hipError_t launch_experts_down(const ExpertArgs & a, int grid, hipStream_t st);
@@ -65,6 +65,8 @@ struct DecodeArgs {
 constexpr size_t DEC_TLOGITS = 8 * 256, DEC_TXQ = (size_t) 8 * 28 * 65, DEC_TH = (size_t) 8 * (MAXK + 1) * 2048,
                  DEC_TO = (size_t) 8 * (MAXK + 1) * 7168;
 hipError_t decode_init(int ncu, int * grid);
+// routing rules the decode block supports (its selection keeps the group scores in registers)
+bool decode_rule_ok(int n_exp, int n_group);
 size_t decode_lds_bytes();
 // grid workgroups (at most one per CU can be resident): a cooperative launch guarantees they are all resident; a
 // regular launch assumes it (nothing else running on the CUs) -- a violation ends in a reported wait timeout
