@@ -9,7 +9,7 @@ timed region. Each step takes a fresh x (so different experts) and the steps rot
 layers (3 x 2.9 GB), so the 256 MB MALL cannot serve repeated weights.
 
 Prints ONE JSON line: value = microseconds per token of the whole block (router, dispatch, experts, combine), plus the
-achieved HBM bandwidth, the roofline of the dominant kernel (decode: k_moe_decode, the whole block in one cooperative
+achieved HBM bandwidth, the roofline of the dominant kernel (decode: k_moe_decode, the whole block in one
 launch; prefill: the gate/up expert kernel), timed live with HIP events recorded on the stream the kernel runs on, and
 the CPU checker timed on this host's cores on a bounded sample of the same workload.
 """
@@ -153,7 +153,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the decode-1 / prefill-512 side measurements")
     ap.add_argument("--fused", type=int, default=None, choices=(0, 1, 2),
-                    help="decode path: 1 cooperative single launch (library default), 2 regular single launch, 0 per pass")
+                    help="decode path: 2 regular single launch (library default), 1 cooperative single launch, 0 per pass")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (the reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
@@ -172,8 +172,9 @@ def main():
     if res["fused"]:   # one launch = the whole block: its bytes are the step's
         kname, k_ms, k_bytes = "k_moe_decode", res["stage_ms"]["gate_up"], res["bytes"]
         stages = {"block": k_ms}
-    else:
-        kname, k_ms, k_bytes = "k_experts<gate_up>", res["stage_ms"]["gate_up"], res["gu_bytes"]
+    else:   # per-pass launches: the gate/up stage (grouped GEMM on MFMA above 8 tokens, else the mat-vec kernel)
+        kname = "k_pf_gemm<gate_up>" if n > 8 else "k_experts<gate_up>"
+        k_ms, k_bytes = res["stage_ms"]["gate_up"], res["gu_bytes"]
         stages = res["stage_ms"]
     k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
     log("[bench] %s: %.1f us/step, %.2f us/token, %.0f GB/s (U=%.1f); kernel %s %.1f us (%.0f GB/s); stages (us): %s" % (

@@ -127,9 +127,10 @@ typedef struct FLDebug {
 } FLDebug;
 int fl_debug(FLCtx *, FLDebug * out);
 int fl_set_debug(FLCtx *, int capture_gate_up);
-/* decode batches (n <= 8, E 7168, H 2048) of fl_moe_layer: 1 (default) = the whole block as one cooperative launch;
- * 2 = the same kernel with a regular launch (assumes nothing else occupies the CUs: waits are bounded and report a
- * timeout through fl_sync otherwise); 0 = one launch per pass */
+/* decode batches (n <= 8, E 7168, H 2048) of fl_moe_layer: 2 (default) = the whole block as one regular launch of one
+ * workgroup per CU (assumes nothing else occupies the CUs, as in a single-stream engine: every device-wide wait is
+ * bounded and reports a timeout through fl_sync otherwise); 1 = the same kernel as a cooperative launch (residency
+ * guaranteed by the runtime, ~18 us more per call at batch 1); 0 = one launch per pass */
 int fl_set_fused(FLCtx *, int mode);
 /* batches above the decode sizes (n > 8, E 7168, H 2048): 1 (default) = the expert products as grouped GEMMs on the
  * matrix cores (no counterpart in the reference, whose wide path is tc_matvec per arena batch, src/fused_layer.cu:540-561);

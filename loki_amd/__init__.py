@@ -201,7 +201,7 @@ class Context:
         self.check(lib().fl_set_prefill_mfma(self.ctx, 1 if on else 0))
 
     def set_fused(self, mode):
-        """Decode batches (n <= 8): 1 / True = one cooperative launch (default), 2 = the same kernel with a regular
+        """Decode batches (n <= 8): 2 = one regular launch (default), 1 / True = the same kernel as a cooperative
         launch, 0 / False = one launch per pass."""
         self.check(lib().fl_set_fused(self.ctx, int(mode)))
 
