@@ -50,7 +50,7 @@ struct FLCtx {
     DBuf<float> terms; DBuf<unsigned> cnt;   // per-pass expert kernels: (unused) term scratch, self-resetting counters
     DBuf<uint4> tab;                         // LDS table image (build_table_image)
     // single-launch decode block: epoch-tagged logits / h / o, wait-timeout word; fused = 0 forces the per-pass kernels
-    DBuf<int> derr; DBuf<uint64_t> dlogit, dtxq, dth, dto; unsigned epoch = 0; int fused = 2; int dec_grid = -1;
+    DBuf<int> derr; DBuf<uint64_t> dlogit, dth, dto; unsigned epoch = 0; int fused = 2; int dec_grid = -1;
     // prefill grouped GEMM on MFMA (batches above the decode sizes): fp16 table image, columns, fp16 activation copies
     int pf_mfma = 1, pf_ready = 0; DBuf<uint4> ptab; DBuf<int4> pcols; DBuf<int> pncols; DBuf<_Float16> xh, hh;
     struct Compat * compat = nullptr;          // reference-API state (compat.hip), created on first use

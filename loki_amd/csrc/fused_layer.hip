@@ -42,7 +42,7 @@ extern "C" void fl_free(FLCtx * c) {
     c->h.release(); c->hd.release(); c->o.release(); c->g.release(); c->u.release();
     c->sel.release(); c->counts.release(); c->offsets.release(); c->perm.release(); c->inv.release(); c->act.release(); c->nact.release();
     compat_free(c); c->zero_i.release(); c->terms.release(); c->cnt.release();
-    c->tab.release(); c->derr.release(); c->dlogit.release(); c->dtxq.release(); c->dth.release(); c->dto.release();
+    c->tab.release(); c->derr.release(); c->dlogit.release(); c->dth.release(); c->dto.release();
     c->ptab.release(); c->pcols.release(); c->pncols.release(); c->xh.release(); c->hh.release();
     for (auto & v : c->ev_free) { for (auto e : v) { (void) hipEventDestroy(e); } }
     for (auto & v : c->ev_pending) { for (auto e : v) { (void) hipEventDestroy(e); } }
@@ -259,13 +259,12 @@ extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, in
     std::vector<hipEvent_t> * ev = prof_begin(c);
     if (fused) {
         if (!c->derr.p) {
-            ALLOC(c, c->derr, 1); ALLOC(c, c->dlogit, DEC_TLOGITS); ALLOC(c, c->dtxq, DEC_TXQ); ALLOC(c, c->dth, DEC_TH); ALLOC(c, c->dto, DEC_TO);
+            ALLOC(c, c->derr, 1); ALLOC(c, c->dlogit, DEC_TLOGITS); ALLOC(c, c->dth, DEC_TH); ALLOC(c, c->dto, DEC_TO);
             TRY(c, hipMemsetAsync(c->derr.p, 0, sizeof(int), st));
         }
         if (++c->epoch == 0) { c->epoch = 1; }   // epoch 0 is the cleared state of the tagged words
         if (c->epoch == 1) {   // first use, or the epoch wrapped: no stale word may carry the new epoch
             TRY(c, hipMemsetAsync(c->dlogit.p, 0, DEC_TLOGITS * sizeof(uint64_t), st));
-            TRY(c, hipMemsetAsync(c->dtxq.p, 0, DEC_TXQ * sizeof(uint64_t), st));
             TRY(c, hipMemsetAsync(c->dth.p, 0, DEC_TH * sizeof(uint64_t), st));
             TRY(c, hipMemsetAsync(c->dto.p, 0, DEC_TO * sizeof(uint64_t), st));
         }
@@ -278,7 +277,7 @@ extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, in
         d.E = E; d.H = H;
         d.xq = c->xq.p; d.xd = c->xd.p; d.logits = c->logits.p; d.probs = c->probs.p; d.sel = c->sel.p; d.wts = c->wts.p;
         d.counts = c->counts.p; d.offsets = c->offsets.p; d.perm = c->perm.p; d.inv = c->inv.p; d.act = c->act.p; d.nact = c->nact.p;
-        d.tlogits = c->dlogit.p; d.txq = c->dtxq.p; d.th = c->dth.p; d.to = c->dto.p; d.y = y;
+        d.tlogits = c->dlogit.p; d.th = c->dth.p; d.to = c->dto.p; d.y = y;
         d.epoch = c->epoch; d.err = c->derr.p;
         // stages: the whole block is one launch, reported as stage 4; the others are empty
         for (int i = 0; i <= 4; ++i) { prof_mark(c, ev, i); }

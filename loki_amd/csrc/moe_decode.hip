@@ -7,13 +7,13 @@
 //   1. on entry every workgroup starts the direct global->LDS copy of the codebook/sign table image; workgroup b then
 //      computes the router logits of expert b for every token (the fp64 chunk-and-tree contract) and publishes each
 //      probability sigmoid(logit) as an epoch-tagged 64-bit word;
-//      Each token block is quantised to Q8_K once (by one workgroup) and published as epoch-tagged words;
-//   2. wave t of every workgroup issues its poll of token t's tagged probabilities, all waves gather the Q8_K token
-//      blocks into LDS, then wave t selects token t's experts and the last selecting wave builds the dispatch (stable
+//   2. wave t of every workgroup issues its poll of token t's tagged probabilities, all waves quantise the token blocks
+//      to Q8_K into LDS (every workgroup from x, which its router pass left in L2), then wave t selects token t's
+//      experts and the last selecting wave builds the dispatch (stable
 //      counting sort of the n * topk pairs) in its own LDS -- redundant, but cheaper than another device-wide hand-off.
 //      Waves without a token meanwhile run the shared expert's gate/up tasks (no routing needed);
-//   3. gate/up tasks round-robin over all waves of the grid: a task computes 8 gate rows and the same 8 up rows of one
-//      expert for its tokens and publishes h = silu(g) * u as epoch-tagged words;
+//   3. gate/up tasks: a task computes 8 gate rows and the same 8 up rows of one expert for its tokens and publishes
+//      h = silu(g) * u as epoch-tagged words; a workgroup's 8 waves take 8 consecutive tasks (one 64-row group);
 //   4. down units round-robin over the workgroups: a unit is 256 output rows of one expert (32 per wave). The waves
 //      issue their weight loads first, then wave w polls the tagged h of Q8_K block w for every token of the expert and
 //      quantises it into LDS; after a barrier each wave computes its rows and publishes o as epoch-tagged words;
@@ -148,59 +148,42 @@ __device__ __forceinline__ void tables_dma(lds_t lds, const uint4 * img, int wav
     }
 }
 
-// Q8_K of the token blocks k = t * NB + j: block k by workgroup k % G (wave k / G % DW), published as 65 epoch-tagged
-// words (word l = the 4 packed int8 of values 4l .. 4l + 3, word 64 = the scale); the quantising workgroup also writes
-// the layer's xq / xd
-__device__ __forceinline__ void quant_publish(const DArgs & a, int wave) {
-    const int G = gridDim.x, nblk = a.n * GG::NB, lane = lane_id();
-    for (int k = blockIdx.x + G * wave; k < nblk; k += G * DW) {
-        const int t = k / GG::NB, j = k % GG::NB;
-        const float4 v = gloadf4(a.x + (size_t) t * DE + (size_t) j * QK + 4 * lane);
-        const float xs[4] = { v.x, v.y, v.z, v.w };
-        float d; const uint32_t packed = q8k_lane(xs, d);
-        st_tag(a.txq + (size_t) k * 65 + lane, a.epoch, __builtin_bit_cast(float, packed));
-        if (lane == 0) { st_tag(a.txq + (size_t) k * 65 + 64, a.epoch, d); }
-        gptr(reinterpret_cast<uint32_t *>(a.xq + (size_t) t * DE + (size_t) j * QK))[lane] = packed;
-        if (lane == 0) { gptr(a.xd)[k] = d; }
-    }
-}
-// every token block into this workgroup's LDS (staged layout): wave w gathers blocks w, w + DW, .., up to GB at a time;
-// false if a wait timed out
-__device__ __forceinline__ bool gather_tokens(const DArgs & a, lds_t lds, int wave) {
-    constexpr int GB = 14;
-    const int nblk = a.n * GG::NB, lane = lane_id();
-    for (int k0 = wave; k0 < nblk; k0 += DW * GB) {
-        uint64_t wq[GB], wd[GB];
-        auto issue = [&]() {
+// Q8_K of every token block into this workgroup's LDS (staged layout): a pass of wave w quantises 4 consecutive
+// blocks, one per 16-lane row (q8k_row16); the wave's passes (up to 7) load first, then compute. x is in L2 after the
+// router's reads. Workgroup 0 also writes the layer's xq / xd.
+__device__ __forceinline__ void local_quant(const DArgs & a, lds_t lds, int wave) {
+    constexpr int MAXP = DMAX_N * GG::NB / (4 * DW);
+    static_assert(GG::NB % 4 == 0 && MAXP * 4 * DW == DMAX_N * GG::NB, "four blocks per pass");
+    const int nblk = a.n * GG::NB, lane = lane_id(), i = lane & 15;
+    float xs[MAXP][16];
 #pragma unroll
-            for (int b = 0; b < GB; ++b) {
-                const int k = k0 + b * DW;
-                if (k < nblk) { wq[b] = ld_tag(a.txq + (size_t) k * 65 + lane); wd[b] = ld_tag(a.txq + (size_t) k * 65 + 64); }
-            }
-        };
-        issue();
-        int it = 0;
-        for (; it < POLL_MAX; ++it) {
-            bool v = true;
+    for (int p = 0; p < MAXP; ++p) {
+        const int k = 4 * (wave + DW * p) + (lane >> 4);
+        if (4 * (wave + DW * p) < nblk) {
+            const float * src = a.x + (size_t) (k / GG::NB) * DE + (size_t) (k % GG::NB) * QK + 16 * i;
 #pragma unroll
-            for (int b = 0; b < GB; ++b) { v = v && (k0 + b * DW >= nblk || (tag_ok(wq[b], a.epoch) && tag_ok(wd[b], a.epoch))); }
-            if (__ballot(!v) == 0) { break; }
-            __builtin_amdgcn_s_sleep(1);
-            issue();
-        }
-        if (it == POLL_MAX) { return false; }
-#pragma unroll
-        for (int b = 0; b < GB; ++b) {
-            const int k = k0 + b * DW;
-            if (k < nblk) {
-                lds_t row = lds + L_XS + (k / GG::NB) * GG::XROW;
-                const int j = k % GG::NB;
-                *reinterpret_cast<LK_LOCAL uint32_t *>(row + j * GG::XBLK + staged_word(lane)) = (uint32_t) wq[b];
-                if (lane == 0) { reinterpret_cast<LK_LOCAL float *>(row + GG::NB * GG::XBLK)[j] = tag_val(wd[b]); }
+            for (int q = 0; q < 4; ++q) {
+                const float4 v = gloadf4(src + 4 * q);
+                xs[p][4 * q] = v.x; xs[p][4 * q + 1] = v.y; xs[p][4 * q + 2] = v.z; xs[p][4 * q + 3] = v.w;
             }
         }
     }
-    return true;
+#pragma unroll
+    for (int p = 0; p < MAXP; ++p) {
+        if (4 * (wave + DW * p) < nblk) {
+            const int k = 4 * (wave + DW * p) + (lane >> 4), t = k / GG::NB, j = k % GG::NB;
+            uint32_t packed[4]; float d;
+            q8k_row16(xs[p], packed, d);
+            lds_t row = lds + L_XS + t * GG::XROW;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) { *reinterpret_cast<LK_LOCAL uint32_t *>(row + j * GG::XBLK + staged_word(4 * i + w)) = packed[w]; }
+            if (i == 0) { reinterpret_cast<LK_LOCAL float *>(row + GG::NB * GG::XBLK)[j] = d; }
+            if (blockIdx.x == 0) {
+                *(LK_GLOBAL u32x4 *) (a.xq + (size_t) t * DE + (size_t) j * QK + 16 * i) = u32x4{ packed[0], packed[1], packed[2], packed[3] };
+                if (i == 0) { gptr(a.xd)[k] = d; }
+            }
+        }
+    }
 }
 
 // Router logits of expert e for all n tokens by the whole workgroup (the contract of moe_device.h: 256 in-order chunk
@@ -641,7 +624,6 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
     tables_dma(lds, a.tab, wave);
     __syncthreads();   // the hand-off words are clear
     for (int e = blockIdx.x; e < a.n_exp; e += G) { router_phase(a, lds, wave, e); }
-    quant_publish(a, wave);
     TRACE(wave, 2);
 
     // 2. wave t polls token t's probabilities while all waves quantise the tokens; wave t then selects token t's experts
@@ -650,7 +632,9 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
     const bool pre = n < DW;
     float bv[4]; uint64_t pw[4];
     if (wave < n) { load_bias(a.bias, a.n_exp, bv); probs_issue(a, wave, pw); }
-    if (!gather_tokens(a, lds, wave)) { report(a.err, 64); }
+    TRACE(wave, 9);
+    local_quant(a, lds, wave);
+    TRACE(wave, 10);
     __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's table loads have landed in LDS
     lds_arrive(ctl + 0, DW);              // [0] counts the waves whose tokens and table share are in LDS
     TRACE(wave, 1);
@@ -689,8 +673,8 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
     // a failed routing wait leaves every later phase without its inputs: all waves leave (the error is reported)
     if (ready != 1) { if (ready == 0) { report(a.err, 8); } return; }
 
-    // 3. gate/up tasks (pair-slot, 8 h rows), round-robin over every wave of the grid (task tk on workgroup tk % G,
-    //    wave tk / G % DW); the shared expert's pair-slots come first unless the early tasks covered them
+    // 3. gate/up tasks (pair-slot, 8 h rows): task tk on workgroup tk / DW % G, wave tk % DW, so a workgroup streams
+    //    whole 64-row groups; the shared expert's pair-slots come first unless the early tasks covered them
     const RT rt(lds);
     const int nact = *rt.nact, nps = *rt.nps, ps0 = pre ? (n + 1) >> 1 : 0;
     const int t_gu = (nps - ps0) * NGU;
@@ -735,7 +719,7 @@ bool decode_rule_ok(int n_exp, int n_group) {   // the selection's DPP group pat
 
 hipError_t launch_moe_decode(const DecodeArgs & a, int grid, bool cooperative, hipStream_t st) {
     if (a.n < 1 || a.n > DMAX_N || a.topk < 1 || a.topk > MAXK || !decode_rule_ok(a.n_exp, a.n_group) ||
-        a.E != DE || a.H != DH || grid < 1 || !a.th || !a.to || !a.tlogits || !a.txq) {
+        a.E != DE || a.H != DH || grid < 1 || !a.th || !a.to || !a.tlogits) {
         return hipErrorInvalidValue;
     }
     if (!cooperative) {   // one workgroup per CU fits the occupancy; co-residency is assumed, waits stay bounded

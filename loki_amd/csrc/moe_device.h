@@ -199,6 +199,39 @@ __device__ __forceinline__ uint32_t q8k_lane(const float (&xs)[4], float & d) {
     return packed;
 }
 
+// Q8_K of four blocks at once, one per 16-lane row: lane 16 m + i holds values 16 i .. 16 i + 15 of row m's block. The
+// operations and tie rules are q8k_lane's (largest |x|, its first occurrence's signed value; q = min(127,
+// round-half-even(iscale * x)), d = 1 / iscale), with the reductions inside the row: max of |x| by DPP, then the lowest
+// lane holding it (DPP min), whose value ds_bpermute fetches. packed[w] = values 16 i + 4 w .. + 3; d = the row's scale.
+__device__ __forceinline__ void q8k_row16(const float (&xs)[16], uint32_t (&packed)[4], float & d) {
+#pragma clang fp contract(off)
+    const int lane = lane_id(), i = lane & 15;
+    float ba = -1.f, bv = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) { const float ax = fabsf(xs[k]); if (ax > ba) { ba = ax; bv = xs[k]; } }
+    uint32_t mk = __builtin_bit_cast(uint32_t, ba);
+    mk = umax32(mk, dpp<DPP_XOR1>(mk)); mk = umax32(mk, dpp<DPP_XOR2>(mk));
+    mk = umax32(mk, dpp<DPP_HALF_MIRROR>(mk)); mk = umax32(mk, dpp<DPP_MIRROR>(mk));
+    uint32_t c = __builtin_bit_cast(uint32_t, ba) == mk ? (uint32_t) i : 16u;
+    c = min(c, dpp<DPP_XOR1>(c)); c = min(c, dpp<DPP_XOR2>(c));
+    c = min(c, dpp<DPP_HALF_MIRROR>(c)); c = min(c, dpp<DPP_MIRROR>(c));
+    const float vmax = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((int) (((lane & 48) | c) * 4), __builtin_bit_cast(int, bv)));
+    const bool nz = __builtin_bit_cast(float, mk) > 0.f;
+    const float iscale = -127.f / (nz ? vmax : 1.f);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        uint32_t pk = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const float p = iscale * xs[4 * w + b];
+            int iv = (int) rintf(p); iv = iv < 127 ? iv : 127;
+            pk |= ((uint32_t) (iv & 0xff)) << (8 * b);
+        }
+        packed[w] = nz ? pk : 0u;
+    }
+    d = nz ? 1.f / iscale : 0.f;
+}
+
 // ---------------------------------------------------------------- staged activations
 // BPQ blocks per K quarter (4 quarters); lane 4 r + q of a task owns row r and blocks j = 4 jj + q, so the 4 lanes of a
 // quad hold 4 consecutive blocks of one row at every step. One token's staged activations: per block 256 int8 (+16 B of

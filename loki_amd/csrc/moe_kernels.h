@@ -55,14 +55,14 @@ struct DecodeArgs {
     int E, H;                                        // 7168, 2048 (the kernel's geometry)
     int8_t * xq; float * xd;                         // Q8_K of x (written by workgroup 0)
     float * logits, * probs; int * sel; float * wts; int * counts, * offsets, * perm, * inv, * act, * nact;
-    // epoch-tagged words {epoch << 32 | 32-bit payload}: probabilities [n][n_exp], Q8_K token blocks [n][E/256][65]
-    // (64 words of 4 packed int8, then the scale), h [P+n][H] and o [P+n][E] per dispatch slot
-    uint64_t * tlogits, * txq, * th, * to;
+    // epoch-tagged words {epoch << 32 | 32-bit payload}: probabilities [n][n_exp], h [P+n][H] and o [P+n][E] per
+    // dispatch slot
+    uint64_t * tlogits, * th, * to;
     float * y;                                       // [n][E]
     unsigned epoch; int * err;
 };
 // sizes (64-bit words) of the tagged buffers for any n <= 8 (topk <= MAXK)
-constexpr size_t DEC_TLOGITS = 8 * 256, DEC_TXQ = (size_t) 8 * 28 * 65, DEC_TH = (size_t) 8 * (MAXK + 1) * 2048,
+constexpr size_t DEC_TLOGITS = 8 * 256, DEC_TH = (size_t) 8 * (MAXK + 1) * 2048,
                  DEC_TO = (size_t) 8 * (MAXK + 1) * 7168;
 hipError_t decode_init(int ncu, int * grid);
 // routing rules the decode block supports (its selection keeps the group scores in registers)
