@@ -274,10 +274,8 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
                 for (int t = 0; t < 8; t += 2) {
                     lookup(t + 1, kb);
                     compute(t, ka);
-                    __builtin_amdgcn_sched_barrier(0);
                     if (t + 2 < 8) { lookup(t + 2, ka); }
                     compute(t + 1, kb);
-                    __builtin_amdgcn_sched_barrier(0);
                 }
                 // block fold, in block order: y += (d_w * d_x) * bsum
                 const f4 dx0 = *(const LK_LOCAL f4 *) (size_t) ((uint32_t) (L_PB + buf * PB_BUF + PB_DX) + 16 * ln.g);
