@@ -33,6 +33,7 @@ WORKLOADS = {
     "prefill512": (512, 0.05, 0, "prefill-512: one MoE layer, 512 tokens"),
     "prefill2048": (2048, 0.05, 16, "prefill-2048: one MoE layer, 2048 tokens, 16 hot experts (+0.5 bias)"),
 }
+STACK_LAYERS = 58   # configs[3]: DeepSeek-R1's MoE layers, every expert of every layer resident (~169 GB)
 
 
 def log(*a):
@@ -107,6 +108,58 @@ def run_workload(ctx, torch, name, steps, warmup, copies, seed=20260101):
     return res
 
 
+def run_stack(ctx, torch, steps, warmup, nlayers=STACK_LAYERS, seed=20260301):
+    """one token through nlayers independently seeded MoE layers, x_{L+1} = RMSNorm(y_L) (weights 1,
+    eps 1e-6). A step is the whole chain for one fresh x; bytes = nlayers x the decode-1 bytes of a layer."""
+    from loki_amd import MoeLayerWeights
+    t0 = time.perf_counter()
+    layers = [MoeLayerWeights.synthetic(ctx, seed + 1000 * L, bias_sigma=0.01) for L in range(nlayers)]
+    torch.cuda.synchronize()
+    t_synth = time.perf_counter() - t0
+    xs = []
+    for i in range(steps + warmup):
+        x = torch.empty((1, E), dtype=torch.float32, device="cuda")
+        ctx.synth_normal(x, seed + 17, 2000 + i, 0.0, 1.0)
+        xs.append(x)
+    y = torch.empty((1, E), dtype=torch.float32, device="cuda")
+    xn = torch.empty((1, E), dtype=torch.float32, device="cuda")
+
+    def token(x):
+        cur = x
+        for L in layers:
+            ctx.moe_layer(L, cur, y)
+            ctx.rmsnorm(y, None, 1e-6, out=xn)
+            cur = xn
+
+    for i in range(warmup):
+        token(xs[i])
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        token(xs[warmup + i])
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    ctx.stage_ms(reset=True)
+    ctx.set_profile(True)
+    for i in range(steps):
+        token(xs[warmup + i])
+    ctx.set_profile(False)
+    calls, stage = ctx.stage_ms(reset=True)
+    k_us = stage["gate_up"] / max(calls, 1) * 1e3 if ctx.debug().fused else None
+    nbytes = nlayers * step_bytes(1, 8)
+    del layers
+    torch.cuda.empty_cache()
+    return {"layers": nlayers, "us_per_token": round(ms * 1e3, 1), "ms_per_step": round(ms, 4),
+            "bytes_per_token": nbytes, "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "us_per_layer": round(ms * 1e3 / nlayers, 2),
+            "kernel_us_per_layer": round(k_us, 2) if k_us is not None else None,
+            "resident_weight_gb": round(nlayers * (257 * EXPERT_BYTES + ROUTER_BYTES) / 1e9, 1),
+            "synth_s": round(t_synth, 1)}
+
+
 def cpu_baseline(ctx, torch, res, budget_s=12.0, max_steps=8):
     """The CPU checker (oracle/, restated ggml CPU semantics) on this host's cores, on a bounded sample of the same
     workload: the first steps' x with the experts they select, timed around the oracle call only."""
@@ -152,6 +205,8 @@ def main():
     ap.add_argument("--copies", type=int, default=3, help="independently seeded layers rotated over the steps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the decode-1 / prefill-512 side measurements")
+    ap.add_argument("--no-stack", action="store_true", help="skip the 58-layer resident stack (configs[3], ~169 GB)")
+    ap.add_argument("--stack-steps", type=int, default=10)
     ap.add_argument("--fused", type=int, default=None, choices=(0, 1, 2),
                     help="decode path: 2 regular single launch (library default), 1 cooperative single launch, 0 per pass")
     ap.add_argument("--copy-probe", action="store_true",
@@ -200,6 +255,10 @@ def main():
                          "stage_us": None if r["fused"] else {k: round(v * 1e3, 2) for k, v in r["stage_ms"].items()}}
             log("[bench] %s: %s" % (wl, json.dumps(extra[wl])))
             del r
+    if not args.no_stack:
+        torch.cuda.empty_cache()
+        extra["stack58"] = run_stack(ctx, torch, args.stack_steps, 2)
+        log("[bench] stack58: %s" % json.dumps(extra["stack58"]))
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(ctx, torch, res)

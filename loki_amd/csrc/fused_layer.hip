@@ -258,10 +258,8 @@ extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, in
     hipStream_t st = c->st;
     std::vector<hipEvent_t> * ev = prof_begin(c);
     if (fused) {
-        if (!c->derr.p) {
-            ALLOC(c, c->derr, 1); ALLOC(c, c->dlogit, DEC_TLOGITS); ALLOC(c, c->dth, DEC_TH); ALLOC(c, c->dto, DEC_TO);
-            TRY(c, hipMemsetAsync(c->derr.p, 0, sizeof(int), st));
-        }
+        if (!c->derr.p) { ALLOC(c, c->derr, 1); TRY(c, hipMemsetAsync(c->derr.p, 0, sizeof(int), st)); }
+        if (!c->dlogit.p) { ALLOC(c, c->dlogit, DEC_TLOGITS); ALLOC(c, c->dth, DEC_TH); ALLOC(c, c->dto, DEC_TO); c->epoch = 0; }
         if (++c->epoch == 0) { c->epoch = 1; }   // epoch 0 is the cleared state of the tagged words
         if (c->epoch == 1) {   // first use, or the epoch wrapped: no stale word may carry the new epoch
             TRY(c, hipMemsetAsync(c->dlogit.p, 0, DEC_TLOGITS * sizeof(uint64_t), st));

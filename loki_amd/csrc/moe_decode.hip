@@ -12,12 +12,12 @@
 //      experts and the last selecting wave builds the dispatch (stable
 //      counting sort of the n * topk pairs) in its own LDS -- redundant, but cheaper than another device-wide hand-off.
 //      Waves without a token meanwhile run the shared expert's gate/up tasks (no routing needed);
-//   3. gate/up tasks: a task computes 8 gate rows and the same 8 up rows of one expert for its tokens and publishes
+//   3. gate/up tasks: a task computes 8 gate rows and the same 8 up rows of one expert for one token and publishes
 //      h = silu(g) * u as epoch-tagged words; a workgroup's 8 waves take 8 consecutive tasks (one 64-row group);
-//   4. down units round-robin over the workgroups: a unit is 256 output rows of one expert (32 per wave). The waves
-//      issue their weight loads first, then wave w polls the tagged h of Q8_K block w for every token of the expert and
-//      quantises it into LDS; after a barrier each wave computes its rows and publishes o as epoch-tagged words;
-//   5. combine units (256 rows each): y = sum_k w_k o_k (k order) + shared, from the tagged o words.
+//   4. down units round-robin over the workgroups: a unit is 256 output rows of one expert for one token (32 per wave).
+//      The waves issue their first weight loads, then wave w polls the tagged h of Q8_K block w and quantises it into
+//      LDS; after a barrier each wave computes its rows and publishes o as epoch-tagged words;
+//   5. combine units (256 rows each) on the last workgroups: y = sum_k w_k o_k (k order) + shared, from the tagged o words.
 // No counter, flag or store-completion wait sits between producer and consumer: a consumer polls the data words
 // themselves, and a word is valid once it carries this launch's epoch (stale words hold older epochs; the host clears
 // the tagged buffers whenever the epoch restarts at 1). Arithmetic is that of the per-pass kernels (same device
@@ -30,7 +30,7 @@ namespace lk {
 
 constexpr int DW = 8, DNT = DW * 64;   // waves / threads per workgroup
 constexpr int DMAX_N = 8, DMAX_P = DMAX_N * MAXK;
-constexpr int DMAX_PS = DMAX_P + DMAX_N;   // pair-slots: the shared expert's ceil(n/2) + one per 1-2 tokens of each active expert
+constexpr int DMAX_PS = DMAX_P + DMAX_N;   // task slots: the shared expert's n + one per routed pair
 constexpr int SH = NEXP_MAX;           // expert-slot marker of the shared expert
 using GG = Geo<7, 0>;                  // gate/up rows: K = 7168 (staged without padding)
 using GD = Geo<2, 0>;                  // down rows: K = 2048
@@ -40,6 +40,7 @@ constexpr int NGU = DH / GU_ROWS;      // gate/up tasks per expert
 constexpr int DN_ROWS = DW * 32;       // output rows per down unit (32 per wave: two row sets of 16)
 constexpr int NDN = DE / DN_ROWS;      // down units per expert (= combine units)
 constexpr int GU_PD = 3, DN_PD = 3;   // blocks in flight per lane
+constexpr int DN_PRE = 2;              // down steps issued before the h staging (register budget)
 static_assert(DH == DW * QK, "a down unit's wave w quantises h block w");
 static_assert(DMAX_N * (MAXK + 1) * DH <= (int) DEC_TH && DMAX_N * (MAXK + 1) * DE <= (int) DEC_TO, "tagged buffer sizes");
 
@@ -50,17 +51,18 @@ constexpr int PRE_BYTES = 2 * 7 * 64 * 4;
 constexpr int L_SCR = L_PRE;                                      // router sums [token][quarter] (phase 1) overlay them
 constexpr int L_RT = L_PRE + PRE_BYTES;                           // routing tables
 constexpr int RT_INTS = 4 * DMAX_P + 3 * (DMAX_P + 1) + 1 + 2 * DMAX_PS + 1;
-constexpr int L_CTL = L_RT + RT_INTS * 4;                         // workgroup hand-off words [8], per-wave flags [2][DW]
-constexpr int DEC_LDS = L_CTL + (8 + 2 * DW) * 4;
+constexpr int L_CTL = L_RT + RT_INTS * 4;                         // hand-off words [8], staging flags [DW]
+constexpr int DEC_LDS = L_CTL + (8 + DW) * 4;
 static_assert(DEC_LDS <= 160 * 1024, "LDS budget");
 static_assert(DMAX_N * 4 * 8 <= PRE_BYTES, "router sums overlay the early task terms");
 
 typedef LK_LOCAL uint8_t * lds_t;
 typedef LK_CONST DecodeArgs DArgs;   // the launch arguments, read in place with scalar loads
 
-// Routing of the launch, in LDS. A pair-slot is one or two tokens of one expert (consecutive dispatch slots): every task
-// and unit works on one pair-slot, so their costs are alike whatever the tokens per expert. ps_mi = act index or SH,
-// ps_s = first slot | token count << 16; the shared expert's pair-slots come first.
+// Routing of the launch, in LDS. The task list ps holds one entry per dispatch slot (one token of one expert), so every
+// gate/up task and down unit costs one pass over its weights and the round-robin assignment is balanced; the two tokens
+// of an expert are adjacent entries, whose tasks run side by side (same workgroup for gate/up) and share the weights
+// through L2. ps_mi = act index or SH, ps_s = slot | token count (1) << 16; the shared expert's slots come first.
 struct RT {
     LK_LOCAL int * sel; LK_LOCAL float * wts; LK_LOCAL int * perm, * inv, * act_e, * act_s0, * act_cnt, * nact;
     LK_LOCAL int * ps_mi, * ps_s, * nps;
@@ -292,16 +294,16 @@ __device__ __noinline__ void dispatch_wave(const DArgs & a, lds_t lds, int P) {
         if (rank == 0) { rt.act_e[dless] = e; rt.act_s0[dless] = less; rt.act_cnt[dless] = __popcll(eq); }
     }
     if (lane == 0) { *rt.nact = __popcll(first); }
-    // pair-slots: the shared expert's (tokens 2k, 2k + 1 at slots P + 2k ..), then every active expert's in act order
+    // task slots: the shared expert's (token t at slot P + t), then every active expert's in act order
     lds_visible();
-    const int nact = __popcll(first), nsh = (a.n + 1) >> 1;
+    const int nact = __popcll(first), nsh = a.n;
     const int cnt_l = lane < nact ? rt.act_cnt[lane] : 0, s_l = lane < nact ? rt.act_s0[lane] : 0;
-    const int np = (cnt_l + 1) >> 1;
+    const int np = cnt_l;
     const int incl = (int) wave_scan_u32((uint32_t) np), pos0 = nsh + incl - np;
     for (int k = 0; k < np; ++k) {
-        if (pos0 + k < DMAX_PS) { rt.ps_mi[pos0 + k] = lane; rt.ps_s[pos0 + k] = (s_l + 2 * k) | ((cnt_l - 2 * k >= 2 ? 2 : 1) << 16); }
+        if (pos0 + k < DMAX_PS) { rt.ps_mi[pos0 + k] = lane; rt.ps_s[pos0 + k] = (s_l + k) | (1 << 16); }
     }
-    if (lane < nsh) { rt.ps_mi[lane] = SH; rt.ps_s[lane] = (P + 2 * lane) | ((a.n - 2 * lane >= 2 ? 2 : 1) << 16); }
+    if (lane < nsh) { rt.ps_mi[lane] = SH; rt.ps_s[lane] = (P + lane) | (1 << 16); }
     if (lane == 63) { *rt.nps = nsh + incl < DMAX_PS ? nsh + incl : DMAX_PS; }
 }
 // the layer's routing outputs from workgroup 0's tables (one wave, after its work: they are read after the launch)
@@ -467,6 +469,7 @@ __device__ __forceinline__ void pre_shared_split(const DArgs & a, lds_t lds, con
 // once into the LDS of the token rows (no longer needed): row 2 k + i = token i of its unit k, wave w quantising Q8_K
 // block w of every row. After one barrier each wave computes its rows of every unit without further synchronisation.
 struct DnUnit { int mi, s, c, rg; };
+
 __device__ __forceinline__ bool dn_unit(const RT & rt, int u, int nps, int nact, int P, int n, DnUnit & d) {
     const int ps = u % nps, mi = rt.ps_mi[ps], sc = rt.ps_s[ps];
     d.mi = mi; d.s = sc & 0xFFFF; d.c = sc >> 16; d.rg = u / nps;
@@ -483,9 +486,23 @@ __device__ __forceinline__ int down_phase(const DArgs & a, lds_t lds, const Lane
     const int K = (int) blockIdx.x < total ? (total - 1 - (int) blockIdx.x) / G + 1 : 0;
     LK_LOCAL unsigned * wok = reinterpret_cast<LK_LOCAL unsigned *>(lds + L_CTL) + 8;   // [DW] per-wave staging results
     const uint32_t lq = (uint32_t) ln.q * 4096 + 16 * ln.r, ld = (uint32_t) ln.q * 128 + 2 * ln.r;
+    // this wave's weight bases (qs, d) of unit k (round-robin index); false for an invalid table entry
+    auto unit_bases = [&](int k, DnUnit & d, const uint8_t * & qb, const uint8_t * & db) -> bool {
+        if (!dn_unit(rt, (int) blockIdx.x + k * G, nps, nact, P, a.n, d)) { return false; }
+        const int e = d.mi != SH ? rt.act_e[d.mi] : 0;
+        const uint8_t * base = uniform_ptr(d.mi != SH ? a.down + (size_t) e * a.estride : a.sh_down);
+        const int g64 = d.rg * (DN_ROWS / 64) + (wave >> 1), sub = (wave & 1) * 2;
+        qb = base + (size_t) g64 * GD::NB * 4096 + sub * 256;
+        db = base + (size_t) (DE / 64) * GD::NB * 4096 + (size_t) g64 * GD::NB * 128 + sub * 32;
+        return true;
+    };
+    RowStream<GD::BPQ, 2, DN_PD> rs;
     for (int k0 = 0; k0 < K; k0 += DN_KC) {
         const int kn = K - k0 < DN_KC ? K - k0 : DN_KC;
         __syncthreads();   // the token rows (or the previous chunk's h) are no longer read
+        // the chunk's first unit: its first DN_PRE steps stream in while the h words are polled and staged
+        DnUnit d0; const uint8_t * qb0 = nullptr, * db0 = nullptr;
+        if (unit_bases(k0, d0, qb0, db0)) { rs.template prologue<0, DN_PRE>(qb0, db0, lq, ld); }
         TRACE(wave, 24);
         // stage: rows r0 .. r0 + 3 at a time, all their words in flight together
         bool ok = true;
@@ -541,17 +558,11 @@ __device__ __forceinline__ int down_phase(const DArgs & a, lds_t lds, const Lane
         TRACE(wave, 25);
         if (!all_ok) { report(a.err, 1); continue; }
         for (int k = 0; k < kn; ++k) {
-            DnUnit d;
-            if (!dn_unit(rt, (int) blockIdx.x + (k0 + k) * G, nps, nact, P, a.n, d)) { report(a.err, 1); continue; }
-            const int e = d.mi != SH ? rt.act_e[d.mi] : 0;
-            const uint8_t * base = uniform_ptr(d.mi != SH ? a.down + (size_t) e * a.estride : a.sh_down);
-            const int g64 = d.rg * (DN_ROWS / 64) + (wave >> 1), sub = (wave & 1) * 2;
-            const uint8_t * qb = base + (size_t) g64 * GD::NB * 4096 + sub * 256;
-            const uint8_t * db = base + (size_t) (DE / 64) * GD::NB * 4096 + (size_t) g64 * GD::NB * 128 + sub * 32;
-            RowStream<GD::BPQ, 2, DN_PD> rs;
+            DnUnit d; const uint8_t * qb, * db;
+            if (!unit_bases(k0 + k, d, qb, db)) { report(a.err, 1); continue; }
             // one token per pass: the second pass re-reads the unit's weights from L2
             for (int i = 0; i < d.c; ++i) {
-                rs.prologue(qb, db, lq, ld);
+                if (k > 0 || i > 0) { rs.prologue(qb, db, lq, ld); } else { rs.template prologue<DN_PRE, DN_PD>(qb, db, lq, ld); }
                 float acc[2];
                 rs.run_dpp<GD>(qb, db, lq, ld, ln.tr, (const uint8_t *) (lds + L_XS + (2 * k + i) * GD::XROW), ln.q, ln.r, acc);
                 if (ln.q == 0) {
@@ -566,38 +577,50 @@ __device__ __forceinline__ int down_phase(const DArgs & a, lds_t lds, const Lane
 }
 
 // ---------------------------------------------------------------- phase 5: combine
-// rows cu * 256 .. + 255 of every token: y = sum_k w_k o_k in k order + the shared expert's o; false on timeout
+// rows cu * 256 .. + 255 of every token: y = sum_k w_k o_k in k order + the shared expert's o. Thread (row, t0) polls
+// the tagged o words of its tokens t0, t0 + 2, .. all at once (one memory round trip per poll); false on timeout
 __device__ __forceinline__ bool combine_unit(const DArgs & a, lds_t lds, int cu, int P) {
 #pragma clang fp contract(off)
+    constexpr int TS = DNT / DN_ROWS, CT = DMAX_N / TS;   // token stride, tokens per thread
     const RT rt(lds);
-    const int rr = cu * DN_ROWS + (threadIdx.x & (DN_ROWS - 1));
-    bool ok = true;
-    // a wave's 64 threads share tok, so the loop and the polls are wave-uniform
-    for (int tok = threadIdx.x / DN_ROWS; tok < a.n; tok += DNT / DN_ROWS) {
-        float ov[MAXK + 1];
-        int it = 0;
-        for (; it < POLL_MAX; ++it) {
-            bool v = true;
+    const int rr = cu * DN_ROWS + (threadIdx.x & (DN_ROWS - 1)), t0 = threadIdx.x / DN_ROWS;
+    uint64_t wv[CT][MAXK + 1];
+    auto used = [&](int c, int k) { return t0 + c * TS < a.n && (k < a.topk || k == MAXK); };
+    auto issue = [&]() {
+#pragma unroll
+        for (int c = 0; c < CT; ++c) {
+            const int tok = t0 + c * TS;
 #pragma unroll
             for (int k = 0; k <= MAXK; ++k) {
-                if (k < a.topk || k == MAXK) {
-                    const int s = k < MAXK ? rt.inv[tok * a.topk + k] : P + tok;
-                    const uint64_t w = ld_tag(a.to + (size_t) s * DE + rr);
-                    v = v && tag_ok(w, a.epoch); ov[k] = tag_val(w);
-                } else {
-                    ov[k] = 0.f;
-                }
+                if (used(c, k)) { wv[c][k] = ld_tag(a.to + (size_t) (k < MAXK ? rt.inv[tok * a.topk + k] : P + tok) * DE + rr); }
             }
-            if (__ballot(!v) == 0) { break; }
-            __builtin_amdgcn_s_sleep(1);
         }
-        if (it == POLL_MAX) { ok = false; continue; }
-        float mv = ov[0] * rt.wts[tok * a.topk];
+    };
+    issue();
+    int it = 0;
+    for (; it < POLL_MAX; ++it) {
+        bool v = true;
 #pragma unroll
-        for (int k = 1; k < MAXK; ++k) { if (k < a.topk) { mv = mv + ov[k] * rt.wts[tok * a.topk + k]; } }
-        gptr(a.y)[(size_t) tok * DE + rr] = mv + ov[MAXK];
+        for (int c = 0; c < CT; ++c) {
+#pragma unroll
+            for (int k = 0; k <= MAXK; ++k) { v = v && (!used(c, k) || tag_ok(wv[c][k], a.epoch)); }
+        }
+        if (__ballot(!v) == 0) { break; }
+        __builtin_amdgcn_s_sleep(1);
+        issue();
     }
-    return ok;
+    if (it == POLL_MAX) { return false; }
+#pragma unroll
+    for (int c = 0; c < CT; ++c) {
+        const int tok = t0 + c * TS;
+        if (tok < a.n) {
+            float mv = tag_val(wv[c][0]) * rt.wts[tok * a.topk];
+#pragma unroll
+            for (int k = 1; k < MAXK; ++k) { if (k < a.topk) { mv = mv + tag_val(wv[c][k]) * rt.wts[tok * a.topk + k]; } }
+            gptr(a.y)[(size_t) tok * DE + rr] = mv + tag_val(wv[c][MAXK]);
+        }
+    }
+    return true;
 }
 
 // ---------------------------------------------------------------- the kernel
@@ -676,7 +699,7 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
     // 3. gate/up tasks (pair-slot, 8 h rows): task tk on workgroup tk / DW % G, wave tk % DW, so a workgroup streams
     //    whole 64-row groups; the shared expert's pair-slots come first unless the early tasks covered them
     const RT rt(lds);
-    const int nact = *rt.nact, nps = *rt.nps, ps0 = pre ? (n + 1) >> 1 : 0;
+    const int nact = *rt.nact, nps = *rt.nps, ps0 = pre ? n : 0;
     const int t_gu = (nps - ps0) * NGU;
     TRACE(wave, 8);
     const int ntask = gate_up_stream<GU_PD>(a, lds, ln, blockIdx.x * DW + wave, G * DW, t_gu, false, ps0, P, nact);

@@ -355,27 +355,34 @@ __device__ __forceinline__ float fold_quad(float acc, float t) {
 // row_newbcast from the lane that holds it -- one LDS read per block instead of 16. Staged dword 16 L + 2 ib + hi
 // (group L, sub-block ib, weights 0..3 / 4..7) lives in lane 4 L + ib / 2, register 2 (ib & 1) + hi.
 template <int CTRL> __device__ __forceinline__ int dppi(int v) { return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false); }
-template <int L, int IB>
+template <int L, int IB, int IBE = 8>
 __device__ __forceinline__ void dot_ib_dpp(const uint2 (&g)[8], const uint4 (&m)[8], const uint32_t (&xq)[4], int (&acc)[8]) {
-    if constexpr (IB < 8) {
+    if constexpr (IB < IBE) {
         uint32_t lo, hi; iq2_apply(g[IB], m[IB], lo, hi);
         constexpr int SRC = 4 * L + IB / 2;
         acc[IB] = __builtin_amdgcn_sdot4(dppi<0x150 + SRC>((int) xq[2 * (IB & 1)]), (int) lo, acc[IB], false);
         acc[IB] = __builtin_amdgcn_sdot4(dppi<0x150 + SRC>((int) xq[2 * (IB & 1) + 1]), (int) hi, acc[IB], false);
-        dot_ib_dpp<L, IB + 1>(g, m, xq, acc);
+        dot_ib_dpp<L, IB + 1, IBE>(g, m, xq, acc);
     }
 }
-template <int L>
+// the group's 16 table reads in batches of IBB sub-blocks (8: all issued before the first is used; 4: half the registers)
+#ifndef LK_IBB
+#define LK_IBB 8
+#endif
+template <int L, int IB0 = 0>
 __device__ __forceinline__ void group_step_dpp(const uint4 (&w)[4], uint32_t tr, const uint32_t (&xq)[4], int (&acc)[8]) {
-    const uint32_t trs = tab_sign_word(tr);
-    uint2 g[8]; uint4 m[8];
+    if constexpr (IB0 < 8) {
+        const uint32_t trs = tab_sign_word(tr);
+        uint2 g[8]; uint4 m[8];
 #pragma unroll
-    for (int ib = 0; ib < 8; ++ib) {
-        const uint4 c = w[ib >> 1];
-        g[ib] = tab_grid<L>((ib & 1) ? c.z : c.x, tr);
-        m[ib] = tab_sign<L>(((ib & 1) ? c.w : c.y) & SIGN_BITS, trs);
+        for (int ib = IB0; ib < IB0 + LK_IBB; ++ib) {
+            const uint4 c = w[ib >> 1];
+            g[ib] = tab_grid<L>((ib & 1) ? c.z : c.x, tr);
+            m[ib] = tab_sign<L>(((ib & 1) ? c.w : c.y) & SIGN_BITS, trs);
+        }
+        dot_ib_dpp<L, IB0, IB0 + LK_IBB>(g, m, xq, acc);
+        group_step_dpp<L, IB0 + LK_IBB>(w, tr, xq, acc);
     }
-    dot_ib_dpp<L, 0>(g, m, xq, acc);
 }
 // block_bsum for one token whose staged block is xb (this lane reads its 16 bytes at xb + 16 r)
 __device__ __forceinline__ int block_bsum_dpp(const uint4 (&w)[4], uint32_t tr, const uint8_t * xb, int r) {
@@ -435,9 +442,11 @@ struct RowStream {
         for (int c = 0; c < 4; ++c) { pf[slot][c] = load_nt(q + lq + c * 1024); }
         pd[slot] = *gptr(reinterpret_cast<const uint16_t *>(db + (size_t) rs * 32 + (size_t) jj * (4 * 128) + ld));
     }
+    // steps [K0, K1) of the first PD (run issues the rest); prologue = all of them
+    template <int K0 = 0, int K1 = PD>
     __device__ __forceinline__ void prologue(const uint8_t * qb, const uint8_t * db, uint32_t lq, uint32_t ld) {
 #pragma unroll
-        for (int k = 0; k < PD; ++k) { if (k < STEPS) { issue(qb, db, lq, ld, k, k); } }
+        for (int k = K0; k < K1; ++k) { if (k < STEPS) { issue(qb, db, lq, ld, k, k); } }
     }
     // row totals (before the final * 0.125) of the lane's RPL rows for T staged tokens xr[u]
     template <int T, class G>

@@ -249,3 +249,53 @@ def test_fused_decode_repeated_launches(ctx, layer):
         y = ctx.moe_layer(layer, xs[n])
         ctx.sync()
         assert np.array_equal(y.cpu().numpy().view(np.uint32), want[n].view(np.uint32)), n
+
+
+def test_rmsnorm_matches_checker(ctx):
+    """The device RMSNorm (fp64 sum of fp32 squares, fp32 mean, 1/sqrtf) against the checker's sequential sum: the
+    sums differ only in fp64 rounding, which the fp32 mean almost never keeps."""
+    import torch
+    rng = np.random.default_rng(77)
+    x = rng.normal(0, 2, (16, E)).astype(np.float32)
+    x[3] *= 1e-3; x[5] *= 40.0; x[7, :] = 0.0
+    y = ctx.rmsnorm(torch.from_numpy(x).cuda())
+    ctx.sync()
+    ref = orc.rmsnorm(x)
+    yg = y.cpu().numpy()
+    ulps = np.abs(yg.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
+    assert ulps.max() <= 1, ulps.max()
+    assert (ulps != 0).mean() < 1e-3
+
+
+def test_stack_chain(ctx):
+    """configs[3] on three independently seeded layers: x_{L+1} = RMSNorm(y_L). Each layer's device output is
+    bit-identical to the checker on the device's input to that layer, and the device chain ends where the checker's
+    own chain (run from x_0 on the CPU) ends, within the task's tolerance."""
+    import torch
+    nl = 3
+    layers = [make_layer(ctx, seed=5000 + 1000 * L) for L in range(nl)]
+    x0 = make_x(ctx, 1, seed=88)
+    xin, outs = [], []
+    cur = x0
+    for L in layers:
+        xin.append(cur.cpu().numpy())
+        y = ctx.moe_layer(L, cur)
+        cur = ctx.rmsnorm(y)
+        outs.append(y.cpu().numpy())
+    ctx.sync()
+    xc = x0.cpu().numpy()
+    for L, layer in enumerate(layers):
+        W, b = layer.gate_inp.cpu().numpy(), layer.probs_b.cpu().numpy()
+        _, _, so, _ = orc.router(W, b, xin[L])
+        _, _, gate, up, down, sh = host_layer(ctx, layer, so.ravel())
+        ref = orc.moe_forward(xin[L], W, b, gate, up, down, *sh)
+        assert np.array_equal(outs[L].view(np.uint32), ref["y"].view(np.uint32)), "layer %d" % L
+        # the checker's own chain
+        _, _, sc, _ = orc.router(W, b, xc)
+        _, _, gate, up, down, sh = host_layer(ctx, layer, sc.ravel())
+        yc = orc.moe_forward(xc, W, b, gate, up, down, *sh)["y"]
+        mx, l2 = rel_errors(outs[L], yc)
+        assert mx <= MAX_REL and l2 <= L2_REL, (L, mx, l2)
+        xc = orc.rmsnorm(yc)
+    del layers
+    torch.cuda.empty_cache()
