@@ -89,9 +89,144 @@ __global__ void __launch_bounds__(256) k_router_gemm(const float * __restrict__ 
     }
 }
 
+// Large batches (K = 7168): register tiles. Lane (tg, eg) = (lane / 8, lane % 8) owns the logits of TT tokens x EE
+// experts of the workgroup's (8 TT) x (8 EE) tile; wave q computes slice q of the contract (chunks q * 256 / NQ ..) with the
+// same in-order fp64 chunk sums and pairwise tree as above, and the slices are combined by the tree's top levels through
+// LDS. Each 16-byte load of x or W now feeds EE or TT fused multiply-adds (the kernel above: 2 or 1).
+template <int TT, int EE> struct RgAcc { double v[TT][EE]; };
+// one chunk's in-order sums (28 products each) for the lane's TT x EE logits; the loads of step i + 1 are in flight
+// while step i computes, and nothing is hoisted further (register budget)
+template <int TT, int EE>
+__device__ __forceinline__ void rg_chunk(const float * const (&xr)[TT], const float * const (&wr)[EE], int c, RgAcc<TT, EE> & s) {
+#pragma clang fp contract(off)
+    constexpr int CL = 28, NS = CL / 4;
+    float4 xv[2][TT], wv[2][EE];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+#pragma unroll
+        for (int e = 0; e < EE; ++e) { s.v[t][e] = 0.0; }
+    }
+    auto load = [&](int i, int b) {
+#pragma unroll
+        for (int t = 0; t < TT; ++t) { xv[b][t] = gloadf4(xr[t] + CL * c + 4 * i); }
+#pragma unroll
+        for (int e = 0; e < EE; ++e) { wv[b][e] = gloadf4(wr[e] + CL * c + 4 * i); }
+    };
+    load(0, 0);
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+        const int b = i & 1;
+        if (i + 1 < NS) { load(i + 1, b ^ 1); }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            double xd[TT], wd[EE];
+#pragma unroll
+            for (int t = 0; t < TT; ++t) { xd[t] = (double) (q == 0 ? xv[b][t].x : q == 1 ? xv[b][t].y : q == 2 ? xv[b][t].z : xv[b][t].w); }
+#pragma unroll
+            for (int e = 0; e < EE; ++e) { wd[e] = (double) (q == 0 ? wv[b][e].x : q == 1 ? wv[b][e].y : q == 2 ? wv[b][e].z : wv[b][e].w); }
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+#pragma unroll
+                for (int e = 0; e < EE; ++e) { s.v[t][e] = __builtin_fma(xd[t], wd[e], s.v[t][e]); }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+template <int TT, int EE>
+__device__ __forceinline__ void rg_add(RgAcc<TT, EE> & d, const RgAcc<TT, EE> & l, const RgAcc<TT, EE> & r) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+#pragma unroll
+        for (int e = 0; e < EE; ++e) { d.v[t][e] = l.v[t][e] + r.v[t][e]; }
+    }
+}
+// the level-4 node over chunks c0 .. c0 + 15: the pairwise tree built as the chunks arrive (binary counter; pend[l]
+// holds the pending left node of level l)
+template <int TT, int EE>
+__device__ __forceinline__ RgAcc<TT, EE> rg_tile16(const float * const (&xr)[TT], const float * const (&wr)[EE], int c0) {
+    RgAcc<TT, EE> pend[4], v;
+#pragma unroll 1
+    for (int c = 0; c < 16; ++c) {
+        rg_chunk<TT, EE>(xr, wr, c0 + c, v);
+        if (!(c & 1)) { pend[0] = v; continue; }
+        rg_add(v, pend[0], v);
+        if (!(c & 2)) { pend[1] = v; continue; }
+        rg_add(v, pend[1], v);
+        if (!(c & 4)) { pend[2] = v; continue; }
+        rg_add(v, pend[2], v);
+        if (!(c & 8)) { pend[3] = v; continue; }
+        rg_add(v, pend[3], v);
+    }
+    return v;
+}
+template <int TT, int EE, int NQ>
+__global__ void __launch_bounds__(64 * NQ) k_router_tile(const float * __restrict__ W, const float * __restrict__ x, int n, int n_exp,
+                                                       float * __restrict__ logits) {
+#pragma clang fp contract(off)
+    constexpr int K = 7168, CPW = 256 / NQ, LW = CPW == 64 ? 6 : CPW == 32 ? 5 : 4;   // chunks per wave, tree levels
+    static_assert(CPW == (1 << LW) && LW >= 4, "slices of 16, 32 or 64 chunks");
+    __shared__ double part[NQ][TT * EE][64];
+    const int q = threadIdx.x >> 6, lane = lane_id(), tg = lane >> 3, eg = lane & 7;
+    const int tb = blockIdx.y * 8 * TT + tg * TT, eb = blockIdx.x * 8 * EE + eg * EE;
+    const float * xr[TT]; const float * wr[EE];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) { xr[t] = x + (size_t) (tb + t < n ? tb + t : 0) * K; }
+#pragma unroll
+    for (int e = 0; e < EE; ++e) { wr[e] = W + (size_t) (eb + e < n_exp ? eb + e : 0) * K; }
+    // the wave's slice as 16-chunk groups (level-4 nodes), combined pairwise in order (levels 5, 6)
+    RgAcc<TT, EE> tot, l4, l5;
+#pragma unroll 1
+    for (int g = 0; g < CPW / 16; ++g) {
+        RgAcc<TT, EE> v = rg_tile16<TT, EE>(xr, wr, q * CPW + 16 * g);
+        if (LW == 4) { tot = v; break; }
+        if (!(g & 1)) { l4 = v; continue; }
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+#pragma unroll
+            for (int e = 0; e < EE; ++e) { v.v[t][e] = l4.v[t][e] + v.v[t][e]; }
+        }
+        if (LW == 5) { tot = v; break; }
+        if (!(g & 2)) { l5 = v; continue; }
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+#pragma unroll
+            for (int e = 0; e < EE; ++e) { tot.v[t][e] = l5.v[t][e] + v.v[t][e]; }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+#pragma unroll
+        for (int e = 0; e < EE; ++e) { part[q][t * EE + e][lane] = tot.v[t][e]; }
+    }
+    __syncthreads();
+    // the tree's top levels over the NQ slices, pairwise in slice order; output o of the lane by wave o % NQ
+    for (int o = q; o < TT * EE; o += NQ) {
+        const int t = tb + o / EE, e = eb + o % EE;
+        double v[NQ];
+#pragma unroll
+        for (int j = 0; j < NQ; ++j) { v[j] = part[j][o][lane]; }
+#pragma unroll
+        for (int w = 1; w < NQ; w *= 2) {
+#pragma unroll
+            for (int j = 0; j + w < NQ; j += 2 * w) { v[j] = v[j] + v[j + w]; }
+        }
+        if (t < n && e < n_exp) { logits[(size_t) t * n_exp + e] = (float) v[0]; }
+    }
+}
+
 hipError_t launch_router_logits(const float * W, const float * x, int n, int n_exp, int K, float * logits, hipStream_t st) {
     if (n <= 0) { return hipSuccess; }
     if (K % 1024 != 0) { return hipErrorInvalidValue; }
+    if (K == 7168 && n >= 1024) {   // 32 x 32 tiles (4 x 4 per lane): enough workgroups from 1024 tokens on
+        k_router_tile<4, 4, 4><<<dim3((n_exp + 31) / 32, (n + 31) / 32), 256, 0, st>>>(W, x, n, n_exp, logits);
+        return hipGetLastError();
+    }
+    if (K == 7168 && n >= 64) {     // 32 x 16 tiles (4 x 2 per lane)
+        k_router_tile<4, 2, 4><<<dim3((n_exp + 15) / 16, (n + 31) / 32), 256, 0, st>>>(W, x, n, n_exp, logits);
+        return hipGetLastError();
+    }
     if (K == 7168 && n >= 16) {
         k_router_gemm<<<dim3((n_exp + 7) / 8, (n + 15) / 16), 256, 0, st>>>(W, x, n, n_exp, logits);
         return hipGetLastError();
