@@ -110,7 +110,8 @@ def run_workload(ctx, torch, name, steps, warmup, copies, seed=20260101):
 
 def run_stack(ctx, torch, steps, warmup, nlayers=STACK_LAYERS, seed=20260301):
     """one token through nlayers independently seeded MoE layers, x_{L+1} = RMSNorm(y_L) (weights 1,
-    eps 1e-6). A step is the whole chain for one fresh x; bytes = nlayers x the decode-1 bytes of a layer."""
+    eps 1e-6; the norm runs inside the next layer's block). A step is the whole chain for one fresh x; bytes = nlayers
+    x the decode-1 bytes of a layer."""
     from loki_amd import MoeLayerWeights
     t0 = time.perf_counter()
     layers = [MoeLayerWeights.synthetic(ctx, seed + 1000 * L, bias_sigma=0.01) for L in range(nlayers)]
@@ -121,15 +122,12 @@ def run_stack(ctx, torch, steps, warmup, nlayers=STACK_LAYERS, seed=20260301):
         x = torch.empty((1, E), dtype=torch.float32, device="cuda")
         ctx.synth_normal(x, seed + 17, 2000 + i, 0.0, 1.0)
         xs.append(x)
-    y = torch.empty((1, E), dtype=torch.float32, device="cuda")
-    xn = torch.empty((1, E), dtype=torch.float32, device="cuda")
+    ys = [torch.empty((1, E), dtype=torch.float32, device="cuda") for _ in range(2)]
 
-    def token(x):
-        cur = x
-        for L in layers:
-            ctx.moe_layer(L, cur, y)
-            ctx.rmsnorm(y, None, 1e-6, out=xn)
-            cur = xn
+    def token(x):   # layer L > 0 normalises y_{L-1} inside its block (fl_moe_layer_normed)
+        ctx.moe_layer(layers[0], x, ys[0])
+        for i, L in enumerate(layers[1:]):
+            ctx.moe_layer_normed(L, ys[i % 2], None, 1e-6, ys[(i + 1) % 2])
 
     for i in range(warmup):
         token(xs[i])

@@ -95,6 +95,10 @@ typedef struct FLMoeLayer {
 /* y[n][E] = MoE(x[n][E]) on the context's stream (x, y device pointers; asynchronous). n <= 65536.
  * Allocation extents are checked against the shapes (hipMemGetAddressRange) before any launch. */
 int fl_moe_layer(FLCtx *, const FLMoeLayer * L, const float * x, int n, float * y);
+/* the same on RMSNorm(h) * ffn_norm (ggml rms_norm with eps, then the norm weight; ffn_norm may be NULL: ones): the
+ * layer's ffn_norm applied inside the block, as the reference's fl_attn applies it before the router (fl.cu:498). For
+ * decode batches the norm runs inside the single launch; bit-identical to fl_rmsnorm_dev followed by fl_moe_layer. */
+int fl_moe_layer_normed(FLCtx *, const FLMoeLayer * L, const float * ffn_norm, float eps, const float * h, int n, float * y);
 /* router only: sel/w [n][topk] (device), logits/probs [n][n_exp] may be NULL */
 int fl_route_dev(FLCtx *, const float * gate_inp, const float * probs_b, const float * x, int n, int n_exp, int E,
                  float * logits, float * probs, int * sel, float * w);
@@ -105,7 +109,7 @@ int fl_quant_q8k_dev(FLCtx *, const float * x, int nrows, int K, int8_t * q, flo
 /* IQ2_XXS ggml layout <-> tiled layout for nmat matrices of R x K at byte strides (device, may not alias) */
 int fl_pack_iq2xxs(FLCtx *, const void * src_ggml, size_t src_stride, void * dst_tiled, size_t dst_stride, int R, int K, int nmat);
 int fl_unpack_iq2xxs(FLCtx *, const void * src_tiled, size_t src_stride, void * dst_ggml, size_t dst_stride, int R, int K, int nmat);
-/* RMSNorm (ggml semantics, eps) of n rows of D floats, w may be NULL (ones) -- the 58-layer chain's norm */
+/* RMSNorm (ggml semantics, eps) of n rows of D floats (D = 1024, 2048, 4096 or 7168), w may be NULL (ones) */
 int fl_rmsnorm_dev(FLCtx *, const float * x, const float * w, float * y, int n, int D, float eps);
 /* synthetic data on the device: IQ2_XXS matrices (qs uniform bytes, d = fp16(|N(0, sigma^2)|)) and normal floats */
 int fl_synth_iq2xxs(FLCtx *, void * dst, size_t dst_stride, int R, int K, int nmat, int layout, uint64_t seed, uint64_t mat0, float sigma);

@@ -53,7 +53,7 @@ class FLOut(ctypes.Structure):
 ABI_SYMBOLS = [
     "fl_init", "fl_attn", "fl_wide_init", "fl_wide_moe", "fl_wide_mark", "fl_wide_wait", "fl_wide_finish", "fl_moe_outs",
     "fl_wide_outs", "fl_wide_skip", "fl_spec", "fl_sketch", "fl_fetch", "fl_moe", "fl_skip", "fl_h2d", "fl_wait_event",
-    "fl_gpu_ms", "fl_ffn_begin", "fl_set_experts", "fl_set_routing", "fl_moe_layer", "fl_route_dev", "fl_dispatch_dev", "fl_quant_q8k_dev",
+    "fl_gpu_ms", "fl_ffn_begin", "fl_set_experts", "fl_set_routing", "fl_moe_layer", "fl_moe_layer_normed", "fl_route_dev", "fl_dispatch_dev", "fl_quant_q8k_dev",
     "fl_pack_iq2xxs", "fl_unpack_iq2xxs", "fl_rmsnorm_dev", "fl_synth_iq2xxs", "fl_synth_normal", "fl_probe_exp",
     "fl_debug", "fl_set_debug", "fl_set_fused", "fl_set_prefill_mfma", "fl_stream", "fl_set_stream", "fl_d2h", "fl_set_profile", "fl_stage_ms", "fl_sync", "fl_last_error", "fl_free",
 ]
@@ -87,6 +87,7 @@ def lib():
             "fl_set_fused": (I, [P_, I]),
             "fl_set_prefill_mfma": (I, [P_, I]),
             "fl_moe_layer": (I, [P_, ctypes.POINTER(FLMoeLayer), P_, I, P_]),
+            "fl_moe_layer_normed": (I, [P_, ctypes.POINTER(FLMoeLayer), P_, F, P_, I, P_]),
             "fl_route_dev": (I, [P_, P_, P_, P_, I, I, I, P_, P_, P_, P_]),
             "fl_dispatch_dev": (I, [P_, P_, I, I, I, P_, P_, P_, P_, P_, P_]),
             "fl_quant_q8k_dev": (I, [P_, P_, I, I, P_, P_]),
@@ -279,6 +280,14 @@ class Context:
         if y is None:
             y = self.torch.empty_like(x)
         self.check(lib().fl_moe_layer(self.ctx, ctypes.byref(layer.abi()), _ptr(x), n, _ptr(y)))
+        return y
+
+    def moe_layer_normed(self, layer, h, norm_w=None, eps=1e-6, y=None):
+        """y = MoE(RMSNorm(h) * norm_w) (norm_w None: ones) -- the layer's ffn_norm inside the block."""
+        n, E = h.shape
+        if y is None:
+            y = self.torch.empty_like(h)
+        self.check(lib().fl_moe_layer_normed(self.ctx, ctypes.byref(layer.abi()), _ptr(norm_w), eps, _ptr(h), n, _ptr(y)))
         return y
 
     def debug(self):

@@ -39,7 +39,7 @@ struct FLCtx {
     double ms_moe = 0.0;
     std::string err;
     int dbg_gu = 0;
-    DBuf<int8_t> xq, hq; DBuf<float> xd, logits, probs, wts, h, hd, o, g, u;
+    DBuf<int8_t> xq, hq; DBuf<float> xd, logits, probs, wts, h, hd, o, g, u, xn;
     DBuf<int> sel, counts, offsets, perm, inv, act, nact;
     int last_n = 0, last_P = 0, last_fused = 0;
     // stage timing (fl_set_profile): one set of NSTAGE+1 events per profiled call, summed by fl_stage_ms

@@ -39,7 +39,7 @@ extern "C" void fl_free(FLCtx * c) {
     if (!c) { return; }
     (void) hipStreamSynchronize(c->st);
     c->xq.release(); c->hq.release(); c->xd.release(); c->logits.release(); c->probs.release(); c->wts.release();
-    c->h.release(); c->hd.release(); c->o.release(); c->g.release(); c->u.release();
+    c->h.release(); c->hd.release(); c->o.release(); c->g.release(); c->u.release(); c->xn.release();
     c->sel.release(); c->counts.release(); c->offsets.release(); c->perm.release(); c->inv.release(); c->act.release(); c->nact.release();
     compat_free(c); c->zero_i.release(); c->terms.release(); c->cnt.release();
     c->tab.release(); c->derr.release(); c->dlogit.release(); c->dth.release(); c->dto.release();
@@ -224,7 +224,8 @@ static bool decode_ready(FLCtx * c) {
 }
 
 // ================================================================ the device-resident block
-extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, float * y) {
+// the block on x, or on RMSNorm(x) * nw when prenorm (nw may be null: ones)
+static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, float * y, bool prenorm, const float * nw, float eps) {
     if (!c) { return FL_EINVAL; }
     if (!L) { return fail(c, FL_EINVAL, "null layer"); }
     if (n < 0 || n > 65536) { return fail(c, FL_ERANGE, "n = %d outside 0..65536", n); }
@@ -243,6 +244,8 @@ extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, in
             !covers(L->sh_gate, mg) || !covers(L->sh_up, mg) || !covers(L->sh_down, mg)) {
             return fail(c, FL_EINVAL, "an allocation of the layer, x or y is smaller than its shape (%d experts, E %d, H %d, n %d)", ne, E, H, n);
         }
+        if (prenorm && nw && !covers(nw, (size_t) E * 4)) { return fail(c, FL_EINVAL, "the norm weight is smaller than E = %d floats", E); }
+        if (prenorm && !(eps >= 0.f)) { return fail(c, FL_EINVAL, "bad norm eps %g", (double) eps); }
     }
     const size_t rows = (size_t) P + n;
     const bool fused = c->fused && n <= 8 && E == 7168 && H == 2048 && decode_rule_ok(ne, c->n_group) && decode_ready(c);
@@ -267,7 +270,7 @@ extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, in
             TRY(c, hipMemsetAsync(c->dto.p, 0, DEC_TO * sizeof(uint64_t), st));
         }
         DecodeArgs d{};
-        d.tab = c->tab.p; d.x = x; d.n = n;
+        d.tab = c->tab.p; d.x = x; d.n = n; d.prenorm = prenorm ? 1 : 0; d.nw = nw; d.eps = eps;
         d.Wr = L->gate_inp; d.bias = L->probs_b; d.n_exp = ne; d.n_group = c->n_group; d.topk_group = c->topk_group; d.topk = tk; d.scale = c->scale;
         d.gate = (const uint8_t *) L->gate_exps; d.up = (const uint8_t *) L->up_exps; d.down = (const uint8_t *) L->down_exps;
         d.estride = (size_t) H * (E / 256) * IQ2B;
@@ -295,6 +298,11 @@ extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, in
         ALLOC(c, c->pcols, rows / 32 + NEXP_MAX + 2); ALLOC(c, c->pncols, 1);
     }
     prof_mark(c, ev, 0);
+    if (prenorm) {   // the per-pass path normalises into a context buffer first (k_rmsnorm: the same arithmetic)
+        ALLOC(c, c->xn, (size_t) n * E);
+        TRY(c, launch_rmsnorm(x, nw, c->xn.p, n, E, eps, st));
+        x = c->xn.p;
+    }
     TRY(c, launch_quant_q8k(x, n, E, c->xq.p, c->xd.p, st));
     if (mfma) { TRY(c, launch_q8_to_h(c->xq.p, c->xh.p, (int64_t) n * E, st)); }
     prof_mark(c, ev, 1);
@@ -344,6 +352,12 @@ extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, in
     TRY(c, launch_experts_down(d, c->ncu, st));
     prof_mark(c, ev, 6);
     return FL_OK;
+}
+extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, float * y) {
+    return moe_layer(c, L, x, n, y, false, nullptr, 0.f);
+}
+extern "C" int fl_moe_layer_normed(FLCtx * c, const FLMoeLayer * L, const float * ffn_norm, float eps, const float * h, int n, float * y) {
+    return moe_layer(c, L, h, n, y, true, ffn_norm, eps);
 }
 
 extern "C" int fl_set_profile(FLCtx * c, int on) { if (!c) { return FL_EINVAL; } c->prof = on ? 1 : 0; return FL_OK; }

@@ -52,7 +52,8 @@ constexpr int L_SCR = L_PRE;                                      // router sums
 constexpr int L_RT = L_PRE + PRE_BYTES;                           // routing tables
 constexpr int RT_INTS = 4 * DMAX_P + 3 * (DMAX_P + 1) + 1 + 2 * DMAX_PS + 1;
 constexpr int L_CTL = L_RT + RT_INTS * 4;                         // hand-off words [8], staging flags [DW]
-constexpr int DEC_LDS = L_CTL + (8 + DW) * 4;
+constexpr int L_NRM = L_CTL + (8 + DW) * 4;                       // pre-norm scale per token [DMAX_N]
+constexpr int DEC_LDS = L_NRM + DMAX_N * 4;
 static_assert(DEC_LDS <= 160 * 1024, "LDS budget");
 static_assert(DMAX_N * 4 * 8 <= PRE_BYTES, "router sums overlay the early task terms");
 
@@ -138,6 +139,33 @@ extern "C" hipError_t fl_trace_clear() {
 #endif
 
 // ---------------------------------------------------------------- phase 1
+// RMSNorm scales of the tokens (prenorm): waves 4 h .. 4 h + 3 take tokens h, h + 2, ..; thread (q = wave & 3, lane)
+// sums chunk 64 q + lane (sumsq_chunk, the contract of k_rmsnorm), so the scale is bit-identical to a separate
+// k_rmsnorm pass. Every workgroup computes them for itself from x (L2).
+__device__ __noinline__ void norm_phase(const DArgs & a, lds_t lds, int wave) {
+    LK_LOCAL double * part = reinterpret_cast<LK_LOCAL double *>(lds + L_SCR);   // [token][quarter]
+    const int lane = lane_id(), qt = wave & 3;
+    for (int t = wave >> 2; t < a.n; t += DW / 4) {
+        const double s = tree64(sumsq_chunk<DE / 1024>(a.x + (size_t) t * DE, qt * 64 + lane));
+        if (lane == 0) { part[t * 4 + qt] = s; }
+    }
+    __syncthreads();
+    if (threadIdx.x < (unsigned) a.n) {
+        const int t = threadIdx.x;
+        reinterpret_cast<LK_LOCAL float *>(lds + L_NRM)[t] = rms_scale(part[t * 4], part[t * 4 + 1], part[t * 4 + 2], part[t * 4 + 3], DE, a.eps);
+    }
+    __syncthreads();
+}
+// the block's input: x, or (x * scale) * w under prenorm (k_rmsnorm's arithmetic), for 4 values at column col of token t
+__device__ __forceinline__ float4 block_in(const DArgs & a, lds_t lds, int t, int col, float4 v) {
+#pragma clang fp contract(off)
+    if (!a.prenorm) { return v; }
+    const float sc = reinterpret_cast<const LK_LOCAL float *>(lds + L_NRM)[t];
+    v.x = v.x * sc; v.y = v.y * sc; v.z = v.z * sc; v.w = v.w * sc;
+    if (a.nw) { const float4 w = gloadf4(a.nw + col); v.x = v.x * w.x; v.y = v.y * w.y; v.z = v.z * w.z; v.w = v.w * w.w; }
+    return v;
+}
+
 // The table image into LDS with direct global->LDS loads (16 B per lane, 1 KB per wave instruction), issued first so
 // they complete under the router's loads; visible to the workgroup after s_waitcnt vmcnt(0) and a barrier.
 __device__ __forceinline__ void tables_dma(lds_t lds, const uint4 * img, int wave) {
@@ -162,10 +190,11 @@ __device__ __forceinline__ void local_quant(const DArgs & a, lds_t lds, int wave
     for (int p = 0; p < MAXP; ++p) {
         const int k = 4 * (wave + DW * p) + (lane >> 4);
         if (4 * (wave + DW * p) < nblk) {
-            const float * src = a.x + (size_t) (k / GG::NB) * DE + (size_t) (k % GG::NB) * QK + 16 * i;
+            const int col = (k % GG::NB) * QK + 16 * i;
+            const float * src = a.x + (size_t) (k / GG::NB) * DE + col;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const float4 v = gloadf4(src + 4 * q);
+                const float4 v = block_in(a, lds, k / GG::NB, col + 4 * q, gloadf4(src + 4 * q));
                 xs[p][4 * q] = v.x; xs[p][4 * q + 1] = v.y; xs[p][4 * q + 2] = v.z; xs[p][4 * q + 3] = v.w;
             }
         }
@@ -212,6 +241,8 @@ __device__ __noinline__ void router_phase(const DArgs & a, lds_t lds, int wave, 
             if (t < a.n) {
 #pragma unroll
                 for (int i = 0; i < L4; ++i) { xv[k][i] = gloadf4(a.x + (size_t) t * DE + (size_t) c * 4 * L4 + 4 * i); }
+#pragma unroll
+                for (int i = 0; i < L4; ++i) { xv[k][i] = block_in(a, lds, t, c * 4 * L4 + 4 * i, xv[k][i]); }
             }
         }
 #pragma unroll
@@ -646,6 +677,7 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
     if (threadIdx.x < 8) { ctl[threadIdx.x] = 0; }
     tables_dma(lds, a.tab, wave);
     __syncthreads();   // the hand-off words are clear
+    if (a.prenorm) { norm_phase(a, lds, wave); }
     for (int e = blockIdx.x; e < a.n_exp; e += G) { router_phase(a, lds, wave, e); }
     TRACE(wave, 2);
 

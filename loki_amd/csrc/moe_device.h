@@ -96,6 +96,28 @@ __device__ __forceinline__ double tree64(double t) {
     t = t + dppd<DPP_MIRROR>(t);
     return (rdlaned(t, 0) + rdlaned(t, 16)) + (rdlaned(t, 32) + rdlaned(t, 48));
 }
+// RMSNorm sum of squares (the contract of k_rmsnorm and the decode block's pre-norm): chunk c = 64 q + lane (c = 0..255)
+// holds values CL c .. CL c + CL - 1 (CL = 4 L4 = D / 256), summed in order in fp64 from fp32 squares; tree64 over the
+// wave's 64 chunks; the four quarters as (q0 + q1) + (q2 + q3).
+template <int L4>
+__device__ __forceinline__ double sumsq_chunk(const float * row, int c) {
+#pragma clang fp contract(off)
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < L4; ++i) {
+        const float4 v = gloadf4(row + (size_t) c * 4 * L4 + 4 * i);
+        const float q0 = v.x * v.x, q1 = v.y * v.y, q2 = v.z * v.z, q3 = v.w * v.w;
+        s += (double) q0; s += (double) q1; s += (double) q2; s += (double) q3;
+    }
+    return s;
+}
+// the norm's scale from the four quarter totals
+__device__ __forceinline__ float rms_scale(double q0, double q1, double q2, double q3, int D, float eps) {
+#pragma clang fp contract(off)
+    const double tot = (q0 + q1) + (q2 + q3);
+    const float mean = (float) (tot / (double) D);
+    return 1.0f / sqrtf(mean + eps);
+}
 // the lane's four chunk sums -> the wave's total (uniform)
 __device__ __forceinline__ double logit_tree(const double (&s)[4]) {
 #pragma clang fp contract(off)

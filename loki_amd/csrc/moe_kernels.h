@@ -49,6 +49,7 @@ hipError_t launch_experts_down(const ExpertArgs & a, int grid, hipStream_t st);
 struct DecodeArgs {
     const uint4 * tab;
     const float * x; int n;                          // tokens [n][E], n <= 8
+    int prenorm; const float * nw; float eps;        // prenorm: the block's input is RMSNorm(x) * nw (nw null: ones)
     const float * Wr; const float * bias; int n_exp, n_group, topk_group, topk; float scale;
     const uint8_t * gate, * up, * down; size_t estride;   // routed experts (tiled), expert e at + e * estride
     const uint8_t * sh_gate, * sh_up, * sh_down;

@@ -271,20 +271,25 @@ def test_rmsnorm_matches_checker(ctx):
 
 
 def test_stack_chain(ctx):
-    """configs[3] on three independently seeded layers: x_{L+1} = RMSNorm(y_L). Each layer's device output is
-    bit-identical to the checker on the device's input to that layer, and the device chain ends where the checker's
-    own chain (run from x_0 on the CPU) ends, within the task's tolerance."""
+    """configs[3] on three independently seeded layers: x_{L+1} = RMSNorm(y_L), the norm fused into the next layer's
+    block (fl_moe_layer_normed). Each layer's device output is bit-identical to the checker on that layer's input
+    (RMSNorm(y_{L-1}) from the separate device norm, which the fused one reproduces), and the device chain ends where
+    the checker's own chain (run from x_0 on the CPU) ends, within the task's tolerance."""
     import torch
     nl = 3
     layers = [make_layer(ctx, seed=5000 + 1000 * L) for L in range(nl)]
     x0 = make_x(ctx, 1, seed=88)
     xin, outs = [], []
-    cur = x0
+    prev = None
     for L in layers:
-        xin.append(cur.cpu().numpy())
-        y = ctx.moe_layer(L, cur)
-        cur = ctx.rmsnorm(y)
+        if prev is None:
+            xin.append(x0.cpu().numpy())
+            y = ctx.moe_layer(L, x0)
+        else:
+            xin.append(ctx.rmsnorm(prev).cpu().numpy())
+            y = ctx.moe_layer_normed(L, prev)
         outs.append(y.cpu().numpy())
+        prev = y
     ctx.sync()
     xc = x0.cpu().numpy()
     for L, layer in enumerate(layers):
@@ -302,3 +307,30 @@ def test_stack_chain(ctx):
         xc = orc.rmsnorm(yc)
     del layers
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("n", [1, 8, 40])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_prenorm_matches_separate_norm(ctx, layer, n, weighted):
+    """fl_moe_layer_normed (the norm inside the decode block for n <= 8, a k_rmsnorm pass before the per-pass path
+    above) is bit-identical to fl_rmsnorm_dev followed by fl_moe_layer."""
+    import torch
+    h = make_x(ctx, n, seed=300 + n) * 3.0
+    w = None
+    if weighted:
+        w = torch.empty(E, dtype=torch.float32, device="cuda")
+        ctx.synth_normal(w, 41, 5, 1.0, 0.1)
+    y1 = ctx.moe_layer_normed(layer, h, w, 1e-6)
+    fused = ctx.debug().fused
+    y2 = ctx.moe_layer(layer, ctx.rmsnorm(h, w, 1e-6))
+    ctx.sync()
+    assert fused == (1 if n <= 8 else 0)
+    assert np.array_equal(y1.cpu().numpy().view(np.uint32), y2.cpu().numpy().view(np.uint32))
+    if n == 1:   # the per-pass kernels take the same normalised input
+        ctx.set_fused(False)
+        try:
+            y3 = ctx.moe_layer_normed(layer, h, w, 1e-6)
+            ctx.sync()
+        finally:
+            ctx.set_fused(True)
+        assert np.array_equal(y3.cpu().numpy().view(np.uint32), y2.cpu().numpy().view(np.uint32))
