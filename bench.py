@@ -199,7 +199,7 @@ def main():
     ap.add_argument("--workload", default="decode8", choices=sorted(WORKLOADS))
     ap.add_argument("--copies", type=int, default=3, help="independently seeded layers rotated over the steps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-extra", action="store_true", help="skip the decode-1 / prefill-512 side measurements")
+    ap.add_argument("--no-extra", action="store_true", help="skip the decode-1 / prefill-512 / prefill-2048 side measurements")
     ap.add_argument("--no-stack", action="store_true", help="skip the 58-layer resident stack (configs[3], ~169 GB)")
     ap.add_argument("--stack-steps", type=int, default=10)
     ap.add_argument("--fused", type=int, default=None, choices=(0, 1, 2),
@@ -239,7 +239,7 @@ def main():
         del a, b
     extra = {}
     if not args.no_extra:
-        for wl, st in (("decode1", 30), ("prefill512", 5)):
+        for wl, st in (("decode1", 30), ("prefill512", 5), ("prefill2048", 3)):
             if wl == args.workload:
                 continue
             r = run_workload(ctx, torch, wl, st, 2, args.copies)
