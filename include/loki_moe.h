@@ -97,8 +97,11 @@ typedef struct FLMoeLayer {
 int fl_moe_layer(FLCtx *, const FLMoeLayer * L, const float * x, int n, float * y);
 /* the same on RMSNorm(h) * ffn_norm (ggml rms_norm with eps, then the norm weight; ffn_norm may be NULL: ones): the
  * layer's ffn_norm applied inside the block, as the reference's fl_attn applies it before the router (fl.cu:498). For
- * decode batches the norm runs inside the single launch; bit-identical to fl_rmsnorm_dev followed by fl_moe_layer. */
-int fl_moe_layer_normed(FLCtx *, const FLMoeLayer * L, const float * ffn_norm, float eps, const float * h, int n, float * y);
+ * decode batches the norm runs inside the single launch; bit-identical to fl_rmsnorm_dev followed by fl_moe_layer.
+ * residual != 0 adds h to the output (y = (moe + shared) + h, the reference combine's lo2 = moe + shared + fi,
+ * fl.cu:366-372); h and y must then not alias. */
+int fl_moe_layer_normed(FLCtx *, const FLMoeLayer * L, const float * ffn_norm, float eps, const float * h, int n,
+                        int residual, float * y);
 /* router only: sel/w [n][topk] (device), logits/probs [n][n_exp] may be NULL */
 int fl_route_dev(FLCtx *, const float * gate_inp, const float * probs_b, const float * x, int n, int n_exp, int E,
                  float * logits, float * probs, int * sel, float * w);

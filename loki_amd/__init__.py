@@ -87,7 +87,7 @@ def lib():
             "fl_set_fused": (I, [P_, I]),
             "fl_set_prefill_mfma": (I, [P_, I]),
             "fl_moe_layer": (I, [P_, ctypes.POINTER(FLMoeLayer), P_, I, P_]),
-            "fl_moe_layer_normed": (I, [P_, ctypes.POINTER(FLMoeLayer), P_, F, P_, I, P_]),
+            "fl_moe_layer_normed": (I, [P_, ctypes.POINTER(FLMoeLayer), P_, F, P_, I, I, P_]),
             "fl_route_dev": (I, [P_, P_, P_, P_, I, I, I, P_, P_, P_, P_]),
             "fl_dispatch_dev": (I, [P_, P_, I, I, I, P_, P_, P_, P_, P_, P_]),
             "fl_quant_q8k_dev": (I, [P_, P_, I, I, P_, P_]),
@@ -282,12 +282,13 @@ class Context:
         self.check(lib().fl_moe_layer(self.ctx, ctypes.byref(layer.abi()), _ptr(x), n, _ptr(y)))
         return y
 
-    def moe_layer_normed(self, layer, h, norm_w=None, eps=1e-6, y=None):
-        """y = MoE(RMSNorm(h) * norm_w) (norm_w None: ones) -- the layer's ffn_norm inside the block."""
+    def moe_layer_normed(self, layer, h, norm_w=None, eps=1e-6, y=None, residual=False):
+        """y = MoE(RMSNorm(h) * norm_w) (norm_w None: ones) -- the layer's ffn_norm inside the block; residual adds h."""
         n, E = h.shape
         if y is None:
             y = self.torch.empty_like(h)
-        self.check(lib().fl_moe_layer_normed(self.ctx, ctypes.byref(layer.abi()), _ptr(norm_w), eps, _ptr(h), n, _ptr(y)))
+        self.check(lib().fl_moe_layer_normed(self.ctx, ctypes.byref(layer.abi()), _ptr(norm_w), eps, _ptr(h), n,
+                                             1 if residual else 0, _ptr(y)))
         return y
 
     def debug(self):

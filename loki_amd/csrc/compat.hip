@@ -94,7 +94,7 @@ inline unsigned nblk(int64_t tot) { return (unsigned) ((tot + 255) / 256); }
 struct Compat {
     // rows of the last fl_ffn_begin (narrow pass)
     int N = 0;
-    DBuf<float> ncur, fi, logits, probs, wts, h, o, sh_o; DBuf<int8_t> xq, hq; DBuf<float> xd, hd; DBuf<int> sel;
+    DBuf<float> ncur, fi, logits, probs, wts, h, o, sh_o, wr32; DBuf<int8_t> xq, hq; DBuf<float> xd, hd; DBuf<int> sel;
     DBuf<uint8_t> sh_t; const void * sh_key[3] = { nullptr, nullptr, nullptr };
     // fl_moe
     DBuf<uint8_t> ag, au, ad; DBuf<int> ids, counts, offsets, perm, inv, act, nact; DBuf<float> w, hout, moe;
@@ -128,7 +128,7 @@ void compat_free(FLCtx * c) {
         if (p) { (void) hipHostFree(p); }
     }
     for (hipEvent_t e : s->wev) { if (e) { (void) hipEventDestroy(e); } }
-    s->ncur.release(); s->fi.release(); s->logits.release(); s->probs.release(); s->wts.release(); s->h.release(); s->o.release(); s->sh_o.release();
+    s->ncur.release(); s->fi.release(); s->logits.release(); s->probs.release(); s->wts.release(); s->h.release(); s->o.release(); s->sh_o.release(); s->wr32.release();
     s->xq.release(); s->hq.release(); s->xd.release(); s->hd.release(); s->sel.release(); s->sh_t.release();
     s->ag.release(); s->au.release(); s->ad.release(); s->ids.release(); s->counts.release(); s->offsets.release(); s->perm.release(); s->inv.release();
     s->act.release(); s->nact.release(); s->w.release(); s->hout.release(); s->moe.release();
@@ -207,13 +207,12 @@ extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur,
     if (!c) { return FL_EINVAL; }
     if (!W || !ncur || !ffn_inp) { return fail(c, FL_EINVAL, "null pointer"); }
     if (N <= 0 || N > RMAX) { return fail(c, FL_ERANGE, "N = %d outside 1..%d", N, RMAX); }
-    if (W->gate_f16) { return fail(c, FL_ESCOPE, "the F16 router (ffn_gate_inp_f16) is not supported; pass the F32 router"); }
     if (!W->gate_inp || !W->probs_b || !W->sh_gate || !W->sh_up || !W->sh_down) { return fail(c, FL_EINVAL, "router or shared-expert weight missing"); }
     Compat * s = cs(c);
     if (wrow >= 0 && (s->wmax == 0 || wrow + N > s->wmax)) { return fail(c, FL_ERANGE, "wide rows %d..%d exceed fl_wide_init's %d", wrow, wrow + N, s->wmax); }
     const size_t R = (size_t) RMAX * E_;
     const int ne = c->n_exp;
-    if (!covers(W->gate_inp, (size_t) ne * E_ * 4) || !covers(W->probs_b, (size_t) ne * 4)) {
+    if (!covers(W->gate_inp, (size_t) ne * E_ * (W->gate_f16 ? 2 : 4)) || !covers(W->probs_b, (size_t) ne * 4)) {
         return fail(c, FL_EINVAL, "router weight or bias allocation is smaller than %d experts x %d", ne, E_);
     }
     if (!covers(W->sh_gate, mat_bytes(H_, E_)) || !covers(W->sh_up, mat_bytes(H_, E_)) || !covers(W->sh_down, mat_bytes(E_, H_))) {
@@ -232,7 +231,15 @@ extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur,
         TRY(c, launch_pack_tiled((const uint8_t *) W->sh_down, mg, s->sh_t.p + 2 * mg, mg, E_, H_, 1, st));
         s->sh_key[0] = W->sh_gate; s->sh_key[1] = W->sh_up; s->sh_key[2] = W->sh_down;
     }
-    if (int rc = fl_route_dev(c, (const float *) W->gate_inp, (const float *) W->probs_b, s->ncur.p, N, ne, E_, s->logits.p, s->probs.p, s->sel.p, s->wts.p)) { return rc; }
+    // the F16 router (W->gate_f16, fl.cu:317-319) is widened exactly to fp32 first; the logits then follow the same
+    // contract as an F32 router holding the same values
+    const float * wr = (const float *) W->gate_inp;
+    if (W->gate_f16) {
+        ALLOC(c, s->wr32, (size_t) ne * E_);
+        TRY(c, launch_f16_to_f32((const uint16_t *) W->gate_inp, s->wr32.p, (int64_t) ne * E_, st));
+        wr = s->wr32.p;
+    }
+    if (int rc = fl_route_dev(c, wr, (const float *) W->probs_b, s->ncur.p, N, ne, E_, s->logits.p, s->probs.p, s->sel.p, s->wts.p)) { return rc; }
     TRY(c, launch_quant_q8k(s->ncur.p, N, E_, s->xq.p, s->xd.p, st));
     shared_expert(c, s, s->xq.p, s->xd.p, N, s->sh_o.p);
     if (wrow >= 0) {

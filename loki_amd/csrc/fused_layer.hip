@@ -224,8 +224,9 @@ static bool decode_ready(FLCtx * c) {
 }
 
 // ================================================================ the device-resident block
-// the block on x, or on RMSNorm(x) * nw when prenorm (nw may be null: ones)
-static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, float * y, bool prenorm, const float * nw, float eps) {
+// the block on x, or on RMSNorm(x) * nw when prenorm (nw may be null: ones); resid (may be null) is added to the output
+static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, float * y, bool prenorm, const float * nw, float eps,
+                     const float * resid) {
     if (!c) { return FL_EINVAL; }
     if (!L) { return fail(c, FL_EINVAL, "null layer"); }
     if (n < 0 || n > 65536) { return fail(c, FL_ERANGE, "n = %d outside 0..65536", n); }
@@ -270,7 +271,7 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
             TRY(c, hipMemsetAsync(c->dto.p, 0, DEC_TO * sizeof(uint64_t), st));
         }
         DecodeArgs d{};
-        d.tab = c->tab.p; d.x = x; d.n = n; d.prenorm = prenorm ? 1 : 0; d.nw = nw; d.eps = eps;
+        d.tab = c->tab.p; d.x = x; d.n = n; d.prenorm = prenorm ? 1 : 0; d.nw = nw; d.eps = eps; d.resid = resid;
         d.Wr = L->gate_inp; d.bias = L->probs_b; d.n_exp = ne; d.n_group = c->n_group; d.topk_group = c->topk_group; d.topk = tk; d.scale = c->scale;
         d.gate = (const uint8_t *) L->gate_exps; d.up = (const uint8_t *) L->up_exps; d.down = (const uint8_t *) L->down_exps;
         d.estride = (size_t) H * (E / 256) * IQ2B;
@@ -328,7 +329,7 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
         d.w[0] = (const uint8_t *) L->down_exps; d.w[1] = nullptr; d.sh[0] = (const uint8_t *) L->sh_down; d.sh[1] = nullptr;
         d.R = E; d.K = H; d.nmat = 1; d.bh = c->hh.p; d.bd = c->hd.p; d.out = c->o.p; d.gdbg = nullptr; d.udbg = nullptr;
         TRY(c, launch_prefill_gemm(d, c->ncu, st));
-        TRY(c, launch_combine(c->o.p, c->inv.p, c->wts.p, n, tk, E, P, nullptr, y, nullptr, st));
+        TRY(c, launch_combine(c->o.p, c->inv.p, c->wts.p, n, tk, E, P, resid, y, nullptr, st));
         prof_mark(c, ev, 6);
         return FL_OK;
     }
@@ -354,10 +355,12 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     return FL_OK;
 }
 extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, float * y) {
-    return moe_layer(c, L, x, n, y, false, nullptr, 0.f);
+    return moe_layer(c, L, x, n, y, false, nullptr, 0.f, nullptr);
 }
-extern "C" int fl_moe_layer_normed(FLCtx * c, const FLMoeLayer * L, const float * ffn_norm, float eps, const float * h, int n, float * y) {
-    return moe_layer(c, L, h, n, y, true, ffn_norm, eps);
+extern "C" int fl_moe_layer_normed(FLCtx * c, const FLMoeLayer * L, const float * ffn_norm, float eps, const float * h, int n,
+                                   int residual, float * y) {
+    if (c && residual && h == y) { return fail(c, FL_EINVAL, "h and y must not alias when the residual is added"); }
+    return moe_layer(c, L, h, n, y, true, ffn_norm, eps, residual ? h : nullptr);
 }
 
 extern "C" int fl_set_profile(FLCtx * c, int on) { if (!c) { return FL_EINVAL; } c->prof = on ? 1 : 0; return FL_OK; }

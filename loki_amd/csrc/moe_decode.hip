@@ -608,7 +608,8 @@ __device__ __forceinline__ int down_phase(const DArgs & a, lds_t lds, const Lane
 }
 
 // ---------------------------------------------------------------- phase 5: combine
-// rows cu * 256 .. + 255 of every token: y = sum_k w_k o_k in k order + the shared expert's o. Thread (row, t0) polls
+// rows cu * 256 .. + 255 of every token: y = sum_k w_k o_k in k order + the shared expert's o (+ the residual when
+// given, the reference combine's moe + shared + ffn_inp order, fl.cu:366-372). Thread (row, t0) polls
 // the tagged o words of its tokens t0, t0 + 2, .. all at once (one memory round trip per poll); false on timeout
 __device__ __forceinline__ bool combine_unit(const DArgs & a, lds_t lds, int cu, int P) {
 #pragma clang fp contract(off)
@@ -648,7 +649,9 @@ __device__ __forceinline__ bool combine_unit(const DArgs & a, lds_t lds, int cu,
             float mv = tag_val(wv[c][0]) * rt.wts[tok * a.topk];
 #pragma unroll
             for (int k = 1; k < MAXK; ++k) { if (k < a.topk) { mv = mv + tag_val(wv[c][k]) * rt.wts[tok * a.topk + k]; } }
-            gptr(a.y)[(size_t) tok * DE + rr] = mv + tag_val(wv[c][MAXK]);
+            float yv = mv + tag_val(wv[c][MAXK]);
+            if (a.resid) { yv = yv + gptr(a.resid)[(size_t) tok * DE + rr]; }
+            gptr(a.y)[(size_t) tok * DE + rr] = yv;
         }
     }
     return true;

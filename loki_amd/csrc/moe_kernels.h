@@ -50,6 +50,7 @@ struct DecodeArgs {
     const uint4 * tab;
     const float * x; int n;                          // tokens [n][E], n <= 8
     int prenorm; const float * nw; float eps;        // prenorm: the block's input is RMSNorm(x) * nw (nw null: ones)
+    const float * resid;                             // added to the block's output when not null ([n][E])
     const float * Wr; const float * bias; int n_exp, n_group, topk_group, topk; float scale;
     const uint8_t * gate, * up, * down; size_t estride;   // routed experts (tiled), expert e at + e * estride
     const uint8_t * sh_gate, * sh_up, * sh_down;
@@ -106,6 +107,8 @@ hipError_t launch_unpack_tiled(const uint8_t * src, size_t src_stride, uint8_t *
 hipError_t launch_synth_iq2(uint8_t * dst, size_t dst_stride, int R, int K, int nmat, int layout, uint64_t seed,
                             uint64_t mat0, float sigma, hipStream_t st);
 hipError_t launch_synth_normal(float * dst, int64_t count, uint64_t seed, uint64_t stream, float mean, float sigma, hipStream_t st);
+// fp16 bits -> fp32 (exact widening)
+hipError_t launch_f16_to_f32(const uint16_t * src, float * dst, int64_t count, hipStream_t st);
 
 // ggml rms_norm (fp64 sum of fp32 squares) then the weight (w may be null = ones); one block per row
 hipError_t launch_rmsnorm(const float * x, const float * w, float * y, int n, int D, float eps, hipStream_t st);

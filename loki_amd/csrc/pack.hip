@@ -107,6 +107,17 @@ __global__ void k_synth_normal(float * __restrict__ dst, int64_t count, uint64_t
     dst[i] = (float) ((double) mean + (double) sigma * gauss(mix64(key), mix64(key + 1)));
 }
 
+// fp16 -> fp32 (exact): the F16 router weight (ffn_gate_inp as F16, fl.cu:317-319) widened for the fp32 router kernels
+__global__ void k_f16_to_f32(const uint16_t * __restrict__ src, float * __restrict__ dst, int64_t count) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) { dst[i] = h2f(src[i]); }
+}
+hipError_t launch_f16_to_f32(const uint16_t * src, float * dst, int64_t count, hipStream_t st) {
+    if (count <= 0) { return hipSuccess; }
+    k_f16_to_f32<<<(unsigned) ((count + 255) / 256), 256, 0, st>>>(src, dst, count);
+    return hipGetLastError();
+}
+
 hipError_t launch_synth_normal(float * dst, int64_t count, uint64_t seed, uint64_t stream, float mean, float sigma, hipStream_t st) {
     if (count <= 0) { return hipSuccess; }
     k_synth_normal<<<(unsigned) ((count + 255) / 256), 256, 0, st>>>(dst, count, seed, stream, mean, sigma);

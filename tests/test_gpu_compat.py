@@ -126,6 +126,30 @@ def test_narrow_pass(ctx, small_layer):
     assert np.array_equal(hs.view(np.uint32), want.view(np.uint32))
 
 
+def test_f16_router(ctx, small_layer):
+    """fl_ffn_begin with an F16 router weight (FLW.gate_f16, fl.cu:317-319): widened exactly, it routes like the F32
+    router holding the same values (selections, weights and the shared-expert path), and like the checker on them."""
+    import torch
+    from loki_amd import FLOut, lib
+    (W, b, gate, up, down, sh), dev = small_layer
+    ctx.set_routing(8, 4, 8, 2.5)
+    n = 4
+    x = gen.uniform(8, 3, (n, E), 2.0); fi = gen.uniform(8, 4, (n, E), 1.0)
+    w16 = dev["W"].to(torch.float16)
+    w32 = w16.to(torch.float32)
+    res = []
+    for wt, f16 in ((w16, 1), (w32, 0)):
+        flw = _flw(dev)
+        flw.gate_inp = wt.data_ptr(); flw.gate_f16 = f16
+        ctx.check(lib().fl_ffn_begin(ctx.ctx, ctypes.byref(flw), n, cptr(x), cptr(fi), -1))
+        out = FLOut()
+        lib().fl_fetch(ctx.ctx, n, 1, ctypes.byref(out))
+        res.append((np.ctypeslib.as_array(out.sel, shape=(n * KE,)).copy(), np.ctypeslib.as_array(out.wts, shape=(n * KE,)).copy()))
+    assert np.array_equal(res[0][0], res[1][0]) and np.array_equal(res[0][1].view(np.uint32), res[1][1].view(np.uint32))
+    _, _, so, wo = orc.router(w32.cpu().numpy(), b, x, 8, 4, 8, 2.5)
+    assert np.array_equal(res[0][0].reshape(n, KE), so) and np.array_equal(res[0][1].reshape(n, KE).view(np.uint32), wo.view(np.uint32))
+
+
 def test_wide_pass(ctx, small_layer):
     """fl_wide_init -> fl_ffn_begin(wrow) per group -> per arena batch fl_wide_moe (slots of <= 8 (row, k) pairs in the
     engine's byexp order) -> fl_wide_finish; h = (ffn_inp + shared) + sum_k w_k o_k (src/fused_layer.cu:351-360)."""

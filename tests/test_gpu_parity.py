@@ -326,6 +326,11 @@ def test_prenorm_matches_separate_norm(ctx, layer, n, weighted):
     ctx.sync()
     assert fused == (1 if n <= 8 else 0)
     assert np.array_equal(y1.cpu().numpy().view(np.uint32), y2.cpu().numpy().view(np.uint32))
+    # the residual variant adds h once more: (moe + shared) + h
+    y4 = ctx.moe_layer_normed(layer, h, w, 1e-6, residual=True)
+    ctx.sync()
+    ref4 = (y1.cpu().numpy() + h.cpu().numpy()).astype(np.float32)
+    assert np.array_equal(y4.cpu().numpy().view(np.uint32), ref4.view(np.uint32))
     if n == 1:   # the per-pass kernels take the same normalised input
         ctx.set_fused(False)
         try:
