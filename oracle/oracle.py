@@ -42,6 +42,10 @@ def lib():
         L.or_dequantize_row_iq2_xxs.restype = None; L.or_dequantize_row_iq2_xxs.argtypes = [P, P, I64]
         L.or_vec_dot_iq2_xxs_q8_K.restype = F; L.or_vec_dot_iq2_xxs_q8_K.argtypes = [I64, P, P, P]
         L.or_matvec_iq2_xxs.restype = None; L.or_matvec_iq2_xxs.argtypes = [P, I64, I64, P, P, P]
+        L.or_kq_block_bytes.restype = ctypes.c_int; L.or_kq_block_bytes.argtypes = [ctypes.c_int]
+        L.or_dequantize_row_kq.restype = None; L.or_dequantize_row_kq.argtypes = [ctypes.c_int, P, P, I64]
+        L.or_vec_dot_kq_q8_K.restype = ctypes.c_float; L.or_vec_dot_kq_q8_K.argtypes = [ctypes.c_int, I64, P, P, P, P]
+        L.or_matvec_kq.restype = None; L.or_matvec_kq.argtypes = [ctypes.c_int, P, I64, I64, P, P, P, I64, P]
         L.or_router_logit.restype = F; L.or_router_logit.argtypes = [P, P, I64]
         L.or_router.restype = I; L.or_router.argtypes = [P, P, P, I64, I, I64, I, I, I, F, P, P, P, P]
         L.or_dispatch.restype = I; L.or_dispatch.argtypes = [P, I64, I, I, P, P, P]
@@ -99,6 +103,38 @@ def quantize_q8k(x):
     for i in range(rows.shape[0]):
         lib().or_quantize_row_q8_K(_p(rows[i]), _p(q[i]), _p(d[i]), _p(bs[i]), K)
     return q.reshape(x.shape), d.reshape(x.shape[:-1] + (K // QK_K,)), bs.reshape(x.shape[:-1] + (K // 16,))
+
+
+# K-quant formats (kquant_oracle.c): the FL_* codes of include/loki_moe.h
+Q2K, Q3K, Q5K, Q6K = 5, 6, 3, 1
+
+
+def kq_block_bytes(fmt):
+    return lib().or_kq_block_bytes(fmt)
+
+
+def dequant_kq(fmt, blocks, K):
+    """blocks uint8 [rows, K/256*bytes] -> fp32 [rows, K] (dequantize_row_q*_K)."""
+    b = _c(blocks, np.uint8).reshape(-1, K // QK_K * kq_block_bytes(fmt))
+    y = np.empty((b.shape[0], K), np.float32)
+    for i in range(b.shape[0]):
+        lib().or_dequantize_row_kq(fmt, _p(b[i]), _p(y[i]), K)
+    return y
+
+
+def vec_dot_kq(fmt, row_blocks, q, d, bsums):
+    """ggml_vec_dot_q*_K_q8_K of one row (blocks) with one Q8_K row (q, d, bsums)."""
+    K = q.shape[-1]
+    return float(lib().or_vec_dot_kq_q8_K(fmt, K, _p(_c(row_blocks, np.uint8)), _p(_c(q, np.int8)), _p(_c(d, np.float32)),
+                                           _p(_c(bsums, np.int16))))
+
+
+def matvec_kq(fmt, w, rows, K, q, d, bsums):
+    """y [nt, rows] = w (rows x K, ggml layout) . Q8_K rows (q [nt, K], d [nt, K/256], bsums [nt, K/16])."""
+    q = _c(q, np.int8).reshape(-1, K); nt = q.shape[0]
+    y = np.empty((nt, rows), np.float32)
+    lib().or_matvec_kq(fmt, _p(_c(w, np.uint8)), rows, K, _p(q), _p(_c(d, np.float32)), _p(_c(bsums, np.int16)), nt, _p(y))
+    return y
 
 
 def dequant_iq2xxs(blocks, K):
