@@ -21,7 +21,8 @@ extern "C" {
 
 typedef struct FLCtx FLCtx;
 
-/* formats (src/fused_layer.h:11); this library computes FL_IQ2 everywhere */
+/* formats (src/fused_layer.h:11): experts in FL_IQ2; routed down also FL_Q2K / FL_Q3K and the shared expert also
+ * K-quants (the reference's real shards), read in place in ggml's block layout */
 enum { FL_Q4K = 0, FL_Q6K = 1, FL_Q80 = 2, FL_Q5K = 3, FL_IQ2 = 4, FL_Q2K = 5, FL_Q3K = 6 };
 /* IQ2_XXS byte layouts of expert matrices: ggml's row-major blocks, or the tiled resident layout of fl_pack_iq2xxs */
 enum { FL_LAYOUT_GGML = 0, FL_LAYOUT_TILED = 1 };
@@ -48,7 +49,8 @@ FLCtx * fl_init(int kvp, int sc_cap);
 void fl_attn(FLCtx *, const FLW *, int N, int pos0, const int * pos, void * KC, void * VC, const float * hin, int dense, int last_row, int wrow);
 /* fl.h:29 -- wide-pass buffers for wmax rows with KE experts per row */
 int fl_wide_init(FLCtx *, int wmax, int KE);
-/* fl.h:30 -- routed experts of one arena batch for up to 8 (row, k) pairs per slot; down_fmt must be FL_IQ2 */
+/* fl.h:30 -- routed experts of one arena batch for up to 8 (row, k) pairs per slot; gate/up IQ2_XXS, down_fmt FL_Q2K,
+ * FL_Q3K (the reference's, src/fused_layer.cu:541-550) or FL_IQ2; other codes exit 7 (the reference maps them to Q2_K) */
 void fl_wide_moe(FLCtx *, const void * gate, const void * up, const void * down, int down_fmt, int nexp, const int * midx, const int * rows,
                  const int * kidx, const float * wk, int nslots, int KE, int par);
 void fl_wide_mark(FLCtx *, int par);                 /* fl.h:31 */
@@ -62,8 +64,9 @@ void fl_spec(FLCtx *, const FLW * W1, void * KC1, void * VC1);
 void fl_sketch(FLCtx *, const float * TPROJ, const void * GSKT, int K);
 /* fl.h:43 -- what & 1: sel/wts/ncur/fi of the last routing (fl_ffn_begin) to the host mirrors, waited; other bits are attention's */
 void fl_fetch(FLCtx *, int n, int what, FLOut * out);
-/* fl.h:45 -- narrow MoE (n <= 8): gate/up/down = arena bases of nexp IQ2_XXS experts in ggml layout at ggml stride,
- * ids/w [n][KE] with ids = slot indices into the arena; -> out->h = routed + shared + ffn_inp, out->moe = routed. Waited. */
+/* fl.h:45 -- narrow MoE (n <= 8): gate/up/down = arena bases of nexp experts in ggml layout at ggml stride (gate/up
+ * IQ2_XXS; down in down_fmt = FL_Q2K or FL_Q3K as the reference, src/fused_layer.cu:599-608, or FL_IQ2), ids/w [n][KE]
+ * with ids = slot indices into the arena; -> out->h = routed + shared + ffn_inp, out->moe = routed. Waited. */
 void fl_moe(FLCtx *, const void * gate, const void * up, const void * down, int nexp, int down_fmt, const int * ids, const float * w, int KE, int n, FLOut * out);
 void fl_skip(FLCtx *, const float * mo, int n, FLOut * out);                /* fl.h:47 -- h = mo + shared + ffn_inp, waited */
 void fl_h2d(FLCtx *, void * dst, const void * src, size_t bytes);           /* fl.h:49 */
@@ -73,8 +76,13 @@ double fl_gpu_ms(FLCtx *, int which);                                       /* f
 /* ---------------------------------------------------------------- additive: the MoE tail of fl_attn without attention
  * Router + shared expert on N rows (N <= 64 per call; wrow >= 0 places them at rows wrow.. of a wide pass), given the
  * ffn-normed rows ncur and the residual ffn_inp as host floats [N][7168] (the reference computes both inside fl_attn,
- * src/fused_layer.cu:498-525). Uses W->gate_inp (F32 [256][7168]), W->probs_b, W->sh_gate/up/down (IQ2_XXS, ggml layout). */
+ * src/fused_layer.cu:498-525). Uses W->gate_inp (F32 [256][7168], or F16 with W->gate_f16), W->probs_b,
+ * W->sh_gate/up/down (ggml layout, formats of fl_set_shared_formats). */
 int fl_ffn_begin(FLCtx *, const FLW * W, int N, const float * ncur, const float * ffn_inp, int wrow);
+/* formats of W->sh_gate / sh_up / sh_down for fl_ffn_begin: FL_IQ2 (default, the all-IQ2_XXS configs) or K-quants;
+ * the reference's shards are (FL_Q5K, FL_Q5K, FL_Q6K) (src/fused_layer.h:14; FLW carries no format). gate and up are
+ * both FL_IQ2 or both K-quants. K-quant matrices are read in place and must be 4-byte aligned. */
+int fl_set_shared_formats(FLCtx *, int gate_fmt, int up_fmt, int down_fmt);
 /* routed experts behind fl_ffn_begin / fl_moe (default 256, the model's count; FLW carries no count) */
 int fl_set_experts(FLCtx *, int n_exp);
 /* routing rule: DeepSeek-V3 groups (default 8 groups, top-4 groups, top-8, x2.5); n_group = topk_group = 1 is the reference's rule */
@@ -109,6 +117,11 @@ int fl_route_dev(FLCtx *, const float * gate_inp, const float * probs_b, const f
 int fl_dispatch_dev(FLCtx *, const int * sel, int n, int topk, int n_exp, int * counts, int * offsets, int * perm, int * inv, int * act, int * nact);
 /* Q8_K of nrows x K floats (device): q [nrows][K] int8, d [nrows][K/256] */
 int fl_quant_q8k_dev(FLCtx *, const float * x, int nrows, int K, int8_t * q, float * d);
+/* y [n][R] = W . x_t for a K-quant matrix W (fmt FL_Q2K, FL_Q3K, FL_Q5K or FL_Q6K; R rows of K/256 ggml blocks, in
+ * place, start and size multiples of 4 bytes) and n Q8_K rows q [n][K], d [n][K/256] (device; K % 256 == 0, K <= 8192).
+ * The per-format mat-vec behind fl_moe / fl_ffn_begin (the reference's tc_matvec<F>, src/fused_layer.cu:102-158,
+ * 203-254): integer sub-block sums exact, fp32 over the blocks in order (Q2_K bit-identical to ggml's scalar dot). */
+int fl_kq_matvec_dev(FLCtx *, int fmt, const void * w, int R, int K, const int8_t * q, const float * d, int n, float * y);
 /* IQ2_XXS ggml layout <-> tiled layout for nmat matrices of R x K at byte strides (device, may not alias) */
 int fl_pack_iq2xxs(FLCtx *, const void * src_ggml, size_t src_stride, void * dst_tiled, size_t dst_stride, int R, int K, int nmat);
 int fl_unpack_iq2xxs(FLCtx *, const void * src_tiled, size_t src_stride, void * dst_ggml, size_t dst_stride, int R, int K, int nmat);

@@ -18,6 +18,8 @@ QK_K = 256
 IQ2_BYTES = 66
 
 FL_IQ2 = 4
+FL_Q6K, FL_Q5K, FL_Q2K, FL_Q3K = 1, 3, 5, 6
+KQ_BYTES = {FL_Q2K: 84, FL_Q3K: 110, FL_Q5K: 176, FL_Q6K: 210}
 FL_LAYOUT_GGML, FL_LAYOUT_TILED = 0, 1
 FL_OK, FL_EINVAL, FL_ENOMEM, FL_EHIP, FL_ERANGE, FL_ESCOPE = 0, -1, -2, -3, -4, -5
 
@@ -53,7 +55,7 @@ class FLOut(ctypes.Structure):
 ABI_SYMBOLS = [
     "fl_init", "fl_attn", "fl_wide_init", "fl_wide_moe", "fl_wide_mark", "fl_wide_wait", "fl_wide_finish", "fl_moe_outs",
     "fl_wide_outs", "fl_wide_skip", "fl_spec", "fl_sketch", "fl_fetch", "fl_moe", "fl_skip", "fl_h2d", "fl_wait_event",
-    "fl_gpu_ms", "fl_ffn_begin", "fl_set_experts", "fl_set_routing", "fl_moe_layer", "fl_moe_layer_normed", "fl_route_dev", "fl_dispatch_dev", "fl_quant_q8k_dev",
+    "fl_gpu_ms", "fl_ffn_begin", "fl_set_experts", "fl_set_routing", "fl_set_shared_formats", "fl_kq_matvec_dev", "fl_moe_layer", "fl_moe_layer_normed", "fl_route_dev", "fl_dispatch_dev", "fl_quant_q8k_dev",
     "fl_pack_iq2xxs", "fl_unpack_iq2xxs", "fl_rmsnorm_dev", "fl_synth_iq2xxs", "fl_synth_normal", "fl_probe_exp",
     "fl_debug", "fl_set_debug", "fl_set_fused", "fl_set_prefill_mfma", "fl_stream", "fl_set_stream", "fl_d2h", "fl_set_profile", "fl_stage_ms", "fl_sync", "fl_last_error", "fl_free",
 ]
@@ -83,6 +85,8 @@ def lib():
             "fl_last_error": (ctypes.c_char_p, [P_]),
             "fl_set_routing": (I, [P_, I, I, I, F]),
             "fl_set_experts": (I, [P_, I]),
+            "fl_set_shared_formats": (I, [P_, I, I, I]),
+            "fl_kq_matvec_dev": (I, [P_, I, P_, I, I, P_, P_, I, P_]),
             "fl_set_debug": (I, [P_, I]),
             "fl_set_fused": (I, [P_, I]),
             "fl_set_prefill_mfma": (I, [P_, I]),
@@ -194,6 +198,10 @@ class Context:
     def set_experts(self, n_exp=N_EXPERT):
         self.check(lib().fl_set_experts(self.ctx, n_exp))
 
+    def set_shared_formats(self, gate=FL_IQ2, up=FL_IQ2, down=FL_IQ2):
+        """Formats of FLW's shared expert for fl_ffn_begin; the reference's shards: (FL_Q5K, FL_Q5K, FL_Q6K)."""
+        self.check(lib().fl_set_shared_formats(self.ctx, gate, up, down))
+
     def set_debug(self, capture_gate_up):
         self.check(lib().fl_set_debug(self.ctx, 1 if capture_gate_up else 0))
 
@@ -214,6 +222,14 @@ class Context:
         d = t.empty((n, K // QK_K), dtype=t.float32, device=x.device)
         self.check(lib().fl_quant_q8k_dev(self.ctx, _ptr(x), n, K, _ptr(q), _ptr(d)))
         return q, d
+
+    def kq_matvec(self, fmt, w, R, K, q, d):
+        """y [n][R] = K-quant matrix w (uint8 device tensor, R x K/256 ggml blocks) . Q8_K rows (q [n][K], d [n][K/256])."""
+        t = self.torch
+        n = q.shape[0]
+        y = t.empty((n, R), dtype=t.float32, device=q.device)
+        self.check(lib().fl_kq_matvec_dev(self.ctx, fmt, _ptr(w), R, K, _ptr(q), _ptr(d), n, _ptr(y)))
+        return y
 
     def route(self, W, bias, x, topk=8):
         t = self.torch

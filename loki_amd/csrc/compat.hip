@@ -95,7 +95,9 @@ struct Compat {
     // rows of the last fl_ffn_begin (narrow pass)
     int N = 0;
     DBuf<float> ncur, fi, logits, probs, wts, h, o, sh_o, wr32; DBuf<int8_t> xq, hq; DBuf<float> xd, hd; DBuf<int> sel;
-    DBuf<uint8_t> sh_t; const void * sh_key[3] = { nullptr, nullptr, nullptr };
+    DBuf<uint8_t> sh_t; const void * sh_key[3] = { nullptr, nullptr, nullptr }; int sh_fkey[3] = { -1, -1, -1 };
+    int shf[3] = { FL_IQ2, FL_IQ2, FL_IQ2 };   // shared gate / up / down formats (fl_set_shared_formats)
+    DBuf<float> sg, su;                         // K-quant shared gate / up outputs
     // fl_moe
     DBuf<uint8_t> ag, au, ad; DBuf<int> ids, counts, offsets, perm, inv, act, nact; DBuf<float> w, hout, moe;
     std::vector<int> last_ids; int last_KE = 0, last_n = 0;
@@ -129,7 +131,7 @@ void compat_free(FLCtx * c) {
     }
     for (hipEvent_t e : s->wev) { if (e) { (void) hipEventDestroy(e); } }
     s->ncur.release(); s->fi.release(); s->logits.release(); s->probs.release(); s->wts.release(); s->h.release(); s->o.release(); s->sh_o.release(); s->wr32.release();
-    s->xq.release(); s->hq.release(); s->xd.release(); s->hd.release(); s->sel.release(); s->sh_t.release();
+    s->xq.release(); s->hq.release(); s->xd.release(); s->hd.release(); s->sel.release(); s->sh_t.release(); s->sg.release(); s->su.release();
     s->ag.release(); s->au.release(); s->ad.release(); s->ids.release(); s->counts.release(); s->offsets.release(); s->perm.release(); s->inv.release();
     s->act.release(); s->nact.release(); s->w.release(); s->hout.release(); s->moe.release();
     s->ncur_all.release(); s->base_all.release(); s->out_all.release(); s->xd_all.release(); s->xq_all.release();
@@ -150,28 +152,55 @@ static const int * zero_int(FLCtx * c) {
 #define FALLOC(buf, n) CK((buf).ensure(n))
 
 static size_t mat_bytes(int R, int K) { return (size_t) R * (K / QK) * IQ2B; }
+// bytes of one R x K matrix in format fmt (IQ2_XXS or a K-quant)
+static size_t fmt_bytes(int fmt, int R, int K) { return (size_t) R * (K / QK) * (size_t) (fmt == FL_IQ2 ? IQ2B : kq_block_bytes(fmt)); }
 
-// shared expert (IQ2_XXS) of N rows whose Q8_K activations are xq/xd -> out [N][E]
+// K-quant mat-vec of one matrix (ggml layout) on n Q8_K rows -> out [n][R]
+static void kq_single(FLCtx * c, int fmt, const void * w, const int8_t * q, const float * d, int n, int K, int R, float * out) {
+    KqArgs k{};
+    k.w = (const uint8_t *) w; k.estride = fmt_bytes(fmt, R, K); k.aq = q; k.ad = d; k.K = K; k.R = R;
+    k.act = nullptr; k.nact = nullptr; k.offsets = nullptr; k.n = n; k.out = out; k.ldo = R;
+    FCK(launch_kq_matvec(k, fmt, n, 1, c->st));
+}
+
+// shared expert of N rows whose Q8_K activations are xq/xd -> out [N][E]: IQ2_XXS matrices from the tiled copy sh_t,
+// K-quant matrices (the reference's Q5_K / Q5_K / Q6_K) read in place
 static void shared_expert(FLCtx * c, Compat * s, const int8_t * xq, const float * xd, int N, float * out) {
     const size_t mg = mat_bytes(H_, E_);
     FALLOC(s->h, (size_t) N * H_); FALLOC(s->hq, (size_t) N * H_); FALLOC(s->hd, (size_t) N * (H_ / QK));
     CK(ensure_expert_scratch(c, (size_t) N, E_, H_) == FL_OK ? hipSuccess : hipErrorOutOfMemory);
     ExpertArgs a = expert_args(c, N, 0, 1);
-    a.sh[0] = s->sh_t.p; a.sh[1] = s->sh_t.p + mg; a.aq = xq; a.ad = xd; a.K = E_; a.R = H_; a.nmat = 2;
-    a.act = zero_int(c); a.nact = zero_int(c); a.offsets = zero_int(c); a.perm = zero_int(c); a.topk = 1;
-    a.h = s->h.p; a.hq = s->hq.p; a.hd = s->hd.p;
-    expert_counters(c, a, 0);
-    FCK(launch_experts_gateup(a, c->ncu, c->st));
-    ExpertArgs d = a;
-    d.sh[0] = s->sh_t.p + 2 * mg; d.sh[1] = nullptr; d.aq = s->hq.p; d.ad = s->hd.p; d.K = H_; d.R = E_; d.nmat = 1;
-    d.h = nullptr; d.hq = nullptr; d.hd = nullptr; d.o = out; d.y = nullptr;
-    expert_counters(c, d, 1);
-    FCK(launch_experts_down(d, c->ncu, c->st));
+    if (s->shf[0] == FL_IQ2) {
+        a.sh[0] = s->sh_t.p; a.sh[1] = s->sh_t.p + mg; a.aq = xq; a.ad = xd; a.K = E_; a.R = H_; a.nmat = 2;
+        a.act = zero_int(c); a.nact = zero_int(c); a.offsets = zero_int(c); a.perm = zero_int(c); a.topk = 1;
+        a.h = s->h.p; a.hq = s->hq.p; a.hd = s->hd.p;
+        expert_counters(c, a, 0);
+        FCK(launch_experts_gateup(a, c->ncu, c->st));
+    } else {   // g, u, then h = silu(g) * u and its Q8_K (src/fused_layer.cu:522-523)
+        FALLOC(s->sg, (size_t) N * H_); FALLOC(s->su, (size_t) N * H_);
+        kq_single(c, s->shf[0], s->sh_key[0], xq, xd, N, E_, H_, s->sg.p);
+        kq_single(c, s->shf[1], s->sh_key[1], xq, xd, N, E_, H_, s->su.p);
+        FCK(launch_swiglu(s->sg.p, s->su.p, (int64_t) N * H_, s->h.p, c->st));
+        FCK(launch_quant_q8k(s->h.p, N, H_, s->hq.p, s->hd.p, c->st));
+    }
+    if (s->shf[2] == FL_IQ2) {
+        ExpertArgs d = a;
+        d.sh[0] = s->sh_t.p + 2 * mg; d.sh[1] = nullptr; d.aq = s->hq.p; d.ad = s->hd.p; d.K = H_; d.R = E_; d.nmat = 1;
+        d.act = zero_int(c); d.nact = zero_int(c); d.offsets = zero_int(c); d.perm = zero_int(c); d.topk = 1;
+        d.h = nullptr; d.hq = nullptr; d.hd = nullptr; d.o = out; d.y = nullptr;
+        expert_counters(c, d, 1);
+        FCK(launch_experts_down(d, c->ncu, c->st));
+    } else {
+        kq_single(c, s->shf[2], s->sh_key[2], s->hq.p, s->hd.p, N, H_, E_, out);   // src/fused_layer.cu:524
+    }
 }
 
 // routed experts of an arena (tiled copy ag/au/ad) for the pairs described by offsets/perm/act/nact -> o [P][E]
+// down_fmt: FL_IQ2 (tiled copy ad) or FL_Q2K / FL_Q3K read in place from down (expert stride E x H/256 blocks);
+// max_slots bounds the pairs of one expert
 static void routed_experts(FLCtx * c, Compat * s, const int8_t * xq, const float * xd, int n, int P, int KE, int nexp,
-                           const int * act, const int * nact, const int * offsets, const int * perm, float * o) {
+                           const int * act, const int * nact, const int * offsets, const int * perm, float * o,
+                           int down_fmt, const void * down, int max_slots) {
     FALLOC(s->h, (size_t) P * H_); FALLOC(s->hq, (size_t) P * H_); FALLOC(s->hd, (size_t) P * (H_ / QK));
     CK(ensure_expert_scratch(c, (size_t) P + n, E_, H_) == FL_OK ? hipSuccess : hipErrorOutOfMemory);
     ExpertArgs a = expert_args(c, n, P, 0);
@@ -180,6 +209,13 @@ static void routed_experts(FLCtx * c, Compat * s, const int8_t * xq, const float
     a.h = s->h.p; a.hq = s->hq.p; a.hd = s->hd.p;
     expert_counters(c, a, 0);
     FCK(launch_experts_gateup(a, c->ncu, c->st));
+    if (down_fmt != FL_IQ2) {   // src/fused_layer.cu:607-608 (tc_matvec<F_Q2K / F_Q3K>)
+        KqArgs k{};
+        k.w = (const uint8_t *) down; k.estride = fmt_bytes(down_fmt, E_, H_); k.aq = s->hq.p; k.ad = s->hd.p; k.K = H_; k.R = E_;
+        k.act = act; k.nact = nact; k.offsets = offsets; k.n = 0; k.out = o; k.ldo = E_;
+        FCK(launch_kq_matvec(k, down_fmt, max_slots, std::min(nexp, P), c->st));
+        return;
+    }
     ExpertArgs d = a;
     d.w[0] = s->ad.p; d.w[1] = nullptr; d.estride = mat_bytes(E_, H_); d.aq = s->hq.p; d.ad = s->hd.p; d.K = H_; d.R = E_; d.nmat = 1;
     d.h = nullptr; d.hq = nullptr; d.hd = nullptr; d.o = o; d.y = nullptr;
@@ -187,17 +223,27 @@ static void routed_experts(FLCtx * c, Compat * s, const int8_t * xq, const float
     FCK(launch_experts_down(d, c->ncu, c->st));
 }
 
-static void pack_arena(FLCtx * c, Compat * s, const void * gate, const void * up, const void * down, int nexp) {
+// IQ2_XXS arena matrices -> tiled copies (a K-quant down stays where it is)
+static void pack_arena(FLCtx * c, Compat * s, const void * gate, const void * up, const void * down, int nexp, int down_fmt) {
     const size_t mg = mat_bytes(H_, E_), md = mat_bytes(E_, H_);
-    FALLOC(s->ag, (size_t) nexp * mg); FALLOC(s->au, (size_t) nexp * mg); FALLOC(s->ad, (size_t) nexp * md);
+    FALLOC(s->ag, (size_t) nexp * mg); FALLOC(s->au, (size_t) nexp * mg);
     FCK(launch_pack_tiled((const uint8_t *) gate, mg, s->ag.p, mg, H_, E_, nexp, c->st));
     FCK(launch_pack_tiled((const uint8_t *) up, mg, s->au.p, mg, H_, E_, nexp, c->st));
-    FCK(launch_pack_tiled((const uint8_t *) down, md, s->ad.p, md, E_, H_, nexp, c->st));
+    if (down_fmt == FL_IQ2) {
+        FALLOC(s->ad, (size_t) nexp * md);
+        FCK(launch_pack_tiled((const uint8_t *) down, md, s->ad.p, md, E_, H_, nexp, c->st));
+    }
 }
 
-static void need_iq2(const char * fn, int fmt) {
-    if (fmt != FL_IQ2) {
-        std::fprintf(stderr, "[fused] %s: down format %d is not supported by this library (IQ2_XXS experts only)\n", fn, fmt);
+// routed down formats: the reference's Q2_K / Q3_K (src/fused_layer.cu:608) and IQ2_XXS (the all-IQ2_XXS configs).
+// The reference maps every code but FL_Q3K to Q2_K; codes outside these three are rejected here instead.
+static void need_down_fmt(const char * fn, int fmt, const void * down) {
+    if (fmt != FL_IQ2 && fmt != FL_Q2K && fmt != FL_Q3K) {
+        std::fprintf(stderr, "[fused] %s: down format %d is not supported (FL_IQ2, FL_Q2K or FL_Q3K)\n", fn, fmt);
+        std::exit(7);
+    }
+    if (fmt != FL_IQ2 && (reinterpret_cast<uintptr_t>(down) & 3u)) {
+        std::fprintf(stderr, "[fused] %s: the down arena must be 4-byte aligned\n", fn);
         std::exit(7);
     }
 }
@@ -215,8 +261,12 @@ extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur,
     if (!covers(W->gate_inp, (size_t) ne * E_ * (W->gate_f16 ? 2 : 4)) || !covers(W->probs_b, (size_t) ne * 4)) {
         return fail(c, FL_EINVAL, "router weight or bias allocation is smaller than %d experts x %d", ne, E_);
     }
-    if (!covers(W->sh_gate, mat_bytes(H_, E_)) || !covers(W->sh_up, mat_bytes(H_, E_)) || !covers(W->sh_down, mat_bytes(E_, H_))) {
-        return fail(c, FL_EINVAL, "shared-expert allocation smaller than one IQ2_XXS matrix");
+    if (!covers(W->sh_gate, fmt_bytes(s->shf[0], H_, E_)) || !covers(W->sh_up, fmt_bytes(s->shf[1], H_, E_)) || !covers(W->sh_down, fmt_bytes(s->shf[2], E_, H_))) {
+        return fail(c, FL_EINVAL, "shared-expert allocation smaller than one matrix of its format (%d, %d, %d)", s->shf[0], s->shf[1], s->shf[2]);
+    }
+    for (int i = 0; i < 3; ++i) {
+        const void * m = i == 0 ? W->sh_gate : i == 1 ? W->sh_up : W->sh_down;
+        if (s->shf[i] != FL_IQ2 && (reinterpret_cast<uintptr_t>(m) & 3u)) { return fail(c, FL_EINVAL, "K-quant shared matrices must be 4-byte aligned"); }
     }
     ALLOC(c, s->ncur, R); ALLOC(c, s->fi, R); ALLOC(c, s->logits, RMAX * ne); ALLOC(c, s->probs, RMAX * ne);
     ALLOC(c, s->sel, RMAX * MAXK); ALLOC(c, s->wts, RMAX * MAXK); ALLOC(c, s->xq, R); ALLOC(c, s->xd, RMAX * (E_ / QK)); ALLOC(c, s->sh_o, R);
@@ -224,12 +274,16 @@ extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur,
     TRY(c, hipMemcpyAsync(s->ncur.p, ncur, (size_t) N * E_ * 4, hipMemcpyHostToDevice, st));
     TRY(c, hipMemcpyAsync(s->fi.p, ffn_inp, (size_t) N * E_ * 4, hipMemcpyHostToDevice, st));
     const size_t mg = mat_bytes(H_, E_);
-    if (s->sh_key[0] != W->sh_gate || s->sh_key[1] != W->sh_up || s->sh_key[2] != W->sh_down) {
+    const void * shm[3] = { W->sh_gate, W->sh_up, W->sh_down };
+    if (s->sh_key[0] != shm[0] || s->sh_key[1] != shm[1] || s->sh_key[2] != shm[2] ||
+        s->sh_fkey[0] != s->shf[0] || s->sh_fkey[1] != s->shf[1] || s->sh_fkey[2] != s->shf[2]) {
         ALLOC(c, s->sh_t, 3 * mg);
-        TRY(c, launch_pack_tiled((const uint8_t *) W->sh_gate, mg, s->sh_t.p, mg, H_, E_, 1, st));
-        TRY(c, launch_pack_tiled((const uint8_t *) W->sh_up, mg, s->sh_t.p + mg, mg, H_, E_, 1, st));
-        TRY(c, launch_pack_tiled((const uint8_t *) W->sh_down, mg, s->sh_t.p + 2 * mg, mg, E_, H_, 1, st));
-        s->sh_key[0] = W->sh_gate; s->sh_key[1] = W->sh_up; s->sh_key[2] = W->sh_down;
+        for (int i = 0; i < 3; ++i) {   // IQ2_XXS matrices get a tiled copy; K-quant ones are read in place
+            if (s->shf[i] == FL_IQ2) {
+                TRY(c, launch_pack_tiled((const uint8_t *) shm[i], mg, s->sh_t.p + i * mg, mg, i < 2 ? H_ : E_, i < 2 ? E_ : H_, 1, st));
+            }
+            s->sh_key[i] = shm[i]; s->sh_fkey[i] = s->shf[i];
+        }
     }
     // the F16 router (W->gate_f16, fl.cu:317-319) is widened exactly to fp32 first; the logits then follow the same
     // contract as an F32 router holding the same values
@@ -270,7 +324,7 @@ extern "C" void fl_fetch(FLCtx * c, int n, int what, FLOut * out) {
 extern "C" void fl_moe(FLCtx * c, const void * gate, const void * up, const void * down, int nexp, int down_fmt, const int * ids,
                        const float * w, int KE, int n, FLOut * out) {
     std::memset(out, 0, sizeof(FLOut));
-    need_iq2("fl_moe", down_fmt);
+    need_down_fmt("fl_moe", down_fmt, down);
     Compat * s = cs(c);
     if (n <= 0 || n > NB || n > s->N || KE <= 0 || KE > MAXK || nexp <= 0 || nexp > NEXP_) {
         std::fprintf(stderr, "[fused] fl_moe: n %d (routed rows %d), KE %d, nexp %d out of range\n", n, s->N, KE, nexp); std::exit(7);
@@ -278,18 +332,20 @@ extern "C" void fl_moe(FLCtx * c, const void * gate, const void * up, const void
     for (int i = 0; i < n * KE; ++i) {
         if (ids[i] < 0 || ids[i] >= nexp) { std::fprintf(stderr, "[fused] fl_moe: slot id %d outside the arena of %d\n", ids[i], nexp); std::exit(7); }
     }
-    if (!covers(gate, nexp * mat_bytes(H_, E_)) || !covers(up, nexp * mat_bytes(H_, E_)) || !covers(down, nexp * mat_bytes(E_, H_))) {
+    if (!covers(gate, nexp * mat_bytes(H_, E_)) || !covers(up, nexp * mat_bytes(H_, E_)) || !covers(down, nexp * fmt_bytes(down_fmt, E_, H_))) {
         std::fprintf(stderr, "[fused] fl_moe: an arena allocation is smaller than %d experts\n", nexp); std::exit(7);
     }
     hipStream_t st = c->st; const int P = n * KE;
+    int max_slots = 1;
+    { std::vector<int> per(nexp, 0); for (int i = 0; i < P; ++i) { max_slots = std::max(max_slots, ++per[ids[i]]); } }
     CK(hipEventRecord(c->em0, st));
     FALLOC(s->ids, P); FALLOC(s->w, P); FALLOC(s->counts, nexp); FALLOC(s->offsets, nexp + 1); FALLOC(s->perm, P); FALLOC(s->inv, P);
     FALLOC(s->act, nexp); FALLOC(s->nact, 1); FALLOC(s->o, (size_t) P * E_); FALLOC(s->hout, (size_t) NB * E_); FALLOC(s->moe, (size_t) NB * E_);
     CK(hipMemcpyAsync(s->ids.p, ids, (size_t) P * 4, hipMemcpyHostToDevice, st));
     CK(hipMemcpyAsync(s->w.p, w, (size_t) P * 4, hipMemcpyHostToDevice, st));
-    pack_arena(c, s, gate, up, down, nexp);
+    pack_arena(c, s, gate, up, down, nexp, down_fmt);
     CK(launch_dispatch(s->ids.p, P, nexp, s->counts.p, s->offsets.p, s->perm.p, s->inv.p, s->act.p, s->nact.p, st));
-    routed_experts(c, s, s->xq.p, s->xd.p, n, P, KE, nexp, s->act.p, s->nact.p, s->offsets.p, s->perm.p, s->o.p);
+    routed_experts(c, s, s->xq.p, s->xd.p, n, P, KE, nexp, s->act.p, s->nact.p, s->offsets.p, s->perm.p, s->o.p, down_fmt, down, max_slots);
     k_combine_slots<<<nblk((int64_t) n * E_), 256, 0, st>>>(s->o.p, s->inv.p, s->ids.p, s->w.p, n, KE, s->sh_o.p, s->fi.p, s->hout.p, s->moe.p);
     CK(hipGetLastError());
     CK(hipMemcpyAsync(s->h_h, s->hout.p, (size_t) n * E_ * 4, hipMemcpyDeviceToHost, st));
@@ -350,7 +406,7 @@ extern "C" int fl_wide_init(FLCtx * c, int wmax, int KE) {
 
 extern "C" void fl_wide_moe(FLCtx * c, const void * gate, const void * up, const void * down, int down_fmt, int nexp, const int * midx,
                             const int * rows, const int * kidx, const float * wk, int nslots, int KE, int par) {
-    need_iq2("fl_wide_moe", down_fmt);
+    need_down_fmt("fl_wide_moe", down_fmt, down);
     Compat * s = cs(c);
     (void) par;
     if (KE != s->wke || nexp <= 0 || nexp > NEXP_ || nslots < 0) { std::fprintf(stderr, "[fused] fl_wide_moe: KE %d (init %d), nexp %d, nslots %d\n", KE, s->wke, nexp, nslots); std::exit(7); }
@@ -368,9 +424,11 @@ extern "C" void fl_wide_moe(FLCtx * c, const void * gate, const void * up, const
     for (int e = 0; e < nexp; ++e) { cnt[e + 1] += cnt[e]; }
     const int P = cnt[nexp];
     if (P == 0) { return; }
-    if (!covers(gate, nexp * mat_bytes(H_, E_)) || !covers(up, nexp * mat_bytes(H_, E_)) || !covers(down, nexp * mat_bytes(E_, H_))) {
+    if (!covers(gate, nexp * mat_bytes(H_, E_)) || !covers(up, nexp * mat_bytes(H_, E_)) || !covers(down, nexp * fmt_bytes(down_fmt, E_, H_))) {
         std::fprintf(stderr, "[fused] fl_wide_moe: an arena allocation is smaller than %d experts\n", nexp); std::exit(7);
     }
+    int max_slots = 1;
+    for (int e = 0; e < nexp; ++e) { max_slots = std::max(max_slots, cnt[e + 1] - cnt[e]); }
     std::vector<int> off(cnt), fillp(cnt.begin(), cnt.end() - 1), perm(P), prow(P), pk(P), act; std::vector<float> pw(P);
     for (int sl = 0; sl < nslots; ++sl) {
         for (int j = 0; j < NB; ++j) {
@@ -392,8 +450,9 @@ extern "C" void fl_wide_moe(FLCtx * c, const void * gate, const void * up, const
     CK(hipMemcpyAsync(s->w_row.p, prow.data(), (size_t) P * 4, hipMemcpyHostToDevice, st));
     CK(hipMemcpyAsync(s->w_k.p, pk.data(), (size_t) P * 4, hipMemcpyHostToDevice, st));
     CK(hipMemcpyAsync(s->w_wk.p, pw.data(), (size_t) P * 4, hipMemcpyHostToDevice, st));
-    pack_arena(c, s, gate, up, down, nexp);
-    routed_experts(c, s, s->xq_all.p, s->xd_all.p, s->wmax, P, KE, nexp, s->w_act.p, s->w_nact.p, s->w_off.p, s->w_perm.p, s->o.p);
+    pack_arena(c, s, gate, up, down, nexp, down_fmt);
+    routed_experts(c, s, s->xq_all.p, s->xd_all.p, s->wmax, P, KE, nexp, s->w_act.p, s->w_nact.p, s->w_off.p, s->w_perm.p, s->o.p,
+                   down_fmt, down, max_slots);
     k_wide_scatter<<<nblk((int64_t) P * E_), 256, 0, st>>>(s->o.p, s->w_row.p, s->w_k.p, s->w_wk.p, P, KE, s->out_all.p);
     CK(hipGetLastError());
     CK(hipStreamSynchronize(st));   // host tables above are stack vectors: they must outlive the queued copies
@@ -435,4 +494,18 @@ extern "C" void fl_wide_outs(FLCtx * c, int row, int KE, float * out) {
     if (row < 0 || row >= s->wmax || KE != s->wke) { std::fprintf(stderr, "[fused] fl_wide_outs: row %d, KE %d\n", row, KE); std::exit(7); }
     CK(hipStreamSynchronize(c->st));
     CK(hipMemcpy(out, s->out_all.p + (size_t) row * KE * E_, (size_t) KE * E_ * 4, hipMemcpyDeviceToHost));
+}
+
+// formats of FLW's shared expert for fl_ffn_begin: IQ2_XXS (default) or the reference's shards' Q5_K / Q5_K / Q6_K
+// (src/fused_layer.h:14, src/fused_layer.cu:520-524); gate and up are both IQ2_XXS or both K-quants
+extern "C" int fl_set_shared_formats(FLCtx * c, int gate_fmt, int up_fmt, int down_fmt) {
+    if (!c) { return FL_EINVAL; }
+    const int f[3] = { gate_fmt, up_fmt, down_fmt };
+    for (int i = 0; i < 3; ++i) {
+        if (f[i] != FL_IQ2 && kq_block_bytes(f[i]) == 0) { return fail(c, FL_EINVAL, "format %d is not IQ2_XXS or a K-quant (Q2_K, Q3_K, Q5_K, Q6_K)", f[i]); }
+    }
+    if ((gate_fmt == FL_IQ2) != (up_fmt == FL_IQ2)) { return fail(c, FL_EINVAL, "gate and up must both be IQ2_XXS or both K-quants"); }
+    Compat * s = cs(c);
+    s->shf[0] = gate_fmt; s->shf[1] = up_fmt; s->shf[2] = down_fmt;
+    return FL_OK;
 }

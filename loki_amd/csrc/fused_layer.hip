@@ -145,6 +145,25 @@ extern "C" int fl_quant_q8k_dev(FLCtx * c, const float * x, int nrows, int K, in
     return FL_OK;
 }
 
+extern "C" int fl_kq_matvec_dev(FLCtx * c, int fmt, const void * w, int R, int K, const int8_t * q, const float * d, int n, float * y) {
+    if (!c) { return FL_EINVAL; }
+    const int bs = kq_block_bytes(fmt);
+    if (bs == 0) { return fail(c, FL_EINVAL, "format %d is not a K-quant (FL_Q2K, FL_Q3K, FL_Q5K, FL_Q6K)", fmt); }
+    if (R <= 0 || K <= 0 || K % 256 || K > 8192 || n < 0) { return fail(c, FL_EINVAL, "R %d, K %d (a multiple of 256, at most 8192), n %d", R, K, n); }
+    if (n == 0) { return FL_OK; }
+    if (!w || !q || !d || !y) { return fail(c, FL_EINVAL, "null pointer"); }
+    const size_t mb = (size_t) R * (size_t) (K / 256) * (size_t) bs;
+    if (mb % 4 || (reinterpret_cast<uintptr_t>(w) & 3u)) { return fail(c, FL_EINVAL, "the matrix must start and end on 4-byte boundaries (%zu bytes)", mb); }
+    if (!covers(w, mb) || !covers(q, (size_t) n * K) || !covers(d, (size_t) n * (K / 256) * 4) || !covers(y, (size_t) n * R * 4)) {
+        return fail(c, FL_EINVAL, "an allocation is smaller than its shape");
+    }
+    KqArgs a{};
+    a.w = (const uint8_t *) w; a.estride = mb; a.aq = q; a.ad = d; a.K = K; a.R = R;
+    a.act = nullptr; a.nact = nullptr; a.offsets = nullptr; a.n = n; a.out = y; a.ldo = R;
+    TRY(c, launch_kq_matvec(a, fmt, n, 1, c->st));
+    return FL_OK;
+}
+
 static int pack_args(FLCtx * c, const void * s, const void * d, int R, int K, int nmat) {
     if (!s || !d) { return fail(c, FL_EINVAL, "null pointer"); }
     if (R <= 0 || R % 4 || K <= 0 || K % 1024 || nmat <= 0) { return fail(c, FL_EINVAL, "tiled layout needs R %% 4 == 0 and K %% 1024 == 0 (R %d, K %d)", R, K); }

@@ -110,6 +110,23 @@ hipError_t launch_synth_normal(float * dst, int64_t count, uint64_t seed, uint64
 // fp16 bits -> fp32 (exact widening)
 hipError_t launch_f16_to_f32(const uint16_t * src, float * dst, int64_t count, hipStream_t st);
 
+// ---------------------------------------------------------------- K-quant mat-vecs (kquant.hip)
+struct KqArgs {
+    const uint8_t * w; size_t estride;   // ggml-layout matrices [R][K/256 blocks], expert e at w + e * estride
+    const int8_t * aq; const float * ad; // Q8_K activation rows [.][K], [.][K/256]: slot s reads row s
+    int K, R;
+    const int * act, * nact, * offsets; // act != null: workgroup row y = active expert act[y] (y < *nact), slots
+                                         // offsets[e] .. offsets[e+1]; act == null: one matrix, slots 0 .. n-1
+    int n;
+    float * out; int ldo;                // out[s * ldo + r]
+};
+// block bytes of a K-quant format code (FL_Q2K 84, FL_Q3K 110, FL_Q5K 176, FL_Q6K 210; 0 = not a K-quant)
+int kq_block_bytes(int fmt);
+// max_slots: an upper bound of the slots of one expert (sizes the token groups); grid_experts >= *nact
+hipError_t launch_kq_matvec(const KqArgs & a, int fmt, int max_slots, int grid_experts, hipStream_t st);
+// h = silu(g) * u, element-wise under the exp contract
+hipError_t launch_swiglu(const float * g, const float * u, int64_t n, float * h, hipStream_t st);
+
 // ggml rms_norm (fp64 sum of fp32 squares) then the weight (w may be null = ones); one block per row
 hipError_t launch_rmsnorm(const float * x, const float * w, float * y, int n, int D, float eps, hipStream_t st);
 

@@ -244,17 +244,33 @@ int or_dispatch(const int32_t * sel, int64_t n, int topk, int n_exp, int32_t * c
 }
 
 /* ---------------------------------------------------------------- whole block */
-static void swiglu_q8(const float * g, const float * u, int64_t H, float * hout, int8_t * q, float * d) {
+static void swiglu_q8(const float * g, const float * u, int64_t H, float * hout, int8_t * q, float * d, int16_t * bs) {
     float * h = hout;
     for (int64_t i = 0; i < H; ++i) { h[i] = or_silu(g[i]) * u[i]; }
-    or_quantize_row_q8_K(h, q, d, NULL, H);
+    or_quantize_row_q8_K(h, q, d, bs, H);
 }
+
+/* one row . Q8_K row in the row's format (IQ2_XXS or a K-quant) */
+static float row_dot(int fmt, int64_t k, const uint8_t * w, const int8_t * q, const float * d, const int16_t * bs) {
+    return fmt == OR_IQ2 ? or_vec_dot_iq2_xxs_q8_K(k, w, q, d) : or_vec_dot_kq_q8_K(fmt, k, w, q, d, bs);
+}
+static size_t row_bytes(int fmt, int64_t k) { return (size_t) (k / QK_K) * (size_t) (fmt == OR_IQ2 ? IQ2_BYTES : or_kq_block_bytes(fmt)); }
 
 int or_moe_experts(const float * x, int64_t n, int64_t E, int64_t H, int topk, const int32_t * sel, const float * wts,
                    const uint8_t * const * gate, const uint8_t * const * up, const uint8_t * const * down,
                    const uint8_t * sh_gate, const uint8_t * sh_up, const uint8_t * sh_down,
                    float * y, float * g, float * u, float * o, float * sh, int nthreads) {
+    return or_moe_experts_fmt(x, n, E, H, topk, sel, wts, gate, up, down, sh_gate, sh_up, sh_down, NULL, y, g, u, o, sh, nthreads);
+}
+
+int or_moe_experts_fmt(const float * x, int64_t n, int64_t E, int64_t H, int topk, const int32_t * sel, const float * wts,
+                       const uint8_t * const * gate, const uint8_t * const * up, const uint8_t * const * down,
+                       const uint8_t * sh_gate, const uint8_t * sh_up, const uint8_t * sh_down, const int * fmts,
+                       float * y, float * g, float * u, float * o, float * sh, int nthreads) {
     if (E % QK_K || H % QK_K || n < 0 || topk <= 0) { return -1; }
+    const int fdn = fmts ? fmts[0] : OR_IQ2, fsg = fmts ? fmts[1] : OR_IQ2, fsu = fmts ? fmts[2] : OR_IQ2, fsd = fmts ? fmts[3] : OR_IQ2;
+    const int ok[4] = { fdn, fsg, fsu, fsd };
+    for (int i = 0; i < 4; ++i) { if (ok[i] != OR_IQ2 && or_kq_block_bytes(ok[i]) == 0) { return -1; } }
 #ifdef _OPENMP
     const int saved = omp_get_max_threads(); if (nthreads > 0) { omp_set_num_threads(nthreads); }
 #else
@@ -268,10 +284,12 @@ int or_moe_experts(const float * x, int64_t n, int64_t E, int64_t H, int topk, c
     int8_t * qh = (int8_t *) malloc((size_t) P * H); float * dh = (float *) malloc((size_t) P * nbH * 4); float * hh = (float *) malloc((size_t) (P > 0 ? P : 1) * H * 4);
     float * gs = (float *) malloc((size_t) n * H * 4), * us = (float *) malloc((size_t) n * H * 4);
     int8_t * qhs = (int8_t *) malloc((size_t) n * H); float * dhs = (float *) malloc((size_t) n * nbH * 4);
-    if (!qx || !dx || !gp || !up_ || !op || !shp || !qh || !dh || !hh || !gs || !us || !qhs || !dhs) { return -3; }
-    const size_t rbE = (size_t) nbE * IQ2_BYTES, rbH = (size_t) nbH * IQ2_BYTES;
+    int16_t * bx = (int16_t *) malloc((size_t) (n > 0 ? n : 1) * (E / 16) * 2), * bh = (int16_t *) malloc((size_t) (P > 0 ? P : 1) * (H / 16) * 2);
+    int16_t * bhs = (int16_t *) malloc((size_t) (n > 0 ? n : 1) * (H / 16) * 2);
+    if (!qx || !dx || !gp || !up_ || !op || !shp || !qh || !dh || !hh || !gs || !us || !qhs || !dhs || !bx || !bh || !bhs) { return -3; }
+    const size_t rbE = row_bytes(OR_IQ2, E), rbEg = row_bytes(fsg, E), rbEu = row_bytes(fsu, E), rbH = row_bytes(fdn, H), rbHs = row_bytes(fsd, H);
     #pragma omp parallel for schedule(static)
-    for (int64_t t = 0; t < n; ++t) { or_quantize_row_q8_K(x + t * E, qx + t * E, dx + t * nbE, NULL, E); }
+    for (int64_t t = 0; t < n; ++t) { or_quantize_row_q8_K(x + t * E, qx + t * E, dx + t * nbE, bx + t * (E / 16), E); }
     /* gate / up of every (t, k) pair and of the shared expert per token */
     #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < (P + n) * H; ++i) {
@@ -282,20 +300,20 @@ int or_moe_experts(const float * x, int64_t n, int64_t E, int64_t H, int topk, c
             up_[p * H + r] = or_vec_dot_iq2_xxs_q8_K(E, up[e] + r * rbE, qx + t * E, dx + t * nbE);
         } else {
             const int64_t t = p - P;
-            gs[t * H + r] = or_vec_dot_iq2_xxs_q8_K(E, sh_gate + r * rbE, qx + t * E, dx + t * nbE);
-            us[t * H + r] = or_vec_dot_iq2_xxs_q8_K(E, sh_up + r * rbE, qx + t * E, dx + t * nbE);
+            gs[t * H + r] = row_dot(fsg, E, sh_gate + r * rbEg, qx + t * E, dx + t * nbE, bx + t * (E / 16));
+            us[t * H + r] = row_dot(fsu, E, sh_up + r * rbEu, qx + t * E, dx + t * nbE, bx + t * (E / 16));
         }
     }
     #pragma omp parallel for schedule(static)
     for (int64_t p = 0; p < P + n; ++p) {
-        if (p < P) { swiglu_q8(gp + p * H, up_ + p * H, H, hh + p * H, qh + p * H, dh + p * nbH); }
-        else { const int64_t t = p - P; swiglu_q8(gs + t * H, us + t * H, H, gs + t * H, qhs + t * H, dhs + t * nbH); }   /* h over g in place */
+        if (p < P) { swiglu_q8(gp + p * H, up_ + p * H, H, hh + p * H, qh + p * H, dh + p * nbH, bh + p * (H / 16)); }
+        else { const int64_t t = p - P; swiglu_q8(gs + t * H, us + t * H, H, gs + t * H, qhs + t * H, dhs + t * nbH, bhs + t * (H / 16)); }   /* h over g in place */
     }
     #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < (P + n) * E; ++i) {
         const int64_t p = i / E, r = i % E;
-        if (p < P) { const int e = sel[p]; op[p * E + r] = or_vec_dot_iq2_xxs_q8_K(H, down[e] + r * rbH, qh + p * H, dh + p * nbH); }
-        else { const int64_t t = p - P; shp[t * E + r] = or_vec_dot_iq2_xxs_q8_K(H, sh_down + r * rbH, qhs + t * H, dhs + t * nbH); }
+        if (p < P) { const int e = sel[p]; op[p * E + r] = row_dot(fdn, H, down[e] + r * rbH, qh + p * H, dh + p * nbH, bh + p * (H / 16)); }
+        else { const int64_t t = p - P; shp[t * E + r] = row_dot(fsd, H, sh_down + r * rbHs, qhs + t * H, dhs + t * nbH, bhs + t * (H / 16)); }
     }
     /* combine as the reference's graph: exo * w, then views added in k order, then + shared (eng:970-975) */
     #pragma omp parallel for schedule(static)
@@ -304,7 +322,7 @@ int or_moe_experts(const float * x, int64_t n, int64_t E, int64_t H, int topk, c
         for (int kk = 1; kk < topk; ++kk) { m = m + op[(t * topk + kk) * E + r] * wts[t * topk + kk]; }
         y[i] = m + shp[i];
     }
-    free(qx); free(dx); free(qh); free(dh); free(hh); free(gs); free(us); free(qhs); free(dhs);
+    free(qx); free(dx); free(qh); free(dh); free(hh); free(gs); free(us); free(qhs); free(dhs); free(bx); free(bh); free(bhs);
     if (!g) { free(gp); } if (!u) { free(up_); } if (!o) { free(op); } if (!sh) { free(shp); }
 #ifdef _OPENMP
     if (nthreads > 0) { omp_set_num_threads(saved); }

@@ -59,12 +59,19 @@ int or_moe_experts(const float * x, int64_t n, int64_t E, int64_t H, int topk, c
 void or_rmsnorm(const float * x, const float * w, float * y, int64_t n, int64_t d, float eps);
 
 /* K-quant formats of the reference's real shards (kquant_oracle.c) */
-enum { OR_Q2K = 5, OR_Q3K = 6, OR_Q5K = 3, OR_Q6K = 1 };   /* the FL_* codes of include/loki_moe.h */
+enum { OR_Q2K = 5, OR_Q3K = 6, OR_Q5K = 3, OR_Q6K = 1, OR_IQ2 = 4 };   /* the FL_* codes of include/loki_moe.h */
 int or_kq_block_bytes(int fmt);
 void or_dequantize_row_kq(int fmt, const uint8_t * blocks, float * y, int64_t k);
 float or_vec_dot_kq_q8_K(int fmt, int64_t k, const uint8_t * w, const int8_t * q8, const float * d8, const int16_t * bsums);
 void or_matvec_kq(int fmt, const uint8_t * w, int64_t rows, int64_t k, const int8_t * q, const float * d, const int16_t * bsums,
                   int64_t nt, float * y);
+/* or_moe_experts with per-matrix formats: fmts = { routed down, shared gate, shared up, shared down } (OR_IQ2 or a
+ * K-quant; routed gate/up stay IQ2_XXS as in the reference's arena), NULL = IQ2_XXS everywhere. Rows are ggml rows of
+ * the format (K/256 blocks). */
+int or_moe_experts_fmt(const float * x, int64_t n, int64_t E, int64_t H, int topk, const int32_t * sel, const float * wts,
+                       const uint8_t * const * gate, const uint8_t * const * up, const uint8_t * const * down,
+                       const uint8_t * sh_gate, const uint8_t * sh_up, const uint8_t * sh_down, const int * fmts,
+                       float * y, float * g, float * u, float * o, float * sh, int nthreads);
 
 #ifdef __cplusplus
 }

@@ -53,6 +53,8 @@ def lib():
         L.or_moe_forward.argtypes = [P, I64, I64, I64, P, P, I, I, I, I, F, P, P, P, P, P, P, P, P, P, P, P, P, P, I]
         L.or_moe_experts.restype = I
         L.or_moe_experts.argtypes = [P, I64, I64, I64, I, P, P, P, P, P, P, P, P, P, P, P, P, P, I]
+        L.or_moe_experts_fmt.restype = I
+        L.or_moe_experts_fmt.argtypes = [P, I64, I64, I64, I, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I]
         L.or_rmsnorm.restype = None; L.or_rmsnorm.argtypes = [P, P, P, I64, I64, F]
         _lib = L
     return _lib
@@ -220,7 +222,9 @@ def moe_forward(x, W, bias, gate, up, down, sh_gate, sh_up, sh_down, n_group=8, 
     return out
 
 
-def moe_experts(x, sel, wts, gate, up, down, sh_gate, sh_up, sh_down, H=2048, want=(), nthreads=0, n_exp=256):
+def moe_experts(x, sel, wts, gate, up, down, sh_gate, sh_up, sh_down, H=2048, want=(), nthreads=0, n_exp=256, fmts=None):
+    """Experts on given routing. fmts = (routed down, shared gate, shared up, shared down) format codes (IQ2 = 4 or a
+    K-quant); None = IQ2_XXS everywhere."""
     x = _c(x, np.float32); n, E = x.shape
     sel = _c(sel, np.int32); wts = _c(wts, np.float32); topk = sel.shape[1]
     y = np.empty((n, E), np.float32); P = n * topk
@@ -228,8 +232,9 @@ def moe_experts(x, sel, wts, gate, up, down, sh_gate, sh_up, sh_down, H=2048, wa
            (("g", (P, H)), ("u", (P, H)), ("o", (P, E)), ("sh", (n, E))) if k in want}
     ga, k1 = _ptr_array(gate, n_exp); ua, k2 = _ptr_array(up, n_exp); da, k3 = _ptr_array(down, n_exp)
     sg, su, sd = _c(sh_gate, np.uint8), _c(sh_up, np.uint8), _c(sh_down, np.uint8)
-    rc = lib().or_moe_experts(_p(x), n, E, H, topk, _p(sel), _p(wts), ga, ua, da, _p(sg), _p(su), _p(sd), _p(y),
-                              _p(out.get("g")), _p(out.get("u")), _p(out.get("o")), _p(out.get("sh")), nthreads)
+    fm = None if fmts is None else np.ascontiguousarray(fmts, np.int32)
+    rc = lib().or_moe_experts_fmt(_p(x), n, E, H, topk, _p(sel), _p(wts), ga, ua, da, _p(sg), _p(su), _p(sd), _p(fm), _p(y),
+                                  _p(out.get("g")), _p(out.get("u")), _p(out.get("o")), _p(out.get("sh")), nthreads)
     if rc != 0:
         raise ValueError("oracle moe_experts failed (%d)" % rc)
     out["y"] = y

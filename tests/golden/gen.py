@@ -40,6 +40,26 @@ def iq2_matrix(seed, stream, rows, cols):
     return blk.reshape(-1)
 
 
+# K-quant block bytes and the offsets of their fp16 d / dmin fields (FL_* format codes)
+KQ_LAYOUT = {5: (84, 80, 82), 6: (110, 108, None), 3: (176, 0, 2), 1: (210, 208, None)}
+
+
+def kq_matrix(seed, stream, fmt, rows, cols):
+    """ggml-layout K-quant matrix bytes (fmt = FL_Q2K 5, FL_Q3K 6, FL_Q5K 3, FL_Q6K 1): quant and scale bytes from
+    hash words, fp16 d (and dmin) bits drawn from [0x0C00, 0x1C00) (about 6e-5 .. 4e-3)."""
+    bs, od, om = KQ_LAYOUT[fmt]
+    nb = rows * (cols // 256)
+    nw = (bs + 7) // 8 + 1
+    w = words(seed, stream, nb * nw).reshape(nb, nw)
+    blk = w[:, :nw - 1].copy().view(np.uint8).reshape(nb, -1)[:, :bs].copy()
+    dd = (np.uint64(0x0C00) + w[:, nw - 1] % np.uint64(0x1000)).astype(np.uint16)
+    blk[:, od:od + 2] = dd.view(np.uint8).reshape(nb, 2)
+    if om is not None:
+        dm = (np.uint64(0x0C00) + (w[:, nw - 1] >> np.uint64(32)) % np.uint64(0x1000)).astype(np.uint16)
+        blk[:, om:om + 2] = dm.view(np.uint8).reshape(nb, 2)
+    return blk.reshape(-1)
+
+
 def layer(seed, n_exp, E, H, bias_scale=0.01):
     W = uniform(seed, 1, (n_exp, E), 0.035)
     b = uniform(seed, 2, (n_exp,), bias_scale)

@@ -1,0 +1,247 @@
+"""GPU: the K-quant formats of the reference's real shards against the CPU checker (oracle/kquant_oracle.c):
+fl_kq_matvec_dev per format and shape (the reference's tc_matvec<F_Q2K/Q3K/Q5K/Q6K>, src/fused_layer.cu:102-158,
+203-254), the routed down in Q2_K / Q3_K through fl_moe and fl_wide_moe (:541-550, 599-608), and the shared expert in
+Q5_K / Q5_K / Q6_K through fl_ffn_begin (:520-524).
+
+Tolerances: the integer sub-block sums are exact, and Q2_K's fp32 order is ggml's (bit-identical). Q3_K / Q5_K / Q6_K
+add the per-block terms in block order where ggml keeps 8 column-residue partial sums, so they differ by fp32 rounding
+only: |y - ref| <= 1e-5 * sum |w x| per output. Block outputs behind a non-exact stage are held to 1e-4 (L2, relative)
+and 1e-3 of the largest |output| (max), inside the 2e-3 / 1e-2 parity bar."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests.golden import gen
+
+pytestmark = pytest.mark.gpu
+
+E, H, KE = 7168, 2048, 8
+FMTS = [orc.Q2K, orc.Q3K, orc.Q5K, orc.Q6K]
+NAMES = {orc.Q2K: "q2_K", orc.Q3K: "q3_K", orc.Q5K: "q5_K", orc.Q6K: "q6_K"}
+
+
+def f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def cptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def within_rounding(got, ref, wd, xd, rel=1e-5):
+    """|got - ref| <= rel * sum |w x| elementwise; wd [R, K] and xd [n, K] dequantized operands"""
+    scale = np.abs(xd.astype(np.float64)) @ np.abs(wd.astype(np.float64)).T
+    err = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    return bool(np.all(err <= rel * scale)), float((err / np.maximum(scale, 1e-30)).max())
+
+
+def bar_close(got, ref, l2=1e-4, mx=1e-3):
+    d = got.astype(np.float64) - ref.astype(np.float64)
+    r = ref.astype(np.float64)
+    e_l2 = np.linalg.norm(d) / max(np.linalg.norm(r), 1e-30)
+    e_mx = np.abs(d).max() / max(np.abs(r).max(), 1e-30)
+    return e_l2 <= l2 and e_mx <= mx, (e_l2, e_mx)
+
+
+@pytest.mark.parametrize("fmt", FMTS, ids=lambda f: NAMES[f])
+@pytest.mark.parametrize("K,R,n", [(2048, 130, 3), (7168, 66, 2), (256, 98, 5), (4096, 64, 1), (2048, 200, 9)])
+def test_kq_matvec(ctx, fmt, K, R, n):
+    import torch
+    w = gen.kq_matrix(31 + fmt, K + R, fmt, R, K)
+    x = gen.uniform(32 + fmt, K + n, (n, K), 3.0)
+    q, d, bs = orc.quantize_q8k(x)
+    ref = orc.matvec_kq(fmt, w, R, K, q, d, bs)
+    print("kq_matvec fmt %d K %d R %d n %d" % (fmt, K, R, n), flush=True)
+    y = ctx.kq_matvec(fmt, torch.from_numpy(w).cuda(), R, K, torch.from_numpy(q).cuda(), torch.from_numpy(d).cuda())
+    ctx.sync()
+    y = y.cpu().numpy()
+    if fmt == orc.Q2K:
+        assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
+    else:
+        wd = orc.dequant_kq(fmt, w, K)
+        xd = q.astype(np.float32) * np.repeat(d, 256, axis=1)
+        ok, worst = within_rounding(y, ref, wd, xd)
+        assert ok, worst
+
+
+def test_kq_matvec_rejects(ctx):
+    """argument errors come back as FL_EINVAL with a message, before any launch"""
+    import torch
+    from loki_amd import lib, FL_EINVAL, FL_Q3K
+    w = torch.zeros(110, dtype=torch.uint8, device="cuda")
+    q = torch.zeros((1, 256), dtype=torch.int8, device="cuda"); d = torch.zeros((1, 1), dtype=torch.float32, device="cuda")
+    y = torch.zeros((1, 1), dtype=torch.float32, device="cuda")
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    assert lib().fl_kq_matvec_dev(ctx.ctx, 4, P(w), 1, 256, P(q), P(d), 1, P(y)) == FL_EINVAL          # IQ2 is not a K-quant
+    assert lib().fl_kq_matvec_dev(ctx.ctx, FL_Q3K, P(w), 1, 256, P(q), P(d), 1, P(y)) == FL_EINVAL     # 110 B: not 4-byte sized
+    assert lib().fl_kq_matvec_dev(ctx.ctx, FL_Q3K, P(w), 2, 256, P(q), P(d), -1, P(y)) == FL_EINVAL    # n < 0
+    assert lib().fl_kq_matvec_dev(ctx.ctx, FL_Q3K, P(w), 1, 300, P(q), P(d), 1, P(y)) == FL_EINVAL     # K % 256
+    assert b"K-quant" in lib().fl_last_error(ctx.ctx) or b"256" in lib().fl_last_error(ctx.ctx)
+
+
+# ---------------------------------------------------------------- the reference-named entry points
+@pytest.fixture(scope="module")
+def real_layer(ctx):
+    """16 routed experts: IQ2_XXS gate/up (ggml layout) with Q2_K and Q3_K downs, IQ2_XXS and K-quant shared experts"""
+    import torch
+    W, b, gate, up, down, sh = gen.layer(202, 16, E, H)
+    kdown = {f: [gen.kq_matrix(203, 40 + e, f, E, H) for e in range(16)] for f in (orc.Q2K, orc.Q3K)}
+    ksh = (gen.kq_matrix(204, 1, orc.Q5K, H, E), gen.kq_matrix(204, 2, orc.Q5K, H, E), gen.kq_matrix(204, 3, orc.Q6K, E, H))
+    dev = dict(W=torch.from_numpy(W).cuda(), b=torch.from_numpy(b).cuda(),
+               gate=torch.from_numpy(np.concatenate(gate)).cuda(), up=torch.from_numpy(np.concatenate(up)).cuda(),
+               kdown={f: torch.from_numpy(np.concatenate(m)).cuda() for f, m in kdown.items()},
+               sh=[torch.from_numpy(m).cuda() for m in sh], ksh=[torch.from_numpy(m).cuda() for m in ksh])
+    ctx.set_experts(16)
+    yield dict(W=W, b=b, gate=gate, up=up, kdown=kdown, sh=sh, ksh=ksh), dev
+    ctx.set_experts()
+    ctx.set_shared_formats()
+
+
+def _flw(dev, kshared):
+    from loki_amd import FLW
+    w = FLW()
+    w.gate_inp = dev["W"].data_ptr(); w.probs_b = dev["b"].data_ptr()
+    w.sh_gate, w.sh_up, w.sh_down = (t.data_ptr() for t in (dev["ksh"] if kshared else dev["sh"]))
+    w.gate_f16 = 0
+    return w
+
+
+def _arena(dev, used, fmt):
+    import torch
+    mg = H * (E // 256) * 66
+    md = E * (H // 256) * orc.kq_block_bytes(fmt)
+    idx = torch.as_tensor(used, dtype=torch.long).cuda()
+    return (dev["gate"].view(16, mg)[idx].contiguous().view(-1), dev["up"].view(16, mg)[idx].contiguous().view(-1),
+            dev["kdown"][fmt].view(16, md)[idx].contiguous().view(-1))
+
+
+def _route(ctx, flw, x, fi, wrow=-1):
+    from loki_amd import FLOut, lib
+    n = x.shape[0]
+    ctx.check(lib().fl_ffn_begin(ctx.ctx, ctypes.byref(flw), n, cptr(x), cptr(fi), wrow))
+    out = FLOut()
+    lib().fl_fetch(ctx.ctx, n, 1, ctypes.byref(out))
+    sel = np.ctypeslib.as_array(out.sel, shape=(n * KE,)).reshape(n, KE).copy()
+    wts = np.ctypeslib.as_array(out.wts, shape=(n * KE,)).reshape(n, KE).copy()
+    return sel, wts
+
+
+@pytest.mark.parametrize("down_fmt", [orc.Q2K, orc.Q3K], ids=["q2_K", "q3_K"])
+@pytest.mark.parametrize("kshared", [False, True], ids=["iq2_shared", "q5q5q6_shared"])
+def test_narrow_real_formats(ctx, real_layer, down_fmt, kshared):
+    """fl_ffn_begin -> fl_fetch -> fl_moe with the routed down in Q2_K / Q3_K and the shared expert in IQ2_XXS or
+    Q5_K / Q5_K / Q6_K; with Q2_K down and the IQ2_XXS shared expert every stage is exact, so h and moe are bit-identical
+    to the checker composed with moe_combine's slot order (src/fused_layer.cu:366-372)."""
+    from loki_amd import FLOut, lib
+    host, dev = real_layer
+    ctx.set_routing(8, 4, 8, 2.5)
+    if kshared:
+        ctx.set_shared_formats(orc.Q5K, orc.Q5K, orc.Q6K)
+    else:
+        ctx.set_shared_formats()
+    n = 5
+    x = gen.uniform(9, 3, (n, E), 2.0); fi = gen.uniform(9, 4, (n, E), 1.0)
+    print("narrow down_fmt %d kshared %d n %d" % (down_fmt, kshared, n), flush=True)
+    sel, wts = _route(ctx, _flw(dev, kshared), x, fi)
+    used = sorted(set(sel.ravel().tolist()))
+    remap = {e: i for i, e in enumerate(used)}
+    ids = np.array([[remap[e] for e in row] for row in sel], np.int32)
+    ga, ua, da = _arena(dev, used, down_fmt)
+    out = FLOut()
+    lib().fl_moe(ctx.ctx, ga.data_ptr(), ua.data_ptr(), da.data_ptr(), len(used), down_fmt, cptr(ids), cptr(f32(wts)), KE, n,
+                 ctypes.byref(out))
+    h = np.ctypeslib.as_array(out.h, shape=(n * E,)).reshape(n, E).copy()
+    moe = np.ctypeslib.as_array(out.moe, shape=(n * E,)).reshape(n, E).copy()
+    sh = host["ksh"] if kshared else host["sh"]
+    fm = (down_fmt,) + ((orc.Q5K, orc.Q5K, orc.Q6K) if kshared else (4, 4, 4))
+    ref = orc.moe_experts(x, sel, wts, host["gate"], host["up"], host["kdown"][down_fmt], *sh, want=("o", "sh"), n_exp=16, fmts=fm)
+    o = ref["o"].reshape(n, KE, E)
+    vm = np.zeros((n, E), np.float32)
+    for t in range(n):
+        for m in range(len(used)):
+            ks = [k for k in range(KE) if ids[t, k] == m]
+            if not ks:
+                continue
+            wt = np.float32(0)
+            for k in ks:
+                wt = np.float32(wt + wts[t, k])
+            vm[t] = (vm[t] + wt * o[t, ks[0]]).astype(np.float32)
+    want_h = ((vm + ref["sh"]).astype(np.float32) + fi).astype(np.float32)
+    if down_fmt == orc.Q2K:
+        assert np.array_equal(moe.view(np.uint32), vm.view(np.uint32))
+    else:
+        ok, err = bar_close(moe, vm)
+        assert ok, err
+    if down_fmt == orc.Q2K and not kshared:
+        assert np.array_equal(h.view(np.uint32), want_h.view(np.uint32))
+    else:
+        ok, err = bar_close(h, want_h)
+        assert ok, err
+
+
+def test_wide_q3k_down(ctx, real_layer):
+    """the wide pass (fl_wide_init / fl_ffn_begin(wrow) / fl_wide_moe / fl_wide_finish) with a Q3_K down and the
+    K-quant shared expert: 16 experts and top-8 give each expert about 20 of the 320 pairs, so the mat-vec runs several
+    token groups per expert"""
+    from loki_amd import FLOut, lib
+    host, dev = real_layer
+    ctx.set_routing(1, 1, 8, 1.0)
+    ctx.set_shared_formats(orc.Q5K, orc.Q5K, orc.Q6K)
+    n, EB = 40, 6
+    assert lib().fl_wide_init(ctx.ctx, 64, KE) == 1
+    x = gen.uniform(10, 3, (n, E), 2.0); fi = gen.uniform(10, 4, (n, E), 1.0)
+    flw = _flw(dev, True)
+    sels, wtss = [], []
+    for r0 in range(0, n, 16):
+        g = min(16, n - r0)
+        s, w = _route(ctx, flw, x[r0:r0 + g].copy(), fi[r0:r0 + g].copy(), r0)
+        sels.append(s); wtss.append(w)
+    sel, wts = np.concatenate(sels), np.concatenate(wtss)
+    used = sorted(set(sel.ravel().tolist()))
+    byexp = {e: [] for e in used}
+    for i in range(n):
+        for k in range(KE):
+            byexp[sel[i, k]].append((i, k))
+    print("wide q3_K: %d experts, max %d pairs" % (len(used), max(len(v) for v in byexp.values())), flush=True)
+    for bi, b0 in enumerate(range(0, len(used), EB)):
+        batch = used[b0:b0 + EB]
+        par = bi & 1
+        lib().fl_wide_wait(ctx.ctx, par)
+        midx, rows, kidx, wk = [], [], [], []
+        for u, e in enumerate(batch):
+            lst = byexp[e]
+            for i0 in range(0, len(lst), 8):
+                midx.append(u)
+                for j in range(8):
+                    if i0 + j < len(lst):
+                        r, k = lst[i0 + j]; rows.append(r); kidx.append(k); wk.append(wts[r, k])
+                    else:
+                        rows.append(-1); kidx.append(0); wk.append(0.0)
+        ga, ua, da = _arena(dev, batch, orc.Q3K)
+        lib().fl_wide_moe(ctx.ctx, ga.data_ptr(), ua.data_ptr(), da.data_ptr(), orc.Q3K, len(batch), cptr(np.int32(midx)),
+                          cptr(np.int32(rows)), cptr(np.int32(kidx)), cptr(f32(wk)), len(midx), KE, par)
+        lib().fl_wide_mark(ctx.ctx, par)
+    out = FLOut()
+    lib().fl_wide_finish(ctx.ctx, n, KE, ctypes.byref(out))
+    h = np.ctypeslib.as_array(out.h, shape=(n * E,)).reshape(n, E).copy()
+    moe = np.ctypeslib.as_array(out.moe, shape=(n * E,)).reshape(n, E).copy()
+    ref = orc.moe_experts(x, sel, wts, host["gate"], host["up"], host["kdown"][orc.Q3K], *host["ksh"], want=("o", "sh"),
+                          n_exp=16, fmts=(orc.Q3K, orc.Q5K, orc.Q5K, orc.Q6K))
+    o = ref["o"].reshape(n, KE, E)
+    m = np.zeros((n, E), np.float32)
+    for k in range(KE):
+        m = (m + wts[:, k:k + 1] * o[:, k]).astype(np.float32)
+    ok, err = bar_close(moe, m)
+    assert ok, err
+    ok, err = bar_close(h, ((fi + ref["sh"]).astype(np.float32) + m).astype(np.float32))
+    assert ok, err
+    ctx.set_routing(8, 4, 8, 2.5)
+
+
+def test_shared_formats_rejects(ctx):
+    from loki_amd import lib, FL_EINVAL
+    assert lib().fl_set_shared_formats(ctx.ctx, 3, 4, 1) == FL_EINVAL   # gate K-quant, up IQ2_XXS
+    assert lib().fl_set_shared_formats(ctx.ctx, 0, 0, 1) == FL_EINVAL   # Q4_K is not supported
+    ctx.set_shared_formats()
