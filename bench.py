@@ -155,6 +155,56 @@ def run_stack(ctx, torch, steps, warmup, nlayers=STACK_LAYERS, seed=20260301):
             "synth_s": round(t_synth, 1)}
 
 
+# K-quant formats of the reference's real shards: block bytes and fp16 d / dmin offsets (FL_* codes)
+KQ = {5: ("q2_K", 84, 80, 82), 6: ("q3_K", 110, 108, None), 3: ("q5_K", 176, 0, 2), 1: ("q6_K", 210, 208, None)}
+
+
+def kq_random(torch, fmt, R, K, seed):
+    """random K-quant matrix bytes on the device: uniform quant/scale bytes, fp16 d (and dmin) in [6e-5, 4e-3]"""
+    _, bs, od, om = KQ[fmt]
+    nb = R * (K // 256)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    blk = torch.randint(0, 256, (nb, bs), dtype=torch.uint8, device="cuda", generator=g)
+    for off in (od, om):
+        if off is not None:
+            d = torch.randint(0x0C00, 0x1C00, (nb,), dtype=torch.int32, device="cuda", generator=g).to(torch.int16)
+            blk[:, off:off + 2] = d.view(torch.uint8).view(nb, 2)
+    return blk.view(-1)
+
+
+def run_kquant(ctx, torch, iters=20, seed=20260401):
+    """fl_kq_matvec_dev on the decode shapes of the reference's real formats, each launch reading weights from HBM
+    (copies rotated past the 256 MB MALL): the routed down of 64 experts x 1 token as one 458,752-row matrix (Q2_K,
+    Q3_K), and the shared expert's gate (Q5_K, [2048, 7168]) and down (Q6_K, [7168, 2048]) on 8 tokens."""
+    out = {}
+    cases = (("routed_down_q2_K_64x1", 5, 64 * E, H, 1, 1), ("routed_down_q3_K_64x1", 6, 64 * E, H, 1, 1),
+             ("shared_gate_q5_K_x8", 3, H, E, 8, 32), ("shared_down_q6_K_x8", 1, E, H, 8, 24))
+    for name, fmt, R, K, n, copies in cases:
+        ws = [kq_random(torch, fmt, R, K, seed + 31 * c + fmt) for c in range(copies)]
+        x = torch.empty((n, K), dtype=torch.float32, device="cuda")
+        ctx.synth_normal(x, seed, fmt, 0.0, 1.0)
+        q, d = ctx.quant_q8k(x)
+        y = torch.empty((n, R), dtype=torch.float32, device="cuda")
+        for i in range(3):
+            ctx.kq_matvec(fmt, ws[i % copies], R, K, q, d, y)
+        torch.cuda.synchronize()
+        reps = max(iters, copies)
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for i in range(reps):
+            ctx.kq_matvec(fmt, ws[i % copies], R, K, q, d, y)
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / reps
+        wb = R * (K // 256) * KQ[fmt][1]
+        out[name] = {"us_per_launch": round(us, 2), "weight_bytes": wb, "hbm_gbs": round(wb / us / 1e3, 1),
+                     "hbm_frac": round(wb / us / 1e3 / HBM_PEAK_GBS, 4)}
+        log("[bench] kquant %s: %s" % (name, json.dumps(out[name])))
+        del ws, x, q, d, y
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(ctx, torch, res, budget_s=12.0, max_steps=8):
     """The CPU checker (oracle/, restated ggml CPU semantics) on this host's cores, on a bounded sample of the same
     workload: the first steps' x with the experts they select, timed around the oracle call only."""
@@ -202,6 +252,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the decode-1 / prefill-512 / prefill-2048 side measurements")
     ap.add_argument("--no-stack", action="store_true", help="skip the 58-layer resident stack (configs[3], ~169 GB)")
     ap.add_argument("--stack-steps", type=int, default=10)
+    ap.add_argument("--only-kquant", action="store_true",
+                    help="run only the K-quant mat-vec leg (the reference's real-shard formats) and print its JSON")
     ap.add_argument("--fused", type=int, default=None, choices=(0, 1, 2),
                     help="decode path: 2 regular single launch (library default), 1 cooperative single launch, 0 per pass")
     ap.add_argument("--copy-probe", action="store_true",
@@ -217,6 +269,9 @@ def main():
     ctx = Context()
     if args.fused is not None:
         ctx.set_fused(args.fused)
+    if args.only_kquant:
+        print(json.dumps({"kquant": run_kquant(ctx, torch)}), flush=True)
+        return
     res = run_workload(ctx, torch, args.workload, args.steps, args.warmup, args.copies)
     n = res["n"]
     if res["fused"]:   # one launch = the whole block: its bytes are the step's
@@ -250,6 +305,9 @@ def main():
                          "stage_us": None if r["fused"] else {k: round(v * 1e3, 2) for k, v in r["stage_ms"].items()}}
             log("[bench] %s: %s" % (wl, json.dumps(extra[wl])))
             del r
+    if not args.no_extra:
+        torch.cuda.empty_cache()
+        extra["kquant"] = run_kquant(ctx, torch)
     if not args.no_stack:
         torch.cuda.empty_cache()
         extra["stack58"] = run_stack(ctx, torch, args.stack_steps, 2)

@@ -223,11 +223,12 @@ class Context:
         self.check(lib().fl_quant_q8k_dev(self.ctx, _ptr(x), n, K, _ptr(q), _ptr(d)))
         return q, d
 
-    def kq_matvec(self, fmt, w, R, K, q, d):
+    def kq_matvec(self, fmt, w, R, K, q, d, y=None):
         """y [n][R] = K-quant matrix w (uint8 device tensor, R x K/256 ggml blocks) . Q8_K rows (q [n][K], d [n][K/256])."""
         t = self.torch
         n = q.shape[0]
-        y = t.empty((n, R), dtype=t.float32, device=q.device)
+        if y is None:
+            y = t.empty((n, R), dtype=t.float32, device=q.device)
         self.check(lib().fl_kq_matvec_dev(self.ctx, fmt, _ptr(w), R, K, _ptr(q), _ptr(d), n, _ptr(y)))
         return y
 

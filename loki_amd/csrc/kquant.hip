@@ -12,11 +12,14 @@
 //   Q5_K:        acc_s += (d * d8) * isum, acc_m -= (dmin * d8) * summ, result acc_m + acc_s    these differ from
 //                ggml's by fp32 rounding of the partial sums only)
 //
-// Work: a wave streams rows of one matrix; lane l owns the 32-weight chunks l, l + 64, .. of the row (chunk i = block
-// i / 8, weights 32 (i % 8) .. +31), so the activation chunks stay in registers for every row of the wave's tile. A
-// workgroup (4 waves) covers 4 * RW rows of one expert for all of that expert's slots (token groups of TT).
+// Work: a workgroup (4 waves) takes one expert, a tile of rows and that expert's slots in token groups of up to 8 (their
+// Q8_K columns held in registers). Lane = (block, column slice of 32 weights); a row's blocks are split over 1-4 waves (8 blocks per
+// wave), the remaining waves take other rows of the tile. The next row's bytes are loaded while the current one is
+// computed. Each block's fp32 term goes to LDS; one lane per (row, token) then adds them in block order.
 #include "moe_common.h"
 #include "moe_kernels.h"
+
+#include <algorithm>
 
 namespace lk {
 
@@ -25,215 +28,300 @@ namespace {
 enum { KF_Q6K = 1, KF_Q5K = 3, KF_Q2K = 5, KF_Q3K = 6 };
 template <int F> constexpr int kbytes() { return F == KF_Q2K ? 84 : F == KF_Q3K ? 110 : F == KF_Q5K ? 176 : 210; }
 
-constexpr int RW = 16;          // rows per wave
 constexpr int KQ_WAVES = 4;     // waves per workgroup
 
-__device__ __forceinline__ uint32_t ld_u16(const uint8_t * p) { return *reinterpret_cast<const uint16_t *>(p); }
+// loads through the global address space (the pointers arrive inside a struct argument, where the compiler would
+// otherwise emit flat loads)
+typedef __attribute__((address_space(1))) const uint32_t g_u32;
+typedef __attribute__((address_space(1))) const uint16_t g_u16;
+__device__ __forceinline__ uint32_t ld32(const void * p) { return *(g_u32 *) p; }
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t * p) { return *(g_u16 *) p; }
 
-// N words from a 2-byte aligned address: aligned word loads, realigned with v_alignbyte. Only words that hold a needed
-// byte are read, so a buffer whose start and size are multiples of 4 bytes is never overrun.
-template <int N> __device__ __forceinline__ void ld_words_a2(const uint8_t * p, uint32_t (&w)[N]) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t * q = reinterpret_cast<const uint32_t *>(a & ~uintptr_t(3));
-    const uint32_t sh = (uint32_t) (a & 3u);
-    uint32_t t[N + 1];
-#pragma unroll
-    for (int i = 0; i < N; ++i) { t[i] = q[i]; }
-    t[N] = sh ? q[N] : 0u;
-#pragma unroll
-    for (int i = 0; i < N; ++i) { w[i] = __builtin_amdgcn_alignbyte(t[i + 1], t[i], sh); }
-}
-template <int N> __device__ __forceinline__ void ld_words_a4(const uint8_t * p, uint32_t (&w)[N]) {
-    const uint32_t * q = reinterpret_cast<const uint32_t *>(p);
-#pragma unroll
-    for (int i = 0; i < N; ++i) { w[i] = q[i]; }
-}
 __device__ __forceinline__ uint32_t byte_of3(uint32_t w0, uint32_t w1, uint32_t w2, int k) {
     const uint32_t w = k < 4 ? w0 : k < 8 ? w1 : w2;
     return (w >> (8 * (k & 3))) & 0xFFu;
 }
 
-// one 32-weight chunk of a block, decoded: u = unsigned quants (4 per word, weight order), per 16-weight half the scale
-// sA/sB, the offset to remove (off * bsum), and min mA/mB (Q2_K: per half; Q5_K: one per chunk in mA, mB = mA)
-struct Chunk {
-    uint32_t u[8];
-    int sA, sB, mA, mB;
-    float d, dmin;
-};
+// Lane slice q (0..7) of a block. 16-weight sub-block formats (Q2_K, Q3_K, Q6_K): n = q / 4 picks the block half,
+// jq = q % 4 the 8 columns l = 8 jq .. 8 jq + 7, taken in all four 32-weight rows s of the half: piece s = weights
+// 128 n + 32 s + l (one sub-block, 2 words). Q5_K (32-weight sub-blocks): columns l = 4 q .. 4 q + 3 of all 8
+// sub-blocks: piece j = weights 32 j + l (1 word). So each lane reads only the bytes of its own columns.
+template <int F> struct Raw;
+template <> struct Raw<KF_Q2K> { uint32_t q[2], sc[2], dd; };
+template <> struct Raw<KF_Q3K> { uint32_t q[3], h[3], s[4], dd; uint32_t shq, shh, shs; };
+template <> struct Raw<KF_Q5K> { uint32_t q[4], h, s[3], dd; };
+template <> struct Raw<KF_Q6K> { uint32_t qa[3], qb[3], h[3], sc[3], dd; uint32_t sha, shb, shh, shs; };
 
-template <int F> __device__ __forceinline__ void load_chunk(const uint8_t * blk, int c, Chunk & k) {
-    if constexpr (F == KF_Q2K) {   // scales[16] qs[64] d dmin: weight 128n + 32s + l = bits 2s of qs[32n + l]
-        const int n = c >> 2, s = c & 3;
-        uint32_t w[8]; ld_words_a4<8>(blk + 16 + 32 * n, w);
+// N + 1 aligned words covering N words at a 2-byte aligned address. Word N is needed only when the address is not
+// 4-aligned; otherwise word N - 1 is read again in its place, so no word past the last needed byte is touched.
+template <int N> __device__ __forceinline__ uint32_t ld_aligned(const uint8_t * p, uint32_t (&t)[N + 1]) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint8_t * q = reinterpret_cast<const uint8_t *>(a & ~uintptr_t(3));
+    const uint32_t sh = (uint32_t) (a & 3u);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) { k.u[i] = (w[i] >> (2 * s)) & 0x03030303u; }
-        const uint32_t sc = ld_u16(blk + 2 * c);
-        k.sA = (int) (sc & 15u); k.mA = (int) ((sc >> 4) & 15u); k.sB = (int) ((sc >> 8) & 15u); k.mB = (int) ((sc >> 12) & 15u);
-        const uint32_t dd = *reinterpret_cast<const uint32_t *>(blk + 80);
-        k.d = h2f((uint16_t) (dd & 0xFFFFu)); k.dmin = h2f((uint16_t) (dd >> 16));
-    } else if constexpr (F == KF_Q3K) {   // hmask[32] qs[64] scales[12] d: high bit clear -> quant - 4
-        const int n = c >> 2, s = c & 3;
-        uint32_t q[8], h[8]; ld_words_a2<8>(blk + 32 + 32 * n, q); ld_words_a2<8>(blk, h);
-        const int hb = 4 * n + s;
+    for (int i = 0; i < N; ++i) { t[i] = ld32(q + 4 * i); }
+    t[N] = ld32(q + 4 * (sh ? N : N - 1));
+    return sh;
+}
+template <int N> __device__ __forceinline__ uint32_t realign(const uint32_t (&t)[N + 1], uint32_t sh, int i) {
+    return __builtin_amdgcn_alignbyte(t[i + 1], t[i], sh);
+}
+
+template <int F> __device__ __forceinline__ void load_raw(const uint8_t * blk, int q, Raw<F> & r) {
+    const int n = q >> 2, jq = q & 3;
+    if constexpr (F == KF_Q2K) {   // scales[16] qs[64] d dmin
+        const uint8_t * qs = blk + 16 + 32 * n + 8 * jq, * sc = blk + 8 * n;
+        r.q[0] = ld32(qs); r.q[1] = ld32(qs + 4); r.sc[0] = ld32(sc); r.sc[1] = ld32(sc + 4);
+        r.dd = ld32(blk + 80);
+    } else if constexpr (F == KF_Q3K) {   // hmask[32] qs[64] scales[12] d
+        r.shq = ld_aligned<2>(blk + 32 + 32 * n + 8 * jq, r.q); r.shh = ld_aligned<2>(blk + 8 * jq, r.h);
+        r.shs = ld_aligned<3>(blk + 96, r.s); r.dd = ld_u16(blk + 108);
+    } else if constexpr (F == KF_Q5K) {   // d dmin scales[12] qh[32] qs[128]
 #pragma unroll
-        for (int i = 0; i < 8; ++i) { k.u[i] = ((q[i] >> (2 * s)) & 0x03030303u) | (((h[i] >> hb) & 0x01010101u) << 2); }
-        uint32_t a[3]; ld_words_a2<3>(blk + 96, a);
-        // 6-bit scales j = 2c, 2c + 1: low nibbles from bytes (j % 8) (j < 8: low, else high nibble), 2 high bits from
-        // byte 8 + j % 4 at bits 2 (j / 4)
-        const int kk = c >> 1;
-        const uint32_t lo = ((kk & 1 ? a[1] : a[0]) >> (kk & 2 ? 4 : 0)) & 0x0F0F0F0Fu;
-        const uint32_t hi = ((a[2] >> (2 * kk)) & 0x03030303u) << 4;
-        const uint32_t sw = (lo | hi) >> (16 * (c & 1));
-        k.sA = (int) (sw & 0xFFu) - 32; k.sB = (int) ((sw >> 8) & 0xFFu) - 32; k.mA = 0; k.mB = 0;
-        k.d = h2f((uint16_t) ld_u16(blk + 108)); k.dmin = 0.f;
-    } else if constexpr (F == KF_Q5K) {   // d dmin scales[12] qh[32] qs[128]: weight 64 (c/2) + 32 (c%2) + l
-        uint32_t l4[8], qh[8]; ld_words_a4<8>(blk + 48 + 32 * (c >> 1), l4); ld_words_a4<8>(blk + 16, qh);
-        const int sh = 4 * (c & 1);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) { k.u[i] = ((l4[i] >> sh) & 0x0F0F0F0Fu) | (((qh[i] >> c) & 0x01010101u) << 4); }
-        uint32_t a[3]; ld_words_a4<3>(blk + 4, a);
-        int s, m;
-        if (c < 4) { s = (int) (byte_of3(a[0], a[1], a[2], c) & 63u); m = (int) (byte_of3(a[0], a[1], a[2], c + 4) & 63u); }
-        else {
-            const uint32_t b8 = byte_of3(a[0], a[1], a[2], c + 4);
-            s = (int) ((b8 & 0xFu) | ((byte_of3(a[0], a[1], a[2], c - 4) >> 6) << 4));
-            m = (int) ((b8 >> 4) | ((byte_of3(a[0], a[1], a[2], c) >> 6) << 4));
-        }
-        k.sA = s; k.sB = s; k.mA = m; k.mB = m;
-        const uint32_t dd = *reinterpret_cast<const uint32_t *>(blk);
-        k.d = h2f((uint16_t) (dd & 0xFFFFu)); k.dmin = h2f((uint16_t) (dd >> 16));
-    } else {   // Q6_K: ql[128] qh[64] scales[16] d; weight 128n + 32p + l: nibble p/2 of ql[64n + 32 (p%2) + l], bits 2p of qh[32n + l], - 32
-        const int n = c >> 2, p = c & 3;
-        uint32_t l4[8], qh[8]; ld_words_a2<8>(blk + 64 * n + 32 * (p & 1), l4); ld_words_a2<8>(blk + 128 + 32 * n, qh);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) { k.u[i] = ((l4[i] >> (4 * (p >> 1))) & 0x0F0F0F0Fu) | (((qh[i] >> (2 * p)) & 0x03030303u) << 4); }
-        const uint32_t sc = ld_u16(blk + 192 + 2 * c);
-        k.sA = (int) (int8_t) (sc & 0xFFu); k.sB = (int) (int8_t) (sc >> 8); k.mA = 0; k.mB = 0;
-        k.d = h2f((uint16_t) ld_u16(blk + 208)); k.dmin = 0.f;
+        for (int j = 0; j < 4; ++j) { r.q[j] = ld32(blk + 48 + 32 * j + 4 * q); }
+        r.h = ld32(blk + 16 + 4 * q);
+        r.s[0] = ld32(blk + 4); r.s[1] = ld32(blk + 8); r.s[2] = ld32(blk + 12); r.dd = ld32(blk);
+    } else {   // Q6_K: ql[128] qh[64] scales[16] d
+        r.sha = ld_aligned<2>(blk + 64 * n + 8 * jq, r.qa); r.shb = ld_aligned<2>(blk + 64 * n + 32 + 8 * jq, r.qb);
+        r.shh = ld_aligned<2>(blk + 128 + 32 * n + 8 * jq, r.h); r.shs = ld_aligned<2>(blk + 192 + 8 * n, r.sc);
+        r.dd = ld_u16(blk + 208);
     }
 }
 
-struct XChunk { uint32_t x[8]; int bA, bB; float d8; };
+// decoded slice: u = unsigned quants (4 per word); piece p's scale sc[p] and min mn[p] (pieces: 4 of 2 words for the
+// 16-weight formats, 8 of 1 word for Q5_K)
+struct Chunk {
+    uint32_t u[8];
+    int sc[8], mn[8];
+    float d, dmin;
+};
 
-__device__ __forceinline__ int dot8(const uint32_t * u, const uint32_t * x) {
-    int s = 0;
+template <int F> __device__ __forceinline__ void decode(const Raw<F> & r, int q, Chunk & k) {
+    const int n = q >> 2, jq = q & 3, hi16 = jq >> 1;   // hi16: the columns sit in the second 16 of each 32-weight row
+    if constexpr (F == KF_Q2K) {   // weight 128 n + 32 s + l = bits 2s of qs[32 n + l]; sub-block 8 n + 2 s + hi16
 #pragma unroll
-    for (int i = 0; i < 4; ++i) { s = __builtin_amdgcn_sdot4((int) u[i], (int) x[i], s, false); }
-    return s;
+        for (int s = 0; s < 4; ++s) {
+            k.u[2 * s] = (r.q[0] >> (2 * s)) & 0x03030303u; k.u[2 * s + 1] = (r.q[1] >> (2 * s)) & 0x03030303u;
+            const uint32_t b = (r.sc[s >> 1] >> (8 * (2 * (s & 1) + hi16))) & 0xFFu;
+            k.sc[s] = (int) (b & 15u); k.mn[s] = (int) (b >> 4);
+        }
+        k.d = h2f((uint16_t) (r.dd & 0xFFFFu)); k.dmin = h2f((uint16_t) (r.dd >> 16));
+    } else if constexpr (F == KF_Q3K) {   // high bit (hmask[l] bit 4 n + s) clear -> quant - 4 (applied as -4 * bsum)
+        const uint32_t q0 = realign<2>(r.q, r.shq, 0), q1 = realign<2>(r.q, r.shq, 1);
+        const uint32_t h0 = realign<2>(r.h, r.shh, 0), h1 = realign<2>(r.h, r.shh, 1);
+        const uint32_t a0 = realign<3>(r.s, r.shs, 0), a1 = realign<3>(r.s, r.shs, 1), a2 = realign<3>(r.s, r.shs, 2);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int hb = 4 * n + s;
+            k.u[2 * s] = ((q0 >> (2 * s)) & 0x03030303u) | (((h0 >> hb) & 0x01010101u) << 2);
+            k.u[2 * s + 1] = ((q1 >> (2 * s)) & 0x03030303u) | (((h1 >> hb) & 0x01010101u) << 2);
+            // 6-bit scale j = 8 n + 2 s + hi16: low nibble of byte j % 8 (j < 8) or its high nibble (j >= 8), 2 high
+            // bits from byte 8 + j % 4 at bits 2 (j / 4)
+            const int j = 8 * n + 2 * s + hi16;
+            const uint32_t lo = ((((j & 4) ? a1 : a0) >> (8 * (j & 3))) >> ((j & 8) ? 4 : 0)) & 0xFu;
+            const uint32_t hh = (a2 >> (8 * (j & 3) + 2 * (j >> 2))) & 3u;
+            k.sc[s] = (int) (lo | (hh << 4)) - 32; k.mn[s] = 0;
+        }
+        k.d = h2f((uint16_t) r.dd); k.dmin = 0.f;
+    } else if constexpr (F == KF_Q5K) {   // weight 64 jj + 32 h + l: nibble h of qs[32 jj + l], bit 2 jj + h of qh[l]
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int j = 2 * jj + h;
+                k.u[j] = ((r.q[jj] >> (4 * h)) & 0x0F0F0F0Fu) | (((r.h >> j) & 0x01010101u) << 4);
+                int sv, mv;
+                if (j < 4) { sv = (int) (byte_of3(r.s[0], r.s[1], r.s[2], j) & 63u); mv = (int) (byte_of3(r.s[0], r.s[1], r.s[2], j + 4) & 63u); }
+                else {
+                    const uint32_t b8 = byte_of3(r.s[0], r.s[1], r.s[2], j + 4);
+                    sv = (int) ((b8 & 0xFu) | ((byte_of3(r.s[0], r.s[1], r.s[2], j - 4) >> 6) << 4));
+                    mv = (int) ((b8 >> 4) | ((byte_of3(r.s[0], r.s[1], r.s[2], j) >> 6) << 4));
+                }
+                k.sc[j] = sv; k.mn[j] = mv;
+            }
+        }
+        k.d = h2f((uint16_t) (r.dd & 0xFFFFu)); k.dmin = h2f((uint16_t) (r.dd >> 16));
+    } else {   // Q6_K: weight 128 n + 32 p + l: nibble p / 2 of ql[64 n + 32 (p % 2) + l], bits 2 p of qh[32 n + l], - 32
+        const uint32_t a0 = realign<2>(r.qa, r.sha, 0), a1 = realign<2>(r.qa, r.sha, 1);
+        const uint32_t b0 = realign<2>(r.qb, r.shb, 0), b1 = realign<2>(r.qb, r.shb, 1);
+        const uint32_t h0 = realign<2>(r.h, r.shh, 0), h1 = realign<2>(r.h, r.shh, 1);
+        const uint32_t s0 = realign<2>(r.sc, r.shs, 0), s1 = realign<2>(r.sc, r.shs, 1);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t l0 = (p & 1) ? b0 : a0, l1 = (p & 1) ? b1 : a1;
+            k.u[2 * p] = ((l0 >> (4 * (p >> 1))) & 0x0F0F0F0Fu) | (((h0 >> (2 * p)) & 0x03030303u) << 4);
+            k.u[2 * p + 1] = ((l1 >> (4 * (p >> 1))) & 0x0F0F0F0Fu) | (((h1 >> (2 * p)) & 0x03030303u) << 4);
+            const int j = 2 * p + hi16;   // scales[8 n + j]
+            k.sc[p] = (int) (int8_t) (((j < 4 ? s0 : s1) >> (8 * (j & 3))) & 0xFFu); k.mn[p] = 0;
+        }
+        k.d = h2f((uint16_t) r.dd); k.dmin = 0.f;
+    }
 }
 
-// integer partials of one chunk against one token: isum (scaled, offsets removed), summ (min term)
+// the lane's activation words (same weight order as u) and per-piece sums of the Q8_K integers
+struct XChunk { uint32_t x[8]; int bx[8]; float d8; };
+
+template <int F> __device__ __forceinline__ void load_x(const int8_t * xb, int q, XChunk & x) {
+    const uint32_t ones = 0x01010101u;
+    if constexpr (F == KF_Q5K) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            x.x[j] = *reinterpret_cast<const uint32_t *>(xb + 32 * j + 4 * q);
+            x.bx[j] = __builtin_amdgcn_sdot4((int) x.x[j], (int) ones, 0, false);
+        }
+    } else {
+        const int n = q >> 2, jq = q & 3;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const uint2 v = *reinterpret_cast<const uint2 *>(xb + 128 * n + 32 * s + 8 * jq);
+            x.x[2 * s] = v.x; x.x[2 * s + 1] = v.y;
+            x.bx[s] = __builtin_amdgcn_sdot4((int) v.y, (int) ones, __builtin_amdgcn_sdot4((int) v.x, (int) ones, 0, false), false);
+            x.bx[4 + s] = 0;
+        }
+    }
+}
+
+// integer partials of the slice against one token: isum (scaled, offsets removed), summ (min term)
 template <int F> __device__ __forceinline__ void chunk_dot(const Chunk & k, const XChunk & x, int & isum, int & summ) {
-    const int dA = dot8(k.u, x.x), dB = dot8(k.u + 4, x.x + 4);
-    if constexpr (F == KF_Q2K) { isum = k.sA * dA + k.sB * dB; summ = k.mA * x.bA + k.mB * x.bB; }
-    else if constexpr (F == KF_Q3K) { isum = k.sA * (dA - 4 * x.bA) + k.sB * (dB - 4 * x.bB); summ = 0; }
-    else if constexpr (F == KF_Q5K) { isum = k.sA * (dA + dB); summ = k.mA * (x.bA + x.bB); }
-    else { isum = k.sA * (dA - 32 * x.bA) + k.sB * (dB - 32 * x.bB); summ = 0; }
+    isum = 0; summ = 0;
+    if constexpr (F == KF_Q5K) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            isum += k.sc[j] * __builtin_amdgcn_sdot4((int) k.u[j], (int) x.x[j], 0, false);
+            summ += k.mn[j] * x.bx[j];
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int dp = __builtin_amdgcn_sdot4((int) k.u[2 * s + 1], (int) x.x[2 * s + 1],
+                                                  __builtin_amdgcn_sdot4((int) k.u[2 * s], (int) x.x[2 * s], 0, false), false);
+            if constexpr (F == KF_Q2K) { isum += k.sc[s] * dp; summ += k.mn[s] * x.bx[s]; }
+            else if constexpr (F == KF_Q3K) { isum += k.sc[s] * (dp - 4 * x.bx[s]); }
+            else { isum += k.sc[s] * (dp - 32 * x.bx[s]); }
+        }
+    }
 }
 
-__device__ __forceinline__ int red8(int v) {   // sum over the 8 lanes of an aligned group
-    v += __shfl_xor(v, 1); v += __shfl_xor(v, 2); v += __shfl_xor(v, 4);
+// sum over the 8 lanes of an aligned group, valid in the group's first lane: quad sums (DPP quad_perm), then lane i
+// adds lane i + 4 (DPP row_shl:4)
+__device__ __forceinline__ int red8(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);    // quad_perm [1,0,3,2]
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);    // quad_perm [2,3,0,1]
+    v += __builtin_amdgcn_update_dpp(0, v, 0x104, 0xF, 0xF, false);   // row_shl:4
     return v;
 }
 
-template <int F, int NJ, int TT>
+constexpr int RT_MAX = 32;      // rows per workgroup tile
+constexpr int NB_MAX = 32;      // blocks per row (K <= 8192)
+
+// Workgroup: one expert, a tile of rt rows, token groups of TT. The row's blocks are split over wk waves (8 blocks
+// per wave, lane = (block, column slice)); the 4 / wk wave groups take the tile's rows in turn. Each block's fp32 term goes
+// to LDS; then one lane per (row, token) adds the terms in block order.
+template <int F, int TT>
 __global__ void __launch_bounds__(64 * KQ_WAVES) k_kq_matvec(KqArgs a) {
 #pragma clang fp contract(off)
     constexpr int BS = kbytes<F>();
+    constexpr bool MINS = F == KF_Q5K;
+    extern __shared__ float s_lds[];   // [rw][TT][nb] terms, then the min terms (Q5_K)
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     int e, s_beg, s_end;
     if (a.act) {
         if ((int) blockIdx.y >= *a.nact) { return; }
         e = a.act[blockIdx.y]; s_beg = a.offsets[e]; s_end = a.offsets[e + 1];
     } else { e = 0; s_beg = 0; s_end = a.n; }
-    const int r0 = ((int) blockIdx.x * KQ_WAVES + wv) * RW;
-    if (r0 >= a.R || s_beg >= s_end) { return; }
-    const int r1 = min(r0 + RW, a.R);
-    const int nb = a.K / QK, nchunk = nb * 8;
+    const int tr0 = (int) blockIdx.x * a.rw;
+    if (tr0 >= a.R || s_beg >= s_end) { return; }
+    const int nrow = min(a.rw, a.R - tr0);
+    const int nb = a.K / QK;
+    float * s_t = s_lds; float * s_m = s_lds + a.rw * TT * nb;
+    const int wk = (nb + 7) / 8, wr = KQ_WAVES / wk;          // waves along K, wave groups along rows
+    const int kw = wv % wk, rg = wv / wk;
+    const int b = 8 * kw + (lane >> 3), c = lane & 7;          // this lane's block and column slice
+    const bool active = rg < wr && b < nb;
     const size_t rowb = (size_t) nb * BS;
-    const uint8_t * W = a.w + (size_t) e * a.estride;
+    const uint8_t * W = a.w + (size_t) e * a.estride + (size_t) b * BS;
 
     for (int sg = s_beg; sg < s_end; sg += TT) {
         const int nt = min(TT, s_end - sg);
-        XChunk xc[TT][NJ];
+        XChunk xc[TT];
 #pragma unroll
         for (int t = 0; t < TT; ++t) {
+            XChunk & x = xc[t];
+            if (active && t < nt) {
+                load_x<F>(a.aq + (size_t) (sg + t) * a.K + 256 * b, c, x);
+                x.d8 = a.ad[(size_t) (sg + t) * nb + b];
+            } else {
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                const int ci = lane + 64 * j;
-                XChunk & x = xc[t][j];
-                if (t < nt && ci < nchunk) {
-                    const int8_t * xr = a.aq + (size_t) (sg + t) * a.K + 32 * ci;
-                    const uint4 v0 = *reinterpret_cast<const uint4 *>(xr), v1 = *reinterpret_cast<const uint4 *>(xr + 16);
-                    x.x[0] = v0.x; x.x[1] = v0.y; x.x[2] = v0.z; x.x[3] = v0.w; x.x[4] = v1.x; x.x[5] = v1.y; x.x[6] = v1.z; x.x[7] = v1.w;
-                    const uint32_t ones[4] = { 0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u };
-                    x.bA = dot8(x.x, ones); x.bB = dot8(x.x + 4, ones);
-                    x.d8 = a.ad[(size_t) (sg + t) * nb + (ci >> 3)];
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) { x.x[i] = 0u; }
-                    x.bA = 0; x.bB = 0; x.d8 = 0.f;
-                }
+                for (int i = 0; i < 8; ++i) { x.x[i] = 0u; x.bx[i] = 0; }
+                x.d8 = 0.f;
             }
         }
-        for (int r = r0; r < r1; ++r) {
-            Chunk ck[NJ];
+        if (active) {
+            auto row = [&](const Raw<F> & raw, int ri) {
+                Chunk ck; decode<F>(raw, c, ck);
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                const int ci = lane + 64 * j;
-                if (ci < nchunk) { load_chunk<F>(W + (size_t) r * rowb + (size_t) (ci >> 3) * BS, ci & 7, ck[j]); }
-                else {
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) { ck[j].u[i] = 0u; }
-                    ck[j].sA = ck[j].sB = ck[j].mA = ck[j].mB = 0; ck[j].d = 0.f; ck[j].dmin = 0.f;
-                }
-            }
-#pragma unroll
-            for (int t = 0; t < TT; ++t) {
-                if (t >= nt) { continue; }
-                float term[NJ], termm[NJ];
-#pragma unroll
-                for (int j = 0; j < NJ; ++j) {
-                    int is, sm;
-                    chunk_dot<F>(ck[j], xc[t][j], is, sm);
-                    is = red8(is);
-                    if constexpr (F == KF_Q2K || F == KF_Q5K) { sm = red8(sm); }
-                    const float d8 = xc[t][j].d8;
-                    if constexpr (F == KF_Q2K) { term[j] = (d8 * ck[j].d) * (float) is - (d8 * ck[j].dmin) * (float) sm; termm[j] = 0.f; }
-                    else if constexpr (F == KF_Q5K) { term[j] = (ck[j].d * d8) * (float) is; termm[j] = (ck[j].dmin * d8) * (float) sm; }
-                    else { term[j] = (ck[j].d * d8) * (float) is; termm[j] = 0.f; }
-                }
-                // blocks in order: block b sits in lanes 8 (b % 8) .. of chunk slot b / 8
-                float acc = 0.f, accm = 0.f;
-#pragma unroll
-                for (int j = 0; j < NJ; ++j) {
-#pragma unroll
-                    for (int g = 0; g < 8; ++g) {
-                        if (8 * j + g < nb) {
-                            acc = acc + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, term[j]), 8 * g));
-                            if constexpr (F == KF_Q5K) {
-                                accm = accm - __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, termm[j]), 8 * g));
-                            }
+                for (int t = 0; t < TT; ++t) {
+                    if (t < nt) {
+                        int is, sm;
+                        chunk_dot<F>(ck, xc[t], is, sm);
+                        is = red8(is);
+                        if constexpr (F == KF_Q2K || F == KF_Q5K) { sm = red8(sm); }
+                        if (c == 0) {
+                            const float d8 = xc[t].d8;
+                            float term;
+                            if constexpr (F == KF_Q2K) { term = (d8 * ck.d) * (float) is - (d8 * ck.dmin) * (float) sm; }
+                            else { term = (ck.d * d8) * (float) is; }
+                            s_t[(ri * TT + t) * nb + b] = term;
+                            if constexpr (MINS) { s_m[(ri * TT + t) * nb + b] = (ck.dmin * d8) * (float) sm; }
                         }
                     }
                 }
-                if constexpr (F == KF_Q5K) { acc = accm + acc; }
-                if (lane == 0) { a.out[(size_t) (sg + t) * a.ldo + r] = acc; }
+            };
+            // two row buffers: the next row's bytes are in flight while the current row is computed
+            const size_t step = (size_t) wr * rowb;
+            const uint8_t * wp = W + (size_t) (tr0 + rg) * rowb;
+            Raw<F> ra, rb;
+            int ri = rg;
+            if (ri < nrow) { load_raw<F>(wp, c, ra); }
+            while (ri < nrow) {
+                if (ri + wr < nrow) { load_raw<F>(wp + step, c, rb); }
+                row(ra, ri);
+                ri += wr; wp += step;
+                if (ri >= nrow) { break; }
+                if (ri + wr < nrow) { load_raw<F>(wp + step, c, ra); }
+                row(rb, ri);
+                ri += wr; wp += step;
             }
         }
+        __syncthreads();
+        // blocks in order, one lane per (row, token)
+        for (int p = threadIdx.x; p < nrow * nt; p += 64 * KQ_WAVES) {
+            const int ri = p / nt, t = p % nt;
+            const float * tp = s_t + (ri * TT + t) * nb;
+            float acc = 0.f;
+            if constexpr (MINS) {
+                const float * mp = s_m + (ri * TT + t) * nb;
+                float accm = 0.f;
+                for (int j = 0; j < nb; ++j) { acc = acc + tp[j]; accm = accm - mp[j]; }
+                acc = accm + acc;
+            } else {
+                for (int j = 0; j < nb; ++j) { acc = acc + tp[j]; }
+            }
+            a.out[(size_t) (sg + t) * a.ldo + tr0 + ri] = acc;
+        }
+        __syncthreads();
     }
 }
 
-template <int F, int NJ, int TT> hipError_t go(const KqArgs & a, unsigned gy, hipStream_t st) {
-    const dim3 grid((unsigned) ((a.R + KQ_WAVES * RW - 1) / (KQ_WAVES * RW)), gy);
-    k_kq_matvec<F, NJ, TT><<<grid, 64 * KQ_WAVES, 0, st>>>(a);
+template <int F, int TT> hipError_t go(const KqArgs & a, unsigned gy, hipStream_t st) {
+    const dim3 grid((unsigned) ((a.R + a.rw - 1) / a.rw), gy);
+    const size_t lds = (size_t) a.rw * TT * (a.K / QK) * sizeof(float) * (F == KF_Q5K ? 2 : 1);
+    k_kq_matvec<F, TT><<<grid, 64 * KQ_WAVES, lds, st>>>(a);
     return hipGetLastError();
 }
 
-template <int F> hipError_t go_f(const KqArgs & a, int nj, int tt, unsigned gy, hipStream_t st) {
-    if (nj == 1) { return tt == 1 ? go<F, 1, 1>(a, gy, st) : tt == 2 ? go<F, 1, 2>(a, gy, st) : go<F, 1, 4>(a, gy, st); }
-    if (nj == 2) { return tt == 1 ? go<F, 2, 1>(a, gy, st) : go<F, 2, 2>(a, gy, st); }
-    return tt == 1 ? go<F, 4, 1>(a, gy, st) : go<F, 4, 2>(a, gy, st);
+template <int F> hipError_t go_f(const KqArgs & a, int tt, unsigned gy, hipStream_t st) {
+    return tt == 1 ? go<F, 1>(a, gy, st) : tt == 2 ? go<F, 2>(a, gy, st) : tt == 4 ? go<F, 4>(a, gy, st) : go<F, 8>(a, gy, st);
 }
 
 }  // namespace
@@ -242,16 +330,20 @@ int kq_block_bytes(int fmt) {
     switch (fmt) { case KF_Q2K: return 84; case KF_Q3K: return 110; case KF_Q5K: return 176; case KF_Q6K: return 210; default: return 0; }
 }
 
-hipError_t launch_kq_matvec(const KqArgs & a, int fmt, int max_slots, int grid_experts, hipStream_t st) {
-    if (a.K <= 0 || a.K % QK || a.K > 8192 || a.R <= 0 || max_slots <= 0 || grid_experts <= 0 || kq_block_bytes(fmt) == 0) { return hipErrorInvalidValue; }
-    const int nj = (a.K / QK * 8 + 63) / 64 <= 1 ? 1 : (a.K / QK * 8 + 63) / 64 <= 2 ? 2 : 4;
-    const int tt = nj == 1 ? (max_slots <= 1 ? 1 : max_slots <= 2 ? 2 : 4) : (max_slots <= 1 ? 1 : 2);
+hipError_t launch_kq_matvec(const KqArgs & args, int fmt, int max_slots, int grid_experts, hipStream_t st) {
+    KqArgs a = args;
+    if (a.K <= 0 || a.K % QK || a.K > QK * NB_MAX || a.R <= 0 || max_slots <= 0 || grid_experts <= 0 || kq_block_bytes(fmt) == 0) { return hipErrorInvalidValue; }
+    // rows per workgroup tile: RT_MAX when the launch has rows enough, else fewer so that it still spreads over
+    // ~1024 workgroups
+    const int64_t rows_total = (int64_t) a.R * (a.act ? grid_experts : 1);
+    a.rw = (int) std::max<int64_t>(1, std::min<int64_t>(RT_MAX, rows_total / 1024));
+    const int tt = max_slots <= 1 ? 1 : max_slots <= 2 ? 2 : max_slots <= 4 ? 4 : 8;
     const unsigned gy = a.act ? (unsigned) grid_experts : 1u;
     switch (fmt) {
-        case KF_Q2K: return go_f<KF_Q2K>(a, nj, tt, gy, st);
-        case KF_Q3K: return go_f<KF_Q3K>(a, nj, tt, gy, st);
-        case KF_Q5K: return go_f<KF_Q5K>(a, nj, tt, gy, st);
-        default: return go_f<KF_Q6K>(a, nj, tt, gy, st);
+        case KF_Q2K: return go_f<KF_Q2K>(a, tt, gy, st);
+        case KF_Q3K: return go_f<KF_Q3K>(a, tt, gy, st);
+        case KF_Q5K: return go_f<KF_Q5K>(a, tt, gy, st);
+        default: return go_f<KF_Q6K>(a, tt, gy, st);
     }
 }
 

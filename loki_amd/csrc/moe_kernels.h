@@ -119,6 +119,7 @@ struct KqArgs {
                                          // offsets[e] .. offsets[e+1]; act == null: one matrix, slots 0 .. n-1
     int n;
     float * out; int ldo;                // out[s * ldo + r]
+    int rw;                              // rows per workgroup tile (set by launch_kq_matvec)
 };
 // block bytes of a K-quant format code (FL_Q2K 84, FL_Q3K 110, FL_Q5K 176, FL_Q6K 210; 0 = not a K-quant)
 int kq_block_bytes(int fmt);
