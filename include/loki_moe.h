@@ -133,6 +133,54 @@ int fl_synth_normal(FLCtx *, float * dst, int64_t count, uint64_t seed, uint64_t
 /* which = 0: exp, 1: sigmoid, 2: silu under the library's exp contract (device arrays) */
 int fl_probe_exp(FLCtx *, const float * x, float * y, int64_t n, int which);
 
+/* ---------------------------------------------------------------- additive: the model's GGUF shards
+ * A tensor index over one or more GGUF files (ggml's container, versions 2 and 3): name -> file, absolute offset, ggml
+ * type, dims; a later file's tensor of the same name replaces an earlier one. It replaces the reference's index built
+ * with ggml's gguf API (src/server_core_fused.cpp:97-110); expert e of an expert tensor starts at offset + e *
+ * expert_stride, expert_stride = ggml_row_size(type, ne[0]) * ne[1] (eng:305). Host only: no GPU needed. */
+typedef struct FLGguf FLGguf;
+typedef struct FLGgufTensor {
+    int file;             /* index into the paths given to fl_gguf_open */
+    int type;             /* ggml type code (F32 0, F16 1, Q2_K 10, Q3_K 11, Q5_K 13, Q6_K 14, IQ2_XXS 16, ...) */
+    int fl_format;        /* the FL_* code of the type, -1 if this library has no kernel for it */
+    int n_dims;
+    int64_t ne[4];        /* ggml order: ne[0] = columns, ne[1] = rows, ne[2] = experts */
+    uint64_t offset;      /* absolute byte offset in its file */
+    uint64_t nbytes;      /* 0 for ggml types this index does not size */
+    uint64_t row_bytes;   /* ggml_row_size(type, ne[0]) */
+} FLGgufTensor;
+/* NULL on failure, with the reason in err (errlen bytes, may be NULL) */
+FLGguf * fl_gguf_open(const char * const * paths, int npaths, char * err, size_t errlen);
+void fl_gguf_close(FLGguf *);
+int fl_gguf_n_tensors(const FLGguf *);
+const char * fl_gguf_tensor_name(const FLGguf *, int i);
+/* FL_OK, FL_ERANGE when absent */
+int fl_gguf_tensor(const FLGguf *, const char * name, FLGgufTensor * out);
+int fl_gguf_tensor_at(const FLGguf *, int i, FLGgufTensor * out);
+/* metadata: integer (u8..i64, bool), float (f32, f64), string; FL_ERANGE when absent, FL_EINVAL on a type mismatch */
+int fl_gguf_get_int(const FLGguf *, const char * key, int64_t * out);
+int fl_gguf_get_float(const FLGguf *, const char * key, double * out);
+const char * fl_gguf_get_str(const FLGguf *, const char * key);
+/* bytes [off, off + bytes) of a tensor's data into host memory */
+int fl_gguf_read(const FLGguf *, const FLGgufTensor *, uint64_t off, uint64_t bytes, void * dst);
+
+/* One MoE layer of the index (blk.<layer>.ffn_gate_inp / exp_probs_b / ffn_norm / ffn_{gate,up,down}_exps /
+ * ffn_{gate,up,down}_shexp) made resident in HBM in one allocation. The router arrives F32 (ffn_gate_inp.weight, or
+ * ffn_gate_inp_f16.weight widened exactly). layout FL_LAYOUT_TILED packs every expert matrix for fl_moe_layer /
+ * fl_moe_layer_normed (all must be IQ2_XXS); FL_LAYOUT_GGML keeps the files' bytes, for fl_moe / fl_wide_moe (the layer
+ * as the arena, ids = expert ids, down_fmt = fmt_down) and fl_ffn_begin (FLW from L, fl_set_shared_formats with
+ * fmt_sh_*). Routed gate/up must be IQ2_XXS, down IQ2_XXS, Q2_K or Q3_K, the shared expert IQ2_XXS or K-quants
+ * (FL_ESCOPE otherwise). */
+typedef struct FLGgufLayer {
+    FLMoeLayer L;
+    const float * ffn_norm;                 /* [E] F32, device; NULL when the layer has no ffn_norm */
+    int fmt_down, fmt_sh_gate, fmt_sh_up, fmt_sh_down;   /* FL_* codes of the files' types */
+    uint64_t expert_stride[3];              /* gate, up, down bytes per expert */
+    void * mem; size_t bytes;               /* the allocation (fl_gguf_free_layer) */
+} FLGgufLayer;
+int fl_gguf_load_moe_layer(FLCtx *, const FLGguf *, int layer, int layout, FLGgufLayer * out);
+void fl_gguf_free_layer(FLGgufLayer *);
+
 /* internal buffers of the last fl_moe_layer (device pointers, valid until the next call that resizes them) */
 typedef struct FLDebug {
     const int8_t * xq; const float * xd;             /* Q8_K of x */

@@ -32,6 +32,75 @@ class FLMoeLayer(ctypes.Structure):
                 ("E", ctypes.c_int), ("H", ctypes.c_int)]
 
 
+class FLGgufTensor(ctypes.Structure):
+    _fields_ = [("file", ctypes.c_int), ("type", ctypes.c_int), ("fl_format", ctypes.c_int), ("n_dims", ctypes.c_int),
+                ("ne", ctypes.c_int64 * 4), ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64), ("row_bytes", ctypes.c_uint64)]
+
+
+class FLGgufLayer(ctypes.Structure):
+    _fields_ = [("L", FLMoeLayer), ("ffn_norm", P_), ("fmt_down", ctypes.c_int), ("fmt_sh_gate", ctypes.c_int),
+                ("fmt_sh_up", ctypes.c_int), ("fmt_sh_down", ctypes.c_int), ("expert_stride", ctypes.c_uint64 * 3),
+                ("mem", P_), ("bytes", ctypes.c_size_t)]
+
+
+class Gguf:
+    """Tensor index over GGUF shard files (libloki_moe's native reader; host only)."""
+
+    def __init__(self, paths):
+        if isinstance(paths, (str, bytes, os.PathLike)):
+            paths = [paths]
+        arr = (ctypes.c_char_p * len(paths))(*[os.fsencode(p) for p in paths])
+        err = ctypes.create_string_buffer(512)
+        self.h = lib().fl_gguf_open(arr, len(paths), err, 512)
+        if not self.h:
+            raise LokiError("fl_gguf_open: " + err.value.decode(errors="replace"))
+
+    def close(self):
+        if self.h:
+            lib().fl_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def names(self):
+        return [lib().fl_gguf_tensor_name(self.h, i).decode() for i in range(lib().fl_gguf_n_tensors(self.h))]
+
+    def tensor(self, name):
+        t = FLGgufTensor()
+        rc = lib().fl_gguf_tensor(self.h, name.encode(), ctypes.byref(t))
+        if rc != FL_OK:
+            raise KeyError(name)
+        return t
+
+    def get_int(self, key):
+        v = ctypes.c_int64()
+        rc = lib().fl_gguf_get_int(self.h, key.encode(), ctypes.byref(v))
+        return v.value if rc == FL_OK else None
+
+    def get_float(self, key):
+        v = ctypes.c_double()
+        rc = lib().fl_gguf_get_float(self.h, key.encode(), ctypes.byref(v))
+        return v.value if rc == FL_OK else None
+
+    def get_str(self, key):
+        v = lib().fl_gguf_get_str(self.h, key.encode())
+        return None if v is None else v.decode()
+
+    def read(self, name, off=0, nbytes=None):
+        import numpy as np
+        t = self.tensor(name)
+        n = t.nbytes - off if nbytes is None else nbytes
+        out = np.empty(n, np.uint8)
+        rc = lib().fl_gguf_read(self.h, ctypes.byref(t), off, n, out.ctypes.data_as(ctypes.c_void_p))
+        if rc != FL_OK:
+            raise LokiError("fl_gguf_read(%s) = %d" % (name, rc))
+        return out
+
+
 class FLDebug(ctypes.Structure):
     _fields_ = [(n, P_) for n in ("xq", "xd", "logits", "probs", "sel", "wts", "counts", "offsets", "perm", "inv",
                                   "act", "nact", "h", "hq", "hd", "o", "g", "u")] + \
@@ -55,7 +124,9 @@ class FLOut(ctypes.Structure):
 ABI_SYMBOLS = [
     "fl_init", "fl_attn", "fl_wide_init", "fl_wide_moe", "fl_wide_mark", "fl_wide_wait", "fl_wide_finish", "fl_moe_outs",
     "fl_wide_outs", "fl_wide_skip", "fl_spec", "fl_sketch", "fl_fetch", "fl_moe", "fl_skip", "fl_h2d", "fl_wait_event",
-    "fl_gpu_ms", "fl_ffn_begin", "fl_set_experts", "fl_set_routing", "fl_set_shared_formats", "fl_kq_matvec_dev", "fl_moe_layer", "fl_moe_layer_normed", "fl_route_dev", "fl_dispatch_dev", "fl_quant_q8k_dev",
+    "fl_gpu_ms", "fl_ffn_begin", "fl_set_experts", "fl_set_routing", "fl_set_shared_formats", "fl_kq_matvec_dev",
+    "fl_gguf_open", "fl_gguf_close", "fl_gguf_n_tensors", "fl_gguf_tensor_name", "fl_gguf_tensor", "fl_gguf_tensor_at",
+    "fl_gguf_get_int", "fl_gguf_get_float", "fl_gguf_get_str", "fl_gguf_read", "fl_gguf_load_moe_layer", "fl_gguf_free_layer", "fl_moe_layer", "fl_moe_layer_normed", "fl_route_dev", "fl_dispatch_dev", "fl_quant_q8k_dev",
     "fl_pack_iq2xxs", "fl_unpack_iq2xxs", "fl_rmsnorm_dev", "fl_synth_iq2xxs", "fl_synth_normal", "fl_probe_exp",
     "fl_debug", "fl_set_debug", "fl_set_fused", "fl_set_prefill_mfma", "fl_stream", "fl_set_stream", "fl_d2h", "fl_set_profile", "fl_stage_ms", "fl_sync", "fl_last_error", "fl_free",
 ]
@@ -87,6 +158,18 @@ def lib():
             "fl_set_experts": (I, [P_, I]),
             "fl_set_shared_formats": (I, [P_, I, I, I]),
             "fl_kq_matvec_dev": (I, [P_, I, P_, I, I, P_, P_, I, P_]),
+            "fl_gguf_open": (P_, [ctypes.POINTER(ctypes.c_char_p), I, ctypes.c_char_p, S]),
+            "fl_gguf_close": (None, [P_]),
+            "fl_gguf_n_tensors": (I, [P_]),
+            "fl_gguf_tensor_name": (ctypes.c_char_p, [P_, I]),
+            "fl_gguf_tensor": (I, [P_, ctypes.c_char_p, ctypes.POINTER(FLGgufTensor)]),
+            "fl_gguf_tensor_at": (I, [P_, I, ctypes.POINTER(FLGgufTensor)]),
+            "fl_gguf_get_int": (I, [P_, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)]),
+            "fl_gguf_get_float": (I, [P_, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]),
+            "fl_gguf_get_str": (ctypes.c_char_p, [P_, ctypes.c_char_p]),
+            "fl_gguf_read": (I, [P_, ctypes.POINTER(FLGgufTensor), U64, U64, P_]),
+            "fl_gguf_load_moe_layer": (I, [P_, P_, I, I, ctypes.POINTER(FLGgufLayer)]),
+            "fl_gguf_free_layer": (None, [ctypes.POINTER(FLGgufLayer)]),
             "fl_set_debug": (I, [P_, I]),
             "fl_set_fused": (I, [P_, I]),
             "fl_set_prefill_mfma": (I, [P_, I]),
@@ -222,6 +305,16 @@ class Context:
         d = t.empty((n, K // QK_K), dtype=t.float32, device=x.device)
         self.check(lib().fl_quant_q8k_dev(self.ctx, _ptr(x), n, K, _ptr(q), _ptr(d)))
         return q, d
+
+    def load_gguf_layer(self, gguf, layer, layout=None):
+        """One MoE layer of a Gguf index, resident in HBM (FLGgufLayer; free with free_gguf_layer)."""
+        out = FLGgufLayer()
+        self.check(lib().fl_gguf_load_moe_layer(self.ctx, gguf.h, layer, FL_LAYOUT_TILED if layout is None else layout,
+                                                ctypes.byref(out)))
+        return out
+
+    def free_gguf_layer(self, gl):
+        lib().fl_gguf_free_layer(ctypes.byref(gl))
 
     def kq_matvec(self, fmt, w, R, K, q, d, y=None):
         """y [n][R] = K-quant matrix w (uint8 device tensor, R x K/256 ggml blocks) . Q8_K rows (q [n][K], d [n][K/256])."""
