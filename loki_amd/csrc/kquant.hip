@@ -30,12 +30,16 @@ template <int F> constexpr int kbytes() { return F == KF_Q2K ? 84 : F == KF_Q3K 
 
 constexpr int KQ_WAVES = 4;     // waves per workgroup
 
-// loads through the global address space (the pointers arrive inside a struct argument, where the compiler would
-// otherwise emit flat loads)
-typedef __attribute__((address_space(1))) const uint32_t g_u32;
-typedef __attribute__((address_space(1))) const uint16_t g_u16;
-__device__ __forceinline__ uint32_t ld32(const void * p) { return *(g_u32 *) p; }
-__device__ __forceinline__ uint32_t ld_u16(const uint8_t * p) { return *(g_u16 *) p; }
+// Weight loads are buffer loads: a scalar resource over the expert's matrix, the lane's block offset (fixed for the
+// whole launch) plus a field offset in one vector register, the row offset in a scalar register. Offsets past the
+// resource's size read 0 instead of memory.
+struct Src {
+    __amdgpu_buffer_rsrc_t rs;
+    uint32_t vb;      // this lane's block: b * block bytes
+    uint32_t so;      // the current row: row * row bytes (wave-uniform)
+};
+__device__ __forceinline__ uint32_t ld32(const Src & s, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(s.rs, s.vb + off, s.so, 0); }
+__device__ __forceinline__ uint32_t ld_u16(const Src & s, uint32_t off) { return (uint32_t) __builtin_amdgcn_raw_buffer_load_b16(s.rs, s.vb + off, s.so, 0); }
 
 __device__ __forceinline__ uint32_t byte_of3(uint32_t w0, uint32_t w1, uint32_t w2, int k) {
     const uint32_t w = k < 4 ? w0 : k < 8 ? w1 : w2;
@@ -52,39 +56,38 @@ template <> struct Raw<KF_Q3K> { uint32_t q[3], h[3], s[4], dd; uint32_t shq, sh
 template <> struct Raw<KF_Q5K> { uint32_t q[4], h, s[3], dd; };
 template <> struct Raw<KF_Q6K> { uint32_t qa[3], qb[3], h[3], sc[3], dd; uint32_t sha, shb, shh, shs; };
 
-// N + 1 aligned words covering N words at a 2-byte aligned address. Word N is needed only when the address is not
-// 4-aligned; otherwise word N - 1 is read again in its place, so no word past the last needed byte is touched.
-template <int N> __device__ __forceinline__ uint32_t ld_aligned(const uint8_t * p, uint32_t (&t)[N + 1]) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint8_t * q = reinterpret_cast<const uint8_t *>(a & ~uintptr_t(3));
-    const uint32_t sh = (uint32_t) (a & 3u);
+// N + 1 aligned words covering N words at a 2-byte aligned offset (rows and the matrix start on 4-byte boundaries, so
+// the alignment is the lane's: block offset + field). Word N is needed only when the offset is not 4-aligned;
+// otherwise word N - 1 is read again in its place, so no word past the last needed byte is touched.
+template <int N> __device__ __forceinline__ uint32_t ld_aligned(const Src & s, uint32_t off, uint32_t (&t)[N + 1]) {
+    const uint32_t sh = (s.vb + off) & 3u, o = off - sh;
 #pragma unroll
-    for (int i = 0; i < N; ++i) { t[i] = ld32(q + 4 * i); }
-    t[N] = ld32(q + 4 * (sh ? N : N - 1));
+    for (int i = 0; i < N; ++i) { t[i] = ld32(s, o + 4 * i); }
+    t[N] = ld32(s, o + 4 * (sh ? N : N - 1));
     return sh;
 }
 template <int N> __device__ __forceinline__ uint32_t realign(const uint32_t (&t)[N + 1], uint32_t sh, int i) {
     return __builtin_amdgcn_alignbyte(t[i + 1], t[i], sh);
 }
 
-template <int F> __device__ __forceinline__ void load_raw(const uint8_t * blk, int q, Raw<F> & r) {
-    const int n = q >> 2, jq = q & 3;
+template <int F> __device__ __forceinline__ void load_raw(const Src & b, int q, Raw<F> & r) {
+    const uint32_t n = (uint32_t) q >> 2, jq = (uint32_t) q & 3u;
     if constexpr (F == KF_Q2K) {   // scales[16] qs[64] d dmin
-        const uint8_t * qs = blk + 16 + 32 * n + 8 * jq, * sc = blk + 8 * n;
-        r.q[0] = ld32(qs); r.q[1] = ld32(qs + 4); r.sc[0] = ld32(sc); r.sc[1] = ld32(sc + 4);
-        r.dd = ld32(blk + 80);
+        const uint32_t qs = 16 + 32 * n + 8 * jq, sc = 8 * n;
+        r.q[0] = ld32(b, qs); r.q[1] = ld32(b, qs + 4); r.sc[0] = ld32(b, sc); r.sc[1] = ld32(b, sc + 4);
+        r.dd = ld32(b, 80);
     } else if constexpr (F == KF_Q3K) {   // hmask[32] qs[64] scales[12] d
-        r.shq = ld_aligned<2>(blk + 32 + 32 * n + 8 * jq, r.q); r.shh = ld_aligned<2>(blk + 8 * jq, r.h);
-        r.shs = ld_aligned<3>(blk + 96, r.s); r.dd = ld_u16(blk + 108);
+        r.shq = ld_aligned<2>(b, 32 + 32 * n + 8 * jq, r.q); r.shh = ld_aligned<2>(b, 8 * jq, r.h);
+        r.shs = ld_aligned<3>(b, 96, r.s); r.dd = ld_u16(b, 108);
     } else if constexpr (F == KF_Q5K) {   // d dmin scales[12] qh[32] qs[128]
 #pragma unroll
-        for (int j = 0; j < 4; ++j) { r.q[j] = ld32(blk + 48 + 32 * j + 4 * q); }
-        r.h = ld32(blk + 16 + 4 * q);
-        r.s[0] = ld32(blk + 4); r.s[1] = ld32(blk + 8); r.s[2] = ld32(blk + 12); r.dd = ld32(blk);
+        for (uint32_t j = 0; j < 4; ++j) { r.q[j] = ld32(b, 48 + 32 * j + 4 * (uint32_t) q); }
+        r.h = ld32(b, 16 + 4 * (uint32_t) q);
+        r.s[0] = ld32(b, 4); r.s[1] = ld32(b, 8); r.s[2] = ld32(b, 12); r.dd = ld32(b, 0);
     } else {   // Q6_K: ql[128] qh[64] scales[16] d
-        r.sha = ld_aligned<2>(blk + 64 * n + 8 * jq, r.qa); r.shb = ld_aligned<2>(blk + 64 * n + 32 + 8 * jq, r.qb);
-        r.shh = ld_aligned<2>(blk + 128 + 32 * n + 8 * jq, r.h); r.shs = ld_aligned<2>(blk + 192 + 8 * n, r.sc);
-        r.dd = ld_u16(blk + 208);
+        r.sha = ld_aligned<2>(b, 64 * n + 8 * jq, r.qa); r.shb = ld_aligned<2>(b, 64 * n + 32 + 8 * jq, r.qb);
+        r.shh = ld_aligned<2>(b, 128 + 32 * n + 8 * jq, r.h); r.shs = ld_aligned<2>(b, 192 + 8 * n, r.sc);
+        r.dd = ld_u16(b, 208);
     }
 }
 
@@ -181,23 +184,24 @@ template <int F> __device__ __forceinline__ void load_x(const int8_t * xb, int q
     }
 }
 
-// integer partials of the slice against one token: isum (scaled, offsets removed), summ (min term)
+// integer partials of the slice against one token: isum (scaled, offsets removed), summ (min term). Every factor fits
+// 24 signed bits (scales and mins <= 8 bits, piece dots |.| < 2^17), so the products use the full-rate 24-bit multiply.
 template <int F> __device__ __forceinline__ void chunk_dot(const Chunk & k, const XChunk & x, int & isum, int & summ) {
     isum = 0; summ = 0;
     if constexpr (F == KF_Q5K) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            isum += k.sc[j] * __builtin_amdgcn_sdot4((int) k.u[j], (int) x.x[j], 0, false);
-            summ += k.mn[j] * x.bx[j];
+            isum += __mul24(k.sc[j], __builtin_amdgcn_sdot4((int) k.u[j], (int) x.x[j], 0, false));
+            summ += __mul24(k.mn[j], x.bx[j]);
         }
     } else {
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const int dp = __builtin_amdgcn_sdot4((int) k.u[2 * s + 1], (int) x.x[2 * s + 1],
                                                   __builtin_amdgcn_sdot4((int) k.u[2 * s], (int) x.x[2 * s], 0, false), false);
-            if constexpr (F == KF_Q2K) { isum += k.sc[s] * dp; summ += k.mn[s] * x.bx[s]; }
-            else if constexpr (F == KF_Q3K) { isum += k.sc[s] * (dp - 4 * x.bx[s]); }
-            else { isum += k.sc[s] * (dp - 32 * x.bx[s]); }
+            if constexpr (F == KF_Q2K) { isum += __mul24(k.sc[s], dp); summ += __mul24(k.mn[s], x.bx[s]); }
+            else if constexpr (F == KF_Q3K) { isum += __mul24(k.sc[s], dp - 4 * x.bx[s]); }
+            else { isum += __mul24(k.sc[s], dp - 32 * x.bx[s]); }
         }
     }
 }
@@ -223,7 +227,7 @@ __global__ void __launch_bounds__(64 * KQ_WAVES) k_kq_matvec(KqArgs a) {
     constexpr int BS = kbytes<F>();
     constexpr bool MINS = F == KF_Q5K;
     extern __shared__ float s_lds[];   // [rw][TT][nb] terms, then the min terms (Q5_K)
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
     int e, s_beg, s_end;
     if (a.act) {
         if ((int) blockIdx.y >= *a.nact) { return; }
@@ -238,8 +242,18 @@ __global__ void __launch_bounds__(64 * KQ_WAVES) k_kq_matvec(KqArgs a) {
     const int kw = wv % wk, rg = wv / wk;
     const int b = 8 * kw + (lane >> 3), c = lane & 7;          // this lane's block and column slice
     const bool active = rg < wr && b < nb;
-    const size_t rowb = (size_t) nb * BS;
-    const uint8_t * W = a.w + (size_t) e * a.estride + (size_t) b * BS;
+    const uint32_t rowb = (uint32_t) (nb * BS);
+    Src src;
+    {
+        const uint8_t * W = a.w + (size_t) e * a.estride;
+        const uint64_t wv = (uint64_t) W;   // wave-uniform: kept in scalar registers
+        const uint32_t hi = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) (wv >> 32));
+        const uint32_t lo = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) wv);
+        const uint64_t mb = (uint64_t) a.R * rowb;
+        src.rs = __builtin_amdgcn_make_buffer_rsrc((void *) (((uint64_t) hi << 32) | lo), (short) 0,
+                                                   (int) (mb < 0x7fffffffull ? mb : 0x7fffffffull), 0x00020000);
+        src.vb = (uint32_t) (b * BS); src.so = 0;
+    }
 
     for (int sg = s_beg; sg < s_end; sg += TT) {
         const int nt = min(TT, s_end - sg);
@@ -278,19 +292,19 @@ __global__ void __launch_bounds__(64 * KQ_WAVES) k_kq_matvec(KqArgs a) {
                 }
             };
             // two row buffers: the next row's bytes are in flight while the current row is computed
-            const size_t step = (size_t) wr * rowb;
-            const uint8_t * wp = W + (size_t) (tr0 + rg) * rowb;
+            const uint32_t step = (uint32_t) wr * rowb;
+            Src sp = src; sp.so = (uint32_t) (tr0 + rg) * rowb;
             Raw<F> ra, rb;
             int ri = rg;
-            if (ri < nrow) { load_raw<F>(wp, c, ra); }
+            if (ri < nrow) { load_raw<F>(sp, c, ra); }
             while (ri < nrow) {
-                if (ri + wr < nrow) { load_raw<F>(wp + step, c, rb); }
+                if (ri + wr < nrow) { Src sn = sp; sn.so += step; load_raw<F>(sn, c, rb); }
                 row(ra, ri);
-                ri += wr; wp += step;
+                ri += wr; sp.so += step;
                 if (ri >= nrow) { break; }
-                if (ri + wr < nrow) { load_raw<F>(wp + step, c, ra); }
+                if (ri + wr < nrow) { Src sn = sp; sn.so += step; load_raw<F>(sn, c, ra); }
                 row(rb, ri);
-                ri += wr; wp += step;
+                ri += wr; sp.so += step;
             }
         }
         __syncthreads();
