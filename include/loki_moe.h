@@ -100,6 +100,10 @@ typedef struct FLMoeLayer {
     int n_exp;                 /* routed experts (<= 256) */
     int E, H;                  /* hidden (7168) and expert intermediate (2048) sizes; E, H multiples of 1024 */
 } FLMoeLayer;
+/* formats of fl_moe_layer's routed down and shared gate / up / down (default FL_IQ2 x 4; FLMoeLayer carries none):
+ * FL_IQ2 matrices in the tiled layout, K-quants (the real shards' Q2_K / Q3_K down, Q5_K / Q5_K / Q6_K shared) read in
+ * place in ggml's layout, 4-byte aligned. With any K-quant the block runs its per-pass kernels for every n. */
+int fl_set_layer_formats(FLCtx *, int down_fmt, int sh_gate_fmt, int sh_up_fmt, int sh_down_fmt);
 /* y[n][E] = MoE(x[n][E]) on the context's stream (x, y device pointers; asynchronous). n <= 65536.
  * Allocation extents are checked against the shapes (hipMemGetAddressRange) before any launch. */
 int fl_moe_layer(FLCtx *, const FLMoeLayer * L, const float * x, int n, float * y);
@@ -166,11 +170,11 @@ int fl_gguf_read(const FLGguf *, const FLGgufTensor *, uint64_t off, uint64_t by
 
 /* One MoE layer of the index (blk.<layer>.ffn_gate_inp / exp_probs_b / ffn_norm / ffn_{gate,up,down}_exps /
  * ffn_{gate,up,down}_shexp) made resident in HBM in one allocation. The router arrives F32 (ffn_gate_inp.weight, or
- * ffn_gate_inp_f16.weight widened exactly). layout FL_LAYOUT_TILED packs every expert matrix for fl_moe_layer /
- * fl_moe_layer_normed (all must be IQ2_XXS); FL_LAYOUT_GGML keeps the files' bytes, for fl_moe / fl_wide_moe (the layer
- * as the arena, ids = expert ids, down_fmt = fmt_down) and fl_ffn_begin (FLW from L, fl_set_shared_formats with
- * fmt_sh_*). Routed gate/up must be IQ2_XXS, down IQ2_XXS, Q2_K or Q3_K, the shared expert IQ2_XXS or K-quants
- * (FL_ESCOPE otherwise). */
+ * ffn_gate_inp_f16.weight widened exactly). layout FL_LAYOUT_TILED packs the IQ2_XXS matrices for fl_moe_layer /
+ * fl_moe_layer_normed (K-quant ones stay as stored: call fl_set_layer_formats with fmt_down / fmt_sh_*);
+ * FL_LAYOUT_GGML keeps every matrix as stored, for fl_moe / fl_wide_moe (the layer as the arena, ids = expert ids,
+ * down_fmt = fmt_down) and fl_ffn_begin (FLW from L, fl_set_shared_formats with fmt_sh_*). Routed gate/up must be
+ * IQ2_XXS, down IQ2_XXS, Q2_K or Q3_K, the shared expert IQ2_XXS or K-quants (FL_ESCOPE otherwise). */
 typedef struct FLGgufLayer {
     FLMoeLayer L;
     const float * ffn_norm;                 /* [E] F32, device; NULL when the layer has no ffn_norm */

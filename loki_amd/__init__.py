@@ -124,7 +124,7 @@ class FLOut(ctypes.Structure):
 ABI_SYMBOLS = [
     "fl_init", "fl_attn", "fl_wide_init", "fl_wide_moe", "fl_wide_mark", "fl_wide_wait", "fl_wide_finish", "fl_moe_outs",
     "fl_wide_outs", "fl_wide_skip", "fl_spec", "fl_sketch", "fl_fetch", "fl_moe", "fl_skip", "fl_h2d", "fl_wait_event",
-    "fl_gpu_ms", "fl_ffn_begin", "fl_set_experts", "fl_set_routing", "fl_set_shared_formats", "fl_kq_matvec_dev",
+    "fl_gpu_ms", "fl_ffn_begin", "fl_set_experts", "fl_set_routing", "fl_set_shared_formats", "fl_set_layer_formats", "fl_kq_matvec_dev",
     "fl_gguf_open", "fl_gguf_close", "fl_gguf_n_tensors", "fl_gguf_tensor_name", "fl_gguf_tensor", "fl_gguf_tensor_at",
     "fl_gguf_get_int", "fl_gguf_get_float", "fl_gguf_get_str", "fl_gguf_read", "fl_gguf_load_moe_layer", "fl_gguf_free_layer", "fl_moe_layer", "fl_moe_layer_normed", "fl_route_dev", "fl_dispatch_dev", "fl_quant_q8k_dev",
     "fl_pack_iq2xxs", "fl_unpack_iq2xxs", "fl_rmsnorm_dev", "fl_synth_iq2xxs", "fl_synth_normal", "fl_probe_exp",
@@ -157,6 +157,7 @@ def lib():
             "fl_set_routing": (I, [P_, I, I, I, F]),
             "fl_set_experts": (I, [P_, I]),
             "fl_set_shared_formats": (I, [P_, I, I, I]),
+            "fl_set_layer_formats": (I, [P_, I, I, I, I]),
             "fl_kq_matvec_dev": (I, [P_, I, P_, I, I, P_, P_, I, P_]),
             "fl_gguf_open": (P_, [ctypes.POINTER(ctypes.c_char_p), I, ctypes.c_char_p, S]),
             "fl_gguf_close": (None, [P_]),
@@ -284,6 +285,10 @@ class Context:
     def set_shared_formats(self, gate=FL_IQ2, up=FL_IQ2, down=FL_IQ2):
         """Formats of FLW's shared expert for fl_ffn_begin; the reference's shards: (FL_Q5K, FL_Q5K, FL_Q6K)."""
         self.check(lib().fl_set_shared_formats(self.ctx, gate, up, down))
+
+    def set_layer_formats(self, down=FL_IQ2, sh_gate=FL_IQ2, sh_up=FL_IQ2, sh_down=FL_IQ2):
+        """Formats of fl_moe_layer's routed down and shared matrices (K-quants read in place, IQ2_XXS tiled)."""
+        self.check(lib().fl_set_layer_formats(self.ctx, down, sh_gate, sh_up, sh_down))
 
     def set_debug(self, capture_gate_up):
         self.check(lib().fl_set_debug(self.ctx, 1 if capture_gate_up else 0))

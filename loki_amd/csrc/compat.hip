@@ -139,7 +139,7 @@ void compat_free(FLCtx * c) {
     delete s; c->compat = nullptr;
 }
 
-static const int * zero_int(FLCtx * c) {
+const int * zero_int(FLCtx * c) {
     if (!c->zero_dev_init) {
         CK(c->zero_i.ensure(1) == hipSuccess ? hipSuccess : hipErrorOutOfMemory);
         const int z = 0; CK(hipMemcpy(c->zero_i.p, &z, sizeof z, hipMemcpyHostToDevice));

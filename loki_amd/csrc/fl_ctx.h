@@ -54,7 +54,13 @@ struct FLCtx {
     // prefill grouped GEMM on MFMA (batches above the decode sizes): fp16 table image, columns, fp16 activation copies
     int pf_mfma = 1, pf_ready = 0; DBuf<uint4> ptab; DBuf<int4> pcols; DBuf<int> pncols; DBuf<_Float16> xh, hh;
     struct Compat * compat = nullptr;          // reference-API state (compat.hip), created on first use
+    // formats of fl_moe_layer's matrices (fl_set_layer_formats): routed down, shared gate, up, down; K-quant matrices
+    // are read in place (ggml layout), IQ2_XXS ones tiled
+    int lf[4] = { FL_IQ2, FL_IQ2, FL_IQ2, FL_IQ2 };
+    DBuf<float> ksg, ksu;                      // K-quant shared gate / up outputs
 };
+// a device int 0 (empty expert lists of the per-pass kernels)
+const int * zero_int(FLCtx * c);
 static const int NSTAGE = 6;   // quant_x, router_logits, router_select, dispatch, gate_up (+SwiGLU, Q8_K(h)), down (+combine)
 // counters of the persistent expert kernels: per (expert slot, row group) and per h block / combine row group
 static const size_t CNT_RG = (size_t) (lk::NEXP_MAX + 1) * 112;           // 112 = 7168 / 64 row groups (the largest R)

@@ -244,6 +244,16 @@ static bool decode_ready(FLCtx * c) {
 
 // ================================================================ the device-resident block
 // the block on x, or on RMSNorm(x) * nw when prenorm (nw may be null: ones); resid (may be null) is added to the output
+// bytes of one R x K matrix in format f (IQ2_XXS or a K-quant)
+static size_t fmt_mat_bytes(int f, int R, int K) { return (size_t) R * (K / 256) * (size_t) (f == FL_IQ2 ? IQ2B : kq_block_bytes(f)); }
+// K-quant mat-vec of one matrix (ggml layout, in place) on n Q8_K rows -> out [n][R]
+static hipError_t kq_one(FLCtx * c, int fmt, const void * w, const int8_t * q, const float * d, int n, int K, int R, float * out) {
+    KqArgs k{};
+    k.w = (const uint8_t *) w; k.estride = fmt_mat_bytes(fmt, R, K); k.aq = q; k.ad = d; k.K = K; k.R = R;
+    k.n = n; k.out = out; k.ldo = R;
+    return launch_kq_matvec(k, fmt, n, 1, c->st);
+}
+
 static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, float * y, bool prenorm, const float * nw, float eps,
                      const float * resid) {
     if (!c) { return FL_EINVAL; }
@@ -257,19 +267,27 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
         return fail(c, FL_EINVAL, "null pointer in the layer or x / y");
     }
     const int E = L->E, H = L->H, ne = L->n_exp, tk = c->topk, P = n * tk;
+    const int * lf = c->lf;
+    const bool kq = lf[0] != FL_IQ2 || lf[1] != FL_IQ2 || lf[2] != FL_IQ2 || lf[3] != FL_IQ2;
     {
-        const size_t mg = (size_t) H * (E / 256) * IQ2B;   // one gate/up (and one down) matrix
+        const size_t mg = (size_t) H * (E / 256) * IQ2B;   // one gate/up matrix
         if (!covers(L->gate_inp, (size_t) ne * E * 4) || !covers(L->probs_b, (size_t) ne * 4) || !covers(x, (size_t) n * E * 4) ||
-            !covers(y, (size_t) n * E * 4) || !covers(L->gate_exps, ne * mg) || !covers(L->up_exps, ne * mg) || !covers(L->down_exps, ne * mg) ||
-            !covers(L->sh_gate, mg) || !covers(L->sh_up, mg) || !covers(L->sh_down, mg)) {
+            !covers(y, (size_t) n * E * 4) || !covers(L->gate_exps, ne * mg) || !covers(L->up_exps, ne * mg) ||
+            !covers(L->down_exps, ne * fmt_mat_bytes(lf[0], E, H)) || !covers(L->sh_gate, fmt_mat_bytes(lf[1], H, E)) ||
+            !covers(L->sh_up, fmt_mat_bytes(lf[2], H, E)) || !covers(L->sh_down, fmt_mat_bytes(lf[3], E, H))) {
             return fail(c, FL_EINVAL, "an allocation of the layer, x or y is smaller than its shape (%d experts, E %d, H %d, n %d)", ne, E, H, n);
         }
         if (prenorm && nw && !covers(nw, (size_t) E * 4)) { return fail(c, FL_EINVAL, "the norm weight is smaller than E = %d floats", E); }
+        const void * km[4] = { L->down_exps, L->sh_gate, L->sh_up, L->sh_down };
+        for (int i = 0; i < 4; ++i) {
+            if (lf[i] != FL_IQ2 && (reinterpret_cast<uintptr_t>(km[i]) & 3u)) { return fail(c, FL_EINVAL, "K-quant matrices must be 4-byte aligned"); }
+        }
         if (prenorm && !(eps >= 0.f)) { return fail(c, FL_EINVAL, "bad norm eps %g", (double) eps); }
     }
     const size_t rows = (size_t) P + n;
-    const bool fused = c->fused && n <= 8 && E == 7168 && H == 2048 && decode_rule_ok(ne, c->n_group) && decode_ready(c);
-    const bool mfma = !fused && c->pf_mfma && n > 8 && E == 7168 && H == 2048;
+    // K-quant matrices run on the per-pass path (the decode block and the MFMA GEMMs read IQ2_XXS tiles)
+    const bool fused = !kq && c->fused && n <= 8 && E == 7168 && H == 2048 && decode_rule_ok(ne, c->n_group) && decode_ready(c);
+    const bool mfma = !kq && !fused && c->pf_mfma && n > 8 && E == 7168 && H == 2048;
     ALLOC(c, c->xq, (size_t) n * E); ALLOC(c, c->xd, (size_t) n * (E / 256));
     ALLOC(c, c->logits, (size_t) n * ne); ALLOC(c, c->probs, (size_t) n * ne);
     ALLOC(c, c->sel, P); ALLOC(c, c->wts, P); ALLOC(c, c->perm, P); ALLOC(c, c->inv, P);
@@ -353,7 +371,8 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
         return FL_OK;
     }
     prof_mark(c, ev, 4);
-    ExpertArgs a = expert_args(c, n, P, 1);
+    const bool ksh = lf[1] != FL_IQ2;   // the shared gate / up in K-quants: run beside the routed IQ2_XXS tasks
+    ExpertArgs a = expert_args(c, n, P, ksh ? 0 : 1);
     a.w[0] = (const uint8_t *) L->gate_exps; a.w[1] = (const uint8_t *) L->up_exps; a.estride = (size_t) H * (E / 256) * IQ2B;
     a.sh[0] = (const uint8_t *) L->sh_gate; a.sh[1] = (const uint8_t *) L->sh_up;
     a.aq = c->xq.p; a.ad = c->xd.p; a.K = E; a.R = H; a.nmat = 2;
@@ -362,7 +381,46 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     a.gdbg = c->dbg_gu ? c->g.p : nullptr; a.udbg = c->dbg_gu ? c->u.p : nullptr;
     expert_counters(c, a, 0);
     TRY(c, launch_experts_gateup(a, c->ncu, st));
+    if (ksh) {   // rows P .. P + n - 1 of h / Q8_K(h): the shared expert (src/fused_layer.cu:520-523)
+        ALLOC(c, c->ksg, (size_t) n * H); ALLOC(c, c->ksu, (size_t) n * H);
+        TRY(c, kq_one(c, lf[1], L->sh_gate, c->xq.p, c->xd.p, n, E, H, c->ksg.p));
+        TRY(c, kq_one(c, lf[2], L->sh_up, c->xq.p, c->xd.p, n, E, H, c->ksu.p));
+        TRY(c, launch_swiglu(c->ksg.p, c->ksu.p, (int64_t) n * H, c->h.p + (size_t) P * H, st));
+        TRY(c, launch_quant_q8k(c->h.p + (size_t) P * H, n, H, c->hq.p + (size_t) P * H, c->hd.p + (size_t) P * (H / 256), st));
+        if (c->dbg_gu) {
+            TRY(c, hipMemcpyAsync(c->g.p + (size_t) P * H, c->ksg.p, (size_t) n * H * 4, hipMemcpyDeviceToDevice, st));
+            TRY(c, hipMemcpyAsync(c->u.p + (size_t) P * H, c->ksu.p, (size_t) n * H * 4, hipMemcpyDeviceToDevice, st));
+        }
+    }
     prof_mark(c, ev, 5);
+    if (kq) {   // o of every slot by its matrix's format, then the k-ordered combine (+ shared, + residual)
+        ExpertArgs d = a;
+        d.shared = 0; d.aq = c->hq.p; d.ad = c->hd.p; d.K = H; d.R = E; d.nmat = 1;
+        d.h = nullptr; d.hq = nullptr; d.hd = nullptr; d.gdbg = nullptr; d.udbg = nullptr; d.o = c->o.p; d.y = nullptr;
+        if (lf[0] == FL_IQ2) {
+            d.w[0] = (const uint8_t *) L->down_exps; d.w[1] = nullptr; d.sh[0] = nullptr; d.sh[1] = nullptr;
+            expert_counters(c, d, 1);
+            TRY(c, launch_experts_down(d, c->ncu, st));
+        } else {   // src/fused_layer.cu:607-608
+            KqArgs k{};
+            k.w = (const uint8_t *) L->down_exps; k.estride = fmt_mat_bytes(lf[0], E, H); k.aq = c->hq.p; k.ad = c->hd.p; k.K = H; k.R = E;
+            k.act = c->act.p; k.nact = c->nact.p; k.offsets = c->offsets.p; k.out = c->o.p; k.ldo = E;
+            TRY(c, launch_kq_matvec(k, lf[0], n, ne < P ? ne : P, st));
+        }
+        if (lf[3] == FL_IQ2) {   // the shared expert alone: an empty routed list, its slots P ..
+            ExpertArgs s = expert_args(c, n, P, 1);
+            s.sh[0] = (const uint8_t *) L->sh_down; s.sh[1] = nullptr; s.aq = c->hq.p; s.ad = c->hd.p; s.K = H; s.R = E; s.nmat = 1;
+            s.act = zero_int(c); s.nact = zero_int(c); s.offsets = zero_int(c); s.perm = zero_int(c); s.topk = tk;
+            s.h = nullptr; s.hq = nullptr; s.hd = nullptr; s.o = c->o.p; s.y = nullptr;
+            expert_counters(c, s, 1);
+            TRY(c, launch_experts_down(s, c->ncu, st));
+        } else {
+            TRY(c, kq_one(c, lf[3], L->sh_down, c->hq.p + (size_t) P * H, c->hd.p + (size_t) P * (H / 256), n, H, E, c->o.p + (size_t) P * E));
+        }
+        TRY(c, launch_combine(c->o.p, c->inv.p, c->wts.p, n, tk, E, P, resid, y, nullptr, st));
+        prof_mark(c, ev, 6);
+        return FL_OK;
+    }
     ExpertArgs d = a;
     d.w[0] = (const uint8_t *) L->down_exps; d.w[1] = nullptr; d.sh[0] = (const uint8_t *) L->sh_down; d.sh[1] = nullptr;
     d.aq = c->hq.p; d.ad = c->hd.p; d.K = H; d.R = E; d.nmat = 1;
@@ -373,6 +431,17 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     prof_mark(c, ev, 6);
     return FL_OK;
 }
+extern "C" int fl_set_layer_formats(FLCtx * c, int down_fmt, int sh_gate_fmt, int sh_up_fmt, int sh_down_fmt) {
+    if (!c) { return FL_EINVAL; }
+    const int f[4] = { down_fmt, sh_gate_fmt, sh_up_fmt, sh_down_fmt };
+    for (int i = 0; i < 4; ++i) {
+        if (f[i] != FL_IQ2 && kq_block_bytes(f[i]) == 0) { return fail(c, FL_EINVAL, "format %d is not IQ2_XXS or a K-quant (Q2_K, Q3_K, Q5_K, Q6_K)", f[i]); }
+    }
+    if ((sh_gate_fmt == FL_IQ2) != (sh_up_fmt == FL_IQ2)) { return fail(c, FL_EINVAL, "shared gate and up must both be IQ2_XXS or both K-quants"); }
+    for (int i = 0; i < 4; ++i) { c->lf[i] = f[i]; }
+    return FL_OK;
+}
+
 extern "C" int fl_moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, float * y) {
     return moe_layer(c, L, x, n, y, false, nullptr, 0.f, nullptr);
 }

@@ -312,8 +312,6 @@ extern "C" int fl_gguf_load_moe_layer(FLCtx * c, const FLGguf * g, int layer, in
         if (fm[k] != FL_IQ2 && kq_block_bytes(fm[k]) == 0) { return fail(c, FL_ESCOPE, "%s: shared-expert type %d (IQ2_XXS or Q2_K / Q3_K / Q5_K / Q6_K)", p.c_str(), ts[k - 3].type); }
     }
     if ((fm[3] == FL_IQ2) != (fm[4] == FL_IQ2)) { return fail(c, FL_ESCOPE, "%s: shared gate and up must both be IQ2_XXS or both K-quants", p.c_str()); }
-    const bool all_iq2 = fm[2] == FL_IQ2 && fm[3] == FL_IQ2 && fm[4] == FL_IQ2 && fm[5] == FL_IQ2;
-    if (layout == FL_LAYOUT_TILED && !all_iq2) { return fail(c, FL_ESCOPE, "%s: the tiled layout (fl_moe_layer) needs every expert matrix in IQ2_XXS", p.c_str()); }
     // one allocation: router (F32), bias, norm, 3 routed tensors, 3 shared matrices; 256-byte aligned parts
     auto al = [](uint64_t v) { return (v + 255) / 256 * 256; };
     const uint64_t szr = (uint64_t) E * ne * 4, szb = (uint64_t) ne * 4, szn = has_norm ? (uint64_t) E * 4 : 0;
@@ -324,7 +322,12 @@ extern "C" int fl_gguf_load_moe_layer(FLCtx * c, const FLGguf * g, int layer, in
     if (hipMalloc((void **) &mem, tot) != hipSuccess) { (void) hipGetLastError(); return fail(c, FL_ENOMEM, "device allocation of %llu bytes", (unsigned long long) tot); }
     uint8_t * stage = nullptr;   // ggml-layout staging for the tiled layout, and for the F16 router
     uint64_t stage_sz = r16 ? tr.nbytes : 0;
-    if (layout == FL_LAYOUT_TILED) { for (int k = 0; k < 3; ++k) { stage_sz = std::max(stage_sz, std::max(te[k].nbytes, ts[k].nbytes)); } }
+    if (layout == FL_LAYOUT_TILED) {
+        for (int k = 0; k < 3; ++k) {
+            if (fm[k] == FL_IQ2) { stage_sz = std::max(stage_sz, te[k].nbytes); }
+            if (fm[3 + k] == FL_IQ2) { stage_sz = std::max(stage_sz, ts[k].nbytes); }
+        }
+    }
     int rc = FL_OK;
     if (stage_sz && hipMalloc((void **) &stage, stage_sz) != hipSuccess) { (void) hipGetLastError(); rc = fail(c, FL_ENOMEM, "staging allocation"); }
     if (rc == FL_OK) {
@@ -341,7 +344,7 @@ extern "C" int fl_gguf_load_moe_layer(FLCtx * c, const FLGguf * g, int layer, in
     for (int k = 0; k < 6 && rc == FL_OK; ++k) {
         uint8_t * dst = mem + off[3 + k];
         const FLGgufTensor & t = *mats[k];
-        if (layout == FL_LAYOUT_TILED) {
+        if (layout == FL_LAYOUT_TILED && fm[k] == FL_IQ2) {   // K-quant matrices stay as stored in either layout
             rc = upload(c, g, t, stage);
             const int R = (int) t.ne[1], K = (int) t.ne[0], nm = (int) t.ne[2];
             const size_t ms = (size_t) t.row_bytes * (size_t) R;

@@ -109,13 +109,60 @@ def test_gguf_layer_ggml_real_formats(ctx, tmp_path):
         g.close()
 
 
+def test_gguf_layer_real_formats_device_resident(ctx, tmp_path):
+    """a real-shard layer loaded tiled (IQ2_XXS gate/up packed, Q2_K down and Q5_K / Q5_K / Q6_K shared as stored) runs
+    on the device with no host round trip: fl_moe_layer at a decode size and fl_moe_layer_normed (ffn_norm from the
+    file, residual added) at a prefill size, against the checker; routing bit-identical"""
+    import torch
+    from loki_amd import Gguf, lib, FL_LAYOUT_TILED
+    W, b, gate, up, _, _ = gen.layer(206, NE, E, H)
+    down = [gen.kq_matrix(207, e, orc.Q2K, E, H) for e in range(NE)]
+    ksh = (gen.kq_matrix(208, 1, orc.Q5K, H, E), gen.kq_matrix(208, 2, orc.Q5K, H, E), gen.kq_matrix(208, 3, orc.Q6K, E, H))
+    norm = gen.uniform(208, 4, (E,), 1.0) + np.float32(1.0)
+    path = str(tmp_path / "layer9.gguf")
+    _gguf.write(path, layer_tensors(9, W, b, gate, up, down, ksh, ["IQ2_XXS", "IQ2_XXS", "Q2_K", "Q5_K", "Q5_K", "Q6_K"], norm=norm))
+    g = Gguf(path)
+    gl = ctx.load_gguf_layer(g, 9, FL_LAYOUT_TILED)
+    fm = (orc.Q2K, orc.Q5K, orc.Q5K, orc.Q6K)
+    try:
+        assert (gl.fmt_down, gl.fmt_sh_gate, gl.fmt_sh_up, gl.fmt_sh_down) == fm
+        ctx.set_experts(NE); ctx.set_routing(8, 4, 8, 2.5)
+        ctx.set_layer_formats(*fm)
+        for n, normed in ((5, False), (40, True)):
+            print("device-resident real formats: n %d normed %d" % (n, normed), flush=True)
+            x = gen.uniform(12, n, (n, E), 2.0)
+            xt = torch.from_numpy(x).cuda(); y = torch.empty_like(xt)
+            if normed:
+                ctx.check(lib().fl_moe_layer_normed(ctx.ctx, ctypes.byref(gl.L), ctypes.c_void_p(gl.ffn_norm), ctypes.c_float(1e-6),
+                                                    ctypes.c_void_p(xt.data_ptr()), n, 1, ctypes.c_void_p(y.data_ptr())))
+                xin = orc.rmsnorm(x, norm, 1e-6)
+            else:
+                ctx.check(lib().fl_moe_layer(ctx.ctx, ctypes.byref(gl.L), ctypes.c_void_p(xt.data_ptr()), n, ctypes.c_void_p(y.data_ptr())))
+                xin = x
+            ctx.sync()
+            dbg = ctx.debug()
+            _, _, so, wo = orc.router(W, b, xin, 8, 4, 8, 2.5)
+            assert np.array_equal(ctx.d2h(dbg.sel, (n, KE), np.int32), so)
+            ref = orc.moe_experts(xin, so, wo, gate, up, down, *ksh, n_exp=NE, fmts=fm)["y"]
+            if normed:
+                ref = (ref + x).astype(np.float32)
+            got = y.cpu().numpy().astype(np.float64)
+            e_l2 = np.linalg.norm(got - ref) / np.linalg.norm(ref.astype(np.float64))
+            e_mx = np.abs(got - ref).max() / np.abs(ref).max()
+            assert e_l2 <= 1e-4 and e_mx <= 1e-3, (n, e_l2, e_mx)
+    finally:
+        ctx.set_layer_formats(); ctx.set_experts()
+        ctx.free_gguf_layer(gl)
+        g.close()
+
+
 def test_gguf_layer_rejects(ctx, tmp_path):
-    """a tiled load of a layer with K-quant matrices and a missing layer come back as error codes"""
+    """an absent layer and a routed gate in a K-quant come back as error codes"""
     from loki_amd import Gguf, LokiError, FL_LAYOUT_TILED
     W, b, gate, up, down, sh = gen.layer(203, NE, E, H)
-    down_q2 = [gen.kq_matrix(205, e, orc.Q2K, E, H) for e in range(NE)]
+    gate_q2 = [gen.kq_matrix(205, e, orc.Q2K, H, E) for e in range(NE)]
     path = str(tmp_path / "l.gguf")
-    _gguf.write(path, layer_tensors(5, W, b, gate, up, down_q2, sh, ["IQ2_XXS", "IQ2_XXS", "Q2_K", "IQ2_XXS", "IQ2_XXS", "IQ2_XXS"]))
+    _gguf.write(path, layer_tensors(5, W, b, gate_q2, up, down, sh, ["Q2_K", "IQ2_XXS", "IQ2_XXS", "IQ2_XXS", "IQ2_XXS", "IQ2_XXS"]))
     g = Gguf(path)
     with pytest.raises(LokiError):
         ctx.load_gguf_layer(g, 5, FL_LAYOUT_TILED)
