@@ -205,6 +205,51 @@ def run_kquant(ctx, torch, iters=20, seed=20260401):
     return out
 
 
+def run_realfmt(ctx, torch, steps=20, warmup=3, copies=2, seed=20260501):
+    """fl_moe_layer on the reference's real-shard formats, device-resident: IQ2_XXS routed gate/up (tiled), Q3_K routed
+    down and a Q5_K / Q5_K / Q6_K shared expert read in place (fl_set_layer_formats); decode-8 and decode-1, fresh x per
+    step, layer copies rotated. Algorithmic bytes: U * (2 IQ2_XXS + 1 Q3_K matrix) + the shared expert + the router."""
+    from loki_amd import MoeLayerWeights
+    layers = []
+    for c in range(copies):
+        base = MoeLayerWeights.synthetic(ctx, seed + 1000 * c)
+        down = kq_random(torch, 6, 256 * E, H, seed + 1000 * c + 1)
+        shg, shu, shd = (kq_random(torch, 3, H, E, seed + 1000 * c + 2), kq_random(torch, 3, H, E, seed + 1000 * c + 3),
+                         kq_random(torch, 1, E, H, seed + 1000 * c + 4))
+        layers.append(MoeLayerWeights(base.gate_inp, base.probs_b, base.gate, base.up, down, shg, shu, shd))
+    ctx.set_layer_formats(6, 3, 3, 1)
+    out = {}
+    try:
+        for name, n in (("decode8", 8), ("decode1", 1)):
+            xs = []
+            for i in range(steps + warmup):
+                x = torch.empty((n, E), dtype=torch.float32, device="cuda")
+                ctx.synth_normal(x, seed + 17, 3000 + i, 0.0, 1.0)
+                xs.append(x)
+            y = torch.empty((n, E), dtype=torch.float32, device="cuda")
+            for i in range(warmup):
+                ctx.moe_layer(layers[i % copies], xs[i], y)
+            torch.cuda.synchronize()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record()
+            for i in range(steps):
+                ctx.moe_layer(layers[(warmup + i) % copies], xs[warmup + i], y)
+            t1.record()
+            torch.cuda.synchronize()
+            ms = t0.elapsed_time(t1) / steps
+            U = sum(distinct_experts(ctx, layers[(warmup + i) % copies], [xs[warmup + i]])[0] for i in range(steps)) / steps
+            b = U * (2 * MAT_BYTES + E * (H // 256) * 110) + 2 * H * (E // 256) * 176 + E * (H // 256) * 210 + ROUTER_BYTES
+            out[name] = {"us_per_token": round(ms * 1e3 / n, 2), "ms_per_step": round(ms, 4), "distinct_experts": round(U, 1),
+                         "bytes_per_step": int(b), "hbm_gbs": round(b / (ms * 1e-3) / 1e9, 1),
+                         "hbm_frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            log("[bench] real formats %s: %s" % (name, json.dumps(out[name])))
+    finally:
+        ctx.set_layer_formats()
+    del layers
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(ctx, torch, res, budget_s=12.0, max_steps=8):
     """The CPU checker (oracle/, restated ggml CPU semantics) on this host's cores, on a bounded sample of the same
     workload: the first steps' x with the experts they select, timed around the oracle call only."""
@@ -270,7 +315,7 @@ def main():
     if args.fused is not None:
         ctx.set_fused(args.fused)
     if args.only_kquant:
-        print(json.dumps({"kquant": run_kquant(ctx, torch)}), flush=True)
+        print(json.dumps({"kquant": run_kquant(ctx, torch), "real_formats": run_realfmt(ctx, torch)}), flush=True)
         return
     res = run_workload(ctx, torch, args.workload, args.steps, args.warmup, args.copies)
     n = res["n"]
@@ -308,6 +353,7 @@ def main():
     if not args.no_extra:
         torch.cuda.empty_cache()
         extra["kquant"] = run_kquant(ctx, torch)
+        extra["real_formats"] = run_realfmt(ctx, torch)
     if not args.no_stack:
         torch.cuda.empty_cache()
         extra["stack58"] = run_stack(ctx, torch, args.stack_steps, 2)

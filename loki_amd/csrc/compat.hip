@@ -178,8 +178,15 @@ static void shared_expert(FLCtx * c, Compat * s, const int8_t * xq, const float 
         FCK(launch_experts_gateup(a, c->ncu, c->st));
     } else {   // g, u, then h = silu(g) * u and its Q8_K (src/fused_layer.cu:522-523)
         FALLOC(s->sg, (size_t) N * H_); FALLOC(s->su, (size_t) N * H_);
-        kq_single(c, s->shf[0], s->sh_key[0], xq, xd, N, E_, H_, s->sg.p);
-        kq_single(c, s->shf[1], s->sh_key[1], xq, xd, N, E_, H_, s->su.p);
+        if (s->shf[0] == s->shf[1]) {   // gate and up in one launch
+            KqArgs k{};
+            k.w = (const uint8_t *) s->sh_key[0]; k.w2 = (const uint8_t *) s->sh_key[1]; k.estride = fmt_bytes(s->shf[0], H_, E_);
+            k.aq = xq; k.ad = xd; k.K = E_; k.R = H_; k.n = N; k.out = s->sg.p; k.out2 = s->su.p; k.ldo = H_;
+            FCK(launch_kq_matvec(k, s->shf[0], N, 1, c->st));
+        } else {
+            kq_single(c, s->shf[0], s->sh_key[0], xq, xd, N, E_, H_, s->sg.p);
+            kq_single(c, s->shf[1], s->sh_key[1], xq, xd, N, E_, H_, s->su.p);
+        }
         FCK(launch_swiglu(s->sg.p, s->su.p, (int64_t) N * H_, s->h.p, c->st));
         FCK(launch_quant_q8k(s->h.p, N, H_, s->hq.p, s->hd.p, c->st));
     }

@@ -27,13 +27,26 @@ __global__ void __launch_bounds__(1024) k_dispatch(const int * __restrict__ sel,
         if (e >= 0 && e < n_exp) { atomicAdd(&cnt[e], 1); }
     }
     __syncthreads();
-    if (tid == 0) {
-        int acc = 0, m = 0;
-        for (int e = 0; e < n_exp; ++e) {
-            base[e] = acc; offsets[e] = acc; counts[e] = cnt[e]; acc += cnt[e];
-            if (cnt[e] > 0) { act[m++] = e; }
+    if (wave == 0) {   // exclusive scan of the counts and the used-expert list: experts 4 lane .. 4 lane + 3 per lane
+        int c[4], s = 0, z = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { const int e = 4 * lane + j; c[j] = e < n_exp ? cnt[e] : 0; s += c[j]; z += c[j] > 0; }
+        int si = s, zi = z;   // inclusive scans over the lanes
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int vs = __shfl_up(si, o), vz = __shfl_up(zi, o);
+            if (lane >= o) { si += vs; zi += vz; }
         }
-        offsets[n_exp] = acc; *nact = m;
+        int acc = si - s, m = zi - z;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = 4 * lane + j;
+            if (e < n_exp) {
+                base[e] = acc; offsets[e] = acc; counts[e] = c[j]; acc += c[j];
+                if (c[j] > 0) { act[m++] = e; }
+            }
+        }
+        if (lane == 63) { offsets[n_exp] = si; *nact = zi; }
     }
     __syncthreads();
     const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));

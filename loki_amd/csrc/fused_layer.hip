@@ -383,8 +383,15 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     TRY(c, launch_experts_gateup(a, c->ncu, st));
     if (ksh) {   // rows P .. P + n - 1 of h / Q8_K(h): the shared expert (src/fused_layer.cu:520-523)
         ALLOC(c, c->ksg, (size_t) n * H); ALLOC(c, c->ksu, (size_t) n * H);
-        TRY(c, kq_one(c, lf[1], L->sh_gate, c->xq.p, c->xd.p, n, E, H, c->ksg.p));
-        TRY(c, kq_one(c, lf[2], L->sh_up, c->xq.p, c->xd.p, n, E, H, c->ksu.p));
+        if (lf[1] == lf[2]) {   // gate and up in one launch
+            KqArgs k{};
+            k.w = (const uint8_t *) L->sh_gate; k.w2 = (const uint8_t *) L->sh_up; k.estride = fmt_mat_bytes(lf[1], H, E);
+            k.aq = c->xq.p; k.ad = c->xd.p; k.K = E; k.R = H; k.n = n; k.out = c->ksg.p; k.out2 = c->ksu.p; k.ldo = H;
+            TRY(c, launch_kq_matvec(k, lf[1], n, 1, st));
+        } else {
+            TRY(c, kq_one(c, lf[1], L->sh_gate, c->xq.p, c->xd.p, n, E, H, c->ksg.p));
+            TRY(c, kq_one(c, lf[2], L->sh_up, c->xq.p, c->xd.p, n, E, H, c->ksu.p));
+        }
         TRY(c, launch_swiglu(c->ksg.p, c->ksu.p, (int64_t) n * H, c->h.p + (size_t) P * H, st));
         TRY(c, launch_quant_q8k(c->h.p + (size_t) P * H, n, H, c->hq.p + (size_t) P * H, c->hd.p + (size_t) P * (H / 256), st));
         if (c->dbg_gu) {

@@ -233,6 +233,9 @@ __global__ void __launch_bounds__(64 * KQ_WAVES) k_kq_matvec(KqArgs a) {
         if ((int) blockIdx.y >= *a.nact) { return; }
         e = a.act[blockIdx.y]; s_beg = a.offsets[e]; s_end = a.offsets[e + 1];
     } else { e = 0; s_beg = 0; s_end = a.n; }
+    const bool second = !a.act && blockIdx.y == 1;   // the second matrix (w2 -> out2)
+    const uint8_t * Wm = second ? a.w2 : a.w;
+    float * Out = second ? a.out2 : a.out;
     const int tr0 = (int) blockIdx.x * a.rw;
     if (tr0 >= a.R || s_beg >= s_end) { return; }
     const int nrow = min(a.rw, a.R - tr0);
@@ -245,7 +248,7 @@ __global__ void __launch_bounds__(64 * KQ_WAVES) k_kq_matvec(KqArgs a) {
     const uint32_t rowb = (uint32_t) (nb * BS);
     Src src;
     {
-        const uint8_t * W = a.w + (size_t) e * a.estride;
+        const uint8_t * W = Wm + (size_t) e * a.estride;
         const uint64_t wv = (uint64_t) W;   // wave-uniform: kept in scalar registers
         const uint32_t hi = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) (wv >> 32));
         const uint32_t lo = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) wv);
@@ -321,7 +324,7 @@ __global__ void __launch_bounds__(64 * KQ_WAVES) k_kq_matvec(KqArgs a) {
             } else {
                 for (int j = 0; j < nb; ++j) { acc = acc + tp[j]; }
             }
-            a.out[(size_t) (sg + t) * a.ldo + tr0 + ri] = acc;
+            Out[(size_t) (sg + t) * a.ldo + tr0 + ri] = acc;
         }
         __syncthreads();
     }
@@ -349,10 +352,10 @@ hipError_t launch_kq_matvec(const KqArgs & args, int fmt, int max_slots, int gri
     if (a.K <= 0 || a.K % QK || a.K > QK * NB_MAX || a.R <= 0 || max_slots <= 0 || grid_experts <= 0 || kq_block_bytes(fmt) == 0) { return hipErrorInvalidValue; }
     // rows per workgroup tile: RT_MAX when the launch has rows enough, else fewer so that it still spreads over
     // ~1024 workgroups
-    const int64_t rows_total = (int64_t) a.R * (a.act ? grid_experts : 1);
+    const int64_t rows_total = (int64_t) a.R * (a.act ? grid_experts : (a.w2 ? 2 : 1));
     a.rw = (int) std::max<int64_t>(1, std::min<int64_t>(RT_MAX, rows_total / 1024));
     const int tt = max_slots <= 1 ? 1 : max_slots <= 2 ? 2 : max_slots <= 4 ? 4 : 8;
-    const unsigned gy = a.act ? (unsigned) grid_experts : 1u;
+    const unsigned gy = a.act ? (unsigned) grid_experts : (a.w2 ? 2u : 1u);
     switch (fmt) {
         case KF_Q2K: return go_f<KF_Q2K>(a, tt, gy, st);
         case KF_Q3K: return go_f<KF_Q3K>(a, tt, gy, st);

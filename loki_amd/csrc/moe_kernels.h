@@ -120,6 +120,8 @@ struct KqArgs {
     int n;
     float * out; int ldo;                // out[s * ldo + r]
     int rw;                              // rows per workgroup tile (set by launch_kq_matvec)
+    const uint8_t * w2; float * out2;    // act == null: a second matrix of the same shape and format on the same rows
+                                         // (workgroup row y = 1), e.g. the shared expert's up beside its gate
 };
 // block bytes of a K-quant format code (FL_Q2K 84, FL_Q3K 110, FL_Q5K 176, FL_Q6K 210; 0 = not a K-quant)
 int kq_block_bytes(int fmt);
