@@ -412,7 +412,8 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
             KqArgs k{};
             k.w = (const uint8_t *) L->down_exps; k.estride = fmt_mat_bytes(lf[0], E, H); k.aq = c->hq.p; k.ad = c->hd.p; k.K = H; k.R = E;
             k.act = c->act.p; k.nact = c->nact.p; k.offsets = c->offsets.p; k.out = c->o.p; k.ldo = E;
-            TRY(c, launch_kq_matvec(k, lf[0], n, ne < P ? ne : P, st));
+            // token groups sized for the expected slots per expert (an expert with more runs extra groups)
+            TRY(c, launch_kq_matvec(k, lf[0], (P + ne - 1) / ne, ne < P ? ne : P, st));
         }
         if (lf[3] == FL_IQ2) {   // the shared expert alone: an empty routed list, its slots P ..
             ExpertArgs s = expert_args(c, n, P, 1);

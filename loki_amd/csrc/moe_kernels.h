@@ -125,7 +125,8 @@ struct KqArgs {
 };
 // block bytes of a K-quant format code (FL_Q2K 84, FL_Q3K 110, FL_Q5K 176, FL_Q6K 210; 0 = not a K-quant)
 int kq_block_bytes(int fmt);
-// max_slots: an upper bound of the slots of one expert (sizes the token groups); grid_experts >= *nact
+// max_slots sizes the token groups (a bound or the expected slots of one expert; more run as extra groups);
+// grid_experts >= *nact
 hipError_t launch_kq_matvec(const KqArgs & a, int fmt, int max_slots, int grid_experts, hipStream_t st);
 // h = silu(g) * u, element-wise under the exp contract
 hipError_t launch_swiglu(const float * g, const float * u, int64_t n, float * h, hipStream_t st);
