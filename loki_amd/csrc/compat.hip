@@ -187,8 +187,7 @@ static void shared_expert(FLCtx * c, Compat * s, const int8_t * xq, const float 
             kq_single(c, s->shf[0], s->sh_key[0], xq, xd, N, E_, H_, s->sg.p);
             kq_single(c, s->shf[1], s->sh_key[1], xq, xd, N, E_, H_, s->su.p);
         }
-        FCK(launch_swiglu(s->sg.p, s->su.p, (int64_t) N * H_, s->h.p, c->st));
-        FCK(launch_quant_q8k(s->h.p, N, H_, s->hq.p, s->hd.p, c->st));
+        FCK(launch_swiglu_q8k(s->sg.p, s->su.p, N, H_, s->h.p, s->hq.p, s->hd.p, c->st));
     }
     if (s->shf[2] == FL_IQ2) {
         ExpertArgs d = a;

@@ -392,8 +392,7 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
             TRY(c, kq_one(c, lf[1], L->sh_gate, c->xq.p, c->xd.p, n, E, H, c->ksg.p));
             TRY(c, kq_one(c, lf[2], L->sh_up, c->xq.p, c->xd.p, n, E, H, c->ksu.p));
         }
-        TRY(c, launch_swiglu(c->ksg.p, c->ksu.p, (int64_t) n * H, c->h.p + (size_t) P * H, st));
-        TRY(c, launch_quant_q8k(c->h.p + (size_t) P * H, n, H, c->hq.p + (size_t) P * H, c->hd.p + (size_t) P * (H / 256), st));
+        TRY(c, launch_swiglu_q8k(c->ksg.p, c->ksu.p, n, H, c->h.p + (size_t) P * H, c->hq.p + (size_t) P * H, c->hd.p + (size_t) P * (H / 256), st));
         if (c->dbg_gu) {
             TRY(c, hipMemcpyAsync(c->g.p + (size_t) P * H, c->ksg.p, (size_t) n * H * 4, hipMemcpyDeviceToDevice, st));
             TRY(c, hipMemcpyAsync(c->u.p + (size_t) P * H, c->ksu.p, (size_t) n * H * 4, hipMemcpyDeviceToDevice, st));

@@ -251,16 +251,26 @@ extern "C" int fl_gguf_read(const FLGguf * g, const FLGgufTensor * t, uint64_t o
 }
 
 // ---------------------------------------------------------------- one MoE layer resident in HBM
-// file bytes of a tensor -> device memory, through two pinned staging buffers (the read of one chunk overlaps the copy
-// of the previous one)
-static int upload(FLCtx * c, const FLGguf * g, const FLGgufTensor & t, uint8_t * dst) {
-    constexpr size_t CH = 32u << 20;
+// two pinned staging buffers and their events, allocated once per layer load
+struct Staging {
+    static constexpr size_t CH = 32u << 20;
     uint8_t * hb[2] = { nullptr, nullptr }; hipEvent_t ev[2] = { nullptr, nullptr };
-    int rc = FL_OK;
-    for (int k = 0; k < 2 && rc == FL_OK; ++k) {
-        if (hipHostMalloc((void **) &hb[k], CH, hipHostMallocDefault) != hipSuccess) { rc = fail(c, FL_ENOMEM, "pinned staging"); }
-        else if (hipEventCreateWithFlags(&ev[k], hipEventDisableTiming) != hipSuccess) { rc = fail(c, FL_EHIP, "event"); }
+    int init(FLCtx * c) {
+        for (int k = 0; k < 2; ++k) {
+            if (hipHostMalloc((void **) &hb[k], CH, hipHostMallocDefault) != hipSuccess) { hb[k] = nullptr; return fail(c, FL_ENOMEM, "pinned staging"); }
+            if (hipEventCreateWithFlags(&ev[k], hipEventDisableTiming) != hipSuccess) { ev[k] = nullptr; return fail(c, FL_EHIP, "event"); }
+        }
+        return FL_OK;
     }
+    ~Staging() { for (int k = 0; k < 2; ++k) { if (ev[k]) { (void) hipEventDestroy(ev[k]); } if (hb[k]) { (void) hipHostFree(hb[k]); } } }
+};
+
+// file bytes of a tensor -> device memory through the staging buffers (the read of one chunk overlaps the copy of the
+// previous one); waits for its copies before returning
+static int upload(FLCtx * c, const FLGguf * g, Staging & sg, const FLGgufTensor & t, uint8_t * dst) {
+    constexpr size_t CH = Staging::CH;
+    uint8_t * const * hb = sg.hb; hipEvent_t * ev = sg.ev;
+    int rc = FL_OK;
     for (uint64_t off = 0, k = 0; rc == FL_OK && off < t.nbytes; off += CH, ++k) {
         const size_t n = (size_t) std::min<uint64_t>(CH, t.nbytes - off);
         const int b = (int) (k & 1);
@@ -271,7 +281,6 @@ static int upload(FLCtx * c, const FLGguf * g, const FLGgufTensor & t, uint8_t *
         }
     }
     if (hipStreamSynchronize(c->st) != hipSuccess && rc == FL_OK) { rc = fail(c, FL_EHIP, "upload sync"); }
-    for (int k = 0; k < 2; ++k) { if (ev[k]) { (void) hipEventDestroy(ev[k]); } if (hb[k]) { (void) hipHostFree(hb[k]); } }
     return rc;
 }
 
@@ -328,30 +337,31 @@ extern "C" int fl_gguf_load_moe_layer(FLCtx * c, const FLGguf * g, int layer, in
             if (fm[3 + k] == FL_IQ2) { stage_sz = std::max(stage_sz, ts[k].nbytes); }
         }
     }
-    int rc = FL_OK;
-    if (stage_sz && hipMalloc((void **) &stage, stage_sz) != hipSuccess) { (void) hipGetLastError(); rc = fail(c, FL_ENOMEM, "staging allocation"); }
+    Staging sg;
+    int rc = sg.init(c);
+    if (rc == FL_OK && stage_sz && hipMalloc((void **) &stage, stage_sz) != hipSuccess) { (void) hipGetLastError(); rc = fail(c, FL_ENOMEM, "staging allocation"); }
     if (rc == FL_OK) {
         if (r16) {
-            rc = upload(c, g, tr, stage);
+            rc = upload(c, g, sg, tr, stage);
             if (rc == FL_OK && launch_f16_to_f32((const uint16_t *) stage, (float *) (mem + off[0]), E * ne, c->st) != hipSuccess) { rc = fail(c, FL_EHIP, "router widening"); }
         } else {
-            rc = upload(c, g, tr, mem + off[0]);
+            rc = upload(c, g, sg, tr, mem + off[0]);
         }
     }
-    if (rc == FL_OK) { rc = upload(c, g, tb, mem + off[1]); }
-    if (rc == FL_OK && has_norm) { rc = upload(c, g, tn, mem + off[2]); }
+    if (rc == FL_OK) { rc = upload(c, g, sg, tb, mem + off[1]); }
+    if (rc == FL_OK && has_norm) { rc = upload(c, g, sg, tn, mem + off[2]); }
     const FLGgufTensor * mats[6] = { &te[0], &te[1], &te[2], &ts[0], &ts[1], &ts[2] };
     for (int k = 0; k < 6 && rc == FL_OK; ++k) {
         uint8_t * dst = mem + off[3 + k];
         const FLGgufTensor & t = *mats[k];
         if (layout == FL_LAYOUT_TILED && fm[k] == FL_IQ2) {   // K-quant matrices stay as stored in either layout
-            rc = upload(c, g, t, stage);
+            rc = upload(c, g, sg, t, stage);
             const int R = (int) t.ne[1], K = (int) t.ne[0], nm = (int) t.ne[2];
             const size_t ms = (size_t) t.row_bytes * (size_t) R;
             if (rc == FL_OK && launch_pack_tiled(stage, ms, dst, ms, R, K, nm, c->st) != hipSuccess) { rc = fail(c, FL_EHIP, "tiled packing"); }
             if (rc == FL_OK && hipStreamSynchronize(c->st) != hipSuccess) { rc = fail(c, FL_EHIP, "packing sync"); }
         } else {
-            rc = upload(c, g, t, dst);
+            rc = upload(c, g, sg, t, dst);
         }
     }
     if (stage) { (void) hipStreamSynchronize(c->st); (void) hipFree(stage); }

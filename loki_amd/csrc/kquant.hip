@@ -16,7 +16,7 @@
 // Q8_K columns held in registers). Lane = (block, column slice of 32 weights); a row's blocks are split over 1-4 waves (8 blocks per
 // wave), the remaining waves take other rows of the tile. The next row's bytes are loaded while the current one is
 // computed. Each block's fp32 term goes to LDS; one lane per (row, token) then adds them in block order.
-#include "moe_common.h"
+#include "moe_device.h"
 #include "moe_kernels.h"
 
 #include <algorithm>
@@ -373,6 +373,31 @@ __global__ void k_swiglu(const float * __restrict__ g, const float * __restrict_
 hipError_t launch_swiglu(const float * g, const float * u, int64_t n, float * h, hipStream_t st) {
     if (n <= 0) { return hipSuccess; }
     k_swiglu<<<(unsigned) ((n + 255) / 256), 256, 0, st>>>(g, u, n, h);
+    return hipGetLastError();
+}
+
+// the same h, and its Q8_K (ggml's quantize_row_q8_K: q8k_lane over one 256-value block per wave, 4 values per lane in
+// element order), in one pass
+__global__ void __launch_bounds__(256) k_swiglu_q8k(const float * __restrict__ g, const float * __restrict__ u, int64_t nblk,
+                                                    float * __restrict__ h, int8_t * __restrict__ q, float * __restrict__ d) {
+#pragma clang fp contract(off)
+    const int64_t b = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= nblk) { return; }
+    const int lane = threadIdx.x & 63;
+    const int64_t i0 = b * QK + 4 * lane;
+    const float4 gv = *reinterpret_cast<const float4 *>(g + i0), uv = *reinterpret_cast<const float4 *>(u + i0);
+    const float xs[4] = { det_silu(gv.x) * uv.x, det_silu(gv.y) * uv.y, det_silu(gv.z) * uv.z, det_silu(gv.w) * uv.w };
+    *reinterpret_cast<float4 *>(h + i0) = make_float4(xs[0], xs[1], xs[2], xs[3]);
+    float dq;
+    const uint32_t packed = q8k_lane(xs, dq);
+    *reinterpret_cast<uint32_t *>(q + i0) = packed;
+    if (lane == 0) { d[b] = dq; }
+}
+hipError_t launch_swiglu_q8k(const float * g, const float * u, int64_t nrows, int K, float * h, int8_t * q, float * d, hipStream_t st) {
+    if (nrows <= 0) { return hipSuccess; }
+    if (K <= 0 || K % QK) { return hipErrorInvalidValue; }
+    const int64_t nblk = nrows * (K / QK);
+    k_swiglu_q8k<<<(unsigned) ((nblk + 3) / 4), 256, 0, st>>>(g, u, nblk, h, q, d);
     return hipGetLastError();
 }
 

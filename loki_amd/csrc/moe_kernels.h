@@ -130,6 +130,8 @@ int kq_block_bytes(int fmt);
 hipError_t launch_kq_matvec(const KqArgs & a, int fmt, int max_slots, int grid_experts, hipStream_t st);
 // h = silu(g) * u, element-wise under the exp contract
 hipError_t launch_swiglu(const float * g, const float * u, int64_t n, float * h, hipStream_t st);
+// the same h for nrows rows of K (K % 256 == 0) and its Q8_K (q [nrows][K], d [nrows][K/256]) in one pass
+hipError_t launch_swiglu_q8k(const float * g, const float * u, int64_t nrows, int K, float * h, int8_t * q, float * d, hipStream_t st);
 
 // ggml rms_norm (fp64 sum of fp32 squares) then the weight (w may be null = ones); one block per row
 hipError_t launch_rmsnorm(const float * x, const float * w, float * y, int n, int D, float eps, hipStream_t st);
