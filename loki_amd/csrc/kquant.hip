@@ -40,6 +40,10 @@ struct Src {
 };
 __device__ __forceinline__ uint32_t ld32(const Src & s, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(s.rs, s.vb + off, s.so, 0); }
 __device__ __forceinline__ uint32_t ld_u16(const Src & s, uint32_t off) { return (uint32_t) __builtin_amdgcn_raw_buffer_load_b16(s.rs, s.vb + off, s.so, 0); }
+// several consecutive 4-byte aligned words in one load (load instructions, not bytes, limit these kernels)
+typedef uint32_t u32v2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u32v2 ld64(const Src & s, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b64(s.rs, s.vb + off, s.so, 0); }
+__device__ __forceinline__ u32x4 ld128(const Src & s, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(s.rs, s.vb + off, s.so, 0); }
 
 __device__ __forceinline__ uint32_t byte_of3(uint32_t w0, uint32_t w1, uint32_t w2, int k) {
     const uint32_t w = k < 4 ? w0 : k < 8 ? w1 : w2;
@@ -57,13 +61,19 @@ template <> struct Raw<KF_Q5K> { uint32_t q[4], h, s[3], dd; };
 template <> struct Raw<KF_Q6K> { uint32_t qa[3], qb[3], h[3], sc[3], dd; uint32_t sha, shb, shh, shs; };
 
 // N + 1 aligned words covering N words at a 2-byte aligned offset (rows and the matrix start on 4-byte boundaries, so
-// the alignment is the lane's: block offset + field). Word N is needed only when the offset is not 4-aligned;
-// otherwise word N - 1 is read again in its place, so no word past the last needed byte is touched.
+// the alignment is the lane's: block offset + field), in one vector load. Word N is needed only when the offset is
+// not 4-aligned; past the matrix's last word the buffer load returns 0 instead of reading memory.
+typedef uint32_t u32v3 __attribute__((ext_vector_type(3)));
 template <int N> __device__ __forceinline__ uint32_t ld_aligned(const Src & s, uint32_t off, uint32_t (&t)[N + 1]) {
-    const uint32_t sh = (s.vb + off) & 3u, o = off - sh;
-#pragma unroll
-    for (int i = 0; i < N; ++i) { t[i] = ld32(s, o + 4 * i); }
-    t[N] = ld32(s, o + 4 * (sh ? N : N - 1));
+    static_assert(N == 2 || N == 3, "3- or 4-word windows");
+    const uint32_t sh = (s.vb + off) & 3u, o = s.vb + off - sh;
+    if constexpr (N == 2) {
+        const u32v3 v = __builtin_amdgcn_raw_buffer_load_b96(s.rs, o, s.so, 0);
+        t[0] = v.x; t[1] = v.y; t[2] = v.z;
+    } else {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(s.rs, o, s.so, 0);
+        t[0] = v.x; t[1] = v.y; t[2] = v.z; t[3] = v.w;
+    }
     return sh;
 }
 template <int N> __device__ __forceinline__ uint32_t realign(const uint32_t (&t)[N + 1], uint32_t sh, int i) {
@@ -73,8 +83,8 @@ template <int N> __device__ __forceinline__ uint32_t realign(const uint32_t (&t)
 template <int F> __device__ __forceinline__ void load_raw(const Src & b, int q, Raw<F> & r) {
     const uint32_t n = (uint32_t) q >> 2, jq = (uint32_t) q & 3u;
     if constexpr (F == KF_Q2K) {   // scales[16] qs[64] d dmin
-        const uint32_t qs = 16 + 32 * n + 8 * jq, sc = 8 * n;
-        r.q[0] = ld32(b, qs); r.q[1] = ld32(b, qs + 4); r.sc[0] = ld32(b, sc); r.sc[1] = ld32(b, sc + 4);
+        const u32v2 q2 = ld64(b, 16 + 32 * n + 8 * jq), s2 = ld64(b, 8 * n);
+        r.q[0] = q2.x; r.q[1] = q2.y; r.sc[0] = s2.x; r.sc[1] = s2.y;
         r.dd = ld32(b, 80);
     } else if constexpr (F == KF_Q3K) {   // hmask[32] qs[64] scales[12] d
         r.shq = ld_aligned<2>(b, 32 + 32 * n + 8 * jq, r.q); r.shh = ld_aligned<2>(b, 8 * jq, r.h);
@@ -83,7 +93,8 @@ template <int F> __device__ __forceinline__ void load_raw(const Src & b, int q, 
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) { r.q[j] = ld32(b, 48 + 32 * j + 4 * (uint32_t) q); }
         r.h = ld32(b, 16 + 4 * (uint32_t) q);
-        r.s[0] = ld32(b, 4); r.s[1] = ld32(b, 8); r.s[2] = ld32(b, 12); r.dd = ld32(b, 0);
+        const u32x4 h4 = ld128(b, 0);   // d dmin, scales[12]
+        r.dd = h4.x; r.s[0] = h4.y; r.s[1] = h4.z; r.s[2] = h4.w;
     } else {   // Q6_K: ql[128] qh[64] scales[16] d
         r.sha = ld_aligned<2>(b, 64 * n + 8 * jq, r.qa); r.shb = ld_aligned<2>(b, 64 * n + 32 + 8 * jq, r.qb);
         r.shh = ld_aligned<2>(b, 128 + 32 * n + 8 * jq, r.h); r.shs = ld_aligned<2>(b, 192 + 8 * n, r.sc);
@@ -118,13 +129,16 @@ template <int F> __device__ __forceinline__ void decode(const Raw<F> & r, int q,
             const int hb = 4 * n + s;
             k.u[2 * s] = ((q0 >> (2 * s)) & 0x03030303u) | (((h0 >> hb) & 0x01010101u) << 2);
             k.u[2 * s + 1] = ((q1 >> (2 * s)) & 0x03030303u) | (((h1 >> hb) & 0x01010101u) << 2);
-            // 6-bit scale j = 8 n + 2 s + hi16: low nibble of byte j % 8 (j < 8) or its high nibble (j >= 8), 2 high
-            // bits from byte 8 + j % 4 at bits 2 (j / 4)
-            const int j = 8 * n + 2 * s + hi16;
-            const uint32_t lo = ((((j & 4) ? a1 : a0) >> (8 * (j & 3))) >> ((j & 8) ? 4 : 0)) & 0xFu;
-            const uint32_t hh = (a2 >> (8 * (j & 3) + 2 * (j >> 2))) & 3u;
-            k.sc[s] = (int) (lo | (hh << 4)) - 32; k.mn[s] = 0;
         }
+        // 6-bit scale j = 8 n + 2 s + hi16: low nibble of byte j % 8 (nibble n), 2 high bits of byte 8 + j % 4 at
+        // bits 2 (j / 4). The lane's four scales sit in bytes hi16 and hi16 + 2: s = 0, 1 in a0 / a2, s = 2, 3 in a1 /
+        // a2 >> 2, so one shift per word puts each pair at bits 0 and 16.
+        const uint32_t sh = 8 * hi16 + 4 * n;
+        const uint32_t p01 = ((a0 >> sh) & 0x000F000Fu) | (((a2 >> sh) & 0x00030003u) << 4);
+        const uint32_t p23 = ((a1 >> sh) & 0x000F000Fu) | (((a2 >> (sh + 2)) & 0x00030003u) << 4);
+        k.sc[0] = (int) (p01 & 0xFFu) - 32; k.sc[1] = (int) (p01 >> 16) - 32;
+        k.sc[2] = (int) (p23 & 0xFFu) - 32; k.sc[3] = (int) (p23 >> 16) - 32;
+        k.mn[0] = k.mn[1] = k.mn[2] = k.mn[3] = 0;
         k.d = h2f((uint16_t) r.dd); k.dmin = 0.f;
     } else if constexpr (F == KF_Q5K) {   // weight 64 jj + 32 h + l: nibble h of qs[32 jj + l], bit 2 jj + h of qh[l]
 #pragma unroll
