@@ -52,12 +52,13 @@ __device__ __forceinline__ uint32_t byte_of3(uint32_t w0, uint32_t w1, uint32_t 
 
 // Lane slice q (0..7) of a block. 16-weight sub-block formats (Q2_K, Q3_K, Q6_K): n = q / 4 picks the block half,
 // jq = q % 4 the 8 columns l = 8 jq .. 8 jq + 7, taken in all four 32-weight rows s of the half: piece s = weights
-// 128 n + 32 s + l (one sub-block, 2 words). Q5_K (32-weight sub-blocks): columns l = 4 q .. 4 q + 3 of all 8
-// sub-blocks: piece j = weights 32 j + l (1 word). So each lane reads only the bytes of its own columns.
+// 128 n + 32 s + l (one sub-block, 2 words). Q5_K (32-weight sub-blocks, 64-weight quant groups jj): jj = q / 2,
+// columns l = 16 (q % 2) .. + 15 of both halves h of the group: piece h = weights 64 jj + 32 h + l (sub-block 2 jj + h,
+// 4 words). So each lane reads only the bytes of its own columns, 16 contiguous bytes per field.
 template <int F> struct Raw;
 template <> struct Raw<KF_Q2K> { uint32_t q[2], sc[2], dd; };
 template <> struct Raw<KF_Q3K> { uint32_t q[3], h[3], s[4], dd; uint32_t shq, shh, shs; };
-template <> struct Raw<KF_Q5K> { uint32_t q[4], h, s[3], dd; };
+template <> struct Raw<KF_Q5K> { uint32_t q[4], h[4], s[3], dd; };
 template <> struct Raw<KF_Q6K> { uint32_t qa[3], qb[3], h[3], sc[3], dd; uint32_t sha, shb, shh, shs; };
 
 // N + 1 aligned words covering N words at a 2-byte aligned offset (rows and the matrix start on 4-byte boundaries, so
@@ -90,11 +91,11 @@ template <int F> __device__ __forceinline__ void load_raw(const Src & b, int q, 
         r.shq = ld_aligned<2>(b, 32 + 32 * n + 8 * jq, r.q); r.shh = ld_aligned<2>(b, 8 * jq, r.h);
         r.shs = ld_aligned<3>(b, 96, r.s); r.dd = ld_u16(b, 108);
     } else if constexpr (F == KF_Q5K) {   // d dmin scales[12] qh[32] qs[128]
-#pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) { r.q[j] = ld32(b, 48 + 32 * j + 4 * (uint32_t) q); }
-        r.h = ld32(b, 16 + 4 * (uint32_t) q);
-        const u32x4 h4 = ld128(b, 0);   // d dmin, scales[12]
-        r.dd = h4.x; r.s[0] = h4.y; r.s[1] = h4.z; r.s[2] = h4.w;
+        const uint32_t jj = (uint32_t) q >> 1, hf = (uint32_t) q & 1u;
+        const u32x4 q4 = ld128(b, 48 + 32 * jj + 16 * hf), h4 = ld128(b, 16 + 16 * hf), hd = ld128(b, 0);   // qs, qh, d dmin scales
+        r.q[0] = q4.x; r.q[1] = q4.y; r.q[2] = q4.z; r.q[3] = q4.w;
+        r.h[0] = h4.x; r.h[1] = h4.y; r.h[2] = h4.z; r.h[3] = h4.w;
+        r.dd = hd.x; r.s[0] = hd.y; r.s[1] = hd.z; r.s[2] = hd.w;
     } else {   // Q6_K: ql[128] qh[64] scales[16] d
         r.sha = ld_aligned<2>(b, 64 * n + 8 * jq, r.qa); r.shb = ld_aligned<2>(b, 64 * n + 32 + 8 * jq, r.qb);
         r.shh = ld_aligned<2>(b, 128 + 32 * n + 8 * jq, r.h); r.shs = ld_aligned<2>(b, 192 + 8 * n, r.sc);
@@ -103,7 +104,7 @@ template <int F> __device__ __forceinline__ void load_raw(const Src & b, int q, 
 }
 
 // decoded slice: u = unsigned quants (4 per word); piece p's scale sc[p] and min mn[p] (pieces: 4 of 2 words for the
-// 16-weight formats, 8 of 1 word for Q5_K)
+// 16-weight formats, 2 of 4 words for Q5_K)
 struct Chunk {
     uint32_t u[8];
     int sc[8], mn[8];
@@ -141,21 +142,20 @@ template <int F> __device__ __forceinline__ void decode(const Raw<F> & r, int q,
         k.mn[0] = k.mn[1] = k.mn[2] = k.mn[3] = 0;
         k.d = h2f((uint16_t) r.dd); k.dmin = 0.f;
     } else if constexpr (F == KF_Q5K) {   // weight 64 jj + 32 h + l: nibble h of qs[32 jj + l], bit 2 jj + h of qh[l]
+        const int jj = q >> 1;
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
+        for (int h = 0; h < 2; ++h) {
+            const int j = 2 * jj + h;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int j = 2 * jj + h;
-                k.u[j] = ((r.q[jj] >> (4 * h)) & 0x0F0F0F0Fu) | (((r.h >> j) & 0x01010101u) << 4);
-                int sv, mv;
-                if (j < 4) { sv = (int) (byte_of3(r.s[0], r.s[1], r.s[2], j) & 63u); mv = (int) (byte_of3(r.s[0], r.s[1], r.s[2], j + 4) & 63u); }
-                else {
-                    const uint32_t b8 = byte_of3(r.s[0], r.s[1], r.s[2], j + 4);
-                    sv = (int) ((b8 & 0xFu) | ((byte_of3(r.s[0], r.s[1], r.s[2], j - 4) >> 6) << 4));
-                    mv = (int) ((b8 >> 4) | ((byte_of3(r.s[0], r.s[1], r.s[2], j) >> 6) << 4));
-                }
-                k.sc[j] = sv; k.mn[j] = mv;
+            for (int i = 0; i < 4; ++i) { k.u[4 * h + i] = ((r.q[i] >> (4 * h)) & 0x0F0F0F0Fu) | (((r.h[i] >> j) & 0x01010101u) << 4); }
+            int sv, mv;
+            if (j < 4) { sv = (int) (byte_of3(r.s[0], r.s[1], r.s[2], j) & 63u); mv = (int) (byte_of3(r.s[0], r.s[1], r.s[2], j + 4) & 63u); }
+            else {
+                const uint32_t b8 = byte_of3(r.s[0], r.s[1], r.s[2], j + 4);
+                sv = (int) ((b8 & 0xFu) | ((byte_of3(r.s[0], r.s[1], r.s[2], j - 4) >> 6) << 4));
+                mv = (int) ((b8 >> 4) | ((byte_of3(r.s[0], r.s[1], r.s[2], j) >> 6) << 4));
             }
+            k.sc[h] = sv; k.mn[h] = mv;
         }
         k.d = h2f((uint16_t) (r.dd & 0xFFFFu)); k.dmin = h2f((uint16_t) (r.dd >> 16));
     } else {   // Q6_K: weight 128 n + 32 p + l: nibble p / 2 of ql[64 n + 32 (p % 2) + l], bits 2 p of qh[32 n + l], - 32
@@ -181,11 +181,18 @@ struct XChunk { uint32_t x[8]; int bx[8]; float d8; };
 template <int F> __device__ __forceinline__ void load_x(const int8_t * xb, int q, XChunk & x) {
     const uint32_t ones = 0x01010101u;
     if constexpr (F == KF_Q5K) {
+        const int jj = q >> 1, hf = q & 1;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            x.x[j] = *reinterpret_cast<const uint32_t *>(xb + 32 * j + 4 * q);
-            x.bx[j] = __builtin_amdgcn_sdot4((int) x.x[j], (int) ones, 0, false);
+        for (int h = 0; h < 2; ++h) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(xb + 64 * jj + 32 * h + 16 * hf);
+            x.x[4 * h] = v.x; x.x[4 * h + 1] = v.y; x.x[4 * h + 2] = v.z; x.x[4 * h + 3] = v.w;
+            int sm = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { sm = __builtin_amdgcn_sdot4((int) x.x[4 * h + i], (int) ones, sm, false); }
+            x.bx[h] = sm;
         }
+#pragma unroll
+        for (int h = 2; h < 8; ++h) { x.bx[h] = 0; }
     } else {
         const int n = q >> 2, jq = q & 3;
 #pragma unroll
@@ -204,9 +211,12 @@ template <int F> __device__ __forceinline__ void chunk_dot(const Chunk & k, cons
     isum = 0; summ = 0;
     if constexpr (F == KF_Q5K) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            isum += __mul24(k.sc[j], __builtin_amdgcn_sdot4((int) k.u[j], (int) x.x[j], 0, false));
-            summ += __mul24(k.mn[j], x.bx[j]);
+        for (int h = 0; h < 2; ++h) {
+            int dp = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { dp = __builtin_amdgcn_sdot4((int) k.u[4 * h + i], (int) x.x[4 * h + i], dp, false); }
+            isum += __mul24(k.sc[h], dp);
+            summ += __mul24(k.mn[h], x.bx[h]);
         }
     } else {
 #pragma unroll
