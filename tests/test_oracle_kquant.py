@@ -121,3 +121,40 @@ def test_dot_matches_fp64_brute_force(fmt):
     w2 = random_blocks(fmt, 3 * K // 256, rng).reshape(3, -1)
     y = orc.matvec_kq(fmt, w2, 3, K, q.reshape(1, -1), d.reshape(1, -1), bs.reshape(1, -1))
     assert np.array_equal(y[0].view(np.uint32), np.array([orc.vec_dot_kq(fmt, w2[r], q, d, bs) for r in range(3)], np.float32).view(np.uint32))
+
+
+def test_expert_composition_per_format():
+    """or_moe_experts_fmt: IQ2_XXS everywhere equals the original composition bit for bit; with K-quant formats each
+    matrix is read in its own format and row stride: the shared expert equals matvec_kq(gate / up) -> silu * u -> Q8_K
+    -> matvec_kq(down), and the routed outputs use the down format (E, H scaled down to keep the check quick)."""
+    from tests.golden import gen
+    E, H, n, topk, n_exp = 512, 256, 2, 2, 4
+    rng = np.random.default_rng(7)
+    x = rng.normal(0, 1, (n, E)).astype(np.float32)
+    sel = np.array([[0, 2], [3, 0]], np.int32); wts = np.array([[0.7, 0.3], [0.6, 0.4]], np.float32)
+    gate = [gen.iq2_matrix(3, e, H, E) for e in range(n_exp)]
+    up = [gen.iq2_matrix(4, e, H, E) for e in range(n_exp)]
+    down_iq2 = [gen.iq2_matrix(5, e, E, H) for e in range(n_exp)]
+    sh_iq2 = (gen.iq2_matrix(6, 0, H, E), gen.iq2_matrix(6, 1, H, E), gen.iq2_matrix(6, 2, E, H))
+    a = orc.moe_experts(x, sel, wts, gate, up, down_iq2, *sh_iq2, H=H, n_exp=n_exp, want=("o", "sh"))
+    b = orc.moe_experts(x, sel, wts, gate, up, down_iq2, *sh_iq2, H=H, n_exp=n_exp, want=("o", "sh"), fmts=(4, 4, 4, 4))
+    assert all(np.array_equal(a[k].view(np.uint32), b[k].view(np.uint32)) for k in ("y", "o", "sh"))
+    # K-quants: Q3_K routed down, Q5_K / Q5_K / Q6_K shared
+    down = [gen.kq_matrix(7, e, orc.Q3K, E, H) for e in range(n_exp)]
+    ksh = (gen.kq_matrix(8, 0, orc.Q5K, H, E), gen.kq_matrix(8, 1, orc.Q5K, H, E), gen.kq_matrix(8, 2, orc.Q6K, E, H))
+    r = orc.moe_experts(x, sel, wts, gate, up, down, *ksh, H=H, n_exp=n_exp, want=("o", "sh"), fmts=(orc.Q3K, orc.Q5K, orc.Q5K, orc.Q6K))
+    q, d, bs = orc.quantize_q8k(x)
+    g = orc.matvec_kq(orc.Q5K, ksh[0], H, E, q, d, bs); u = orc.matvec_kq(orc.Q5K, ksh[1], H, E, q, d, bs)
+    h = (orc.silu(g).reshape(g.shape) * u).astype(np.float32)
+    hq, hd, hb = orc.quantize_q8k(h)
+    sh = orc.matvec_kq(orc.Q6K, ksh[2], E, H, hq, hd, hb)
+    assert np.array_equal(r["sh"].view(np.uint32), sh.view(np.uint32))
+    # a routed output: token 1, k = 0 (expert 3) -> its h from the IQ2_XXS gate/up (the IQ2 run's o of the same pair
+    # differs only by the down format), through the Q3_K down
+    o_iq2 = b["o"].reshape(n, topk, E)[1, 0]
+    o_q3 = r["o"].reshape(n, topk, E)[1, 0]
+    assert not np.array_equal(o_iq2, o_q3)
+    gi = orc.matvec(gate[3], H, E, q[1], d[1]); ui = orc.matvec(up[3], H, E, q[1], d[1])
+    hi = (orc.silu(gi) * ui).astype(np.float32)
+    hiq, hid, hib = orc.quantize_q8k(hi.reshape(1, -1))
+    assert np.array_equal(o_q3.view(np.uint32), orc.matvec_kq(orc.Q3K, down[3], E, H, hiq, hid, hib)[0].view(np.uint32))
