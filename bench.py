@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """bench.py -- one DeepSeek-R1 MoE layer (loki's fused_layer MoE block) on one MI355X.
 
-Default workload (the BASELINE metric's decode config): one MoE layer decoding a batch of 8 tokens:
+Default workload (the headline metric's decode config): one MoE layer decoding a batch of 8 tokens:
 x [8, 7168] ~ N(0,1), fp32 router [256, 7168] ~ N(0, 0.02^2), bias ~ N(0, 0.01^2), grouped sigmoid routing
 (8 groups, top-4 groups, top-8, x2.5), 256 routed + 1 shared IQ2_XXS experts (gate/up [2048, 7168], down [7168, 2048],
 qs uniform bytes, d = fp16(|N(0, 0.002^2)|)). All inputs are generated on the device and resident in HBM before the
@@ -372,7 +372,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (device-generated, seeded; BASELINE.json configs distribution)",
+        "data": "synthetic (device-generated, seeded; the benchmark configs' distribution)",
         "config": {"workload": res["desc"], "tokens": n, "hidden": E, "expert_ffn": H, "routed_experts": 256,
                    "shared_experts": 1, "routing": "sigmoid, 8 groups, top-4 groups, top-8, x2.5",
                    "weights": "IQ2_XXS (activations Q8_K)", "layer_copies": args.copies},
