@@ -31,6 +31,53 @@ __global__ void __launch_bounds__(64) k_router_logits(const float * __restrict__
     }
 }
 
+// Small batches (K = 7168, n < 16): one workgroup (4 waves) per expert; thread c owns chunk c (28 values) of every
+// token and keeps its 28 weights in registers. Per token the chunk sum runs in element order with v_fma_f64 (exact
+// products, one rounding each), tree levels 1-6 are lane butterflies inside the wave (chunks 64 q .. 64 q + 63 of wave
+// q), and levels 7-8 add the four waves' totals as (q0 + q1) + (q2 + q3) through LDS. Four tokens per pass.
+constexpr int RW_MAXN = 16;
+__global__ void __launch_bounds__(256) k_router_wg(const float * __restrict__ W, const float * __restrict__ x, int n, int n_exp,
+                                                   float * __restrict__ logits) {
+#pragma clang fp contract(off)
+    constexpr int CL = 28;
+    __shared__ double part[RW_MAXN][4];
+    const int e = blockIdx.x, c = threadIdx.x, q = c >> 6, lane = c & 63;
+    float wv[CL];
+#pragma unroll
+    for (int i = 0; i < CL / 4; ++i) {
+        const float4 v = gloadf4(W + (size_t) e * 7168 + CL * c + 4 * i);
+        wv[4 * i] = v.x; wv[4 * i + 1] = v.y; wv[4 * i + 2] = v.z; wv[4 * i + 3] = v.w;
+    }
+    for (int t0 = 0; t0 < n; t0 += 4) {
+        double sv[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            sv[k] = 0.0;
+            if (t0 + k < n) {
+                const float * xr = x + (size_t) (t0 + k) * 7168 + CL * c;
+#pragma unroll
+                for (int i = 0; i < CL / 4; ++i) {
+                    const float4 v = gloadf4(xr + 4 * i);
+                    const float xv[4] = { v.x, v.y, v.z, v.w };
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) { sv[k] = __builtin_fma((double) xv[j], (double) wv[4 * i + j], sv[k]); }
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) { sv[k] = sv[k] + __shfl_xor(sv[k], o); }
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) { if (t0 + k < n) { part[t0 + k][q] = sv[k]; } }
+        }
+    }
+    __syncthreads();
+    if (c < n) { logits[(size_t) c * n_exp + e] = (float) ((part[c][0] + part[c][1]) + (part[c][2] + part[c][3])); }
+}
+
 // Batches (K = 7168): lane 8 t + e owns the logits of tokens t and t + 8 of the workgroup's 16-token tile with expert e
 // of its 8-expert tile; wave q of the workgroup computes the contract's quarter q (chunks 64 q .. 64 q + 63) in
 // registers: each chunk's 28 products summed in element order with v_fma_f64 (the fp32 x fp32 product is exact in
@@ -229,6 +276,10 @@ hipError_t launch_router_logits(const float * W, const float * x, int n, int n_e
     }
     if (K == 7168 && n >= 16) {
         k_router_gemm<<<dim3((n_exp + 7) / 8, (n + 15) / 16), 256, 0, st>>>(W, x, n, n_exp, logits);
+        return hipGetLastError();
+    }
+    if (K == 7168) {   // n < 16
+        k_router_wg<<<dim3(n_exp), 256, 0, st>>>(W, x, n, n_exp, logits);
         return hipGetLastError();
     }
     k_router_logits<<<dim3(n_exp, (n + RT - 1) / RT), 64, 0, st>>>(W, x, n, n_exp, K, logits);
