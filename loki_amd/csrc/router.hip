@@ -31,11 +31,11 @@ __global__ void __launch_bounds__(64) k_router_logits(const float * __restrict__
     }
 }
 
-// Small batches (K = 7168, n < 16): one workgroup (4 waves) per expert; thread c owns chunk c (28 values) of every
+// Batches below 256 tokens (K = 7168): one workgroup (4 waves) per expert; thread c owns chunk c (28 values) of every
 // token and keeps its 28 weights in registers. Per token the chunk sum runs in element order with v_fma_f64 (exact
 // products, one rounding each), tree levels 1-6 are lane butterflies inside the wave (chunks 64 q .. 64 q + 63 of wave
 // q), and levels 7-8 add the four waves' totals as (q0 + q1) + (q2 + q3) through LDS. Four tokens per pass.
-constexpr int RW_MAXN = 16;
+constexpr int RW_MAXN = 256;
 __global__ void __launch_bounds__(256) k_router_wg(const float * __restrict__ W, const float * __restrict__ x, int n, int n_exp,
                                                    float * __restrict__ logits) {
 #pragma clang fp contract(off)
@@ -78,68 +78,10 @@ __global__ void __launch_bounds__(256) k_router_wg(const float * __restrict__ W,
     if (c < n) { logits[(size_t) c * n_exp + e] = (float) ((part[c][0] + part[c][1]) + (part[c][2] + part[c][3])); }
 }
 
-// Batches (K = 7168): lane 8 t + e owns the logits of tokens t and t + 8 of the workgroup's 16-token tile with expert e
-// of its 8-expert tile; wave q of the workgroup computes the contract's quarter q (chunks 64 q .. 64 q + 63) in
-// registers: each chunk's 28 products summed in element order with v_fma_f64 (the fp32 x fp32 product is exact in
-// fp64, so fma(x, w, s) is s + x * w rounded once), the pairwise tree built as it goes (levels 1-4 by recursion inside
-// a 16-chunk group, 5-6 across the quarter's four groups). Wave 0 then adds the quarters as (q0 + q1) + (q2 + q3)
-// (levels 7-8) through LDS.
-struct RgPair { double a, b; };   // the lane's two logits (tokens t, t + 8)
-template <int L>
-__device__ __forceinline__ RgPair rg_tree(const float * xa, const float * xb, const float * wr, int c0) {
-#pragma clang fp contract(off)
-    if constexpr (L == 0) {
-        constexpr int CL = 28;
-        RgPair s{0.0, 0.0};
-#pragma unroll
-        for (int i = 0; i < CL / 4; ++i) {
-            const float4 wv = gloadf4(wr + CL * c0 + 4 * i), av = gloadf4(xa + CL * c0 + 4 * i), bv = gloadf4(xb + CL * c0 + 4 * i);
-            const float w4[4] = { wv.x, wv.y, wv.z, wv.w }, a4[4] = { av.x, av.y, av.z, av.w }, b4[4] = { bv.x, bv.y, bv.z, bv.w };
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const double wd = (double) w4[q];
-                s.a = __builtin_fma((double) a4[q], wd, s.a);
-                s.b = __builtin_fma((double) b4[q], wd, s.b);
-            }
-        }
-        return s;
-    } else {
-        const RgPair l = rg_tree<L - 1>(xa, xb, wr, c0), r = rg_tree<L - 1>(xa, xb, wr, c0 + (1 << (L - 1)));
-        return RgPair{ l.a + r.a, l.b + r.b };
-    }
-}
-__global__ void __launch_bounds__(256) k_router_gemm(const float * __restrict__ W, const float * __restrict__ x, int n, int n_exp,
-                                                   float * __restrict__ logits) {
-#pragma clang fp contract(off)
-    constexpr int K = 7168;
-    __shared__ double part[4][2][64];
-    const int q = threadIdx.x >> 6, lane = lane_id();
-    const int t = blockIdx.y * 16 + (lane >> 3), e = blockIdx.x * 8 + (lane & 7);
-    const float * xa = x + (size_t) (t < n ? t : 0) * K, * xb = x + (size_t) (t + 8 < n ? t + 8 : 0) * K;
-    const float * wr = W + (size_t) (e < n_exp ? e : 0) * K;
-    RgPair l4{0.0, 0.0}, l5{0.0, 0.0}, tot{0.0, 0.0};
-#pragma unroll 1
-    for (int g = 0; g < 4; ++g) {   // the quarter's 16-chunk groups: a level-4 node each; levels 5-6 by g's bits
-        RgPair v = rg_tree<4>(xa, xb, wr, 64 * q + 16 * g);
-        if (!(g & 1)) { l4 = v; continue; }
-        v = RgPair{ l4.a + v.a, l4.b + v.b };
-        if (!(g & 2)) { l5 = v; continue; }
-        tot = RgPair{ l5.a + v.a, l5.b + v.b };
-    }
-    part[q][0][lane] = tot.a; part[q][1][lane] = tot.b;
-    __syncthreads();
-    if (q == 0 && e < n_exp) {
-        const double a = (part[0][0][lane] + part[1][0][lane]) + (part[2][0][lane] + part[3][0][lane]);
-        const double b = (part[0][1][lane] + part[1][1][lane]) + (part[2][1][lane] + part[3][1][lane]);
-        if (t < n) { logits[(size_t) t * n_exp + e] = (float) a; }
-        if (t + 8 < n) { logits[(size_t) (t + 8) * n_exp + e] = (float) b; }
-    }
-}
-
 // Large batches (K = 7168): register tiles. Lane (tg, eg) = (lane / 8, lane % 8) owns the logits of TT tokens x EE
 // experts of the workgroup's (8 TT) x (8 EE) tile; wave q computes slice q of the contract (chunks q * 256 / NQ ..) with the
-// same in-order fp64 chunk sums and pairwise tree as above, and the slices are combined by the tree's top levels through
-// LDS. Each 16-byte load of x or W now feeds EE or TT fused multiply-adds (the kernel above: 2 or 1).
+// same in-order fp64 chunk sums and pairwise tree as k_router_wg, and the slices are combined by the tree's top levels
+// through LDS. Each 16-byte load of x or W feeds EE or TT fused multiply-adds, so x and W are read once per tile.
 template <int TT, int EE> struct RgAcc { double v[TT][EE]; };
 // one chunk's in-order sums (28 products each) for the lane's TT x EE logits; the loads of step i + 1 are in flight
 // while step i computes, and nothing is hoisted further (register budget)
@@ -266,19 +208,17 @@ __global__ void __launch_bounds__(64 * NQ) k_router_tile(const float * __restric
 hipError_t launch_router_logits(const float * W, const float * x, int n, int n_exp, int K, float * logits, hipStream_t st) {
     if (n <= 0) { return hipSuccess; }
     if (K % 1024 != 0) { return hipErrorInvalidValue; }
-    if (K == 7168 && n >= 1024) {   // 32 x 32 tiles (4 x 4 per lane): enough workgroups from 1024 tokens on
+    // measured on MI355X: k_router_wg costs ~0.6 us per token (every workgroup reads all of x), the 4 x 2 tiles a flat
+    // ~150 us from 64 to 512 tokens; the crossover is near 256
+    if (K == 7168 && n >= 1024) {   // 32 x 32 tiles (4 x 4 per lane)
         k_router_tile<4, 4, 4><<<dim3((n_exp + 31) / 32, (n + 31) / 32), 256, 0, st>>>(W, x, n, n_exp, logits);
         return hipGetLastError();
     }
-    if (K == 7168 && n >= 64) {     // 32 x 16 tiles (4 x 2 per lane)
+    if (K == 7168 && n >= RW_MAXN) {   // 32 x 16 tiles (4 x 2 per lane)
         k_router_tile<4, 2, 4><<<dim3((n_exp + 15) / 16, (n + 31) / 32), 256, 0, st>>>(W, x, n, n_exp, logits);
         return hipGetLastError();
     }
-    if (K == 7168 && n >= 16) {
-        k_router_gemm<<<dim3((n_exp + 7) / 8, (n + 15) / 16), 256, 0, st>>>(W, x, n, n_exp, logits);
-        return hipGetLastError();
-    }
-    if (K == 7168) {   // n < 16
+    if (K == 7168) {
         k_router_wg<<<dim3(n_exp), 256, 0, st>>>(W, x, n, n_exp, logits);
         return hipGetLastError();
     }

@@ -67,7 +67,7 @@ def test_pack_layout(ctx):
 
 # n covers every logit kernel: per-wave (< 16), 16-token pairs (16..63), 32 x 16 tiles (64..1023) and 32 x 32 tiles
 # (>= 1024), with ragged last tiles
-@pytest.mark.parametrize("n,rule", [(1, (8, 4)), (8, (8, 4)), (21, (8, 4)), (64, (8, 4)), (77, (8, 4)), (1037, (8, 4)),
+@pytest.mark.parametrize("n,rule", [(1, (8, 4)), (8, (8, 4)), (21, (8, 4)), (64, (8, 4)), (77, (8, 4)), (300, (8, 4)), (1037, (8, 4)),
                                     (8, (1, 1))])
 def test_router_bitwise(ctx, layer, n, rule):
     x = make_x(ctx, n, seed=10 + n)
