@@ -1,8 +1,8 @@
 #!/usr/bin/env python3
 """bench.py -- one DeepSeek-R1 MoE layer (loki's fused_layer MoE block) on one MI355X.
 
-Default workload (the headline metric's decode config): one MoE layer decoding a batch of 8 tokens:
-x [8, 7168] ~ N(0,1), fp32 router [256, 7168] ~ N(0, 0.02^2), bias ~ N(0, 0.01^2), grouped sigmoid routing
+Default workload (the north star's target config, configs[0]): one MoE layer decoding 1 token:
+x [1, 7168] ~ N(0,1), fp32 router [256, 7168] ~ N(0, 0.02^2), bias ~ N(0, 0.01^2), grouped sigmoid routing
 (8 groups, top-4 groups, top-8, x2.5), 256 routed + 1 shared IQ2_XXS experts (gate/up [2048, 7168], down [7168, 2048],
 qs uniform bytes, d = fp16(|N(0, 0.002^2)|)). All inputs are generated on the device and resident in HBM before the
 timed region. Each step takes a fresh x (so different experts) and the steps rotate over --copies independently seeded
@@ -11,7 +11,10 @@ layers (3 x 2.9 GB), so the 256 MB MALL cannot serve repeated weights.
 Prints ONE JSON line: value = microseconds per token of the whole block (router, dispatch, experts, combine), plus the
 achieved HBM bandwidth, the roofline of the dominant kernel (decode: k_moe_decode, the whole block in one
 launch; prefill: the gate/up expert kernel), timed live with HIP events recorded on the stream the kernel runs on, and
-the CPU checker timed on this host's cores on a bounded sample of the same workload.
+the CPU checker timed on this host's cores on a bounded sample of every config. decode-8, prefill-512, prefill-2048,
+the 58-layer stack and the real-shard formats are reported under `extra`. Every timed loop ends with fl_sync: a
+device-side failure (a bounded wait of the decode block that timed out) makes the run exit non-zero instead of
+recording a fast invalid step.
 """
 import argparse
 import json
@@ -52,6 +55,27 @@ def gateup_bytes(n, U, topk=8):
     return 2 * (U + 1) * MAT_BYTES + n * (E + E // 256 * 4) + (P + n) * H * 4
 
 
+def routing_margins(probs, bias, n_group=8, topk_group=4, topk=8):
+    """How close the routing of these rows came to a tie: per row, the gap between the topk-th and the next eligible
+    biased score c = p + bias (inside the kept groups), and the gap between the topk_group-th and the next group score
+    (top1 + top2 of c per group). Returns the minimum of each over the rows (fp32, as the selection compares them)."""
+    import numpy as np
+    c = (np.asarray(probs, np.float32) + np.asarray(bias, np.float32)[None, :]).astype(np.float32)
+    n, ne = c.shape
+    per = ne // n_group
+    g = np.sort(c.reshape(n, n_group, per), axis=2)[:, :, ::-1]
+    gs = (g[:, :, 0] + g[:, :, 1]).astype(np.float32)
+    order = np.argsort(-gs, axis=1, kind="stable")
+    gsort = np.take_along_axis(gs, order, axis=1)
+    gmargin = gsort[:, topk_group - 1] - gsort[:, topk_group] if topk_group < n_group else np.full(n, np.inf)
+    keep = np.zeros((n, n_group), bool)
+    np.put_along_axis(keep, order[:, :topk_group], True, axis=1)
+    ce = np.where(np.repeat(keep, per, axis=1), c, -np.inf)
+    cs = -np.sort(-ce, axis=1)
+    kmargin = cs[:, topk - 1] - cs[:, topk]
+    return float(np.min(kmargin)), float(np.min(gmargin))
+
+
 def distinct_experts(ctx, layer, xs):
     """Number of distinct routed experts per x (routing recomputed outside the timed region)."""
     out = []
@@ -84,10 +108,13 @@ def run_workload(ctx, torch, name, steps, warmup, copies, seed=20260101):
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
+    h0 = time.perf_counter()
     for i in range(steps):
         ctx.moe_layer(layers[(warmup + i) % copies], xs[warmup + i], y)
+    host_us = (time.perf_counter() - h0) * 1e6 / steps
     end.record()
     torch.cuda.synchronize()
+    ctx.sync()   # a device-side failure in any timed step raises here
     ms = start.elapsed_time(end) / steps
     fused = bool(ctx.debug().fused)
     if fused:
@@ -102,10 +129,19 @@ def run_workload(ctx, torch, name, steps, warmup, copies, seed=20260101):
             ctx.moe_layer(layers[(warmup + i) % copies], xs[warmup + i], y)
         ctx.set_profile(False)
         calls, stage = ctx.stage_ms(reset=True)
+        ctx.sync()
         stage = {k: v / max(calls, 1) for k, v in stage.items()}
-    U = [distinct_experts(ctx, layers[(warmup + i) % copies], [xs[warmup + i]])[0] for i in range(steps)]
+    U, km, gm = [], [], []
+    for i in range(steps):
+        L = layers[(warmup + i) % copies]
+        _, probs, sel, _ = ctx.route(L.gate_inp, L.probs_b, xs[warmup + i])
+        U.append(int(sel.unique().numel()))
+        k, g = routing_margins(probs.cpu().numpy(), L.probs_b.cpu().numpy())
+        km.append(k); gm.append(g)
+    ctx.sync()
     mean_U = sum(U) / len(U)
-    res = dict(name=name, desc=desc, n=n, ms=ms, U=mean_U, stage_ms=stage, fused=fused,
+    res = dict(name=name, desc=desc, n=n, ms=ms, U=mean_U, stage_ms=stage, fused=fused, host_us=host_us,
+               margins={"topk_min": min(km), "group_min": min(gm)},
                bytes=sum(step_bytes(n, u) for u in U) / len(U),
                gu_bytes=sum(gateup_bytes(n, u) for u in U) / len(U))
     res["gbs"] = res["bytes"] / (ms * 1e-3) / 1e9
@@ -113,7 +149,7 @@ def run_workload(ctx, torch, name, steps, warmup, copies, seed=20260101):
     return res
 
 
-def run_stack(ctx, torch, steps, warmup, nlayers=STACK_LAYERS, seed=20260301):
+def run_stack(ctx, torch, steps, warmup, nlayers=STACK_LAYERS, seed=20260301, cpu_sample=False):
     """one token through nlayers independently seeded MoE layers, x_{L+1} = RMSNorm(y_L) (weights 1,
     eps 1e-6; the norm runs inside the next layer's block). A step is the whole chain for one fresh x; bytes = nlayers
     x the decode-1 bytes of a layer."""
@@ -143,11 +179,13 @@ def run_stack(ctx, torch, steps, warmup, nlayers=STACK_LAYERS, seed=20260301):
         token(xs[warmup + i])
     end.record()
     torch.cuda.synchronize()
+    ctx.sync()
     ms = start.elapsed_time(end) / steps
     nbytes = nlayers * step_bytes(1, 8)
+    cpu = cpu_stack_sample(ctx, layers, xs[warmup]) if cpu_sample else None
     del layers
     torch.cuda.empty_cache()
-    return {"layers": nlayers, "us_per_token": round(ms * 1e3, 1), "ms_per_step": round(ms, 4),
+    return {"layers": nlayers, "us_per_token": round(ms * 1e3, 1), "ms_per_step": round(ms, 4), "cpu": cpu,
             "bytes_per_token": nbytes, "hbm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "us_per_layer": round(ms * 1e3 / nlayers, 2),
@@ -195,6 +233,7 @@ def run_kquant(ctx, torch, iters=20, seed=20260401):
             ctx.kq_matvec(fmt, ws[i % copies], R, K, q, d, y)
         t1.record()
         torch.cuda.synchronize()
+        ctx.sync()
         us = t0.elapsed_time(t1) * 1e3 / reps
         wb = R * (K // 256) * KQ[fmt][1]
         out[name] = {"us_per_launch": round(us, 2), "weight_bytes": wb, "hbm_gbs": round(wb / us / 1e3, 1),
@@ -236,6 +275,7 @@ def run_realfmt(ctx, torch, steps=20, warmup=3, copies=2, seed=20260501):
                 ctx.moe_layer(layers[(warmup + i) % copies], xs[warmup + i], y)
             t1.record()
             torch.cuda.synchronize()
+            ctx.sync()
             ms = t0.elapsed_time(t1) / steps
             U = sum(distinct_experts(ctx, layers[(warmup + i) % copies], [xs[warmup + i]])[0] for i in range(steps)) / steps
             b = U * (2 * MAT_BYTES + E * (H // 256) * 110) + 2 * H * (E // 256) * 176 + E * (H // 256) * 210 + ROUTER_BYTES
@@ -250,31 +290,61 @@ def run_realfmt(ctx, torch, steps=20, warmup=3, copies=2, seed=20260501):
     return out
 
 
-def cpu_baseline(ctx, torch, res, budget_s=12.0, max_steps=8):
-    """The CPU checker (oracle/, restated ggml CPU semantics) on this host's cores, on a bounded sample of the same
-    workload: the first steps' x with the experts they select, timed around the oracle call only."""
-    import numpy as np
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads():
+    """All-cores thread count: the host cores this process may use, capped at 16 (a one-GPU box's CPU share)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def time_oracle(ctx, layer, x, threads, n_group=8, topk_group=4):
+    """Seconds of one oracle block call on x (numpy [n, E]) with the layer's weights; the selected experts are copied to
+    the host first, outside the timed call."""
     from oracle import oracle as orc
     from tests._helpers import host_layer
-    threads = min(16, os.cpu_count() or 1)
-    layers, xs, n = res["layers"], res["xs"], res["n"]
-    tot_s, toks, nsteps = 0.0, 0, 0
-    for i in range(min(max_steps, len(xs))):
-        layer = layers[i % len(layers)]
-        x = xs[i].cpu().numpy()
-        W, b = layer.gate_inp.cpu().numpy(), layer.probs_b.cpu().numpy()
-        _, _, sel, _ = orc.router(W, b, x)
-        _, _, gate, up, down, sh = host_layer(ctx, layer, sel.ravel())
-        t0 = time.perf_counter()
-        orc.moe_forward(x, W, b, gate, up, down, *sh, nthreads=threads)
-        tot_s += time.perf_counter() - t0
-        toks += n; nsteps += 1
-        if tot_s >= budget_s:
-            break
-    return {"value": round(tot_s / toks * 1e6, 1), "unit": "us/token", "cores": threads, "kind": "port",
-            "sample": "%d %s step(s) (%d tokens) through oracle/moe_oracle.c (restated ggml CPU semantics: Q8_K, "
-                      "vec_dot_iq2_xxs_q8_K, grouped router, swiglu, k-ordered combine), OpenMP %d threads, "
-                      "same x and weights as the GPU steps" % (nsteps, res["name"], toks, threads)}
+    W, b = layer.gate_inp.cpu().numpy(), layer.probs_b.cpu().numpy()
+    _, _, sel, _ = orc.router(W, b, x, n_group, topk_group)
+    _, _, gate, up, down, sh = host_layer(ctx, layer, sel.ravel())
+    t0 = time.perf_counter()
+    out = orc.moe_forward(x, W, b, gate, up, down, *sh, n_group=n_group, topk_group=topk_group, nthreads=threads)
+    return time.perf_counter() - t0, out["y"]
+
+
+def cpu_sample(ctx, res, rows, threads):
+    """us/token of the oracle on the first `rows` tokens of the workload's first step, at `threads` threads."""
+    x = res["xs"][0].cpu().numpy()[:rows]
+    dt, _ = time_oracle(ctx, res["layers"][0], x, threads)
+    return dt * 1e6 / x.shape[0]
+
+
+def cpu_stack_sample(ctx, layers, x0, nlayers=2):
+    """The first `nlayers` layers of the stack chain for one token on the CPU (the oracle's own chain: x_{L+1} =
+    RMSNorm(y_L)); per-token time scaled to all layers. Each layer's selected experts are copied to the host outside
+    the timed call."""
+    from oracle import oracle as orc
+    out = {}
+    for threads in (cpu_threads(), 1):
+        x = x0.cpu().numpy()
+        tot = 0.0
+        for L in layers[:nlayers]:
+            dt, y = time_oracle(ctx, L, x, threads)
+            tot += dt
+            x = orc.rmsnorm(y)
+        out["us_per_token_%dt" % threads] = round(tot / nlayers * len(layers) * 1e6, 1)
+    return out
 
 
 def load_traffic(kernel, workload):
@@ -286,50 +356,55 @@ def load_traffic(kernel, workload):
     return None
 
 
-def main():
-    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="decode8", choices=sorted(WORKLOADS))
-    ap.add_argument("--copies", type=int, default=3, help="independently seeded layers rotated over the steps")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-extra", action="store_true", help="skip the decode-1 / prefill-512 / prefill-2048 side measurements")
-    ap.add_argument("--no-stack", action="store_true", help="skip the 58-layer resident stack (configs[3], ~169 GB)")
-    ap.add_argument("--stack-steps", type=int, default=10)
-    ap.add_argument("--only-kquant", action="store_true",
-                    help="run only the K-quant mat-vec leg (the reference's real-shard formats) and print its JSON")
-    ap.add_argument("--fused", type=int, default=None, choices=(0, 1, 2),
-                    help="decode path: 2 regular single launch (library default), 1 cooperative single launch, 0 per pass")
-    ap.add_argument("--copy-probe", action="store_true",
-                    help="also run a plain 1 GiB device copy (the reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
-    args = ap.parse_args()
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        log("bench.py: this build runs on one GPU only (the MoE block is not sharded across GPUs); got --gpus %d, "
-            "WORLD_SIZE %d" % (args.gpus, world))
-        sys.exit(2)
-    import torch
-    from loki_amd import Context
-    ctx = Context()
+def kernel_roofline(res):
+    """Dominant kernel of a workload's step, its algorithmic bytes and average duration: the single decode launch
+    (its bytes are the step's), else the gate/up stage (grouped GEMM on MFMA above 8 tokens, else the mat-vec kernel)."""
+    n = res["n"]
+    if res["fused"]:
+        kname, k_ms, k_bytes = "k_moe_decode", res["stage_ms"]["gate_up"], res["bytes"]
+        stages = {"block": k_ms}
+    else:
+        kname = "k_pf_gemm<gate_up>" if n > 8 else "k_experts<gate_up>"
+        k_ms, k_bytes = res["stage_ms"]["gate_up"], res["gu_bytes"]
+        stages = res["stage_ms"]
+    k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
+    roof = {"kernel": kname, "bound": "hbm", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic(kname, res["name"]),
+            "algorithmic_bytes_per_launch": int(k_bytes), "avg_launch_us": round(k_ms * 1e3, 2)}
+    return roof, stages
+
+
+def summary(res):
+    roof, stages = kernel_roofline(res)
+    return {"us_per_token": round(res["ms"] * 1e3 / res["n"], 3), "ms_per_step": round(res["ms"], 4),
+            "tokens_per_s": round(res["n"] / (res["ms"] * 1e-3), 1), "hbm_gbs": round(res["gbs"], 1),
+            "hbm_frac": round(res["gbs"] / HBM_PEAK_GBS, 4), "distinct_experts": round(res["U"], 1),
+            "host_us_per_call": round(res["host_us"], 2), "routing_margin": res["margins"], "roofline": roof,
+            "stage_us": {k: round(v * 1e3, 2) for k, v in stages.items()}}
+
+
+def bench(args, ctx, torch):
     if args.fused is not None:
         ctx.set_fused(args.fused)
     if args.only_kquant:
         print(json.dumps({"kquant": run_kquant(ctx, torch), "real_formats": run_realfmt(ctx, torch)}), flush=True)
         return
+    thr = cpu_threads()
+    cpu_per = {}
+
+    def cpu_leg(res):
+        if args.no_cpu:
+            return
+        rows = min(res["n"], 8)
+        cpu_per[res["name"]] = {"us_per_token_%dt" % thr: round(cpu_sample(ctx, res, rows, thr), 1),
+                                "us_per_token_1t": round(cpu_sample(ctx, res, rows, 1), 1), "tokens": rows}
+        log("[bench] cpu %s: %s" % (res["name"], json.dumps(cpu_per[res["name"]])))
+
     res = run_workload(ctx, torch, args.workload, args.steps, args.warmup, args.copies)
     n = res["n"]
-    if res["fused"]:   # one launch = the whole block: its bytes are the step's
-        kname, k_ms, k_bytes = "k_moe_decode", res["stage_ms"]["gate_up"], res["bytes"]
-        stages = {"block": k_ms}
-    else:   # per-pass launches: the gate/up stage (grouped GEMM on MFMA above 8 tokens, else the mat-vec kernel)
-        kname = "k_pf_gemm<gate_up>" if n > 8 else "k_experts<gate_up>"
-        k_ms, k_bytes = res["stage_ms"]["gate_up"], res["gu_bytes"]
-        stages = res["stage_ms"]
-    k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
-    log("[bench] %s: %.1f us/step, %.2f us/token, %.0f GB/s (U=%.1f); kernel %s %.1f us (%.0f GB/s); stages (us): %s" % (
-        args.workload, res["ms"] * 1e3, res["ms"] * 1e3 / n, res["gbs"], res["U"], kname, k_ms * 1e3, k_gbs,
-        ", ".join("%s %.1f" % (k, v * 1e3) for k, v in stages.items())))
+    head = summary(res)
+    log("[bench] %s: %s" % (args.workload, json.dumps(head)))
+    cpu_leg(res)
     if args.copy_probe:
         a = torch.empty(1 << 28, dtype=torch.float32, device="cuda"); b = torch.empty_like(a)
         for _ in range(3):
@@ -339,28 +414,33 @@ def main():
         del a, b
     extra = {}
     if not args.no_extra:
-        for wl, st in (("decode1", 30), ("prefill512", 5), ("prefill2048", 3)):
+        for wl, st in (("decode8", 30), ("decode1", 30), ("prefill512", 5), ("prefill2048", 3)):
             if wl == args.workload:
                 continue
             r = run_workload(ctx, torch, wl, st, 2, args.copies)
-            extra[wl] = {"us_per_token": round(r["ms"] * 1e3 / r["n"], 3), "ms_per_step": round(r["ms"], 4),
-                         "tokens_per_s": round(r["n"] / (r["ms"] * 1e-3), 1), "hbm_gbs": round(r["gbs"], 1),
-                         "hbm_frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "distinct_experts": round(r["U"], 1),
-                         "kernel_us": round(r["stage_ms"]["gate_up"] * 1e3, 2) if r["fused"] else None,
-                         "stage_us": None if r["fused"] else {k: round(v * 1e3, 2) for k, v in r["stage_ms"].items()}}
+            extra[wl] = summary(r)
             log("[bench] %s: %s" % (wl, json.dumps(extra[wl])))
+            cpu_leg(r)
             del r
-    if not args.no_extra:
-        torch.cuda.empty_cache()
+            torch.cuda.empty_cache()
         extra["kquant"] = run_kquant(ctx, torch)
         extra["real_formats"] = run_realfmt(ctx, torch)
     if not args.no_stack:
         torch.cuda.empty_cache()
-        extra["stack58"] = run_stack(ctx, torch, args.stack_steps, 2)
+        extra["stack58"] = run_stack(ctx, torch, args.stack_steps, 2, cpu_sample=not args.no_cpu)
+        if extra["stack58"].get("cpu"):
+            cpu_per["stack58"] = extra["stack58"].pop("cpu")
         log("[bench] stack58: %s" % json.dumps(extra["stack58"]))
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(ctx, torch, res)
+        key = "us_per_token_%dt" % thr
+        cpu = {"value": cpu_per[args.workload][key], "unit": "us/token", "cores": thr, "kind": "port",
+               "sample": "%s: %d token(s) of the first step through oracle/moe_oracle.c (restated ggml CPU semantics: "
+                         "Q8_K, vec_dot_iq2_xxs_q8_K, grouped router, swiglu, k-ordered combine), OpenMP %d threads, "
+                         "same x and weights as the GPU steps; per_config holds every config at %d threads and at 1 "
+                         "thread (prefill: the batch's first 8 tokens; stack58: 2 layers of the chain, scaled to 58)"
+                         % (args.workload, cpu_per[args.workload]["tokens"], thr, thr),
+               "cpu_model": cpu_model(), "nproc": os.cpu_count(), "per_config": cpu_per}
         log("[bench] cpu baseline: %s" % json.dumps(cpu))
     out = {
         "metric": "MoE-layer decode µs/token (HBM GB/s, % peak); prefill-512 tokens/s",
@@ -376,18 +456,57 @@ def main():
         "config": {"workload": res["desc"], "tokens": n, "hidden": E, "expert_ffn": H, "routed_experts": 256,
                    "shared_experts": 1, "routing": "sigmoid, 8 groups, top-4 groups, top-8, x2.5",
                    "weights": "IQ2_XXS (activations Q8_K)", "layer_copies": args.copies},
-        "hbm_gbs": round(res["gbs"], 1),
-        "hbm_frac": round(res["gbs"] / HBM_PEAK_GBS, 4),
-        "distinct_experts": round(res["U"], 1),
-        "roofline": {"kernel": kname, "bound": "hbm", "achieved": round(k_gbs, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(k_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": load_traffic(kname, args.workload),
-                     "algorithmic_bytes_per_launch": int(k_bytes), "avg_launch_us": round(k_ms * 1e3, 2)},
-        "stage_us": {k: round(v * 1e3, 2) for k, v in stages.items()},
+        "hbm_gbs": head["hbm_gbs"],
+        "hbm_frac": head["hbm_frac"],
+        "distinct_experts": head["distinct_experts"],
+        "routing_margin": head["routing_margin"],
+        "host_us_per_call": head["host_us_per_call"],
+        "roofline": head["roofline"],
+        "stage_us": head["stage_us"],
         "cpu_baseline": cpu,
         "extra": extra,
     }
     print(json.dumps(out), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="decode1", choices=sorted(WORKLOADS))
+    ap.add_argument("--copies", type=int, default=3, help="independently seeded layers rotated over the steps")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="skip the other decode / prefill workloads and the K-quant legs")
+    ap.add_argument("--no-stack", action="store_true", help="skip the 58-layer resident stack (configs[3], ~169 GB)")
+    ap.add_argument("--stack-steps", type=int, default=10)
+    ap.add_argument("--only-kquant", action="store_true",
+                    help="run only the K-quant mat-vec leg (the reference's real-shard formats) and print its JSON")
+    ap.add_argument("--fused", type=int, default=None, choices=(0, 1, 2),
+                    help="decode path: 2 regular single launch (library default), 1 cooperative single launch, 0 per pass")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a plain 1 GiB device copy (the reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        log("bench.py: this build runs on one GPU only (the MoE block is not sharded across GPUs); got --gpus %d, "
+            "WORLD_SIZE %d" % (args.gpus, world))
+        sys.exit(2)
+    import torch
+    from loki_amd import Context, LokiError
+    ctx = Context()
+    rc = 0
+    try:
+        bench(args, ctx, torch)
+    except LokiError as e:   # a device-side failure reported by fl_sync: no bench line
+        log("bench.py: %s" % e)
+        rc = 3
+    finally:
+        # the context's HIP objects are released before interpreter exit (exit-time destructors would otherwise run
+        # them after a profiler's own teardown)
+        torch.cuda.synchronize()
+        ctx.close()
+    sys.exit(rc)
 
 
 if __name__ == "__main__":

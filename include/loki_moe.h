@@ -87,6 +87,13 @@ int fl_set_shared_formats(FLCtx *, int gate_fmt, int up_fmt, int down_fmt);
 int fl_set_experts(FLCtx *, int n_exp);
 /* routing rule: DeepSeek-V3 groups (default 8 groups, top-4 groups, top-8, x2.5); n_group = topk_group = 1 is the reference's rule */
 int fl_set_routing(FLCtx *, int n_group, int topk_group, int topk, float scale);
+/* keep-KE for fl_moe_layer / fl_moe_layer_normed (additive; the reference does it on the host between fl_fetch and
+ * fl_moe, src/server_core_fused.cpp:793-813, with KE = 2 in production, :340): each row keeps its `keep` heaviest
+ * routed experts (weight descending, equal weights in pick order) and, with renorm > 0, every kept weight is multiplied
+ * by renorm / (their fp32 sum in kept order) when that sum exceeds 1e-6 (the reference: renorm 2.5, RENORM_EXPERTS on).
+ * The block then runs keep slots per row; FLDebug's sel / wts hold [n][keep]. keep = 0 (default) keeps all topk.
+ * fl_route_dev and fl_ffn_begin are unaffected (the engine's host dispatch applies its own keep). */
+int fl_set_keep(FLCtx *, int keep, float renorm);
 
 /* ---------------------------------------------------------------- additive: device-resident block (the measured path) */
 typedef struct FLMoeLayer {
@@ -193,16 +200,19 @@ typedef struct FLDebug {
     const float * h; const int8_t * hq; const float * hd; /* [P+n][H]: per slot, shared rows at P.. (per-pass path) */
     const float * o;                                   /* [P+n][E] (per-pass path) */
     const float * g, * u;                              /* gate / up outputs when debug capture is on (per-pass path) */
-    int n, P, topk;
+    int n, P, topk;                                    /* topk: slots per row of the last call (the kept count) */
     int fused;                                         /* 1: the last call ran as the single-launch decode block, which
                                                         * keeps h and o internal (h .. u are NULL then) */
 } FLDebug;
 int fl_debug(FLCtx *, FLDebug * out);
 int fl_set_debug(FLCtx *, int capture_gate_up);
 /* decode batches (n <= 8, E 7168, H 2048) of fl_moe_layer: 2 (default) = the whole block as one regular launch of one
- * workgroup per CU (assumes nothing else occupies the CUs, as in a single-stream engine: every device-wide wait is
- * bounded and reports a timeout through fl_sync otherwise); 1 = the same kernel as a cooperative launch (residency
- * guaranteed by the runtime, ~18 us more per call at batch 1); 0 = one launch per pass */
+ * workgroup per CU (assumes nothing else occupies the CUs, as in a single-stream engine); 1 = the same kernel as a
+ * cooperative launch (residency guaranteed by the runtime, ~18 us more per call at batch 1); 0 = one launch per pass.
+ * Every device-wide wait of the single launch is bounded: if workgroups are not co-resident (another stream or process
+ * holds CUs) a wait times out, the launch's outputs are invalid, and the code is reported twice -- by fl_sync, which
+ * the caller must check before trusting any output of a mode-2 decode, and, without waiting, by the next
+ * fl_moe_layer / fl_moe_layer_normed call on the context, which returns FL_EHIP until fl_sync has reported it. */
 int fl_set_fused(FLCtx *, int mode);
 /* batches above the decode sizes (n > 8, E 7168, H 2048): 1 (default) = the expert products as grouped GEMMs on the
  * matrix cores (no counterpart in the reference, whose wide path is tc_matvec per arena batch, src/fused_layer.cu:540-561);
@@ -219,6 +229,8 @@ hipStream_t fl_stream(FLCtx *);
 int fl_set_stream(FLCtx *, hipStream_t s);
 /* device -> host copy on the context's stream, waited (tests read internal buffers with it) */
 int fl_d2h(FLCtx *, void * host, const void * dev, size_t bytes);
+/* waits for the context's stream; FL_EHIP (with the code in fl_last_error) if a kernel reported a device-side failure
+ * since the last fl_sync (decode block: a bounded wait timed out; MFMA prefill: a misaligned LDS base), then clears it */
 int fl_sync(FLCtx *);
 const char * fl_last_error(FLCtx *);
 void fl_free(FLCtx *);

@@ -124,7 +124,7 @@ class FLOut(ctypes.Structure):
 ABI_SYMBOLS = [
     "fl_init", "fl_attn", "fl_wide_init", "fl_wide_moe", "fl_wide_mark", "fl_wide_wait", "fl_wide_finish", "fl_moe_outs",
     "fl_wide_outs", "fl_wide_skip", "fl_spec", "fl_sketch", "fl_fetch", "fl_moe", "fl_skip", "fl_h2d", "fl_wait_event",
-    "fl_gpu_ms", "fl_ffn_begin", "fl_set_experts", "fl_set_routing", "fl_set_shared_formats", "fl_set_layer_formats", "fl_kq_matvec_dev",
+    "fl_gpu_ms", "fl_ffn_begin", "fl_set_experts", "fl_set_routing", "fl_set_keep", "fl_set_shared_formats", "fl_set_layer_formats", "fl_kq_matvec_dev",
     "fl_gguf_open", "fl_gguf_close", "fl_gguf_n_tensors", "fl_gguf_tensor_name", "fl_gguf_tensor", "fl_gguf_tensor_at",
     "fl_gguf_get_int", "fl_gguf_get_float", "fl_gguf_get_str", "fl_gguf_read", "fl_gguf_load_moe_layer", "fl_gguf_free_layer", "fl_moe_layer", "fl_moe_layer_normed", "fl_route_dev", "fl_dispatch_dev", "fl_quant_q8k_dev",
     "fl_pack_iq2xxs", "fl_unpack_iq2xxs", "fl_rmsnorm_dev", "fl_synth_iq2xxs", "fl_synth_normal", "fl_probe_exp",
@@ -156,6 +156,7 @@ def lib():
             "fl_last_error": (ctypes.c_char_p, [P_]),
             "fl_set_routing": (I, [P_, I, I, I, F]),
             "fl_set_experts": (I, [P_, I]),
+            "fl_set_keep": (I, [P_, I, F]),
             "fl_set_shared_formats": (I, [P_, I, I, I]),
             "fl_set_layer_formats": (I, [P_, I, I, I, I]),
             "fl_kq_matvec_dev": (I, [P_, I, P_, I, I, P_, P_, I, P_]),
@@ -279,6 +280,10 @@ class Context:
     def set_routing(self, n_group=8, topk_group=4, topk=8, scale=2.5):
         self.check(lib().fl_set_routing(self.ctx, n_group, topk_group, topk, scale))
 
+    def set_keep(self, keep=0, renorm=2.5):
+        """fl_moe_layer keeps each row's `keep` heaviest experts, rescaled to sum to renorm (0 = all topk, default)."""
+        self.check(lib().fl_set_keep(self.ctx, keep, renorm))
+
     def set_experts(self, n_exp=N_EXPERT):
         self.check(lib().fl_set_experts(self.ctx, n_exp))
 
@@ -298,9 +303,29 @@ class Context:
         self.check(lib().fl_set_prefill_mfma(self.ctx, 1 if on else 0))
 
     def set_fused(self, mode):
-        """Decode batches (n <= 8): 2 = one regular launch (default), 1 / True = the same kernel as a cooperative
-        launch, 0 / False = one launch per pass."""
+        """Decode batches (n <= 8): 2 = one regular launch (default), 1 = the same kernel as a cooperative launch,
+        0 = one launch per pass."""
         self.check(lib().fl_set_fused(self.ctx, int(mode)))
+        self._fused = int(mode)
+
+    @property
+    def fused_mode(self):
+        """The decode mode last set on this context (the library's default 2 until set_fused is called)."""
+        return getattr(self, "_fused", 2)
+
+    def using_fused(self, mode):
+        """Context manager: run the body with decode mode `mode`, then restore the previous mode."""
+        import contextlib
+
+        @contextlib.contextmanager
+        def cm():
+            prev = self.fused_mode
+            self.set_fused(mode)
+            try:
+                yield self
+            finally:
+                self.set_fused(prev)
+        return cm()
 
     # ---- building blocks
     def quant_q8k(self, x):

@@ -35,6 +35,7 @@ struct FLCtx {
     hipStream_t st = nullptr, own = nullptr; int dev = 0, ncu = 0;
     hipEvent_t em0 = nullptr, em1 = nullptr;
     int n_group = 8, topk_group = 4, topk = 8; float scale = 2.5f;
+    int keep = 0; float renorm = 0.f;   // fl_moe_layer keeps each row's `keep` heaviest experts (0: all topk)
     int n_exp = 256;   // routed experts behind the reference-named entry points (FLW carries no count)
     double ms_moe = 0.0;
     std::string err;
@@ -51,6 +52,9 @@ struct FLCtx {
     DBuf<uint4> tab;                         // LDS table image (build_table_image)
     // single-launch decode block: epoch-tagged logits / h / o, wait-timeout word; fused = 0 forces the per-pass kernels
     DBuf<int> derr; DBuf<uint64_t> dlogit, dth, dto; unsigned epoch = 0; int fused = 2; int dec_grid = -1;
+    // pinned, device-mapped copy of the last code a kernel reported (null if the host allocation failed): every
+    // fl_moe_layer call checks it without waiting for the stream, fl_sync reports and clears it
+    int * herr = nullptr, * herr_dev = nullptr;   // host pointer, and the address kernels store to
     // prefill grouped GEMM on MFMA (batches above the decode sizes): fp16 table image, columns, fp16 activation copies
     int pf_mfma = 1, pf_ready = 0; DBuf<uint4> ptab; DBuf<int4> pcols; DBuf<int> pncols; DBuf<_Float16> xh, hh;
     struct Compat * compat = nullptr;          // reference-API state (compat.hip), created on first use

@@ -32,6 +32,13 @@ extern "C" FLCtx * fl_init(int kvp, int sc_cap) {
     CK(hipDeviceGetAttribute(&c->ncu, hipDeviceAttributeMultiprocessorCount, c->dev));
     CK(hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking)); c->st = c->own;
     CK(hipEventCreate(&c->em0)); CK(hipEventCreate(&c->em1));
+    if (hipHostMalloc((void **) &c->herr, sizeof(int), hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess) {
+        (void) hipGetLastError(); c->herr = nullptr;
+    } else if (hipHostGetDevicePointer((void **) &c->herr_dev, c->herr, 0) != hipSuccess) {
+        (void) hipGetLastError(); (void) hipHostFree(c->herr); c->herr = nullptr;
+    } else {
+        __atomic_store_n(c->herr, 0, __ATOMIC_RELEASE);
+    }
     return c;
 }
 
@@ -47,6 +54,7 @@ extern "C" void fl_free(FLCtx * c) {
     for (auto & v : c->ev_free) { for (auto e : v) { (void) hipEventDestroy(e); } }
     for (auto & v : c->ev_pending) { for (auto e : v) { (void) hipEventDestroy(e); } }
     (void) hipEventDestroy(c->em0); (void) hipEventDestroy(c->em1); (void) hipStreamDestroy(c->own);
+    if (c->herr) { (void) hipHostFree(c->herr); }
     delete c;
 }
 
@@ -68,13 +76,14 @@ extern "C" int fl_d2h(FLCtx * c, void * host, const void * dev, size_t bytes) {
 extern "C" int fl_sync(FLCtx * c) {
     if (!c) { return FL_EINVAL; }
     TRY(c, hipStreamSynchronize(c->st));
+    int e = 0;
     if (c->derr.p) {
-        int e = 0;
         TRY(c, hipMemcpy(&e, c->derr.p, sizeof e, hipMemcpyDeviceToHost));
-        if (e) {
-            TRY(c, hipMemset(c->derr.p, 0, sizeof e));
-            return fail(c, FL_EHIP, "a device kernel reported error code %d (decode block: a wait timed out; prefill: bad LDS base); its outputs are invalid", e);
-        }
+        if (e) { TRY(c, hipMemset(c->derr.p, 0, sizeof e)); }
+    }
+    if (c->herr) { e |= __atomic_exchange_n(c->herr, 0, __ATOMIC_ACQ_REL); }
+    if (e) {
+        return fail(c, FL_EHIP, "a device kernel reported error code %d (decode block: a wait timed out; prefill: bad LDS base); its outputs are invalid", e);
     }
     return FL_OK;
 }
@@ -86,6 +95,11 @@ extern "C" int fl_set_routing(FLCtx * c, int n_group, int topk_group, int topk, 
         return fail(c, FL_EINVAL, "bad routing rule (n_group %d, topk_group %d, topk %d, scale %g)", n_group, topk_group, topk, (double) scale);
     }
     c->n_group = n_group; c->topk_group = topk_group; c->topk = topk; c->scale = scale; return FL_OK;
+}
+extern "C" int fl_set_keep(FLCtx * c, int keep, float renorm) {
+    if (!c) { return FL_EINVAL; }
+    if (keep < 0 || keep > MAXK || !(renorm >= 0.f)) { return fail(c, FL_EINVAL, "keep %d outside 0..%d or renorm %g negative", keep, MAXK, (double) renorm); }
+    c->keep = keep; c->renorm = renorm; return FL_OK;
 }
 extern "C" int fl_set_experts(FLCtx * c, int n_exp) {
     if (!c) { return FL_EINVAL; }
@@ -262,11 +276,18 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     if (L->layout != FL_LAYOUT_TILED) { return fail(c, FL_EINVAL, "fl_moe_layer reads the tiled layout; convert with fl_pack_iq2xxs"); }
     if (L->E <= 0 || L->E % 1024 || L->H <= 0 || L->H % 1024) { return fail(c, FL_EINVAL, "E %d and H %d must be positive multiples of 1024", L->E, L->H); }
     if (int rc = check_rule(c, L->n_exp)) { return rc; }
+    if (c->herr) {   // an earlier launch on this context failed (seen without waiting); fl_sync reports and clears it
+        const int e = __atomic_load_n(c->herr, __ATOMIC_ACQUIRE);
+        if (e) { return fail(c, FL_EHIP, "an earlier launch on this context reported device error code %d; call fl_sync", e); }
+    }
     if (n == 0) { return FL_OK; }
     if (!x || !y || !L->gate_inp || !L->probs_b || !L->gate_exps || !L->up_exps || !L->down_exps || !L->sh_gate || !L->sh_up || !L->sh_down) {
         return fail(c, FL_EINVAL, "null pointer in the layer or x / y");
     }
-    const int E = L->E, H = L->H, ne = L->n_exp, tk = c->topk, P = n * tk;
+    if (c->keep > c->topk) { return fail(c, FL_EINVAL, "keep %d above topk %d", c->keep, c->topk); }
+    // the selection draws topk experts per row; the block runs the kept ones (fl_set_keep), tk per row
+    const int E = L->E, H = L->H, ne = L->n_exp, tsel = c->topk, tk = c->keep > 0 ? c->keep : tsel, P = n * tk;
+    const float renorm = c->keep > 0 ? c->renorm : 0.f;
     const int * lf = c->lf;
     const bool kq = lf[0] != FL_IQ2 || lf[1] != FL_IQ2 || lf[2] != FL_IQ2 || lf[3] != FL_IQ2;
     {
@@ -309,7 +330,8 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
         }
         DecodeArgs d{};
         d.tab = c->tab.p; d.x = x; d.n = n; d.prenorm = prenorm ? 1 : 0; d.nw = nw; d.eps = eps; d.resid = resid;
-        d.Wr = L->gate_inp; d.bias = L->probs_b; d.n_exp = ne; d.n_group = c->n_group; d.topk_group = c->topk_group; d.topk = tk; d.scale = c->scale;
+        d.Wr = L->gate_inp; d.bias = L->probs_b; d.n_exp = ne; d.n_group = c->n_group; d.topk_group = c->topk_group; d.topk = tsel; d.scale = c->scale;
+        d.keep = tk; d.renorm = renorm;
         d.gate = (const uint8_t *) L->gate_exps; d.up = (const uint8_t *) L->up_exps; d.down = (const uint8_t *) L->down_exps;
         d.estride = (size_t) H * (E / 256) * IQ2B;
         d.sh_gate = (const uint8_t *) L->sh_gate; d.sh_up = (const uint8_t *) L->sh_up; d.sh_down = (const uint8_t *) L->sh_down;
@@ -317,7 +339,7 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
         d.xq = c->xq.p; d.xd = c->xd.p; d.logits = c->logits.p; d.probs = c->probs.p; d.sel = c->sel.p; d.wts = c->wts.p;
         d.counts = c->counts.p; d.offsets = c->offsets.p; d.perm = c->perm.p; d.inv = c->inv.p; d.act = c->act.p; d.nact = c->nact.p;
         d.tlogits = c->dlogit.p; d.th = c->dth.p; d.to = c->dto.p; d.y = y;
-        d.epoch = c->epoch; d.err = c->derr.p;
+        d.epoch = c->epoch; d.err = c->derr.p; d.herr = c->herr ? c->herr_dev : nullptr;
         // stages: the whole block is one launch, reported as stage 4; the others are empty
         for (int i = 0; i <= 4; ++i) { prof_mark(c, ev, i); }
         TRY(c, launch_moe_decode(d, c->dec_grid, c->fused == 1, st));
@@ -346,7 +368,7 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     prof_mark(c, ev, 1);
     TRY(c, launch_router_logits(L->gate_inp, x, n, ne, E, c->logits.p, st));
     prof_mark(c, ev, 2);
-    TRY(c, launch_router_select(c->logits.p, L->probs_b, n, ne, c->n_group, c->topk_group, tk, c->scale, c->probs.p, c->sel.p, c->wts.p, st));
+    TRY(c, launch_router_select(c->logits.p, L->probs_b, n, ne, c->n_group, c->topk_group, tsel, c->scale, c->probs.p, c->sel.p, c->wts.p, st, tk, renorm));
     prof_mark(c, ev, 3);
     TRY(c, launch_dispatch(c->sel.p, P, ne, c->counts.p, c->offsets.p, c->perm.p, c->inv.p, c->act.p, c->nact.p, st));
     if (mfma) {
@@ -357,7 +379,7 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
         g.estride = (size_t) H * (E / 256) * IQ2B; g.sh[0] = (const uint8_t *) L->sh_gate; g.sh[1] = (const uint8_t *) L->sh_up;
         g.perm = c->perm.p; g.topk = tk; g.P = P; g.R = H; g.K = E; g.nmat = 2; g.cols = c->pcols.p; g.ncols = c->pncols.p;
         g.bh = c->xh.p; g.bd = c->xd.p; g.out = c->h.p; g.gdbg = c->dbg_gu ? c->g.p : nullptr; g.udbg = c->dbg_gu ? c->u.p : nullptr;
-        g.err = c->derr.p;
+        g.err = c->derr.p; g.herr = c->herr ? c->herr_dev : nullptr;
         TRY(c, launch_prefill_gemm(g, c->ncu, st));
         TRY(c, launch_quant_q8k(c->h.p, (int64_t) rows, H, c->hq.p, c->hd.p, st));
         TRY(c, launch_q8_to_h(c->hq.p, c->hh.p, (int64_t) rows * H, st));
@@ -432,9 +454,11 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     d.w[0] = (const uint8_t *) L->down_exps; d.w[1] = nullptr; d.sh[0] = (const uint8_t *) L->sh_down; d.sh[1] = nullptr;
     d.aq = c->hq.p; d.ad = c->hd.p; d.K = H; d.R = E; d.nmat = 1;
     d.h = nullptr; d.hq = nullptr; d.hd = nullptr; d.gdbg = nullptr; d.udbg = nullptr;
-    d.o = c->o.p; d.inv = c->inv.p; d.wts = c->wts.p; d.y = y;
+    // the down kernel's fused combine has no residual term: with one, the k-ordered combine runs after it
+    d.o = c->o.p; d.inv = c->inv.p; d.wts = c->wts.p; d.y = resid ? nullptr : y;
     expert_counters(c, d, 1);
     TRY(c, launch_experts_down(d, c->ncu, st));
+    if (resid) { TRY(c, launch_combine(c->o.p, c->inv.p, c->wts.p, n, tk, E, P, resid, y, nullptr, st)); }
     prof_mark(c, ev, 6);
     return FL_OK;
 }
@@ -483,7 +507,7 @@ extern "C" int fl_debug(FLCtx * c, FLDebug * out) {
     if (!c->last_fused) {   // the single-launch block keeps h and o in its epoch-tagged buffers only
         out->h = c->h.p; out->hq = c->hq.p; out->hd = c->hd.p; out->o = c->o.p; out->g = c->dbg_gu ? c->g.p : nullptr; out->u = c->dbg_gu ? c->u.p : nullptr;
     }
-    out->n = c->last_n; out->P = c->last_P; out->topk = c->topk; out->fused = c->last_fused;
+    out->n = c->last_n; out->P = c->last_P; out->topk = c->last_n > 0 ? c->last_P / c->last_n : c->topk; out->fused = c->last_fused;
     return FL_OK;
 }
 

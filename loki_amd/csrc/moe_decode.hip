@@ -75,7 +75,14 @@ struct RT {
     }
 };
 
-__device__ __forceinline__ void report(int * err, int code) { if (lane_id() == 0) { __hip_atomic_fetch_or(gptr(err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); } }
+// an error code into the device word (OR of every code) and, when the context has one, the host-mapped word (a plain
+// system-scope store: the host checks it at its next call without waiting for the stream)
+__device__ __forceinline__ void report(const DArgs & a, int code) {
+    if (lane_id() == 0) {
+        __hip_atomic_fetch_or(gptr(a.err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (a.herr) { __hip_atomic_store(gptr(a.herr), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); }
+    }
+}
 
 // epoch-tagged words: {epoch (bits 32..63), fp32 bits}, one 64-bit store / load each (single-copy atomic)
 __device__ __forceinline__ void st_tag(uint64_t * p, uint32_t epoch, float v) {
@@ -379,7 +386,7 @@ __device__ __forceinline__ bool gu_task(const DArgs & a, lds_t lds, const Lane l
     } else {
         const int sc = rt.ps_s[ps0 + k];
         t.mi = rt.ps_mi[ps0 + k]; t.s = sc & 0xFFFF; t.c = sc >> 16;
-        if (!((t.mi == SH || (unsigned) t.mi < (unsigned) nact) && (t.c == 1 || t.c == 2) && t.s + t.c <= P + a.n)) { report(a.err, 32); return false; }
+        if (!((t.mi == SH || (unsigned) t.mi < (unsigned) nact) && (t.c == 1 || t.c == 2) && t.s + t.c <= P + a.n)) { report(a, 32); return false; }
     }
     const bool routed = t.mi != SH;
     const int e = routed ? rt.act_e[t.mi] : 0;
@@ -431,7 +438,7 @@ __device__ __forceinline__ void gu_publish(const DArgs & a, const Lane ln, const
 __device__ __forceinline__ const uint8_t * gu_xrow(const DArgs & a, lds_t lds, const GuTask & t, int P) {
     const RT rt(lds);
     const int slot = t.s + t.u;
-    return (const uint8_t *) (lds + L_XS + (t.mi != SH ? rt.perm[slot] / a.topk : slot - P) * GG::XROW);
+    return (const uint8_t *) (lds + L_XS + (t.mi != SH ? rt.perm[slot] / a.keep : slot - P) * GG::XROW);
 }
 
 // the wave's tasks tk, tk + tstep, .. < t_end (every token pass of each) as one stream; returns the number of passes
@@ -587,10 +594,10 @@ __device__ __forceinline__ int down_phase(const DArgs & a, lds_t lds, const Lane
 #pragma unroll
         for (int w2 = 0; w2 < DW; ++w2) { all_ok = all_ok && wok[w2] != 0u; }
         TRACE(wave, 25);
-        if (!all_ok) { report(a.err, 1); continue; }
+        if (!all_ok) { report(a, 1); continue; }
         for (int k = 0; k < kn; ++k) {
             DnUnit d; const uint8_t * qb, * db;
-            if (!unit_bases(k0 + k, d, qb, db)) { report(a.err, 1); continue; }
+            if (!unit_bases(k0 + k, d, qb, db)) { report(a, 1); continue; }
             // one token per pass: the second pass re-reads the unit's weights from L2
             for (int i = 0; i < d.c; ++i) {
                 if (k > 0 || i > 0) { rs.prologue(qb, db, lq, ld); } else { rs.template prologue<DN_PRE, DN_PD>(qb, db, lq, ld); }
@@ -617,14 +624,14 @@ __device__ __forceinline__ bool combine_unit(const DArgs & a, lds_t lds, int cu,
     const RT rt(lds);
     const int rr = cu * DN_ROWS + (threadIdx.x & (DN_ROWS - 1)), t0 = threadIdx.x / DN_ROWS;
     uint64_t wv[CT][MAXK + 1];
-    auto used = [&](int c, int k) { return t0 + c * TS < a.n && (k < a.topk || k == MAXK); };
+    auto used = [&](int c, int k) { return t0 + c * TS < a.n && (k < a.keep || k == MAXK); };
     auto issue = [&]() {
 #pragma unroll
         for (int c = 0; c < CT; ++c) {
             const int tok = t0 + c * TS;
 #pragma unroll
             for (int k = 0; k <= MAXK; ++k) {
-                if (used(c, k)) { wv[c][k] = ld_tag(a.to + (size_t) (k < MAXK ? rt.inv[tok * a.topk + k] : P + tok) * DE + rr); }
+                if (used(c, k)) { wv[c][k] = ld_tag(a.to + (size_t) (k < MAXK ? rt.inv[tok * a.keep + k] : P + tok) * DE + rr); }
             }
         }
     };
@@ -646,9 +653,9 @@ __device__ __forceinline__ bool combine_unit(const DArgs & a, lds_t lds, int cu,
     for (int c = 0; c < CT; ++c) {
         const int tok = t0 + c * TS;
         if (tok < a.n) {
-            float mv = tag_val(wv[c][0]) * rt.wts[tok * a.topk];
+            float mv = tag_val(wv[c][0]) * rt.wts[tok * a.keep];
 #pragma unroll
-            for (int k = 1; k < MAXK; ++k) { if (k < a.topk) { mv = mv + tag_val(wv[c][k]) * rt.wts[tok * a.topk + k]; } }
+            for (int k = 1; k < MAXK; ++k) { if (k < a.keep) { mv = mv + tag_val(wv[c][k]) * rt.wts[tok * a.keep + k]; } }
             float yv = mv + tag_val(wv[c][MAXK]);
             if (a.resid) { yv = yv + gptr(a.resid)[(size_t) tok * DE + rr]; }
             gptr(a.y)[(size_t) tok * DE + rr] = yv;
@@ -666,7 +673,7 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
     extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds[];
     const lds_t lds = (lds_t) dyn_lds;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
-    const int G = gridDim.x, n = a.n, P = n * a.topk;
+    const int G = gridDim.x, n = a.n, P = n * a.keep;
     // [0] waves with tokens and tables staged, [1] selections done, [2] routing ready (1 ok, 2 failed), [3] a wait failed,
     // [4] early shared task: waves done
     LK_LOCAL unsigned * ctl = reinterpret_cast<LK_LOCAL unsigned *>(lds + L_CTL);
@@ -676,7 +683,7 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
 
     // 1. table copy in flight; router (the whole workgroup)
     TRACE(wave, 0);
-    if (lds_addr(dyn_lds) & 0xFFFFu) { report(a.err, 4); return; }   // table addressing needs a 64 KB aligned base
+    if (lds_addr(dyn_lds) & 0xFFFFu) { report(a, 4); return; }   // table addressing needs a 64 KB aligned base
     if (threadIdx.x < 8) { ctl[threadIdx.x] = 0; }
     tables_dma(lds, a.tab, wave);
     __syncthreads();   // the hand-off words are clear
@@ -702,10 +709,10 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
         float pv[4];
         const bool ok = probs_wait(a, wave, pw, pv);
         TRACE(wave, 3);
-        if (!ok) { report(a.err, 2); }
+        if (!ok) { report(a, 2); }
         const RT rt(lds);
         if (ok) {
-            select_token_p<false>(pv, bv, a.n_exp, a.n_group, a.topk_group, a.topk, a.scale, nullptr, (int *) (rt.sel + wave * a.topk), (float *) (rt.wts + wave * a.topk));
+            select_token_p<false>(pv, bv, a.n_exp, a.n_group, a.topk_group, a.topk, a.scale, nullptr, (int *) (rt.sel + wave * a.keep), (float *) (rt.wts + wave * a.keep), a.keep, a.renorm);
         } else if (lane == 0) {
             __hip_atomic_fetch_or(ctl + 3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
@@ -729,7 +736,7 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
     const unsigned ready = lds_wait(ctl + 2);
     TRACE(wave, 5);
     // a failed routing wait leaves every later phase without its inputs: all waves leave (the error is reported)
-    if (ready != 1) { if (ready == 0) { report(a.err, 8); } return; }
+    if (ready != 1) { if (ready == 0) { report(a, 8); } return; }
 
     // 3. gate/up tasks (pair-slot, 8 h rows): task tk on workgroup tk / DW % G, wave tk % DW, so a workgroup streams
     //    whole 64-row groups; the shared expert's pair-slots come first unless the early tasks covered them
@@ -746,7 +753,7 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
     // 5. combine units on the last workgroups
     for (int cu = G - 1 - blockIdx.x; cu < NDN; cu += G) {
         TRACE(wave, 56);
-        if (!combine_unit(a, lds, cu, P)) { report(a.err, 16); }
+        if (!combine_unit(a, lds, cu, P)) { report(a, 16); }
         TRACE(wave, 58);
     }
     if (blockIdx.x == 0 && wave == DW - 1) { routing_outputs(a, lds, P); }
@@ -776,7 +783,7 @@ bool decode_rule_ok(int n_exp, int n_group) {   // the selection's DPP group pat
 }
 
 hipError_t launch_moe_decode(const DecodeArgs & a, int grid, bool cooperative, hipStream_t st) {
-    if (a.n < 1 || a.n > DMAX_N || a.topk < 1 || a.topk > MAXK || !decode_rule_ok(a.n_exp, a.n_group) ||
+    if (a.n < 1 || a.n > DMAX_N || a.topk < 1 || a.topk > MAXK || a.keep < 1 || a.keep > a.topk || !decode_rule_ok(a.n_exp, a.n_group) ||
         a.E != DE || a.H != DH || grid < 1 || !a.th || !a.to || !a.tlogits) {
         return hipErrorInvalidValue;
     }

@@ -539,6 +539,9 @@ struct RowStream {
 // Grouped sigmoid top-k (the rule of router.hip): p = sigmoid(logit), c = p + bias; group score = top1 + top2 of c in
 // the group; groups ranked by score (ties to the lower group) keep topk_group; topk rounds of argmax over eligible
 // experts (ties to the lower index); w_r = p_r / max(sum_r p_r, 2^-14) * scale with the sum in pick order.
+// keep < topk then keeps the keep largest weights (the engine's narrow dispatch, src/server_core_fused.cpp:793-811):
+// ordered by weight descending, equal weights in pick order, and, with renorm > 0, every kept weight multiplied by
+// f = renorm / sw when the kept sum sw (in kept order, fp32) exceeds 1e-6. sel_out / w_out receive keep entries.
 // lg[j] = logit of expert 4 lane + j. scr: per-wave LDS scratch of n_exp + 2 * n_group floats (general group sizes only).
 template <int CTRL> __device__ __forceinline__ void top2_step(float & v1, float & v2) {
     const float o1 = dppf<CTRL>(v1), o2 = dppf<CTRL>(v2);
@@ -555,7 +558,7 @@ __device__ __forceinline__ void load_bias(const float * bias, int n_exp, float (
 // SCRATCH = false: the caller guarantees the DPP group path (decode_rule_ok) and passes no scratch
 template <bool SCRATCH = true>
 __device__ __forceinline__ void select_token_p(const float (&p)[4], const float (&bias)[4], int n_exp, int n_group, int topk_group, int topk,
-                                               float scale, float * scr, int * sel_out, float * w_out) {
+                                               float scale, float * scr, int * sel_out, float * w_out, int keep, float renorm) {
 #pragma clang fp contract(off)
     const int lane = lane_id(), per = n_exp / n_group;
     float c[4];
@@ -642,11 +645,33 @@ __device__ __forceinline__ void select_token_p(const float (&p)[4], const float 
         if (lane == r) { sel_mine = bi; p_mine = bp; }
     }
     sum = sum > 6.103515625e-5f ? sum : 6.103515625e-5f;
-    if (lane < topk) { sel_out[lane] = sel_mine; w_out[lane] = p_mine / sum * scale; }
+    const float w_mine = p_mine / sum * scale;
+    if (keep >= topk) {
+        if (lane < topk) { sel_out[lane] = sel_mine; w_out[lane] = w_mine; }
+        return;
+    }
+    // rank of lane r's weight among the topk picks: heavier picks, then equal ones picked earlier
+    int rank = 0;
+    for (int j = 0; j < topk; ++j) {
+        const float o = __builtin_bit_cast(float, rdlane(__builtin_bit_cast(uint32_t, w_mine), j));
+        rank += (o > w_mine || (o == w_mine && j < lane)) ? 1 : 0;
+    }
+    const bool kept = lane < topk && rank < keep;
+    float f = 1.f; bool rescale = false;
+    if (renorm > 0.f) {
+        float sw = 0.0f;
+        for (int q = 0; q < keep; ++q) {   // the kept weights in kept order
+            const int l = first_lane(lane < topk && rank == q);
+            sw = sw + __builtin_bit_cast(float, rdlane(__builtin_bit_cast(uint32_t, w_mine), l));
+        }
+        if (sw > 1e-6f) { f = renorm / sw; rescale = true; }
+    }
+    if (kept) { sel_out[rank] = sel_mine; w_out[rank] = rescale ? w_mine * f : w_mine; }
 }
 // the same from the lane's 4 logits; probs_out (optional) receives the n_exp probabilities
 __device__ __forceinline__ void select_token(const float (&lg)[4], const float (&bias)[4], int n_exp, int n_group, int topk_group, int topk,
-                                             float scale, float * scr, int * sel_out, float * w_out, float * probs_out) {
+                                             float scale, float * scr, int * sel_out, float * w_out, float * probs_out,
+                                             int keep, float renorm) {
     const int lane = lane_id();
     float p[4];
 #pragma unroll
@@ -658,7 +683,7 @@ __device__ __forceinline__ void select_token(const float (&lg)[4], const float (
             if (probs_out) { gptr(probs_out)[e] = p[j]; }
         }
     }
-    select_token_p(p, bias, n_exp, n_group, topk_group, topk, scale, scr, sel_out, w_out);
+    select_token_p(p, bias, n_exp, n_group, topk_group, topk, scale, scr, sel_out, w_out, keep, renorm);
 }
 
 }  // namespace lk

@@ -12,9 +12,11 @@ hipError_t launch_quant_q8k(const float * x, int64_t nrows, int K, int8_t * q, f
 
 // router logits [n][n_exp] under the fp64 chunk contract (K % 256 == 0)
 hipError_t launch_router_logits(const float * W, const float * x, int n, int n_exp, int K, float * logits, hipStream_t st);
-// sigmoid, bias, grouped top-k, normalised weights; probs [n][n_exp], sel/wts [n][topk]
+// sigmoid, bias, grouped top-k, normalised weights; probs [n][n_exp], sel/wts [n][keep]: with 0 < keep < topk each
+// row keeps its keep heaviest picks (rescaled to sum to renorm when renorm > 0), else all topk
 hipError_t launch_router_select(const float * logits, const float * bias, int n, int n_exp, int n_group, int topk_group,
-                                int topk, float scale, float * probs, int * sel, float * wts, hipStream_t st);
+                                int topk, float scale, float * probs, int * sel, float * wts, hipStream_t st, int keep = 0,
+                                float renorm = 0.f);
 
 // stable counting sort of the P = n*topk pairs by expert: counts [n_exp], offsets [n_exp+1], perm/inv [P],
 // act = used experts ascending, nact = their number (device scalar)
@@ -52,6 +54,7 @@ struct DecodeArgs {
     int prenorm; const float * nw; float eps;        // prenorm: the block's input is RMSNorm(x) * nw (nw null: ones)
     const float * resid;                             // added to the block's output when not null ([n][E])
     const float * Wr; const float * bias; int n_exp, n_group, topk_group, topk; float scale;
+    int keep; float renorm;                          // experts kept per token (keep <= topk; the slots use keep), rescale
     const uint8_t * gate, * up, * down; size_t estride;   // routed experts (tiled), expert e at + e * estride
     const uint8_t * sh_gate, * sh_up, * sh_down;
     int E, H;                                        // 7168, 2048 (the kernel's geometry)
@@ -62,6 +65,8 @@ struct DecodeArgs {
     uint64_t * tlogits, * th, * to;
     float * y;                                       // [n][E]
     unsigned epoch; int * err;
+    int * herr;                                      // host-mapped copy of a reported error code (may be null): the
+                                                     // host sees a failed launch without synchronising
 };
 // sizes (64-bit words) of the tagged buffers for any n <= 8 (topk <= MAXK)
 constexpr size_t DEC_TLOGITS = 8 * 256, DEC_TH = (size_t) 8 * (MAXK + 1) * 2048,
@@ -86,6 +91,7 @@ struct PrefillArgs {
     float * out;                         // gate/up: h [P+n][R] (silu(g) * u); down: o [P+n][R]
     float * gdbg, * udbg;                // optional gate / up outputs
     int * err;                           // bit 4: the LDS base is not 64 KB aligned
+    int * herr;                          // host-mapped copy of the code (may be null)
 };
 hipError_t prefill_init();
 size_t prefill_table_bytes();

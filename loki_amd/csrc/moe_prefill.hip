@@ -12,9 +12,12 @@
 //     packed fp16 multiply per two weights. Every w is an integer of magnitude <= 43 * 31, exact in fp16.
 //   * The column's activations (the Q8_K integers as fp16, exact) are copied block by block into LDS with direct
 //     global->LDS loads, double-buffered; v_mfma_f32_16x16x32_f16 then forms, per 256-value block, the block sum
-//     bsum = sum_ib (2 s_ib + 1) sum_k g s q over a 16-token x 16-row tile. Products and partial sums are integers below
-//     2^24 in magnitude (|bsum| < 2^24 whenever the activations are Q8_K of real data: the worst case needs every
-//     product at its maximum), so the fp32 accumulation is exact and equals ggml's int32 block sum.
+//     bsum = sum_ib (2 s_ib + 1) sum_k g s q over a 16-token x 16-row tile, as two chains of four MFMA steps: steps
+//     0-3 cover sub-blocks 0, 2, 4, 6 (one per lane group) and steps 4-7 the odd ones. No codebook entry's 8 bytes
+//     sum above 203, so a chain's products and every partial sum are integers of magnitude at most
+//     16 * 203 * 31 * 127 = 12,787,376 < 2^24: each chain total is exact, whatever order the matrix core adds in. The
+//     block sum is then one fp32 addition of the two exact totals, i.e. the exact integer rounded to nearest even --
+//     exactly ggml's (float) of its int32 block sum, also where |bsum| exceeds 2^24 (up to 25.6 M).
 //   * Each output then advances in block order, y += (d_w * d_x) * bsum, and ends * 0.125: the fp32 operations and their
 //     order are those of ggml_vec_dot_iq2_xxs_q8_K, so every output is bit-identical to the CPU checker's.
 //   * Gate/up tiles write h = silu(g) * u per slot; down tiles write o per slot (the combine runs after).
@@ -147,7 +150,10 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
     LK_LOCAL uint8_t * lds = (LK_LOCAL uint8_t *) dyn_lds;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
     if (lds_addr(dyn_lds) & 0xFFFFu) {   // table addressing needs a 64 KB aligned base
-        if (threadIdx.x == 0) { __hip_atomic_fetch_or(gptr(a.err), 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+        if (threadIdx.x == 0) {
+            __hip_atomic_fetch_or(gptr(a.err), 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (a.herr) { __hip_atomic_store(gptr(a.herr), 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); }
+        }
         return;
     }
     // tables into LDS (direct loads), visible after vmcnt(0) + the first barrier
@@ -226,7 +232,7 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
             auto block = [&](int j, const PfW (&w)[C], int buf) {
                 static_assert((L_PB % 512) == 0 && (PB_BUF % 512) == 0, "XOR addressing inside 512-byte rows");
                 const uint32_t bx = ((uint32_t) (L_PB + buf * PB_BUF) + (uint32_t) ln.r * 512) | ((uint32_t) ((8 * ln.g) ^ ln.r) << 4);
-                f4 cc[C][NT];
+                f4 cc[C][NT], cd[C][NT];   // the two exact chains: steps 0-3, steps 4-7
                 h2v sc[C][2];
                 uint32_t ms[C][2];
 #pragma unroll
@@ -262,9 +268,13 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
                         const h8 gs = __builtin_bit_cast(h8, k.g[c] ^ k.s[c]);
                         const h2v s = sc[c][t >> 2];
                         const h8 wv = gs * (h8) { s[0], s[1], s[0], s[1], s[0], s[1], s[0], s[1] };
-                        cc[c][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k.x0, wv, t == 0 ? (f4) { 0.f, 0.f, 0.f, 0.f } : cc[c][0], 0, 0, 0);
-                        if (NT > 1) {
-                            cc[c][NT - 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k.x1, wv, t == 0 ? (f4) { 0.f, 0.f, 0.f, 0.f } : cc[c][NT - 1], 0, 0, 0);
+                        const f4 z = (f4) { 0.f, 0.f, 0.f, 0.f };
+                        if (t < 4) {
+                            cc[c][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k.x0, wv, t == 0 ? z : cc[c][0], 0, 0, 0);
+                            if (NT > 1) { cc[c][NT - 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k.x1, wv, t == 0 ? z : cc[c][NT - 1], 0, 0, 0); }
+                        } else {
+                            cd[c][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k.x0, wv, t == 4 ? z : cd[c][0], 0, 0, 0);
+                            if (NT > 1) { cd[c][NT - 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k.x1, wv, t == 4 ? z : cd[c][NT - 1], 0, 0, 0); }
                         }
                     }
                 };
@@ -277,49 +287,58 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
                     if (t + 2 < 8) { lookup(t + 2, ka); }
                     compute(t + 1, kb);
                 }
-                // block fold, in block order: y += (d_w * d_x) * bsum
+                // block fold, in block order: y += (d_w * d_x) * bsum, bsum = the two chains' exact totals added once
                 const f4 dx0 = *(const LK_LOCAL f4 *) (size_t) ((uint32_t) (L_PB + buf * PB_BUF + PB_DX) + 16 * ln.g);
                 const f4 dx1 = NT > 1 ? *(const LK_LOCAL f4 *) (size_t) ((uint32_t) (L_PB + buf * PB_BUF + PB_DX) + 64 + 16 * ln.g) : dx0;
 #pragma unroll
                 for (int c = 0; c < C; ++c) {
                     const float dw = h2f(w[c].d);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) { acc[c][0][i] = acc[c][0][i] + (dw * dx0[i]) * cc[c][0][i]; }
+                    for (int i = 0; i < 4; ++i) { acc[c][0][i] = acc[c][0][i] + (dw * dx0[i]) * (cc[c][0][i] + cd[c][0][i]); }
                     if (NT > 1) {
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) { acc[c][NT - 1][i] = acc[c][NT - 1][i] + (dw * dx1[i]) * cc[c][NT - 1][i]; }
+                        for (int i = 0; i < 4; ++i) { acc[c][NT - 1][i] = acc[c][NT - 1][i] + (dw * dx1[i]) * (cc[c][NT - 1][i] + cd[c][NT - 1][i]); }
                     }
                 }
                 (void) j;
             };
 
-            // pipeline: weights three blocks ahead (four register stages), activations one block ahead (registers, then
+            // pipeline: weights two blocks ahead (three register stages), activations one block ahead (registers, then
             // the other of two LDS buffers). Every step issues the same loads (indices clamped at the last blocks: those
             // copies land in registers nobody reads any more), so the compiler's waits count them exactly.
-            PfW w0[C], w1[C], w2[C], w3[C];
+            PfW w0[C], w1[C], w2[C];
             PfB bq;
             load_w(0, w0);
-            load_w(1 < NB ? 1 : NB - 1, w1);
-            load_w(2 < NB ? 2 : NB - 1, w2);
+            if (NB > 8) { load_w(1, w1); }
             load_b(0, bq);
             store_b(bq, 0);
             __syncthreads();
+            // short rows (down, 8 blocks) keep the weights one block ahead (two stages): their register budget is tighter
+            constexpr int WA = NB <= 8 ? 1 : 2;
             auto step = [&](int j, PfW (&cur)[C], PfW (&ahead)[C]) {
                 load_b(j + 1 < NB ? j + 1 : NB - 1, bq);
-                load_w(j + 3 < NB ? j + 3 : NB - 1, ahead);
+                load_w(j + WA < NB ? j + WA : NB - 1, ahead);
                 __builtin_amdgcn_sched_barrier(0);   // nothing of the block moves above the loads
                 block(j, cur, j & 1);
                 store_b(bq, (j + 1) & 1);           // buffer (j + 1) & 1 was last read in step j - 1, before its barrier
                 __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the writes are done before the barrier publishes them
                 __builtin_amdgcn_s_barrier();
             };
-            static_assert(NB % 4 == 0, "four steps per trip");
+            if constexpr (WA == 1) {   // step j uses stage j % 2 and refills the other with block j + 1
+                static_assert(NB % 2 == 0, "two steps per trip");
 #pragma unroll 1
-            for (int j = 0; j < NB; j += 4) {
-                step(j, w0, w3);
-                step(j + 1, w1, w0);
-                step(j + 2, w2, w1);
-                step(j + 3, w3, w2);
+                for (int j = 0; j < NB; j += 2) { step(j, w0, w1); step(j + 1, w1, w0); }
+            } else {                   // step j uses stage j % 3 and refills the stage of block j - 1 with block j + 2
+                constexpr int NB3 = NB - NB % 3;
+                int j = 0;
+#pragma unroll 1
+                for (; j < NB3; j += 3) {
+                    step(j, w0, w2);
+                    step(j + 1, w1, w0);
+                    step(j + 2, w2, w1);
+                }
+                if (NB % 3 >= 1) { step(j, w0, w2); }
+                if (NB % 3 == 2) { step(j + 1, w1, w0); }
             }
 
             // outputs: lane (r, g) holds tokens 4 g + i of each token tile for row r of each of its tiles

@@ -226,9 +226,10 @@ hipError_t launch_router_logits(const float * W, const float * x, int n, int n_e
     return hipGetLastError();
 }
 
-// one wave per token; lane l holds experts 4l..4l+3 (n_exp <= 256); the rule is select_token's (moe_device.h)
+// one wave per token; lane l holds experts 4l..4l+3 (n_exp <= 256); the rule is select_token's (moe_device.h), with
+// keep entries per token written (keep = topk: all of them)
 __global__ void __launch_bounds__(64) k_router_select(const float * __restrict__ logits, const float * __restrict__ bias, int n, int n_exp,
-                                                      int n_group, int topk_group, int topk, float scale,
+                                                      int n_group, int topk_group, int topk, float scale, int keep, float renorm,
                                                       float * __restrict__ probs, int * __restrict__ sel, float * __restrict__ wts) {
     __shared__ float scr[NEXP_MAX + 2 * 64];
     __shared__ int so[MAXK]; __shared__ float wo[MAXK];
@@ -237,18 +238,20 @@ __global__ void __launch_bounds__(64) k_router_select(const float * __restrict__
     load_bias(bias, n_exp, bv);
 #pragma unroll
     for (int j = 0; j < 4; ++j) { const int e = 4 * lane + j; lg[j] = e < n_exp ? logits[(size_t) t * n_exp + e] : 0.f; }
-    select_token(lg, bv, n_exp, n_group, topk_group, topk, scale, scr, so, wo, probs ? probs + (size_t) t * n_exp : nullptr);
+    select_token(lg, bv, n_exp, n_group, topk_group, topk, scale, scr, so, wo, probs ? probs + (size_t) t * n_exp : nullptr, keep, renorm);
     lds_visible();
-    if (lane < topk) { sel[(size_t) t * topk + lane] = so[lane]; wts[(size_t) t * topk + lane] = wo[lane]; }
+    if (lane < keep) { sel[(size_t) t * keep + lane] = so[lane]; wts[(size_t) t * keep + lane] = wo[lane]; }
 }
 
 hipError_t launch_router_select(const float * logits, const float * bias, int n, int n_exp, int n_group, int topk_group,
-                                int topk, float scale, float * probs, int * sel, float * wts, hipStream_t st) {
+                                int topk, float scale, float * probs, int * sel, float * wts, hipStream_t st, int keep, float renorm) {
     if (n <= 0) { return hipSuccess; }
-    if (n_exp > NEXP_MAX || n_exp % n_group || topk > MAXK || topk_group > n_group || topk > topk_group * (n_exp / n_group) || n_exp / n_group < 2 || n_group > 64) {
+    if (keep <= 0) { keep = topk; }
+    if (n_exp > NEXP_MAX || n_exp % n_group || topk > MAXK || topk_group > n_group || topk > topk_group * (n_exp / n_group) ||
+        n_exp / n_group < 2 || n_group > 64 || keep > topk) {
         return hipErrorInvalidValue;
     }
-    k_router_select<<<n, 64, 0, st>>>(logits, bias, n, n_exp, n_group, topk_group, topk, scale, probs, sel, wts);
+    k_router_select<<<n, 64, 0, st>>>(logits, bias, n, n_exp, n_group, topk_group, topk, scale, keep, renorm, probs, sel, wts);
     return hipGetLastError();
 }
 

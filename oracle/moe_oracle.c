@@ -231,6 +231,38 @@ int or_router(const float * W, const float * bias, const float * x, int64_t n, i
     return rc;
 }
 
+/* ---------------------------------------------------------------- keep-KE (the engine's narrow host dispatch)
+ * src/server_core_fused.cpp:793-815: each row's topk (sel, w) are ordered by weight, descending -- std::sort over 8
+ * indices with `w[a] > w[b]`, which for ranges this short is an insertion sort in the standard libraries (libstdc++
+ * below 16 elements, MSVC below 32), so equal weights keep their k order -- and the first ke are kept in that order.
+ * renorm > 0 (RENORM_EXPERTS, on by default, :811 with the literal 2.5): sw = the kept weights summed in kept order in
+ * fp32; if sw > 1e-6f every kept weight is multiplied by f = renorm / sw. Rows >= n_pad (fixed-width pass padding,
+ * :815) take row 0's kept experts at weight 0. */
+int or_keep_experts(const int32_t * sel, const float * w, int64_t n, int topk, int ke, float renorm, int64_t n_pad,
+                    int32_t * sel_out, float * w_out) {
+    if (topk <= 0 || topk > 64 || ke <= 0 || ke > topk || n < 0) { return -1; }
+    for (int64_t i = 0; i < n; ++i) {
+        int ord[64];
+        for (int k = 0; k < topk; ++k) { ord[k] = k; }
+        for (int a = 1; a < topk; ++a) {   /* insertion sort, strict comparison: stable */
+            const int v = ord[a]; int b = a;
+            while (b > 0 && w[i * topk + v] > w[i * topk + ord[b - 1]]) { ord[b] = ord[b - 1]; --b; }
+            ord[b] = v;
+        }
+        for (int k = 0; k < ke; ++k) { sel_out[i * ke + k] = sel[i * topk + ord[k]]; w_out[i * ke + k] = w[i * topk + ord[k]]; }
+        if (renorm > 0.f) {
+            float sw = 0.0f;
+            for (int k = 0; k < ke; ++k) { sw += w_out[i * ke + k]; }
+            if (sw > 1e-6f) { const float f = renorm / sw; for (int k = 0; k < ke; ++k) { w_out[i * ke + k] *= f; } }
+        }
+    }
+    for (int64_t i = n_pad; i < n; ++i) {
+        if (i < 1) { continue; }
+        for (int k = 0; k < ke; ++k) { sel_out[i * ke + k] = sel_out[k]; w_out[i * ke + k] = 0.0f; }
+    }
+    return 0;
+}
+
 /* ---------------------------------------------------------------- dispatch (mul_mat_id row mapping)
  * For each token t ascending and k ascending, pair (t, k) is appended to its expert's list (the order of
  * ggml_compute_forward_mul_mat_id's matrix_rows and of the reference's byexp, src/server_core_fused.cpp:937). */

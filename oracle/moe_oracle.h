@@ -36,6 +36,11 @@ float or_router_logit(const float * w, const float * x, int64_t k);
  * wts [n][topk] = p[sel] / max(sum p[sel], 2^-14) * scale. Ties go to the lower index (groups and experts). */
 int or_router(const float * W, const float * bias, const float * x, int64_t n, int n_exp, int64_t k,
               int n_group, int topk_group, int topk, float scale, float * logits, float * probs, int32_t * sel, float * wts);
+/* keep-KE of the engine's narrow dispatch (src/server_core_fused.cpp:793-815): per row the ke largest weights, stably
+ * ordered by weight descending, optionally rescaled so they sum to renorm (renorm <= 0: off); rows >= n_pad take row
+ * 0's kept experts at weight 0. sel_out / w_out [n][ke]. */
+int or_keep_experts(const int32_t * sel, const float * w, int64_t n, int topk, int ke, float renorm, int64_t n_pad,
+                    int32_t * sel_out, float * w_out);
 /* stable counting sort of the n*topk (token, k) pairs by expert; perm[j] = t*topk + k */
 int or_dispatch(const int32_t * sel, int64_t n, int topk, int n_exp, int32_t * counts, int32_t * offsets, int32_t * perm);
 

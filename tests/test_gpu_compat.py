@@ -209,3 +209,47 @@ def test_wide_pass(ctx, small_layer):
     lib().fl_wide_skip(ctx.ctx, cptr(mo), n, ctypes.byref(out))
     hs = np.ctypeslib.as_array(out.h, shape=(n * E,)).reshape(n, E).copy()
     assert np.array_equal(hs.view(np.uint32), (base + mo).astype(np.float32).view(np.uint32))
+
+
+def test_narrow_pass_keep2_with_pad_rows(ctx, small_layer):
+    """The engine's production decode call (src/server_core_fused.cpp:793-818, KE = 2 at :340): a fixed-width pass of
+    8 rows whose last 3 are padding. fl_fetch's routing goes through the host keep-2 with the 2.5 rescale, pad rows take
+    row 0's kept experts at weight 0, the used experts become the arena, and fl_moe runs KE = 2. h and moe follow
+    moe_combine's ascending-slot order with merged weights (src/fused_layer.cu:366-372)."""
+    from loki_amd import FLOut, lib
+    (W, b, gate, up, down, sh), dev = small_layer
+    ctx.set_routing(8, 4, 8, 2.5)
+    n, n_real, ke = 8, 5, 2
+    x = gen.uniform(9, 3, (n, E), 2.0); fi = gen.uniform(9, 4, (n, E), 1.0)
+    flw = _flw(dev)
+    ctx.check(lib().fl_ffn_begin(ctx.ctx, ctypes.byref(flw), n, cptr(x), cptr(fi), -1))
+    out = FLOut()
+    lib().fl_fetch(ctx.ctx, n, 1, ctypes.byref(out))
+    sel = np.ctypeslib.as_array(out.sel, shape=(n * KE,)).reshape(n, KE).copy()
+    wts = np.ctypeslib.as_array(out.wts, shape=(n * KE,)).reshape(n, KE).copy()
+    _, _, so, wo = orc.router(W, b, x, 8, 4, 8, 2.5)
+    assert np.array_equal(sel, so) and np.array_equal(wts.view(np.uint32), wo.view(np.uint32))
+    sk, wk = orc.keep_experts(sel, wts, ke, 2.5, n_real)
+    assert np.all(wk[n_real:] == 0) and np.all(sk[n_real:] == sk[0])
+    used = sorted(set(sk.ravel().tolist()))
+    remap = {e: i for i, e in enumerate(used)}
+    ids = np.array([[remap[e] for e in row] for row in sk], np.int32)
+    ga, ua, da = _arena(dev, used)
+    lib().fl_moe(ctx.ctx, ga.data_ptr(), ua.data_ptr(), da.data_ptr(), len(used), 4, cptr(ids), cptr(f32(wk)), ke, n, ctypes.byref(out))
+    h = np.ctypeslib.as_array(out.h, shape=(n * E,)).reshape(n, E).copy()
+    moe = np.ctypeslib.as_array(out.moe, shape=(n * E,)).reshape(n, E).copy()
+    ref = orc.moe_experts(x, sk, wk, gate, up, down, *sh, want=("o", "sh"), n_exp=16)
+    o = ref["o"].reshape(n, ke, E)
+    for t in range(n):
+        v = np.zeros(E, np.float32)
+        for m in range(len(used)):
+            ks = [k for k in range(ke) if ids[t, k] == m]
+            if not ks:
+                continue
+            wt = np.float32(0)
+            for k in ks:
+                wt = np.float32(wt + wk[t, k])
+            v = (v + wt * o[t, ks[0]]).astype(np.float32)
+        assert np.array_equal(moe[t].view(np.uint32), v.view(np.uint32)), t
+        want = ((v + ref["sh"][t]).astype(np.float32) + fi[t]).astype(np.float32)
+        assert np.array_equal(h[t].view(np.uint32), want.view(np.uint32)), t

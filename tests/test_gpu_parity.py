@@ -7,7 +7,8 @@ probabilities, selections, weights, dispatch, gate/up/h, down outputs and the bl
 import numpy as np
 import pytest
 
-from tests._helpers import E, H, NEXP, host_layer, make_layer, make_x, numpy_pack_tiled, rel_errors, iq2_bytes
+from tests._helpers import (E, H, NEXP, adversarial_iq2, host_layer, iq2_bytes, make_layer, make_x, numpy_pack_tiled,
+                            rel_errors, sign_pattern_even)
 from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -65,8 +66,8 @@ def test_pack_layout(ctx):
     assert np.array_equal(t2.cpu().numpy(), t.cpu().numpy())
 
 
-# n covers every logit kernel: per-wave (< 16), 16-token pairs (16..63), 32 x 16 tiles (64..1023) and 32 x 32 tiles
-# (>= 1024), with ragged last tiles
+# n covers every logit kernel: one workgroup per expert (k_router_wg, n < 256), 4 x 2 register tiles (256..1023) and
+# 4 x 4 tiles (>= 1024), with ragged last tiles
 @pytest.mark.parametrize("n,rule", [(1, (8, 4)), (8, (8, 4)), (21, (8, 4)), (64, (8, 4)), (77, (8, 4)), (300, (8, 4)), (1037, (8, 4)),
                                     (8, (1, 1))])
 def test_router_bitwise(ctx, layer, n, rule):
@@ -128,8 +129,7 @@ def _block_vs_oracle(ctx, layer, x, tokens, capture=True):
 def test_block_decode_bitwise(ctx, layer, n):
     x = make_x(ctx, n, seed=200 + n)
     tokens = np.arange(n)
-    ctx.set_fused(False)   # the per-pass kernels keep their intermediates in plain buffers
-    try:
+    with ctx.using_fused(0):   # the per-pass kernels keep their intermediates in plain buffers
         y, ref, dbg = _block_vs_oracle(ctx, layer, x, tokens)
         mx, l2 = rel_errors(y, ref["y"])
         assert mx <= MAX_REL and l2 <= L2_REL, (mx, l2)
@@ -143,13 +143,19 @@ def test_block_decode_bitwise(ctx, layer, n):
         assert np.array_equal(o[inv].view(np.uint32), ref["o"].view(np.uint32))
         assert np.array_equal(o[P:].view(np.uint32), ref["sh"].view(np.uint32))
         assert np.array_equal(y.view(np.uint32), ref["y"].view(np.uint32)), "block output not bit-identical (max rel %.3g)" % mx
-    finally:
-        ctx.set_fused(True)
-    # the single-launch decode block on the same rows
-    yf = ctx.moe_layer(layer, x)
-    ctx.sync()
-    assert ctx.debug().fused == 1
-    assert np.array_equal(yf.cpu().numpy()[tokens].view(np.uint32), ref["y"].view(np.uint32))
+    # the single-launch decode block on the same rows: regular launch (mode 2, the library default and what bench.py
+    # times) and cooperative launch (mode 1); routing outputs too
+    W, b = layer.gate_inp.cpu().numpy(), layer.probs_b.cpu().numpy()
+    _, _, so, wo = orc.router(W, b, x.cpu().numpy())
+    for mode in (2, 1):
+        with ctx.using_fused(mode):
+            yf = ctx.moe_layer(layer, x)
+            ctx.sync()
+            assert ctx.debug().fused == 1
+            st = _routing_state(ctx, n)
+        assert np.array_equal(yf.cpu().numpy()[tokens].view(np.uint32), ref["y"].view(np.uint32)), mode
+        assert np.array_equal(st["sel"], so.ravel()), mode
+        assert np.array_equal(st["wts"].view(np.uint32), wo.ravel().view(np.uint32)), mode
 
 
 def test_block_prefill512_rows(ctx):
@@ -218,39 +224,44 @@ def _routing_state(ctx, n):
     return out
 
 
+@pytest.mark.parametrize("mode", [2, 1])
 @pytest.mark.parametrize("n", [1, 2, 5, 8])
-def test_fused_decode_matches_per_pass(ctx, layer, n):
-    """The single-launch decode block and the per-pass kernels give bit-identical outputs and routing."""
+def test_fused_decode_matches_per_pass(ctx, layer, n, mode):
+    """The single-launch decode block (regular or cooperative launch) and the per-pass kernels give bit-identical
+    outputs and routing."""
     x = make_x(ctx, n, seed=300 + n)
-    try:
-        ctx.set_fused(False)
+    with ctx.using_fused(0):
         y_ref = ctx.moe_layer(layer, x).clone()
         ctx.sync()
         ref = _routing_state(ctx, n)
-        ctx.set_fused(True)
+    with ctx.using_fused(mode):
         y = ctx.moe_layer(layer, x)
         ctx.sync()
+        assert ctx.debug().fused == 1
         got = _routing_state(ctx, n)
-    finally:
-        ctx.set_fused(True)
     for k in ref:
         assert np.array_equal(np.asarray(got[k]).view(np.uint8), np.asarray(ref[k]).view(np.uint8)), k
     assert np.array_equal(y.cpu().numpy().view(np.uint32), y_ref.cpu().numpy().view(np.uint32))
 
 
-def test_fused_decode_repeated_launches(ctx, layer):
-    """Epoch flags and self-resetting counters: a sequence of launches with changing batch sizes stays exact."""
+@pytest.mark.parametrize("mode", [2, 1])
+def test_fused_decode_repeated_launches(ctx, layer, mode):
+    """Epoch flags and self-resetting counters: a sequence of launches with changing batch sizes stays exact, both
+    back to back without a host wait in between and with one after every launch."""
     xs = {n: make_x(ctx, n, seed=400 + n) for n in (1, 3, 8)}
     want = {}
-    try:
-        ctx.set_fused(False)
+    with ctx.using_fused(0):
         for n, x in xs.items():
             want[n] = ctx.moe_layer(layer, x).cpu().numpy()
-    finally:
-        ctx.set_fused(True)
-    for n in (1, 8, 3, 1, 1, 8, 3, 8):
-        y = ctx.moe_layer(layer, xs[n])
+    order = (1, 8, 3, 1, 1, 8, 3, 8)
+    with ctx.using_fused(mode):
+        for n in order:
+            y = ctx.moe_layer(layer, xs[n])
+            ctx.sync()
+            assert np.array_equal(y.cpu().numpy().view(np.uint32), want[n].view(np.uint32)), n
+        ys = [ctx.moe_layer(layer, xs[n]) for n in order]
         ctx.sync()
+    for n, y in zip(order, ys):
         assert np.array_equal(y.cpu().numpy().view(np.uint32), want[n].view(np.uint32)), n
 
 
@@ -331,11 +342,207 @@ def test_prenorm_matches_separate_norm(ctx, layer, n, weighted):
     ctx.sync()
     ref4 = (y1.cpu().numpy() + h.cpu().numpy()).astype(np.float32)
     assert np.array_equal(y4.cpu().numpy().view(np.uint32), ref4.view(np.uint32))
-    if n == 1:   # the per-pass kernels take the same normalised input
-        ctx.set_fused(False)
-        try:
+    if n <= 8:   # the per-pass kernels take the same normalised input, with and without the residual
+        with ctx.using_fused(0):
             y3 = ctx.moe_layer_normed(layer, h, w, 1e-6)
+            y5 = ctx.moe_layer_normed(layer, h, w, 1e-6, residual=True)
             ctx.sync()
-        finally:
-            ctx.set_fused(True)
+            assert ctx.debug().fused == 0
         assert np.array_equal(y3.cpu().numpy().view(np.uint32), y2.cpu().numpy().view(np.uint32))
+        assert np.array_equal(y5.cpu().numpy().view(np.uint32), ref4.view(np.uint32))
+
+
+@pytest.mark.parametrize("n", [1, 8])
+def test_residual_reference_rule(ctx, layer, n):
+    """The reference's ungrouped routing rule (one group: the decode block's selection does not take it, so the
+    per-pass kernels run): the residual variant is (moe + shared) + h bit for bit, and moe + shared equals the checker."""
+    h = make_x(ctx, n, seed=620 + n) * 2.0
+    ctx.set_routing(1, 1, 8, 2.5)
+    try:
+        y0 = ctx.moe_layer_normed(layer, h)
+        y1 = ctx.moe_layer_normed(layer, h, residual=True)
+        xn = ctx.rmsnorm(h)
+        ctx.sync()
+        assert ctx.debug().fused == 0
+    finally:
+        ctx.set_routing()
+    hn = h.cpu().numpy()
+    ref = (y0.cpu().numpy() + hn).astype(np.float32)
+    assert np.array_equal(y1.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    xs = xn.cpu().numpy()
+    W, b = layer.gate_inp.cpu().numpy(), layer.probs_b.cpu().numpy()
+    _, _, so, _ = orc.router(W, b, xs, 1, 1, 8, 2.5)
+    _, _, gate, up, down, sh = host_layer(ctx, layer, so.ravel())
+    want = orc.moe_forward(xs, W, b, gate, up, down, *sh, n_group=1, topk_group=1)["y"]
+    assert np.array_equal(y0.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def _hot_ids(seed):
+    """16 hot experts drawn the way bench.py draws them for prefill-2048."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    return torch.randperm(NEXP, generator=g)[:16].tolist()
+
+
+def _margins(probs, bias, n_group=8, topk_group=4, topk=8):
+    """Smallest gap between the topk-th and the next eligible biased score, and between the kept and the next group."""
+    c = (probs + bias[None, :]).astype(np.float32)
+    n = c.shape[0]
+    g = np.sort(c.reshape(n, n_group, -1), axis=2)[:, :, ::-1]
+    gs = (g[:, :, 0] + g[:, :, 1]).astype(np.float32)
+    gsort = -np.sort(-gs, axis=1)
+    keep = gs >= gsort[:, topk_group - 1:topk_group]
+    ce = np.where(np.repeat(keep, c.shape[1] // n_group, axis=1), c, -np.inf)
+    cs = -np.sort(-ce, axis=1)
+    return float(np.min(cs[:, topk - 1] - cs[:, topk])), float(np.min(gsort[:, topk_group - 1] - gsort[:, topk_group]))
+
+
+@pytest.mark.parametrize("n,hot", [(512, False), (2048, True)])
+def test_routing_all_rows_prefill(ctx, n, hot):
+    """configs[2] (512 tokens, bias sigma 0.05) and configs[4] (2048 tokens, +0.5 on 16 hot experts): the routing of
+    every row through fl_moe_layer -- selections, weights, the dispatch permutation and its inverse, counts, offsets and
+    the active-expert list -- is bit-identical to the checker's router and dispatch. Output rows of the most and the least
+    hot-routed tokens are bit-identical to the checker's block as well."""
+    hot_ids = _hot_ids(20260101) if hot else None
+    layer = make_layer(ctx, seed=20260101 + n, bias_sigma=0.05, hot=hot_ids)
+    x = make_x(ctx, n, seed=7000 + n)
+    y = ctx.moe_layer(layer, x)
+    ctx.sync()
+    st = _routing_state(ctx, n)
+    W, b = layer.gate_inp.cpu().numpy(), layer.probs_b.cpu().numpy()
+    xs = x.cpu().numpy()
+    _, po, so, wo = orc.router(W, b, xs)
+    co, oo, pe = orc.dispatch(so)
+    invo = np.empty_like(pe); invo[pe] = np.arange(pe.size, dtype=np.int32)
+    used = np.nonzero(co)[0]
+    assert np.array_equal(st["sel"], so.ravel())
+    assert np.array_equal(st["wts"].view(np.uint32), wo.ravel().view(np.uint32))
+    assert np.array_equal(st["perm"], pe)
+    assert np.array_equal(st["inv"], invo)
+    assert np.array_equal(st["counts"], co)
+    assert np.array_equal(st["offsets"], oo)
+    assert int(st["nact"][0]) == used.size and np.array_equal(st["act"], used)
+    km, gm = _margins(po, b)
+    print("routing margins n=%d hot=%s: top-8 gap %.3g, group gap %.3g" % (n, hot, km, gm))
+    if hot:
+        nhot = np.isin(so, hot_ids).sum(axis=1)
+        order = np.argsort(nhot, kind="stable")
+        rows = np.concatenate([order[:4], order[-4:]])
+        assert nhot[order[-1]] > nhot[order[0]]
+    else:
+        rows = np.array([0, 3, 200, 511])
+    _, _, gate, up, down, sh = host_layer(ctx, layer, so[rows].ravel())
+    ref = orc.moe_forward(xs[rows], W, b, gate, up, down, *sh)
+    assert np.array_equal(y.cpu().numpy()[rows].view(np.uint32), ref["y"].view(np.uint32))
+
+
+def test_stack58_routing(ctx):
+    """all 58 independently seeded layers resident (~170 GB), one token chained through them with the norm
+    inside each next layer's launch. Every layer's routing (selections and weights) is bit-identical to the checker's
+    router on that layer's own input, RMSNorm(y_{L-1}) from the separate device norm (bit-identical to the fused one)."""
+    import torch
+    nl = 58
+    layers = [make_layer(ctx, seed=20260301 + 1000 * L) for L in range(nl)]
+    x = make_x(ctx, 1, seed=2001)
+    prev = None
+    kmin = np.inf
+    try:
+        for L, layer in enumerate(layers):
+            if prev is None:
+                xin = x
+                y = ctx.moe_layer(layer, x)
+            else:
+                xin = ctx.rmsnorm(prev)
+                y = ctx.moe_layer_normed(layer, prev)
+            ctx.sync()
+            assert ctx.debug().fused == 1
+            st = _routing_state(ctx, 1)
+            W, b = layer.gate_inp.cpu().numpy(), layer.probs_b.cpu().numpy()
+            _, po, so, wo = orc.router(W, b, xin.cpu().numpy())
+            assert np.array_equal(st["sel"], so.ravel()), L
+            assert np.array_equal(st["wts"].view(np.uint32), wo.ravel().view(np.uint32)), L
+            kmin = min(kmin, _margins(po, b)[0])
+            prev = y
+        print("stack routing: smallest top-8 gap over 58 layers %.3g" % kmin)
+    finally:
+        del layers
+        torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("n,mode", [(1, 2), (8, 2), (8, 0), (40, 2)])
+def test_keep2_layer_bitwise(ctx, layer, n, mode):
+    """The reference engine's production setting: each row keeps its 2 heaviest experts, rescaled to 2.5
+    (src/server_core_fused.cpp:793-813, KE = 2 at :340). fl_moe_layer with fl_set_keep(2, 2.5) -- inside the single
+    decode launch (mode 2), on the per-pass kernels (mode 0) and on the MFMA grouped GEMMs (n = 40) -- gives the
+    checker's router -> keep_experts -> expert block bit for bit, kept selections and weights included."""
+    x = make_x(ctx, n, seed=900 + n)
+    ctx.set_keep(2, 2.5)
+    try:
+        with ctx.using_fused(mode):
+            y = ctx.moe_layer(layer, x)
+            ctx.sync()
+            dbg = ctx.debug()
+            assert dbg.P == 2 * n and dbg.topk == 2
+            assert dbg.fused == (1 if (mode and n <= 8) else 0)
+            sel = ctx.d2h(dbg.sel, (n, 2), np.int32); wts = ctx.d2h(dbg.wts, (n, 2), np.float32)
+    finally:
+        ctx.set_keep(0)
+    xs = x.cpu().numpy()
+    W, b = layer.gate_inp.cpu().numpy(), layer.probs_b.cpu().numpy()
+    _, _, so, wo = orc.router(W, b, xs)
+    sk, wk = orc.keep_experts(so, wo, 2, 2.5)
+    assert np.array_equal(sel, sk)
+    assert np.array_equal(wts.view(np.uint32), wk.view(np.uint32))
+    rows = np.arange(n) if n <= 8 else np.array([0, 1, 17, 39])
+    _, _, gate, up, down, sh = host_layer(ctx, layer, sk[rows].ravel())
+    ref = orc.moe_experts(xs[rows], sk[rows], wk[rows], gate, up, down, *sh)
+    assert np.array_equal(y.cpu().numpy()[rows].view(np.uint32), ref["y"].view(np.uint32))
+
+
+@pytest.mark.parametrize("n", [16, 40])
+def test_prefill_mfma_exact_on_extreme_blocks(ctx, n):
+    """Blocks at the format's extreme (scale nibble 15, the codebook's largest entries, signs aligned with the tokens,
+    |q| = 127): every block sum of the routed gate rows is odd and above 2^24 in magnitude. The MFMA grouped GEMM
+    (two exact four-step chains per block, one fp32 addition) gives the gate outputs of ggml's int32 block sums --
+    bit-identical to the per-pass integer kernels and to the checker -- for a 16-slot and a 32 + 8-slot column."""
+    import torch
+    from loki_amd import MoeLayerWeights
+    base = make_layer(ctx, seed=31337)
+    chosen = [0, 1, 32, 33, 64, 65, 96, 97]          # two per group in groups 0..3: every token routes to them
+    pattern = sign_pattern_even(E, 5)
+    mb = iq2_bytes(H, E)
+    gate = base.gate.clone()
+    for i, e in enumerate(chosen):
+        w, sums = adversarial_iq2(H, E, 100 + i, pattern)
+        assert (sums * 3937).min() > (1 << 24)
+        ctx.pack(torch.from_numpy(w).cuda(), H, E, 1, dst=gate[e * mb:(e + 1) * mb])
+    W = torch.zeros_like(base.gate_inp)
+    b = torch.zeros_like(base.probs_b); b[chosen] = 1.0
+    layer = MoeLayerWeights(W, b, gate, base.up, base.down, base.sh_gate, base.sh_up, base.sh_down)
+    scale = np.linspace(0.5, 2.0, n, dtype=np.float32)[:, None]
+    x = torch.from_numpy(np.ascontiguousarray(pattern[None, :] * scale)).cuda()
+    ref = _prefill_state(ctx, layer, x, False)
+    got = _prefill_state(ctx, layer, x, True)
+    for k in ("g", "u", "h", "hq", "hd", "o", "y"):
+        assert np.array_equal(got[k].view(np.uint8), ref[k].view(np.uint8)), k
+    # the checker on two tokens (their gate rows are the extreme ones)
+    tokens = np.array([0, n - 1])
+    xs = x.cpu().numpy()[tokens]
+    Wn, bn = W.cpu().numpy(), b.cpu().numpy()
+    _, _, so, _ = orc.router(Wn, bn, xs)
+    assert set(so.ravel().tolist()) == set(chosen)
+    _, _, gt, up, down, sh = host_layer(ctx, layer, so.ravel())
+    want = orc.moe_forward(xs, Wn, bn, gt, up, down, *sh, want=("g",))
+    with ctx.using_fused(0):
+        ctx.set_prefill_mfma(True)
+        ctx.set_debug(True)
+        try:
+            ctx.moe_layer(layer, x)
+            ctx.sync()
+            dbg = ctx.debug()
+            inv = ctx.d2h(dbg.inv, (n * 8,), np.int32)
+            g = ctx.d2h(dbg.g, (n * 9, H), np.float32)
+        finally:
+            ctx.set_debug(False)
+    for i, t in enumerate(tokens):
+        assert np.array_equal(g[inv[t * 8:(t + 1) * 8]].view(np.uint32), want["g"][i * 8:(i + 1) * 8].view(np.uint32)), t

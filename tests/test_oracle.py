@@ -266,6 +266,60 @@ def test_dispatch_rejects_out_of_range():
         orc.dispatch(np.array([[0, 256]], np.int32))
 
 
+# ---------------------------------------------------------------- keep-KE (engine narrow dispatch)
+def _keep_brute(sel, w, ke, renorm, n_pad):
+    """Pure-Python statement of eng:793-815: order the k of a row by weight descending with equal weights in k order
+    (what a stable insertion sort with `w[a] > w[b]` leaves), keep the first ke, sum them in that order in fp32 and
+    multiply each by f = renorm / sum when the sum exceeds 1e-6; pad rows copy row 0's kept experts at weight 0."""
+    n, topk = sel.shape
+    so = np.empty((n, ke), np.int32); wo = np.empty((n, ke), np.float32)
+    for i in range(n):
+        order = sorted(range(topk), key=lambda k: (-float(w[i, k]), k))[:ke]
+        so[i] = sel[i, order]; wo[i] = w[i, order]
+        if renorm > 0:
+            sw = np.float32(0)
+            for k in range(ke):
+                sw = np.float32(sw + wo[i, k])
+            if sw > np.float32(1e-6):
+                f = np.float32(np.float32(renorm) / sw)
+                wo[i] = (wo[i] * f).astype(np.float32)
+    for i in range(max(n_pad, 1), n):
+        so[i] = so[0]; wo[i] = 0
+    return so, wo
+
+
+@pytest.mark.parametrize("ke,renorm", [(2, 2.5), (1, 2.5), (4, 2.5), (2, 0.0), (8, 2.5)])
+def test_keep_experts_matches_brute_force(ke, renorm):
+    rng = np.random.default_rng(ke * 7 + int(renorm))
+    n = 40
+    sel = np.stack([rng.choice(256, 8, replace=False) for _ in range(n)]).astype(np.int32)
+    w = rng.uniform(0.01, 0.8, (n, 8)).astype(np.float32)
+    w[3, :] = 0.3125                          # all weights equal: k order
+    w[4, [1, 6]] = w[4].max() + 0.25          # a tie at the top: the lower k first
+    w[5, :] = 0.0                             # sum below the threshold: no rescale
+    for n_pad in (n, 33):
+        so, wo = orc.keep_experts(sel, w, ke, renorm, n_pad)
+        bs, bw = _keep_brute(sel, w, ke, renorm, n_pad)
+        assert np.array_equal(so, bs)
+        assert np.array_equal(wo.view(np.uint32), bw.view(np.uint32))
+    so, wo = orc.keep_experts(sel, w, ke, renorm)
+    assert list(so[4][:2]) == [sel[4, 1], sel[4, 6]][:min(ke, 2)] or ke == 1 and so[4][0] == sel[4, 1]
+    assert np.all(wo[5] == 0)
+    if renorm > 0:   # the kept weights carry the routed scale (within the fp32 rounding of the rescale)
+        rows = [i for i in range(n) if i != 5]
+        assert np.allclose(wo[rows].sum(axis=1, dtype=np.float64), renorm, rtol=ke * 2e-7)
+
+
+def test_keep_experts_is_top_ke_set():
+    """Invariant independent of the ordering rule: the kept weights are the ke largest of the row."""
+    rng = np.random.default_rng(5)
+    sel = np.tile(np.arange(8, dtype=np.int32), (200, 1))
+    w = rng.uniform(0, 1, (200, 8)).astype(np.float32)
+    so, wo = orc.keep_experts(sel, w, 3, 0.0)
+    assert np.array_equal(np.sort(wo, axis=1)[:, ::-1], -np.sort(-w, axis=1)[:, :3])
+    assert np.all(np.diff(wo, axis=1) <= 0)
+
+
 # ---------------------------------------------------------------- whole block
 def _rand_experts(rng, n_exp, E, H):
     def mat(rows, cols):
