@@ -121,6 +121,17 @@ int fl_moe_layer(FLCtx *, const FLMoeLayer * L, const float * x, int n, float * 
  * fl.cu:366-372); h and y must then not alias. */
 int fl_moe_layer_normed(FLCtx *, const FLMoeLayer * L, const float * ffn_norm, float eps, const float * h, int n,
                         int residual, float * y);
+/* fl_moe_layer for one decode batch (1 <= n <= 8) that allocates no device memory. No counterpart in the reference: it
+ * is for callers that cannot allocate -- code under HIP graph capture, serving loops that forbid hipMalloc. Same
+ * arguments and result as fl_moe_layer (bit-identical y), under the context's routing rule and fl_set_keep. It runs the
+ * single-launch decode block (tiled IQ2_XXS, E 7168, H 2048, a routing rule the decode block takes: FL_ESCOPE
+ * otherwise) on a file-scope device array of 5,502,720 bytes that each GPU the library runs on holds until the
+ * process ends (routing outputs, epoch-tagged hand-off words, the table image, an error word), resolved per device by
+ * fl_init; it calls no hipMalloc / hipFree and clears that array with a kernel, never a memset. n above 8 is rejected
+ * with FL_ERANGE. Every call on one GPU shares that GPU's array, which keeps the last call's contents: calls that
+ * overlap on one GPU (two streams, two contexts, two threads) race and give wrong results. Device-side failures are
+ * reported through fl_sync on the context. FLDebug does not see this path's buffers. */
+int fl_moe_layer_noalloc(FLCtx *, const FLMoeLayer * L, const float * x, int n, float * y);
 /* router only: sel/w [n][topk] (device), logits/probs [n][n_exp] may be NULL */
 int fl_route_dev(FLCtx *, const float * gate_inp, const float * probs_b, const float * x, int n, int n_exp, int E,
                  float * logits, float * probs, int * sel, float * w);

@@ -126,7 +126,7 @@ ABI_SYMBOLS = [
     "fl_wide_outs", "fl_wide_skip", "fl_spec", "fl_sketch", "fl_fetch", "fl_moe", "fl_skip", "fl_h2d", "fl_wait_event",
     "fl_gpu_ms", "fl_ffn_begin", "fl_set_experts", "fl_set_routing", "fl_set_keep", "fl_set_shared_formats", "fl_set_layer_formats", "fl_kq_matvec_dev",
     "fl_gguf_open", "fl_gguf_close", "fl_gguf_n_tensors", "fl_gguf_tensor_name", "fl_gguf_tensor", "fl_gguf_tensor_at",
-    "fl_gguf_get_int", "fl_gguf_get_float", "fl_gguf_get_str", "fl_gguf_read", "fl_gguf_load_moe_layer", "fl_gguf_free_layer", "fl_moe_layer", "fl_moe_layer_normed", "fl_route_dev", "fl_dispatch_dev", "fl_quant_q8k_dev",
+    "fl_gguf_get_int", "fl_gguf_get_float", "fl_gguf_get_str", "fl_gguf_read", "fl_gguf_load_moe_layer", "fl_gguf_free_layer", "fl_moe_layer", "fl_moe_layer_normed", "fl_moe_layer_noalloc", "fl_route_dev", "fl_dispatch_dev", "fl_quant_q8k_dev",
     "fl_pack_iq2xxs", "fl_unpack_iq2xxs", "fl_rmsnorm_dev", "fl_synth_iq2xxs", "fl_synth_normal", "fl_probe_exp",
     "fl_debug", "fl_set_debug", "fl_set_fused", "fl_set_prefill_mfma", "fl_stream", "fl_set_stream", "fl_d2h", "fl_set_profile", "fl_stage_ms", "fl_sync", "fl_last_error", "fl_free",
 ]
@@ -177,6 +177,7 @@ def lib():
             "fl_set_prefill_mfma": (I, [P_, I]),
             "fl_moe_layer": (I, [P_, ctypes.POINTER(FLMoeLayer), P_, I, P_]),
             "fl_moe_layer_normed": (I, [P_, ctypes.POINTER(FLMoeLayer), P_, F, P_, I, I, P_]),
+            "fl_moe_layer_noalloc": (I, [P_, ctypes.POINTER(FLMoeLayer), P_, I, P_]),
             "fl_route_dev": (I, [P_, P_, P_, P_, I, I, I, P_, P_, P_, P_]),
             "fl_dispatch_dev": (I, [P_, P_, I, I, I, P_, P_, P_, P_, P_, P_]),
             "fl_quant_q8k_dev": (I, [P_, P_, I, I, P_, P_]),

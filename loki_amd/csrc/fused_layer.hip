@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -22,6 +23,60 @@ using namespace lk;
 [[noreturn]] static void out_of_scope(const char * fn) {
     std::fprintf(stderr, "[fused] %s: attention, speculation and sketches are not part of the MoE-block library\n", fn);
     std::exit(7);
+}
+
+// ================================================================ allocation-free decode (fl_moe_layer_noalloc)
+// Every device buffer the single-launch decode block needs beyond the caller's inputs and outputs, in one file-scope
+// array that each GPU holds from module load until the process ends. Byte offsets (256-aligned):
+namespace {
+constexpr size_t NA_ALIGN = 256;
+constexpr size_t na_up(size_t v) { return (v + NA_ALIGN - 1) / NA_ALIGN * NA_ALIGN; }
+constexpr int NA_MAXN = 8;                          // tokens per call (the decode block's batch)
+constexpr int NA_MAXP = NA_MAXN * MAXK;             // routed pairs per call
+constexpr size_t NA_TAB = 0;                                                   // LDS table image
+constexpr size_t NA_TLOG = na_up(NA_TAB + TAB_BYTES);                          // tagged probabilities
+constexpr size_t NA_TH = na_up(NA_TLOG + DEC_TLOGITS * 8);                     // tagged h
+constexpr size_t NA_TO = na_up(NA_TH + DEC_TH * 8);                            // tagged o
+constexpr size_t NA_ERR = na_up(NA_TO + DEC_TO * 8);                           // error word
+constexpr size_t NA_XQ = na_up(NA_ERR + 4);                                    // Q8_K of x
+constexpr size_t NA_XD = na_up(NA_XQ + (size_t) NA_MAXN * 7168);
+constexpr size_t NA_LOG = na_up(NA_XD + (size_t) NA_MAXN * 28 * 4);            // logits, probabilities
+constexpr size_t NA_PRB = na_up(NA_LOG + (size_t) NA_MAXN * NEXP_MAX * 4);
+constexpr size_t NA_SEL = na_up(NA_PRB + (size_t) NA_MAXN * NEXP_MAX * 4);     // routing and dispatch outputs
+constexpr size_t NA_WTS = na_up(NA_SEL + NA_MAXP * 4);
+constexpr size_t NA_PERM = na_up(NA_WTS + NA_MAXP * 4);
+constexpr size_t NA_INV = na_up(NA_PERM + NA_MAXP * 4);
+constexpr size_t NA_CNT = na_up(NA_INV + NA_MAXP * 4);
+constexpr size_t NA_OFF = na_up(NA_CNT + NEXP_MAX * 4);
+constexpr size_t NA_ACT = na_up(NA_OFF + (NEXP_MAX + 1) * 4);
+constexpr size_t NA_NACT = na_up(NA_ACT + NEXP_MAX * 4);
+constexpr size_t NA_BYTES = na_up(NA_NACT + 4);
+static_assert(NA_BYTES == 5502720, "the allocation-free entry point's documented scratch size (5.25 MiB per GPU)");
+constexpr size_t NA_CLEAR0 = NA_TLOG, NA_CLEAR1 = NA_XQ;   // the tagged words and the error word start at zero
+constexpr int NA_MAXDEV = 64;
+}  // namespace
+static __device__ __align__(256) uint8_t scratch[NA_BYTES];
+
+struct NaDev { uint8_t * ptr = nullptr; int resolved = 0; unsigned epoch = 0; int tab_built = 0; };
+static NaDev g_na[NA_MAXDEV];
+static std::mutex g_na_mu;
+
+// the device address of `scratch` on device dev (current), once per device; null if HIP cannot resolve it
+static uint8_t * na_resolve(int dev) {
+    if (dev < 0 || dev >= NA_MAXDEV) { return nullptr; }
+    std::lock_guard<std::mutex> lk(g_na_mu);
+    NaDev & d = g_na[dev];
+    if (!d.resolved) {
+        void * p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) { (void) hipGetLastError(); p = nullptr; }
+        d.ptr = (uint8_t *) p; d.resolved = 1;
+    }
+    return d.ptr;
+}
+
+// zero fill of 16-byte words (no memset node: the call may be captured into a graph)
+__global__ void __launch_bounds__(256) k_zero16(uint4 * p, size_t n) {
+    for (size_t i = (size_t) blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t) gridDim.x * 256) { p[i] = make_uint4(0, 0, 0, 0); }
 }
 
 // ================================================================ lifecycle
@@ -39,6 +94,7 @@ extern "C" FLCtx * fl_init(int kvp, int sc_cap) {
     } else {
         __atomic_store_n(c->herr, 0, __ATOMIC_RELEASE);
     }
+    (void) na_resolve(c->dev);   // the allocation-free entry point's scratch on this device
     return c;
 }
 
@@ -480,6 +536,76 @@ extern "C" int fl_moe_layer_normed(FLCtx * c, const FLMoeLayer * L, const float 
                                    int residual, float * y) {
     if (c && residual && h == y) { return fail(c, FL_EINVAL, "h and y must not alias when the residual is added"); }
     return moe_layer(c, L, h, n, y, true, ffn_norm, eps, residual ? h : nullptr);
+}
+
+// fl_moe_layer for decode batches with no device allocation: the single-launch decode block on the file-scope scratch of
+// the context's device (routing outputs, tagged hand-off words, table image, error word) instead of the context's
+// buffers. The epoch that tags the hand-off words is per device, so calls from any context on one device follow one
+// sequence; calls that overlap on one device race on the scratch.
+extern "C" int fl_moe_layer_noalloc(FLCtx * c, const FLMoeLayer * L, const float * x, int n, float * y) {
+    if (!c) { return FL_EINVAL; }
+    if (!L || !x || !y) { return fail(c, FL_EINVAL, "null layer, x or y"); }
+    if (n < 1 || n > NA_MAXN) { return fail(c, FL_ERANGE, "fl_moe_layer_noalloc: n = %d outside 1..%d (its scratch holds one decode batch)", n, NA_MAXN); }
+    if (L->layout != FL_LAYOUT_TILED || L->E != 7168 || L->H != 2048) {
+        return fail(c, FL_ESCOPE, "fl_moe_layer_noalloc runs the decode block only: tiled IQ2_XXS, E 7168, H 2048");
+    }
+    for (int i = 0; i < 4; ++i) { if (c->lf[i] != FL_IQ2) { return fail(c, FL_ESCOPE, "fl_moe_layer_noalloc reads IQ2_XXS matrices only"); } }
+    if (int rc = check_rule(c, L->n_exp)) { return rc; }
+    if (!decode_rule_ok(L->n_exp, c->n_group)) { return fail(c, FL_ESCOPE, "routing rule outside the decode block's selection"); }
+    if (c->keep > c->topk) { return fail(c, FL_EINVAL, "keep %d above topk %d", c->keep, c->topk); }
+    if (!L->gate_inp || !L->probs_b || !L->gate_exps || !L->up_exps || !L->down_exps || !L->sh_gate || !L->sh_up || !L->sh_down) {
+        return fail(c, FL_EINVAL, "null pointer in the layer");
+    }
+    {
+        const size_t mg = (size_t) 2048 * 28 * IQ2B;
+        const int ne = L->n_exp;
+        if (!covers(L->gate_inp, (size_t) ne * 7168 * 4) || !covers(L->probs_b, (size_t) ne * 4) || !covers(x, (size_t) n * 7168 * 4) ||
+            !covers(y, (size_t) n * 7168 * 4) || !covers(L->gate_exps, ne * mg) || !covers(L->up_exps, ne * mg) ||
+            !covers(L->down_exps, ne * mg) || !covers(L->sh_gate, mg) || !covers(L->sh_up, mg) || !covers(L->sh_down, mg)) {
+            return fail(c, FL_EINVAL, "an allocation of the layer, x or y is smaller than its shape");
+        }
+    }
+    if (c->herr) {
+        const int e = __atomic_load_n(c->herr, __ATOMIC_ACQUIRE);
+        if (e) { return fail(c, FL_EHIP, "an earlier launch on this context reported device error code %d; call fl_sync", e); }
+    }
+    if (!decode_ready(c)) { return fail(c, FL_ESCOPE, "the single-launch decode block is not available on this device"); }
+    uint8_t * S = na_resolve(c->dev);
+    if (!S) { return fail(c, FL_EHIP, "hipGetSymbolAddress of the decode scratch failed on device %d", c->dev); }
+    NaDev & nd = g_na[c->dev];
+    hipStream_t st = c->st;
+    unsigned epoch;
+    {
+        std::lock_guard<std::mutex> lk(g_na_mu);
+        if (!nd.tab_built) { TRY(c, build_table_image(reinterpret_cast<uint4 *>(S + NA_TAB), st)); nd.tab_built = 1; }
+        if (++nd.epoch == 0) { nd.epoch = 1; }
+        epoch = nd.epoch;
+        if (epoch == 1) {   // first call on the device, or the epoch wrapped: no stale word may carry the new epoch
+            const size_t n16 = (NA_CLEAR1 - NA_CLEAR0) / 16;
+            k_zero16<<<512, 256, 0, st>>>(reinterpret_cast<uint4 *>(S + NA_CLEAR0), n16);
+            TRY(c, hipGetLastError());
+        }
+    }
+    const int tk = c->keep > 0 ? c->keep : c->topk;
+    DecodeArgs d{};
+    d.tab = reinterpret_cast<const uint4 *>(S + NA_TAB); d.x = x; d.n = n; d.prenorm = 0; d.nw = nullptr; d.eps = 0.f; d.resid = nullptr;
+    d.Wr = L->gate_inp; d.bias = L->probs_b; d.n_exp = L->n_exp; d.n_group = c->n_group; d.topk_group = c->topk_group;
+    d.topk = c->topk; d.scale = c->scale; d.keep = tk; d.renorm = c->keep > 0 ? c->renorm : 0.f;
+    d.gate = (const uint8_t *) L->gate_exps; d.up = (const uint8_t *) L->up_exps; d.down = (const uint8_t *) L->down_exps;
+    d.estride = (size_t) 2048 * 28 * IQ2B;
+    d.sh_gate = (const uint8_t *) L->sh_gate; d.sh_up = (const uint8_t *) L->sh_up; d.sh_down = (const uint8_t *) L->sh_down;
+    d.E = 7168; d.H = 2048;
+    d.xq = reinterpret_cast<int8_t *>(S + NA_XQ); d.xd = reinterpret_cast<float *>(S + NA_XD);
+    d.logits = reinterpret_cast<float *>(S + NA_LOG); d.probs = reinterpret_cast<float *>(S + NA_PRB);
+    d.sel = reinterpret_cast<int *>(S + NA_SEL); d.wts = reinterpret_cast<float *>(S + NA_WTS);
+    d.counts = reinterpret_cast<int *>(S + NA_CNT); d.offsets = reinterpret_cast<int *>(S + NA_OFF);
+    d.perm = reinterpret_cast<int *>(S + NA_PERM); d.inv = reinterpret_cast<int *>(S + NA_INV);
+    d.act = reinterpret_cast<int *>(S + NA_ACT); d.nact = reinterpret_cast<int *>(S + NA_NACT);
+    d.tlogits = reinterpret_cast<uint64_t *>(S + NA_TLOG); d.th = reinterpret_cast<uint64_t *>(S + NA_TH);
+    d.to = reinterpret_cast<uint64_t *>(S + NA_TO); d.y = y;
+    d.epoch = epoch; d.err = reinterpret_cast<int *>(S + NA_ERR); d.herr = c->herr ? c->herr_dev : nullptr;
+    TRY(c, launch_moe_decode(d, c->dec_grid, c->fused == 1, st));
+    return FL_OK;
 }
 
 extern "C" int fl_set_profile(FLCtx * c, int on) { if (!c) { return FL_EINVAL; } c->prof = on ? 1 : 0; return FL_OK; }
