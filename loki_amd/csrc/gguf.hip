@@ -162,7 +162,12 @@ extern "C" FLGguf * fl_gguf_open(const char * const * paths, int npaths, char * 
             TypeInfo ti;
             if (type_info(t.type, ti)) {
                 if (t.ne[0] % ti.blck) { return bad("tensor row not a whole number of blocks", f); }
-                t.nbytes = (uint64_t) (t.ne[0] / ti.blck) * (uint64_t) ti.bytes * (uint64_t) t.ne[1] * (uint64_t) t.ne[2] * (uint64_t) t.ne[3];
+                // the size as a checked product: a wrapped value would skip the end-of-file test below
+                uint64_t nb = (uint64_t) (t.ne[0] / ti.blck);
+                bool ovf = __builtin_mul_overflow(nb, (uint64_t) ti.bytes, &nb);
+                for (int d = 1; d < 4; ++d) { ovf = ovf || __builtin_mul_overflow(nb, (uint64_t) t.ne[d], &nb); }
+                if (ovf) { return bad("tensor size overflows 64 bits", f); }
+                t.nbytes = nb;
             }
             if (t.offset % align) { return bad("tensor offset not aligned", f); }
             local.push_back(t); lnames.push_back(name);
@@ -170,8 +175,10 @@ extern "C" FLGguf * fl_gguf_open(const char * const * paths, int npaths, char * 
         const uint64_t data0 = (r.pos + align - 1) / align * align;
         for (size_t k = 0; k < local.size(); ++k) {
             FLGguf::T t = local[k];
-            t.offset += data0;
-            if (t.offset + t.nbytes > r.size) { return bad("tensor data past the end of the file", f); }
+            uint64_t end = 0;
+            if (__builtin_add_overflow(t.offset, data0, &t.offset) || __builtin_add_overflow(t.offset, t.nbytes, &end) || end > r.size) {
+                return bad("tensor data past the end of the file", f);
+            }
             auto it = g->by_name.find(lnames[k]);
             if (it != g->by_name.end()) { g->tensors[it->second] = t; continue; }   // a later file's tensor replaces it (eng:105)
             g->by_name[lnames[k]] = (int) g->tensors.size();
@@ -312,7 +319,7 @@ extern "C" int fl_gguf_load_moe_layer(FLCtx * c, const FLGguf * g, int layer, in
         return fail(c, FL_EINVAL, "%s: tensor shapes do not form one MoE layer (E %lld, H %lld, experts %lld)", p.c_str(), (long long) E, (long long) H, (long long) ne);
     }
     if (tr.type != (r16 ? 1 : 0) || tb.type != 0 || (has_norm && tn.type != 0)) { return fail(c, FL_EINVAL, "%s: router, bias and norm must be F32 (router F16 as ffn_gate_inp_f16)", p.c_str()); }
-    if (ne <= 0 || ne > 256 || E % 1024 || H % 1024) { return fail(c, FL_EINVAL, "%s: %lld experts, E %lld, H %lld (experts <= 256, E and H multiples of 1024)", p.c_str(), (long long) ne, (long long) E, (long long) H); }
+    if (ne <= 0 || ne > 256 || E <= 0 || H <= 0 || E > 65536 || H > 65536 || E % 1024 || H % 1024) { return fail(c, FL_EINVAL, "%s: %lld experts, E %lld, H %lld (experts <= 256, E and H positive multiples of 1024 up to 65536)", p.c_str(), (long long) ne, (long long) E, (long long) H); }
     int fm[6];
     for (int k = 0; k < 3; ++k) { fm[k] = te[k].fl_format; fm[3 + k] = ts[k].fl_format; }
     if (fm[0] != FL_IQ2 || fm[1] != FL_IQ2) { return fail(c, FL_ESCOPE, "%s: routed gate/up must be IQ2_XXS (types %d, %d)", p.c_str(), te[0].type, te[1].type); }

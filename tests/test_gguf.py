@@ -119,3 +119,29 @@ def test_rejects_malformed(tmp_path):
     with pytest.raises(lk.LokiError):
         lk.Gguf(p)
     lk.Gguf(good).close()
+
+
+def test_rejects_wrapping_sizes_and_offsets(tmp_path):
+    """A tensor whose byte size overflows 64 bits (dims each within the 2^40 limit) and one whose offset wraps when the
+    data section's base is added are rejected, not indexed with a wrapped size that passes the end-of-file test."""
+    lk = loki()
+    ts = [("blk.0.ffn_gate_exps.weight", "IQ2_XXS", [512, 64, 3], gen.iq2_matrix(1, 2, 64 * 3, 512))]
+    good = str(tmp_path / "g.gguf")
+    _gguf.write(good, ts)
+    data = bytearray(open(good, "rb").read())
+    name = ts[0][0].encode()
+    dims = data.index(name) + len(name) + 4                      # ne[0..2], then type, then offset
+    huge = bytearray(data)
+    for d in (1, 2):                                             # 64 * 3 rows -> 2^40 x 2^40: the product wraps
+        huge[dims + 8 * d:dims + 8 * d + 8] = (1 << 40).to_bytes(8, "little")
+    p = str(tmp_path / "huge.gguf")
+    open(p, "wb").write(bytes(huge))
+    with pytest.raises(lk.LokiError):
+        lk.Gguf(p)
+    wrap = bytearray(data)
+    off = dims + 8 * 3 + 4
+    wrap[off:off + 8] = ((1 << 64) - 32 * 8).to_bytes(8, "little")   # aligned; + the data base wraps past 2^64
+    p = str(tmp_path / "wrap.gguf")
+    open(p, "wb").write(bytes(wrap))
+    with pytest.raises(lk.LokiError):
+        lk.Gguf(p)
