@@ -9,8 +9,8 @@ timed region. Each step takes a fresh x (so different experts) and the steps rot
 layers (3 x 2.9 GB), so the 256 MB MALL cannot serve repeated weights.
 
 Prints ONE JSON line: value = microseconds per token of the whole block (router, dispatch, experts, combine), plus the
-achieved HBM bandwidth, the roofline of the dominant kernel (decode: k_moe_decode, the whole block in one
-launch; prefill: the gate/up expert kernel), timed live with HIP events recorded on the stream the kernel runs on, and
+achieved HBM bandwidth, the roofline of the dominant kernel (decode: the whole block in one launch, k_moe_decode1
+for one token, k_moe_decode for batches; prefill: the gate/up expert kernel), timed live with HIP events recorded on the stream the kernel runs on, and
 the CPU checker timed on this host's cores on a bounded sample of every config. decode-8, prefill-512, prefill-2048,
 the 58-layer stack and the real-shard formats are reported under `extra`. Every timed loop ends with fl_sync: a
 device-side failure (a bounded wait of the decode block that timed out) makes the run exit non-zero instead of
@@ -116,7 +116,8 @@ def run_workload(ctx, torch, name, steps, warmup, copies, seed=20260101):
     torch.cuda.synchronize()
     ctx.sync()   # a device-side failure in any timed step raises here
     ms = start.elapsed_time(end) / steps
-    fused = bool(ctx.debug().fused)
+    dbg = ctx.debug()
+    fused, dkernel = bool(dbg.fused), dbg.kernel
     if fused:
         # one launch per step, issued back to back on the library's stream: the timed region's per-step time is the
         # launch's average duration
@@ -140,7 +141,7 @@ def run_workload(ctx, torch, name, steps, warmup, copies, seed=20260101):
         km.append(k); gm.append(g)
     ctx.sync()
     mean_U = sum(U) / len(U)
-    res = dict(name=name, desc=desc, n=n, ms=ms, U=mean_U, stage_ms=stage, fused=fused, host_us=host_us,
+    res = dict(name=name, desc=desc, n=n, ms=ms, U=mean_U, stage_ms=stage, fused=fused, dkernel=dkernel, host_us=host_us,
                margins={"topk_min": min(km), "group_min": min(gm)},
                bytes=sum(step_bytes(n, u) for u in U) / len(U),
                gu_bytes=sum(gateup_bytes(n, u) for u in U) / len(U))
@@ -361,7 +362,8 @@ def kernel_roofline(res):
     (its bytes are the step's), else the gate/up stage (grouped GEMM on MFMA above 8 tokens, else the mat-vec kernel)."""
     n = res["n"]
     if res["fused"]:
-        kname, k_ms, k_bytes = "k_moe_decode", res["stage_ms"]["gate_up"], res["bytes"]
+        kname = "k_moe_decode1" if res["dkernel"] == 2 else "k_moe_decode"
+        k_ms, k_bytes = res["stage_ms"]["gate_up"], res["bytes"]
         stages = {"block": k_ms}
     else:
         kname = "k_pf_gemm<gate_up>" if n > 8 else "k_experts<gate_up>"

@@ -214,6 +214,8 @@ typedef struct FLDebug {
     int n, P, topk;                                    /* topk: slots per row of the last call (the kept count) */
     int fused;                                         /* 1: the last call ran as the single-launch decode block, which
                                                         * keeps h and o internal (h .. u are NULL then) */
+    int kernel;                                        /* the last call's decode launch: 0 none (per-pass or wide path),
+                                                        * 1 the general block, 2 the one-token block organised by XCD */
 } FLDebug;
 int fl_debug(FLCtx *, FLDebug * out);
 int fl_set_debug(FLCtx *, int capture_gate_up);
@@ -225,6 +227,10 @@ int fl_set_debug(FLCtx *, int capture_gate_up);
  * the caller must check before trusting any output of a mode-2 decode, and, without waiting, by the next
  * fl_moe_layer / fl_moe_layer_normed call on the context, which returns FL_EHIP until fl_sync has reported it. */
 int fl_set_fused(FLCtx *, int mode);
+/* single-token decode with all 8 picks kept, on a 256-CU device: 1 (default) = the single launch organised by XCD
+ * (pick k's expert runs on the 32 CUs of XCD k, its down split by K-block among the four workgroups that produce each
+ * h block), 0 = the general single-launch decode block. Both give bit-identical outputs. */
+int fl_set_decode1(FLCtx *, int on);
 /* batches above the decode sizes (n > 8, E 7168, H 2048): 1 (default) = the expert products as grouped GEMMs on the
  * matrix cores (no counterpart in the reference, whose wide path is tc_matvec per arena batch, src/fused_layer.cu:540-561);
  * 0 = the per-pass mat-vec kernels. Both give bit-identical outputs. */

@@ -104,7 +104,8 @@ class Gguf:
 class FLDebug(ctypes.Structure):
     _fields_ = [(n, P_) for n in ("xq", "xd", "logits", "probs", "sel", "wts", "counts", "offsets", "perm", "inv",
                                   "act", "nact", "h", "hq", "hd", "o", "g", "u")] + \
-               [("n", ctypes.c_int), ("P", ctypes.c_int), ("topk", ctypes.c_int), ("fused", ctypes.c_int)]
+               [("n", ctypes.c_int), ("P", ctypes.c_int), ("topk", ctypes.c_int), ("fused", ctypes.c_int),
+                                                                           ("kernel", ctypes.c_int)]
 
 
 class FLW(ctypes.Structure):
@@ -128,7 +129,7 @@ ABI_SYMBOLS = [
     "fl_gguf_open", "fl_gguf_close", "fl_gguf_n_tensors", "fl_gguf_tensor_name", "fl_gguf_tensor", "fl_gguf_tensor_at",
     "fl_gguf_get_int", "fl_gguf_get_float", "fl_gguf_get_str", "fl_gguf_read", "fl_gguf_load_moe_layer", "fl_gguf_free_layer", "fl_moe_layer", "fl_moe_layer_normed", "fl_moe_layer_noalloc", "fl_route_dev", "fl_dispatch_dev", "fl_quant_q8k_dev",
     "fl_pack_iq2xxs", "fl_unpack_iq2xxs", "fl_rmsnorm_dev", "fl_synth_iq2xxs", "fl_synth_normal", "fl_probe_exp",
-    "fl_debug", "fl_set_debug", "fl_set_fused", "fl_set_prefill_mfma", "fl_stream", "fl_set_stream", "fl_d2h", "fl_set_profile", "fl_stage_ms", "fl_sync", "fl_last_error", "fl_free",
+    "fl_debug", "fl_set_debug", "fl_set_fused", "fl_set_decode1", "fl_set_prefill_mfma", "fl_stream", "fl_set_stream", "fl_d2h", "fl_set_profile", "fl_stage_ms", "fl_sync", "fl_last_error", "fl_free",
 ]
 
 _lib = None
@@ -174,6 +175,7 @@ def lib():
             "fl_gguf_free_layer": (None, [ctypes.POINTER(FLGgufLayer)]),
             "fl_set_debug": (I, [P_, I]),
             "fl_set_fused": (I, [P_, I]),
+            "fl_set_decode1": (I, [P_, I]),
             "fl_set_prefill_mfma": (I, [P_, I]),
             "fl_moe_layer": (I, [P_, ctypes.POINTER(FLMoeLayer), P_, I, P_]),
             "fl_moe_layer_normed": (I, [P_, ctypes.POINTER(FLMoeLayer), P_, F, P_, I, I, P_]),
@@ -308,6 +310,10 @@ class Context:
         0 = one launch per pass."""
         self.check(lib().fl_set_fused(self.ctx, int(mode)))
         self._fused = int(mode)
+
+    def set_decode1(self, on):
+        """One-token decode: True (default) = the kernel organised by XCD, False = the general decode block."""
+        self.check(lib().fl_set_decode1(self.ctx, 1 if on else 0))
 
     @property
     def fused_mode(self):

@@ -42,7 +42,7 @@ struct FLCtx {
     int dbg_gu = 0;
     DBuf<int8_t> xq, hq; DBuf<float> xd, logits, probs, wts, h, hd, o, g, u, xn;
     DBuf<int> sel, counts, offsets, perm, inv, act, nact;
-    int last_n = 0, last_P = 0, last_fused = 0;
+    int last_n = 0, last_P = 0, last_fused = 0, last_kernel = 0;
     // stage timing (fl_set_profile): one set of NSTAGE+1 events per profiled call, summed by fl_stage_ms
     int prof = 0;
     std::vector<std::vector<hipEvent_t>> ev_free, ev_pending;
@@ -52,6 +52,7 @@ struct FLCtx {
     DBuf<uint4> tab;                         // LDS table image (build_table_image)
     // single-launch decode block: epoch-tagged logits / h / o, wait-timeout word; fused = 0 forces the per-pass kernels
     DBuf<int> derr; DBuf<uint64_t> dlogit, dth, dto; unsigned epoch = 0; int fused = 2; int dec_grid = -1;
+    int d1 = 1, d1_ok = -1;   // decode-1 kernel organised by XCD (fl_set_decode1); availability on this device
     // pinned, device-mapped copy of the last code a kernel reported (null if the host allocation failed): every
     // fl_moe_layer call checks it without waiting for the stream, fl_sync reports and clears it
     int * herr = nullptr, * herr_dev = nullptr;   // host pointer, and the address kernels store to

@@ -164,6 +164,7 @@ extern "C" int fl_set_experts(FLCtx * c, int n_exp) {
 }
 extern "C" int fl_set_debug(FLCtx * c, int capture) { if (!c) { return FL_EINVAL; } c->dbg_gu = capture ? 1 : 0; return FL_OK; }
 extern "C" int fl_set_prefill_mfma(FLCtx * c, int on) { if (!c) { return FL_EINVAL; } c->pf_mfma = on ? 1 : 0; return FL_OK; }
+extern "C" int fl_set_decode1(FLCtx * c, int on) { if (!c) { return FL_EINVAL; } c->d1 = on ? 1 : 0; return FL_OK; }
 extern "C" int fl_set_fused(FLCtx * c, int mode) {
     if (!c) { return FL_EINVAL; }
     if (mode < 0 || mode > 2) { return fail(c, FL_EINVAL, "fused mode %d outside 0..2", mode); }
@@ -312,6 +313,21 @@ static bool decode_ready(FLCtx * c) {
     return c->dec_grid > 0;
 }
 
+// the decode-1 kernel organised by XCD is available (a 256-CU device) and selected
+static bool decode1_ready(FLCtx * c) {
+    if (c->d1_ok < 0) {
+        int ok = 0;
+        if (decode1_init(c->ncu, &ok) != hipSuccess) { (void) hipGetLastError(); ok = 0; }
+        c->d1_ok = ok;
+    }
+    return c->d1 && c->d1_ok > 0;
+}
+static hipError_t launch_decode(FLCtx * c, const DecodeArgs & d, hipStream_t st) {
+    if (d.n == 1 && d.topk == MAXK && d.keep == MAXK && decode1_ready(c)) { c->last_kernel = 2; return launch_moe_decode1(d, c->fused == 1, st); }
+    c->last_kernel = 1;
+    return launch_moe_decode(d, c->dec_grid, c->fused == 1, st);
+}
+
 // ================================================================ the device-resident block
 // the block on x, or on RMSNorm(x) * nw when prenorm (nw may be null: ones); resid (may be null) is added to the output
 // bytes of one R x K matrix in format f (IQ2_XXS or a K-quant)
@@ -372,7 +388,7 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     if (!fused) { ALLOC(c, c->h, rows * H); ALLOC(c, c->hq, rows * H); ALLOC(c, c->hd, rows * (H / 256)); ALLOC(c, c->o, rows * E); }
     if (c->dbg_gu) { ALLOC(c, c->g, rows * H); ALLOC(c, c->u, rows * H); }
     if (int rc = ensure_expert_scratch(c, rows, E, H)) { return rc; }
-    c->last_n = n; c->last_P = P; c->last_fused = fused ? 1 : 0;
+    c->last_n = n; c->last_P = P; c->last_fused = fused ? 1 : 0; c->last_kernel = 0;
     hipStream_t st = c->st;
     std::vector<hipEvent_t> * ev = prof_begin(c);
     if (fused) {
@@ -398,7 +414,7 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
         d.epoch = c->epoch; d.err = c->derr.p; d.herr = c->herr ? c->herr_dev : nullptr;
         // stages: the whole block is one launch, reported as stage 4; the others are empty
         for (int i = 0; i <= 4; ++i) { prof_mark(c, ev, i); }
-        TRY(c, launch_moe_decode(d, c->dec_grid, c->fused == 1, st));
+        TRY(c, launch_decode(c, d, st));
         prof_mark(c, ev, 5); prof_mark(c, ev, 6);
         return FL_OK;
     }
@@ -604,7 +620,7 @@ extern "C" int fl_moe_layer_noalloc(FLCtx * c, const FLMoeLayer * L, const float
     d.tlogits = reinterpret_cast<uint64_t *>(S + NA_TLOG); d.th = reinterpret_cast<uint64_t *>(S + NA_TH);
     d.to = reinterpret_cast<uint64_t *>(S + NA_TO); d.y = y;
     d.epoch = epoch; d.err = reinterpret_cast<int *>(S + NA_ERR); d.herr = c->herr ? c->herr_dev : nullptr;
-    TRY(c, launch_moe_decode(d, c->dec_grid, c->fused == 1, st));
+    TRY(c, launch_decode(c, d, st));
     return FL_OK;
 }
 
@@ -633,7 +649,7 @@ extern "C" int fl_debug(FLCtx * c, FLDebug * out) {
     if (!c->last_fused) {   // the single-launch block keeps h and o in its epoch-tagged buffers only
         out->h = c->h.p; out->hq = c->hq.p; out->hd = c->hd.p; out->o = c->o.p; out->g = c->dbg_gu ? c->g.p : nullptr; out->u = c->dbg_gu ? c->u.p : nullptr;
     }
-    out->n = c->last_n; out->P = c->last_P; out->topk = c->last_n > 0 ? c->last_P / c->last_n : c->topk; out->fused = c->last_fused;
+    out->n = c->last_n; out->P = c->last_P; out->topk = c->last_n > 0 ? c->last_P / c->last_n : c->topk; out->fused = c->last_fused; out->kernel = c->last_kernel;
     return FL_OK;
 }
 

@@ -1,0 +1,606 @@
+// moe_decode1.hip -- the MoE block for one decode token (top-8 kept) in one launch, organised by XCD.
+//
+// Reference path (src/fused_layer.cu): router_probs + router_topk (:313-332), the host round-trip (fl_fetch :587-598,
+// eng:793-818), fl_moe (:599-612): quant_x, tc_matvec gate/up, swiglu_q8, tc_matvec down, moe_combine. Here the
+// 256 workgroups (one per CU, 16 waves, 32 per XCD; workgroup b runs on XCD b % 8) run the block end to end:
+//   1. every workgroup b computes the router logit of expert b (the fp64 chunk-and-tree contract, waves 0-3) and
+//      publishes p = sigmoid(logit) as an epoch-tagged word, while waves 4-15 stage the codebook/sign tables and Q8_K(x)
+//      in LDS and the last 7 waves then run one gate/up task of the shared expert (routing-independent: shared h rows
+//      8 t .. 8 t + 7 with t = 32 (b % 8) + b / 8, so XCD x produces the shared expert's h block x);
+//   2. wave 0 selects the token's experts; pick k (0..7, selection order) is slot k, and slot k runs on XCD k:
+//      workgroup b computes h rows kb * 256 + q * 64 .. + 63 of expert sel[b % 8] (kb = (b / 8) / 4, q = (b / 8) % 4)
+//      as 56 items (one matrix, one 256-weight block, 64 rows) that the waves claim from an LDS counter;
+//   3. the four workgroups of (slot, kb) complete h block kb of their slot; each of them quantises that block to Q8_K
+//      and runs K-block kb of the slot's down for a quarter of its 7168 rows (split-K: one 256-weight block per row,
+//      one row per lane), plus 3 or 4 row groups of the shared expert's down for K-block b % 8, again claimed by the
+//      waves unit by unit. Each row's block term (d_w * d_x) * bsum is published as a tagged word;
+//   4. workgroup b combines rows 28 b .. 28 b + 27: per slot the 8 block terms folded in block order (ggml's sumf),
+//      * 0.125, then y = sum_k w_k o_k in k order + the shared o (+ the residual).
+// The arithmetic is that of the other decode kernels and the CPU checker step for step (the same device functions and
+// fold orders), so y is bit-identical to them. The down waits on four workgroups of its own XCD rather than on every
+// gate/up task of the expert, and no dispatch table is built (one token: the picks are distinct experts). Every wait is
+// bounded: a timeout sets the error word and the wave skips the work, so the grid always drains.
+#include "moe_device.h"
+#include "moe_kernels.h"
+
+namespace lk {
+
+#ifdef LK_D1_WAVES
+constexpr int W1 = LK_D1_WAVES;
+#else
+constexpr int W1 = 16;                 // waves per workgroup: 4 per SIMD (the block product's issue rate rises with them)
+#endif
+constexpr int NT1 = W1 * 64;
+constexpr int NQW1 = W1 - 4;           // waves staging the tables and the token (the router runs on waves 0-3)
+static_assert(NQW1 >= 4 && W1 >= 8, "four router waves and at least four staging waves");
+constexpr int G1 = 256, NX1 = 8;       // workgroups, XCDs
+constexpr int E1 = 7168, H1 = 2048;
+using GX1 = Geo<7, 0>;                 // the token's staged Q8_K row: 28 blocks, no padding
+constexpr int NBX1 = E1 / QK, NBH1 = H1 / QK;    // 28, 8 blocks
+constexpr int SLOTS1 = 9;              // 8 picks + the shared expert (slot 8)
+constexpr int QROWS1 = E1 / 4;         // routed down rows per workgroup (a quarter): 1792 = 28 row groups
+constexpr int RGQ1 = QROWS1 / 64;      // 28
+constexpr int RGE1 = E1 / 64;          // 112 row groups of the shared expert's down block
+constexpr int CROWS1 = E1 / G1;        // combine rows per workgroup: 28
+constexpr int GU_STEPS1 = NBX1 / 4;    // 7
+constexpr int NITEM1 = 2 * NBX1;       // routed gate/up items of a workgroup: (matrix, block) of its 64 h rows
+static_assert(G1 == 32 * NX1 && H1 == NX1 * QK && CROWS1 * G1 == E1, "decode-1 geometry");
+static_assert((size_t) SLOTS1 * H1 <= DEC_TH && (size_t) SLOTS1 * NBH1 * E1 <= DEC_TO, "tagged buffers");
+
+// LDS layout (bytes)
+constexpr int M_X = TAB_BYTES;                     // staged Q8_K of the token
+constexpr int M_HR = M_X + GX1::XROW;              // staged Q8_K of the routed h block (256 B + scale)
+constexpr int M_HS = M_HR + 272;                   // staged Q8_K of the shared h block
+constexpr int M_PRE = M_HS + 272;                  // shared task block terms [7 steps][64 lanes]
+constexpr int M_TERMS = M_PRE + GU_STEPS1 * 64 * 4;   // routed block terms [matrix][block][64 rows]
+constexpr int M_SCR = M_TERMS + NITEM1 * 64 * 4;   // router / norm partial sums [4] (fp64)
+constexpr int M_CMB = M_SCR + 64;                  // combine: o [28 rows][9 slots]
+constexpr int M_SEL = M_CMB + CROWS1 * SLOTS1 * 4; // picks [8] and weights [8]
+constexpr int NCTL1 = 32;
+constexpr int M_CTL = M_SEL + 2 * MAXK * 4;        // control words
+constexpr int M_NRM = M_CTL + NCTL1 * 4;           // RMSNorm scale
+constexpr int DEC1_LDS = M_NRM + 16;
+static_assert(DEC1_LDS <= 160 * 1024 && (M_X % 16) == 0 && (M_HR % 16) == 0 && (M_HS % 16) == 0, "LDS layout");
+enum { C_RT = 0, C_STAGED = 1, C_SH = 2, C_READY = 3, C_HR = 4, C_HS = 5, C_CMBFAIL = 6, C_NRM = 7, C_RISSUED = 8,
+       C_GUCLAIM = 9, C_DNCLAIM = 10, C_GUDONE = 11 };
+
+typedef LK_LOCAL uint8_t * lds1_t;
+typedef LK_CONST DecodeArgs D1Args;
+
+__device__ __forceinline__ void report1(const D1Args & a, int code) {
+    if (lane_id() == 0) {
+        __hip_atomic_fetch_or(gptr(a.err), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (a.herr) { __hip_atomic_store(gptr(a.herr), code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); }
+    }
+}
+__device__ __forceinline__ void st_tag1(uint64_t * p, uint32_t epoch, float v) {
+    __hip_atomic_store(gptr(p), ((uint64_t) epoch << 32) | __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_tag1(const uint64_t * p) { return __hip_atomic_load(gptr(const_cast<uint64_t *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ bool tag1_ok(uint64_t w, uint32_t epoch) { return (uint32_t) (w >> 32) == epoch; }
+__device__ __forceinline__ float tag1_val(uint64_t w) { return __builtin_bit_cast(float, (uint32_t) w); }
+constexpr int POLL1 = 1 << 20;   // polls before a wait gives up (each poll is a memory round trip)
+
+// LDS hand-offs between the waves of one workgroup (always co-resident)
+__device__ __forceinline__ bool arrive1(LK_LOCAL unsigned * c, unsigned expected) {
+    lds_visible();
+    unsigned old = 0;
+    if (lane_id() == 0) { old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+    old = __builtin_amdgcn_readfirstlane(old);
+    return old + 1 == expected;
+}
+__device__ __forceinline__ unsigned wait1(LK_LOCAL unsigned * w, unsigned want_at_least) {
+    for (int i = 0; i < (1 << 24); ++i) {
+        const unsigned v = __builtin_amdgcn_readfirstlane(__hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+        if (v >= want_at_least) { return v; }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return 0;
+}
+__device__ __forceinline__ void flag1(LK_LOCAL unsigned * w, unsigned v) {
+    lds_visible();
+    if (lane_id() == 0) { __hip_atomic_store(w, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+}
+__device__ __forceinline__ const uint8_t * uniform1(const uint8_t * p) {
+    const uint64_t v = (uint64_t) p;
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) (v >> 32));
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) v);
+    return (const uint8_t *) (((uint64_t) hi << 32) | (uint64_t) lo);
+}
+
+#ifdef LOKI_TRACE
+constexpr int TRACE1_SLOTS = 64;
+__device__ uint64_t g_trace1[1024 * W1 * TRACE1_SLOTS];
+#define TRACE1(slot) do { if (lane_id() == 0) { g_trace1[(blockIdx.x * W1 + (threadIdx.x >> 6)) * TRACE1_SLOTS + (slot)] = __builtin_amdgcn_s_memrealtime(); } } while (0)
+extern "C" hipError_t fl_trace1_copy(void * host, size_t bytes) { return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace1), bytes); }
+extern "C" hipError_t fl_trace1_clear() {
+    void * p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_trace1));
+    return e == hipSuccess ? hipMemset(p, 0, sizeof(g_trace1)) : e;
+}
+#else
+#define TRACE1(slot) do { } while (0)
+#endif
+
+// the block's input at column col: x, or (x * scale) * w under prenorm (k_rmsnorm's arithmetic)
+__device__ __forceinline__ float4 in1(const D1Args & a, lds1_t lds, int col, float4 v) {
+#pragma clang fp contract(off)
+    if (!a.prenorm) { return v; }
+    const float sc = *reinterpret_cast<const LK_LOCAL float *>(lds + M_NRM);
+    v.x = v.x * sc; v.y = v.y * sc; v.z = v.z * sc; v.w = v.w * sc;
+    if (a.nw) { const float4 w = gloadf4(a.nw + col); v.x = v.x * w.x; v.y = v.y * w.y; v.z = v.z * w.z; v.w = v.w * w.w; }
+    return v;
+}
+
+// ---------------------------------------------------------------- 1. router (waves 0-3) and staging (waves 4-7)
+// Thread (quarter w = wave, lane) owns chunk 64 w + lane (28 values) of expert b's logit: in-order fp64 chunk sum,
+// tree levels 1-6 by DPP (tree64), levels 7-8 over the four waves' totals in LDS; the last wave to arrive publishes
+// p = sigmoid(logit). Under prenorm the same threads first form the token's RMSNorm scale (the chunked sum-of-squares
+// contract of k_rmsnorm, over the same chunks). Workgroups past the layer's experts only form the scale.
+__device__ __noinline__ void router1(const D1Args & a, lds1_t lds, int wave, LK_LOCAL unsigned * ctl) {
+#pragma clang fp contract(off)
+    constexpr int L4 = E1 / 1024;
+    const int lane = lane_id(), c = wave * 64 + lane, e = blockIdx.x;
+    LK_LOCAL double * part = reinterpret_cast<LK_LOCAL double *>(lds + M_SCR);
+    const bool has_e = e < a.n_exp;
+    float4 wv[L4], xv[L4];
+    const float * wc = a.Wr + (size_t) (has_e ? e : 0) * E1 + (size_t) c * 4 * L4;
+    const float * xc = a.x + (size_t) c * 4 * L4;
+    if (has_e) {
+#pragma unroll
+        for (int i = 0; i < L4; ++i) { wv[i] = gloadf4(wc + 4 * i); }
+    }
+#pragma unroll
+    for (int i = 0; i < L4; ++i) { xv[i] = gloadf4(xc + 4 * i); }
+    // the router's loads are in the CU's memory queue: the table copy (waves 4-7) may follow
+    __builtin_amdgcn_sched_barrier(0);
+    if (lane == 0) { __hip_atomic_fetch_add(reinterpret_cast<LK_LOCAL unsigned *>(lds + M_CTL) + C_RISSUED, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+    if (a.prenorm) {
+        double s = 0.0;
+#pragma unroll
+        for (int i = 0; i < L4; ++i) {
+            const float q0 = xv[i].x * xv[i].x, q1 = xv[i].y * xv[i].y, q2 = xv[i].z * xv[i].z, q3 = xv[i].w * xv[i].w;
+            s += (double) q0; s += (double) q1; s += (double) q2; s += (double) q3;
+        }
+        const double q = tree64(s);
+        if (lane == 0) { part[wave] = q; }
+        if (arrive1(ctl + C_RT, 4)) {
+            if (lane == 0) {
+                *reinterpret_cast<LK_LOCAL float *>(lds + M_NRM) = rms_scale(part[0], part[1], part[2], part[3], E1, a.eps);
+            }
+            flag1(ctl + C_NRM, 1);   // the scale is ready
+        }
+        if (!has_e) { return; }
+        if (!wait1(ctl + C_NRM, 1)) { report1(a, 64); return; }
+        lds_visible();
+#pragma unroll
+        for (int i = 0; i < L4; ++i) { xv[i] = in1(a, lds, c * 4 * L4 + 4 * i, xv[i]); }
+    }
+    if (!has_e) { return; }
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < L4; ++i) {
+        s += (double) xv[i].x * (double) wv[i].x; s += (double) xv[i].y * (double) wv[i].y;
+        s += (double) xv[i].z * (double) wv[i].z; s += (double) xv[i].w * (double) wv[i].w;
+    }
+    const double q = tree64(s);
+    lds_visible();   // (prenorm) every wave has read part[] as norm sums before it is reused
+    if (a.prenorm) {
+        if (lane == 0) { reinterpret_cast<LK_LOCAL double *>(lds + M_SCR + 32)[wave] = q; }
+    } else if (lane == 0) {
+        part[wave] = q;
+    }
+    const unsigned want = a.prenorm ? 8u : 4u;
+    if (arrive1(ctl + C_RT, want) && lane == 0) {
+        const LK_LOCAL double * pp = a.prenorm ? reinterpret_cast<const LK_LOCAL double *>(lds + M_SCR + 32) : part;
+        const float l = (float) ((pp[0] + pp[1]) + (pp[2] + pp[3]));
+        const float p = det_sigmoid(l);
+        st_tag1(a.tlogits + e, a.epoch, p);
+        gptr(a.logits)[e] = l;
+        if (a.probs) { gptr(a.probs)[e] = p; }
+    }
+}
+
+// Q8_K of the token's 28 blocks into LDS (staged layout) by the staging waves: a pass quantises 4 consecutive blocks,
+// one per 16-lane row (q8k_row16); workgroup 0 also writes the layer's xq / xd.
+__device__ __forceinline__ void quant1(const D1Args & a, lds1_t lds, int w4) {
+    const int lane = lane_id(), i = lane & 15;
+    for (int p = w4; p < NBX1 / 4; p += NQW1) {
+        const int j = 4 * p + (lane >> 4), col = j * QK + 16 * i;
+        float xs[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 v = in1(a, lds, col + 4 * q, gloadf4(a.x + col + 4 * q));
+            xs[4 * q] = v.x; xs[4 * q + 1] = v.y; xs[4 * q + 2] = v.z; xs[4 * q + 3] = v.w;
+        }
+        uint32_t packed[4]; float d;
+        q8k_row16(xs, packed, d);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) { *reinterpret_cast<LK_LOCAL uint32_t *>(lds + M_X + j * GX1::XBLK + staged_word(4 * i + w)) = packed[w]; }
+        if (i == 0) { reinterpret_cast<LK_LOCAL float *>(lds + M_X + NBX1 * GX1::XBLK)[j] = d; }
+        if (blockIdx.x == 0) {
+            *(LK_GLOBAL u32x4 *) (a.xq + (size_t) j * QK + 16 * i) = u32x4{ packed[0], packed[1], packed[2], packed[3] };
+            if (i == 0) { gptr(a.xd)[j] = d; }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- the shared expert's gate/up task: 8 h rows
+// Lane 16 q + r reads row r of the task's 16 weight rows (r < 8: gate rows, r >= 8: the same h rows of up) and blocks
+// 4 jj + q at step jj. Per step: the block's exact integer sum against the staged token (block_bsum_dpp), the term
+// (d_w * d_x) * bsum, and the row total advanced in block order (fold_rows). h = silu(0.125 g) * (0.125 u).
+struct Gu1 { const uint8_t * ql; const uint8_t * dl; };
+__device__ __forceinline__ Gu1 gu1_task(const uint8_t * gm, const uint8_t * um, int hrow0, int q, int r) {
+    const uint8_t * mat = r >= 8 ? um : gm;
+    const int row = hrow0 + (r & 7);
+    Gu1 t;
+    t.ql = mat + (size_t) (row >> 6) * NBX1 * 4096 + q * 4096 + (row & 63) * 16;
+    t.dl = mat + (size_t) (H1 / 64) * NBX1 * 4096 + (size_t) (row >> 6) * NBX1 * 128 + q * 128 + (row & 63) * 2;
+    return t;
+}
+constexpr size_t GU1_QSTEP = 4 * 4096, GU1_DSTEP = 4 * 128;
+__device__ __forceinline__ void gu1_issue(const Gu1 & t, int s, uint4 (&pf)[4], uint16_t & pd) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) { pf[c] = load_nt(t.ql + s * GU1_QSTEP + c * 1024); }
+    pd = *gptr(reinterpret_cast<const uint16_t *>(t.dl + s * GU1_DSTEP));
+}
+// h of the task's 8 rows: lanes 0..7 hold the gate totals, lanes 8..15 the up totals (row_ror:8 brings them over)
+__device__ __forceinline__ void gu1_publish(const D1Args & a, int slot, int hrow0, int q, int r, float acc) {
+#pragma clang fp contract(off)
+    const float other = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, acc), 0x128, 0xF, 0xF, false));
+    if (q == 0 && r < 8) { st_tag1(a.th + (size_t) slot * H1 + hrow0 + r, a.epoch, det_silu(0.125f * acc) * (0.125f * other)); }
+}
+
+// The shared expert's task (8 h rows) split over the last 7 waves (one step each): block terms to LDS, the last wave
+// folds them in block order and publishes h -- a pass's arithmetic, finished while the routing runs.
+__device__ __forceinline__ void shared_gu1(const D1Args & a, lds1_t lds, int wave, uint32_t tr, int q, int r, LK_LOCAL unsigned * ctl) {
+#pragma clang fp contract(off)
+    const int lane = lane_id(), hrow0 = ((blockIdx.x % NX1) * 32 + blockIdx.x / NX1) * 8;
+    const Gu1 t = gu1_task(uniform1(a.sh_gate), uniform1(a.sh_up), hrow0, q, r);
+    LK_LOCAL float * terms = reinterpret_cast<LK_LOCAL float *>(lds + M_PRE);
+    const uint8_t * xr = (const uint8_t *) (lds + M_X);
+    const int s = wave - (W1 - GU_STEPS1);
+    uint4 pf[4]; uint16_t pd;
+    gu1_issue(t, s, pf, pd);
+    const int j = s * 4 + q;
+    const int bsum = block_bsum_dpp(pf, tr, xr + j * GX1::XBLK, r);
+    const float dx = reinterpret_cast<const float *>(xr + NBX1 * GX1::XBLK)[j];
+    terms[s * 64 + lane] = (h2f(pd) * dx) * (float) bsum;
+    if (!arrive1(ctl + C_SH, GU_STEPS1)) { return; }
+    float acc = 0.f;
+#pragma unroll
+    for (int k = 0; k < GU_STEPS1; ++k) { acc = fold_rows(acc, terms[k * 64 + lane]); }
+    gu1_publish(a, 8, hrow0, q, r, acc);
+}
+
+// The workgroup's routed gate/up: h rows hrow0 .. hrow0 + 63 (one 64-row group of both matrices) as 56 items, item c =
+// matrix c % 2 (gate, up) at block c / 2, claimed in order by all waves from an LDS counter; a wave claims its next
+// item when it has used the last. Lane l owns row hrow0 + l of the item's matrix, so each of its 16-byte loads is one contiguous 1 KB
+// per wave (the tiled layout's chunk of 64 rows) and the scales one 128-byte line; every lane uses the same staged
+// token block, whose words come by DPP (block_bsum_dpp). The block terms (d_w * d_x) * bsum go to LDS; the wave that
+// completes the 56th item folds each row's 28 terms in block order (ggml's sumf, the order of every other path) and
+// publishes h = silu(0.125 g) * (0.125 u) for the 64 rows.
+struct GuItem { uint4 w[4]; uint16_t d; int c; };
+__device__ __forceinline__ void gate_up1(const D1Args & a, lds1_t lds, LK_LOCAL unsigned * ctl, const uint8_t * gm,
+                                         const uint8_t * um, int slot, int hrow0, uint32_t tr, int r) {
+#pragma clang fp contract(off)
+    const int lane = lane_id(), g64 = hrow0 >> 6;
+    LK_LOCAL float * terms = reinterpret_cast<LK_LOCAL float *>(lds + M_TERMS);   // [matrix][block][64 rows]
+    const uint8_t * xr = (const uint8_t *) (lds + M_X);
+    auto claim = [&](GuItem & it) {
+        unsigned c = 0;
+        if (lane == 0) { c = __hip_atomic_fetch_add(ctl + C_GUCLAIM, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+        it.c = (int) __builtin_amdgcn_readfirstlane(c);
+        if (it.c >= NITEM1) { return; }
+        const int j = it.c >> 1;
+        const uint8_t * mat = uniform1((it.c & 1) ? um : gm);
+        // the scale first: memory waits count loads in issue order
+        it.d = *gptr(reinterpret_cast<const uint16_t *>(mat + (size_t) (H1 / 64) * NBX1 * 4096 + ((size_t) g64 * NBX1 + j) * 128 + lane * 2));
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t * qb = mat + ((size_t) g64 * NBX1 + j) * 4096 + lane * 16;
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) { it.w[c4] = load_nt(qb + c4 * 1024); }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // false past the end (claims rise across the workgroup, so every later item of this wave is past the end too)
+    auto run = [&](const GuItem & it) -> bool {
+        if (it.c >= NITEM1) { return false; }
+        const int j = it.c >> 1;
+        const int bsum = block_bsum_dpp(it.w, tr, xr + j * GX1::XBLK, r);
+        const float dx = reinterpret_cast<const float *>(xr + NBX1 * GX1::XBLK)[j];
+        terms[it.c * 64 + lane] = (h2f(it.d) * dx) * (float) bsum;   // [matrix][block] = item c
+        if (arrive1(ctl + C_GUDONE, NITEM1)) {
+            float g = 0.f, u = 0.f;
+#pragma unroll 4
+            for (int k = 0; k < NBX1; ++k) { g = g + terms[(2 * k) * 64 + lane]; u = u + terms[(2 * k + 1) * 64 + lane]; }
+            st_tag1(a.th + (size_t) slot * H1 + hrow0 + lane, a.epoch, det_silu(0.125f * g) * (0.125f * u));
+        }
+        return true;
+    };
+    // one item in flight per wave: with 16 waves per CU, deeper look-ahead measured slower (more bytes in flight per
+    // CU than the memory path serves without queueing)
+    GuItem it;
+    claim(it);
+    while (run(it)) { claim(it); }
+}
+
+// ---------------------------------------------------------------- down: one 256-weight block per row
+// A unit is one 64-row group of one down matrix at one K-block: lane l owns row l (4 chunks + d); every lane's block
+// product uses the same staged h block, so the activations come by DPP from the 16 lanes that hold them.
+struct Dn1 { uint4 w[4]; uint16_t d; };
+__device__ __forceinline__ void dn1_issue(const uint8_t * mat, int g64, int kb, Dn1 & u) {
+    const int lane = lane_id();
+    const uint8_t * q = mat + ((size_t) g64 * NBH1 + kb) * 4096 + lane * 16;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) { u.w[c] = load_nt(q + c * 1024); }
+    u.d = *gptr(reinterpret_cast<const uint16_t *>(mat + (size_t) (E1 / 64) * NBH1 * 4096 + ((size_t) g64 * NBH1 + kb) * 128 + lane * 2));
+}
+// polls the 256 tagged h values of one block and stages their Q8_K (one wave); false on timeout
+__device__ __forceinline__ bool stage_h1(const D1Args & a, const uint64_t * src, LK_LOCAL uint8_t * dst) {
+    const int lane = lane_id();
+    uint64_t w[4];
+    auto issue = [&]() {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) { w[k] = ld_tag1(src + 4 * lane + k); }
+    };
+    issue();
+    int it = 0;
+    for (; it < POLL1; ++it) {
+        bool v = true;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) { v = v && tag1_ok(w[k], a.epoch); }
+        if (__ballot(!v) == 0) { break; }
+        __builtin_amdgcn_s_sleep(1);
+        issue();
+    }
+    if (it == POLL1) { return false; }
+    const float xs[4] = { tag1_val(w[0]), tag1_val(w[1]), tag1_val(w[2]), tag1_val(w[3]) };
+    float dq; const uint32_t packed = q8k_lane(xs, dq);
+    *reinterpret_cast<LK_LOCAL uint32_t *>(dst + staged_word(lane)) = packed;
+    if (lane == 0) { *reinterpret_cast<LK_LOCAL float *>(dst + QK) = dq; }
+    return true;
+}
+
+// ---------------------------------------------------------------- 4. combine
+// thread (row i, slot s) of the first 252: the 8 tagged block terms of its row and slot, folded in block order,
+// * 0.125; then thread i < 28 forms y = sum_k w_k o_k (k order) + o_shared (+ the residual)
+__device__ __forceinline__ bool combine1(const D1Args & a, lds1_t lds) {
+#pragma clang fp contract(off)
+    LK_LOCAL float * cmb = reinterpret_cast<LK_LOCAL float *>(lds + M_CMB);
+    const LK_LOCAL float * wts = reinterpret_cast<const LK_LOCAL float *>(lds + M_SEL + MAXK * 4);
+    const int t = threadIdx.x, row0 = blockIdx.x * CROWS1;
+    bool ok = true;
+    if (t < CROWS1 * SLOTS1) {
+        const int i = t / SLOTS1, s = t % SLOTS1, row = row0 + i;
+        uint64_t w[NBH1];
+        auto issue = [&]() {
+#pragma unroll
+            for (int kb = 0; kb < NBH1; ++kb) { w[kb] = ld_tag1(a.to + ((size_t) s * NBH1 + kb) * E1 + row); }
+        };
+        issue();
+        int it = 0;
+        for (; it < POLL1; ++it) {
+            bool v = true;
+#pragma unroll
+            for (int kb = 0; kb < NBH1; ++kb) { v = v && tag1_ok(w[kb], a.epoch); }
+            if (v) { break; }
+            __builtin_amdgcn_s_sleep(1);
+            issue();
+        }
+        ok = it < POLL1;
+        if (!ok) { __hip_atomic_store(reinterpret_cast<LK_LOCAL unsigned *>(lds + M_CTL) + C_CMBFAIL, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+        float o = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < NBH1; ++kb) { o = o + tag1_val(w[kb]); }
+        cmb[i * SLOTS1 + s] = 0.125f * o;
+    }
+    __syncthreads();
+    if (t < CROWS1) {
+        const int row = row0 + t;
+        float mv = cmb[t * SLOTS1] * wts[0];
+#pragma unroll
+        for (int k = 1; k < MAXK; ++k) { mv = mv + cmb[t * SLOTS1 + k] * wts[k]; }
+        float yv = mv + cmb[t * SLOTS1 + MAXK];
+        if (a.resid) { yv = yv + gptr(a.resid)[row]; }
+        gptr(a.y)[row] = yv;
+    }
+    (void) ok;
+    return true;
+}
+
+// the layer's routing outputs from the picks (workgroup 0): for one token the eight picks are distinct experts, so the
+// dispatch is their sort by expert id (ties impossible): perm / inv / act from the ranks, counts / offsets by expert
+__device__ __noinline__ void routing1(const D1Args & a, lds1_t lds) {
+    const LK_LOCAL int * sel = reinterpret_cast<const LK_LOCAL int *>(lds + M_SEL);
+    const LK_LOCAL float * wts = reinterpret_cast<const LK_LOCAL float *>(lds + M_SEL + MAXK * 4);
+    const int lane = lane_id();
+    if (lane < MAXK) {
+        const int e = sel[lane];
+        int rank = 0;
+#pragma unroll
+        for (int j = 0; j < MAXK; ++j) { rank += sel[j] < e ? 1 : 0; }
+        gptr(a.sel)[lane] = e; gptr(a.wts)[lane] = wts[lane];
+        gptr(a.perm)[rank] = lane; gptr(a.inv)[lane] = rank; gptr(a.act)[rank] = e;
+    }
+    if (lane == 0) { *gptr(a.nact) = MAXK; }
+    for (int x = lane; x <= a.n_exp; x += 64) {
+        int lt = 0, eq = 0;
+#pragma unroll
+        for (int j = 0; j < MAXK; ++j) { const int ej = sel[j]; lt += ej < x ? 1 : 0; eq += ej == x ? 1 : 0; }
+        gptr(a.offsets)[x] = lt;
+        if (x < a.n_exp) { gptr(a.counts)[x] = eq; }
+    }
+}
+
+// ---------------------------------------------------------------- the kernel
+__global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
+#pragma clang fp contract(off)
+    (void) sizeof(args);   // read in place in the kernarg segment (scalar loads), as the general decode kernel does
+    const D1Args & a = *(const D1Args *) __builtin_amdgcn_kernarg_segment_ptr();
+    extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds1[];
+    const lds1_t lds = (lds1_t) dyn_lds1;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
+    const int xcd = blockIdx.x % NX1, li = blockIdx.x / NX1;
+    LK_LOCAL unsigned * ctl = reinterpret_cast<LK_LOCAL unsigned *>(lds + M_CTL);
+    const int q = lane >> 4, r = lane & 15;
+    const uint32_t tr = tab_word_grid(lds_addr(dyn_lds1), lane);
+    TRACE1(0);
+    if (lds_addr(dyn_lds1) & 0xFFFFu) { report1(a, 4); return; }   // table addressing needs a 64 KB aligned base
+    if (threadIdx.x < NCTL1) { ctl[threadIdx.x] = 0; }
+    __syncthreads();
+
+    // 1. router on waves 0-3; table copy and token quantisation on the others; the shared gate/up task on the last 7
+    if (wave < 4) {
+        router1(a, lds, wave, ctl);
+        TRACE1(1);
+    } else {
+        (void) wait1(ctl + C_RISSUED, 4);   // the router's weight and token loads go first (the critical path)
+        static_assert(TAB_BYTES % (1024 * NQW1) == 0, "table image split over the staging waves");
+        constexpr int PER = TAB_BYTES / 1024 / NQW1;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int cc = (wave - 4) * PER + k;
+            __builtin_amdgcn_global_load_lds((const LK_GLOBAL void *) (a.tab + cc * 64 + lane), (LK_LOCAL void *) (lds + cc * 1024), 16, 0, 0);
+        }
+        if (a.prenorm && !wait1(ctl + C_NRM, 1)) { report1(a, 64); return; }
+        quant1(a, lds, wave - 4);
+        __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's table loads have landed in LDS
+        arrive1(ctl + C_STAGED, NQW1);
+        TRACE1(1);
+    }
+    if (wave >= W1 - GU_STEPS1) {   // the shared expert's gate/up task, one step per wave
+        if (!wait1(ctl + C_STAGED, NQW1)) { report1(a, 8); return; }
+        lds_visible();
+        shared_gu1(a, lds, wave, tr, q, r, ctl);
+        TRACE1(2);
+    }
+
+    // 2. selection (wave 0): the 256 tagged probabilities, then the picks and weights into LDS
+    if (wave == 0) {
+        __builtin_amdgcn_s_setprio(3);
+        float bv[4]; uint64_t pw[4]; float pv[4];
+        load_bias(a.bias, a.n_exp, bv);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { const int e = 4 * lane + j; pw[j] = e < a.n_exp ? ld_tag1(a.tlogits + e) : 0; }
+        bool ok = false;
+        for (int it = 0; it < POLL1; ++it) {
+            bool v = true;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { v = v && (4 * lane + j >= a.n_exp || tag1_ok(pw[j], a.epoch)); }
+            if (__ballot(!v) == 0) { ok = true; break; }
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { const int e = 4 * lane + j; pw[j] = e < a.n_exp ? ld_tag1(a.tlogits + e) : 0; }
+        }
+        TRACE1(3);
+        if (ok) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { pv[j] = 4 * lane + j < a.n_exp ? tag1_val(pw[j]) : 0.f; }
+            select_token_p<false>(pv, bv, a.n_exp, a.n_group, a.topk_group, a.topk, a.scale, nullptr,
+                                  (int *) (lds + M_SEL), (float *) (lds + M_SEL + MAXK * 4), MAXK, 0.f);
+        } else {
+            report1(a, 2);
+        }
+        __builtin_amdgcn_s_setprio(0);
+        flag1(ctl + C_READY, ok ? 1u : 2u);
+        TRACE1(4);
+    }
+    const unsigned ready = wait1(ctl + C_READY, 1);
+    if (ready != 1) { if (ready == 0) { report1(a, 8); } return; }
+    lds_visible();
+
+    // 3. routed gate/up: expert sel[xcd], h rows kb * 256 + qq * 64 .. + 63 (one row group of gate and up), as items
+    //    the waves claim from an LDS counter
+    const int kb = li / 4, qq = li % 4;
+    {
+        const int e = reinterpret_cast<const LK_LOCAL int *>(lds + M_SEL)[xcd];
+        if ((unsigned) e >= (unsigned) a.n_exp) { report1(a, 32); return; }
+        const uint8_t * gm = uniform1(a.gate + (size_t) e * a.estride), * um = uniform1(a.up + (size_t) e * a.estride);
+        TRACE1(5);
+        gate_up1(a, lds, ctl, gm, um, xcd, kb * QK + qq * 64, tr, r);
+        TRACE1(6);
+    }
+
+    // 4. down: the workgroup's units (28 routed row groups at K-block kb, 3 or 4 shared row groups at K-block xcd),
+    //    claimed by the waves in order; each wave's first unit streams in while the h blocks are polled and staged
+    const int nsh = li < RGE1 - 3 * 32 ? 4 : 3;   // shared row groups li, li + 32, .. (< 112)
+    const int nunits = RGQ1 + nsh;
+    const uint8_t * dmat = nullptr;
+    {
+        const int e = reinterpret_cast<const LK_LOCAL int *>(lds + M_SEL)[xcd];
+        dmat = uniform1(a.down + (size_t) e * a.estride);
+    }
+    auto unit = [&](int u, const uint8_t * & mat, int & g64, int & blk, int & slot) {
+        if (u < RGQ1) { mat = dmat; g64 = qq * RGQ1 + u; blk = kb; slot = xcd; }
+        else { mat = uniform1(a.sh_down); g64 = li + 32 * (u - RGQ1); blk = xcd; slot = 8; }
+    };
+    // the waves claim units from an LDS counter, one in flight per wave (as the gate/up items)
+    LK_LOCAL unsigned * dclaim = ctl + C_DNCLAIM;
+    auto claim_unit = [&](Dn1 & d, int & u) {
+        unsigned c = 0;
+        if (lane == 0) { c = __hip_atomic_fetch_add(dclaim, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+        u = (int) __builtin_amdgcn_readfirstlane(c);
+        if (u < nunits) { const uint8_t * m; int g, b, sl; unit(u, m, g, b, sl); dn1_issue(m, g, b, d); }
+    };
+    Dn1 dn; int un;
+    claim_unit(dn, un);
+    if (wave == 0) {
+        const bool ok = stage_h1(a, a.th + (size_t) xcd * H1 + (size_t) kb * QK, lds + M_HR);
+        if (!ok) { report1(a, 1); }
+        flag1(ctl + C_HR, ok ? 1u : 2u);
+    } else if (wave == 1) {
+        const bool ok = stage_h1(a, a.th + (size_t) 8 * H1 + (size_t) xcd * QK, lds + M_HS);
+        if (!ok) { report1(a, 1); }
+        flag1(ctl + C_HS, ok ? 1u : 2u);
+    }
+    TRACE1(7);
+    if (wait1(ctl + C_HR, 1) != 1 || wait1(ctl + C_HS, 1) != 1) { return; }
+    lds_visible();
+    TRACE1(8);
+    auto run_unit = [&](const Dn1 & d, int u) {
+        const uint8_t * m; int g, b, sl; unit(u, m, g, b, sl);
+        const uint8_t * hb = (const uint8_t *) (lds + (sl == 8 ? M_HS : M_HR));
+        const int bsum = block_bsum_dpp(d.w, tr, hb, r);
+        const float dx = *reinterpret_cast<const float *>(hb + QK);
+        st_tag1(a.to + ((size_t) sl * NBH1 + b) * E1 + (size_t) g * 64 + lane, a.epoch, (h2f(d.d) * dx) * (float) bsum);
+    };
+    while (un < nunits) { run_unit(dn, un); claim_unit(dn, un); }   // claims rise: the first past the end ends the list
+    TRACE1(9);
+
+    // 5. combine rows 28 b .. 28 b + 27 (a timed-out poll is flagged in LDS; no __syncthreads_and: it would take static
+    //    LDS and move the table base off its 64 KB alignment)
+    combine1(a, lds);
+    if (wave == 0 && __hip_atomic_load(ctl + C_CMBFAIL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) { report1(a, 16); }
+    TRACE1(10);
+    if (blockIdx.x == 0 && wave == W1 - 1) { routing1(a, lds); }
+}
+
+size_t decode1_lds_bytes() { return DEC1_LDS; }
+
+hipError_t decode1_init(int ncu, int * ok) {
+    *ok = 0;
+    if (ncu != G1) { return hipSuccess; }   // the XCD mapping needs one workgroup on each of 256 CUs
+    hipError_t e = hipFuncSetAttribute((const void *) k_moe_decode1, hipFuncAttributeMaxDynamicSharedMemorySize, DEC1_LDS);
+    if (e != hipSuccess) { return e; }
+    int per = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *) k_moe_decode1, NT1, DEC1_LDS);
+    if (e != hipSuccess) { return e; }
+    *ok = per >= 1 ? 1 : 0;
+    return hipSuccess;
+}
+
+hipError_t launch_moe_decode1(const DecodeArgs & a, bool cooperative, hipStream_t st) {
+    if (a.n != 1 || a.topk != MAXK || a.keep != MAXK || !decode_rule_ok(a.n_exp, a.n_group) || a.E != E1 || a.H != H1 ||
+        !a.th || !a.to || !a.tlogits || a.n_exp > NEXP_MAX) {
+        return hipErrorInvalidValue;
+    }
+    if (!cooperative) {
+        k_moe_decode1<<<G1, NT1, DEC1_LDS, st>>>(a);
+        return hipGetLastError();
+    }
+    DecodeArgs arg = a;
+    void * params[] = { &arg };
+    return hipLaunchCooperativeKernel((const void *) k_moe_decode1, dim3(G1), dim3(NT1), params, DEC1_LDS, st);
+}
+
+}  // namespace lk

@@ -78,6 +78,11 @@ size_t decode_lds_bytes();
 // grid workgroups (at most one per CU can be resident): a cooperative launch guarantees they are all resident; a
 // regular launch assumes it (nothing else running on the CUs) -- a violation ends in a reported wait timeout
 hipError_t launch_moe_decode(const DecodeArgs & a, int grid, bool cooperative, hipStream_t st);
+// one decode token with all topk = 8 picks kept, organised by XCD (moe_decode1.hip): 256 workgroups, one per CU of a
+// 256-CU device (*ok = 0 on other devices); same arguments, tagged buffers and results as launch_moe_decode
+hipError_t decode1_init(int ncu, int * ok);
+size_t decode1_lds_bytes();
+hipError_t launch_moe_decode1(const DecodeArgs & a, bool cooperative, hipStream_t st);
 
 // ---------------------------------------------------------------- prefill grouped GEMM on MFMA (moe_prefill.hip)
 struct PrefillArgs {

@@ -546,3 +546,86 @@ def test_prefill_mfma_exact_on_extreme_blocks(ctx, n):
             ctx.set_debug(False)
     for i, t in enumerate(tokens):
         assert np.array_equal(g[inv[t * 8:(t + 1) * 8]].view(np.uint32), want["g"][i * 8:(i + 1) * 8].view(np.uint32)), t
+
+
+@pytest.mark.parametrize("mode", [2, 1])
+def test_decode1_matches_general_and_checker(ctx, layer, mode):
+    """The one-token kernel organised by XCD (fl_set_decode1, default on) against the general single-launch decode
+    block and the per-pass kernels: y, the Q8_K of x, logits, probabilities and every routing output bit for bit, for
+    several tokens in a row; y also against the checker."""
+    W, b = layer.gate_inp.cpu().numpy(), layer.probs_b.cpu().numpy()
+    for i in range(3):
+        x = make_x(ctx, 1, seed=1100 + i)
+        got = {}
+        for name, m, d1 in (("decode1", mode, True), ("general", mode, False), ("per_pass", 0, True)):
+            ctx.set_decode1(d1)
+            try:
+                with ctx.using_fused(m):
+                    y = ctx.moe_layer(layer, x).clone()
+                    ctx.sync()
+                    st = _routing_state(ctx, 1)
+                    dbg = ctx.debug()
+                    assert dbg.kernel == {"decode1": 2, "general": 1, "per_pass": 0}[name], (name, dbg.kernel)
+                    st["logits"] = ctx.d2h(dbg.logits, (NEXP,), np.float32)
+                    st["probs"] = ctx.d2h(dbg.probs, (NEXP,), np.float32)
+                    st["y"] = y.cpu().numpy()
+                    got[name] = st
+            finally:
+                ctx.set_decode1(True)
+        for k in got["per_pass"]:
+            for other in ("decode1", "general"):
+                assert np.array_equal(np.asarray(got[other][k]).view(np.uint8), np.asarray(got["per_pass"][k]).view(np.uint8)), (other, k, i)
+        xs = x.cpu().numpy()
+        _, _, so, _ = orc.router(W, b, xs)
+        _, _, gate, up, down, sh = host_layer(ctx, layer, so.ravel())
+        ref = orc.moe_forward(xs, W, b, gate, up, down, *sh)
+        assert np.array_equal(got["decode1"]["y"].view(np.uint32), ref["y"].view(np.uint32)), i
+
+
+@pytest.mark.parametrize("weighted", [False, True])
+def test_decode1_prenorm_residual(ctx, layer, weighted):
+    """fl_moe_layer_normed at n = 1 (the 58-layer stack's call) through the kernel organised by XCD: the norm inside
+    the launch and the residual in its combine, bit-identical to the general decode block."""
+    import torch
+    h = make_x(ctx, 1, seed=1200) * 4.0
+    w = None
+    if weighted:
+        w = torch.empty(E, dtype=torch.float32, device="cuda")
+        ctx.synth_normal(w, 43, 6, 1.0, 0.1)
+    out = {}
+    for d1 in (True, False):
+        ctx.set_decode1(d1)
+        try:
+            out[d1] = (ctx.moe_layer_normed(layer, h, w, 1e-6).cpu().numpy(),
+                       ctx.moe_layer_normed(layer, h, w, 1e-6, residual=True).cpu().numpy())
+            ctx.sync()
+            assert ctx.debug().kernel == (2 if d1 else 1)
+        finally:
+            ctx.set_decode1(True)
+    for i in range(2):
+        assert np.array_equal(out[True][i].view(np.uint32), out[False][i].view(np.uint32)), i
+    assert np.array_equal(out[True][1].view(np.uint32), (out[True][0] + h.cpu().numpy()).astype(np.float32).view(np.uint32))
+
+
+def test_decode1_fewer_experts(ctx):
+    """A 64-expert layer (8 groups of 8): workgroups 64..255 own no router expert but still run their gate/up, down and
+    combine shares. The one-token kernel is bit-identical to the per-pass kernels and the checker."""
+    import torch
+    from loki_amd import MoeLayerWeights
+    layer = MoeLayerWeights.synthetic(ctx, 6464, n_exp=64)
+    x = make_x(ctx, 1, seed=6465)
+    y1 = ctx.moe_layer(layer, x).clone()
+    ctx.sync()
+    assert ctx.debug().fused == 1 and ctx.debug().kernel == 2
+    with ctx.using_fused(0):
+        y0 = ctx.moe_layer(layer, x)
+        ctx.sync()
+    assert np.array_equal(y1.cpu().numpy().view(np.uint32), y0.cpu().numpy().view(np.uint32))
+    xs = x.cpu().numpy()
+    W, b = layer.gate_inp.cpu().numpy(), layer.probs_b.cpu().numpy()
+    _, _, so, _ = orc.router(W, b, xs)
+    _, _, gate, up, down, sh = host_layer(ctx, layer, so.ravel())
+    ref = orc.moe_forward(xs, W, b, gate, up, down, *sh)
+    assert np.array_equal(y1.cpu().numpy().view(np.uint32), ref["y"].view(np.uint32))
+    del layer
+    torch.cuda.empty_cache()
