@@ -79,6 +79,8 @@ __global__ void __launch_bounds__(256) k_zero16(uint4 * p, size_t n) {
     for (size_t i = (size_t) blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t) gridDim.x * 256) { p[i] = make_uint4(0, 0, 0, 0); }
 }
 
+static bool decode1_ready(FLCtx * c);
+
 // ================================================================ lifecycle
 extern "C" FLCtx * fl_init(int kvp, int sc_cap) {
     (void) kvp; (void) sc_cap;
@@ -95,6 +97,7 @@ extern "C" FLCtx * fl_init(int kvp, int sc_cap) {
         __atomic_store_n(c->herr, 0, __ATOMIC_RELEASE);
     }
     (void) na_resolve(c->dev);   // the allocation-free entry point's scratch on this device
+    (void) decode1_ready(c);     // its set-up (attributes, XCD probe) here, not in a call that must not allocate
     return c;
 }
 
@@ -139,7 +142,7 @@ extern "C" int fl_sync(FLCtx * c) {
     }
     if (c->herr) { e |= __atomic_exchange_n(c->herr, 0, __ATOMIC_ACQ_REL); }
     if (e) {
-        return fail(c, FL_EHIP, "a device kernel reported error code %d (decode block: a wait timed out; prefill: bad LDS base); its outputs are invalid", e);
+        return fail(c, FL_EHIP, "a device kernel reported error code %d (decode block: a wait timed out or a workgroup ran on an unexpected XCD; prefill: bad LDS base); its outputs are invalid", e);
     }
     return FL_OK;
 }

@@ -2,24 +2,29 @@
 //
 // Reference path (src/fused_layer.cu): router_probs + router_topk (:313-332), the host round-trip (fl_fetch :587-598,
 // eng:793-818), fl_moe (:599-612): quant_x, tc_matvec gate/up, swiglu_q8, tc_matvec down, moe_combine. Here the
-// 256 workgroups (one per CU, 16 waves, 32 per XCD; workgroup b runs on XCD b % 8) run the block end to end:
+// 256 workgroups (one per CU, 16 waves, 32 per XCD) run the block end to end. A workgroup's role is (x, i): x the XCD
+// it runs on (hardware register XCC_ID), i = b / 8; the dispatch places workgroup b on XCD (r + b) % 8, so every role
+// is taken once.
 //   1. every workgroup b computes the router logit of expert b (the fp64 chunk-and-tree contract, waves 0-3) and
-//      publishes p = sigmoid(logit) as an epoch-tagged word, while waves 4-15 stage the codebook/sign tables and Q8_K(x)
+//      publishes the logit as an epoch-tagged word, while waves 4-15 stage the codebook/sign tables and Q8_K(x)
 //      in LDS and the last 7 waves then run one gate/up task of the shared expert (routing-independent: shared h rows
-//      8 t .. 8 t + 7 with t = 32 (b % 8) + b / 8, so XCD x produces the shared expert's h block x);
-//   2. wave 0 selects the token's experts; pick k (0..7, selection order) is slot k, and slot k runs on XCD k:
-//      workgroup b computes h rows kb * 256 + q * 64 .. + 63 of expert sel[b % 8] (kb = (b / 8) / 4, q = (b / 8) % 4)
-//      as 56 items (one matrix, one 256-weight block, 64 rows) that the waves claim from an LDS counter;
+//      8 t .. 8 t + 7 with t = 32 x + i, so XCD x produces the shared expert's h block x);
+//   2. one workgroup per XCD selects the token's experts and broadcasts the picks to its XCD; pick k (0..7, selection
+//      order) is slot k, and slot k runs on XCD k: role (x, i) computes h rows kb * 256 + q * 64 .. + 63 of expert
+//      sel[x] (kb = i / 4, q = i % 4) as 56 items (one matrix, one 256-weight block, 64 rows) that the waves claim
+//      from an LDS counter;
 //   3. the four workgroups of (slot, kb) complete h block kb of their slot; each of them quantises that block to Q8_K
 //      and runs K-block kb of the slot's down for a quarter of its 7168 rows (split-K: one 256-weight block per row,
-//      one row per lane), plus 3 or 4 row groups of the shared expert's down for K-block b % 8, again claimed by the
+//      one row per lane), plus 3 or 4 row groups of the shared expert's down for K-block x, again claimed by the
 //      waves unit by unit. Each row's block term (d_w * d_x) * bsum is published as a tagged word;
 //   4. workgroup b combines rows 28 b .. 28 b + 27: per slot the 8 block terms folded in block order (ggml's sumf),
 //      * 0.125, then y = sum_k w_k o_k in k order + the shared o (+ the residual).
 // The arithmetic is that of the other decode kernels and the CPU checker step for step (the same device functions and
 // fold orders), so y is bit-identical to them. The down waits on four workgroups of its own XCD rather than on every
-// gate/up task of the expert, and no dispatch table is built (one token: the picks are distinct experts). Every wait is
-// bounded: a timeout sets the error word and the wave skips the work, so the grid always drains.
+// gate/up task of the expert, and no dispatch table is built (one token: the picks are distinct experts). Hand-offs
+// inside an XCD (the picks, h) stay in its L2; those across XCDs (logits, down partials) go through the device's
+// coherence point. Every wait is bounded: a timeout sets the error word and the wave skips the work, so the grid
+// always drains.
 #include "moe_device.h"
 #include "moe_kernels.h"
 
@@ -38,6 +43,7 @@ constexpr int E1 = 7168, H1 = 2048;
 using GX1 = Geo<7, 0>;                 // the token's staged Q8_K row: 28 blocks, no padding
 constexpr int NBX1 = E1 / QK, NBH1 = H1 / QK;    // 28, 8 blocks
 constexpr int SLOTS1 = 9;              // 8 picks + the shared expert (slot 8)
+constexpr int BCAST1 = 1024;           // tagged words 1024 + 16 x .. + 15: XCD x's picks and weights (one-token calls use 0..255)
 constexpr int QROWS1 = E1 / 4;         // routed down rows per workgroup (a quarter): 1792 = 28 row groups
 constexpr int RGQ1 = QROWS1 / 64;      // 28
 constexpr int RGE1 = E1 / 64;          // 112 row groups of the shared expert's down block
@@ -45,7 +51,8 @@ constexpr int CROWS1 = E1 / G1;        // combine rows per workgroup: 28
 constexpr int GU_STEPS1 = NBX1 / 4;    // 7
 constexpr int NITEM1 = 2 * NBX1;       // routed gate/up items of a workgroup: (matrix, block) of its 64 h rows
 static_assert(G1 == 32 * NX1 && H1 == NX1 * QK && CROWS1 * G1 == E1, "decode-1 geometry");
-static_assert((size_t) SLOTS1 * H1 <= DEC_TH && (size_t) SLOTS1 * NBH1 * E1 <= DEC_TO, "tagged buffers");
+static_assert((size_t) SLOTS1 * H1 <= DEC_TH && (size_t) SLOTS1 * NBH1 * E1 <= DEC_TO && BCAST1 >= 256 &&
+              (size_t) BCAST1 + 16 * 8 <= DEC_TLOGITS, "tagged buffers");
 
 // LDS layout (bytes)
 constexpr int M_X = TAB_BYTES;                     // staged Q8_K of the token
@@ -62,7 +69,7 @@ constexpr int M_NRM = M_CTL + NCTL1 * 4;           // RMSNorm scale
 constexpr int DEC1_LDS = M_NRM + 16;
 static_assert(DEC1_LDS <= 160 * 1024 && (M_X % 16) == 0 && (M_HR % 16) == 0 && (M_HS % 16) == 0, "LDS layout");
 enum { C_RT = 0, C_STAGED = 1, C_SH = 2, C_READY = 3, C_HR = 4, C_HS = 5, C_CMBFAIL = 6, C_NRM = 7, C_RISSUED = 8,
-       C_GUCLAIM = 9, C_DNCLAIM = 10, C_GUDONE = 11 };
+       C_GUCLAIM = 9, C_DNCLAIM = 10, C_GUDONE = 11, C_SB1 = 12, C_SELFAIL = 13 };
 
 typedef LK_LOCAL uint8_t * lds1_t;
 typedef LK_CONST DecodeArgs D1Args;
@@ -75,6 +82,14 @@ __device__ __forceinline__ void report1(const D1Args & a, int code) {
 }
 __device__ __forceinline__ void st_tag1(uint64_t * p, uint32_t epoch, float v) {
     __hip_atomic_store(gptr(p), ((uint64_t) epoch << 32) | __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// A tagged word for readers on the writer's own XCD: a plain 64-bit store (workgroup scope emits no write-through), which
+// stays in the XCD's shared L2 where the readers' device-scope loads (ld_tag1) find it, instead of travelling to the
+// device's coherence point and back. Writer and readers share an XCD by construction (roles come from XCC_ID; set-up
+// checks that the dispatch is a rotation over the XCDs); were a role missing, the readers' bounded waits would time out
+// and report the error -- never a stale value, since every word carries the call's epoch.
+__device__ __forceinline__ void st_xcd1(uint64_t * p, uint32_t epoch, uint32_t bits) {
+    __hip_atomic_store(gptr(p), ((uint64_t) epoch << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 __device__ __forceinline__ uint64_t ld_tag1(const uint64_t * p) { return __hip_atomic_load(gptr(const_cast<uint64_t *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 __device__ __forceinline__ bool tag1_ok(uint64_t w, uint32_t epoch) { return (uint32_t) (w >> 32) == epoch; }
@@ -100,6 +115,12 @@ __device__ __forceinline__ unsigned wait1(LK_LOCAL unsigned * w, unsigned want_a
 __device__ __forceinline__ void flag1(LK_LOCAL unsigned * w, unsigned v) {
     lds_visible();
     if (lane_id() == 0) { __hip_atomic_store(w, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+}
+// the XCD this workgroup runs on (hardware register XCC_ID)
+__device__ __forceinline__ int xcc_id1() {
+    unsigned x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return (int) (x & 0xFu);
 }
 __device__ __forceinline__ const uint8_t * uniform1(const uint8_t * p) {
     const uint64_t v = (uint64_t) p;
@@ -135,7 +156,7 @@ __device__ __forceinline__ float4 in1(const D1Args & a, lds1_t lds, int col, flo
 // ---------------------------------------------------------------- 1. router (waves 0-3) and staging (waves 4-7)
 // Thread (quarter w = wave, lane) owns chunk 64 w + lane (28 values) of expert b's logit: in-order fp64 chunk sum,
 // tree levels 1-6 by DPP (tree64), levels 7-8 over the four waves' totals in LDS; the last wave to arrive publishes
-// p = sigmoid(logit). Under prenorm the same threads first form the token's RMSNorm scale (the chunked sum-of-squares
+// the logit (the selecting waves form p = sigmoid(logit)). Under prenorm the same threads first form the token's RMSNorm scale (the chunked sum-of-squares
 // contract of k_rmsnorm, over the same chunks). Workgroups past the layer's experts only form the scale.
 __device__ __noinline__ void router1(const D1Args & a, lds1_t lds, int wave, LK_LOCAL unsigned * ctl) {
 #pragma clang fp contract(off)
@@ -194,11 +215,54 @@ __device__ __noinline__ void router1(const D1Args & a, lds1_t lds, int wave, LK_
     if (arrive1(ctl + C_RT, want) && lane == 0) {
         const LK_LOCAL double * pp = a.prenorm ? reinterpret_cast<const LK_LOCAL double *>(lds + M_SCR + 32) : part;
         const float l = (float) ((pp[0] + pp[1]) + (pp[2] + pp[3]));
-        const float p = det_sigmoid(l);
-        st_tag1(a.tlogits + e, a.epoch, p);
+        st_tag1(a.tlogits + e, a.epoch, l);   // the logit goes out first: the selecting waves form the sigmoid
         gptr(a.logits)[e] = l;
-        if (a.probs) { gptr(a.probs)[e] = p; }
+        if (a.probs) { gptr(a.probs)[e] = det_sigmoid(l); }
     }
+}
+
+// ---------------------------------------------------------------- selection (one workgroup per XCD)
+// Waves 0-3 each poll 64 of the tagged logits and form their probabilities (one sigmoid per lane, into LDS); wave 0 then
+// runs select_token_p on them (four per lane). The sigmoid's fp64 chain is the longest part of the per-lane work, so
+// spreading it over four waves takes three quarters of it off the selecting wave.
+constexpr int S_P = M_TERMS;   // f32 [256] probabilities (the gate/up terms' space, unused until the picks are known)
+static_assert(S_P + NEXP_MAX * 4 <= M_TERMS + NITEM1 * 64 * 4, "probabilities inside the gate/up terms");
+
+// waves 0-3; returns (wave 0) whether the picks and weights in M_SEL are valid
+__device__ __forceinline__ bool select4(const D1Args & a, lds1_t lds, int wave, LK_LOCAL unsigned * ctl) {
+#pragma clang fp contract(off)
+    const int lane = lane_id(), e = wave * 64 + lane;
+    LK_LOCAL float * ps = reinterpret_cast<LK_LOCAL float *>(lds + S_P);
+    const bool mine = e < a.n_exp;
+    float bv[4];
+    if (wave == 0) { load_bias(a.bias, a.n_exp, bv); }   // issued before the polls: its latency hides behind them
+    uint64_t w = mine ? ld_tag1(a.tlogits + e) : 0;
+    bool ok = false;
+    for (int it = 0; it < POLL1; ++it) {
+        if (__ballot(mine && !tag1_ok(w, a.epoch)) == 0) { ok = true; break; }
+        __builtin_amdgcn_s_sleep(1);
+        if (mine) { w = ld_tag1(a.tlogits + e); }
+    }
+    TRACE1(3);
+    ps[e] = mine ? det_sigmoid(tag1_val(w)) : 0.f;
+    if (!ok) { report1(a, 2); __hip_atomic_store(ctl + C_SELFAIL, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+    arrive1(ctl + C_SB1, 4);
+    if (wave != 0) { return ok; }
+    ok = wait1(ctl + C_SB1, 4) == 4 && ok;
+    lds_visible();
+    ok = ok && __hip_atomic_load(ctl + C_SELFAIL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == 0;
+    if (!ok) { return false; }
+    const f32x4 p4 = *reinterpret_cast<const LK_LOCAL f32x4 *>(ps + 4 * lane);
+    const float pv[4] = {p4[0], p4[1], p4[2], p4[3]};
+    int * so = (int *) (lds + M_SEL); float * wo = (float *) (lds + M_SEL + MAXK * 4);
+    if (a.n_exp == 256 && a.n_group == 8 && a.topk_group == 4) {
+        // DeepSeek's rule as constants: the same function, its divisions, bounds and loop counts folded (about twice
+        // as fast as with the rule read from the arguments)
+        select_token_p<false>(pv, bv, 256, 8, 4, MAXK, a.scale, nullptr, so, wo, MAXK, 0.f);
+    } else {
+        select_token_p<false>(pv, bv, a.n_exp, a.n_group, a.topk_group, MAXK, a.scale, nullptr, so, wo, MAXK, 0.f);
+    }
+    return true;
 }
 
 // Q8_K of the token's 28 blocks into LDS (staged layout) by the staging waves: a pass quantises 4 consecutive blocks,
@@ -248,14 +312,17 @@ __device__ __forceinline__ void gu1_issue(const Gu1 & t, int s, uint4 (&pf)[4], 
 __device__ __forceinline__ void gu1_publish(const D1Args & a, int slot, int hrow0, int q, int r, float acc) {
 #pragma clang fp contract(off)
     const float other = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, acc), 0x128, 0xF, 0xF, false));
-    if (q == 0 && r < 8) { st_tag1(a.th + (size_t) slot * H1 + hrow0 + r, a.epoch, det_silu(0.125f * acc) * (0.125f * other)); }
+    if (q == 0 && r < 8) {
+        st_xcd1(a.th + (size_t) slot * H1 + hrow0 + r, a.epoch, __builtin_bit_cast(uint32_t, det_silu(0.125f * acc) * (0.125f * other)));
+    }
 }
 
 // The shared expert's task (8 h rows) split over the last 7 waves (one step each): block terms to LDS, the last wave
 // folds them in block order and publishes h -- a pass's arithmetic, finished while the routing runs.
-__device__ __forceinline__ void shared_gu1(const D1Args & a, lds1_t lds, int wave, uint32_t tr, int q, int r, LK_LOCAL unsigned * ctl) {
+__device__ __forceinline__ void shared_gu1(const D1Args & a, lds1_t lds, int wave, int xcd, int li, uint32_t tr, int q, int r,
+                                           LK_LOCAL unsigned * ctl) {
 #pragma clang fp contract(off)
-    const int lane = lane_id(), hrow0 = ((blockIdx.x % NX1) * 32 + blockIdx.x / NX1) * 8;
+    const int lane = lane_id(), hrow0 = (xcd * 32 + li) * 8;
     const Gu1 t = gu1_task(uniform1(a.sh_gate), uniform1(a.sh_up), hrow0, q, r);
     LK_LOCAL float * terms = reinterpret_cast<LK_LOCAL float *>(lds + M_PRE);
     const uint8_t * xr = (const uint8_t *) (lds + M_X);
@@ -313,7 +380,7 @@ __device__ __forceinline__ void gate_up1(const D1Args & a, lds1_t lds, LK_LOCAL 
             float g = 0.f, u = 0.f;
 #pragma unroll 4
             for (int k = 0; k < NBX1; ++k) { g = g + terms[(2 * k) * 64 + lane]; u = u + terms[(2 * k + 1) * 64 + lane]; }
-            st_tag1(a.th + (size_t) slot * H1 + hrow0 + lane, a.epoch, det_silu(0.125f * g) * (0.125f * u));
+            st_xcd1(a.th + (size_t) slot * H1 + hrow0 + lane, a.epoch, __builtin_bit_cast(uint32_t, det_silu(0.125f * g) * (0.125f * u)));
         }
         return true;
     };
@@ -440,7 +507,10 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
     extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds1[];
     const lds1_t lds = (lds1_t) dyn_lds1;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
-    const int xcd = blockIdx.x % NX1, li = blockIdx.x / NX1;
+    // roles by the XCD the workgroup runs on: the hardware dispatches workgroups round-robin over the XCDs from
+    // wherever the previous dispatch stopped, so XCD (r + b) % 8 runs workgroup b; under any such rotation
+    // (XCC_ID, b / 8) takes each of the 8 x 32 roles once
+    const int xcd = xcc_id1(), li = blockIdx.x / NX1;
     LK_LOCAL unsigned * ctl = reinterpret_cast<LK_LOCAL unsigned *>(lds + M_CTL);
     const int q = lane >> 4, r = lane & 15;
     const uint32_t tr = tab_word_grid(lds_addr(dyn_lds1), lane);
@@ -471,37 +541,38 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
     if (wave >= W1 - GU_STEPS1) {   // the shared expert's gate/up task, one step per wave
         if (!wait1(ctl + C_STAGED, NQW1)) { report1(a, 8); return; }
         lds_visible();
-        shared_gu1(a, lds, wave, tr, q, r, ctl);
+        shared_gu1(a, lds, wave, xcd, li, tr, q, r, ctl);
         TRACE1(2);
     }
 
-    // 2. selection (wave 0): the 256 tagged probabilities, then the picks and weights into LDS
-    if (wave == 0) {
+    // 2. selection, two levels: on each XCD one workgroup (li = 0) selects (select4: its four router waves poll the
+    //    logits and form the probabilities, wave 0 selects) and broadcasts the picks and weights through its XCD's L2
+    //    (st_xcd1); the XCD's other workgroups poll that one line. Only 8 workgroups poll the device-wide logits, which
+    //    every router workgroup is writing at the same time.
+    if (li == 0 && wave < 4) {
         __builtin_amdgcn_s_setprio(3);
-        float bv[4]; uint64_t pw[4]; float pv[4];
-        load_bias(a.bias, a.n_exp, bv);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) { const int e = 4 * lane + j; pw[j] = e < a.n_exp ? ld_tag1(a.tlogits + e) : 0; }
+        const bool ok = select4(a, lds, wave, ctl);
+        __builtin_amdgcn_s_setprio(0);
+        if (wave == 0) {
+            lds_visible();
+            if (ok && lane < 16) {
+                st_xcd1(a.tlogits + BCAST1 + xcd * 16 + lane, a.epoch, reinterpret_cast<const LK_LOCAL uint32_t *>(lds + M_SEL)[lane]);
+            }
+            flag1(ctl + C_READY, ok ? 1u : 2u);
+            TRACE1(4);
+        }
+    } else if (li != 0 && wave == 0) {
+        const uint64_t * bc = a.tlogits + BCAST1 + xcd * 16;   // [8 picks, 8 weights] of this XCD
+        uint64_t w = lane < 16 ? ld_tag1(bc + lane) : 0;
         bool ok = false;
         for (int it = 0; it < POLL1; ++it) {
-            bool v = true;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) { v = v && (4 * lane + j >= a.n_exp || tag1_ok(pw[j], a.epoch)); }
-            if (__ballot(!v) == 0) { ok = true; break; }
+            if (__ballot(lane < 16 && !tag1_ok(w, a.epoch)) == 0) { ok = true; break; }
             __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) { const int e = 4 * lane + j; pw[j] = e < a.n_exp ? ld_tag1(a.tlogits + e) : 0; }
+            if (lane < 16) { w = ld_tag1(bc + lane); }
         }
         TRACE1(3);
-        if (ok) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) { pv[j] = 4 * lane + j < a.n_exp ? tag1_val(pw[j]) : 0.f; }
-            select_token_p<false>(pv, bv, a.n_exp, a.n_group, a.topk_group, a.topk, a.scale, nullptr,
-                                  (int *) (lds + M_SEL), (float *) (lds + M_SEL + MAXK * 4), MAXK, 0.f);
-        } else {
-            report1(a, 2);
-        }
-        __builtin_amdgcn_s_setprio(0);
+        if (ok && lane < 16) { reinterpret_cast<LK_LOCAL uint32_t *>(lds + M_SEL)[lane] = (uint32_t) w; }
+        if (!ok) { report1(a, 2); }
         flag1(ctl + C_READY, ok ? 1u : 2u);
         TRACE1(4);
     }
@@ -577,6 +648,10 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
 
 size_t decode1_lds_bytes() { return DEC1_LDS; }
 
+// set-up probe: the XCD of every workgroup of a 256-workgroup launch
+__device__ int g_xcc1[G1];
+__global__ void k_xcc_probe1() { if (threadIdx.x == 0) { g_xcc1[blockIdx.x] = xcc_id1(); } }
+
 hipError_t decode1_init(int ncu, int * ok) {
     *ok = 0;
     if (ncu != G1) { return hipSuccess; }   // the XCD mapping needs one workgroup on each of 256 CUs
@@ -585,7 +660,15 @@ hipError_t decode1_init(int ncu, int * ok) {
     int per = 0;
     e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *) k_moe_decode1, NT1, DEC1_LDS);
     if (e != hipSuccess) { return e; }
-    *ok = per >= 1 ? 1 : 0;
+    if (per < 1) { return hipSuccess; }
+    // roles come from the XCD a workgroup runs on, and hand-offs inside an XCD go through its L2: the dispatch must
+    // place workgroup b on XCD (r + b) % 8 for one r
+    hipLaunchKernelGGL(k_xcc_probe1, dim3(G1), dim3(64), 0, 0);
+    if ((e = hipGetLastError()) != hipSuccess) { return e; }
+    int x[G1];
+    if ((e = hipMemcpyFromSymbol(x, HIP_SYMBOL(g_xcc1), sizeof x)) != hipSuccess) { return e; }
+    for (int b = 0; b < G1; ++b) { if (x[b] != (x[0] + b) % NX1) { return hipSuccess; } }
+    *ok = 1;
     return hipSuccess;
 }
 

@@ -629,3 +629,48 @@ def test_decode1_fewer_experts(ctx):
     assert np.array_equal(y1.cpu().numpy().view(np.uint32), ref["y"].view(np.uint32))
     del layer
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("pattern", ["pairs", "groups", "quads"])
+def test_decode1_selection_ties(ctx, pattern):
+    """Exact ties in the selection, made by copying router rows and biases: "pairs" (expert e ^ 1 = e: tied keys
+    inside every group), "groups" (group g ^ 1 = group g: tied group scores at every rank), "quads" (expert e % 64 for
+    all e: four copies of every key and group scores tied in two classes of four). The one-token kernel (its selection on
+    four waves, one expert per thread) gives the picks, weights and y of the general decode block, the per-pass kernels
+    and the checker bit for bit: ties to the lower index, groups tied to the lower group."""
+    import torch
+    from loki_amd import MoeLayerWeights
+    layer = MoeLayerWeights.synthetic(ctx, 7070)
+    W, b = layer.gate_inp, layer.probs_b
+    idx = torch.arange(NEXP, device=W.device)
+    src = {"pairs": idx & ~1, "groups": idx & ~32, "quads": idx % 64}[pattern]
+    W.copy_(W[src].clone())
+    b.copy_(b[src].clone())
+    torch.cuda.synchronize()
+    Wh, bh = W.cpu().numpy(), b.cpu().numpy()
+    for i in range(2):
+        x = make_x(ctx, 1, seed=7100 + i)
+        got = {}
+        for name, m, d1 in (("decode1", 2, True), ("general", 2, False), ("per_pass", 0, True)):
+            ctx.set_decode1(d1)
+            try:
+                with ctx.using_fused(m):
+                    y = ctx.moe_layer(layer, x).clone()
+                    ctx.sync()
+                    assert ctx.debug().kernel == {"decode1": 2, "general": 1, "per_pass": 0}[name]
+                    st = _routing_state(ctx, 1)
+                    got[name] = (st["sel"], st["wts"], y.cpu().numpy())
+            finally:
+                ctx.set_decode1(True)
+        for other in ("decode1", "general"):
+            for k in range(3):
+                assert np.array_equal(np.asarray(got[other][k]).view(np.uint8), np.asarray(got["per_pass"][k]).view(np.uint8)), (pattern, other, k, i)
+        xs = x.cpu().numpy()
+        _, _, so, wo = orc.router(Wh, bh, xs)
+        assert np.array_equal(got["decode1"][0], so.ravel().astype(np.int32)) and np.array_equal(got["decode1"][1].view(np.uint32), wo.ravel().view(np.uint32))
+        _, _, gate, up, down, sh = host_layer(ctx, layer, so.ravel())
+        ref = orc.moe_forward(xs, Wh, bh, gate, up, down, *sh)
+        assert np.array_equal(got["decode1"][2].view(np.uint32), ref["y"].view(np.uint32)), (pattern, i)
+        assert len(set(so.ravel().tolist())) == 8
+    del layer
+    torch.cuda.empty_cache()
