@@ -245,6 +245,74 @@ def run_kquant(ctx, torch, iters=20, seed=20260401):
     return out
 
 
+def run_dropin(ctx, torch, steps=30, warmup=3, ggml_steps=3, seed=20260601):
+    """The reference-named path at decode-1, as the engine drives it (src/server_core_fused.cpp:946-953): per token
+    fl_ffn_begin (router input and residual from the host; routing and shared expert) -> fl_fetch (routing to the host,
+    waited) -> fl_moe on the layer's resident 256-expert arena (ids = expert ids, waited; h and moe to the host). The
+    arena and the shared expert are tiled and declared (fl_register_tiled), so fl_moe reads them in place; the same
+    layer in ggml's layout (undeclared: repacked on every call, the reference's refilled-arena contract) is timed over a
+    few tokens for comparison. Times are host wall clock per token (every step ends in a host wait)."""
+    import ctypes
+    import numpy as np
+    from loki_amd import FLOut, FLW, MoeLayerWeights, lib
+    L = MoeLayerWeights.synthetic(ctx, seed)
+    mats = (L.gate, L.up, L.down, L.sh_gate, L.sh_up, L.sh_down)
+    for t in mats:
+        ctx.register_tiled(t)
+    rng = np.random.default_rng(seed)
+    xs = rng.standard_normal((steps + warmup, E)).astype(np.float32)
+    fis = rng.standard_normal((steps + warmup, E)).astype(np.float32)
+    out = FLOut()
+    ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+
+    def flw(sh):
+        w = FLW()
+        w.gate_inp = L.gate_inp.data_ptr(); w.probs_b = L.probs_b.data_ptr(); w.gate_f16 = 0
+        w.sh_gate, w.sh_up, w.sh_down = (m.data_ptr() for m in sh)
+        return w
+
+    def token(i, w, g, u, d, split):
+        t0 = time.perf_counter()
+        ctx.check(lib().fl_ffn_begin(ctx.ctx, ctypes.byref(w), 1, ptr(xs[i]), ptr(fis[i]), -1))
+        t1 = time.perf_counter()
+        lib().fl_fetch(ctx.ctx, 1, 1, ctypes.byref(out))
+        t2 = time.perf_counter()
+        sel = np.ctypeslib.as_array(out.sel, shape=(8,)).astype(np.int32)   # the resident arena: slot id = expert id
+        wts = np.ctypeslib.as_array(out.wts, shape=(8,)).copy()
+        lib().fl_moe(ctx.ctx, g.data_ptr(), u.data_ptr(), d.data_ptr(), 256, 4, ptr(sel), ptr(wts), 8, 1, ctypes.byref(out))
+        t3 = time.perf_counter()
+        split[0] += t1 - t0; split[1] += t2 - t1; split[2] += t3 - t2
+
+    res = {}
+    try:
+        w = flw((L.sh_gate, L.sh_up, L.sh_down))
+        split = [0.0, 0.0, 0.0]
+        for i in range(warmup):
+            token(i, w, L.gate, L.up, L.down, [0.0, 0.0, 0.0])
+        for i in range(steps):
+            token(warmup + i, w, L.gate, L.up, L.down, split)
+        res["us_per_token"] = round(sum(split) / steps * 1e6, 1)
+        res["ffn_begin_us"], res["fetch_us"], res["moe_us"] = (round(v / steps * 1e6, 1) for v in split)
+        res["tokens"] = steps
+    finally:
+        for t in mats:
+            ctx.unregister_tiled(t)
+    # the same layer in ggml's layout, undeclared: fl_ffn_begin packs the shared expert once (cached by pointer) and
+    # fl_moe repacks the 256-expert arena on every call
+    gg = [ctx.unpack(m, r, c, n) for m, (r, c, n) in zip(mats, ((2048, E, 256), (2048, E, 256), (E, 2048, 256), (2048, E, 1), (2048, E, 1), (E, 2048, 1)))]
+    torch.cuda.synchronize()
+    w = flw(gg[3:])
+    split = [0.0, 0.0, 0.0]
+    token(0, w, gg[0], gg[1], gg[2], [0.0, 0.0, 0.0])
+    for i in range(ggml_steps):
+        token(1 + i, w, gg[0], gg[1], gg[2], split)
+    res["ggml_arena_us_per_token"] = round(sum(split) / ggml_steps * 1e6, 1)
+    res["ggml_arena_tokens"] = ggml_steps
+    del gg, L
+    torch.cuda.empty_cache()
+    return res
+
+
 def run_realfmt(ctx, torch, steps=20, warmup=3, copies=2, seed=20260501):
     """fl_moe_layer on the reference's real-shard formats, device-resident: IQ2_XXS routed gate/up (tiled), Q3_K routed
     down and a Q5_K / Q5_K / Q6_K shared expert read in place (fl_set_layer_formats); decode-8 and decode-1, fresh x per
@@ -425,6 +493,8 @@ def bench(args, ctx, torch):
             cpu_leg(r)
             del r
             torch.cuda.empty_cache()
+        extra["dropin_decode1"] = run_dropin(ctx, torch)
+        log("[bench] dropin_decode1: %s" % json.dumps(extra["dropin_decode1"]))
         extra["kquant"] = run_kquant(ctx, torch)
         extra["real_formats"] = run_realfmt(ctx, torch)
     if not args.no_stack:

@@ -147,6 +147,15 @@ int fl_kq_matvec_dev(FLCtx *, int fmt, const void * w, int R, int K, const int8_
 /* IQ2_XXS ggml layout <-> tiled layout for nmat matrices of R x K at byte strides (device, may not alias) */
 int fl_pack_iq2xxs(FLCtx *, const void * src_ggml, size_t src_stride, void * dst_tiled, size_t dst_stride, int R, int K, int nmat);
 int fl_unpack_iq2xxs(FLCtx *, const void * src_tiled, size_t src_stride, void * dst_ggml, size_t dst_stride, int R, int K, int nmat);
+/* Declares [base, base + bytes) (device) to hold IQ2_XXS matrices in the tiled layout (fl_pack_iq2xxs's output, or
+ * fl_synth_iq2xxs with FL_LAYOUT_TILED); process-wide. fl_moe, fl_wide_moe and fl_ffn_begin read an arena or shared
+ * matrix that lies wholly inside a declared range as it is, instead of repacking it from ggml's layout on every call
+ * (the reference refills its arenas in place, src/server_core_fused.cpp:295-305, so memory not declared is always
+ * repacked). A resident 256-expert arena is the case this serves. No counterpart in the reference. Layers loaded by
+ * fl_gguf_load_moe_layer with FL_LAYOUT_TILED are declared by it and forgotten by fl_gguf_free_layer. */
+int fl_register_tiled(FLCtx *, const void * base, size_t bytes);
+/* forgets every declared range inside [base, base + bytes): call it before the memory is freed or holds ggml bytes */
+int fl_unregister_tiled(FLCtx *, const void * base, size_t bytes);
 /* RMSNorm (ggml semantics, eps) of n rows of D floats (D = 1024, 2048, 4096 or 7168), w may be NULL (ones) */
 int fl_rmsnorm_dev(FLCtx *, const float * x, const float * w, float * y, int n, int D, float eps);
 /* synthetic data on the device: IQ2_XXS matrices (qs uniform bytes, d = fp16(|N(0, sigma^2)|)) and normal floats */

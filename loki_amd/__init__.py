@@ -128,7 +128,7 @@ ABI_SYMBOLS = [
     "fl_gpu_ms", "fl_ffn_begin", "fl_set_experts", "fl_set_routing", "fl_set_keep", "fl_set_shared_formats", "fl_set_layer_formats", "fl_kq_matvec_dev",
     "fl_gguf_open", "fl_gguf_close", "fl_gguf_n_tensors", "fl_gguf_tensor_name", "fl_gguf_tensor", "fl_gguf_tensor_at",
     "fl_gguf_get_int", "fl_gguf_get_float", "fl_gguf_get_str", "fl_gguf_read", "fl_gguf_load_moe_layer", "fl_gguf_free_layer", "fl_moe_layer", "fl_moe_layer_normed", "fl_moe_layer_noalloc", "fl_route_dev", "fl_dispatch_dev", "fl_quant_q8k_dev",
-    "fl_pack_iq2xxs", "fl_unpack_iq2xxs", "fl_rmsnorm_dev", "fl_synth_iq2xxs", "fl_synth_normal", "fl_probe_exp",
+    "fl_pack_iq2xxs", "fl_unpack_iq2xxs", "fl_register_tiled", "fl_unregister_tiled", "fl_rmsnorm_dev", "fl_synth_iq2xxs", "fl_synth_normal", "fl_probe_exp",
     "fl_debug", "fl_set_debug", "fl_set_fused", "fl_set_decode1", "fl_set_prefill_mfma", "fl_stream", "fl_set_stream", "fl_d2h", "fl_set_profile", "fl_stage_ms", "fl_sync", "fl_last_error", "fl_free",
 ]
 
@@ -184,6 +184,8 @@ def lib():
             "fl_dispatch_dev": (I, [P_, P_, I, I, I, P_, P_, P_, P_, P_, P_]),
             "fl_quant_q8k_dev": (I, [P_, P_, I, I, P_, P_]),
             "fl_pack_iq2xxs": (I, [P_, P_, S, P_, S, I, I, I]),
+            "fl_register_tiled": (I, [P_, P_, S]),
+            "fl_unregister_tiled": (I, [P_, P_, S]),
             "fl_unpack_iq2xxs": (I, [P_, P_, S, P_, S, I, I, I]),
             "fl_rmsnorm_dev": (I, [P_, P_, P_, P_, I, I, F]),
             "fl_synth_iq2xxs": (I, [P_, P_, S, I, I, I, I, U64, U64, F]),
@@ -392,6 +394,13 @@ class Context:
             dst = t.empty(nmat * mb, dtype=t.uint8, device=src.device)
         self.check(lib().fl_pack_iq2xxs(self.ctx, _ptr(src), src_stride or mb, _ptr(dst), mb, rows, cols, nmat))
         return dst
+
+    def register_tiled(self, t):
+        """Declare a device tensor as tiled IQ2_XXS matrices: fl_moe / fl_wide_moe / fl_ffn_begin read it in place."""
+        self.check(lib().fl_register_tiled(self.ctx, _ptr(t), t.numel() * t.element_size()))
+
+    def unregister_tiled(self, t):
+        self.check(lib().fl_unregister_tiled(self.ctx, _ptr(t), t.numel() * t.element_size()))
 
     def unpack(self, src, rows, cols, nmat, dst=None):
         t = self.torch

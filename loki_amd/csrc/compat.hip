@@ -6,12 +6,51 @@
 // residual ffn_inp; src/fused_layer.cu:498-525) from the host. Everything else keeps the reference's names, parameters,
 // ownership (context-owned pinned mirrors, overwritten by the next call) and synchronisation (fl_fetch, fl_moe, fl_skip,
 // fl_wide_finish and fl_wide_skip wait; fl_ffn_begin and fl_wide_moe only enqueue). Expert arenas arrive in ggml's
-// layout and are repacked into the tiled layout on the device before the mat-vecs.
+// layout and are repacked into the tiled layout on the device before the mat-vecs -- on every call, since the reference's
+// engine refills its arenas in place (src/server_core_fused.cpp:295-305) -- unless they lie in a range declared tiled
+// (fl_register_tiled, or a layer loaded with FL_LAYOUT_TILED), which is read as it is.
 // Summation orders follow each reference kernel: moe_combine (src/fused_layer.cu:366-372) adds slots in ascending slot
 // order with the weights of equal slots merged; base_rows/wide_finish (:351-360) add fi + shared, then the k outputs.
 #include "fl_ctx.h"
 
+#include <mutex>
+
 using namespace lk;
+
+// ---------------------------------------------------------------- declared tiled ranges
+namespace {
+std::mutex g_tiled_mu;
+std::vector<std::pair<uintptr_t, uintptr_t>> g_tiled;   // [begin, end)
+}
+void tiled_add(const void * p, size_t bytes) {
+    std::lock_guard<std::mutex> lk(g_tiled_mu);
+    g_tiled.emplace_back((uintptr_t) p, (uintptr_t) p + bytes);
+}
+void tiled_remove_within(const void * p, size_t bytes) {
+    const uintptr_t b = (uintptr_t) p, e = b + bytes;
+    std::lock_guard<std::mutex> lk(g_tiled_mu);
+    std::vector<std::pair<uintptr_t, uintptr_t>> keep;
+    for (const auto & r : g_tiled) { if (r.first < b || r.second > e) { keep.push_back(r); } }
+    g_tiled.swap(keep);
+}
+bool tiled_holds(const void * p, size_t bytes) {
+    const uintptr_t b = (uintptr_t) p, e = b + bytes;
+    std::lock_guard<std::mutex> lk(g_tiled_mu);
+    for (const auto & r : g_tiled) { if (r.first <= b && e <= r.second) { return true; } }
+    return false;
+}
+extern "C" int fl_register_tiled(FLCtx * c, const void * base, size_t bytes) {
+    if (!c) { return FL_EINVAL; }
+    if (!base || bytes == 0) { return fail(c, FL_EINVAL, "fl_register_tiled: empty range"); }
+    if (!covers(base, bytes)) { return fail(c, FL_EINVAL, "fl_register_tiled: the range runs past its allocation"); }
+    tiled_add(base, bytes);
+    return FL_OK;
+}
+extern "C" int fl_unregister_tiled(FLCtx * c, const void * base, size_t bytes) {
+    if (!c) { return FL_EINVAL; }
+    tiled_remove_within(base, bytes);
+    return FL_OK;
+}
 
 namespace {
 
@@ -96,6 +135,7 @@ struct Compat {
     int N = 0;
     DBuf<float> ncur, fi, logits, probs, wts, h, o, sh_o, wr32; DBuf<int8_t> xq, hq; DBuf<float> xd, hd; DBuf<int> sel;
     DBuf<uint8_t> sh_t; const void * sh_key[3] = { nullptr, nullptr, nullptr }; int sh_fkey[3] = { -1, -1, -1 };
+    bool sh_tkey[3] = { false, false, false };   // whether each was a declared-tiled matrix when sh_t was filled
     int shf[3] = { FL_IQ2, FL_IQ2, FL_IQ2 };   // shared gate / up / down formats (fl_set_shared_formats)
     DBuf<float> sg, su;                         // K-quant shared gate / up outputs
     // fl_moe
@@ -106,6 +146,10 @@ struct Compat {
     DBuf<float> ncur_all, base_all, out_all, xd_all; DBuf<int8_t> xq_all;
     DBuf<int> w_act, w_off, w_perm, w_nact, w_row, w_k; DBuf<float> w_wk;
     hipEvent_t wev[2] = { nullptr, nullptr };
+    // fl_wide_moe's slot tables for each parity in pinned host memory (act | off | perm | row | k | nact, then wk): the
+    // call only enqueues, so a parity's tables stay untouched until fl_wide_wait(par) (the engine's own discipline)
+    int * wt_i[2] = { nullptr, nullptr }; float * wt_w[2] = { nullptr, nullptr }; size_t wt_cap[2] = { 0, 0 };
+    hipEvent_t wt_ev[2] = { nullptr, nullptr }; bool wt_rec[2] = { false, false };   // after each parity's table copies
     // pinned host mirrors
     int * h_sel = nullptr; float * h_wts = nullptr, * h_ncur = nullptr, * h_fi = nullptr, * h_h = nullptr, * h_moe = nullptr;
     float * h_wh = nullptr, * h_wmoe = nullptr;
@@ -130,6 +174,10 @@ void compat_free(FLCtx * c) {
         if (p) { (void) hipHostFree(p); }
     }
     for (hipEvent_t e : s->wev) { if (e) { (void) hipEventDestroy(e); } }
+    for (int p = 0; p < 2; ++p) {
+        if (s->wt_i[p]) { (void) hipHostFree(s->wt_i[p]); } if (s->wt_w[p]) { (void) hipHostFree(s->wt_w[p]); }
+        if (s->wt_ev[p]) { (void) hipEventDestroy(s->wt_ev[p]); }
+    }
     s->ncur.release(); s->fi.release(); s->logits.release(); s->probs.release(); s->wts.release(); s->h.release(); s->o.release(); s->sh_o.release(); s->wr32.release();
     s->xq.release(); s->hq.release(); s->xd.release(); s->hd.release(); s->sel.release(); s->sh_t.release(); s->sg.release(); s->su.release();
     s->ag.release(); s->au.release(); s->ad.release(); s->ids.release(); s->counts.release(); s->offsets.release(); s->perm.release(); s->inv.release();
@@ -167,11 +215,17 @@ static void kq_single(FLCtx * c, int fmt, const void * w, const int8_t * q, cons
 // K-quant matrices (the reference's Q5_K / Q5_K / Q6_K) read in place
 static void shared_expert(FLCtx * c, Compat * s, const int8_t * xq, const float * xd, int N, float * out) {
     const size_t mg = mat_bytes(H_, E_);
+    // IQ2_XXS shared matrices: a declared-tiled one as it is, else its tiled copy in sh_t
+    const uint8_t * tm[3];
+    for (int i = 0; i < 3; ++i) {
+        const size_t b = i < 2 ? mg : mat_bytes(E_, H_);
+        tm[i] = tiled_holds(s->sh_key[i], b) ? (const uint8_t *) s->sh_key[i] : s->sh_t.p + i * mg;
+    }
     FALLOC(s->h, (size_t) N * H_); FALLOC(s->hq, (size_t) N * H_); FALLOC(s->hd, (size_t) N * (H_ / QK));
     CK(ensure_expert_scratch(c, (size_t) N, E_, H_) == FL_OK ? hipSuccess : hipErrorOutOfMemory);
     ExpertArgs a = expert_args(c, N, 0, 1);
     if (s->shf[0] == FL_IQ2) {
-        a.sh[0] = s->sh_t.p; a.sh[1] = s->sh_t.p + mg; a.aq = xq; a.ad = xd; a.K = E_; a.R = H_; a.nmat = 2;
+        a.sh[0] = tm[0]; a.sh[1] = tm[1]; a.aq = xq; a.ad = xd; a.K = E_; a.R = H_; a.nmat = 2;
         a.act = zero_int(c); a.nact = zero_int(c); a.offsets = zero_int(c); a.perm = zero_int(c); a.topk = 1;
         a.h = s->h.p; a.hq = s->hq.p; a.hd = s->hd.p;
         expert_counters(c, a, 0);
@@ -191,7 +245,7 @@ static void shared_expert(FLCtx * c, Compat * s, const int8_t * xq, const float 
     }
     if (s->shf[2] == FL_IQ2) {
         ExpertArgs d = a;
-        d.sh[0] = s->sh_t.p + 2 * mg; d.sh[1] = nullptr; d.aq = s->hq.p; d.ad = s->hd.p; d.K = H_; d.R = E_; d.nmat = 1;
+        d.sh[0] = tm[2]; d.sh[1] = nullptr; d.aq = s->hq.p; d.ad = s->hd.p; d.K = H_; d.R = E_; d.nmat = 1;
         d.act = zero_int(c); d.nact = zero_int(c); d.offsets = zero_int(c); d.perm = zero_int(c); d.topk = 1;
         d.h = nullptr; d.hq = nullptr; d.hd = nullptr; d.o = out; d.y = nullptr;
         expert_counters(c, d, 1);
@@ -201,16 +255,19 @@ static void shared_expert(FLCtx * c, Compat * s, const int8_t * xq, const float 
     }
 }
 
-// routed experts of an arena (tiled copy ag/au/ad) for the pairs described by offsets/perm/act/nact -> o [P][E]
-// down_fmt: FL_IQ2 (tiled copy ad) or FL_Q2K / FL_Q3K read in place from down (expert stride E x H/256 blocks);
+// an arena's matrices in the tiled layout: declared-tiled matrices as they are, the others repacked into ag/au/ad
+struct Arena { const uint8_t * g, * u, * d; };
+
+// routed experts of an arena (tiled gate/up/down in ar) for the pairs described by offsets/perm/act/nact -> o [P][E]
+// down_fmt: FL_IQ2 (tiled ar.d) or FL_Q2K / FL_Q3K read in place from down (expert stride E x H/256 blocks);
 // max_slots bounds the pairs of one expert
-static void routed_experts(FLCtx * c, Compat * s, const int8_t * xq, const float * xd, int n, int P, int KE, int nexp,
+static void routed_experts(FLCtx * c, Compat * s, const Arena & ar, const int8_t * xq, const float * xd, int n, int P, int KE, int nexp,
                            const int * act, const int * nact, const int * offsets, const int * perm, float * o,
                            int down_fmt, const void * down, int max_slots) {
     FALLOC(s->h, (size_t) P * H_); FALLOC(s->hq, (size_t) P * H_); FALLOC(s->hd, (size_t) P * (H_ / QK));
     CK(ensure_expert_scratch(c, (size_t) P + n, E_, H_) == FL_OK ? hipSuccess : hipErrorOutOfMemory);
     ExpertArgs a = expert_args(c, n, P, 0);
-    a.w[0] = s->ag.p; a.w[1] = s->au.p; a.estride = mat_bytes(H_, E_); a.aq = xq; a.ad = xd; a.K = E_; a.R = H_; a.nmat = 2;
+    a.w[0] = ar.g; a.w[1] = ar.u; a.estride = mat_bytes(H_, E_); a.aq = xq; a.ad = xd; a.K = E_; a.R = H_; a.nmat = 2;
     a.act = act; a.nact = nact; a.offsets = offsets; a.perm = perm; a.topk = KE;
     a.h = s->h.p; a.hq = s->hq.p; a.hd = s->hd.p;
     expert_counters(c, a, 0);
@@ -223,22 +280,33 @@ static void routed_experts(FLCtx * c, Compat * s, const int8_t * xq, const float
         return;
     }
     ExpertArgs d = a;
-    d.w[0] = s->ad.p; d.w[1] = nullptr; d.estride = mat_bytes(E_, H_); d.aq = s->hq.p; d.ad = s->hd.p; d.K = H_; d.R = E_; d.nmat = 1;
+    d.w[0] = ar.d; d.w[1] = nullptr; d.estride = mat_bytes(E_, H_); d.aq = s->hq.p; d.ad = s->hd.p; d.K = H_; d.R = E_; d.nmat = 1;
     d.h = nullptr; d.hq = nullptr; d.hd = nullptr; d.o = o; d.y = nullptr;
     expert_counters(c, d, 1);
     FCK(launch_experts_down(d, c->ncu, c->st));
 }
 
-// IQ2_XXS arena matrices -> tiled copies (a K-quant down stays where it is)
-static void pack_arena(FLCtx * c, Compat * s, const void * gate, const void * up, const void * down, int nexp, int down_fmt) {
+// IQ2_XXS arena matrices in the tiled layout: declared-tiled ones as they are, the others repacked into the context's
+// copies (a K-quant down stays where it is)
+static Arena pack_arena(FLCtx * c, Compat * s, const void * gate, const void * up, const void * down, int nexp, int down_fmt) {
     const size_t mg = mat_bytes(H_, E_), md = mat_bytes(E_, H_);
-    FALLOC(s->ag, (size_t) nexp * mg); FALLOC(s->au, (size_t) nexp * mg);
-    FCK(launch_pack_tiled((const uint8_t *) gate, mg, s->ag.p, mg, H_, E_, nexp, c->st));
-    FCK(launch_pack_tiled((const uint8_t *) up, mg, s->au.p, mg, H_, E_, nexp, c->st));
-    if (down_fmt == FL_IQ2) {
+    Arena ar{ (const uint8_t *) gate, (const uint8_t *) up, (const uint8_t *) down };
+    if (!tiled_holds(gate, (size_t) nexp * mg)) {
+        FALLOC(s->ag, (size_t) nexp * mg);
+        FCK(launch_pack_tiled((const uint8_t *) gate, mg, s->ag.p, mg, H_, E_, nexp, c->st));
+        ar.g = s->ag.p;
+    }
+    if (!tiled_holds(up, (size_t) nexp * mg)) {
+        FALLOC(s->au, (size_t) nexp * mg);
+        FCK(launch_pack_tiled((const uint8_t *) up, mg, s->au.p, mg, H_, E_, nexp, c->st));
+        ar.u = s->au.p;
+    }
+    if (down_fmt == FL_IQ2 && !tiled_holds(down, (size_t) nexp * md)) {
         FALLOC(s->ad, (size_t) nexp * md);
         FCK(launch_pack_tiled((const uint8_t *) down, md, s->ad.p, md, E_, H_, nexp, c->st));
+        ar.d = s->ad.p;
     }
+    return ar;
 }
 
 // routed down formats: the reference's Q2_K / Q3_K (src/fused_layer.cu:608) and IQ2_XXS (the all-IQ2_XXS configs).
@@ -281,14 +349,17 @@ extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur,
     TRY(c, hipMemcpyAsync(s->fi.p, ffn_inp, (size_t) N * E_ * 4, hipMemcpyHostToDevice, st));
     const size_t mg = mat_bytes(H_, E_);
     const void * shm[3] = { W->sh_gate, W->sh_up, W->sh_down };
+    bool sht[3];
+    for (int i = 0; i < 3; ++i) { sht[i] = s->shf[i] == FL_IQ2 && tiled_holds(shm[i], i < 2 ? mg : mat_bytes(E_, H_)); }
     if (s->sh_key[0] != shm[0] || s->sh_key[1] != shm[1] || s->sh_key[2] != shm[2] ||
-        s->sh_fkey[0] != s->shf[0] || s->sh_fkey[1] != s->shf[1] || s->sh_fkey[2] != s->shf[2]) {
+        s->sh_fkey[0] != s->shf[0] || s->sh_fkey[1] != s->shf[1] || s->sh_fkey[2] != s->shf[2] ||
+        s->sh_tkey[0] != sht[0] || s->sh_tkey[1] != sht[1] || s->sh_tkey[2] != sht[2]) {
         ALLOC(c, s->sh_t, 3 * mg);
-        for (int i = 0; i < 3; ++i) {   // IQ2_XXS matrices get a tiled copy; K-quant ones are read in place
-            if (s->shf[i] == FL_IQ2) {
+        for (int i = 0; i < 3; ++i) {   // IQ2_XXS matrices get a tiled copy unless declared tiled; K-quant ones are read in place
+            if (s->shf[i] == FL_IQ2 && !sht[i]) {
                 TRY(c, launch_pack_tiled((const uint8_t *) shm[i], mg, s->sh_t.p + i * mg, mg, i < 2 ? H_ : E_, i < 2 ? E_ : H_, 1, st));
             }
-            s->sh_key[i] = shm[i]; s->sh_fkey[i] = s->shf[i];
+            s->sh_key[i] = shm[i]; s->sh_fkey[i] = s->shf[i]; s->sh_tkey[i] = sht[i];
         }
     }
     // the F16 router (W->gate_f16, fl.cu:317-319) is widened exactly to fp32 first; the logits then follow the same
@@ -349,9 +420,9 @@ extern "C" void fl_moe(FLCtx * c, const void * gate, const void * up, const void
     FALLOC(s->act, nexp); FALLOC(s->nact, 1); FALLOC(s->o, (size_t) P * E_); FALLOC(s->hout, (size_t) NB * E_); FALLOC(s->moe, (size_t) NB * E_);
     CK(hipMemcpyAsync(s->ids.p, ids, (size_t) P * 4, hipMemcpyHostToDevice, st));
     CK(hipMemcpyAsync(s->w.p, w, (size_t) P * 4, hipMemcpyHostToDevice, st));
-    pack_arena(c, s, gate, up, down, nexp, down_fmt);
+    const Arena ar = pack_arena(c, s, gate, up, down, nexp, down_fmt);
     CK(launch_dispatch(s->ids.p, P, nexp, s->counts.p, s->offsets.p, s->perm.p, s->inv.p, s->act.p, s->nact.p, st));
-    routed_experts(c, s, s->xq.p, s->xd.p, n, P, KE, nexp, s->act.p, s->nact.p, s->offsets.p, s->perm.p, s->o.p, down_fmt, down, max_slots);
+    routed_experts(c, s, ar, s->xq.p, s->xd.p, n, P, KE, nexp, s->act.p, s->nact.p, s->offsets.p, s->perm.p, s->o.p, down_fmt, down, max_slots);
     k_combine_slots<<<nblk((int64_t) n * E_), 256, 0, st>>>(s->o.p, s->inv.p, s->ids.p, s->w.p, n, KE, s->sh_o.p, s->fi.p, s->hout.p, s->moe.p);
     CK(hipGetLastError());
     CK(hipMemcpyAsync(s->h_h, s->hout.p, (size_t) n * E_ * 4, hipMemcpyDeviceToHost, st));
@@ -414,7 +485,6 @@ extern "C" void fl_wide_moe(FLCtx * c, const void * gate, const void * up, const
                             const int * rows, const int * kidx, const float * wk, int nslots, int KE, int par) {
     need_down_fmt("fl_wide_moe", down_fmt, down);
     Compat * s = cs(c);
-    (void) par;
     if (KE != s->wke || nexp <= 0 || nexp > NEXP_ || nslots < 0) { std::fprintf(stderr, "[fused] fl_wide_moe: KE %d (init %d), nexp %d, nslots %d\n", KE, s->wke, nexp, nslots); std::exit(7); }
     // the slot tables as (expert, row, k, w) pairs, grouped by expert in slot order (a stable counting sort)
     std::vector<int> cnt(nexp + 1, 0);
@@ -435,33 +505,53 @@ extern "C" void fl_wide_moe(FLCtx * c, const void * gate, const void * up, const
     }
     int max_slots = 1;
     for (int e = 0; e < nexp; ++e) { max_slots = std::max(max_slots, cnt[e + 1] - cnt[e]); }
-    std::vector<int> off(cnt), fillp(cnt.begin(), cnt.end() - 1), perm(P), prow(P), pk(P), act; std::vector<float> pw(P);
+    // the tables go to this parity's pinned buffers: [act nexp | off nexp + 1 | perm P | row P | k P | nact 1], wk P.
+    // Their previous copies were queued two batches ago (the engine alternates parities and waits for each before
+    // reusing it); the event recorded after those copies makes sure of it whatever the caller does.
+    const int pb = par & 1;
+    if (!s->wt_ev[pb]) { CK(hipEventCreateWithFlags(&s->wt_ev[pb], hipEventDisableTiming)); }
+    if (s->wt_rec[pb]) { CK(hipEventSynchronize(s->wt_ev[pb])); }
+    const size_t ni = (size_t) nexp + (nexp + 1) + 3 * (size_t) P + 1;
+    if (ni > s->wt_cap[pb] || (size_t) P > s->wt_cap[pb]) {
+        if (s->wt_i[pb]) { (void) hipHostFree(s->wt_i[pb]); } if (s->wt_w[pb]) { (void) hipHostFree(s->wt_w[pb]); }
+        const size_t cap = std::max(ni, (size_t) 4096);
+        s->wt_i[pb] = pinned<int>(cap); s->wt_w[pb] = pinned<float>(cap);
+        if (!s->wt_i[pb] || !s->wt_w[pb]) { fatal("hipHostMalloc (wide-pass slot tables)", hipErrorOutOfMemory, __FILE__, __LINE__); }
+        s->wt_cap[pb] = cap;
+    }
+    int * h_act = s->wt_i[pb], * h_off = h_act + nexp, * h_perm = h_off + nexp + 1, * h_row = h_perm + P, * h_k = h_row + P, * h_nact = h_k + P;
+    float * h_wk = s->wt_w[pb];
+    std::vector<int> fillp(cnt.begin(), cnt.end() - 1);
+    for (int e = 0; e <= nexp; ++e) { h_off[e] = cnt[e]; }
     for (int sl = 0; sl < nslots; ++sl) {
         for (int j = 0; j < NB; ++j) {
             const int r = rows[sl * NB + j];
             if (r < 0) { continue; }
             const int pos = fillp[midx[sl]]++;
-            perm[pos] = r * KE + kidx[sl * NB + j]; prow[pos] = r; pk[pos] = kidx[sl * NB + j]; pw[pos] = wk[sl * NB + j];
+            h_perm[pos] = r * KE + kidx[sl * NB + j]; h_row[pos] = r; h_k[pos] = kidx[sl * NB + j]; h_wk[pos] = wk[sl * NB + j];
         }
     }
-    for (int e = 0; e < nexp; ++e) { if (off[e + 1] > off[e]) { act.push_back(e); } }
-    const int na = (int) act.size();
+    int na = 0;
+    for (int e = 0; e < nexp; ++e) { if (cnt[e + 1] > cnt[e]) { h_act[na++] = e; } }
+    *h_nact = na;
     hipStream_t st = c->st;
     FALLOC(s->w_act, nexp); FALLOC(s->w_off, nexp + 1); FALLOC(s->w_perm, P); FALLOC(s->w_nact, 1); FALLOC(s->w_row, P); FALLOC(s->w_k, P); FALLOC(s->w_wk, P);
     FALLOC(s->o, (size_t) P * E_);
-    CK(hipMemcpyAsync(s->w_act.p, act.data(), (size_t) na * 4, hipMemcpyHostToDevice, st));
-    CK(hipMemcpyAsync(s->w_off.p, off.data(), (size_t) (nexp + 1) * 4, hipMemcpyHostToDevice, st));
-    CK(hipMemcpyAsync(s->w_perm.p, perm.data(), (size_t) P * 4, hipMemcpyHostToDevice, st));
-    CK(hipMemcpyAsync(s->w_nact.p, &na, 4, hipMemcpyHostToDevice, st));
-    CK(hipMemcpyAsync(s->w_row.p, prow.data(), (size_t) P * 4, hipMemcpyHostToDevice, st));
-    CK(hipMemcpyAsync(s->w_k.p, pk.data(), (size_t) P * 4, hipMemcpyHostToDevice, st));
-    CK(hipMemcpyAsync(s->w_wk.p, pw.data(), (size_t) P * 4, hipMemcpyHostToDevice, st));
-    pack_arena(c, s, gate, up, down, nexp, down_fmt);
-    routed_experts(c, s, s->xq_all.p, s->xd_all.p, s->wmax, P, KE, nexp, s->w_act.p, s->w_nact.p, s->w_off.p, s->w_perm.p, s->o.p,
+    CK(hipMemcpyAsync(s->w_act.p, h_act, (size_t) na * 4, hipMemcpyHostToDevice, st));
+    CK(hipMemcpyAsync(s->w_off.p, h_off, (size_t) (nexp + 1) * 4, hipMemcpyHostToDevice, st));
+    CK(hipMemcpyAsync(s->w_perm.p, h_perm, (size_t) P * 4, hipMemcpyHostToDevice, st));
+    CK(hipMemcpyAsync(s->w_nact.p, h_nact, 4, hipMemcpyHostToDevice, st));
+    CK(hipMemcpyAsync(s->w_row.p, h_row, (size_t) P * 4, hipMemcpyHostToDevice, st));
+    CK(hipMemcpyAsync(s->w_k.p, h_k, (size_t) P * 4, hipMemcpyHostToDevice, st));
+    CK(hipMemcpyAsync(s->w_wk.p, h_wk, (size_t) P * 4, hipMemcpyHostToDevice, st));
+    CK(hipEventRecord(s->wt_ev[pb], st)); s->wt_rec[pb] = true;
+    const Arena ar = pack_arena(c, s, gate, up, down, nexp, down_fmt);
+    routed_experts(c, s, ar, s->xq_all.p, s->xd_all.p, s->wmax, P, KE, nexp, s->w_act.p, s->w_nact.p, s->w_off.p, s->w_perm.p, s->o.p,
                    down_fmt, down, max_slots);
     k_wide_scatter<<<nblk((int64_t) P * E_), 256, 0, st>>>(s->o.p, s->w_row.p, s->w_k.p, s->w_wk.p, P, KE, s->out_all.p);
     CK(hipGetLastError());
-    CK(hipStreamSynchronize(st));   // host tables above are stack vectors: they must outlive the queued copies
+    // no wait: the reference's call only enqueues too (src/fused_layer.cu:528-555); fl_wide_mark / fl_wide_wait order
+    // the engine's reuse of its staging and of these tables
 }
 
 extern "C" void fl_wide_mark(FLCtx * c, int par) { Compat * s = cs(c); if (s->wev[par & 1]) { CK(hipEventRecord(s->wev[par & 1], c->st)); } }

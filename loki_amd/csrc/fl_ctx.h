@@ -99,6 +99,11 @@ static std::vector<hipEvent_t> * prof_begin(FLCtx * c) {
 static void prof_mark(FLCtx * c, std::vector<hipEvent_t> * ev, int i) { if (ev) { (void) hipEventRecord((*ev)[i], c->st); } }
 
 void compat_free(FLCtx * c);   // compat.hip
+// device ranges declared to hold IQ2_XXS matrices in the tiled layout (compat.hip; process-wide): fl_register_tiled,
+// and the tiled layers of fl_gguf_load_moe_layer
+void tiled_add(const void * p, size_t bytes);
+void tiled_remove_within(const void * p, size_t bytes);
+bool tiled_holds(const void * p, size_t bytes);
 int ensure_expert_scratch(FLCtx * c, size_t rows, int E, int H);   // fused_layer.hip
 lk::ExpertArgs expert_args(FLCtx * c, int n, int P, int shared);
 // counter sets of the two persistent kernels inside FLCtx::cnt

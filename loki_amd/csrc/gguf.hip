@@ -383,11 +383,14 @@ extern "C" int fl_gguf_load_moe_layer(FLCtx * c, const FLGguf * g, int layer, in
     out->expert_stride[0] = te[0].row_bytes * (uint64_t) H; out->expert_stride[1] = te[1].row_bytes * (uint64_t) H;
     out->expert_stride[2] = te[2].row_bytes * (uint64_t) E;
     out->mem = mem; out->bytes = tot;
+    if (layout == FL_LAYOUT_TILED) {   // the tiled IQ2_XXS matrices are read in place by fl_moe / fl_wide_moe / fl_ffn_begin
+        for (int k = 0; k < 6; ++k) { if (fm[k] == FL_IQ2) { tiled_add(mem + off[3 + k], mats[k]->nbytes); } }
+    }
     return FL_OK;
 }
 
 extern "C" void fl_gguf_free_layer(FLGgufLayer * l) {
     if (!l) { return; }
-    if (l->mem) { (void) hipDeviceSynchronize(); (void) hipFree(l->mem); }
+    if (l->mem) { tiled_remove_within(l->mem, l->bytes); (void) hipDeviceSynchronize(); (void) hipFree(l->mem); }
     std::memset(l, 0, sizeof *l);
 }

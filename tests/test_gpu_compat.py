@@ -150,9 +150,12 @@ def test_f16_router(ctx, small_layer):
     assert np.array_equal(res[0][0].reshape(n, KE), so) and np.array_equal(res[0][1].reshape(n, KE).view(np.uint32), wo.view(np.uint32))
 
 
-def test_wide_pass(ctx, small_layer):
+@pytest.mark.parametrize("waits", [True, False])
+def test_wide_pass(ctx, small_layer, waits):
     """fl_wide_init -> fl_ffn_begin(wrow) per group -> per arena batch fl_wide_moe (slots of <= 8 (row, k) pairs in the
-    engine's byexp order) -> fl_wide_finish; h = (ffn_inp + shared) + sum_k w_k o_k (src/fused_layer.cu:351-360)."""
+    engine's byexp order) -> fl_wide_finish; h = (ffn_inp + shared) + sum_k w_k o_k (src/fused_layer.cu:351-360).
+    fl_wide_moe only enqueues: with waits=False the batches are issued back to back without fl_wide_wait, and the
+    library's own per-parity guard keeps each parity's slot tables intact until their copies ran."""
     from loki_amd import FLOut, lib
     (W, b, gate, up, down, sh), dev = small_layer
     n, EB = 40, 5
@@ -176,7 +179,8 @@ def test_wide_pass(ctx, small_layer):
     for bi, b0 in enumerate(range(0, len(used), EB)):
         batch = used[b0:b0 + EB]
         par = bi & 1
-        lib().fl_wide_wait(ctx.ctx, par)
+        if waits:
+            lib().fl_wide_wait(ctx.ctx, par)
         midx, rows, kidx, wk = [], [], [], []
         for u, e in enumerate(batch):
             lst = byexp[e]
@@ -209,6 +213,45 @@ def test_wide_pass(ctx, small_layer):
     lib().fl_wide_skip(ctx.ctx, cptr(mo), n, ctypes.byref(out))
     hs = np.ctypeslib.as_array(out.h, shape=(n * E,)).reshape(n, E).copy()
     assert np.array_equal(hs.view(np.uint32), (base + mo).astype(np.float32).view(np.uint32))
+
+
+def test_narrow_pass_declared_tiled(ctx, small_layer):
+    """A resident arena of every expert (ids = expert ids) in the tiled layout, declared with fl_register_tiled, and a
+    declared-tiled shared expert: fl_ffn_begin / fl_moe read them in place (no repack) and give h and moe bit for bit
+    as the same arena and shared expert in ggml's layout; after fl_unregister_tiled the ggml arena still runs."""
+    import torch
+    from loki_amd import FLOut, lib
+    (W, b, gate, up, down, sh), dev = small_layer
+    ctx.set_routing(8, 4, 8, 2.5)
+    n = 2
+    x = gen.uniform(9, 3, (n, E), 2.0); fi = gen.uniform(9, 4, (n, E), 1.0)
+    tiled = dict(gate=ctx.pack(dev["gate"], H, E, 16), up=ctx.pack(dev["up"], H, E, 16), down=ctx.pack(dev["down"], E, H, 16),
+                 sh=[ctx.pack(dev["sh"][0], H, E, 1), ctx.pack(dev["sh"][1], H, E, 1), ctx.pack(dev["sh"][2], E, H, 1)])
+    torch.cuda.synchronize()
+
+    def run(g, u, d, shm):
+        flw = _flw(dict(dev, sh=shm))
+        ctx.check(lib().fl_ffn_begin(ctx.ctx, ctypes.byref(flw), n, cptr(x), cptr(fi), -1))
+        out = FLOut()
+        lib().fl_fetch(ctx.ctx, n, 1, ctypes.byref(out))
+        sel = np.ctypeslib.as_array(out.sel, shape=(n * KE,)).copy().astype(np.int32)
+        wts = np.ctypeslib.as_array(out.wts, shape=(n * KE,)).copy()
+        lib().fl_moe(ctx.ctx, g.data_ptr(), u.data_ptr(), d.data_ptr(), 16, 4, cptr(sel), cptr(f32(wts)), KE, n, ctypes.byref(out))
+        return (np.ctypeslib.as_array(out.h, shape=(n * E,)).copy(), np.ctypeslib.as_array(out.moe, shape=(n * E,)).copy())
+
+    want = run(dev["gate"], dev["up"], dev["down"], dev["sh"])
+    for t in (tiled["gate"], tiled["up"], tiled["down"], *tiled["sh"]):
+        ctx.register_tiled(t)
+    try:
+        got = run(tiled["gate"], tiled["up"], tiled["down"], tiled["sh"])
+    finally:
+        for t in (tiled["gate"], tiled["up"], tiled["down"], *tiled["sh"]):
+            ctx.unregister_tiled(t)
+    for a_, b_ in zip(got, want):
+        assert np.array_equal(a_.view(np.uint32), b_.view(np.uint32))
+    again = run(dev["gate"], dev["up"], dev["down"], dev["sh"])
+    for a_, b_ in zip(again, want):
+        assert np.array_equal(a_.view(np.uint32), b_.view(np.uint32))
 
 
 def test_narrow_pass_keep2_with_pad_rows(ctx, small_layer):
