@@ -459,6 +459,9 @@ def bench(args, ctx, torch):
     if args.only_kquant:
         print(json.dumps({"kquant": run_kquant(ctx, torch), "real_formats": run_realfmt(ctx, torch)}), flush=True)
         return
+    if args.only_dropin:
+        print(json.dumps({"dropin_decode1": run_dropin(ctx, torch)}), flush=True)
+        return
     thr = cpu_threads()
     cpu_per = {}
 
@@ -554,6 +557,8 @@ def main():
     ap.add_argument("--stack-steps", type=int, default=10)
     ap.add_argument("--only-kquant", action="store_true",
                     help="run only the K-quant mat-vec leg (the reference's real-shard formats) and print its JSON")
+    ap.add_argument("--only-dropin", action="store_true",
+                    help="run only the reference-named path (fl_ffn_begin -> fl_fetch -> fl_moe) and print its JSON")
     ap.add_argument("--fused", type=int, default=None, choices=(0, 1, 2),
                     help="decode path: 2 regular single launch (library default), 1 cooperative single launch, 0 per pass")
     ap.add_argument("--copy-probe", action="store_true",

@@ -66,25 +66,35 @@ template <class T> T * pinned(size_t n) {
 }
 
 // ---------------------------------------------------------------- small kernels with the reference's orders
-__global__ void k_combine_slots(const float * __restrict__ o, const int * __restrict__ inv, const int * __restrict__ ids,
-                                const float * __restrict__ w, int n, int KE, const float * __restrict__ sh, const float * __restrict__ fi,
-                                float * __restrict__ h, float * __restrict__ moe) {
+// block (x, b): elements 256 x .. of row b. The row's distinct slot ids in ascending order, each with its weights
+// summed in k order and its first k, are formed once in LDS; every element then adds them in that order.
+__global__ void __launch_bounds__(256) k_combine_slots(const float * __restrict__ o, const int * __restrict__ inv, const int * __restrict__ ids,
+                                                      const float * __restrict__ w, int n, int KE, const float * __restrict__ sh, const float * __restrict__ fi,
+                                                      float * __restrict__ h, float * __restrict__ moe) {
 #pragma clang fp contract(off)
-    const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
-    if (i >= (int64_t) n * E_) { return; }
-    const int b = (int) (i / E_), e = (int) (i % E_);
-    const int * idr = ids + b * KE; const float * wr = w + b * KE;
-    float v = 0.f; int prev = -1;
-    for (;;) {   // distinct slot ids of the row, ascending
-        int m = 0x7fffffff;
-        for (int k = 0; k < KE; ++k) { if (idr[k] > prev && idr[k] < m) { m = idr[k]; } }
-        if (m == 0x7fffffff) { break; }
-        float wt = 0.f; int kf = -1;
-        for (int k = 0; k < KE; ++k) { if (idr[k] == m) { wt += wr[k]; if (kf < 0) { kf = k; } } }
-        prev = m;
-        if (wt == 0.f) { continue; }
-        v += wt * o[(size_t) inv[b * KE + kf] * E_ + e];
+    __shared__ float s_wt[MAXK]; __shared__ int s_row[MAXK]; __shared__ int s_cnt;
+    const int b = blockIdx.y;
+    if (threadIdx.x == 0) {
+        const int * idr = ids + b * KE; const float * wr = w + b * KE;
+        int prev = -1, cnt = 0;
+        for (;;) {   // distinct slot ids of the row, ascending
+            int m = 0x7fffffff;
+            for (int k = 0; k < KE; ++k) { if (idr[k] > prev && idr[k] < m) { m = idr[k]; } }
+            if (m == 0x7fffffff) { break; }
+            float wt = 0.f; int kf = -1;
+            for (int k = 0; k < KE; ++k) { if (idr[k] == m) { wt += wr[k]; if (kf < 0) { kf = k; } } }
+            prev = m;
+            if (wt == 0.f) { continue; }
+            s_wt[cnt] = wt; s_row[cnt] = inv[b * KE + kf]; ++cnt;
+        }
+        s_cnt = cnt;
     }
+    __syncthreads();
+    const int e = blockIdx.x * 256 + threadIdx.x;
+    if (e >= E_) { return; }
+    float v = 0.f;
+    for (int q = 0; q < s_cnt; ++q) { v += s_wt[q] * o[(size_t) s_row[q] * E_ + e]; }
+    const size_t i = (size_t) b * E_ + e;
     if (moe) { moe[i] = v; }
     h[i] = (v + sh[i]) + fi[i];
 }
@@ -153,6 +163,10 @@ struct Compat {
     // pinned host mirrors
     int * h_sel = nullptr; float * h_wts = nullptr, * h_ncur = nullptr, * h_fi = nullptr, * h_h = nullptr, * h_moe = nullptr;
     float * h_wh = nullptr, * h_wmoe = nullptr;
+    // pinned staging of the host inputs (pageable copies would wait for the stream): fl_ffn_begin's ncur / ffn_inp,
+    // fl_moe's ids / w; in_ev is recorded after their copies and waited before the buffers are refilled
+    float * in_ncur = nullptr, * in_fi = nullptr, * in_w = nullptr; int * in_ids = nullptr;
+    hipEvent_t in_ev = nullptr; bool in_rec = false;
 };
 
 static Compat * cs(FLCtx * c) {
@@ -161,7 +175,12 @@ static Compat * cs(FLCtx * c) {
         s->h_sel = pinned<int>(RMAX * MAXK); s->h_wts = pinned<float>(RMAX * MAXK);
         s->h_ncur = pinned<float>((size_t) RMAX * E_); s->h_fi = pinned<float>((size_t) RMAX * E_);
         s->h_h = pinned<float>((size_t) RMAX * E_); s->h_moe = pinned<float>((size_t) RMAX * E_);
-        if (!s->h_sel || !s->h_wts || !s->h_ncur || !s->h_fi || !s->h_h || !s->h_moe) { fatal("hipHostMalloc (fused-layer mirrors)", hipErrorOutOfMemory, __FILE__, __LINE__); }
+        s->in_ncur = pinned<float>((size_t) RMAX * E_); s->in_fi = pinned<float>((size_t) RMAX * E_);
+        s->in_ids = pinned<int>(NB * MAXK); s->in_w = pinned<float>(NB * MAXK);
+        if (!s->h_sel || !s->h_wts || !s->h_ncur || !s->h_fi || !s->h_h || !s->h_moe || !s->in_ncur || !s->in_fi || !s->in_ids || !s->in_w) {
+            fatal("hipHostMalloc (fused-layer mirrors)", hipErrorOutOfMemory, __FILE__, __LINE__);
+        }
+        CK(hipEventCreateWithFlags(&s->in_ev, hipEventDisableTiming));
         c->compat = s;
     }
     return c->compat;
@@ -170,7 +189,9 @@ static Compat * cs(FLCtx * c) {
 void compat_free(FLCtx * c) {
     Compat * s = c->compat;
     if (!s) { return; }
-    for (void * p : { (void *) s->h_sel, (void *) s->h_wts, (void *) s->h_ncur, (void *) s->h_fi, (void *) s->h_h, (void *) s->h_moe, (void *) s->h_wh, (void *) s->h_wmoe }) {
+    if (s->in_ev) { (void) hipEventSynchronize(s->in_ev); (void) hipEventDestroy(s->in_ev); }
+    for (void * p : { (void *) s->h_sel, (void *) s->h_wts, (void *) s->h_ncur, (void *) s->h_fi, (void *) s->h_h, (void *) s->h_moe, (void *) s->h_wh, (void *) s->h_wmoe,
+                      (void *) s->in_ncur, (void *) s->in_fi, (void *) s->in_ids, (void *) s->in_w }) {
         if (p) { (void) hipHostFree(p); }
     }
     for (hipEvent_t e : s->wev) { if (e) { (void) hipEventDestroy(e); } }
@@ -345,8 +366,11 @@ extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur,
     ALLOC(c, s->ncur, R); ALLOC(c, s->fi, R); ALLOC(c, s->logits, RMAX * ne); ALLOC(c, s->probs, RMAX * ne);
     ALLOC(c, s->sel, RMAX * MAXK); ALLOC(c, s->wts, RMAX * MAXK); ALLOC(c, s->xq, R); ALLOC(c, s->xd, RMAX * (E_ / QK)); ALLOC(c, s->sh_o, R);
     hipStream_t st = c->st;
-    TRY(c, hipMemcpyAsync(s->ncur.p, ncur, (size_t) N * E_ * 4, hipMemcpyHostToDevice, st));
-    TRY(c, hipMemcpyAsync(s->fi.p, ffn_inp, (size_t) N * E_ * 4, hipMemcpyHostToDevice, st));
+    if (s->in_rec) { TRY(c, hipEventSynchronize(s->in_ev)); }   // the staging's previous copies have run
+    std::memcpy(s->in_ncur, ncur, (size_t) N * E_ * 4); std::memcpy(s->in_fi, ffn_inp, (size_t) N * E_ * 4);
+    TRY(c, hipMemcpyAsync(s->ncur.p, s->in_ncur, (size_t) N * E_ * 4, hipMemcpyHostToDevice, st));
+    TRY(c, hipMemcpyAsync(s->fi.p, s->in_fi, (size_t) N * E_ * 4, hipMemcpyHostToDevice, st));
+    TRY(c, hipEventRecord(s->in_ev, st)); s->in_rec = true;
     const size_t mg = mat_bytes(H_, E_);
     const void * shm[3] = { W->sh_gate, W->sh_up, W->sh_down };
     bool sht[3];
@@ -418,12 +442,15 @@ extern "C" void fl_moe(FLCtx * c, const void * gate, const void * up, const void
     CK(hipEventRecord(c->em0, st));
     FALLOC(s->ids, P); FALLOC(s->w, P); FALLOC(s->counts, nexp); FALLOC(s->offsets, nexp + 1); FALLOC(s->perm, P); FALLOC(s->inv, P);
     FALLOC(s->act, nexp); FALLOC(s->nact, 1); FALLOC(s->o, (size_t) P * E_); FALLOC(s->hout, (size_t) NB * E_); FALLOC(s->moe, (size_t) NB * E_);
-    CK(hipMemcpyAsync(s->ids.p, ids, (size_t) P * 4, hipMemcpyHostToDevice, st));
-    CK(hipMemcpyAsync(s->w.p, w, (size_t) P * 4, hipMemcpyHostToDevice, st));
+    if (s->in_rec) { CK(hipEventSynchronize(s->in_ev)); }
+    std::memcpy(s->in_ids, ids, (size_t) P * 4); std::memcpy(s->in_w, w, (size_t) P * 4);
+    CK(hipMemcpyAsync(s->ids.p, s->in_ids, (size_t) P * 4, hipMemcpyHostToDevice, st));
+    CK(hipMemcpyAsync(s->w.p, s->in_w, (size_t) P * 4, hipMemcpyHostToDevice, st));
+    CK(hipEventRecord(s->in_ev, st)); s->in_rec = true;
     const Arena ar = pack_arena(c, s, gate, up, down, nexp, down_fmt);
     CK(launch_dispatch(s->ids.p, P, nexp, s->counts.p, s->offsets.p, s->perm.p, s->inv.p, s->act.p, s->nact.p, st));
     routed_experts(c, s, ar, s->xq.p, s->xd.p, n, P, KE, nexp, s->act.p, s->nact.p, s->offsets.p, s->perm.p, s->o.p, down_fmt, down, max_slots);
-    k_combine_slots<<<nblk((int64_t) n * E_), 256, 0, st>>>(s->o.p, s->inv.p, s->ids.p, s->w.p, n, KE, s->sh_o.p, s->fi.p, s->hout.p, s->moe.p);
+    k_combine_slots<<<dim3(E_ / 256, n), 256, 0, st>>>(s->o.p, s->inv.p, s->ids.p, s->w.p, n, KE, s->sh_o.p, s->fi.p, s->hout.p, s->moe.p);
     CK(hipGetLastError());
     CK(hipMemcpyAsync(s->h_h, s->hout.p, (size_t) n * E_ * 4, hipMemcpyDeviceToHost, st));
     CK(hipMemcpyAsync(s->h_moe, s->moe.p, (size_t) n * E_ * 4, hipMemcpyDeviceToHost, st));
