@@ -33,12 +33,14 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int PF_W = 8, PF_NT = PF_W * 64;   // waves / threads per workgroup
-constexpr int PF_TOK = 32;                   // slots per column (two 16-token MFMA tiles)
+constexpr int PF_W = 8, PF_NT = PF_W * 64;   // waves / threads per workgroup (two per SIMD: each hides the other's latency)
+constexpr int PF_NTM = 4;                    // 16-token MFMA tiles per column at most
+constexpr int PF_TOK = 16 * PF_NTM;          // slots per column: the dequantised weights of an item serve all of them
 // LDS: fp16 codebook (256 lines x 16 copies x 16 B), fp16 sign masks (128 lines, the 7 stored sign bits), then two
-// activation buffers (32 token rows x 512 B, each row's 16-byte chunks XOR-swizzled by the row, then 32 scales)
+// activation buffers (64 token rows x 512 B, each row's 16-byte chunks XOR-swizzled by the row): exactly 160 KB. The
+// tokens' block scales stay in registers (one per lane, handed to the lanes that fold them by ds_bpermute).
 constexpr int L_PG = 0, L_PS = 65536, L_PB = L_PS + 128 * 256;
-constexpr int PB_TILE = 16 * 512, PB_DX = 2 * PB_TILE, PB_BUF = PB_DX + 512;   // buffers 512-byte aligned
+constexpr int PB_TILE = 16 * 512, PB_BUF = PF_NTM * PB_TILE;   // buffers 512-byte aligned
 constexpr int PF_LDS = L_PB + 2 * PB_BUF;
 constexpr int PTAB_BYTES = L_PB;             // the table image copied to LDS offset 0
 static_assert(PF_LDS <= 160 * 1024, "LDS budget");
@@ -66,7 +68,7 @@ hipError_t build_prefill_tables(uint4 * img, hipStream_t st) {
 }
 size_t prefill_table_bytes() { return PTAB_BYTES; }
 
-// columns: the shared expert's slots first (P + 32 c ..), then every active expert's slots in act order, 32 per column
+// columns: the shared expert's slots first (P + 64 c ..), then every active expert's slots in act order, 64 per column
 __global__ void __launch_bounds__(256) k_pf_cols(const int * __restrict__ act, const int * __restrict__ nact_p, const int * __restrict__ offsets,
                                                 int n, int P, int4 * __restrict__ cols, int * __restrict__ ncols) {
     __shared__ int scan[256];
@@ -137,6 +139,15 @@ __device__ __forceinline__ const uint8_t * pf_uniform(const uint8_t * p) {
     return (const uint8_t *) (((uint64_t) hi << 32) | (uint64_t) lo);
 }
 
+// 16 bytes per lane from a buffer straight into LDS (lane L at dst + 16 L); the builtin exists for the device pass only,
+// so the host pass (which instantiates the kernel's launch stub) sees an empty body
+__device__ __forceinline__ void buf_lds16(__amdgpu_buffer_rsrc_t r, LK_LOCAL uint8_t * dst, uint32_t voff, uint32_t soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LK_LOCAL void *) dst, 16, voff, soff, 0, 0);
+#else
+    (void) r; (void) dst; (void) voff; (void) soff;
+#endif
+}
 __device__ __forceinline__ void dma16(const void * src, LK_LOCAL uint8_t * dst) {
     __builtin_amdgcn_global_load_lds((const LK_GLOBAL void *) src, (LK_LOCAL void *) dst, 16, 0, 0);
 }
@@ -179,29 +190,10 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
             const int s = sb + (n32 < sc ? n32 : 0);
             return NMAT == 2 ? (routed ? gptr(a.perm)[s] / a.topk : s - a.P) : s;
         };
-        const int rA = brow(4 * wave + (lane >> 5)), rB = brow(4 * wave + 2 + (lane >> 5));
-        const int rX = brow(lane & 31);
-        const int p = lane & 31;
-        const int cA = p ^ ((4 * wave + (lane >> 5)) & 15), cB = p ^ ((4 * wave + 2 + (lane >> 5)) & 15);
         // Buffer loads: a scalar resource (base, no bounds that matter) + a 32-bit lane offset + a scalar block offset,
         // so no 64-bit per-lane address lives in vector registers.
         const __amdgpu_buffer_rsrc_t rb = pf_rsrc(a.bh), rd = pf_rsrc(a.bd);
-        const uint32_t oA = (uint32_t) rA * (Geo::K * 2) + (uint32_t) cA * 16, oB = (uint32_t) rB * (Geo::K * 2) + (uint32_t) cB * 16;
-        const uint32_t oX = (uint32_t) rX * (NB * 4);
-        // the column's activations of block j: this wave's rows 4 w .. 4 w + 3 (two 1 KB pieces) and the 32 scales,
-        // loaded into registers, then written to LDS (after the block that reads the other buffer)
-        struct PfB { u32x4 a, b; float dx; };
-        auto load_b = [&](int j, PfB & bq) {
-            bq.a = __builtin_amdgcn_raw_buffer_load_b128(rb, oA, j * (QK * 2), 0);
-            bq.b = __builtin_amdgcn_raw_buffer_load_b128(rb, oB, j * (QK * 2), 0);
-            bq.dx = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, oX, j * 4, 0));
-        };
-        auto store_b = [&](const PfB & bq, int buf) {
-            LK_LOCAL uint8_t * dst = lds + L_PB + buf * PB_BUF;
-            *(LK_LOCAL u32x4 *) (dst + (4 * wave) * 512 + lane * 16) = bq.a;
-            *(LK_LOCAL u32x4 *) (dst + (4 * wave + 2) * 512 + lane * 16) = bq.b;
-            if (wave == 0 && lane < 32) { *(LK_LOCAL float *) (dst + PB_DX + lane * 4) = bq.dx; }
-        };
+        const uint32_t oX = (uint32_t) brow(lane) * (NB * 4);   // lane n loads the scale of token n of the column
         // the wave's tiles: combo c = (matrix c / RGI, 16-row tile c % RGI): scalar resources at the tile's qs / d
         // bases, the lane's offset (chunk g of row r) in one vector register
         __amdgpu_buffer_rsrc_t uq[C], ud[C];
@@ -223,13 +215,34 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
             }
         };
         auto run_item = [&](auto ntc) {
-            constexpr int NT = decltype(ntc)::value;   // token tiles of the column (1 or 2)
+            constexpr int NT = decltype(ntc)::value;   // token tiles of the column (1, 2 or 4)
+            // the column's activations of block j go straight from memory into LDS buffer j % 2 (buffer loads to LDS:
+            // lane L's 16 bytes land at L * 16 of the instruction's 1 KB, no registers): wave w copies token rows
+            // RW w + 2 i + (lane / 32), i < RW / 2 (RW = 16 NT / PF_W rows per wave), lane L < 32 of a row taking the
+            // row's chunk L ^ (row % 16) -- the XOR swizzle applied on the memory side. Lane n also loads token n's
+            // block scale into a register.
+            constexpr int RW = 16 * NT / PF_W, NI = RW / 2;
+            struct PfB { float dx; };
+            uint32_t ob[NI];
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int row = RW * wave + 2 * i + (lane >> 5);
+                ob[i] = (uint32_t) brow(row) * (Geo::K * 2) + (uint32_t) ((lane & 31) ^ (row & 15)) * 16;
+            }
+            auto load_b = [&](int j, PfB & bq, int buf) {
+                LK_LOCAL uint8_t * dst = lds + L_PB + buf * PB_BUF;
+#pragma unroll
+                for (int i = 0; i < NI; ++i) {
+                    buf_lds16(rb, dst + (RW * wave + 2 * i) * 512, ob[i], j * (QK * 2));
+                }
+                bq.dx = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, oX, j * 4, 0));
+            };
             f4 acc[C][NT];
 #pragma unroll
             for (int c = 0; c < C; ++c) { for (int tt = 0; tt < NT; ++tt) { acc[c][tt] = (f4) { 0.f, 0.f, 0.f, 0.f }; } }
 
             // one block: dequantise the C tiles step by step and run the MFMA chains of both token tiles
-            auto block = [&](int j, const PfW (&w)[C], int buf) {
+            auto block = [&](int j, const PfW (&w)[C], int buf, float dxl) {
                 static_assert((L_PB % 512) == 0 && (PB_BUF % 512) == 0, "XOR addressing inside 512-byte rows");
                 const uint32_t bx = ((uint32_t) (L_PB + buf * PB_BUF) + (uint32_t) ln.r * 512) | ((uint32_t) ((8 * ln.g) ^ ln.r) << 4);
                 f4 cc[C][NT], cd[C][NT];   // the two exact chains: steps 0-3, steps 4-7
@@ -243,11 +256,11 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
                 }
                 // step t's LDS reads (two activation chunks, per tile a codebook and a sign entry) are issued one step
                 // ahead of their use, into the other of two register sets
-                struct Lk { u32x4 g[C], s[C]; h8 x0, x1; };
+                struct Lk { u32x4 g[C], s[C]; h8 x[NT]; };
                 auto lookup = [&](int t, Lk & k) {
                     const uint32_t bo = bx ^ ((uint32_t) t << 4);   // chunk (8 g + t) ^ r of the lane's token row
-                    k.x0 = __builtin_bit_cast(h8, *(const LK_LOCAL u32x4 *) (size_t) bo);
-                    if (NT > 1) { k.x1 = __builtin_bit_cast(h8, *(const LK_LOCAL u32x4 *) (size_t) (bo + PB_TILE)); }
+#pragma unroll
+                    for (int tt = 0; tt < NT; ++tt) { k.x[tt] = __builtin_bit_cast(h8, *(const LK_LOCAL u32x4 *) (size_t) (bo + tt * PB_TILE)); }
 #pragma unroll
                     for (int c = 0; c < C; ++c) {
                         const uint32_t a0 = t < 4 ? w[c].q.x : w[c].q.z, a1 = ms[c][t >> 2];
@@ -269,60 +282,77 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
                         const h2v s = sc[c][t >> 2];
                         const h8 wv = gs * (h8) { s[0], s[1], s[0], s[1], s[0], s[1], s[0], s[1] };
                         const f4 z = (f4) { 0.f, 0.f, 0.f, 0.f };
-                        if (t < 4) {
-                            cc[c][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k.x0, wv, t == 0 ? z : cc[c][0], 0, 0, 0);
-                            if (NT > 1) { cc[c][NT - 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k.x1, wv, t == 0 ? z : cc[c][NT - 1], 0, 0, 0); }
-                        } else {
-                            cd[c][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k.x0, wv, t == 4 ? z : cd[c][0], 0, 0, 0);
-                            if (NT > 1) { cd[c][NT - 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k.x1, wv, t == 4 ? z : cd[c][NT - 1], 0, 0, 0); }
+#pragma unroll
+                        for (int tt = 0; tt < NT; ++tt) {
+                            if (t < 4) {
+                                cc[c][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k.x[tt], wv, t == 0 ? z : cc[c][tt], 0, 0, 0);
+                            } else {
+                                cd[c][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k.x[tt], wv, t == 4 ? z : cd[c][tt], 0, 0, 0);
+                            }
                         }
                     }
                 };
-                Lk ka, kb;
-                lookup(0, ka);
+                if constexpr (C * NT <= 4) {   // two register sets: step t + 1's reads issued before step t's MFMAs
+                    Lk ka, kb;
+                    lookup(0, ka);
 #pragma unroll
-                for (int t = 0; t < 8; t += 2) {
-                    lookup(t + 1, kb);
-                    compute(t, ka);
-                    if (t + 2 < 8) { lookup(t + 2, ka); }
-                    compute(t + 1, kb);
+                    for (int t = 0; t < 8; t += 2) {
+                        lookup(t + 1, kb);
+                        compute(t, ka);
+                        if (t + 2 < 8) { lookup(t + 2, ka); }
+                        compute(t + 1, kb);
+                    }
+                } else {                       // more tiles: one set (the step's MFMAs cover the next reads' latency)
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        Lk k; lookup(t, k); compute(t, k);
+                        __builtin_amdgcn_sched_barrier(0);   // steps stay in order: reads of later steps are not hoisted
+                    }
                 }
-                // block fold, in block order: y += (d_w * d_x) * bsum, bsum = the two chains' exact totals added once
-                const f4 dx0 = *(const LK_LOCAL f4 *) (size_t) ((uint32_t) (L_PB + buf * PB_BUF + PB_DX) + 16 * ln.g);
-                const f4 dx1 = NT > 1 ? *(const LK_LOCAL f4 *) (size_t) ((uint32_t) (L_PB + buf * PB_BUF + PB_DX) + 64 + 16 * ln.g) : dx0;
+                // block fold, in block order: y += (d_w * d_x) * bsum, bsum = the two chains' exact totals added once; the
+                // scale of token 16 tt + 4 g + i comes from the lane that loaded it
+                float dx[NT][4];
+#pragma unroll
+                for (int tt = 0; tt < NT; ++tt) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        dx[tt][i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * (16 * tt + 4 * ln.g + i), __builtin_bit_cast(int, dxl)));
+                    }
+                }
 #pragma unroll
                 for (int c = 0; c < C; ++c) {
                     const float dw = h2f(w[c].d);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) { acc[c][0][i] = acc[c][0][i] + (dw * dx0[i]) * (cc[c][0][i] + cd[c][0][i]); }
-                    if (NT > 1) {
+                    for (int tt = 0; tt < NT; ++tt) {
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) { acc[c][NT - 1][i] = acc[c][NT - 1][i] + (dw * dx1[i]) * (cc[c][NT - 1][i] + cd[c][NT - 1][i]); }
+                        for (int i = 0; i < 4; ++i) { acc[c][tt][i] = acc[c][tt][i] + (dw * dx[tt][i]) * (cc[c][tt][i] + cd[c][tt][i]); }
                     }
                 }
-                (void) j;
+                (void) j; (void) buf;
             };
 
             // pipeline: weights two blocks ahead (three register stages), activations one block ahead (registers, then
             // the other of two LDS buffers). Every step issues the same loads (indices clamped at the last blocks: those
             // copies land in registers nobody reads any more), so the compiler's waits count them exactly.
+            // short rows (down, 8 blocks) and items of many tiles keep the weights one block ahead (two stages): their
+            // register budget is tighter
+            constexpr int WA = (NB <= 8 || C * NT > 4) ? 1 : 2;
             PfW w0[C], w1[C], w2[C];
             PfB bq;
             load_w(0, w0);
-            if (NB > 8) { load_w(1, w1); }
-            load_b(0, bq);
-            store_b(bq, 0);
+            if (WA == 2) { load_w(1, w1); }
+            load_b(0, bq, 0);
+            __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): block 0's activations are in LDS
             __syncthreads();
-            // short rows (down, 8 blocks) keep the weights one block ahead (two stages): their register budget is tighter
-            constexpr int WA = NB <= 8 ? 1 : 2;
             auto step = [&](int j, PfW (&cur)[C], PfW (&ahead)[C]) {
-                load_b(j + 1 < NB ? j + 1 : NB - 1, bq);
+                const float dxl = bq.dx;             // block j's scale (loaded with its activations)
+                // buffer (j + 1) % 2 was last read in step j - 1, before its barrier
+                load_b(j + 1 < NB ? j + 1 : NB - 1, bq, (j + 1) & 1);
                 load_w(j + WA < NB ? j + WA : NB - 1, ahead);
                 __builtin_amdgcn_sched_barrier(0);   // nothing of the block moves above the loads
-                block(j, cur, j & 1);
-                store_b(bq, (j + 1) & 1);           // buffer (j + 1) & 1 was last read in step j - 1, before its barrier
-                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the writes are done before the barrier publishes them
-                __builtin_amdgcn_s_barrier();
+                block(j, cur, j & 1, dxl);
+                __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): block j + 1's activations have landed in LDS (and the
+                __builtin_amdgcn_s_barrier();       // weights of the next block are in): the barrier publishes them
             };
             if constexpr (WA == 1) {   // step j uses stage j % 2 and refills the other with block j + 1
                 static_assert(NB % 2 == 0, "two steps per trip");
@@ -364,7 +394,9 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
                 }
             }
         };
-        if (sc > 16) { run_item(std::integral_constant<int, 2>{}); } else { run_item(std::integral_constant<int, 1>{}); }
+        if (sc > 32) { run_item(std::integral_constant<int, 4>{}); }
+        else if (sc > 16) { run_item(std::integral_constant<int, 2>{}); }
+        else { run_item(std::integral_constant<int, 1>{}); }
     }
 }
 
