@@ -381,8 +381,13 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
         if (prenorm && !(eps >= 0.f)) { return fail(c, FL_EINVAL, "bad norm eps %g", (double) eps); }
     }
     const size_t rows = (size_t) P + n;
-    // K-quant matrices run on the per-pass path (the decode block and the MFMA GEMMs read IQ2_XXS tiles)
-    const bool fused = !kq && c->fused && n <= 8 && E == 7168 && H == 2048 && decode_rule_ok(ne, c->n_group) && decode_ready(c);
+    // K-quant matrices run on the per-pass path (the decode block and the MFMA GEMMs read IQ2_XXS tiles), except for
+    // one token on the real shards' formats (routed down Q2_K / Q3_K, shared expert Q5_K / Q5_K / Q6_K), which the
+    // one-token kernel reads in place
+    static_assert(FL_Q6K == 1 && FL_Q5K == 3 && FL_Q2K == 5 && FL_Q3K == 6, "the FL_ codes are the K-quant kernels' format codes");
+    const int kd1 = (lf[0] == FL_Q2K || lf[0] == FL_Q3K) && lf[1] == FL_Q5K && lf[2] == FL_Q5K && lf[3] == FL_Q6K ? lf[0] : 0;
+    const bool kq1 = kq && kd1 != 0 && n == 1 && tsel == MAXK && tk == MAXK && decode1_ready(c);
+    const bool fused = (!kq || kq1) && c->fused && n <= 8 && E == 7168 && H == 2048 && decode_rule_ok(ne, c->n_group) && decode_ready(c);
     const bool mfma = !kq && !fused && c->pf_mfma && n > 8 && E == 7168 && H == 2048;
     ALLOC(c, c->xq, (size_t) n * E); ALLOC(c, c->xd, (size_t) n * (E / 256));
     ALLOC(c, c->logits, (size_t) n * ne); ALLOC(c, c->probs, (size_t) n * ne);
@@ -410,6 +415,7 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
         d.gate = (const uint8_t *) L->gate_exps; d.up = (const uint8_t *) L->up_exps; d.down = (const uint8_t *) L->down_exps;
         d.estride = (size_t) H * (E / 256) * IQ2B;
         d.sh_gate = (const uint8_t *) L->sh_gate; d.sh_up = (const uint8_t *) L->sh_up; d.sh_down = (const uint8_t *) L->sh_down;
+        d.kdown = kq ? kd1 : 0; d.dstride = fmt_mat_bytes(lf[0], E, H);
         d.E = E; d.H = H;
         d.xq = c->xq.p; d.xd = c->xd.p; d.logits = c->logits.p; d.probs = c->probs.p; d.sel = c->sel.p; d.wts = c->wts.p;
         d.counts = c->counts.p; d.offsets = c->offsets.p; d.perm = c->perm.p; d.inv = c->inv.p; d.act = c->act.p; d.nact = c->nact.p;

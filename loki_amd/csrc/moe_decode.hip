@@ -784,7 +784,7 @@ bool decode_rule_ok(int n_exp, int n_group) {   // the selection's DPP group pat
 
 hipError_t launch_moe_decode(const DecodeArgs & a, int grid, bool cooperative, hipStream_t st) {
     if (a.n < 1 || a.n > DMAX_N || a.topk < 1 || a.topk > MAXK || a.keep < 1 || a.keep > a.topk || !decode_rule_ok(a.n_exp, a.n_group) ||
-        a.E != DE || a.H != DH || grid < 1 || !a.th || !a.to || !a.tlogits) {
+        a.E != DE || a.H != DH || grid < 1 || !a.th || !a.to || !a.tlogits || a.kdown != 0) {   // IQ2_XXS matrices only
         return hipErrorInvalidValue;
     }
     if (!cooperative) {   // one workgroup per CU fits the occupancy; co-residency is assumed, waits stay bounded

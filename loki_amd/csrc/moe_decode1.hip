@@ -25,7 +25,7 @@
 // inside an XCD (the picks, h) stay in its L2; those across XCDs (logits, down partials) go through the device's
 // coherence point. Every wait is bounded: a timeout sets the error word and the wave skips the work, so the grid
 // always drains.
-#include "moe_device.h"
+#include "kquant_device.h"
 #include "moe_kernels.h"
 
 namespace lk {
@@ -58,8 +58,11 @@ static_assert((size_t) SLOTS1 * H1 <= DEC_TH && (size_t) SLOTS1 * NBH1 * E1 <= D
 constexpr int M_X = TAB_BYTES;                     // staged Q8_K of the token
 constexpr int M_HR = M_X + GX1::XROW;              // staged Q8_K of the routed h block (256 B + scale)
 constexpr int M_HS = M_HR + 272;                   // staged Q8_K of the shared h block
-constexpr int M_PRE = M_HS + 272;                  // shared task block terms [7 steps][64 lanes]
-constexpr int M_TERMS = M_PRE + GU_STEPS1 * 64 * 4;   // routed block terms [matrix][block][64 rows]
+constexpr int SHKP1 = 2 * NBX1;                    // K-quant shared task: (matrix, block) passes of 8 rows
+// shared task block terms: IQ2_XXS [7 steps][64 lanes]; K-quant [matrix][8 rows][28 blocks], then the min terms
+constexpr int PRE1 = GU_STEPS1 * 64 * 4 > 2 * SHKP1 * 8 * 4 ? GU_STEPS1 * 64 * 4 : 2 * SHKP1 * 8 * 4;
+constexpr int M_PRE = M_HS + 272;
+constexpr int M_TERMS = M_PRE + PRE1;                  // routed block terms [matrix][block][64 rows]
 constexpr int M_SCR = M_TERMS + NITEM1 * 64 * 4;   // router / norm partial sums [4] (fp64)
 constexpr int M_CMB = M_SCR + 64;                  // combine: o [28 rows][9 slots]
 constexpr int M_SEL = M_CMB + CROWS1 * SLOTS1 * 4; // picks [8] and weights [8]
@@ -340,6 +343,119 @@ __device__ __forceinline__ void shared_gu1(const D1Args & a, lds1_t lds, int wav
     gu1_publish(a, 8, hrow0, q, r, acc);
 }
 
+// ---------------------------------------------------------------- K-quant matrices (ggml's block layout, in place)
+// The token and the h blocks are staged for the IQ2_XXS lookups (staged_word): values 8 w .. 8 w + 7 of a block sit
+// contiguously at (w % 4) * 64 + (w / 4) * 8, so a K-quant slice's 8-byte runs are read from there.
+__device__ __forceinline__ int staged8(int v) { return ((v >> 3) & 3) * 64 + (v >> 5) * 8; }
+// load_x (kquant_device.h) on a staged block: the same words and per-piece sums
+template <int F> __device__ __forceinline__ void load_x_st(const LK_LOCAL int8_t * xb, int q, XChunk & x) {
+    const int ones = 0x01010101;
+    if constexpr (F == KF_Q5K) {
+        const int jj = q >> 1, hf = q & 1;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int v0 = 64 * jj + 32 * h + 16 * hf;
+            const uint2 a0 = kx8(xb + staged8(v0)), a1 = kx8(xb + staged8(v0 + 8));
+            x.x[4 * h] = a0.x; x.x[4 * h + 1] = a0.y; x.x[4 * h + 2] = a1.x; x.x[4 * h + 3] = a1.y;
+            int sm = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { sm = __builtin_amdgcn_sdot4((int) x.x[4 * h + i], ones, sm, false); }
+            x.bx[h] = sm;
+        }
+#pragma unroll
+        for (int h = 2; h < 8; ++h) { x.bx[h] = 0; }
+    } else {
+        const int n = q >> 2, jq = q & 3;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const uint2 v = kx8(xb + staged8(128 * n + 32 * s + 8 * jq));
+            x.x[2 * s] = v.x; x.x[2 * s + 1] = v.y;
+            x.bx[s] = __builtin_amdgcn_sdot4((int) v.y, ones, __builtin_amdgcn_sdot4((int) v.x, ones, 0, false), false);
+            x.bx[4 + s] = 0;
+        }
+    }
+}
+// a buffer resource over a matrix of `bytes` (wave-uniform base); lane offsets in vb, the row offset in so
+__device__ __forceinline__ Src src1(const uint8_t * mat, uint64_t bytes, uint32_t vb) {
+    Src s;
+    s.rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(uniform1(mat)), (short) 0,
+                                             (int) (bytes < 0x7fffffffull ? bytes : 0x7fffffffull), 0x00020000);
+    s.vb = vb; s.so = 0;
+    return s;
+}
+// a slice's exact integer block sums (red8 over the 8 lanes of its row) and the fp32 block term of the K-quant
+// mat-vec (kquant.hip), valid in the row's first lane: Q2_K (d8 d) isum - (d8 dmin) summ, Q3_K / Q6_K (d d8) isum,
+// Q5_K (d d8) isum with the min term (dmin d8) summ beside it
+template <int F> __device__ __forceinline__ float kq_term1(const Raw<F> & raw, const XChunk & xc, int c, float & tmin) {
+#pragma clang fp contract(off)
+    Chunk ck; decode<F>(raw, c, ck);
+    int is, sm;
+    chunk_dot<F>(ck, xc, is, sm);
+    is = red8(is);
+    const float d8 = xc.d8;
+    tmin = 0.f;
+    if constexpr (F == KF_Q2K) { sm = red8(sm); return (d8 * ck.d) * (float) is - (d8 * ck.dmin) * (float) sm; }
+    else if constexpr (F == KF_Q5K) { sm = red8(sm); tmin = (ck.dmin * d8) * (float) sm; return (ck.d * d8) * (float) is; }
+    else { return (ck.d * d8) * (float) is; }
+}
+
+// The shared expert's gate/up task in Q5_K (h rows 8 t .. 8 t + 7, t = 32 x + i): 56 passes (matrix, block), each 8
+// rows (lane = row r8, slice c), spread over the staging waves (pass p on wave 4 + p % 12). Block terms to LDS; the
+// wave that completes the 56th pass folds each row's terms in block order (the K-quant mat-vec's order: acc += t,
+// accm -= t_min, acc_m + acc) and publishes h = silu(g) * u.
+constexpr int QR5 = NBX1 * kbytes<KF_Q5K>();   // Q5_K row bytes at K = 7168
+__device__ __forceinline__ bool shared_gu1_kq(const D1Args & a, lds1_t lds, int wave, int xcd, int li, LK_LOCAL unsigned * ctl) {
+#pragma clang fp contract(off)
+    const int lane = lane_id(), r8 = lane >> 3, c = lane & 7, hrow0 = (xcd * 32 + li) * 8;
+    LK_LOCAL float * ts = reinterpret_cast<LK_LOCAL float *>(lds + M_PRE);   // [matrix][row][block]
+    LK_LOCAL float * tm = ts + 2 * 8 * NBX1;
+    const LK_LOCAL int8_t * xs = reinterpret_cast<const LK_LOCAL int8_t *>(lds + M_X);
+    const LK_LOCAL float * dx = reinterpret_cast<const LK_LOCAL float *>(lds + M_X + NBX1 * GX1::XBLK);
+    Src sm[2] = { src1(a.sh_gate, (uint64_t) H1 * QR5, (uint32_t) r8 * QR5), src1(a.sh_up, (uint64_t) H1 * QR5, (uint32_t) r8 * QR5) };
+    sm[0].so = sm[1].so = (uint32_t) hrow0 * QR5;
+    auto issue = [&](int p, Raw<KF_Q5K> & r) {
+        Src s = sm[p & 1];
+        s.vb += (uint32_t) (p >> 1) * kbytes<KF_Q5K>();
+        load_raw<KF_Q5K>(s, c, r);
+    };
+    auto run = [&](const Raw<KF_Q5K> & r, int p) {
+        const int m = p & 1, j = p >> 1;
+        XChunk xc;
+        load_x_st<KF_Q5K>(xs + j * GX1::XBLK, c, xc);
+        xc.d8 = dx[j];
+        float tmin;
+        const float t = kq_term1<KF_Q5K>(r, xc, c, tmin);
+        if (c == 0) { ts[(m * 8 + r8) * NBX1 + j] = t; tm[(m * 8 + r8) * NBX1 + j] = tmin; }
+        if (arrive1(ctl + C_SH, SHKP1)) {
+            float v = 0.f;
+            if (lane < 16) {
+                const LK_LOCAL float * tp = ts + lane * NBX1, * mp = tm + lane * NBX1;   // lanes 0-7: gate rows, 8-15: up
+                float acc = 0.f, accm = 0.f;
+                for (int k = 0; k < NBX1; ++k) { acc = acc + tp[k]; accm = accm - mp[k]; }
+                v = accm + acc;
+            }
+            const float u = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));
+            if (lane < 8) { st_xcd1(a.th + (size_t) 8 * H1 + hrow0 + lane, a.epoch, __builtin_bit_cast(uint32_t, det_silu(v) * u)); }
+        }
+    };
+    const int w = wave - 4;
+    Raw<KF_Q5K> ra, rb;
+    int p = w;
+    if (p < SHKP1) { issue(p, ra); }
+    if (!wait1(ctl + C_STAGED, NQW1)) { report1(a, 8); return false; }
+    lds_visible();
+    while (p < SHKP1) {   // the next pass's bytes are in flight while the current one is computed
+        if (p + NQW1 < SHKP1) { issue(p + NQW1, rb); }
+        run(ra, p);
+        p += NQW1;
+        if (p >= SHKP1) { break; }
+        if (p + NQW1 < SHKP1) { issue(p + NQW1, ra); }
+        run(rb, p);
+        p += NQW1;
+    }
+    return true;
+}
+
 // The workgroup's routed gate/up: h rows hrow0 .. hrow0 + 63 (one 64-row group of both matrices) as 56 items, item c =
 // matrix c % 2 (gate, up) at block c / 2, claimed in order by all waves from an LDS counter; a wave claims its next
 // item when it has used the last. Lane l owns row hrow0 + l of the item's matrix, so each of its 16-byte loads is one contiguous 1 KB
@@ -428,10 +544,49 @@ __device__ __forceinline__ bool stage_h1(const D1Args & a, const uint64_t * src,
     return true;
 }
 
+// K-quant down units (one 64-row group at one K-block): 8 passes of 8 rows (lane = row r8, slice c), each row's block
+// term published as a tagged word as the IQ2_XXS units publish theirs. Runs the wave's claimed units below uend
+// (rows g64_of(u) * 64 ..), claiming the next when it starts a unit's last pass so that its first bytes are in flight;
+// returns the first claim at or past uend. `loaded`: ra already holds pass 0 of unit u.
+template <int F, class G64, class Claim>
+__device__ __forceinline__ int down_kq1(const D1Args & a, int u, int uend, bool loaded, Raw<F> & ra, const Src & base,
+                                        const LK_LOCAL int8_t * hb, float d8, int slot, int blk, G64 g64_of, Claim claim) {
+#pragma clang fp contract(off)
+    constexpr uint32_t RB = NBH1 * kbytes<F>();   // row bytes at K = 2048
+    const int lane = lane_id(), r8 = lane >> 3, c = lane & 7;
+    XChunk xc;
+    load_x_st<F>(hb, c, xc);
+    xc.d8 = d8;
+    auto issue = [&](int uu, int p, Raw<F> & r) { Src s = base; s.so = (uint32_t) (g64_of(uu) * 64 + 8 * p) * RB; load_raw<F>(s, c, r); };
+    auto step = [&](const Raw<F> & r, int uu, int p) {
+        float tmin;
+        const float t = kq_term1<F>(r, xc, c, tmin);
+        if (c == 0) { st_tag1(a.to + ((size_t) slot * NBH1 + blk) * E1 + (size_t) g64_of(uu) * 64 + 8 * p + r8, a.epoch, t); }
+    };
+    auto next = [&](int & uu, int & p) { if (++p == 8) { uu = claim(); p = 0; } };
+    if (!loaded && u < uend) { issue(u, 0, ra); }
+    Raw<F> rb;
+    int p = 0;
+    while (u < uend) {
+        int un = u, pn = p;
+        next(un, pn);
+        if (un < uend) { issue(un, pn, rb); }
+        step(ra, u, p);
+        u = un; p = pn;
+        if (u >= uend) { break; }
+        next(un, pn);
+        if (un < uend) { issue(un, pn, ra); }
+        step(rb, u, p);
+        u = un; p = pn;
+    }
+    return u;
+}
+
 // ---------------------------------------------------------------- 4. combine
 // thread (row i, slot s) of the first 252: the 8 tagged block terms of its row and slot, folded in block order,
-// * 0.125; then thread i < 28 forms y = sum_k w_k o_k (k order) + o_shared (+ the residual)
-__device__ __forceinline__ bool combine1(const D1Args & a, lds1_t lds) {
+// * 0.125 for an IQ2_XXS matrix (its grid scale; the K-quant terms carry their scales); then thread i < 28 forms
+// y = sum_k w_k o_k (k order) + o_shared (+ the residual)
+template <bool KQ> __device__ __forceinline__ bool combine1(const D1Args & a, lds1_t lds) {
 #pragma clang fp contract(off)
     LK_LOCAL float * cmb = reinterpret_cast<LK_LOCAL float *>(lds + M_CMB);
     const LK_LOCAL float * wts = reinterpret_cast<const LK_LOCAL float *>(lds + M_SEL + MAXK * 4);
@@ -459,7 +614,7 @@ __device__ __forceinline__ bool combine1(const D1Args & a, lds1_t lds) {
         float o = 0.f;
 #pragma unroll
         for (int kb = 0; kb < NBH1; ++kb) { o = o + tag1_val(w[kb]); }
-        cmb[i * SLOTS1 + s] = 0.125f * o;
+        cmb[i * SLOTS1 + s] = KQ ? o : 0.125f * o;
     }
     __syncthreads();
     if (t < CROWS1) {
@@ -500,6 +655,8 @@ __device__ __noinline__ void routing1(const D1Args & a, lds1_t lds) {
 }
 
 // ---------------------------------------------------------------- the kernel
+// FD: 0 (every matrix IQ2_XXS), or the routed down's K-quant (the shared expert then Q5_K / Q5_K / Q6_K)
+template <int FD>
 __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
 #pragma clang fp contract(off)
     (void) sizeof(args);   // read in place in the kernarg segment (scalar loads), as the general decode kernel does
@@ -538,10 +695,15 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
         arrive1(ctl + C_STAGED, NQW1);
         TRACE1(1);
     }
-    if (wave >= W1 - GU_STEPS1) {   // the shared expert's gate/up task, one step per wave
-        if (!wait1(ctl + C_STAGED, NQW1)) { report1(a, 8); return; }
-        lds_visible();
-        shared_gu1(a, lds, wave, xcd, li, tr, q, r, ctl);
+    if constexpr (FD == 0) {
+        if (wave >= W1 - GU_STEPS1) {   // the shared expert's gate/up task, one step per wave
+            if (!wait1(ctl + C_STAGED, NQW1)) { report1(a, 8); return; }
+            lds_visible();
+            shared_gu1(a, lds, wave, xcd, li, tr, q, r, ctl);
+            TRACE1(2);
+        }
+    } else if (wave >= 4) {   // in Q5_K: 56 passes over the staging waves
+        if (!shared_gu1_kq(a, lds, wave, xcd, li, ctl)) { return; }
         TRACE1(2);
     }
 
@@ -596,51 +758,78 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
     //    claimed by the waves in order; each wave's first unit streams in while the h blocks are polled and staged
     const int nsh = li < RGE1 - 3 * 32 ? 4 : 3;   // shared row groups li, li + 32, .. (< 112)
     const int nunits = RGQ1 + nsh;
-    const uint8_t * dmat = nullptr;
-    {
-        const int e = reinterpret_cast<const LK_LOCAL int *>(lds + M_SEL)[xcd];
-        dmat = uniform1(a.down + (size_t) e * a.estride);
-    }
-    auto unit = [&](int u, const uint8_t * & mat, int & g64, int & blk, int & slot) {
-        if (u < RGQ1) { mat = dmat; g64 = qq * RGQ1 + u; blk = kb; slot = xcd; }
-        else { mat = uniform1(a.sh_down); g64 = li + 32 * (u - RGQ1); blk = xcd; slot = 8; }
-    };
-    // the waves claim units from an LDS counter, one in flight per wave (as the gate/up items)
+    const int e_dn = reinterpret_cast<const LK_LOCAL int *>(lds + M_SEL)[xcd];
     LK_LOCAL unsigned * dclaim = ctl + C_DNCLAIM;
-    auto claim_unit = [&](Dn1 & d, int & u) {
-        unsigned c = 0;
-        if (lane == 0) { c = __hip_atomic_fetch_add(dclaim, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
-        u = (int) __builtin_amdgcn_readfirstlane(c);
-        if (u < nunits) { const uint8_t * m; int g, b, sl; unit(u, m, g, b, sl); dn1_issue(m, g, b, d); }
+    // waves 0 and 1 poll and stage the routed and the shared h block; every wave then waits for both
+    auto stage_both = [&]() -> bool {
+        if (wave == 0) {
+            const bool ok = stage_h1(a, a.th + (size_t) xcd * H1 + (size_t) kb * QK, lds + M_HR);
+            if (!ok) { report1(a, 1); }
+            flag1(ctl + C_HR, ok ? 1u : 2u);
+        } else if (wave == 1) {
+            const bool ok = stage_h1(a, a.th + (size_t) 8 * H1 + (size_t) xcd * QK, lds + M_HS);
+            if (!ok) { report1(a, 1); }
+            flag1(ctl + C_HS, ok ? 1u : 2u);
+        }
+        TRACE1(7);
+        if (wait1(ctl + C_HR, 1) != 1 || wait1(ctl + C_HS, 1) != 1) { return false; }
+        lds_visible();
+        TRACE1(8);
+        return true;
     };
-    Dn1 dn; int un;
-    claim_unit(dn, un);
-    if (wave == 0) {
-        const bool ok = stage_h1(a, a.th + (size_t) xcd * H1 + (size_t) kb * QK, lds + M_HR);
-        if (!ok) { report1(a, 1); }
-        flag1(ctl + C_HR, ok ? 1u : 2u);
-    } else if (wave == 1) {
-        const bool ok = stage_h1(a, a.th + (size_t) 8 * H1 + (size_t) xcd * QK, lds + M_HS);
-        if (!ok) { report1(a, 1); }
-        flag1(ctl + C_HS, ok ? 1u : 2u);
+    if constexpr (FD == 0) {
+        const uint8_t * dmat = uniform1(a.down + (size_t) e_dn * a.estride);
+        auto unit = [&](int u, const uint8_t * & mat, int & g64, int & blk, int & slot) {
+            if (u < RGQ1) { mat = dmat; g64 = qq * RGQ1 + u; blk = kb; slot = xcd; }
+            else { mat = uniform1(a.sh_down); g64 = li + 32 * (u - RGQ1); blk = xcd; slot = 8; }
+        };
+        // the waves claim units from an LDS counter, one in flight per wave (as the gate/up items)
+        auto claim_unit = [&](Dn1 & d, int & u) {
+            unsigned c = 0;
+            if (lane == 0) { c = __hip_atomic_fetch_add(dclaim, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+            u = (int) __builtin_amdgcn_readfirstlane(c);
+            if (u < nunits) { const uint8_t * m; int g, b, sl; unit(u, m, g, b, sl); dn1_issue(m, g, b, d); }
+        };
+        Dn1 dn; int un;
+        claim_unit(dn, un);
+        if (!stage_both()) { return; }
+        auto run_unit = [&](const Dn1 & d, int u) {
+            const uint8_t * m; int g, b, sl; unit(u, m, g, b, sl);
+            const uint8_t * hb = (const uint8_t *) (lds + (sl == 8 ? M_HS : M_HR));
+            const int bsum = block_bsum_dpp(d.w, tr, hb, r);
+            const float dx = *reinterpret_cast<const float *>(hb + QK);
+            st_tag1(a.to + ((size_t) sl * NBH1 + b) * E1 + (size_t) g * 64 + lane, a.epoch, (h2f(d.d) * dx) * (float) bsum);
+        };
+        while (un < nunits) { run_unit(dn, un); claim_unit(dn, un); }   // claims rise: the first past the end ends the list
+    } else {
+        // K-quant: the routed units (format FD) first, then the shared expert's (Q6_K), as the claims come
+        constexpr uint32_t RBD = NBH1 * kbytes<FD>(), RB6 = NBH1 * kbytes<KF_Q6K>();
+        auto claim = [&]() -> int {
+            unsigned c = 0;
+            if (lane == 0) { c = __hip_atomic_fetch_add(dclaim, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+            return (int) __builtin_amdgcn_readfirstlane(c);
+        };
+        const uint32_t r8 = (uint32_t) lane >> 3;
+        const Src rsrc = src1(a.down + (size_t) e_dn * a.dstride, (uint64_t) E1 * RBD, r8 * RBD + (uint32_t) kb * kbytes<FD>());
+        const Src ssrc = src1(a.sh_down, (uint64_t) E1 * RB6, r8 * RB6 + (uint32_t) xcd * kbytes<KF_Q6K>());
+        auto g_r = [&](int u) { return qq * RGQ1 + u; };
+        auto g_s = [&](int u) { return li + 32 * (u - RGQ1); };
+        int un = claim();
+        Raw<FD> ra;
+        const bool pre = un < RGQ1;
+        if (pre) { Src s0 = rsrc; s0.so = (uint32_t) g_r(un) * 64 * RBD; load_raw<FD>(s0, lane & 7, ra); }
+        if (!stage_both()) { return; }
+        const LK_LOCAL int8_t * hr = reinterpret_cast<const LK_LOCAL int8_t *>(lds + M_HR);
+        const LK_LOCAL int8_t * hs = reinterpret_cast<const LK_LOCAL int8_t *>(lds + M_HS);
+        un = down_kq1<FD>(a, un, RGQ1, pre, ra, rsrc, hr, *reinterpret_cast<const LK_LOCAL float *>(lds + M_HR + QK), xcd, kb, g_r, claim);
+        Raw<KF_Q6K> rs;
+        (void) down_kq1<KF_Q6K>(a, un, nunits, false, rs, ssrc, hs, *reinterpret_cast<const LK_LOCAL float *>(lds + M_HS + QK), 8, xcd, g_s, claim);
     }
-    TRACE1(7);
-    if (wait1(ctl + C_HR, 1) != 1 || wait1(ctl + C_HS, 1) != 1) { return; }
-    lds_visible();
-    TRACE1(8);
-    auto run_unit = [&](const Dn1 & d, int u) {
-        const uint8_t * m; int g, b, sl; unit(u, m, g, b, sl);
-        const uint8_t * hb = (const uint8_t *) (lds + (sl == 8 ? M_HS : M_HR));
-        const int bsum = block_bsum_dpp(d.w, tr, hb, r);
-        const float dx = *reinterpret_cast<const float *>(hb + QK);
-        st_tag1(a.to + ((size_t) sl * NBH1 + b) * E1 + (size_t) g * 64 + lane, a.epoch, (h2f(d.d) * dx) * (float) bsum);
-    };
-    while (un < nunits) { run_unit(dn, un); claim_unit(dn, un); }   // claims rise: the first past the end ends the list
     TRACE1(9);
 
     // 5. combine rows 28 b .. 28 b + 27 (a timed-out poll is flagged in LDS; no __syncthreads_and: it would take static
     //    LDS and move the table base off its 64 KB alignment)
-    combine1(a, lds);
+    combine1<FD != 0>(a, lds);
     if (wave == 0 && __hip_atomic_load(ctl + C_CMBFAIL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) { report1(a, 16); }
     TRACE1(10);
     if (blockIdx.x == 0 && wave == W1 - 1) { routing1(a, lds); }
@@ -652,15 +841,20 @@ size_t decode1_lds_bytes() { return DEC1_LDS; }
 __device__ int g_xcc1[G1];
 __global__ void k_xcc_probe1() { if (threadIdx.x == 0) { g_xcc1[blockIdx.x] = xcc_id1(); } }
 
+// the kernel's variants: every matrix IQ2_XXS; routed down Q2_K or Q3_K with the shared expert in Q5_K / Q5_K / Q6_K
+static const void * const kernels1[3] = { (const void *) k_moe_decode1<0>, (const void *) k_moe_decode1<KF_Q2K>,
+                                          (const void *) k_moe_decode1<KF_Q3K> };
+
 hipError_t decode1_init(int ncu, int * ok) {
     *ok = 0;
     if (ncu != G1) { return hipSuccess; }   // the XCD mapping needs one workgroup on each of 256 CUs
-    hipError_t e = hipFuncSetAttribute((const void *) k_moe_decode1, hipFuncAttributeMaxDynamicSharedMemorySize, DEC1_LDS);
-    if (e != hipSuccess) { return e; }
-    int per = 0;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *) k_moe_decode1, NT1, DEC1_LDS);
-    if (e != hipSuccess) { return e; }
-    if (per < 1) { return hipSuccess; }
+    hipError_t e = hipSuccess;
+    for (const void * k : kernels1) {   // every format variant fits one workgroup per CU
+        if ((e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, DEC1_LDS)) != hipSuccess) { return e; }
+        int per = 0;
+        if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, NT1, DEC1_LDS)) != hipSuccess) { return e; }
+        if (per < 1) { return hipSuccess; }
+    }
     // roles come from the XCD a workgroup runs on, and hand-offs inside an XCD go through its L2: the dispatch must
     // place workgroup b on XCD (r + b) % 8 for one r
     hipLaunchKernelGGL(k_xcc_probe1, dim3(G1), dim3(64), 0, 0);
@@ -674,16 +868,16 @@ hipError_t decode1_init(int ncu, int * ok) {
 
 hipError_t launch_moe_decode1(const DecodeArgs & a, bool cooperative, hipStream_t st) {
     if (a.n != 1 || a.topk != MAXK || a.keep != MAXK || !decode_rule_ok(a.n_exp, a.n_group) || a.E != E1 || a.H != H1 ||
-        !a.th || !a.to || !a.tlogits || a.n_exp > NEXP_MAX) {
-        return hipErrorInvalidValue;
+        !a.th || !a.to || !a.tlogits || a.n_exp > NEXP_MAX || (a.kdown != 0 && a.kdown != KF_Q2K && a.kdown != KF_Q3K) ||
+        (a.kdown != 0 && ((reinterpret_cast<uintptr_t>(a.down) | reinterpret_cast<uintptr_t>(a.sh_gate) |
+                           reinterpret_cast<uintptr_t>(a.sh_up) | reinterpret_cast<uintptr_t>(a.sh_down) | a.dstride) & 3u))) {
+        return hipErrorInvalidValue;   // K-quant matrices: 4-byte aligned (the slices' word loads)
     }
-    if (!cooperative) {
-        k_moe_decode1<<<G1, NT1, DEC1_LDS, st>>>(a);
-        return hipGetLastError();
-    }
+    const void * k = kernels1[a.kdown == 0 ? 0 : a.kdown == KF_Q2K ? 1 : 2];
     DecodeArgs arg = a;
     void * params[] = { &arg };
-    return hipLaunchCooperativeKernel((const void *) k_moe_decode1, dim3(G1), dim3(NT1), params, DEC1_LDS, st);
+    if (!cooperative) { return hipLaunchKernel(k, dim3(G1), dim3(NT1), params, DEC1_LDS, st); }
+    return hipLaunchCooperativeKernel(k, dim3(G1), dim3(NT1), params, DEC1_LDS, st);
 }
 
 }  // namespace lk

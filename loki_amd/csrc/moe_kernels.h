@@ -57,6 +57,10 @@ struct DecodeArgs {
     int keep; float renorm;                          // experts kept per token (keep <= topk; the slots use keep), rescale
     const uint8_t * gate, * up, * down; size_t estride;   // routed experts (tiled), expert e at + e * estride
     const uint8_t * sh_gate, * sh_up, * sh_down;
+    // 0: every matrix IQ2_XXS (tiled). KF_Q2K / KF_Q3K (kquant_device.h; the one-token kernel only): the routed down
+    // in that K-quant and the shared expert in Q5_K / Q5_K / Q6_K, ggml's block layout read in place, routed down
+    // expert e at down + e * dstride
+    int kdown; size_t dstride;
     int E, H;                                        // 7168, 2048 (the kernel's geometry)
     int8_t * xq; float * xd;                         // Q8_K of x (written by workgroup 0)
     float * logits, * probs; int * sel; float * wts; int * counts, * offsets, * perm, * inv, * act, * nact;

@@ -245,3 +245,72 @@ def test_shared_formats_rejects(ctx):
     assert lib().fl_set_shared_formats(ctx.ctx, 3, 4, 1) == FL_EINVAL   # gate K-quant, up IQ2_XXS
     assert lib().fl_set_shared_formats(ctx.ctx, 0, 0, 1) == FL_EINVAL   # Q4_K is not supported
     ctx.set_shared_formats()
+
+
+# (block bytes, offset of d, offset of dmin) of the ggml K-quant blocks
+KQ_BLOCK = {orc.Q2K: (84, 80, 82), orc.Q3K: (110, 108, None), orc.Q5K: (176, 0, 2), orc.Q6K: (210, 208, None)}
+
+
+def _kq_device(torch, fmt, R, K, seed):
+    """random K-quant matrix bytes on the device: uniform quant and scale bytes, fp16 d (and dmin) in [6e-5, 4e-3]"""
+    bs, od, om = KQ_BLOCK[fmt]
+    nb = R * (K // 256)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    blk = torch.randint(0, 256, (nb, bs), dtype=torch.uint8, device="cuda", generator=g)
+    for off in (od, om):
+        if off is not None:
+            d = torch.randint(0x0C00, 0x1C00, (nb,), dtype=torch.int32, device="cuda", generator=g).to(torch.int16)
+            blk[:, off:off + 2] = d.view(torch.uint8).view(nb, 2)
+    return blk.view(-1)
+
+
+@pytest.mark.parametrize("down_fmt", [orc.Q2K, orc.Q3K], ids=["q2_K", "q3_K"])
+def test_decode1_real_formats(ctx, down_fmt):
+    """One decode token on the real shards' formats (routed gate/up IQ2_XXS tiled; routed down Q2_K / Q3_K and the
+    shared expert Q5_K / Q5_K / Q6_K read in place) through the one-token kernel: y, picks and weights bit-identical to
+    the per-pass kernels for tokens in a row, also under fl_moe_layer_normed with the residual; y against the checker
+    within the K-quant bar. A 64-expert layer (the kernel's workgroups past the experts still run their shares)."""
+    import torch
+    from loki_amd import MoeLayerWeights
+    from tests._helpers import make_x, host_matrix
+    ne = 64
+    base = MoeLayerWeights.synthetic(ctx, 8080 + down_fmt, n_exp=ne)
+    down = _kq_device(torch, down_fmt, ne * E, H, 8090 + down_fmt)
+    sh = (_kq_device(torch, orc.Q5K, H, E, 8091), _kq_device(torch, orc.Q5K, H, E, 8092), _kq_device(torch, orc.Q6K, E, H, 8093))
+    layer = MoeLayerWeights(base.gate_inp, base.probs_b, base.gate, base.up, down, *sh, n_exp=ne)
+    fm = (down_fmt, orc.Q5K, orc.Q5K, orc.Q6K)
+    W, b = layer.gate_inp.cpu().numpy(), layer.probs_b.cpu().numpy()
+    mb = E * (H // 256) * KQ_BLOCK[down_fmt][0]
+    ctx.set_layer_formats(*fm)
+    try:
+        for i in range(3):
+            x = make_x(ctx, 1, seed=8100 + i)
+            print("decode-1 real formats: down %s token %d" % (NAMES[down_fmt], i), flush=True)
+            got = {}
+            for name, m in (("decode1", 2), ("per_pass", 0)):
+                with ctx.using_fused(m):
+                    y = ctx.moe_layer(layer, x).clone()
+                    ctx.sync()
+                    dbg = ctx.debug()
+                    assert dbg.kernel == {"decode1": 2, "per_pass": 0}[name], (name, dbg.kernel)
+                    got[name] = (ctx.d2h(dbg.sel, (KE,), np.int32), ctx.d2h(dbg.wts, (KE,), np.float32), y.cpu().numpy())
+                    if i == 0:
+                        got[name] += (ctx.moe_layer_normed(layer, x * 3.0, None, 1e-6, residual=True).cpu().numpy(),)
+                        ctx.sync()
+                        assert ctx.debug().kernel == {"decode1": 2, "per_pass": 0}[name]
+            for k in range(len(got["per_pass"])):
+                assert np.array_equal(got["decode1"][k].view(np.uint8), got["per_pass"][k].view(np.uint8)), (i, k)
+            xs = x.cpu().numpy()
+            _, _, so, wo = orc.router(W, b, xs)
+            assert np.array_equal(got["decode1"][0], so.ravel().astype(np.int32))
+            sel = sorted(set(int(e) for e in so.ravel()))
+            gate = {e: host_matrix(ctx, layer.expert_slice("gate", e), H, E) for e in sel}
+            up = {e: host_matrix(ctx, layer.expert_slice("up", e), H, E) for e in sel}
+            dn = {e: down[e * mb:(e + 1) * mb].cpu().numpy() for e in sel}
+            ref = orc.moe_experts(xs, so, wo, gate, up, dn, *(m.cpu().numpy() for m in sh), n_exp=ne, fmts=fm)["y"]
+            ok, err = bar_close(got["decode1"][2], ref)
+            assert ok, (i, err)
+    finally:
+        ctx.set_layer_formats()
+    del layer, base, down, sh
+    torch.cuda.empty_cache()
