@@ -411,11 +411,11 @@ __device__ __forceinline__ bool shared_gu1_kq(const D1Args & a, lds1_t lds, int 
     LK_LOCAL float * tm = ts + 2 * 8 * NBX1;
     const LK_LOCAL int8_t * xs = reinterpret_cast<const LK_LOCAL int8_t *>(lds + M_X);
     const LK_LOCAL float * dx = reinterpret_cast<const LK_LOCAL float *>(lds + M_X + NBX1 * GX1::XBLK);
-    Src sm[2] = { src1(a.sh_gate, (uint64_t) H1 * QR5, (uint32_t) r8 * QR5), src1(a.sh_up, (uint64_t) H1 * QR5, (uint32_t) r8 * QR5) };
-    sm[0].so = sm[1].so = (uint32_t) hrow0 * QR5;
+    // the resource is formed per pass from the wave-uniform matrix pointer (scalar registers; a resource picked from
+    // an array would be taken as per-lane and every load would loop over its lanes' resources)
     auto issue = [&](int p, Raw<KF_Q5K> & r) {
-        Src s = sm[p & 1];
-        s.vb += (uint32_t) (p >> 1) * kbytes<KF_Q5K>();
+        Src s = src1((p & 1) ? a.sh_up : a.sh_gate, (uint64_t) H1 * QR5, (uint32_t) r8 * QR5 + (uint32_t) (p >> 1) * kbytes<KF_Q5K>());
+        s.so = (uint32_t) hrow0 * QR5;
         load_raw<KF_Q5K>(s, c, r);
     };
     auto run = [&](const Raw<KF_Q5K> & r, int p) {
@@ -760,24 +760,24 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
     const int nunits = RGQ1 + nsh;
     const int e_dn = reinterpret_cast<const LK_LOCAL int *>(lds + M_SEL)[xcd];
     LK_LOCAL unsigned * dclaim = ctl + C_DNCLAIM;
-    // waves 0 and 1 poll and stage the routed and the shared h block; every wave then waits for both
-    auto stage_both = [&]() -> bool {
-        if (wave == 0) {
-            const bool ok = stage_h1(a, a.th + (size_t) xcd * H1 + (size_t) kb * QK, lds + M_HR);
-            if (!ok) { report1(a, 1); }
-            flag1(ctl + C_HR, ok ? 1u : 2u);
-        } else if (wave == 1) {
-            const bool ok = stage_h1(a, a.th + (size_t) 8 * H1 + (size_t) xcd * QK, lds + M_HS);
-            if (!ok) { report1(a, 1); }
-            flag1(ctl + C_HS, ok ? 1u : 2u);
-        }
-        TRACE1(7);
-        if (wait1(ctl + C_HR, 1) != 1 || wait1(ctl + C_HS, 1) != 1) { return false; }
-        lds_visible();
-        TRACE1(8);
-        return true;
-    };
     if constexpr (FD == 0) {
+        // waves 0 and 1 poll and stage the routed and the shared h block; every wave then waits for both
+        auto stage_both = [&]() -> bool {
+            if (wave == 0) {
+                const bool ok = stage_h1(a, a.th + (size_t) xcd * H1 + (size_t) kb * QK, lds + M_HR);
+                if (!ok) { report1(a, 1); }
+                flag1(ctl + C_HR, ok ? 1u : 2u);
+            } else if (wave == 1) {
+                const bool ok = stage_h1(a, a.th + (size_t) 8 * H1 + (size_t) xcd * QK, lds + M_HS);
+                if (!ok) { report1(a, 1); }
+                flag1(ctl + C_HS, ok ? 1u : 2u);
+            }
+            TRACE1(7);
+            if (wait1(ctl + C_HR, 1) != 1 || wait1(ctl + C_HS, 1) != 1) { return false; }
+            lds_visible();
+            TRACE1(8);
+            return true;
+        };
         const uint8_t * dmat = uniform1(a.down + (size_t) e_dn * a.estride);
         auto unit = [&](int u, const uint8_t * & mat, int & g64, int & blk, int & slot) {
             if (u < RGQ1) { mat = dmat; g64 = qq * RGQ1 + u; blk = kb; slot = xcd; }
@@ -802,7 +802,9 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
         };
         while (un < nunits) { run_unit(dn, un); claim_unit(dn, un); }   // claims rise: the first past the end ends the list
     } else {
-        // K-quant: the routed units (format FD) first, then the shared expert's (Q6_K), as the claims come
+        // K-quant: the shared expert's units (Q6_K) first -- its h block is complete long before the routed one, so
+        // waves that finish their gate/up items early run them while the routed h block is still being formed -- then
+        // the routed units (format FD); each stream waits only for its own h block
         constexpr uint32_t RBD = NBH1 * kbytes<FD>(), RB6 = NBH1 * kbytes<KF_Q6K>();
         auto claim = [&]() -> int {
             unsigned c = 0;
@@ -810,20 +812,34 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
             return (int) __builtin_amdgcn_readfirstlane(c);
         };
         const uint32_t r8 = (uint32_t) lane >> 3;
-        const Src rsrc = src1(a.down + (size_t) e_dn * a.dstride, (uint64_t) E1 * RBD, r8 * RBD + (uint32_t) kb * kbytes<FD>());
         const Src ssrc = src1(a.sh_down, (uint64_t) E1 * RB6, r8 * RB6 + (uint32_t) xcd * kbytes<KF_Q6K>());
-        auto g_r = [&](int u) { return qq * RGQ1 + u; };
-        auto g_s = [&](int u) { return li + 32 * (u - RGQ1); };
+        const Src rsrc = src1(a.down + (size_t) e_dn * a.dstride, (uint64_t) E1 * RBD, r8 * RBD + (uint32_t) kb * kbytes<FD>());
+        auto g_s = [&](int u) { return li + 32 * u; };              // units 0 .. nsh - 1
+        auto g_r = [&](int u) { return qq * RGQ1 + (u - nsh); };    // units nsh .. nunits - 1
         int un = claim();
-        Raw<FD> ra;
-        const bool pre = un < RGQ1;
-        if (pre) { Src s0 = rsrc; s0.so = (uint32_t) g_r(un) * 64 * RBD; load_raw<FD>(s0, lane & 7, ra); }
-        if (!stage_both()) { return; }
-        const LK_LOCAL int8_t * hr = reinterpret_cast<const LK_LOCAL int8_t *>(lds + M_HR);
-        const LK_LOCAL int8_t * hs = reinterpret_cast<const LK_LOCAL int8_t *>(lds + M_HS);
-        un = down_kq1<FD>(a, un, RGQ1, pre, ra, rsrc, hr, *reinterpret_cast<const LK_LOCAL float *>(lds + M_HR + QK), xcd, kb, g_r, claim);
         Raw<KF_Q6K> rs;
-        (void) down_kq1<KF_Q6K>(a, un, nunits, false, rs, ssrc, hs, *reinterpret_cast<const LK_LOCAL float *>(lds + M_HS + QK), 8, xcd, g_s, claim);
+        const bool pre = un < nsh;
+        if (pre) { Src s0 = ssrc; s0.so = (uint32_t) g_s(un) * 64 * RB6; load_raw<KF_Q6K>(s0, lane & 7, rs); }
+        if (wave == 0) {
+            const bool ok = stage_h1(a, a.th + (size_t) xcd * H1 + (size_t) kb * QK, lds + M_HR);
+            if (!ok) { report1(a, 1); }
+            flag1(ctl + C_HR, ok ? 1u : 2u);
+        } else if (wave == 1) {
+            const bool ok = stage_h1(a, a.th + (size_t) 8 * H1 + (size_t) xcd * QK, lds + M_HS);
+            if (!ok) { report1(a, 1); }
+            flag1(ctl + C_HS, ok ? 1u : 2u);
+        }
+        TRACE1(7);
+        if (wait1(ctl + C_HS, 1) != 1) { return; }
+        lds_visible();
+        un = down_kq1<KF_Q6K>(a, un, nsh, pre, rs, ssrc, reinterpret_cast<const LK_LOCAL int8_t *>(lds + M_HS),
+                              *reinterpret_cast<const LK_LOCAL float *>(lds + M_HS + QK), 8, xcd, g_s, claim);
+        if (wait1(ctl + C_HR, 1) != 1) { return; }
+        lds_visible();
+        TRACE1(8);
+        Raw<FD> ra;
+        (void) down_kq1<FD>(a, un, nunits, false, ra, rsrc, reinterpret_cast<const LK_LOCAL int8_t *>(lds + M_HR),
+                            *reinterpret_cast<const LK_LOCAL float *>(lds + M_HR + QK), xcd, kb, g_r, claim);
     }
     TRACE1(9);
 
