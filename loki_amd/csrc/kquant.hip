@@ -79,7 +79,9 @@ __global__ void __launch_bounds__(64 * KQ_WAVES) k_kq_matvec(KqArgs a) {
                 x.d8 = a.ad[(size_t) (sg + t) * nb + b];
             } else {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) { x.x[i] = 0u; x.bx[i] = 0; }
+                for (int i = 0; i < 8; ++i) { x.x[i] = 0u; }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) { x.c0[i] = 0; x.bx[i] = 0; }
                 x.d8 = 0.f;
             }
         }

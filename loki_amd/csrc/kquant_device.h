@@ -87,13 +87,17 @@ template <int F> __device__ __forceinline__ void load_raw(const Src & b, int q, 
     }
 }
 
-// decoded slice: u = unsigned quants (4 per word); piece p's scale sc[p] and min mn[p] (pieces: 4 of 2 words for the
-// 16-weight formats, 2 of 4 words for Q5_K)
+// decoded slice: u = unsigned quants (4 per word, an offset quant with its offset still added); piece p's scale sc[p]
+// and min mn[p] (pieces: 4 of 2 words for the 16-weight formats, 2 of 4 words for Q5_K)
 struct Chunk {
     uint32_t u[8];
-    int sc[8], mn[8];
+    int sc[4], mn[4];
     float d, dmin;
 };
+
+// rotate right: bit b of the result is bit (b + n) % 32 of w. Moves a bit plane of every byte to another position in
+// one instruction (no bit of another byte lands on the kept position: each caller masks one plane per byte).
+__device__ __forceinline__ uint32_t rotr(uint32_t w, uint32_t n) { return __builtin_amdgcn_alignbit(w, w, n & 31u); }
 
 template <int F> __device__ __forceinline__ void decode(const Raw<F> & r, int q, Chunk & k) {
     const int n = q >> 2, jq = q & 3, hi16 = jq >> 1;   // hi16: the columns sit in the second 16 of each 32-weight row
@@ -101,28 +105,29 @@ template <int F> __device__ __forceinline__ void decode(const Raw<F> & r, int q,
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             k.u[2 * s] = (r.q[0] >> (2 * s)) & 0x03030303u; k.u[2 * s + 1] = (r.q[1] >> (2 * s)) & 0x03030303u;
-            const uint32_t b = (r.sc[s >> 1] >> (8 * (2 * (s & 1) + hi16))) & 0xFFu;
-            k.sc[s] = (int) (b & 15u); k.mn[s] = (int) (b >> 4);
+            const uint32_t o = 8u * (2 * (s & 1) + hi16);   // the sub-block's byte: scale nibble, min nibble
+            k.sc[s] = (int) __builtin_amdgcn_ubfe(r.sc[s >> 1], o, 4u); k.mn[s] = (int) __builtin_amdgcn_ubfe(r.sc[s >> 1], o + 4u, 4u);
         }
         k.d = h2f((uint16_t) (r.dd & 0xFFFFu)); k.dmin = h2f((uint16_t) (r.dd >> 16));
-    } else if constexpr (F == KF_Q3K) {   // high bit (hmask[l] bit 4 n + s) clear -> quant - 4 (applied as -4 * bsum)
+    } else if constexpr (F == KF_Q3K) {   // high bit (hmask[l] bit 4 n + s) clear -> quant - 4 (the -4 is in the dot's start)
         const uint32_t q0 = realign<2>(r.q, r.shq, 0), q1 = realign<2>(r.q, r.shq, 1);
         const uint32_t h0 = realign<2>(r.h, r.shh, 0), h1 = realign<2>(r.h, r.shh, 1);
         const uint32_t a0 = realign<3>(r.s, r.shs, 0), a1 = realign<3>(r.s, r.shs, 1), a2 = realign<3>(r.s, r.shs, 2);
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            const int hb = 4 * n + s;
-            k.u[2 * s] = ((q0 >> (2 * s)) & 0x03030303u) | (((h0 >> hb) & 0x01010101u) << 2);
-            k.u[2 * s + 1] = ((q1 >> (2 * s)) & 0x03030303u) | (((h1 >> hb) & 0x01010101u) << 2);
+            const uint32_t hr = (uint32_t) (4 * n + s) - 2u;   // hmask bit 4 n + s of each byte -> bit 2
+            k.u[2 * s] = ((q0 >> (2 * s)) & 0x03030303u) | (rotr(h0, hr) & 0x04040404u);
+            k.u[2 * s + 1] = ((q1 >> (2 * s)) & 0x03030303u) | (rotr(h1, hr) & 0x04040404u);
         }
         // 6-bit scale j = 8 n + 2 s + hi16: low nibble of byte j % 8 (nibble n), 2 high bits of byte 8 + j % 4 at
         // bits 2 (j / 4). The lane's four scales sit in bytes hi16 and hi16 + 2: s = 0, 1 in a0 / a2, s = 2, 3 in a1 /
-        // a2 >> 2, so one shift per word puts each pair at bits 0 and 16.
+        // a2 >> 2, so one shift per word puts each pair at bits 0 and 16 (the high bits by a rotate to bits 4, 5);
+        // scale - 32 is the 6-bit field with its top bit flipped, read signed
         const uint32_t sh = 8 * hi16 + 4 * n;
-        const uint32_t p01 = ((a0 >> sh) & 0x000F000Fu) | (((a2 >> sh) & 0x00030003u) << 4);
-        const uint32_t p23 = ((a1 >> sh) & 0x000F000Fu) | (((a2 >> (sh + 2)) & 0x00030003u) << 4);
-        k.sc[0] = (int) (p01 & 0xFFu) - 32; k.sc[1] = (int) (p01 >> 16) - 32;
-        k.sc[2] = (int) (p23 & 0xFFu) - 32; k.sc[3] = (int) (p23 >> 16) - 32;
+        const uint32_t p01 = (((a0 >> sh) & 0x000F000Fu) | (rotr(a2, sh - 4u) & 0x00300030u)) ^ 0x00200020u;
+        const uint32_t p23 = (((a1 >> sh) & 0x000F000Fu) | (rotr(a2, sh - 2u) & 0x00300030u)) ^ 0x00200020u;
+        k.sc[0] = __builtin_amdgcn_sbfe((int) p01, 0u, 6u); k.sc[1] = __builtin_amdgcn_sbfe((int) p01, 16u, 6u);
+        k.sc[2] = __builtin_amdgcn_sbfe((int) p23, 0u, 6u); k.sc[3] = __builtin_amdgcn_sbfe((int) p23, 16u, 6u);
         k.mn[0] = k.mn[1] = k.mn[2] = k.mn[3] = 0;
         k.d = h2f((uint16_t) r.dd); k.dmin = 0.f;
     } else if constexpr (F == KF_Q5K) {   // weight 64 jj + 32 h + l: nibble h of qs[32 jj + l], bit 2 jj + h of qh[l]
@@ -131,7 +136,7 @@ template <int F> __device__ __forceinline__ void decode(const Raw<F> & r, int q,
         for (int h = 0; h < 2; ++h) {
             const int j = 2 * jj + h;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) { k.u[4 * h + i] = ((r.q[i] >> (4 * h)) & 0x0F0F0F0Fu) | (((r.h[i] >> j) & 0x01010101u) << 4); }
+            for (int i = 0; i < 4; ++i) { k.u[4 * h + i] = ((r.q[i] >> (4 * h)) & 0x0F0F0F0Fu) | (rotr(r.h[i], (uint32_t) j - 4u) & 0x10101010u); }
             int sv, mv;
             if (j < 4) { sv = (int) (byte_of3(r.s[0], r.s[1], r.s[2], j) & 63u); mv = (int) (byte_of3(r.s[0], r.s[1], r.s[2], j + 4) & 63u); }
             else {
@@ -141,6 +146,7 @@ template <int F> __device__ __forceinline__ void decode(const Raw<F> & r, int q,
             }
             k.sc[h] = sv; k.mn[h] = mv;
         }
+        k.sc[2] = k.sc[3] = k.mn[2] = k.mn[3] = 0;
         k.d = h2f((uint16_t) (r.dd & 0xFFFFu)); k.dmin = h2f((uint16_t) (r.dd >> 16));
     } else {   // Q6_K: weight 128 n + 32 p + l: nibble p / 2 of ql[64 n + 32 (p % 2) + l], bits 2 p of qh[32 n + l], - 32
         const uint32_t a0 = realign<2>(r.qa, r.sha, 0), a1 = realign<2>(r.qa, r.sha, 1);
@@ -150,17 +156,20 @@ template <int F> __device__ __forceinline__ void decode(const Raw<F> & r, int q,
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             const uint32_t l0 = (p & 1) ? b0 : a0, l1 = (p & 1) ? b1 : a1;
-            k.u[2 * p] = ((l0 >> (4 * (p >> 1))) & 0x0F0F0F0Fu) | (((h0 >> (2 * p)) & 0x03030303u) << 4);
-            k.u[2 * p + 1] = ((l1 >> (4 * (p >> 1))) & 0x0F0F0F0Fu) | (((h1 >> (2 * p)) & 0x03030303u) << 4);
-            const int j = 2 * p + hi16;   // scales[8 n + j]
-            k.sc[p] = (int) (int8_t) (((j < 4 ? s0 : s1) >> (8 * (j & 3))) & 0xFFu); k.mn[p] = 0;
+            const uint32_t hr = (uint32_t) (2 * p) - 4u;   // qh bits 2 p, 2 p + 1 of each byte -> bits 4, 5
+            k.u[2 * p] = ((l0 >> (4 * (p >> 1))) & 0x0F0F0F0Fu) | (rotr(h0, hr) & 0x30303030u);
+            k.u[2 * p + 1] = ((l1 >> (4 * (p >> 1))) & 0x0F0F0F0Fu) | (rotr(h1, hr) & 0x30303030u);
+            // scales[8 n + j], j = 2 p + hi16: byte j % 4 of s0 (j < 4) or s1, signed
+            k.sc[p] = __builtin_amdgcn_sbfe((int) (p < 2 ? s0 : s1), 16u * (p & 1) + 8u * hi16, 8u); k.mn[p] = 0;
         }
         k.d = h2f((uint16_t) r.dd); k.dmin = 0.f;
     }
 }
 
-// the lane's activation words (same weight order as u) and per-piece sums of the Q8_K integers
-struct XChunk { uint32_t x[8]; int bx[8]; float d8; };
+// the lane's activation words (same weight order as u), per piece the start value of its dot accumulator (the
+// quants' offset folded in: Q3_K -4 * bsum, Q6_K -32 * bsum, else 0) and the sum of its Q8_K integers (bsum: the
+// min term of Q2_K / Q5_K)
+struct XChunk { uint32_t x[8]; int c0[4], bx[4]; float d8; };
 
 // 8- and 16-byte activation reads from global memory or LDS
 __device__ __forceinline__ uint4 kx16(const int8_t * p) { return *reinterpret_cast<const uint4 *>(p); }
@@ -170,6 +179,10 @@ __device__ __forceinline__ uint4 kx16(const LK_LOCAL int8_t * p) {
 }
 __device__ __forceinline__ uint2 kx8(const LK_LOCAL int8_t * p) {
     const u32x2 v = *reinterpret_cast<const LK_LOCAL u32x2 *>(p); return make_uint2(v.x, v.y);
+}
+template <int F> __device__ __forceinline__ void x_starts(XChunk & x) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) { x.c0[s] = F == KF_Q3K ? -4 * x.bx[s] : F == KF_Q6K ? -32 * x.bx[s] : 0; }
 }
 
 // xb: the block's 256 Q8_K integers in element order (global memory or LDS)
@@ -186,8 +199,7 @@ template <int F, class P> __device__ __forceinline__ void load_x(P xb, int q, XC
             for (int i = 0; i < 4; ++i) { sm = __builtin_amdgcn_sdot4((int) x.x[4 * h + i], (int) ones, sm, false); }
             x.bx[h] = sm;
         }
-#pragma unroll
-        for (int h = 2; h < 8; ++h) { x.bx[h] = 0; }
+        x.bx[2] = x.bx[3] = 0;
     } else {
         const int n = q >> 2, jq = q & 3;
 #pragma unroll
@@ -195,9 +207,9 @@ template <int F, class P> __device__ __forceinline__ void load_x(P xb, int q, XC
             const uint2 v = kx8(xb + 128 * n + 32 * s + 8 * jq);
             x.x[2 * s] = v.x; x.x[2 * s + 1] = v.y;
             x.bx[s] = __builtin_amdgcn_sdot4((int) v.y, (int) ones, __builtin_amdgcn_sdot4((int) v.x, (int) ones, 0, false), false);
-            x.bx[4 + s] = 0;
         }
     }
+    x_starts<F>(x);
 }
 
 // integer partials of the slice against one token: isum (scaled, offsets removed), summ (min term). Every factor fits
@@ -217,10 +229,9 @@ template <int F> __device__ __forceinline__ void chunk_dot(const Chunk & k, cons
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const int dp = __builtin_amdgcn_sdot4((int) k.u[2 * s + 1], (int) x.x[2 * s + 1],
-                                                  __builtin_amdgcn_sdot4((int) k.u[2 * s], (int) x.x[2 * s], 0, false), false);
-            if constexpr (F == KF_Q2K) { isum += __mul24(k.sc[s], dp); summ += __mul24(k.mn[s], x.bx[s]); }
-            else if constexpr (F == KF_Q3K) { isum += __mul24(k.sc[s], dp - 4 * x.bx[s]); }
-            else { isum += __mul24(k.sc[s], dp - 32 * x.bx[s]); }
+                                                  __builtin_amdgcn_sdot4((int) k.u[2 * s], (int) x.x[2 * s], x.c0[s], false), false);
+            isum += __mul24(k.sc[s], dp);
+            if constexpr (F == KF_Q2K) { summ += __mul24(k.mn[s], x.bx[s]); }
         }
     }
 }

@@ -72,7 +72,7 @@ constexpr int M_NRM = M_CTL + NCTL1 * 4;           // RMSNorm scale
 constexpr int DEC1_LDS = M_NRM + 16;
 static_assert(DEC1_LDS <= 160 * 1024 && (M_X % 16) == 0 && (M_HR % 16) == 0 && (M_HS % 16) == 0, "LDS layout");
 enum { C_RT = 0, C_STAGED = 1, C_SH = 2, C_READY = 3, C_HR = 4, C_HS = 5, C_CMBFAIL = 6, C_NRM = 7, C_RISSUED = 8,
-       C_GUCLAIM = 9, C_DNCLAIM = 10, C_GUDONE = 11, C_SB1 = 12, C_SELFAIL = 13 };
+       C_GUCLAIM = 9, C_DNCLAIM = 10, C_GUDONE = 11, C_SB1 = 12, C_SELFAIL = 13, C_SHCLAIM = 14 };
 
 typedef LK_LOCAL uint8_t * lds1_t;
 typedef LK_CONST DecodeArgs D1Args;
@@ -362,8 +362,7 @@ template <int F> __device__ __forceinline__ void load_x_st(const LK_LOCAL int8_t
             for (int i = 0; i < 4; ++i) { sm = __builtin_amdgcn_sdot4((int) x.x[4 * h + i], ones, sm, false); }
             x.bx[h] = sm;
         }
-#pragma unroll
-        for (int h = 2; h < 8; ++h) { x.bx[h] = 0; }
+        x.bx[2] = x.bx[3] = 0;
     } else {
         const int n = q >> 2, jq = q & 3;
 #pragma unroll
@@ -371,9 +370,9 @@ template <int F> __device__ __forceinline__ void load_x_st(const LK_LOCAL int8_t
             const uint2 v = kx8(xb + staged8(128 * n + 32 * s + 8 * jq));
             x.x[2 * s] = v.x; x.x[2 * s + 1] = v.y;
             x.bx[s] = __builtin_amdgcn_sdot4((int) v.y, ones, __builtin_amdgcn_sdot4((int) v.x, ones, 0, false), false);
-            x.bx[4 + s] = 0;
         }
     }
+    x_starts<F>(x);
 }
 // a buffer resource over a matrix of `bytes` (wave-uniform base); lane offsets in vb, the row offset in so
 __device__ __forceinline__ Src src1(const uint8_t * mat, uint64_t bytes, uint32_t vb) {
@@ -400,23 +399,32 @@ template <int F> __device__ __forceinline__ float kq_term1(const Raw<F> & raw, c
 }
 
 // The shared expert's gate/up task in Q5_K (h rows 8 t .. 8 t + 7, t = 32 x + i): 56 passes (matrix, block), each 8
-// rows (lane = row r8, slice c), spread over the staging waves (pass p on wave 4 + p % 12). Block terms to LDS; the
-// wave that completes the 56th pass folds each row's terms in block order (the K-quant mat-vec's order: acc += t,
-// accm -= t_min, acc_m + acc) and publishes h = silu(g) * u.
+// rows (lane = row r8, slice c), claimed from an LDS counter by the waves free before the picks arrive, each keeping
+// DS1 passes' bytes in flight. Block terms to LDS; the wave that completes the 56th pass folds each row's terms in block
+// order (the K-quant mat-vec's order: acc += t, accm -= t_min, acc_m + acc) and publishes h = silu(g) * u.
 constexpr int QR5 = NBX1 * kbytes<KF_Q5K>();   // Q5_K row bytes at K = 7168
-__device__ __forceinline__ bool shared_gu1_kq(const D1Args & a, lds1_t lds, int wave, int xcd, int li, LK_LOCAL unsigned * ctl) {
+constexpr int DS1 = 3;
+__device__ __forceinline__ bool shared_gu1_kq(const D1Args & a, lds1_t lds, int xcd, int li, LK_LOCAL unsigned * ctl) {
 #pragma clang fp contract(off)
     const int lane = lane_id(), r8 = lane >> 3, c = lane & 7, hrow0 = (xcd * 32 + li) * 8;
     LK_LOCAL float * ts = reinterpret_cast<LK_LOCAL float *>(lds + M_PRE);   // [matrix][row][block]
     LK_LOCAL float * tm = ts + 2 * 8 * NBX1;
     const LK_LOCAL int8_t * xs = reinterpret_cast<const LK_LOCAL int8_t *>(lds + M_X);
     const LK_LOCAL float * dx = reinterpret_cast<const LK_LOCAL float *>(lds + M_X + NBX1 * GX1::XBLK);
+    Raw<KF_Q5K> rg[DS1];
+    int sp[DS1];   // the pass each slot holds (>= 56: empty); claims rise, so the slots hold passes in order
     // the resource is formed per pass from the wave-uniform matrix pointer (scalar registers; a resource picked from
     // an array would be taken as per-lane and every load would loop over its lanes' resources)
-    auto issue = [&](int p, Raw<KF_Q5K> & r) {
-        Src s = src1((p & 1) ? a.sh_up : a.sh_gate, (uint64_t) H1 * QR5, (uint32_t) r8 * QR5 + (uint32_t) (p >> 1) * kbytes<KF_Q5K>());
-        s.so = (uint32_t) hrow0 * QR5;
-        load_raw<KF_Q5K>(s, c, r);
+    auto refill = [&](int k) {
+        unsigned cl = 0;
+        if (lane == 0) { cl = __hip_atomic_fetch_add(ctl + C_SHCLAIM, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+        const int p = (int) __builtin_amdgcn_readfirstlane(cl);
+        sp[k] = p;
+        if (p < SHKP1) {
+            Src s = src1((p & 1) ? a.sh_up : a.sh_gate, (uint64_t) H1 * QR5, (uint32_t) r8 * QR5 + (uint32_t) (p >> 1) * kbytes<KF_Q5K>());
+            s.so = (uint32_t) hrow0 * QR5;
+            load_raw<KF_Q5K>(s, c, rg[k]);
+        }
     };
     auto run = [&](const Raw<KF_Q5K> & r, int p) {
         const int m = p & 1, j = p >> 1;
@@ -438,20 +446,17 @@ __device__ __forceinline__ bool shared_gu1_kq(const D1Args & a, lds1_t lds, int 
             if (lane < 8) { st_xcd1(a.th + (size_t) 8 * H1 + hrow0 + lane, a.epoch, __builtin_bit_cast(uint32_t, det_silu(v) * u)); }
         }
     };
-    const int w = wave - 4;
-    Raw<KF_Q5K> ra, rb;
-    int p = w;
-    if (p < SHKP1) { issue(p, ra); }
-    if (!wait1(ctl + C_STAGED, NQW1)) { report1(a, 8); return false; }
+#pragma unroll
+    for (int k = 0; k < DS1; ++k) { refill(k); }
+    if (!wait1(ctl + C_STAGED, NQW1)) { report1(a, 8); return false; }   // the token's Q8_K
     lds_visible();
-    while (p < SHKP1) {   // the next pass's bytes are in flight while the current one is computed
-        if (p + NQW1 < SHKP1) { issue(p + NQW1, rb); }
-        run(ra, p);
-        p += NQW1;
-        if (p >= SHKP1) { break; }
-        if (p + NQW1 < SHKP1) { issue(p + NQW1, ra); }
-        run(rb, p);
-        p += NQW1;
+    bool more = sp[0] < SHKP1;
+    while (more) {
+#pragma unroll
+        for (int k = 0; k < DS1; ++k) {
+            if (more && sp[k] >= SHKP1) { more = false; }
+            if (more) { run(rg[k], sp[k]); refill(k); }
+        }
     }
     return true;
 }
@@ -545,41 +550,56 @@ __device__ __forceinline__ bool stage_h1(const D1Args & a, const uint64_t * src,
 }
 
 // K-quant down units (one 64-row group at one K-block): 8 passes of 8 rows (lane = row r8, slice c), each row's block
-// term published as a tagged word as the IQ2_XXS units publish theirs. Runs the wave's claimed units below uend
-// (rows g64_of(u) * 64 ..), claiming the next when it starts a unit's last pass so that its first bytes are in flight;
-// returns the first claim at or past uend. `loaded`: ra already holds pass 0 of unit u.
+// term published as a tagged word as the IQ2_XXS units publish theirs. A pass's arithmetic is short against the load
+// latency, so a wave keeps DR1 passes' bytes in flight, in a ring of raw slices refilled as each pass is used. The
+// wave's claimed units below the stream's end run in order; the next unit is claimed when the look-ahead reaches it.
+constexpr int DR1 = 4;
+template <int F> struct DnRing1 {
+    Raw<F> r[DR1];
+    int su[DR1], sp[DR1];   // the (unit, pass) each slot holds; su at or past the end: empty
+    int ul, pl;             // the next pass to issue
+};
 template <int F, class G64, class Claim>
-__device__ __forceinline__ int down_kq1(const D1Args & a, int u, int uend, bool loaded, Raw<F> & ra, const Src & base,
-                                        const LK_LOCAL int8_t * hb, float d8, int slot, int blk, G64 g64_of, Claim claim) {
-#pragma clang fp contract(off)
+__device__ __forceinline__ void dn_issue1(DnRing1<F> & g, int k, int uend, const Src & base, G64 g64_of, Claim claim) {
     constexpr uint32_t RB = NBH1 * kbytes<F>();   // row bytes at K = 2048
+    g.su[k] = g.ul; g.sp[k] = g.pl;
+    if (g.ul < uend) {
+        Src s = base;
+        s.so = (uint32_t) (g64_of(g.ul) * 64 + 8 * g.pl) * RB;
+        load_raw<F>(s, lane_id() & 7, g.r[k]);
+        if (++g.pl == 8) { g.ul = claim(); g.pl = 0; }
+    }
+}
+// fills the ring from unit u (claimed) on
+template <int F, class G64, class Claim>
+__device__ __forceinline__ void dn_prime1(DnRing1<F> & g, int u, int uend, const Src & base, G64 g64_of, Claim claim) {
+    g.ul = u; g.pl = 0;
+#pragma unroll
+    for (int k = 0; k < DR1; ++k) { dn_issue1<F>(g, k, uend, base, g64_of, claim); }
+}
+// runs the ring's passes against the staged h block hb; returns the first claim at or past uend
+template <int F, class G64, class Claim>
+__device__ __forceinline__ int dn_run1(const D1Args & a, DnRing1<F> & g, int uend, const Src & base, const LK_LOCAL int8_t * hb,
+                                       float d8, int slot, int blk, G64 g64_of, Claim claim) {
+#pragma clang fp contract(off)
     const int lane = lane_id(), r8 = lane >> 3, c = lane & 7;
     XChunk xc;
     load_x_st<F>(hb, c, xc);
     xc.d8 = d8;
-    auto issue = [&](int uu, int p, Raw<F> & r) { Src s = base; s.so = (uint32_t) (g64_of(uu) * 64 + 8 * p) * RB; load_raw<F>(s, c, r); };
-    auto step = [&](const Raw<F> & r, int uu, int p) {
-        float tmin;
-        const float t = kq_term1<F>(r, xc, c, tmin);
-        if (c == 0) { st_tag1(a.to + ((size_t) slot * NBH1 + blk) * E1 + (size_t) g64_of(uu) * 64 + 8 * p + r8, a.epoch, t); }
-    };
-    auto next = [&](int & uu, int & p) { if (++p == 8) { uu = claim(); p = 0; } };
-    if (!loaded && u < uend) { issue(u, 0, ra); }
-    Raw<F> rb;
-    int p = 0;
-    while (u < uend) {
-        int un = u, pn = p;
-        next(un, pn);
-        if (un < uend) { issue(un, pn, rb); }
-        step(ra, u, p);
-        u = un; p = pn;
-        if (u >= uend) { break; }
-        next(un, pn);
-        if (un < uend) { issue(un, pn, ra); }
-        step(rb, u, p);
-        u = un; p = pn;
+    bool more = g.su[0] < uend;
+    while (more) {
+#pragma unroll
+        for (int k = 0; k < DR1; ++k) {
+            if (more && g.su[k] >= uend) { more = false; }   // the ring holds consecutive passes: the rest are empty too
+            if (more) {
+                float tmin;
+                const float t = kq_term1<F>(g.r[k], xc, c, tmin);
+                if (c == 0) { st_tag1(a.to + ((size_t) slot * NBH1 + blk) * E1 + (size_t) g64_of(g.su[k]) * 64 + 8 * g.sp[k] + r8, a.epoch, t); }
+                dn_issue1<F>(g, k, uend, base, g64_of, claim);
+            }
+        }
     }
-    return u;
+    return g.ul;
 }
 
 // ---------------------------------------------------------------- 4. combine
@@ -695,6 +715,13 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
         arrive1(ctl + C_STAGED, NQW1);
         TRACE1(1);
     }
+    if (li == 0 && wave >= 4) {
+        // the selecting workgroups keep their CU quiet until the picks are out: the selection is a serial chain of
+        // cross-lane steps on one wave, and work of the other waves beside it (the shared expert's task) slows it by
+        // about half; their shared task runs after the picks, beside the routed gate/up
+        const unsigned rd = wait1(ctl + C_READY, 1);
+        if (rd != 1) { if (rd == 0) { report1(a, 8); } return; }
+    }
     if constexpr (FD == 0) {
         if (wave >= W1 - GU_STEPS1) {   // the shared expert's gate/up task, one step per wave
             if (!wait1(ctl + C_STAGED, NQW1)) { report1(a, 8); return; }
@@ -702,8 +729,10 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
             shared_gu1(a, lds, wave, xcd, li, tr, q, r, ctl);
             TRACE1(2);
         }
-    } else if (wave >= 4) {   // in Q5_K: 56 passes over the staging waves
-        if (!shared_gu1_kq(a, lds, wave, xcd, li, ctl)) { return; }
+    } else if (wave >= (li == 0 ? 4 : 1)) {
+        // in Q5_K: every wave but the one polling the picks (wave 0), after its router part; in the selecting
+        // workgroups not the router waves, which form the probabilities and select
+        if (!shared_gu1_kq(a, lds, xcd, li, ctl)) { return; }
         TRACE1(2);
     }
 
@@ -816,15 +845,16 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
         const Src rsrc = src1(a.down + (size_t) e_dn * a.dstride, (uint64_t) E1 * RBD, r8 * RBD + (uint32_t) kb * kbytes<FD>());
         auto g_s = [&](int u) { return li + 32 * u; };              // units 0 .. nsh - 1
         auto g_r = [&](int u) { return qq * RGQ1 + (u - nsh); };    // units nsh .. nunits - 1
-        int un = claim();
-        Raw<KF_Q6K> rs;
-        const bool pre = un < nsh;
-        if (pre) { Src s0 = ssrc; s0.so = (uint32_t) g_s(un) * 64 * RB6; load_raw<KF_Q6K>(s0, lane & 7, rs); }
+        // wave 0 stages the routed h block first (it polls until the block is complete), the others claim and
+        // prime their rings while the h blocks form
         if (wave == 0) {
             const bool ok = stage_h1(a, a.th + (size_t) xcd * H1 + (size_t) kb * QK, lds + M_HR);
             if (!ok) { report1(a, 1); }
             flag1(ctl + C_HR, ok ? 1u : 2u);
-        } else if (wave == 1) {
+        }
+        DnRing1<KF_Q6K> rs;
+        dn_prime1<KF_Q6K>(rs, claim(), nsh, ssrc, g_s, claim);
+        if (wave == 1) {
             const bool ok = stage_h1(a, a.th + (size_t) 8 * H1 + (size_t) xcd * QK, lds + M_HS);
             if (!ok) { report1(a, 1); }
             flag1(ctl + C_HS, ok ? 1u : 2u);
@@ -832,14 +862,15 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
         TRACE1(7);
         if (wait1(ctl + C_HS, 1) != 1) { return; }
         lds_visible();
-        un = down_kq1<KF_Q6K>(a, un, nsh, pre, rs, ssrc, reinterpret_cast<const LK_LOCAL int8_t *>(lds + M_HS),
-                              *reinterpret_cast<const LK_LOCAL float *>(lds + M_HS + QK), 8, xcd, g_s, claim);
+        const int un = dn_run1<KF_Q6K>(a, rs, nsh, ssrc, reinterpret_cast<const LK_LOCAL int8_t *>(lds + M_HS),
+                                       *reinterpret_cast<const LK_LOCAL float *>(lds + M_HS + QK), 8, xcd, g_s, claim);
+        DnRing1<FD> rr;
+        dn_prime1<FD>(rr, un, nunits, rsrc, g_r, claim);
         if (wait1(ctl + C_HR, 1) != 1) { return; }
         lds_visible();
         TRACE1(8);
-        Raw<FD> ra;
-        (void) down_kq1<FD>(a, un, nunits, false, ra, rsrc, reinterpret_cast<const LK_LOCAL int8_t *>(lds + M_HR),
-                            *reinterpret_cast<const LK_LOCAL float *>(lds + M_HR + QK), xcd, kb, g_r, claim);
+        (void) dn_run1<FD>(a, rr, nunits, rsrc, reinterpret_cast<const LK_LOCAL int8_t *>(lds + M_HR),
+                           *reinterpret_cast<const LK_LOCAL float *>(lds + M_HR + QK), xcd, kb, g_r, claim);
     }
     TRACE1(9);
 
