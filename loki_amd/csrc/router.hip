@@ -205,13 +205,146 @@ __global__ void __launch_bounds__(64 * NQ) k_router_tile(const float * __restric
     }
 }
 
+// Large batches (K = 7168), LDS-staged: the tiles, lanes and contract of k_router_tile<4, 4, NQ> (32 tokens x 32 experts
+// per workgroup, lane (tg, eg) owns tokens 4 tg .. + 3 x experts 4 eg .. + 3, wave q the chunks q * 256 / NQ ..), but a
+// chunk's 32 x rows and 32 W rows (28 values each) are loaded once per wave with coalesced 16-byte loads, converted to
+// fp64 once and staged in the wave's own LDS buffer, where the lanes read them back (8 lanes share each row: a broadcast).
+// Without the staging every lane loads and converts its 8 rows itself: 8x the load instructions and the conversions, and
+// the texture unit's load rate bounds the kernel. The next chunk's raw values are in registers while a chunk computes.
+// Buffer layout, per operand: [block i (4 values)][row r % 4][half h][row r / 4] of 16 bytes (2 doubles), so a read of
+// one (i, r % 4, h) by the wave touches 8 consecutive 16-byte slots: every bank once.
+constexpr int RL_SLOTS = 7 * 4 * 2 * 8;   // 16-byte slots per operand and chunk
+template <int NQ>
+__global__ void __launch_bounds__(64 * NQ) k_router_lds(const float * __restrict__ W, const float * __restrict__ x, int n, int n_exp,
+                                                         float * __restrict__ logits) {
+#pragma clang fp contract(off)
+    constexpr int K = 7168, CL = 28, CPW = 256 / NQ, LW = CPW == 64 ? 6 : CPW == 32 ? 5 : 4;
+    static_assert(CPW == (1 << LW) && LW >= 4, "slices of 16, 32 or 64 chunks");
+    static_assert(NQ * 16 * 64 * 8 <= NQ * 2 * RL_SLOTS * 16, "the slices' totals fit the staging buffers");
+    __shared__ __attribute__((aligned(16))) double2 buf[NQ][2][RL_SLOTS];   // [wave][x, W][slot]; then the slices' totals
+    const int q = threadIdx.x >> 6, lane = lane_id(), tg = lane >> 3, eg = lane & 7;
+    const int tb = blockIdx.y * 32, eb = blockIdx.x * 32;
+    // the lane's staging share: 16-byte pieces f = lane + 64 k (k < 7) of the chunk's 448 (x rows first, then W rows)
+    const float * src[7]; int dst[7];
+#pragma unroll
+    for (int k = 0; k < 7; ++k) {
+        const int f = lane + 64 * k, op = f >= 224, g = f - 224 * op, r = g / 7, i = g % 7;
+        const int row = op ? (eb + r < n_exp ? eb + r : 0) : (tb + r < n ? tb + r : 0);
+        src[k] = (op ? W : x) + (size_t) row * K + 4 * i;
+        dst[k] = op * RL_SLOTS + ((i * 4 + (r & 3)) * 2) * 8 + (r >> 2);   // half 0; half 1 is 8 slots on
+    }
+    double2 * wb = &buf[q][0][0];
+    float4 nv[7];
+    auto fetch = [&](int c) {
+#pragma unroll
+        for (int k = 0; k < 7; ++k) { nv[k] = gloadf4(src[k] + CL * c); }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int k = 0; k < 7; ++k) {
+            wb[dst[k]] = make_double2((double) nv[k].x, (double) nv[k].y);
+            wb[dst[k] + 8] = make_double2((double) nv[k].z, (double) nv[k].w);
+        }
+    };
+    // chunk c's in-order sums for the lane's 4 x 4 logits, from the staged buffer
+    auto chunk = [&](RgAcc<4, 4> & s) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { s.v[t][e] = 0.0; }
+        }
+#pragma unroll
+        for (int i = 0; i < 7; ++i) {
+            double xa[4][4], wa[4][4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const double2 v = wb[((i * 4 + t) * 2 + h) * 8 + tg];
+                    xa[t][2 * h] = v.x; xa[t][2 * h + 1] = v.y;
+                    const double2 u = wb[RL_SLOTS + ((i * 4 + t) * 2 + h) * 8 + eg];
+                    wa[t][2 * h] = u.x; wa[t][2 * h + 1] = u.y;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) { s.v[t][e] = __builtin_fma(xa[t][j], wa[e][j], s.v[t][e]); }
+                }
+            }
+        }
+    };
+    const int c0 = q * CPW;
+    fetch(c0);
+    int cn = 0;   // chunks of the slice consumed
+    // one chunk: stage the fetched values, fetch the next chunk's, compute (a wave's LDS operations run in order, so the
+    // staging writes follow the previous chunk's reads)
+    auto next_chunk = [&](RgAcc<4, 4> & v) {
+        stage();
+        if (cn + 1 < CPW) { fetch(c0 + cn + 1); }
+        chunk(v);
+        ++cn;
+    };
+    // the slice's pairwise tree: 16-chunk groups built as the chunks arrive (binary counter), then levels 5 and 6
+    auto tile16 = [&]() {
+        RgAcc<4, 4> pend[4], v;
+#pragma unroll 1
+        for (int c = 0; c < 16; ++c) {
+            next_chunk(v);
+            if (!(c & 1)) { pend[0] = v; continue; }
+            rg_add(v, pend[0], v);
+            if (!(c & 2)) { pend[1] = v; continue; }
+            rg_add(v, pend[1], v);
+            if (!(c & 4)) { pend[2] = v; continue; }
+            rg_add(v, pend[2], v);
+            if (!(c & 8)) { pend[3] = v; continue; }
+            rg_add(v, pend[3], v);
+        }
+        return v;
+    };
+    RgAcc<4, 4> tot, l4, l5;
+#pragma unroll 1
+    for (int g = 0; g < CPW / 16; ++g) {
+        RgAcc<4, 4> v = tile16();
+        if (LW == 4) { tot = v; break; }
+        if (!(g & 1)) { l4 = v; continue; }
+        rg_add(v, l4, v);
+        if (LW == 5) { tot = v; break; }
+        if (!(g & 2)) { l5 = v; continue; }
+        rg_add(tot, l5, v);
+    }
+    __syncthreads();   // every wave is done with its staging buffer: it now holds the slices' totals
+    double * part = reinterpret_cast<double *>(&buf[0][0][0]);   // [NQ][16][64]
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { part[(q * 16 + t * 4 + e) * 64 + lane] = tot.v[t][e]; }
+    }
+    __syncthreads();
+    // the tree's top levels over the NQ slices, pairwise in slice order; output o of the lane by wave o % NQ
+    for (int o = q; o < 16; o += NQ) {
+        const int t = tb + tg * 4 + o / 4, e = eb + eg * 4 + o % 4;
+        double v[NQ];
+#pragma unroll
+        for (int j = 0; j < NQ; ++j) { v[j] = part[(j * 16 + o) * 64 + lane]; }
+#pragma unroll
+        for (int w = 1; w < NQ; w *= 2) {
+#pragma unroll
+            for (int j = 0; j + w < NQ; j += 2 * w) { v[j] = v[j] + v[j + w]; }
+        }
+        if (t < n && e < n_exp) { logits[(size_t) t * n_exp + e] = (float) v[0]; }
+    }
+}
+
 hipError_t launch_router_logits(const float * W, const float * x, int n, int n_exp, int K, float * logits, hipStream_t st) {
     if (n <= 0) { return hipSuccess; }
     if (K % 1024 != 0) { return hipErrorInvalidValue; }
     // measured on MI355X: k_router_wg costs ~0.6 us per token (every workgroup reads all of x), the 4 x 2 tiles a flat
     // ~150 us from 64 to 512 tokens; the crossover is near 256
-    if (K == 7168 && n >= 1024) {   // 32 x 32 tiles (4 x 4 per lane)
-        k_router_tile<4, 4, 4><<<dim3((n_exp + 31) / 32, (n + 31) / 32), 256, 0, st>>>(W, x, n, n_exp, logits);
+    if (K == 7168 && n >= 1024) {   // 32 x 32 tiles (4 x 4 per lane), staged in LDS
+        k_router_lds<4><<<dim3((n_exp + 31) / 32, (n + 31) / 32), 256, 0, st>>>(W, x, n, n_exp, logits);
         return hipGetLastError();
     }
     if (K == 7168 && n >= RW_MAXN) {   // 32 x 16 tiles (4 x 2 per lane)
