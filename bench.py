@@ -245,13 +245,15 @@ def run_kquant(ctx, torch, iters=20, seed=20260401):
     return out
 
 
-def run_dropin(ctx, torch, steps=30, warmup=3, ggml_steps=3, seed=20260601):
+def run_dropin(ctx, torch, steps=60, warmup=5, ggml_steps=3, seed=20260601):
     """The reference-named path at decode-1, as the engine drives it (src/server_core_fused.cpp:946-953): per token
     fl_ffn_begin (router input and residual from the host; routing and shared expert) -> fl_fetch (routing to the host,
     waited) -> fl_moe on the layer's resident 256-expert arena (ids = expert ids, waited; h and moe to the host). The
     arena and the shared expert are tiled and declared (fl_register_tiled), so fl_moe reads them in place; the same
     layer in ggml's layout (undeclared: repacked on every call, the reference's refilled-arena contract) is timed over a
-    few tokens for comparison. Times are host wall clock per token (every step ends in a host wait)."""
+    few tokens for comparison. Times are host wall clock per token (every step ends in a host wait): medians over the
+    tokens (the measurement protocol's statistic; an occasional host stall of a few ms moves the mean), the mean beside
+    them."""
     import ctypes
     import numpy as np
     from loki_amd import FLOut, FLW, MoeLayerWeights, lib
@@ -281,18 +283,20 @@ def run_dropin(ctx, torch, steps=30, warmup=3, ggml_steps=3, seed=20260601):
         wts = np.ctypeslib.as_array(out.wts, shape=(8,)).copy()
         lib().fl_moe(ctx.ctx, g.data_ptr(), u.data_ptr(), d.data_ptr(), 256, 4, ptr(sel), ptr(wts), 8, 1, ctypes.byref(out))
         t3 = time.perf_counter()
-        split[0] += t1 - t0; split[1] += t2 - t1; split[2] += t3 - t2
+        split.append((t1 - t0, t2 - t1, t3 - t2))
 
     res = {}
     try:
         w = flw((L.sh_gate, L.sh_up, L.sh_down))
-        split = [0.0, 0.0, 0.0]
+        split = []
         for i in range(warmup):
-            token(i, w, L.gate, L.up, L.down, [0.0, 0.0, 0.0])
+            token(i, w, L.gate, L.up, L.down, [])
         for i in range(steps):
             token(warmup + i, w, L.gate, L.up, L.down, split)
-        res["us_per_token"] = round(sum(split) / steps * 1e6, 1)
-        res["ffn_begin_us"], res["fetch_us"], res["moe_us"] = (round(v / steps * 1e6, 1) for v in split)
+        sp = np.array(split) * 1e6
+        res["us_per_token"] = round(float(np.median(sp.sum(axis=1))), 1)
+        res["ffn_begin_us"], res["fetch_us"], res["moe_us"] = (round(float(v), 1) for v in np.median(sp, axis=0))
+        res["mean_us_per_token"] = round(float(sp.sum(axis=1).mean()), 1)
         res["tokens"] = steps
     finally:
         for t in mats:
@@ -302,11 +306,11 @@ def run_dropin(ctx, torch, steps=30, warmup=3, ggml_steps=3, seed=20260601):
     gg = [ctx.unpack(m, r, c, n) for m, (r, c, n) in zip(mats, ((2048, E, 256), (2048, E, 256), (E, 2048, 256), (2048, E, 1), (2048, E, 1), (E, 2048, 1)))]
     torch.cuda.synchronize()
     w = flw(gg[3:])
-    split = [0.0, 0.0, 0.0]
-    token(0, w, gg[0], gg[1], gg[2], [0.0, 0.0, 0.0])
+    split = []
+    token(0, w, gg[0], gg[1], gg[2], [])
     for i in range(ggml_steps):
         token(1 + i, w, gg[0], gg[1], gg[2], split)
-    res["ggml_arena_us_per_token"] = round(sum(split) / ggml_steps * 1e6, 1)
+    res["ggml_arena_us_per_token"] = round(float(np.median(np.array(split).sum(axis=1))) * 1e6, 1)
     res["ggml_arena_tokens"] = ggml_steps
     del gg, L
     torch.cuda.empty_cache()

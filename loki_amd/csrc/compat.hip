@@ -13,6 +13,7 @@
 // order with the weights of equal slots merged; base_rows/wide_finish (:351-360) add fi + shared, then the k outputs.
 #include "fl_ctx.h"
 
+#include <chrono>
 #include <mutex>
 
 using namespace lk;
@@ -57,11 +58,33 @@ namespace {
 constexpr int RMAX = 64;           // rows per fl_ffn_begin call (the reference's RMAX, src/fused_layer.cu:402)
 constexpr int NB = 8;              // rows of a narrow pass (src/fused_layer.cu:18)
 constexpr int E_ = 7168, H_ = 2048, NEXP_ = 256;
+constexpr int ZS_DONE = 2 * RMAX * MAXK + 16;   // the routing's done word in z_sel (its own cache line)
 
 template <class T> T * pinned(size_t n) {
     void * p = nullptr;
     if (hipHostMalloc(&p, n * sizeof(T) > 0 ? n * sizeof(T) : 1, hipHostMallocDefault) != hipSuccess) { (void) hipGetLastError(); return nullptr; }
     std::memset(p, 0, n * sizeof(T));
+    return static_cast<T *>(p);
+}
+// pinned host memory that kernels read and write in place (coherent: not cached on the device, a kernel's stores are
+// seen by the host once the stream has been waited); *dev = the address kernels use
+// spins until every word of w[0 .. n) reads tag (stores of a kernel to host memory), at most max_us; false: not seen
+static bool spin_words(const unsigned * w, int n, unsigned tag, double max_us) {
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int i = 0; i < n; ++i) {
+        for (unsigned it = 0; __atomic_load_n(w + i, __ATOMIC_ACQUIRE) != tag; ++it) {
+            if ((it & 255u) == 255u && std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count() > max_us) {
+                return false;
+            }
+        }
+    }
+    return true;
+}
+template <class T> T * mapped(size_t n, T ** dev) {
+    void * p = nullptr;
+    if (hipHostMalloc(&p, n * sizeof(T), hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess) { (void) hipGetLastError(); return nullptr; }
+    std::memset(p, 0, n * sizeof(T));
+    if (hipHostGetDevicePointer(reinterpret_cast<void **>(dev), p, 0) != hipSuccess) { (void) hipGetLastError(); (void) hipHostFree(p); return nullptr; }
     return static_cast<T *>(p);
 }
 
@@ -141,16 +164,18 @@ inline unsigned nblk(int64_t tot) { return (unsigned) ((tot + 255) / 256); }
 }  // namespace
 
 struct Compat {
-    // rows of the last fl_ffn_begin (narrow pass)
-    int N = 0;
-    DBuf<float> ncur, fi, logits, probs, wts, h, o, sh_o, wr32; DBuf<int8_t> xq, hq; DBuf<float> xd, hd; DBuf<int> sel;
+    // rows of the last fl_ffn_begin (narrow pass); sh_pending / xq_pending: its shared expert / the Q8_K of its rows not
+    // computed yet (fl_moe's one-token launch computes both itself; the per-pass fl_moe and fl_skip compute them first)
+    int N = 0; bool sh_pending = false, xq_pending = false;
+    // ncur: the N rows of ncur then the N rows of ffn_inp (one copy in); fi points at the second part
+    DBuf<float> ncur, logits, probs, wts, h, o, sh_o, wr32; float * fi = nullptr; DBuf<int8_t> xq, hq; DBuf<float> xd, hd;
     DBuf<uint8_t> sh_t; const void * sh_key[3] = { nullptr, nullptr, nullptr }; int sh_fkey[3] = { -1, -1, -1 };
     bool sh_tkey[3] = { false, false, false };   // whether each was a declared-tiled matrix when sh_t was filled
     int shf[3] = { FL_IQ2, FL_IQ2, FL_IQ2 };   // shared gate / up / down formats (fl_set_shared_formats)
     DBuf<float> sg, su;                         // K-quant shared gate / up outputs
     // fl_moe
     DBuf<uint8_t> ag, au, ad; DBuf<int> ids, counts, offsets, perm, inv, act, nact; DBuf<float> w, hout, moe;
-    std::vector<int> last_ids; int last_KE = 0, last_n = 0;
+    std::vector<int> last_ids; int last_KE = 0, last_n = 0; bool last_fast = false;   // last_fast: o holds slot k at row k
     // wide pass
     int wmax = 0, wke = 0;
     DBuf<float> ncur_all, base_all, out_all, xd_all; DBuf<int8_t> xq_all;
@@ -162,9 +187,15 @@ struct Compat {
     hipEvent_t wt_ev[2] = { nullptr, nullptr }; bool wt_rec[2] = { false, false };   // after each parity's table copies
     // pinned host mirrors
     int * h_sel = nullptr; float * h_wts = nullptr, * h_ncur = nullptr, * h_fi = nullptr, * h_h = nullptr, * h_moe = nullptr;
+    // kernel-written host memory (no copies): the router's picks of the RMAX rows then their weights (z_sel), then
+    // the one-launch routing's done word (at ZS_DONE); fl_moe's one-token launch's ids then weights (z_in) and its h
+    // then moe (z_out); *_d = the device addresses. r_tagged: the last fl_ffn_begin's routing sets the done word, to rtag
+    int * z_sel = nullptr, * z_sel_d = nullptr, * z_in = nullptr, * z_in_d = nullptr; float * z_out = nullptr, * z_out_d = nullptr;
+    unsigned rtag = 0; bool r_tagged = false;
     float * h_wh = nullptr, * h_wmoe = nullptr;
     // pinned staging of the host inputs (pageable copies would wait for the stream): fl_ffn_begin's ncur / ffn_inp,
     // fl_moe's ids / w; in_ev is recorded after their copies and waited before the buffers are refilled
+    // (in_ncur holds ncur's rows then ffn_inp's, in_fi points at the latter)
     float * in_ncur = nullptr, * in_fi = nullptr, * in_w = nullptr; int * in_ids = nullptr;
     hipEvent_t in_ev = nullptr; bool in_rec = false;
 };
@@ -172,12 +203,14 @@ struct Compat {
 static Compat * cs(FLCtx * c) {
     if (!c->compat) {
         Compat * s = new Compat();
+        s->z_sel = mapped<int>(ZS_DONE + 16, &s->z_sel_d); s->z_in = mapped<int>(2 * MAXK, &s->z_in_d);
+        s->z_out = mapped<float>(2 * E_, &s->z_out_d);
         s->h_sel = pinned<int>(RMAX * MAXK); s->h_wts = pinned<float>(RMAX * MAXK);
         s->h_ncur = pinned<float>((size_t) RMAX * E_); s->h_fi = pinned<float>((size_t) RMAX * E_);
         s->h_h = pinned<float>((size_t) RMAX * E_); s->h_moe = pinned<float>((size_t) RMAX * E_);
-        s->in_ncur = pinned<float>((size_t) RMAX * E_); s->in_fi = pinned<float>((size_t) RMAX * E_);
-        s->in_ids = pinned<int>(NB * MAXK); s->in_w = pinned<float>(NB * MAXK);
-        if (!s->h_sel || !s->h_wts || !s->h_ncur || !s->h_fi || !s->h_h || !s->h_moe || !s->in_ncur || !s->in_fi || !s->in_ids || !s->in_w) {
+        s->in_ncur = pinned<float>((size_t) 2 * RMAX * E_);
+        s->in_ids = pinned<int>(2 * NB * MAXK); s->in_w = pinned<float>(NB * MAXK);   // in_ids: ids, then the weights
+        if (!s->z_sel || !s->z_in || !s->z_out || !s->h_sel || !s->h_wts || !s->h_ncur || !s->h_fi || !s->h_h || !s->h_moe || !s->in_ncur || !s->in_ids || !s->in_w) {
             fatal("hipHostMalloc (fused-layer mirrors)", hipErrorOutOfMemory, __FILE__, __LINE__);
         }
         CK(hipEventCreateWithFlags(&s->in_ev, hipEventDisableTiming));
@@ -190,8 +223,8 @@ void compat_free(FLCtx * c) {
     Compat * s = c->compat;
     if (!s) { return; }
     if (s->in_ev) { (void) hipEventSynchronize(s->in_ev); (void) hipEventDestroy(s->in_ev); }
-    for (void * p : { (void *) s->h_sel, (void *) s->h_wts, (void *) s->h_ncur, (void *) s->h_fi, (void *) s->h_h, (void *) s->h_moe, (void *) s->h_wh, (void *) s->h_wmoe,
-                      (void *) s->in_ncur, (void *) s->in_fi, (void *) s->in_ids, (void *) s->in_w }) {
+    for (void * p : { (void *) s->z_sel, (void *) s->z_in, (void *) s->z_out, (void *) s->h_sel, (void *) s->h_wts, (void *) s->h_ncur, (void *) s->h_fi, (void *) s->h_h, (void *) s->h_moe, (void *) s->h_wh, (void *) s->h_wmoe,
+                      (void *) s->in_ncur, (void *) s->in_ids, (void *) s->in_w }) {
         if (p) { (void) hipHostFree(p); }
     }
     for (hipEvent_t e : s->wev) { if (e) { (void) hipEventDestroy(e); } }
@@ -199,8 +232,8 @@ void compat_free(FLCtx * c) {
         if (s->wt_i[p]) { (void) hipHostFree(s->wt_i[p]); } if (s->wt_w[p]) { (void) hipHostFree(s->wt_w[p]); }
         if (s->wt_ev[p]) { (void) hipEventDestroy(s->wt_ev[p]); }
     }
-    s->ncur.release(); s->fi.release(); s->logits.release(); s->probs.release(); s->wts.release(); s->h.release(); s->o.release(); s->sh_o.release(); s->wr32.release();
-    s->xq.release(); s->hq.release(); s->xd.release(); s->hd.release(); s->sel.release(); s->sh_t.release(); s->sg.release(); s->su.release();
+    s->ncur.release(); s->logits.release(); s->probs.release(); s->wts.release(); s->h.release(); s->o.release(); s->sh_o.release(); s->wr32.release();
+    s->xq.release(); s->hq.release(); s->xd.release(); s->hd.release(); s->sh_t.release(); s->sg.release(); s->su.release();
     s->ag.release(); s->au.release(); s->ad.release(); s->ids.release(); s->counts.release(); s->offsets.release(); s->perm.release(); s->inv.release();
     s->act.release(); s->nact.release(); s->w.release(); s->hout.release(); s->moe.release();
     s->ncur_all.release(); s->base_all.release(); s->out_all.release(); s->xd_all.release(); s->xq_all.release();
@@ -274,6 +307,19 @@ static void shared_expert(FLCtx * c, Compat * s, const int8_t * xq, const float 
     } else {
         kq_single(c, s->shf[2], s->sh_key[2], s->hq.p, s->hd.p, N, H_, E_, out);   // src/fused_layer.cu:524
     }
+}
+
+// the shared expert of the last fl_ffn_begin into sh_o, if not computed yet
+static void quant_now(FLCtx * c, Compat * s) {
+    if (!s->xq_pending) { return; }
+    CK(launch_quant_q8k(s->ncur.p, s->N, E_, s->xq.p, s->xd.p, c->st));
+    s->xq_pending = false;
+}
+static void shared_now(FLCtx * c, Compat * s) {
+    if (!s->sh_pending) { return; }
+    quant_now(c, s);
+    shared_expert(c, s, s->xq.p, s->xd.p, s->N, s->sh_o.p);
+    s->sh_pending = false;
 }
 
 // an arena's matrices in the tiled layout: declared-tiled matrices as they are, the others repacked into ag/au/ad
@@ -363,13 +409,13 @@ extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur,
         const void * m = i == 0 ? W->sh_gate : i == 1 ? W->sh_up : W->sh_down;
         if (s->shf[i] != FL_IQ2 && (reinterpret_cast<uintptr_t>(m) & 3u)) { return fail(c, FL_EINVAL, "K-quant shared matrices must be 4-byte aligned"); }
     }
-    ALLOC(c, s->ncur, R); ALLOC(c, s->fi, R); ALLOC(c, s->logits, RMAX * ne); ALLOC(c, s->probs, RMAX * ne);
-    ALLOC(c, s->sel, RMAX * MAXK); ALLOC(c, s->wts, RMAX * MAXK); ALLOC(c, s->xq, R); ALLOC(c, s->xd, RMAX * (E_ / QK)); ALLOC(c, s->sh_o, R);
+    ALLOC(c, s->ncur, 2 * R); ALLOC(c, s->logits, RMAX * ne); ALLOC(c, s->probs, RMAX * ne);
+    ALLOC(c, s->xq, R); ALLOC(c, s->xd, RMAX * (E_ / QK)); ALLOC(c, s->sh_o, R);
     hipStream_t st = c->st;
     if (s->in_rec) { TRY(c, hipEventSynchronize(s->in_ev)); }   // the staging's previous copies have run
+    s->in_fi = s->in_ncur + (size_t) N * E_; s->fi = s->ncur.p + (size_t) N * E_;
     std::memcpy(s->in_ncur, ncur, (size_t) N * E_ * 4); std::memcpy(s->in_fi, ffn_inp, (size_t) N * E_ * 4);
-    TRY(c, hipMemcpyAsync(s->ncur.p, s->in_ncur, (size_t) N * E_ * 4, hipMemcpyHostToDevice, st));
-    TRY(c, hipMemcpyAsync(s->fi.p, s->in_fi, (size_t) N * E_ * 4, hipMemcpyHostToDevice, st));
+    TRY(c, hipMemcpyAsync(s->ncur.p, s->in_ncur, (size_t) 2 * N * E_ * 4, hipMemcpyHostToDevice, st));
     TRY(c, hipEventRecord(s->in_ev, st)); s->in_rec = true;
     const size_t mg = mat_bytes(H_, E_);
     const void * shm[3] = { W->sh_gate, W->sh_up, W->sh_down };
@@ -394,17 +440,24 @@ extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur,
         TRY(c, launch_f16_to_f32((const uint16_t *) W->gate_inp, s->wr32.p, (int64_t) ne * E_, st));
         wr = s->wr32.p;
     }
-    if (int rc = fl_route_dev(c, wr, (const float *) W->probs_b, s->ncur.p, N, ne, E_, s->logits.p, s->probs.p, s->sel.p, s->wts.p)) { return rc; }
-    TRY(c, launch_quant_q8k(s->ncur.p, N, E_, s->xq.p, s->xd.p, st));
-    shared_expert(c, s, s->xq.p, s->xd.p, N, s->sh_o.p);
+    // the picks of row t at z_sel[t * topk ..], their weights right after the N rows' picks, written by the selection
+    // straight into host memory (fl_fetch only waits)
+    float * wts = reinterpret_cast<float *>(s->z_sel_d + (size_t) N * c->topk);
+    unsigned * done = reinterpret_cast<unsigned *>(s->z_sel_d + ZS_DONE);
+    if (int rc = route_dev(c, wr, (const float *) W->probs_b, s->ncur.p, N, ne, E_, s->logits.p, s->probs.p, s->z_sel_d, wts, done)) {
+        return rc;
+    }
+    s->r_tagged = router_fused_ok(N, E_); s->rtag = c->epoch;
+    s->N = N;
+    s->sh_pending = true; s->xq_pending = true;
+    if (wrow >= 0) { shared_now(c, s); }   // the wide pass's base rows need it now
     if (wrow >= 0) {
         TRY(c, hipMemcpyAsync(s->ncur_all.p + (size_t) wrow * E_, s->ncur.p, (size_t) N * E_ * 4, hipMemcpyDeviceToDevice, st));
         TRY(c, hipMemcpyAsync(s->xq_all.p + (size_t) wrow * E_, s->xq.p, (size_t) N * E_, hipMemcpyDeviceToDevice, st));
         TRY(c, hipMemcpyAsync(s->xd_all.p + (size_t) wrow * (E_ / QK), s->xd.p, (size_t) N * (E_ / QK) * 4, hipMemcpyDeviceToDevice, st));
-        k_base_rows<<<nblk((int64_t) N * E_), 256, 0, st>>>(s->fi.p, s->sh_o.p, (int64_t) N * E_, s->base_all.p + (size_t) wrow * E_);
+        k_base_rows<<<nblk((int64_t) N * E_), 256, 0, st>>>(s->fi, s->sh_o.p, (int64_t) N * E_, s->base_all.p + (size_t) wrow * E_);
         TRY(c, hipGetLastError());
     }
-    s->N = N;
     return FL_OK;
 }
 
@@ -412,14 +465,19 @@ extern "C" void fl_fetch(FLCtx * c, int n, int what, FLOut * out) {
     std::memset(out, 0, sizeof(FLOut));
     Compat * s = cs(c);
     if (n < 0 || n > s->N) { std::fprintf(stderr, "[fused] fl_fetch: %d rows requested, %d routed\n", n, s->N); std::exit(7); }
+    // the picks and weights are in z_sel once the routing has run: its done word says so for a routing in one launch
+    // (nothing else that the call returns is pending then); otherwise, or if the word is late, the stream is waited
+    const bool seen = (what & ~1) == 0 && s->r_tagged && spin_words(reinterpret_cast<const unsigned *>(s->z_sel + ZS_DONE), 1, s->rtag, 20000.0);
+    if (!seen) { CK(hipStreamSynchronize(c->st)); }
     if (what & 1) {
-        CK(hipMemcpyAsync(s->h_sel, s->sel.p, (size_t) n * c->topk * 4, hipMemcpyDeviceToHost, c->st));
-        CK(hipMemcpyAsync(s->h_wts, s->wts.p, (size_t) n * c->topk * 4, hipMemcpyDeviceToHost, c->st));
-        CK(hipMemcpyAsync(s->h_ncur, s->ncur.p, (size_t) n * E_ * 4, hipMemcpyDeviceToHost, c->st));
-        CK(hipMemcpyAsync(s->h_fi, s->fi.p, (size_t) n * E_ * 4, hipMemcpyDeviceToHost, c->st));
+        // the mirrors keep this call's values until the next fl_fetch whatever is enqueued meanwhile (the reference's
+        // lifetime). ncur and ffn_inp are on the device exactly as the caller handed them to fl_ffn_begin (nothing
+        // writes them), and its pinned staging still holds them: their mirrors are filled from there
+        const size_t pk = (size_t) n * c->topk;
+        std::memcpy(s->h_sel, s->z_sel, pk * 4); std::memcpy(s->h_wts, s->z_sel + (size_t) s->N * c->topk, pk * 4);
+        std::memcpy(s->h_ncur, s->in_ncur, (size_t) n * E_ * 4); std::memcpy(s->h_fi, s->in_fi, (size_t) n * E_ * 4);
         out->sel = s->h_sel; out->wts = s->h_wts; out->ncur = s->h_ncur; out->fi = s->h_fi;
     }
-    CK(hipStreamSynchronize(c->st));
 }
 
 extern "C" void fl_moe(FLCtx * c, const void * gate, const void * up, const void * down, int nexp, int down_fmt, const int * ids,
@@ -437,28 +495,67 @@ extern "C" void fl_moe(FLCtx * c, const void * gate, const void * up, const void
         std::fprintf(stderr, "[fused] fl_moe: an arena allocation is smaller than %d experts\n", nexp); std::exit(7);
     }
     hipStream_t st = c->st; const int P = n * KE;
+    c->last_kernel = 0;   // fl_debug: 2 when the one-token kernel below runs the call
     int max_slots = 1;
     { std::vector<int> per(nexp, 0); for (int i = 0; i < P; ++i) { max_slots = std::max(max_slots, ++per[ids[i]]); } }
     CK(hipEventRecord(c->em0, st));
-    FALLOC(s->ids, P); FALLOC(s->w, P); FALLOC(s->counts, nexp); FALLOC(s->offsets, nexp + 1); FALLOC(s->perm, P); FALLOC(s->inv, P);
+    FALLOC(s->ids, 2 * P); FALLOC(s->counts, nexp); FALLOC(s->offsets, nexp + 1); FALLOC(s->perm, P); FALLOC(s->inv, P);
     FALLOC(s->act, nexp); FALLOC(s->nact, 1); FALLOC(s->o, (size_t) P * E_); FALLOC(s->hout, (size_t) NB * E_); FALLOC(s->moe, (size_t) NB * E_);
-    if (s->in_rec) { CK(hipEventSynchronize(s->in_ev)); }
-    std::memcpy(s->in_ids, ids, (size_t) P * 4); std::memcpy(s->in_w, w, (size_t) P * 4);
-    CK(hipMemcpyAsync(s->ids.p, s->in_ids, (size_t) P * 4, hipMemcpyHostToDevice, st));
-    CK(hipMemcpyAsync(s->w.p, s->in_w, (size_t) P * 4, hipMemcpyHostToDevice, st));
-    CK(hipEventRecord(s->in_ev, st)); s->in_rec = true;
+    // One row with all 8 picks: one launch of the one-token kernel on the caller's picks (router and selection skipped;
+    // the shared expert and the Q8_K of fl_ffn_begin's row computed in the same launch; the combine in this function's
+    // order), when the formats are one of its variants: every matrix IQ2_XXS, or the routed down Q2_K / Q3_K with a
+    // Q5_K / Q5_K / Q6_K shared expert. Results bit-identical to the per-pass kernels below. The launch reads the picks
+    // from host memory and writes h and moe there (z_in, z_out): no copies either way.
+    const bool kq_sh = s->shf[0] == FL_Q5K && s->shf[1] == FL_Q5K && s->shf[2] == FL_Q6K;
+    const bool iq_sh = s->shf[0] == FL_IQ2 && s->shf[1] == FL_IQ2 && s->shf[2] == FL_IQ2;
+    const bool fast = n == 1 && KE == MAXK && decode1_available(c) &&
+                      ((down_fmt == FL_IQ2 && iq_sh) || ((down_fmt == FL_Q2K || down_fmt == FL_Q3K) && kq_sh && !(reinterpret_cast<uintptr_t>(down) & 3u)));
+    const float * dw = nullptr;   // the device weights of the per-pass path
+    if (!fast) {
+        if (s->in_rec) { CK(hipEventSynchronize(s->in_ev)); }
+        std::memcpy(s->in_ids, ids, (size_t) P * 4); std::memcpy(s->in_ids + P, w, (size_t) P * 4);   // ids, then weights
+        CK(hipMemcpyAsync(s->ids.p, s->in_ids, (size_t) 2 * P * 4, hipMemcpyHostToDevice, st));
+        dw = reinterpret_cast<const float *>(s->ids.p + P);
+        CK(hipEventRecord(s->in_ev, st)); s->in_rec = true;
+    } else {   // the previous fl_moe has ended (each call waits for its stream): the launch that read z_in is done
+        std::memcpy(s->z_in, ids, MAXK * 4); std::memcpy(s->z_in + MAXK, w, MAXK * 4);
+    }
     const Arena ar = pack_arena(c, s, gate, up, down, nexp, down_fmt);
-    CK(launch_dispatch(s->ids.p, P, nexp, s->counts.p, s->offsets.p, s->perm.p, s->inv.p, s->act.p, s->nact.p, st));
-    routed_experts(c, s, ar, s->xq.p, s->xd.p, n, P, KE, nexp, s->act.p, s->nact.p, s->offsets.p, s->perm.p, s->o.p, down_fmt, down, max_slots);
-    k_combine_slots<<<dim3(E_ / 256, n), 256, 0, st>>>(s->o.p, s->inv.p, s->ids.p, s->w.p, n, KE, s->sh_o.p, s->fi.p, s->hout.p, s->moe.p);
-    CK(hipGetLastError());
-    CK(hipMemcpyAsync(s->h_h, s->hout.p, (size_t) n * E_ * 4, hipMemcpyDeviceToHost, st));
-    CK(hipMemcpyAsync(s->h_moe, s->moe.p, (size_t) n * E_ * 4, hipMemcpyDeviceToHost, st));
+    if (fast) {
+        CK(ensure_expert_scratch(c, 1, E_, H_) == FL_OK ? hipSuccess : hipErrorOutOfMemory);
+        const size_t mg = mat_bytes(H_, E_);
+        DecodeArgs d{};
+        d.x = s->ncur.p; d.n = 1; d.resid = s->fi;
+        d.n_exp = nexp; d.n_group = c->n_group; d.topk_group = c->topk_group; d.topk = MAXK; d.keep = MAXK; d.scale = c->scale;
+        d.gate = ar.g; d.up = ar.u; d.estride = mg;
+        d.down = down_fmt == FL_IQ2 ? ar.d : (const uint8_t *) down; d.dstride = fmt_bytes(down_fmt, E_, H_);
+        for (int i = 0; i < 3; ++i) {   // IQ2_XXS: declared tiled as it is, else the tiled copy; K-quants in place
+            const uint8_t * m = (const uint8_t *) s->sh_key[i];
+            if (iq_sh && !tiled_holds(m, i < 2 ? mg : mat_bytes(E_, H_))) { m = s->sh_t.p + i * mg; }
+            (i == 0 ? d.sh_gate : i == 1 ? d.sh_up : d.sh_down) = m;
+        }
+        d.kdown = down_fmt == FL_IQ2 ? 0 : down_fmt;
+        d.E = E_; d.H = H_; d.xq = s->xq.p; d.xd = s->xd.p;
+        d.ext_sel = s->z_in_d; d.ext_w = reinterpret_cast<const float *>(s->z_in_d + MAXK);
+        d.moe_out = s->z_out_d + E_; d.o_out = s->o.p; d.y = s->z_out_d;
+        if (decode1_picks(c, d) != FL_OK) { std::fprintf(stderr, "[fused] fl_moe: %s\n", c->err.c_str()); std::exit(7); }
+    } else {
+        quant_now(c, s); shared_now(c, s);
+        CK(launch_dispatch(s->ids.p, P, nexp, s->counts.p, s->offsets.p, s->perm.p, s->inv.p, s->act.p, s->nact.p, st));
+        routed_experts(c, s, ar, s->xq.p, s->xd.p, n, P, KE, nexp, s->act.p, s->nact.p, s->offsets.p, s->perm.p, s->o.p, down_fmt, down, max_slots);
+        k_combine_slots<<<dim3(E_ / 256, n), 256, 0, st>>>(s->o.p, s->inv.p, s->ids.p, dw, n, KE, s->sh_o.p, s->fi, s->hout.p, s->moe.p);
+        CK(hipGetLastError());
+        CK(hipMemcpyAsync(s->h_h, s->hout.p, (size_t) n * E_ * 4, hipMemcpyDeviceToHost, st));
+        CK(hipMemcpyAsync(s->h_moe, s->moe.p, (size_t) n * E_ * 4, hipMemcpyDeviceToHost, st));
+    }
     CK(hipEventRecord(c->em1, st));
     CK(hipStreamSynchronize(st));
     float ms = 0.f; CK(hipEventElapsedTime(&ms, c->em0, c->em1)); c->ms_moe += ms;
-    s->last_ids.assign(ids, ids + P); s->last_KE = KE; s->last_n = n;
-    out->h = s->h_h; out->moe = s->h_moe;
+    if (fast && c->herr && __atomic_load_n(c->herr, __ATOMIC_ACQUIRE)) {   // a wait of the launch timed out
+        std::fprintf(stderr, "[fused] fl_moe: the one-token launch reported device code %d\n", *c->herr); std::exit(7);
+    }
+    s->last_ids.assign(ids, ids + P); s->last_KE = KE; s->last_n = n; s->last_fast = fast;
+    out->h = fast ? s->z_out : s->h_h; out->moe = fast ? s->z_out + E_ : s->h_moe;
 }
 
 extern "C" void fl_skip(FLCtx * c, const float * mo, int n, FLOut * out) {
@@ -468,8 +565,9 @@ extern "C" void fl_skip(FLCtx * c, const float * mo, int n, FLOut * out) {
     hipStream_t st = c->st;
     CK(hipEventRecord(c->em0, st));
     FALLOC(s->moe, (size_t) RMAX * E_); FALLOC(s->hout, (size_t) RMAX * E_);
+    shared_now(c, s);
     CK(hipMemcpyAsync(s->moe.p, mo, (size_t) n * E_ * 4, hipMemcpyHostToDevice, st));
-    k_skip_rows<<<nblk((int64_t) n * E_), 256, 0, st>>>(s->moe.p, s->sh_o.p, s->fi.p, (int64_t) n * E_, s->hout.p);
+    k_skip_rows<<<nblk((int64_t) n * E_), 256, 0, st>>>(s->moe.p, s->sh_o.p, s->fi, (int64_t) n * E_, s->hout.p);
     CK(hipGetLastError());
     CK(hipMemcpyAsync(s->h_h, s->hout.p, (size_t) n * E_ * 4, hipMemcpyDeviceToHost, st));
     CK(hipEventRecord(c->em1, st));
@@ -483,7 +581,8 @@ extern "C" void fl_moe_outs(FLCtx * c, int b, const int * ids, const float * w, 
     CK(hipStreamSynchronize(c->st));
     if (b < 0 || b >= s->last_n || KE != s->last_KE) { std::fprintf(stderr, "[fused] fl_moe_outs: row %d / KE %d do not match the last fl_moe\n", b, KE); std::exit(7); }
     std::vector<int> inv((size_t) s->last_n * KE);
-    CK(hipMemcpy(inv.data(), s->inv.p, inv.size() * 4, hipMemcpyDeviceToHost));
+    if (s->last_fast) { for (size_t i = 0; i < inv.size(); ++i) { inv[i] = (int) i; } }   // the one-token launch: slot k at row k
+    else { CK(hipMemcpy(inv.data(), s->inv.p, inv.size() * 4, hipMemcpyDeviceToHost)); }
     std::vector<float> row(E_);
     for (int k = 0; k < KE; ++k) {
         int kf = -1;

@@ -63,7 +63,12 @@ struct FLCtx {
     // are read in place (ggml layout), IQ2_XXS ones tiled
     int lf[4] = { FL_IQ2, FL_IQ2, FL_IQ2, FL_IQ2 };
     DBuf<float> ksg, ksu;                      // K-quant shared gate / up outputs
+    DBuf<unsigned> rcnt;                       // the one-launch routing's self-resetting counter (launch_router_fused)
 };
+// fl_route_dev with, for the one-launch routing of a few rows (router_fused_ok), a host word set to the context's epoch
+// (as it is after the call) once the picks are written; done may be null, other sizes leave it alone
+int route_dev(FLCtx * c, const float * W, const float * bias, const float * x, int n, int n_exp, int E, float * logits, float * probs,
+              int * sel, float * w, unsigned * done);
 // a device int 0 (empty expert lists of the per-pass kernels)
 const int * zero_int(FLCtx * c);
 static const int NSTAGE = 6;   // quant_x, router_logits, router_select, dispatch, gate_up (+SwiGLU, Q8_K(h)), down (+combine)
@@ -105,6 +110,10 @@ void tiled_add(const void * p, size_t bytes);
 void tiled_remove_within(const void * p, size_t bytes);
 bool tiled_holds(const void * p, size_t bytes);
 int ensure_expert_scratch(FLCtx * c, size_t rows, int E, int H);   // fused_layer.hip
+// the one-token kernel is available (a 256-CU device, the fused decode not switched off), and its launch on caller-given
+// picks (d.ext_sel / ext_w set; this fills the tables, tagged buffers, epoch and error words of d)
+bool decode1_available(FLCtx * c);
+int decode1_picks(FLCtx * c, lk::DecodeArgs & d);
 lk::ExpertArgs expert_args(FLCtx * c, int n, int P, int shared);
 // counter sets of the two persistent kernels inside FLCtx::cnt
 inline void expert_counters(FLCtx * c, lk::ExpertArgs & a, int down) {

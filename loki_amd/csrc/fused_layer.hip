@@ -110,6 +110,7 @@ extern "C" void fl_free(FLCtx * c) {
     compat_free(c); c->zero_i.release(); c->terms.release(); c->cnt.release();
     c->tab.release(); c->derr.release(); c->dlogit.release(); c->dth.release(); c->dto.release();
     c->ptab.release(); c->pcols.release(); c->pncols.release(); c->xh.release(); c->hh.release();
+    c->ksg.release(); c->ksu.release(); c->rcnt.release();
     for (auto & v : c->ev_free) { for (auto e : v) { (void) hipEventDestroy(e); } }
     for (auto & v : c->ev_pending) { for (auto e : v) { (void) hipEventDestroy(e); } }
     (void) hipEventDestroy(c->em0); (void) hipEventDestroy(c->em1); (void) hipStreamDestroy(c->own);
@@ -184,8 +185,9 @@ static int check_rule(FLCtx * c, int n_exp) {
     return FL_OK;
 }
 
-extern "C" int fl_route_dev(FLCtx * c, const float * W, const float * bias, const float * x, int n, int n_exp, int E,
-                            float * logits, float * probs, int * sel, float * w) {
+static int decode_tagged(FLCtx * c, hipStream_t st);
+int route_dev(FLCtx * c, const float * W, const float * bias, const float * x, int n, int n_exp, int E, float * logits, float * probs,
+              int * sel, float * w, unsigned * done) {
     if (!c) { return FL_EINVAL; }
     if (n < 0 || n > 65536) { return fail(c, FL_ERANGE, "n = %d outside 0..65536", n); }
     if (n == 0) { return FL_OK; }
@@ -196,9 +198,20 @@ extern "C" int fl_route_dev(FLCtx * c, const float * W, const float * bias, cons
         return fail(c, FL_EINVAL, "router weight, bias or x allocation smaller than its shape (%d experts, %d rows of %d)", n_exp, n, E);
     }
     if (!logits) { ALLOC(c, c->logits, (size_t) n * n_exp); logits = c->logits.p; }
+    if (router_fused_ok(n, E)) {   // a few rows: logits and selection in one launch, the logits handed over tagged
+        if (!c->rcnt.p) { ALLOC(c, c->rcnt, 1); TRY(c, hipMemsetAsync(c->rcnt.p, 0, sizeof(unsigned), c->st)); }
+        if (int rc = decode_tagged(c, c->st)) { return rc; }   // a fresh epoch for the tagged logit buffer
+        TRY(c, launch_router_fused(W, x, n, n_exp, E, logits, bias, c->n_group, c->topk_group, c->topk, c->scale, probs, sel, w, c->dlogit.p,
+                                   c->epoch, c->rcnt.p, done, c->st));
+        return FL_OK;
+    }
     TRY(c, launch_router_logits(W, x, n, n_exp, E, logits, c->st));
     TRY(c, launch_router_select(logits, bias, n, n_exp, c->n_group, c->topk_group, c->topk, c->scale, probs, sel, w, c->st));
     return FL_OK;
+}
+extern "C" int fl_route_dev(FLCtx * c, const float * W, const float * bias, const float * x, int n, int n_exp, int E,
+                            float * logits, float * probs, int * sel, float * w) {
+    return route_dev(c, W, bias, x, n, n_exp, E, logits, probs, sel, w, nullptr);
 }
 
 extern "C" int fl_dispatch_dev(FLCtx * c, const int * sel, int n, int topk, int n_exp, int * counts, int * offsets, int * perm, int * inv, int * act, int * nact) {
@@ -325,6 +338,28 @@ static bool decode1_ready(FLCtx * c) {
     }
     return c->d1 && c->d1_ok > 0;
 }
+// the single-launch blocks' shared state: error word, tagged buffers and a new epoch per launch (the buffers cleared on
+// first use and whenever the epoch wraps, so no stale word can carry the new epoch)
+static int decode_tagged(FLCtx * c, hipStream_t st) {
+    if (!c->derr.p) { ALLOC(c, c->derr, 1); TRY(c, hipMemsetAsync(c->derr.p, 0, sizeof(int), st)); }
+    if (!c->dlogit.p) { ALLOC(c, c->dlogit, DEC_TLOGITS); ALLOC(c, c->dth, DEC_TH); ALLOC(c, c->dto, DEC_TO); c->epoch = 0; }
+    if (++c->epoch == 0) { c->epoch = 1; }   // epoch 0 is the cleared state of the tagged words
+    if (c->epoch == 1) {
+        TRY(c, hipMemsetAsync(c->dlogit.p, 0, DEC_TLOGITS * sizeof(uint64_t), st));
+        TRY(c, hipMemsetAsync(c->dth.p, 0, DEC_TH * sizeof(uint64_t), st));
+        TRY(c, hipMemsetAsync(c->dto.p, 0, DEC_TO * sizeof(uint64_t), st));
+    }
+    return FL_OK;
+}
+bool decode1_available(FLCtx * c) { return c->fused != 0 && decode_ready(c) && decode1_ready(c); }
+int decode1_picks(FLCtx * c, DecodeArgs & d) {
+    if (int rc = decode_tagged(c, c->st)) { return rc; }
+    d.tab = c->tab.p; d.tlogits = c->dlogit.p; d.th = c->dth.p; d.to = c->dto.p;
+    d.epoch = c->epoch; d.err = c->derr.p; d.herr = c->herr ? c->herr_dev : nullptr;
+    TRY(c, launch_moe_decode1(d, c->fused == 1, c->st));
+    c->last_kernel = 2; c->last_fused = 1;
+    return FL_OK;
+}
 static hipError_t launch_decode(FLCtx * c, const DecodeArgs & d, hipStream_t st) {
     if (d.n == 1 && d.topk == MAXK && d.keep == MAXK && decode1_ready(c)) { c->last_kernel = 2; return launch_moe_decode1(d, c->fused == 1, st); }
     c->last_kernel = 1;
@@ -400,14 +435,7 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     hipStream_t st = c->st;
     std::vector<hipEvent_t> * ev = prof_begin(c);
     if (fused) {
-        if (!c->derr.p) { ALLOC(c, c->derr, 1); TRY(c, hipMemsetAsync(c->derr.p, 0, sizeof(int), st)); }
-        if (!c->dlogit.p) { ALLOC(c, c->dlogit, DEC_TLOGITS); ALLOC(c, c->dth, DEC_TH); ALLOC(c, c->dto, DEC_TO); c->epoch = 0; }
-        if (++c->epoch == 0) { c->epoch = 1; }   // epoch 0 is the cleared state of the tagged words
-        if (c->epoch == 1) {   // first use, or the epoch wrapped: no stale word may carry the new epoch
-            TRY(c, hipMemsetAsync(c->dlogit.p, 0, DEC_TLOGITS * sizeof(uint64_t), st));
-            TRY(c, hipMemsetAsync(c->dth.p, 0, DEC_TH * sizeof(uint64_t), st));
-            TRY(c, hipMemsetAsync(c->dto.p, 0, DEC_TO * sizeof(uint64_t), st));
-        }
+        if (int rc = decode_tagged(c, st)) { return rc; }
         DecodeArgs d{};
         d.tab = c->tab.p; d.x = x; d.n = n; d.prenorm = prenorm ? 1 : 0; d.nw = nw; d.eps = eps; d.resid = resid;
         d.Wr = L->gate_inp; d.bias = L->probs_b; d.n_exp = ne; d.n_group = c->n_group; d.topk_group = c->topk_group; d.topk = tsel; d.scale = c->scale;

@@ -69,7 +69,8 @@ constexpr int M_SEL = M_CMB + CROWS1 * SLOTS1 * 4; // picks [8] and weights [8]
 constexpr int NCTL1 = 32;
 constexpr int M_CTL = M_SEL + 2 * MAXK * 4;        // control words
 constexpr int M_NRM = M_CTL + NCTL1 * 4;           // RMSNorm scale
-constexpr int DEC1_LDS = M_NRM + 16;
+constexpr int M_EXT = M_NRM + 16;                  // caller's picks: the distinct ids' slots [8], summed weights [8], count
+constexpr int DEC1_LDS = M_EXT + 2 * MAXK * 4 + 16;
 static_assert(DEC1_LDS <= 160 * 1024 && (M_X % 16) == 0 && (M_HR % 16) == 0 && (M_HS % 16) == 0, "LDS layout");
 enum { C_RT = 0, C_STAGED = 1, C_SH = 2, C_READY = 3, C_HR = 4, C_HS = 5, C_CMBFAIL = 6, C_NRM = 7, C_RISSUED = 8,
        C_GUCLAIM = 9, C_DNCLAIM = 10, C_GUDONE = 11, C_SB1 = 12, C_SELFAIL = 13, C_SHCLAIM = 14 };
@@ -634,17 +635,29 @@ template <bool KQ> __device__ __forceinline__ bool combine1(const D1Args & a, ld
         float o = 0.f;
 #pragma unroll
         for (int kb = 0; kb < NBH1; ++kb) { o = o + tag1_val(w[kb]); }
-        cmb[i * SLOTS1 + s] = KQ ? o : 0.125f * o;
+        const float ov = KQ ? o : 0.125f * o;
+        cmb[i * SLOTS1 + s] = ov;
+        if (a.o_out && s < MAXK) { gptr(a.o_out)[(size_t) s * E1 + row] = ov; }
     }
     __syncthreads();
     if (t < CROWS1) {
         const int row = row0 + t;
-        float mv = cmb[t * SLOTS1] * wts[0];
+        if (a.ext_sel) {   // fl_moe's combine: the distinct ids ascending, moe = their weighted sum, y = (moe + shared) + resid
+            const LK_LOCAL int * xs = reinterpret_cast<const LK_LOCAL int *>(lds + M_EXT);
+            const LK_LOCAL float * xw = reinterpret_cast<const LK_LOCAL float *>(lds + M_EXT + MAXK * 4);
+            const int cnt = reinterpret_cast<const LK_LOCAL int *>(lds + M_EXT + 2 * MAXK * 4)[0];
+            float v = 0.f;
+            for (int q = 0; q < cnt; ++q) { v = v + xw[q] * cmb[t * SLOTS1 + xs[q]]; }
+            gptr(a.moe_out)[row] = v;
+            gptr(a.y)[row] = (v + cmb[t * SLOTS1 + MAXK]) + gptr(a.resid)[row];
+        } else {
+            float mv = cmb[t * SLOTS1] * wts[0];
 #pragma unroll
-        for (int k = 1; k < MAXK; ++k) { mv = mv + cmb[t * SLOTS1 + k] * wts[k]; }
-        float yv = mv + cmb[t * SLOTS1 + MAXK];
-        if (a.resid) { yv = yv + gptr(a.resid)[row]; }
-        gptr(a.y)[row] = yv;
+            for (int k = 1; k < MAXK; ++k) { mv = mv + cmb[t * SLOTS1 + k] * wts[k]; }
+            float yv = mv + cmb[t * SLOTS1 + MAXK];
+            if (a.resid) { yv = yv + gptr(a.resid)[row]; }
+            gptr(a.y)[row] = yv;
+        }
     }
     (void) ok;
     return true;
@@ -698,10 +711,10 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
 
     // 1. router on waves 0-3; table copy and token quantisation on the others; the shared gate/up task on the last 7
     if (wave < 4) {
-        router1(a, lds, wave, ctl);
+        if (!a.ext_sel) { router1(a, lds, wave, ctl); }   // with the caller's picks there is no routing
         TRACE1(1);
     } else {
-        (void) wait1(ctl + C_RISSUED, 4);   // the router's weight and token loads go first (the critical path)
+        if (!a.ext_sel) { (void) wait1(ctl + C_RISSUED, 4); }   // the router's weight and token loads go first (the critical path)
         static_assert(TAB_BYTES % (1024 * NQW1) == 0, "table image split over the staging waves");
         constexpr int PER = TAB_BYTES / 1024 / NQW1;
 #pragma unroll
@@ -740,7 +753,34 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
     //    logits and form the probabilities, wave 0 selects) and broadcasts the picks and weights through its XCD's L2
     //    (st_xcd1); the XCD's other workgroups poll that one line. Only 8 workgroups poll the device-wide logits, which
     //    every router workgroup is writing at the same time.
-    if (li == 0 && wave < 4) {
+    if (a.ext_sel) {
+        // the caller's picks: pick k is slot k (on XCD k); lane 0 also lists the distinct ids in ascending order, each
+        // with its weights summed in k order and its first slot, for the combine (zero sums are dropped, as fl_moe does)
+        if (wave == 0) {
+            LK_LOCAL int * so = reinterpret_cast<LK_LOCAL int *>(lds + M_SEL);
+            LK_LOCAL float * wo = reinterpret_cast<LK_LOCAL float *>(lds + M_SEL + MAXK * 4);
+            int idv = 0; float wv = 0.f;
+            if (lane < MAXK) { idv = gptr(a.ext_sel)[lane]; wv = gptr(a.ext_w)[lane]; so[lane] = idv; wo[lane] = wv; }
+            lds_visible();
+            if (lane == 0) {
+                LK_LOCAL int * xs = reinterpret_cast<LK_LOCAL int *>(lds + M_EXT);
+                LK_LOCAL float * xw = reinterpret_cast<LK_LOCAL float *>(lds + M_EXT + MAXK * 4);
+                int prev = -1, cnt = 0;
+                for (int it = 0; it < MAXK; ++it) {
+                    int m = 0x7fffffff;
+                    for (int k = 0; k < MAXK; ++k) { if (so[k] > prev && so[k] < m) { m = so[k]; } }
+                    if (m == 0x7fffffff) { break; }
+                    float wt = 0.f; int kf = -1;
+                    for (int k = 0; k < MAXK; ++k) { if (so[k] == m) { wt += wo[k]; if (kf < 0) { kf = k; } } }
+                    prev = m;
+                    if (wt == 0.f) { continue; }
+                    xs[cnt] = kf; xw[cnt] = wt; ++cnt;
+                }
+                reinterpret_cast<LK_LOCAL int *>(lds + M_EXT + 2 * MAXK * 4)[0] = cnt;
+            }
+            flag1(ctl + C_READY, 1u);
+        }
+    } else if (li == 0 && wave < 4) {
         __builtin_amdgcn_s_setprio(3);
         const bool ok = select4(a, lds, wave, ctl);
         __builtin_amdgcn_s_setprio(0);
@@ -879,7 +919,7 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
     combine1<FD != 0>(a, lds);
     if (wave == 0 && __hip_atomic_load(ctl + C_CMBFAIL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) { report1(a, 16); }
     TRACE1(10);
-    if (blockIdx.x == 0 && wave == W1 - 1) { routing1(a, lds); }
+    if (blockIdx.x == 0 && wave == W1 - 1 && !a.ext_sel) { routing1(a, lds); }
 }
 
 size_t decode1_lds_bytes() { return DEC1_LDS; }
@@ -914,7 +954,8 @@ hipError_t decode1_init(int ncu, int * ok) {
 }
 
 hipError_t launch_moe_decode1(const DecodeArgs & a, bool cooperative, hipStream_t st) {
-    if (a.n != 1 || a.topk != MAXK || a.keep != MAXK || !decode_rule_ok(a.n_exp, a.n_group) || a.E != E1 || a.H != H1 ||
+    if (a.ext_sel && (!a.ext_w || !a.moe_out || !a.resid || a.prenorm)) { return hipErrorInvalidValue; }   // the caller's picks
+    if (a.n != 1 || a.topk != MAXK || a.keep != MAXK || (!a.ext_sel && !decode_rule_ok(a.n_exp, a.n_group)) || a.E != E1 || a.H != H1 ||
         !a.th || !a.to || !a.tlogits || a.n_exp > NEXP_MAX || (a.kdown != 0 && a.kdown != KF_Q2K && a.kdown != KF_Q3K) ||
         (a.kdown != 0 && ((reinterpret_cast<uintptr_t>(a.down) | reinterpret_cast<uintptr_t>(a.sh_gate) |
                            reinterpret_cast<uintptr_t>(a.sh_up) | reinterpret_cast<uintptr_t>(a.sh_down) | a.dstride) & 3u))) {

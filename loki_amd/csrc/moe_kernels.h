@@ -18,6 +18,15 @@ hipError_t launch_router_select(const float * logits, const float * bias, int n,
                                 int topk, float scale, float * probs, int * sel, float * wts, hipStream_t st, int keep = 0,
                                 float renorm = 0.f);
 
+// both in one launch for n <= 8 tokens and K = 7168 (router_fused_ok): the last workgroup to finish its logits selects,
+// reading the others' logits as epoch-tagged words tl [n][n_exp] (zero or older epochs before the launch). cnt: a
+// device word that is zero before the launch and left zero; done (may be null): host memory set to epoch once sel and
+// wts are written (system scope)
+bool router_fused_ok(int n, int K);
+hipError_t launch_router_fused(const float * W, const float * x, int n, int n_exp, int K, float * logits, const float * bias, int n_group,
+                               int topk_group, int topk, float scale, float * probs, int * sel, float * wts, uint64_t * tl,
+                               unsigned epoch, unsigned * cnt, unsigned * done, hipStream_t st, int keep = 0, float renorm = 0.f);
+
 // stable counting sort of the P = n*topk pairs by expert: counts [n_exp], offsets [n_exp+1], perm/inv [P],
 // act = used experts ascending, nact = their number (device scalar)
 hipError_t launch_dispatch(const int * sel, int P, int n_exp, int * counts, int * offsets, int * perm, int * inv,
@@ -61,6 +70,11 @@ struct DecodeArgs {
     // in that K-quant and the shared expert in Q5_K / Q5_K / Q6_K, ggml's block layout read in place, routed down
     // expert e at down + e * dstride
     int kdown; size_t dstride;
+    // the one-token kernel only: the caller's picks (8 expert ids and weights on the device; null: the kernel routes).
+    // Then the router and the selection are skipped and the combine is the reference fl_moe's (distinct ids ascending,
+    // their weights summed in k order): moe_out = that sum, y = (moe_out + shared) + resid
+    // (o_out, may be null: the 8 slots' outputs [slot][E], for the reference's per-slot attribution)
+    const int * ext_sel; const float * ext_w; float * moe_out; float * o_out;
     int E, H;                                        // 7168, 2048 (the kernel's geometry)
     int8_t * xq; float * xd;                         // Q8_K of x (written by workgroup 0)
     float * logits, * probs; int * sel; float * wts; int * counts, * offsets, * perm, * inv, * act, * nact;

@@ -36,11 +36,10 @@ __global__ void __launch_bounds__(64) k_router_logits(const float * __restrict__
 // products, one rounding each), tree levels 1-6 are lane butterflies inside the wave (chunks 64 q .. 64 q + 63 of wave
 // q), and levels 7-8 add the four waves' totals as (q0 + q1) + (q2 + q3) through LDS. Four tokens per pass.
 constexpr int RW_MAXN = 256;
-__global__ void __launch_bounds__(256) k_router_wg(const float * __restrict__ W, const float * __restrict__ x, int n, int n_exp,
-                                                   float * __restrict__ logits) {
+__device__ __forceinline__ void router_wg_logits(const float * __restrict__ W, const float * __restrict__ x, int n, int n_exp,
+                                                 float * __restrict__ logits, double (*part)[4]) {
 #pragma clang fp contract(off)
     constexpr int CL = 28;
-    __shared__ double part[RW_MAXN][4];
     const int e = blockIdx.x, c = threadIdx.x, q = c >> 6, lane = c & 63;
     float wv[CL];
 #pragma unroll
@@ -76,6 +75,77 @@ __global__ void __launch_bounds__(256) k_router_wg(const float * __restrict__ W,
     }
     __syncthreads();
     if (c < n) { logits[(size_t) c * n_exp + e] = (float) ((part[c][0] + part[c][1]) + (part[c][2] + part[c][3])); }
+}
+__global__ void __launch_bounds__(256) k_router_wg(const float * __restrict__ W, const float * __restrict__ x, int n, int n_exp,
+                                                   float * __restrict__ logits) {
+    __shared__ double part[RW_MAXN][4];
+    router_wg_logits(W, x, n, n_exp, logits, part);
+}
+
+// A few tokens (n <= RF_MAXN): k_router_wg's logits, then k_router_select's rule for every token in the workgroup that
+// finishes last (wave q selects tokens q, q + 4, ..), so the routing is one launch. The logits reach that workgroup as
+// epoch-tagged words tl [n][n_exp] (agent-scope stores and loads, polled until they carry this launch's epoch) and the
+// workgroups count themselves on cnt (zero before the launch, reset by the last one): no memory fences, which cost an
+// L2 write-back per workgroup. Wave 0 writes every token's picks, then (done != null) one system-scope release and
+// done = epoch, so the host can read them from host memory without waiting for the stream. A poll that times out
+// (stores that never land) leaves the picks -1.
+constexpr int RF_MAXN = 8, RF_POLL = 1 << 20;
+__global__ void __launch_bounds__(256) k_router_wg_sel(const float * __restrict__ W, const float * __restrict__ x, int n, int n_exp,
+                                                       float * __restrict__ logits, const float * __restrict__ bias, int n_group,
+                                                       int topk_group, int topk, float scale, int keep, float renorm,
+                                                       float * __restrict__ probs, int * __restrict__ sel, float * __restrict__ wts,
+                                                       uint64_t * tl, unsigned epoch, unsigned * cnt, unsigned * done) {
+    __shared__ double part[RF_MAXN][4];
+    __shared__ float scr[4][NEXP_MAX + 2 * 64];
+    __shared__ int so[RF_MAXN][MAXK]; __shared__ float wo[RF_MAXN][MAXK];
+    __shared__ unsigned last;
+    router_wg_logits(W, x, n, n_exp, logits, part);
+    const int e0 = blockIdx.x, c = threadIdx.x;
+    if (c < n) {   // the same logit again as a tagged word (part[] is final after router_wg_logits' barrier)
+        const float v = (float) ((part[c][0] + part[c][1]) + (part[c][2] + part[c][3]));
+        __hip_atomic_store(gptr(tl) + (size_t) c * n_exp + e0, ((uint64_t) epoch << 32) | __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (c == 0) { last = atomicAdd(cnt, 1u) == gridDim.x - 1; }
+    __syncthreads();
+    if (!last) { return; }
+    const int q = c >> 6, lane = c & 63;
+    if (c == 0) { *cnt = 0u; }
+    float bv[4];
+    load_bias(bias, n_exp, bv);
+    for (int t = q; t < n; t += 4) {
+        uint64_t w[4];
+        bool ok = false;
+        for (int it = 0; it < RF_POLL && !ok; ++it) {
+            ok = true;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int e = 4 * lane + j;
+                w[j] = e < n_exp ? __hip_atomic_load(gptr(tl) + (size_t) t * n_exp + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+                ok = ok && (e >= n_exp || (unsigned) (w[j] >> 32) == epoch);
+            }
+            ok = __ballot(!ok) == 0;
+            if (!ok) { __builtin_amdgcn_s_sleep(1); }
+        }
+        if (!ok) {   // unreachable unless stores are lost: no picks rather than wrong ones
+            if (lane < keep) { so[t][lane] = -1; wo[t][lane] = 0.f; }
+            continue;
+        }
+        float lg[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { lg[j] = __builtin_bit_cast(float, (uint32_t) w[j]); }
+        select_token(lg, bv, n_exp, n_group, topk_group, topk, scale, scr[q], so[t], wo[t], probs ? probs + (size_t) t * n_exp : nullptr,
+                     keep, renorm);
+    }
+    __syncthreads();
+    if (q == 0) {
+        for (int i = lane; i < n * keep; i += 64) { sel[i] = so[i / keep][i % keep]; wts[i] = wo[i / keep][i % keep]; }
+        if (done) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");   // system scope: the picks before the word
+            if (lane == 0) { __hip_atomic_store(gptr(done), epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); }
+        }
+    }
 }
 
 // Large batches (K = 7168): register tiles. Lane (tg, eg) = (lane / 8, lane % 8) owns the logits of TT tokens x EE
@@ -376,14 +446,30 @@ __global__ void __launch_bounds__(64) k_router_select(const float * __restrict__
     if (lane < keep) { sel[(size_t) t * keep + lane] = so[lane]; wts[(size_t) t * keep + lane] = wo[lane]; }
 }
 
+static bool select_rule_ok(int n_exp, int n_group, int topk_group, int topk, int keep) {
+    return !(n_exp > NEXP_MAX || n_exp % n_group || topk > MAXK || topk_group > n_group || topk > topk_group * (n_exp / n_group) ||
+             n_exp / n_group < 2 || n_group > 64 || keep > topk);
+}
+
+bool router_fused_ok(int n, int K) { return n >= 1 && n <= RF_MAXN && K == 7168; }
+
+hipError_t launch_router_fused(const float * W, const float * x, int n, int n_exp, int K, float * logits, const float * bias, int n_group,
+                               int topk_group, int topk, float scale, float * probs, int * sel, float * wts, uint64_t * tl,
+                               unsigned epoch, unsigned * cnt, unsigned * done, hipStream_t st, int keep, float renorm) {
+    if (keep <= 0) { keep = topk; }
+    if (!router_fused_ok(n, K) || !cnt || !tl || epoch == 0 || !select_rule_ok(n_exp, n_group, topk_group, topk, keep)) {
+        return hipErrorInvalidValue;
+    }
+    k_router_wg_sel<<<dim3(n_exp), 256, 0, st>>>(W, x, n, n_exp, logits, bias, n_group, topk_group, topk, scale, keep, renorm, probs, sel,
+                                                 wts, tl, epoch, cnt, done);
+    return hipGetLastError();
+}
+
 hipError_t launch_router_select(const float * logits, const float * bias, int n, int n_exp, int n_group, int topk_group,
                                 int topk, float scale, float * probs, int * sel, float * wts, hipStream_t st, int keep, float renorm) {
     if (n <= 0) { return hipSuccess; }
     if (keep <= 0) { keep = topk; }
-    if (n_exp > NEXP_MAX || n_exp % n_group || topk > MAXK || topk_group > n_group || topk > topk_group * (n_exp / n_group) ||
-        n_exp / n_group < 2 || n_group > 64 || keep > topk) {
-        return hipErrorInvalidValue;
-    }
+    if (!select_rule_ok(n_exp, n_group, topk_group, topk, keep)) { return hipErrorInvalidValue; }
     k_router_select<<<n, 64, 0, st>>>(logits, bias, n, n_exp, n_group, topk_group, topk, scale, keep, renorm, probs, sel, wts);
     return hipGetLastError();
 }

@@ -296,3 +296,56 @@ def test_narrow_pass_keep2_with_pad_rows(ctx, small_layer):
         assert np.array_equal(moe[t].view(np.uint32), v.view(np.uint32)), t
         want = ((v + ref["sh"][t]).astype(np.float32) + fi[t]).astype(np.float32)
         assert np.array_equal(h[t].view(np.uint32), want.view(np.uint32)), t
+
+
+@pytest.mark.parametrize("case", ["picks", "repeats"])
+def test_narrow_one_row_single_launch(ctx, small_layer, case):
+    """fl_moe on one row with all 8 picks runs as one launch of the one-token kernel on the caller's picks (router and
+    selection skipped, the shared expert recomputed in the launch, fl_moe's combine: the distinct ids ascending with
+    their weights summed in k order, zero sums dropped). h and moe are bit-identical to the per-pass kernels and to the
+    checker's experts combined by that rule; "repeats" gives the row a repeated id and a zero weight."""
+    from loki_amd import FLOut, lib
+    (W, b, gate, up, down, sh), dev = small_layer
+    ctx.set_routing(8, 4, 8, 2.5)
+    x = gen.uniform(11, 3, (1, E), 2.0); fi = gen.uniform(11, 4, (1, E), 1.0)
+    flw = _flw(dev)
+    out = FLOut()
+    _, _, so, wo = orc.router(W, b, x, 8, 4, 8, 2.5)
+    ids = so[0].astype(np.int32).copy(); wts = f32(wo[0]).copy()
+    if case == "repeats":
+        ids[3] = ids[1]; wts[5] = np.float32(0)
+    mo = gen.uniform(11, 5, (1, E), 3.0)
+    got = {}
+    for mode in (2, 0):   # 2: the library default (the one-token kernel); 0: the per-pass kernels
+        with ctx.using_fused(mode):
+            ctx.check(lib().fl_ffn_begin(ctx.ctx, ctypes.byref(flw), 1, cptr(x), cptr(fi), -1))
+            lib().fl_fetch(ctx.ctx, 1, 1, ctypes.byref(out))
+            lib().fl_moe(ctx.ctx, dev["gate"].data_ptr(), dev["up"].data_ptr(), dev["down"].data_ptr(), 16, 4, cptr(ids), cptr(wts),
+                         KE, 1, ctypes.byref(out))
+            assert ctx.debug().kernel == (2 if mode else 0), mode
+            hm = (np.ctypeslib.as_array(out.h, shape=(E,)).copy(), np.ctypeslib.as_array(out.moe, shape=(E,)).copy())
+            att = np.zeros((KE, E), np.float32)   # the per-slot attribution of that call
+            lib().fl_moe_outs(ctx.ctx, 0, cptr(ids), cptr(wts), KE, cptr(att))
+            lib().fl_skip(ctx.ctx, cptr(mo), 1, ctypes.byref(out))   # needs the shared expert the launch did not keep
+            got[mode] = hm + (att, np.ctypeslib.as_array(out.h, shape=(E,)).copy())
+    for a_, b_ in zip(got[2], got[0]):
+        assert np.array_equal(a_.view(np.uint32), b_.view(np.uint32)), case
+    ref = orc.moe_experts(x, ids[None, :], wts[None, :], gate, up, down, *sh, want=("o", "sh"), n_exp=16)
+    o = ref["o"].reshape(KE, E)
+    v = np.zeros(E, np.float32)
+    for m in sorted(set(ids.tolist())):
+        ks = [k for k in range(KE) if ids[k] == m]
+        wt = np.float32(0)
+        for k in ks:
+            wt = np.float32(wt + wts[k])
+        if wt == 0:
+            continue
+        v = (v + wt * o[ks[0]]).astype(np.float32)
+    assert np.array_equal(got[2][1].view(np.uint32), v.view(np.uint32))
+    want = ((v + ref["sh"][0]).astype(np.float32) + fi[0]).astype(np.float32)
+    assert np.array_equal(got[2][0].view(np.uint32), want.view(np.uint32))
+    first = [list(ids).index(ids[k]) for k in range(KE)]
+    att = (wts[:, None] * o[first]).astype(np.float32)
+    assert np.array_equal(got[2][2].view(np.uint32), att.view(np.uint32))
+    skip = (((np.float32(0) + mo[0]) + ref["sh"][0]).astype(np.float32) + fi[0]).astype(np.float32)
+    assert np.array_equal(got[2][3].view(np.uint32), skip.view(np.uint32))

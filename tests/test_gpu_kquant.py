@@ -181,6 +181,33 @@ def test_narrow_real_formats(ctx, real_layer, down_fmt, kshared):
         assert ok, err
 
 
+@pytest.mark.parametrize("down_fmt", [orc.Q2K, orc.Q3K], ids=["q2_K", "q3_K"])
+def test_narrow_one_row_real_formats_single_launch(ctx, real_layer, down_fmt):
+    """fl_moe on one row with all 8 picks, routed down Q2_K / Q3_K and the shared expert Q5_K / Q5_K / Q6_K (the real
+    shards' formats): one launch of the one-token kernel's K-quant variant on the caller's picks, h and moe bit-identical
+    to the per-pass kernels (fl_set_fused(0)), on a remapped arena of the picked experts"""
+    from loki_amd import FLOut, lib
+    host, dev = real_layer
+    ctx.set_routing(8, 4, 8, 2.5)
+    ctx.set_shared_formats(orc.Q5K, orc.Q5K, orc.Q6K)
+    x = gen.uniform(13, 3, (1, E), 2.0); fi = gen.uniform(13, 4, (1, E), 1.0)
+    got = {}
+    for mode in (2, 0):
+        with ctx.using_fused(mode):
+            sel, wts = _route(ctx, _flw(dev, True), x, fi)
+            used = sorted(set(sel.ravel().tolist()))
+            remap = {e: i for i, e in enumerate(used)}
+            ids = np.array([remap[e] for e in sel[0]], np.int32)
+            ga, ua, da = _arena(dev, used, down_fmt)
+            out = FLOut()
+            lib().fl_moe(ctx.ctx, ga.data_ptr(), ua.data_ptr(), da.data_ptr(), len(used), down_fmt, cptr(ids), cptr(f32(wts[0])), KE, 1,
+                         ctypes.byref(out))
+            assert ctx.debug().kernel == (2 if mode else 0), mode
+            got[mode] = (np.ctypeslib.as_array(out.h, shape=(E,)).copy(), np.ctypeslib.as_array(out.moe, shape=(E,)).copy())
+    for a_, b_ in zip(got[2], got[0]):
+        assert np.array_equal(a_.view(np.uint32), b_.view(np.uint32)), down_fmt
+
+
 def test_wide_q3k_down(ctx, real_layer):
     """the wide pass (fl_wide_init / fl_ffn_begin(wrow) / fl_wide_moe / fl_wide_finish) with a Q3_K down and the
     K-quant shared expert: 16 experts and top-8 give each expert about 20 of the 320 pairs, so the mat-vec runs several
