@@ -319,8 +319,9 @@ def run_dropin(ctx, torch, steps=60, warmup=5, ggml_steps=3, seed=20260601):
 
 def run_realfmt(ctx, torch, steps=20, warmup=3, copies=2, seed=20260501):
     """fl_moe_layer on the reference's real-shard formats, device-resident: IQ2_XXS routed gate/up (tiled), Q3_K routed
-    down and a Q5_K / Q5_K / Q6_K shared expert read in place (fl_set_layer_formats); decode-8 and decode-1, fresh x per
-    step, layer copies rotated. Algorithmic bytes: U * (2 IQ2_XXS + 1 Q3_K matrix) + the shared expert + the router."""
+    down and a Q5_K / Q5_K / Q6_K shared expert read in place (fl_set_layer_formats); decode-8, decode-1 and prefill-512
+    (routed gate/up on the MFMA GEMM, the K-quants on their mat-vecs), fresh x per step, layer copies rotated.
+    Algorithmic bytes: U * (2 IQ2_XXS + 1 Q3_K matrix) + the shared expert + the router."""
     from loki_amd import MoeLayerWeights
     layers = []
     for c in range(copies):
@@ -332,7 +333,7 @@ def run_realfmt(ctx, torch, steps=20, warmup=3, copies=2, seed=20260501):
     ctx.set_layer_formats(6, 3, 3, 1)
     out = {}
     try:
-        for name, n in (("decode8", 8), ("decode1", 1)):
+        for name, n in (("decode8", 8), ("decode1", 1), ("prefill512", 512)):
             xs = []
             for i in range(steps + warmup):
                 x = torch.empty((n, E), dtype=torch.float32, device="cuda")
@@ -353,6 +354,7 @@ def run_realfmt(ctx, torch, steps=20, warmup=3, copies=2, seed=20260501):
             U = sum(distinct_experts(ctx, layers[(warmup + i) % copies], [xs[warmup + i]])[0] for i in range(steps)) / steps
             b = U * (2 * MAT_BYTES + E * (H // 256) * 110) + 2 * H * (E // 256) * 176 + E * (H // 256) * 210 + ROUTER_BYTES
             out[name] = {"us_per_token": round(ms * 1e3 / n, 2), "ms_per_step": round(ms, 4), "distinct_experts": round(U, 1),
+                         "tokens_per_s": round(n / (ms * 1e-3)),
                          "bytes_per_step": int(b), "hbm_gbs": round(b / (ms * 1e-3) / 1e9, 1),
                          "hbm_frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
             log("[bench] real formats %s: %s" % (name, json.dumps(out[name])))

@@ -378,6 +378,62 @@ static hipError_t kq_one(FLCtx * c, int fmt, const void * w, const int8_t * q, c
     return launch_kq_matvec(k, fmt, n, 1, c->st);
 }
 
+// The shared expert outside the GEMM columns / the routed tasks (fl_moe_layer, formats c->lf), on the context's buffers.
+// Gate/up: h rows P .. P + n - 1 and their Q8_K from the rows' Q8_K (xq / xd): K-quants (src/fused_layer.cu:520-523)
+// by one mat-vec launch for both matrices (or one each) and swiglu_q8k; IQ2_XXS by the per-pass kernel on an empty
+// routed list.
+static int shared_gateup_sep(FLCtx * c, const FLMoeLayer * L, int n, int P, int E, int H, int tk) {
+    hipStream_t st = c->st; const int * lf = c->lf;
+    if (lf[1] == FL_IQ2) {
+        ExpertArgs s = expert_args(c, n, P, 1);
+        s.sh[0] = (const uint8_t *) L->sh_gate; s.sh[1] = (const uint8_t *) L->sh_up; s.aq = c->xq.p; s.ad = c->xd.p; s.K = E; s.R = H; s.nmat = 2;
+        s.act = zero_int(c); s.nact = zero_int(c); s.offsets = zero_int(c); s.perm = zero_int(c); s.topk = tk;
+        s.h = c->h.p; s.hq = c->hq.p; s.hd = c->hd.p;
+        s.gdbg = c->dbg_gu ? c->g.p : nullptr; s.udbg = c->dbg_gu ? c->u.p : nullptr;
+        expert_counters(c, s, 0);
+        TRY(c, launch_experts_gateup(s, c->ncu, st));
+        return FL_OK;
+    }
+    ALLOC(c, c->ksg, (size_t) n * H); ALLOC(c, c->ksu, (size_t) n * H);
+    if (lf[1] == lf[2]) {   // gate and up in one launch
+        KqArgs k{};
+        k.w = (const uint8_t *) L->sh_gate; k.w2 = (const uint8_t *) L->sh_up; k.estride = fmt_mat_bytes(lf[1], H, E);
+        k.aq = c->xq.p; k.ad = c->xd.p; k.K = E; k.R = H; k.n = n; k.out = c->ksg.p; k.out2 = c->ksu.p; k.ldo = H;
+        TRY(c, launch_kq_matvec(k, lf[1], n, 1, st));
+    } else {
+        TRY(c, kq_one(c, lf[1], L->sh_gate, c->xq.p, c->xd.p, n, E, H, c->ksg.p));
+        TRY(c, kq_one(c, lf[2], L->sh_up, c->xq.p, c->xd.p, n, E, H, c->ksu.p));
+    }
+    TRY(c, launch_swiglu_q8k(c->ksg.p, c->ksu.p, n, H, c->h.p + (size_t) P * H, c->hq.p + (size_t) P * H, c->hd.p + (size_t) P * (H / 256), st));
+    if (c->dbg_gu) {
+        TRY(c, hipMemcpyAsync(c->g.p + (size_t) P * H, c->ksg.p, (size_t) n * H * 4, hipMemcpyDeviceToDevice, st));
+        TRY(c, hipMemcpyAsync(c->u.p + (size_t) P * H, c->ksu.p, (size_t) n * H * 4, hipMemcpyDeviceToDevice, st));
+    }
+    return FL_OK;
+}
+// Down: o rows P .. P + n - 1 from h's Q8_K (hq / hd rows P ..): a K-quant mat-vec, or the per-pass kernel alone.
+static int shared_down_sep(FLCtx * c, const FLMoeLayer * L, int n, int P, int E, int H, int tk) {
+    if (c->lf[3] != FL_IQ2) {
+        TRY(c, kq_one(c, c->lf[3], L->sh_down, c->hq.p + (size_t) P * H, c->hd.p + (size_t) P * (H / 256), n, H, E, c->o.p + (size_t) P * E));
+        return FL_OK;
+    }
+    ExpertArgs s = expert_args(c, n, P, 1);
+    s.sh[0] = (const uint8_t *) L->sh_down; s.sh[1] = nullptr; s.aq = c->hq.p; s.ad = c->hd.p; s.K = H; s.R = E; s.nmat = 1;
+    s.act = zero_int(c); s.nact = zero_int(c); s.offsets = zero_int(c); s.perm = zero_int(c); s.topk = tk;
+    s.h = nullptr; s.hq = nullptr; s.hd = nullptr; s.o = c->o.p; s.y = nullptr;
+    expert_counters(c, s, 1);
+    TRY(c, launch_experts_down(s, c->ncu, c->st));
+    return FL_OK;
+}
+// The routed down in a K-quant (src/fused_layer.cu:607-608): o of every routed slot, each active expert's slots in
+// token groups sized for the expected slots per expert (an expert with more runs extra groups).
+static hipError_t routed_down_kq(FLCtx * c, const FLMoeLayer * L, int P, int E, int H, int ne) {
+    KqArgs k{};
+    k.w = (const uint8_t *) L->down_exps; k.estride = fmt_mat_bytes(c->lf[0], E, H); k.aq = c->hq.p; k.ad = c->hd.p; k.K = H; k.R = E;
+    k.act = c->act.p; k.nact = c->nact.p; k.offsets = c->offsets.p; k.out = c->o.p; k.ldo = E;
+    return launch_kq_matvec(k, c->lf[0], (P + ne - 1) / ne, ne < P ? ne : P, c->st);
+}
+
 static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, float * y, bool prenorm, const float * nw, float eps,
                      const float * resid) {
     if (!c) { return FL_EINVAL; }
@@ -416,14 +472,17 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
         if (prenorm && !(eps >= 0.f)) { return fail(c, FL_EINVAL, "bad norm eps %g", (double) eps); }
     }
     const size_t rows = (size_t) P + n;
-    // K-quant matrices run on the per-pass path (the decode block and the MFMA GEMMs read IQ2_XXS tiles), except for
+    // K-quant matrices: at decode sizes the per-pass path (the n <= 8 decode block reads IQ2_XXS tiles), except for
     // one token on the real shards' formats (routed down Q2_K / Q3_K, shared expert Q5_K / Q5_K / Q6_K), which the
-    // one-token kernel reads in place
+    // one-token kernel reads in place; at prefill sizes the routed gate/up (always IQ2_XXS) on the MFMA GEMM and the
+    // K-quant matrices on the K-quant mat-vecs
     static_assert(FL_Q6K == 1 && FL_Q5K == 3 && FL_Q2K == 5 && FL_Q3K == 6, "the FL_ codes are the K-quant kernels' format codes");
     const int kd1 = (lf[0] == FL_Q2K || lf[0] == FL_Q3K) && lf[1] == FL_Q5K && lf[2] == FL_Q5K && lf[3] == FL_Q6K ? lf[0] : 0;
     const bool kq1 = kq && kd1 != 0 && n == 1 && tsel == MAXK && tk == MAXK && decode1_ready(c);
     const bool fused = (!kq || kq1) && c->fused && n <= 8 && E == 7168 && H == 2048 && decode_rule_ok(ne, c->n_group) && decode_ready(c);
-    const bool mfma = !kq && !fused && c->pf_mfma && n > 8 && E == 7168 && H == 2048;
+    const bool mfma = !fused && c->pf_mfma && n > 8 && E == 7168 && H == 2048;
+    // the shared expert as GEMM columns when all of it is IQ2_XXS; otherwise its own kernels (shared_*_sep below)
+    const bool shc = lf[1] == FL_IQ2 && lf[3] == FL_IQ2;
     ALLOC(c, c->xq, (size_t) n * E); ALLOC(c, c->xd, (size_t) n * (E / 256));
     ALLOC(c, c->logits, (size_t) n * ne); ALLOC(c, c->probs, (size_t) n * ne);
     ALLOC(c, c->sel, P); ALLOC(c, c->wts, P); ALLOC(c, c->perm, P); ALLOC(c, c->inv, P);
@@ -481,7 +540,7 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     prof_mark(c, ev, 3);
     TRY(c, launch_dispatch(c->sel.p, P, ne, c->counts.p, c->offsets.p, c->perm.p, c->inv.p, c->act.p, c->nact.p, st));
     if (mfma) {
-        TRY(c, launch_prefill_cols(c->act.p, c->nact.p, c->offsets.p, n, P, c->pcols.p, c->pncols.p, st));
+        TRY(c, launch_prefill_cols(c->act.p, c->nact.p, c->offsets.p, shc ? n : 0, P, c->pcols.p, c->pncols.p, st));
         prof_mark(c, ev, 4);
         PrefillArgs g{};
         g.ptab = c->ptab.p; g.w[0] = (const uint8_t *) L->gate_exps; g.w[1] = (const uint8_t *) L->up_exps;
@@ -490,13 +549,21 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
         g.bh = c->xh.p; g.bd = c->xd.p; g.out = c->h.p; g.gdbg = c->dbg_gu ? c->g.p : nullptr; g.udbg = c->dbg_gu ? c->u.p : nullptr;
         g.err = c->derr.p; g.herr = c->herr ? c->herr_dev : nullptr;
         TRY(c, launch_prefill_gemm(g, c->ncu, st));
+        if (!shc) { if (int rc = shared_gateup_sep(c, L, n, P, E, H, tk)) { return rc; } }   // h rows P .. P + n - 1
         TRY(c, launch_quant_q8k(c->h.p, (int64_t) rows, H, c->hq.p, c->hd.p, st));
-        TRY(c, launch_q8_to_h(c->hq.p, c->hh.p, (int64_t) rows * H, st));
+        if (lf[0] == FL_IQ2) { TRY(c, launch_q8_to_h(c->hq.p, c->hh.p, (int64_t) rows * H, st)); }
         prof_mark(c, ev, 5);
-        PrefillArgs d = g;
-        d.w[0] = (const uint8_t *) L->down_exps; d.w[1] = nullptr; d.sh[0] = (const uint8_t *) L->sh_down; d.sh[1] = nullptr;
-        d.R = E; d.K = H; d.nmat = 1; d.bh = c->hh.p; d.bd = c->hd.p; d.out = c->o.p; d.gdbg = nullptr; d.udbg = nullptr;
-        TRY(c, launch_prefill_gemm(d, c->ncu, st));
+        if (lf[0] == FL_IQ2) {
+            PrefillArgs d = g;
+            d.w[0] = (const uint8_t *) L->down_exps; d.w[1] = nullptr; d.sh[0] = (const uint8_t *) L->sh_down; d.sh[1] = nullptr;
+            d.R = E; d.K = H; d.nmat = 1; d.bh = c->hh.p; d.bd = c->hd.p; d.out = c->o.p; d.gdbg = nullptr; d.udbg = nullptr;
+            TRY(c, launch_prefill_gemm(d, c->ncu, st));
+        } else {
+            TRY(c, routed_down_kq(c, L, P, E, H, ne));
+        }
+        if (!(shc && lf[0] == FL_IQ2)) {   // o rows P .. P + n - 1 when the down GEMM did not hold them
+            if (int rc = shared_down_sep(c, L, n, P, E, H, tk)) { return rc; }
+        }
         TRY(c, launch_combine(c->o.p, c->inv.p, c->wts.p, n, tk, E, P, resid, y, nullptr, st));
         prof_mark(c, ev, 6);
         return FL_OK;
@@ -512,49 +579,20 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     a.gdbg = c->dbg_gu ? c->g.p : nullptr; a.udbg = c->dbg_gu ? c->u.p : nullptr;
     expert_counters(c, a, 0);
     TRY(c, launch_experts_gateup(a, c->ncu, st));
-    if (ksh) {   // rows P .. P + n - 1 of h / Q8_K(h): the shared expert (src/fused_layer.cu:520-523)
-        ALLOC(c, c->ksg, (size_t) n * H); ALLOC(c, c->ksu, (size_t) n * H);
-        if (lf[1] == lf[2]) {   // gate and up in one launch
-            KqArgs k{};
-            k.w = (const uint8_t *) L->sh_gate; k.w2 = (const uint8_t *) L->sh_up; k.estride = fmt_mat_bytes(lf[1], H, E);
-            k.aq = c->xq.p; k.ad = c->xd.p; k.K = E; k.R = H; k.n = n; k.out = c->ksg.p; k.out2 = c->ksu.p; k.ldo = H;
-            TRY(c, launch_kq_matvec(k, lf[1], n, 1, st));
-        } else {
-            TRY(c, kq_one(c, lf[1], L->sh_gate, c->xq.p, c->xd.p, n, E, H, c->ksg.p));
-            TRY(c, kq_one(c, lf[2], L->sh_up, c->xq.p, c->xd.p, n, E, H, c->ksu.p));
-        }
-        TRY(c, launch_swiglu_q8k(c->ksg.p, c->ksu.p, n, H, c->h.p + (size_t) P * H, c->hq.p + (size_t) P * H, c->hd.p + (size_t) P * (H / 256), st));
-        if (c->dbg_gu) {
-            TRY(c, hipMemcpyAsync(c->g.p + (size_t) P * H, c->ksg.p, (size_t) n * H * 4, hipMemcpyDeviceToDevice, st));
-            TRY(c, hipMemcpyAsync(c->u.p + (size_t) P * H, c->ksu.p, (size_t) n * H * 4, hipMemcpyDeviceToDevice, st));
-        }
-    }
+    if (ksh) { if (int rc = shared_gateup_sep(c, L, n, P, E, H, tk)) { return rc; } }   // h rows P .. P + n - 1
     prof_mark(c, ev, 5);
     if (kq) {   // o of every slot by its matrix's format, then the k-ordered combine (+ shared, + residual)
-        ExpertArgs d = a;
-        d.shared = 0; d.aq = c->hq.p; d.ad = c->hd.p; d.K = H; d.R = E; d.nmat = 1;
-        d.h = nullptr; d.hq = nullptr; d.hd = nullptr; d.gdbg = nullptr; d.udbg = nullptr; d.o = c->o.p; d.y = nullptr;
         if (lf[0] == FL_IQ2) {
+            ExpertArgs d = a;
+            d.shared = 0; d.aq = c->hq.p; d.ad = c->hd.p; d.K = H; d.R = E; d.nmat = 1;
+            d.h = nullptr; d.hq = nullptr; d.hd = nullptr; d.gdbg = nullptr; d.udbg = nullptr; d.o = c->o.p; d.y = nullptr;
             d.w[0] = (const uint8_t *) L->down_exps; d.w[1] = nullptr; d.sh[0] = nullptr; d.sh[1] = nullptr;
             expert_counters(c, d, 1);
             TRY(c, launch_experts_down(d, c->ncu, st));
-        } else {   // src/fused_layer.cu:607-608
-            KqArgs k{};
-            k.w = (const uint8_t *) L->down_exps; k.estride = fmt_mat_bytes(lf[0], E, H); k.aq = c->hq.p; k.ad = c->hd.p; k.K = H; k.R = E;
-            k.act = c->act.p; k.nact = c->nact.p; k.offsets = c->offsets.p; k.out = c->o.p; k.ldo = E;
-            // token groups sized for the expected slots per expert (an expert with more runs extra groups)
-            TRY(c, launch_kq_matvec(k, lf[0], (P + ne - 1) / ne, ne < P ? ne : P, st));
-        }
-        if (lf[3] == FL_IQ2) {   // the shared expert alone: an empty routed list, its slots P ..
-            ExpertArgs s = expert_args(c, n, P, 1);
-            s.sh[0] = (const uint8_t *) L->sh_down; s.sh[1] = nullptr; s.aq = c->hq.p; s.ad = c->hd.p; s.K = H; s.R = E; s.nmat = 1;
-            s.act = zero_int(c); s.nact = zero_int(c); s.offsets = zero_int(c); s.perm = zero_int(c); s.topk = tk;
-            s.h = nullptr; s.hq = nullptr; s.hd = nullptr; s.o = c->o.p; s.y = nullptr;
-            expert_counters(c, s, 1);
-            TRY(c, launch_experts_down(s, c->ncu, st));
         } else {
-            TRY(c, kq_one(c, lf[3], L->sh_down, c->hq.p + (size_t) P * H, c->hd.p + (size_t) P * (H / 256), n, H, E, c->o.p + (size_t) P * E));
+            TRY(c, routed_down_kq(c, L, P, E, H, ne));
         }
+        if (int rc = shared_down_sep(c, L, n, P, E, H, tk)) { return rc; }
         TRY(c, launch_combine(c->o.p, c->inv.p, c->wts.p, n, tk, E, P, resid, y, nullptr, st));
         prof_mark(c, ev, 6);
         return FL_OK;

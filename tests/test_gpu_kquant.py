@@ -341,3 +341,64 @@ def test_decode1_real_formats(ctx, down_fmt):
         ctx.set_layer_formats()
     del layer, base, down, sh
     torch.cuda.empty_cache()
+
+
+# (routed down, shared gate, up, down): the real shards'; a K-quant routed down with the shared expert in IQ2_XXS (GEMM
+# columns); a K-quant shared expert beside an IQ2_XXS routed down (the down GEMM); an IQ2_XXS shared gate/up with a
+# Q6_K shared down (the shared gate/up on the per-pass kernel)
+PF_FMTS = [(orc.Q3K, orc.Q5K, orc.Q5K, orc.Q6K), (orc.Q2K, 4, 4, 4), (4, orc.Q5K, orc.Q5K, orc.Q6K), (4, 4, 4, orc.Q6K)]
+
+
+@pytest.mark.parametrize("n", [40, 512])
+@pytest.mark.parametrize("fm", PF_FMTS, ids=["q3k_q5q5q6", "q2k_iq2", "iq2_q5q5q6", "iq2_iq2iq2q6"])
+def test_prefill_mixed_formats_mfma(ctx, fm, n):
+    """fl_moe_layer at prefill sizes with K-quant matrices: the routed gate/up on the MFMA GEMM (the shared expert's
+    columns only when all of it is IQ2_XXS) and the K-quant matrices on their mat-vecs give g, u, h and its Q8_K, o and
+    y bit-identical to the per-pass kernels (fl_set_prefill_mfma(0)). A 64-expert layer; the real shards' formats are
+    also checked against the CPU checker on sampled rows."""
+    import torch
+    from loki_amd import MoeLayerWeights
+    from tests._helpers import make_x, host_matrix
+    ne = 64
+    seed = 8200 + 10 * PF_FMTS.index(fm)
+    base = MoeLayerWeights.synthetic(ctx, seed, n_exp=ne, bias_sigma=0.05)
+    down = _kq_device(torch, fm[0], ne * E, H, seed + 1) if fm[0] != 4 else base.down
+    shg = _kq_device(torch, fm[1], H, E, seed + 2) if fm[1] != 4 else base.sh_gate
+    shu = _kq_device(torch, fm[2], H, E, seed + 3) if fm[2] != 4 else base.sh_up
+    shd = _kq_device(torch, fm[3], E, H, seed + 4) if fm[3] != 4 else base.sh_down
+    layer = MoeLayerWeights(base.gate_inp, base.probs_b, base.gate, base.up, down, shg, shu, shd, n_exp=ne)
+    x = make_x(ctx, n, seed=seed + 5)
+    ctx.set_layer_formats(*fm)
+    got = {}
+    try:
+        for mfma in (True, False):
+            print("prefill mixed formats %s n %d mfma %d" % (fm, n, mfma), flush=True)
+            ctx.set_prefill_mfma(mfma)
+            ctx.set_debug(True)
+            y = ctx.moe_layer(layer, x).clone()
+            ctx.sync()
+            d = ctx.debug()
+            P = d.P
+            got[mfma] = {"y": y.cpu().numpy(), "h": ctx.d2h(d.h, (P + n, H), np.float32), "o": ctx.d2h(d.o, (P + n, E), np.float32),
+                         "g": ctx.d2h(d.g, (P + n, H), np.float32), "u": ctx.d2h(d.u, (P + n, H), np.float32),
+                         "hd": ctx.d2h(d.hd, (P + n, H // 256), np.float32), "hq": ctx.d2h(d.hq, (P + n, H), np.int8),
+                         "sel": ctx.d2h(d.sel, (n, KE), np.int32), "wts": ctx.d2h(d.wts, (n, KE), np.float32)}
+            ctx.set_debug(False)
+    finally:
+        ctx.set_debug(False); ctx.set_prefill_mfma(True); ctx.set_layer_formats()
+    for k in got[False]:
+        assert np.array_equal(got[True][k].view(np.uint8), got[False][k].view(np.uint8)), k
+    if fm == PF_FMTS[0]:   # sampled rows against the checker
+        rows = np.array([0, 1, n // 2, n - 1])
+        xs = x.cpu().numpy()[rows]
+        so, wo = got[True]["sel"][rows], got[True]["wts"][rows]
+        sel = sorted(set(int(e) for e in so.ravel()))
+        mb = E * (H // 256) * KQ_BLOCK[fm[0]][0]
+        gate = {e: host_matrix(ctx, layer.expert_slice("gate", e), H, E) for e in sel}
+        up = {e: host_matrix(ctx, layer.expert_slice("up", e), H, E) for e in sel}
+        dn = {e: down[e * mb:(e + 1) * mb].cpu().numpy() for e in sel}
+        ref = orc.moe_experts(xs, so, wo, gate, up, dn, shg.cpu().numpy(), shu.cpu().numpy(), shd.cpu().numpy(), n_exp=ne, fmts=fm)["y"]
+        ok, err = bar_close(got[True]["y"][rows], ref)
+        assert ok, err
+    del layer, base, down, shg, shu, shd
+    torch.cuda.empty_cache()
