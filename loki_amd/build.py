@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIBDIR = os.path.join(HERE, "_lib")
 LIB = os.path.join(LIBDIR, "libloki_moe.so")
-SOURCES = ["quant.hip", "router.hip", "dispatch.hip", "iq2_gemv.hip", "moe_decode.hip", "moe_decode1.hip", "moe_prefill.hip", "pack.hip", "kquant.hip", "gguf.hip", "fused_layer.hip", "compat.hip"]
+SOURCES = ["quant.hip", "router.hip", "dispatch.hip", "iq2_gemv.hip", "moe_decode.hip", "moe_decode1.hip", "moe_prefill.hip", "pack.hip", "kquant.hip", "kq_gemm.hip", "gguf.hip", "fused_layer.hip", "compat.hip"]
 HEADERS = ["moe_common.h", "moe_device.h", "moe_kernels.h", "fl_ctx.h", "iq2xxs_grid.inc"]
 ARCH = os.environ.get("LOKI_OFFLOAD_ARCH", "gfx950")
 

@@ -519,6 +519,7 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
             ALLOC(c, c->ptab, prefill_table_bytes() / 16);
             TRY(c, build_prefill_tables(c->ptab.p, st));
             TRY(c, prefill_init());
+            TRY(c, kq_gemm_init());
             if (!c->derr.p) { ALLOC(c, c->derr, 1); TRY(c, hipMemsetAsync(c->derr.p, 0, sizeof(int), st)); }
             c->pf_ready = 1;
         }
@@ -551,15 +552,19 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
         TRY(c, launch_prefill_gemm(g, c->ncu, st));
         if (!shc) { if (int rc = shared_gateup_sep(c, L, n, P, E, H, tk)) { return rc; } }   // h rows P .. P + n - 1
         TRY(c, launch_quant_q8k(c->h.p, (int64_t) rows, H, c->hq.p, c->hd.p, st));
-        if (lf[0] == FL_IQ2) { TRY(c, launch_q8_to_h(c->hq.p, c->hh.p, (int64_t) rows * H, st)); }
+        TRY(c, launch_q8_to_h(c->hq.p, c->hh.p, (int64_t) rows * H, st));
         prof_mark(c, ev, 5);
         if (lf[0] == FL_IQ2) {
             PrefillArgs d = g;
             d.w[0] = (const uint8_t *) L->down_exps; d.w[1] = nullptr; d.sh[0] = (const uint8_t *) L->sh_down; d.sh[1] = nullptr;
             d.R = E; d.K = H; d.nmat = 1; d.bh = c->hh.p; d.bd = c->hd.p; d.out = c->o.p; d.gdbg = nullptr; d.udbg = nullptr;
             TRY(c, launch_prefill_gemm(d, c->ncu, st));
-        } else {
-            TRY(c, routed_down_kq(c, L, P, E, H, ne));
+        } else {   // Q2_K / Q3_K on the matrix cores (kq_gemm.hip), the same columns
+            PrefillArgs d = g;
+            d.w[0] = (const uint8_t *) L->down_exps; d.w[1] = nullptr; d.sh[0] = nullptr; d.sh[1] = nullptr;
+            d.estride = fmt_mat_bytes(lf[0], E, H); d.R = E; d.K = H; d.nmat = 1; d.bh = c->hh.p; d.bd = c->hd.p; d.out = c->o.p;
+            d.gdbg = nullptr; d.udbg = nullptr;
+            TRY(c, launch_kq_gemm(d, lf[0], c->ncu, st));
         }
         if (!(shc && lf[0] == FL_IQ2)) {   // o rows P .. P + n - 1 when the down GEMM did not hold them
             if (int rc = shared_down_sep(c, L, n, P, E, H, tk)) { return rc; }

@@ -124,6 +124,13 @@ hipError_t launch_prefill_cols(const int * act, const int * nact, const int * of
 hipError_t launch_q8_to_h(const int8_t * q, _Float16 * h, int64_t n, hipStream_t st);
 hipError_t launch_prefill_gemm(const PrefillArgs & a, int grid, hipStream_t st);
 
+// the routed down in Q2_K / Q3_K (fmt = KF_Q2K / KF_Q3K, ggml's blocks read in place, expert e at w[0] + e * estride)
+// on the matrix cores (kq_gemm.hip): the routed columns of launch_prefill_cols (shared ones skipped), activations bh / bd
+// = Q8_K of h as fp16 [slots][K] and its scales, o [slots][R] into out; K = 2048, R % 128 == 0. Bit-identical to
+// launch_kq_matvec.
+hipError_t kq_gemm_init();
+hipError_t launch_kq_gemm(const PrefillArgs & a, int fmt, int grid, hipStream_t st);
+
 // y[t] = sum_k (o[inv[t*topk+k]] * w[t][k]) in k order + o[P+t] (+ resid[t] when given)
 hipError_t launch_combine(const float * o, const int * inv, const float * wts, int n, int topk, int E, int P,
                           const float * resid, float * y, float * moe, hipStream_t st);
