@@ -382,6 +382,16 @@ static hipError_t kq_one(FLCtx * c, int fmt, const void * w, const int8_t * q, c
 // Gate/up: h rows P .. P + n - 1 and their Q8_K from the rows' Q8_K (xq / xd): K-quants (src/fused_layer.cu:520-523)
 // by one mat-vec launch for both matrices (or one each) and swiglu_q8k; IQ2_XXS by the per-pass kernel on an empty
 // routed list.
+// h = silu(g) * u of the shared expert's K-quant gate / up outputs (ksg, ksu) into rows P .. P + n - 1 of h and Q8_K(h)
+static int shared_swiglu(FLCtx * c, int n, int P, int H) {
+    hipStream_t st = c->st;
+    TRY(c, launch_swiglu_q8k(c->ksg.p, c->ksu.p, n, H, c->h.p + (size_t) P * H, c->hq.p + (size_t) P * H, c->hd.p + (size_t) P * (H / 256), st));
+    if (c->dbg_gu) {
+        TRY(c, hipMemcpyAsync(c->g.p + (size_t) P * H, c->ksg.p, (size_t) n * H * 4, hipMemcpyDeviceToDevice, st));
+        TRY(c, hipMemcpyAsync(c->u.p + (size_t) P * H, c->ksu.p, (size_t) n * H * 4, hipMemcpyDeviceToDevice, st));
+    }
+    return FL_OK;
+}
 static int shared_gateup_sep(FLCtx * c, const FLMoeLayer * L, int n, int P, int E, int H, int tk) {
     hipStream_t st = c->st; const int * lf = c->lf;
     if (lf[1] == FL_IQ2) {
@@ -404,12 +414,7 @@ static int shared_gateup_sep(FLCtx * c, const FLMoeLayer * L, int n, int P, int 
         TRY(c, kq_one(c, lf[1], L->sh_gate, c->xq.p, c->xd.p, n, E, H, c->ksg.p));
         TRY(c, kq_one(c, lf[2], L->sh_up, c->xq.p, c->xd.p, n, E, H, c->ksu.p));
     }
-    TRY(c, launch_swiglu_q8k(c->ksg.p, c->ksu.p, n, H, c->h.p + (size_t) P * H, c->hq.p + (size_t) P * H, c->hd.p + (size_t) P * (H / 256), st));
-    if (c->dbg_gu) {
-        TRY(c, hipMemcpyAsync(c->g.p + (size_t) P * H, c->ksg.p, (size_t) n * H * 4, hipMemcpyDeviceToDevice, st));
-        TRY(c, hipMemcpyAsync(c->u.p + (size_t) P * H, c->ksu.p, (size_t) n * H * 4, hipMemcpyDeviceToDevice, st));
-    }
-    return FL_OK;
+    return shared_swiglu(c, n, P, H);
 }
 // Down: o rows P .. P + n - 1 from h's Q8_K (hq / hd rows P ..): a K-quant mat-vec, or the per-pass kernel alone.
 static int shared_down_sep(FLCtx * c, const FLMoeLayer * L, int n, int P, int E, int H, int tk) {
@@ -481,8 +486,6 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     const bool kq1 = kq && kd1 != 0 && n == 1 && tsel == MAXK && tk == MAXK && decode1_ready(c);
     const bool fused = (!kq || kq1) && c->fused && n <= 8 && E == 7168 && H == 2048 && decode_rule_ok(ne, c->n_group) && decode_ready(c);
     const bool mfma = !fused && c->pf_mfma && n > 8 && E == 7168 && H == 2048;
-    // the shared expert as GEMM columns when all of it is IQ2_XXS; otherwise its own kernels (shared_*_sep below)
-    const bool shc = lf[1] == FL_IQ2 && lf[3] == FL_IQ2;
     ALLOC(c, c->xq, (size_t) n * E); ALLOC(c, c->xd, (size_t) n * (E / 256));
     ALLOC(c, c->logits, (size_t) n * ne); ALLOC(c, c->probs, (size_t) n * ne);
     ALLOC(c, c->sel, P); ALLOC(c, c->wts, P); ALLOC(c, c->perm, P); ALLOC(c, c->inv, P);
@@ -541,32 +544,54 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     prof_mark(c, ev, 3);
     TRY(c, launch_dispatch(c->sel.p, P, ne, c->counts.p, c->offsets.p, c->perm.p, c->inv.p, c->act.p, c->nact.p, st));
     if (mfma) {
-        TRY(c, launch_prefill_cols(c->act.p, c->nact.p, c->offsets.p, shc ? n : 0, P, c->pcols.p, c->pncols.p, st));
+        TRY(c, launch_prefill_cols(c->act.p, c->nact.p, c->offsets.p, n, P, c->pcols.p, c->pncols.p, st));
         prof_mark(c, ev, 4);
+        // Columns: the shared expert's first (nsh of them), then the routed experts'. Each matrix runs where its format
+        // does: IQ2_XXS on the IQ2_XXS GEMM, Q2_K / Q3_K / Q6_K downs and a Q5_K shared gate / up on the K-quant GEMM,
+        // any other K-quant on the mat-vecs.
+        const int nsh = prefill_shared_cols(n);
         PrefillArgs g{};
         g.ptab = c->ptab.p; g.w[0] = (const uint8_t *) L->gate_exps; g.w[1] = (const uint8_t *) L->up_exps;
         g.estride = (size_t) H * (E / 256) * IQ2B; g.sh[0] = (const uint8_t *) L->sh_gate; g.sh[1] = (const uint8_t *) L->sh_up;
         g.perm = c->perm.p; g.topk = tk; g.P = P; g.R = H; g.K = E; g.nmat = 2; g.cols = c->pcols.p; g.ncols = c->pncols.p;
         g.bh = c->xh.p; g.bd = c->xd.p; g.out = c->h.p; g.gdbg = c->dbg_gu ? c->g.p : nullptr; g.udbg = c->dbg_gu ? c->u.p : nullptr;
         g.err = c->derr.p; g.herr = c->herr ? c->herr_dev : nullptr;
+        g.col0 = lf[1] == FL_IQ2 ? 0 : nsh;
         TRY(c, launch_prefill_gemm(g, c->ncu, st));
-        if (!shc) { if (int rc = shared_gateup_sep(c, L, n, P, E, H, tk)) { return rc; } }   // h rows P .. P + n - 1
+        if (lf[1] == FL_Q5K && lf[2] == FL_Q5K) {   // the real shards' shared gate / up: ksg / ksu rows 0 .. n - 1
+            ALLOC(c, c->ksg, (size_t) n * H); ALLOC(c, c->ksu, (size_t) n * H);
+            for (int m = 0; m < 2; ++m) {
+                PrefillArgs k{};
+                k.sh[0] = (const uint8_t *) (m ? L->sh_up : L->sh_gate); k.w[0] = k.sh[0];
+                k.R = H; k.K = E; k.cols = c->pcols.p; k.ncols = c->pncols.p; k.col0 = 0; k.col1 = nsh;
+                k.bh = c->xh.p; k.bd = c->xd.p; k.arow0 = P; k.orow0 = P; k.out = m ? c->ksu.p : c->ksg.p;
+                TRY(c, launch_kq_gemm(k, FL_Q5K, c->ncu, st));
+            }
+            if (int rc = shared_swiglu(c, n, P, H)) { return rc; }
+        } else if (lf[1] != FL_IQ2) {
+            if (int rc = shared_gateup_sep(c, L, n, P, E, H, tk)) { return rc; }
+        }
         TRY(c, launch_quant_q8k(c->h.p, (int64_t) rows, H, c->hq.p, c->hd.p, st));
         TRY(c, launch_q8_to_h(c->hq.p, c->hh.p, (int64_t) rows * H, st));
         prof_mark(c, ev, 5);
-        if (lf[0] == FL_IQ2) {
-            PrefillArgs d = g;
-            d.w[0] = (const uint8_t *) L->down_exps; d.w[1] = nullptr; d.sh[0] = (const uint8_t *) L->sh_down; d.sh[1] = nullptr;
-            d.R = E; d.K = H; d.nmat = 1; d.bh = c->hh.p; d.bd = c->hd.p; d.out = c->o.p; d.gdbg = nullptr; d.udbg = nullptr;
+        PrefillArgs d = g;   // the down pass: activations Q8_K(h) of every slot, o rows by slot
+        d.w[0] = (const uint8_t *) L->down_exps; d.w[1] = nullptr; d.sh[0] = (const uint8_t *) L->sh_down; d.sh[1] = nullptr;
+        d.R = E; d.K = H; d.nmat = 1; d.bh = c->hh.p; d.bd = c->hd.p; d.out = c->o.p; d.gdbg = nullptr; d.udbg = nullptr;
+        const bool sh_iq = lf[3] == FL_IQ2, sh_kg = lf[3] == FL_Q2K || lf[3] == FL_Q3K || lf[3] == FL_Q6K;
+        if (lf[0] == FL_IQ2) {   // routed (+ the shared expert when it is IQ2_XXS)
+            d.col0 = sh_iq ? 0 : nsh;
             TRY(c, launch_prefill_gemm(d, c->ncu, st));
-        } else {   // Q2_K / Q3_K on the matrix cores (kq_gemm.hip), the same columns
-            PrefillArgs d = g;
-            d.w[0] = (const uint8_t *) L->down_exps; d.w[1] = nullptr; d.sh[0] = nullptr; d.sh[1] = nullptr;
-            d.estride = fmt_mat_bytes(lf[0], E, H); d.R = E; d.K = H; d.nmat = 1; d.bh = c->hh.p; d.bd = c->hd.p; d.out = c->o.p;
-            d.gdbg = nullptr; d.udbg = nullptr;
-            TRY(c, launch_kq_gemm(d, lf[0], c->ncu, st));
+        } else {
+            PrefillArgs k = d;
+            k.estride = fmt_mat_bytes(lf[0], E, H); k.col0 = nsh;
+            TRY(c, launch_kq_gemm(k, lf[0], c->ncu, st));
+            if (sh_iq) { d.col0 = 0; d.col1 = nsh; TRY(c, launch_prefill_gemm(d, c->ncu, st)); }
         }
-        if (!(shc && lf[0] == FL_IQ2)) {   // o rows P .. P + n - 1 when the down GEMM did not hold them
+        if (sh_kg) {
+            PrefillArgs k = d;
+            k.col0 = 0; k.col1 = nsh;
+            TRY(c, launch_kq_gemm(k, lf[3], c->ncu, st));
+        } else if (!sh_iq) {
             if (int rc = shared_down_sep(c, L, n, P, E, H, tk)) { return rc; }
         }
         TRY(c, launch_combine(c->o.p, c->inv.p, c->wts.p, n, tk, E, P, resid, y, nullptr, st));

@@ -115,19 +115,27 @@ struct PrefillArgs {
     float * gdbg, * udbg;                // optional gate / up outputs
     int * err;                           // bit 4: the LDS base is not 64 KB aligned
     int * herr;                          // host-mapped copy of the code (may be null)
+    // the columns col0 .. col1 - 1 of launch_prefill_cols (col1 <= 0: to the last); the shared expert's come first,
+    // ceil(n / 64) of them
+    int col0, col1;
+    // launch_kq_gemm only: activation row = slot - arow0, output row = slot - orow0 (the shared expert's gate / up
+    // read the tokens' rows and write rows 0 .. n - 1 of their own outputs)
+    int arow0, orow0;
 };
 hipError_t prefill_init();
 size_t prefill_table_bytes();
 hipError_t build_prefill_tables(uint4 * img, hipStream_t st);
 // columns of <= 32 slots of one expert: the shared expert's first, then act order; cols sized >= (n+P)/32 + NEXP_MAX + 2
 hipError_t launch_prefill_cols(const int * act, const int * nact, const int * offsets, int n, int P, int4 * cols, int * ncols, hipStream_t st);
+int prefill_shared_cols(int n);   // the shared expert's columns (the first ones) for n tokens
 hipError_t launch_q8_to_h(const int8_t * q, _Float16 * h, int64_t n, hipStream_t st);
 hipError_t launch_prefill_gemm(const PrefillArgs & a, int grid, hipStream_t st);
 
-// the routed down in Q2_K / Q3_K (fmt = KF_Q2K / KF_Q3K, ggml's blocks read in place, expert e at w[0] + e * estride)
-// on the matrix cores (kq_gemm.hip): the routed columns of launch_prefill_cols (shared ones skipped), activations bh / bd
-// = Q8_K of h as fp16 [slots][K] and its scales, o [slots][R] into out; K = 2048, R % 128 == 0. Bit-identical to
-// launch_kq_matvec.
+// K-quant matrices on the matrix cores (kq_gemm.hip), bit-identical to launch_kq_matvec: columns col0 .. col1 - 1 of
+// launch_prefill_cols (routed: expert e at w[0] + e * estride; the shared expert's: sh[0]), ggml's blocks read in
+// place; activations bh / bd = Q8_K integers as fp16 [rows][K] and their scales (row = slot - arow0), outputs
+// out[(slot - orow0) * R + r]. fmt KF_Q2K / KF_Q3K / KF_Q6K with K = 2048 (downs), KF_Q5K with K = 7168 (the shared
+// gate / up); R % 128 == 0.
 hipError_t kq_gemm_init();
 hipError_t launch_kq_gemm(const PrefillArgs & a, int fmt, int grid, hipStream_t st);
 

@@ -89,6 +89,7 @@ __global__ void __launch_bounds__(256) k_pf_cols(const int * __restrict__ act, c
     for (int c = i; c < nsh; c += 256) { cols[c] = make_int4(-1, P + PF_TOK * c, min(PF_TOK, n - PF_TOK * c), 0); }
     if (i == 255) { *ncols = nsh + scan[255]; }
 }
+int prefill_shared_cols(int n) { return (n + PF_TOK - 1) / PF_TOK; }
 hipError_t launch_prefill_cols(const int * act, const int * nact, const int * offsets, int n, int P, int4 * cols, int * ncols, hipStream_t st) {
     k_pf_cols<<<1, 256, 0, st>>>(act, nact, offsets, n, P, cols, ncols);
     return hipGetLastError();
@@ -173,14 +174,14 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
     ln.r = lane & 15; ln.g = lane >> 4;
     ln.trg = (uint32_t) L_PG | ((uint32_t) ln.r << 4);
     ln.trs = (uint32_t) L_PS | ((uint32_t) ln.r << 4);
-    const int ncols = *gptr(a.ncols);
+    const int col0 = a.col0, ncols = (a.col1 > 0 ? a.col1 : *gptr(a.ncols)) - col0;
     const int nrg = a.R / Geo::ROWS;
     const size_t dreg = (size_t) (a.R / 64) * NB * 4096;   // d region offset of a tiled matrix
     __builtin_amdgcn_s_waitcnt(0x0f70);
     __syncthreads();
 
     for (int it = blockIdx.x; it < ncols * nrg; it += gridDim.x) {
-        const int col = it / nrg, rg = it - col * nrg;
+        const int col = col0 + it / nrg, rg = it % nrg;
         const u32x4 cv = *(const LK_GLOBAL u32x4 *) (a.cols + col);
         const int4 cd = make_int4((int) cv.x, (int) cv.y, (int) cv.z, (int) cv.w);
         const bool routed = cd.x >= 0;
