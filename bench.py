@@ -317,6 +317,80 @@ def run_dropin(ctx, torch, steps=60, warmup=5, ggml_steps=3, seed=20260601):
     return res
 
 
+def run_dropin_wide(ctx, torch, n=512, steps=10, warmup=2, seed=20260611):
+    """The reference-named prefill path (the engine's wide pass, src/server_core_fused.cpp:733-744, 931-949) at
+    prefill-512: per 64-row group fl_ffn_begin(wrow) -> fl_fetch; then the pairs in slots of <= 8 rows per expert (the
+    engine's byexp order) as one fl_wide_moe on the layer's resident 256-expert arena (declared tiled; ids = expert ids),
+    then fl_wide_finish. The slot tables are built on the host outside the timed calls (the engine's own dispatch); the
+    time is the host wall clock of the library calls per step, median over the steps. The same x / ffn_inp every step
+    (fresh inputs would only change the routing)."""
+    import ctypes
+    import numpy as np
+    from loki_amd import FLOut, FLW, MoeLayerWeights, lib
+    KE, G = 8, 64
+    L = MoeLayerWeights.synthetic(ctx, seed, bias_sigma=0.05)
+    mats = (L.gate, L.up, L.down, L.sh_gate, L.sh_up, L.sh_down)
+    for t in mats:
+        ctx.register_tiled(t)
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((n, E)).astype(np.float32)
+    fi = rng.standard_normal((n, E)).astype(np.float32)
+    ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    w = FLW()
+    w.gate_inp = L.gate_inp.data_ptr(); w.probs_b = L.probs_b.data_ptr(); w.gate_f16 = 0
+    w.sh_gate, w.sh_up, w.sh_down = (m.data_ptr() for m in (L.sh_gate, L.sh_up, L.sh_down))
+    out = FLOut()
+    res = {}
+    try:
+        assert lib().fl_wide_init(ctx.ctx, n, KE) == 1
+
+        def step():
+            t_lib = 0.0
+            sel = np.empty((n, KE), np.int32); wts = np.empty((n, KE), np.float32)
+            for r0 in range(0, n, G):
+                t0 = time.perf_counter()
+                ctx.check(lib().fl_ffn_begin(ctx.ctx, ctypes.byref(w), G, ptr(x[r0:r0 + G]), ptr(fi[r0:r0 + G]), r0))
+                lib().fl_fetch(ctx.ctx, G, 1, ctypes.byref(out))
+                t_lib += time.perf_counter() - t0
+                sel[r0:r0 + G] = np.ctypeslib.as_array(out.sel, shape=(G, KE))
+                wts[r0:r0 + G] = np.ctypeslib.as_array(out.wts, shape=(G, KE))
+            # slots: each expert's (row, k) pairs in row-major order, 8 per slot (vectorised host dispatch)
+            fe = sel.ravel()
+            order = np.argsort(fe, kind="stable")
+            es = fe[order]
+            cnt = np.bincount(es, minlength=256)
+            first = np.concatenate([[0], np.cumsum(cnt)[:-1]])
+            rank = np.arange(es.size) - first[es]
+            nsl = (cnt + 7) // 8
+            soff = np.concatenate([[0], np.cumsum(nsl)[:-1]])
+            slot = soff[es] + rank // 8
+            ns = int(nsl.sum())
+            midx = np.repeat(np.arange(256, dtype=np.int32), nsl)
+            rows = np.full(ns * 8, -1, np.int32); kidx = np.zeros(ns * 8, np.int32); wk = np.zeros(ns * 8, np.float32)
+            pos = slot * 8 + rank % 8
+            rows[pos] = (order // KE).astype(np.int32); kidx[pos] = (order % KE).astype(np.int32); wk[pos] = wts.ravel()[order]
+            t0 = time.perf_counter()
+            lib().fl_wide_moe(ctx.ctx, L.gate.data_ptr(), L.up.data_ptr(), L.down.data_ptr(), 4, 256, ptr(midx), ptr(rows), ptr(kidx),
+                              ptr(wk), ns, KE, 0)
+            lib().fl_wide_finish(ctx.ctx, n, KE, ctypes.byref(out))
+            return t_lib + time.perf_counter() - t0
+
+        for _ in range(warmup):
+            step()
+        ts = [step() for _ in range(steps)]
+        torch.cuda.synchronize()
+        ctx.sync()
+        ms = float(np.median(ts)) * 1e3
+        res = {"ms_per_step": round(ms, 3), "tokens_per_s": round(n / (ms * 1e-3)), "tokens": n, "steps": steps}
+        log("[bench] drop-in prefill-%d (wide pass): %s" % (n, json.dumps(res)))
+    finally:
+        for t in mats:
+            ctx.unregister_tiled(t)
+    del L
+    torch.cuda.empty_cache()
+    return res
+
+
 def run_realfmt(ctx, torch, steps=20, warmup=3, copies=2, seed=20260501):
     """fl_moe_layer on the reference's real-shard formats, device-resident: IQ2_XXS routed gate/up (tiled), Q3_K routed
     down and a Q5_K / Q5_K / Q6_K shared expert read in place (fl_set_layer_formats); decode-8, decode-1 and prefill-512
@@ -466,7 +540,7 @@ def bench(args, ctx, torch):
         print(json.dumps({"kquant": run_kquant(ctx, torch), "real_formats": run_realfmt(ctx, torch)}), flush=True)
         return
     if args.only_dropin:
-        print(json.dumps({"dropin_decode1": run_dropin(ctx, torch)}), flush=True)
+        print(json.dumps({"dropin_decode1": run_dropin(ctx, torch), "dropin_prefill512": run_dropin_wide(ctx, torch)}), flush=True)
         return
     thr = cpu_threads()
     cpu_per = {}
@@ -503,6 +577,7 @@ def bench(args, ctx, torch):
             del r
             torch.cuda.empty_cache()
         extra["dropin_decode1"] = run_dropin(ctx, torch)
+        extra["dropin_prefill512"] = run_dropin_wide(ctx, torch)
         log("[bench] dropin_decode1: %s" % json.dumps(extra["dropin_decode1"]))
         extra["kquant"] = run_kquant(ctx, torch)
         extra["real_formats"] = run_realfmt(ctx, torch)

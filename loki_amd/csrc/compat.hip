@@ -175,10 +175,15 @@ struct Compat {
     DBuf<float> sg, su;                         // K-quant shared gate / up outputs
     // fl_moe
     DBuf<uint8_t> ag, au, ad; DBuf<int> ids, counts, offsets, perm, inv, act, nact; DBuf<float> w, hout, moe;
+    // the grouped GEMMs of routed_experts: the rows' Q8_K as fp16, Q8_K(h) as fp16, the columns
+    DBuf<_Float16> xh, hh; DBuf<int4> pcols; DBuf<int> pncols;
     std::vector<int> last_ids; int last_KE = 0, last_n = 0; bool last_fast = false;   // last_fast: o holds slot k at row k
     // wide pass
     int wmax = 0, wke = 0;
-    DBuf<float> ncur_all, base_all, out_all, xd_all; DBuf<int8_t> xq_all;
+    // wide pass: ffn_inp and the Q8_K of every row (fl_ffn_begin(wrow)); the shared expert of all rows (sh_all) and
+    // base = ffn_inp + shared, formed once by the first fl_wide_finish / fl_wide_skip after the rows came in
+    // (wide_pending), so the shared expert runs on all the rows in one pass
+    DBuf<float> fi_all, sh_all, base_all, out_all, xd_all; DBuf<int8_t> xq_all; bool wide_pending = false;
     DBuf<int> w_act, w_off, w_perm, w_nact, w_row, w_k; DBuf<float> w_wk;
     hipEvent_t wev[2] = { nullptr, nullptr };
     // fl_wide_moe's slot tables for each parity in pinned host memory (act | off | perm | row | k | nact, then wk): the
@@ -236,7 +241,8 @@ void compat_free(FLCtx * c) {
     s->xq.release(); s->hq.release(); s->xd.release(); s->hd.release(); s->sh_t.release(); s->sg.release(); s->su.release();
     s->ag.release(); s->au.release(); s->ad.release(); s->ids.release(); s->counts.release(); s->offsets.release(); s->perm.release(); s->inv.release();
     s->act.release(); s->nact.release(); s->w.release(); s->hout.release(); s->moe.release();
-    s->ncur_all.release(); s->base_all.release(); s->out_all.release(); s->xd_all.release(); s->xq_all.release();
+    s->xh.release(); s->hh.release(); s->pcols.release(); s->pncols.release();
+    s->fi_all.release(); s->sh_all.release(); s->base_all.release(); s->out_all.release(); s->xd_all.release(); s->xq_all.release();
     s->w_act.release(); s->w_off.release(); s->w_perm.release(); s->w_nact.release(); s->w_row.release(); s->w_k.release(); s->w_wk.release();
     delete s; c->compat = nullptr;
 }
@@ -277,8 +283,40 @@ static void shared_expert(FLCtx * c, Compat * s, const int8_t * xq, const float 
     }
     FALLOC(s->h, (size_t) N * H_); FALLOC(s->hq, (size_t) N * H_); FALLOC(s->hd, (size_t) N * (H_ / QK));
     CK(ensure_expert_scratch(c, (size_t) N, E_, H_) == FL_OK ? hipSuccess : hipErrorOutOfMemory);
+    // Above 8 rows the matrices whose format has one run on the grouped GEMMs, as the shared expert's columns (slots
+    // 0 .. N - 1 = the rows): IQ2_XXS on the IQ2_XXS GEMM, a Q5_K gate / up and a Q2_K / Q3_K / Q6_K down on the
+    // K-quant GEMM. Same bits as the per-pass kernels below.
+    const bool kq_gu = s->shf[0] == FL_Q5K && s->shf[1] == FL_Q5K;
+    const bool kq_dn = s->shf[2] == FL_Q2K || s->shf[2] == FL_Q3K || s->shf[2] == FL_Q6K;
+    const bool gemm = N > 8 && c->pf_mfma;
+    const bool gu_gemm = gemm && (s->shf[0] == FL_IQ2 || kq_gu), dn_gemm = gemm && (s->shf[2] == FL_IQ2 || kq_dn);
+    PrefillArgs g{};
+    if (gu_gemm || dn_gemm) {
+        CK(prefill_ready(c) == FL_OK ? hipSuccess : hipErrorOutOfMemory);
+        FALLOC(s->pcols, (size_t) NEXP_MAX + 2); FALLOC(s->pncols, 1);
+        FCK(launch_prefill_cols(zero_int(c), zero_int(c), zero_int(c), N, 0, s->pcols.p, s->pncols.p, c->st));   // no routed columns
+        g.ptab = c->ptab.p; g.perm = zero_int(c); g.topk = 1; g.P = 0; g.cols = s->pcols.p; g.ncols = s->pncols.p;
+        g.err = c->derr.p; g.herr = c->herr ? c->herr_dev : nullptr;
+    }
     ExpertArgs a = expert_args(c, N, 0, 1);
-    if (s->shf[0] == FL_IQ2) {
+    if (gu_gemm) {
+        FALLOC(s->xh, (size_t) N * E_);
+        FCK(launch_q8_to_h(xq, s->xh.p, (int64_t) N * E_, c->st));
+        PrefillArgs k = g;
+        k.R = H_; k.K = E_; k.bh = s->xh.p; k.bd = xd;
+        if (s->shf[0] == FL_IQ2) {
+            k.w[0] = tm[0]; k.w[1] = tm[1]; k.sh[0] = tm[0]; k.sh[1] = tm[1]; k.nmat = 2; k.out = s->h.p;
+            FCK(launch_prefill_gemm(k, c->ncu, c->st));
+        } else {
+            FALLOC(s->sg, (size_t) N * H_); FALLOC(s->su, (size_t) N * H_);
+            for (int m = 0; m < 2; ++m) {
+                k.sh[0] = k.w[0] = (const uint8_t *) s->sh_key[m]; k.nmat = 1; k.out = m ? s->su.p : s->sg.p;
+                FCK(launch_kq_gemm(k, FL_Q5K, c->ncu, c->st));
+            }
+            FCK(launch_swiglu(s->sg.p, s->su.p, (int64_t) N * H_, s->h.p, c->st));
+        }
+        FCK(launch_quant_q8k(s->h.p, N, H_, s->hq.p, s->hd.p, c->st));
+    } else if (s->shf[0] == FL_IQ2) {
         a.sh[0] = tm[0]; a.sh[1] = tm[1]; a.aq = xq; a.ad = xd; a.K = E_; a.R = H_; a.nmat = 2;
         a.act = zero_int(c); a.nact = zero_int(c); a.offsets = zero_int(c); a.perm = zero_int(c); a.topk = 1;
         a.h = s->h.p; a.hq = s->hq.p; a.hd = s->hd.p;
@@ -297,7 +335,19 @@ static void shared_expert(FLCtx * c, Compat * s, const int8_t * xq, const float 
         }
         FCK(launch_swiglu_q8k(s->sg.p, s->su.p, N, H_, s->h.p, s->hq.p, s->hd.p, c->st));
     }
-    if (s->shf[2] == FL_IQ2) {
+    if (dn_gemm) {
+        FALLOC(s->hh, (size_t) N * H_);
+        FCK(launch_q8_to_h(s->hq.p, s->hh.p, (int64_t) N * H_, c->st));
+        PrefillArgs k = g;
+        k.R = E_; k.K = H_; k.nmat = 1; k.bh = s->hh.p; k.bd = s->hd.p; k.out = out;
+        if (s->shf[2] == FL_IQ2) {
+            k.w[0] = k.sh[0] = tm[2];
+            FCK(launch_prefill_gemm(k, c->ncu, c->st));
+        } else {
+            k.w[0] = k.sh[0] = (const uint8_t *) s->sh_key[2];
+            FCK(launch_kq_gemm(k, s->shf[2], c->ncu, c->st));
+        }
+    } else if (s->shf[2] == FL_IQ2) {
         ExpertArgs d = a;
         d.sh[0] = tm[2]; d.sh[1] = nullptr; d.aq = s->hq.p; d.ad = s->hd.p; d.K = H_; d.R = E_; d.nmat = 1;
         d.act = zero_int(c); d.nact = zero_int(c); d.offsets = zero_int(c); d.perm = zero_int(c); d.topk = 1;
@@ -328,10 +378,38 @@ struct Arena { const uint8_t * g, * u, * d; };
 // routed experts of an arena (tiled gate/up/down in ar) for the pairs described by offsets/perm/act/nact -> o [P][E]
 // down_fmt: FL_IQ2 (tiled ar.d) or FL_Q2K / FL_Q3K read in place from down (expert stride E x H/256 blocks);
 // max_slots bounds the pairs of one expert
+// With two or more pairs per arena expert on average (a wide batch), the pairs run on the grouped MFMA GEMMs (gate/up,
+// then Q8_K(h), then the down on the IQ2_XXS or the K-quant GEMM), else on the per-pass kernels; both give the same
+// bits. fl_set_prefill_mfma(0) keeps the per-pass kernels.
 static void routed_experts(FLCtx * c, Compat * s, const Arena & ar, const int8_t * xq, const float * xd, int n, int P, int KE, int nexp,
                            const int * act, const int * nact, const int * offsets, const int * perm, float * o,
                            int down_fmt, const void * down, int max_slots) {
     FALLOC(s->h, (size_t) P * H_); FALLOC(s->hq, (size_t) P * H_); FALLOC(s->hd, (size_t) P * (H_ / QK));
+    if (c->pf_mfma && P >= 32 && P >= 2 * nexp) {
+        CK(prefill_ready(c) == FL_OK ? hipSuccess : hipErrorOutOfMemory);
+        hipStream_t st = c->st;
+        FALLOC(s->xh, (size_t) n * E_); FALLOC(s->hh, (size_t) P * H_);
+        FALLOC(s->pcols, (size_t) P / 32 + NEXP_MAX + 2); FALLOC(s->pncols, 1);
+        FCK(launch_q8_to_h(xq, s->xh.p, (int64_t) n * E_, st));
+        FCK(launch_prefill_cols(act, nact, offsets, 0, P, s->pcols.p, s->pncols.p, st));
+        PrefillArgs g{};
+        g.ptab = c->ptab.p; g.w[0] = ar.g; g.w[1] = ar.u; g.estride = mat_bytes(H_, E_); g.sh[0] = ar.g; g.sh[1] = ar.u;   // no shared columns
+        g.perm = perm; g.topk = KE; g.P = P; g.R = H_; g.K = E_; g.nmat = 2; g.cols = s->pcols.p; g.ncols = s->pncols.p;
+        g.bh = s->xh.p; g.bd = xd; g.out = s->h.p; g.err = c->derr.p; g.herr = c->herr ? c->herr_dev : nullptr;
+        FCK(launch_prefill_gemm(g, c->ncu, st));
+        FCK(launch_quant_q8k(s->h.p, P, H_, s->hq.p, s->hd.p, st));
+        FCK(launch_q8_to_h(s->hq.p, s->hh.p, (int64_t) P * H_, st));
+        PrefillArgs d = g;
+        d.R = E_; d.K = H_; d.nmat = 1; d.bh = s->hh.p; d.bd = s->hd.p; d.out = o; d.w[1] = nullptr; d.sh[1] = nullptr;
+        if (down_fmt == FL_IQ2) {
+            d.w[0] = ar.d; d.sh[0] = ar.d; d.estride = mat_bytes(E_, H_);
+            FCK(launch_prefill_gemm(d, c->ncu, st));
+        } else {   // src/fused_layer.cu:607-608 (tc_matvec<F_Q2K / F_Q3K>)
+            d.w[0] = (const uint8_t *) down; d.sh[0] = (const uint8_t *) down; d.estride = fmt_bytes(down_fmt, E_, H_);
+            FCK(launch_kq_gemm(d, down_fmt, c->ncu, st));
+        }
+        return;
+    }
     CK(ensure_expert_scratch(c, (size_t) P + n, E_, H_) == FL_OK ? hipSuccess : hipErrorOutOfMemory);
     ExpertArgs a = expert_args(c, n, P, 0);
     a.w[0] = ar.g; a.w[1] = ar.u; a.estride = mat_bytes(H_, E_); a.aq = xq; a.ad = xd; a.K = E_; a.R = H_; a.nmat = 2;
@@ -450,13 +528,12 @@ extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur,
     s->r_tagged = router_fused_ok(N, E_); s->rtag = c->epoch;
     s->N = N;
     s->sh_pending = true; s->xq_pending = true;
-    if (wrow >= 0) { shared_now(c, s); }   // the wide pass's base rows need it now
-    if (wrow >= 0) {
-        TRY(c, hipMemcpyAsync(s->ncur_all.p + (size_t) wrow * E_, s->ncur.p, (size_t) N * E_ * 4, hipMemcpyDeviceToDevice, st));
+    if (wrow >= 0) {   // the wide pass: the rows' Q8_K (fl_wide_moe) and ffn_inp (base = ffn_inp + shared, formed later)
+        quant_now(c, s);
         TRY(c, hipMemcpyAsync(s->xq_all.p + (size_t) wrow * E_, s->xq.p, (size_t) N * E_, hipMemcpyDeviceToDevice, st));
         TRY(c, hipMemcpyAsync(s->xd_all.p + (size_t) wrow * (E_ / QK), s->xd.p, (size_t) N * (E_ / QK) * 4, hipMemcpyDeviceToDevice, st));
-        k_base_rows<<<nblk((int64_t) N * E_), 256, 0, st>>>(s->fi, s->sh_o.p, (int64_t) N * E_, s->base_all.p + (size_t) wrow * E_);
-        TRY(c, hipGetLastError());
+        TRY(c, hipMemcpyAsync(s->fi_all.p + (size_t) wrow * E_, s->fi, (size_t) N * E_ * 4, hipMemcpyDeviceToDevice, st));
+        s->wide_pending = true;
     }
     return FL_OK;
 }
@@ -598,7 +675,7 @@ extern "C" int fl_wide_init(FLCtx * c, int wmax, int KE) {
     if (wmax <= 0 || KE <= 0 || KE > MAXK) { std::fprintf(stderr, "[fused] fl_wide_init: wmax %d, KE %d\n", wmax, KE); std::exit(7); }
     s->wmax = wmax; s->wke = KE;
     const size_t R = (size_t) wmax * E_;
-    FALLOC(s->ncur_all, R); FALLOC(s->base_all, R); FALLOC(s->out_all, R * KE); FALLOC(s->xq_all, R); FALLOC(s->xd_all, (size_t) wmax * (E_ / QK));
+    FALLOC(s->fi_all, R); FALLOC(s->sh_all, R); FALLOC(s->base_all, R); s->wide_pending = false; FALLOC(s->out_all, R * KE); FALLOC(s->xq_all, R); FALLOC(s->xd_all, (size_t) wmax * (E_ / QK));
     CK(hipMemset(s->out_all.p, 0, R * KE * 4));
     if (s->h_wh) { (void) hipHostFree(s->h_wh); } if (s->h_wmoe) { (void) hipHostFree(s->h_wmoe); }
     s->h_wh = pinned<float>(R); s->h_wmoe = pinned<float>(R);
@@ -683,12 +760,23 @@ extern "C" void fl_wide_moe(FLCtx * c, const void * gate, const void * up, const
 extern "C" void fl_wide_mark(FLCtx * c, int par) { Compat * s = cs(c); if (s->wev[par & 1]) { CK(hipEventRecord(s->wev[par & 1], c->st)); } }
 extern "C" void fl_wide_wait(FLCtx * c, int par) { Compat * s = cs(c); if (s->wev[par & 1]) { CK(hipEventSynchronize(s->wev[par & 1])); } }
 
+// base = ffn_inp + shared for the wide pass's rows 0 .. n - 1: the shared expert on all of them at once (the rows'
+// Q8_K as fl_ffn_begin(wrow) left them), once per set of rows
+static void wide_base(FLCtx * c, Compat * s, int n) {
+    if (!s->wide_pending) { return; }
+    shared_expert(c, s, s->xq_all.p, s->xd_all.p, n, s->sh_all.p);
+    k_base_rows<<<nblk((int64_t) n * E_), 256, 0, c->st>>>(s->fi_all.p, s->sh_all.p, (int64_t) n * E_, s->base_all.p);
+    CK(hipGetLastError());
+    s->wide_pending = false;
+}
+
 extern "C" void fl_wide_finish(FLCtx * c, int n, int KE, FLOut * out) {
     std::memset(out, 0, sizeof(FLOut));
     Compat * s = cs(c);
     if (n <= 0 || n > s->wmax || KE != s->wke) { std::fprintf(stderr, "[fused] fl_wide_finish: n %d (wmax %d), KE %d (init %d)\n", n, s->wmax, KE, s->wke); std::exit(7); }
     hipStream_t st = c->st; const int64_t tot = (int64_t) n * E_;
     FALLOC(s->hout, (size_t) tot); FALLOC(s->moe, (size_t) tot);
+    wide_base(c, s, n);
     k_wide_finish<<<nblk(tot), 256, 0, st>>>(s->base_all.p, s->out_all.p, KE, tot, s->hout.p, s->moe.p);
     CK(hipGetLastError());
     CK(hipMemcpyAsync(s->h_wh, s->hout.p, (size_t) tot * 4, hipMemcpyDeviceToHost, st));
@@ -703,6 +791,7 @@ extern "C" void fl_wide_skip(FLCtx * c, const float * mo, int n, FLOut * out) {
     if (n <= 0 || n > s->wmax) { std::fprintf(stderr, "[fused] fl_wide_skip: n %d (wmax %d)\n", n, s->wmax); std::exit(7); }
     hipStream_t st = c->st; const int64_t tot = (int64_t) n * E_;
     FALLOC(s->hout, (size_t) tot); FALLOC(s->moe, (size_t) tot);
+    wide_base(c, s, n);
     CK(hipMemcpyAsync(s->moe.p, mo, (size_t) tot * 4, hipMemcpyHostToDevice, st));
     k_wide_skip<<<nblk(tot), 256, 0, st>>>(s->base_all.p, s->moe.p, tot, s->hout.p);
     CK(hipGetLastError());

@@ -110,6 +110,7 @@ void tiled_add(const void * p, size_t bytes);
 void tiled_remove_within(const void * p, size_t bytes);
 bool tiled_holds(const void * p, size_t bytes);
 int ensure_expert_scratch(FLCtx * c, size_t rows, int E, int H);   // fused_layer.hip
+int prefill_ready(FLCtx * c);   // fused_layer.hip: the grouped GEMMs' set-up (tables, attributes), once per context
 // the one-token kernel is available (a 256-CU device, the fused decode not switched off), and its launch on caller-given
 // picks (d.ext_sel / ext_w set; this fills the tables, tagged buffers, epoch and error words of d)
 bool decode1_available(FLCtx * c);

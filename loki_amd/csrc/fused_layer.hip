@@ -439,6 +439,18 @@ static hipError_t routed_down_kq(FLCtx * c, const FLMoeLayer * L, int P, int E, 
     return launch_kq_matvec(k, c->lf[0], (P + ne - 1) / ne, ne < P ? ne : P, c->st);
 }
 
+// the grouped GEMMs' one-time set-up on this context: fp16 table image, launch attributes, error word
+int prefill_ready(FLCtx * c) {
+    if (c->pf_ready) { return FL_OK; }
+    ALLOC(c, c->ptab, prefill_table_bytes() / 16);
+    TRY(c, build_prefill_tables(c->ptab.p, c->st));
+    TRY(c, prefill_init());
+    TRY(c, kq_gemm_init());
+    if (!c->derr.p) { ALLOC(c, c->derr, 1); TRY(c, hipMemsetAsync(c->derr.p, 0, sizeof(int), c->st)); }
+    c->pf_ready = 1;
+    return FL_OK;
+}
+
 static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, float * y, bool prenorm, const float * nw, float eps,
                      const float * resid) {
     if (!c) { return FL_EINVAL; }
@@ -518,14 +530,7 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
         return FL_OK;
     }
     if (mfma) {
-        if (!c->pf_ready) {
-            ALLOC(c, c->ptab, prefill_table_bytes() / 16);
-            TRY(c, build_prefill_tables(c->ptab.p, st));
-            TRY(c, prefill_init());
-            TRY(c, kq_gemm_init());
-            if (!c->derr.p) { ALLOC(c, c->derr, 1); TRY(c, hipMemsetAsync(c->derr.p, 0, sizeof(int), st)); }
-            c->pf_ready = 1;
-        }
+        if (int rc = prefill_ready(c)) { return rc; }
         ALLOC(c, c->xh, (size_t) n * E); ALLOC(c, c->hh, rows * H);
         ALLOC(c, c->pcols, rows / 32 + NEXP_MAX + 2); ALLOC(c, c->pncols, 1);
     }

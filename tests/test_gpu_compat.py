@@ -150,12 +150,22 @@ def test_f16_router(ctx, small_layer):
     assert np.array_equal(res[0][0].reshape(n, KE), so) and np.array_equal(res[0][1].reshape(n, KE).view(np.uint32), wo.view(np.uint32))
 
 
+@pytest.mark.parametrize("mfma", [True, False], ids=["gemm", "per_pass"])
 @pytest.mark.parametrize("waits", [True, False])
-def test_wide_pass(ctx, small_layer, waits):
+def test_wide_pass(ctx, small_layer, waits, mfma):
     """fl_wide_init -> fl_ffn_begin(wrow) per group -> per arena batch fl_wide_moe (slots of <= 8 (row, k) pairs in the
     engine's byexp order) -> fl_wide_finish; h = (ffn_inp + shared) + sum_k w_k o_k (src/fused_layer.cu:351-360).
     fl_wide_moe only enqueues: with waits=False the batches are issued back to back without fl_wide_wait, and the
-    library's own per-parity guard keeps each parity's slot tables intact until their copies ran."""
+    library's own per-parity guard keeps each parity's slot tables intact until their copies ran. The batches (about
+    20 pairs per expert) run on the grouped MFMA GEMMs, or with fl_set_prefill_mfma(0) on the per-pass kernels."""
+    ctx.set_prefill_mfma(mfma)
+    try:
+        _wide_pass(ctx, small_layer, waits)
+    finally:
+        ctx.set_prefill_mfma(True)
+
+
+def _wide_pass(ctx, small_layer, waits):
     from loki_amd import FLOut, lib
     (W, b, gate, up, down, sh), dev = small_layer
     n, EB = 40, 5

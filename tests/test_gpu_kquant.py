@@ -210,8 +210,9 @@ def test_narrow_one_row_real_formats_single_launch(ctx, real_layer, down_fmt):
 
 def test_wide_q3k_down(ctx, real_layer):
     """the wide pass (fl_wide_init / fl_ffn_begin(wrow) / fl_wide_moe / fl_wide_finish) with a Q3_K down and the
-    K-quant shared expert: 16 experts and top-8 give each expert about 20 of the 320 pairs, so the mat-vec runs several
-    token groups per expert"""
+    K-quant shared expert: 16 experts and top-8 give each expert about 20 of the 320 pairs. The batches run on the
+    grouped GEMMs (IQ2_XXS gate/up, Q3_K down) and again on the per-pass kernels (fl_set_prefill_mfma(0), the mat-vec
+    in several token groups per expert): h and moe bit-identical, and within the K-quant bar of the checker"""
     from loki_amd import FLOut, lib
     host, dev = real_layer
     ctx.set_routing(1, 1, 8, 1.0)
@@ -232,28 +233,38 @@ def test_wide_q3k_down(ctx, real_layer):
         for k in range(KE):
             byexp[sel[i, k]].append((i, k))
     print("wide q3_K: %d experts, max %d pairs" % (len(used), max(len(v) for v in byexp.values())), flush=True)
-    for bi, b0 in enumerate(range(0, len(used), EB)):
-        batch = used[b0:b0 + EB]
-        par = bi & 1
-        lib().fl_wide_wait(ctx.ctx, par)
-        midx, rows, kidx, wk = [], [], [], []
-        for u, e in enumerate(batch):
-            lst = byexp[e]
-            for i0 in range(0, len(lst), 8):
-                midx.append(u)
-                for j in range(8):
-                    if i0 + j < len(lst):
-                        r, k = lst[i0 + j]; rows.append(r); kidx.append(k); wk.append(wts[r, k])
-                    else:
-                        rows.append(-1); kidx.append(0); wk.append(0.0)
-        ga, ua, da = _arena(dev, batch, orc.Q3K)
-        lib().fl_wide_moe(ctx.ctx, ga.data_ptr(), ua.data_ptr(), da.data_ptr(), orc.Q3K, len(batch), cptr(np.int32(midx)),
-                          cptr(np.int32(rows)), cptr(np.int32(kidx)), cptr(f32(wk)), len(midx), KE, par)
-        lib().fl_wide_mark(ctx.ctx, par)
-    out = FLOut()
-    lib().fl_wide_finish(ctx.ctx, n, KE, ctypes.byref(out))
-    h = np.ctypeslib.as_array(out.h, shape=(n * E,)).reshape(n, E).copy()
-    moe = np.ctypeslib.as_array(out.moe, shape=(n * E,)).reshape(n, E).copy()
+
+    def batches():
+        for bi, b0 in enumerate(range(0, len(used), EB)):
+            batch = used[b0:b0 + EB]
+            par = bi & 1
+            lib().fl_wide_wait(ctx.ctx, par)
+            midx, rows, kidx, wk = [], [], [], []
+            for u, e in enumerate(batch):
+                lst = byexp[e]
+                for i0 in range(0, len(lst), 8):
+                    midx.append(u)
+                    for j in range(8):
+                        if i0 + j < len(lst):
+                            r, k = lst[i0 + j]; rows.append(r); kidx.append(k); wk.append(wts[r, k])
+                        else:
+                            rows.append(-1); kidx.append(0); wk.append(0.0)
+            ga, ua, da = _arena(dev, batch, orc.Q3K)
+            lib().fl_wide_moe(ctx.ctx, ga.data_ptr(), ua.data_ptr(), da.data_ptr(), orc.Q3K, len(batch), cptr(np.int32(midx)),
+                              cptr(np.int32(rows)), cptr(np.int32(kidx)), cptr(f32(wk)), len(midx), KE, par)
+            lib().fl_wide_mark(ctx.ctx, par)
+        out = FLOut()
+        lib().fl_wide_finish(ctx.ctx, n, KE, ctypes.byref(out))
+        return (np.ctypeslib.as_array(out.h, shape=(n * E,)).reshape(n, E).copy(),
+                np.ctypeslib.as_array(out.moe, shape=(n * E,)).reshape(n, E).copy())
+
+    h, moe = batches()   # the grouped GEMMs (about 20 pairs per expert)
+    ctx.set_prefill_mfma(False)
+    try:
+        h_pp, moe_pp = batches()   # the per-pass kernels
+    finally:
+        ctx.set_prefill_mfma(True)
+    assert np.array_equal(h.view(np.uint32), h_pp.view(np.uint32)) and np.array_equal(moe.view(np.uint32), moe_pp.view(np.uint32))
     ref = orc.moe_experts(x, sel, wts, host["gate"], host["up"], host["kdown"][orc.Q3K], *host["ksh"], want=("o", "sh"),
                           n_exp=16, fmts=(orc.Q3K, orc.Q5K, orc.Q5K, orc.Q6K))
     o = ref["o"].reshape(n, KE, E)
