@@ -317,6 +317,53 @@ def run_dropin(ctx, torch, steps=60, warmup=5, ggml_steps=3, seed=20260601):
     return res
 
 
+def run_dropin_rows(ctx, torch, n=8, steps=30, warmup=5, seed=20260621):
+    """The reference-named path at decode-8 (src/server_core_fused.cpp:946-953 with n = 8 rows): per step fl_ffn_begin
+    (8 rows) -> fl_fetch -> fl_moe on the resident, declared 256-expert arena (ids = expert ids). Medians of the host
+    wall clock per step over the steps."""
+    import ctypes
+    import numpy as np
+    from loki_amd import FLOut, FLW, MoeLayerWeights, lib
+    L = MoeLayerWeights.synthetic(ctx, seed)
+    mats = (L.gate, L.up, L.down, L.sh_gate, L.sh_up, L.sh_down)
+    for t in mats:
+        ctx.register_tiled(t)
+    rng = np.random.default_rng(seed)
+    xs = rng.standard_normal((steps + warmup, n, E)).astype(np.float32)
+    fis = rng.standard_normal((steps + warmup, n, E)).astype(np.float32)
+    out = FLOut()
+    ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    w = FLW()
+    w.gate_inp = L.gate_inp.data_ptr(); w.probs_b = L.probs_b.data_ptr(); w.gate_f16 = 0
+    w.sh_gate, w.sh_up, w.sh_down = (m.data_ptr() for m in (L.sh_gate, L.sh_up, L.sh_down))
+    res = {}
+    try:
+        split = []
+        for i in range(steps + warmup):
+            t0 = time.perf_counter()
+            ctx.check(lib().fl_ffn_begin(ctx.ctx, ctypes.byref(w), n, ptr(xs[i]), ptr(fis[i]), -1))
+            t1 = time.perf_counter()
+            lib().fl_fetch(ctx.ctx, n, 1, ctypes.byref(out))
+            t2 = time.perf_counter()
+            sel = np.ctypeslib.as_array(out.sel, shape=(n * 8,)).astype(np.int32)
+            wts = np.ctypeslib.as_array(out.wts, shape=(n * 8,)).copy()
+            lib().fl_moe(ctx.ctx, L.gate.data_ptr(), L.up.data_ptr(), L.down.data_ptr(), 256, 4, ptr(sel), ptr(wts), 8, n, ctypes.byref(out))
+            t3 = time.perf_counter()
+            if i >= warmup:
+                split.append((t1 - t0, t2 - t1, t3 - t2))
+        sp = np.array(split) * 1e6
+        step_us = float(np.median(sp.sum(axis=1)))
+        res = {"us_per_step": round(step_us, 1), "us_per_token": round(step_us / n, 2), "ffn_begin_us": round(float(np.median(sp[:, 0])), 1),
+               "fetch_us": round(float(np.median(sp[:, 1])), 1), "moe_us": round(float(np.median(sp[:, 2])), 1), "tokens": n, "steps": steps}
+        log("[bench] drop-in decode-%d: %s" % (n, json.dumps(res)))
+    finally:
+        for t in mats:
+            ctx.unregister_tiled(t)
+    del L
+    torch.cuda.empty_cache()
+    return res
+
+
 def run_dropin_wide(ctx, torch, n=512, steps=10, warmup=2, seed=20260611):
     """The reference-named prefill path (the engine's wide pass, src/server_core_fused.cpp:733-744, 931-949) at
     prefill-512: per 64-row group fl_ffn_begin(wrow) -> fl_fetch; then the pairs in slots of <= 8 rows per expert (the
@@ -540,7 +587,8 @@ def bench(args, ctx, torch):
         print(json.dumps({"kquant": run_kquant(ctx, torch), "real_formats": run_realfmt(ctx, torch)}), flush=True)
         return
     if args.only_dropin:
-        print(json.dumps({"dropin_decode1": run_dropin(ctx, torch), "dropin_prefill512": run_dropin_wide(ctx, torch)}), flush=True)
+        print(json.dumps({"dropin_decode1": run_dropin(ctx, torch), "dropin_decode8": run_dropin_rows(ctx, torch),
+                          "dropin_prefill512": run_dropin_wide(ctx, torch)}), flush=True)
         return
     thr = cpu_threads()
     cpu_per = {}
@@ -577,6 +625,7 @@ def bench(args, ctx, torch):
             del r
             torch.cuda.empty_cache()
         extra["dropin_decode1"] = run_dropin(ctx, torch)
+        extra["dropin_decode8"] = run_dropin_rows(ctx, torch)
         extra["dropin_prefill512"] = run_dropin_wide(ctx, torch)
         log("[bench] dropin_decode1: %s" % json.dumps(extra["dropin_decode1"]))
         extra["kquant"] = run_kquant(ctx, torch)

@@ -193,8 +193,8 @@ struct Compat {
     // pinned host mirrors
     int * h_sel = nullptr; float * h_wts = nullptr, * h_ncur = nullptr, * h_fi = nullptr, * h_h = nullptr, * h_moe = nullptr;
     // kernel-written host memory (no copies): the router's picks of the RMAX rows then their weights (z_sel), then
-    // the one-launch routing's done word (at ZS_DONE); fl_moe's one-token launch's ids then weights (z_in) and its h
-    // then moe (z_out); *_d = the device addresses. r_tagged: the last fl_ffn_begin's routing sets the done word, to rtag
+    // the one-launch routing's done word (at ZS_DONE); fl_moe's single launch's ids then (at NB * MAXK) weights (z_in)
+    // and its h rows then (at NB * E) moe rows (z_out); *_d = the device addresses. r_tagged: the last fl_ffn_begin's routing sets the done word, to rtag
     int * z_sel = nullptr, * z_sel_d = nullptr, * z_in = nullptr, * z_in_d = nullptr; float * z_out = nullptr, * z_out_d = nullptr;
     unsigned rtag = 0; bool r_tagged = false;
     float * h_wh = nullptr, * h_wmoe = nullptr;
@@ -208,8 +208,8 @@ struct Compat {
 static Compat * cs(FLCtx * c) {
     if (!c->compat) {
         Compat * s = new Compat();
-        s->z_sel = mapped<int>(ZS_DONE + 16, &s->z_sel_d); s->z_in = mapped<int>(2 * MAXK, &s->z_in_d);
-        s->z_out = mapped<float>(2 * E_, &s->z_out_d);
+        s->z_sel = mapped<int>(ZS_DONE + 16, &s->z_sel_d); s->z_in = mapped<int>(2 * NB * MAXK, &s->z_in_d);
+        s->z_out = mapped<float>((size_t) 2 * NB * E_, &s->z_out_d);
         s->h_sel = pinned<int>(RMAX * MAXK); s->h_wts = pinned<float>(RMAX * MAXK);
         s->h_ncur = pinned<float>((size_t) RMAX * E_); s->h_fi = pinned<float>((size_t) RMAX * E_);
         s->h_h = pinned<float>((size_t) RMAX * E_); s->h_moe = pinned<float>((size_t) RMAX * E_);
@@ -572,21 +572,23 @@ extern "C" void fl_moe(FLCtx * c, const void * gate, const void * up, const void
         std::fprintf(stderr, "[fused] fl_moe: an arena allocation is smaller than %d experts\n", nexp); std::exit(7);
     }
     hipStream_t st = c->st; const int P = n * KE;
-    c->last_kernel = 0;   // fl_debug: 2 when the one-token kernel below runs the call
+    c->last_kernel = 0;   // fl_debug: 2 / 1 when the one-token kernel / the n <= 8 block below runs the call
     int max_slots = 1;
     { std::vector<int> per(nexp, 0); for (int i = 0; i < P; ++i) { max_slots = std::max(max_slots, ++per[ids[i]]); } }
     CK(hipEventRecord(c->em0, st));
     FALLOC(s->ids, 2 * P); FALLOC(s->counts, nexp); FALLOC(s->offsets, nexp + 1); FALLOC(s->perm, P); FALLOC(s->inv, P);
     FALLOC(s->act, nexp); FALLOC(s->nact, 1); FALLOC(s->o, (size_t) P * E_); FALLOC(s->hout, (size_t) NB * E_); FALLOC(s->moe, (size_t) NB * E_);
-    // One row with all 8 picks: one launch of the one-token kernel on the caller's picks (router and selection skipped;
-    // the shared expert and the Q8_K of fl_ffn_begin's row computed in the same launch; the combine in this function's
-    // order), when the formats are one of its variants: every matrix IQ2_XXS, or the routed down Q2_K / Q3_K with a
-    // Q5_K / Q5_K / Q6_K shared expert. Results bit-identical to the per-pass kernels below. The launch reads the picks
-    // from host memory and writes h and moe there (z_in, z_out): no copies either way.
+    // One launch on the caller's picks (router and selection skipped; the shared expert and the Q8_K of fl_ffn_begin's
+    // rows computed in the same launch; the combine in this function's order): one row with all 8 picks on the
+    // one-token kernel, when the formats are one of its variants (every matrix IQ2_XXS, or the routed down Q2_K / Q3_K
+    // with a Q5_K / Q5_K / Q6_K shared expert); up to 8 rows of an all-IQ2_XXS layer on the n <= 8 block. Results
+    // bit-identical to the per-pass kernels below. The launch reads the picks from host memory and writes h and moe
+    // there (z_in, z_out): no copies either way.
     const bool kq_sh = s->shf[0] == FL_Q5K && s->shf[1] == FL_Q5K && s->shf[2] == FL_Q6K;
     const bool iq_sh = s->shf[0] == FL_IQ2 && s->shf[1] == FL_IQ2 && s->shf[2] == FL_IQ2;
-    const bool fast = n == 1 && KE == MAXK && decode1_available(c) &&
-                      ((down_fmt == FL_IQ2 && iq_sh) || ((down_fmt == FL_Q2K || down_fmt == FL_Q3K) && kq_sh && !(reinterpret_cast<uintptr_t>(down) & 3u)));
+    const bool fast1 = n == 1 && KE == MAXK && decode1_available(c) &&
+                       ((down_fmt == FL_IQ2 && iq_sh) || ((down_fmt == FL_Q2K || down_fmt == FL_Q3K) && kq_sh && !(reinterpret_cast<uintptr_t>(down) & 3u)));
+    const bool fast = fast1 || (down_fmt == FL_IQ2 && iq_sh && decode_block_available(c));
     const float * dw = nullptr;   // the device weights of the per-pass path
     if (!fast) {
         if (s->in_rec) { CK(hipEventSynchronize(s->in_ev)); }
@@ -595,15 +597,15 @@ extern "C" void fl_moe(FLCtx * c, const void * gate, const void * up, const void
         dw = reinterpret_cast<const float *>(s->ids.p + P);
         CK(hipEventRecord(s->in_ev, st)); s->in_rec = true;
     } else {   // the previous fl_moe has ended (each call waits for its stream): the launch that read z_in is done
-        std::memcpy(s->z_in, ids, MAXK * 4); std::memcpy(s->z_in + MAXK, w, MAXK * 4);
+        std::memcpy(s->z_in, ids, (size_t) P * 4); std::memcpy(s->z_in + NB * MAXK, w, (size_t) P * 4);
     }
     const Arena ar = pack_arena(c, s, gate, up, down, nexp, down_fmt);
     if (fast) {
-        CK(ensure_expert_scratch(c, 1, E_, H_) == FL_OK ? hipSuccess : hipErrorOutOfMemory);
+        CK(ensure_expert_scratch(c, (size_t) n, E_, H_) == FL_OK ? hipSuccess : hipErrorOutOfMemory);
         const size_t mg = mat_bytes(H_, E_);
         DecodeArgs d{};
-        d.x = s->ncur.p; d.n = 1; d.resid = s->fi;
-        d.n_exp = nexp; d.n_group = c->n_group; d.topk_group = c->topk_group; d.topk = MAXK; d.keep = MAXK; d.scale = c->scale;
+        d.x = s->ncur.p; d.n = n; d.resid = s->fi;
+        d.n_exp = nexp; d.n_group = c->n_group; d.topk_group = c->topk_group; d.topk = KE; d.keep = KE; d.scale = c->scale;
         d.gate = ar.g; d.up = ar.u; d.estride = mg;
         d.down = down_fmt == FL_IQ2 ? ar.d : (const uint8_t *) down; d.dstride = fmt_bytes(down_fmt, E_, H_);
         for (int i = 0; i < 3; ++i) {   // IQ2_XXS: declared tiled as it is, else the tiled copy; K-quants in place
@@ -613,9 +615,9 @@ extern "C" void fl_moe(FLCtx * c, const void * gate, const void * up, const void
         }
         d.kdown = down_fmt == FL_IQ2 ? 0 : down_fmt;
         d.E = E_; d.H = H_; d.xq = s->xq.p; d.xd = s->xd.p;
-        d.ext_sel = s->z_in_d; d.ext_w = reinterpret_cast<const float *>(s->z_in_d + MAXK);
-        d.moe_out = s->z_out_d + E_; d.o_out = s->o.p; d.y = s->z_out_d;
-        if (decode1_picks(c, d) != FL_OK) { std::fprintf(stderr, "[fused] fl_moe: %s\n", c->err.c_str()); std::exit(7); }
+        d.ext_sel = s->z_in_d; d.ext_w = reinterpret_cast<const float *>(s->z_in_d + NB * MAXK);
+        d.moe_out = s->z_out_d + (size_t) NB * E_; d.o_out = s->o.p; d.y = s->z_out_d;
+        if (decode_picks(c, d) != FL_OK) { std::fprintf(stderr, "[fused] fl_moe: %s\n", c->err.c_str()); std::exit(7); }
     } else {
         quant_now(c, s); shared_now(c, s);
         CK(launch_dispatch(s->ids.p, P, nexp, s->counts.p, s->offsets.p, s->perm.p, s->inv.p, s->act.p, s->nact.p, st));
@@ -632,7 +634,7 @@ extern "C" void fl_moe(FLCtx * c, const void * gate, const void * up, const void
         std::fprintf(stderr, "[fused] fl_moe: the one-token launch reported device code %d\n", *c->herr); std::exit(7);
     }
     s->last_ids.assign(ids, ids + P); s->last_KE = KE; s->last_n = n; s->last_fast = fast;
-    out->h = fast ? s->z_out : s->h_h; out->moe = fast ? s->z_out + E_ : s->h_moe;
+    out->h = fast ? s->z_out : s->h_h; out->moe = fast ? s->z_out + (size_t) NB * E_ : s->h_moe;
 }
 
 extern "C" void fl_skip(FLCtx * c, const float * mo, int n, FLOut * out) {

@@ -111,10 +111,12 @@ void tiled_remove_within(const void * p, size_t bytes);
 bool tiled_holds(const void * p, size_t bytes);
 int ensure_expert_scratch(FLCtx * c, size_t rows, int E, int H);   // fused_layer.hip
 int prefill_ready(FLCtx * c);   // fused_layer.hip: the grouped GEMMs' set-up (tables, attributes), once per context
-// the one-token kernel is available (a 256-CU device, the fused decode not switched off), and its launch on caller-given
-// picks (d.ext_sel / ext_w set; this fills the tables, tagged buffers, epoch and error words of d)
+// the one-token kernel is available (a 256-CU device, the fused decode not switched off); the n <= 8 single-launch
+// block is; and their launch on caller-given picks (d.ext_sel / ext_w set; this fills the tables, tagged buffers,
+// epoch and error words of d): the one-token kernel for one row with all 8 picks when it is available, else the block
 bool decode1_available(FLCtx * c);
-int decode1_picks(FLCtx * c, lk::DecodeArgs & d);
+bool decode_block_available(FLCtx * c);
+int decode_picks(FLCtx * c, lk::DecodeArgs & d);
 lk::ExpertArgs expert_args(FLCtx * c, int n, int P, int shared);
 // counter sets of the two persistent kernels inside FLCtx::cnt
 inline void expert_counters(FLCtx * c, lk::ExpertArgs & a, int down) {

@@ -352,12 +352,19 @@ static int decode_tagged(FLCtx * c, hipStream_t st) {
     return FL_OK;
 }
 bool decode1_available(FLCtx * c) { return c->fused != 0 && decode_ready(c) && decode1_ready(c); }
-int decode1_picks(FLCtx * c, DecodeArgs & d) {
+bool decode_block_available(FLCtx * c) { return c->fused != 0 && decode_ready(c); }
+int decode_picks(FLCtx * c, DecodeArgs & d) {
     if (int rc = decode_tagged(c, c->st)) { return rc; }
     d.tab = c->tab.p; d.tlogits = c->dlogit.p; d.th = c->dth.p; d.to = c->dto.p;
     d.epoch = c->epoch; d.err = c->derr.p; d.herr = c->herr ? c->herr_dev : nullptr;
-    TRY(c, launch_moe_decode1(d, c->fused == 1, c->st));
-    c->last_kernel = 2; c->last_fused = 1;
+    if (d.n == 1 && d.topk == MAXK && d.keep == MAXK && decode1_ready(c)) {
+        TRY(c, launch_moe_decode1(d, c->fused == 1, c->st));
+        c->last_kernel = 2;
+    } else {
+        TRY(c, launch_moe_decode(d, c->dec_grid, c->fused == 1, c->st));
+        c->last_kernel = 1;
+    }
+    c->last_fused = 1;
     return FL_OK;
 }
 static hipError_t launch_decode(FLCtx * c, const DecodeArgs & d, hipStream_t st) {

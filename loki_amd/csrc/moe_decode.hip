@@ -53,7 +53,9 @@ constexpr int L_RT = L_PRE + PRE_BYTES;                           // routing tab
 constexpr int RT_INTS = 4 * DMAX_P + 3 * (DMAX_P + 1) + 1 + 2 * DMAX_PS + 1;
 constexpr int L_CTL = L_RT + RT_INTS * 4;                         // hand-off words [8], staging flags [DW]
 constexpr int L_NRM = L_CTL + (8 + DW) * 4;                       // pre-norm scale per token [DMAX_N]
-constexpr int DEC_LDS = L_NRM + DMAX_N * 4;
+// the caller's picks (ext_sel): per token its distinct ids ascending as [first k][summed weight], then their count
+constexpr int L_EXT = L_NRM + DMAX_N * 4, EXT_TOK = 2 * MAXK + 1;
+constexpr int DEC_LDS = L_EXT + DMAX_N * EXT_TOK * 4;
 static_assert(DEC_LDS <= 160 * 1024, "LDS budget");
 static_assert(DMAX_N * 4 * 8 <= PRE_BYTES, "router sums overlay the early task terms");
 
@@ -649,6 +651,31 @@ __device__ __forceinline__ bool combine_unit(const DArgs & a, lds_t lds, int cu,
         issue();
     }
     if (it == POLL_MAX) { return false; }
+    if (a.ext_sel) {   // fl_moe's combine: the distinct ids ascending, moe = their weighted sum, y = (moe + shared) + resid
+#pragma unroll
+        for (int c = 0; c < CT; ++c) {
+            const int tok = t0 + c * TS;
+            if (tok >= a.n) { continue; }
+            const LK_LOCAL int * xe = reinterpret_cast<const LK_LOCAL int *>(lds + L_EXT) + tok * EXT_TOK;
+            const LK_LOCAL float * xw = reinterpret_cast<const LK_LOCAL float *>(xe + MAXK);
+            const int cnt = xe[2 * MAXK];
+            float v = 0.f;
+            for (int q = 0; q < cnt; ++q) {
+                const int kf = xe[q];
+                float ov = 0.f;
+#pragma unroll
+                for (int k = 0; k < MAXK; ++k) { ov = k == kf ? tag_val(wv[c][k]) : ov; }
+                v = v + xw[q] * ov;
+            }
+            gptr(a.moe_out)[(size_t) tok * DE + rr] = v;
+            gptr(a.y)[(size_t) tok * DE + rr] = (v + tag_val(wv[c][MAXK])) + gptr(a.resid)[(size_t) tok * DE + rr];
+            if (a.o_out) {   // the slots' outputs by pair index (token * keep + k)
+#pragma unroll
+                for (int k = 0; k < MAXK; ++k) { if (k < a.keep) { gptr(a.o_out)[(size_t) (tok * a.keep + k) * DE + rr] = tag_val(wv[c][k]); } }
+            }
+        }
+        return true;
+    }
 #pragma unroll
     for (int c = 0; c < CT; ++c) {
         const int tok = t0 + c * TS;
@@ -688,7 +715,9 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
     tables_dma(lds, a.tab, wave);
     __syncthreads();   // the hand-off words are clear
     if (a.prenorm) { norm_phase(a, lds, wave); }
-    for (int e = blockIdx.x; e < a.n_exp; e += G) { router_phase(a, lds, wave, e); }
+    if (!a.ext_sel) {   // with the caller's picks there is no routing
+        for (int e = blockIdx.x; e < a.n_exp; e += G) { router_phase(a, lds, wave, e); }
+    }
     TRACE(wave, 2);
 
     // 2. wave t polls token t's probabilities while all waves quantise the tokens; wave t then selects token t's experts
@@ -696,7 +725,7 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
     //    without a token run the shared expert's gate/up meanwhile.
     const bool pre = n < DW;
     float bv[4]; uint64_t pw[4];
-    if (wave < n) { load_bias(a.bias, a.n_exp, bv); probs_issue(a, wave, pw); }
+    if (wave < n && !a.ext_sel) { load_bias(a.bias, a.n_exp, bv); probs_issue(a, wave, pw); }
     TRACE(wave, 9);
     local_quant(a, lds, wave);
     TRACE(wave, 10);
@@ -706,15 +735,40 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
     if (wave < n) {
         // the selecting waves run ahead of the streaming ones on their SIMDs until the dispatch is built
         __builtin_amdgcn_s_setprio(3);
-        float pv[4];
-        const bool ok = probs_wait(a, wave, pw, pv);
-        TRACE(wave, 3);
-        if (!ok) { report(a, 2); }
         const RT rt(lds);
-        if (ok) {
-            select_token_p<false>(pv, bv, a.n_exp, a.n_group, a.topk_group, a.topk, a.scale, nullptr, (int *) (rt.sel + wave * a.keep), (float *) (rt.wts + wave * a.keep), a.keep, a.renorm);
-        } else if (lane == 0) {
-            __hip_atomic_fetch_or(ctl + 3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (a.ext_sel) {
+            // the caller's picks of token `wave`; lane 0 also lists its distinct ids ascending, each with its weights
+            // summed in k order and its first k, for the combine (zero sums are dropped, as fl_moe does)
+            const int kk = a.keep, b0 = wave * kk;
+            if (lane < kk) { rt.sel[b0 + lane] = gptr(a.ext_sel)[b0 + lane]; rt.wts[b0 + lane] = gptr(a.ext_w)[b0 + lane]; }
+            lds_visible();
+            if (lane == 0) {
+                LK_LOCAL int * xe = reinterpret_cast<LK_LOCAL int *>(lds + L_EXT) + wave * EXT_TOK;
+                LK_LOCAL float * xw = reinterpret_cast<LK_LOCAL float *>(xe + MAXK);
+                int prev = -1, cnt = 0;
+                for (int it = 0; it < MAXK; ++it) {
+                    int m = 0x7fffffff;
+                    for (int k = 0; k < kk; ++k) { const int v = rt.sel[b0 + k]; if (v > prev && v < m) { m = v; } }
+                    if (m == 0x7fffffff) { break; }
+                    float wt = 0.f; int kf = -1;
+                    for (int k = 0; k < kk; ++k) { if (rt.sel[b0 + k] == m) { wt += rt.wts[b0 + k]; if (kf < 0) { kf = k; } } }
+                    prev = m;
+                    if (wt == 0.f) { continue; }
+                    xe[cnt] = kf; xw[cnt] = wt; ++cnt;
+                }
+                xe[2 * MAXK] = cnt;
+            }
+            TRACE(wave, 3);
+        } else {
+            float pv[4];
+            const bool ok = probs_wait(a, wave, pw, pv);
+            TRACE(wave, 3);
+            if (!ok) { report(a, 2); }
+            if (ok) {
+                select_token_p<false>(pv, bv, a.n_exp, a.n_group, a.topk_group, a.topk, a.scale, nullptr, (int *) (rt.sel + wave * a.keep), (float *) (rt.wts + wave * a.keep), a.keep, a.renorm);
+            } else if (lane == 0) {
+                __hip_atomic_fetch_or(ctl + 3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
         }
         TRACE(wave, 4);
         if (lds_arrive(ctl + 1, (unsigned) n)) {
@@ -756,7 +810,7 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
         if (!combine_unit(a, lds, cu, P)) { report(a, 16); }
         TRACE(wave, 58);
     }
-    if (blockIdx.x == 0 && wave == DW - 1) { routing_outputs(a, lds, P); }
+    if (blockIdx.x == 0 && wave == DW - 1 && !a.ext_sel) { routing_outputs(a, lds, P); }
 #ifdef LOKI_TRACE
     if (lane == 0) { g_trace[(blockIdx.x * DW + wave) * TRACE_SLOTS + 63] = (uint64_t) ntask | ((uint64_t) nunit << 16) | ((uint64_t) t_gu << 32); }
 #endif
@@ -783,8 +837,10 @@ bool decode_rule_ok(int n_exp, int n_group) {   // the selection's DPP group pat
 }
 
 hipError_t launch_moe_decode(const DecodeArgs & a, int grid, bool cooperative, hipStream_t st) {
-    if (a.n < 1 || a.n > DMAX_N || a.topk < 1 || a.topk > MAXK || a.keep < 1 || a.keep > a.topk || !decode_rule_ok(a.n_exp, a.n_group) ||
-        a.E != DE || a.H != DH || grid < 1 || !a.th || !a.to || !a.tlogits || a.kdown != 0) {   // IQ2_XXS matrices only
+    if (a.ext_sel && (!a.ext_w || !a.moe_out || !a.resid || a.prenorm)) { return hipErrorInvalidValue; }   // the caller's picks
+    if (a.n < 1 || a.n > DMAX_N || a.topk < 1 || a.topk > MAXK || a.keep < 1 || a.keep > a.topk ||
+        (!a.ext_sel && !decode_rule_ok(a.n_exp, a.n_group)) || a.E != DE || a.H != DH || grid < 1 || !a.th || !a.to || !a.tlogits ||
+        a.kdown != 0) {   // IQ2_XXS matrices only
         return hipErrorInvalidValue;
     }
     if (!cooperative) {   // one workgroup per CU fits the occupancy; co-residency is assumed, waits stay bounded

@@ -126,6 +126,44 @@ def test_narrow_pass(ctx, small_layer):
     assert np.array_equal(hs.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("n", [3, 8])
+def test_narrow_rows_single_launch(ctx, small_layer, n):
+    """fl_moe on up to 8 rows of an all-IQ2_XXS layer runs as one launch of the n <= 8 block on the caller's picks
+    (regular or cooperative launch; router and selection skipped, the shared expert recomputed in the launch, fl_moe's
+    combine: the distinct ids ascending with their weights summed in k order, zero sums dropped). h, moe, the per-slot
+    attribution (fl_moe_outs) and a following fl_skip are bit-identical to the per-pass kernels; one row gets a repeated
+    id and one pick a zero weight."""
+    from loki_amd import FLOut, lib
+    (W, b, gate, up, down, sh), dev = small_layer
+    ctx.set_routing(8, 4, 8, 2.5)
+    x = gen.uniform(12, n, (n, E), 2.0); fi = gen.uniform(12, n + 10, (n, E), 1.0)
+    mo = gen.uniform(12, n + 20, (n, E), 3.0)
+    flw = _flw(dev)
+    out = FLOut()
+    _, _, so, wo = orc.router(W, b, x, 8, 4, 8, 2.5)
+    ids = so.astype(np.int32).copy(); wts = f32(wo).copy()
+    ids[1, 4] = ids[1, 2]; wts[n - 1, 6] = np.float32(0)
+    got = {}
+    for mode in (2, 1, 0):   # 2: the library default (regular launch); 1: cooperative; 0: the per-pass kernels
+        with ctx.using_fused(mode):
+            ctx.check(lib().fl_ffn_begin(ctx.ctx, ctypes.byref(flw), n, cptr(x), cptr(fi), -1))
+            lib().fl_fetch(ctx.ctx, n, 1, ctypes.byref(out))
+            lib().fl_moe(ctx.ctx, dev["gate"].data_ptr(), dev["up"].data_ptr(), dev["down"].data_ptr(), 16, 4, cptr(ids.ravel().copy()),
+                         cptr(wts.ravel().copy()), KE, n, ctypes.byref(out))
+            assert ctx.debug().kernel == (1 if mode else 0), mode
+            hm = (np.ctypeslib.as_array(out.h, shape=(n * E,)).copy(), np.ctypeslib.as_array(out.moe, shape=(n * E,)).copy())
+            atts = []
+            for r in (0, 1, n - 1):
+                att = np.zeros((KE, E), np.float32)
+                lib().fl_moe_outs(ctx.ctx, r, cptr(ids[r].copy()), cptr(wts[r].copy()), KE, cptr(att))
+                atts.append(att)
+            lib().fl_skip(ctx.ctx, cptr(mo), n, ctypes.byref(out))
+            got[mode] = hm + tuple(atts) + (np.ctypeslib.as_array(out.h, shape=(n * E,)).copy(),)
+    for mode in (2, 1):
+        for i, (a_, b_) in enumerate(zip(got[mode], got[0])):
+            assert np.array_equal(a_.view(np.uint32), b_.view(np.uint32)), (mode, i)
+
+
 def test_f16_router(ctx, small_layer):
     """fl_ffn_begin with an F16 router weight (FLW.gate_f16, fl.cu:317-319): widened exactly, it routes like the F32
     router holding the same values (selections, weights and the shared-expert path), and like the checker on them."""
