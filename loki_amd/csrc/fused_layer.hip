@@ -110,7 +110,7 @@ extern "C" void fl_free(FLCtx * c) {
     compat_free(c); c->zero_i.release(); c->terms.release(); c->cnt.release();
     c->tab.release(); c->derr.release(); c->dlogit.release(); c->dth.release(); c->dto.release();
     c->ptab.release(); c->pcols.release(); c->pncols.release(); c->xh.release(); c->hh.release();
-    c->ksg.release(); c->ksu.release(); c->rcnt.release();
+    c->ksg.release(); c->ksu.release(); c->rcnt.release(); c->rpart.release();
     for (auto & v : c->ev_free) { for (auto e : v) { (void) hipEventDestroy(e); } }
     for (auto & v : c->ev_pending) { for (auto e : v) { (void) hipEventDestroy(e); } }
     (void) hipEventDestroy(c->em0); (void) hipEventDestroy(c->em1); (void) hipStreamDestroy(c->own);
@@ -205,7 +205,9 @@ int route_dev(FLCtx * c, const float * W, const float * bias, const float * x, i
                                    c->epoch, c->rcnt.p, done, c->st));
         return FL_OK;
     }
-    TRY(c, launch_router_logits(W, x, n, n_exp, E, logits, c->st));
+    double * rp = nullptr;   // the K-split tiles' halves (n from RL_SPLIT_MIN to 1023)
+    if (E == 7168 && n >= RL_SPLIT_MIN && n < 1024) { ALLOC(c, c->rpart, (size_t) 2 * n * n_exp); rp = c->rpart.p; }
+    TRY(c, launch_router_logits(W, x, n, n_exp, E, logits, rp, c->st));
     TRY(c, launch_router_select(logits, bias, n, n_exp, c->n_group, c->topk_group, c->topk, c->scale, probs, sel, w, c->st));
     return FL_OK;
 }
@@ -550,7 +552,9 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     TRY(c, launch_quant_q8k(x, n, E, c->xq.p, c->xd.p, st));
     if (mfma) { TRY(c, launch_q8_to_h(c->xq.p, c->xh.p, (int64_t) n * E, st)); }
     prof_mark(c, ev, 1);
-    TRY(c, launch_router_logits(L->gate_inp, x, n, ne, E, c->logits.p, st));
+    double * rp = nullptr;   // the K-split tiles' halves (n from RL_SPLIT_MIN to 1023)
+    if (E == 7168 && n >= RL_SPLIT_MIN && n < 1024) { ALLOC(c, c->rpart, (size_t) 2 * n * ne); rp = c->rpart.p; }
+    TRY(c, launch_router_logits(L->gate_inp, x, n, ne, E, c->logits.p, rp, st));
     prof_mark(c, ev, 2);
     TRY(c, launch_router_select(c->logits.p, L->probs_b, n, ne, c->n_group, c->topk_group, tsel, c->scale, c->probs.p, c->sel.p, c->wts.p, st, tk, renorm));
     prof_mark(c, ev, 3);

@@ -11,7 +11,9 @@ namespace lk {
 hipError_t launch_quant_q8k(const float * x, int64_t nrows, int K, int8_t * q, float * d, hipStream_t st);
 
 // router logits [n][n_exp] under the fp64 chunk contract (K % 256 == 0)
-hipError_t launch_router_logits(const float * W, const float * x, int n, int n_exp, int K, float * logits, hipStream_t st);
+// part2: fp64 scratch of 2 * n * n_exp for the K-split tiles (RL_SPLIT_MIN <= n < 1024, K 7168); may be null
+constexpr int RL_SPLIT_MIN = 256;
+hipError_t launch_router_logits(const float * W, const float * x, int n, int n_exp, int K, float * logits, double * part2, hipStream_t st);
 // sigmoid, bias, grouped top-k, normalised weights; probs [n][n_exp], sel/wts [n][keep]: with 0 < keep < topk each
 // row keeps its keep heaviest picks (rescaled to sum to renorm when renorm > 0), else all topk
 hipError_t launch_router_select(const float * logits, const float * bias, int n, int n_exp, int n_group, int topk_group,

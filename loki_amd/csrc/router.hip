@@ -281,14 +281,17 @@ __global__ void __launch_bounds__(64 * NQ) k_router_tile(const float * __restric
 // fp64 once and staged in the wave's own LDS buffer, where the lanes read them back (8 lanes share each row: a broadcast).
 // Without the staging every lane loads and converts its 8 rows itself: 8x the load instructions and the conversions, and
 // the texture unit's load rate bounds the kernel. The next chunk's raw values are in registers while a chunk computes.
+// With KS = 2 the chunks are split over two workgroups (blockIdx.z: the first or second 128), each forming its half's
+// subtree (levels 1-7) into part2[z]; k_router_join adds the halves, the tree's top level (one fp64 add, commutative).
+// That puts twice the workgroups on the chip where 32 x 32 tiles alone leave CUs idle (under 1024 tokens).
 // Buffer layout, per operand: [block i (4 values)][row r % 4][half h][row r / 4] of 16 bytes (2 doubles), so a read of
 // one (i, r % 4, h) by the wave touches 8 consecutive 16-byte slots: every bank once.
 constexpr int RL_SLOTS = 7 * 4 * 2 * 8;   // 16-byte slots per operand and chunk
-template <int NQ>
+template <int NQ, int KS>
 __global__ void __launch_bounds__(64 * NQ) k_router_lds(const float * __restrict__ W, const float * __restrict__ x, int n, int n_exp,
-                                                         float * __restrict__ logits) {
+                                                         float * __restrict__ logits, double * __restrict__ part2) {
 #pragma clang fp contract(off)
-    constexpr int K = 7168, CL = 28, CPW = 256 / NQ, LW = CPW == 64 ? 6 : CPW == 32 ? 5 : 4;
+    constexpr int K = 7168, CL = 28, CPW = 256 / (NQ * KS), LW = CPW == 64 ? 6 : CPW == 32 ? 5 : 4;
     static_assert(CPW == (1 << LW) && LW >= 4, "slices of 16, 32 or 64 chunks");
     static_assert(NQ * 16 * 64 * 8 <= NQ * 2 * RL_SLOTS * 16, "the slices' totals fit the staging buffers");
     __shared__ __attribute__((aligned(16))) double2 buf[NQ][2][RL_SLOTS];   // [wave][x, W][slot]; then the slices' totals
@@ -346,7 +349,7 @@ __global__ void __launch_bounds__(64 * NQ) k_router_lds(const float * __restrict
             }
         }
     };
-    const int c0 = q * CPW;
+    const int c0 = (KS == 1 ? 0 : (int) blockIdx.z * (256 / KS)) + q * CPW;
     fetch(c0);
     int cn = 0;   // chunks of the slice consumed
     // one chunk: stage the fetched values, fetch the next chunk's, compute (a wave's LDS operations run in order, so the
@@ -404,17 +407,32 @@ __global__ void __launch_bounds__(64 * NQ) k_router_lds(const float * __restrict
 #pragma unroll
             for (int j = 0; j + w < NQ; j += 2 * w) { v[j] = v[j] + v[j + w]; }
         }
-        if (t < n && e < n_exp) { logits[(size_t) t * n_exp + e] = (float) v[0]; }
+        if (t < n && e < n_exp) {
+            if constexpr (KS == 1) { logits[(size_t) t * n_exp + e] = (float) v[0]; }
+            else { part2[((size_t) blockIdx.z * n + t) * n_exp + e] = v[0]; }
+        }
     }
 }
+// the top level of the K-split tree: logit = (float) (first half + second half)
+__global__ void __launch_bounds__(256) k_router_join(const double * __restrict__ part2, int total, float * __restrict__ logits) {
+#pragma clang fp contract(off)
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < total) { logits[i] = (float) (part2[i] + part2[(size_t) total + i]); }
+}
 
-hipError_t launch_router_logits(const float * W, const float * x, int n, int n_exp, int K, float * logits, hipStream_t st) {
+hipError_t launch_router_logits(const float * W, const float * x, int n, int n_exp, int K, float * logits, double * part2, hipStream_t st) {
     if (n <= 0) { return hipSuccess; }
     if (K % 1024 != 0) { return hipErrorInvalidValue; }
     // measured on MI355X: k_router_wg costs ~0.6 us per token (every workgroup reads all of x), the 4 x 2 tiles a flat
     // ~150 us from 64 to 512 tokens; the crossover is near 256
     if (K == 7168 && n >= 1024) {   // 32 x 32 tiles (4 x 4 per lane), staged in LDS
-        k_router_lds<4><<<dim3((n_exp + 31) / 32, (n + 31) / 32), 256, 0, st>>>(W, x, n, n_exp, logits);
+        k_router_lds<4, 1><<<dim3((n_exp + 31) / 32, (n + 31) / 32), 256, 0, st>>>(W, x, n, n_exp, logits, nullptr);
+        return hipGetLastError();
+    }
+    if (K == 7168 && n >= RL_SPLIT_MIN && part2) {   // the same tiles, K split over two workgroups, then the join
+        k_router_lds<4, 2><<<dim3((n_exp + 31) / 32, (n + 31) / 32, 2), 256, 0, st>>>(W, x, n, n_exp, nullptr, part2);
+        const int total = n * n_exp;
+        k_router_join<<<dim3((total + 255) / 256), 256, 0, st>>>(part2, total, logits);
         return hipGetLastError();
     }
     if (K == 7168 && n >= RW_MAXN) {   // 32 x 16 tiles (4 x 2 per lane)
