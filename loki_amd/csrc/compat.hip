@@ -191,17 +191,21 @@ struct Compat {
     int * wt_i[2] = { nullptr, nullptr }; float * wt_w[2] = { nullptr, nullptr }; size_t wt_cap[2] = { 0, 0 };
     hipEvent_t wt_ev[2] = { nullptr, nullptr }; bool wt_rec[2] = { false, false };   // after each parity's table copies
     // pinned host mirrors
-    int * h_sel = nullptr; float * h_wts = nullptr, * h_ncur = nullptr, * h_fi = nullptr, * h_h = nullptr, * h_moe = nullptr;
+    int * h_sel = nullptr; float * h_wts = nullptr, * h_h = nullptr, * h_moe = nullptr;
     // kernel-written host memory (no copies): the router's picks of the RMAX rows then their weights (z_sel), then
     // the one-launch routing's done word (at ZS_DONE); fl_moe's single launch's ids then (at NB * MAXK) weights (z_in)
     // and its h rows then (at NB * E) moe rows (z_out); *_d = the device addresses. r_tagged: the last fl_ffn_begin's routing sets the done word, to rtag
     int * z_sel = nullptr, * z_sel_d = nullptr, * z_in = nullptr, * z_in_d = nullptr; float * z_out = nullptr, * z_out_d = nullptr;
     unsigned rtag = 0; bool r_tagged = false;
-    float * h_wh = nullptr, * h_wmoe = nullptr;
-    // pinned staging of the host inputs (pageable copies would wait for the stream): fl_ffn_begin's ncur / ffn_inp,
-    // fl_moe's ids / w; in_ev is recorded after their copies and waited before the buffers are refilled
-    // (in_ncur holds ncur's rows then ffn_inp's, in_fi points at the latter)
-    float * in_ncur = nullptr, * in_fi = nullptr, * in_w = nullptr; int * in_ids = nullptr;
+    // the wide pass's h / moe rows in mapped host memory, written there by k_wide_finish / k_wide_skip (no copy back)
+    float * h_wh = nullptr, * h_wmoe = nullptr, * h_wh_d = nullptr, * h_wmoe_d = nullptr;
+    // pinned staging of the host inputs (pageable copies would wait for the stream). fl_ffn_begin's ncur / ffn_inp go
+    // to in_st[p] (ncur's rows, then ffn_inp's), p alternating per call; in_ncur / in_fi point at the last call's, and
+    // fl_fetch hands them out as its ncur / fi mirrors, which therefore hold until the second fl_ffn_begin after it
+    // (the reference's mirrors are replaced by the next call). st_ev[p] is recorded after in_st[p]'s copy and waited
+    // before it is refilled. fl_moe's ids / w go to in_ids, in_ev likewise.
+    float * in_st[2] = { nullptr, nullptr }, * in_ncur = nullptr, * in_fi = nullptr, * in_w = nullptr; int * in_ids = nullptr;
+    hipEvent_t st_ev[2] = { nullptr, nullptr }; bool st_rec[2] = { false, false }; int st_par = 0;
     hipEvent_t in_ev = nullptr; bool in_rec = false;
 };
 
@@ -211,14 +215,14 @@ static Compat * cs(FLCtx * c) {
         s->z_sel = mapped<int>(ZS_DONE + 16, &s->z_sel_d); s->z_in = mapped<int>(2 * NB * MAXK, &s->z_in_d);
         s->z_out = mapped<float>((size_t) 2 * NB * E_, &s->z_out_d);
         s->h_sel = pinned<int>(RMAX * MAXK); s->h_wts = pinned<float>(RMAX * MAXK);
-        s->h_ncur = pinned<float>((size_t) RMAX * E_); s->h_fi = pinned<float>((size_t) RMAX * E_);
         s->h_h = pinned<float>((size_t) RMAX * E_); s->h_moe = pinned<float>((size_t) RMAX * E_);
-        s->in_ncur = pinned<float>((size_t) 2 * RMAX * E_);
+        s->in_st[0] = pinned<float>((size_t) 2 * RMAX * E_); s->in_st[1] = pinned<float>((size_t) 2 * RMAX * E_);
         s->in_ids = pinned<int>(2 * NB * MAXK); s->in_w = pinned<float>(NB * MAXK);   // in_ids: ids, then the weights
-        if (!s->z_sel || !s->z_in || !s->z_out || !s->h_sel || !s->h_wts || !s->h_ncur || !s->h_fi || !s->h_h || !s->h_moe || !s->in_ncur || !s->in_ids || !s->in_w) {
+        if (!s->z_sel || !s->z_in || !s->z_out || !s->h_sel || !s->h_wts || !s->h_h || !s->h_moe || !s->in_st[0] || !s->in_st[1] || !s->in_ids || !s->in_w) {
             fatal("hipHostMalloc (fused-layer mirrors)", hipErrorOutOfMemory, __FILE__, __LINE__);
         }
         CK(hipEventCreateWithFlags(&s->in_ev, hipEventDisableTiming));
+        for (hipEvent_t & e : s->st_ev) { CK(hipEventCreateWithFlags(&e, hipEventDisableTiming)); }
         c->compat = s;
     }
     return c->compat;
@@ -228,8 +232,9 @@ void compat_free(FLCtx * c) {
     Compat * s = c->compat;
     if (!s) { return; }
     if (s->in_ev) { (void) hipEventSynchronize(s->in_ev); (void) hipEventDestroy(s->in_ev); }
-    for (void * p : { (void *) s->z_sel, (void *) s->z_in, (void *) s->z_out, (void *) s->h_sel, (void *) s->h_wts, (void *) s->h_ncur, (void *) s->h_fi, (void *) s->h_h, (void *) s->h_moe, (void *) s->h_wh, (void *) s->h_wmoe,
-                      (void *) s->in_ncur, (void *) s->in_ids, (void *) s->in_w }) {
+    for (hipEvent_t e : s->st_ev) { if (e) { (void) hipEventSynchronize(e); (void) hipEventDestroy(e); } }
+    for (void * p : { (void *) s->z_sel, (void *) s->z_in, (void *) s->z_out, (void *) s->h_sel, (void *) s->h_wts, (void *) s->h_h, (void *) s->h_moe, (void *) s->h_wh, (void *) s->h_wmoe,
+                      (void *) s->in_st[0], (void *) s->in_st[1], (void *) s->in_ids, (void *) s->in_w }) {
         if (p) { (void) hipHostFree(p); }
     }
     for (hipEvent_t e : s->wev) { if (e) { (void) hipEventDestroy(e); } }
@@ -490,11 +495,24 @@ extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur,
     ALLOC(c, s->ncur, 2 * R); ALLOC(c, s->logits, RMAX * ne); ALLOC(c, s->probs, RMAX * ne);
     ALLOC(c, s->xq, R); ALLOC(c, s->xd, RMAX * (E_ / QK)); ALLOC(c, s->sh_o, R);
     hipStream_t st = c->st;
-    if (s->in_rec) { TRY(c, hipEventSynchronize(s->in_ev)); }   // the staging's previous copies have run
-    s->in_fi = s->in_ncur + (size_t) N * E_; s->fi = s->ncur.p + (size_t) N * E_;
-    std::memcpy(s->in_ncur, ncur, (size_t) N * E_ * 4); std::memcpy(s->in_fi, ffn_inp, (size_t) N * E_ * 4);
-    TRY(c, hipMemcpyAsync(s->ncur.p, s->in_ncur, (size_t) 2 * N * E_ * 4, hipMemcpyHostToDevice, st));
-    TRY(c, hipEventRecord(s->in_ev, st)); s->in_rec = true;
+    const int sp = s->st_par ^= 1;
+    if (s->st_rec[sp]) { TRY(c, hipEventSynchronize(s->st_ev[sp])); }   // this staging's previous copy has run
+    s->in_ncur = s->in_st[sp]; s->in_fi = s->in_ncur + (size_t) N * E_; s->fi = s->ncur.p + (size_t) N * E_;
+    {   // staged and sent in pieces: each piece's DMA runs while the next piece is copied into the staging
+        constexpr size_t PIECE = (size_t) 1 << 20;
+        const size_t nb = (size_t) N * E_ * 4;
+        const uint8_t * src[2] = { reinterpret_cast<const uint8_t *>(ncur), reinterpret_cast<const uint8_t *>(ffn_inp) };
+        uint8_t * stg[2] = { reinterpret_cast<uint8_t *>(s->in_ncur), reinterpret_cast<uint8_t *>(s->in_fi) };
+        uint8_t * dst[2] = { reinterpret_cast<uint8_t *>(s->ncur.p), reinterpret_cast<uint8_t *>(s->fi) };
+        for (int a = 0; a < 2; ++a) {
+            for (size_t o = 0; o < nb; o += PIECE) {
+                const size_t len = std::min(PIECE, nb - o);
+                std::memcpy(stg[a] + o, src[a] + o, len);
+                TRY(c, hipMemcpyAsync(dst[a] + o, stg[a] + o, len, hipMemcpyHostToDevice, st));
+            }
+        }
+    }
+    TRY(c, hipEventRecord(s->st_ev[sp], st)); s->st_rec[sp] = true;
     const size_t mg = mat_bytes(H_, E_);
     const void * shm[3] = { W->sh_gate, W->sh_up, W->sh_down };
     bool sht[3];
@@ -549,11 +567,11 @@ extern "C" void fl_fetch(FLCtx * c, int n, int what, FLOut * out) {
     if (what & 1) {
         // the mirrors keep this call's values until the next fl_fetch whatever is enqueued meanwhile (the reference's
         // lifetime). ncur and ffn_inp are on the device exactly as the caller handed them to fl_ffn_begin (nothing
-        // writes them), and its pinned staging still holds them: their mirrors are filled from there
+        // writes them), and that call's pinned staging holds them until the second fl_ffn_begin after it: the ncur and
+        // fi mirrors are that staging itself
         const size_t pk = (size_t) n * c->topk;
         std::memcpy(s->h_sel, s->z_sel, pk * 4); std::memcpy(s->h_wts, s->z_sel + (size_t) s->N * c->topk, pk * 4);
-        std::memcpy(s->h_ncur, s->in_ncur, (size_t) n * E_ * 4); std::memcpy(s->h_fi, s->in_fi, (size_t) n * E_ * 4);
-        out->sel = s->h_sel; out->wts = s->h_wts; out->ncur = s->h_ncur; out->fi = s->h_fi;
+        out->sel = s->h_sel; out->wts = s->h_wts; out->ncur = s->in_ncur; out->fi = s->in_fi;
     }
 }
 
@@ -680,7 +698,7 @@ extern "C" int fl_wide_init(FLCtx * c, int wmax, int KE) {
     FALLOC(s->fi_all, R); FALLOC(s->sh_all, R); FALLOC(s->base_all, R); s->wide_pending = false; FALLOC(s->out_all, R * KE); FALLOC(s->xq_all, R); FALLOC(s->xd_all, (size_t) wmax * (E_ / QK));
     CK(hipMemset(s->out_all.p, 0, R * KE * 4));
     if (s->h_wh) { (void) hipHostFree(s->h_wh); } if (s->h_wmoe) { (void) hipHostFree(s->h_wmoe); }
-    s->h_wh = pinned<float>(R); s->h_wmoe = pinned<float>(R);
+    s->h_wh = mapped<float>(R, &s->h_wh_d); s->h_wmoe = mapped<float>(R, &s->h_wmoe_d);
     if (!s->h_wh || !s->h_wmoe) { fatal("hipHostMalloc (wide-pass mirrors)", hipErrorOutOfMemory, __FILE__, __LINE__); }
     for (hipEvent_t & e : s->wev) { if (!e) { CK(hipEventCreateWithFlags(&e, hipEventDisableTiming)); } }
     return 1;
@@ -777,12 +795,9 @@ extern "C" void fl_wide_finish(FLCtx * c, int n, int KE, FLOut * out) {
     Compat * s = cs(c);
     if (n <= 0 || n > s->wmax || KE != s->wke) { std::fprintf(stderr, "[fused] fl_wide_finish: n %d (wmax %d), KE %d (init %d)\n", n, s->wmax, KE, s->wke); std::exit(7); }
     hipStream_t st = c->st; const int64_t tot = (int64_t) n * E_;
-    FALLOC(s->hout, (size_t) tot); FALLOC(s->moe, (size_t) tot);
     wide_base(c, s, n);
-    k_wide_finish<<<nblk(tot), 256, 0, st>>>(s->base_all.p, s->out_all.p, KE, tot, s->hout.p, s->moe.p);
+    k_wide_finish<<<nblk(tot), 256, 0, st>>>(s->base_all.p, s->out_all.p, KE, tot, s->h_wh_d, s->h_wmoe_d);
     CK(hipGetLastError());
-    CK(hipMemcpyAsync(s->h_wh, s->hout.p, (size_t) tot * 4, hipMemcpyDeviceToHost, st));
-    CK(hipMemcpyAsync(s->h_wmoe, s->moe.p, (size_t) tot * 4, hipMemcpyDeviceToHost, st));
     CK(hipStreamSynchronize(st));
     out->h = s->h_wh; out->moe = s->h_wmoe;
 }
@@ -792,12 +807,11 @@ extern "C" void fl_wide_skip(FLCtx * c, const float * mo, int n, FLOut * out) {
     Compat * s = cs(c);
     if (n <= 0 || n > s->wmax) { std::fprintf(stderr, "[fused] fl_wide_skip: n %d (wmax %d)\n", n, s->wmax); std::exit(7); }
     hipStream_t st = c->st; const int64_t tot = (int64_t) n * E_;
-    FALLOC(s->hout, (size_t) tot); FALLOC(s->moe, (size_t) tot);
+    FALLOC(s->moe, (size_t) tot);
     wide_base(c, s, n);
     CK(hipMemcpyAsync(s->moe.p, mo, (size_t) tot * 4, hipMemcpyHostToDevice, st));
-    k_wide_skip<<<nblk(tot), 256, 0, st>>>(s->base_all.p, s->moe.p, tot, s->hout.p);
+    k_wide_skip<<<nblk(tot), 256, 0, st>>>(s->base_all.p, s->moe.p, tot, s->h_wh_d);
     CK(hipGetLastError());
-    CK(hipMemcpyAsync(s->h_wh, s->hout.p, (size_t) tot * 4, hipMemcpyDeviceToHost, st));
     CK(hipStreamSynchronize(st));
     out->h = s->h_wh;
 }

@@ -74,6 +74,32 @@ def _arena(dev, used):
     return take(dev["gate"]), take(dev["up"]), take(dev["down"])
 
 
+def test_fetch_mirrors_hold(ctx, small_layer):
+    """fl_fetch's ncur / fi mirrors: the rows handed to fl_ffn_begin, still intact after the next fl_ffn_begin (the
+    reference replaces its mirrors at the next call; here they hold until the second fl_ffn_begin after them), and the
+    next fl_fetch hands out that call's rows."""
+    from loki_amd import FLOut, lib
+    (W, b, gate, up, down, sh), dev = small_layer
+    ctx.set_routing(8, 4, 8, 2.5)
+    flw = _flw(dev)
+    rows = [(gen.uniform(7, 30 + i, (n, E), 2.0), gen.uniform(7, 40 + i, (n, E), 1.0)) for i, n in enumerate((5, 64, 2))]
+    outs = []
+    for x, fi in rows:
+        ctx.check(lib().fl_ffn_begin(ctx.ctx, ctypes.byref(flw), x.shape[0], cptr(x), cptr(fi), -1))
+        if outs:   # the previous fetch's mirrors survive this call
+            px, pfi, po = outs[-1]
+            n0 = px.shape[0]
+            assert np.array_equal(np.ctypeslib.as_array(po.ncur, shape=(n0 * E,)).reshape(n0, E), px)
+            assert np.array_equal(np.ctypeslib.as_array(po.fi, shape=(n0 * E,)).reshape(n0, E), pfi)
+        out = FLOut()
+        lib().fl_fetch(ctx.ctx, x.shape[0], 1, ctypes.byref(out))
+        n = x.shape[0]
+        assert np.array_equal(np.ctypeslib.as_array(out.ncur, shape=(n * E,)).reshape(n, E), x)
+        assert np.array_equal(np.ctypeslib.as_array(out.fi, shape=(n * E,)).reshape(n, E), fi)
+        outs.append((x, fi, out))
+    ctx.sync()
+
+
 def test_narrow_pass(ctx, small_layer):
     """fl_ffn_begin -> fl_fetch -> host dispatch (sorted unique experts, slot ids) -> fl_moe, as the engine does;
     h = routed + shared + ffn_inp with moe_combine's ascending-slot order (src/fused_layer.cu:366-372)."""
