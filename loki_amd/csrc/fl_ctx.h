@@ -64,7 +64,7 @@ struct FLCtx {
     int lf[4] = { FL_IQ2, FL_IQ2, FL_IQ2, FL_IQ2 };
     DBuf<float> ksg, ksu;                      // K-quant shared gate / up outputs
     DBuf<unsigned> rcnt;                       // the one-launch routing's self-resetting counter (launch_router_fused)
-    DBuf<double> rpart;                        // the K-split router tiles' two halves [2][n][n_exp]
+    DBuf<double> rpart;                        // the K-split router tiles' parts [KS][n][n_exp]
 };
 // fl_route_dev with, for the one-launch routing of a few rows (router_fused_ok), a host word set to the context's epoch
 // (as it is after the call) once the picks are written; done may be null, other sizes leave it alone

@@ -281,9 +281,10 @@ __global__ void __launch_bounds__(64 * NQ) k_router_tile(const float * __restric
 // fp64 once and staged in the wave's own LDS buffer, where the lanes read them back (8 lanes share each row: a broadcast).
 // Without the staging every lane loads and converts its 8 rows itself: 8x the load instructions and the conversions, and
 // the texture unit's load rate bounds the kernel. The next chunk's raw values are in registers while a chunk computes.
-// With KS = 2 the chunks are split over two workgroups (blockIdx.z: the first or second 128), each forming its half's
-// subtree (levels 1-7) into part2[z]; k_router_join adds the halves, the tree's top level (one fp64 add, commutative).
-// That puts twice the workgroups on the chip where 32 x 32 tiles alone leave CUs idle (under 1024 tokens).
+// With KS > 1 the chunks are split over KS workgroups (blockIdx.z takes chunks z * 256 / KS ..), each forming its
+// part's subtree into part2[z]; k_router_join adds the parts pairwise in order, the tree's top log2(KS) levels (for
+// KS = 2 one fp64 add, commutative). That puts KS times the workgroups on the chip where 32 x 32 tiles alone leave CUs
+// idle (under 1024 tokens); a 16-way split runs one wave per workgroup.
 // Buffer layout, per operand: [block i (4 values)][row r % 4][half h][row r / 4] of 16 bytes (2 doubles), so a read of
 // one (i, r % 4, h) by the wave touches 8 consecutive 16-byte slots: every bank once.
 constexpr int RL_SLOTS = 7 * 4 * 2 * 8;   // 16-byte slots per operand and chunk
@@ -413,26 +414,56 @@ __global__ void __launch_bounds__(64 * NQ) k_router_lds(const float * __restrict
         }
     }
 }
-// the top level of the K-split tree: logit = (float) (first half + second half)
+// the top levels of the K-split tree: the KS parts added pairwise in order, then rounded to fp32
+template <int KS>
 __global__ void __launch_bounds__(256) k_router_join(const double * __restrict__ part2, int total, float * __restrict__ logits) {
 #pragma clang fp contract(off)
     const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < total) { logits[i] = (float) (part2[i] + part2[(size_t) total + i]); }
+    if (i >= total) { return; }
+    double v[KS];
+#pragma unroll
+    for (int j = 0; j < KS; ++j) { v[j] = part2[(size_t) j * total + i]; }
+#pragma unroll
+    for (int w = 1; w < KS; w *= 2) {
+#pragma unroll
+        for (int j = 0; j + w < KS; j += 2 * w) { v[j] = v[j] + v[j + w]; }
+    }
+    logits[i] = (float) v[0];
+}
+
+// the K split for n tokens: enough parts that tiles x parts reach the 256 CUs (1 below RL_SPLIT_MIN and from 1024)
+static int router_split(int n, int n_exp, int K) {
+    if (K != 7168 || n < RL_SPLIT_MIN || n >= 1024) { return 1; }
+    const int tiles = ((n_exp + 31) / 32) * ((n + 31) / 32);
+    int ks = 2;
+    while (ks < 16 && tiles * ks < 256) { ks *= 2; }
+    return ks;
+}
+size_t router_split_doubles(int n, int n_exp, int K) {
+    const int ks = router_split(n, n_exp, K);
+    return ks > 1 ? (size_t) ks * n * n_exp : 0;
 }
 
 hipError_t launch_router_logits(const float * W, const float * x, int n, int n_exp, int K, float * logits, double * part2, hipStream_t st) {
     if (n <= 0) { return hipSuccess; }
     if (K % 1024 != 0) { return hipErrorInvalidValue; }
-    // measured on MI355X: k_router_wg costs ~0.6 us per token (every workgroup reads all of x), the 4 x 2 tiles a flat
-    // ~150 us from 64 to 512 tokens; the crossover is near 256
+    // measured on MI355X (route call wall time): k_router_wg costs ~0.6 us per token (every workgroup reads all of x);
+    // the K-split tiles a flat ~40 us to 64 tokens, 46 us at 128, 57 us at 255 (16 chunks per wave), 102 us from 300
+    // to 512 (32); the crossover is near 64-96 tokens
     if (K == 7168 && n >= 1024) {   // 32 x 32 tiles (4 x 4 per lane), staged in LDS
         k_router_lds<4, 1><<<dim3((n_exp + 31) / 32, (n + 31) / 32), 256, 0, st>>>(W, x, n, n_exp, logits, nullptr);
         return hipGetLastError();
     }
-    if (K == 7168 && n >= RL_SPLIT_MIN && part2) {   // the same tiles, K split over two workgroups, then the join
-        k_router_lds<4, 2><<<dim3((n_exp + 31) / 32, (n + 31) / 32, 2), 256, 0, st>>>(W, x, n, n_exp, nullptr, part2);
+    if (const int ks = router_split(n, n_exp, K); ks > 1 && part2) {   // the same tiles, K split, then the join
+        const dim3 g((n_exp + 31) / 32, (n + 31) / 32, ks);
         const int total = n * n_exp;
-        k_router_join<<<dim3((total + 255) / 256), 256, 0, st>>>(part2, total, logits);
+        const dim3 gj((total + 255) / 256);
+        switch (ks) {
+        case 2: k_router_lds<4, 2><<<g, 256, 0, st>>>(W, x, n, n_exp, nullptr, part2); k_router_join<2><<<gj, 256, 0, st>>>(part2, total, logits); break;
+        case 4: k_router_lds<4, 4><<<g, 256, 0, st>>>(W, x, n, n_exp, nullptr, part2); k_router_join<4><<<gj, 256, 0, st>>>(part2, total, logits); break;
+        case 8: k_router_lds<2, 8><<<g, 128, 0, st>>>(W, x, n, n_exp, nullptr, part2); k_router_join<8><<<gj, 256, 0, st>>>(part2, total, logits); break;
+        default: k_router_lds<1, 16><<<g, 64, 0, st>>>(W, x, n, n_exp, nullptr, part2); k_router_join<16><<<gj, 256, 0, st>>>(part2, total, logits); break;
+        }
         return hipGetLastError();
     }
     if (K == 7168 && n >= RW_MAXN) {   // 32 x 16 tiles (4 x 2 per lane)
