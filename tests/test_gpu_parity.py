@@ -88,6 +88,24 @@ def test_router_bitwise(ctx, layer, n, rule):
     assert np.array_equal(w.cpu().numpy().view(np.uint32), wo.view(np.uint32))
 
 
+# a layer whose expert count is not a multiple of the 32-expert tiles (48 = 8 groups of 6): the last expert tile is
+# ragged in every logit kernel, the K-split tiles (96: 16 parts, 300: 4 parts) and whole tiles (1030) included
+@pytest.mark.parametrize("n", [9, 96, 300, 1030])
+def test_router_bitwise_ragged_experts(ctx, n):
+    import torch
+    g = torch.Generator(device="cpu").manual_seed(500 + n)
+    W = (torch.randn(48, E, generator=g) * 0.02).cuda()
+    b = (torch.randn(48, generator=g) * 0.05).cuda()
+    x = make_x(ctx, n, seed=600 + n)
+    logits, probs, sel, w = ctx.route(W, b, x)
+    ctx.sync()
+    lo, po, so, wo = orc.router(W.cpu().numpy(), b.cpu().numpy(), x.cpu().numpy(), 8, 4, 8, 2.5)
+    assert np.array_equal(logits.cpu().numpy().view(np.uint32), lo.view(np.uint32))
+    assert np.array_equal(probs.cpu().numpy().view(np.uint32), po.view(np.uint32))
+    assert np.array_equal(sel.cpu().numpy(), so)
+    assert np.array_equal(w.cpu().numpy().view(np.uint32), wo.view(np.uint32))
+
+
 @pytest.mark.parametrize("n,skew", [(1, 0), (8, 0), (512, 0), (2048, 1), (2048, 2)])
 def test_dispatch_bitwise(ctx, n, skew):
     import torch
