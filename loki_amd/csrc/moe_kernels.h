@@ -11,9 +11,10 @@ namespace lk {
 hipError_t launch_quant_q8k(const float * x, int64_t nrows, int K, int8_t * q, float * d, hipStream_t st);
 
 // router logits [n][n_exp] under the fp64 chunk contract (K % 256 == 0)
-// part2: fp64 scratch of router_split_doubles(n, n_exp, K) for the K-split tiles (RL_SPLIT_MIN <= n < 1024, K 7168);
-// may be null (then the split is not used)
-constexpr int RL_SPLIT_MIN = 80;   // below it one workgroup per expert (k_router_wg) is as fast or faster
+// part2: fp64 scratch of router_split_doubles(n, n_exp, K) for the K-split tiles (RL_SPLIT_MIN <= n <= RL_SPLIT_MAX,
+// K 7168); may be null (then the split is not used)
+constexpr int RL_SPLIT_MIN = 40;     // below it one workgroup per expert (k_router_wg) is as fast or faster
+constexpr int RL_SPLIT_MAX = 2048;   // above it the whole LDS tiles (scratch 16 x n x n_exp doubles at most 64 MiB)
 size_t router_split_doubles(int n, int n_exp, int K);
 hipError_t launch_router_logits(const float * W, const float * x, int n, int n_exp, int K, float * logits, double * part2, hipStream_t st);
 // sigmoid, bias, grouped top-k, normalised weights; probs [n][n_exp], sel/wts [n][keep]: with 0 < keep < topk each

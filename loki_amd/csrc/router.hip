@@ -282,9 +282,9 @@ __global__ void __launch_bounds__(64 * NQ) k_router_tile(const float * __restric
 // Without the staging every lane loads and converts its 8 rows itself: 8x the load instructions and the conversions, and
 // the texture unit's load rate bounds the kernel. The next chunk's raw values are in registers while a chunk computes.
 // With KS > 1 the chunks are split over KS workgroups (blockIdx.z takes chunks z * 256 / KS ..), each forming its
-// part's subtree into part2[z]; k_router_join adds the parts pairwise in order, the tree's top log2(KS) levels (for
-// KS = 2 one fp64 add, commutative). That puts KS times the workgroups on the chip where 32 x 32 tiles alone leave CUs
-// idle (under 1024 tokens); a 16-way split runs one wave per workgroup.
+// part's subtree into part2[z]; k_router_join adds the parts pairwise in order, the tree's top log2(KS) levels. The
+// split that is launched, <2, 16>, gives each wave 8 chunks and needs 250 VGPRs, so two waves share a SIMD: the chunks'
+// load latencies, which bound the whole tiles (64 chunks per wave, one wave per SIMD), overlap.
 // Buffer layout, per operand: [block i (4 values)][row r % 4][half h][row r / 4] of 16 bytes (2 doubles), so a read of
 // one (i, r % 4, h) by the wave touches 8 consecutive 16-byte slots: every bank once.
 constexpr int RL_SLOTS = 7 * 4 * 2 * 8;   // 16-byte slots per operand and chunk
@@ -292,8 +292,9 @@ template <int NQ, int KS>
 __global__ void __launch_bounds__(64 * NQ) k_router_lds(const float * __restrict__ W, const float * __restrict__ x, int n, int n_exp,
                                                          float * __restrict__ logits, double * __restrict__ part2) {
 #pragma clang fp contract(off)
-    constexpr int K = 7168, CL = 28, CPW = 256 / (NQ * KS), LW = CPW == 64 ? 6 : CPW == 32 ? 5 : 4;
-    static_assert(CPW == (1 << LW) && LW >= 4, "slices of 16, 32 or 64 chunks");
+    constexpr int K = 7168, CL = 28, CPW = 256 / (NQ * KS), LW = CPW == 64 ? 6 : CPW == 32 ? 5 : CPW == 16 ? 4 : 3;
+    constexpr int GN = CPW < 16 ? CPW : 16;   // chunks per tree group (the group's levels run as the chunks arrive)
+    static_assert(CPW == (1 << LW) && LW >= 3, "slices of 8, 16, 32 or 64 chunks");
     static_assert(NQ * 16 * 64 * 8 <= NQ * 2 * RL_SLOTS * 16, "the slices' totals fit the staging buffers");
     __shared__ __attribute__((aligned(16))) double2 buf[NQ][2][RL_SLOTS];   // [wave][x, W][slot]; then the slices' totals
     const int q = threadIdx.x >> 6, lane = lane_id(), tg = lane >> 3, eg = lane & 7;
@@ -362,10 +363,10 @@ __global__ void __launch_bounds__(64 * NQ) k_router_lds(const float * __restrict
         ++cn;
     };
     // the slice's pairwise tree: 16-chunk groups built as the chunks arrive (binary counter), then levels 5 and 6
-    auto tile16 = [&]() {
+    auto tile16 = [&]() {   // GN chunks (16; for 8-chunk slices the loop ends at c = 7 with v the group's total)
         RgAcc<4, 4> pend[4], v;
 #pragma unroll 1
-        for (int c = 0; c < 16; ++c) {
+        for (int c = 0; c < GN; ++c) {
             next_chunk(v);
             if (!(c & 1)) { pend[0] = v; continue; }
             rg_add(v, pend[0], v);
@@ -380,9 +381,9 @@ __global__ void __launch_bounds__(64 * NQ) k_router_lds(const float * __restrict
     };
     RgAcc<4, 4> tot, l4, l5;
 #pragma unroll 1
-    for (int g = 0; g < CPW / 16; ++g) {
+    for (int g = 0; g < CPW / GN; ++g) {
         RgAcc<4, 4> v = tile16();
-        if (LW == 4) { tot = v; break; }
+        if (LW <= 4) { tot = v; break; }
         if (!(g & 1)) { l4 = v; continue; }
         rg_add(v, l4, v);
         if (LW == 5) { tot = v; break; }
@@ -431,13 +432,10 @@ __global__ void __launch_bounds__(256) k_router_join(const double * __restrict__
     logits[i] = (float) v[0];
 }
 
-// the K split for n tokens: enough parts that tiles x parts reach the 256 CUs (1 below RL_SPLIT_MIN and from 1024)
+// the K split for n tokens: 16 parts from RL_SPLIT_MIN to RL_SPLIT_MAX tokens, else none
 static int router_split(int n, int n_exp, int K) {
-    if (K != 7168 || n < RL_SPLIT_MIN || n >= 1024) { return 1; }
-    const int tiles = ((n_exp + 31) / 32) * ((n + 31) / 32);
-    int ks = 2;
-    while (ks < 16 && tiles * ks < 256) { ks *= 2; }
-    return ks;
+    (void) n_exp;
+    return K == 7168 && n >= RL_SPLIT_MIN && n <= RL_SPLIT_MAX ? 16 : 1;
 }
 size_t router_split_doubles(int n, int n_exp, int K) {
     const int ks = router_split(n, n_exp, K);
@@ -447,23 +445,17 @@ size_t router_split_doubles(int n, int n_exp, int K) {
 hipError_t launch_router_logits(const float * W, const float * x, int n, int n_exp, int K, float * logits, double * part2, hipStream_t st) {
     if (n <= 0) { return hipSuccess; }
     if (K % 1024 != 0) { return hipErrorInvalidValue; }
-    // measured on MI355X (route call wall time): k_router_wg costs ~0.6 us per token (every workgroup reads all of x);
-    // the K-split tiles a flat ~40 us to 64 tokens, 46 us at 128, 57 us at 255 (16 chunks per wave), 102 us from 300
-    // to 512 (32); the crossover is near 64-96 tokens
-    if (K == 7168 && n >= 1024) {   // 32 x 32 tiles (4 x 4 per lane), staged in LDS
-        k_router_lds<4, 1><<<dim3((n_exp + 31) / 32, (n + 31) / 32), 256, 0, st>>>(W, x, n, n_exp, logits, nullptr);
+    // measured on MI355X (route call wall time): k_router_wg costs ~0.6 us per token (every workgroup reads all of x),
+    // 25 us at 32 tokens, 33 at 48; the split tiles 28 us to 64 tokens, 35 at 96, 53 at 255, 72 at 300, 103 at 512,
+    // 180 at 1024, 343 at 2048 (the whole tiles 375)
+    if (router_split(n, n_exp, K) > 1 && part2) {   // 32 x 32 tiles, the chunks split over 16 workgroups, then the join
+        const int total = n * n_exp;
+        k_router_lds<2, 16><<<dim3((n_exp + 31) / 32, (n + 31) / 32, 16), 128, 0, st>>>(W, x, n, n_exp, nullptr, part2);
+        k_router_join<16><<<dim3((total + 255) / 256), 256, 0, st>>>(part2, total, logits);
         return hipGetLastError();
     }
-    if (const int ks = router_split(n, n_exp, K); ks > 1 && part2) {   // the same tiles, K split, then the join
-        const dim3 g((n_exp + 31) / 32, (n + 31) / 32, ks);
-        const int total = n * n_exp;
-        const dim3 gj((total + 255) / 256);
-        switch (ks) {
-        case 2: k_router_lds<4, 2><<<g, 256, 0, st>>>(W, x, n, n_exp, nullptr, part2); k_router_join<2><<<gj, 256, 0, st>>>(part2, total, logits); break;
-        case 4: k_router_lds<4, 4><<<g, 256, 0, st>>>(W, x, n, n_exp, nullptr, part2); k_router_join<4><<<gj, 256, 0, st>>>(part2, total, logits); break;
-        case 8: k_router_lds<2, 8><<<g, 128, 0, st>>>(W, x, n, n_exp, nullptr, part2); k_router_join<8><<<gj, 256, 0, st>>>(part2, total, logits); break;
-        default: k_router_lds<1, 16><<<g, 64, 0, st>>>(W, x, n, n_exp, nullptr, part2); k_router_join<16><<<gj, 256, 0, st>>>(part2, total, logits); break;
-        }
+    if (K == 7168 && n >= 1024) {   // 32 x 32 tiles (4 x 4 per lane), staged in LDS
+        k_router_lds<4, 1><<<dim3((n_exp + 31) / 32, (n + 31) / 32), 256, 0, st>>>(W, x, n, n_exp, logits, nullptr);
         return hipGetLastError();
     }
     if (K == 7168 && n >= RW_MAXN) {   // 32 x 16 tiles (4 x 2 per lane)

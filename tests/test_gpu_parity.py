@@ -67,11 +67,10 @@ def test_pack_layout(ctx):
 
 
 # n covers every logit kernel: the logits and the selection in one launch (n <= 8; 5 gives one wave two tokens), one
-# workgroup per expert (k_router_wg, n < 80), LDS-staged 32 x 32 tiles with the chunks split over 16, 8, 4 or 2
-# workgroups and joined (80..1023: n = 96 splits 16 ways, 200 8 ways, 256 and 300 4 ways, 1023 2 ways) and whole
-# (>= 1024), with ragged last tiles
-@pytest.mark.parametrize("n,rule", [(1, (8, 4)), (5, (8, 4)), (8, (8, 4)), (21, (8, 4)), (64, (8, 4)), (77, (8, 4)), (96, (8, 4)),
-                                    (200, (8, 4)), (256, (8, 4)), (300, (8, 4)), (1023, (8, 4)), (1037, (8, 4)), (8, (1, 1))])
+# workgroup per expert (k_router_wg, n < 40), LDS-staged 32 x 32 tiles with the chunks split over 16 workgroups and
+# joined (40..2048) and whole (above 2048: the ragged-expert test), with ragged last tiles
+@pytest.mark.parametrize("n,rule", [(1, (8, 4)), (5, (8, 4)), (8, (8, 4)), (21, (8, 4)), (39, (8, 4)), (40, (8, 4)), (77, (8, 4)),
+                                    (200, (8, 4)), (300, (8, 4)), (1037, (8, 4)), (8, (1, 1))])
 def test_router_bitwise(ctx, layer, n, rule):
     x = make_x(ctx, n, seed=10 + n)
     ctx.set_routing(rule[0], rule[1], 8, 2.5)
@@ -89,8 +88,8 @@ def test_router_bitwise(ctx, layer, n, rule):
 
 
 # a layer whose expert count is not a multiple of the 32-expert tiles (48 = 8 groups of 6): the last expert tile is
-# ragged in every logit kernel, the K-split tiles (96: 16 parts, 300: 4 parts) and whole tiles (1030) included
-@pytest.mark.parametrize("n", [9, 96, 300, 1030])
+# ragged in every logit kernel, the K-split tiles (96, 1030) and the whole tiles (2050) included
+@pytest.mark.parametrize("n", [9, 96, 1030, 2050])
 def test_router_bitwise_ragged_experts(ctx, n):
     import torch
     g = torch.Generator(device="cpu").manual_seed(500 + n)
