@@ -206,6 +206,25 @@ def _prefill_state(ctx, layer, x, mfma):
     return out
 
 
+def test_combine_unaligned_output(ctx):
+    """The k-ordered combine's 4-wide kernel needs 16-byte aligned rows; an output 4 bytes off takes the one-column
+    kernel, with the same arithmetic: y bit-identical to the aligned call (prefill-40, plain and normed with the
+    residual; the inputs stay aligned, as the other kernels read them 16 bytes at a time)."""
+    import torch
+    n = 40
+    layer = make_layer(ctx, seed=950, bias_sigma=0.05)
+    x = make_x(ctx, n, seed=951)
+    off = lambda: torch.empty(n * E + 1, dtype=torch.float32, device="cuda")[1:].view(n, E)
+    ref = ctx.moe_layer(layer, x).cpu().numpy()
+    y = off()
+    got = ctx.moe_layer(layer, x, y).cpu().numpy()
+    assert y.data_ptr() % 16 == 4
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    refn = ctx.moe_layer_normed(layer, x, residual=True).cpu().numpy()
+    gotn = ctx.moe_layer_normed(layer, x, y=off(), residual=True).cpu().numpy()
+    assert np.array_equal(gotn.view(np.uint32), refn.view(np.uint32))
+
+
 @pytest.mark.parametrize("n,hot", [(9, False), (40, False), (512, False), (2048, True)])
 def test_prefill_mfma_matches_per_pass(ctx, n, hot):
     """The grouped GEMMs on the matrix cores reproduce the per-pass mat-vec kernels bit for bit: gate/up outputs, h and
