@@ -65,6 +65,7 @@ struct FLCtx {
     DBuf<float> ksg, ksu;                      // K-quant shared gate / up outputs
     DBuf<unsigned> rcnt;                       // the one-launch routing's self-resetting counter (launch_router_fused)
     DBuf<double> rpart;                        // the K-split router tiles' parts [KS][n][n_exp]
+    DBuf<int> dscr;                            // the multi-workgroup dispatch's per-round counts and bases
 };
 // fl_route_dev with, for the one-launch routing of a few rows (router_fused_ok), a host word set to the context's epoch
 // (as it is after the call) once the picks are written; done may be null, other sizes leave it alone

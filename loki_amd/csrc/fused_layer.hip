@@ -110,7 +110,7 @@ extern "C" void fl_free(FLCtx * c) {
     compat_free(c); c->zero_i.release(); c->terms.release(); c->cnt.release();
     c->tab.release(); c->derr.release(); c->dlogit.release(); c->dth.release(); c->dto.release();
     c->ptab.release(); c->pcols.release(); c->pncols.release(); c->xh.release(); c->hh.release();
-    c->ksg.release(); c->ksu.release(); c->rcnt.release(); c->rpart.release();
+    c->ksg.release(); c->ksu.release(); c->rcnt.release(); c->rpart.release(); c->dscr.release();
     for (auto & v : c->ev_free) { for (auto e : v) { (void) hipEventDestroy(e); } }
     for (auto & v : c->ev_pending) { for (auto e : v) { (void) hipEventDestroy(e); } }
     (void) hipEventDestroy(c->em0); (void) hipEventDestroy(c->em1); (void) hipStreamDestroy(c->own);
@@ -221,7 +221,9 @@ extern "C" int fl_dispatch_dev(FLCtx * c, const int * sel, int n, int topk, int 
     if (n < 0 || topk <= 0 || topk > MAXK || (int64_t) n * topk > (1 << 24)) { return fail(c, FL_ERANGE, "n*topk out of range"); }
     if (n_exp <= 0 || n_exp > NEXP_MAX) { return fail(c, FL_EINVAL, "n_exp %d outside 1..%d", n_exp, NEXP_MAX); }
     if (!sel || !counts || !offsets || !perm || !inv || !act || !nact) { return fail(c, FL_EINVAL, "null pointer"); }
-    TRY(c, launch_dispatch(sel, n * topk, n_exp, counts, offsets, perm, inv, act, nact, c->st));
+    int * dsc = nullptr;
+    if (const size_t nd = dispatch_scratch_ints(n * topk)) { ALLOC(c, c->dscr, nd); dsc = c->dscr.p; }
+    TRY(c, launch_dispatch(sel, n * topk, n_exp, counts, offsets, perm, inv, act, nact, c->st, dsc));
     return FL_OK;
 }
 
@@ -558,7 +560,9 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     prof_mark(c, ev, 2);
     TRY(c, launch_router_select(c->logits.p, L->probs_b, n, ne, c->n_group, c->topk_group, tsel, c->scale, c->probs.p, c->sel.p, c->wts.p, st, tk, renorm));
     prof_mark(c, ev, 3);
-    TRY(c, launch_dispatch(c->sel.p, P, ne, c->counts.p, c->offsets.p, c->perm.p, c->inv.p, c->act.p, c->nact.p, st));
+    int * dsc = nullptr;
+    if (const size_t nd = dispatch_scratch_ints(P)) { ALLOC(c, c->dscr, nd); dsc = c->dscr.p; }
+    TRY(c, launch_dispatch(c->sel.p, P, ne, c->counts.p, c->offsets.p, c->perm.p, c->inv.p, c->act.p, c->nact.p, st, dsc));
     if (mfma) {
         TRY(c, launch_prefill_cols(c->act.p, c->nact.p, c->offsets.p, n, P, c->pcols.p, c->pncols.p, st));
         prof_mark(c, ev, 4);

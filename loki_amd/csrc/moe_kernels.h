@@ -34,8 +34,10 @@ hipError_t launch_router_fused(const float * W, const float * x, int n, int n_ex
 
 // stable counting sort of the P = n*topk pairs by expert: counts [n_exp], offsets [n_exp+1], perm/inv [P],
 // act = used experts ascending, nact = their number (device scalar)
+// scratch (may be null: one workgroup for every size): dispatch_scratch_ints(P) ints, used above 4096 pairs
+size_t dispatch_scratch_ints(int P);
 hipError_t launch_dispatch(const int * sel, int P, int n_exp, int * counts, int * offsets, int * perm, int * inv,
-                           int * act, int * nact, hipStream_t st);
+                           int * act, int * nact, hipStream_t st, int * scratch = nullptr);
 
 struct ExpertArgs {
     const uint4 * tab;               // LDS table image (build_table_image)

@@ -105,7 +105,9 @@ def test_router_bitwise_ragged_experts(ctx, n):
     assert np.array_equal(w.cpu().numpy().view(np.uint32), wo.view(np.uint32))
 
 
-@pytest.mark.parametrize("n,skew", [(1, 0), (8, 0), (512, 0), (2048, 1), (2048, 2)])
+# n * 8 pairs: one workgroup (rounds of 1024 in turn) up to 4096 pairs, the rounds as workgroups of their own above
+# (129, 513: a ragged last round)
+@pytest.mark.parametrize("n,skew", [(1, 0), (8, 0), (129, 0), (512, 0), (513, 1), (2048, 1), (2048, 2)])
 def test_dispatch_bitwise(ctx, n, skew):
     import torch
     rng = np.random.default_rng(n + 17 * skew)
