@@ -39,6 +39,22 @@ WORKLOADS = {
 STACK_LAYERS = 58   # configs[3]: DeepSeek-R1's MoE layers, every expert of every layer resident (~169 GB)
 
 
+class no_gc:
+    """The host-timed loops of the drop-in flows run with Python's garbage collector off (collected once before): a
+    collection pass in a process holding many objects stalls the timing thread for tens of ms, which is the
+    harness's, not the library's."""
+    def __enter__(self):
+        import gc
+        gc.collect(); self.was = gc.isenabled(); gc.disable()
+        return self
+
+    def __exit__(self, *exc):
+        import gc
+        if self.was:
+            gc.enable()
+        return False
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -291,8 +307,9 @@ def run_dropin(ctx, torch, steps=60, warmup=5, ggml_steps=3, seed=20260601):
         split = []
         for i in range(warmup):
             token(i, w, L.gate, L.up, L.down, [])
-        for i in range(steps):
-            token(warmup + i, w, L.gate, L.up, L.down, split)
+        with no_gc():
+            for i in range(steps):
+                token(warmup + i, w, L.gate, L.up, L.down, split)
         sp = np.array(split) * 1e6
         res["us_per_token"] = round(float(np.median(sp.sum(axis=1))), 1)
         res["ffn_begin_us"], res["fetch_us"], res["moe_us"] = (round(float(v), 1) for v in np.median(sp, axis=0))
@@ -339,18 +356,19 @@ def run_dropin_rows(ctx, torch, n=8, steps=30, warmup=5, seed=20260621):
     res = {}
     try:
         split = []
-        for i in range(steps + warmup):
-            t0 = time.perf_counter()
-            ctx.check(lib().fl_ffn_begin(ctx.ctx, ctypes.byref(w), n, ptr(xs[i]), ptr(fis[i]), -1))
-            t1 = time.perf_counter()
-            lib().fl_fetch(ctx.ctx, n, 1, ctypes.byref(out))
-            t2 = time.perf_counter()
-            sel = np.ctypeslib.as_array(out.sel, shape=(n * 8,)).astype(np.int32)
-            wts = np.ctypeslib.as_array(out.wts, shape=(n * 8,)).copy()
-            lib().fl_moe(ctx.ctx, L.gate.data_ptr(), L.up.data_ptr(), L.down.data_ptr(), 256, 4, ptr(sel), ptr(wts), 8, n, ctypes.byref(out))
-            t3 = time.perf_counter()
-            if i >= warmup:
-                split.append((t1 - t0, t2 - t1, t3 - t2))
+        with no_gc():
+            for i in range(steps + warmup):
+                t0 = time.perf_counter()
+                ctx.check(lib().fl_ffn_begin(ctx.ctx, ctypes.byref(w), n, ptr(xs[i]), ptr(fis[i]), -1))
+                t1 = time.perf_counter()
+                lib().fl_fetch(ctx.ctx, n, 1, ctypes.byref(out))
+                t2 = time.perf_counter()
+                sel = np.ctypeslib.as_array(out.sel, shape=(n * 8,)).astype(np.int32)
+                wts = np.ctypeslib.as_array(out.wts, shape=(n * 8,)).copy()
+                lib().fl_moe(ctx.ctx, L.gate.data_ptr(), L.up.data_ptr(), L.down.data_ptr(), 256, 4, ptr(sel), ptr(wts), 8, n, ctypes.byref(out))
+                t3 = time.perf_counter()
+                if i >= warmup:
+                    split.append((t1 - t0, t2 - t1, t3 - t2))
         sp = np.array(split) * 1e6
         step_us = float(np.median(sp.sum(axis=1)))
         res = {"us_per_step": round(step_us, 1), "us_per_token": round(step_us / n, 2), "ffn_begin_us": round(float(np.median(sp[:, 0])), 1),
@@ -424,7 +442,8 @@ def run_dropin_wide(ctx, torch, n=512, steps=10, warmup=2, seed=20260611):
 
         for _ in range(warmup):
             step()
-        ts = [step() for _ in range(steps)]
+        with no_gc():
+            ts = [step() for _ in range(steps)]
         torch.cuda.synchronize()
         ctx.sync()
         ms = float(np.median(ts)) * 1e3
