@@ -40,9 +40,10 @@ STACK_LAYERS = 58   # configs[3]: DeepSeek-R1's MoE layers, every expert of ever
 
 
 class no_gc:
-    """The host-timed loops of the drop-in flows run with Python's garbage collector off (collected once before): a
-    collection pass in a process holding many objects stalls the timing thread for tens of ms, which is the
-    harness's, not the library's."""
+    """The drop-in flows' warm-up and host-timed loops run with Python's garbage collector off, collected once before
+    the warm-up: a collection pass in a process holding many objects stalled one library call per full run by tens of
+    ms of host time, which is the harness's, not the library's. (The device-timed loops keep the collector: a
+    collection right before them idles the GPU and lowers its clocks for the first timed steps.)"""
     def __enter__(self):
         import gc
         gc.collect(); self.was = gc.isenabled(); gc.disable()
@@ -305,9 +306,9 @@ def run_dropin(ctx, torch, steps=60, warmup=5, ggml_steps=3, seed=20260601):
     try:
         w = flw((L.sh_gate, L.sh_up, L.sh_down))
         split = []
-        for i in range(warmup):
-            token(i, w, L.gate, L.up, L.down, [])
-        with no_gc():
+        with no_gc():   # collected before the warm-up tokens
+            for i in range(warmup):
+                token(i, w, L.gate, L.up, L.down, [])
             for i in range(steps):
                 token(warmup + i, w, L.gate, L.up, L.down, split)
         sp = np.array(split) * 1e6
@@ -440,9 +441,9 @@ def run_dropin_wide(ctx, torch, n=512, steps=10, warmup=2, seed=20260611):
             lib().fl_wide_finish(ctx.ctx, n, KE, ctypes.byref(out))
             return t_lib + time.perf_counter() - t0
 
-        for _ in range(warmup):
-            step()
-        with no_gc():
+        with no_gc():   # collected before the warm-up steps
+            for _ in range(warmup):
+                step()
             ts = [step() for _ in range(steps)]
         torch.cuda.synchronize()
         ctx.sync()
