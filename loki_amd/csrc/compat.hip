@@ -135,12 +135,18 @@ __global__ void k_base_rows(const float * __restrict__ fi, const float * __restr
     if (i < tot) { base[i] = fi[i] + sh[i]; }
 }
 
-__global__ void k_wide_scatter(const float * __restrict__ o, const int * __restrict__ prow, const int * __restrict__ pk, const float * __restrict__ pw,
-                               int npairs, int KE, float * __restrict__ out_all) {
-    const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
-    if (i >= (int64_t) npairs * E_) { return; }
-    const int p = (int) (i / E_), e = (int) (i % E_);
-    out_all[((size_t) prow[p] * KE + pk[p]) * E_ + e] = pw[p] * o[(size_t) p * E_ + e];
+// block (x, p): pair p's columns 1024 x .. + 1023, four per thread (rows of E_ floats in hipMalloc'd buffers: 16-byte
+// aligned); the pair's row, slot and weight are uniform per block
+__global__ void __launch_bounds__(256) k_wide_scatter(const float * __restrict__ o, const int * __restrict__ prow, const int * __restrict__ pk,
+                                                      const float * __restrict__ pw, int npairs, int KE, float * __restrict__ out_all) {
+    static_assert(E_ % 4 == 0, "4-wide rows");
+    const int e = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (e >= E_) { return; }
+    for (int p = blockIdx.y; p < npairs; p += gridDim.y) {   // the grid's y extent is capped at 65535
+        const float w = pw[p];
+        const float4 v = *reinterpret_cast<const float4 *>(o + (size_t) p * E_ + e);
+        *reinterpret_cast<float4 *>(out_all + ((size_t) prow[p] * KE + pk[p]) * E_ + e) = make_float4(w * v.x, w * v.y, w * v.z, w * v.w);
+    }
 }
 
 __global__ void k_wide_finish(const float * __restrict__ base, const float * __restrict__ out_all, int KE, int64_t tot,
@@ -774,7 +780,7 @@ extern "C" void fl_wide_moe(FLCtx * c, const void * gate, const void * up, const
     const Arena ar = pack_arena(c, s, gate, up, down, nexp, down_fmt);
     routed_experts(c, s, ar, s->xq_all.p, s->xd_all.p, s->wmax, P, KE, nexp, s->w_act.p, s->w_nact.p, s->w_off.p, s->w_perm.p, s->o.p,
                    down_fmt, down, max_slots);
-    k_wide_scatter<<<nblk((int64_t) P * E_), 256, 0, st>>>(s->o.p, s->w_row.p, s->w_k.p, s->w_wk.p, P, KE, s->out_all.p);
+    k_wide_scatter<<<dim3((E_ / 4 + 255) / 256, std::min(P, 65535)), 256, 0, st>>>(s->o.p, s->w_row.p, s->w_k.p, s->w_wk.p, P, KE, s->out_all.p);
     CK(hipGetLastError());
     // no wait: the reference's call only enqueues too (src/fused_layer.cu:528-555); fl_wide_mark / fl_wide_wait order
     // the engine's reuse of its staging and of these tables

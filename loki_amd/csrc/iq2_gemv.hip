@@ -254,28 +254,30 @@ __global__ void __launch_bounds__(256) k_combine(const float * __restrict__ o, c
                                                  int n, int topk, int E, int P, const float * __restrict__ resid,
                                                  float * __restrict__ y, float * __restrict__ moe) {
 #pragma clang fp contract(off)
-    const int t = blockIdx.y, r = (blockIdx.x * 256 + threadIdx.x) * 4;
-    if (t >= n || r >= E) { return; }
-    const int * iv = inv + (size_t) t * topk; const float * w = wts + (size_t) t * topk;
-    auto ld4 = [&](int slot) { return *reinterpret_cast<const float4 *>(o + (size_t) slot * E + r); };
-    float4 m;
-    {
-        const float4 a = ld4(iv[0]); const float w0 = w[0];
-        m = make_float4(a.x * w0, a.y * w0, a.z * w0, a.w * w0);
+    const int r = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (r >= E) { return; }
+    for (int t = blockIdx.y; t < n; t += gridDim.y) {   // the grid's y extent is capped at 65535
+        const int * iv = inv + (size_t) t * topk; const float * w = wts + (size_t) t * topk;
+        auto ld4 = [&](int slot) { return *reinterpret_cast<const float4 *>(o + (size_t) slot * E + r); };
+        float4 m;
+        {
+            const float4 a = ld4(iv[0]); const float w0 = w[0];
+            m = make_float4(a.x * w0, a.y * w0, a.z * w0, a.w * w0);
+        }
+        for (int k = 1; k < topk; ++k) {
+            const float4 a = ld4(iv[k]); const float wk = w[k];
+            m = make_float4(m.x + a.x * wk, m.y + a.y * wk, m.z + a.z * wk, m.w + a.w * wk);
+        }
+        const size_t i = (size_t) t * E + r;
+        if (moe) { *reinterpret_cast<float4 *>(moe + i) = m; }
+        const float4 sh = ld4(P + t);
+        float4 v = make_float4(m.x + sh.x, m.y + sh.y, m.z + sh.z, m.w + sh.w);
+        if (resid) {
+            const float4 h = *reinterpret_cast<const float4 *>(resid + i);
+            v = make_float4(v.x + h.x, v.y + h.y, v.z + h.z, v.w + h.w);
+        }
+        *reinterpret_cast<float4 *>(y + i) = v;
     }
-    for (int k = 1; k < topk; ++k) {
-        const float4 a = ld4(iv[k]); const float wk = w[k];
-        m = make_float4(m.x + a.x * wk, m.y + a.y * wk, m.z + a.z * wk, m.w + a.w * wk);
-    }
-    const size_t i = (size_t) t * E + r;
-    if (moe) { *reinterpret_cast<float4 *>(moe + i) = m; }
-    const float4 sh = ld4(P + t);
-    float4 v = make_float4(m.x + sh.x, m.y + sh.y, m.z + sh.z, m.w + sh.w);
-    if (resid) {
-        const float4 h = *reinterpret_cast<const float4 *>(resid + i);
-        v = make_float4(v.x + h.x, v.y + h.y, v.z + h.z, v.w + h.w);
-    }
-    *reinterpret_cast<float4 *>(y + i) = v;
 }
 
 // the same, one output per thread: for rows or pointers that are not 16-byte aligned
@@ -283,16 +285,18 @@ __global__ void __launch_bounds__(256) k_combine1(const float * __restrict__ o, 
                                                   int n, int topk, int E, int P, const float * __restrict__ resid,
                                                   float * __restrict__ y, float * __restrict__ moe) {
 #pragma clang fp contract(off)
-    const int t = blockIdx.y, r = blockIdx.x * 256 + threadIdx.x;
-    if (t >= n || r >= E) { return; }
-    const int * iv = inv + (size_t) t * topk; const float * w = wts + (size_t) t * topk;
-    float m = o[(size_t) iv[0] * E + r] * w[0];
-    for (int k = 1; k < topk; ++k) { m = m + o[(size_t) iv[k] * E + r] * w[k]; }
-    const size_t i = (size_t) t * E + r;
-    if (moe) { moe[i] = m; }
-    float v = m + o[(size_t) (P + t) * E + r];
-    if (resid) { v = v + resid[i]; }
-    y[i] = v;
+    const int r = blockIdx.x * 256 + threadIdx.x;
+    if (r >= E) { return; }
+    for (int t = blockIdx.y; t < n; t += gridDim.y) {   // the grid's y extent is capped at 65535
+        const int * iv = inv + (size_t) t * topk; const float * w = wts + (size_t) t * topk;
+        float m = o[(size_t) iv[0] * E + r] * w[0];
+        for (int k = 1; k < topk; ++k) { m = m + o[(size_t) iv[k] * E + r] * w[k]; }
+        const size_t i = (size_t) t * E + r;
+        if (moe) { moe[i] = m; }
+        float v = m + o[(size_t) (P + t) * E + r];
+        if (resid) { v = v + resid[i]; }
+        y[i] = v;
+    }
 }
 
 hipError_t launch_combine(const float * o, const int * inv, const float * wts, int n, int topk, int E, int P,
@@ -300,9 +304,9 @@ hipError_t launch_combine(const float * o, const int * inv, const float * wts, i
     if ((int64_t) n * E <= 0) { return hipSuccess; }
     if (E % 4 == 0 && ((reinterpret_cast<uintptr_t>(o) | reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(moe) |
                         reinterpret_cast<uintptr_t>(resid)) & 15u) == 0) {
-        k_combine<<<dim3((unsigned) ((E / 4 + 255) / 256), (unsigned) n), 256, 0, st>>>(o, inv, wts, n, topk, E, P, resid, y, moe);
+        k_combine<<<dim3((unsigned) ((E / 4 + 255) / 256), (unsigned) std::min(n, 65535)), 256, 0, st>>>(o, inv, wts, n, topk, E, P, resid, y, moe);
     } else {
-        k_combine1<<<dim3((unsigned) ((E + 255) / 256), (unsigned) n), 256, 0, st>>>(o, inv, wts, n, topk, E, P, resid, y, moe);
+        k_combine1<<<dim3((unsigned) ((E + 255) / 256), (unsigned) std::min(n, 65535)), 256, 0, st>>>(o, inv, wts, n, topk, E, P, resid, y, moe);
     }
     return hipGetLastError();
 }
