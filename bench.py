@@ -563,13 +563,36 @@ def cpu_stack_sample(ctx, layers, x0, nlayers=2):
     return out
 
 
-def load_traffic(kernel, workload):
-    """HBM bytes per launch from committed rocprofv3 --pmc summaries (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)."""
-    p = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_%s_%s.json" % (kernel.split("<")[0], workload))
-    if os.path.exists(p):
-        with open(p) as f:
-            return json.load(f).get("bytes_per_launch")
-    return None
+_LIB_SHA = None
+
+
+def lib_sha16():
+    """SHA-256 prefix of the library this process loads: profiles/ summaries carry the one their run loaded."""
+    global _LIB_SHA
+    if _LIB_SHA is None:
+        import hashlib
+        from loki_amd import LIB_PATH
+        with open(LIB_PATH, "rb") as f:
+            _LIB_SHA = hashlib.sha256(f.read()).hexdigest()[:16]
+    return _LIB_SHA
+
+
+# roofline kernel -> the key of its profiles/ summaries
+PROFILE_KEY = {"k_moe_decode1": "k_moe_decode1", "k_moe_decode": "k_moe_decode", "k_pf_gemm<gate_up>": "k_pf_gemm_gate_up",
+               "k_experts<gate_up>": "k_experts_gate_up"}
+
+
+def load_profile(kind, kernel, workload):
+    """A committed profiles/<kind>_<key>_<workload>.json, if it was made with this very library (else None, and why)."""
+    p = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                     "%s_%s_%s.json" % (kind, PROFILE_KEY.get(kernel, kernel), workload))
+    if not os.path.exists(p):
+        return None, "no %s" % os.path.basename(p)
+    with open(p) as f:
+        js = json.load(f)
+    if js.get("lib_sha16") != lib_sha16():
+        return None, "%s was made with library %s, this run loads %s" % (os.path.basename(p), js.get("lib_sha16"), lib_sha16())
+    return js, os.path.join("profiles", os.path.basename(p))
 
 
 def kernel_roofline(res):
@@ -585,9 +608,17 @@ def kernel_roofline(res):
         k_ms, k_bytes = res["stage_ms"]["gate_up"], res["gu_bytes"]
         stages = res["stage_ms"]
     k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
+    tr, tr_src = load_profile("traffic", kname, res["name"])
+    kt, kt_src = load_profile("trace", kname, res["name"])
     roof = {"kernel": kname, "bound": "hbm", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic(kname, res["name"]),
-            "algorithmic_bytes_per_launch": int(k_bytes), "avg_launch_us": round(k_ms * 1e3, 2)}
+            "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": tr["bytes_per_launch"] if tr else None,
+            "algorithmic_bytes_per_launch": int(k_bytes), "avg_launch_us": round(k_ms * 1e3, 2),
+            "lib_sha16": lib_sha16(), "traffic_source": tr_src,
+            # the same kernel's average duration over the timed steps of a committed rocprofv3 kernel trace made with
+            # this library (profiles/trace_*.json): the frac it implies, to set beside the live one
+            "profile_avg_us": kt["avg_us_last"] if kt else None,
+            "profile_frac": round(k_bytes / (kt["avg_us_last"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if kt else None,
+            "profile_source": kt_src}
     return roof, stages
 
 
@@ -604,11 +635,11 @@ def bench(args, ctx, torch):
     if args.fused is not None:
         ctx.set_fused(args.fused)
     if args.only_kquant:
-        print(json.dumps({"kquant": run_kquant(ctx, torch), "real_formats": run_realfmt(ctx, torch)}), flush=True)
+        print(json.dumps({"kquant": run_kquant(ctx, torch), "real_formats": run_realfmt(ctx, torch), "lib_sha16": lib_sha16()}), flush=True)
         return
     if args.only_dropin:
         print(json.dumps({"dropin_decode1": run_dropin(ctx, torch), "dropin_decode8": run_dropin_rows(ctx, torch),
-                          "dropin_prefill512": run_dropin_wide(ctx, torch)}), flush=True)
+                          "dropin_prefill512": run_dropin_wide(ctx, torch), "lib_sha16": lib_sha16()}), flush=True)
         return
     thr = cpu_threads()
     cpu_per = {}
@@ -688,6 +719,7 @@ def bench(args, ctx, torch):
         "host_us_per_call": head["host_us_per_call"],
         "roofline": head["roofline"],
         "stage_us": head["stage_us"],
+        "lib_sha16": lib_sha16(),
         "cpu_baseline": cpu,
         "extra": extra,
     }
@@ -700,7 +732,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="decode1", choices=sorted(WORKLOADS))
-    ap.add_argument("--copies", type=int, default=3, help="independently seeded layers rotated over the steps")
+    ap.add_argument("--copies", type=int, default=8,
+                    help="independently seeded layers rotated over the steps (8 x 2.9 GB: a layer's router and shared "
+                         "expert recur after 7 other layers' ~770 MB, well past the 256 MB MALL)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the other decode / prefill workloads and the K-quant legs")
     ap.add_argument("--no-stack", action="store_true", help="skip the 58-layer resident stack (configs[3], ~169 GB)")

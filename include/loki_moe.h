@@ -69,9 +69,15 @@ void fl_fetch(FLCtx *, int n, int what, FLOut * out);
  * with ids = slot indices into the arena; -> out->h = routed + shared + ffn_inp, out->moe = routed. Waited. */
 void fl_moe(FLCtx *, const void * gate, const void * up, const void * down, int nexp, int down_fmt, const int * ids, const float * w, int KE, int n, FLOut * out);
 void fl_skip(FLCtx *, const float * mo, int n, FLOut * out);                /* fl.h:47 -- h = mo + shared + ffn_inp, waited */
-void fl_h2d(FLCtx *, void * dst, const void * src, size_t bytes);           /* fl.h:49 */
+/* fl.h:49 -- host -> device on the context's stream, enqueued: a kernel reading the mapped memory when src is pinned
+ * (hipHostMalloc'd; no copy engine, as src/fused_layer.cu:414-420), the copy engine when HIP cannot map src */
+void fl_h2d(FLCtx *, void * dst, const void * src, size_t bytes);
 void fl_wait_event(FLCtx *, hipEvent_t ev);                                 /* fl.h:51 */
 double fl_gpu_ms(FLCtx *, int which);                                       /* fl.h:52 -- 1 = experts (ms, accumulated) */
+
+/* additive: fl_h2d's bytes so far by kernel (mapped pinned) and by copy engine (the reference keeps the same two
+ * counts and prints them once past 64 MB, src/fused_layer.cu:418-419) */
+int fl_h2d_bytes(FLCtx *, size_t * by_kernel, size_t * by_copy_engine);
 
 /* ---------------------------------------------------------------- additive: the MoE tail of fl_attn without attention
  * Router + shared expert on N rows (N <= 64 per call; wrow >= 0 places them at rows wrow.. of a wide pass), given the
@@ -94,6 +100,12 @@ int fl_set_routing(FLCtx *, int n_group, int topk_group, int topk, float scale);
  * The block then runs keep slots per row; FLDebug's sel / wts hold [n][keep]. keep = 0 (default) keeps all topk.
  * fl_route_dev and fl_ffn_begin are unaffected (the engine's host dispatch applies its own keep). */
 int fl_set_keep(FLCtx *, int keep, float renorm);
+/* the engine's --share-experts rule for that keep (src/server_core_fused.cpp:798-806, flag at :376; loki/chat.py:35
+ * runs the engine with --experts 3 --share-experts): with on != 0, keep < topk and n > 1 rows, every row keeps its own
+ * min(2, keep) heaviest experts, then prefers its other picks (weight order) whose expert is among the rows' own, then
+ * the rest in weight order, each such expert joining that set for the rows after it (rows in order). The kept list is
+ * in that pick order, renormalised in that order. Default off. */
+int fl_set_share_experts(FLCtx *, int on);
 
 /* ---------------------------------------------------------------- additive: device-resident block (the measured path) */
 typedef struct FLMoeLayer {
@@ -123,14 +135,17 @@ int fl_moe_layer_normed(FLCtx *, const FLMoeLayer * L, const float * ffn_norm, f
                         int residual, float * y);
 /* fl_moe_layer for one decode batch (1 <= n <= 8) that allocates no device memory. No counterpart in the reference: it
  * is for callers that cannot allocate -- code under HIP graph capture, serving loops that forbid hipMalloc. Same
- * arguments and result as fl_moe_layer (bit-identical y), under the context's routing rule and fl_set_keep. It runs the
- * single-launch decode block (tiled IQ2_XXS, E 7168, H 2048, a routing rule the decode block takes: FL_ESCOPE
- * otherwise) on a file-scope device array of 5,502,720 bytes that each GPU the library runs on holds until the
- * process ends (routing outputs, epoch-tagged hand-off words, the table image, an error word), resolved per device by
- * fl_init; it calls no hipMalloc / hipFree and clears that array with a kernel, never a memset. n above 8 is rejected
- * with FL_ERANGE. Every call on one GPU shares that GPU's array, which keeps the last call's contents: calls that
- * overlap on one GPU (two streams, two contexts, two threads) race and give wrong results. Device-side failures are
- * reported through fl_sync on the context. FLDebug does not see this path's buffers. */
+ * arguments and result as fl_moe_layer (bit-identical y), under the context's routing rule, fl_set_keep and
+ * fl_set_share_experts. It runs the single-launch decode block (tiled IQ2_XXS, E 7168, H 2048, a routing rule the
+ * decode block takes: FL_ESCOPE otherwise) on a file-scope device array of 5,502,720 bytes that each GPU the library
+ * runs on holds until the process ends (routing outputs, epoch-tagged hand-off words, the table image, an error word),
+ * resolved and prepared per device by fl_init; it calls no hipMalloc / hipFree. Each call enqueues a fill kernel that
+ * clears the hand-off words (never a memset) and the decode block, which tags them with one fixed epoch; it changes no
+ * host-side state, so a call captured into a HIP graph is correct on every replay (set the context's stream to the
+ * capture stream first). n above 8 is rejected with FL_ERANGE. Every call on one GPU shares that GPU's array, which
+ * keeps the last call's contents: calls that overlap on one GPU (two streams, two contexts, two threads, two graphs)
+ * race and give wrong results. Device-side failures are reported through fl_sync on the context that made the call.
+ * FLDebug does not see this path's buffers. */
 int fl_moe_layer_noalloc(FLCtx *, const FLMoeLayer * L, const float * x, int n, float * y);
 /* router only: sel/w [n][topk] (device), logits/probs [n][n_exp] may be NULL */
 int fl_route_dev(FLCtx *, const float * gate_inp, const float * probs_b, const float * x, int n, int n_exp, int E,

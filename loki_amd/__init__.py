@@ -124,8 +124,8 @@ class FLOut(ctypes.Structure):
 # every symbol include/loki_moe.h declares (the ABI test checks the library exports all of them)
 ABI_SYMBOLS = [
     "fl_init", "fl_attn", "fl_wide_init", "fl_wide_moe", "fl_wide_mark", "fl_wide_wait", "fl_wide_finish", "fl_moe_outs",
-    "fl_wide_outs", "fl_wide_skip", "fl_spec", "fl_sketch", "fl_fetch", "fl_moe", "fl_skip", "fl_h2d", "fl_wait_event",
-    "fl_gpu_ms", "fl_ffn_begin", "fl_set_experts", "fl_set_routing", "fl_set_keep", "fl_set_shared_formats", "fl_set_layer_formats", "fl_kq_matvec_dev",
+    "fl_wide_outs", "fl_wide_skip", "fl_spec", "fl_sketch", "fl_fetch", "fl_moe", "fl_skip", "fl_h2d", "fl_h2d_bytes", "fl_wait_event",
+    "fl_gpu_ms", "fl_ffn_begin", "fl_set_experts", "fl_set_routing", "fl_set_keep", "fl_set_share_experts", "fl_set_shared_formats", "fl_set_layer_formats", "fl_kq_matvec_dev",
     "fl_gguf_open", "fl_gguf_close", "fl_gguf_n_tensors", "fl_gguf_tensor_name", "fl_gguf_tensor", "fl_gguf_tensor_at",
     "fl_gguf_get_int", "fl_gguf_get_float", "fl_gguf_get_str", "fl_gguf_read", "fl_gguf_load_moe_layer", "fl_gguf_free_layer", "fl_moe_layer", "fl_moe_layer_normed", "fl_moe_layer_noalloc", "fl_route_dev", "fl_dispatch_dev", "fl_quant_q8k_dev",
     "fl_pack_iq2xxs", "fl_unpack_iq2xxs", "fl_register_tiled", "fl_unregister_tiled", "fl_rmsnorm_dev", "fl_synth_iq2xxs", "fl_synth_normal", "fl_probe_exp",
@@ -158,6 +158,7 @@ def lib():
             "fl_set_routing": (I, [P_, I, I, I, F]),
             "fl_set_experts": (I, [P_, I]),
             "fl_set_keep": (I, [P_, I, F]),
+            "fl_set_share_experts": (I, [P_, I]),
             "fl_set_shared_formats": (I, [P_, I, I, I]),
             "fl_set_layer_formats": (I, [P_, I, I, I, I]),
             "fl_kq_matvec_dev": (I, [P_, I, P_, I, I, P_, P_, I, P_]),
@@ -206,6 +207,8 @@ def lib():
             "fl_wide_outs": (None, [P_, I, I, P_]),
             "fl_wide_skip": (None, [P_, P_, I, ctypes.POINTER(FLOut)]),
             "fl_h2d": (None, [P_, P_, P_, S]),
+            "fl_h2d_bytes": (I, [P_, ctypes.POINTER(S), ctypes.POINTER(S)]),
+            "fl_wait_event": (None, [P_, P_]),
             "fl_set_profile": (I, [P_, I]),
             "fl_stage_ms": (I, [P_, ctypes.POINTER(ctypes.c_double), I, I]),
         }
@@ -288,6 +291,10 @@ class Context:
     def set_keep(self, keep=0, renorm=2.5):
         """fl_moe_layer keeps each row's `keep` heaviest experts, rescaled to sum to renorm (0 = all topk, default)."""
         self.check(lib().fl_set_keep(self.ctx, keep, renorm))
+
+    def set_share_experts(self, on=True):
+        """The engine's --share-experts rule for set_keep's keep (rows prefer experts other rows already use)."""
+        self.check(lib().fl_set_share_experts(self.ctx, 1 if on else 0))
 
     def set_experts(self, n_exp=N_EXPERT):
         self.check(lib().fl_set_experts(self.ctx, n_exp))

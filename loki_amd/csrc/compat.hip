@@ -167,6 +167,21 @@ __global__ void k_wide_skip(const float * __restrict__ base, const float * __res
 
 inline unsigned nblk(int64_t tot) { return (unsigned) ((tot + 255) / 256); }
 
+// fl_h2d's copy by kernel: 16-byte words, four loads in flight per thread (each a PCIe read of the mapped host
+// memory), grid-stride; and the byte copy for unaligned ranges
+__global__ void __launch_bounds__(256) k_copy16(const uint4 * __restrict__ src, uint4 * __restrict__ dst, size_t n) {
+    const size_t stride = (size_t) gridDim.x * 256;
+    size_t i = (size_t) blockIdx.x * 256 + threadIdx.x;
+    for (; i + 3 * stride < n; i += 4 * stride) {
+        const uint4 a = src[i], b = src[i + stride], c2 = src[i + 2 * stride], d = src[i + 3 * stride];
+        dst[i] = a; dst[i + stride] = b; dst[i + 2 * stride] = c2; dst[i + 3 * stride] = d;
+    }
+    for (; i < n; i += stride) { dst[i] = src[i]; }
+}
+__global__ void __launch_bounds__(256) k_copy1(const uint8_t * __restrict__ src, uint8_t * __restrict__ dst, size_t n) {
+    for (size_t i = (size_t) blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t) gridDim.x * 256) { dst[i] = src[i]; }
+}
+
 }  // namespace
 
 struct Compat {
@@ -304,7 +319,8 @@ static void shared_expert(FLCtx * c, Compat * s, const int8_t * xq, const float 
     PrefillArgs g{};
     if (gu_gemm || dn_gemm) {
         CK(prefill_ready(c) == FL_OK ? hipSuccess : hipErrorOutOfMemory);
-        FALLOC(s->pcols, (size_t) NEXP_MAX + 2); FALLOC(s->pncols, 1);
+        // ceil(N / 64) shared columns (wide_base runs every row of a wide pass here, so N is not bounded by 64)
+        FALLOC(s->pcols, (size_t) prefill_shared_cols(N) + NEXP_MAX + 2); FALLOC(s->pncols, 1);
         FCK(launch_prefill_cols(zero_int(c), zero_int(c), zero_int(c), N, 0, s->pcols.p, s->pncols.p, c->st));   // no routed columns
         g.ptab = c->ptab.p; g.perm = zero_int(c); g.topk = 1; g.P = 0; g.cols = s->pcols.p; g.ncols = s->pncols.p;
         g.err = c->derr.p; g.herr = c->herr ? c->herr_dev : nullptr;
@@ -479,8 +495,23 @@ static void need_down_fmt(const char * fn, int fmt, const void * down) {
 }
 
 // ================================================================ entry points
+static int ffn_begin_body(FLCtx * c, const FLW * W, int N, const float * ncur, const float * ffn_inp, int wrow);
+// fl_ffn_begin's enqueued work is bracketed by a pair of events, folded into fl_gpu_ms(0 / 2) when that is read
 extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur, const float * ffn_inp, int wrow) {
     if (!c) { return FL_EINVAL; }
+    if (!c->ffn_ev_pending.empty()) { fold_ffn_events(c, c->ffn_ev_pending.size() >= 64); }   // bounded: never more than 64 pairs
+    std::pair<hipEvent_t, hipEvent_t> ev{ nullptr, nullptr };
+    if (!c->ffn_ev_free.empty()) { ev = c->ffn_ev_free.back(); c->ffn_ev_free.pop_back(); }
+    else if (hipEventCreate(&ev.first) != hipSuccess || hipEventCreate(&ev.second) != hipSuccess) {
+        (void) hipGetLastError(); return fail(c, FL_EHIP, "hipEventCreate");
+    }
+    TRY(c, hipEventRecord(ev.first, c->st));
+    const int rc = ffn_begin_body(c, W, N, ncur, ffn_inp, wrow);
+    TRY(c, hipEventRecord(ev.second, c->st));
+    c->ffn_ev_pending.push_back(ev);
+    return rc;
+}
+static int ffn_begin_body(FLCtx * c, const FLW * W, int N, const float * ncur, const float * ffn_inp, int wrow) {
     if (!W || !ncur || !ffn_inp) { return fail(c, FL_EINVAL, "null pointer"); }
     if (N <= 0 || N > RMAX) { return fail(c, FL_ERANGE, "N = %d outside 1..%d", N, RMAX); }
     if (!W->gate_inp || !W->probs_b || !W->sh_gate || !W->sh_up || !W->sh_down) { return fail(c, FL_EINVAL, "router or shared-expert weight missing"); }
@@ -565,6 +596,40 @@ extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur,
     return FL_OK;
 }
 
+// Pinned host -> device on the context's stream (src/fused_layer.cu:414-420): a kernel reads the mapped host memory, so
+// the copy is ordered with the context's launches and uses no copy engine; memory HIP cannot map (pageable) goes
+// through the copy engine instead. Either way the call only enqueues: src must stay valid until the stream reaches it.
+extern "C" void fl_h2d(FLCtx * c, void * dst, const void * src, size_t bytes) {
+    if (bytes == 0) { return; }
+    if (!dst || !src) { std::fprintf(stderr, "[fused] fl_h2d: null pointer\n"); std::exit(7); }
+    void * dp = nullptr;
+    if (hipHostGetDevicePointer(&dp, const_cast<void *>(src), 0) != hipSuccess) { (void) hipGetLastError(); dp = nullptr; }
+    if (dp) {
+        if ((((uintptr_t) dst | (uintptr_t) dp | bytes) & 15) == 0) {
+            const size_t n = bytes / 16;
+            k_copy16<<<(unsigned) std::min<size_t>((n + 1023) / 1024, 2048), 256, 0, c->st>>>((const uint4 *) dp, (uint4 *) dst, n);
+        } else {
+            k_copy1<<<(unsigned) std::min<size_t>((bytes + 255) / 256, 8192), 256, 0, c->st>>>((const uint8_t *) dp, (uint8_t *) dst, bytes);
+        }
+        CK(hipGetLastError());
+        c->h2d_zc += bytes;
+    } else {
+        CK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->st));
+        c->h2d_ce += bytes;
+    }
+    if (!c->h2d_said && c->h2d_zc + c->h2d_ce > ((size_t) 64 << 20)) {
+        c->h2d_said = 1;
+        std::fprintf(stderr, "[fused] host->device by kernel (mapped pinned) %.0f MB, by copy engine %.0f MB so far\n",
+                     c->h2d_zc / 1048576.0, c->h2d_ce / 1048576.0);
+    }
+}
+extern "C" int fl_h2d_bytes(FLCtx * c, size_t * by_kernel, size_t * by_copy_engine) {
+    if (!c) { return FL_EINVAL; }
+    if (by_kernel) { *by_kernel = c->h2d_zc; }
+    if (by_copy_engine) { *by_copy_engine = c->h2d_ce; }
+    return FL_OK;
+}
+
 extern "C" void fl_fetch(FLCtx * c, int n, int what, FLOut * out) {
     std::memset(out, 0, sizeof(FLOut));
     Compat * s = cs(c);
@@ -573,6 +638,9 @@ extern "C" void fl_fetch(FLCtx * c, int n, int what, FLOut * out) {
     // (nothing else that the call returns is pending then); otherwise, or if the word is late, the stream is waited
     const bool seen = (what & ~1) == 0 && s->r_tagged && spin_words(reinterpret_cast<const unsigned *>(s->z_sel + ZS_DONE), 1, s->rtag, 20000.0);
     if (!seen) { CK(hipStreamSynchronize(c->st)); }
+    if (c->herr && __atomic_load_n(c->herr, __ATOMIC_ACQUIRE)) {   // the routing's poll timed out: its picks are -1
+        std::fprintf(stderr, "[fused] fl_fetch: the routing launch reported device code %d\n", *c->herr); std::exit(7);
+    }
     if (what & 1) {
         // the mirrors keep this call's values until the next fl_fetch whatever is enqueued meanwhile (the reference's
         // lifetime). ncur and ffn_inp are on the device exactly as the caller handed them to fl_ffn_begin (nothing

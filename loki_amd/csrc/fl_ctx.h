@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <string>
+#include <utility>
 #include <vector>
 
 template <class T> struct DBuf {
@@ -36,6 +37,9 @@ struct FLCtx {
     hipEvent_t em0 = nullptr, em1 = nullptr;
     int n_group = 8, topk_group = 4, topk = 8; float scale = 2.5f;
     int keep = 0; float renorm = 0.f;   // fl_moe_layer keeps each row's `keep` heaviest experts (0: all topk)
+    int share = 0;                       // ... by the engine's --share-experts rule (fl_set_share_experts)
+    int na_used = 0;                     // fl_moe_layer_noalloc ran on this context: fl_sync reads the scratch's error word
+    DBuf<int> sel8; DBuf<float> w8;      // every row's topk picks before that keep (per-pass path)
     int n_exp = 256;   // routed experts behind the reference-named entry points (FLW carries no count)
     double ms_moe = 0.0;
     std::string err;
@@ -66,6 +70,9 @@ struct FLCtx {
     DBuf<unsigned> rcnt;                       // the one-launch routing's self-resetting counter (launch_router_fused)
     DBuf<double> rpart;                        // the K-split router tiles' parts [KS][n][n_exp]
     DBuf<int> dscr;                            // the multi-workgroup dispatch's per-round counts and bases
+    size_t h2d_zc = 0, h2d_ce = 0; int h2d_said = 0;   // fl_h2d bytes by kernel (mapped pinned) / by copy engine
+    // fl_ffn_begin's event pairs (recorded, not yet folded into ms_ffn by fl_gpu_ms) and the reusable ones
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> ffn_ev_pending, ffn_ev_free; double ms_ffn = 0.0;
 };
 // fl_route_dev with, for the one-launch routing of a few rows (router_fused_ok), a host word set to the context's epoch
 // (as it is after the call) once the picks are written; done may be null, other sizes leave it alone
@@ -104,6 +111,21 @@ static std::vector<hipEvent_t> * prof_begin(FLCtx * c) {
     return &c->ev_pending.back();
 }
 static void prof_mark(FLCtx * c, std::vector<hipEvent_t> * ev, int i) { if (ev) { (void) hipEventRecord((*ev)[i], c->st); } }
+
+// fold fl_ffn_begin's recorded event pairs into ms_ffn: every pair when wait, else only those already complete
+inline void fold_ffn_events(FLCtx * c, bool wait) {
+    size_t keep = 0;
+    for (size_t i = 0; i < c->ffn_ev_pending.size(); ++i) {
+        auto ev = c->ffn_ev_pending[i];
+        hipError_t q = wait ? hipEventSynchronize(ev.second) : hipEventQuery(ev.second);
+        float ms = 0.f;
+        if (q == hipSuccess && hipEventElapsedTime(&ms, ev.first, ev.second) == hipSuccess) { c->ms_ffn += ms; c->ffn_ev_free.push_back(ev); continue; }
+        (void) hipGetLastError();
+        if (q == hipSuccess) { c->ffn_ev_free.push_back(ev); continue; }   // an unmeasurable pair is dropped, not kept
+        c->ffn_ev_pending[keep++] = ev;
+    }
+    c->ffn_ev_pending.resize(keep);
+}
 
 void compat_free(FLCtx * c);   // compat.hip
 // device ranges declared to hold IQ2_XXS matrices in the tiled layout (compat.hip; process-wide): fl_register_tiled,

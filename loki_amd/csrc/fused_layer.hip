@@ -53,11 +53,13 @@ constexpr size_t NA_NACT = na_up(NA_ACT + NEXP_MAX * 4);
 constexpr size_t NA_BYTES = na_up(NA_NACT + 4);
 static_assert(NA_BYTES == 5502720, "the allocation-free entry point's documented scratch size (5.25 MiB per GPU)");
 constexpr size_t NA_CLEAR0 = NA_TLOG, NA_CLEAR1 = NA_XQ;   // the tagged words and the error word start at zero
+static_assert((NA_ERR - NA_CLEAR0) % 16 == 0 && (NA_CLEAR1 - NA_CLEAR0) % 16 == 0, "cleared as 16-byte words");
+constexpr unsigned NA_EPOCH = 1;   // every call tags its hand-off words with this one epoch, after clearing them (below)
 constexpr int NA_MAXDEV = 64;
 }  // namespace
 static __device__ __align__(256) uint8_t scratch[NA_BYTES];
 
-struct NaDev { uint8_t * ptr = nullptr; int resolved = 0; unsigned epoch = 0; int tab_built = 0; };
+struct NaDev { uint8_t * ptr = nullptr; int resolved = 0; int ready = 0; };   // ready: table image built, words cleared
 static NaDev g_na[NA_MAXDEV];
 static std::mutex g_na_mu;
 
@@ -79,6 +81,7 @@ __global__ void __launch_bounds__(256) k_zero16(uint4 * p, size_t n) {
     for (size_t i = (size_t) blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t) gridDim.x * 256) { p[i] = make_uint4(0, 0, 0, 0); }
 }
 
+static bool decode_ready(FLCtx * c);
 static bool decode1_ready(FLCtx * c);
 
 // ================================================================ lifecycle
@@ -96,8 +99,21 @@ extern "C" FLCtx * fl_init(int kvp, int sc_cap) {
     } else {
         __atomic_store_n(c->herr, 0, __ATOMIC_RELEASE);
     }
-    (void) na_resolve(c->dev);   // the allocation-free entry point's scratch on this device
-    (void) decode1_ready(c);     // its set-up (attributes, XCD probe) here, not in a call that must not allocate
+    // the allocation-free entry point's scratch on this device: resolved, its table image built and its tagged words
+    // and error word cleared here, once per device, so that entry point only launches kernels
+    if (uint8_t * S = na_resolve(c->dev)) {
+        std::lock_guard<std::mutex> lk(g_na_mu);
+        NaDev & nd = g_na[c->dev];
+        if (!nd.ready) {
+            CK(build_table_image(reinterpret_cast<uint4 *>(S + NA_TAB), c->st));
+            k_zero16<<<512, 256, 0, c->st>>>(reinterpret_cast<uint4 *>(S + NA_CLEAR0), (NA_CLEAR1 - NA_CLEAR0) / 16);
+            CK(hipGetLastError());
+            CK(hipStreamSynchronize(c->st));
+            nd.ready = 1;
+        }
+    }
+    (void) decode_ready(c);      // its set-up (attributes, XCD probe) here, not in a call that must not allocate
+    (void) decode1_ready(c);
     return c;
 }
 
@@ -106,6 +122,7 @@ extern "C" void fl_free(FLCtx * c) {
     (void) hipStreamSynchronize(c->st);
     c->xq.release(); c->hq.release(); c->xd.release(); c->logits.release(); c->probs.release(); c->wts.release();
     c->h.release(); c->hd.release(); c->o.release(); c->g.release(); c->u.release(); c->xn.release();
+    c->sel8.release(); c->w8.release();
     c->sel.release(); c->counts.release(); c->offsets.release(); c->perm.release(); c->inv.release(); c->act.release(); c->nact.release();
     compat_free(c); c->zero_i.release(); c->terms.release(); c->cnt.release();
     c->tab.release(); c->derr.release(); c->dlogit.release(); c->dth.release(); c->dto.release();
@@ -113,6 +130,7 @@ extern "C" void fl_free(FLCtx * c) {
     c->ksg.release(); c->ksu.release(); c->rcnt.release(); c->rpart.release(); c->dscr.release();
     for (auto & v : c->ev_free) { for (auto e : v) { (void) hipEventDestroy(e); } }
     for (auto & v : c->ev_pending) { for (auto e : v) { (void) hipEventDestroy(e); } }
+    for (auto * l : { &c->ffn_ev_pending, &c->ffn_ev_free }) { for (auto & e : *l) { (void) hipEventDestroy(e.first); (void) hipEventDestroy(e.second); } }
     (void) hipEventDestroy(c->em0); (void) hipEventDestroy(c->em1); (void) hipStreamDestroy(c->own);
     if (c->herr) { (void) hipHostFree(c->herr); }
     delete c;
@@ -141,6 +159,14 @@ extern "C" int fl_sync(FLCtx * c) {
         TRY(c, hipMemcpy(&e, c->derr.p, sizeof e, hipMemcpyDeviceToHost));
         if (e) { TRY(c, hipMemset(c->derr.p, 0, sizeof e)); }
     }
+    if (c->na_used) {   // fl_moe_layer_noalloc reports into the scratch's error word of the device
+        if (uint8_t * S = na_resolve(c->dev)) {
+            int w = 0;
+            TRY(c, hipMemcpy(&w, S + NA_ERR, sizeof w, hipMemcpyDeviceToHost));
+            if (w) { const int z = 0; TRY(c, hipMemcpy(S + NA_ERR, &z, sizeof z, hipMemcpyHostToDevice)); }
+            e |= w;
+        }
+    }
     if (c->herr) { e |= __atomic_exchange_n(c->herr, 0, __ATOMIC_ACQ_REL); }
     if (e) {
         return fail(c, FL_EHIP, "a device kernel reported error code %d (decode block: a wait timed out or a workgroup ran on an unexpected XCD; prefill: bad LDS base); its outputs are invalid", e);
@@ -160,6 +186,10 @@ extern "C" int fl_set_keep(FLCtx * c, int keep, float renorm) {
     if (!c) { return FL_EINVAL; }
     if (keep < 0 || keep > MAXK || !(renorm >= 0.f)) { return fail(c, FL_EINVAL, "keep %d outside 0..%d or renorm %g negative", keep, MAXK, (double) renorm); }
     c->keep = keep; c->renorm = renorm; return FL_OK;
+}
+extern "C" int fl_set_share_experts(FLCtx * c, int on) {
+    if (!c) { return FL_EINVAL; }
+    c->share = on ? 1 : 0; return FL_OK;
 }
 extern "C" int fl_set_experts(FLCtx * c, int n_exp) {
     if (!c) { return FL_EINVAL; }
@@ -202,7 +232,7 @@ int route_dev(FLCtx * c, const float * W, const float * bias, const float * x, i
         if (!c->rcnt.p) { ALLOC(c, c->rcnt, 1); TRY(c, hipMemsetAsync(c->rcnt.p, 0, sizeof(unsigned), c->st)); }
         if (int rc = decode_tagged(c, c->st)) { return rc; }   // a fresh epoch for the tagged logit buffer
         TRY(c, launch_router_fused(W, x, n, n_exp, E, logits, bias, c->n_group, c->topk_group, c->topk, c->scale, probs, sel, w, c->dlogit.p,
-                                   c->epoch, c->rcnt.p, done, c->st));
+                                   c->epoch, c->rcnt.p, done, c->derr.p, c->herr ? c->herr_dev : nullptr, c->st));
         return FL_OK;
     }
     double * rp = nullptr;   // the K-split tiles' parts (n from RL_SPLIT_MIN to 1023)
@@ -482,6 +512,7 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     // the selection draws topk experts per row; the block runs the kept ones (fl_set_keep), tk per row
     const int E = L->E, H = L->H, ne = L->n_exp, tsel = c->topk, tk = c->keep > 0 ? c->keep : tsel, P = n * tk;
     const float renorm = c->keep > 0 ? c->renorm : 0.f;
+    const bool share = c->share && c->keep > 0 && tk < tsel && n > 1;   // the --share-experts keep across the rows
     const int * lf = c->lf;
     const bool kq = lf[0] != FL_IQ2 || lf[1] != FL_IQ2 || lf[2] != FL_IQ2 || lf[3] != FL_IQ2;
     {
@@ -524,7 +555,7 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
         DecodeArgs d{};
         d.tab = c->tab.p; d.x = x; d.n = n; d.prenorm = prenorm ? 1 : 0; d.nw = nw; d.eps = eps; d.resid = resid;
         d.Wr = L->gate_inp; d.bias = L->probs_b; d.n_exp = ne; d.n_group = c->n_group; d.topk_group = c->topk_group; d.topk = tsel; d.scale = c->scale;
-        d.keep = tk; d.renorm = renorm;
+        d.keep = tk; d.renorm = renorm; d.share = share ? 1 : 0;
         d.gate = (const uint8_t *) L->gate_exps; d.up = (const uint8_t *) L->up_exps; d.down = (const uint8_t *) L->down_exps;
         d.estride = (size_t) H * (E / 256) * IQ2B;
         d.sh_gate = (const uint8_t *) L->sh_gate; d.sh_up = (const uint8_t *) L->sh_up; d.sh_down = (const uint8_t *) L->sh_down;
@@ -558,7 +589,13 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     if (const size_t nd = router_split_doubles(n, ne, E)) { ALLOC(c, c->rpart, nd); rp = c->rpart.p; }
     TRY(c, launch_router_logits(L->gate_inp, x, n, ne, E, c->logits.p, rp, st));
     prof_mark(c, ev, 2);
-    TRY(c, launch_router_select(c->logits.p, L->probs_b, n, ne, c->n_group, c->topk_group, tsel, c->scale, c->probs.p, c->sel.p, c->wts.p, st, tk, renorm));
+    if (share) {   // every row's topk picks, then the keep across the rows
+        ALLOC(c, c->sel8, (size_t) n * tsel); ALLOC(c, c->w8, (size_t) n * tsel);
+        TRY(c, launch_router_select(c->logits.p, L->probs_b, n, ne, c->n_group, c->topk_group, tsel, c->scale, c->probs.p, c->sel8.p, c->w8.p, st, tsel, 0.f));
+        TRY(c, launch_keep_share(c->sel8.p, c->w8.p, n, tsel, tk, renorm, c->sel.p, c->wts.p, st));
+    } else {
+        TRY(c, launch_router_select(c->logits.p, L->probs_b, n, ne, c->n_group, c->topk_group, tsel, c->scale, c->probs.p, c->sel.p, c->wts.p, st, tk, renorm));
+    }
     prof_mark(c, ev, 3);
     int * dsc = nullptr;
     if (const size_t nd = dispatch_scratch_ints(P)) { ALLOC(c, c->dscr, nd); dsc = c->dscr.p; }
@@ -681,8 +718,10 @@ extern "C" int fl_moe_layer_normed(FLCtx * c, const FLMoeLayer * L, const float 
 
 // fl_moe_layer for decode batches with no device allocation: the single-launch decode block on the file-scope scratch of
 // the context's device (routing outputs, tagged hand-off words, table image, error word) instead of the context's
-// buffers. The epoch that tags the hand-off words is per device, so calls from any context on one device follow one
-// sequence; calls that overlap on one device race on the scratch.
+// buffers. Every call enqueues the same two kernels with arguments that depend only on its own inputs -- a fill kernel
+// that clears the tagged words, then the decode block tagging them with the fixed epoch NA_EPOCH -- and changes no
+// host-side state, so a call captured into a HIP graph stays correct on every replay (a consumer's wait is satisfied
+// only by a word this call's launch wrote). Calls that overlap on one device race on the scratch.
 extern "C" int fl_moe_layer_noalloc(FLCtx * c, const FLMoeLayer * L, const float * x, int n, float * y) {
     if (!c) { return FL_EINVAL; }
     if (!L || !x || !y) { return fail(c, FL_EINVAL, "null layer, x or y"); }
@@ -713,25 +752,18 @@ extern "C" int fl_moe_layer_noalloc(FLCtx * c, const FLMoeLayer * L, const float
     if (!decode_ready(c)) { return fail(c, FL_ESCOPE, "the single-launch decode block is not available on this device"); }
     uint8_t * S = na_resolve(c->dev);
     if (!S) { return fail(c, FL_EHIP, "hipGetSymbolAddress of the decode scratch failed on device %d", c->dev); }
-    NaDev & nd = g_na[c->dev];
+    if (!g_na[c->dev].ready) { return fail(c, FL_EHIP, "the decode scratch of device %d was not set up by fl_init", c->dev); }
+    c->na_used = 1;
     hipStream_t st = c->st;
-    unsigned epoch;
-    {
-        std::lock_guard<std::mutex> lk(g_na_mu);
-        if (!nd.tab_built) { TRY(c, build_table_image(reinterpret_cast<uint4 *>(S + NA_TAB), st)); nd.tab_built = 1; }
-        if (++nd.epoch == 0) { nd.epoch = 1; }
-        epoch = nd.epoch;
-        if (epoch == 1) {   // first call on the device, or the epoch wrapped: no stale word may carry the new epoch
-            const size_t n16 = (NA_CLEAR1 - NA_CLEAR0) / 16;
-            k_zero16<<<512, 256, 0, st>>>(reinterpret_cast<uint4 *>(S + NA_CLEAR0), n16);
-            TRY(c, hipGetLastError());
-        }
-    }
+    // the tagged words (not the error word, which fl_sync reads) back to zero: no word holds NA_EPOCH when the block starts
+    k_zero16<<<1024, 256, 0, st>>>(reinterpret_cast<uint4 *>(S + NA_CLEAR0), (NA_ERR - NA_CLEAR0) / 16);
+    TRY(c, hipGetLastError());
     const int tk = c->keep > 0 ? c->keep : c->topk;
     DecodeArgs d{};
     d.tab = reinterpret_cast<const uint4 *>(S + NA_TAB); d.x = x; d.n = n; d.prenorm = 0; d.nw = nullptr; d.eps = 0.f; d.resid = nullptr;
     d.Wr = L->gate_inp; d.bias = L->probs_b; d.n_exp = L->n_exp; d.n_group = c->n_group; d.topk_group = c->topk_group;
     d.topk = c->topk; d.scale = c->scale; d.keep = tk; d.renorm = c->keep > 0 ? c->renorm : 0.f;
+    d.share = c->share && c->keep > 0 && tk < c->topk && n > 1 ? 1 : 0;
     d.gate = (const uint8_t *) L->gate_exps; d.up = (const uint8_t *) L->up_exps; d.down = (const uint8_t *) L->down_exps;
     d.estride = (size_t) 2048 * 28 * IQ2B;
     d.sh_gate = (const uint8_t *) L->sh_gate; d.sh_up = (const uint8_t *) L->sh_up; d.sh_down = (const uint8_t *) L->sh_down;
@@ -744,7 +776,7 @@ extern "C" int fl_moe_layer_noalloc(FLCtx * c, const FLMoeLayer * L, const float
     d.act = reinterpret_cast<int *>(S + NA_ACT); d.nact = reinterpret_cast<int *>(S + NA_NACT);
     d.tlogits = reinterpret_cast<uint64_t *>(S + NA_TLOG); d.th = reinterpret_cast<uint64_t *>(S + NA_TH);
     d.to = reinterpret_cast<uint64_t *>(S + NA_TO); d.y = y;
-    d.epoch = epoch; d.err = reinterpret_cast<int *>(S + NA_ERR); d.herr = c->herr ? c->herr_dev : nullptr;
+    d.epoch = NA_EPOCH; d.err = reinterpret_cast<int *>(S + NA_ERR); d.herr = c->herr ? c->herr_dev : nullptr;
     TRY(c, launch_decode(c, d, st));
     return FL_OK;
 }
@@ -783,9 +815,12 @@ extern "C" void fl_attn(FLCtx *, const FLW *, int, int, const int *, void *, voi
 extern "C" void fl_spec(FLCtx *, const FLW *, void *, void *) { out_of_scope("fl_spec"); }
 extern "C" void fl_sketch(FLCtx *, const float *, const void *, int) { out_of_scope("fl_sketch"); }
 
-extern "C" void fl_h2d(FLCtx * c, void * dst, const void * src, size_t bytes) {
-    if (bytes == 0) { return; }
-    CK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->st));
-}
 extern "C" void fl_wait_event(FLCtx * c, hipEvent_t ev) { CK(hipStreamWaitEvent(c->st, ev, 0)); }
-extern "C" double fl_gpu_ms(FLCtx * c, int which) { return which == 1 ? c->ms_moe : 0.0; }
+// accumulated GPU time in ms (src/fused_layer.cu:620): 1 = the experts (fl_moe, fl_skip: their launches to their
+// stream wait, as the reference times them); 0 and 2 = fl_ffn_begin's work, the MoE tail of the reference's attention
+// phase that this library owns (the router, and the copy in of its rows); 3..7 (speculation, attention parts) = 0
+extern "C" double fl_gpu_ms(FLCtx * c, int which) {
+    if (!c) { return 0.0; }
+    fold_ffn_events(c, true);
+    return which == 1 ? c->ms_moe : which == 0 || which == 2 ? c->ms_ffn : 0.0;
+}

@@ -765,7 +765,11 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
             TRACE(wave, 3);
             if (!ok) { report(a, 2); }
             if (ok) {
-                select_token_p<false>(pv, bv, a.n_exp, a.n_group, a.topk_group, a.topk, a.scale, nullptr, (int *) (rt.sel + wave * a.keep), (float *) (rt.wts + wave * a.keep), a.keep, a.renorm);
+                // with --share-experts every pick first (stride topk), the keep across the rows then runs in the
+                // dispatch wave
+                const int ks = a.share ? a.topk : a.keep;
+                select_token_p<false>(pv, bv, a.n_exp, a.n_group, a.topk_group, a.topk, a.scale, nullptr, (int *) (rt.sel + wave * ks),
+                                      (float *) (rt.wts + wave * ks), ks, a.share ? 0.f : a.renorm);
             } else if (lane == 0) {
                 __hip_atomic_fetch_or(ctl + 3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
@@ -773,6 +777,10 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
         TRACE(wave, 4);
         if (lds_arrive(ctl + 1, (unsigned) n)) {
             const bool all_ok = __builtin_amdgcn_readfirstlane(__hip_atomic_load(ctl + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) == 0;
+            if (a.share && all_ok) {   // the rows' kept picks, in place ([n][topk] -> [n][keep]); the set U in the EXT area
+                keep_share_rows(rt.sel, rt.wts, n, a.topk, a.keep, a.renorm, rt.sel, rt.wts, reinterpret_cast<LK_LOCAL unsigned *>(lds + L_EXT), true);
+                lds_visible();
+            }
             dispatch_wave(a, lds, all_ok ? P : 0);
             const bool staged = lds_wait_count(ctl + 0, DW);   // the tasks read the tables and the tokens
             lds_visible();

@@ -686,4 +686,68 @@ __device__ __forceinline__ void select_token(const float (&lg)[4], const float (
     select_token_p(p, bias, n_exp, n_group, topk_group, topk, scale, scr, sel_out, w_out, keep, renorm);
 }
 
+// --share-experts keep (src/server_core_fused.cpp:798-806) by one wave over n rows, in row order. Row i's topk picks
+// (expert, weight) are sel8 / w8 [i * topk ..] in pick order; each row keeps its own min(2, ke) heaviest (weight
+// descending, equal weights in pick order), then, in that weight order, its other picks whose expert is in the set U,
+// then its remaining picks, each of which joins U as it is taken; renorm > 0 rescales the kept weights by renorm / sw
+// with sw their fp32 sum in kept order (when sw > 1e-6). Outputs [i * ke ..] in kept order may alias sel8 / w8 (ke <=
+// topk: row i is read whole before it is written, and later rows are never overwritten). U: 8 words of 32 expert bits
+// (n_exp <= 256), filled here from every row's own picks when init, else given.
+template <class SI, class SF, class DI, class DF, class PU>
+__device__ __noinline__ void keep_share_rows(SI sel8, SF w8, int n, int topk, int ke, float renorm, DI sel_out, DF w_out, PU U, bool init) {
+#pragma clang fp contract(off)
+    const int lane = lane_id(), own = ke < 2 ? ke : 2;
+    const bool act = lane < topk;
+    auto rank_of = [&](float wv) {
+        int r = 0;
+        for (int j = 0; j < topk; ++j) {
+            const float o = __builtin_bit_cast(float, rdlane(__builtin_bit_cast(uint32_t, wv), j));
+            r += (o > wv || (o == wv && j < lane)) ? 1 : 0;
+        }
+        return r;
+    };
+    auto visible = [&]() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront"); __builtin_amdgcn_s_waitcnt(0); __builtin_amdgcn_wave_barrier(); };
+    if (init) {
+        if (lane < 8) { U[lane] = 0u; }
+        visible();
+        for (int i = 0; i < n; ++i) {
+            const int e = act ? sel8[i * topk + lane] : 0;
+            const float wv = act ? w8[i * topk + lane] : 0.f;
+            const int r = rank_of(wv);
+            if (act && r < own) { __hip_atomic_fetch_or(&U[(e >> 5) & 7], 1u << (e & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT); }
+        }
+        visible();
+    }
+    for (int i = 0; i < n; ++i) {
+        const int e = act ? sel8[i * topk + lane] : 0;
+        const float wv = act ? w8[i * topk + lane] : 0.f;
+        const int r = rank_of(wv);
+        const bool inU = act && ((U[(e >> 5) & 7] >> (e & 31)) & 1u);
+        // phase 1: the row's other picks whose expert U holds, by rank; phase 2 (only if phase 1 leaves slots): the rest
+        const bool c1 = act && r >= own && inU;
+        const bool c2 = act && r >= own && !inU;
+        const uint64_t m1 = __ballot(c1), m2 = __ballot(c2);
+        int p1 = 0, p2 = 0;   // candidates of the same phase ranked above this lane's pick
+        for (int j = 0; j < topk; ++j) {
+            const int rj = (int) rdlane((uint32_t) r, j);
+            p1 += ((m1 >> j) & 1) && rj < r ? 1 : 0;
+            p2 += ((m2 >> j) & 1) && rj < r ? 1 : 0;
+        }
+        const int n1 = __popcll(m1), t1 = n1 < ke - own ? n1 : ke - own;
+        const bool take1 = c1 && p1 < ke - own;
+        const bool take2 = c2 && own + t1 + p2 < ke;
+        const int pos = !act ? -1 : r < own ? r : take1 ? own + p1 : take2 ? own + t1 + p2 : -1;
+        float f = 1.f; bool rescale = false;
+        if (renorm > 0.f) {
+            float sw = 0.0f;
+            for (int q = 0; q < ke; ++q) { sw = sw + __builtin_bit_cast(float, rdlane(__builtin_bit_cast(uint32_t, wv), first_lane(pos == q))); }
+            if (sw > 1e-6f) { f = renorm / sw; rescale = true; }
+        }
+        visible();   // the whole row is read before any of it is written (in place)
+        if (pos >= 0) { sel_out[i * ke + pos] = e; w_out[i * ke + pos] = rescale ? wv * f : wv; }
+        if (take2) { __hip_atomic_fetch_or(&U[(e >> 5) & 7], 1u << (e & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT); }
+        visible();
+    }
+}
+
 }  // namespace lk

@@ -23,14 +23,20 @@ hipError_t launch_router_select(const float * logits, const float * bias, int n,
                                 int topk, float scale, float * probs, int * sel, float * wts, hipStream_t st, int keep = 0,
                                 float renorm = 0.f);
 
+// the engine's --share-experts keep (src/server_core_fused.cpp:798-806) of n rows' topk picks sel8 / w8 [n][topk] (pick
+// order, n_exp <= 256) into sel / wts [n][ke] in kept order, rescaled to renorm when renorm > 0
+hipError_t launch_keep_share(const int * sel8, const float * w8, int n, int topk, int ke, float renorm, int * sel, float * wts, hipStream_t st);
+
 // both in one launch for n <= 8 tokens and K = 7168 (router_fused_ok): the last workgroup to finish its logits selects,
 // reading the others' logits as epoch-tagged words tl [n][n_exp] (zero or older epochs before the launch). cnt: a
 // device word that is zero before the launch and left zero; done (may be null): host memory set to epoch once sel and
-// wts are written (system scope)
+// wts are written (system scope); err / herr (may be null): device and mapped host words that get code 2 if a poll of
+// the tagged logits times out (the picks are then -1)
 bool router_fused_ok(int n, int K);
 hipError_t launch_router_fused(const float * W, const float * x, int n, int n_exp, int K, float * logits, const float * bias, int n_group,
                                int topk_group, int topk, float scale, float * probs, int * sel, float * wts, uint64_t * tl,
-                               unsigned epoch, unsigned * cnt, unsigned * done, hipStream_t st, int keep = 0, float renorm = 0.f);
+                               unsigned epoch, unsigned * cnt, unsigned * done, int * err, int * herr, hipStream_t st, int keep = 0,
+                               float renorm = 0.f);
 
 // stable counting sort of the P = n*topk pairs by expert: counts [n_exp], offsets [n_exp+1], perm/inv [P],
 // act = used experts ascending, nact = their number (device scalar)
@@ -82,6 +88,7 @@ struct DecodeArgs {
     // their weights summed in k order): moe_out = that sum, y = (moe_out + shared) + resid
     // (o_out, may be null: the 8 slots' outputs [slot][E], for the reference's per-slot attribution)
     const int * ext_sel; const float * ext_w; float * moe_out; float * o_out;
+    int share;                                       // keep < topk by the engine's --share-experts rule (n <= 8 block)
     int E, H;                                        // 7168, 2048 (the kernel's geometry)
     int8_t * xq; float * xd;                         // Q8_K of x (written by workgroup 0)
     float * logits, * probs; int * sel; float * wts; int * counts, * offsets, * perm, * inv, * act, * nact;
@@ -132,7 +139,8 @@ struct PrefillArgs {
 hipError_t prefill_init();
 size_t prefill_table_bytes();
 hipError_t build_prefill_tables(uint4 * img, hipStream_t st);
-// columns of <= 32 slots of one expert: the shared expert's first, then act order; cols sized >= (n+P)/32 + NEXP_MAX + 2
+// columns of <= 64 slots (PF_TOK) of one expert: the shared expert's ceil(n / 64) first, then act order; cols sized
+// >= prefill_shared_cols(n) + P / 64 + NEXP_MAX + 2
 hipError_t launch_prefill_cols(const int * act, const int * nact, const int * offsets, int n, int P, int4 * cols, int * ncols, hipStream_t st);
 int prefill_shared_cols(int n);   // the shared expert's columns (the first ones) for n tokens
 hipError_t launch_q8_to_h(const int8_t * q, _Float16 * h, int64_t n, hipStream_t st);

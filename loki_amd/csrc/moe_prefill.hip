@@ -4,7 +4,7 @@
 // of <= 8 rows each with mma.m16n8k32 s8 tiles, then swiglu_q8 (:334-341) and the down pass; the semantics are ggml's
 // mul_mat_id over IQ2_XXS x Q8_K (ggml_vec_dot_iq2_xxs_q8_K per output). Here one launch covers every expert of the
 // layer:
-//   * A column is up to 32 dispatch slots of one expert (the shared expert's slots P .. P + n - 1 included); an item is
+//   * A column is up to 64 dispatch slots (PF_TOK) of one expert (the shared expert's slots P .. P + n - 1 included); an item is
 //     (column, 256 or 512 rows). The workgroups (one per CU: the tables fill most of the LDS) take the items round-robin.
 //   * The weights are dequantised once per item into fp16 MFMA operands: lane (r, g) of a wave owns row r of a 16-row
 //     tile and the 16-byte chunk g of each block (sub-blocks 2g, 2g + 1, both with their scale nibbles), so it builds

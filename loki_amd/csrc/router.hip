@@ -94,7 +94,8 @@ __global__ void __launch_bounds__(256) k_router_wg_sel(const float * __restrict_
                                                        float * __restrict__ logits, const float * __restrict__ bias, int n_group,
                                                        int topk_group, int topk, float scale, int keep, float renorm,
                                                        float * __restrict__ probs, int * __restrict__ sel, float * __restrict__ wts,
-                                                       uint64_t * tl, unsigned epoch, unsigned * cnt, unsigned * done) {
+                                                       uint64_t * tl, unsigned epoch, unsigned * cnt, unsigned * done, int * err,
+                                                       int * herr) {
     __shared__ double part[RF_MAXN][4];
     __shared__ float scr[4][NEXP_MAX + 2 * 64];
     __shared__ int so[RF_MAXN][MAXK]; __shared__ float wo[RF_MAXN][MAXK];
@@ -128,8 +129,12 @@ __global__ void __launch_bounds__(256) k_router_wg_sel(const float * __restrict_
             ok = __ballot(!ok) == 0;
             if (!ok) { __builtin_amdgcn_s_sleep(1); }
         }
-        if (!ok) {   // unreachable unless stores are lost: no picks rather than wrong ones
+        if (!ok) {   // unreachable unless stores are lost: no picks rather than wrong ones, and the error reported
             if (lane < keep) { so[t][lane] = -1; wo[t][lane] = 0.f; }
+            if (lane == 0) {
+                if (err) { __hip_atomic_fetch_or(gptr(err), 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+                if (herr) { __hip_atomic_store(gptr(herr), 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); }
+            }
             continue;
         }
         float lg[4];
@@ -496,13 +501,42 @@ bool router_fused_ok(int n, int K) { return n >= 1 && n <= RF_MAXN && K == 7168;
 
 hipError_t launch_router_fused(const float * W, const float * x, int n, int n_exp, int K, float * logits, const float * bias, int n_group,
                                int topk_group, int topk, float scale, float * probs, int * sel, float * wts, uint64_t * tl,
-                               unsigned epoch, unsigned * cnt, unsigned * done, hipStream_t st, int keep, float renorm) {
+                               unsigned epoch, unsigned * cnt, unsigned * done, int * err, int * herr, hipStream_t st, int keep,
+                               float renorm) {
     if (keep <= 0) { keep = topk; }
     if (!router_fused_ok(n, K) || !cnt || !tl || epoch == 0 || !select_rule_ok(n_exp, n_group, topk_group, topk, keep)) {
         return hipErrorInvalidValue;
     }
     k_router_wg_sel<<<dim3(n_exp), 256, 0, st>>>(W, x, n, n_exp, logits, bias, n_group, topk_group, topk, scale, keep, renorm, probs, sel,
-                                                 wts, tl, epoch, cnt, done);
+                                                 wts, tl, epoch, cnt, done, err, herr);
+    return hipGetLastError();
+}
+
+// --share-experts keep of n rows (keep_share_rows): every thread adds its rows' own picks to the LDS set, then wave 0
+// runs the rows in order
+__global__ void __launch_bounds__(256) k_keep_share(const int * __restrict__ sel8, const float * __restrict__ w8, int n, int topk, int ke,
+                                                    float renorm, int * __restrict__ sel, float * __restrict__ wts) {
+    __shared__ unsigned U[8];
+    if (threadIdx.x < 8) { U[threadIdx.x] = 0u; }
+    __syncthreads();
+    const int own = ke < 2 ? ke : 2;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        for (int k = 0; k < topk; ++k) {
+            const float wk = gptr(w8)[(size_t) i * topk + k];
+            int r = 0;
+            for (int j = 0; j < topk; ++j) { const float o = gptr(w8)[(size_t) i * topk + j]; r += (o > wk || (o == wk && j < k)) ? 1 : 0; }
+            if (r < own) { const int e = gptr(sel8)[(size_t) i * topk + k]; atomicOr(&U[(e >> 5) & 7], 1u << (e & 31)); }
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        keep_share_rows(gptr(sel8), gptr(w8), n, topk, ke, renorm, gptr(sel), gptr(wts), (LK_LOCAL unsigned *) U, false);
+    }
+}
+hipError_t launch_keep_share(const int * sel8, const float * w8, int n, int topk, int ke, float renorm, int * sel, float * wts, hipStream_t st) {
+    if (n <= 0) { return hipSuccess; }
+    if (topk < 1 || topk > MAXK || ke < 1 || ke > topk) { return hipErrorInvalidValue; }
+    k_keep_share<<<1, 256, 0, st>>>(sel8, w8, n, topk, ke, renorm, sel, wts);
     return hipGetLastError();
 }
 

@@ -240,16 +240,62 @@ int or_router(const float * W, const float * bias, const float * x, int64_t n, i
  * :815) take row 0's kept experts at weight 0. */
 int or_keep_experts(const int32_t * sel, const float * w, int64_t n, int topk, int ke, float renorm, int64_t n_pad,
                     int32_t * sel_out, float * w_out) {
+    return or_keep_experts_share(sel, w, n, topk, ke, renorm, n_pad, 0, sel_out, w_out);
+}
+
+/* The same with --share-experts (src/server_core_fused.cpp:798-806, the flag at :376; the production client passes it,
+ * loki/chat.py:35): when share != 0 and n > 1 every row keeps its own min(2, ke) heaviest experts; U = the set of those
+ * experts over the rows below n_pad; then row by row, in row order, the row's remaining slots are filled first by its
+ * other picks (weight order) whose expert is in U, then by its remaining picks (weight order), each such expert being
+ * added to U as it is taken (so later rows see it). The kept list is in that pick order, and the renorm sums it in
+ * that order. */
+int or_keep_experts_share(const int32_t * sel, const float * w, int64_t n, int topk, int ke, float renorm, int64_t n_pad,
+                          int share, int32_t * sel_out, float * w_out) {
     if (topk <= 0 || topk > 64 || ke <= 0 || ke > topk || n < 0) { return -1; }
+    int * ords = (int *) malloc((size_t) (n > 0 ? n : 1) * (size_t) topk * sizeof(int));
+    if (!ords) { return -3; }
     for (int64_t i = 0; i < n; ++i) {
-        int ord[64];
+        int * ord = ords + i * topk;
         for (int k = 0; k < topk; ++k) { ord[k] = k; }
         for (int a = 1; a < topk; ++a) {   /* insertion sort, strict comparison: stable */
             const int v = ord[a]; int b = a;
             while (b > 0 && w[i * topk + v] > w[i * topk + ord[b - 1]]) { ord[b] = ord[b - 1]; --b; }
             ord[b] = v;
         }
-        for (int k = 0; k < ke; ++k) { sel_out[i * ke + k] = sel[i * topk + ord[k]]; w_out[i * ke + k] = w[i * topk + ord[k]]; }
+    }
+    if (share && n > 1) {
+        const int own = ke < 2 ? ke : 2;
+        unsigned char inU[65536];
+        memset(inU, 0, sizeof inU);
+        for (int64_t i = 0; i < n && i < n_pad; ++i) {
+            for (int k = 0; k < own; ++k) { const int32_t e = sel[i * topk + ords[i * topk + k]]; if (e < 0 || e > 65535) { free(ords); return -2; } inU[e] = 1; }
+        }
+        for (int64_t i = 0; i < n; ++i) {
+            const int * ord = ords + i * topk;
+            int pick[64], np_ = 0;
+            for (int k = 0; k < own; ++k) { pick[np_++] = ord[k]; }
+            for (int k = own; k < topk && np_ < ke; ++k) {
+                const int32_t e = sel[i * topk + ord[k]];
+                if (e >= 0 && e <= 65535 && inU[e]) { pick[np_++] = ord[k]; }
+            }
+            for (int k = own; k < topk && np_ < ke; ++k) {
+                int taken = 0;
+                for (int j = 0; j < np_; ++j) { if (pick[j] == ord[k]) { taken = 1; break; } }
+                if (!taken) {
+                    pick[np_++] = ord[k];
+                    const int32_t e = sel[i * topk + ord[k]];
+                    if (e >= 0 && e <= 65535) { inU[e] = 1; }
+                }
+            }
+            for (int k = 0; k < ke; ++k) { sel_out[i * ke + k] = sel[i * topk + pick[k]]; w_out[i * ke + k] = w[i * topk + pick[k]]; }
+        }
+    } else {
+        for (int64_t i = 0; i < n; ++i) {
+            for (int k = 0; k < ke; ++k) { sel_out[i * ke + k] = sel[i * topk + ords[i * topk + k]]; w_out[i * ke + k] = w[i * topk + ords[i * topk + k]]; }
+        }
+    }
+    free(ords);
+    for (int64_t i = 0; i < n; ++i) {
         if (renorm > 0.f) {
             float sw = 0.0f;
             for (int k = 0; k < ke; ++k) { sw += w_out[i * ke + k]; }

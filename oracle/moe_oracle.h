@@ -41,6 +41,11 @@ int or_router(const float * W, const float * bias, const float * x, int64_t n, i
  * 0's kept experts at weight 0. sel_out / w_out [n][ke]. */
 int or_keep_experts(const int32_t * sel, const float * w, int64_t n, int topk, int ke, float renorm, int64_t n_pad,
                     int32_t * sel_out, float * w_out);
+/* the same with the engine's --share-experts rule when share != 0 and n > 1 (src/server_core_fused.cpp:798-806): each
+ * row keeps its own min(2, ke) heaviest, then prefers experts already in the set U of the rows' own picks (rows below
+ * n_pad), then takes the rest in weight order, adding them to U row by row; kept lists in that pick order */
+int or_keep_experts_share(const int32_t * sel, const float * w, int64_t n, int topk, int ke, float renorm, int64_t n_pad,
+                          int share, int32_t * sel_out, float * w_out);
 /* stable counting sort of the n*topk (token, k) pairs by expert; perm[j] = t*topk + k */
 int or_dispatch(const int32_t * sel, int64_t n, int topk, int n_exp, int32_t * counts, int32_t * offsets, int32_t * perm);
 

@@ -50,6 +50,7 @@ def lib():
         L.or_router.restype = I; L.or_router.argtypes = [P, P, P, I64, I, I64, I, I, I, F, P, P, P, P]
         L.or_dispatch.restype = I; L.or_dispatch.argtypes = [P, I64, I, I, P, P, P]
         L.or_keep_experts.restype = I; L.or_keep_experts.argtypes = [P, P, I64, I, I, F, I64, P, P]
+        L.or_keep_experts_share.restype = I; L.or_keep_experts_share.argtypes = [P, P, I64, I, I, F, I64, I, P, P]
         L.or_moe_forward.restype = I
         L.or_moe_forward.argtypes = [P, I64, I64, I64, P, P, I, I, I, I, F, P, P, P, P, P, P, P, P, P, P, P, P, P, I]
         L.or_moe_experts.restype = I
@@ -179,13 +180,15 @@ def router(W, bias, x, n_group=8, topk_group=4, topk=8, scale=2.5):
     return logits, probs, sel, wts
 
 
-def keep_experts(sel, w, ke, renorm=2.5, n_pad=None):
+def keep_experts(sel, w, ke, renorm=2.5, n_pad=None, share=False):
     """The engine's keep-KE (src/server_core_fused.cpp:793-815): per row the ke heaviest experts (stable, weight
-    descending), rescaled to sum to renorm (<= 0: off); rows >= n_pad take row 0's kept experts at weight 0."""
+    descending), rescaled to sum to renorm (<= 0: off); rows >= n_pad take row 0's kept experts at weight 0. share:
+    the --share-experts rule (:798-806) for n > 1."""
     sel = _c(sel, np.int32); w = _c(w, np.float32)
     n, topk = sel.shape
     so = np.empty((n, ke), np.int32); wo = np.empty((n, ke), np.float32)
-    rc = lib().or_keep_experts(_p(sel), _p(w), n, topk, ke, renorm, n if n_pad is None else n_pad, _p(so), _p(wo))
+    rc = lib().or_keep_experts_share(_p(sel), _p(w), n, topk, ke, renorm, n if n_pad is None else n_pad, 1 if share else 0,
+                                     _p(so), _p(wo))
     if rc != 0:
         raise ValueError("oracle keep_experts failed (%d)" % rc)
     return so, wo

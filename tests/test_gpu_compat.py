@@ -423,3 +423,107 @@ def test_narrow_one_row_single_launch(ctx, small_layer, case):
     assert np.array_equal(got[2][2].view(np.uint32), att.view(np.uint32))
     skip = (((np.float32(0) + mo[0]) + ref["sh"][0]).astype(np.float32) + fi[0]).astype(np.float32)
     assert np.array_equal(got[2][3].view(np.uint32), skip.view(np.uint32))
+
+
+def _hip():
+    """The HIP runtime, for the host allocations an engine makes itself (pinned staging, events)."""
+    h = ctypes.CDLL("libamdhip64.so")
+    h.hipHostMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t, ctypes.c_uint]
+    h.hipHostFree.argtypes = [ctypes.c_void_p]
+    return h
+
+
+def test_h2d_kernel_and_copy_engine(ctx):
+    """fl_h2d (src/fused_layer.cu:414-420): pinned sources are copied by a kernel reading the mapped memory (aligned
+    16-byte words and the unaligned byte path), pageable ones by the copy engine; the counts of fl_h2d_bytes say which
+    path ran, and every destination byte equals its source."""
+    import torch
+    from loki_amd import lib
+    hip = _hip()
+    nbytes = (3 << 20) + 4096
+    p = ctypes.c_void_p()
+    assert hip.hipHostMalloc(ctypes.byref(p), nbytes, 0) == 0
+    try:
+        pinned = np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_uint8)), shape=(nbytes,))
+        pinned[:] = np.random.default_rng(5).integers(0, 256, nbytes, dtype=np.uint8)
+        dst = torch.zeros(nbytes + 64, dtype=torch.uint8, device="cuda")
+        zc0, ce0 = ctypes.c_size_t(), ctypes.c_size_t()
+        ctx.check(lib().fl_h2d_bytes(ctx.ctx, ctypes.byref(zc0), ctypes.byref(ce0)))
+        cases = [(0, 0, 3 << 20), (16, 32, 4096 * 7), (3, 5, 100_003), (1, 0, 17)]   # (src off, dst off, bytes)
+        for so, do, n in cases:
+            lib().fl_h2d(ctx.ctx, dst.data_ptr() + do, p.value + so, n)
+        ctx.sync()
+        zc1, ce1 = ctypes.c_size_t(), ctypes.c_size_t()
+        ctx.check(lib().fl_h2d_bytes(ctx.ctx, ctypes.byref(zc1), ctypes.byref(ce1)))
+        assert zc1.value - zc0.value == sum(n for _, _, n in cases) and ce1.value == ce0.value
+        got = dst.cpu().numpy()
+        # later cases overwrite earlier ones' bytes: check each case on its own, in order, against a host replay
+        want = np.zeros(nbytes + 64, np.uint8)
+        for so, do, n in cases:
+            want[do:do + n] = pinned[so:so + n]
+        assert np.array_equal(got, want)
+        # pageable host memory: the copy engine
+        page = np.random.default_rng(6).integers(0, 256, 50_001, dtype=np.uint8)
+        lib().fl_h2d(ctx.ctx, dst.data_ptr() + 7, page.ctypes.data, page.size)
+        ctx.sync()
+        zc2, ce2 = ctypes.c_size_t(), ctypes.c_size_t()
+        ctx.check(lib().fl_h2d_bytes(ctx.ctx, ctypes.byref(zc2), ctypes.byref(ce2)))
+        assert zc2.value == zc1.value and ce2.value - ce1.value == page.size
+        assert np.array_equal(dst[7:7 + page.size].cpu().numpy(), page)
+    finally:
+        hip.hipHostFree(p)
+
+
+def test_wait_event_orders_the_context_stream(ctx):
+    """fl_wait_event (src/fused_layer.cu:421): work enqueued on the context's stream after the call starts only once
+    the event of another stream (the engine's loader) has completed. Another stream is kept busy for milliseconds
+    before it writes a marker and records the event; a copy of the marker on the context's stream reads the old value
+    without the wait (the control) and the new one with it."""
+    import torch
+    from loki_amd import lib
+    big = torch.ones(1 << 27, dtype=torch.float32, device="cuda")   # 512 MB: each pass ~0.15 ms
+    side = torch.cuda.Stream()
+    assert torch.cuda.current_stream().cuda_stream == (ctx.stream_handle or 0)   # the context runs on torch's current stream
+    for waited in (False, True):
+        marker = torch.zeros(1 << 16, dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        with torch.cuda.stream(side):
+            for _ in range(200):
+                big.mul_(1.0)
+            marker.fill_(7.0)
+            ev = torch.cuda.Event()
+            ev.record(side)
+        if waited:
+            lib().fl_wait_event(ctx.ctx, ctypes.c_void_p(ev.cuda_event))
+        seen = marker.clone()   # on the context's stream
+        torch.cuda.synchronize()
+        assert bool((seen == (7.0 if waited else 0.0)).all()), "waited=%s" % waited
+
+
+def test_gpu_ms_accounts_the_calls(ctx, small_layer):
+    """fl_gpu_ms (src/fused_layer.cu:620): 1 accumulates the experts' GPU time of fl_moe / fl_skip, 0 and 2 that of
+    fl_ffn_begin (the router this library runs in the reference's attention phase), 3 (speculation) stays 0."""
+    from loki_amd import FLOut, lib
+    (W, b, gate, up, down, sh), dev = small_layer
+    ctx.set_routing(8, 4, 8, 2.5)
+    flw = _flw(dev)
+    n = 2
+    x = gen.uniform(7, 13, (n, E), 2.0); fi = gen.uniform(7, 14, (n, E), 1.0)
+    m0, a0, s0 = (lib().fl_gpu_ms(ctx.ctx, w) for w in (1, 0, 3))
+    ctx.check(lib().fl_ffn_begin(ctx.ctx, ctypes.byref(flw), n, cptr(x), cptr(fi), -1))
+    out = FLOut()
+    lib().fl_fetch(ctx.ctx, n, 1, ctypes.byref(out))
+    a1 = lib().fl_gpu_ms(ctx.ctx, 0)
+    assert a1 > a0 and lib().fl_gpu_ms(ctx.ctx, 2) == a1
+    sel = np.ctypeslib.as_array(out.sel, shape=(n * KE,)).reshape(n, KE).copy()
+    wts = np.ctypeslib.as_array(out.wts, shape=(n * KE,)).reshape(n, KE).copy()
+    used = sorted(set(sel.ravel().tolist()))
+    ids = np.array([[used.index(e) for e in row] for row in sel], np.int32)
+    ga, ua, da = _arena(dev, used)
+    lib().fl_moe(ctx.ctx, ga.data_ptr(), ua.data_ptr(), da.data_ptr(), len(used), 4, cptr(ids), cptr(f32(wts)), KE, n, ctypes.byref(out))
+    m1 = lib().fl_gpu_ms(ctx.ctx, 1)
+    assert m1 > m0
+    mo = gen.uniform(7, 15, (n, E), 3.0)
+    lib().fl_skip(ctx.ctx, cptr(mo), n, ctypes.byref(out))
+    assert lib().fl_gpu_ms(ctx.ctx, 1) > m1
+    assert lib().fl_gpu_ms(ctx.ctx, 3) == s0 == 0.0

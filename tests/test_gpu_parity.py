@@ -539,6 +539,50 @@ def test_keep2_layer_bitwise(ctx, layer, n, mode):
     assert np.array_equal(y.cpu().numpy()[rows].view(np.uint32), ref["y"].view(np.uint32))
 
 
+@pytest.fixture(scope="module")
+def hot_layer(ctx):
+    """A layer whose router favours 12 experts (+0.3 bias), so the rows of a batch keep running into each other's
+    experts: the case the engine's --share-experts rule is for."""
+    return make_layer(ctx, seed=4242, bias_sigma=0.01, hot=[3, 40, 77, 90, 130, 131, 160, 199, 200, 222, 240, 251], hot_bias=0.3)
+
+
+@pytest.mark.parametrize("n,mode", [(8, 2), (8, 1), (8, 0), (2, 2), (40, 2), (300, 2)])
+def test_keep3_share_experts_bitwise(ctx, hot_layer, n, mode):
+    """The production client's setting, --experts 3 --share-experts (loki/chat.py:35; src/server_core_fused.cpp:798-806):
+    fl_set_keep(3, 2.5) with fl_set_share_experts -- across the rows inside the single decode launch (mode 2, and
+    cooperative: mode 1), on the per-pass kernels (mode 0), and before the MFMA grouped GEMMs (n = 40, 300) -- gives the
+    checker's router -> keep_experts(share) -> expert block bit for bit, kept selections and weights included. From 8
+    rows the batch is one where the rule changes some row's kept experts (checked on the checker)."""
+    layer = hot_layer
+    x = make_x(ctx, n, seed=1900 + n)
+    ctx.set_keep(3, 2.5)
+    ctx.set_share_experts(True)
+    try:
+        with ctx.using_fused(mode):
+            y = ctx.moe_layer(layer, x)
+            ctx.sync()
+            dbg = ctx.debug()
+            assert dbg.P == 3 * n and dbg.topk == 3
+            assert dbg.fused == (1 if (mode and n <= 8) else 0)
+            sel = ctx.d2h(dbg.sel, (n, 3), np.int32); wts = ctx.d2h(dbg.wts, (n, 3), np.float32)
+    finally:
+        ctx.set_share_experts(False)
+        ctx.set_keep(0)
+    xs = x.cpu().numpy()
+    W, b = layer.gate_inp.cpu().numpy(), layer.probs_b.cpu().numpy()
+    _, _, so, wo = orc.router(W, b, xs)
+    sk, wk = orc.keep_experts(so, wo, 3, 2.5, share=True)
+    plain, _ = orc.keep_experts(so, wo, 3, 2.5)
+    if n >= 8:
+        assert not np.array_equal(sk, plain), "the batch does not exercise the shared-expert preference"
+    assert np.array_equal(sel, sk)
+    assert np.array_equal(wts.view(np.uint32), wk.view(np.uint32))
+    rows = np.arange(n) if n <= 8 else np.array([0, 1, 17, 39])
+    _, _, gate, up, down, sh = host_layer(ctx, layer, sk[rows].ravel())
+    ref = orc.moe_experts(xs[rows], sk[rows], wk[rows], gate, up, down, *sh)
+    assert np.array_equal(y.cpu().numpy()[rows].view(np.uint32), ref["y"].view(np.uint32))
+
+
 @pytest.mark.parametrize("n", [16, 40])
 def test_prefill_mfma_exact_on_extreme_blocks(ctx, n):
     """Blocks at the format's extreme (scale nibble 15, the codebook's largest entries, signs aligned with the tokens,

@@ -320,6 +320,70 @@ def test_keep_experts_is_top_ke_set():
     assert np.all(np.diff(wo, axis=1) <= 0)
 
 
+def _share_brute(sel, w, ke, renorm, n_pad):
+    """--share-experts (src/server_core_fused.cpp:798-806) stated over Python sets: rank each row's picks by weight
+    (descending, ties in k order); own = the top min(2, ke); U = the union of the own experts of the real rows; rows in
+    order take their own, then (weight order) picks whose expert U holds, then the rest, which join U."""
+    n, topk = sel.shape
+    so = np.zeros((n, ke), np.int32); wo = np.zeros((n, ke), np.float32)
+    rank = [sorted(range(topk), key=lambda k, i=i: (-float(w[i, k]), k)) for i in range(n)]
+    own = min(2, ke)
+    U = {int(sel[i, k]) for i in range(min(n, n_pad)) for k in rank[i][:own]}
+    for i in range(n):
+        rest = rank[i][own:]
+        shared = [k for k in rest if int(sel[i, k]) in U]
+        take = rank[i][:own] + shared[:ke - own]
+        fill = [k for k in rest if k not in take][:ke - len(take)]
+        U |= {int(sel[i, k]) for k in fill}
+        take += fill
+        so[i] = sel[i, take]; wo[i] = w[i, take]
+        if renorm > 0:
+            sw = np.float32(0)
+            for k in range(ke):
+                sw = np.float32(sw + wo[i, k])
+            if sw > np.float32(1e-6):
+                wo[i] = (wo[i] * np.float32(np.float32(renorm) / sw)).astype(np.float32)
+    for i in range(max(n_pad, 1), n):
+        so[i] = so[0]; wo[i] = 0
+    return so, wo
+
+
+@pytest.mark.parametrize("ke,renorm", [(3, 2.5), (2, 2.5), (4, 0.0), (1, 2.5), (8, 2.5)])
+def test_keep_experts_share_matches_brute_force(ke, renorm):
+    """The --share-experts rule against the set formulation, on rows drawing from a small expert pool (so rows share
+    experts) with ties and a pad tail; share=False and n = 1 reduce to the plain keep."""
+    rng = np.random.default_rng(100 + ke)
+    n = 24
+    sel = np.stack([rng.choice(20, 8, replace=False) for _ in range(n)]).astype(np.int32)
+    w = rng.uniform(0.01, 0.8, (n, 8)).astype(np.float32)
+    w[2, :] = 0.25                            # all equal: k order
+    w[7, [0, 5]] = w[7].max() + 0.1           # a tie at the top
+    for n_pad in (n, 17):
+        so, wo = orc.keep_experts(sel, w, ke, renorm, n_pad, share=True)
+        bs, bw = _share_brute(sel, w, ke, renorm, n_pad)
+        assert np.array_equal(so, bs)
+        assert np.array_equal(wo.view(np.uint32), bw.view(np.uint32))
+    a = orc.keep_experts(sel, w, ke, renorm, share=False); b = orc.keep_experts(sel, w, ke, renorm)
+    assert all(np.array_equal(x.view(np.uint32), y.view(np.uint32)) for x, y in zip(a, b))
+    a = orc.keep_experts(sel[:1], w[:1], ke, renorm, share=True); b = orc.keep_experts(sel[:1], w[:1], ke, renorm)
+    assert all(np.array_equal(x.view(np.uint32), y.view(np.uint32)) for x, y in zip(a, b))
+
+
+def test_keep_experts_share_known_answer():
+    """Three rows worked by hand (ke = 3, weights descending in k so rank = k): own tops {10, 11}, {20, 21}, {30, 31},
+    U = {10, 11, 20, 21, 30, 31}. Row 0 = 10 11 | 12 20 ..: 12 is not in U, 20 is -> 10 11 20. Row 1 = 20 21 | 40 41
+    ..: none in U -> the next by weight, 40, which joins U. Row 2 = 30 31 | 41 40 ..: 40 is in U now, 41 is not -> 30
+    31 40 (the plain keep would take 41)."""
+    sel = np.array([[10, 11, 12, 20, 13, 14, 15, 16], [20, 21, 40, 41, 42, 43, 44, 45], [30, 31, 41, 40, 46, 47, 48, 49]], np.int32)
+    w = np.tile(np.linspace(0.8, 0.1, 8, dtype=np.float32), (3, 1))
+    so, wo = orc.keep_experts(sel, w, 3, 0.0, share=True)
+    assert so.tolist() == [[10, 11, 20], [20, 21, 40], [30, 31, 40]]
+    want_w = np.array([[w[0, 0], w[0, 1], w[0, 3]], [w[1, 0], w[1, 1], w[1, 2]], [w[2, 0], w[2, 1], w[2, 3]]], np.float32)
+    assert np.array_equal(wo, want_w)
+    plain, _ = orc.keep_experts(sel, w, 3, 0.0)
+    assert plain.tolist() == [[10, 11, 12], [20, 21, 40], [30, 31, 41]]
+
+
 # ---------------------------------------------------------------- whole block
 def _rand_experts(rng, n_exp, E, H):
     def mat(rows, cols):

@@ -2,7 +2,8 @@
 
 Its output must equal fl_moe_layer's bit for bit on the same inputs, on consecutive calls with shrinking batches (the
 file-scope scratch keeps the previous call's contents), interleaved with the regular entry point, and with keep-2
-routing; it must leave the context's own buffers unallocated and reject batches above its scratch's size."""
+routing; it must leave the context's own buffers unallocated and reject batches above its scratch's size. Captured
+into a HIP graph, every replay on a new x must equal fl_moe_layer on that x."""
 import ctypes
 
 import numpy as np
@@ -61,6 +62,47 @@ def test_noalloc_matches_moe_layer():
         x9 = make_x(ref, 9, seed=77)
         y9 = torch.empty_like(x9)
         assert _noalloc(na, layer, x9, y9) == FL_ERANGE
+    finally:
+        torch.cuda.synchronize()
+        na.close(); ref.close()
+
+
+@pytest.mark.parametrize("n", [1, 8])
+def test_noalloc_graph_replays(n):
+    """One call captured into a HIP graph (torch.cuda.CUDAGraph on the context's stream), replayed nine times over
+    three inputs copied into the captured x, with the program's own eager work and a synchronisation between replays:
+    every replay's y equals fl_moe_layer's on that input bit for bit (the one-token kernel at n = 1, the n <= 8 block at
+    n = 8), and fl_sync reports no device error afterwards."""
+    import torch
+    from loki_amd import FL_OK, Context, lib
+    na = Context()
+    ref = Context()
+    try:
+        layer = make_layer(ref, seed=4243)
+        xs = [make_x(ref, n, seed=300 + 10 * n + i) for i in range(3)]
+        want = [ref.moe_layer(layer, x).cpu().numpy() for x in xs]
+        ref.sync()
+        x_in, y_out = torch.empty_like(xs[0]), torch.empty_like(xs[0])
+        x_in.copy_(xs[0])
+        torch.cuda.synchronize()
+        side = torch.cuda.Stream()
+        na.check(lib().fl_set_stream(na.ctx, ctypes.c_void_p(side.cuda_stream)))   # before the capture starts
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            rc = _noalloc(na, layer, x_in, y_out)
+        na.check(lib().fl_set_stream(na.ctx, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+        assert rc == FL_OK
+        for rep in range(3):
+            for i, x in enumerate(xs):
+                x_in.copy_(x)
+                y_out.fill_(float("nan"))
+                torch.cuda.synchronize()
+                g.replay()
+                torch.cuda.synchronize()
+                got = y_out.cpu().numpy()
+                assert np.array_equal(got.view(np.uint32), want[i].view(np.uint32)), (n, rep, i)
+        na.sync()
+        del g
     finally:
         torch.cuda.synchronize()
         na.close(); ref.close()
