@@ -476,6 +476,60 @@ def test_routing_all_rows_prefill(ctx, n, hot):
     assert np.array_equal(y.cpu().numpy()[rows].view(np.uint32), ref["y"].view(np.uint32))
 
 
+def test_prefill512_every_row_vs_checker(ctx):
+    """configs[2] at full size: all 512 output rows of fl_moe_layer (MFMA grouped GEMMs, columns of up to 64 slots)
+    against the CPU checker's whole block (router, keep-all dispatch, Q8_K, IQ2_XXS x Q8_K products, SwiGLU, k-ordered
+    combine, shared expert): bit for bit, and within the task's tolerance."""
+    n = 512
+    layer = make_layer(ctx, seed=20260512, bias_sigma=0.05)
+    x = make_x(ctx, n, seed=9512)
+    y = ctx.moe_layer(layer, x).cpu().numpy()
+    ctx.sync()
+    xs = x.cpu().numpy()
+    W, b = layer.gate_inp.cpu().numpy(), layer.probs_b.cpu().numpy()
+    _, _, so, _ = orc.router(W, b, xs)
+    _, _, gate, up, down, sh = host_layer(ctx, layer, so.ravel())
+    ref = orc.moe_forward(xs, W, b, gate, up, down, *sh)
+    mx, l2 = rel_errors(y, ref["y"])
+    assert mx <= MAX_REL and l2 <= L2_REL, (mx, l2)
+    bad = np.nonzero(~np.all(y.view(np.uint32) == ref["y"].view(np.uint32), axis=1))[0]
+    assert bad.size == 0, "rows not bit-identical: %s (max rel %.3g)" % (bad[:16].tolist(), mx)
+
+
+def test_prefill2048_hot_columns_vs_checker(ctx):
+    """configs[4] (2048 tokens, +0.5 on 16 hot experts): the output rows whose dispatch slots fall in each hot expert's
+    first, middle and last (partial) 64-slot column -- first and last slot of each -- and the tokens of the shared
+    expert's first and last columns, against the CPU checker's whole block, bit for bit (at least 64 rows)."""
+    n = 2048
+    hot_ids = _hot_ids(20260101)
+    layer = make_layer(ctx, seed=20262048, bias_sigma=0.05, hot=hot_ids)
+    x = make_x(ctx, n, seed=92048)
+    y = ctx.moe_layer(layer, x).cpu().numpy()
+    ctx.sync()
+    st = _routing_state(ctx, n)
+    rows = set()
+    for e in hot_ids:
+        s0, s1 = int(st["offsets"][e]), int(st["offsets"][e + 1])
+        ncol = (s1 - s0 + 63) // 64
+        assert ncol >= 3, (e, s1 - s0)   # every hot expert spans several columns at this load
+        for c in (0, ncol // 2, ncol - 1):
+            first, last = s0 + 64 * c, min(s0 + 64 * c + 63, s1 - 1)
+            rows.add(int(st["perm"][first]) // 8); rows.add(int(st["perm"][last]) // 8)
+    rows |= {0, 1, 62, 63, n - 64, n - 63, n - 2, n - 1}   # the shared expert's first and last 64-token columns
+    rows = np.array(sorted(rows))
+    assert rows.size >= 64, rows.size
+    xs = x.cpu().numpy()[rows]
+    W, b = layer.gate_inp.cpu().numpy(), layer.probs_b.cpu().numpy()
+    _, _, so, _ = orc.router(W, b, xs)
+    assert np.array_equal(so.ravel(), st["sel"].reshape(n, 8)[rows].ravel())
+    _, _, gate, up, down, sh = host_layer(ctx, layer, so.ravel())
+    ref = orc.moe_forward(xs, W, b, gate, up, down, *sh)
+    mx, l2 = rel_errors(y[rows], ref["y"])
+    assert mx <= MAX_REL and l2 <= L2_REL, (mx, l2)
+    bad = rows[~np.all(y[rows].view(np.uint32) == ref["y"].view(np.uint32), axis=1)]
+    assert bad.size == 0, "rows not bit-identical: %s (max rel %.3g)" % (bad[:16].tolist(), mx)
+
+
 def test_stack58_routing(ctx):
     """all 58 independently seeded layers resident (~170 GB), one token chained through them with the norm
     inside each next layer's launch. Every layer's routing (selections and weights) is bit-identical to the checker's
