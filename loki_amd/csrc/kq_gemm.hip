@@ -126,14 +126,14 @@ __global__ void __launch_bounds__(KG_NT, 1) k_kq_gemm(const PrefillArgs a) {
             const int ar0 = sb - a.arow0;   // the first activation row
             const uint32_t oX = (uint32_t) (ar0 + (lane < sc ? lane : 0)) * (NB * 4);   // lane n: token n's block scales
             // activation rows: wave w copies token rows RW w + 2 i + (lane / 32), lane L < 32 of a row taking the row's
-            // chunk L ^ (row % 16)
+            // chunk pf_swz(L ^ (row % 16)), so chunk c sits at slot pf_swz(c) ^ (row % 16)
             constexpr int RW = 16 * NT / KG_W, NI = RW / 2;
             static_assert(RW % 2 == 0, "two token rows per copy instruction");
             uint32_t ob[NI];
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
                 const int row = RW * wave + 2 * i + (lane >> 5);
-                ob[i] = (uint32_t) (ar0 + (row < sc ? row : 0)) * (NB * QK * 2) + (uint32_t) ((lane & 31) ^ (row & 15)) * 16;
+                ob[i] = (uint32_t) (ar0 + (row < sc ? row : 0)) * (NB * QK * 2) + pf_swz((uint32_t) ((lane & 31) ^ (row & 15))) * 16;
             }
             auto load_b = [&](int j, int buf) -> float {
                 LK_LOCAL uint8_t * dst = lds + buf * KG_BUF;
@@ -175,7 +175,7 @@ __global__ void __launch_bounds__(KG_NT, 1) k_kq_gemm(const PrefillArgs a) {
                         kh8 x[NT];
 #pragma unroll
                         for (int tt = 0; tt < NT; ++tt) {
-                            x[tt] = __builtin_bit_cast(kh8, *(const LK_LOCAL u32x4 *) (size_t) (base + tt * KG_TILE + ((uint32_t) (ch ^ r) << 4)));
+                            x[tt] = __builtin_bit_cast(kh8, *(const LK_LOCAL u32x4 *) (size_t) (base + tt * KG_TILE + ((pf_swz((uint32_t) ch) ^ (uint32_t) r) << 4)));
                         }
                         const int scv = ck.sc[p];
                         const _Float16 sf = (_Float16) scv, cf = (_Float16) (Fm::Q6 ? 0.f : -1024.f * (float) scv);

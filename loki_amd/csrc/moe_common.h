@@ -118,6 +118,15 @@ __device__ __forceinline__ int iq2_scale(uint32_t a1t) {
     return (int) __builtin_amdgcn_udot4((a1t >> 7) & 0x01010101u, 0x10080402u, 1u, false);
 }
 
+// Activation rows of the MFMA GEMMs in LDS: a row (one token's 256-value block: 32 chunks of 16 B in a 512-byte row)
+// keeps chunk c at slot pf_swz(c) ^ r, r = row % 16 (flips only the low four bits). gfx950 serves a ds_read_b128 in
+// four passes of 16 lanes, each pass the lanes with equal bit 5 and equal (bit 4 ^ bit 3) of the lane id; a lane's bank
+// quad is its slot mod 16. In the GEMMs lane (r, g) = 16 g + r reads row r: a pass holds every r once, g's bit 1 fixed
+// and g's bit 0 = bit 3 of r ^ const. Chunk c's bits 3 and 4 being g's bits 0 and 1, pf_swz (which swaps them) moves
+// g's bit 0 out of the slot's low four bits: the 16 lanes of a pass read 16 different bank quads. With the plain slot
+// c ^ r two lanes of every pass would share one.
+__device__ __forceinline__ uint32_t pf_swz(uint32_t c) { return (c & 7u) | ((c & 8u) << 1) | ((c & 16u) >> 1); }
+
 __device__ __forceinline__ uint4 load_nt(const uint8_t * p) {   // streaming (non-temporal) 16-byte global load
     const u32x4 v = __builtin_nontemporal_load((const LK_GLOBAL u32x4 *) p);
     return make_uint4(v.x, v.y, v.z, v.w);

@@ -125,6 +125,9 @@ struct PfLane {
     uint32_t trg, trs;        // table addresses with this lane's copy
 };
 
+// activation rows in LDS: see pf_swz (moe_common.h); lane (r, g)'s chunk 8 g + t sits at slot (8 pf_swz2(g) + t) ^ r
+__device__ __forceinline__ int pf_swz2(int g) { return ((g & 1) << 1) | (g >> 1); }
+
 // one block of one 16-row tile: the tiled chunk g of row r (qs) and d
 struct PfW { u32x4 q; uint16_t d; };
 
@@ -220,15 +223,15 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
             // the column's activations of block j go straight from memory into LDS buffer j % 2 (buffer loads to LDS:
             // lane L's 16 bytes land at L * 16 of the instruction's 1 KB, no registers): wave w copies token rows
             // RW w + 2 i + (lane / 32), i < RW / 2 (RW = 16 NT / PF_W rows per wave), lane L < 32 of a row taking the
-            // row's chunk L ^ (row % 16) -- the XOR swizzle applied on the memory side. Lane n also loads token n's
-            // block scale into a register.
+            // row's chunk pf_swz(L ^ (row % 16)) -- the swizzle applied on the memory side. Lane n also loads token
+            // n's block scale into a register.
             constexpr int RW = 16 * NT / PF_W, NI = RW / 2;
             struct PfB { float dx; };
             uint32_t ob[NI];
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
                 const int row = RW * wave + 2 * i + (lane >> 5);
-                ob[i] = (uint32_t) brow(row) * (Geo::K * 2) + (uint32_t) ((lane & 31) ^ (row & 15)) * 16;
+                ob[i] = (uint32_t) brow(row) * (Geo::K * 2) + pf_swz((uint32_t) ((lane & 31) ^ (row & 15))) * 16;
             }
             auto load_b = [&](int j, PfB & bq, int buf) {
                 LK_LOCAL uint8_t * dst = lds + L_PB + buf * PB_BUF;
@@ -245,7 +248,7 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
             // one block: dequantise the C tiles step by step and run the MFMA chains of both token tiles
             auto block = [&](int j, const PfW (&w)[C], int buf, float dxl) {
                 static_assert((L_PB % 512) == 0 && (PB_BUF % 512) == 0, "XOR addressing inside 512-byte rows");
-                const uint32_t bx = ((uint32_t) (L_PB + buf * PB_BUF) + (uint32_t) ln.r * 512) | ((uint32_t) ((8 * ln.g) ^ ln.r) << 4);
+                const uint32_t bx = ((uint32_t) (L_PB + buf * PB_BUF) + (uint32_t) ln.r * 512) | ((uint32_t) ((8 * pf_swz2(ln.g)) ^ ln.r) << 4);
                 f4 cc[C][NT], cd[C][NT];   // the two exact chains: steps 0-3, steps 4-7
                 h2v sc[C][2];
                 uint32_t ms[C][2];
