@@ -10,18 +10,21 @@
 //      in LDS and the last 7 waves then run one gate/up task of the shared expert (routing-independent: shared h rows
 //      8 t .. 8 t + 7 with t = 32 x + i, so XCD x produces the shared expert's h block x);
 //   2. one workgroup per XCD selects the token's experts and broadcasts the picks to its XCD; pick k (0..7, selection
-//      order) is slot k, and slot k runs on XCD k: role (x, i) computes h rows kb * 256 + q * 64 .. + 63 of expert
-//      sel[x] (kb = i / 4, q = i % 4) as 56 items (one matrix, one 256-weight block, 64 rows) that the waves claim
-//      from an LDS counter;
-//   3. the four workgroups of (slot, kb) complete h block kb of their slot; each of them quantises that block to Q8_K
-//      and runs K-block kb of the slot's down for a quarter of its 7168 rows (split-K: one 256-weight block per row,
-//      one row per lane), plus 3 or 4 row groups of the shared expert's down for K-block x, again claimed by the
-//      waves unit by unit. Each row's block term (d_w * d_x) * bsum is published as a tagged word;
+//      order) is slot k, and slot k runs on XCD k. With every matrix IQ2_XXS, role (x, i) computes the h rows of
+//      expert sel[x] in two phases of 32 rows, 256 kb_p + 32 (i % 8) .. + 31 with kb_0 = i / 8 and kb_1 = 4 + i / 8,
+//      each 28 items (one matrix, two 256-weight blocks, 32 rows) that the waves claim from an LDS counter, so the
+//      eight workgroups of (slot, i / 8) complete h block kb_0 half-way through the gate/up and h block kb_1 at its end
+//      (the K-quant variants: h rows kb * 256 + q * 64 .. + 63 with kb = i / 4, q = i % 4, as 56 items of 64 rows);
+//   3. each workgroup quantises the h blocks it needs to Q8_K and runs the slot's down on them (split-K: one
+//      256-weight block per row, one row per lane): K-block kb_0 for an eighth of its 7168 rows, 3 or 4 row groups of
+//      the shared expert's down for K-block x, then K-block kb_1 for the same eighth -- the first two while block kb_1's
+//      hand-off completes (K-quant variants: K-block kb for a quarter of the rows). Each row's block term
+//      (d_w * d_x) * bsum is published as a tagged word;
 //   4. workgroup b combines rows 28 b .. 28 b + 27: per slot the 8 block terms folded in block order (ggml's sumf),
 //      * 0.125, then y = sum_k w_k o_k in k order + the shared o (+ the residual).
 // The arithmetic is that of the other decode kernels and the CPU checker step for step (the same device functions and
-// fold orders), so y is bit-identical to them. The down waits on four workgroups of its own XCD rather than on every
-// gate/up task of the expert, and no dispatch table is built (one token: the picks are distinct experts). Hand-offs
+// fold orders), so y is bit-identical to them. The down waits on the workgroups of its own XCD that complete its h
+// block rather than on every gate/up task of the expert, and no dispatch table is built (one token: the picks are distinct experts). Hand-offs
 // inside an XCD (the picks, h) stay in its L2; those across XCDs (logits, down partials) go through the device's
 // coherence point. Every wait is bounded: a timeout sets the error word and the wave skips the work, so the grid
 // always drains.
@@ -58,10 +61,11 @@ static_assert((size_t) SLOTS1 * H1 <= DEC_TH && (size_t) SLOTS1 * NBH1 * E1 <= D
 constexpr int M_X = TAB_BYTES;                     // staged Q8_K of the token
 constexpr int M_HR = M_X + GX1::XROW;              // staged Q8_K of the routed h block (256 B + scale)
 constexpr int M_HS = M_HR + 272;                   // staged Q8_K of the shared h block
+constexpr int M_HB = M_HS + 272;                   // staged Q8_K of the second routed h block (two-phase gate/up)
 constexpr int SHKP1 = 2 * NBX1;                    // K-quant shared task: (matrix, block) passes of 8 rows
 // shared task block terms: IQ2_XXS [7 steps][64 lanes]; K-quant [matrix][8 rows][28 blocks], then the min terms
 constexpr int PRE1 = GU_STEPS1 * 64 * 4 > 2 * SHKP1 * 8 * 4 ? GU_STEPS1 * 64 * 4 : 2 * SHKP1 * 8 * 4;
-constexpr int M_PRE = M_HS + 272;
+constexpr int M_PRE = M_HB + 272;
 constexpr int M_TERMS = M_PRE + PRE1;                  // routed block terms [matrix][block][64 rows]
 constexpr int M_SCR = M_TERMS + NITEM1 * 64 * 4;   // router / norm partial sums [4] (fp64)
 constexpr int M_CMB = M_SCR + 64;                  // combine: o [28 rows][9 slots]
@@ -73,7 +77,8 @@ constexpr int M_EXT = M_NRM + 16;                  // caller's picks: the distin
 constexpr int DEC1_LDS = M_EXT + 2 * MAXK * 4 + 16;
 static_assert(DEC1_LDS <= 160 * 1024 && (M_X % 16) == 0 && (M_HR % 16) == 0 && (M_HS % 16) == 0, "LDS layout");
 enum { C_RT = 0, C_STAGED = 1, C_SH = 2, C_READY = 3, C_HR = 4, C_HS = 5, C_CMBFAIL = 6, C_NRM = 7, C_RISSUED = 8,
-       C_GUCLAIM = 9, C_DNCLAIM = 10, C_GUDONE = 11, C_SB1 = 12, C_SELFAIL = 13, C_SHCLAIM = 14 };
+       C_GUCLAIM = 9, C_DNCLAIM = 10, C_GUDONE = 11, C_SB1 = 12, C_SELFAIL = 13, C_SHCLAIM = 14, C_GUDONE2 = 15,
+       C_HB = 16, C_LR = 17, C_LS = 18, C_LB = 19 };
 
 typedef LK_LOCAL uint8_t * lds1_t;
 typedef LK_CONST DecodeArgs D1Args;
@@ -529,6 +534,72 @@ __device__ __forceinline__ void gate_up1(const D1Args & a, lds1_t lds, LK_LOCAL 
     __builtin_amdgcn_s_setprio(0);
 }
 
+// The routed gate/up of an all-IQ2_XXS layer in two phases. Phase p of role (x, i) computes the 32 h rows
+// 256 kb_p + 32 (i % 8) .. + 31 of expert sel[x], kb_0 = i / 8, kb_1 = 4 + i / 8: the eight workgroups i / 8 = const
+// of an XCD complete h block kb_0 in phase 0 and kb_1 in phase 1. A phase is 28 items (matrix c % 2, blocks 2 (c / 2)
+// and 2 (c / 2) + 1: lanes 0-31 the first, lanes 32-63 the second, lane l row l % 32), each one 512-byte run of 32 rows
+// per chunk and block, claimed in order by all waves (phase 0's first). The wave completing a phase's 28th item folds
+// each row's 28 terms per matrix in block order (the gate rows in lanes 0-31, the up rows in lanes 32-63) and publishes
+// that phase's 32 h values. Block kb_0 is complete while phase 1 streams, so the down of K-block kb_0 runs while block
+// kb_1's hand-off completes (the single-phase order leaves every CU idle for that hand-off).
+constexpr int NIT2 = NBX1;               // items per phase: 2 matrices x 14 block pairs
+constexpr int TERMS2 = 2 * NBX1 * 32;    // a phase's terms: [matrix][block][32 rows]
+static_assert(2 * TERMS2 * 4 <= NITEM1 * 64 * 4, "both phases' terms in the gate/up terms' space");
+__device__ __forceinline__ int hrow2(int li, int ph) { return ((ph ? 4 : 0) + (li >> 3)) * QK + 32 * (li & 7); }
+__device__ __forceinline__ void gate_up2(const D1Args & a, lds1_t lds, LK_LOCAL unsigned * ctl, const uint8_t * gm,
+                                         const uint8_t * um, int slot, int li, uint32_t tr, int r) {
+#pragma clang fp contract(off)
+    const int lane = lane_id(), hl = lane >> 5, rr = lane & 31;
+    LK_LOCAL float * terms = reinterpret_cast<LK_LOCAL float *>(lds + M_TERMS);   // [phase][matrix][block][32 rows]
+    const uint8_t * xr = (const uint8_t *) (lds + M_X);
+    constexpr size_t DREG = (size_t) (H1 / 64) * NBX1 * 4096;
+    auto claim = [&](GuItem & it) {
+        unsigned c = 0;
+        if (lane == 0) { c = __hip_atomic_fetch_add(ctl + C_GUCLAIM, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+        it.c = (int) __builtin_amdgcn_readfirstlane(c);
+        if (it.c >= 2 * NIT2) { return; }
+        const int ph = it.c >= NIT2 ? 1 : 0, ci = it.c - ph * NIT2, j = 2 * (ci >> 1) + hl;
+        const int h0 = hrow2(li, ph), g64 = h0 >> 6, row = (h0 & 63) + rr;   // a 32-row half of one 64-row group
+        const uint8_t * mat = uniform1((ci & 1) ? um : gm);
+        // the scale first: memory waits count loads in issue order
+        it.d = *gptr(reinterpret_cast<const uint16_t *>(mat + DREG + ((size_t) g64 * NBX1 + j) * 128 + row * 2));
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t * qb = mat + ((size_t) g64 * NBX1 + j) * 4096 + row * 16;
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) { it.w[c4] = load_nt(qb + c4 * 1024); }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto run = [&](const GuItem & it) -> bool {
+        if (it.c >= 2 * NIT2) { return false; }
+        const int ph = it.c >= NIT2 ? 1 : 0, ci = it.c - ph * NIT2, j = 2 * (ci >> 1) + hl, m = ci & 1;
+        const int bsum = block_bsum_dpp(it.w, tr, xr + j * GX1::XBLK, r);   // each 16-lane row reads its own block
+        const float dx = reinterpret_cast<const float *>(xr + NBX1 * GX1::XBLK)[j];
+        terms[ph * TERMS2 + (m * NBX1 + j) * 32 + rr] = (h2f(it.d) * dx) * (float) bsum;
+        if (arrive1(ctl + (ph ? C_GUDONE2 : C_GUDONE), NIT2)) {
+            TRACE1(ph ? 13 : 12);
+            const LK_LOCAL float * tp = terms + ph * TERMS2 + hl * NBX1 * 32 + rr;
+            float v = 0.f;
+#pragma unroll 4
+            for (int k = 0; k < NBX1; ++k) { v = v + tp[k * 32]; }
+            const float u = __builtin_bit_cast(float, lanes_32_63(__builtin_bit_cast(uint32_t, v)));   // lanes 0-31: the up sums
+            if (hl == 0) {
+                st_xcd1(a.th + (size_t) slot * H1 + hrow2(li, ph) + rr, a.epoch, __builtin_bit_cast(uint32_t, det_silu(0.125f * v) * (0.125f * u)));
+            }
+        }
+        return true;
+    };
+    switch ((threadIdx.x >> 8) & 3) {   // staggered priorities, as in gate_up1
+        case 0: __builtin_amdgcn_s_setprio(0); break;
+        case 1: __builtin_amdgcn_s_setprio(1); break;
+        case 2: __builtin_amdgcn_s_setprio(2); break;
+        default: __builtin_amdgcn_s_setprio(3); break;
+    }
+    GuItem it;
+    claim(it);
+    while (run(it)) { claim(it); }
+    __builtin_amdgcn_s_setprio(0);
+}
+
 // ---------------------------------------------------------------- down: one 256-weight block per row
 // A unit is one 64-row group of one down matrix at one K-block: lane l owns row l (4 chunks + d); every lane's block
 // product uses the same staged h block, so the activations come by DPP from the 16 lanes that hold them.
@@ -563,6 +634,37 @@ __device__ __forceinline__ bool stage_h1(const D1Args & a, const uint64_t * src,
     float dq; const uint32_t packed = q8k_lane(xs, dq);
     *reinterpret_cast<LK_LOCAL uint32_t *>(dst + staged_word(lane)) = packed;
     if (lane == 0) { *reinterpret_cast<LK_LOCAL float *>(dst + QK) = dq; }
+    return true;
+}
+
+// the same for two blocks polled together (one memory round trip per poll for both); false on timeout
+__device__ __forceinline__ bool stage_h2(const D1Args & a, const uint64_t * s0, LK_LOCAL uint8_t * d0, const uint64_t * s1,
+                                         LK_LOCAL uint8_t * d1) {
+    const int lane = lane_id();
+    uint64_t w[8];
+    auto issue = [&]() {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) { w[k] = ld_tag1(s0 + 4 * lane + k); w[4 + k] = ld_tag1(s1 + 4 * lane + k); }
+    };
+    issue();
+    int it = 0;
+    for (; it < POLL1; ++it) {
+        bool v = true;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) { v = v && tag1_ok(w[k], a.epoch); }
+        if (__ballot(!v) == 0) { break; }
+        __builtin_amdgcn_s_sleep(1);
+        issue();
+    }
+    if (it == POLL1) { return false; }
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const float xs[4] = { tag1_val(w[4 * b]), tag1_val(w[4 * b + 1]), tag1_val(w[4 * b + 2]), tag1_val(w[4 * b + 3]) };
+        float dq; const uint32_t packed = q8k_lane(xs, dq);
+        LK_LOCAL uint8_t * dst = b ? d1 : d0;
+        *reinterpret_cast<LK_LOCAL uint32_t *>(dst + staged_word(lane)) = packed;
+        if (lane == 0) { *reinterpret_cast<LK_LOCAL float *>(dst + QK) = dq; }
+    }
     return true;
 }
 
@@ -838,7 +940,8 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
         if ((unsigned) e >= (unsigned) a.n_exp) { report1(a, 32); return; }
         const uint8_t * gm = uniform1(a.gate + (size_t) e * a.estride), * um = uniform1(a.up + (size_t) e * a.estride);
         TRACE1(5);
-        gate_up1(a, lds, ctl, gm, um, xcd, kb * QK + qq * 64, tr, r);
+        if constexpr (FD == 0) { gate_up2(a, lds, ctl, gm, um, xcd, li, tr, r); }
+        else { gate_up1(a, lds, ctl, gm, um, xcd, kb * QK + qq * 64, tr, r); }
         TRACE1(6);
     }
 
@@ -849,46 +952,65 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
     const int e_dn = reinterpret_cast<const LK_LOCAL int *>(lds + M_SEL)[xcd];
     LK_LOCAL unsigned * dclaim = ctl + C_DNCLAIM;
     if constexpr (FD == 0) {
-        // waves 0 and 1 poll and stage the routed and the shared h block; every wave then waits for both
-        auto stage_both = [&]() -> bool {
-            if (wave == 0) {
-                const bool ok = stage_h1(a, a.th + (size_t) xcd * H1 + (size_t) kb * QK, lds + M_HR);
-                if (!ok) { report1(a, 1); }
-                flag1(ctl + C_HR, ok ? 1u : 2u);
-            } else if (wave == 1) {
-                const bool ok = stage_h1(a, a.th + (size_t) 8 * H1 + (size_t) xcd * QK, lds + M_HS);
-                if (!ok) { report1(a, 1); }
-                flag1(ctl + C_HS, ok ? 1u : 2u);
-            }
-            TRACE1(7);
-            if (wait1(ctl + C_HR, 1) != 1 || wait1(ctl + C_HS, 1) != 1) { return false; }
-            lds_visible();
-            TRACE1(8);
-            return true;
-        };
+        // units in claim order: the 14 row groups (i % 8) * 14 .. + 13 at K-block kb_0 (h block kb_0, complete since
+        // phase 1), the shared expert's row groups at K-block x, then the same 14 row groups at K-block kb_1. The first
+        // wave to need an h block polls and stages it (the others wait on its LDS flag), so the hand-off of block kb_1
+        // overlaps the units before it.
+        constexpr int RG2 = E1 / 64 / 8;   // 14
+        const int hs = li & 7, kb0 = li >> 3, kb1 = 4 + (li >> 3);
+        const int nu2 = 2 * RG2 + nsh;
         const uint8_t * dmat = uniform1(a.down + (size_t) e_dn * a.estride);
-        auto unit = [&](int u, const uint8_t * & mat, int & g64, int & blk, int & slot) {
-            if (u < RGQ1) { mat = dmat; g64 = qq * RGQ1 + u; blk = kb; slot = xcd; }
-            else { mat = uniform1(a.sh_down); g64 = li + 32 * (u - RGQ1); blk = xcd; slot = 8; }
+        // unit u -> (matrix, row group, K-block, slot, staged block: 0 kb_0, 1 shared, 2 kb_1)
+        auto unit = [&](int u, const uint8_t * & mat, int & g64, int & blk, int & slot, int & hb) {
+            if (u < RG2) { mat = dmat; g64 = hs * RG2 + u; blk = kb0; slot = xcd; hb = 0; }
+            else if (u < RG2 + nsh) { mat = uniform1(a.sh_down); g64 = li + 32 * (u - RG2); blk = xcd; slot = 8; hb = 1; }
+            else { mat = dmat; g64 = hs * RG2 + (u - RG2 - nsh); blk = kb1; slot = xcd; hb = 2; }
         };
-        // the waves claim units from an LDS counter, one in flight per wave (as the gate/up items)
         auto claim_unit = [&](Dn1 & d, int & u) {
             unsigned c = 0;
             if (lane == 0) { c = __hip_atomic_fetch_add(dclaim, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
             u = (int) __builtin_amdgcn_readfirstlane(c);
-            if (u < nunits) { const uint8_t * m; int g, b, sl; unit(u, m, g, b, sl); dn1_issue(m, g, b, d); }
+            if (u < nu2) { const uint8_t * m; int g, b, sl, hb; unit(u, m, g, b, sl, hb); dn1_issue(m, g, b, d); }
+        };
+        // The first wave out of gate/up items stages the h blocks in the order they complete: kb_0 and the shared
+        // block together (both long complete by now, polled in one round trip), then kb_1; the other waves claim their
+        // units (loads in flight) and wait on the block's LDS flag.
+        {
+            unsigned got = 0;
+            if (lane == 0) { got = __hip_atomic_fetch_add(ctl + C_LR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+            if (__builtin_amdgcn_readfirstlane(got) == 0) {
+                bool ok = stage_h2(a, a.th + (size_t) xcd * H1 + (size_t) kb0 * QK, lds + M_HR, a.th + (size_t) 8 * H1 + (size_t) xcd * QK, lds + M_HS);
+                if (!ok) { report1(a, 1); }
+                flag1(ctl + C_HR, ok ? 1u : 2u); flag1(ctl + C_HS, ok ? 1u : 2u);
+                TRACE1(60);
+                ok = stage_h1(a, a.th + (size_t) xcd * H1 + (size_t) kb1 * QK, lds + M_HB);
+                if (!ok) { report1(a, 1); }
+                flag1(ctl + C_HB, ok ? 1u : 2u);
+                TRACE1(7);
+            }
+        }
+        auto ensure = [&](int hb) -> bool {
+            const unsigned v = wait1(ctl + (hb == 0 ? C_HR : hb == 1 ? C_HS : C_HB), 1);
+            lds_visible();
+            if (v == 0) { report1(a, 8); }
+            return v == 1;
         };
         Dn1 dn; int un;
         claim_unit(dn, un);
-        if (!stage_both()) { return; }
-        auto run_unit = [&](const Dn1 & d, int u) {
-            const uint8_t * m; int g, b, sl; unit(u, m, g, b, sl);
-            const uint8_t * hb = (const uint8_t *) (lds + (sl == 8 ? M_HS : M_HR));
-            const int bsum = block_bsum_dpp(d.w, tr, hb, r);
-            const float dx = *reinterpret_cast<const float *>(hb + QK);
-            st_tag1(a.to + ((size_t) sl * NBH1 + b) * E1 + (size_t) g * 64 + lane, a.epoch, (h2f(d.d) * dx) * (float) bsum);
-        };
-        while (un < nunits) { run_unit(dn, un); claim_unit(dn, un); }   // claims rise: the first past the end ends the list
+        while (un < nu2) {
+            const uint8_t * m; int g, b, sl, hb; unit(un, m, g, b, sl, hb);
+#ifdef LOKI_TRACE
+            if (un == 0) { TRACE1(58); }
+            if (un == RG2 + nsh) { TRACE1(59); }
+#endif
+            if (!ensure(hb)) { return; }
+            const uint8_t * hbp = (const uint8_t *) (lds + (hb == 0 ? M_HR : hb == 1 ? M_HS : M_HB));
+            const int bsum = block_bsum_dpp(dn.w, tr, hbp, r);
+            const float dx = *reinterpret_cast<const float *>(hbp + QK);
+            st_tag1(a.to + ((size_t) sl * NBH1 + b) * E1 + (size_t) g * 64 + lane, a.epoch, (h2f(dn.d) * dx) * (float) bsum);
+            claim_unit(dn, un);   // claims rise: the first past the end ends the list
+        }
+        TRACE1(8);
     } else {
         // K-quant: the shared expert's units (Q6_K) first -- its h block is complete long before the routed one, so
         // waves that finish their gate/up items early run them while the routed h block is still being formed -- then
