@@ -835,17 +835,10 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
         TRACE1(1);
     } else {
         if (!a.ext_sel) { (void) wait1(ctl + C_RISSUED, 4); }   // the router's weight and token loads go first (the critical path)
-        static_assert(TAB_BYTES % (1024 * NQW1) == 0, "table image split over the staging waves");
-        constexpr int PER = TAB_BYTES / 1024 / NQW1;
-#pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            const int cc = (wave - 4) * PER + k;
-            __builtin_amdgcn_global_load_lds((const LK_GLOBAL void *) (a.tab + cc * 64 + lane), (LK_LOCAL void *) (lds + cc * 1024), 16, 0, 0);
-        }
+        tables_fill(reinterpret_cast<const uint8_t *>(a.tab), lds, threadIdx.x - 256, NQW1 * 64);
         if (a.prenorm && !wait1(ctl + C_NRM, 1)) { report1(a, 64); return; }
         quant1(a, lds, wave - 4);
-        __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's table loads have landed in LDS
-        arrive1(ctl + C_STAGED, NQW1);
+        arrive1(ctl + C_STAGED, NQW1);   // (its LDS writes are done: arrive1 waits for them)
         TRACE1(1);
     }
     if (li == 0 && wave >= 4) {

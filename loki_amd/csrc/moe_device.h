@@ -62,6 +62,21 @@ __device__ __forceinline__ void tables_copy(uint8_t * lds, const uint4 * img) {
     for (int k = 0; k < PER; ++k) { reinterpret_cast<uint4 *>(lds)[k * NT + threadIdx.x] = v[k]; }
 }
 
+// The same image rebuilt from 16 bytes per line: each 256-byte line is 16 copies of its first 16 bytes (two copies of a
+// codebook entry, or one sign entry), so a workgroup reads 6 KB of the image instead of 96 KB (a launch of 256
+// workgroups then moves 1.5 MB through the L2 instead of 24 MB) and writes the copies into LDS. Thread t of nt fills
+// the line halves t, t + nt, ..; its k-th write goes to 16-byte slot (k + line) % 8 of its half, so any 16 lanes with
+// distinct (line % 8, half) write 16 different bank quads.
+__device__ __forceinline__ void tables_fill(const uint8_t * img, LK_LOCAL uint8_t * lds, int t, int nt) {
+    for (int p = t; p < 2 * (TAB_BYTES / 256); p += nt) {
+        const int line = p >> 1, half = p & 1;
+        const u32x4 v = *(const LK_GLOBAL u32x4 *) (img + (size_t) line * 256);
+        LK_LOCAL u32x4 * dst = reinterpret_cast<LK_LOCAL u32x4 *>(lds + line * 256 + half * 128);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) { dst[(k + line) & 7] = v; }
+    }
+}
+
 // ---------------------------------------------------------------- wave reductions without LDS
 // Pure-VALU reductions: DPP inside 16-lane rows (quad_perm xor 1, xor 2, row_half_mirror, row_mirror), then
 // row_bcast:15 / row_bcast:31 carry row results upwards so lane 63 ends with the result, read back once. __shfl would
