@@ -77,7 +77,7 @@ constexpr int M_EXT = M_NRM + 16;                  // caller's picks: the distin
 constexpr int DEC1_LDS = M_EXT + 2 * MAXK * 4 + 16;
 static_assert(DEC1_LDS <= 160 * 1024 && (M_X % 16) == 0 && (M_HR % 16) == 0 && (M_HS % 16) == 0, "LDS layout");
 enum { C_RT = 0, C_STAGED = 1, C_SH = 2, C_READY = 3, C_HR = 4, C_HS = 5, C_CMBFAIL = 6, C_NRM = 7, C_RISSUED = 8,
-       C_GUCLAIM = 9, C_DNCLAIM = 10, C_GUDONE = 11, C_SB1 = 12, C_SELFAIL = 13, C_SHCLAIM = 14, C_GUDONE2 = 15,
+       C_GUCLAIM = 9, C_DNCLAIM = 10, C_GUDONE = 11, C_SHCLAIM = 14, C_GUDONE2 = 15,
        C_HB = 16, C_LR = 17, C_LS = 18, C_LB = 19 };
 
 typedef LK_LOCAL uint8_t * lds1_t;
@@ -167,7 +167,7 @@ __device__ __forceinline__ float4 in1(const D1Args & a, lds1_t lds, int col, flo
 // ---------------------------------------------------------------- 1. router (waves 0-3) and staging (waves 4-7)
 // Thread (quarter w = wave, lane) owns chunk 64 w + lane (28 values) of expert b's logit: in-order fp64 chunk sum,
 // tree levels 1-6 by DPP (tree64), levels 7-8 over the four waves' totals in LDS; the last wave to arrive publishes
-// the logit (the selecting waves form p = sigmoid(logit)). Under prenorm the same threads first form the token's RMSNorm scale (the chunked sum-of-squares
+// p = sigmoid(logit) (the selecting wave reads probabilities; the logit goes to the layer's logits output). Under prenorm the same threads first form the token's RMSNorm scale (the chunked sum-of-squares
 // contract of k_rmsnorm, over the same chunks). Workgroups past the layer's experts only form the scale.
 __device__ __noinline__ void router1(const D1Args & a, lds1_t lds, int wave, LK_LOCAL unsigned * ctl) {
 #pragma clang fp contract(off)
@@ -227,52 +227,55 @@ __device__ __noinline__ void router1(const D1Args & a, lds1_t lds, int wave, LK_
     if (arrive1(ctl + C_RT, want) && lane == 0) {
         const LK_LOCAL double * pp = a.prenorm ? reinterpret_cast<const LK_LOCAL double *>(lds + M_SCR + 32) : part;
         const float l = (float) ((pp[0] + pp[1]) + (pp[2] + pp[3]));
-        st_tag1(a.tlogits + e, a.epoch, l);   // the logit goes out first: the selecting waves form the sigmoid
+        const float pe = det_sigmoid(l);
+        st_tag1(a.tlogits + e, a.epoch, pe);   // the selecting wave reads probabilities
         gptr(a.logits)[e] = l;
-        if (a.probs) { gptr(a.probs)[e] = det_sigmoid(l); }
+        if (a.probs) { gptr(a.probs)[e] = pe; }
     }
 }
 
 // ---------------------------------------------------------------- selection (one workgroup per XCD)
-// Waves 0-3 each poll 64 of the tagged logits and form their probabilities (one sigmoid per lane, into LDS); wave 0 then
-// runs select_token_p on them (four per lane). The sigmoid's fp64 chain is the longest part of the per-lane work, so
-// spreading it over four waves takes three quarters of it off the selecting wave.
-constexpr int S_P = M_TERMS;   // f32 [256] probabilities (the gate/up terms' space, unused until the picks are known)
-static_assert(S_P + NEXP_MAX * 4 <= M_TERMS + NITEM1 * 64 * 4, "probabilities inside the gate/up terms");
+// Wave 0 of the selecting workgroup polls the 256 tagged probabilities, four per lane (experts 4 lane .. + 3, the
+// order the selection reads them), and selects; every other wave of that workgroup stays idle until the picks are out
+// (the selection is a serial chain on one wave, and work beside it slows it).
+constexpr int S_P = M_TERMS;   // select_ds8's scratch (the gate/up terms' space, unused until the picks are known)
+static_assert(S_P + 112 * 4 <= M_TERMS + NITEM1 * 64 * 4, "select_ds8's scratch inside the gate/up terms");
 
-// waves 0-3; returns (wave 0) whether the picks and weights in M_SEL are valid
-__device__ __forceinline__ bool select4(const D1Args & a, lds1_t lds, int wave, LK_LOCAL unsigned * ctl) {
+// returns whether the picks and weights in M_SEL are valid
+__device__ __forceinline__ bool select1(const D1Args & a, lds1_t lds) {
 #pragma clang fp contract(off)
-    const int lane = lane_id(), e = wave * 64 + lane;
-    LK_LOCAL float * ps = reinterpret_cast<LK_LOCAL float *>(lds + S_P);
-    const bool mine = e < a.n_exp;
+    const int lane = lane_id();
     float bv[4];
-    if (wave == 0) { load_bias(a.bias, a.n_exp, bv); }   // issued before the polls: its latency hides behind them
-    uint64_t w = mine ? ld_tag1(a.tlogits + e) : 0;
+    load_bias(a.bias, a.n_exp, bv);   // issued before the polls: its latency hides behind them
+    uint64_t w[4];
+    auto issue = [&]() {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { w[j] = 4 * lane + j < a.n_exp ? ld_tag1(a.tlogits + 4 * lane + j) : 0; }
+    };
+    issue();
     bool ok = false;
     for (int it = 0; it < POLL1; ++it) {
-        if (__ballot(mine && !tag1_ok(w, a.epoch)) == 0) { ok = true; break; }
+        bool v = true;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { v = v && (4 * lane + j >= a.n_exp || tag1_ok(w[j], a.epoch)); }
+        if (__ballot(!v) == 0) { ok = true; break; }
         __builtin_amdgcn_s_sleep(1);
-        if (mine) { w = ld_tag1(a.tlogits + e); }
+        issue();
     }
     TRACE1(3);
-    ps[e] = mine ? det_sigmoid(tag1_val(w)) : 0.f;
-    TRACE1(19);
-    if (!ok) { report1(a, 2); __hip_atomic_store(ctl + C_SELFAIL, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
-    arrive1(ctl + C_SB1, 4);
-    if (wave != 0) { return ok; }
-    ok = wait1(ctl + C_SB1, 4) == 4 && ok;
-    lds_visible();
-    TRACE1(20);
-    ok = ok && __hip_atomic_load(ctl + C_SELFAIL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == 0;
-    if (!ok) { return false; }
-    const f32x4 p4 = *reinterpret_cast<const LK_LOCAL f32x4 *>(ps + 4 * lane);
-    const float pv[4] = {p4[0], p4[1], p4[2], p4[3]};
+    if (!ok) { report1(a, 2); return false; }
+    float pv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { pv[j] = 4 * lane + j < a.n_exp ? tag1_val(w[j]) : 0.f; }
     int * so = (int *) (lds + M_SEL); float * wo = (float *) (lds + M_SEL + MAXK * 4);
     if (a.n_exp == 256 && a.n_group == 8 && a.topk_group == 4) {
-        // DeepSeek's rule as constants: the same function, its divisions, bounds and loop counts folded (about twice
-        // as fast as with the rule read from the arguments)
-        select_token_p<false>(pv, bv, 256, 8, 4, MAXK, a.scale, nullptr, so, wo, MAXK, 0.f);
+        // DeepSeek's rule: the threshold selection, or the same rule as constants (its divisions, bounds and loop
+        // counts folded) for what it leaves
+        TRACE1(22);
+        const bool fast = select_ds8(pv, bv, a.scale, reinterpret_cast<LK_LOCAL uint32_t *>(lds + S_P), so, wo);
+        TRACE1(23);
+        if (!fast) { select_token_p<false>(pv, bv, 256, 8, 4, MAXK, a.scale, nullptr, so, wo, MAXK, 0.f); }
+        TRACE1V(24, fast ? 1 : 2);
     } else {
         select_token_p<false>(pv, bv, a.n_exp, a.n_group, a.topk_group, MAXK, a.scale, nullptr, so, wo, MAXK, 0.f);
     }
@@ -862,10 +865,10 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
         TRACE1(2);
     }
 
-    // 2. selection, two levels: on each XCD one workgroup (li = 0) selects (select4: its four router waves poll the
-    //    logits and form the probabilities, wave 0 selects) and broadcasts the picks and weights through its XCD's L2
-    //    (st_xcd1); the XCD's other workgroups poll that one line. Only 8 workgroups poll the device-wide logits, which
-    //    every router workgroup is writing at the same time.
+    // 2. selection, two levels: on each XCD one workgroup (li = 0) selects (select1: its wave 0 polls the probabilities
+    //    and selects) and broadcasts the picks and weights through its XCD's L2 (st_xcd1); the XCD's other workgroups
+    //    poll that one line. Only 8 workgroups poll the device-wide probabilities, which every router workgroup is
+    //    writing at the same time.
     if (a.ext_sel) {
         // the caller's picks: pick k is slot k (on XCD k); lane 0 also lists the distinct ids in ascending order, each
         // with its weights summed in k order and its first slot, for the combine (zero sums are dropped, as fl_moe does)
@@ -893,11 +896,11 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
             }
             flag1(ctl + C_READY, 1u);
         }
-    } else if (li == 0 && wave < 4) {
+    } else if (li == 0 && wave == 0) {
         __builtin_amdgcn_s_setprio(3);
-        const bool ok = select4(a, lds, wave, ctl);
+        const bool ok = select1(a, lds);
         __builtin_amdgcn_s_setprio(0);
-        if (wave == 0) {
+        {
             lds_visible();
             TRACE1(21);
             if (ok && lane < 16) {

@@ -683,6 +683,79 @@ __device__ __forceinline__ void select_token_p(const float (&p)[4], const float 
     }
     if (kept) { sel_out[rank] = sel_mine; w_out[rank] = rescale ? w_mine * f : w_mine; }
 }
+// DeepSeek's rule (256 experts, 8 groups of 32, 4 groups kept, top 8 kept whole) on one wave, with the same picks in
+// the same order and the same weights as select_token_p, in far fewer dependent steps. The group stage is
+// select_token_p's. Then, instead of 8 rounds of a wave-wide argmax: L = the smallest second-best c of the kept groups.
+// The kept groups' best and second-best are 8 distinct eligible experts with c >= L, so the 8th largest eligible c is
+// at least L and every pick is among the candidates {eligible e : c_e >= L}. The candidates (usually 8-14) are
+// compacted into scr and each is ranked against the others by (c descending, index ascending) -- the rounds' order,
+// ties to the lower index -- which gives pick r = the candidate of rank r. The weights follow as in select_token_p:
+// the sum in pick order, clamped, p / sum * scale. Falls back (returns false, outputs untouched) if some c is NaN (c
+// is never -0: p > 0 or p = +0) or more than 32 candidates remain. scr: 112 words of LDS.
+__device__ __forceinline__ bool select_ds8(const float (&p)[4], const float (&bias)[4], float scale, LK_LOCAL uint32_t * scr,
+                                           int * sel_out, float * w_out) {
+#pragma clang fp contract(off)
+    const int lane = lane_id();
+    float c[4];
+    bool nan = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { c[j] = p[j] + bias[j]; nan = nan || c[j] != c[j]; }
+    if (__ballot(nan)) { return false; }
+    float v1 = -INFINITY, v2 = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { const float v = c[j]; if (v > v1) { v2 = v1; v1 = v; } else if (v > v2) { v2 = v; } }
+    top2_step<DPP_XOR1>(v1, v2); top2_step<DPP_XOR2>(v1, v2); top2_step<DPP_HALF_MIRROR>(v1, v2);   // 8 lanes per group
+    const float mine = v1 + v2;
+    const int gme = lane >> 3;
+    int rank = 0;
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {
+        const float o = __builtin_bit_cast(float, rdlane(__builtin_bit_cast(uint32_t, mine), h * 8));
+        rank += (o > mine || (o == mine && h < gme)) ? 1 : 0;
+    }
+    const bool elig = rank < 4;
+    // L as an ordered key: the minimum over the kept groups of ord_key(v2)
+    const uint32_t lk = ~wave_max_u32(elig ? ~ord_key(v2) : 0u);
+    uint32_t kk[4]; int cand = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { kk[j] = ord_key(c[j]); cand |= (elig && kk[j] >= lk) ? 1 << j : 0; }
+    const uint32_t cnt = (uint32_t) __builtin_popcount(cand), incl = wave_scan_u32(cnt);
+    const int ncand = (int) rdlane(incl, 63);
+    if (ncand < 8 || ncand > 32) { return false; }
+    // compact: candidate i at scr[i] (key), scr[32 + i] (index), scr[64 + i] (p)
+    int at = (int) (incl - cnt);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (cand & (1 << j)) { scr[at] = kk[j]; scr[32 + at] = (uint32_t) (4 * lane + j); scr[64 + at] = __builtin_bit_cast(uint32_t, p[j]); ++at; }
+    }
+    lds_visible();
+    const bool mine_c = lane < ncand;
+    const uint32_t ki = mine_c ? scr[lane] : 0u, ii = mine_c ? scr[32 + lane] : 0u;
+    int rk = 0;
+    for (int t0 = 0; t0 < ncand; t0 += 4) {
+        const u32x4 kt = *reinterpret_cast<const LK_LOCAL u32x4 *>(scr + t0), it = *reinterpret_cast<const LK_LOCAL u32x4 *>(scr + 32 + t0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            rk += (t0 + q < ncand && (kt[q] > ki || (kt[q] == ki && it[q] < ii))) ? 1 : 0;
+        }
+    }
+    lds_visible();   // every lane has read the candidates before the picks overwrite the index words
+    if (mine_c && rk < MAXK) { scr[96 + rk] = ii; scr[104 + rk] = scr[64 + lane]; }
+    lds_visible();
+    const u32x4 s0 = *reinterpret_cast<const LK_LOCAL u32x4 *>(scr + 104), s1 = *reinterpret_cast<const LK_LOCAL u32x4 *>(scr + 108);
+    const uint32_t pb[8] = { s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3] };
+    float sum = 0.f;
+#pragma unroll
+    for (int r = 0; r < MAXK; ++r) { sum = sum + __builtin_bit_cast(float, pb[r]); }
+    sum = sum > 6.103515625e-5f ? sum : 6.103515625e-5f;
+    if (lane < MAXK) {
+        const float pl = __builtin_bit_cast(float, scr[104 + lane]);
+        sel_out[lane] = (int) scr[96 + lane];
+        w_out[lane] = pl / sum * scale;
+    }
+    return true;
+}
+
 // the same from the lane's 4 logits; probs_out (optional) receives the n_exp probabilities
 __device__ __forceinline__ void select_token(const float (&lg)[4], const float (&bias)[4], int n_exp, int n_group, int topk_group, int topk,
                                              float scale, float * scr, int * sel_out, float * w_out, float * probs_out,

@@ -812,3 +812,52 @@ def test_decode1_selection_ties(ctx, pattern):
         assert len(set(so.ravel().tolist())) == 8
     del layer
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("kind", ["continuous", "levels16", "levels3", "hot", "flat"])
+def test_decode1_selection_crafted_logits(ctx, kind):
+    """The one-token kernel's selection (a threshold from the kept groups' second-best scores, then a rank of the
+    candidates, with the round-by-round argmax as the fallback for more than 32 candidates) against the per-pass
+    router (the round-by-round argmax) and the checker, on logits set directly: x = e_0 and router column 0 = the
+    logits, so each logit is W[e, 0] exactly. "levels16" / "levels3" draw the logits and biases from 16 or 3 values
+    (ties in scores, group scores and at the threshold; "levels3" mostly takes the fallback), "hot" adds +0.5 to 16
+    experts, "flat" makes every logit equal (ties decided by index alone)."""
+    import torch
+    from loki_amd import MoeLayerWeights
+    layer = MoeLayerWeights.synthetic(ctx, 7300)
+    W, b = layer.gate_inp, layer.probs_b
+    rng = np.random.default_rng({"continuous": 1, "levels16": 2, "levels3": 3, "hot": 4, "flat": 5}[kind])
+    x = torch.zeros((1, E), dtype=torch.float32, device="cuda")
+    x[0, 0] = 1.0
+    for case in range(6):
+        if kind == "continuous":
+            lg, bias = rng.normal(0, 1.2, NEXP), rng.normal(0, 0.01, NEXP)
+        elif kind == "levels16":
+            lg, bias = rng.integers(-8, 8, NEXP) / 4.0, rng.integers(-2, 3, NEXP) / 64.0
+        elif kind == "levels3":
+            lg, bias = rng.integers(-1, 2, NEXP).astype(np.float64), rng.integers(0, 2, NEXP) / 8.0
+        elif kind == "hot":
+            lg, bias = rng.normal(0, 1.2, NEXP), rng.normal(0, 0.05, NEXP)
+            bias[rng.choice(NEXP, 16, replace=False)] += 0.5
+        else:
+            lg, bias = np.full(NEXP, 0.25), np.zeros(NEXP)
+        Wh = W.cpu().numpy()
+        Wh[:, 0] = lg.astype(np.float32)
+        W.copy_(torch.from_numpy(Wh))
+        b.copy_(torch.from_numpy(bias.astype(np.float32)))
+        torch.cuda.synchronize()
+        got = {}
+        for name, m in (("decode1", 2), ("per_pass", 0)):
+            with ctx.using_fused(m):
+                ctx.moe_layer(layer, x)
+                ctx.sync()
+                assert ctx.debug().kernel == {"decode1": 2, "per_pass": 0}[name]
+                st = _routing_state(ctx, 1)
+                got[name] = (st["sel"], st["wts"])
+        assert np.array_equal(got["decode1"][0], got["per_pass"][0]), (kind, case)
+        assert np.array_equal(got["decode1"][1].view(np.uint32), got["per_pass"][1].view(np.uint32)), (kind, case)
+        _, _, so, wo = orc.router(W.cpu().numpy(), b.cpu().numpy(), x.cpu().numpy())
+        assert np.array_equal(got["decode1"][0], so.ravel().astype(np.int32)), (kind, case)
+        assert np.array_equal(got["decode1"][1].view(np.uint32), wo.ravel().view(np.uint32)), (kind, case)
+    del layer
+    torch.cuda.empty_cache()
