@@ -19,25 +19,31 @@
 using namespace lk;
 
 // ---------------------------------------------------------------- declared tiled ranges
+// The registry is created on first use and never destroyed: the library registers no exit-time destructor of its own,
+// so process exit runs nothing of it but the HIP runtime's module unregistration (a destructor here would run from
+// __cxa_finalize, interleaved with whatever teardown the runtime or a profiler's preloaded tool does at exit).
 namespace {
-std::mutex g_tiled_mu;
-std::vector<std::pair<uintptr_t, uintptr_t>> g_tiled;   // [begin, end)
+std::mutex g_tiled_mu;   // trivially destructible
+std::vector<std::pair<uintptr_t, uintptr_t>> & g_tiled() {   // [begin, end)
+    static auto * v = new std::vector<std::pair<uintptr_t, uintptr_t>>();
+    return *v;
+}
 }
 void tiled_add(const void * p, size_t bytes) {
     std::lock_guard<std::mutex> lk(g_tiled_mu);
-    g_tiled.emplace_back((uintptr_t) p, (uintptr_t) p + bytes);
+    g_tiled().emplace_back((uintptr_t) p, (uintptr_t) p + bytes);
 }
 void tiled_remove_within(const void * p, size_t bytes) {
     const uintptr_t b = (uintptr_t) p, e = b + bytes;
     std::lock_guard<std::mutex> lk(g_tiled_mu);
     std::vector<std::pair<uintptr_t, uintptr_t>> keep;
-    for (const auto & r : g_tiled) { if (r.first < b || r.second > e) { keep.push_back(r); } }
-    g_tiled.swap(keep);
+    for (const auto & r : g_tiled()) { if (r.first < b || r.second > e) { keep.push_back(r); } }
+    g_tiled().swap(keep);
 }
 bool tiled_holds(const void * p, size_t bytes) {
     const uintptr_t b = (uintptr_t) p, e = b + bytes;
     std::lock_guard<std::mutex> lk(g_tiled_mu);
-    for (const auto & r : g_tiled) { if (r.first <= b && e <= r.second) { return true; } }
+    for (const auto & r : g_tiled()) { if (r.first <= b && e <= r.second) { return true; } }
     return false;
 }
 extern "C" int fl_register_tiled(FLCtx * c, const void * base, size_t bytes) {
