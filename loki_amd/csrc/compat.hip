@@ -326,7 +326,7 @@ static void shared_expert(FLCtx * c, Compat * s, const int8_t * xq, const float 
     if (gu_gemm || dn_gemm) {
         CK(prefill_ready(c) == FL_OK ? hipSuccess : hipErrorOutOfMemory);
         // ceil(N / 64) shared columns (wide_base runs every row of a wide pass here, so N is not bounded by 64)
-        FALLOC(s->pcols, (size_t) prefill_shared_cols(N) + NEXP_MAX + 2); FALLOC(s->pncols, 1);
+        FALLOC(s->pcols, (size_t) prefill_shared_cols(N) + NEXP_MAX + 2); FALLOC(s->pncols, PF_NCOLS);
         FCK(launch_prefill_cols(zero_int(c), zero_int(c), zero_int(c), N, 0, s->pcols.p, s->pncols.p, c->st));   // no routed columns
         g.ptab = c->ptab.p; g.perm = zero_int(c); g.topk = 1; g.P = 0; g.cols = s->pcols.p; g.ncols = s->pncols.p;
         g.err = c->derr.p; g.herr = c->herr ? c->herr_dev : nullptr;
@@ -422,7 +422,7 @@ static void routed_experts(FLCtx * c, Compat * s, const Arena & ar, const int8_t
         CK(prefill_ready(c) == FL_OK ? hipSuccess : hipErrorOutOfMemory);
         hipStream_t st = c->st;
         FALLOC(s->xh, (size_t) n * E_); FALLOC(s->hh, (size_t) P * H_);
-        FALLOC(s->pcols, (size_t) P / 32 + NEXP_MAX + 2); FALLOC(s->pncols, 1);
+        FALLOC(s->pcols, (size_t) P / 32 + NEXP_MAX + 2); FALLOC(s->pncols, PF_NCOLS);
         FCK(launch_q8_to_h(xq, s->xh.p, (int64_t) n * E_, st));
         FCK(launch_prefill_cols(act, nact, offsets, 0, P, s->pcols.p, s->pncols.p, st));
         PrefillArgs g{};

@@ -574,7 +574,7 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     if (mfma) {
         if (int rc = prefill_ready(c)) { return rc; }
         ALLOC(c, c->xh, (size_t) n * E); ALLOC(c, c->hh, rows * H);
-        ALLOC(c, c->pcols, rows / 32 + NEXP_MAX + 2); ALLOC(c, c->pncols, 1);
+        ALLOC(c, c->pcols, rows / 32 + NEXP_MAX + 2); ALLOC(c, c->pncols, PF_NCOLS);
     }
     prof_mark(c, ev, 0);
     if (prenorm) {   // the per-pass path normalises into a context buffer first (k_rmsnorm: the same arithmetic)

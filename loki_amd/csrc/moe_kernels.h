@@ -141,6 +141,7 @@ size_t prefill_table_bytes();
 hipError_t build_prefill_tables(uint4 * img, hipStream_t st);
 // columns of <= 64 slots (PF_TOK) of one expert: the shared expert's ceil(n / 64) first, then act order; cols sized
 // >= prefill_shared_cols(n) + P / 64 + NEXP_MAX + 2
+constexpr int PF_NCOLS = 4;   // the counts launch_prefill_cols writes (ncols[0] = all columns; the class boundaries)
 hipError_t launch_prefill_cols(const int * act, const int * nact, const int * offsets, int n, int P, int4 * cols, int * ncols, hipStream_t st);
 int prefill_shared_cols(int n);   // the shared expert's columns (the first ones) for n tokens
 hipError_t launch_q8_to_h(const int8_t * q, _Float16 * h, int64_t n, hipStream_t st);

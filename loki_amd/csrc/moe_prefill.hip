@@ -33,17 +33,15 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int PF_W = 8, PF_NT = PF_W * 64;   // waves / threads per workgroup (two per SIMD: each hides the other's latency)
 constexpr int PF_NTM = 4;                    // 16-token MFMA tiles per column at most
 constexpr int PF_TOK = 16 * PF_NTM;          // slots per column: the dequantised weights of an item serve all of them
 // LDS: fp16 codebook (256 lines x 16 copies x 16 B), fp16 sign masks (128 lines, the 7 stored sign bits), then two
-// activation buffers (64 token rows x 512 B, each row's 16-byte chunks XOR-swizzled by the row): exactly 160 KB. The
-// tokens' block scales stay in registers (one per lane, handed to the lanes that fold them by ds_bpermute).
+// activation buffers (up to 64 token rows x 512 B, each row's 16-byte chunks XOR-swizzled by the row; the wide kernel's
+// fill the 160 KB exactly), then (narrow gate/up) the exchange of g. The tokens' block scales stay in registers (one per
+// lane, handed to the lanes that fold them by ds_bpermute).
 constexpr int L_PG = 0, L_PS = 65536, L_PB = L_PS + 128 * 256;
-constexpr int PB_TILE = 16 * 512, PB_BUF = PF_NTM * PB_TILE;   // buffers 512-byte aligned
-constexpr int PF_LDS = L_PB + 2 * PB_BUF;
+constexpr int PB_TILE = 16 * 512;            // one 16-token tile of a buffer (512-byte aligned)
 constexpr int PTAB_BYTES = L_PB;             // the table image copied to LDS offset 0
-static_assert(PF_LDS <= 160 * 1024, "LDS budget");
 
 // fp16 table image: line e of the codebook = 16 copies of the 8 fp16 values of grid[e]; line b of the signs = 16
 // copies of 8 fp16 sign masks (0x8000 for a negative weight) of the stored sign bits b (0..127) plus parity
@@ -68,26 +66,34 @@ hipError_t build_prefill_tables(uint4 * img, hipStream_t st) {
 }
 size_t prefill_table_bytes() { return PTAB_BYTES; }
 
-// columns: the shared expert's slots first (P + 64 c ..), then every active expert's slots in act order, 64 per column
+// Columns: the shared expert's slots first (P + 64 c ..), then every active expert's slots, 64 per column. A column of
+// at most 32 slots is narrow (the narrow GEMM takes it), every other one wide; only an expert's last column can be
+// narrow. Order: the shared expert's columns (its last one the only narrow one), then the routed wide columns in act
+// order, then the routed narrow columns in act order, so each class is at most two runs: ncols[0] = all columns,
+// ncols[1] = the shared wide columns, ncols[2] = the shared columns, ncols[3] = the end of the routed wide ones.
 __global__ void __launch_bounds__(256) k_pf_cols(const int * __restrict__ act, const int * __restrict__ nact_p, const int * __restrict__ offsets,
                                                 int n, int P, int4 * __restrict__ cols, int * __restrict__ ncols) {
-    __shared__ int scan[256];
+    __shared__ int scw[256], scn[256];
     const int i = threadIdx.x, nact = *nact_p, nsh = (n + PF_TOK - 1) / PF_TOK;
     int e = 0, s0 = 0, cnt = 0;
     if (i < nact) { e = act[i]; s0 = offsets[e]; cnt = offsets[e + 1] - s0; }
-    const int nc = (cnt + PF_TOK - 1) / PF_TOK;
-    scan[i] = nc;
+    const int rem = cnt % PF_TOK, nw = cnt / PF_TOK + (rem > PF_TOK / 2 ? 1 : 0), nn = rem > 0 && rem <= PF_TOK / 2 ? 1 : 0;
+    scw[i] = nw; scn[i] = nn;
     __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {   // inclusive scan
-        const int v = i >= off ? scan[i - off] : 0;
+    for (int off = 1; off < 256; off <<= 1) {   // inclusive scans
+        const int vw = i >= off ? scw[i - off] : 0, vn = i >= off ? scn[i - off] : 0;
         __syncthreads();
-        scan[i] += v;
+        scw[i] += vw; scn[i] += vn;
         __syncthreads();
     }
-    const int base = nsh + scan[i] - nc;
-    for (int c = 0; c < nc; ++c) { cols[base + c] = make_int4(i, s0 + PF_TOK * c, min(PF_TOK, cnt - PF_TOK * c), e); }
+    const int tw = scw[255], bw = nsh + scw[i] - nw, bn = nsh + tw + scn[i] - nn;
+    for (int c = 0; c < nw; ++c) { cols[bw + c] = make_int4(i, s0 + PF_TOK * c, min(PF_TOK, cnt - PF_TOK * c), e); }
+    if (nn) { cols[bn] = make_int4(i, s0 + cnt - rem, rem, e); }
     for (int c = i; c < nsh; c += 256) { cols[c] = make_int4(-1, P + PF_TOK * c, min(PF_TOK, n - PF_TOK * c), 0); }
-    if (i == 255) { *ncols = nsh + scan[255]; }
+    if (i == 255) {
+        const int rs = n % PF_TOK;
+        ncols[0] = nsh + tw + scn[255]; ncols[1] = nsh - (rs > 0 && rs <= PF_TOK / 2 ? 1 : 0); ncols[2] = nsh; ncols[3] = nsh + tw;
+    }
 }
 int prefill_shared_cols(int n) { return (n + PF_TOK - 1) / PF_TOK; }
 hipError_t launch_prefill_cols(const int * act, const int * nact, const int * offsets, int n, int P, int4 * cols, int * ncols, hipStream_t st) {
@@ -114,10 +120,26 @@ hipError_t launch_q8_to_h(const int8_t * q, _Float16 * h, int64_t n, hipStream_t
 
 // ---------------------------------------------------------------- the grouped GEMM
 // NMAT = 2: gate/up (K = 7168, rows 2048, B rows = tokens, writes h); NMAT = 1: down (K = 2048, rows 7168, B rows =
-// slots, writes o). RGI 16-row tiles per wave: combos = NMAT * RGI = 2 dequantised tiles per block either way.
-template <int NMAT, int RGI, int NB>
+// slots, writes o). Two kernels take the columns of launch_prefill_cols by class:
+//   * wide (W = 8 waves, CPW = 2 16-row tiles per wave, columns of 33-64 slots, up to 4 token tiles): a wave's tiles
+//     are the gate and up rows of one 16-row tile (gate/up: h forms in registers) or two row tiles (down);
+//   * narrow (W = 16 waves, CPW = 1, columns of at most 32 slots, up to 2 token tiles): about half the registers per
+//     wave, so four waves share a SIMD and hide more of the LDS read -> dequantise -> MFMA chain; gate/up hands g to
+//     the up waves through LDS.
+// Either way an item is (column, row group) and every output is computed once, in the same arithmetic.
+template <int NMAT, int NB, int W, int CPW>
 struct PfGeo {
-    static constexpr int COMBOS = NMAT * RGI, ROWS = PF_W * 16 * RGI, K = NB * QK;
+    static constexpr bool NARROW = CPW == 1;
+    static constexpr int NTM = NARROW ? 2 : PF_NTM;             // token tiles per column at most
+    static constexpr int TPM = W * CPW / NMAT;                  // 16-row tiles per matrix in an item
+    static constexpr int ROWS = TPM * 16, K = NB * QK, NTH = W * 64;
+    static constexpr int BUF = NTM * PB_TILE;                   // one activation buffer
+    static constexpr int L_G = L_PB + 2 * BUF;                  // narrow gate/up: g of the gate waves [8][64 lanes][2 tiles][4]
+    static constexpr int LDS = L_G + (NARROW && NMAT == 2 ? 8 * 64 * NTM * 16 : 0);
+    static_assert(LDS <= 160 * 1024 && W * CPW % NMAT == 0, "prefill GEMM geometry");
+    // the matrix and the 16-row tile (within the item) of combo c of wave w
+    __device__ static constexpr int mat(int w, int c) { return CPW == NMAT ? c : NMAT == 1 ? 0 : w / (W / NMAT); }
+    __device__ static constexpr int tile(int w, int c) { return CPW == NMAT ? w : NMAT == 1 ? w * CPW + c : w % (W / NMAT); }
 };
 
 struct PfLane {
@@ -156,11 +178,32 @@ __device__ __forceinline__ void dma16(const void * src, LK_LOCAL uint8_t * dst) 
     __builtin_amdgcn_global_load_lds((const LK_GLOBAL void *) src, (LK_LOCAL void *) dst, 16, 0, 0);
 }
 
-template <int NMAT, int RGI, int NB>
-__global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
+// the columns of one class inside [col0, col1): two runs [a0, a1) and [b0, b1) of the column table (k_pf_cols' order)
+struct PfRuns {
+    int a0, na, b0, nb;
+    __device__ int count() const { return na + nb; }
+    __device__ int col(int j) const { return j < na ? a0 + j : b0 + (j - na); }
+};
+__device__ __forceinline__ int pf_clip(int lo, int hi, int c0, int c1, int & start) {
+    start = lo > c0 ? lo : c0;
+    const int end = hi < c1 ? hi : c1;
+    return end > start ? end - start : 0;
+}
+template <bool NARROW>
+__device__ __forceinline__ PfRuns pf_runs(const PrefillArgs & a) {
+    const int total = gptr(a.ncols)[0], shw = gptr(a.ncols)[1], sh = gptr(a.ncols)[2], rw = gptr(a.ncols)[3];
+    const int c0 = a.col0, c1 = a.col1 > 0 ? a.col1 : total;
+    PfRuns r;
+    if (NARROW) { r.na = pf_clip(shw, sh, c0, c1, r.a0); r.nb = pf_clip(rw, total, c0, c1, r.b0); }
+    else { r.na = pf_clip(0, shw, c0, c1, r.a0); r.nb = pf_clip(sh, rw, c0, c1, r.b0); }
+    return r;
+}
+
+template <int NMAT, int NB, int W, int CPW>
+__global__ void __launch_bounds__(W * 64, 1) k_pf_gemm(const PrefillArgs a) {
 #pragma clang fp contract(off)
-    using Geo = PfGeo<NMAT, RGI, NB>;
-    constexpr int C = Geo::COMBOS;
+    using Geo = PfGeo<NMAT, NB, W, CPW>;
+    constexpr int C = CPW;
     extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds[];
     LK_LOCAL uint8_t * lds = (LK_LOCAL uint8_t *) dyn_lds;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
@@ -172,24 +215,24 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
         return;
     }
     // tables into LDS (direct loads), visible after vmcnt(0) + the first barrier
-    for (int c = wave; c < PTAB_BYTES / 1024; c += PF_W) { dma16(a.ptab + c * 64 + lane, lds + c * 1024); }
+    for (int c = wave; c < PTAB_BYTES / 1024; c += W) { dma16(a.ptab + c * 64 + lane, lds + c * 1024); }
     PfLane ln;
     ln.r = lane & 15; ln.g = lane >> 4;
     ln.trg = (uint32_t) L_PG | ((uint32_t) ln.r << 4);
     ln.trs = (uint32_t) L_PS | ((uint32_t) ln.r << 4);
-    const int col0 = a.col0, ncols = (a.col1 > 0 ? a.col1 : *gptr(a.ncols)) - col0;
+    const PfRuns runs = pf_runs<Geo::NARROW>(a);
     const int nrg = a.R / Geo::ROWS;
     const size_t dreg = (size_t) (a.R / 64) * NB * 4096;   // d region offset of a tiled matrix
     __builtin_amdgcn_s_waitcnt(0x0f70);
     __syncthreads();
 
-    for (int it = blockIdx.x; it < ncols * nrg; it += gridDim.x) {
-        const int col = col0 + it / nrg, rg = it % nrg;
+    for (int it = blockIdx.x; it < runs.count() * nrg; it += gridDim.x) {
+        const int col = runs.col(it / nrg), rg = it % nrg;
         const u32x4 cv = *(const LK_GLOBAL u32x4 *) (a.cols + col);
         const int4 cd = make_int4((int) cv.x, (int) cv.y, (int) cv.z, (int) cv.w);
         const bool routed = cd.x >= 0;
         const int sb = cd.y, sc = cd.z;
-        // B rows of this wave's copy instructions: rows 4 w + {0,1} (instruction 0) and 4 w + {2,3} (1), lane half L >> 5
+        // B rows of the copy instructions: instruction i copies rows 2 i and 2 i + 1 (lane half L >> 5)
         auto brow = [&](int n32) -> int {
             const int s = sb + (n32 < sc ? n32 : 0);
             return NMAT == 2 ? (routed ? gptr(a.perm)[s] / a.topk : s - a.P) : s;
@@ -198,17 +241,17 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
         // so no 64-bit per-lane address lives in vector registers.
         const __amdgpu_buffer_rsrc_t rb = pf_rsrc(a.bh), rd = pf_rsrc(a.bd);
         const uint32_t oX = (uint32_t) brow(lane) * (NB * 4);   // lane n loads the scale of token n of the column
-        // the wave's tiles: combo c = (matrix c / RGI, 16-row tile c % RGI): scalar resources at the tile's qs / d
+        // the wave's tiles: combo c = (matrix Geo::mat, 16-row tile Geo::tile): scalar resources at the tile's qs / d
         // bases, the lane's offset (chunk g of row r) in one vector register
         __amdgpu_buffer_rsrc_t uq[C], ud[C];
 #pragma unroll
         for (int c = 0; c < C; ++c) {
-            const int mat = c / RGI, ti = c % RGI;
-            const uint8_t * W = routed ? a.w[mat] + (size_t) cd.w * a.estride : a.sh[mat];
-            const int row0 = rg * Geo::ROWS + (wave * RGI + ti) * 16;   // a 16-row tile lies inside one 64-row group
+            const int mat = Geo::mat(wave, c), ti = Geo::tile(wave, c);
+            const uint8_t * Wm = routed ? a.w[mat] + (size_t) cd.w * a.estride : a.sh[mat];
+            const int row0 = rg * Geo::ROWS + ti * 16;   // a 16-row tile lies inside one 64-row group
             const int g64 = row0 >> 6, r0 = row0 & 63;
-            uq[c] = pf_rsrc(pf_uniform(W + (size_t) g64 * NB * 4096 + r0 * 16));
-            ud[c] = pf_rsrc(pf_uniform(W + dreg + (size_t) g64 * NB * 128 + r0 * 2));
+            uq[c] = pf_rsrc(pf_uniform(Wm + (size_t) g64 * NB * 4096 + r0 * 16));
+            ud[c] = pf_rsrc(pf_uniform(Wm + dreg + (size_t) g64 * NB * 128 + r0 * 2));
         }
         const uint32_t lq = (uint32_t) ln.g * 1024 + (uint32_t) ln.r * 16, ldo = (uint32_t) ln.r * 2;
         auto load_w = [&](int j, PfW (&w)[C]) {
@@ -221,23 +264,23 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
         auto run_item = [&](auto ntc) {
             constexpr int NT = decltype(ntc)::value;   // token tiles of the column (1, 2 or 4)
             // the column's activations of block j go straight from memory into LDS buffer j % 2 (buffer loads to LDS:
-            // lane L's 16 bytes land at L * 16 of the instruction's 1 KB, no registers): wave w copies token rows
-            // RW w + 2 i + (lane / 32), i < RW / 2 (RW = 16 NT / PF_W rows per wave), lane L < 32 of a row taking the
-            // row's chunk pf_swz(L ^ (row % 16)) -- the swizzle applied on the memory side. Lane n also loads token
-            // n's block scale into a register.
-            constexpr int RW = 16 * NT / PF_W, NI = RW / 2;
+            // lane L's 16 bytes land at L * 16 of the instruction's 1 KB, no registers): copy instruction i covers token
+            // rows 2 i + (lane / 32), i < 8 NT, taken by waves i % W; lane L < 32 of a row takes the row's chunk
+            // pf_swz(L ^ (row % 16)) -- the swizzle applied on the memory side. Lane n also loads token n's block scale
+            // into a register.
+            constexpr int NI = (8 * NT + W - 1) / W;   // copy instructions per wave (some waves of the narrow kernel none)
             struct PfB { float dx; };
             uint32_t ob[NI];
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
-                const int row = RW * wave + 2 * i + (lane >> 5);
-                ob[i] = (uint32_t) brow(row) * (Geo::K * 2) + pf_swz((uint32_t) ((lane & 31) ^ (row & 15))) * 16;
+                const int row = 2 * (wave + W * i) + (lane >> 5);
+                ob[i] = (uint32_t) brow(row < 16 * NT ? row : 0) * (Geo::K * 2) + pf_swz((uint32_t) ((lane & 31) ^ (row & 15))) * 16;
             }
             auto load_b = [&](int j, PfB & bq, int buf) {
-                LK_LOCAL uint8_t * dst = lds + L_PB + buf * PB_BUF;
+                LK_LOCAL uint8_t * dst = lds + L_PB + buf * Geo::BUF;
 #pragma unroll
                 for (int i = 0; i < NI; ++i) {
-                    buf_lds16(rb, dst + (RW * wave + 2 * i) * 512, ob[i], j * (QK * 2));
+                    if (wave + W * i < 8 * NT) { buf_lds16(rb, dst + 2 * (wave + W * i) * 512, ob[i], j * (QK * 2)); }
                 }
                 bq.dx = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, oX, j * 4, 0));
             };
@@ -245,10 +288,10 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
 #pragma unroll
             for (int c = 0; c < C; ++c) { for (int tt = 0; tt < NT; ++tt) { acc[c][tt] = (f4) { 0.f, 0.f, 0.f, 0.f }; } }
 
-            // one block: dequantise the C tiles step by step and run the MFMA chains of both token tiles
+            // one block: dequantise the C tiles step by step and run the MFMA chains of the token tiles
             auto block = [&](int j, const PfW (&w)[C], int buf, float dxl) {
-                static_assert((L_PB % 512) == 0 && (PB_BUF % 512) == 0, "XOR addressing inside 512-byte rows");
-                const uint32_t bx = ((uint32_t) (L_PB + buf * PB_BUF) + (uint32_t) ln.r * 512) | ((uint32_t) ((8 * pf_swz2(ln.g)) ^ ln.r) << 4);
+                static_assert((L_PB % 512) == 0 && (Geo::BUF % 512) == 0, "XOR addressing inside 512-byte rows");
+                const uint32_t bx = ((uint32_t) (L_PB + buf * Geo::BUF) + (uint32_t) ln.r * 512) | ((uint32_t) ((8 * pf_swz2(ln.g)) ^ ln.r) << 4);
                 f4 cc[C][NT], cd[C][NT];   // the two exact chains: steps 0-3, steps 4-7
                 h2v sc[C][2];
                 uint32_t ms[C][2];
@@ -258,7 +301,7 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
                     sc[c][0] = (h2v) { s0, s0 }; sc[c][1] = (h2v) { s1, s1 };
                     ms[c][0] = w[c].q.y & 0x7f7f7f7fu; ms[c][1] = w[c].q.w & 0x7f7f7f7fu;
                 }
-                // step t's LDS reads (two activation chunks, per tile a codebook and a sign entry) are issued one step
+                // step t's LDS reads (the activation chunks, per tile a codebook and a sign entry) are issued one step
                 // ahead of their use, into the other of two register sets
                 struct Lk { u32x4 g[C], s[C]; h8 x[NT]; };
                 auto lookup = [&](int t, Lk & k) {
@@ -340,7 +383,7 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
             // copies land in registers nobody reads any more), so the compiler's waits count them exactly.
             // short rows (down, 8 blocks) and items of many tiles keep the weights one block ahead (two stages): their
             // register budget is tighter
-            constexpr int WA = (NB <= 8 || C * NT > 4) ? 1 : 2;
+            constexpr int WA = (NB <= 8 || C * NT > 4 || Geo::NARROW) ? 1 : 2;   // narrow: four waves per SIMD hide it instead
             PfW w0[C], w1[C], w2[C];
             PfB bq;
             load_w(0, w0);
@@ -376,52 +419,95 @@ __global__ void __launch_bounds__(PF_NT, 1) k_pf_gemm(const PrefillArgs a) {
             }
 
             // outputs: lane (r, g) holds tokens 4 g + i of each token tile for row r of each of its tiles
+            if constexpr (NMAT == 2 && C == 1) {
+                // narrow gate/up: the gate waves (0..7) leave 0.125 g in LDS, the up waves (8..15) form h for the same
+                // tile. The exchange area is last read in this item; the next item's first barrier orders its reuse.
+                LK_LOCAL float * xg = reinterpret_cast<LK_LOCAL float *>(lds + Geo::L_G);
+                const int ti = Geo::tile(wave, 0);
+                if (Geo::mat(wave, 0) == 0) {
 #pragma unroll
-            for (int ti = 0; ti < RGI; ++ti) {
-                const int row = rg * Geo::ROWS + (wave * RGI + ti) * 16 + ln.r;
+                    for (int tt = 0; tt < NT; ++tt) {
 #pragma unroll
-                for (int tt = 0; tt < NT; ++tt) {
+                        for (int i = 0; i < 4; ++i) { xg[((ti * 64 + lane) * Geo::NTM + tt) * 4 + i] = 0.125f * acc[0][tt][i]; }
+                    }
+                }
+                __syncthreads();
+                if (Geo::mat(wave, 0) == 1) {
+                    const int row = rg * Geo::ROWS + ti * 16 + ln.r;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int n32 = 16 * tt + 4 * ln.g + i;
-                        if (n32 < sc) {
-                            const size_t o = (size_t) (sb + n32) * a.R + row;
-                            if (NMAT == 2) {
-                                const float gv = 0.125f * acc[ti][tt][i], uv = 0.125f * acc[RGI + ti][tt][i];
+                    for (int tt = 0; tt < NT; ++tt) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int n32 = 16 * tt + 4 * ln.g + i;
+                            if (n32 < sc) {
+                                const size_t o = (size_t) (sb + n32) * a.R + row;
+                                const float gv = xg[((ti * 64 + lane) * Geo::NTM + tt) * 4 + i], uv = 0.125f * acc[0][tt][i];
                                 a.out[o] = det_silu(gv) * uv;
                                 if (a.gdbg) { a.gdbg[o] = gv; a.udbg[o] = uv; }
-                            } else {
-                                a.out[o] = 0.125f * acc[ti][tt][i];
+                            }
+                        }
+                    }
+                }
+            } else {
+                constexpr int RT = NMAT == 2 ? 1 : C;   // row tiles of the wave (gate/up wide: one, both matrices)
+#pragma unroll
+                for (int c = 0; c < RT; ++c) {
+                    const int row = rg * Geo::ROWS + Geo::tile(wave, c) * 16 + ln.r;
+#pragma unroll
+                    for (int tt = 0; tt < NT; ++tt) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int n32 = 16 * tt + 4 * ln.g + i;
+                            if (n32 < sc) {
+                                const size_t o = (size_t) (sb + n32) * a.R + row;
+                                if (NMAT == 2) {
+                                    const float gv = 0.125f * acc[0][tt][i], uv = 0.125f * acc[1][tt][i];
+                                    a.out[o] = det_silu(gv) * uv;
+                                    if (a.gdbg) { a.gdbg[o] = gv; a.udbg[o] = uv; }
+                                } else {
+                                    a.out[o] = 0.125f * acc[c][tt][i];
+                                }
                             }
                         }
                     }
                 }
             }
         };
-        if (sc > 32) { run_item(std::integral_constant<int, 4>{}); }
-        else if (sc > 16) { run_item(std::integral_constant<int, 2>{}); }
-        else { run_item(std::integral_constant<int, 1>{}); }
+        if constexpr (Geo::NARROW) {
+            if (sc > 16) { run_item(std::integral_constant<int, 2>{}); }
+            else { run_item(std::integral_constant<int, 1>{}); }
+        } else {
+            run_item(std::integral_constant<int, 4>{});   // a wide column: 33..64 slots
+        }
     }
 }
 
-template <int NMAT, int RGI, int NB>
+template <int NMAT, int NB, int W, int CPW>
 static hipError_t pf_setup() {
-    return hipFuncSetAttribute((const void *) k_pf_gemm<NMAT, RGI, NB>, hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS);
+    return hipFuncSetAttribute((const void *) k_pf_gemm<NMAT, NB, W, CPW>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               PfGeo<NMAT, NB, W, CPW>::LDS);
 }
 hipError_t prefill_init() {
-    hipError_t e = pf_setup<2, 1, 28>();
-    if (e == hipSuccess) { e = pf_setup<1, 2, 8>(); }
+    hipError_t e = pf_setup<2, 28, 8, 2>();
+    if (e == hipSuccess) { e = pf_setup<1, 8, 8, 2>(); }
+    if (e == hipSuccess) { e = pf_setup<2, 28, 16, 1>(); }
+    if (e == hipSuccess) { e = pf_setup<1, 8, 16, 1>(); }
     return e;
 }
 
+// the wide kernel, then the narrow one, over the columns col0 .. col1 - 1 (each takes its class)
 hipError_t launch_prefill_gemm(const PrefillArgs & a, int grid, hipStream_t st) {
     if (grid < 1 || !a.ptab || !a.cols || !a.ncols || !a.bh || !a.bd || !a.out || !a.err) { return hipErrorInvalidValue; }
     if (a.nmat == 2) {
-        if (a.K != 28 * QK || a.R % PfGeo<2, 1, 28>::ROWS || !a.w[0] || !a.w[1] || !a.sh[0] || !a.sh[1] || !a.perm) { return hipErrorInvalidValue; }
-        k_pf_gemm<2, 1, 28><<<grid, PF_NT, PF_LDS, st>>>(a);
+        if (a.K != 28 * QK || a.R % PfGeo<2, 28, 8, 2>::ROWS || a.R % PfGeo<2, 28, 16, 1>::ROWS || !a.w[0] || !a.w[1] || !a.sh[0] || !a.sh[1] || !a.perm) {
+            return hipErrorInvalidValue;
+        }
+        k_pf_gemm<2, 28, 8, 2><<<grid, 8 * 64, PfGeo<2, 28, 8, 2>::LDS, st>>>(a);
+        k_pf_gemm<2, 28, 16, 1><<<grid, 16 * 64, PfGeo<2, 28, 16, 1>::LDS, st>>>(a);
     } else if (a.nmat == 1) {
-        if (a.K != 8 * QK || a.R % PfGeo<1, 2, 8>::ROWS || !a.w[0] || !a.sh[0]) { return hipErrorInvalidValue; }
-        k_pf_gemm<1, 2, 8><<<grid, PF_NT, PF_LDS, st>>>(a);
+        if (a.K != 8 * QK || a.R % PfGeo<1, 8, 8, 2>::ROWS || a.R % PfGeo<1, 8, 16, 1>::ROWS || !a.w[0] || !a.sh[0]) { return hipErrorInvalidValue; }
+        k_pf_gemm<1, 8, 8, 2><<<grid, 8 * 64, PfGeo<1, 8, 8, 2>::LDS, st>>>(a);
+        k_pf_gemm<1, 8, 16, 1><<<grid, 16 * 64, PfGeo<1, 8, 16, 1>::LDS, st>>>(a);
     } else {
         return hipErrorInvalidValue;
     }
