@@ -83,7 +83,11 @@ int fl_h2d_bytes(FLCtx *, size_t * by_kernel, size_t * by_copy_engine);
  * Router + shared expert on N rows (N <= 64 per call; wrow >= 0 places them at rows wrow.. of a wide pass), given the
  * ffn-normed rows ncur and the residual ffn_inp as host floats [N][7168] (the reference computes both inside fl_attn,
  * src/fused_layer.cu:498-525). Uses W->gate_inp (F32 [256][7168], or F16 with W->gate_f16), W->probs_b,
- * W->sh_gate/up/down (ggml layout, formats of fl_set_shared_formats). */
+ * W->sh_gate/up/down (ggml layout, formats of fl_set_shared_formats).
+ * One row after an fl_moe that ran on the routing's own picks over an arena declared with fl_register_tiled (a resident
+ * arena, ids = expert ids): this call also runs that fl_moe's block on its own picks in the same launch as the routing
+ * (speculatively; its outputs are used only by an fl_moe with exactly those ids, weights and arena pointers, which then
+ * just waits for it -- FLDebug.kernel 3 -- and any other call runs as usual). Its time counts as fl_gpu_ms(1). */
 int fl_ffn_begin(FLCtx *, const FLW * W, int N, const float * ncur, const float * ffn_inp, int wrow);
 /* formats of W->sh_gate / sh_up / sh_down for fl_ffn_begin: FL_IQ2 (default, the all-IQ2_XXS configs) or K-quants;
  * the reference's shards are (FL_Q5K, FL_Q5K, FL_Q6K) (src/fused_layer.h:14; FLW carries no format). gate and up are
@@ -239,7 +243,8 @@ typedef struct FLDebug {
     int fused;                                         /* 1: the last call ran as the single-launch decode block, which
                                                         * keeps h and o internal (h .. u are NULL then) */
     int kernel;                                        /* the last call's decode launch: 0 none (per-pass or wide path),
-                                                        * 1 the general block, 2 the one-token block organised by XCD */
+                                                        * 1 the general block, 2 the one-token block organised by XCD,
+                                                        * 3 that block launched by fl_ffn_begin on its own picks (fl_moe) */
 } FLDebug;
 int fl_debug(FLCtx *, FLDebug * out);
 int fl_set_debug(FLCtx *, int capture_gate_up);

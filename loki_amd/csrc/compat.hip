@@ -65,6 +65,7 @@ constexpr int RMAX = 64;           // rows per fl_ffn_begin call (the reference'
 constexpr int NB = 8;              // rows of a narrow pass (src/fused_layer.cu:18)
 constexpr int E_ = 7168, H_ = 2048, NEXP_ = 256;
 constexpr int ZS_DONE = 2 * RMAX * MAXK + 16;   // the routing's done word in z_sel (its own cache line)
+constexpr int ZS_FDONE = ZS_DONE + 1;           // fl_moe's one-token launch's completion word
 
 template <class T> T * pinned(size_t n) {
     void * p = nullptr;
@@ -224,6 +225,14 @@ struct Compat {
     // and its h rows then (at NB * E) moe rows (z_out); *_d = the device addresses. r_tagged: the last fl_ffn_begin's routing sets the done word, to rtag
     int * z_sel = nullptr, * z_sel_d = nullptr, * z_in = nullptr, * z_in_d = nullptr; float * z_out = nullptr, * z_out_d = nullptr;
     unsigned rtag = 0; bool r_tagged = false;
+    // fl_moe's one-token launch signals its end in z_sel[ZS_FDONE] (fcnt: its workgroup counter, zero between launches)
+    DBuf<unsigned> fcnt; bool fcnt_zero = false;
+    // The speculative one-token launch. After an fl_moe on one row whose ids and weights were the routing's own picks
+    // and whose arena is declared resident and tiled (fl_register_tiled), spec_ok holds that arena; the next
+    // fl_ffn_begin on one row then routes and runs the whole block in one launch on its picks (fl_moe's combine, h and
+    // moe into z_out), and fl_moe, if called on exactly those picks, weights and arena, only waits for it (spec_live)
+    bool spec_ok = false, spec_live = false; const void * spec_g = nullptr, * spec_u = nullptr, * spec_d = nullptr;
+    int spec_nexp = 0; unsigned spec_epoch = 0;
     // the wide pass's h / moe rows in mapped host memory, written there by k_wide_finish / k_wide_skip (no copy back)
     float * h_wh = nullptr, * h_wmoe = nullptr, * h_wh_d = nullptr, * h_wmoe_d = nullptr;
     // pinned staging of the host inputs (pageable copies would wait for the stream). fl_ffn_begin's ncur / ffn_inp go
@@ -274,6 +283,7 @@ void compat_free(FLCtx * c) {
     s->ag.release(); s->au.release(); s->ad.release(); s->ids.release(); s->counts.release(); s->offsets.release(); s->perm.release(); s->inv.release();
     s->act.release(); s->nact.release(); s->w.release(); s->hout.release(); s->moe.release();
     s->xh.release(); s->hh.release(); s->pcols.release(); s->pncols.release();
+    s->fcnt.release();
     s->fi_all.release(); s->sh_all.release(); s->base_all.release(); s->out_all.release(); s->xd_all.release(); s->xq_all.release();
     s->w_act.release(); s->w_off.release(); s->w_perm.release(); s->w_nact.release(); s->w_row.release(); s->w_k.release(); s->w_wk.release();
     delete s; c->compat = nullptr;
@@ -501,7 +511,7 @@ static void need_down_fmt(const char * fn, int fmt, const void * down) {
 }
 
 // ================================================================ entry points
-static int ffn_begin_body(FLCtx * c, const FLW * W, int N, const float * ncur, const float * ffn_inp, int wrow);
+static int ffn_begin_body(FLCtx * c, const FLW * W, int N, const float * ncur, const float * ffn_inp, int wrow, DecodeArgs * spec);
 // fl_ffn_begin's enqueued work is bracketed by a pair of events, folded into fl_gpu_ms(0 / 2) when that is read
 extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur, const float * ffn_inp, int wrow) {
     if (!c) { return FL_EINVAL; }
@@ -512,12 +522,44 @@ extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur,
         (void) hipGetLastError(); return fail(c, FL_EHIP, "hipEventCreate");
     }
     TRY(c, hipEventRecord(ev.first, c->st));
-    const int rc = ffn_begin_body(c, W, N, ncur, ffn_inp, wrow);
+    DecodeArgs spec{};
+    const int rc = ffn_begin_body(c, W, N, ncur, ffn_inp, wrow, &spec);
     TRY(c, hipEventRecord(ev.second, c->st));
     c->ffn_ev_pending.push_back(ev);
+    if (rc == FL_OK && cs(c)->spec_live) {
+        // the speculative one-token launch: its time is the experts' (fl_gpu_ms(1)), as fl_moe's launch would be
+        std::pair<hipEvent_t, hipEvent_t> mv;
+        if (!take_events(c->moe_ev_free, mv)) { return fail(c, FL_EHIP, "hipEventCreate"); }
+        TRY(c, hipEventRecord(mv.first, c->st));
+        if (int r2 = decode_picks(c, spec)) { cs(c)->spec_live = false; return r2; }
+        TRY(c, hipEventRecord(mv.second, c->st));
+        c->moe_ev_pending.push_back(mv);
+        Compat * s = cs(c);
+        s->spec_epoch = c->epoch; s->r_tagged = true; s->rtag = c->epoch;
+    }
     return rc;
 }
-static int ffn_begin_body(FLCtx * c, const FLW * W, int N, const float * ncur, const float * ffn_inp, int wrow) {
+// the device counter behind fl_moe's completion word (zero before the first launch; each launch's last workgroup
+// resets it)
+static unsigned * fcnt_of(FLCtx * c, Compat * s) {
+    if (!s->fcnt_zero) {
+        FALLOC(s->fcnt, 1);
+        CK(hipMemsetAsync(s->fcnt.p, 0, sizeof(unsigned), c->st));
+        s->fcnt_zero = true;
+    }
+    return s->fcnt.p;
+}
+// a one-token launch's shared expert: IQ2_XXS matrices declared tiled as they are, else fl_ffn_begin's tiled copy;
+// K-quants in place
+static void one_token_shared(Compat * s, bool iq_sh, DecodeArgs & d) {
+    const size_t mg = mat_bytes(H_, E_);
+    for (int i = 0; i < 3; ++i) {
+        const uint8_t * m = (const uint8_t *) s->sh_key[i];
+        if (iq_sh && !tiled_holds(m, i < 2 ? mg : mat_bytes(E_, H_))) { m = s->sh_t.p + i * mg; }
+        (i == 0 ? d.sh_gate : i == 1 ? d.sh_up : d.sh_down) = m;
+    }
+}
+static int ffn_begin_body(FLCtx * c, const FLW * W, int N, const float * ncur, const float * ffn_inp, int wrow, DecodeArgs * spec) {
     if (!W || !ncur || !ffn_inp) { return fail(c, FL_EINVAL, "null pointer"); }
     if (N <= 0 || N > RMAX) { return fail(c, FL_ERANGE, "N = %d outside 1..%d", N, RMAX); }
     if (!W->gate_inp || !W->probs_b || !W->sh_gate || !W->sh_up || !W->sh_down) { return fail(c, FL_EINVAL, "router or shared-expert weight missing"); }
@@ -586,10 +628,35 @@ static int ffn_begin_body(FLCtx * c, const FLW * W, int N, const float * ncur, c
     // straight into host memory (fl_fetch only waits)
     float * wts = reinterpret_cast<float *>(s->z_sel_d + (size_t) N * c->topk);
     unsigned * done = reinterpret_cast<unsigned *>(s->z_sel_d + ZS_DONE);
-    if (int rc = route_dev(c, wr, (const float *) W->probs_b, s->ncur.p, N, ne, E_, s->logits.p, s->probs.p, s->z_sel_d, wts, done)) {
-        return rc;
+    const size_t mg1 = mat_bytes(H_, E_), md1 = mat_bytes(E_, H_);
+    const bool iq_sh = s->shf[0] == FL_IQ2 && s->shf[1] == FL_IQ2 && s->shf[2] == FL_IQ2;
+    s->spec_live = N == 1 && wrow < 0 && s->spec_ok && iq_sh && s->spec_nexp == ne && c->topk == MAXK && decode1_available(c) &&
+                   decode_rule_ok(ne, c->n_group) && tiled_holds(s->spec_g, (size_t) ne * mg1) && tiled_holds(s->spec_u, (size_t) ne * mg1) &&
+                   tiled_holds(s->spec_d, (size_t) ne * md1);
+    if (s->spec_live) {
+        // route and run the block in one launch on the last fl_moe's arena (the launch itself is fl_ffn_begin's last)
+        FALLOC(s->ids, 2 * MAXK); FALLOC(s->w, MAXK); FALLOC(s->counts, ne); FALLOC(s->offsets, ne + 1); FALLOC(s->perm, MAXK);
+        FALLOC(s->inv, MAXK); FALLOC(s->act, ne); FALLOC(s->nact, 1); FALLOC(s->o, (size_t) MAXK * E_);
+        if (int rc = ensure_expert_scratch(c, 1, E_, H_)) { s->spec_live = false; return rc; }
+        DecodeArgs & d = *spec;
+        d.x = s->ncur.p; d.n = 1; d.resid = s->fi;
+        d.Wr = wr; d.bias = (const float *) W->probs_b;
+        d.n_exp = ne; d.n_group = c->n_group; d.topk_group = c->topk_group; d.topk = MAXK; d.keep = MAXK; d.scale = c->scale;
+        d.gate = (const uint8_t *) s->spec_g; d.up = (const uint8_t *) s->spec_u; d.down = (const uint8_t *) s->spec_d; d.estride = mg1;
+        d.dstride = md1; d.kdown = 0;
+        one_token_shared(s, true, d);
+        d.E = E_; d.H = H_; d.xq = s->xq.p; d.xd = s->xd.p;
+        d.logits = s->logits.p; d.probs = s->probs.p; d.sel = s->ids.p; d.wts = s->w.p; d.counts = s->counts.p; d.offsets = s->offsets.p;
+        d.perm = s->perm.p; d.inv = s->inv.p; d.act = s->act.p; d.nact = s->nact.p;
+        d.moe_out = s->z_out_d + (size_t) NB * E_; d.o_out = s->o.p; d.y = s->z_out_d;
+        d.spec_combine = 1; d.hsel = s->z_sel_d; d.hdone = done;
+        d.fcnt = fcnt_of(c, s); d.fdone = reinterpret_cast<unsigned *>(s->z_sel_d + ZS_FDONE);
+    } else {
+        if (int rc = route_dev(c, wr, (const float *) W->probs_b, s->ncur.p, N, ne, E_, s->logits.p, s->probs.p, s->z_sel_d, wts, done)) {
+            return rc;
+        }
+        s->r_tagged = router_fused_ok(N, E_); s->rtag = c->epoch;
     }
-    s->r_tagged = router_fused_ok(N, E_); s->rtag = c->epoch;
     s->N = N;
     s->sh_pending = true; s->xq_pending = true;
     if (wrow >= 0) {   // the wide pass: the rows' Q8_K (fl_wide_moe) and ffn_inp (base = ffn_inp + shared, formed later)
@@ -673,10 +740,32 @@ extern "C" void fl_moe(FLCtx * c, const void * gate, const void * up, const void
         std::fprintf(stderr, "[fused] fl_moe: an arena allocation is smaller than %d experts\n", nexp); std::exit(7);
     }
     hipStream_t st = c->st; const int P = n * KE;
+    if (!c->moe_ev_pending.empty()) { fold_events(c->moe_ev_pending, c->moe_ev_free, c->ms_moe, c->moe_ev_pending.size() >= 64); }
+    const bool kq_sh = s->shf[0] == FL_Q5K && s->shf[1] == FL_Q5K && s->shf[2] == FL_Q6K;
+    const bool iq_sh = s->shf[0] == FL_IQ2 && s->shf[1] == FL_IQ2 && s->shf[2] == FL_IQ2;
+    // the routing's own picks and weights of the last fl_ffn_begin on one row (z_sel: 8 ids, then 8 weights)
+    const bool own_picks = n == 1 && KE == MAXK && s->N == 1 && s->r_tagged &&
+                           std::memcmp(ids, s->z_sel, MAXK * 4) == 0 && std::memcmp(w, s->z_sel + MAXK, MAXK * 4) == 0;
+    if (s->spec_live) {
+        s->spec_live = false;
+        if (own_picks && gate == s->spec_g && up == s->spec_u && down == s->spec_d && nexp == s->spec_nexp && down_fmt == FL_IQ2 && iq_sh) {
+            // fl_ffn_begin's launch computed exactly this call: wait for its completion word (or the stream)
+            if (!spin_words(reinterpret_cast<const unsigned *>(s->z_sel + ZS_FDONE), 1, s->spec_epoch, 20000.0)) { CK(hipStreamSynchronize(st)); }
+            if (c->herr && __atomic_load_n(c->herr, __ATOMIC_ACQUIRE)) {
+                std::fprintf(stderr, "[fused] fl_moe: the one-token launch reported device code %d\n", *c->herr); std::exit(7);
+            }
+            c->last_kernel = 3; c->last_fused = 1;
+            s->last_ids.assign(ids, ids + P); s->last_KE = KE; s->last_n = n; s->last_fast = true;
+            out->h = s->z_out; out->moe = s->z_out + (size_t) NB * E_;
+            return;
+        }
+    }
     c->last_kernel = 0;   // fl_debug: 2 / 1 when the one-token kernel / the n <= 8 block below runs the call
     int max_slots = 1;
     { std::vector<int> per(nexp, 0); for (int i = 0; i < P; ++i) { max_slots = std::max(max_slots, ++per[ids[i]]); } }
-    CK(hipEventRecord(c->em0, st));
+    std::pair<hipEvent_t, hipEvent_t> mv;
+    if (!take_events(c->moe_ev_free, mv)) { fatal("hipEventCreate", hipErrorOutOfMemory, __FILE__, __LINE__); }
+    CK(hipEventRecord(mv.first, st));
     FALLOC(s->ids, 2 * P); FALLOC(s->counts, nexp); FALLOC(s->offsets, nexp + 1); FALLOC(s->perm, P); FALLOC(s->inv, P);
     FALLOC(s->act, nexp); FALLOC(s->nact, 1); FALLOC(s->o, (size_t) P * E_); FALLOC(s->hout, (size_t) NB * E_); FALLOC(s->moe, (size_t) NB * E_);
     // One launch on the caller's picks (router and selection skipped; the shared expert and the Q8_K of fl_ffn_begin's
@@ -685,8 +774,6 @@ extern "C" void fl_moe(FLCtx * c, const void * gate, const void * up, const void
     // with a Q5_K / Q5_K / Q6_K shared expert); up to 8 rows of an all-IQ2_XXS layer on the n <= 8 block. Results
     // bit-identical to the per-pass kernels below. The launch reads the picks from host memory and writes h and moe
     // there (z_in, z_out): no copies either way.
-    const bool kq_sh = s->shf[0] == FL_Q5K && s->shf[1] == FL_Q5K && s->shf[2] == FL_Q6K;
-    const bool iq_sh = s->shf[0] == FL_IQ2 && s->shf[1] == FL_IQ2 && s->shf[2] == FL_IQ2;
     const bool fast1 = n == 1 && KE == MAXK && decode1_available(c) &&
                        ((down_fmt == FL_IQ2 && iq_sh) || ((down_fmt == FL_Q2K || down_fmt == FL_Q3K) && kq_sh && !(reinterpret_cast<uintptr_t>(down) & 3u)));
     const bool fast = fast1 || (down_fmt == FL_IQ2 && iq_sh && decode_block_available(c));
@@ -709,15 +796,12 @@ extern "C" void fl_moe(FLCtx * c, const void * gate, const void * up, const void
         d.n_exp = nexp; d.n_group = c->n_group; d.topk_group = c->topk_group; d.topk = KE; d.keep = KE; d.scale = c->scale;
         d.gate = ar.g; d.up = ar.u; d.estride = mg;
         d.down = down_fmt == FL_IQ2 ? ar.d : (const uint8_t *) down; d.dstride = fmt_bytes(down_fmt, E_, H_);
-        for (int i = 0; i < 3; ++i) {   // IQ2_XXS: declared tiled as it is, else the tiled copy; K-quants in place
-            const uint8_t * m = (const uint8_t *) s->sh_key[i];
-            if (iq_sh && !tiled_holds(m, i < 2 ? mg : mat_bytes(E_, H_))) { m = s->sh_t.p + i * mg; }
-            (i == 0 ? d.sh_gate : i == 1 ? d.sh_up : d.sh_down) = m;
-        }
+        one_token_shared(s, iq_sh, d);
         d.kdown = down_fmt == FL_IQ2 ? 0 : down_fmt;
         d.E = E_; d.H = H_; d.xq = s->xq.p; d.xd = s->xd.p;
         d.ext_sel = s->z_in_d; d.ext_w = reinterpret_cast<const float *>(s->z_in_d + NB * MAXK);
         d.moe_out = s->z_out_d + (size_t) NB * E_; d.o_out = s->o.p; d.y = s->z_out_d;
+        if (fast1) { d.fcnt = fcnt_of(c, s); d.fdone = reinterpret_cast<unsigned *>(s->z_sel_d + ZS_FDONE); }
         if (decode_picks(c, d) != FL_OK) { std::fprintf(stderr, "[fused] fl_moe: %s\n", c->err.c_str()); std::exit(7); }
     } else {
         quant_now(c, s); shared_now(c, s);
@@ -728,12 +812,24 @@ extern "C" void fl_moe(FLCtx * c, const void * gate, const void * up, const void
         CK(hipMemcpyAsync(s->h_h, s->hout.p, (size_t) n * E_ * 4, hipMemcpyDeviceToHost, st));
         CK(hipMemcpyAsync(s->h_moe, s->moe.p, (size_t) n * E_ * 4, hipMemcpyDeviceToHost, st));
     }
-    CK(hipEventRecord(c->em1, st));
-    CK(hipStreamSynchronize(st));
-    float ms = 0.f; CK(hipEventElapsedTime(&ms, c->em0, c->em1)); c->ms_moe += ms;
+    CK(hipEventRecord(mv.second, st));
+    // the one-token launch is waited for on its completion word (its outputs are in host memory by then); otherwise,
+    // or if the word is late, on the stream
+    const bool seen = fast1 && c->last_kernel == 2 && spin_words(reinterpret_cast<const unsigned *>(s->z_sel + ZS_FDONE), 1, c->epoch, 20000.0);
+    if (seen) {
+        c->moe_ev_pending.push_back(mv);
+    } else {
+        CK(hipStreamSynchronize(st));
+        float ms = 0.f; CK(hipEventElapsedTime(&ms, mv.first, mv.second)); c->ms_moe += ms;
+        c->moe_ev_free.push_back(mv);
+    }
     if (fast && c->herr && __atomic_load_n(c->herr, __ATOMIC_ACQUIRE)) {   // a wait of the launch timed out
         std::fprintf(stderr, "[fused] fl_moe: the one-token launch reported device code %d\n", *c->herr); std::exit(7);
     }
+    // a resident arena used on the routing's own picks: the next fl_ffn_begin on one row may run this block itself
+    s->spec_ok = fast1 && own_picks && down_fmt == FL_IQ2 && iq_sh && tiled_holds(gate, (size_t) nexp * mat_bytes(H_, E_)) &&
+                 tiled_holds(up, (size_t) nexp * mat_bytes(H_, E_)) && tiled_holds(down, (size_t) nexp * mat_bytes(E_, H_));
+    if (s->spec_ok) { s->spec_g = gate; s->spec_u = up; s->spec_d = down; s->spec_nexp = nexp; }
     s->last_ids.assign(ids, ids + P); s->last_KE = KE; s->last_n = n; s->last_fast = fast;
     out->h = fast ? s->z_out : s->h_h; out->moe = fast ? s->z_out + (size_t) NB * E_ : s->h_moe;
 }

@@ -73,6 +73,8 @@ struct FLCtx {
     size_t h2d_zc = 0, h2d_ce = 0; int h2d_said = 0;   // fl_h2d bytes by kernel (mapped pinned) / by copy engine
     // fl_ffn_begin's event pairs (recorded, not yet folded into ms_ffn by fl_gpu_ms) and the reusable ones
     std::vector<std::pair<hipEvent_t, hipEvent_t>> ffn_ev_pending, ffn_ev_free; double ms_ffn = 0.0;
+    // fl_moe's pairs when the call returned on the launch's completion word rather than the stream (folded likewise)
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> moe_ev_pending, moe_ev_free;
 };
 // fl_route_dev with, for the one-launch routing of a few rows (router_fused_ok), a host word set to the context's epoch
 // (as it is after the call) once the picks are written; done may be null, other sizes leave it alone
@@ -112,19 +114,32 @@ static std::vector<hipEvent_t> * prof_begin(FLCtx * c) {
 }
 static void prof_mark(FLCtx * c, std::vector<hipEvent_t> * ev, int i) { if (ev) { (void) hipEventRecord((*ev)[i], c->st); } }
 
-// fold fl_ffn_begin's recorded event pairs into ms_ffn: every pair when wait, else only those already complete
-inline void fold_ffn_events(FLCtx * c, bool wait) {
+// fold recorded event pairs into a millisecond total: every pair when wait, else only those already complete
+typedef std::vector<std::pair<hipEvent_t, hipEvent_t>> EvPairs;
+inline void fold_events(EvPairs & pending, EvPairs & freel, double & acc, bool wait) {
     size_t keep = 0;
-    for (size_t i = 0; i < c->ffn_ev_pending.size(); ++i) {
-        auto ev = c->ffn_ev_pending[i];
+    for (size_t i = 0; i < pending.size(); ++i) {
+        auto ev = pending[i];
         hipError_t q = wait ? hipEventSynchronize(ev.second) : hipEventQuery(ev.second);
         float ms = 0.f;
-        if (q == hipSuccess && hipEventElapsedTime(&ms, ev.first, ev.second) == hipSuccess) { c->ms_ffn += ms; c->ffn_ev_free.push_back(ev); continue; }
+        if (q == hipSuccess && hipEventElapsedTime(&ms, ev.first, ev.second) == hipSuccess) { acc += ms; freel.push_back(ev); continue; }
         (void) hipGetLastError();
-        if (q == hipSuccess) { c->ffn_ev_free.push_back(ev); continue; }   // an unmeasurable pair is dropped, not kept
-        c->ffn_ev_pending[keep++] = ev;
+        if (q == hipSuccess) { freel.push_back(ev); continue; }   // an unmeasurable pair is dropped, not kept
+        pending[keep++] = ev;
     }
-    c->ffn_ev_pending.resize(keep);
+    pending.resize(keep);
+}
+// a pair to record around a call's enqueued work (reused or created); false if HIP cannot create events
+inline bool take_events(EvPairs & freel, std::pair<hipEvent_t, hipEvent_t> & ev) {
+    if (!freel.empty()) { ev = freel.back(); freel.pop_back(); return true; }
+    ev = { nullptr, nullptr };
+    if (hipEventCreate(&ev.first) != hipSuccess || hipEventCreate(&ev.second) != hipSuccess) { (void) hipGetLastError(); return false; }
+    return true;
+}
+// fl_ffn_begin's pairs into ms_ffn, fl_moe's (those not waited for at once) into ms_moe
+inline void fold_ffn_events(FLCtx * c, bool wait) {
+    fold_events(c->ffn_ev_pending, c->ffn_ev_free, c->ms_ffn, wait);
+    fold_events(c->moe_ev_pending, c->moe_ev_free, c->ms_moe, wait);
 }
 
 void compat_free(FLCtx * c);   // compat.hip

@@ -130,7 +130,7 @@ extern "C" void fl_free(FLCtx * c) {
     c->ksg.release(); c->ksu.release(); c->rcnt.release(); c->rpart.release(); c->dscr.release();
     for (auto & v : c->ev_free) { for (auto e : v) { (void) hipEventDestroy(e); } }
     for (auto & v : c->ev_pending) { for (auto e : v) { (void) hipEventDestroy(e); } }
-    for (auto * l : { &c->ffn_ev_pending, &c->ffn_ev_free }) { for (auto & e : *l) { (void) hipEventDestroy(e.first); (void) hipEventDestroy(e.second); } }
+    for (auto * l : { &c->ffn_ev_pending, &c->ffn_ev_free, &c->moe_ev_pending, &c->moe_ev_free }) { for (auto & e : *l) { (void) hipEventDestroy(e.first); (void) hipEventDestroy(e.second); } }
     (void) hipEventDestroy(c->em0); (void) hipEventDestroy(c->em1); (void) hipStreamDestroy(c->own);
     if (c->herr) { (void) hipHostFree(c->herr); }
     delete c;

@@ -764,7 +764,7 @@ template <bool KQ> __device__ __forceinline__ bool combine1(const D1Args & a, ld
     __syncthreads();
     if (t < CROWS1) {
         const int row = row0 + t;
-        if (a.ext_sel) {   // fl_moe's combine: the distinct ids ascending, moe = their weighted sum, y = (moe + shared) + resid
+        if (a.ext_sel || a.spec_combine) {   // fl_moe's combine: the distinct ids ascending, moe = their weighted sum, y = (moe + shared) + resid
             const LK_LOCAL int * xs = reinterpret_cast<const LK_LOCAL int *>(lds + M_EXT);
             const LK_LOCAL float * xw = reinterpret_cast<const LK_LOCAL float *>(lds + M_EXT + MAXK * 4);
             const int cnt = reinterpret_cast<const LK_LOCAL int *>(lds + M_EXT + 2 * MAXK * 4)[0];
@@ -807,6 +807,28 @@ __device__ __noinline__ void routing1(const D1Args & a, lds1_t lds) {
         gptr(a.offsets)[x] = lt;
         if (x < a.n_exp) { gptr(a.counts)[x] = eq; }
     }
+}
+
+// fl_moe's combine list from the picks and weights in M_SEL (lane 0): the distinct ids in ascending order, each with
+// its weights summed in k order and its first slot; zero sums are dropped, as fl_moe does
+__device__ __forceinline__ void ext_list1(lds1_t lds) {
+    if (lane_id() != 0) { return; }
+    const LK_LOCAL int * so = reinterpret_cast<const LK_LOCAL int *>(lds + M_SEL);
+    const LK_LOCAL float * wo = reinterpret_cast<const LK_LOCAL float *>(lds + M_SEL + MAXK * 4);
+    LK_LOCAL int * xs = reinterpret_cast<LK_LOCAL int *>(lds + M_EXT);
+    LK_LOCAL float * xw = reinterpret_cast<LK_LOCAL float *>(lds + M_EXT + MAXK * 4);
+    int prev = -1, cnt = 0;
+    for (int it = 0; it < MAXK; ++it) {
+        int m = 0x7fffffff;
+        for (int k = 0; k < MAXK; ++k) { if (so[k] > prev && so[k] < m) { m = so[k]; } }
+        if (m == 0x7fffffff) { break; }
+        float wt = 0.f; int kf = -1;
+        for (int k = 0; k < MAXK; ++k) { if (so[k] == m) { wt += wo[k]; if (kf < 0) { kf = k; } } }
+        prev = m;
+        if (wt == 0.f) { continue; }
+        xs[cnt] = kf; xw[cnt] = wt; ++cnt;
+    }
+    reinterpret_cast<LK_LOCAL int *>(lds + M_EXT + 2 * MAXK * 4)[0] = cnt;
 }
 
 // ---------------------------------------------------------------- the kernel
@@ -875,25 +897,9 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
         if (wave == 0) {
             LK_LOCAL int * so = reinterpret_cast<LK_LOCAL int *>(lds + M_SEL);
             LK_LOCAL float * wo = reinterpret_cast<LK_LOCAL float *>(lds + M_SEL + MAXK * 4);
-            int idv = 0; float wv = 0.f;
-            if (lane < MAXK) { idv = gptr(a.ext_sel)[lane]; wv = gptr(a.ext_w)[lane]; so[lane] = idv; wo[lane] = wv; }
+            if (lane < MAXK) { so[lane] = gptr(a.ext_sel)[lane]; wo[lane] = gptr(a.ext_w)[lane]; }
             lds_visible();
-            if (lane == 0) {
-                LK_LOCAL int * xs = reinterpret_cast<LK_LOCAL int *>(lds + M_EXT);
-                LK_LOCAL float * xw = reinterpret_cast<LK_LOCAL float *>(lds + M_EXT + MAXK * 4);
-                int prev = -1, cnt = 0;
-                for (int it = 0; it < MAXK; ++it) {
-                    int m = 0x7fffffff;
-                    for (int k = 0; k < MAXK; ++k) { if (so[k] > prev && so[k] < m) { m = so[k]; } }
-                    if (m == 0x7fffffff) { break; }
-                    float wt = 0.f; int kf = -1;
-                    for (int k = 0; k < MAXK; ++k) { if (so[k] == m) { wt += wo[k]; if (kf < 0) { kf = k; } } }
-                    prev = m;
-                    if (wt == 0.f) { continue; }
-                    xs[cnt] = kf; xw[cnt] = wt; ++cnt;
-                }
-                reinterpret_cast<LK_LOCAL int *>(lds + M_EXT + 2 * MAXK * 4)[0] = cnt;
-            }
+            ext_list1(lds);
             flag1(ctl + C_READY, 1u);
         }
     } else if (li == 0 && wave == 0) {
@@ -908,6 +914,11 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
             }
             flag1(ctl + C_READY, ok ? 1u : 2u);
             TRACE1(4);
+            if (a.spec_combine && xcd == 0 && a.hsel) {   // the picks and weights for fl_fetch, then its done word
+                if (lane < 16) { gptr(a.hsel)[lane] = ok ? reinterpret_cast<const LK_LOCAL int *>(lds + M_SEL)[lane] : (lane < MAXK ? -1 : 0); }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");   // system scope: the picks before the word
+                if (lane == 0) { __hip_atomic_store(gptr(a.hdone), a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); }
+            }
         }
     } else if (li != 0 && wave == 0) {
         const uint64_t * bc = a.tlogits + BCAST1 + xcd * 16;   // [8 picks, 8 weights] of this XCD
@@ -927,6 +938,7 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
     const unsigned ready = wait1(ctl + C_READY, 1);
     if (ready != 1) { if (ready == 0) { report1(a, 8); } return; }
     lds_visible();
+    if (a.spec_combine && wave == 0) { ext_list1(lds); }   // fl_moe's combine on the kernel's own picks
 
     // 3. routed gate/up: expert sel[xcd], h rows kb * 256 + qq * 64 .. + 63 (one row group of gate and up), as items
     //    the waves claim from an LDS counter
@@ -1057,6 +1069,20 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
     if (wave == 0 && __hip_atomic_load(ctl + C_CMBFAIL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) { report1(a, 16); }
     TRACE1(10);
     if (blockIdx.x == 0 && wave == W1 - 1 && !a.ext_sel) { routing1(a, lds); }
+    if (a.fdone && wave == 0) {
+        // this workgroup's combine rows are written (wave 0 wrote them): count it; the last one tells the host. No fence
+        // per workgroup (an L2 write-back each): the rows go to the caller's memory before the count, and the last
+        // workgroup's system-scope release orders them before the word
+        stores_done();
+        unsigned old = 0;
+        if (lane == 0) { old = __hip_atomic_fetch_add(gptr(a.fcnt), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+        old = __builtin_amdgcn_readfirstlane(old);
+        if (old + 1 == (unsigned) G1) {
+            if (lane == 0) { __hip_atomic_store(gptr(a.fcnt), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
+            if (lane == 0) { __hip_atomic_store(gptr(a.fdone), a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); }
+        }
+    }
 }
 
 size_t decode1_lds_bytes() { return DEC1_LDS; }
@@ -1091,7 +1117,8 @@ hipError_t decode1_init(int ncu, int * ok) {
 }
 
 hipError_t launch_moe_decode1(const DecodeArgs & a, bool cooperative, hipStream_t st) {
-    if (a.ext_sel && (!a.ext_w || !a.moe_out || !a.resid || a.prenorm)) { return hipErrorInvalidValue; }   // the caller's picks
+    if ((a.ext_sel || a.spec_combine) && ((a.ext_sel && !a.ext_w) || !a.moe_out || !a.resid || a.prenorm)) { return hipErrorInvalidValue; }   // fl_moe's combine
+    if ((a.spec_combine && (a.ext_sel || !a.hsel || !a.hdone)) || (a.fdone && !a.fcnt)) { return hipErrorInvalidValue; }
     if (a.n != 1 || a.topk != MAXK || a.keep != MAXK || (!a.ext_sel && !decode_rule_ok(a.n_exp, a.n_group)) || a.E != E1 || a.H != H1 ||
         !a.th || !a.to || !a.tlogits || a.n_exp > NEXP_MAX || (a.kdown != 0 && a.kdown != KF_Q2K && a.kdown != KF_Q3K) ||
         (a.kdown != 0 && ((reinterpret_cast<uintptr_t>(a.down) | reinterpret_cast<uintptr_t>(a.sh_gate) |

@@ -89,6 +89,12 @@ struct DecodeArgs {
     // (o_out, may be null: the 8 slots' outputs [slot][E], for the reference's per-slot attribution)
     const int * ext_sel; const float * ext_w; float * moe_out; float * o_out;
     int share;                                       // keep < topk by the engine's --share-experts rule (n <= 8 block)
+    // the one-token kernel only. spec_combine: the kernel routes, then combines as fl_moe does on those picks (the
+    // ext_sel combine; moe_out and resid required), and XCD 0's selecting wave writes the picks and weights to hsel
+    // (8 ids, then 8 weights) and then *hdone = epoch (host-mapped, for fl_fetch). fdone (either path, may be null):
+    // *fdone = epoch once every workgroup's outputs are written (fcnt: a device counter, zero before the launch,
+    // reset by the last workgroup), so the host can wait on a word instead of the stream
+    int spec_combine; int * hsel; unsigned * hdone; unsigned * fcnt, * fdone;
     int E, H;                                        // 7168, 2048 (the kernel's geometry)
     int8_t * xq; float * xd;                         // Q8_K of x (written by workgroup 0)
     float * logits, * probs; int * sel; float * wts; int * counts, * offsets, * perm, * inv, * act, * nact;

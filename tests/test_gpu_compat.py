@@ -527,3 +527,62 @@ def test_gpu_ms_accounts_the_calls(ctx, small_layer):
     lib().fl_skip(ctx.ctx, cptr(mo), n, ctypes.byref(out))
     assert lib().fl_gpu_ms(ctx.ctx, 1) > m1
     assert lib().fl_gpu_ms(ctx.ctx, 3) == s0 == 0.0
+
+
+def test_speculative_one_token_launch(ctx):
+    """The engine's decode-1 loop on a resident arena of all 256 experts, declared tiled (ids = expert ids): after the
+    first fl_moe on the routing's own picks, each fl_ffn_begin runs the whole block in its routing launch and fl_moe
+    only waits for it (FLDebug.kernel 3). h and moe are bit-identical to the per-pass kernels on the same calls. A call
+    whose weights differ from the routing's (one weight scaled) runs its own launch on them (kernel 2), and so does
+    the call after it (the speculation restarts only after an fl_moe on the routing's own picks)."""
+    import torch
+    from loki_amd import FLOut, FLW, MoeLayerWeights, lib
+    L = MoeLayerWeights.synthetic(ctx, 7400)
+    mats = (L.gate, L.up, L.down, L.sh_gate, L.sh_up, L.sh_down)
+    ctx.set_routing(8, 4, 8, 2.5)
+    ctx.set_experts(256)   # this module's other tests route over 16 experts
+    rng = np.random.default_rng(7400)
+    T = 6
+    xs = rng.standard_normal((T, E)).astype(np.float32)
+    fis = rng.standard_normal((T, E)).astype(np.float32)
+    w = FLW()
+    w.gate_inp = L.gate_inp.data_ptr(); w.probs_b = L.probs_b.data_ptr(); w.gate_f16 = 0
+    w.sh_gate, w.sh_up, w.sh_down = (m.data_ptr() for m in mats[3:])
+
+    def run(changed):
+        out = FLOut()
+        res = []
+        for i in range(T):
+            ctx.check(lib().fl_ffn_begin(ctx.ctx, ctypes.byref(w), 1, cptr(xs[i]), cptr(fis[i]), -1))
+            lib().fl_fetch(ctx.ctx, 1, 1, ctypes.byref(out))
+            sel = np.ctypeslib.as_array(out.sel, shape=(KE,)).astype(np.int32).copy()
+            wts = np.ctypeslib.as_array(out.wts, shape=(KE,)).copy()
+            if i == changed:
+                wts[3] = np.float32(wts[3] * np.float32(0.5))
+            lib().fl_moe(ctx.ctx, L.gate.data_ptr(), L.up.data_ptr(), L.down.data_ptr(), 256, 4, cptr(sel), cptr(f32(wts)), KE, 1,
+                         ctypes.byref(out))
+            res.append((ctx.debug().kernel, np.ctypeslib.as_array(out.h, shape=(E,)).copy(),
+                        np.ctypeslib.as_array(out.moe, shape=(E,)).copy(), sel))
+        return res
+
+    for t in mats:
+        ctx.register_tiled(t)
+    try:
+        for changed in (-1, 2):
+            spec = run(changed)
+            with ctx.using_fused(0):
+                plain = run(changed)
+            kernels = [r[0] for r in spec]
+            want = [2, 3, 3, 3, 3, 3] if changed < 0 else [2, 3, 2, 2, 3, 3]
+            assert kernels == want, (changed, kernels)
+            assert all(r[0] == 0 for r in plain)
+            for i in range(T):
+                assert np.array_equal(spec[i][3], plain[i][3]), (changed, i)
+                assert np.array_equal(spec[i][1].view(np.uint32), plain[i][1].view(np.uint32)), (changed, i)
+                assert np.array_equal(spec[i][2].view(np.uint32), plain[i][2].view(np.uint32)), (changed, i)
+    finally:
+        for t in mats:
+            ctx.unregister_tiled(t)
+        ctx.set_experts(16)
+    del L
+    torch.cuda.empty_cache()
