@@ -66,6 +66,8 @@ constexpr int NB = 8;              // rows of a narrow pass (src/fused_layer.cu:
 constexpr int E_ = 7168, H_ = 2048, NEXP_ = 256;
 constexpr int ZS_DONE = 2 * RMAX * MAXK + 16;   // the routing's done word in z_sel (its own cache line)
 constexpr int ZS_FDONE = ZS_DONE + 1;           // fl_moe's one-token launch's completion word
+constexpr int ZS_TSTAMP = ZS_DONE + 4;          // its start and end clocks (two 64-bit words, 16-byte aligned)
+static_assert(ZS_TSTAMP % 4 == 0 && ZS_TSTAMP + 4 <= ZS_DONE + 16, "z_sel layout");
 
 template <class T> T * pinned(size_t n) {
     void * p = nullptr;
@@ -241,7 +243,8 @@ struct Compat {
     // (the reference's mirrors are replaced by the next call). st_ev[p] is recorded after in_st[p]'s copy and waited
     // before it is refilled. fl_moe's ids / w go to in_ids, in_ev likewise.
     float * in_st[2] = { nullptr, nullptr }, * in_ncur = nullptr, * in_fi = nullptr, * in_w = nullptr; int * in_ids = nullptr;
-    hipEvent_t st_ev[2] = { nullptr, nullptr }; bool st_rec[2] = { false, false }; int st_par = 0;
+    hipEvent_t st_ev[2] = { nullptr, nullptr }; bool st_rec[2] = { false, false }; int st_par = 0, st_spec = 0;
+    float * in_st_d[2] = { nullptr, nullptr };   // the stagings' device addresses (the speculative launch reads them)
     hipEvent_t in_ev = nullptr; bool in_rec = false;
 };
 
@@ -252,7 +255,7 @@ static Compat * cs(FLCtx * c) {
         s->z_out = mapped<float>((size_t) 2 * NB * E_, &s->z_out_d);
         s->h_sel = pinned<int>(RMAX * MAXK); s->h_wts = pinned<float>(RMAX * MAXK);
         s->h_h = pinned<float>((size_t) RMAX * E_); s->h_moe = pinned<float>((size_t) RMAX * E_);
-        s->in_st[0] = pinned<float>((size_t) 2 * RMAX * E_); s->in_st[1] = pinned<float>((size_t) 2 * RMAX * E_);
+        s->in_st[0] = mapped<float>((size_t) 2 * RMAX * E_, &s->in_st_d[0]); s->in_st[1] = mapped<float>((size_t) 2 * RMAX * E_, &s->in_st_d[1]);
         s->in_ids = pinned<int>(2 * NB * MAXK); s->in_w = pinned<float>(NB * MAXK);   // in_ids: ids, then the weights
         if (!s->z_sel || !s->z_in || !s->z_out || !s->h_sel || !s->h_wts || !s->h_h || !s->h_moe || !s->in_st[0] || !s->in_st[1] || !s->in_ids || !s->in_w) {
             fatal("hipHostMalloc (fused-layer mirrors)", hipErrorOutOfMemory, __FILE__, __LINE__);
@@ -512,6 +515,16 @@ static void need_down_fmt(const char * fn, int fmt, const void * down) {
 
 // ================================================================ entry points
 static int ffn_begin_body(FLCtx * c, const FLW * W, int N, const float * ncur, const float * ffn_inp, int wrow, DecodeArgs * spec);
+// whether fl_ffn_begin on these rows runs the speculative one-token launch (the last fl_moe's arena still declared)
+static bool spec_candidate(FLCtx * c, int N, int wrow) {
+    Compat * s = c->compat;
+    if (!s || N != 1 || wrow >= 0 || !s->spec_ok) { return false; }
+    const size_t mg = (size_t) H_ * (E_ / QK) * IQ2B, md = (size_t) E_ * (H_ / QK) * IQ2B;
+    const int ne = c->n_exp;
+    return s->shf[0] == FL_IQ2 && s->shf[1] == FL_IQ2 && s->shf[2] == FL_IQ2 && s->spec_nexp == ne && c->topk == MAXK &&
+           decode1_available(c) && decode_rule_ok(ne, c->n_group) && tiled_holds(s->spec_g, (size_t) ne * mg) &&
+           tiled_holds(s->spec_u, (size_t) ne * mg) && tiled_holds(s->spec_d, (size_t) ne * md);
+}
 // fl_ffn_begin's enqueued work is bracketed by a pair of events, folded into fl_gpu_ms(0 / 2) when that is read
 extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur, const float * ffn_inp, int wrow) {
     if (!c) { return FL_EINVAL; }
@@ -521,20 +534,24 @@ extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur,
     else if (hipEventCreate(&ev.first) != hipSuccess || hipEventCreate(&ev.second) != hipSuccess) {
         (void) hipGetLastError(); return fail(c, FL_EHIP, "hipEventCreate");
     }
-    TRY(c, hipEventRecord(ev.first, c->st));
+    // the pair brackets the call's enqueued work, except on the speculative path (the launch keeps its own clock, and
+    // the call enqueues nothing else once the shared expert is packed)
+    const bool timed = !spec_candidate(c, N, wrow);
+    if (timed) { TRY(c, hipEventRecord(ev.first, c->st)); }
     DecodeArgs spec{};
     const int rc = ffn_begin_body(c, W, N, ncur, ffn_inp, wrow, &spec);
-    TRY(c, hipEventRecord(ev.second, c->st));
-    c->ffn_ev_pending.push_back(ev);
+    if (timed) { TRY(c, hipEventRecord(ev.second, c->st)); c->ffn_ev_pending.push_back(ev); }
+    else { c->ffn_ev_free.push_back(ev); }
     if (rc == FL_OK && cs(c)->spec_live) {
-        // the speculative one-token launch: its time is the experts' (fl_gpu_ms(1)), as fl_moe's launch would be
-        std::pair<hipEvent_t, hipEvent_t> mv;
-        if (!take_events(c->moe_ev_free, mv)) { return fail(c, FL_EHIP, "hipEventCreate"); }
-        TRY(c, hipEventRecord(mv.first, c->st));
-        if (int r2 = decode_picks(c, spec)) { cs(c)->spec_live = false; return r2; }
-        TRY(c, hipEventRecord(mv.second, c->st));
-        c->moe_ev_pending.push_back(mv);
+        // the speculative one-token launch: no events around it (each costs several us here); its GPU time comes from
+        // its own clock words and counts as the experts' (fl_gpu_ms(1)) once fl_moe has waited for it
         Compat * s = cs(c);
+        if (int r2 = decode_picks(c, spec)) {   // not launched: the row goes in by the copy engine after all
+            s->spec_live = false;
+            (void) hipMemcpyAsync(s->ncur.p, s->in_ncur, (size_t) 2 * E_ * 4, hipMemcpyHostToDevice, c->st);
+            return r2;
+        }
+        TRY(c, hipEventRecord(s->st_ev[s->st_spec], c->st)); s->st_rec[s->st_spec] = true;   // it read the staging
         s->spec_epoch = c->epoch; s->r_tagged = true; s->rtag = c->epoch;
     }
     return rc;
@@ -580,10 +597,15 @@ static int ffn_begin_body(FLCtx * c, const FLW * W, int N, const float * ncur, c
     ALLOC(c, s->ncur, 2 * R); ALLOC(c, s->logits, RMAX * ne); ALLOC(c, s->probs, RMAX * ne);
     ALLOC(c, s->xq, R); ALLOC(c, s->xd, RMAX * (E_ / QK)); ALLOC(c, s->sh_o, R);
     hipStream_t st = c->st;
+    const size_t mg1 = mat_bytes(H_, E_), md1 = mat_bytes(E_, H_);
+    s->spec_live = spec_candidate(c, N, wrow);
     const int sp = s->st_par ^= 1;
-    if (s->st_rec[sp]) { TRY(c, hipEventSynchronize(s->st_ev[sp])); }   // this staging's previous copy has run
+    if (s->st_rec[sp]) { TRY(c, hipEventSynchronize(s->st_ev[sp])); }   // this staging's previous reader has run
     s->in_ncur = s->in_st[sp]; s->in_fi = s->in_ncur + (size_t) N * E_; s->fi = s->ncur.p + (size_t) N * E_;
-    if ((size_t) N * E_ * 4 <= ((size_t) 1 << 20)) {   // a few rows: one copy in (each copy costs a DMA start, ~2-5 us)
+    s->st_spec = sp;
+    if (s->spec_live) {   // the launch copies the row and its residual in itself (no copy engine): only staged here
+        std::memcpy(s->in_ncur, ncur, (size_t) E_ * 4); std::memcpy(s->in_fi, ffn_inp, (size_t) E_ * 4);
+    } else if ((size_t) N * E_ * 4 <= ((size_t) 1 << 20)) {   // a few rows: one copy in (each copy costs a DMA start, ~2-5 us)
         std::memcpy(s->in_ncur, ncur, (size_t) N * E_ * 4); std::memcpy(s->in_fi, ffn_inp, (size_t) N * E_ * 4);
         TRY(c, hipMemcpyAsync(s->ncur.p, s->in_ncur, (size_t) 2 * N * E_ * 4, hipMemcpyHostToDevice, st));
     } else {   // staged and sent in pieces: each piece's DMA runs while the next piece is copied into the staging
@@ -600,7 +622,7 @@ static int ffn_begin_body(FLCtx * c, const FLW * W, int N, const float * ncur, c
             }
         }
     }
-    TRY(c, hipEventRecord(s->st_ev[sp], st)); s->st_rec[sp] = true;
+    if (!s->spec_live) { TRY(c, hipEventRecord(s->st_ev[sp], st)); s->st_rec[sp] = true; }   // the launch records it (fl_ffn_begin)
     const size_t mg = mat_bytes(H_, E_);
     const void * shm[3] = { W->sh_gate, W->sh_up, W->sh_down };
     bool sht[3];
@@ -628,11 +650,6 @@ static int ffn_begin_body(FLCtx * c, const FLW * W, int N, const float * ncur, c
     // straight into host memory (fl_fetch only waits)
     float * wts = reinterpret_cast<float *>(s->z_sel_d + (size_t) N * c->topk);
     unsigned * done = reinterpret_cast<unsigned *>(s->z_sel_d + ZS_DONE);
-    const size_t mg1 = mat_bytes(H_, E_), md1 = mat_bytes(E_, H_);
-    const bool iq_sh = s->shf[0] == FL_IQ2 && s->shf[1] == FL_IQ2 && s->shf[2] == FL_IQ2;
-    s->spec_live = N == 1 && wrow < 0 && s->spec_ok && iq_sh && s->spec_nexp == ne && c->topk == MAXK && decode1_available(c) &&
-                   decode_rule_ok(ne, c->n_group) && tiled_holds(s->spec_g, (size_t) ne * mg1) && tiled_holds(s->spec_u, (size_t) ne * mg1) &&
-                   tiled_holds(s->spec_d, (size_t) ne * md1);
     if (s->spec_live) {
         // route and run the block in one launch on the last fl_moe's arena (the launch itself is fl_ffn_begin's last)
         FALLOC(s->ids, 2 * MAXK); FALLOC(s->w, MAXK); FALLOC(s->counts, ne); FALLOC(s->offsets, ne + 1); FALLOC(s->perm, MAXK);
@@ -640,6 +657,7 @@ static int ffn_begin_body(FLCtx * c, const FLW * W, int N, const float * ncur, c
         if (int rc = ensure_expert_scratch(c, 1, E_, H_)) { s->spec_live = false; return rc; }
         DecodeArgs & d = *spec;
         d.x = s->ncur.p; d.n = 1; d.resid = s->fi;
+        d.hx = s->in_st_d[sp]; d.hfi = s->in_st_d[sp] + E_;   // the staging (device addresses): copied in by the launch
         d.Wr = wr; d.bias = (const float *) W->probs_b;
         d.n_exp = ne; d.n_group = c->n_group; d.topk_group = c->topk_group; d.topk = MAXK; d.keep = MAXK; d.scale = c->scale;
         d.gate = (const uint8_t *) s->spec_g; d.up = (const uint8_t *) s->spec_u; d.down = (const uint8_t *) s->spec_d; d.estride = mg1;
@@ -650,6 +668,7 @@ static int ffn_begin_body(FLCtx * c, const FLW * W, int N, const float * ncur, c
         d.perm = s->perm.p; d.inv = s->inv.p; d.act = s->act.p; d.nact = s->nact.p;
         d.moe_out = s->z_out_d + (size_t) NB * E_; d.o_out = s->o.p; d.y = s->z_out_d;
         d.spec_combine = 1; d.hsel = s->z_sel_d; d.hdone = done;
+        d.tstamp = reinterpret_cast<uint64_t *>(s->z_sel_d + ZS_TSTAMP);
         d.fcnt = fcnt_of(c, s); d.fdone = reinterpret_cast<unsigned *>(s->z_sel_d + ZS_FDONE);
     } else {
         if (int rc = route_dev(c, wr, (const float *) W->probs_b, s->ncur.p, N, ne, E_, s->logits.p, s->probs.p, s->z_sel_d, wts, done)) {
@@ -751,6 +770,9 @@ extern "C" void fl_moe(FLCtx * c, const void * gate, const void * up, const void
         if (own_picks && gate == s->spec_g && up == s->spec_u && down == s->spec_d && nexp == s->spec_nexp && down_fmt == FL_IQ2 && iq_sh) {
             // fl_ffn_begin's launch computed exactly this call: wait for its completion word (or the stream)
             if (!spin_words(reinterpret_cast<const unsigned *>(s->z_sel + ZS_FDONE), 1, s->spec_epoch, 20000.0)) { CK(hipStreamSynchronize(st)); }
+            const uint64_t * ts = reinterpret_cast<const uint64_t *>(s->z_sel + ZS_TSTAMP);
+            const uint64_t t0 = __atomic_load_n(ts, __ATOMIC_ACQUIRE), t1 = __atomic_load_n(ts + 1, __ATOMIC_ACQUIRE);
+            if (t1 > t0) { c->ms_moe += (double) (t1 - t0) * 1e-5; }   // 100 MHz ticks
             if (c->herr && __atomic_load_n(c->herr, __ATOMIC_ACQUIRE)) {
                 std::fprintf(stderr, "[fused] fl_moe: the one-token launch reported device code %d\n", *c->herr); std::exit(7);
             }
