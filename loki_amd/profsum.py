@@ -12,9 +12,10 @@ bench.py in its JSON line), so bench.py can refuse figures that belong to anothe
   each is scaled by what the same counter reads for the probe's plain 1 GiB device copy (1 GiB read + 1 GiB written).
 
 usage:
-  python -m loki_amd.profsum trace DIR --kernel REGEX --key KEY --workload W --last N --log BENCH_STDOUT --cmd "..."
+  python -m loki_amd.profsum trace DIR --kernel REGEX --key KEY --workload W --last N --log BENCH_STDOUT --cmd "..." [--group G]
   python -m loki_amd.profsum traffic FETCH_DIR WRITE_DIR --kernel REGEX --key KEY --workload W --last N
-         --alg BYTES --log-fetch LOG --log-write LOG --cmd-fetch "..." --cmd-write "..." [--notes "..."]
+         --alg BYTES --log-fetch LOG --log-write LOG --cmd-fetch "..." --cmd-write "..." [--notes "..."] [--group G]
+(--group G: a stage launched as G kernels back to back, their consecutive dispatches summed per step)
 """
 import argparse
 import csv
@@ -80,10 +81,18 @@ def _durations(trace_csv, pat):
     return [d for _, d in out]
 
 
+def _grouped(d, g):
+    """Consecutive dispatches summed in groups of g (a stage launched as g kernels back to back, e.g. the prefill
+    GEMM's wide and narrow kernels); trailing partial groups are dropped."""
+    if g <= 1:
+        return d
+    return [sum(d[i:i + g]) for i in range(0, len(d) - len(d) % g, g)]
+
+
 def trace(a):
     tcsv, scsv = _find(a.dir, "kernel_trace.csv"), _find(a.dir, "kernel_stats.csv")
     sha, line = lib_of(a.log)
-    d = _durations(tcsv, a.kernel)
+    d = _grouped(_durations(tcsv, a.kernel), a.group)
     if not d:
         raise SystemExit("kernel /%s/ not in %s" % (a.kernel, tcsv))
     last = d[-a.last:] if a.last else d
@@ -92,7 +101,7 @@ def trace(a):
           "dispatches": len(d), "avg_us_all": round(sum(d) / len(d), 3),
           "last_n": len(last), "avg_us_last": round(sum(last) / len(last), 3),
           "median_us_last": round(statistics.median(last), 3), "min_us_last": round(min(last), 3),
-          "max_us_last": round(max(last), 3), "command": a.cmd,
+          "max_us_last": round(max(last), 3), "kernels_per_step": a.group, "command": a.cmd,
           "bench_roofline": line.get("roofline") if line else None,
           "bench_value": line.get("value") if line else None}
     os.makedirs(PROFILES, exist_ok=True)
@@ -135,7 +144,7 @@ def traffic(a):
     def kv(rs):
         v = [(int(r["Dispatch_Id"]), float(r["Counter_Value"])) for r in rs if rx.search(r["Kernel_Name"])]
         v.sort()
-        return [x for _, x in v][-a.last:]
+        return _grouped([x for _, x in v], a.group)[-a.last:]
 
     def probe(rs):
         v = [float(r["Counter_Value"]) for r in rs if "copyBuffer" in r["Kernel_Name"] and int(r["Grid_Size"]) >= 1 << 17]
@@ -152,7 +161,7 @@ def traffic(a):
     rb, wb = f_mean * 1024 * fs, w_mean * 1024 * ws
     out = {"kernel": a.key, "kernel_regex": a.kernel, "workload": a.workload, "lib_sha16": sf,
            "fetch_size_kib_per_dispatch": round(f_mean, 3), "write_size_kib_per_dispatch": round(w_mean, 3),
-           "dispatches_averaged": len(fk),
+           "dispatches_averaged": len(fk), "kernels_per_step": a.group,
            "copy_probe": {"bytes_read": GiB, "bytes_written": GiB, "fetch_size_kib": cf, "write_size_kib": cw},
            "fetch_scale": fs, "write_scale": ws, "bytes_per_launch": int(rb + wb), "read_bytes_per_launch": int(rb),
            "write_bytes_per_launch": int(wb), "algorithmic_bytes_per_launch": a.alg,
@@ -173,6 +182,7 @@ def main(argv=None):
     for k in ("--kernel", "--key", "--workload", "--log", "--cmd"):
         t.add_argument(k, required=True)
     t.add_argument("--last", type=int, default=0)
+    t.add_argument("--group", type=int, default=1, help="kernels per step, summed (consecutive dispatches)")
     t.add_argument("--top", type=int, default=12)
     t.add_argument("--notes", default="")
     p = sub.add_parser("traffic")
@@ -181,6 +191,7 @@ def main(argv=None):
     for k in ("--kernel", "--key", "--workload", "--log-fetch", "--log-write", "--cmd-fetch", "--cmd-write"):
         p.add_argument(k, required=True)
     p.add_argument("--last", type=int, default=10)
+    p.add_argument("--group", type=int, default=1, help="kernels per step, summed (consecutive dispatches)")
     p.add_argument("--alg", type=int, required=True)
     p.add_argument("--notes", default="")
     a = ap.parse_args(argv)
