@@ -309,9 +309,15 @@ def run_dropin(ctx, torch, steps=60, warmup=5, ggml_steps=3, seed=20260601):
         with no_gc():   # collected before the warm-up tokens
             for i in range(warmup):
                 token(i, w, L.gate, L.up, L.down, [])
+            g0 = ctx.gpu_ms(1)
             for i in range(steps):
                 token(warmup + i, w, L.gate, L.up, L.down, split)
+            g1 = ctx.gpu_ms(1)
         sp = np.array(split) * 1e6
+        # the experts' GPU time per token as the library accounts it (fl_gpu_ms(1): HIP events around each launch, or
+        # the one-token launch's own device clock when fl_ffn_begin ran the block): the rest of us_per_token is host
+        # calls and launch latency
+        res["gpu_moe_us"] = round((g1 - g0) * 1e3 / steps, 1)
         res["us_per_token"] = round(float(np.median(sp.sum(axis=1))), 1)
         res["ffn_begin_us"], res["fetch_us"], res["moe_us"] = (round(float(v), 1) for v in np.median(sp, axis=0))
         res["mean_us_per_token"] = round(float(sp.sum(axis=1).mean()), 1)

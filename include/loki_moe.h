@@ -87,7 +87,8 @@ int fl_h2d_bytes(FLCtx *, size_t * by_kernel, size_t * by_copy_engine);
  * One row after an fl_moe that ran on the routing's own picks over an arena declared with fl_register_tiled (a resident
  * arena, ids = expert ids): this call also runs that fl_moe's block on its own picks in the same launch as the routing
  * (speculatively; its outputs are used only by an fl_moe with exactly those ids, weights and arena pointers, which then
- * just waits for it -- FLDebug.kernel 3 -- and any other call runs as usual). Its time counts as fl_gpu_ms(1). */
+ * just waits for it -- FLDebug.kernel 3 -- and any other call runs as usual). The row and its residual go in by a small
+ * copy kernel reading the pinned staging (no copy engine). Its time counts as fl_gpu_ms(1). */
 int fl_ffn_begin(FLCtx *, const FLW * W, int N, const float * ncur, const float * ffn_inp, int wrow);
 /* formats of W->sh_gate / sh_up / sh_down for fl_ffn_begin: FL_IQ2 (default, the all-IQ2_XXS configs) or K-quants;
  * the reference's shards are (FL_Q5K, FL_Q5K, FL_Q6K) (src/fused_layer.h:14; FLW carries no format). gate and up are

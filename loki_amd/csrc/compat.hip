@@ -244,7 +244,7 @@ struct Compat {
     // before it is refilled. fl_moe's ids / w go to in_ids, in_ev likewise.
     float * in_st[2] = { nullptr, nullptr }, * in_ncur = nullptr, * in_fi = nullptr, * in_w = nullptr; int * in_ids = nullptr;
     hipEvent_t st_ev[2] = { nullptr, nullptr }; bool st_rec[2] = { false, false }; int st_par = 0, st_spec = 0;
-    float * in_st_d[2] = { nullptr, nullptr };   // the stagings' device addresses (the speculative launch reads them)
+    float * in_st_d[2] = { nullptr, nullptr };   // the stagings' device addresses (the one-row copy kernel reads them)
     hipEvent_t in_ev = nullptr; bool in_rec = false;
 };
 
@@ -534,8 +534,8 @@ extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur,
     else if (hipEventCreate(&ev.first) != hipSuccess || hipEventCreate(&ev.second) != hipSuccess) {
         (void) hipGetLastError(); return fail(c, FL_EHIP, "hipEventCreate");
     }
-    // the pair brackets the call's enqueued work, except on the speculative path (the launch keeps its own clock, and
-    // the call enqueues nothing else once the shared expert is packed)
+    // the pair brackets the call's enqueued work, except on the speculative path (the launch keeps its own clock; the
+    // call enqueues only the row's copy kernel besides it once the shared expert is packed)
     const bool timed = !spec_candidate(c, N, wrow);
     if (timed) { TRY(c, hipEventRecord(ev.first, c->st)); }
     DecodeArgs spec{};
@@ -546,12 +546,8 @@ extern "C" int fl_ffn_begin(FLCtx * c, const FLW * W, int N, const float * ncur,
         // the speculative one-token launch: no events around it (each costs several us here); its GPU time comes from
         // its own clock words and counts as the experts' (fl_gpu_ms(1)) once fl_moe has waited for it
         Compat * s = cs(c);
-        if (int r2 = decode_picks(c, spec)) {   // not launched: the row goes in by the copy engine after all
-            s->spec_live = false;
-            (void) hipMemcpyAsync(s->ncur.p, s->in_ncur, (size_t) 2 * E_ * 4, hipMemcpyHostToDevice, c->st);
-            return r2;
-        }
-        TRY(c, hipEventRecord(s->st_ev[s->st_spec], c->st)); s->st_rec[s->st_spec] = true;   // it read the staging
+        if (int r2 = decode_picks(c, spec)) { s->spec_live = false; return r2; }
+        TRY(c, hipEventRecord(s->st_ev[s->st_spec], c->st)); s->st_rec[s->st_spec] = true;   // the copy kernel read the staging
         s->spec_epoch = c->epoch; s->r_tagged = true; s->rtag = c->epoch;
     }
     return rc;
@@ -603,8 +599,10 @@ static int ffn_begin_body(FLCtx * c, const FLW * W, int N, const float * ncur, c
     if (s->st_rec[sp]) { TRY(c, hipEventSynchronize(s->st_ev[sp])); }   // this staging's previous reader has run
     s->in_ncur = s->in_st[sp]; s->in_fi = s->in_ncur + (size_t) N * E_; s->fi = s->ncur.p + (size_t) N * E_;
     s->st_spec = sp;
-    if (s->spec_live) {   // the launch copies the row and its residual in itself (no copy engine): only staged here
+    if (s->spec_live) {   // one row: the row and its residual in by a small copy kernel reading the mapped staging (no copy engine)
         std::memcpy(s->in_ncur, ncur, (size_t) E_ * 4); std::memcpy(s->in_fi, ffn_inp, (size_t) E_ * 4);
+        k_copy16<<<(2 * E_ / 4 + 255) / 256, 256, 0, st>>>((const uint4 *) s->in_st_d[sp], (uint4 *) s->ncur.p, (size_t) 2 * E_ / 4);
+        TRY(c, hipGetLastError());
     } else if ((size_t) N * E_ * 4 <= ((size_t) 1 << 20)) {   // a few rows: one copy in (each copy costs a DMA start, ~2-5 us)
         std::memcpy(s->in_ncur, ncur, (size_t) N * E_ * 4); std::memcpy(s->in_fi, ffn_inp, (size_t) N * E_ * 4);
         TRY(c, hipMemcpyAsync(s->ncur.p, s->in_ncur, (size_t) 2 * N * E_ * 4, hipMemcpyHostToDevice, st));
@@ -657,7 +655,6 @@ static int ffn_begin_body(FLCtx * c, const FLW * W, int N, const float * ncur, c
         if (int rc = ensure_expert_scratch(c, 1, E_, H_)) { s->spec_live = false; return rc; }
         DecodeArgs & d = *spec;
         d.x = s->ncur.p; d.n = 1; d.resid = s->fi;
-        d.hx = s->in_st_d[sp]; d.hfi = s->in_st_d[sp] + E_;   // the staging (device addresses): copied in by the launch
         d.Wr = wr; d.bias = (const float *) W->probs_b;
         d.n_exp = ne; d.n_group = c->n_group; d.topk_group = c->topk_group; d.topk = MAXK; d.keep = MAXK; d.scale = c->scale;
         d.gate = (const uint8_t *) s->spec_g; d.up = (const uint8_t *) s->spec_u; d.down = (const uint8_t *) s->spec_d; d.estride = mg1;

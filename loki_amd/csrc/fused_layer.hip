@@ -390,7 +390,6 @@ bool decode_block_available(FLCtx * c) { return c->fused != 0 && decode_ready(c)
 int decode_picks(FLCtx * c, DecodeArgs & d) {
     if (int rc = decode_tagged(c, c->st)) { return rc; }
     d.tab = c->tab.p; d.tlogits = c->dlogit.p; d.th = c->dth.p; d.to = c->dto.p;
-    if (d.hx) { d.tx = c->dth.p + DEC_TX; }   // the copied-in row's tagged words: a part of th the one-token kernel leaves unused
     d.epoch = c->epoch; d.err = c->derr.p; d.herr = c->herr ? c->herr_dev : nullptr;
     if (d.n == 1 && d.topk == MAXK && d.keep == MAXK && decode1_ready(c)) {
         TRY(c, launch_moe_decode1(d, c->fused == 1, c->st));

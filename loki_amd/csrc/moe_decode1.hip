@@ -154,39 +154,6 @@ extern "C" hipError_t fl_trace1_clear() {
 #define TRACE1V(slot, v) do { } while (0)
 #endif
 
-// four values of x at col: the device row, or (hx) the tagged words the workgroup owning them wrote in this launch
-// (polled; zeros and the error word after the bound)
-__device__ __forceinline__ float4 x4(const D1Args & a, int col) {
-    if (!a.hx) { return gloadf4(a.x + col); }
-    const uint64_t * p = a.tx + col;
-    uint64_t w[4];
-    for (int it = 0; it < POLL1; ++it) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) { w[k] = ld_tag1(p + k); }
-        if (tag1_ok(w[0], a.epoch) && tag1_ok(w[1], a.epoch) && tag1_ok(w[2], a.epoch) && tag1_ok(w[3], a.epoch)) {
-            return make_float4(tag1_val(w[0]), tag1_val(w[1]), tag1_val(w[2]), tag1_val(w[3]));
-        }
-        __builtin_amdgcn_s_sleep(1);
-    }
-    report1(a, 2);
-    return make_float4(0.f, 0.f, 0.f, 0.f);
-}
-// hx: workgroup b copies values 28 b .. 28 b + 27 of the row (lanes 0-6, also as tagged words) and of its residual
-// (lanes 7-13) from host memory to the device (one wave)
-__device__ __forceinline__ void copy_in1(const D1Args & a) {
-    const int lane = lane_id(), b = blockIdx.x;
-    if (lane < 14) {
-        const bool xr = lane < 7;
-        const int col = CROWS1 * b + 4 * (xr ? lane : lane - 7);
-        const float4 v = gloadf4((xr ? a.hx : a.hfi) + col);
-        *(LK_GLOBAL f32x4 *) gptr(const_cast<float *>(xr ? a.x : a.resid) + col) = f32x4{ v.x, v.y, v.z, v.w };
-        if (xr) {
-            st_tag1(a.tx + col, a.epoch, v.x); st_tag1(a.tx + col + 1, a.epoch, v.y);
-            st_tag1(a.tx + col + 2, a.epoch, v.z); st_tag1(a.tx + col + 3, a.epoch, v.w);
-        }
-    }
-}
-
 // the block's input at column col: x, or (x * scale) * w under prenorm (k_rmsnorm's arithmetic)
 __device__ __forceinline__ float4 in1(const D1Args & a, lds1_t lds, int col, float4 v) {
 #pragma clang fp contract(off)
@@ -215,17 +182,11 @@ __device__ __noinline__ void router1(const D1Args & a, lds1_t lds, int wave, LK_
 #pragma unroll
         for (int i = 0; i < L4; ++i) { wv[i] = gloadf4(wc + 4 * i); }
     }
-    if (!a.hx) {
 #pragma unroll
-        for (int i = 0; i < L4; ++i) { xv[i] = gloadf4(xc + 4 * i); }
-    }
+    for (int i = 0; i < L4; ++i) { xv[i] = gloadf4(xc + 4 * i); }
     // the router's loads are in the CU's memory queue: the table copy (waves 4-7) may follow
     __builtin_amdgcn_sched_barrier(0);
     if (lane == 0) { __hip_atomic_fetch_add(reinterpret_cast<LK_LOCAL unsigned *>(lds + M_CTL) + C_RISSUED, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
-    if (a.hx) {   // chunk c of x is what workgroup c copies in
-#pragma unroll
-        for (int i = 0; i < L4; ++i) { xv[i] = x4(a, c * 4 * L4 + 4 * i); }
-    }
     if (a.prenorm) {
         double s = 0.0;
 #pragma unroll
@@ -330,7 +291,7 @@ __device__ __forceinline__ void quant1(const D1Args & a, lds1_t lds, int w4) {
         float xs[16];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const float4 v = in1(a, lds, col + 4 * q, x4(a, col + 4 * q));
+            const float4 v = in1(a, lds, col + 4 * q, gloadf4(a.x + col + 4 * q));
             xs[4 * q] = v.x; xs[4 * q + 1] = v.y; xs[4 * q + 2] = v.z; xs[4 * q + 3] = v.w;
         }
         uint32_t packed[4]; float d;
@@ -901,7 +862,6 @@ __global__ void __launch_bounds__(NT1, 1) k_moe_decode1(const DecodeArgs args) {
         if (!a.ext_sel) { router1(a, lds, wave, ctl); }   // with the caller's picks there is no routing
         TRACE1(1);
     } else {
-        if (a.hx && wave == 4) { copy_in1(a); }   // this workgroup's slice of the row and its residual
         if (!a.ext_sel) { (void) wait1(ctl + C_RISSUED, 4); }   // the router's weight and token loads go first (the critical path)
         tables_fill(reinterpret_cast<const uint8_t *>(a.tab), lds, threadIdx.x - 256, NQW1 * 64);
         if (a.prenorm && !wait1(ctl + C_NRM, 1)) { report1(a, 64); return; }
@@ -1165,7 +1125,6 @@ hipError_t decode1_init(int ncu, int * ok) {
 hipError_t launch_moe_decode1(const DecodeArgs & a, bool cooperative, hipStream_t st) {
     if ((a.ext_sel || a.spec_combine) && ((a.ext_sel && !a.ext_w) || !a.moe_out || !a.resid || a.prenorm)) { return hipErrorInvalidValue; }   // fl_moe's combine
     if ((a.spec_combine && (a.ext_sel || !a.hsel || !a.hdone)) || (a.fdone && !a.fcnt)) { return hipErrorInvalidValue; }
-    if ((a.hx || a.hfi) && (!a.hx || !a.hfi || !a.tx || !a.resid || a.ext_sel || a.prenorm)) { return hipErrorInvalidValue; }   // the copy in
     if (a.n != 1 || a.topk != MAXK || a.keep != MAXK || (!a.ext_sel && !decode_rule_ok(a.n_exp, a.n_group)) || a.E != E1 || a.H != H1 ||
         !a.th || !a.to || !a.tlogits || a.n_exp > NEXP_MAX || (a.kdown != 0 && a.kdown != KF_Q2K && a.kdown != KF_Q3K) ||
         (a.kdown != 0 && ((reinterpret_cast<uintptr_t>(a.down) | reinterpret_cast<uintptr_t>(a.sh_gate) |

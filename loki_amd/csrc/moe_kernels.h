@@ -95,10 +95,6 @@ struct DecodeArgs {
     // *fdone = epoch once every workgroup's outputs are written (fcnt: a device counter, zero before the launch,
     // reset by the last workgroup), so the host can wait on a word instead of the stream
     int spec_combine; int * hsel; unsigned * hdone; unsigned * fcnt, * fdone;
-    // the one-token kernel only: hx / hfi (may be null) are the row and its residual in host memory (device addresses);
-    // workgroup b then copies values 28 b .. 28 b + 27 of each to x and resid itself, and hands its x values to the other
-    // workgroups as tagged words tx [7168] (no copy before the launch)
-    const float * hx, * hfi; uint64_t * tx;
     // the one-token kernel, with fdone: tstamp [0] = workgroup 0's entry, [1] = the last workgroup's end (the 100 MHz
     // s_memrealtime clock; may be null), the launch's GPU time without events around it
     uint64_t * tstamp;
@@ -116,8 +112,6 @@ struct DecodeArgs {
 // sizes (64-bit words) of the tagged buffers for any n <= 8 (topk <= MAXK)
 constexpr size_t DEC_TLOGITS = 8 * 256, DEC_TH = (size_t) 8 * (MAXK + 1) * 2048,
                  DEC_TO = (size_t) 8 * (MAXK + 1) * 7168;
-constexpr size_t DEC_TX = (size_t) (MAXK + 1) * 2048;   // the one-token kernel's tagged copy of x: th words DEC_TX .. + 7168
-static_assert(DEC_TX + 7168 <= DEC_TH, "tagged x inside th");
 hipError_t decode_init(int ncu, int * grid);
 // routing rules the decode block supports (its selection keeps the group scores in registers)
 bool decode_rule_ok(int n_exp, int n_group);
