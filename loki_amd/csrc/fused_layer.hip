@@ -235,7 +235,7 @@ int route_dev(FLCtx * c, const float * W, const float * bias, const float * x, i
                                    c->epoch, c->rcnt.p, done, c->derr.p, c->herr ? c->herr_dev : nullptr, c->st));
         return FL_OK;
     }
-    double * rp = nullptr;   // the K-split tiles' parts (n from RL_SPLIT_MIN to 1023)
+    double * rp = nullptr;   // the K-split tiles' parts (n from RL_SPLIT_MIN to RL_SPLIT_MAX)
     if (const size_t nd = router_split_doubles(n, n_exp, E)) { ALLOC(c, c->rpart, nd); rp = c->rpart.p; }
     TRY(c, launch_router_logits(W, x, n, n_exp, E, logits, rp, c->st));
     TRY(c, launch_router_select(logits, bias, n, n_exp, c->n_group, c->topk_group, c->topk, c->scale, probs, sel, w, c->st));
@@ -585,7 +585,7 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     TRY(c, launch_quant_q8k(x, n, E, c->xq.p, c->xd.p, st));
     if (mfma) { TRY(c, launch_q8_to_h(c->xq.p, c->xh.p, (int64_t) n * E, st)); }
     prof_mark(c, ev, 1);
-    double * rp = nullptr;   // the K-split tiles' parts (n from RL_SPLIT_MIN to 1023)
+    double * rp = nullptr;   // the K-split tiles' parts (n from RL_SPLIT_MIN to RL_SPLIT_MAX)
     if (const size_t nd = router_split_doubles(n, ne, E)) { ALLOC(c, c->rpart, nd); rp = c->rpart.p; }
     TRY(c, launch_router_logits(L->gate_inp, x, n, ne, E, c->logits.p, rp, st));
     prof_mark(c, ev, 2);
