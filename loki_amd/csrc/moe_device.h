@@ -392,13 +392,23 @@ __device__ __forceinline__ float fold_quad(float acc, float t) {
 // row_newbcast from the lane that holds it -- one LDS read per block instead of 16. Staged dword 16 L + 2 ib + hi
 // (group L, sub-block ib, weights 0..3 / 4..7) lives in lane 4 L + ib / 2, register 2 (ib & 1) + hi.
 template <int CTRL> __device__ __forceinline__ int dppi(int v) { return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false); }
+// acc += dot4(x of lane SRC of this lane's DPP row, w): v_dot4c_i32_i8 with the broadcast as its DPP source modifier,
+// one instruction where v_mov_b32_dpp + v_dot4c took two (the compiler does not fold row_newbcast into the dot; the
+// block product is VALU-bound at 16 waves per CU, and this removes 64 of its ~300 instructions per 256 weights).
+// The DPP source must not be written by a VALU instruction in the two wait states before: the compiler does not see
+// the DPP inside the asm, so the callers pass LDS-loaded words (xq, from ds_read), and tests/test_isa.py checks the
+// built library's disassembly for such a write.
+template <int SRC> __device__ __forceinline__ int dot4_bcast(int acc, uint32_t x, uint32_t w) {
+    asm("v_dot4c_i32_i8_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(x), "v"(w), "i"(SRC));
+    return acc;
+}
 template <int L, int IB, int IBE = 8>
 __device__ __forceinline__ void dot_ib_dpp(const uint2 (&g)[8], const uint4 (&m)[8], const uint32_t (&xq)[4], int (&acc)[8]) {
     if constexpr (IB < IBE) {
         uint32_t lo, hi; iq2_apply(g[IB], m[IB], lo, hi);
         constexpr int SRC = 4 * L + IB / 2;
-        acc[IB] = __builtin_amdgcn_sdot4(dppi<0x150 + SRC>((int) xq[2 * (IB & 1)]), (int) lo, acc[IB], false);
-        acc[IB] = __builtin_amdgcn_sdot4(dppi<0x150 + SRC>((int) xq[2 * (IB & 1) + 1]), (int) hi, acc[IB], false);
+        acc[IB] = dot4_bcast<SRC>(acc[IB], xq[2 * (IB & 1)], lo);
+        acc[IB] = dot4_bcast<SRC>(acc[IB], xq[2 * (IB & 1) + 1], hi);
         dot_ib_dpp<L, IB + 1, IBE>(g, m, xq, acc);
     }
 }
