@@ -55,7 +55,7 @@ struct FLCtx {
     DBuf<float> terms; DBuf<unsigned> cnt;   // per-pass expert kernels: (unused) term scratch, self-resetting counters
     DBuf<uint4> tab;                         // LDS table image (build_table_image)
     // single-launch decode block: epoch-tagged logits / h / o, wait-timeout word; fused = 0 forces the per-pass kernels
-    DBuf<int> derr; DBuf<uint64_t> dlogit, dth, dto; unsigned epoch = 0; int fused = 2; int dec_grid = -1;
+    DBuf<int> derr; DBuf<uint64_t> dlogit, dth, dto, dxq; unsigned epoch = 0; int fused = 2; int dec_grid = -1;
     int d1 = 1, d1_ok = -1;   // decode-1 kernel organised by XCD (fl_set_decode1); availability on this device
     // pinned, device-mapped copy of the last code a kernel reported (null if the host allocation failed): every
     // fl_moe_layer call checks it without waiting for the stream, fl_sync reports and clears it

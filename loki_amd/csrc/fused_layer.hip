@@ -125,7 +125,7 @@ extern "C" void fl_free(FLCtx * c) {
     c->sel8.release(); c->w8.release();
     c->sel.release(); c->counts.release(); c->offsets.release(); c->perm.release(); c->inv.release(); c->act.release(); c->nact.release();
     compat_free(c); c->zero_i.release(); c->terms.release(); c->cnt.release();
-    c->tab.release(); c->derr.release(); c->dlogit.release(); c->dth.release(); c->dto.release();
+    c->tab.release(); c->derr.release(); c->dlogit.release(); c->dth.release(); c->dto.release(); c->dxq.release();
     c->ptab.release(); c->pcols.release(); c->pncols.release(); c->xh.release(); c->hh.release();
     c->ksg.release(); c->ksu.release(); c->rcnt.release(); c->rpart.release(); c->dscr.release();
     for (auto & v : c->ev_free) { for (auto e : v) { (void) hipEventDestroy(e); } }
@@ -376,20 +376,30 @@ static bool decode1_ready(FLCtx * c) {
 // first use and whenever the epoch wraps, so no stale word can carry the new epoch)
 static int decode_tagged(FLCtx * c, hipStream_t st) {
     if (!c->derr.p) { ALLOC(c, c->derr, 1); TRY(c, hipMemsetAsync(c->derr.p, 0, sizeof(int), st)); }
-    if (!c->dlogit.p) { ALLOC(c, c->dlogit, DEC_TLOGITS); ALLOC(c, c->dth, DEC_TH); ALLOC(c, c->dto, DEC_TO); c->epoch = 0; }
+    if (!c->dlogit.p) {
+        ALLOC(c, c->dlogit, DEC_TLOGITS); ALLOC(c, c->dth, DEC_TH); ALLOC(c, c->dto, DEC_TO); ALLOC(c, c->dxq, decode_xq_bytes() / 8);
+        c->epoch = 0;
+    }
     if (++c->epoch == 0) { c->epoch = 1; }   // epoch 0 is the cleared state of the tagged words
     if (c->epoch == 1) {
         TRY(c, hipMemsetAsync(c->dlogit.p, 0, DEC_TLOGITS * sizeof(uint64_t), st));
         TRY(c, hipMemsetAsync(c->dth.p, 0, DEC_TH * sizeof(uint64_t), st));
         TRY(c, hipMemsetAsync(c->dto.p, 0, DEC_TO * sizeof(uint64_t), st));
+        TRY(c, hipMemsetAsync(c->dxq.p, 0, decode_xq_bytes(), st));   // its tagged words
     }
     return FL_OK;
+}
+// the n <= 8 block may share each XCD's Q8_K of the tokens: a grid of 256 workgroups that the dispatch places
+// round-robin over the 8 XCDs (decode1_init's probe)
+static uint8_t * decode_xq(FLCtx * c) {
+    if (c->d1_ok < 0) { (void) decode1_ready(c); }
+    return c->dec_grid == 256 && c->d1_ok > 0 ? reinterpret_cast<uint8_t *>(c->dxq.p) : nullptr;
 }
 bool decode1_available(FLCtx * c) { return c->fused != 0 && decode_ready(c) && decode1_ready(c); }
 bool decode_block_available(FLCtx * c) { return c->fused != 0 && decode_ready(c); }
 int decode_picks(FLCtx * c, DecodeArgs & d) {
     if (int rc = decode_tagged(c, c->st)) { return rc; }
-    d.tab = c->tab.p; d.tlogits = c->dlogit.p; d.th = c->dth.p; d.to = c->dto.p;
+    d.tab = c->tab.p; d.tlogits = c->dlogit.p; d.th = c->dth.p; d.to = c->dto.p; d.xqx = decode_xq(c);
     d.epoch = c->epoch; d.err = c->derr.p; d.herr = c->herr ? c->herr_dev : nullptr;
     if (d.n == 1 && d.topk == MAXK && d.keep == MAXK && decode1_ready(c)) {
         TRY(c, launch_moe_decode1(d, c->fused == 1, c->st));
@@ -563,7 +573,7 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
         d.E = E; d.H = H;
         d.xq = c->xq.p; d.xd = c->xd.p; d.logits = c->logits.p; d.probs = c->probs.p; d.sel = c->sel.p; d.wts = c->wts.p;
         d.counts = c->counts.p; d.offsets = c->offsets.p; d.perm = c->perm.p; d.inv = c->inv.p; d.act = c->act.p; d.nact = c->nact.p;
-        d.tlogits = c->dlogit.p; d.th = c->dth.p; d.to = c->dto.p; d.y = y;
+        d.tlogits = c->dlogit.p; d.th = c->dth.p; d.to = c->dto.p; d.xqx = decode_xq(c); d.y = y;
         d.epoch = c->epoch; d.err = c->derr.p; d.herr = c->herr ? c->herr_dev : nullptr;
         // stages: the whole block is one launch, reported as stage 4; the others are empty
         for (int i = 0; i <= 4; ++i) { prof_mark(c, ev, i); }

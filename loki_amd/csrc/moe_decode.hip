@@ -194,18 +194,34 @@ __device__ __forceinline__ void local_quant(const DArgs & a, lds_t lds, int wave
     constexpr int MAXP = DMAX_N * GG::NB / (4 * DW);
     static_assert(GG::NB % 4 == 0 && MAXP * 4 * DW == DMAX_N * GG::NB, "four blocks per pass");
     const int nblk = a.n * GG::NB, lane = lane_id(), i = lane & 15;
-    float xs[MAXP][16];
+    // every pass's loads are issued before any value is used (with the prenorm input transform applied per load the
+    // compiler waited for each load before issuing the next)
+    float4 xv[MAXP][4];
 #pragma unroll
     for (int p = 0; p < MAXP; ++p) {
         const int k = 4 * (wave + DW * p) + (lane >> 4);
         if (4 * (wave + DW * p) < nblk) {
-            const int col = (k % GG::NB) * QK + 16 * i;
-            const float * src = a.x + (size_t) (k / GG::NB) * DE + col;
+            const float * src = a.x + (size_t) (k / GG::NB) * DE + (k % GG::NB) * QK + 16 * i;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float4 v = block_in(a, lds, k / GG::NB, col + 4 * q, gloadf4(src + 4 * q));
-                xs[p][4 * q] = v.x; xs[p][4 * q + 1] = v.y; xs[p][4 * q + 2] = v.z; xs[p][4 * q + 3] = v.w;
+            for (int q = 0; q < 4; ++q) { xv[p][q] = gloadf4(src + 4 * q); }
+        }
+    }
+    if (a.prenorm) {
+#pragma unroll
+        for (int p = 0; p < MAXP; ++p) {
+            const int k = 4 * (wave + DW * p) + (lane >> 4);
+            if (4 * (wave + DW * p) < nblk) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) { xv[p][q] = block_in(a, lds, k / GG::NB, (k % GG::NB) * QK + 16 * i + 4 * q, xv[p][q]); }
             }
+        }
+    }
+    float xs[MAXP][16];
+#pragma unroll
+    for (int p = 0; p < MAXP; ++p) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            xs[p][4 * q] = xv[p][q].x; xs[p][4 * q + 1] = xv[p][q].y; xs[p][4 * q + 2] = xv[p][q].z; xs[p][4 * q + 3] = xv[p][q].w;
         }
     }
 #pragma unroll
@@ -225,6 +241,83 @@ __device__ __forceinline__ void local_quant(const DArgs & a, lds_t lds, int wave
         }
     }
 }
+
+// XCD-shared Q8_K of the tokens (a.xqx): workgroup (x, li) -- x its XCD (hardware register XCC_ID), li = b / 8 --
+// quantises blocks li, li + 32, .. of the n tokens (block k: token k / 28, block k % 28), one per 16-lane row
+// (q8k_row16, as local_quant), into XCD x's copy of the staged token rows, waits for those stores (vmcnt(0): acknowledged
+// by the XCD's L2) and tags each block's word with the launch's epoch (a plain store, read in the same L2). Every
+// workgroup of the XCD then polls the tagged words of all n * 28 blocks and copies the rows into its LDS with direct
+// loads (the launch started with an invalidated L1, and nothing of the copy was read before the tags: the loads come
+// from the L2). One quantisation per block per XCD instead of per workgroup: local_quant costs every workgroup ~8 us
+// at n = 8. Returns false on a timed-out wait.
+constexpr size_t XQX_ROWS = (size_t) DMAX_N * GG::XROW;                          // staged rows of the n tokens
+constexpr size_t XQX_BYTES = (XQX_ROWS + (size_t) DMAX_N * GG::NB * 8 + 255) / 256 * 256;   // + one tagged word per block
+static_assert(XQX_ROWS % 16 == 0 && GG::XROW % 16 == 0, "16-byte copies of the staged rows");
+__device__ __forceinline__ int xcc_id_d() {
+    unsigned x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return (int) (x & 0xFu);
+}
+__device__ __forceinline__ bool xcd_quant(const DArgs & a, lds_t lds, int wave) {
+    const int lane = lane_id(), i = lane & 15, nblk = a.n * GG::NB, xcd = xcc_id_d(), li = (int) blockIdx.x / 8;
+    uint8_t * mir = a.xqx + (size_t) xcd * XQX_BYTES;
+    uint64_t * tags = reinterpret_cast<uint64_t *>(mir + XQX_ROWS);
+    // produce: block k = li + 32 (4 wave + row)
+    const int k = li + 32 * (4 * wave + (lane >> 4));
+    if (4 * wave * 32 + li < nblk) {   // this wave has at least one block (rows past nblk idle)
+        float4 xv[4];
+        const int t = k < nblk ? k / GG::NB : 0, j = k < nblk ? k % GG::NB : 0;
+        const float * src = a.x + (size_t) t * DE + j * QK + 16 * i;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) { xv[q] = k < nblk ? gloadf4(src + 4 * q) : make_float4(0.f, 0.f, 0.f, 0.f); }
+        if (a.prenorm && k < nblk) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) { xv[q] = block_in(a, lds, t, j * QK + 16 * i + 4 * q, xv[q]); }
+        }
+        float xs[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) { xs[4 * q] = xv[q].x; xs[4 * q + 1] = xv[q].y; xs[4 * q + 2] = xv[q].z; xs[4 * q + 3] = xv[q].w; }
+        uint32_t packed[4]; float d;
+        q8k_row16(xs, packed, d);   // (every lane of the wave joins the row reductions)
+        if (k < nblk) {
+            uint8_t * row = mir + (size_t) t * GG::XROW;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) { *gptr(reinterpret_cast<uint32_t *>(row + j * GG::XBLK + staged_word(4 * i + w))) = packed[w]; }
+            if (i == 0) { *gptr(reinterpret_cast<float *>(row + GG::NB * GG::XBLK + 4 * j)) = d; }
+            if (xcd == 0) {   // the layer's xq / xd (XCD 0's producers)
+                *(LK_GLOBAL u32x4 *) (a.xq + (size_t) t * DE + (size_t) j * QK + 16 * i) = u32x4{ packed[0], packed[1], packed[2], packed[3] };
+                if (i == 0) { gptr(a.xd)[k] = d; }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): the block's stores are in the L2
+        if (k < nblk && i == 0) {
+            __hip_atomic_store(gptr(tags + k), (uint64_t) a.epoch << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+    }
+    // consume: every block tagged, then the rows into LDS (16 bytes per lane per copy, wave-interleaved)
+    constexpr int TPL = (DMAX_N * GG::NB + 63) / 64;   // tags per lane
+    bool ok = false;
+    for (int it = 0; it < POLL_MAX; ++it) {
+        bool v = true;
+#pragma unroll
+        for (int q = 0; q < TPL; ++q) {
+            const int kk = lane + 64 * q;
+            if (kk < nblk) { v = v && tag_ok(ld_tag(tags + kk), a.epoch); }
+        }
+        if (__ballot(!v) == 0) { ok = true; break; }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if (!ok) { return false; }
+    const int nchunk = (int) (a.n * GG::XROW / 1024), tail = (int) (a.n * GG::XROW % 1024);
+    for (int c = wave; c < nchunk; c += DW) {
+        __builtin_amdgcn_global_load_lds((const LK_GLOBAL void *) (mir + (size_t) c * 1024 + 16 * lane), (LK_LOCAL void *) (lds + L_XS + c * 1024), 16, 0, 0);
+    }
+    if (tail && wave == (nchunk % DW) && 16 * lane < tail) {
+        *reinterpret_cast<LK_LOCAL u32x4 *>(lds + L_XS + nchunk * 1024 + 16 * lane) = *(const LK_GLOBAL u32x4 *) (mir + (size_t) nchunk * 1024 + 16 * lane);
+    }
+    return true;
+}
+size_t decode_xq_bytes() { return 8 * XQX_BYTES; }
 
 // Router logits of expert e for all n tokens by the whole workgroup (the contract of moe_device.h: 256 in-order chunk
 // sums, pairwise tree, one rounding). Thread (quarter w = wave & 3, lane) owns chunk 64 w + lane (K/256 = 28 values)
@@ -727,7 +820,11 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
     float bv[4]; uint64_t pw[4];
     if (wave < n && !a.ext_sel) { load_bias(a.bias, a.n_exp, bv); probs_issue(a, wave, pw); }
     TRACE(wave, 9);
-    local_quant(a, lds, wave);
+    if (a.xqx) {
+        if (!xcd_quant(a, lds, wave)) { report(a, 64); }
+    } else {
+        local_quant(a, lds, wave);
+    }
     TRACE(wave, 10);
     __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's table loads have landed in LDS
     lds_arrive(ctl + 0, DW);              // [0] counts the waves whose tokens and table share are in LDS

@@ -288,12 +288,18 @@ __device__ __forceinline__ void quant1(const D1Args & a, lds1_t lds, int w4) {
     const int lane = lane_id(), i = lane & 15;
     for (int p = w4; p < NBX1 / 4; p += NQW1) {
         const int j = 4 * p + (lane >> 4), col = j * QK + 16 * i;
+        // the four loads are issued before any is used (with the input transform applied per load the compiler
+        // waited for each load before issuing the next)
+        float4 xv[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) { xv[q] = gloadf4(a.x + col + 4 * q); }
+        if (a.prenorm) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) { xv[q] = in1(a, lds, col + 4 * q, xv[q]); }
+        }
         float xs[16];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float4 v = in1(a, lds, col + 4 * q, gloadf4(a.x + col + 4 * q));
-            xs[4 * q] = v.x; xs[4 * q + 1] = v.y; xs[4 * q + 2] = v.z; xs[4 * q + 3] = v.w;
-        }
+        for (int q = 0; q < 4; ++q) { xs[4 * q] = xv[q].x; xs[4 * q + 1] = xv[q].y; xs[4 * q + 2] = xv[q].z; xs[4 * q + 3] = xv[q].w; }
         uint32_t packed[4]; float d;
         q8k_row16(xs, packed, d);
 #pragma unroll

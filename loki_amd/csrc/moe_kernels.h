@@ -104,6 +104,10 @@ struct DecodeArgs {
     // epoch-tagged words {epoch << 32 | 32-bit payload}: probabilities [n][n_exp], h [P+n][H] and o [P+n][E] per
     // dispatch slot
     uint64_t * tlogits, * th, * to;
+    // the n <= 8 block's XCD-shared Q8_K of the tokens (null: every workgroup quantises all of them): per XCD a copy
+    // of the staged token rows plus one epoch-tagged word per block (decode_xq_bytes() in all); only for a grid of 256
+    // workgroups placed round-robin over the 8 XCDs (decode1_init's probe)
+    uint8_t * xqx;
     float * y;                                       // [n][E]
     unsigned epoch; int * err;
     int * herr;                                      // host-mapped copy of a reported error code (may be null): the
@@ -116,6 +120,7 @@ hipError_t decode_init(int ncu, int * grid);
 // routing rules the decode block supports (its selection keeps the group scores in registers)
 bool decode_rule_ok(int n_exp, int n_group);
 size_t decode_lds_bytes();
+size_t decode_xq_bytes();
 // grid workgroups (at most one per CU can be resident): a cooperative launch guarantees they are all resident; a
 // regular launch assumes it (nothing else running on the CUs) -- a violation ends in a reported wait timeout
 hipError_t launch_moe_decode(const DecodeArgs & a, int grid, bool cooperative, hipStream_t st);
