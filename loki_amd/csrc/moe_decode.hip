@@ -57,7 +57,7 @@ constexpr int L_NRM = L_CTL + (8 + DW) * 4;                       // pre-norm sc
 constexpr int L_EXT = L_NRM + DMAX_N * 4, EXT_TOK = 2 * MAXK + 1;
 constexpr int DEC_LDS = L_EXT + DMAX_N * EXT_TOK * 4;
 static_assert(DEC_LDS <= 160 * 1024, "LDS budget");
-static_assert(DMAX_N * 4 * 8 <= PRE_BYTES, "router sums overlay the early task terms");
+static_assert(DMAX_N * 4 * 8 <= PRE_BYTES && DW * 112 * 4 <= PRE_BYTES, "router sums and selection scratch overlay the early task terms");
 
 typedef LK_LOCAL uint8_t * lds_t;
 typedef LK_CONST DecodeArgs DArgs;   // the launch arguments, read in place with scalar loads
@@ -865,8 +865,18 @@ __global__ void __launch_bounds__(DNT, 1) k_moe_decode(const DecodeArgs args) {
                 // with --share-experts every pick first (stride topk), the keep across the rows then runs in the
                 // dispatch wave
                 const int ks = a.share ? a.topk : a.keep;
-                select_token_p<false>(pv, bv, a.n_exp, a.n_group, a.topk_group, a.topk, a.scale, nullptr, (int *) (rt.sel + wave * ks),
-                                      (float *) (rt.wts + wave * ks), ks, a.share ? 0.f : a.renorm);
+                int * so = (int *) (rt.sel + wave * ks); float * wo = (float *) (rt.wts + wave * ks);
+                // DeepSeek's rule with every pick kept: the threshold selection (select_ds8, the same picks and
+                // weights in fewer dependent steps), its scratch in the early shared task's area (unused: no wave is
+                // without a token)
+                bool done = false;
+                if (!pre && a.n_exp == 256 && a.n_group == 8 && a.topk_group == 4 && a.topk == MAXK && ks == MAXK) {
+                    done = select_ds8(pv, bv, a.scale, reinterpret_cast<LK_LOCAL uint32_t *>(lds + L_PRE) + wave * 112, so, wo);
+                }
+                if (!done) {
+                    select_token_p<false>(pv, bv, a.n_exp, a.n_group, a.topk_group, a.topk, a.scale, nullptr, so, wo, ks,
+                                          a.share ? 0.f : a.renorm);
+                }
             } else if (lane == 0) {
                 __hip_atomic_fetch_or(ctl + 3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
