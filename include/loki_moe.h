@@ -248,7 +248,9 @@ typedef struct FLDebug {
                                                         * 3 that block launched by fl_ffn_begin on its own picks (fl_moe) */
 } FLDebug;
 int fl_debug(FLCtx *, FLDebug * out);
-int fl_set_debug(FLCtx *, int capture_gate_up);
+/* flags: bit 0 = capture the per-pass gate / up outputs (fl_debug's g, u); bit 1 = cap the y extent of the row-looping
+ * combine / scatter grids at 7 (for every context of the process: tests of their row loops at small sizes) */
+int fl_set_debug(FLCtx *, int flags);
 /* decode batches (n <= 8, E 7168, H 2048) of fl_moe_layer: 2 (default) = the whole block as one regular launch of one
  * workgroup per CU (assumes nothing else occupies the CUs, as in a single-stream engine); 1 = the same kernel as a
  * cooperative launch (residency guaranteed by the runtime, ~18 us more per call at batch 1); 0 = one launch per pass.

@@ -969,7 +969,7 @@ extern "C" void fl_wide_moe(FLCtx * c, const void * gate, const void * up, const
     const Arena ar = pack_arena(c, s, gate, up, down, nexp, down_fmt);
     routed_experts(c, s, ar, s->xq_all.p, s->xd_all.p, s->wmax, P, KE, nexp, s->w_act.p, s->w_nact.p, s->w_off.p, s->w_perm.p, s->o.p,
                    down_fmt, down, max_slots);
-    k_wide_scatter<<<dim3((E_ / 4 + 255) / 256, std::min(P, 65535)), 256, 0, st>>>(s->o.p, s->w_row.p, s->w_k.p, s->w_wk.p, P, KE, s->out_all.p);
+    k_wide_scatter<<<dim3((E_ / 4 + 255) / 256, grid_y(P)), 256, 0, st>>>(s->o.p, s->w_row.p, s->w_k.p, s->w_wk.p, P, KE, s->out_all.p);
     CK(hipGetLastError());
     // no wait: the reference's call only enqueues too (src/fused_layer.cu:528-555); fl_wide_mark / fl_wide_wait order
     // the engine's reuse of its staging and of these tables

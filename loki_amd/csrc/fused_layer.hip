@@ -196,7 +196,12 @@ extern "C" int fl_set_experts(FLCtx * c, int n_exp) {
     if (n_exp <= 0 || n_exp > NEXP_MAX) { return fail(c, FL_EINVAL, "n_exp %d outside 1..%d", n_exp, NEXP_MAX); }
     c->n_exp = n_exp; return FL_OK;
 }
-extern "C" int fl_set_debug(FLCtx * c, int capture) { if (!c) { return FL_EINVAL; } c->dbg_gu = capture ? 1 : 0; return FL_OK; }
+extern "C" int fl_set_debug(FLCtx * c, int flags) {
+    if (!c) { return FL_EINVAL; }
+    c->dbg_gu = (flags & 1) ? 1 : 0;
+    set_grid_ycap((flags & 2) ? 7 : 65535);   // process-wide: the row loops of the combine / scatter kernels at small sizes
+    return FL_OK;
+}
 extern "C" int fl_set_prefill_mfma(FLCtx * c, int on) { if (!c) { return FL_EINVAL; } c->pf_mfma = on ? 1 : 0; return FL_OK; }
 extern "C" int fl_set_decode1(FLCtx * c, int on) { if (!c) { return FL_EINVAL; } c->d1 = on ? 1 : 0; return FL_OK; }
 extern "C" int fl_set_fused(FLCtx * c, int mode) {

@@ -299,14 +299,20 @@ __global__ void __launch_bounds__(256) k_combine1(const float * __restrict__ o, 
     }
 }
 
+// the y extent of the row-looping grids (k_combine, k_combine1, k_wide_scatter): the hardware's 65535, or a small cap
+// that a test sets (fl_set_debug) so that the loops over rows run at small sizes too
+static int g_grid_ycap = 65535;
+void set_grid_ycap(int cap) { g_grid_ycap = cap >= 1 && cap <= 65535 ? cap : 65535; }
+unsigned grid_y(int rows) { return (unsigned) std::min(rows, g_grid_ycap); }
+
 hipError_t launch_combine(const float * o, const int * inv, const float * wts, int n, int topk, int E, int P,
                           const float * resid, float * y, float * moe, hipStream_t st) {
     if ((int64_t) n * E <= 0) { return hipSuccess; }
     if (E % 4 == 0 && ((reinterpret_cast<uintptr_t>(o) | reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(moe) |
                         reinterpret_cast<uintptr_t>(resid)) & 15u) == 0) {
-        k_combine<<<dim3((unsigned) ((E / 4 + 255) / 256), (unsigned) std::min(n, 65535)), 256, 0, st>>>(o, inv, wts, n, topk, E, P, resid, y, moe);
+        k_combine<<<dim3((unsigned) ((E / 4 + 255) / 256), grid_y(n)), 256, 0, st>>>(o, inv, wts, n, topk, E, P, resid, y, moe);
     } else {
-        k_combine1<<<dim3((unsigned) ((E + 255) / 256), (unsigned) std::min(n, 65535)), 256, 0, st>>>(o, inv, wts, n, topk, E, P, resid, y, moe);
+        k_combine1<<<dim3((unsigned) ((E + 255) / 256), grid_y(n)), 256, 0, st>>>(o, inv, wts, n, topk, E, P, resid, y, moe);
     }
     return hipGetLastError();
 }

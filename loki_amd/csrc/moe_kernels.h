@@ -170,6 +170,9 @@ hipError_t kq_gemm_init();
 hipError_t launch_kq_gemm(const PrefillArgs & a, int fmt, int grid, hipStream_t st);
 
 // y[t] = sum_k (o[inv[t*topk+k]] * w[t][k]) in k order + o[P+t] (+ resid[t] when given)
+// grid y extent of the row-looping kernels: min(rows, cap); the cap is 65535 unless a test lowers it
+void set_grid_ycap(int cap);
+unsigned grid_y(int rows);
 hipError_t launch_combine(const float * o, const int * inv, const float * wts, int n, int topk, int E, int P,
                           const float * resid, float * y, float * moe, hipStream_t st);
 

@@ -229,6 +229,16 @@ def test_wide_pass(ctx, small_layer, waits, mfma):
         ctx.set_prefill_mfma(True)
 
 
+def test_wide_pass_row_loop(ctx, small_layer):
+    """The wide pass's scatter kernel loops over (row, k) pairs beyond its grid's y extent (65535 pairs); with the extent
+    capped at 7 (fl_set_debug bit 1) the loop runs over the 320 pairs here, and every output still equals the checker's."""
+    ctx.set_debug(False, small_grids=True)
+    try:
+        _wide_pass(ctx, small_layer, True)
+    finally:
+        ctx.set_debug(False)
+
+
 def _wide_pass(ctx, small_layer, waits):
     from loki_amd import FLOut, lib
     (W, b, gate, up, down, sh), dev = small_layer

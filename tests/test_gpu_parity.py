@@ -227,6 +227,27 @@ def test_combine_unaligned_output(ctx):
     assert np.array_equal(gotn.view(np.uint32), refn.view(np.uint32))
 
 
+def test_combine_row_loops(ctx):
+    """The k-ordered combine kernels loop over token rows beyond their grid's y extent (65535 rows); with the extent
+    capped at 7 (fl_set_debug bit 1) the loops run at prefill-40: y bit-identical to the uncapped call, for an aligned
+    output (the 4-wide kernel) and one 4 bytes off (the one-column kernel)."""
+    import torch
+    n = 40
+    layer = make_layer(ctx, seed=952, bias_sigma=0.05)
+    x = make_x(ctx, n, seed=953)
+    ref = ctx.moe_layer(layer, x).cpu().numpy()
+    y1 = torch.empty(n * E + 1, dtype=torch.float32, device="cuda")[1:].view(n, E)
+    ctx.set_debug(False, small_grids=True)
+    try:
+        got = ctx.moe_layer(layer, x).cpu().numpy()
+        got1 = ctx.moe_layer(layer, x, y1).cpu().numpy()
+        ctx.sync()
+    finally:
+        ctx.set_debug(False)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(got1.view(np.uint32), ref.view(np.uint32))
+
+
 @pytest.mark.parametrize("n,hot", [(9, False), (40, False), (512, False), (2048, True)])
 def test_prefill_mfma_matches_per_pass(ctx, n, hot):
     """The grouped GEMMs on the matrix cores reproduce the per-pass mat-vec kernels bit for bit: gate/up outputs, h and
