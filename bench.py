@@ -5,7 +5,8 @@ Default workload (the north star's target config, configs[0]): one MoE layer dec
 x [1, 7168] ~ N(0,1), fp32 router [256, 7168] ~ N(0, 0.02^2), bias ~ N(0, 0.01^2), grouped sigmoid routing
 (8 groups, top-4 groups, top-8, x2.5), 256 routed + 1 shared IQ2_XXS experts (gate/up [2048, 7168], down [7168, 2048],
 qs uniform bytes, d = fp16(|N(0, 0.002^2)|)). All inputs are generated on the device and resident in HBM before the
-timed region. Each step takes a fresh x (so different experts) and the steps rotate over --copies independently seeded
+timed region. Before each workload's warm-up steps the GPU runs the same workload untimed for --preheat-ms (default
+100 ms): a cold GPU's first ~20-30 ms of load run at lower clocks. Each step takes a fresh x (so different experts) and the steps rotate over --copies independently seeded
 layers (3 x 2.9 GB), so the 256 MB MALL cannot serve repeated weights.
 
 Prints ONE JSON line: value = microseconds per token of the whole block (router, dispatch, experts, combine), plus the
@@ -102,6 +103,25 @@ def distinct_experts(ctx, layer, xs):
     return out
 
 
+PREHEAT_MS = 100.0   # --preheat-ms
+
+
+def preheat(torch, step):
+    """Runs step(i) untimed for PREHEAT_MS of wall time before a workload's warm-up steps. An idle MI355X runs its first
+    ~20-30 ms of load at lower clocks (measured: decode-8 per-50-step averages 216, 184, 174, 171, 170 us from a cold
+    start, decode-1 41.5, 33.5, 33.9, 32.6, 31.6, 30.8, 30.4, 30.2 us), so a handful of warm-up steps would time the
+    power management's ramp rather than the kernels; the timed steps themselves are unchanged."""
+    t0 = time.perf_counter()
+    i = 0
+    while True:
+        step(i)
+        i += 1
+        if i % 8 == 0:
+            torch.cuda.synchronize()
+            if (time.perf_counter() - t0) * 1e3 >= PREHEAT_MS:
+                return i
+
+
 def run_workload(ctx, torch, name, steps, warmup, copies, seed=20260101):
     from loki_amd import MoeLayerWeights
     n, bias_sigma, nhot, desc = WORKLOADS[name]
@@ -120,6 +140,7 @@ def run_workload(ctx, torch, name, steps, warmup, copies, seed=20260101):
         xs.append(x)
     y = torch.empty((n, E), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
+    preheat(torch, lambda i: ctx.moe_layer(layers[i % copies], xs[i % nx], y))
     for i in range(warmup):
         ctx.moe_layer(layers[i % copies], xs[i], y)
     torch.cuda.synchronize()
@@ -188,6 +209,7 @@ def run_stack(ctx, torch, steps, warmup, nlayers=STACK_LAYERS, seed=20260301, cp
         for i, L in enumerate(layers[1:]):
             ctx.moe_layer_normed(L, ys[i % 2], None, 1e-6, ys[(i + 1) % 2])
 
+    preheat(torch, lambda i: token(xs[i % len(xs)]))
     for i in range(warmup):
         token(xs[i])
     torch.cuda.synchronize()
@@ -717,7 +739,7 @@ def bench(args, ctx, torch):
         "data": "synthetic (device-generated, seeded; the benchmark configs' distribution)",
         "config": {"workload": res["desc"], "tokens": n, "hidden": E, "expert_ffn": H, "routed_experts": 256,
                    "shared_experts": 1, "routing": "sigmoid, 8 groups, top-4 groups, top-8, x2.5",
-                   "weights": "IQ2_XXS (activations Q8_K)", "layer_copies": args.copies},
+                   "weights": "IQ2_XXS (activations Q8_K)", "layer_copies": args.copies, "preheat_ms": args.preheat_ms},
         "hbm_gbs": head["hbm_gbs"],
         "hbm_frac": head["hbm_frac"],
         "distinct_experts": head["distinct_experts"],
@@ -753,7 +775,11 @@ def main():
                     help="decode path: 2 regular single launch (library default), 1 cooperative single launch, 0 per pass")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (the reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--preheat-ms", type=float, default=PREHEAT_MS,
+                    help="untimed load before each decode / prefill / stack workload's warm-up steps, so the timed steps run "
+                         "at the clocks of a loaded GPU (0: none)")
     args = ap.parse_args()
+    globals()["PREHEAT_MS"] = args.preheat_ms
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         log("bench.py: this build runs on one GPU only (the MoE block is not sharded across GPUs); got --gpus %d, "
