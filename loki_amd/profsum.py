@@ -11,7 +11,12 @@ bench.py in its JSON line), so bench.py can refuse figures that belong to anothe
   bench.py --copy-probe): `profiles/traffic_<key>_<workload>.json`. FETCH_SIZE and WRITE_SIZE are in KiB per dispatch;
   each is scaled by what the same counter reads for the probe's plain 1 GiB device copy (1 GiB read + 1 GiB written).
 
+* matrix-core, LDS and VALU counters (`rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F16
+  SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_ACTIVE_INST_LDS SQ_ACTIVE_INST_VALU SQ_BUSY_CU_CYCLES SQ_INSTS_LDS
+  GRBM_GUI_ACTIVE ...`, one run per workload): a markdown table `profiles/<out>.md`, one row per (workload, kernel).
+
 usage:
+  python -m loki_amd.profsum counters --out NAME --cmd "..." --last N WORKLOAD=DIR=LOG ... --kernels REGEX ...
   python -m loki_amd.profsum trace DIR --kernel REGEX --key KEY --workload W --last N --log BENCH_STDOUT --cmd "..." [--group G]
   python -m loki_amd.profsum traffic FETCH_DIR WRITE_DIR --kernel REGEX --key KEY --workload W --last N
          --alg BYTES --log-fetch LOG --log-write LOG --cmd-fetch "..." --cmd-write "..." [--notes "..."] [--group G]
@@ -174,6 +179,58 @@ def traffic(a):
     print(json.dumps(out, indent=1))
 
 
+PMC = ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_F16", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE",
+       "SQ_ACTIVE_INST_LDS", "SQ_ACTIVE_INST_VALU", "SQ_BUSY_CU_CYCLES", "SQ_INSTS_LDS", "GRBM_GUI_ACTIVE")
+
+
+def counters(a):
+    """Per (workload, kernel): the mean of each counter over the kernel's last N dispatches, then MFMA busy =
+    SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 x 1024 SIMDs) (GRBM_GUI_ACTIVE is summed over the 8 XCDs),
+    bank conflicts per LDS access = SQ_LDS_BANK_CONFLICT / (SQ_LDS_IDX_ACTIVE - SQ_LDS_BANK_CONFLICT), LDS / VALU
+    active = SQ_ACTIVE_INST_LDS / SQ_ACTIVE_INST_VALU over SQ_BUSY_CU_CYCLES."""
+    md = ["# %s -- rocprofv3 counters" % a.out, "",
+          "Command (repo root, on the MI355X box; WL = each workload below, one run each):", "", "    " + a.cmd, ""]
+    shas = set()
+    table = ["| workload | kernel | dispatches | MFMA busy | MFMA ops (F16 MOPs) | LDS instructions | LDS conflicts / access | "
+             "LDS active | VALU active |", "|---|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for spec in a.runs:
+        wl, d, log = spec.split("=")
+        shas.add(lib_of(log)[0])
+        rows = _counter_rows(d)
+        for krx in a.kernels:
+            rx = re.compile(krx)
+            names = sorted({r["Kernel_Name"] for r in rows if rx.search(r["Kernel_Name"])})
+            for name in names:
+                per = {}
+                for r in rows:
+                    if r["Kernel_Name"] == name and r["Counter_Name"] in PMC:
+                        per.setdefault(int(r["Dispatch_Id"]), {})[r["Counter_Name"]] = float(r["Counter_Value"])
+                ds = [per[k] for k in sorted(per) if len(per[k]) == len(PMC)][-a.last:]
+                if not ds:
+                    continue
+                m = {c: sum(x[c] for x in ds) / len(ds) for c in PMC}
+                busy = m["SQ_VALU_MFMA_BUSY_CYCLES"] / (m["GRBM_GUI_ACTIVE"] / 8 * 1024) if m["GRBM_GUI_ACTIVE"] else 0.0
+                acc = m["SQ_LDS_IDX_ACTIVE"] - m["SQ_LDS_BANK_CONFLICT"]
+                conf = m["SQ_LDS_BANK_CONFLICT"] / acc if acc > 0 else 0.0
+                cu = m["SQ_BUSY_CU_CYCLES"] or 1.0
+                table.append("| %s | `%s` | %d | %.1f %% | %.0f M | %.1f M | %.3f | %.0f %% | %.0f %% |" % (
+                    wl, _short(name), len(ds), 100 * busy, m["SQ_INSTS_VALU_MFMA_MOPS_F16"] / 1e6, m["SQ_INSTS_LDS"] / 1e6,
+                    conf, 100 * m["SQ_ACTIVE_INST_LDS"] / cu, 100 * m["SQ_ACTIVE_INST_VALU"] / cu))
+    md.insert(1, "Library `libloki_moe.so` sha256 prefix %s (the bench lines' `lib_sha16`)." % ", ".join("`%s`" % s for s in sorted(shas)))
+    md.insert(2, "")
+    md += table + ["", counters.__doc__.split("\n", 1)[0].strip().replace("Per (workload, kernel): t", "T") + " " +
+                   " ".join(l.strip() for l in counters.__doc__.split("\n")[1:]) + " Mean of the last %d dispatches." % a.last]
+    if a.notes:
+        md += ["", a.notes]
+    with open(os.path.join(PROFILES, a.out + ".md"), "w") as f:
+        f.write("\n".join(md) + "\n")
+    print("\n".join(table))
+
+
+def _counter_rows(d):
+    return list(csv.DictReader(open(_find(d, "counter_collection.csv"))))
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description="rocprofv3 output -> profiles/ summaries")
     sub = ap.add_subparsers(dest="what", required=True)
@@ -194,8 +251,15 @@ def main(argv=None):
     p.add_argument("--group", type=int, default=1, help="kernels per step, summed (consecutive dispatches)")
     p.add_argument("--alg", type=int, required=True)
     p.add_argument("--notes", default="")
+    c = sub.add_parser("counters")
+    c.add_argument("runs", nargs="+", help="WORKLOAD=DIR=BENCH_LOG")
+    c.add_argument("--kernels", nargs="+", required=True)
+    c.add_argument("--out", required=True)
+    c.add_argument("--cmd", required=True)
+    c.add_argument("--last", type=int, default=3)
+    c.add_argument("--notes", default="")
     a = ap.parse_args(argv)
-    (trace if a.what == "trace" else traffic)(a)
+    {"trace": trace, "traffic": traffic, "counters": counters}[a.what](a)
 
 
 if __name__ == "__main__":
