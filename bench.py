@@ -7,7 +7,7 @@ x [1, 7168] ~ N(0,1), fp32 router [256, 7168] ~ N(0, 0.02^2), bias ~ N(0, 0.01^2
 qs uniform bytes, d = fp16(|N(0, 0.002^2)|)). All inputs are generated on the device and resident in HBM before the
 timed region. Before each workload's warm-up steps the GPU runs the same workload untimed for --preheat-ms (default
 100 ms): a cold GPU's first ~20-30 ms of load run at lower clocks. Each step takes a fresh x (so different experts) and the steps rotate over --copies independently seeded
-layers (3 x 2.9 GB), so the 256 MB MALL cannot serve repeated weights.
+layers (default 8 x 2.9 GB), so the 256 MB MALL cannot serve repeated weights.
 
 Prints ONE JSON line: value = microseconds per token of the whole block (router, dispatch, experts, combine), plus the
 achieved HBM bandwidth, the roofline of the dominant kernel (decode: the whole block in one launch, k_moe_decode1
@@ -645,6 +645,9 @@ def kernel_roofline(res):
             # the same kernel's average duration over the timed steps of a committed rocprofv3 kernel trace made with
             # this library (profiles/trace_*.json): the frac it implies, to set beside the live one
             "profile_avg_us": kt["avg_us_last"] if kt else None,
+            # (the median of the same launches: the protocol's statistic; an event between steps, the other way to
+            # get per-step times, adds microseconds to each)
+            "profile_median_us": kt["median_us_last"] if kt else None,
             "profile_frac": round(k_bytes / (kt["avg_us_last"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if kt else None,
             "profile_source": kt_src}
     return roof, stages
