@@ -162,11 +162,13 @@ int kq_block_bytes(int fmt) {
 hipError_t launch_kq_matvec(const KqArgs & args, int fmt, int max_slots, int grid_experts, hipStream_t st) {
     KqArgs a = args;
     if (a.K <= 0 || a.K % QK || a.K > QK * NB_MAX || a.R <= 0 || max_slots <= 0 || grid_experts <= 0 || kq_block_bytes(fmt) == 0) { return hipErrorInvalidValue; }
-    // rows per workgroup tile: RT_MAX when the launch has rows enough, else fewer so that it still spreads over
-    // ~1024 workgroups
-    const int64_t rows_total = (int64_t) a.R * (a.act ? grid_experts : (a.w2 ? 2 : 1));
-    a.rw = (int) std::max<int64_t>(1, std::min<int64_t>(RT_MAX, rows_total / 1024));
     const int tt = max_slots <= 1 ? 1 : max_slots <= 2 ? 2 : max_slots <= 4 ? 4 : 8;
+    // rows per workgroup tile: RT_MAX when the launch has rows enough, else fewer so that it still spreads over ~1024
+    // workgroups (~512 for token groups of 8: every workgroup loads the group's activations for its whole K range, so
+    // two rows per workgroup re-read them 5.8x the Q5_K weights' bytes; the 10 MB shared gate at 8 tokens takes 17.4 us
+    // over 1024 workgroups, 13.0 over 512, while a 1-token launch is fastest over 1024)
+    const int64_t rows_total = (int64_t) a.R * (a.act ? grid_experts : (a.w2 ? 2 : 1));
+    a.rw = (int) std::max<int64_t>(1, std::min<int64_t>(RT_MAX, rows_total / (tt >= 8 ? 512 : 1024)));
     const unsigned gy = a.act ? (unsigned) grid_experts : (a.w2 ? 2u : 1u);
     switch (fmt) {
         case KF_Q2K: return go_f<KF_Q2K>(a, tt, gy, st);
