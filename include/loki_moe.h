@@ -249,7 +249,9 @@ typedef struct FLDebug {
 } FLDebug;
 int fl_debug(FLCtx *, FLDebug * out);
 /* flags: bit 0 = capture the per-pass gate / up outputs (fl_debug's g, u); bit 1 = cap the y extent of the row-looping
- * combine / scatter grids at 7 (for every context of the process: tests of their row loops at small sizes) */
+ * combine / scatter grids at 7 (for every context of the process: tests of their row loops at small sizes); bit 2 = run
+ * the per-pass decode's K-quant shared expert on the context's stream, not on its second stream beside the routed
+ * launches (same results: tests compare the two) */
 int fl_set_debug(FLCtx *, int flags);
 /* decode batches (n <= 8, E 7168, H 2048) of fl_moe_layer: 2 (default) = the whole block as one regular launch of one
  * workgroup per CU (assumes nothing else occupies the CUs, as in a single-stream engine); 1 = the same kernel as a

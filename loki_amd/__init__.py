@@ -307,10 +307,12 @@ class Context:
         """Formats of fl_moe_layer's routed down and shared matrices (K-quants read in place, IQ2_XXS tiled)."""
         self.check(lib().fl_set_layer_formats(self.ctx, down, sh_gate, sh_up, sh_down))
 
-    def set_debug(self, capture_gate_up, small_grids=False):
+    def set_debug(self, capture_gate_up, small_grids=False, shared_on_stream=False):
         """capture_gate_up: keep the per-pass gate / up outputs (debug()); small_grids: the row-looping combine / scatter
-        kernels run with a y extent of 7 (process-wide), so their loops over rows are exercised at small sizes."""
-        self.check(lib().fl_set_debug(self.ctx, (1 if capture_gate_up else 0) | (2 if small_grids else 0)))
+        kernels run with a y extent of 7 (process-wide), so their loops over rows are exercised at small sizes;
+        shared_on_stream: the per-pass decode's K-quant shared expert runs on the context's stream instead of beside the
+        routed launches on a second stream."""
+        self.check(lib().fl_set_debug(self.ctx, (1 if capture_gate_up else 0) | (2 if small_grids else 0) | (4 if shared_on_stream else 0)))
 
     def set_prefill_mfma(self, on):
         """Batches above 8 tokens: True (default) = grouped GEMMs on the matrix cores, False = the per-pass kernels."""

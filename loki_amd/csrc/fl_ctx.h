@@ -34,6 +34,8 @@ template <class T> struct DBuf {
 
 struct FLCtx {
     hipStream_t st = nullptr, own = nullptr; int dev = 0, ncu = 0;
+    hipStream_t side = nullptr; hipEvent_t efork = nullptr, ejoin = nullptr;   // the per-pass decode's shared K-quant expert
+    int no_side = 0;                     // fl_set_debug bit 2: that expert on the context's stream instead
     hipEvent_t em0 = nullptr, em1 = nullptr;
     int n_group = 8, topk_group = 4, topk = 8; float scale = 2.5f;
     int keep = 0; float renorm = 0.f;   // fl_moe_layer keeps each row's `keep` heaviest experts (0: all topk)

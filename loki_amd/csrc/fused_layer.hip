@@ -91,6 +91,8 @@ extern "C" FLCtx * fl_init(int kvp, int sc_cap) {
     CK(hipGetDevice(&c->dev));
     CK(hipDeviceGetAttribute(&c->ncu, hipDeviceAttributeMultiprocessorCount, c->dev));
     CK(hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking)); c->st = c->own;
+    CK(hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking));
+    CK(hipEventCreateWithFlags(&c->efork, hipEventDisableTiming)); CK(hipEventCreateWithFlags(&c->ejoin, hipEventDisableTiming));
     CK(hipEventCreate(&c->em0)); CK(hipEventCreate(&c->em1));
     if (hipHostMalloc((void **) &c->herr, sizeof(int), hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess) {
         (void) hipGetLastError(); c->herr = nullptr;
@@ -132,6 +134,7 @@ extern "C" void fl_free(FLCtx * c) {
     for (auto & v : c->ev_pending) { for (auto e : v) { (void) hipEventDestroy(e); } }
     for (auto * l : { &c->ffn_ev_pending, &c->ffn_ev_free, &c->moe_ev_pending, &c->moe_ev_free }) { for (auto & e : *l) { (void) hipEventDestroy(e.first); (void) hipEventDestroy(e.second); } }
     (void) hipEventDestroy(c->em0); (void) hipEventDestroy(c->em1); (void) hipStreamDestroy(c->own);
+    (void) hipEventDestroy(c->efork); (void) hipEventDestroy(c->ejoin); (void) hipStreamDestroy(c->side);
     if (c->herr) { (void) hipHostFree(c->herr); }
     delete c;
 }
@@ -199,6 +202,7 @@ extern "C" int fl_set_experts(FLCtx * c, int n_exp) {
 extern "C" int fl_set_debug(FLCtx * c, int flags) {
     if (!c) { return FL_EINVAL; }
     c->dbg_gu = (flags & 1) ? 1 : 0;
+    c->no_side = (flags & 4) ? 1 : 0;
     set_grid_ycap((flags & 2) ? 7 : 65535);   // process-wide: the row loops of the combine / scatter kernels at small sizes
     return FL_OK;
 }
@@ -427,11 +431,11 @@ static hipError_t launch_decode(FLCtx * c, const DecodeArgs & d, hipStream_t st)
 // bytes of one R x K matrix in format f (IQ2_XXS or a K-quant)
 static size_t fmt_mat_bytes(int f, int R, int K) { return (size_t) R * (K / 256) * (size_t) (f == FL_IQ2 ? IQ2B : kq_block_bytes(f)); }
 // K-quant mat-vec of one matrix (ggml layout, in place) on n Q8_K rows -> out [n][R]
-static hipError_t kq_one(FLCtx * c, int fmt, const void * w, const int8_t * q, const float * d, int n, int K, int R, float * out) {
+static hipError_t kq_one(FLCtx * c, int fmt, const void * w, const int8_t * q, const float * d, int n, int K, int R, float * out, hipStream_t st) {
     KqArgs k{};
     k.w = (const uint8_t *) w; k.estride = fmt_mat_bytes(fmt, R, K); k.aq = q; k.ad = d; k.K = K; k.R = R;
     k.n = n; k.out = out; k.ldo = R;
-    return launch_kq_matvec(k, fmt, n, 1, c->st);
+    return launch_kq_matvec(k, fmt, n, 1, st);
 }
 
 // The shared expert outside the GEMM columns / the routed tasks (fl_moe_layer, formats c->lf), on the context's buffers.
@@ -439,8 +443,7 @@ static hipError_t kq_one(FLCtx * c, int fmt, const void * w, const int8_t * q, c
 // by one mat-vec launch for both matrices (or one each) and swiglu_q8k; IQ2_XXS by the per-pass kernel on an empty
 // routed list.
 // h = silu(g) * u of the shared expert's K-quant gate / up outputs (ksg, ksu) into rows P .. P + n - 1 of h and Q8_K(h)
-static int shared_swiglu(FLCtx * c, int n, int P, int H) {
-    hipStream_t st = c->st;
+static int shared_swiglu(FLCtx * c, int n, int P, int H, hipStream_t st) {
     TRY(c, launch_swiglu_q8k(c->ksg.p, c->ksu.p, n, H, c->h.p + (size_t) P * H, c->hq.p + (size_t) P * H, c->hd.p + (size_t) P * (H / 256), st));
     if (c->dbg_gu) {
         TRY(c, hipMemcpyAsync(c->g.p + (size_t) P * H, c->ksg.p, (size_t) n * H * 4, hipMemcpyDeviceToDevice, st));
@@ -448,8 +451,8 @@ static int shared_swiglu(FLCtx * c, int n, int P, int H) {
     }
     return FL_OK;
 }
-static int shared_gateup_sep(FLCtx * c, const FLMoeLayer * L, int n, int P, int E, int H, int tk) {
-    hipStream_t st = c->st; const int * lf = c->lf;
+static int shared_gateup_sep(FLCtx * c, const FLMoeLayer * L, int n, int P, int E, int H, int tk, hipStream_t st) {
+    const int * lf = c->lf;
     if (lf[1] == FL_IQ2) {
         ExpertArgs s = expert_args(c, n, P, 1);
         s.sh[0] = (const uint8_t *) L->sh_gate; s.sh[1] = (const uint8_t *) L->sh_up; s.aq = c->xq.p; s.ad = c->xd.p; s.K = E; s.R = H; s.nmat = 2;
@@ -467,15 +470,15 @@ static int shared_gateup_sep(FLCtx * c, const FLMoeLayer * L, int n, int P, int 
         k.aq = c->xq.p; k.ad = c->xd.p; k.K = E; k.R = H; k.n = n; k.out = c->ksg.p; k.out2 = c->ksu.p; k.ldo = H;
         TRY(c, launch_kq_matvec(k, lf[1], n, 1, st));
     } else {
-        TRY(c, kq_one(c, lf[1], L->sh_gate, c->xq.p, c->xd.p, n, E, H, c->ksg.p));
-        TRY(c, kq_one(c, lf[2], L->sh_up, c->xq.p, c->xd.p, n, E, H, c->ksu.p));
+        TRY(c, kq_one(c, lf[1], L->sh_gate, c->xq.p, c->xd.p, n, E, H, c->ksg.p, st));
+        TRY(c, kq_one(c, lf[2], L->sh_up, c->xq.p, c->xd.p, n, E, H, c->ksu.p, st));
     }
-    return shared_swiglu(c, n, P, H);
+    return shared_swiglu(c, n, P, H, st);
 }
 // Down: o rows P .. P + n - 1 from h's Q8_K (hq / hd rows P ..): a K-quant mat-vec, or the per-pass kernel alone.
-static int shared_down_sep(FLCtx * c, const FLMoeLayer * L, int n, int P, int E, int H, int tk) {
+static int shared_down_sep(FLCtx * c, const FLMoeLayer * L, int n, int P, int E, int H, int tk, hipStream_t st) {
     if (c->lf[3] != FL_IQ2) {
-        TRY(c, kq_one(c, c->lf[3], L->sh_down, c->hq.p + (size_t) P * H, c->hd.p + (size_t) P * (H / 256), n, H, E, c->o.p + (size_t) P * E));
+        TRY(c, kq_one(c, c->lf[3], L->sh_down, c->hq.p + (size_t) P * H, c->hd.p + (size_t) P * (H / 256), n, H, E, c->o.p + (size_t) P * E, st));
         return FL_OK;
     }
     ExpertArgs s = expert_args(c, n, P, 1);
@@ -483,7 +486,7 @@ static int shared_down_sep(FLCtx * c, const FLMoeLayer * L, int n, int P, int E,
     s.act = zero_int(c); s.nact = zero_int(c); s.offsets = zero_int(c); s.perm = zero_int(c); s.topk = tk;
     s.h = nullptr; s.hq = nullptr; s.hd = nullptr; s.o = c->o.p; s.y = nullptr;
     expert_counters(c, s, 1);
-    TRY(c, launch_experts_down(s, c->ncu, c->st));
+    TRY(c, launch_experts_down(s, c->ncu, st));
     return FL_OK;
 }
 // The routed down in a K-quant (src/fused_layer.cu:607-608): o of every routed slot, each active expert's slots in
@@ -639,9 +642,9 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
                 k.bh = c->xh.p; k.bd = c->xd.p; k.arow0 = P; k.orow0 = P; k.out = m ? c->ksu.p : c->ksg.p;
                 TRY(c, launch_kq_gemm(k, FL_Q5K, c->ncu, st));
             }
-            if (int rc = shared_swiglu(c, n, P, H)) { return rc; }
+            if (int rc = shared_swiglu(c, n, P, H, st)) { return rc; }
         } else if (lf[1] != FL_IQ2) {
-            if (int rc = shared_gateup_sep(c, L, n, P, E, H, tk)) { return rc; }
+            if (int rc = shared_gateup_sep(c, L, n, P, E, H, tk, st)) { return rc; }
         }
         TRY(c, launch_quant_q8k(c->h.p, (int64_t) rows, H, c->hq.p, c->hd.p, st));
         TRY(c, launch_q8_to_h(c->hq.p, c->hh.p, (int64_t) rows * H, st));
@@ -664,7 +667,7 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
             k.col0 = 0; k.col1 = nsh;
             TRY(c, launch_kq_gemm(k, lf[3], c->ncu, st));
         } else if (!sh_iq) {
-            if (int rc = shared_down_sep(c, L, n, P, E, H, tk)) { return rc; }
+            if (int rc = shared_down_sep(c, L, n, P, E, H, tk, st)) { return rc; }
         }
         TRY(c, launch_combine(c->o.p, c->inv.p, c->wts.p, n, tk, E, P, resid, y, nullptr, st));
         prof_mark(c, ev, 6);
@@ -680,8 +683,19 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
     a.h = c->h.p; a.hq = c->hq.p; a.hd = c->hd.p;
     a.gdbg = c->dbg_gu ? c->g.p : nullptr; a.udbg = c->dbg_gu ? c->u.p : nullptr;
     expert_counters(c, a, 0);
+    // A K-quant shared expert (one latency-bound mat-vec of 10-12 MB per matrix) runs on the side stream beside the
+    // routed launches: it reads x's Q8_K and writes only its own rows (h / Q8_K(h) rows P .. P + n - 1, o rows P ..,
+    // ksg / ksu), which no routed kernel touches; the combine waits for it.
+    const bool side = ksh && kq && lf[3] != FL_IQ2 && !c->no_side;
+    if (side) {
+        ALLOC(c, c->ksg, (size_t) n * H); ALLOC(c, c->ksu, (size_t) n * H);
+        TRY(c, hipEventRecord(c->efork, st)); TRY(c, hipStreamWaitEvent(c->side, c->efork, 0));
+        if (int rc = shared_gateup_sep(c, L, n, P, E, H, tk, c->side)) { return rc; }
+        if (int rc = shared_down_sep(c, L, n, P, E, H, tk, c->side)) { return rc; }
+        TRY(c, hipEventRecord(c->ejoin, c->side));
+    }
     TRY(c, launch_experts_gateup(a, c->ncu, st));
-    if (ksh) { if (int rc = shared_gateup_sep(c, L, n, P, E, H, tk)) { return rc; } }   // h rows P .. P + n - 1
+    if (ksh && !side) { if (int rc = shared_gateup_sep(c, L, n, P, E, H, tk, st)) { return rc; } }   // h rows P .. P + n - 1
     prof_mark(c, ev, 5);
     if (kq) {   // o of every slot by its matrix's format, then the k-ordered combine (+ shared, + residual)
         if (lf[0] == FL_IQ2) {
@@ -694,7 +708,8 @@ static int moe_layer(FLCtx * c, const FLMoeLayer * L, const float * x, int n, fl
         } else {
             TRY(c, routed_down_kq(c, L, P, E, H, ne));
         }
-        if (int rc = shared_down_sep(c, L, n, P, E, H, tk)) { return rc; }
+        if (side) { TRY(c, hipStreamWaitEvent(st, c->ejoin, 0)); }
+        else if (int rc = shared_down_sep(c, L, n, P, E, H, tk, st)) { return rc; }
         TRY(c, launch_combine(c->o.p, c->inv.p, c->wts.p, n, tk, E, P, resid, y, nullptr, st));
         prof_mark(c, ev, 6);
         return FL_OK;

@@ -354,6 +354,63 @@ def test_decode1_real_formats(ctx, down_fmt):
     torch.cuda.empty_cache()
 
 
+DEC_FMTS = [(orc.Q3K, orc.Q5K, orc.Q5K, orc.Q6K), (4, orc.Q5K, orc.Q5K, orc.Q6K)]
+
+
+@pytest.mark.parametrize("fm", DEC_FMTS, ids=["q3k_q5q5q6", "iq2_q5q5q6"])
+def test_decode_batch_real_formats(ctx, fm):
+    """fl_moe_layer on 2..8 rows with a K-quant shared expert (the per-pass kernels; the shared expert's mat-vecs run
+    on a second stream beside the routed launches and the combine waits for them): calls of 8, 3 and 8 rows in a row
+    give the first result again, bit for bit (each call's second-stream work is ordered after the previous call's
+    combine), and equal the same calls with the shared expert on the context's stream (fl_set_debug bit 2); y against
+    the checker within the parity bar at n = 8 and 3 (the Q5_K / Q6_K shared outputs differ from ggml's by fp32
+    rounding, which the Q8_K of h can carry to a quantisation step). A 64-expert layer."""
+    import torch
+    from loki_amd import MoeLayerWeights
+    from tests._helpers import make_x, host_matrix
+    ne = 64
+    seed = 8300 + 10 * DEC_FMTS.index(fm)
+    base = MoeLayerWeights.synthetic(ctx, seed, n_exp=ne, bias_sigma=0.01)
+    down = _kq_device(torch, fm[0], ne * E, H, seed + 1) if fm[0] != 4 else base.down
+    sh = (_kq_device(torch, fm[1], H, E, seed + 2), _kq_device(torch, fm[2], H, E, seed + 3), _kq_device(torch, fm[3], E, H, seed + 4))
+    layer = MoeLayerWeights(base.gate_inp, base.probs_b, base.gate, base.up, down, *sh, n_exp=ne)
+    x8, x3 = make_x(ctx, 8, seed=seed + 5), make_x(ctx, 3, seed=seed + 6)
+    ctx.set_layer_formats(*fm)
+    try:
+        print("decode batch real formats %s: n 8, 3, 8" % (fm,), flush=True)
+        y8 = ctx.moe_layer(layer, x8).clone()
+        y3 = ctx.moe_layer(layer, x3).clone()
+        y8b = ctx.moe_layer(layer, x8).clone()
+        ctx.sync()
+        assert ctx.debug().kernel == 0
+        print("decode batch real formats %s: shared expert on the context's stream" % (fm,), flush=True)
+        ctx.set_debug(False, shared_on_stream=True)
+        y8s = ctx.moe_layer(layer, x8).clone()
+        y3s = ctx.moe_layer(layer, x3).clone()
+        ctx.sync()
+    finally:
+        ctx.set_debug(False); ctx.set_layer_formats()
+    for a_, b_ in ((y8, y8b), (y8, y8s), (y3, y3s)):
+        assert np.array_equal(a_.cpu().numpy().view(np.uint8), b_.cpu().numpy().view(np.uint8))
+    W, b = layer.gate_inp.cpu().numpy(), layer.probs_b.cpu().numpy()
+    for x, y in ((x8, y8), (x3, y3)):
+        xs = x.cpu().numpy()
+        _, _, so, wo = orc.router(W, b, xs)
+        sel = sorted(set(int(e) for e in so.ravel()))
+        gate = {e: host_matrix(ctx, layer.expert_slice("gate", e), H, E) for e in sel}
+        up = {e: host_matrix(ctx, layer.expert_slice("up", e), H, E) for e in sel}
+        if fm[0] == 4:
+            dn = {e: host_matrix(ctx, layer.expert_slice("down", e), E, H) for e in sel}
+        else:
+            mb = E * (H // 256) * KQ_BLOCK[fm[0]][0]
+            dn = {e: down[e * mb:(e + 1) * mb].cpu().numpy() for e in sel}
+        ref = orc.moe_experts(xs, so, wo, gate, up, dn, *(m.cpu().numpy() for m in sh), n_exp=ne, fmts=fm)["y"]
+        ok, err = bar_close(y.cpu().numpy(), ref, l2=2e-3, mx=1e-2)
+        assert ok, (x.shape[0], err)
+    del layer, base, down, sh
+    torch.cuda.empty_cache()
+
+
 # (routed down, shared gate, up, down): the real shards'; a K-quant routed down with the shared expert in IQ2_XXS (GEMM
 # columns); a K-quant shared expert beside an IQ2_XXS routed down (the down GEMM); an IQ2_XXS shared gate/up with a
 # Q6_K shared down (the shared gate/up on the per-pass kernel)
